@@ -1,0 +1,104 @@
+/*
+ * libvault_amd — C ABI of the MI355X (gfx950) kernels for the VAULT v3 decode/prefill hot path.
+ *
+ * Conventions (mirroring runtime/vault3.h:9-12, 35-49, 89, 153-161 of the reference):
+ *   - Every entry point is stream-ordered on `stream` (a hipStream_t; NULL = default stream),
+ *     takes device pointers and plain sizes, never allocates, never synchronises.
+ *   - Return value: 0 = VGX_OK, negative = error (codes reuse the reference's V3_E_* numbers
+ *     where the meaning matches).  Launch failures return VGX_E_HIP.
+ *   - Dtype tags are the VLT3 tensor dtypes (tools/vlt3.py:29; runtime/vault3.h:51).
+ *
+ * Quantized weights live on the device in a packed "row-quad" layout produced by
+ * vgx_qweight_pack from the VLT3 AoS blocks (34-byte Q8_0, 18-byte Q4_0; tools/vlt3.py:98-99):
+ *   rows are padded to a multiple of 4 (padding rows have scale 0);
+ *   quants: [rows/4][cols/32][4][QB]   QB = 32 (Q8_0 int8), 16 (Q4_0 nibble bytes), 128 (F32 floats)
+ *   scales: [rows/4][cols/32][4] fp16, at byte offset vgx_qweight_scale_offset() (Q8_0/Q4_0 only)
+ * The byte count per block is unchanged (34 / 18 B); the layout lets one lane fetch one 32-weight
+ * block of four rows with aligned 128-bit loads.
+ */
+#ifndef VAULT_AMD_H
+#define VAULT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VGX_ABI_VERSION 1
+
+enum {
+    VGX_OK = 0,
+    VGX_E_SIZE = -1,   /* V3_E_SIZE: a size or count is out of range */
+    VGX_E_DTYPE = -5,  /* V3_E_DTYPE: unsupported dtype for this entry point */
+    VGX_E_SHAPE = -7,  /* V3_E_SHAPE: inconsistent shapes (e.g. cols not a multiple of 32) */
+    VGX_E_ARENA = -8,  /* V3_E_ARENA: caller workspace too small or misaligned */
+    VGX_E_LIMIT = -10, /* V3_E_LIMIT: exceeds a compiled limit */
+    VGX_E_ALIGN = -11, /* V3_E_ALIGN: pointer not aligned as required */
+    VGX_E_ARG = -31,   /* null pointer or invalid flag */
+    VGX_E_HIP = -32    /* a HIP launch failed */
+};
+
+enum { VGX_F32 = 0, VGX_F16 = 1, VGX_BF16 = 2, VGX_Q8_0 = 8, VGX_Q4_0 = 9 };
+
+/* ---------------------------------------------------------------- version ---------------------- */
+
+/* ABI version of this library (VGX_ABI_VERSION).  No counterpart in the reference. */
+int vgx_abi_version(void);
+
+/* ---------------------------------------------------------------- weights ---------------------- */
+
+/* Bytes of the packed device layout for a [rows x cols] tensor of `dtype` (Q8_0, Q4_0 or F32);
+ * negative on error.  Replaces the reference's in-place use of file blocks
+ * (runtime/vault3.c:172-196 dtype_nbytes, 536-598 block walks). */
+int64_t vgx_qweight_packed_bytes(int dtype, int64_t rows, int64_t cols);
+
+/* Byte offset of the fp16 scale plane inside a packed Q8_0/Q4_0 tensor. */
+int64_t vgx_qweight_scale_offset(int dtype, int64_t rows, int64_t cols);
+
+/* VLT3 AoS blocks (device copy of the file payload) -> packed layout.  F32 takes row-major
+ * floats.  Replaces the file-layout reads of runtime/vault3.c:499-602 / tools/vlt3.py:114-157. */
+int vgx_qweight_pack(int dtype, const void *src_blocks, void *dst_packed, int64_t rows, int64_t cols,
+                     void *stream);
+
+/* Gate and up projections (same dtype, [rows x cols] each) packed into one tensor of 2*rows rows,
+ * row-quad q holding gate rows 2q,2q+1 and up rows 2q,2q+1, for vgx_qlinear_swiglu.
+ * Replaces the paired row walk of runtime/vault3.c:1942-1956 (mlp_gu_run). */
+int vgx_qweight_pack_gateup(int dtype, const void *gate_blocks, const void *up_blocks, void *dst_packed,
+                            int64_t rows, int64_t cols, void *stream);
+
+/* Packed layout -> VLT3 AoS blocks (inverse of vgx_qweight_pack; bit-exact round trip). */
+int vgx_qweight_unpack(int dtype, const void *packed, void *dst_blocks, int64_t rows, int64_t cols,
+                       void *stream);
+
+/* Packed weights -> fp32 [rows x cols]: w = f32(d) * q (Q8_0), (n - 8) * f32(d) (Q4_0).
+ * Bit-exact restatement of tools/vlt3.py:114-116, 152-157 (dequantize_q8_0 / dequantize_q4_0). */
+int vgx_qweight_dequant(int dtype, const void *packed, float *out, int64_t rows, int64_t cols, void *stream);
+
+/* Embedding lookup: out[i, :] = dequant(row ids[i]) for i < n_ids; ids outside [0, rows) read row
+ * `pad_row` (runtime/vault3.c:2040 substitutes pad_id).  Replaces embed_row (runtime/vault3.c:626-654)
+ * and nn.Embedding (src/vault_v3_model.py:1169, 2285). */
+int vgx_embed_rows(int dtype, const void *packed, int64_t rows, int64_t cols, const int64_t *ids, int64_t n_ids,
+                   int64_t pad_row, float *out, int64_t ldo, void *stream);
+
+/* ---------------------------------------------------------------- linear ----------------------- */
+
+/* y[b, r] (+)= sum_c W[r, c] * x[b, c] (+ bias[r]) for b < batch, r < rows.
+ * accumulate = 0 overwrites y, 1 adds into y (fused residual add).  bias may be NULL.
+ * Replaces matvec/row_dot (runtime/vault3.c:499-624) and every nn.Linear / F.linear of the
+ * decode and prefill paths (src/vault_v3_model.py:1036-1047, 1139, 1145-1150, 2150-2151). */
+int vgx_qlinear(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
+                int64_t batch, const float *bias, float *y, int64_t ldy, int accumulate, void *stream);
+
+/* h[b, r] = silu(gate_r . x_b) * (up_r . x_b) over a vgx_qweight_pack_gateup tensor; `rows` is
+ * the number of output rows (d_ff).  Replaces mlp_gu_run (runtime/vault3.c:1942-1956) and
+ * F.silu(gate_proj(x)) * up_proj(x) (src/vault_v3_model.py:1149-1150). */
+int vgx_qlinear_swiglu(int dtype, const void *w_gateup_packed, int64_t rows, int64_t cols, const float *x,
+                       int64_t ldx, int64_t batch, float *h, int64_t ldh, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VAULT_AMD_H */

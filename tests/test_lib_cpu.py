@@ -1,0 +1,53 @@
+"""libvault_amd loads, exports every symbol include/vault_amd.h declares, and its host-side
+argument validation returns the documented codes (no GPU needed: these calls return before any
+HIP call)."""
+import ctypes as C
+
+import pytest
+
+from vault_amd import _lib as L
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return L.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    declared = L.declared_symbols()
+    assert len(declared) >= 10
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, missing
+    assert set(declared) == set(L._SIGS), "ctypes signatures and header disagree"
+
+
+def test_abi_version(lib):
+    assert lib.vgx_abi_version() == 1
+
+
+@pytest.mark.parametrize("dt,rows,cols,expect", [
+    (L.Q4_0, 13, 96, 256 + 16 * 3 * 2),          # rows padded to 16: quants 16*3*16=768 -> 768, scales 96 B
+    (L.Q8_0, 4, 32, 256 + 8),
+    (L.F32, 5, 64, 8 * 64 * 4),
+])
+def test_packed_bytes(lib, dt, rows, cols, expect):
+    if dt == L.Q4_0:
+        q = 16 * 3 * 16
+        expect = (q + 255) // 256 * 256 + 16 * 3 * 2
+    elif dt == L.Q8_0:
+        q = 4 * 1 * 32
+        expect = (q + 255) // 256 * 256 + 4 * 1 * 2
+    assert lib.vgx_qweight_packed_bytes(dt, rows, cols) == expect
+
+
+def test_host_validation_codes(lib):
+    assert lib.vgx_qweight_packed_bytes(L.Q4_0, 4, 33) == -7
+    assert lib.vgx_qweight_packed_bytes(3, 4, 32) == -5
+    assert lib.vgx_qweight_packed_bytes(L.Q8_0, 0, 32) == -1
+    assert lib.vgx_qlinear(L.Q4_0, None, 4, 32, None, 32, 1, None, None, 4, 0, None) == -31
+    p = C.c_void_p(64)   # never dereferenced: validation fails first
+    assert lib.vgx_qlinear(L.Q4_0, p, 4, 33, p, 33, 1, None, p, 4, 0, None) == -7
+    assert lib.vgx_qlinear(L.Q4_0, p, 4, 32, p, 16, 1, None, p, 4, 0, None) == -1
+    assert lib.vgx_qlinear(L.Q4_0, p, 4, 32, p, 32, 1, None, p, 4, 2, None) == -31
+    assert lib.vgx_qlinear_swiglu(L.Q4_0, p, 3, 32, p, 32, 1, p, 3, None) == -7
+    assert lib.vgx_qlinear(L.Q4_0, p, 4, 32, p, 32, 0, None, p, 4, 0, None) == 0   # empty batch: no-op

@@ -1,0 +1,76 @@
+"""ctypes binding of libvault_amd.so (the C ABI declared in include/vault_amd.h).
+
+There is no fallback: if the library is missing or a symbol is absent, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_lib", "libvault_amd.so")
+HEADER = os.path.join(HERE, "..", "include", "vault_amd.h")
+
+VGX_OK = 0
+ERRORS = {
+    -1: "VGX_E_SIZE", -5: "VGX_E_DTYPE", -7: "VGX_E_SHAPE", -8: "VGX_E_ARENA", -10: "VGX_E_LIMIT",
+    -11: "VGX_E_ALIGN", -31: "VGX_E_ARG", -32: "VGX_E_HIP",
+}
+
+F32, F16, BF16, Q8_0, Q4_0 = 0, 1, 2, 8, 9
+
+P = C.c_void_p
+I32 = C.c_int
+I64 = C.c_int64
+F = C.c_float
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "vgx_abi_version": (I32, []),
+    "vgx_qweight_packed_bytes": (I64, [I32, I64, I64]),
+    "vgx_qweight_scale_offset": (I64, [I32, I64, I64]),
+    "vgx_qweight_pack": (I32, [I32, P, P, I64, I64, P]),
+    "vgx_qweight_pack_gateup": (I32, [I32, P, P, P, I64, I64, P]),
+    "vgx_qweight_unpack": (I32, [I32, P, P, I64, I64, P]),
+    "vgx_qweight_dequant": (I32, [I32, P, P, I64, I64, P]),
+    "vgx_embed_rows": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
+    "vgx_qlinear": (I32, [I32, P, I64, I64, P, I64, I64, P, P, I64, I32, P]),
+    "vgx_qlinear_swiglu": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
+}
+
+
+class VGXError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def declared_symbols() -> list:
+    """Every vgx_* function declared in include/vault_amd.h."""
+    with open(HEADER) as f:
+        txt = f.read()
+    return sorted(set(re.findall(r"\b(vgx_[a-z0-9_]+)\s*\(", txt)))
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise VGXError(f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.vgx_abi_version() != 1:
+        raise VGXError("ABI version mismatch")
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != VGX_OK:
+        raise VGXError(f"{what} failed: {ERRORS.get(rc, rc)}")

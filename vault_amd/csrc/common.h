@@ -1,0 +1,76 @@
+// Shared device helpers for the gfx950 kernels of libvault_amd.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/vault_amd.h"
+
+#define VGX_DEV __device__ __forceinline__
+
+namespace vgx {
+
+constexpr int kWave = 64;
+constexpr int QK = 32;
+
+// DPP control words (GFX9 encoding).
+constexpr int DPP_QUAD_1032 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_2301 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_MIRROR = 0x140;
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+
+template <int CTRL>
+VGX_DEV float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row receives the total.
+VGX_DEV float row16_sum(float v) {
+    v += dpp_f<DPP_QUAD_1032>(v);
+    v += dpp_f<DPP_QUAD_2301>(v);
+    v += dpp_f<DPP_ROW_HALF_MIRROR>(v);
+    v += dpp_f<DPP_ROW_MIRROR>(v);
+    return v;
+}
+
+VGX_DEV float row16_max(float v) {
+    v = fmaxf(v, dpp_f<DPP_QUAD_1032>(v));
+    v = fmaxf(v, dpp_f<DPP_QUAD_2301>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_f<DPP_ROW_MIRROR>(v));
+    return v;
+}
+
+VGX_DEV float wave_sum(float v) {
+    v = row16_sum(v);
+    v += __shfl_xor(v, 16, kWave);
+    v += __shfl_xor(v, 32, kWave);
+    return v;
+}
+
+VGX_DEV float wave_max(float v) {
+    v = row16_max(v);
+    v = fmaxf(v, __shfl_xor(v, 16, kWave));
+    v = fmaxf(v, __shfl_xor(v, 32, kWave));
+    return v;
+}
+
+VGX_DEV float half_bits_to_float(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
+}
+
+VGX_DEV float bf16_bits_to_float(uint32_t b) { return __uint_as_float((b & 0xFFFFu) << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 bits (finite inputs).
+VGX_DEV uint32_t float_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+
+}  // namespace vgx
+
+#define VGX_CHECK_LAUNCH()                                  \
+    do {                                                    \
+        if (hipGetLastError() != hipSuccess) return VGX_E_HIP; \
+    } while (0)
