@@ -97,6 +97,66 @@ int vgx_qlinear(int dtype, const void *w_packed, int64_t rows, int64_t cols, con
 int vgx_qlinear_swiglu(int dtype, const void *w_gateup_packed, int64_t rows, int64_t cols, const float *x,
                        int64_t ldx, int64_t batch, float *h, int64_t ldh, void *stream);
 
+/* ---------------------------------------------------------------- attention -------------------- */
+
+/* One contiguous run of key/value rows per (batch, kv group): row t of (b, g) is at element offset
+ * b*batch_stride + g*group_stride + t*head_dim of k (and of v).  Element type is the KV dtype. */
+typedef struct {
+    const void *k;
+    const void *v;
+    int64_t len;
+    int64_t batch_stride;
+    int64_t group_stride;
+} vgx_kv_span;
+
+/* Workspace bytes vgx_attn_decode needs for these sizes (0 when one split suffices). */
+int64_t vgx_attn_decode_workspace_bytes(int64_t B, int64_t H, int64_t G, int64_t D, int64_t n_keys);
+
+/* Decode attention: out[b, h, :] = softmax_j(q[b,h].k_j * scale + bias[h, j]) v_j over the keys of
+ * all spans concatenated in order, kv group g = h / (H/G).  q/out: [B][H][D] fp32 (q post-RoPE).
+ * kv_dtype: VGX_F32 or VGX_BF16.  n_spans <= 4.  bias (may be NULL) is fp32 [H][bias_hstride],
+ * added to the keys of span `bias_span` (the segment-memory span).  D in {64, 128}.
+ * Replaces VAULTv3Attention.step's SDPA / explicit biased softmax (src/vault_v3_model.py:1098-1136)
+ * and attn_run (runtime/vault3.c:1958-2032). */
+int vgx_attn_decode(int kv_dtype, const float *q, const vgx_kv_span *spans, int n_spans, const float *bias,
+                    int64_t bias_hstride, int bias_span, float *out, int64_t B, int64_t H, int64_t G, int64_t D,
+                    float scale, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------- small fused ops -------------- */
+
+/* RMSNorm rows: y[r, :] = w * (x[r, :] / sqrt(mean(x[r, :]^2) + eps)).
+ * Replaces RMSNorm.forward (src/vault_v3_model.py:764-774) and rmsnorm (runtime/vault3.c:656-660). */
+int vgx_rmsnorm(const float *x, int64_t ldx, const float *w, float *y, int64_t ldy, int64_t n_rows, int64_t dim,
+                float eps, void *stream);
+
+/* RoPE + KV-cache write for N tokens (decode: one token per sequence; prefill: a run of tokens).
+ * q [N][H][D] fp32 is rotated in place; k [N][G][D] is rotated into k_rot (if non-NULL) and copied
+ * raw into k_raw (if non-NULL); v [N][G][D] is copied into v_dst.  Destination row of token t,
+ * group g: t*dst_tstride + g*dst_gstride (elements, KV dtype).  The first n_sink tokens are also
+ * copied raw into sink_k_raw / sink_v at t*sink_tstride + g*sink_gstride.  table: fp32 rows
+ * [cos(D/2) | sin(D/2)]; token t uses row table + t*table_rstride.
+ * Replaces the ring write + RoPE of src/vault_v3_model.py:1079-1094, 2049-2058 and
+ * runtime/vault3.c:2162-2179. */
+int vgx_rope_qkv_write(int kv_dtype, float *q, const float *k, const float *v, int64_t N, int64_t H, int64_t G,
+                       int64_t D, const float *table, int64_t table_rstride, void *k_rot, void *k_raw, void *v_dst,
+                       int64_t dst_tstride, int64_t dst_gstride, void *sink_k_raw, void *sink_v, int64_t n_sink,
+                       int64_t sink_tstride, int64_t sink_gstride, void *stream);
+
+/* Rotate rows: dst[o, i, :] = R(src[o, i, :]) with angle row table + i*table_rstride, for o < n_outer,
+ * i < n_rows (rows contiguous, D elements each; src may equal dst).  Replaces the chunk-boundary
+ * re-base of k_prev by R_{-W} and the prefix re-rotation of segment/sink keys
+ * (src/vault_v3_model.py:1842-1856, 1926-1927; runtime/vault3.c:859-896, 1930-1940). */
+int vgx_rope_rotate(int kv_dtype, const void *src, void *dst, int64_t n_outer, int64_t src_ostride,
+                    int64_t dst_ostride, int64_t n_rows, int64_t D, const float *table, int64_t table_rstride,
+                    void *stream);
+
+/* Row gather: dst[o, j, :] = src[o, idx[j], :] for j < n_idx, o < n_outer (D elements per row,
+ * element size from dtype VGX_F32 / VGX_BF16); an index outside [0, src_rows) writes zeros.
+ * src and dst must not overlap.  Replaces the segment-bank KV compaction
+ * (src/vault_v3_model.py:1914-1920; runtime/vault3.c:1892-1913). */
+int vgx_gather_rows(int dtype, const void *src, void *dst, const int32_t *idx, int64_t n_idx, int64_t src_rows,
+                    int64_t n_outer, int64_t src_ostride, int64_t dst_ostride, int64_t D, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

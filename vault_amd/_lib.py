@@ -37,7 +37,19 @@ _SIGS = {
     "vgx_embed_rows": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
     "vgx_qlinear": (I32, [I32, P, I64, I64, P, I64, I64, P, P, I64, I32, P]),
     "vgx_qlinear_swiglu": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
+    "vgx_attn_decode_workspace_bytes": (I64, [I64, I64, I64, I64, I64]),
+    "vgx_attn_decode": (I32, [I32, P, P, I32, P, I64, I32, P, I64, I64, I64, I64, F, P, I64, P]),
+    "vgx_rmsnorm": (I32, [P, I64, P, P, I64, I64, I64, F, P]),
+    "vgx_rope_qkv_write": (I32, [I32, P, P, P, I64, I64, I64, I64, P, I64, P, P, P, I64, I64, P, P, I64, I64, I64, P]),
+    "vgx_rope_rotate": (I32, [I32, P, P, I64, I64, I64, I64, I64, P, I64, P]),
+    "vgx_gather_rows": (I32, [I32, P, P, P, I64, I64, I64, I64, I64, I64, P]),
 }
+
+
+class KVSpan(C.Structure):
+    """vgx_kv_span (include/vault_amd.h)."""
+    _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("len", C.c_int64),
+                ("batch_stride", C.c_int64), ("group_stride", C.c_int64)]
 
 
 class VGXError(RuntimeError):

@@ -154,3 +154,124 @@ def embed(w: QWeight, ids: torch.Tensor, pad_row: int = 0, out: Optional[torch.T
     L.check(L.load().vgx_embed_rows(w.dtype, w.packed.data_ptr(), w.rows, w.cols, ids64.data_ptr(), n, pad_row,
                                     o2.data_ptr(), o2.stride(0), _stream(w.device)), "vgx_embed_rows")
     return out
+
+
+# ------------------------------------------------------------------------------------------
+# attention and row ops
+# ------------------------------------------------------------------------------------------
+
+KV_DTYPES = {torch.float32: L.F32, torch.bfloat16: L.BF16}
+
+
+class Workspace:
+    """Grow-only device scratch owned by the caller (the library never allocates)."""
+
+    def __init__(self, device):
+        self.device = device
+        self.buf = torch.empty(0, dtype=torch.uint8, device=device)
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.buf.numel() < nbytes:
+            self.buf = torch.empty(max(nbytes, 2 * self.buf.numel()), dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+def attn_decode(q: torch.Tensor, spans, out: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
+                bias_span: int = -1, scale: Optional[float] = None, ws: Optional[Workspace] = None) -> torch.Tensor:
+    """q: [B, H, D] fp32 post-RoPE.  spans: list of (K, V) views shaped [B, G, n, D] (unit stride in D
+    and n; any batch / group stride).  bias: [H, n_bias] fp32 or None.  Returns [B, H, D] fp32."""
+    _need(q, torch.float32, "q")
+    B, H, D = q.shape
+    q = q.contiguous()
+    kv_dt = None
+    arr = (L.KVSpan * 4)()
+    n_tot = 0
+    G = None
+    for i, (k, v) in enumerate(spans):
+        if kv_dt is None:
+            kv_dt = KV_DTYPES[k.dtype]
+        if KV_DTYPES[k.dtype] != kv_dt or v.dtype != k.dtype:
+            raise ValueError("mixed KV dtypes")
+        if k.shape != v.shape or k.dim() != 4 or k.shape[0] != B or k.shape[3] != D:
+            raise ValueError(f"span {i} shape {tuple(k.shape)}")
+        G = k.shape[1]
+        if k.shape[2] == 0:
+            arr[i] = L.KVSpan(None, None, 0, 0, 0)
+            continue
+        if k.stride(3) != 1 or k.stride(2) != D or v.stride(3) != 1 or v.stride(2) != D or \
+                k.stride(0) != v.stride(0) or k.stride(1) != v.stride(1):
+            raise ValueError(f"span {i} strides")
+        G = k.shape[1]
+        n = k.shape[2]
+        arr[i] = L.KVSpan(k.data_ptr() if n else None, v.data_ptr() if n else None, n, k.stride(0), k.stride(1))
+        n_tot += n
+    if out is None:
+        out = torch.empty(B, H, D, dtype=torch.float32, device=q.device)
+    lib = L.load()
+    need = int(lib.vgx_attn_decode_workspace_bytes(B, H, G, D, n_tot))
+    L.check(0 if need >= 0 else need, "vgx_attn_decode_workspace_bytes")
+    ws = ws or Workspace(q.device)
+    wbuf = ws.get(max(need, 1))
+    if bias is not None:
+        _need(bias, torch.float32, "bias")
+        if bias.stride(1) != 1:
+            raise ValueError("bias needs unit stride along keys")
+        if not 0 <= bias_span < len(spans) or bias.shape[0] != H or bias.shape[1] < spans[bias_span][0].shape[2]:
+            raise ValueError("bias must be [H, >= len(bias span)]")
+    L.check(lib.vgx_attn_decode(kv_dt, q.data_ptr(), arr, len(spans), _ptr(bias),
+                                bias.stride(0) if bias is not None else 0, bias_span, out.data_ptr(), B, H, G, D,
+                                float(scale if scale is not None else D ** -0.5), wbuf.data_ptr(), wbuf.numel(),
+                                _stream(q.device)), "vgx_attn_decode")
+    return out
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    _need(x, torch.float32, "x")
+    d = x.shape[-1]
+    x2 = x.reshape(-1, d)
+    if out is None:
+        out = torch.empty_like(x2)
+    o2 = out.view(-1, d)
+    L.check(L.load().vgx_rmsnorm(x2.data_ptr(), x2.stride(0), w.data_ptr(), o2.data_ptr(), o2.stride(0), x2.shape[0],
+                                 d, float(eps), _stream(x.device)), "vgx_rmsnorm")
+    return out.view(x.shape)
+
+
+def rope_qkv_write(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor, table: torch.Tensor,
+                   table_rstride: int, k_rot: Optional[torch.Tensor], k_raw: Optional[torch.Tensor],
+                   v_dst: torch.Tensor, dst_tstride: int, dst_gstride: int,
+                   sink_k: Optional[torch.Tensor] = None, sink_v: Optional[torch.Tensor] = None, n_sink: int = 0,
+                   sink_tstride: int = 0, sink_gstride: int = 0) -> None:
+    """q [N,H,D] (rotated in place), k/v [N,G,D] fp32; destinations are the first rows to write
+    (views into the KV cache), strides in elements."""
+    N, G, D = k.shape
+    H = 0 if q is None else q.shape[1]
+    kv_dt = KV_DTYPES[v_dst.dtype]
+    L.check(L.load().vgx_rope_qkv_write(kv_dt, _ptr(q), k.data_ptr(), v.data_ptr(), N, H, G, D, table.data_ptr(),
+                                        table_rstride, _ptr(k_rot), _ptr(k_raw), v_dst.data_ptr(), dst_tstride,
+                                        dst_gstride, _ptr(sink_k), _ptr(sink_v), n_sink, sink_tstride, sink_gstride,
+                                        _stream(k.device)), "vgx_rope_qkv_write")
+
+
+def rope_rotate(src: torch.Tensor, dst: torch.Tensor, table: torch.Tensor, table_rstride: int) -> None:
+    """src/dst: [O, n, D] views with contiguous rows (any outer stride); row i of every outer slice is
+    rotated by table row i * table_rstride (fp32 [cos(D/2) | sin(D/2)])."""
+    O, n, D = src.shape
+    if dst.shape != src.shape or dst.dtype != src.dtype:
+        raise ValueError("src/dst mismatch")
+    for t in (src, dst):
+        if t.stride(2) != 1 or t.stride(1) != D:
+            raise ValueError("rows must be contiguous")
+    L.check(L.load().vgx_rope_rotate(KV_DTYPES[src.dtype], src.data_ptr(), dst.data_ptr(), O, src.stride(0),
+                                     dst.stride(0), n, D, table.data_ptr(), table_rstride, _stream(src.device)),
+            "vgx_rope_rotate")
+
+
+def gather_rows(src: torch.Tensor, dst: torch.Tensor, idx: torch.Tensor) -> None:
+    """src: [O, n_src, D], dst: [O, n_idx, D] (views, uniform outer stride); idx int32 [n_idx]."""
+    O, n_src, D = src.shape
+    assert dst.shape[0] == O and dst.shape[2] == D and idx.numel() == dst.shape[1]
+    idx32 = idx.to(device=src.device, dtype=torch.int32).contiguous()
+    L.check(L.load().vgx_gather_rows(KV_DTYPES[src.dtype], src.data_ptr(), dst.data_ptr(), idx32.data_ptr(),
+                                     idx32.numel(), n_src, O, src.stride(0), dst.stride(0), D, _stream(src.device)),
+            "vgx_gather_rows")
