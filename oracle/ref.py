@@ -1,0 +1,104 @@
+"""ctypes driver of the reference C runtime built into oracle/_ref/libv3ref.so (TEST INFRASTRUCTURE ONLY).
+
+The library is runtime/vault3.c compiled from the reference tree by oracle/Makefile with the shim
+in oracle/ref_shim.c.  It is an independent oracle for the whole decode step: Q8_0/Q4_0 row dots
+(runtime/vault3.c:499-602), attention (:1958-2032), boundary re-basing and segment eviction
+(:1833-1915, 2076-2105), scorer and habituation (:961-977, 2201-2216).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "_ref", "libv3ref.so")
+
+
+def available() -> bool:
+    return os.path.exists(LIB)
+
+
+def build() -> bool:
+    """Build oracle/_ref/libv3ref.so when the reference tree is present; True if the library exists."""
+    import subprocess
+    if os.path.isdir("/root/reference/runtime"):
+        subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return available()
+
+
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        lib = C.CDLL(LIB)
+        lib.ref_open.restype = C.c_void_p
+        lib.ref_open.argtypes = [C.c_char_p, C.c_uint64, C.c_int, C.POINTER(C.c_int)]
+        lib.ref_close.argtypes = [C.c_void_p]
+        lib.ref_reset.argtypes = [C.c_void_p]
+        lib.ref_set_threads.argtypes = [C.c_void_p, C.c_int]
+        lib.ref_set_pinned.argtypes = [C.c_void_p, C.c_uint32]
+        lib.ref_set_pinned.restype = C.c_int
+        lib.ref_step.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p]
+        lib.ref_vocab.argtypes = [C.c_void_p]
+        lib.ref_vocab.restype = C.c_uint32
+        lib.ref_arena_bytes.argtypes = [C.c_void_p]
+        lib.ref_arena_bytes.restype = C.c_uint64
+        lib.ref_state_info.argtypes = [C.c_void_p] + [C.c_void_p] * 4
+        lib.ref_mem_pos.argtypes = [C.c_void_p, C.c_void_p]
+        lib.ref_seed_long_context.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint64]
+        lib.ref_seed_long_context.restype = C.c_int
+        _lib = lib
+    return _lib
+
+
+class RefRuntime:
+    def __init__(self, vlt3_bytes: bytes, threads: int = 1, verify: bool = True):
+        lib = _load()
+        err = C.c_int(0)
+        self._h = lib.ref_open(vlt3_bytes, len(vlt3_bytes), 1 if verify else 0, C.byref(err))
+        if not self._h:
+            raise RuntimeError(f"v3_load / v3_state_init failed: {err.value}")
+        self.vocab = lib.ref_vocab(self._h)
+        self.threads = threads
+        lib.ref_set_threads(self._h, threads)
+
+    def close(self):
+        if self._h:
+            _load().ref_close(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def reset(self):
+        _load().ref_reset(self._h)
+
+    def set_pinned(self, n: int) -> None:
+        rc = _load().ref_set_pinned(self._h, n)
+        if rc:
+            raise RuntimeError(f"v3_set_pinned: {rc}")
+
+    def step(self, tok: int, out: np.ndarray | None = None) -> np.ndarray:
+        if out is None:
+            out = np.empty(self.vocab, dtype=np.float32)
+        _load().ref_step(self._h, int(tok), out.ctypes.data)
+        return out
+
+    def info(self):
+        pos, n_pin, mem, off = C.c_uint64(), C.c_uint32(), C.c_uint32(), C.c_uint32()
+        _load().ref_state_info(self._h, C.byref(pos), C.byref(n_pin), C.byref(mem), C.byref(off))
+        return dict(pos=pos.value, n_pin=n_pin.value, mem_cnt=mem.value, seg_id_offset=off.value)
+
+    def mem_pos(self) -> np.ndarray:
+        n = self.info()["mem_cnt"]
+        out = np.zeros(max(1, n), dtype=np.uint64)
+        _load().ref_mem_pos(self._h, out.ctypes.data)
+        return out[:n].astype(np.int64)
+
+    def seed_long_context(self, pos: int, n_pin: int, mem_cnt: int, seed: int = 0) -> None:
+        rc = _load().ref_seed_long_context(self._h, pos, n_pin, mem_cnt, seed)
+        if rc:
+            raise RuntimeError("seed_long_context rejected the arguments")

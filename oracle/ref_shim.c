@@ -1,0 +1,245 @@
+/* ctypes-facing shim around the reference C runtime (runtime/vault3.h API).
+ *
+ * TEST INFRASTRUCTURE ONLY.  Compiled together with the reference's runtime/vault3.c into
+ * oracle/_ref/libv3ref.so by oracle/Makefile; never linked into the product.
+ *
+ * Provides: an aligned model buffer + v3_load (runtime/vault3.c:273-455), a state arena +
+ * v3_state_init (:828-852), v3_step (:2034-2222), v3_set_pinned (:898-928), an optional persistent
+ * thread pool implementing the v3_parallel_for_fn hook (runtime/vault3.h:103-106), and a helper that
+ * seeds the fixed-size state as it stands deep into a long stream (for timing at long context).
+ */
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "vault3.h"
+
+typedef struct pool pool_t;
+
+typedef struct {
+    v3_model m;
+    v3_state s;
+    uint8_t *buf;
+    void *arena;
+    size_t arena_size;
+    pool_t *pool;
+} ref_ctx;
+
+/* ---------------------------------------------------------------- thread pool ---------------- */
+
+struct pool {
+    int n;
+    pthread_t *th;
+    pthread_mutex_t mu;
+    pthread_cond_t cv_go, cv_done;
+    uint64_t gen;
+    int pending;
+    int quit;
+    v3_task_fn fn;
+    void *arg;
+    uint32_t total;
+};
+
+typedef struct {
+    pool_t *p;
+    int idx;
+} worker_arg;
+
+static void run_share(pool_t *p, int idx) {
+    uint32_t per = (p->total + (uint32_t)p->n - 1u) / (uint32_t)p->n;
+    uint32_t i0 = (uint32_t)idx * per, i1 = i0 + per;
+    if (i1 > p->total) i1 = p->total;
+    if (i0 < i1) p->fn(p->arg, i0, i1);
+}
+
+static void *worker(void *a) {
+    worker_arg *wa = (worker_arg *)a;
+    pool_t *p = wa->p;
+    int idx = wa->idx;
+    free(wa);
+    uint64_t seen = 0;
+    for (;;) {
+        pthread_mutex_lock(&p->mu);
+        while (!p->quit && p->gen == seen) pthread_cond_wait(&p->cv_go, &p->mu);
+        if (p->quit) {
+            pthread_mutex_unlock(&p->mu);
+            return 0;
+        }
+        seen = p->gen;
+        pthread_mutex_unlock(&p->mu);
+        run_share(p, idx);
+        pthread_mutex_lock(&p->mu);
+        if (--p->pending == 0) pthread_cond_signal(&p->cv_done);
+        pthread_mutex_unlock(&p->mu);
+    }
+}
+
+static void pool_for(void *ctx, v3_task_fn fn, void *arg, uint32_t n) {
+    pool_t *p = (pool_t *)ctx;
+    pthread_mutex_lock(&p->mu);
+    p->fn = fn;
+    p->arg = arg;
+    p->total = n;
+    p->pending = p->n - 1;
+    p->gen++;
+    pthread_cond_broadcast(&p->cv_go);
+    pthread_mutex_unlock(&p->mu);
+    run_share(p, 0);
+    pthread_mutex_lock(&p->mu);
+    while (p->pending > 0) pthread_cond_wait(&p->cv_done, &p->mu);
+    pthread_mutex_unlock(&p->mu);
+}
+
+static void pool_free(pool_t *p) {
+    if (!p) return;
+    pthread_mutex_lock(&p->mu);
+    p->quit = 1;
+    pthread_cond_broadcast(&p->cv_go);
+    pthread_mutex_unlock(&p->mu);
+    for (int i = 0; i < p->n - 1; i++) pthread_join(p->th[i], 0);
+    free(p->th);
+    free(p);
+}
+
+static pool_t *pool_new(int n) {
+    pool_t *p = (pool_t *)calloc(1, sizeof(pool_t));
+    p->n = n;
+    pthread_mutex_init(&p->mu, 0);
+    pthread_cond_init(&p->cv_go, 0);
+    pthread_cond_init(&p->cv_done, 0);
+    p->th = (pthread_t *)calloc((size_t)n, sizeof(pthread_t));
+    for (int i = 1; i < n; i++) {
+        worker_arg *wa = (worker_arg *)malloc(sizeof(worker_arg));
+        wa->p = p;
+        wa->idx = i;
+        pthread_create(&p->th[i - 1], 0, worker, wa);
+    }
+    return p;
+}
+
+/* ---------------------------------------------------------------- API -------------------------- */
+
+ref_ctx *ref_open(const uint8_t *data, uint64_t size, int verify, int *err) {
+    ref_ctx *c = (ref_ctx *)calloc(1, sizeof(ref_ctx));
+    c->buf = (uint8_t *)aligned_alloc(64, (size + 63) & ~(uint64_t)63);
+    memcpy(c->buf, data, size);
+    int rc = v3_load(&c->m, c->buf, size, verify);
+    if (rc != V3_OK) {
+        *err = rc;
+        free(c->buf);
+        free(c);
+        return 0;
+    }
+    c->arena_size = v3_state_arena_size(&c->m);
+    c->arena = aligned_alloc(64, (c->arena_size + 63) & ~(size_t)63);
+    rc = v3_state_init(&c->s, &c->m, c->arena, c->arena_size);
+    if (rc != V3_OK) {
+        *err = rc;
+        free(c->arena);
+        free(c->buf);
+        free(c);
+        return 0;
+    }
+    *err = 0;
+    return c;
+}
+
+int ref_set_threads(ref_ctx *c, int n) {
+    pool_free(c->pool);
+    c->pool = 0;
+    c->s.par_for = 0;
+    c->s.par_ctx = 0;
+    if (n > 1) {
+        c->pool = pool_new(n);
+        c->s.par_for = pool_for;
+        c->s.par_ctx = c->pool;
+    }
+    return 0;
+}
+
+void ref_close(ref_ctx *c) {
+    if (!c) return;
+    pool_free(c->pool);
+    free(c->arena);
+    free(c->buf);
+    free(c);
+}
+
+void ref_reset(ref_ctx *c) { v3_state_reset(&c->s); }
+
+int ref_set_pinned(ref_ctx *c, uint32_t n) { return v3_set_pinned(&c->s, n); }
+
+uint64_t ref_arena_bytes(ref_ctx *c) { return (uint64_t)c->arena_size; }
+
+uint32_t ref_vocab(ref_ctx *c) { return c->m.vocab_size; }
+
+int ref_step(ref_ctx *c, uint32_t tok, float *out) {
+    const float *lg = v3_step(&c->s, tok);
+    if (out) memcpy(out, lg, sizeof(float) * c->m.vocab_size);
+    return 0;
+}
+
+/* Host-visible scalar state for cross-checks. */
+void ref_state_info(ref_ctx *c, uint64_t *pos, uint32_t *n_pin, uint32_t *mem_cnt, uint32_t *seg_id_offset) {
+    *pos = c->s.pos;
+    *n_pin = c->s.n_pin;
+    *mem_cnt = c->s.mem_cnt;
+    *seg_id_offset = c->s.seg_id_offset;
+}
+
+void ref_mem_pos(ref_ctx *c, uint64_t *out) {
+    for (uint32_t i = 0; i < c->s.mem_cnt; i++) out[i] = c->s.mem_pos[i];
+}
+
+static uint64_t splitmix(uint64_t *x) {
+    uint64_t z = (*x += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static void fill(float *p, uint64_t n, uint64_t *rng) {
+    for (uint64_t i = 0; i < n; i++) {
+        /* sum of 4 uniforms, centred and scaled to unit variance */
+        double s = 0.0;
+        for (int k = 0; k < 4; k++) s += (double)(splitmix(rng) >> 11) * (1.0 / 9007199254740992.0);
+        p[i] = (float)((s - 2.0) * 1.7320508075688772);
+    }
+}
+
+/* Put the state where a long stream leaves it: position `pos` (chunk index >= 2), `n_pin` sinks
+ * locked, `mem_cnt` occupied segment-memory slots, every KV row filled with unit-variance values.
+ * Steps taken from here stay inside the current chunk while pos % W < W - 1. */
+int ref_seed_long_context(ref_ctx *c, uint64_t pos, uint32_t n_pin, uint32_t mem_cnt, uint64_t seed) {
+    v3_state *s = &c->s;
+    const v3_model *m = &c->m;
+    uint64_t W = m->window, G = m->n_kv_heads, D = m->head_dim;
+    if (pos < 2 * W || n_pin > s->sink_cap || mem_cnt > s->seg_budget) return -1;
+    uint64_t rng = seed;
+    for (uint32_t l = 0; l < m->n_layers; l++) {
+        v3_layer_state *L = &s->ls[l];
+        fill(L->k_prev, G * W * D, &rng); fill(L->k_cur, G * W * D, &rng);
+        fill(L->v_prev, G * W * D, &rng); fill(L->v_cur, G * W * D, &rng);
+        fill(L->kraw_prev, G * W * D, &rng); fill(L->kraw_cur, G * W * D, &rng);
+        fill(L->k_sink_raw, G * s->sink_cap * D, &rng); fill(L->k_sink, G * s->sink_cap * D, &rng);
+        fill(L->v_sink, G * s->sink_cap * D, &rng);
+        if (s->seg_cap) {
+            fill(L->k_seg_raw, G * s->seg_cap * D, &rng); fill(L->k_seg, G * s->seg_cap * D, &rng);
+            fill(L->v_seg, G * s->seg_cap * D, &rng);
+        }
+    }
+    s->pos = pos;
+    s->n_pin = n_pin;
+    s->pin_locked = 1;
+    s->mem_cnt = mem_cnt;
+    for (uint32_t i = 0; i < mem_cnt; i++) {
+        s->mem_pos[i] = (uint64_t)i * 8u;
+        s->mem_score[i] = 0.0f;
+        s->mem_tok[i] = 0;
+        s->mem_seg[i] = i / 16u;
+    }
+    s->n_uniq_segs = 0;   /* no shingles: resonance stays inactive */
+    s->ema_ready = 1;
+    return 0;
+}

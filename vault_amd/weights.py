@@ -1,0 +1,193 @@
+"""Model weights on the device: every projection as a packed QWeight, norms / biases as fp32.
+
+Projections that share a dtype are fused into one packed tensor so that one GEMV launch streams
+them: q|k|v when all three share a dtype (else q alone and k|v), and gate/up interleaved for the
+SwiGLU epilogue.  The tied LM head reuses the embedding tensor (src/vault_v3_model.py:2150-2151).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, List, Optional
+
+import numpy as np
+import torch
+
+from . import ops, vlt3
+from .config import VAULTv3Config
+
+Tensor = vlt3.Tensor
+
+
+@dataclass
+class LayerWeights:
+    ln1: torch.Tensor
+    ln2: torch.Tensor
+    wq: Optional[ops.QWeight]        # None when fused into wqkv
+    wqkv: ops.QWeight                # q|k|v fused, or k|v when q is separate
+    bq: torch.Tensor
+    bqkv: torch.Tensor               # bias matching wqkv's rows
+    wo: ops.QWeight
+    wgu: ops.QWeight
+    wd: ops.QWeight
+
+
+@dataclass
+class ScorerWeights:
+    ln_w: torch.Tensor
+    ln_b: torch.Tensor
+    w1: ops.QWeight
+    b1: torch.Tensor
+    w2: torch.Tensor   # [hidden] fp32
+    b2: torch.Tensor   # [1]
+
+
+def _f32(t: Tensor, device) -> torch.Tensor:
+    if t.dtype != vlt3.F32:
+        raise vlt3.VLT3Error(f"{t.name} must be F32")
+    return torch.from_numpy(np.frombuffer(t.data, dtype="<f4").copy()).to(device)
+
+
+def _block_dtype(t: Tensor) -> int:
+    if t.dtype not in (vlt3.Q8_0, vlt3.Q4_0, vlt3.F32):
+        raise vlt3.VLT3Error(f"{t.name}: dtype {t.dtype} is not supported on the device path")
+    return t.dtype
+
+
+class ModelWeights:
+    def __init__(self, cfg: VAULTv3Config, device):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.layers: List[LayerWeights] = []
+        self.embed: Optional[ops.QWeight] = None
+        self.norm: Optional[torch.Tensor] = None
+        self.scorer: Optional[ScorerWeights] = None
+
+    # ------------------------------------------------------------------ construction
+    @classmethod
+    def from_tensors(cls, cfg: VAULTv3Config, tensors: Dict[str, Tensor], device) -> "ModelWeights":
+        self = cls(cfg, device)
+        dev = self.device
+        emb = tensors["embed_tokens.weight"]
+        self.embed = ops.QWeight.from_blocks(_block_dtype(emb), cfg.vocab_size, cfg.d_model, emb.data, dev)
+        self.norm = _f32(tensors["norm.weight"], dev)
+        H, G, D, d, F = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_model, cfg.d_ff
+        for li in range(cfg.n_layers):
+            p = f"layers.{li}."
+            t = {k[len(p):]: v for k, v in tensors.items() if k.startswith(p)}
+            q, k, v = t["self_attn.q_proj.weight"], t["self_attn.k_proj.weight"], t["self_attn.v_proj.weight"]
+            bq, bk, bv = (_f32(t[f"self_attn.{n}_proj.bias"], dev) for n in "qkv")
+            if _block_dtype(q) == _block_dtype(k) == _block_dtype(v):
+                wq = None
+                wqkv = ops.QWeight.from_blocks(q.dtype, H * D + 2 * G * D, d, q.data + k.data + v.data, dev)
+                bqkv = torch.cat([bq, bk, bv])
+            else:
+                if _block_dtype(k) != _block_dtype(v):
+                    raise vlt3.VLT3Error("k_proj and v_proj must share a dtype")
+                wq = ops.QWeight.from_blocks(q.dtype, H * D, d, q.data, dev)
+                wqkv = ops.QWeight.from_blocks(k.dtype, 2 * G * D, d, k.data + v.data, dev)
+                bqkv = torch.cat([bk, bv])
+            o = t["self_attn.o_proj.weight"]
+            g, u, dn = t["mlp.gate_proj.weight"], t["mlp.up_proj.weight"], t["mlp.down_proj.weight"]
+            if _block_dtype(g) != _block_dtype(u):
+                raise vlt3.VLT3Error("gate_proj and up_proj must share a dtype")
+            self.layers.append(LayerWeights(
+                ln1=_f32(t["input_layernorm.weight"], dev), ln2=_f32(t["post_attention_layernorm.weight"], dev),
+                wq=wq, wqkv=wqkv, bq=bq, bqkv=bqkv,
+                wo=ops.QWeight.from_blocks(_block_dtype(o), d, H * D, o.data, dev),
+                wgu=ops.QWeight.gateup_from_blocks(g.dtype, F, d, g.data, u.data, dev),
+                wd=ops.QWeight.from_blocks(_block_dtype(dn), d, F, dn.data, dev),
+            ))
+        if cfg.has_seg_scorer and "seg_scorer.ln.weight" in tensors:
+            fd = len(cfg.seg_layers) * d
+            w2 = _f32(tensors["seg_scorer.fc2.weight"], dev)
+            self.scorer = ScorerWeights(
+                ln_w=_f32(tensors["seg_scorer.ln.weight"], dev), ln_b=_f32(tensors["seg_scorer.ln.bias"], dev),
+                w1=ops.QWeight.from_blocks(vlt3.F32, cfg.seg_hidden, fd, tensors["seg_scorer.fc1.weight"].data, dev),
+                b1=_f32(tensors["seg_scorer.fc1.bias"], dev), w2=w2.reshape(-1),
+                b2=_f32(tensors["seg_scorer.fc2.bias"], dev))
+        torch.cuda.synchronize(dev)
+        return self
+
+    @classmethod
+    def from_vlt3(cls, path: str, device) -> "ModelWeights":
+        vf = vlt3.read_vlt3(path)
+        cfg = VAULTv3Config.from_vlt3_header(vf.header)
+        return cls.from_tensors(cfg, vf.tensors, device)
+
+    # ------------------------------------------------------------------ accounting
+    def layer_stream_bytes(self) -> int:
+        tot = 0
+        for lw in self.layers:
+            for w in (lw.wq, lw.wqkv, lw.wo, lw.wgu, lw.wd):
+                if w is not None:
+                    tot += w.stream_bytes
+        return tot
+
+
+# ----------------------------------------------------------------------------------------------
+# tensor sets (quantized per the hybrid policy, or drawn directly as quantized blocks)
+# ----------------------------------------------------------------------------------------------
+
+def tensor_shapes(cfg: VAULTv3Config) -> Dict[str, tuple]:
+    H, G, D, d, F = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_model, cfg.d_ff
+    s = {"embed_tokens.weight": (cfg.vocab_size, d), "norm.weight": (d,)}
+    for li in range(cfg.n_layers):
+        p = f"layers.{li}."
+        s.update({
+            p + "input_layernorm.weight": (d,), p + "self_attn.q_proj.weight": (H * D, d), p + "self_attn.q_proj.bias": (H * D,),
+            p + "self_attn.k_proj.weight": (G * D, d), p + "self_attn.k_proj.bias": (G * D,),
+            p + "self_attn.v_proj.weight": (G * D, d), p + "self_attn.v_proj.bias": (G * D,),
+            p + "self_attn.o_proj.weight": (d, H * D), p + "post_attention_layernorm.weight": (d,),
+            p + "mlp.gate_proj.weight": (F, d), p + "mlp.up_proj.weight": (F, d), p + "mlp.down_proj.weight": (d, F),
+        })
+    if cfg.has_seg_scorer:
+        fd = len(cfg.seg_layers) * d
+        s.update({"seg_scorer.ln.weight": (fd,), "seg_scorer.ln.bias": (fd,), "seg_scorer.fc1.weight": (cfg.seg_hidden, fd),
+                  "seg_scorer.fc1.bias": (cfg.seg_hidden,), "seg_scorer.fc2.weight": (1, cfg.seg_hidden),
+                  "seg_scorer.fc2.bias": (1,)})
+    return s
+
+
+def quantize_state(cfg: VAULTv3Config, state: Dict[str, np.ndarray], fmt: str) -> Dict[str, Tensor]:
+    """fp32 arrays -> VLT3 tensors with the hybrid dtype policy (tools/vlt3.py:312-330)."""
+    out = {}
+    for name, arr in state.items():
+        dt = vlt3.choose_dtype(name, fmt, cfg.n_layers)
+        a = np.asarray(arr, dtype=np.float32)
+        if dt in (vlt3.Q8_0, vlt3.Q4_0) and a.shape[-1] % 32:
+            dt = vlt3.F32
+        out[name] = Tensor(name, dt, tuple(a.shape), vlt3.quantize(dt, a))
+    return out
+
+
+def random_state(cfg: VAULTv3Config, seed: int, std: float = 0.15) -> Dict[str, np.ndarray]:
+    """fp32 random-init weights in the recipe of the reference's runtime tests
+    (tests/test_vlt3_runtime.py:33-49): norms U(0.8, 1.2), scorer LN bias N(0, 0.05), else N(0, std)."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shp in tensor_shapes(cfg).items():
+        if "layernorm" in name or name in ("norm.weight", "seg_scorer.ln.weight"):
+            out[name] = rng.uniform(0.8, 1.2, shp).astype(np.float32)
+        elif name == "seg_scorer.ln.bias":
+            out[name] = (rng.standard_normal(shp) * 0.05).astype(np.float32)
+        else:
+            out[name] = (rng.standard_normal(shp) * std).astype(np.float32)
+    return out
+
+
+def synthetic_tensors(cfg: VAULTv3Config, fmt: str, seed: int) -> Dict[str, Tensor]:
+    """Random-init weights drawn directly as quantized blocks (hybrid policy), F32 norms U(0.8,1.2),
+    biases N(0, 0.02), scorer fp32 N(0, 0.02): the synthetic recipe of the 1.54B decode workload."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shp in tensor_shapes(cfg).items():
+        dt = vlt3.choose_dtype(name, fmt, cfg.n_layers)
+        if dt in (vlt3.Q8_0, vlt3.Q4_0):
+            out[name] = Tensor(name, dt, shp, vlt3.synthetic_blocks(dt, shp[0], shp[1], rng))
+            continue
+        if "layernorm" in name or name in ("norm.weight", "seg_scorer.ln.weight"):
+            a = rng.uniform(0.8, 1.2, shp).astype(np.float32)
+        else:
+            a = (rng.standard_normal(shp) * 0.02).astype(np.float32)
+        out[name] = Tensor(name, vlt3.F32, shp, a.astype("<f4").tobytes())
+    return out
