@@ -113,14 +113,18 @@ typedef struct {
 int64_t vgx_attn_decode_workspace_bytes(int64_t B, int64_t H, int64_t G, int64_t D, int64_t n_keys);
 
 /* Decode attention: out[b, h, :] = softmax_j(q[b,h].k_j * scale + bias[h, j]) v_j over the keys of
- * all spans concatenated in order, kv group g = h / (H/G).  q/out: [B][H][D] fp32 (q post-RoPE).
- * kv_dtype: VGX_F32 or VGX_BF16.  n_spans <= 4.  bias (may be NULL) is fp32 [H][bias_hstride],
- * added to the keys of span `bias_span` (the segment-memory span).  D in {64, 128}.
- * Replaces VAULTv3Attention.step's SDPA / explicit biased softmax (src/vault_v3_model.py:1098-1136)
- * and attn_run (runtime/vault3.c:1958-2032). */
-int vgx_attn_decode(int kv_dtype, const float *q, const vgx_kv_span *spans, int n_spans, const float *bias,
-                    int64_t bias_hstride, int bias_span, float *out, int64_t B, int64_t H, int64_t G, int64_t D,
-                    float scale, void *workspace, int64_t workspace_bytes, void *stream);
+ * all spans concatenated in order, kv group g = h / (H/G).  q: fp32, head h of batch entry b at
+ * b*ldq + h*D (post-RoPE); out: [B][H][D] fp32.  kv_dtype: VGX_F32 or VGX_BF16.  n_spans <= 4.
+ * bias (may be NULL) is fp32 [H][bias_hstride], added to the keys of span `bias_span` (the
+ * segment-memory span).  causal_base >= 0 makes the last span causal: batch entry b sees only its
+ * first causal_base + b + 1 keys (chunked prefill, one query per entry); -1 disables it.
+ * D in {64, 128}.
+ * Replaces VAULTv3Attention.step's SDPA / explicit biased softmax (src/vault_v3_model.py:1098-1136),
+ * the chunk attention of _forward_chunk_recurrent (:2064-2093) and attn_run (runtime/vault3.c:1958-2032). */
+int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span *spans, int n_spans,
+                    const float *bias, int64_t bias_hstride, int bias_span, int64_t causal_base, float *out, int64_t B,
+                    int64_t H, int64_t G, int64_t D, float scale, void *workspace, int64_t workspace_bytes,
+                    void *stream);
 
 /* ---------------------------------------------------------------- small fused ops -------------- */
 
@@ -130,15 +134,17 @@ int vgx_rmsnorm(const float *x, int64_t ldx, const float *w, float *y, int64_t l
                 float eps, void *stream);
 
 /* RoPE + KV-cache write for N tokens (decode: one token per sequence; prefill: a run of tokens).
- * q [N][H][D] fp32 is rotated in place; k [N][G][D] is rotated into k_rot (if non-NULL) and copied
- * raw into k_raw (if non-NULL); v [N][G][D] is copied into v_dst.  Destination row of token t,
+ * q (token t, head h at t*ldq + h*D; fp32) is rotated in place (q may be NULL when H = 0);
+ * k (t*ldk + g*D) is rotated into k_rot (if non-NULL) and copied raw into k_raw (if non-NULL);
+ * v (t*ldv + g*D) is copied into v_dst.  Destination row of token t,
  * group g: t*dst_tstride + g*dst_gstride (elements, KV dtype).  The first n_sink tokens are also
  * copied raw into sink_k_raw / sink_v at t*sink_tstride + g*sink_gstride.  table: fp32 rows
  * [cos(D/2) | sin(D/2)]; token t uses row table + t*table_rstride.
  * Replaces the ring write + RoPE of src/vault_v3_model.py:1079-1094, 2049-2058 and
  * runtime/vault3.c:2162-2179. */
-int vgx_rope_qkv_write(int kv_dtype, float *q, const float *k, const float *v, int64_t N, int64_t H, int64_t G,
-                       int64_t D, const float *table, int64_t table_rstride, void *k_rot, void *k_raw, void *v_dst,
+int vgx_rope_qkv_write(int kv_dtype, float *q, int64_t ldq, const float *k, int64_t ldk, const float *v, int64_t ldv,
+                       int64_t N, int64_t H, int64_t G, int64_t D, const float *table, int64_t table_rstride,
+                       void *k_rot, void *k_raw, void *v_dst,
                        int64_t dst_tstride, int64_t dst_gstride, void *sink_k_raw, void *sink_v, int64_t n_sink,
                        int64_t sink_tstride, int64_t sink_gstride, void *stream);
 
@@ -156,6 +162,26 @@ int vgx_rope_rotate(int kv_dtype, const void *src, void *dst, int64_t n_outer, i
  * (src/vault_v3_model.py:1914-1920; runtime/vault3.c:1892-1913). */
 int vgx_gather_rows(int dtype, const void *src, void *dst, const int32_t *idx, int64_t n_idx, int64_t src_rows,
                     int64_t n_outer, int64_t src_ostride, int64_t dst_ostride, int64_t D, void *stream);
+
+/* ---------------------------------------------------------------- segment-memory scorer -------- */
+
+/* Causal EMA habituation of scorer features over T tokens (rows t*ldf of f, fd features each):
+ * hab[t] = f[t] - 0.65 e, then e = 0.985 e + 0.015 f[t]; e starts from ema (or f[0] when first != 0,
+ * which also skips the first update) and is stored back into ema.
+ * Replaces _score_chunk_habituated (src/vault_v3_model.py:1224-1247) and the EMA of step (:2299-2304). */
+int vgx_ema_habituate(const float *f, int64_t ldf, float *hab, int64_t ldh, float *ema, int64_t T, int64_t fd,
+                      int first, void *stream);
+
+/* LayerNorm rows: y = (x - mean) / sqrt(var + eps) * w + b (biased variance).
+ * Replaces the scorer LayerNorm (src/vault_v3_model.py:879-880; runtime/vault3.c:963-971). */
+int vgx_layernorm(const float *x, int64_t ldx, const float *w, const float *b, float *y, int64_t ldy, int64_t n_rows,
+                  int64_t dim, float eps, void *stream);
+
+/* Scorer tail for T tokens: h holds 2T rows of fc1 outputs (rows 0..T-1 raw features, T..2T-1
+ * habituated).  out[t] = raw_t + 0.35 max(0, hab_t - raw_t), raw_t/hab_t = gelu_erf(h) . w2 + b2[0];
+ * out[0] = raw_0 when first != 0.  Replaces src/vault_v3_model.py:881-883, 1238-1246, 2295-2305. */
+int vgx_seg_score_tail(const float *h, int64_t ldh, const float *w2, const float *b2, int64_t hidden, int64_t T,
+                       int first, float *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -63,12 +63,23 @@ class OState:
     ema: Optional[np.ndarray] = None
 
 
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """float -> fp32 -> bf16 (round to nearest even) -> float64."""
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
 class OracleModel:
-    def __init__(self, cfg, weights: Dict[str, np.ndarray], table=orope.table_c):
+    """kv="bf16" stores every cached key/value rounded to bf16 (the model's bf16 KV cache: keys are
+    rotated in fp32 and rounded on store, raw keys and values rounded on store)."""
+
+    def __init__(self, cfg, weights: Dict[str, np.ndarray], table=orope.table_c, kv: str = "fp32"):
         self.cfg = cfg
         self.w = {k: np.asarray(v, dtype=np.float64) for k, v in weights.items()}
         self.table = table
         self.has_scorer = cfg.has_seg_scorer and "seg_scorer.ln.weight" in weights
+        self._kv = bf16_round if kv == "bf16" else (lambda a: np.asarray(a, dtype=np.float64))
 
     # ------------------------------------------------------------------ state
     def new_state(self, seg_budget: Optional[int] = None) -> OState:
@@ -194,7 +205,7 @@ class OracleModel:
         st.kraw_prev, st.kraw_cur = st.kraw_cur.copy(), st.kraw_prev
         if pos >= 2 * W:
             cs, sn = self._cs([-W])
-            st.k_prev = orope.rotate(st.k_prev, cs, sn)
+            st.k_prev = self._kv(orope.rotate(st.k_prev, cs, sn))
         st.tok_prev, st.tok_cur = st.tok_cur.copy(), st.tok_prev
         st.sc_prev, st.sc_cur = st.sc_cur.copy(), st.sc_prev
         st.seg_prev, st.seg_cur = st.seg_cur.copy(), st.seg_prev
@@ -209,10 +220,10 @@ class OracleModel:
         S = st.n_pin
         if M:
             cs, sn = self._cs(np.arange(-M, 0))
-            st.k_seg_rot[:, :, :M] = orope.rotate(st.k_seg_raw[:, :, :M], cs, sn)
+            st.k_seg_rot[:, :, :M] = self._kv(orope.rotate(st.k_seg_raw[:, :, :M], cs, sn))
         if S:
             cs, sn = self._cs(np.arange(-(M + S), -M))
-            st.k_sink_rot[:, :, :S] = orope.rotate(st.k_sink_raw[:, :, :S], cs, sn)
+            st.k_sink_rot[:, :, :S] = self._kv(orope.rotate(st.k_sink_raw[:, :, :S], cs, sn))
 
     # ------------------------------------------------------------------ step
     def step(self, tok: int, st: OState) -> np.ndarray:
@@ -249,12 +260,12 @@ class OracleModel:
             v = (w[p + "self_attn.v_proj.weight"] @ u + w[p + "self_attn.v_proj.bias"]).reshape(G, D)
             qr = orope.rotate(q, cs, sn)
             kr = orope.rotate(k, cs, sn)
-            st.k_cur[li, :, cc] = kr
-            st.v_cur[li, :, cc] = v
-            st.kraw_cur[li, :, cc] = k
+            st.k_cur[li, :, cc] = self._kv(kr)
+            st.v_cur[li, :, cc] = self._kv(v)
+            st.kraw_cur[li, :, cc] = self._kv(k)
             if pos < S_cap:
-                st.k_sink_raw[li, :, pos] = k
-                st.v_sink[li, :, pos] = v
+                st.k_sink_raw[li, :, pos] = self._kv(k)
+                st.v_sink[li, :, pos] = self._kv(v)
             parts_k, parts_v = [], []
             if pos >= 2 * W:
                 S = st.n_pin

@@ -38,11 +38,15 @@ _SIGS = {
     "vgx_qlinear": (I32, [I32, P, I64, I64, P, I64, I64, P, P, I64, I32, P]),
     "vgx_qlinear_swiglu": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
     "vgx_attn_decode_workspace_bytes": (I64, [I64, I64, I64, I64, I64]),
-    "vgx_attn_decode": (I32, [I32, P, P, I32, P, I64, I32, P, I64, I64, I64, I64, F, P, I64, P]),
+    "vgx_attn_decode": (I32, [I32, P, I64, P, I32, P, I64, I32, I64, P, I64, I64, I64, I64, F, P, I64, P]),
     "vgx_rmsnorm": (I32, [P, I64, P, P, I64, I64, I64, F, P]),
-    "vgx_rope_qkv_write": (I32, [I32, P, P, P, I64, I64, I64, I64, P, I64, P, P, P, I64, I64, P, P, I64, I64, I64, P]),
+    "vgx_rope_qkv_write": (I32, [I32, P, I64, P, I64, P, I64, I64, I64, I64, I64, P, I64, P, P, P, I64, I64, P, P, I64,
+                                 I64, I64, P]),
     "vgx_rope_rotate": (I32, [I32, P, P, I64, I64, I64, I64, I64, P, I64, P]),
     "vgx_gather_rows": (I32, [I32, P, P, P, I64, I64, I64, I64, I64, I64, P]),
+    "vgx_ema_habituate": (I32, [P, I64, P, I64, P, I64, I64, I32, P]),
+    "vgx_layernorm": (I32, [P, I64, P, P, P, I64, I64, I64, F, P]),
+    "vgx_seg_score_tail": (I32, [P, I64, P, P, I64, I64, I32, P, P]),
 }
 
 

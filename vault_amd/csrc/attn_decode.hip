@@ -65,11 +65,12 @@ __device__ __forceinline__ void load_chunk(const void *base, int64_t elem_off, f
 }
 
 template <int KV, int GRP, int DPL>
-__global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict__ q, SpanArgs sp,
+__global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict__ q, int64_t ldq, SpanArgs sp,
                                                           const float *__restrict__ bias, int64_t bias_hstride,
                                                           int bias_span, float *__restrict__ out,
                                                           float *__restrict__ ws, int H, int G, float scale,
-                                                          int64_t n_tot, int64_t kps, int n_splits) {
+                                                          int64_t n_tot, int64_t kps, int n_splits,
+                                                          int64_t causal_base) {
     constexpr int D = DPL * 16;
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x, l16 = lane & 15, row = lane >> 4;
@@ -77,7 +78,7 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict
     float qr[GRP][DPL];
 #pragma unroll
     for (int hh = 0; hh < GRP; ++hh) {
-        const float *qp = q + ((int64_t)b * H + (int64_t)g * GRP + hh) * D + l16 * DPL;
+        const float *qp = q + (int64_t)b * ldq + ((int64_t)g * GRP + hh) * D + l16 * DPL;
 #pragma unroll
         for (int d = 0; d < DPL; ++d) qr[hh][d] = qp[d] * scale;
     }
@@ -94,8 +95,11 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict
     const int64_t k1 = min(n_tot, k0 + kps);
     int64_t base = 0;
     for (int s = 0; s < sp.n; ++s) {
-        const int64_t len = sp.len[s];
-        const int64_t lo = max(k0, base) - base, hi = min(k1, base + len) - base;
+        int64_t len = sp.len[s];
+        const int64_t lo = max(k0, base) - base;
+        int64_t hi = min(k1, base + len) - base;
+        // Causal last span: batch entry b sees its first causal_base + b + 1 keys.
+        if (causal_base >= 0 && s == sp.n - 1) hi = min(hi, causal_base + (int64_t)b + 1);
         base += len;
         if (lo >= hi) continue;
         const int64_t off = (int64_t)b * sp.bstride[s] + (int64_t)g * sp.gstride[s] + l16 * DPL;
@@ -235,33 +239,34 @@ int choose_splits(int64_t B, int64_t G, int64_t n_tot, int64_t *kps) {
 }
 
 template <int KV, int GRP, int DPL>
-void launch_decode(dim3 grid, hipStream_t st, const float *q, const SpanArgs &sp, const float *bias, int64_t bhs,
-                   int bspan, float *out, float *ws, int H, int G, float scale, int64_t n_tot, int64_t kps, int ns) {
-    hipLaunchKernelGGL((attn_decode_kernel<KV, GRP, DPL>), grid, dim3(64), 0, st, q, sp, bias, bhs, bspan, out, ws,
-                       H, G, scale, n_tot, kps, ns);
+void launch_decode(dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp, const float *bias,
+                   int64_t bhs, int bspan, float *out, float *ws, int H, int G, float scale, int64_t n_tot, int64_t kps,
+                   int ns, int64_t cb) {
+    hipLaunchKernelGGL((attn_decode_kernel<KV, GRP, DPL>), grid, dim3(64), 0, st, q, ldq, sp, bias, bhs, bspan, out,
+                       ws, H, G, scale, n_tot, kps, ns, cb);
 }
 
 template <int KV, int GRP>
-bool dispatch_dpl(int D, dim3 grid, hipStream_t st, const float *q, const SpanArgs &sp, const float *bias,
-                  int64_t bhs, int bspan, float *out, float *ws, int H, int G, float scale, int64_t n_tot,
-                  int64_t kps, int ns) {
+bool dispatch_dpl(int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp,
+                  const float *bias, int64_t bhs, int bspan, float *out, float *ws, int H, int G, float scale,
+                  int64_t n_tot, int64_t kps, int ns, int64_t cb) {
     switch (D) {
-        case 64: launch_decode<KV, GRP, 4>(grid, st, q, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns); return true;
-        case 128: launch_decode<KV, GRP, 8>(grid, st, q, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns); return true;
+        case 64: launch_decode<KV, GRP, 4>(grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb); return true;
+        case 128: launch_decode<KV, GRP, 8>(grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb); return true;
     }
     return false;
 }
 
 template <int KV>
-bool dispatch_grp(int grp, int D, dim3 grid, hipStream_t st, const float *q, const SpanArgs &sp, const float *bias,
-                  int64_t bhs, int bspan, float *out, float *ws, int H, int G, float scale, int64_t n_tot,
-                  int64_t kps, int ns) {
+bool dispatch_grp(int grp, int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp,
+                  const float *bias, int64_t bhs, int bspan, float *out, float *ws, int H, int G, float scale,
+                  int64_t n_tot, int64_t kps, int ns, int64_t cb) {
     switch (grp) {
-        case 1: return dispatch_dpl<KV, 1>(D, grid, st, q, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns);
-        case 2: return dispatch_dpl<KV, 2>(D, grid, st, q, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns);
-        case 4: return dispatch_dpl<KV, 4>(D, grid, st, q, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns);
-        case 6: return dispatch_dpl<KV, 6>(D, grid, st, q, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns);
-        case 8: return dispatch_dpl<KV, 8>(D, grid, st, q, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns);
+        case 1: return dispatch_dpl<KV, 1>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb);
+        case 2: return dispatch_dpl<KV, 2>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb);
+        case 4: return dispatch_dpl<KV, 4>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb);
+        case 6: return dispatch_dpl<KV, 6>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb);
+        case 8: return dispatch_dpl<KV, 8>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb);
     }
     return false;
 }
@@ -278,9 +283,10 @@ int64_t vgx_attn_decode_workspace_bytes(int64_t B, int64_t H, int64_t G, int64_t
     return B * H * (int64_t)ns * (D + 2) * (int64_t)sizeof(float);
 }
 
-int vgx_attn_decode(int kv_dtype, const float *q, const vgx_kv_span *spans, int n_spans, const float *bias,
-                    int64_t bias_hstride, int bias_span, float *out, int64_t B, int64_t H, int64_t G, int64_t D,
-                    float scale, void *workspace, int64_t workspace_bytes, void *stream) {
+int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span *spans, int n_spans,
+                    const float *bias, int64_t bias_hstride, int bias_span, int64_t causal_base, float *out, int64_t B,
+                    int64_t H, int64_t G, int64_t D, float scale, void *workspace, int64_t workspace_bytes,
+                    void *stream) {
     if (kv_dtype != VGX_F32 && kv_dtype != VGX_BF16) return VGX_E_DTYPE;
     if (!q || !spans || !out) return VGX_E_ARG;
     if (n_spans < 1 || n_spans > 4) return VGX_E_LIMIT;
@@ -288,6 +294,7 @@ int vgx_attn_decode(int kv_dtype, const float *q, const vgx_kv_span *spans, int 
     if (D != 64 && D != 128) return VGX_E_LIMIT;
     if (B > 65535 || G > 65535) return VGX_E_LIMIT;
     if (bias && (bias_span < 0 || bias_span >= n_spans)) return VGX_E_ARG;
+    if (ldq < H * D) return VGX_E_SIZE;
     SpanArgs sp{};
     sp.n = n_spans;
     int64_t n_tot = 0;
@@ -317,10 +324,10 @@ int vgx_attn_decode(int kv_dtype, const float *q, const vgx_kv_span *spans, int 
     dim3 grid((unsigned)ns, (unsigned)G, (unsigned)B);
     float *ws = static_cast<float *>(workspace);
     bool ok = kv_dtype == VGX_F32
-                  ? dispatch_grp<VGX_F32>(grp, (int)D, grid, st, q, sp, bias, bias_hstride, bias_span, out, ws, (int)H,
-                                          (int)G, scale, n_tot, kps, ns)
-                  : dispatch_grp<VGX_BF16>(grp, (int)D, grid, st, q, sp, bias, bias_hstride, bias_span, out, ws,
-                                           (int)H, (int)G, scale, n_tot, kps, ns);
+                  ? dispatch_grp<VGX_F32>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out, ws,
+                                          (int)H, (int)G, scale, n_tot, kps, ns, causal_base)
+                  : dispatch_grp<VGX_BF16>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out, ws,
+                                           (int)H, (int)G, scale, n_tot, kps, ns, causal_base);
     if (!ok) return VGX_E_LIMIT;
     VGX_CHECK_LAUNCH();
     if (ns > 1) {

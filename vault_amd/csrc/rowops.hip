@@ -44,8 +44,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ 
 
 // grid.x = N tokens, grid.y = H + G heads; threads over D/2 rotation pairs.
 template <int KV>
-__global__ void rope_qkv_write_kernel(float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
-                                      int H, int G, int D, const float *__restrict__ table, int64_t trs,
+__global__ void rope_qkv_write_kernel(float *__restrict__ q, int64_t ldq, const float *__restrict__ k, int64_t ldk,
+                                      const float *__restrict__ v, int64_t ldv, int H, int G, int D,
+                                      const float *__restrict__ table, int64_t trs,
                                       void *k_rot, void *k_raw, void *v_dst, int64_t dts, int64_t dgs, void *sk,
                                       void *sv, int64_t n_sink, int64_t sts, int64_t sgs) {
     const int64_t t = blockIdx.x;
@@ -55,14 +56,14 @@ __global__ void rope_qkv_write_kernel(float *__restrict__ q, const float *__rest
     for (int i = threadIdx.x; i < h2; i += blockDim.x) {
         const float c = cs[i], s = cs[h2 + i];
         if (hd < H) {
-            float *qp = q + (t * H + hd) * D;
+            float *qp = q + t * ldq + (int64_t)hd * D;
             const float a = qp[i], b = qp[i + h2];
             qp[i] = a * c - b * s;
             qp[i + h2] = b * c + a * s;
         } else {
             const int g = hd - H;
-            const float *kp = k + (t * G + g) * D;
-            const float *vp = v + (t * G + g) * D;
+            const float *kp = k + t * ldk + (int64_t)g * D;
+            const float *vp = v + t * ldv + (int64_t)g * D;
             const float a = kp[i], b = kp[i + h2];
             const int64_t o = t * dts + g * dgs;
             if (k_rot) {
@@ -137,8 +138,9 @@ int vgx_rmsnorm(const float *x, int64_t ldx, const float *w, float *y, int64_t l
     return VGX_OK;
 }
 
-int vgx_rope_qkv_write(int kv_dtype, float *q, const float *k, const float *v, int64_t N, int64_t H, int64_t G,
-                       int64_t D, const float *table, int64_t table_rstride, void *k_rot, void *k_raw, void *v_dst,
+int vgx_rope_qkv_write(int kv_dtype, float *q, int64_t ldq, const float *k, int64_t ldk, const float *v, int64_t ldv,
+                       int64_t N, int64_t H, int64_t G, int64_t D, const float *table, int64_t table_rstride,
+                       void *k_rot, void *k_raw, void *v_dst,
                        int64_t dst_tstride, int64_t dst_gstride, void *sink_k_raw, void *sink_v, int64_t n_sink,
                        int64_t sink_tstride, int64_t sink_gstride, void *stream) {
     if (kv_dtype != VGX_F32 && kv_dtype != VGX_BF16) return VGX_E_DTYPE;
@@ -146,17 +148,18 @@ int vgx_rope_qkv_write(int kv_dtype, float *q, const float *k, const float *v, i
     if (H > 0 && !q) return VGX_E_ARG;
     if (n_sink > 0 && (!sink_k_raw || !sink_v)) return VGX_E_ARG;
     if (N < 0 || H < 0 || G <= 0 || D <= 0 || (D & 1) || n_sink < 0 || n_sink > N) return VGX_E_SIZE;
+    if ((H > 0 && ldq < H * D) || ldk < G * D || ldv < G * D) return VGX_E_SIZE;
     if (N == 0) return VGX_OK;
     if (N > 0x7FFFFFFF || H + G > 65535) return VGX_E_LIMIT;
     dim3 grid((unsigned)N, (unsigned)(H + G));
     const int thr = (int)std::min<int64_t>(256, std::max<int64_t>(32, D / 2));
     hipStream_t st = (hipStream_t)stream;
     if (kv_dtype == VGX_F32)
-        hipLaunchKernelGGL(rope_qkv_write_kernel<VGX_F32>, grid, dim3(thr), 0, st, q, k, v, (int)H, (int)G, (int)D,
+        hipLaunchKernelGGL(rope_qkv_write_kernel<VGX_F32>, grid, dim3(thr), 0, st, q, ldq, k, ldk, v, ldv, (int)H, (int)G, (int)D,
                            table, table_rstride, k_rot, k_raw, v_dst, dst_tstride, dst_gstride, sink_k_raw, sink_v,
                            n_sink, sink_tstride, sink_gstride);
     else
-        hipLaunchKernelGGL(rope_qkv_write_kernel<VGX_BF16>, grid, dim3(thr), 0, st, q, k, v, (int)H, (int)G, (int)D,
+        hipLaunchKernelGGL(rope_qkv_write_kernel<VGX_BF16>, grid, dim3(thr), 0, st, q, ldq, k, ldk, v, ldv, (int)H, (int)G, (int)D,
                            table, table_rstride, k_rot, k_raw, v_dst, dst_tstride, dst_gstride, sink_k_raw, sink_v,
                            n_sink, sink_tstride, sink_gstride);
     VGX_CHECK_LAUNCH();

@@ -1,0 +1,116 @@
+// Segment-memory scorer on the device: causal EMA habituation of the scorer features, LayerNorm,
+// and the GELU . fc2 tail with the habituated-score combine.
+//
+// Reference semantics: src/vault_v3_model.py:870-883 (SegmentScorer: LayerNorm eps 1e-5 ->
+// Linear -> exact-erf GELU -> Linear), :1224-1247 (_score_chunk_habituated) and :2294-2305 (step);
+// runtime/vault3.c:961-977, 2201-2216.  Per token t with features f_t and EMA state e:
+//   hab_in_t = f_t - 0.65 e_{t-1};  e_t = 0.985 e_{t-1} + 0.015 f_t   (e_0 = f_0 on the first token)
+//   score_t  = raw_t + 0.35 max(0, hab_t - raw_t)                     (score_0 = raw_0 on the first)
+// The fc1 GEMV between LayerNorm and the tail runs through vgx_qlinear (F32 weights).
+#include "common.h"
+
+using namespace vgx;
+
+namespace {
+
+// One thread per feature; scans the T tokens in order.
+__global__ void ema_habituate_kernel(const float *__restrict__ f, int64_t ldf, float *__restrict__ hab,
+                                     int64_t ldh, float *__restrict__ ema, int64_t T, int64_t fd, int first) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= fd) return;
+    float e = first ? f[i] : ema[i];
+    for (int64_t t = 0; t < T; ++t) {
+        const float ft = f[t * ldf + i];
+        hab[t * ldh + i] = ft - 0.65f * e;
+        if (!(first && t == 0)) e = 0.985f * e + 0.015f * ft;
+    }
+    ema[i] = e;
+}
+
+__global__ __launch_bounds__(256) void layernorm_kernel(const float *__restrict__ x, int64_t ldx,
+                                                         const float *__restrict__ w, const float *__restrict__ b,
+                                                         float *__restrict__ y, int64_t ldy, int64_t dim, float eps) {
+    __shared__ float red[4];
+    __shared__ float stat[2];
+    const float *xr = x + (int64_t)blockIdx.x * ldx;
+    float s = 0.0f;
+    for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) s += xr[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) stat[0] = (red[0] + red[1] + red[2] + red[3]) / (float)dim;
+    __syncthreads();
+    const float mean = stat[0];
+    float v = 0.0f;
+    for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) {
+        const float d = xr[i] - mean;
+        v = fmaf(d, d, v);
+    }
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) stat[1] = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)dim + eps);
+    __syncthreads();
+    const float inv = stat[1];
+    float *yr = y + (int64_t)blockIdx.x * ldy;
+    for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) yr[i] = (xr[i] - mean) * inv * w[i] + b[i];
+}
+
+// One wave per token t: raw = gelu(h[t]) . w2 + b2, hab = gelu(h[T + t]) . w2 + b2.
+__global__ __launch_bounds__(64) void score_tail_kernel(const float *__restrict__ h, int64_t ldh,
+                                                         const float *__restrict__ w2, const float *__restrict__ b2,
+                                                         int64_t hidden, int64_t T, int first,
+                                                         float *__restrict__ out) {
+    const int64_t t = blockIdx.x;
+    float r = 0.0f, a = 0.0f;
+    for (int64_t i = threadIdx.x; i < hidden; i += 64) {
+        const float x0 = h[t * ldh + i], x1 = h[(T + t) * ldh + i];
+        r = fmaf(0.5f * x0 * (1.0f + erff(x0 * 0.70710678118654752f)), w2[i], r);
+        a = fmaf(0.5f * x1 * (1.0f + erff(x1 * 0.70710678118654752f)), w2[i], a);
+    }
+    r = wave_sum(r) + b2[0];
+    a = wave_sum(a) + b2[0];
+    if (threadIdx.x == 0) out[t] = (first && t == 0) ? r : r + 0.35f * fmaxf(0.0f, a - r);
+}
+
+}  // namespace
+
+extern "C" {
+
+int vgx_ema_habituate(const float *f, int64_t ldf, float *hab, int64_t ldh, float *ema, int64_t T, int64_t fd,
+                      int first, void *stream) {
+    if (!f || !hab || !ema) return VGX_E_ARG;
+    if (T < 0 || fd <= 0 || ldf < fd || ldh < fd) return VGX_E_SIZE;
+    if (T == 0) return VGX_OK;
+    hipLaunchKernelGGL(ema_habituate_kernel, dim3((unsigned)((fd + 255) / 256)), dim3(256), 0, (hipStream_t)stream, f,
+                       ldf, hab, ldh, ema, T, fd, first ? 1 : 0);
+    VGX_CHECK_LAUNCH();
+    return VGX_OK;
+}
+
+int vgx_layernorm(const float *x, int64_t ldx, const float *w, const float *b, float *y, int64_t ldy, int64_t n_rows,
+                  int64_t dim, float eps, void *stream) {
+    if (!x || !w || !b || !y) return VGX_E_ARG;
+    if (n_rows < 0 || dim <= 0 || ldx < dim || ldy < dim || !(eps > 0.0f)) return VGX_E_SIZE;
+    if (n_rows == 0) return VGX_OK;
+    if (n_rows > 0x7FFFFFFF) return VGX_E_LIMIT;
+    hipLaunchKernelGGL(layernorm_kernel, dim3((unsigned)n_rows), dim3(256), 0, (hipStream_t)stream, x, ldx, w, b, y,
+                       ldy, dim, eps);
+    VGX_CHECK_LAUNCH();
+    return VGX_OK;
+}
+
+int vgx_seg_score_tail(const float *h, int64_t ldh, const float *w2, const float *b2, int64_t hidden, int64_t T,
+                       int first, float *out, void *stream) {
+    if (!h || !w2 || !b2 || !out) return VGX_E_ARG;
+    if (T < 0 || hidden <= 0 || ldh < hidden) return VGX_E_SIZE;
+    if (T == 0) return VGX_OK;
+    if (T > 0x7FFFFFFF) return VGX_E_LIMIT;
+    hipLaunchKernelGGL(score_tail_kernel, dim3((unsigned)T), dim3(64), 0, (hipStream_t)stream, h, ldh, w2, b2, hidden,
+                       T, first ? 1 : 0, out);
+    VGX_CHECK_LAUNCH();
+    return VGX_OK;
+}
+
+}  // extern "C"

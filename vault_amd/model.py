@@ -1,0 +1,497 @@
+"""Drop-in VAULT v3 streaming model over the libvault_amd kernels.
+
+Mirrors ``VAULTv3ForCausalLM`` / ``VAULTv3State`` of src/vault_v3_model.py (new_state :2159,
+prefill :2163-2212, step :2214-2311, forward :2153) with the same argument meaning and state
+fields; every projection, attention, RoPE, norm, KV-cache write, chunk-boundary re-base/re-rotation,
+segment-bank compaction and scorer op is a call into the HIP library.  Host-side control stays in
+Python as in the reference: the auto-pin FSM, segment-id bookkeeping, and the top-B eviction merge
+(on at most budget + W candidates once per W tokens).
+
+Offline configuration: there is no tokenizer, so every token's segment-break tier is 0 (segments
+close at seg_max or at the chunk end), there are no shingles, and resonance biases and spoof
+quarantine are inert, exactly as the reference behaves without a tokenizer.  A caller-supplied
+per-head bias (``st.seg_head_bias``, ``st.seg_bias_active``) is honoured by the attention kernel.
+
+Differences by design:
+* The KV caches of all layers are single tensors [n_layers, B, G, n, D]; prev/cur are swapped by
+  reference at chunk boundaries instead of copied (the reference copies cur into prev; the old cur
+  content is never read before being overwritten).
+* RoPE uses one device table of fp32 cos/sin rows computed from double-precision angles, as the C
+  runtime does (runtime/vault3.c:840-849, 2126-2133).
+* prefill() with batch > 1 and forward() with batch > 1 run the streaming step token by token (the
+  reference asserts these equal its parallel block-sliding forms, tests/test_vault_v3.py:52-90).
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, List, Optional, Tuple
+
+import numpy as np
+import torch
+
+from . import ops
+from .config import VAULTv3Config
+from .weights import ModelWeights
+
+V3_MAX_SINK = 512
+
+
+def sink_capacity(cfg: VAULTv3Config) -> int:
+    """Sink slots (runtime/vault3.c:706-710): min(W, 512), at least n_sink, at least 1."""
+    return max(1, min(cfg.window, V3_MAX_SINK), cfg.n_sink)
+
+
+class LayerView:
+    """Per-layer views of the stacked caches, with the reference's LayerState field names."""
+
+    _FIELDS = ("k_prev", "k_cur", "v_prev", "v_cur", "kraw_prev", "kraw_cur", "k_sink_raw", "k_sink_rot",
+               "v_sink", "k_seg_raw", "k_seg_rot", "v_seg")
+
+    def __init__(self, st: "VAULTv3State", li: int):
+        self._st, self._li = st, li
+
+    def __getattr__(self, name):
+        if name in LayerView._FIELDS:
+            return getattr(self._st, name)[self._li]
+        raise AttributeError(name)
+
+
+class VAULTv3State:
+    def __init__(self, cfg: VAULTv3Config, batch: int, device, kv_dtype=torch.float32, seg_budget: Optional[int] = None):
+        self.cfg = cfg
+        self.batch = batch
+        self.device = torch.device(device)
+        self.kv_dtype = kv_dtype
+        self.pos = 0
+        self.seg_budget = cfg.seg_budget if seg_budget is None else int(seg_budget)
+        self.sink_cap = sink_capacity(cfg)
+        self.n_pin = min(cfg.n_sink, cfg.window, self.sink_cap)
+        self.pin_locked = not cfg.auto_pin_system
+        self.saw_im_start = False
+        self.awaiting_sys_nl = False
+        W, G, D, L = cfg.window, cfg.n_kv_heads, cfg.head_dim, cfg.n_layers
+        M_cap = max(1, self.seg_budget)
+        z = lambda n: torch.zeros(L, batch, G, n, D, dtype=kv_dtype, device=self.device)
+        self.k_prev, self.k_cur, self.v_prev, self.v_cur = z(W), z(W), z(W), z(W)
+        self.kraw_prev, self.kraw_cur = z(W), z(W)
+        self.k_sink_raw, self.k_sink_rot, self.v_sink = z(self.sink_cap), z(self.sink_cap), z(self.sink_cap)
+        self.k_seg_raw, self.k_seg_rot, self.v_seg = z(M_cap), z(M_cap), z(M_cap)
+        self._seg_tmp_k, self._seg_tmp_v = z(M_cap), z(M_cap)
+        # segment memory bookkeeping (batch 1)
+        self.tok_prev = np.zeros((batch, W), dtype=np.int64)
+        self.tok_cur = np.zeros((batch, W), dtype=np.int64)
+        self.seg_prev_ids = np.zeros((batch, W), dtype=np.int64)
+        self.seg_cur_ids = np.zeros((batch, W), dtype=np.int64)
+        self.sc_prev = torch.zeros(W, dtype=torch.float32, device=self.device)
+        self.sc_cur = torch.zeros(W, dtype=torch.float32, device=self.device)
+        self.seg_id_offset = 0
+        self.cur_seg_id = 0
+        self.seg_len = 0
+        self.mem_pos = torch.empty(0, dtype=torch.long)
+        self.mem_score = torch.empty(0, dtype=torch.float32)
+        self.mem_tok = torch.empty(0, dtype=torch.long)
+        self.mem_seg = torch.empty(0, dtype=torch.long)
+        fd = max(1, len(cfg.seg_layers) * cfg.d_model)
+        self.ema_ready = False
+        self.seg_feat_ema = torch.zeros(fd, dtype=torch.float32, device=self.device)
+        self.seg_bias_mode = 0
+        self.seg_bias_active = False
+        self.seg_head_bias: Optional[torch.Tensor] = None
+        self.seg_head_bias_hop1: Optional[torch.Tensor] = None
+        self.layers = [LayerView(self, li) for li in range(L)]
+
+    def set_pinned(self, n_pin: int) -> None:
+        cap = min(self.cfg.window, self.sink_cap)
+        self.n_pin = max(0, min(int(n_pin), cap))
+        self.pin_locked = True
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (
+            self.k_prev, self.k_cur, self.v_prev, self.v_cur, self.kraw_prev, self.kraw_cur, self.k_sink_raw,
+            self.k_sink_rot, self.v_sink, self.k_seg_raw, self.k_seg_rot, self.v_seg))
+
+
+class VAULTv3ForCausalLM:
+    def __init__(self, weights: ModelWeights, kv_dtype: torch.dtype = torch.float32):
+        self.w = weights
+        self.cfg = weights.cfg
+        self.device = weights.device
+        self.kv_dtype = kv_dtype
+        self.ws = ops.Workspace(self.device)
+        self._table = None
+        self._p0 = 0
+        self._ensure_table(sink_capacity(self.cfg) + max(1, self.cfg.seg_budget))
+
+    # ------------------------------------------------------------------ RoPE table
+    def _ensure_table(self, neg: int) -> None:
+        """Rows for positions [-neg, 2W): [cos(D/2) | sin(D/2)] fp32 from double-precision angles of a
+        fp32 inverse frequency (runtime/vault3.c:840-849)."""
+        c = self.cfg
+        neg = max(neg, c.window)
+        if self._table is not None and -self._p0 >= neg:
+            return
+        D = c.head_dim
+        i = np.arange(D // 2, dtype=np.float64)
+        inv = (1.0 / np.exp(np.log(np.float64(np.float32(c.rope_theta))) * (2.0 * i) / D)).astype(np.float32)
+        pos = np.arange(-neg, 2 * c.window, dtype=np.float64)
+        ang = pos[:, None] * inv.astype(np.float64)[None, :]
+        tab = np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
+        self._table = torch.from_numpy(tab).to(self.device)
+        self._p0 = -neg
+
+    def _rows(self, p: int) -> torch.Tensor:
+        """Table rows starting at position p."""
+        return self._table[p - self._p0:]
+
+    # ------------------------------------------------------------------ API
+    def new_state(self, batch: int = 1, seg_budget: Optional[int] = None) -> VAULTv3State:
+        st = VAULTv3State(self.cfg, batch, self.device, self.kv_dtype, seg_budget=seg_budget)
+        self._ensure_table(st.sink_cap + max(1, st.seg_budget))
+        return st
+
+    def _seg_active(self, st: VAULTv3State, batch: int) -> bool:
+        return self.w.scorer is not None and st.seg_budget > 0 and batch == 1
+
+    @torch.no_grad()
+    def step(self, token_ids: torch.Tensor, st: VAULTv3State, vault_on: bool = False) -> torch.Tensor:
+        """token_ids: (B,) -> logits (B, V) fp32 on the device.  Mutates ``st``."""
+        _ = vault_on
+        ids = token_ids.reshape(-1).to("cpu", torch.int64)
+        B = ids.numel()
+        if B != st.batch:
+            raise ValueError("batch size differs from the state's")
+        cfg = self.cfg
+        W = cfg.window
+        pos = st.pos
+        c = pos % W
+        seg_active = self._seg_active(st, B)
+        if not st.pin_locked and B == 1:
+            self._auto_pin(st, int(ids[0]), pos)
+        if c == 0 and pos > 0:
+            self._boundary(st, seg_active)
+        st.tok_cur[:, c] = ids.numpy()
+        if seg_active:
+            st.seg_cur_ids[0, c] = st.cur_seg_id
+            st.seg_len += 1
+            if c == W - 1 or st.seg_len >= cfg.seg_max:   # break tiers are all 0 without a tokenizer
+                st.cur_seg_id += 1
+                st.seg_len = 0
+        if not seg_active or not (pos >= 2 * W and st.mem_pos.numel() > 0):
+            st.seg_bias_mode = 0
+            st.seg_bias_active = False
+            st.seg_head_bias = None
+            st.seg_head_bias_hop1 = None
+        x = ops.embed(self.w.embed, ids.to(self.device), pad_row=0)            # [B, d]
+        h, feats = self._layers(x, st, ids_q=B, pos=pos, c=c, seg_active=seg_active, chunk=False)
+        if seg_active:
+            self._score(st, feats, T=1, c0=c)
+        st.pos = pos + 1
+        return self._logits(h)
+
+    @torch.no_grad()
+    def prefill(self, input_ids: torch.Tensor, vault_on: bool = False,
+                seg_budget: Optional[int] = None) -> Tuple[torch.Tensor, VAULTv3State]:
+        """Prefill from position 0; returns last-token logits (B, V) and the streaming state."""
+        _ = vault_on
+        B, L = input_ids.shape
+        bud = self.cfg.seg_budget if seg_budget is None else int(seg_budget)
+        if B == 1:
+            h, st = self._chunk_recurrent(input_ids, bud, all_logits=False)
+            return self._logits(h), st
+        st = self.new_state(B, seg_budget=0)
+        st.set_pinned(self.cfg.n_sink)
+        lg = None
+        for t in range(L):
+            lg = self.step(input_ids[:, t], st)
+        return lg, st
+
+    @torch.no_grad()
+    def forward(self, input_ids: torch.Tensor, mode: str = "block", vault_on: bool = False,
+                seg_budget: Optional[int] = None) -> torch.Tensor:
+        """Logits for every position, (B, L, V)."""
+        _ = vault_on
+        B, L = input_ids.shape
+        if mode == "full" and L > 2 * self.cfg.window:
+            raise NotImplementedError("full causal attention beyond 2W is not part of the streaming path")
+        bud = self.cfg.seg_budget if seg_budget is None else int(seg_budget)
+        if B == 1:
+            h, _ = self._chunk_recurrent(input_ids, bud, all_logits=True)
+            return self._logits(h).unsqueeze(0)
+        st = self.new_state(B, seg_budget=0)
+        st.set_pinned(self.cfg.n_sink)
+        return torch.stack([self.step(input_ids[:, t], st) for t in range(L)], dim=1)
+
+    __call__ = forward
+
+    # ------------------------------------------------------------------ host control
+    def _auto_pin(self, st: VAULTv3State, tid: int, pos: int) -> None:
+        """Online ChatML system-prompt pinning (src/vault_v3_model.py:2224-2252)."""
+        cfg = self.cfg
+        limit = min(cfg.max_sink, cfg.window, st.sink_cap)
+        if pos == 0:
+            if tid == cfg.im_start_id and limit >= 2:
+                st.saw_im_start = True
+            else:
+                st.pin_locked = True
+        elif pos == 1 and st.saw_im_start:
+            if tid != cfg.system_tok_id:
+                st.saw_im_start = False
+                st.pin_locked = True
+        elif st.saw_im_start and pos < limit:
+            if st.awaiting_sys_nl:
+                st.n_pin = max(st.n_pin, pos + 1 if tid == 198 else pos)
+                st.pin_locked = True
+                st.awaiting_sys_nl = False
+            elif tid == cfg.im_end_id:
+                st.n_pin = max(st.n_pin, pos + 1)
+                if pos + 1 < limit:
+                    st.awaiting_sys_nl = True
+                else:
+                    st.pin_locked = True
+        elif pos >= limit:
+            if st.saw_im_start and not st.awaiting_sys_nl:
+                st.n_pin = max(st.n_pin, limit)
+            st.pin_locked = True
+            st.awaiting_sys_nl = False
+
+    def _flat(self, t: torch.Tensor) -> torch.Tensor:
+        """[L, B, G, n, D] -> [L*B*G, n, D] view."""
+        return t.view(-1, t.shape[-2], t.shape[-1])
+
+    def _boundary(self, st: VAULTv3State, seg_active: bool) -> None:
+        """Chunk boundary at c == 0, pos > 0 (src/vault_v3_model.py:1858-1935)."""
+        cfg = self.cfg
+        W = cfg.window
+        pos = st.pos
+        if pos >= 2 * W and seg_active and st.seg_budget > 0:
+            self._evict(st, pos // W - 2)
+        st.k_prev, st.k_cur = st.k_cur, st.k_prev
+        st.v_prev, st.v_cur = st.v_cur, st.v_prev
+        st.kraw_prev, st.kraw_cur = st.kraw_cur, st.kraw_prev
+        if pos >= 2 * W:
+            kp = self._flat(st.k_prev)
+            ops.rope_rotate(kp, kp, self._rows(-W), 0)
+        st.tok_prev, st.tok_cur = st.tok_cur, st.tok_prev
+        st.sc_prev, st.sc_cur = st.sc_cur, st.sc_prev
+        st.seg_prev_ids, st.seg_cur_ids = st.seg_cur_ids, st.seg_prev_ids
+        st.cur_seg_id = 0
+        st.seg_len = 0
+        if pos >= 2 * W:
+            self._refresh_prefix(st, seg_active)
+
+    def _refresh_prefix(self, st: VAULTv3State, seg_active: bool) -> None:
+        """Segment keys at positions [-M, 0), sinks at [-(M+S), -M) (src/vault_v3_model.py:1842-1856)."""
+        M = int(st.mem_pos.numel()) if seg_active else 0
+        S = st.n_pin
+        if M > 0:
+            ops.rope_rotate(self._flat(st.k_seg_raw)[:, :M], self._flat(st.k_seg_rot)[:, :M], self._rows(-M),
+                            self.cfg.head_dim)
+        if S > 0:
+            ops.rope_rotate(self._flat(st.k_sink_raw)[:, :S], self._flat(st.k_sink_rot)[:, :S],
+                            self._rows(-(M + S)), self.cfg.head_dim)
+
+    def _evict(self, st: VAULTv3State, ev: int) -> None:
+        """Segment-memory update for the evicted chunk `ev` (src/vault_v3_model.py:1865-1921;
+        runtime/vault3.c:1833-1915): quarantine, per-segment max with the -1e-6 * (seg id mod 16384)
+        tie-break, exact top-B merge ordered by (score desc, position asc), chronological compaction."""
+        W = self.cfg.window
+        sc = st.sc_prev.to("cpu", torch.float32).numpy().copy()
+        seg_ids = st.seg_prev_ids[0]
+        bad = sc <= -1.0e29
+        if bad.any():
+            bad_seg = np.zeros(int(seg_ids.max()) + 1, dtype=bool)
+            bad_seg[seg_ids[bad]] = True
+            sc[bad_seg[seg_ids]] = np.float32(-1.0e30)
+            st.sc_prev.copy_(torch.from_numpy(sc))
+        n_loc = int(seg_ids.max()) + 1
+        mx = np.full(n_loc, -np.inf, dtype=np.float32)
+        np.maximum.at(mx, seg_ids, sc)
+        full_seg = seg_ids + st.seg_id_offset
+        cand_all = (mx[seg_ids] - np.float32(1e-6) * (full_seg % 16384).astype(np.float32)).astype(np.float32)
+        st.seg_id_offset += n_loc
+        t0 = st.n_pin if ev == 0 else 0
+        if t0 >= W:
+            return
+        t = np.arange(t0, W)
+        ok = cand_all[t0:] > -1.0e29
+        c_pos = ev * W + t[ok]
+        c_sc = cand_all[t0:][ok]
+        c_src = t[ok]
+        c_tok = st.tok_prev[0, t0:][ok]
+        c_seg = full_seg[t0:][ok]
+        M = int(st.mem_pos.numel())
+        all_pos = np.concatenate([st.mem_pos.numpy(), c_pos])
+        all_sc = np.concatenate([st.mem_score.numpy(), c_sc]).astype(np.float32)
+        if all_pos.size <= st.seg_budget:
+            win = np.arange(all_pos.size)
+        else:
+            win = np.sort(np.argsort(-all_sc, kind="stable")[:st.seg_budget])
+        keep = win[win < M]
+        add = win[win >= M] - M
+        nk, na = keep.size, add.size
+        # compaction: new bank = old[keep] ++ prev_chunk[c_src[add]], built out of place then swapped in
+        for bank, tmp, src_prev in ((st.k_seg_raw, st._seg_tmp_k, st.kraw_prev), (st.v_seg, st._seg_tmp_v, st.v_prev)):
+            ft = self._flat(tmp)
+            if nk:
+                ops.gather_rows(self._flat(bank), ft[:, :nk], torch.from_numpy(keep.astype(np.int32)))
+            if na:
+                ops.gather_rows(self._flat(src_prev), ft[:, nk:nk + na], torch.from_numpy(c_src[add].astype(np.int32)))
+        st.k_seg_raw, st._seg_tmp_k = st._seg_tmp_k, st.k_seg_raw
+        st.v_seg, st._seg_tmp_v = st._seg_tmp_v, st.v_seg
+        mem_tok = np.concatenate([st.mem_tok.numpy()[keep], c_tok[add]])
+        mem_seg = np.concatenate([st.mem_seg.numpy()[keep], c_seg[add]])
+        st.mem_pos = torch.from_numpy(all_pos[win].astype(np.int64))
+        st.mem_score = torch.from_numpy(all_sc[win])
+        st.mem_tok = torch.from_numpy(mem_tok.astype(np.int64))
+        st.mem_seg = torch.from_numpy(mem_seg.astype(np.int64))
+
+    # ------------------------------------------------------------------ device compute
+    def _seg_bias(self, st: VAULTv3State, li: int, M: int) -> Optional[torch.Tensor]:
+        """Per-head bias on the segment span (src/vault_v3_model.py:1115-1132)."""
+        L = self.cfg.n_layers
+        if not (st.seg_bias_active and st.seg_head_bias is not None and M > 0 and L // 4 <= li < L - L // 14):
+            return None
+        hb = st.seg_head_bias_hop1 if (st.seg_bias_mode == 2 and li < L // 2 and st.seg_head_bias_hop1 is not None) \
+            else st.seg_head_bias
+        return hb.reshape(self.cfg.n_heads, -1).to(torch.float32).contiguous()
+
+    def _layers(self, x: torch.Tensor, st: VAULTv3State, ids_q: int, pos: int, c: int, seg_active: bool,
+                chunk: bool, clen: int = 0) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """Run all layers on x [N, d] in place.  Decode (chunk=False): N = batch, one token per sequence
+        at position pos (slot c).  Chunk prefill (chunk=True, batch 1): N = clen tokens at slots [0, clen)
+        of chunk pos // W."""
+        cfg, w = self.cfg, self.w
+        W, H, G, D, d = cfg.window, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_model
+        N = x.shape[0]
+        HD, GD = H * D, G * D
+        ci = pos // W
+        feats = None
+        if seg_active:
+            feats = torch.empty(N, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device)
+        # attention extents
+        if chunk:
+            n_sk = st.n_pin if ci >= 2 else 0
+            n_seg = int(st.mem_pos.numel()) if (seg_active and ci >= 2) else 0
+            n_prev = W if ci >= 1 else 0
+            eff0 = W if ci >= 1 else 0
+            table, trs = self._rows(eff0), D
+        else:
+            n_sk = st.n_pin if pos >= 2 * W else 0
+            n_seg = int(st.mem_pos.numel()) if (pos >= 2 * W and seg_active) else 0
+            n_prev = W if pos >= W else 0
+            eff = W + c if pos >= W else c
+            table, trs = self._rows(eff), 0
+        u = torch.empty(N, d, dtype=torch.float32, device=self.device)
+        ao = torch.empty(N, H, D, dtype=torch.float32, device=self.device)
+        hbuf = torch.empty(N, cfg.d_ff, dtype=torch.float32, device=self.device)
+        scale = 1.0 / math.sqrt(D)
+        for li, lw in enumerate(w.layers):
+            if seg_active and li in cfg.seg_layers:
+                j = cfg.seg_layers.index(li)
+                feats[:, j * d:(j + 1) * d].copy_(x)
+            ops.rmsnorm(x, lw.ln1, cfg.rms_eps, out=u)
+            if lw.wq is None:
+                qkv = ops.qlinear(lw.wqkv, u, bias=lw.bqkv)
+                q = qkv[:, :HD].view(N, H, D)
+                k = qkv[:, HD:HD + GD].view(N, G, D)
+                v = qkv[:, HD + GD:].view(N, G, D)
+            else:
+                q = ops.qlinear(lw.wq, u, bias=lw.bq).view(N, H, D)
+                kv = ops.qlinear(lw.wqkv, u, bias=lw.bqkv)
+                k = kv[:, :GD].view(N, G, D)
+                v = kv[:, GD:].view(N, G, D)
+            kc, kr, vc = st.k_cur[li], st.kraw_cur[li], st.v_cur[li]          # [B, G, W, D]
+            ks, vs = st.k_sink_raw[li], st.v_sink[li]                          # [B, G, S_cap, D]
+            if chunk:
+                take = max(0, min(N, st.sink_cap - pos))
+                ops.rope_qkv_write(q, k, v, table, trs, kc[0], kr[0], vc[0], D, kc.stride(1),
+                                   ks[0, :, pos] if take else None, vs[0, :, pos] if take else None, take,
+                                   D, ks.stride(1))
+            else:
+                take = N if pos < st.sink_cap else 0
+                ops.rope_qkv_write(q, k, v, table, trs, kc[:, :, c], kr[:, :, c], vc[:, :, c], kc.stride(0),
+                                   kc.stride(1), ks[:, :, pos] if take else None, vs[:, :, pos] if take else None,
+                                   take, ks.stride(0), ks.stride(1))
+            spans = []
+            if n_sk:
+                spans.append((st.k_sink_rot[li][:, :, :n_sk], st.v_sink[li][:, :, :n_sk]))
+            bias, bspan = None, -1
+            if n_seg:
+                bias = self._seg_bias(st, li, n_seg) if not chunk else None
+                bspan = len(spans)
+                spans.append((st.k_seg_rot[li][:, :, :n_seg], st.v_seg[li][:, :, :n_seg]))
+            if n_prev:
+                spans.append((st.k_prev[li], st.v_prev[li]))
+            if chunk:
+                spans.append((kc[:, :, :N], st.v_cur[li][:, :, :N]))
+                ops.attn_decode(q, spans, out=ao, bias=bias, bias_span=bspan, scale=scale, ws=self.ws, causal_base=0)
+            else:
+                spans.append((kc[:, :, :c + 1], st.v_cur[li][:, :, :c + 1]))
+                ops.attn_decode(q, spans, out=ao, bias=bias, bias_span=bspan, scale=scale, ws=self.ws)
+            ops.qlinear(lw.wo, ao.view(N, HD), out=x, accumulate=True)
+            ops.rmsnorm(x, lw.ln2, cfg.rms_eps, out=u)
+            ops.qlinear_swiglu(lw.wgu, u, out=hbuf)
+            ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
+        return x, feats
+
+    def _score(self, st: VAULTv3State, feats: torch.Tensor, T: int, c0: int) -> None:
+        """Habituated segment scores of T tokens into sc_cur[c0:c0+T]
+        (src/vault_v3_model.py:1224-1247, 2294-2305)."""
+        sw = self.w.scorer
+        fd = feats.shape[1]
+        first = not st.ema_ready
+        rows = torch.empty(2 * T, fd, dtype=torch.float32, device=self.device)
+        ops.ema_habituate(feats, rows[T:], st.seg_feat_ema, first)
+        ops.layernorm(feats, sw.ln_w, sw.ln_b, 1e-5, rows[:T])
+        ops.layernorm(rows[T:], sw.ln_w, sw.ln_b, 1e-5, rows[T:])
+        h1 = ops.qlinear(sw.w1, rows, bias=sw.b1)
+        ops.seg_score_tail(h1, sw.w2, sw.b2, T, first, st.sc_cur[c0:c0 + T])
+        st.ema_ready = True
+
+    def _logits(self, h: torch.Tensor) -> torch.Tensor:
+        u = ops.rmsnorm(h, self.w.norm, self.cfg.rms_eps)
+        return ops.qlinear(self.w.embed, u)
+
+    def _chunk_recurrent(self, input_ids: torch.Tensor, bud: int, all_logits: bool):
+        """Chunk-recurrent prefill / forward for batch 1 (src/vault_v3_model.py:1938-2116)."""
+        cfg = self.cfg
+        W = cfg.window
+        ids_all = input_ids.reshape(-1).to("cpu", torch.int64)
+        L = ids_all.numel()
+        st = self.new_state(1, seg_budget=bud)
+        seg_active = self._seg_active(st, 1)
+        limit = min(cfg.max_sink, W, st.sink_cap)
+        for p in range(min(L, limit + 1)):
+            if st.pin_locked:
+                break
+            self._auto_pin(st, int(ids_all[p]), p)
+        outs = []
+        last = None
+        for ci in range((L + W - 1) // W):
+            r0, r1 = ci * W, min(L, (ci + 1) * W)
+            clen = r1 - r0
+            st.pos = r0
+            if ci > 0:
+                self._boundary(st, seg_active)
+            ch = ids_all[r0:r1]
+            st.tok_cur[0, :clen] = ch.numpy()
+            if seg_active:
+                s_loc, slen = 0, 0
+                for j in range(clen):
+                    st.seg_cur_ids[0, j] = s_loc
+                    slen += 1
+                    if j == W - 1 or slen >= cfg.seg_max:
+                        s_loc += 1
+                        slen = 0
+                st.cur_seg_id, st.seg_len = s_loc, slen
+            x = ops.embed(self.w.embed, ch.to(self.device), pad_row=0)
+            x, feats = self._layers(x, st, ids_q=clen, pos=r0, c=0, seg_active=seg_active, chunk=True)
+            if seg_active:
+                self._score(st, feats, T=clen, c0=0)
+            if all_logits:
+                outs.append(x)
+            last = x[-1:]
+        st.pos = L
+        st.seg_bias_active = False
+        h = torch.cat(outs, dim=0) if all_logits else last
+        return h, st

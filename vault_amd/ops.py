@@ -177,12 +177,16 @@ class Workspace:
 
 
 def attn_decode(q: torch.Tensor, spans, out: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
-                bias_span: int = -1, scale: Optional[float] = None, ws: Optional[Workspace] = None) -> torch.Tensor:
-    """q: [B, H, D] fp32 post-RoPE.  spans: list of (K, V) views shaped [B, G, n, D] (unit stride in D
-    and n; any batch / group stride).  bias: [H, n_bias] fp32 or None.  Returns [B, H, D] fp32."""
+                bias_span: int = -1, scale: Optional[float] = None, ws: Optional[Workspace] = None,
+                causal_base: int = -1) -> torch.Tensor:
+    """q: [B, H, D] fp32 post-RoPE (heads and dims contiguous, any batch stride).  spans: list of
+    (K, V) views shaped [B, G, n, D] (unit stride in D and n; any batch / group stride; batch stride 0
+    shares one span across entries).  bias: [H, n_bias] fp32 or None.  causal_base >= 0: the last
+    span is causal (entry b sees causal_base + b + 1 keys).  Returns [B, H, D] fp32."""
     _need(q, torch.float32, "q")
     B, H, D = q.shape
-    q = q.contiguous()
+    if q.stride(2) != 1 or q.stride(1) != D:
+        q = q.contiguous()
     kv_dt = None
     arr = (L.KVSpan * 4)()
     n_tot = 0
@@ -192,7 +196,7 @@ def attn_decode(q: torch.Tensor, spans, out: Optional[torch.Tensor] = None, bias
             kv_dt = KV_DTYPES[k.dtype]
         if KV_DTYPES[k.dtype] != kv_dt or v.dtype != k.dtype:
             raise ValueError("mixed KV dtypes")
-        if k.shape != v.shape or k.dim() != 4 or k.shape[0] != B or k.shape[3] != D:
+        if k.shape != v.shape or k.dim() != 4 or k.shape[3] != D or k.shape[0] not in (B, 1):
             raise ValueError(f"span {i} shape {tuple(k.shape)}")
         G = k.shape[1]
         if k.shape[2] == 0:
@@ -203,7 +207,8 @@ def attn_decode(q: torch.Tensor, spans, out: Optional[torch.Tensor] = None, bias
             raise ValueError(f"span {i} strides")
         G = k.shape[1]
         n = k.shape[2]
-        arr[i] = L.KVSpan(k.data_ptr() if n else None, v.data_ptr() if n else None, n, k.stride(0), k.stride(1))
+        bs = k.stride(0) if k.shape[0] == B and B > 1 else 0
+        arr[i] = L.KVSpan(k.data_ptr(), v.data_ptr(), n, bs, k.stride(1))
         n_tot += n
     if out is None:
         out = torch.empty(B, H, D, dtype=torch.float32, device=q.device)
@@ -218,8 +223,9 @@ def attn_decode(q: torch.Tensor, spans, out: Optional[torch.Tensor] = None, bias
             raise ValueError("bias needs unit stride along keys")
         if not 0 <= bias_span < len(spans) or bias.shape[0] != H or bias.shape[1] < spans[bias_span][0].shape[2]:
             raise ValueError("bias must be [H, >= len(bias span)]")
-    L.check(lib.vgx_attn_decode(kv_dt, q.data_ptr(), arr, len(spans), _ptr(bias),
-                                bias.stride(0) if bias is not None else 0, bias_span, out.data_ptr(), B, H, G, D,
+    L.check(lib.vgx_attn_decode(kv_dt, q.data_ptr(), q.stride(0), arr, len(spans), _ptr(bias),
+                                bias.stride(0) if bias is not None else 0, bias_span, causal_base, out.data_ptr(),
+                                B, H, G, D,
                                 float(scale if scale is not None else D ** -0.5), wbuf.data_ptr(), wbuf.numel(),
                                 _stream(q.device)), "vgx_attn_decode")
     return out
@@ -242,12 +248,16 @@ def rope_qkv_write(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor, 
                    v_dst: torch.Tensor, dst_tstride: int, dst_gstride: int,
                    sink_k: Optional[torch.Tensor] = None, sink_v: Optional[torch.Tensor] = None, n_sink: int = 0,
                    sink_tstride: int = 0, sink_gstride: int = 0) -> None:
-    """q [N,H,D] (rotated in place), k/v [N,G,D] fp32; destinations are the first rows to write
-    (views into the KV cache), strides in elements."""
+    """q [N,H,D] (rotated in place), k/v [N,G,D] fp32 (heads and dims contiguous, any token stride);
+    destinations are the first rows to write (views into the KV cache), strides in elements."""
     N, G, D = k.shape
     H = 0 if q is None else q.shape[1]
+    for t in (q, k, v):
+        if t is not None and (t.stride(2) != 1 or t.stride(1) != D):
+            raise ValueError("q/k/v need contiguous heads")
     kv_dt = KV_DTYPES[v_dst.dtype]
-    L.check(L.load().vgx_rope_qkv_write(kv_dt, _ptr(q), k.data_ptr(), v.data_ptr(), N, H, G, D, table.data_ptr(),
+    L.check(L.load().vgx_rope_qkv_write(kv_dt, _ptr(q), q.stride(0) if q is not None else 0, k.data_ptr(), k.stride(0),
+                                        v.data_ptr(), v.stride(0), N, H, G, D, table.data_ptr(),
                                         table_rstride, _ptr(k_rot), _ptr(k_raw), v_dst.data_ptr(), dst_tstride,
                                         dst_gstride, _ptr(sink_k), _ptr(sink_v), n_sink, sink_tstride, sink_gstride,
                                         _stream(k.device)), "vgx_rope_qkv_write")
@@ -275,3 +285,21 @@ def gather_rows(src: torch.Tensor, dst: torch.Tensor, idx: torch.Tensor) -> None
     L.check(L.load().vgx_gather_rows(KV_DTYPES[src.dtype], src.data_ptr(), dst.data_ptr(), idx32.data_ptr(),
                                      idx32.numel(), n_src, O, src.stride(0), dst.stride(0), D, _stream(src.device)),
             "vgx_gather_rows")
+
+
+def ema_habituate(f: torch.Tensor, hab: torch.Tensor, ema: torch.Tensor, first: bool) -> None:
+    T, fd = f.shape
+    L.check(L.load().vgx_ema_habituate(f.data_ptr(), f.stride(0), hab.data_ptr(), hab.stride(0), ema.data_ptr(), T, fd,
+                                       1 if first else 0, _stream(f.device)), "vgx_ema_habituate")
+
+
+def layernorm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float, out: torch.Tensor) -> torch.Tensor:
+    n, d = x.shape
+    L.check(L.load().vgx_layernorm(x.data_ptr(), x.stride(0), w.data_ptr(), b.data_ptr(), out.data_ptr(), out.stride(0),
+                                   n, d, float(eps), _stream(x.device)), "vgx_layernorm")
+    return out
+
+
+def seg_score_tail(h: torch.Tensor, w2: torch.Tensor, b2: torch.Tensor, T: int, first: bool, out: torch.Tensor) -> None:
+    L.check(L.load().vgx_seg_score_tail(h.data_ptr(), h.stride(0), w2.data_ptr(), b2.data_ptr(), h.shape[1], T,
+                                        1 if first else 0, out.data_ptr(), _stream(h.device)), "vgx_seg_score_tail")
