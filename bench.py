@@ -1,0 +1,271 @@
+"""Decode throughput of the VAULT v3 hot path on one MI355X.
+
+Workload (one "step"): one full 28-layer decode step of a random-init 1.54B VAULT v3 model
+(d=1536, 12 query / 2 KV heads, head_dim 128, SwiGLU 8960, vocab 151665) in hybrid Q4_0
+(Q8_0 embeddings / tied LM head, Q8_0 k/v projections, Q8_0 q/o projections in layers 0, 1, 26, 27;
+Q4_0 elsewhere) at 100K-token context: 512 pinned sinks, 1024 segment-memory slots and the 2W=2048
+window (W=1024), segment scorer on, batch 1 (``--batch`` for more; segment memory is off for
+batch > 1 as in the reference).  The state is seeded where a long stream leaves it (fixed-size
+state), weights are drawn directly as quantized blocks from a seeded generator.
+
+Prints one JSON line: tokens/s, plus the roofline of the dominant kernel (the fused gate/up SwiGLU
+Q4_0 GEMV, 28 launches per token), secondary kernel figures (Q8_0/Q4_0 GEMV at the model's shapes,
+batched bf16 decode attention at 3584 keys) and the reference C runtime timed on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+CTX_POS = 100_000          # first decoded position: 100K tokens of context already streamed
+N_PIN, MEM_CNT = 512, 1024
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def model_config(vocab: int = 151665):
+    from vault_amd.config import QWEN25_1P5B
+    from dataclasses import replace
+    return replace(QWEN25_1P5B, vocab_size=vocab, auto_pin_system=False)
+
+
+def build_model(cfg, dev, kv_dtype, seed: int = 1234):
+    from vault_amd.model import VAULTv3ForCausalLM
+    from vault_amd.weights import ModelWeights, synthetic_tensors
+    t0 = time.time()
+    tensors = synthetic_tensors(cfg, "q4_0", seed)
+    _log(f"synthetic weights generated in {time.time() - t0:.1f}s")
+    w = ModelWeights.from_tensors(cfg, tensors, dev)
+    return VAULTv3ForCausalLM(w, kv_dtype=kv_dtype), tensors
+
+
+def seeded_state(model, batch: int, seed: int = 99):
+    import torch
+    st = model.new_state(batch, seg_budget=None if batch == 1 else 0)
+    gen = torch.Generator().manual_seed(seed)
+    st.seed_long_context(CTX_POS, N_PIN, MEM_CNT if batch == 1 else 0,
+                         lambda li, name, shape: torch.randn(shape, generator=gen))
+    return st
+
+
+def _events():
+    import torch
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_decode(model, st, steps: int, warmup: int, batch: int, seed: int = 5):
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, model.cfg.vocab_size, (warmup + steps, batch), generator=g)
+    for i in range(warmup):
+        model.step(ids[i], st)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        logits = model.step(ids[warmup + i], st)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    assert torch.isfinite(logits).all()
+    return dt
+
+
+def dominant_kernel(model, rounds: int = 20):
+    """Fused gate/up SwiGLU Q4_0 GEMV (2 x 8960 x 1536) over the 28 layers' weights in turn, as in the
+    step (433 MB of weights, beyond the 256 MB last-level cache); HIP events on the launch stream."""
+    import torch
+    from vault_amd import ops
+    cfg = model.cfg
+    x = torch.randn(1, cfg.d_model, device=model.device)
+    h = torch.empty(1, cfg.d_ff, device=model.device)
+    layers = model.w.layers
+    for lw in layers:
+        ops.qlinear_swiglu(lw.wgu, x, out=h)
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(rounds):
+        for lw in layers:
+            ops.qlinear_swiglu(lw.wgu, x, out=h)
+    e1.record()
+    torch.cuda.synchronize()
+    n = rounds * len(layers)
+    us = e0.elapsed_time(e1) * 1e3 / n
+    wb = layers[0].wgu.stream_bytes
+    algo = wb + 4 * cfg.d_model + 4 * cfg.d_ff
+    return {"kernel": "qgemv_kernel<Q4_0, batch 1, SwiGLU epilogue> (gate|up 2x8960x1536)",
+            "launches": n, "avg_us": us, "bytes_per_launch": algo, "gbs": algo / us / 1e3}
+
+
+def gemv_figures(dev, batches=(1, 16), reps: int = 20):
+    """Q8_0 / Q4_0 GEMV at the model's projection shapes, weights rotated over copies that exceed the
+    last-level cache; GB/s of algorithmic bytes (weights + x + y)."""
+    import numpy as np
+    import torch
+    from vault_amd import ops, vlt3
+    shapes = [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (151665, 1536)]
+    rng = np.random.default_rng(7)
+    out = []
+    for dt, name in ((vlt3.Q8_0, "q8_0"), (vlt3.Q4_0, "q4_0")):
+        for rows, cols in shapes:
+            raw = vlt3.synthetic_blocks(dt, rows, cols, rng)
+            w0 = ops.QWeight.from_blocks(dt, rows, cols, raw, dev)
+            ncopy = max(2, math.ceil(768e6 / w0.stream_bytes))
+            ws = [w0] + [ops.QWeight(dt, rows, cols, w0.packed.clone()) for _ in range(ncopy - 1)]
+            for b in batches:
+                x = torch.randn(b, cols, device=dev)
+                y = torch.empty(b, rows, device=dev)
+                for w in ws:
+                    ops.qlinear(w, x, out=y)
+                e0, e1 = _events()
+                e0.record()
+                for _ in range(reps):
+                    for w in ws:
+                        ops.qlinear(w, x, out=y)
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / (reps * len(ws))
+                algo = w0.stream_bytes + 4 * b * (rows + cols)
+                out.append({"dtype": name, "out": rows, "in": cols, "batch": b, "us": round(us, 2),
+                            "gbs": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 3)})
+            del ws, w0
+    return out
+
+
+def attn_figures(dev, reps: int = 20):
+    """Batched decode attention, bf16 KV: B=64, 12 q / 2 KV heads, D=128, keys 512 sink + 1024 segment
+    + 2048 window = 3584; algorithmic bytes = K and V once (234,881,024 B) + q + out."""
+    import torch
+    from vault_amd import ops
+    B, H, G, D = 64, 12, 2, 128
+    lens = (512, 1024, 1024, 1024)
+    g = torch.Generator().manual_seed(11)
+    spans = [(torch.randn(B, G, n, D, generator=g).to(dev, torch.bfloat16),
+              torch.randn(B, G, n, D, generator=g).to(dev, torch.bfloat16)) for n in lens]
+    q = torch.randn(B, H, D, generator=g).to(dev)
+    out = torch.empty(B, H, D, device=dev)
+    ws = ops.Workspace(dev)
+    ops.attn_decode(q, spans, out=out, ws=ws)
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(reps):
+        ops.attn_decode(q, spans, out=out, ws=ws)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    algo = B * sum(lens) * G * D * 2 * 2 + 2 * B * H * D * 4
+    return {"config": "B=64 bf16 KV, 3584 keys (512 sink | 1024 seg | 2048 window)", "us": round(us, 2),
+            "gbs": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 3)}
+
+
+def cpu_baseline(cfg, tensors, budget_s: float = 15.0):
+    """The reference C runtime (runtime/vault3.c, compiled into oracle/_ref) stepping the same model
+    from a state seeded at the same context position, on the host's cores."""
+    from oracle import ref
+    from vault_amd import vlt3
+    if not ref.available():
+        return None
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    with tempfile.TemporaryDirectory() as td:
+        path = os.path.join(td, "m.vlt3")
+        vlt3.write_vlt3(path, list(tensors.values()), cfg, vlt3.Q4_0)
+        with open(path, "rb") as f:
+            image = f.read()
+    rt = ref.RefRuntime(image, threads=threads, verify=False)
+    del image
+    rt.seed_long_context(CTX_POS, N_PIN, MEM_CNT, seed=3)
+    rt.step(1)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and n < 300:
+        rt.step(2 + n)
+        n += 1
+    dt = time.perf_counter() - t0
+    rt.close()
+    return {"value": round(n / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"{n} decode steps of the same 1.54B hybrid-Q4_0 model from position {CTX_POS + 1} "
+                      f"(512 sinks, 1024 segment slots, fp32 state) with runtime/vault3.c v3_step, "
+                      f"{threads} threads"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--kv", choices=("fp32", "bf16"), default="fp32")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the secondary kernel figures")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (decode shards by "
+              "independent sequences with no exchange); run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    from vault_amd import _lib
+    _lib.load()
+    dev = torch.device("cuda:0")
+    kv_dtype = torch.float32 if args.kv == "fp32" else torch.bfloat16
+    cfg = model_config()
+    model, tensors = build_model(cfg, dev, kv_dtype)
+    st = seeded_state(model, args.batch)
+    _log(f"model and state ready (state {st.nbytes() / 2**20:.0f} MiB); timing {args.steps} steps")
+    dt = time_decode(model, st, args.steps, args.warmup, args.batch)
+    tok_s = args.batch * args.steps / dt
+    ms = dt * 1e3 / args.steps
+    _log(f"decode: {tok_s:.1f} tokens/s ({ms:.3f} ms/step)")
+
+    dom = dominant_kernel(model)
+    _log(f"dominant kernel: {dom['avg_us']:.2f} us, {dom['gbs']:.0f} GB/s")
+    kernels = {}
+    if not args.no_kernels:
+        kernels["gemv"] = gemv_figures(dev)
+        kernels["attn_decode"] = attn_figures(dev)
+        _log("kernel figures done")
+    cpu = None
+    if not args.no_cpu and args.batch == 1 and args.kv == "fp32":
+        cpu = cpu_baseline(cfg, tensors)
+        if cpu:
+            _log(f"cpu baseline: {cpu['value']} tokens/s on {cpu['cores']} threads")
+
+    # algorithmic bytes of one decode step (weights + LM head + scorer + KV read)
+    n_keys_avg = N_PIN + (MEM_CNT if args.batch == 1 else 0) + cfg.window + (CTX_POS % cfg.window) + \
+        args.warmup + (args.steps + 1) / 2
+    kv_bytes = cfg.n_layers * n_keys_avg * 2 * cfg.head_dim * 2 * (4 if args.kv == "fp32" else 2) * args.batch
+    step_bytes = model.w.layer_stream_bytes() + model.w.embed.stream_bytes + kv_bytes + \
+        (model.w.scorer.w1.stream_bytes if (model.w.scorer is not None and args.batch == 1) else 0)
+    line = {
+        "metric": "decode tokens/s, 1.54B hybrid-Q4_0 @100K ctx (with decode attn + Q8/Q4 GEMV GB/s)",
+        "value": round(tok_s, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32" if args.kv == "fp32" else "f32 (bf16 KV)", "data": "synthetic (seeded random-init weights as quantized blocks, seeded KV state)",
+        "config": {"workload": "28-layer 1.54B hybrid-Q4_0 decode step at 100K context (512 sinks, 1024 segment KV, "
+                               "2048 window, segment scorer on)", "batch": args.batch, "context": CTX_POS,
+                   "kv_dtype": args.kv, "parallelism": "single GPU"},
+        "step_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+        "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": dom["kernel"], "avg_us": round(dom["avg_us"], 3),
+                     "bytes_per_launch": dom["bytes_per_launch"]},
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -67,9 +67,9 @@ class RefRuntime:
         lib.ref_set_threads(self._h, threads)
 
     def close(self):
-        if self._h:
-            _load().ref_close(self._h)
-            self._h = None
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.ref_close(self._h)
+        self._h = None
 
     __del__ = close
 

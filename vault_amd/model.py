@@ -105,10 +105,35 @@ class VAULTv3State:
         self.n_pin = max(0, min(int(n_pin), cap))
         self.pin_locked = True
 
+    KV_FIELDS = ("k_prev", "k_cur", "v_prev", "v_cur", "kraw_prev", "kraw_cur", "k_sink_raw", "k_sink_rot",
+                 "v_sink", "k_seg_raw", "k_seg_rot", "v_seg")
+
     def nbytes(self) -> int:
-        return sum(t.numel() * t.element_size() for t in (
-            self.k_prev, self.k_cur, self.v_prev, self.v_cur, self.kraw_prev, self.kraw_cur, self.k_sink_raw,
-            self.k_sink_rot, self.v_sink, self.k_seg_raw, self.k_seg_rot, self.v_seg))
+        return sum(getattr(self, n).numel() * getattr(self, n).element_size() for n in self.KV_FIELDS)
+
+    def seed_long_context(self, pos: int, n_pin: int, mem_cnt: int, fill) -> None:
+        """Put the state where a long stream leaves it: position ``pos`` (chunk index >= 2), ``n_pin``
+        sinks locked, ``mem_cnt`` occupied segment-memory slots (mem_pos[i] = 8 i, segment i // 16,
+        score 0), EMA ready.  ``fill(layer, field, shape)`` returns the host values of one layer's KV
+        tensor (shape [B, G, n, D]).  Steps taken from here stay in the current chunk while
+        pos % W < W - 1.  The fixed-size state makes this exactly the state a stream reaches, up to
+        the values of the cached rows."""
+        W = self.cfg.window
+        if pos < 2 * W or n_pin > self.sink_cap or mem_cnt > max(0, self.seg_budget):
+            raise ValueError("seed_long_context: pos < 2W, or n_pin / mem_cnt beyond capacity")
+        for name in self.KV_FIELDS:
+            t = getattr(self, name)
+            for li in range(t.shape[0]):
+                t[li].copy_(fill(li, name, tuple(t.shape[1:])).to(t.dtype))
+        self.pos = int(pos)
+        self.n_pin = int(n_pin)
+        self.pin_locked = True
+        i = np.arange(mem_cnt, dtype=np.int64)
+        self.mem_pos = torch.from_numpy(i * 8)
+        self.mem_score = torch.zeros(mem_cnt, dtype=torch.float32)
+        self.mem_tok = torch.zeros(mem_cnt, dtype=torch.long)
+        self.mem_seg = torch.from_numpy(i // 16)
+        self.ema_ready = True
 
 
 class VAULTv3ForCausalLM:

@@ -166,11 +166,12 @@ def synthetic_blocks(dtype: int, rows: int, cols: int, rng: np.random.Generator)
     nblk = rows * (cols // QK)
     d = (np.abs(rng.standard_normal(nblk, dtype=np.float32)) * np.float32(0.02 / 127.0)).astype(np.float16)
     if dtype == Q8_0:
-        q = rng.integers(-127, 128, size=(nblk, QK), dtype=np.int16).astype(np.int8).view(np.uint8)
+        q = rng.integers(-127, 128, size=(nblk, QK), dtype=np.int8).view(np.uint8)
         return _pack_blocks(d, q).tobytes()
     if dtype == Q4_0:
-        nib = rng.integers(0, 16, size=(nblk, QK), dtype=np.uint8)
-        return _pack_blocks(d, nib[:, :16] | (nib[:, 16:] << 4)).tobytes()
+        # 16 uniform bytes per block = 32 independent uniform nibbles (q + 8 in [0, 15])
+        qs = np.frombuffer(rng.bytes(nblk * 16), dtype=np.uint8).reshape(nblk, 16)
+        return _pack_blocks(d, qs).tobytes()
     raise VLT3Error(f"dtype {dtype}")
 
 
