@@ -65,6 +65,30 @@ def _events():
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
+def graph_time_us(fn, launches_per_call: int, reps: int = 20) -> float:
+    """Average GPU time per launch of ``fn`` (a sequence of library calls), measured by capturing one
+    call into a HIP graph and replaying it ``reps`` times between HIP events on the replay stream."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()                                  # warm (allocations, workspaces) outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * launches_per_call)
+
+
 def time_decode(model, st, steps: int, warmup: int, batch: int, seed: int = 5):
     import torch
     g = torch.Generator().manual_seed(seed)
@@ -90,20 +114,17 @@ def dominant_kernel(model, rounds: int = 20):
     x = torch.randn(1, cfg.d_model, device=model.device)
     h = torch.empty(1, cfg.d_ff, device=model.device)
     layers = model.w.layers
-    for lw in layers:
-        ops.qlinear_swiglu(lw.wgu, x, out=h)
-    e0, e1 = _events()
-    e0.record()
-    for _ in range(rounds):
+    lnw = layers[0].ln2
+
+    def one_round():
         for lw in layers:
-            ops.qlinear_swiglu(lw.wgu, x, out=h)
-    e1.record()
-    torch.cuda.synchronize()
+            ops.qlinear_swiglu(lw.wgu, x, out=h, norm=(lnw, cfg.rms_eps))
+
+    us = graph_time_us(one_round, len(layers), reps=rounds)
     n = rounds * len(layers)
-    us = e0.elapsed_time(e1) * 1e3 / n
     wb = layers[0].wgu.stream_bytes
     algo = wb + 4 * cfg.d_model + 4 * cfg.d_ff
-    return {"kernel": "qgemv_kernel<Q4_0, batch 1, SwiGLU epilogue> (gate|up 2x8960x1536)",
+    return {"kernel": "qgemv_kernel<Q4_0, batch 1, SwiGLU epilogue, split-K x1, RMSNorm prologue> (gate|up 2x8960x1536)",
             "launches": n, "avg_us": us, "bytes_per_launch": algo, "gbs": algo / us / 1e3}
 
 
@@ -125,16 +146,12 @@ def gemv_figures(dev, batches=(1, 16), reps: int = 20):
             for b in batches:
                 x = torch.randn(b, cols, device=dev)
                 y = torch.empty(b, rows, device=dev)
-                for w in ws:
-                    ops.qlinear(w, x, out=y)
-                e0, e1 = _events()
-                e0.record()
-                for _ in range(reps):
+
+                def run():
                     for w in ws:
                         ops.qlinear(w, x, out=y)
-                e1.record()
-                torch.cuda.synchronize()
-                us = e0.elapsed_time(e1) * 1e3 / (reps * len(ws))
+
+                us = graph_time_us(run, len(ws), reps=reps)
                 algo = w0.stream_bytes + 4 * b * (rows + cols)
                 out.append({"dtype": name, "out": rows, "in": cols, "batch": b, "us": round(us, 2),
                             "gbs": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 3)})
@@ -155,14 +172,7 @@ def attn_figures(dev, reps: int = 20):
     q = torch.randn(B, H, D, generator=g).to(dev)
     out = torch.empty(B, H, D, device=dev)
     ws = ops.Workspace(dev)
-    ops.attn_decode(q, spans, out=out, ws=ws)
-    e0, e1 = _events()
-    e0.record()
-    for _ in range(reps):
-        ops.attn_decode(q, spans, out=out, ws=ws)
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
+    us = graph_time_us(lambda: ops.attn_decode(q, spans, out=out, ws=ws), 1, reps=reps)
     algo = B * sum(lens) * G * D * 2 * 2 + 2 * B * H * D * 4
     return {"config": "B=64 bf16 KV, 3584 keys (512 sink | 1024 seg | 2048 window)", "us": round(us, 2),
             "gbs": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 3)}

@@ -91,6 +91,22 @@ int vgx_embed_rows(int dtype, const void *packed, int64_t rows, int64_t cols, co
 int vgx_qlinear(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
                 int64_t batch, const float *bias, float *y, int64_t ldy, int accumulate, void *stream);
 
+/* GEMV epilogues of vgx_qlinear_ex. */
+enum { VGX_EPI_STORE = 0, VGX_EPI_ACCUM = 1, VGX_EPI_SWIGLU = 2 };
+
+/* Fused RMSNorm + GEMV: with u_b = norm_w * (x_b / sqrt(mean(x_b^2) + eps)) (or u_b = x_b when norm_w
+ * is NULL), computes for b < batch
+ *   VGX_EPI_STORE:  y[b, r]  = W[r] . u_b (+ bias[r])
+ *   VGX_EPI_ACCUM:  y[b, r] += W[r] . u_b (+ bias[r])              (residual add)
+ *   VGX_EPI_SWIGLU: y[b, r]  = silu(gate_r . u_b) * (up_r . u_b)   (vgx_qweight_pack_gateup tensor,
+ *                                                                    `rows` = d_ff, bias must be NULL)
+ * x and y must not overlap.  Replaces RMSNorm + nn.Linear pairs of the decode layer
+ * (src/vault_v3_model.py:2289-2292, 1041-1047, 1145-1150, 2150-2151) and rmsnorm + matvec /
+ * mlp_gu_run of runtime/vault3.c:2152-2160, 2193-2197, 2218-2219. */
+int vgx_qlinear_ex(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
+                   int64_t batch, const float *norm_w, float eps, const float *bias, float *y, int64_t ldy,
+                   int epilogue, void *stream);
+
 /* h[b, r] = silu(gate_r . x_b) * (up_r . x_b) over a vgx_qweight_pack_gateup tensor; `rows` is
  * the number of output rows (d_ff).  Replaces mlp_gu_run (runtime/vault3.c:1942-1956) and
  * F.silu(gate_proj(x)) * up_proj(x) (src/vault_v3_model.py:1149-1150). */
@@ -99,17 +115,33 @@ int vgx_qlinear_swiglu(int dtype, const void *w_gateup_packed, int64_t rows, int
 
 /* ---------------------------------------------------------------- attention -------------------- */
 
+/* Decode step descriptor: a small int32 device array that the host rewrites before every step, so
+ * that one captured HIP graph of the decode step replays at every position of a chunk.  No
+ * counterpart in the reference (its step reads pos from the host state, runtime/vault3.c:2034-2143). */
+enum {
+    VGX_STEP_SLOT = 0,       /* ring slot c = pos % W written by this step */
+    VGX_STEP_TABLE_ROW = 1,  /* RoPE table row of the query/key position */
+    VGX_STEP_SINK_SLOT = 2,  /* sink slot to fill (pos while pos < sink capacity), -1 for none */
+    VGX_STEP_N_CUR = 3,      /* keys of the current chunk visible to this step (c + 1) */
+    VGX_STEP_WORDS = 4
+};
+
 /* One contiguous run of key/value rows per (batch, kv group): row t of (b, g) is at element offset
- * b*batch_stride + g*group_stride + t*head_dim of k (and of v).  Element type is the KV dtype. */
+ * b*batch_stride + g*group_stride + t*head_dim of k (and of v).  Element type is the KV dtype.
+ * dyn_len (may be NULL): device int32; when set, only the first min(len, *dyn_len) rows are keys
+ * (the current-chunk span of a graph-captured decode step points at step[VGX_STEP_N_CUR]). */
 typedef struct {
     const void *k;
     const void *v;
     int64_t len;
     int64_t batch_stride;
     int64_t group_stride;
+    const int32_t *dyn_len;
 } vgx_kv_span;
 
-/* Workspace bytes vgx_attn_decode needs for these sizes (0 when one split suffices). */
+/* Workspace bytes vgx_attn_decode needs for these sizes (0 when one split suffices): the per-split
+ * softmax partials (m, l, acc) that a second, merge launch combines.  16-byte aligned.  Calls sharing
+ * one workspace must not overlap in time. */
 int64_t vgx_attn_decode_workspace_bytes(int64_t B, int64_t H, int64_t G, int64_t D, int64_t n_keys);
 
 /* Decode attention: out[b, h, :] = softmax_j(q[b,h].k_j * scale + bias[h, j]) v_j over the keys of
@@ -148,6 +180,20 @@ int vgx_rope_qkv_write(int kv_dtype, float *q, int64_t ldq, const float *k, int6
                        int64_t dst_tstride, int64_t dst_gstride, void *sink_k_raw, void *sink_v, int64_t n_sink,
                        int64_t sink_tstride, int64_t sink_gstride, void *stream);
 
+/* Decode-step form of vgx_rope_qkv_write for B sequences with one token each: the ring slot, the
+ * RoPE table row and the sink slot are read from the device step descriptor `step`
+ * (VGX_STEP_SLOT / _TABLE_ROW / _SINK_SLOT).  q [B][H][D] (row stride ldq) is rotated in place; k/v
+ * [B][G][D]; row (b, g) of slot c lands at b*dst_bstride + g*dst_gstride + c*dst_rstride of
+ * k_rot / k_raw / v_dst, and of sink_k_raw / sink_v with the sink strides when the sink slot is >= 0
+ * (sink pointers may be NULL).  Replaces src/vault_v3_model.py:1079-1094 and
+ * runtime/vault3.c:2162-2179 inside a captured step. */
+int vgx_rope_qkv_write_step(int kv_dtype, float *q, int64_t ldq, const float *k, int64_t ldk, const float *v,
+                            int64_t ldv, int64_t B, int64_t H, int64_t G, int64_t D, const float *table,
+                            int64_t table_rstride, const int32_t *step, void *k_rot, void *k_raw, void *v_dst,
+                            int64_t dst_bstride, int64_t dst_gstride, int64_t dst_rstride, void *sink_k_raw,
+                            void *sink_v, int64_t sink_bstride, int64_t sink_gstride, int64_t sink_rstride,
+                            void *stream);
+
 /* Rotate rows: dst[o, i, :] = R(src[o, i, :]) with angle row table + i*table_rstride, for o < n_outer,
  * i < n_rows (rows contiguous, D elements each; src may equal dst).  Replaces the chunk-boundary
  * re-base of k_prev by R_{-W} and the prefix re-rotation of segment/sink keys
@@ -179,9 +225,11 @@ int vgx_layernorm(const float *x, int64_t ldx, const float *w, const float *b, f
 
 /* Scorer tail for T tokens: h holds 2T rows of fc1 outputs (rows 0..T-1 raw features, T..2T-1
  * habituated).  out[t] = raw_t + 0.35 max(0, hab_t - raw_t), raw_t/hab_t = gelu_erf(h) . w2 + b2[0];
- * out[0] = raw_0 when first != 0.  Replaces src/vault_v3_model.py:881-883, 1238-1246, 2295-2305. */
+ * out[0] = raw_0 when first != 0.  out_index (may be NULL): device int32 added to out (a step
+ * descriptor's VGX_STEP_SLOT, for the captured decode step).
+ * Replaces src/vault_v3_model.py:881-883, 1238-1246, 2295-2305. */
 int vgx_seg_score_tail(const float *h, int64_t ldh, const float *w2, const float *b2, int64_t hidden, int64_t T,
-                       int first, float *out, void *stream);
+                       int first, float *out, const int32_t *out_index, void *stream);
 
 #ifdef __cplusplus
 }

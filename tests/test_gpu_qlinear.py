@@ -123,3 +123,60 @@ def test_swiglu(dev, dt, rows, cols, batch):
     tol = 1.1 * np.abs(u) * tg + np.abs(g) * tu + 1e-6 * np.abs(ref) + 1e-30
     err = np.abs(h - ref)
     assert np.all(err <= tol), float((err / tol).max())
+
+
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0, codec.F32])
+@pytest.mark.parametrize("rows,cols,batch,epi", [(2048, 1536, 1, "store"), (1536, 8960, 2, "accum"),
+                                                 (8960, 1536, 1, "swiglu"), (40000, 1536, 3, "store"),
+                                                 (256, 4608, 4, "store"), (12, 64, 5, "swiglu")])
+def test_gemv_fused_rmsnorm(dev, dt, rows, cols, batch, epi):
+    """u = RMSNorm(x) staged inside the GEMV (row mode, split-K mode, several LDS chunks) against
+    oracle rmsnorm -> fp64 GEMV; the norm's own fp32 rounding (relative 1e-6 of |u|) is folded into
+    the accumulation bound."""
+    rng = np.random.default_rng(rows + cols + batch)
+    x = (rng.standard_normal((batch, cols)) * 3.0).astype(np.float32)
+    g = rng.uniform(0.8, 1.2, cols).astype(np.float32)
+    u = linalg.rmsnorm(x, g, 1e-6)
+    xt, gt = torch.from_numpy(x).to(dev), torch.from_numpy(g).to(dev)
+    if epi == "swiglu":
+        gate = _blocks(dt, rows, cols, seed=41, kind="quantized")
+        up = _blocks(dt, rows, cols, seed=42, kind="quantized")
+        w = ops.QWeight.gateup_from_blocks(dt, rows, cols, gate, up, dev)
+        h = ops.qlinear_swiglu(w, xt, norm=(gt, 1e-6)).cpu().numpy().astype(np.float64)
+        gf, uf = codec.decode(dt, gate, rows, cols), codec.decode(dt, up, rows, cols)
+        gg, uu = linalg.gemv(gf, u), linalg.gemv(uf, u)
+        ref = linalg.swiglu(gg, uu)
+        tg, tu = 2 * linalg.gemv_bound(gf, u, dt), 2 * linalg.gemv_bound(uf, u, dt)
+        tol = 1.1 * np.abs(uu) * tg + np.abs(gg) * tu + 1e-6 * np.abs(ref) + 1e-30
+        err = np.abs(h - ref)
+        assert np.all(err <= tol), float((err / tol).max())
+        return
+    raw = _blocks(dt, rows, cols, seed=43, kind="quantized")
+    wq = ops.QWeight.from_blocks(dt, rows, cols, raw, dev)
+    wf = codec.decode(dt, raw, rows, cols)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    ref = linalg.gemv(wf, u, bias)
+    out = None
+    if epi == "accum":
+        y0 = rng.standard_normal((batch, rows)).astype(np.float32)
+        ref = ref + y0
+        out = torch.from_numpy(y0).to(dev)
+    y = ops.qlinear(wq, xt, bias=torch.from_numpy(bias).to(dev), out=out, accumulate=epi == "accum",
+                    norm=(gt, 1e-6)).cpu().numpy().astype(np.float64)
+    tol = 2 * linalg.gemv_bound(wf, u, dt) + np.abs(ref) * 2e-7
+    err = np.abs(y - ref)
+    assert np.all(err <= tol), float((err / tol).max())
+
+
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
+def test_gemv_fused_rmsnorm_equals_separate(dev, dt):
+    """Fused prologue == standalone RMSNorm kernel followed by the plain GEMV (same fp32 expression;
+    only the order of the sum of squares may differ)."""
+    rows, cols = 1536, 1536
+    raw = _blocks(dt, rows, cols, seed=44, kind="quantized")
+    wq = ops.QWeight.from_blocks(dt, rows, cols, raw, dev)
+    g = torch.rand(cols, generator=torch.Generator().manual_seed(1)).to(dev) + 0.5
+    x = torch.randn(2, cols, generator=torch.Generator().manual_seed(2)).to(dev)
+    fused = ops.qlinear(wq, x, norm=(g, 1e-6))
+    sep = ops.qlinear(wq, ops.rmsnorm(x, g, 1e-6))
+    assert torch.allclose(fused, sep, rtol=0, atol=1e-5 * float(sep.abs().max()))

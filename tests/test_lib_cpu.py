@@ -51,3 +51,25 @@ def test_host_validation_codes(lib):
     assert lib.vgx_qlinear(L.Q4_0, p, 4, 32, p, 32, 1, None, p, 4, 2, None) == -31
     assert lib.vgx_qlinear_swiglu(L.Q4_0, p, 3, 32, p, 32, 1, p, 3, None) == -7
     assert lib.vgx_qlinear(L.Q4_0, p, 4, 32, p, 32, 0, None, p, 4, 0, None) == 0   # empty batch: no-op
+
+
+def test_state_has_no_reference_cycle():
+    """A decode state must be freed by reference counting alone: a state left to the cyclic garbage
+    collector can be collected while a decode graph is being captured, and its destructors (pinned
+    host buffers, events, graphs) are not allowed during a capture."""
+    import gc
+    import weakref
+
+    from tests import modelgen
+    from vault_amd.model import VAULTv3State
+
+    cfg = modelgen.tiny_cfg()
+    gc.disable()
+    try:
+        st = VAULTv3State(cfg, 1, "cpu")
+        _ = st.layers[0].k_cur
+        ref = weakref.ref(st)
+        del st, _
+        assert ref() is None
+    finally:
+        gc.enable()

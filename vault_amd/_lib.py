@@ -19,6 +19,8 @@ ERRORS = {
 }
 
 F32, F16, BF16, Q8_0, Q4_0 = 0, 1, 2, 8, 9
+EPI_STORE, EPI_ACCUM, EPI_SWIGLU = 0, 1, 2
+STEP_SLOT, STEP_TABLE_ROW, STEP_SINK_SLOT, STEP_N_CUR, STEP_WORDS = 0, 1, 2, 3, 4
 
 P = C.c_void_p
 I32 = C.c_int
@@ -37,6 +39,7 @@ _SIGS = {
     "vgx_embed_rows": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
     "vgx_qlinear": (I32, [I32, P, I64, I64, P, I64, I64, P, P, I64, I32, P]),
     "vgx_qlinear_swiglu": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
+    "vgx_qlinear_ex": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P]),
     "vgx_attn_decode_workspace_bytes": (I64, [I64, I64, I64, I64, I64]),
     "vgx_attn_decode": (I32, [I32, P, I64, P, I32, P, I64, I32, I64, P, I64, I64, I64, I64, F, P, I64, P]),
     "vgx_rmsnorm": (I32, [P, I64, P, P, I64, I64, I64, F, P]),
@@ -46,14 +49,16 @@ _SIGS = {
     "vgx_gather_rows": (I32, [I32, P, P, P, I64, I64, I64, I64, I64, I64, P]),
     "vgx_ema_habituate": (I32, [P, I64, P, I64, P, I64, I64, I32, P]),
     "vgx_layernorm": (I32, [P, I64, P, P, P, I64, I64, I64, F, P]),
-    "vgx_seg_score_tail": (I32, [P, I64, P, P, I64, I64, I32, P, P]),
+    "vgx_seg_score_tail": (I32, [P, I64, P, P, I64, I64, I32, P, P, P]),
+    "vgx_rope_qkv_write_step": (I32, [I32, P, I64, P, I64, P, I64, I64, I64, I64, I64, P, I64, P, P, P, P, I64, I64,
+                                      I64, P, P, I64, I64, I64, P]),
 }
 
 
 class KVSpan(C.Structure):
     """vgx_kv_span (include/vault_amd.h)."""
     _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("len", C.c_int64),
-                ("batch_stride", C.c_int64), ("group_stride", C.c_int64)]
+                ("batch_stride", C.c_int64), ("group_stride", C.c_int64), ("dyn_len", C.c_void_p)]
 
 
 class VGXError(RuntimeError):

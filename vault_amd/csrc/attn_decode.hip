@@ -3,21 +3,28 @@
 // Reference semantics: src/vault_v3_model.py:1098-1136 (concat spans, _expand_kv, optional fp32
 // bias on the segment span, softmax, P V) and runtime/vault3.c:1958-2032 (attn_run).
 //
-// Mapping.  One workgroup = one wave = one (batch b, kv group g, key split).  The wave holds the
-// GRP query heads of group g, so every K/V row is fetched once for all GRP heads (the reference
-// re-reads K/V per head).  The 4 DPP rows (16 lanes each) of the wave each stream their own keys:
-// a DPP row holds one key row spread over its 16 lanes (D/16 contiguous elements per lane, one
-// 128-bit load for bf16 D=128, two for fp32), so one load instruction fetches four whole key rows.
-// q.k partials are reduced across the 16 lanes with DPP; each DPP row keeps its own online-softmax
-// state (m, l, acc), merged across rows with cross-lane shuffles at the end.  Splits write
-// (m, l, acc) partials that attn_merge_kernel combines; a single split writes the output directly.
+// Mapping.  One workgroup = kWaves waves = one (batch b, kv group g, key split).  Every wave holds
+// the GRP query heads of group g, so each K/V row is fetched once for all GRP heads (the reference
+// re-reads K/V per head).  The split's keys are dealt to the waves in 16-key tiles; inside a wave
+// the 4 DPP rows (16 lanes each) take 4 keys of the tile each, one key row spread over the 16 lanes
+// of a DPP row (D/16 contiguous elements per lane: one 128-bit load for bf16 D=128, two for fp32),
+// so one load instruction fetches four whole key rows.  q.k partials are reduced over the 16 lanes
+// with DPP; every DPP row keeps its own online-softmax state (m, l, acc).  The states are merged
+// across DPP rows with lane shuffles and across the waves of the workgroup through LDS; with more
+// than one split, each split writes (m, l, acc) partials to the workspace and attn_merge_kernel
+// combines them (a second launch: merging inside the first kernel would need a device-scope
+// release fence per workgroup, an L2 write-back that measured 2x slower at batch 64).
 #include "common.h"
 
 using namespace vgx;
 
 namespace {
 
-constexpr int kKB = 4;   // keys per DPP row per tile (16 keys per wave tile)
+constexpr int kKB = 4;       // keys per DPP row per 16-key tile
+constexpr int kWaves = 4;    // waves per workgroup
+constexpr int kMinKeysPerWave = 16;
+constexpr int kTargetWaves = 2048;
+constexpr int kMaxSplits = 64;
 constexpr float kNegBig = -1.0e30f;
 
 struct SpanArgs {
@@ -26,6 +33,7 @@ struct SpanArgs {
     int64_t len[4];
     int64_t bstride[4];
     int64_t gstride[4];
+    const int32_t *dyn_len[4];
     int n;
 };
 
@@ -64,16 +72,19 @@ __device__ __forceinline__ void load_chunk(const void *base, int64_t elem_off, f
     }
 }
 
+// Workspace layout: partials per (b, g, split, head): D accumulators, then m, l.
+
 template <int KV, int GRP, int DPL>
-__global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict__ q, int64_t ldq, SpanArgs sp,
-                                                          const float *__restrict__ bias, int64_t bias_hstride,
-                                                          int bias_span, float *__restrict__ out,
-                                                          float *__restrict__ ws, int H, int G, float scale,
-                                                          int64_t n_tot, int64_t kps, int n_splits,
-                                                          int64_t causal_base) {
+__global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
+    const float *__restrict__ q, int64_t ldq, SpanArgs sp, const float *__restrict__ bias, int64_t bias_hstride,
+    int bias_span, float *__restrict__ out, float *__restrict__ part, int H, int G,
+    float scale, int64_t n_tot, int64_t kps, int n_splits, int64_t causal_base) {
     constexpr int D = DPL * 16;
+    constexpr int SLOT = D + 2;
+    __shared__ float red[kWaves][GRP][SLOT];
+
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x, l16 = lane & 15, row = lane >> 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, row = lane >> 4;
 
     float qr[GRP][DPL];
 #pragma unroll
@@ -95,9 +106,10 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict
     const int64_t k1 = min(n_tot, k0 + kps);
     int64_t base = 0;
     for (int s = 0; s < sp.n; ++s) {
-        int64_t len = sp.len[s];
+        const int64_t len = sp.len[s];
         const int64_t lo = max(k0, base) - base;
         int64_t hi = min(k1, base + len) - base;
+        if (sp.dyn_len[s] != nullptr) hi = min(hi, (int64_t)*sp.dyn_len[s]);  // device-side length
         // Causal last span: batch entry b sees its first causal_base + b + 1 keys.
         if (causal_base >= 0 && s == sp.n - 1) hi = min(hi, causal_base + (int64_t)b + 1);
         base += len;
@@ -106,7 +118,7 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict
         const void *kb = sp.k[s];
         const void *vb = sp.v[s];
         const float *bb = (bias != nullptr && s == bias_span) ? bias + (int64_t)g * GRP * bias_hstride : nullptr;
-        for (int64_t t0 = lo; t0 < hi; t0 += 4 * kKB) {
+        for (int64_t t0 = lo + wave * 4 * kKB; t0 < hi; t0 += kWaves * 4 * kKB) {
             float kf[kKB][DPL], vf[kKB][DPL];
             bool valid[kKB];
 #pragma unroll
@@ -168,7 +180,7 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict
         }
     }
 
-    // Merge the online-softmax states of the four DPP rows.
+    // Merge the online-softmax states of the four DPP rows of the wave.
 #pragma unroll
     for (int sh = 16; sh <= 32; sh <<= 1) {
 #pragma unroll
@@ -186,87 +198,129 @@ __global__ __launch_bounds__(64) void attn_decode_kernel(const float *__restrict
             m[hh] = mn;
         }
     }
-    if (row != 0) return;
+    if (row == 0) {
 #pragma unroll
-    for (int hh = 0; hh < GRP; ++hh) {
-        if (n_splits == 1) {
-            float *op = out + ((int64_t)b * H + (int64_t)g * GRP + hh) * D + l16 * DPL;
-            const float inv = 1.0f / l[hh];
+        for (int hh = 0; hh < GRP; ++hh) {
 #pragma unroll
-            for (int d = 0; d < DPL; ++d) op[d] = acc[hh][d] * inv;
-        } else {
-            float *wp = ws + ((((int64_t)b * G + g) * n_splits + split) * GRP + hh) * (D + 2);
-#pragma unroll
-            for (int d = 0; d < DPL; ++d) wp[l16 * DPL + d] = acc[hh][d];
+            for (int d = 0; d < DPL; ++d) red[wave][hh][l16 * DPL + d] = acc[hh][d];
             if (l16 == 0) {
-                wp[D] = m[hh];
-                wp[D + 1] = l[hh];
+                red[wave][hh][D] = m[hh];
+                red[wave][hh][D + 1] = l[hh];
+            }
+        }
+    }
+    __syncthreads();
+
+    // Merge the waves: thread t owns (head t / D, dim t % D).
+    const int64_t pair = (int64_t)b * G + g;
+    for (int t = threadIdx.x; t < GRP * D; t += 64 * kWaves) {
+        const int hh = t / D, d = t - hh * D;
+        float M = kNegBig;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red[w][hh][D]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float c = __expf(red[w][hh][D] - M);
+            L = fmaf(c, red[w][hh][D + 1], L);
+            A = fmaf(c, red[w][hh][d], A);
+        }
+        if (n_splits == 1) {
+            out[((int64_t)b * H + (int64_t)g * GRP + hh) * D + d] = A / L;
+        } else {
+            float *pp = part + ((pair * n_splits + split) * GRP + hh) * SLOT;
+            pp[d] = A;
+            if (d == 0) {
+                pp[D] = M;
+                pp[D + 1] = L;
             }
         }
     }
 }
 
-// One workgroup per (b, h): out = sum_s e^{m_s - M} acc_s / sum_s e^{m_s - M} l_s.
-__global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ ws, float *__restrict__ out,
+// One workgroup per (b, h): out = sum_s e^{m_s - M} acc_s / sum_s e^{m_s - M} l_s.  The split
+// weights are computed once into LDS; every thread then sums its dimension over the splits with
+// eight loads in flight.
+__global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ part, float *__restrict__ out,
                                                           int H, int G, int D, int n_splits) {
+    __shared__ float wgt[kMaxSplits];
+    __shared__ float inv_l;
     const int bh = blockIdx.x;
     const int b = bh / H, h = bh - b * H;
     const int grp = H / G, g = h / grp, hh = h - g * grp;
     const int64_t stride = (int64_t)grp * (D + 2);
-    const float *w0 = ws + (((int64_t)b * G + g) * n_splits * grp + hh) * (D + 2);
-    float M = kNegBig;
-    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, w0[s * stride + D]);
-    float L = 0.0f;
-    for (int s = 0; s < n_splits; ++s) L += __expf(w0[s * stride + D] - M) * w0[s * stride + D + 1];
-    const float inv = 1.0f / L;
+    const float *p0 = part + (((int64_t)b * G + g) * n_splits * grp + hh) * (D + 2);
+    if (threadIdx.x < 64) {
+        const int s = threadIdx.x;
+        const float ms = s < n_splits ? p0[s * stride + D] : kNegBig;
+        const float ls = s < n_splits ? p0[s * stride + D + 1] : 0.0f;
+        const float M = wave_max(ms);
+        const float w = s < n_splits ? __expf(ms - M) : 0.0f;
+        const float L = wave_sum(w * ls);
+        if (s < n_splits) wgt[s] = w;
+        if (s == 0) inv_l = 1.0f / L;
+    }
+    __syncthreads();
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
         float a = 0.0f;
-        for (int s = 0; s < n_splits; ++s) a = fmaf(__expf(w0[s * stride + D] - M), w0[s * stride + d], a);
-        out[((int64_t)b * H + h) * D + d] = a * inv;
+        int s = 0;
+        for (; s + 8 <= n_splits; s += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p0[(s + u) * stride + d];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a = fmaf(wgt[s + u], v[u], a);
+        }
+        for (; s < n_splits; ++s) a = fmaf(wgt[s], p0[s * stride + d], a);
+        out[((int64_t)b * H + h) * D + d] = a * inv_l;
     }
 }
 
 int choose_splits(int64_t B, int64_t G, int64_t n_tot, int64_t *kps) {
-    // Aim for ~2048 waves in flight, at least 16 keys and at most 1024 keys per split.
+    // About kTargetWaves waves in flight, at least kMinKeysPerWave keys per wave, at most kMaxSplits.
     const int64_t pairs = B * G;
-    int64_t want = (2048 + pairs - 1) / pairs;
+    int64_t want = (kTargetWaves / kWaves + pairs - 1) / pairs;
+    const int64_t cap = (n_tot + kWaves * kMinKeysPerWave - 1) / (kWaves * kMinKeysPerWave);
+    want = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(want, cap), kMaxSplits));
     int64_t k = (n_tot + want - 1) / want;
     k = (k + 15) / 16 * 16;
-    k = std::max<int64_t>(64, std::min<int64_t>(1024, k));
-    if (n_tot <= 64) k = (n_tot + 15) / 16 * 16;
     *kps = k;
     return (int)((n_tot + k - 1) / k);
 }
 
+int64_t partial_bytes(int64_t B, int64_t H, int64_t D, int ns) {
+    return B * H * (int64_t)ns * (D + 2) * (int64_t)sizeof(float);
+}
+
 template <int KV, int GRP, int DPL>
 void launch_decode(dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp, const float *bias,
-                   int64_t bhs, int bspan, float *out, float *ws, int H, int G, float scale, int64_t n_tot, int64_t kps,
-                   int ns, int64_t cb) {
-    hipLaunchKernelGGL((attn_decode_kernel<KV, GRP, DPL>), grid, dim3(64), 0, st, q, ldq, sp, bias, bhs, bspan, out,
-                       ws, H, G, scale, n_tot, kps, ns, cb);
+                   int64_t bhs, int bspan, float *out, float *part, int H, int G, float scale, int64_t n_tot,
+                   int64_t kps, int ns, int64_t cb) {
+    hipLaunchKernelGGL((attn_decode_kernel<KV, GRP, DPL>), grid, dim3(64 * kWaves), 0, st, q, ldq, sp, bias, bhs,
+                       bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
 }
 
 template <int KV, int GRP>
 bool dispatch_dpl(int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp,
-                  const float *bias, int64_t bhs, int bspan, float *out, float *ws, int H, int G, float scale,
-                  int64_t n_tot, int64_t kps, int ns, int64_t cb) {
+                  const float *bias, int64_t bhs, int bspan, float *out, float *part, int H, int G,
+                  float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb) {
     switch (D) {
-        case 64: launch_decode<KV, GRP, 4>(grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb); return true;
-        case 128: launch_decode<KV, GRP, 8>(grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb); return true;
+        case 64: launch_decode<KV, GRP, 4>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb); return true;
+        case 128: launch_decode<KV, GRP, 8>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb); return true;
     }
     return false;
 }
 
 template <int KV>
 bool dispatch_grp(int grp, int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp,
-                  const float *bias, int64_t bhs, int bspan, float *out, float *ws, int H, int G, float scale,
-                  int64_t n_tot, int64_t kps, int ns, int64_t cb) {
+                  const float *bias, int64_t bhs, int bspan, float *out, float *part, int H, int G,
+                  float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb) {
     switch (grp) {
-        case 1: return dispatch_dpl<KV, 1>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb);
-        case 2: return dispatch_dpl<KV, 2>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb);
-        case 4: return dispatch_dpl<KV, 4>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb);
-        case 6: return dispatch_dpl<KV, 6>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb);
-        case 8: return dispatch_dpl<KV, 8>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, ws, H, G, scale, n_tot, kps, ns, cb);
+        case 1: return dispatch_dpl<KV, 1>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
+        case 2: return dispatch_dpl<KV, 2>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
+        case 4: return dispatch_dpl<KV, 4>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
+        case 6: return dispatch_dpl<KV, 6>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
+        case 8: return dispatch_dpl<KV, 8>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
     }
     return false;
 }
@@ -280,7 +334,7 @@ int64_t vgx_attn_decode_workspace_bytes(int64_t B, int64_t H, int64_t G, int64_t
     int64_t kps = 0;
     const int ns = choose_splits(B, G, n_keys, &kps);
     if (ns <= 1) return 0;
-    return B * H * (int64_t)ns * (D + 2) * (int64_t)sizeof(float);
+    return partial_bytes(B, H, D, ns);
 }
 
 int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span *spans, int n_spans,
@@ -309,29 +363,31 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
         sp.len[s] = spans[s].len;
         sp.bstride[s] = spans[s].batch_stride;
         sp.gstride[s] = spans[s].group_stride;
+        sp.dyn_len[s] = spans[s].dyn_len;
         n_tot += spans[s].len;
     }
     if (n_tot <= 0) return VGX_E_SIZE;
     int64_t kps = 0;
     const int ns = choose_splits(B, G, n_tot, &kps);
+    float *part = nullptr;
     if (ns > 1) {
-        const int64_t need = B * H * (int64_t)ns * (D + 2) * (int64_t)sizeof(float);
-        if (!workspace || workspace_bytes < need) return VGX_E_ARENA;
+        if (!workspace || workspace_bytes < partial_bytes(B, H, D, ns)) return VGX_E_ARENA;
+        if ((uintptr_t)workspace % 16) return VGX_E_ALIGN;
+        part = static_cast<float *>(workspace);
     }
-    if (ns > 65535) return VGX_E_LIMIT;
     const int grp = (int)(H / G);
     hipStream_t st = (hipStream_t)stream;
     dim3 grid((unsigned)ns, (unsigned)G, (unsigned)B);
-    float *ws = static_cast<float *>(workspace);
     bool ok = kv_dtype == VGX_F32
-                  ? dispatch_grp<VGX_F32>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out, ws,
-                                          (int)H, (int)G, scale, n_tot, kps, ns, causal_base)
-                  : dispatch_grp<VGX_BF16>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out, ws,
-                                           (int)H, (int)G, scale, n_tot, kps, ns, causal_base);
+                  ? dispatch_grp<VGX_F32>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out,
+                                          part, (int)H, (int)G, scale, n_tot, kps, ns, causal_base)
+                  : dispatch_grp<VGX_BF16>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out,
+                                           part, (int)H, (int)G, scale, n_tot, kps, ns, causal_base);
     if (!ok) return VGX_E_LIMIT;
     VGX_CHECK_LAUNCH();
     if (ns > 1) {
-        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * H)), dim3(64), 0, st, ws, out, (int)H, (int)G, (int)D, ns);
+        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * H)), dim3(128), 0, st, part, out, (int)H, (int)G,
+                           (int)D, ns);
         VGX_CHECK_LAUNCH();
     }
     return VGX_OK;

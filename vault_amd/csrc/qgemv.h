@@ -1,0 +1,429 @@
+// HBM-streaming Q8_0 / Q4_0 / F32 GEMV for gfx950 (batch 1..4 rows per pass) with fused RMSNorm
+// prologue and bias / residual / SwiGLU epilogues.  Instantiated per weight dtype in
+// qgemv_q8.hip, qgemv_q4.hip and qgemv_f32.hip so the three compile in parallel.
+//
+// Reference semantics: runtime/vault3.c:499-624 (row_dot, matvec), 656-660 (rmsnorm),
+// 1942-1956 (mlp_gu_run); src/vault_v3_model.py:764-774, 1041-1047, 1139, 1145-1150, 2150-2151.
+//
+// Weights are in the packed row-quad layout (include/vault_amd.h): a 32-weight block of four
+// consecutive rows is one contiguous 64-byte (Q4_0) / 128-byte (Q8_0) / 512-byte (F32) run, and the
+// four fp16 scales of that block are one 8-byte word of the scale plane.  A lane processes whole
+// blocks of one row-quad: one set of 128-bit loads brings 4 x 32 weights, the 32 activations of
+// the block are read from LDS once and used for the four rows.
+//
+// Two mappings:
+//  * row mode (many rows, e.g. the 151665-row LM head): 16 lanes (one DPP row) per row-quad, four
+//    row-quads per wave, four independent waves per workgroup; lanes stride the blocks by 16.
+//  * split-K mode (fewer rows): a whole wave per row-quad, KW waves of the workgroup split the
+//    blocks of the same row-quad (lane stride 64 * KW) and are reduced through LDS.  This keeps
+//    >= ~1500 waves in flight for 1536 x 8960 (down projection) where row mode had 96.
+// Each lane requests the weights of up to U blocks at once, the first ones before the activations
+// are staged, to keep enough bytes in flight for HBM.
+//
+// Arithmetic is fp32 throughout, as in the reference: per block s = sum_j q_j x_j, acc += d * s.
+// Q4_0 nibbles n are converted unsigned (v_cvt_f32_ubyte*) and the -8 offset is applied once per
+// block as acc += d * (sum_j n_j x_j - 8 * sum_j x_j), with sum_j x_j staged in LDS per block.
+// With the RMSNorm prologue the staged activations are lnw[c] * x[c]; sum x^2 is accumulated while
+// staging and the dot products are scaled by inv_rms = 1 / sqrt(mean(x^2) + eps) before the
+// epilogue (the GEMV is linear in its input).
+#pragma once
+
+#include "common.h"
+
+namespace vgx {
+
+enum { EPI_STORE = 0, EPI_ACCUM = 1, EPI_SWIGLU = 2 };
+enum { MODE_ROWS = 0, MODE_SPLITK = 1 };
+
+constexpr int kGemvMaxChunkFloats = 8192;  // activations staged in LDS per chunk (all batch rows)
+constexpr int kGemvPad = 36;               // floats per staged 32-float block (4 floats of padding)
+
+__host__ __device__ constexpr int gemv_quant_bytes(int dt) {
+    return dt == VGX_Q8_0 ? 32 : dt == VGX_Q4_0 ? 16 : dt == VGX_F32 ? 128 : 0;
+}
+
+struct GemvArgs {
+    const uint8_t *w;
+    int nblk;            // 32-weight blocks per row
+    int64_t soff;        // byte offset of the scale plane
+    int64_t n_rq;        // packed row-quads
+    int64_t rows_out;    // output rows (SwiGLU: half the packed rows)
+    const float *x;
+    int64_t ldx;
+    int64_t batch;
+    const float *lnw;    // RMSNorm weight (nullptr: no prologue)
+    float eps;
+    const float *bias;   // may be nullptr
+    float *y;
+    int64_t ldy;
+    int epi;
+};
+
+__device__ __forceinline__ float gemv_cvt_u8(uint32_t w, int k) {
+    switch (k) {  // each pattern maps onto one v_cvt_f32_ubyte{0..3}
+        case 0: return (float)(w & 0xFFu);
+        case 1: return (float)((w >> 8) & 0xFFu);
+        case 2: return (float)((w >> 16) & 0xFFu);
+        default: return (float)(w >> 24);
+    }
+}
+
+__device__ __forceinline__ float gemv_cvt_s8(uint32_t w, int k) { return (float)(int)(int8_t)(w >> (8 * k)); }
+
+// w & 0x0F0F0F0F, opaque to the optimiser: otherwise each later byte extract is folded back into a
+// per-nibble v_bfe_u32, doubling the conversion cost.  With the mask opaque, every nibble converts
+// with a single v_cvt_f32_ubyte{0..3}.
+__device__ __forceinline__ uint32_t gemv_nibble_mask(uint32_t w) {
+    uint32_t r;
+    asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(w));
+    return r;
+}
+
+// Weights of one 32-weight block of a row-quad, held in registers.
+template <int DT>
+struct BlockRegs;
+template <>
+struct BlockRegs<VGX_Q4_0> {
+    uint4 q[4];
+    uint2 s;
+};
+template <>
+struct BlockRegs<VGX_Q8_0> {
+    uint4 q[8];
+    uint2 s;
+};
+template <>
+struct BlockRegs<VGX_F32> {
+    const float4 *p;  // F32 weights are read at use (512 bytes per block would not fit twice)
+};
+
+template <int DT>
+__device__ __forceinline__ void gemv_load(BlockRegs<DT> &r, const uint8_t *__restrict__ W, int64_t soff, int64_t rq,
+                                          int nblk, int64_t gb) {
+    constexpr int QB = gemv_quant_bytes(DT);
+    const uint8_t *qp = W + (rq * nblk + gb) * 4 * QB;
+    if constexpr (DT == VGX_F32) {
+        r.p = reinterpret_cast<const float4 *>(qp);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4 * QB / 16; ++i) r.q[i] = reinterpret_cast<const uint4 *>(qp)[i];
+        r.s = *reinterpret_cast<const uint2 *>(W + soff + (rq * nblk + gb) * 8);
+    }
+}
+
+// acc[r][n] += row r of the block . x_n (staged block xb_n = xs + n * stride_n).
+template <int DT, int NB>
+__device__ __forceinline__ void gemv_block(const BlockRegs<DT> &br, const float *__restrict__ xb, int stride_n,
+                                           const float *__restrict__ xsum, int xsum_stride, float (&acc)[4][NB]) {
+    if constexpr (DT == VGX_F32) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float wv[QK];
+#pragma unroll
+            for (int j4 = 0; j4 < 8; ++j4) {
+                const float4 t = br.p[r * 8 + j4];
+                wv[j4 * 4 + 0] = t.x; wv[j4 * 4 + 1] = t.y; wv[j4 * 4 + 2] = t.z; wv[j4 * 4 + 3] = t.w;
+            }
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const float *xn = xb + n * stride_n;
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < QK; ++j) s = fmaf(wv[j], xn[j], s);
+                acc[r][n] += s;
+            }
+        }
+    } else {
+        const float d[4] = {half_bits_to_float(br.s.x), half_bits_to_float(br.s.x >> 16),
+                            half_bits_to_float(br.s.y), half_bits_to_float(br.s.y >> 16)};
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const float *xn = xb + n * stride_n;
+            float xv[QK];
+#pragma unroll
+            for (int j4 = 0; j4 < 8; ++j4) {
+                const float4 t = *reinterpret_cast<const float4 *>(xn + j4 * 4);
+                xv[j4 * 4 + 0] = t.x; xv[j4 * 4 + 1] = t.y; xv[j4 * 4 + 2] = t.z; xv[j4 * 4 + 3] = t.w;
+            }
+            if constexpr (DT == VGX_Q4_0) {
+                const float s8 = 8.0f * xsum[n * xsum_stride];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t wq[4] = {br.q[r].x, br.q[r].y, br.q[r].z, br.q[r].w};
+                    float s = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t lo = gemv_nibble_mask(wq[k]);
+                        const uint32_t hi = gemv_nibble_mask(wq[k] >> 4);
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+                            s = fmaf(gemv_cvt_u8(lo, t), xv[4 * k + t], s);
+                            s = fmaf(gemv_cvt_u8(hi, t), xv[16 + 4 * k + t], s);
+                        }
+                    }
+                    acc[r][n] = fmaf(d[r], s - s8, acc[r][n]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint4 a = br.q[2 * r], b = br.q[2 * r + 1];
+                    const uint32_t wq[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                    float s = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < 8; ++k)
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) s = fmaf(gemv_cvt_s8(wq[k], t), xv[4 * k + t], s);
+                    acc[r][n] = fmaf(d[r], s, acc[r][n]);
+                }
+            }
+        }
+    }
+}
+
+template <int DT, int NB, int EPI, int MODE, int KW, bool NORM>
+__global__ __launch_bounds__(256) void qgemv_kernel(GemvArgs a, int cbk) {
+    extern __shared__ float smem[];
+    constexpr int LPR = MODE == MODE_ROWS ? 16 : 64;     // lanes per row-quad
+    constexpr int RQW = 64 / LPR;                          // row-quads per wave
+    constexpr int WPG = MODE == MODE_ROWS ? 4 : KW;        // waves per workgroup
+    constexpr int RQG = MODE == MODE_ROWS ? RQW * WPG : 1; // row-quads per workgroup
+    constexpr int NT = 64 * WPG;
+    float *xs = smem;                       // [NB][cbk][kGemvPad]
+    float *xsum = smem + NB * cbk * kGemvPad;   // [NB][cbk]
+    __shared__ float red[WPG][4][NB];
+    __shared__ float rsum[WPG][NB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int li = lane % LPR;
+    const int64_t rq = MODE == MODE_ROWS ? (int64_t)blockIdx.x * RQG + wave * RQW + lane / LPR : (int64_t)blockIdx.x;
+    const bool act = rq < a.n_rq;
+    const int nblk = a.nblk;
+    const int cols = nblk * QK;
+    const int first = MODE == MODE_ROWS ? li : wave * 64 + li;
+    const int stride = MODE == MODE_ROWS ? 16 : 64 * KW;
+
+    float acc[4][NB];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int n = 0; n < NB; ++n) acc[r][n] = 0.0f;
+    float ssq[NB];  // RMSNorm: this thread's part of sum x^2 over the staged activations
+#pragma unroll
+    for (int n = 0; n < NB; ++n) ssq[n] = 0.0f;
+
+    // Each lane issues the loads of U blocks at once (all of its blocks for the model's shapes), the
+    // first batch before the activations are staged, so a lane has up to U x 64 B (Q4_0) /
+    // U x 128 B (Q8_0) of weights in flight.
+    constexpr int U = DT == VGX_Q4_0 ? 4 : DT == VGX_Q8_0 ? 3 : 1;
+    BlockRegs<DT> br[U];
+    int cb = min(cbk, nblk);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        if (act && first + u * stride < cb) gemv_load<DT>(br[u], a.w, a.soff, rq, nblk, first + u * stride);
+
+    for (int c0 = 0; c0 < nblk; c0 += cbk) {
+        cb = min(cbk, nblk - c0);
+        if (c0) __syncthreads();
+        const bool vec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0) && (a.ldx % 4 == 0);
+        if (vec) {
+            // 4 float4 loads per thread in flight per round
+            const int n4 = NB * cb * 8;
+            for (int i0 = tid; i0 < n4; i0 += 4 * NT) {
+                float4 v[4], gw[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int i = i0 + u * NT;
+                    if (i < n4) {
+                        const int n = i / (cb * 8), rem = i - n * cb * 8;
+                        const int64_t c = (int64_t)c0 * QK + rem * 4;
+                        v[u] = *reinterpret_cast<const float4 *>(a.x + n * a.ldx + c);
+                        if constexpr (NORM) gw[u] = *reinterpret_cast<const float4 *>(a.lnw + c);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int i = i0 + u * NT;
+                    if (i < n4) {
+                        const int n = i / (cb * 8), rem = i - n * cb * 8, blk = rem >> 3, j4 = rem & 7;
+                        float4 t = v[u];
+                        if constexpr (NORM) {
+                            const float q2 = fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, t.w * t.w)));
+#pragma unroll
+                            for (int nn = 0; nn < NB; ++nn)
+                                if (nn == n) ssq[nn] += q2;  // static register index
+                            t.x *= gw[u].x; t.y *= gw[u].y; t.z *= gw[u].z; t.w *= gw[u].w;
+                        }
+                        *reinterpret_cast<float4 *>(xs + (n * cbk + blk) * kGemvPad + j4 * 4) = t;
+                    }
+                }
+            }
+        } else {
+            for (int i = tid; i < NB * cb * QK; i += NT) {
+                const int n = i / (cb * QK), rem = i - n * cb * QK, blk = rem >> 5, j = rem & 31;
+                const int64_t c = (int64_t)(c0 + blk) * QK + j;
+                float v = a.x[n * a.ldx + c];
+                if constexpr (NORM) {
+#pragma unroll
+                    for (int nn = 0; nn < NB; ++nn)
+                        if (nn == n) ssq[nn] = fmaf(v, v, ssq[nn]);
+                    v *= a.lnw[c];
+                }
+                xs[(n * cbk + blk) * kGemvPad + j] = v;
+            }
+        }
+        __syncthreads();
+        if constexpr (DT == VGX_Q4_0) {
+            for (int i = tid; i < NB * cb; i += NT) {
+                const int n = i / cb, blk = i - n * cb;
+                const float *p = xs + (n * cbk + blk) * kGemvPad;
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < QK; ++j) s += p[j];
+                xsum[n * cbk + blk] = s;
+            }
+            __syncthreads();
+        }
+        if (!act) continue;
+        for (int b = first; b < cb; b += U * stride) {
+            if (b != first) {
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (b + u * stride < cb) gemv_load<DT>(br[u], a.w, a.soff, rq, nblk, c0 + b + u * stride);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int bb = b + u * stride;
+                if (bb < cb) gemv_block<DT, NB>(br[u], xs + bb * kGemvPad, cbk * kGemvPad, xsum + bb, cbk, acc);
+            }
+        }
+        // first batch of the next chunk
+        const int cn = min(cbk, nblk - c0 - cbk);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (first + u * stride < cn) gemv_load<DT>(br[u], a.w, a.soff, rq, nblk, c0 + cbk + first + u * stride);
+    }
+
+    // RMSNorm: the staged activations were lnw * x, so every dot product is scaled by 1/rms here
+    // (W . (lnw * x * inv) = inv * W . (lnw * x)).
+    if constexpr (NORM) {
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const float t = wave_sum(ssq[n]);
+            if (lane == 0) rsum[wave][n] = t;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            float tot = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WPG; ++w) tot += rsum[w][n];
+            const float inv = 1.0f / sqrtf(tot / (float)cols + a.eps);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r][n] *= inv;
+        }
+    }
+
+    // Reduce over the lanes of the row-quad, then (split-K) over the waves of the workgroup.
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int n = 0; n < NB; ++n) acc[r][n] = LPR == 16 ? row16_sum(acc[r][n]) : wave_sum(acc[r][n]);
+    if constexpr (MODE == MODE_SPLITK && KW > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int n = 0; n < NB; ++n) red[wave][r][n] = acc[r][n];
+        }
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                float s = red[0][r][n];
+#pragma unroll
+                for (int w = 1; w < KW; ++w) s += red[w][r][n];
+                acc[r][n] = s;
+            }
+    }
+    if (!act || li != 0) return;
+    if constexpr (EPI == EPI_SWIGLU) {
+        const int64_t o0 = rq * 2;
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                if (o0 + k >= a.rows_out) continue;
+                const float g = acc[k][n], u = acc[2 + k][n];
+                a.y[n * a.ldy + o0 + k] = g / (1.0f + __expf(-g)) * u;
+            }
+    } else {
+        const int64_t r0 = rq * 4;
+#pragma unroll
+        for (int n = 0; n < NB; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = r0 + r;
+                if (row >= a.rows_out) continue;
+                float v = acc[r][n];
+                if (a.bias) v += a.bias[row];
+                if constexpr (EPI == EPI_ACCUM) v += a.y[n * a.ldy + row];
+                a.y[n * a.ldy + row] = v;
+            }
+    }
+}
+
+// Launch the GEMV over all batch rows (passes of up to 4).  Mode and split chosen from the shape.
+template <int DT>
+int qgemv_launch(GemvArgs a, hipStream_t st) {
+    const bool rows_mode = a.n_rq >= 2048;
+    int kw = 1;
+    if (!rows_mode) kw = a.nblk >= 192 ? 4 : a.nblk >= 96 ? 2 : 1;
+    const bool norm = a.lnw != nullptr;
+    for (int64_t b0 = 0; b0 < a.batch; b0 += 4) {
+        GemvArgs p = a;
+        const int nb = (int)std::min<int64_t>(4, a.batch - b0);
+        p.x = a.x + b0 * a.ldx;
+        p.y = a.y + b0 * a.ldy;
+        const int cbk = std::min(a.nblk, kGemvMaxChunkFloats / (QK * nb));
+        const size_t lds = (size_t)nb * cbk * (kGemvPad + 1) * sizeof(float);
+        const unsigned grid = rows_mode ? (unsigned)((a.n_rq + 15) / 16) : (unsigned)a.n_rq;
+        const unsigned threads = rows_mode ? 256u : 64u * (unsigned)kw;
+#define VGX_GEMV_GO(NBV, EPIV, MODEV, KWV, NORMV)                                                      \
+    hipLaunchKernelGGL((qgemv_kernel<DT, NBV, EPIV, MODEV, KWV, NORMV>), dim3(grid), dim3(threads), lds, st, p, cbk)
+#define VGX_GEMV_KW(NBV, EPIV, NORMV)                                                                  \
+    do {                                                                                               \
+        if (rows_mode) VGX_GEMV_GO(NBV, EPIV, MODE_ROWS, 1, NORMV);                                    \
+        else if (kw == 4) VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 4, NORMV);                               \
+        else if (kw == 2) VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 2, NORMV);                               \
+        else VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 1, NORMV);                                            \
+    } while (0)
+#define VGX_GEMV_EPI(NBV)                                                                              \
+    do {                                                                                               \
+        if (a.epi == EPI_SWIGLU) { if (norm) VGX_GEMV_KW(NBV, EPI_SWIGLU, true); else VGX_GEMV_KW(NBV, EPI_SWIGLU, false); } \
+        else if (a.epi == EPI_ACCUM) { if (norm) VGX_GEMV_KW(NBV, EPI_ACCUM, true); else VGX_GEMV_KW(NBV, EPI_ACCUM, false); } \
+        else { if (norm) VGX_GEMV_KW(NBV, EPI_STORE, true); else VGX_GEMV_KW(NBV, EPI_STORE, false); } \
+    } while (0)
+        switch (nb) {
+            case 1: VGX_GEMV_EPI(1); break;
+            case 2: VGX_GEMV_EPI(2); break;
+            case 3: VGX_GEMV_EPI(3); break;
+            default: VGX_GEMV_EPI(4); break;
+        }
+#undef VGX_GEMV_EPI
+#undef VGX_GEMV_KW
+#undef VGX_GEMV_GO
+        if (hipGetLastError() != hipSuccess) return VGX_E_HIP;
+    }
+    return VGX_OK;
+}
+
+}  // namespace vgx
+
+// One launcher per weight dtype (defined in qgemv_q8.hip / qgemv_q4.hip / qgemv_f32.hip).
+int vgx_detail_qgemv_q8(const vgx::GemvArgs &a, hipStream_t st);
+int vgx_detail_qgemv_q4(const vgx::GemvArgs &a, hipStream_t st);
+int vgx_detail_qgemv_f32(const vgx::GemvArgs &a, hipStream_t st);

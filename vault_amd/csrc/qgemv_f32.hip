@@ -1,0 +1,4 @@
+// F32 instantiation of the GEMV kernels (qgemv.h).
+#include "qgemv.h"
+
+int vgx_detail_qgemv_f32(const vgx::GemvArgs &a, hipStream_t st) { return vgx::qgemv_launch<VGX_F32>(a, st); }

@@ -1,27 +1,13 @@
-// Q8_0 / Q4_0 / F32 weights on gfx950: packing, bit-exact dequant, embedding rows and the
-// HBM-streaming GEMV (batch 1..4 per pass) with fused bias / residual / SwiGLU epilogues.
+// Q8_0 / Q4_0 / F32 weights on gfx950: packing into the row-quad layout, bit-exact dequant,
+// embedding rows, and the C entry points of the GEMV (kernels in qgemv.h).
 //
 // Reference semantics: runtime/vault3.c:499-654 (row_dot, matvec, embed_row), 1942-1956
 // (mlp_gu_run); tools/vlt3.py:98-157 (block layouts and dequantization).
-//
-// GEMV mapping.  A wave owns 4 row-quads (16 rows); each 16-lane DPP row of the wave owns one
-// row-quad and walks its 32-weight blocks with stride 16 (lane l16 takes blocks l16, l16+16, ...).
-// Per block a lane issues one contiguous 64-byte (Q4_0) / 128-byte (Q8_0) load covering the four
-// rows, one 8-byte scale load, and reads the 32 activations of that block from LDS once for all
-// four rows.  The 16 lanes of a row-quad read 16 consecutive blocks: 1 KiB (Q4_0) / 2 KiB (Q8_0)
-// contiguous per wave-row per step.  Partial sums are reduced across the 16 lanes with DPP.
-//
-// Arithmetic is fp32 throughout, as in the reference: per block s = sum_j q_j x_j, acc += d * s.
-// Q4_0 nibbles n are converted unsigned (v_cvt_f32_ubyte*) and the -8 offset is applied once per
-// block as acc += d * (sum_j n_j x_j - 8 * sum_j x_j), with sum_j x_j staged in LDS per block.
-#include "common.h"
+#include "qgemv.h"
 
 using namespace vgx;
 
 namespace {
-
-constexpr int kMaxChunkFloats = 8192;  // activations staged in LDS per chunk (all batch rows)
-constexpr int kPad = 36;               // floats per staged 32-float block (4 floats of padding)
 
 __host__ __device__ constexpr int quant_bytes(int dt) {
     return dt == VGX_Q8_0 ? 32 : dt == VGX_Q4_0 ? 16 : dt == VGX_F32 ? 128 : 0;
@@ -142,252 +128,6 @@ __global__ void embed_kernel(const uint8_t *__restrict__ w, const int64_t *__res
     dequant_block<DT>(w, nblk, soff, r, b, out + t * ldo + b * QK);
 }
 
-// ------------------------------------------------------------------------------------------
-// GEMV
-// ------------------------------------------------------------------------------------------
-
-enum { EPI_STORE = 0, EPI_ACCUM = 1, EPI_SWIGLU = 2 };
-
-__device__ __forceinline__ float cvt_u8(uint32_t w, int k) {
-    // Each pattern maps onto one v_cvt_f32_ubyte{0..3}.
-    switch (k) {
-        case 0: return (float)(w & 0xFFu);
-        case 1: return (float)((w >> 8) & 0xFFu);
-        case 2: return (float)((w >> 16) & 0xFFu);
-        default: return (float)(w >> 24);
-    }
-}
-
-__device__ __forceinline__ float cvt_s8(uint32_t w, int k) { return (float)(int)(int8_t)(w >> (8 * k)); }
-
-// w & 0x0F0F0F0F, opaque to the optimiser: otherwise each later byte extract is folded back
-// into a per-nibble v_bfe_u32, doubling the conversion cost.  With the mask opaque, every
-// nibble converts with a single v_cvt_f32_ubyte{0..3}.
-__device__ __forceinline__ uint32_t nibble_mask(uint32_t w) {
-    uint32_t r;
-    asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(w));
-    return r;
-}
-
-template <int DT, int NB, int EPI>
-__global__ __launch_bounds__(256) void qgemv_kernel(const uint8_t *__restrict__ W, int nblk, int64_t soff,
-                                                     int64_t n_rq, const float *__restrict__ x, int64_t ldx,
-                                                     const float *__restrict__ bias, float *__restrict__ y,
-                                                     int64_t ldy, int64_t rows_out, int cbk, int vec_x) {
-    extern __shared__ float smem[];
-    float *xs = smem;                       // [NB][cbk][kPad]
-    float *xsum = smem + NB * cbk * kPad;   // [NB][cbk]
-    constexpr int QB = quant_bytes(DT);
-
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int l16 = lane & 15;
-    const int qtr = lane >> 4;
-    const int waves = blockDim.x >> 6;
-    const int64_t rq = ((int64_t)blockIdx.x * waves + wave) * 4 + qtr;
-    const bool act = rq < n_rq;
-
-    float acc[4][NB];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int n = 0; n < NB; ++n) acc[r][n] = 0.0f;
-
-    for (int c0 = 0; c0 < nblk; c0 += cbk) {
-        const int cb = min(cbk, nblk - c0);
-        if (c0) __syncthreads();
-        if (vec_x) {
-            for (int i = threadIdx.x; i < NB * cb * 8; i += blockDim.x) {
-                const int n = i / (cb * 8), rem = i - n * cb * 8, blk = rem >> 3, j4 = rem & 7;
-                const float4 v = *reinterpret_cast<const float4 *>(x + n * ldx + (int64_t)(c0 + blk) * QK + j4 * 4);
-                *reinterpret_cast<float4 *>(xs + (n * cbk + blk) * kPad + j4 * 4) = v;
-            }
-        } else {
-            for (int i = threadIdx.x; i < NB * cb * QK; i += blockDim.x) {
-                const int n = i / (cb * QK), rem = i - n * cb * QK, blk = rem >> 5, j = rem & 31;
-                xs[(n * cbk + blk) * kPad + j] = x[n * ldx + (int64_t)(c0 + blk) * QK + j];
-            }
-        }
-        __syncthreads();
-        if constexpr (DT == VGX_Q4_0) {
-            for (int i = threadIdx.x; i < NB * cb; i += blockDim.x) {
-                const int n = i / cb, blk = i - n * cb;
-                const float *p = xs + (n * cbk + blk) * kPad;
-                float s = 0.0f;
-#pragma unroll
-                for (int j = 0; j < QK; ++j) s += p[j];
-                xsum[n * cbk + blk] = s;
-            }
-            __syncthreads();
-        }
-        if (!act) continue;
-        for (int b = l16; b < cb; b += 16) {
-            const int64_t gb = c0 + b;
-            const uint8_t *qp = W + (rq * nblk + gb) * 4 * QB;
-            if constexpr (DT == VGX_Q4_0) {
-                uint4 qv[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) qv[r] = reinterpret_cast<const uint4 *>(qp)[r];
-                const uint2 sv = *reinterpret_cast<const uint2 *>(W + soff + (rq * nblk + gb) * 8);
-                const float d[4] = {half_bits_to_float(sv.x), half_bits_to_float(sv.x >> 16),
-                                    half_bits_to_float(sv.y), half_bits_to_float(sv.y >> 16)};
-#pragma unroll
-                for (int n = 0; n < NB; ++n) {
-                    const float *xb = xs + (n * cbk + b) * kPad;
-                    float xv[QK];
-#pragma unroll
-                    for (int j4 = 0; j4 < 8; ++j4) {
-                        const float4 t = *reinterpret_cast<const float4 *>(xb + j4 * 4);
-                        xv[j4 * 4 + 0] = t.x; xv[j4 * 4 + 1] = t.y; xv[j4 * 4 + 2] = t.z; xv[j4 * 4 + 3] = t.w;
-                    }
-                    const float s8 = 8.0f * xsum[n * cbk + b];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const uint32_t wq[4] = {qv[r].x, qv[r].y, qv[r].z, qv[r].w};
-                        float s = 0.0f;
-#pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            const uint32_t lo = nibble_mask(wq[k]);
-                            const uint32_t hi = nibble_mask(wq[k] >> 4);
-#pragma unroll
-                            for (int t = 0; t < 4; ++t) {
-                                s = fmaf(cvt_u8(lo, t), xv[4 * k + t], s);
-                                s = fmaf(cvt_u8(hi, t), xv[16 + 4 * k + t], s);
-                            }
-                        }
-                        acc[r][n] = fmaf(d[r], s - s8, acc[r][n]);
-                    }
-                }
-            } else if constexpr (DT == VGX_Q8_0) {
-                uint4 qv[4][2];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    qv[r][0] = reinterpret_cast<const uint4 *>(qp)[2 * r];
-                    qv[r][1] = reinterpret_cast<const uint4 *>(qp)[2 * r + 1];
-                }
-                const uint2 sv = *reinterpret_cast<const uint2 *>(W + soff + (rq * nblk + gb) * 8);
-                const float d[4] = {half_bits_to_float(sv.x), half_bits_to_float(sv.x >> 16),
-                                    half_bits_to_float(sv.y), half_bits_to_float(sv.y >> 16)};
-#pragma unroll
-                for (int n = 0; n < NB; ++n) {
-                    const float *xb = xs + (n * cbk + b) * kPad;
-                    float xv[QK];
-#pragma unroll
-                    for (int j4 = 0; j4 < 8; ++j4) {
-                        const float4 t = *reinterpret_cast<const float4 *>(xb + j4 * 4);
-                        xv[j4 * 4 + 0] = t.x; xv[j4 * 4 + 1] = t.y; xv[j4 * 4 + 2] = t.z; xv[j4 * 4 + 3] = t.w;
-                    }
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const uint32_t wq[8] = {qv[r][0].x, qv[r][0].y, qv[r][0].z, qv[r][0].w,
-                                                qv[r][1].x, qv[r][1].y, qv[r][1].z, qv[r][1].w};
-                        float s = 0.0f;
-#pragma unroll
-                        for (int k = 0; k < 8; ++k)
-#pragma unroll
-                            for (int t = 0; t < 4; ++t) s = fmaf(cvt_s8(wq[k], t), xv[4 * k + t], s);
-                        acc[r][n] = fmaf(d[r], s, acc[r][n]);
-                    }
-                }
-            } else {  // F32 weights
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    float wv[QK];
-#pragma unroll
-                    for (int j4 = 0; j4 < 8; ++j4) {
-                        const float4 t = reinterpret_cast<const float4 *>(qp + r * QB)[j4];
-                        wv[j4 * 4 + 0] = t.x; wv[j4 * 4 + 1] = t.y; wv[j4 * 4 + 2] = t.z; wv[j4 * 4 + 3] = t.w;
-                    }
-#pragma unroll
-                    for (int n = 0; n < NB; ++n) {
-                        const float *xb = xs + (n * cbk + b) * kPad;
-                        float s = 0.0f;
-#pragma unroll
-                        for (int j = 0; j < QK; ++j) s = fmaf(wv[j], xb[j], s);
-                        acc[r][n] += s;
-                    }
-                }
-            }
-        }
-    }
-
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int n = 0; n < NB; ++n) acc[r][n] = row16_sum(acc[r][n]);
-
-    if (!act || l16 != 0) return;
-    if constexpr (EPI == EPI_SWIGLU) {
-        const int64_t o0 = rq * 2;
-#pragma unroll
-        for (int n = 0; n < NB; ++n)
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                if (o0 + k >= rows_out) continue;
-                const float g = acc[k][n], u = acc[2 + k][n];
-                y[n * ldy + o0 + k] = g / (1.0f + __expf(-g)) * u;
-            }
-    } else {
-        const int64_t r0 = rq * 4;
-#pragma unroll
-        for (int n = 0; n < NB; ++n)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t row = r0 + r;
-                if (row >= rows_out) continue;
-                float v = acc[r][n];
-                if (bias) v += bias[row];
-                if constexpr (EPI == EPI_ACCUM) v += y[n * ldy + row];
-                y[n * ldy + row] = v;
-            }
-    }
-}
-
-template <int DT, int EPI>
-int launch_qgemv_dt(const void *w, int64_t rows_packed, int64_t rows_out, int64_t cols, const float *x,
-                    int64_t ldx, int64_t batch, const float *bias, float *y, int64_t ldy, hipStream_t st) {
-    const int nblk = (int)(cols / QK);
-    const int64_t n_rq = rows4(rows_packed) / 4;
-    const int64_t soff = DT == VGX_F32 ? 0 : scale_off(DT, rows_packed, cols);
-    // Small matrices: one wave per workgroup spreads the few row-quads over more CUs.
-    const int waves = n_rq >= 4096 ? 4 : 1;
-    const int64_t grid = (n_rq + waves * 4 - 1) / (waves * 4);
-    for (int64_t b0 = 0; b0 < batch; b0 += 4) {
-        const int nb = (int)std::min<int64_t>(4, batch - b0);
-        const int cbk = std::min(nblk, kMaxChunkFloats / (QK * nb));
-        const size_t lds = (size_t)nb * cbk * (kPad + 1) * sizeof(float);
-        const float *xb = x + b0 * ldx;
-        float *yb = y + b0 * ldy;
-        const int vec = ((reinterpret_cast<uintptr_t>(xb) & 15) == 0) && (ldx % 4 == 0);
-#define VGX_QGEMV_CASE(NBV)                                                                               \
-    case NBV:                                                                                             \
-        hipLaunchKernelGGL((qgemv_kernel<DT, NBV, EPI>), dim3((unsigned)grid), dim3(64 * waves), lds, st,    \
-                           static_cast<const uint8_t *>(w), nblk, soff, n_rq, xb, ldx, bias, yb, ldy, rows_out, \
-                           cbk, vec);                                                                     \
-        break;
-        switch (nb) {
-            VGX_QGEMV_CASE(1)
-            VGX_QGEMV_CASE(2)
-            VGX_QGEMV_CASE(3)
-            VGX_QGEMV_CASE(4)
-        }
-#undef VGX_QGEMV_CASE
-        VGX_CHECK_LAUNCH();
-    }
-    return VGX_OK;
-}
-
-template <int EPI>
-int launch_qgemv(int dt, const void *w, int64_t rows_packed, int64_t rows_out, int64_t cols, const float *x,
-                 int64_t ldx, int64_t batch, const float *bias, float *y, int64_t ldy, hipStream_t st) {
-    switch (dt) {
-        case VGX_Q4_0: return launch_qgemv_dt<VGX_Q4_0, EPI>(w, rows_packed, rows_out, cols, x, ldx, batch, bias, y, ldy, st);
-        case VGX_Q8_0: return launch_qgemv_dt<VGX_Q8_0, EPI>(w, rows_packed, rows_out, cols, x, ldx, batch, bias, y, ldy, st);
-        case VGX_F32: return launch_qgemv_dt<VGX_F32, EPI>(w, rows_packed, rows_out, cols, x, ldx, batch, bias, y, ldy, st);
-    }
-    return VGX_E_DTYPE;
-}
-
 inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
 }  // namespace
@@ -503,29 +243,61 @@ int vgx_embed_rows(int dtype, const void *packed, int64_t rows, int64_t cols, co
     return VGX_OK;
 }
 
-int vgx_qlinear(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
-                int64_t batch, const float *bias, float *y, int64_t ldy, int accumulate, void *stream) {
+static int qgemv_dispatch(int dtype, const void *w, int64_t rows_packed, int64_t rows_out, int64_t cols,
+                          const float *x, int64_t ldx, int64_t batch, const float *lnw, float eps, const float *bias,
+                          float *y, int64_t ldy, int epi, void *stream) {
+    GemvArgs a{};
+    a.w = static_cast<const uint8_t *>(w);
+    a.nblk = (int)(cols / QK);
+    a.soff = dtype == VGX_F32 ? 0 : scale_off(dtype, rows_packed, cols);
+    a.n_rq = rows4(rows_packed) / 4;
+    a.rows_out = rows_out;
+    a.x = x;
+    a.ldx = ldx;
+    a.batch = batch;
+    a.lnw = lnw;
+    a.eps = eps;
+    a.bias = bias;
+    a.y = y;
+    a.ldy = ldy;
+    a.epi = epi;
+    hipStream_t st = (hipStream_t)stream;
+    switch (dtype) {
+        case VGX_Q8_0: return vgx_detail_qgemv_q8(a, st);
+        case VGX_Q4_0: return vgx_detail_qgemv_q4(a, st);
+        case VGX_F32: return vgx_detail_qgemv_f32(a, st);
+    }
+    return VGX_E_DTYPE;
+}
+
+int vgx_qlinear_ex(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
+                   int64_t batch, const float *norm_w, float eps, const float *bias, float *y, int64_t ldy,
+                   int epilogue, void *stream) {
     if (!dtype_ok(dtype)) return VGX_E_DTYPE;
     if (!w_packed || !x || !y) return VGX_E_ARG;
-    if (accumulate != 0 && accumulate != 1) return VGX_E_ARG;
+    if (epilogue != VGX_EPI_STORE && epilogue != VGX_EPI_ACCUM && epilogue != VGX_EPI_SWIGLU) return VGX_E_ARG;
+    if (epilogue == VGX_EPI_SWIGLU && bias) return VGX_E_ARG;
     if (rows <= 0 || cols <= 0 || batch < 0 || ldx < cols || ldy < rows) return VGX_E_SIZE;
-    if (cols % QK) return VGX_E_SHAPE;
+    if (cols % QK || (epilogue == VGX_EPI_SWIGLU && rows % 2)) return VGX_E_SHAPE;
     if (cols / QK > (1 << 24)) return VGX_E_LIMIT;
+    if (norm_w && !(eps > 0.0f)) return VGX_E_ARG;
     if (batch == 0) return VGX_OK;
-    hipStream_t st = (hipStream_t)stream;
-    if (accumulate) return launch_qgemv<EPI_ACCUM>(dtype, w_packed, rows, rows, cols, x, ldx, batch, bias, y, ldy, st);
-    return launch_qgemv<EPI_STORE>(dtype, w_packed, rows, rows, cols, x, ldx, batch, bias, y, ldy, st);
+    const int64_t rows_packed = epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows;
+    return qgemv_dispatch(dtype, w_packed, rows_packed, rows, cols, x, ldx, batch, norm_w, eps, bias, y, ldy,
+                          epilogue, stream);
+}
+
+int vgx_qlinear(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
+                int64_t batch, const float *bias, float *y, int64_t ldy, int accumulate, void *stream) {
+    if (accumulate != 0 && accumulate != 1) return VGX_E_ARG;
+    return vgx_qlinear_ex(dtype, w_packed, rows, cols, x, ldx, batch, nullptr, 0.0f, bias, y, ldy,
+                          accumulate ? VGX_EPI_ACCUM : VGX_EPI_STORE, stream);
 }
 
 int vgx_qlinear_swiglu(int dtype, const void *w_gateup_packed, int64_t rows, int64_t cols, const float *x,
                        int64_t ldx, int64_t batch, float *h, int64_t ldh, void *stream) {
-    if (!dtype_ok(dtype)) return VGX_E_DTYPE;
-    if (!w_gateup_packed || !x || !h) return VGX_E_ARG;
-    if (rows <= 0 || cols <= 0 || batch < 0 || ldx < cols || ldh < rows) return VGX_E_SIZE;
-    if (cols % QK || rows % 2) return VGX_E_SHAPE;
-    if (batch == 0) return VGX_OK;
-    return launch_qgemv<EPI_SWIGLU>(dtype, w_gateup_packed, 2 * rows, rows, cols, x, ldx, batch, nullptr, h, ldh,
-                                    (hipStream_t)stream);
+    return vgx_qlinear_ex(dtype, w_gateup_packed, rows, cols, x, ldx, batch, nullptr, 0.0f, nullptr, h, ldh,
+                          VGX_EPI_SWIGLU, stream);
 }
 
 }  // extern "C"

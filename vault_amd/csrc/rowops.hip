@@ -87,6 +87,56 @@ __global__ void rope_qkv_write_kernel(float *__restrict__ q, int64_t ldq, const 
     }
 }
 
+// Decode-step variant: grid.x = B sequences (one token each), grid.y = H + G heads.  The ring slot,
+// RoPE table row and sink slot come from the device step descriptor, so a captured graph replays
+// at every position of a chunk.
+template <int KV>
+__global__ void rope_qkv_write_step_kernel(float *__restrict__ q, int64_t ldq, const float *__restrict__ k, int64_t ldk,
+                                           const float *__restrict__ v, int64_t ldv, int H, int G, int D,
+                                           const float *__restrict__ table, int64_t trs,
+                                           const int32_t *__restrict__ step, void *k_rot, void *k_raw, void *v_dst,
+                                           int64_t dbs, int64_t dgs, int64_t drs, void *sk, void *sv, int64_t sbs,
+                                           int64_t sgs, int64_t srs) {
+    const int64_t t = blockIdx.x;
+    const int hd = blockIdx.y;
+    const int h2 = D / 2;
+    const int64_t slot = step[VGX_STEP_SLOT];
+    const int64_t sink = step[VGX_STEP_SINK_SLOT];
+    const float *cs = table + (int64_t)step[VGX_STEP_TABLE_ROW] * trs;
+    for (int i = threadIdx.x; i < h2; i += blockDim.x) {
+        const float c = cs[i], s = cs[h2 + i];
+        if (hd < H) {
+            float *qp = q + t * ldq + (int64_t)hd * D;
+            const float a = qp[i], b = qp[i + h2];
+            qp[i] = a * c - b * s;
+            qp[i + h2] = b * c + a * s;
+        } else {
+            const int g = hd - H;
+            const float *kp = k + t * ldk + (int64_t)g * D;
+            const float *vp = v + t * ldv + (int64_t)g * D;
+            const float a = kp[i], b = kp[i + h2];
+            const int64_t o = t * dbs + g * dgs + slot * drs;
+            if (k_rot) {
+                store_kv<KV>(k_rot, o + i, a * c - b * s);
+                store_kv<KV>(k_rot, o + i + h2, b * c + a * s);
+            }
+            if (k_raw) {
+                store_kv<KV>(k_raw, o + i, a);
+                store_kv<KV>(k_raw, o + i + h2, b);
+            }
+            store_kv<KV>(v_dst, o + i, vp[i]);
+            store_kv<KV>(v_dst, o + i + h2, vp[i + h2]);
+            if (sink >= 0 && sk) {
+                const int64_t so = t * sbs + g * sgs + sink * srs;
+                store_kv<KV>(sk, so + i, a);
+                store_kv<KV>(sk, so + i + h2, b);
+                store_kv<KV>(sv, so + i, vp[i]);
+                store_kv<KV>(sv, so + i + h2, vp[i + h2]);
+            }
+        }
+    }
+}
+
 // grid.x = n_rows, grid.y = n_outer (chunked); threads over D/2 pairs.
 template <int KV>
 __global__ void rope_rotate_kernel(const void *src, void *dst, int64_t n_outer, int64_t sos, int64_t dos, int D,
@@ -162,6 +212,35 @@ int vgx_rope_qkv_write(int kv_dtype, float *q, int64_t ldq, const float *k, int6
         hipLaunchKernelGGL(rope_qkv_write_kernel<VGX_BF16>, grid, dim3(thr), 0, st, q, ldq, k, ldk, v, ldv, (int)H, (int)G, (int)D,
                            table, table_rstride, k_rot, k_raw, v_dst, dst_tstride, dst_gstride, sink_k_raw, sink_v,
                            n_sink, sink_tstride, sink_gstride);
+    VGX_CHECK_LAUNCH();
+    return VGX_OK;
+}
+
+int vgx_rope_qkv_write_step(int kv_dtype, float *q, int64_t ldq, const float *k, int64_t ldk, const float *v,
+                            int64_t ldv, int64_t B, int64_t H, int64_t G, int64_t D, const float *table,
+                            int64_t table_rstride, const int32_t *step, void *k_rot, void *k_raw, void *v_dst,
+                            int64_t dst_bstride, int64_t dst_gstride, int64_t dst_rstride, void *sink_k_raw,
+                            void *sink_v, int64_t sink_bstride, int64_t sink_gstride, int64_t sink_rstride,
+                            void *stream) {
+    if (kv_dtype != VGX_F32 && kv_dtype != VGX_BF16) return VGX_E_DTYPE;
+    if (!k || !v || !table || !v_dst || !step) return VGX_E_ARG;
+    if (H > 0 && !q) return VGX_E_ARG;
+    if ((sink_k_raw == nullptr) != (sink_v == nullptr)) return VGX_E_ARG;
+    if (B < 0 || H < 0 || G <= 0 || D <= 0 || (D & 1)) return VGX_E_SIZE;
+    if ((H > 0 && ldq < H * D) || ldk < G * D || ldv < G * D) return VGX_E_SIZE;
+    if (B == 0) return VGX_OK;
+    if (B > 0x7FFFFFFF || H + G > 65535) return VGX_E_LIMIT;
+    dim3 grid((unsigned)B, (unsigned)(H + G));
+    const int thr = (int)std::min<int64_t>(256, std::max<int64_t>(32, D / 2));
+    hipStream_t st = (hipStream_t)stream;
+    if (kv_dtype == VGX_F32)
+        hipLaunchKernelGGL(rope_qkv_write_step_kernel<VGX_F32>, grid, dim3(thr), 0, st, q, ldq, k, ldk, v, ldv, (int)H,
+                           (int)G, (int)D, table, table_rstride, step, k_rot, k_raw, v_dst, dst_bstride, dst_gstride,
+                           dst_rstride, sink_k_raw, sink_v, sink_bstride, sink_gstride, sink_rstride);
+    else
+        hipLaunchKernelGGL(rope_qkv_write_step_kernel<VGX_BF16>, grid, dim3(thr), 0, st, q, ldq, k, ldk, v, ldv, (int)H,
+                           (int)G, (int)D, table, table_rstride, step, k_rot, k_raw, v_dst, dst_bstride, dst_gstride,
+                           dst_rstride, sink_k_raw, sink_v, sink_bstride, sink_gstride, sink_rstride);
     VGX_CHECK_LAUNCH();
     return VGX_OK;
 }

@@ -61,8 +61,10 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float *__restrict_
 __global__ __launch_bounds__(64) void score_tail_kernel(const float *__restrict__ h, int64_t ldh,
                                                          const float *__restrict__ w2, const float *__restrict__ b2,
                                                          int64_t hidden, int64_t T, int first,
-                                                         float *__restrict__ out) {
+                                                         float *__restrict__ out,
+                                                         const int32_t *__restrict__ out_index) {
     const int64_t t = blockIdx.x;
+    if (out_index) out += *out_index;
     float r = 0.0f, a = 0.0f;
     for (int64_t i = threadIdx.x; i < hidden; i += 64) {
         const float x0 = h[t * ldh + i], x1 = h[(T + t) * ldh + i];
@@ -102,13 +104,13 @@ int vgx_layernorm(const float *x, int64_t ldx, const float *w, const float *b, f
 }
 
 int vgx_seg_score_tail(const float *h, int64_t ldh, const float *w2, const float *b2, int64_t hidden, int64_t T,
-                       int first, float *out, void *stream) {
+                       int first, float *out, const int32_t *out_index, void *stream) {
     if (!h || !w2 || !b2 || !out) return VGX_E_ARG;
     if (T < 0 || hidden <= 0 || ldh < hidden) return VGX_E_SIZE;
     if (T == 0) return VGX_OK;
     if (T > 0x7FFFFFFF) return VGX_E_LIMIT;
     hipLaunchKernelGGL(score_tail_kernel, dim3((unsigned)T), dim3(64), 0, (hipStream_t)stream, h, ldh, w2, b2, hidden,
-                       T, first ? 1 : 0, out);
+                       T, first ? 1 : 0, out, out_index);
     VGX_CHECK_LAUNCH();
     return VGX_OK;
 }

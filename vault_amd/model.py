@@ -23,7 +23,9 @@ Differences by design:
 """
 from __future__ import annotations
 
+import gc
 import math
+from collections import OrderedDict
 from typing import Dict, List, Optional, Tuple
 
 import numpy as np
@@ -54,6 +56,36 @@ class LayerView:
         if name in LayerView._FIELDS:
             return getattr(self._st, name)[self._li]
         raise AttributeError(name)
+
+
+class StepIO:
+    """Device words of a decode step (the int32 step descriptor, include/vault_amd.h VGX_STEP_*, and
+    the token ids) plus a ring of pinned host buffers they are copied from, stream-ordered before
+    each launch.  A host buffer is reused only after the event of its previous copy completed."""
+
+    RING = 8
+
+    def __init__(self, batch: int, device):
+        self.nbytes = 64 + 8 * batch
+        self.dev = torch.zeros(self.nbytes, dtype=torch.uint8, device=device)
+        self.step = self.dev[:16].view(torch.int32)
+        self.ids = self.dev[64:].view(torch.int64)
+        self.host = [torch.zeros(self.nbytes, dtype=torch.uint8).pin_memory() for _ in range(self.RING)]
+        self.events: List[Optional[torch.cuda.Event]] = [None] * self.RING
+        self.i = 0
+
+    def write(self, ids: torch.Tensor, slot: int, row: int, sink: int, n_cur: int) -> None:
+        k = self.i % self.RING
+        self.i += 1
+        if self.events[k] is not None:
+            self.events[k].synchronize()
+        h = self.host[k]
+        h[:16].view(torch.int32).copy_(torch.tensor([slot, row, sink, n_cur], dtype=torch.int32))
+        h[64:].view(torch.int64).copy_(ids)
+        self.dev.copy_(h, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.events[k] = ev
 
 
 class VAULTv3State:
@@ -98,7 +130,19 @@ class VAULTv3State:
         self.seg_bias_active = False
         self.seg_head_bias: Optional[torch.Tensor] = None
         self.seg_head_bias_hop1: Optional[torch.Tensor] = None
-        self.layers = [LayerView(self, li) for li in range(L)]
+        self.graphs: "OrderedDict[tuple, tuple]" = OrderedDict()   # captured decode steps
+        self._io: Optional[StepIO] = None
+
+    @property
+    def layers(self) -> List[LayerView]:
+        """Per-layer views (built on access: a stored list would make a reference cycle, leaving the
+        state to the cyclic garbage collector, which may run while a decode graph is captured)."""
+        return [LayerView(self, li) for li in range(self.cfg.n_layers)]
+
+    def step_io(self) -> StepIO:
+        if self._io is None:
+            self._io = StepIO(self.batch, self.device)
+        return self._io
 
     def set_pinned(self, n_pin: int) -> None:
         cap = min(self.cfg.window, self.sink_cap)
@@ -143,6 +187,7 @@ class VAULTv3ForCausalLM:
         self.device = weights.device
         self.kv_dtype = kv_dtype
         self.ws = ops.Workspace(self.device)
+        self.use_graphs = True          # replay captured HIP graphs for decode steps
         self._table = None
         self._p0 = 0
         self._ensure_table(sink_capacity(self.cfg) + max(1, self.cfg.seg_budget))
@@ -206,12 +251,11 @@ class VAULTv3ForCausalLM:
             st.seg_bias_active = False
             st.seg_head_bias = None
             st.seg_head_bias_hop1 = None
-        x = ops.embed(self.w.embed, ids.to(self.device), pad_row=0)            # [B, d]
-        h, feats = self._layers(x, st, ids_q=B, pos=pos, c=c, seg_active=seg_active, chunk=False)
+        logits = self._decode(st, ids, pos, c, seg_active)
         if seg_active:
-            self._score(st, feats, T=1, c0=c)
+            st.ema_ready = True
         st.pos = pos + 1
-        return self._logits(h)
+        return logits
 
     @torch.no_grad()
     def prefill(self, input_ids: torch.Tensor, vault_on: bool = False,
@@ -370,6 +414,111 @@ class VAULTv3ForCausalLM:
         st.mem_tok = torch.from_numpy(mem_tok.astype(np.int64))
         st.mem_seg = torch.from_numpy(mem_seg.astype(np.int64))
 
+    # ------------------------------------------------------------------ decode step on the device
+    def _decode(self, st: VAULTv3State, ids: torch.Tensor, pos: int, c: int, seg_active: bool) -> torch.Tensor:
+        """One decode step on the device.  The position-dependent words (ring slot, RoPE row, sink
+        slot, current-chunk length) and the token ids go through a small device buffer written
+        before the launch, so the launch sequence only depends on the chunk configuration; that
+        sequence is captured once per configuration as a HIP graph and replayed at every position
+        of the chunk (re-captured when the configuration changes: at most twice per W tokens)."""
+        cfg = self.cfg
+        W, B = cfg.window, ids.numel()
+        io = st.step_io()
+        eff = W + c if pos >= W else c
+        io.write(ids, slot=c, row=eff - self._p0, sink=pos if pos < st.sink_cap else -1, n_cur=c + 1)
+        n_sk = st.n_pin if pos >= 2 * W else 0
+        n_seg = int(st.mem_pos.numel()) if (pos >= 2 * W and seg_active) else 0
+        n_prev = W if pos >= W else 0
+        bias_on = bool(n_seg and st.seg_bias_active and st.seg_head_bias is not None)
+        ema_first = seg_active and not st.ema_ready
+        spec = (B, n_sk, n_seg, n_prev, seg_active, ema_first)
+        if bias_on or not self.use_graphs:
+            return self._decode_launch(st, spec, bias_on)
+        self._size_workspace(st)
+        key = spec + tuple(t.data_ptr() for t in (st.k_prev, st.k_cur, st.v_prev, st.v_cur, st.kraw_cur, st.k_seg_rot,
+                                                   st.v_seg, st.sc_cur, self._table, self.ws.buf))
+        ent = st.graphs.get(key)
+        if ent is None:
+            # No destructor may run HIP calls while the stream captures: collect garbage now and keep
+            # the collector off during the capture.
+            gc.collect()
+            gc_was_on = gc.isenabled()
+            gc.disable()
+            try:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    out = self._decode_launch(st, spec, False)
+            finally:
+                if gc_was_on:
+                    gc.enable()
+            ent = (g, out)
+            st.graphs[key] = ent
+            while len(st.graphs) > 4:
+                st.graphs.pop(next(iter(st.graphs)))
+        ent[0].replay()
+        return ent[1].clone()
+
+    def _size_workspace(self, st: VAULTv3State) -> None:
+        """Grow the attention workspace before a capture (a captured graph holds its address) to the
+        bound of any decode step of this batch size: B * H * 64 splits * (D + 2) floats."""
+        cfg = self.cfg
+        self.ws.get(st.batch * cfg.n_heads * 64 * (cfg.head_dim + 2) * 4)
+
+    def _decode_launch(self, st: VAULTv3State, spec: tuple, bias_on: bool) -> torch.Tensor:
+        """Every kernel of one decode step (embedding -> 28 layers -> scorer -> LM head) for the chunk
+        configuration ``spec``; position-dependent values are read from the step buffer."""
+        B, n_sk, n_seg, n_prev, seg_active, ema_first = spec
+        cfg, w = self.cfg, self.w
+        H, G, D, d = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_model
+        HD, GD = H * D, G * D
+        io = st.step_io()
+        step, n_cur = io.step, io.step[ops.L.STEP_N_CUR:ops.L.STEP_N_CUR + 1]
+        x = ops.embed(w.embed, io.ids, pad_row=0)                              # [B, d]
+        feats = torch.empty(B, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device) \
+            if seg_active else None
+        ao = torch.empty(B, H, D, dtype=torch.float32, device=self.device)
+        hbuf = torch.empty(B, cfg.d_ff, dtype=torch.float32, device=self.device)
+        table = self._rows(self._p0)
+        scale = 1.0 / math.sqrt(D)
+        for li, lw in enumerate(w.layers):
+            if seg_active and li in cfg.seg_layers:
+                j = cfg.seg_layers.index(li)
+                feats[:, j * d:(j + 1) * d].copy_(x)
+            q, k, v = self._qkv(lw, x, B)
+            ops.rope_qkv_write_step(q, k, v, table, D, step, st.k_cur[li], st.kraw_cur[li], st.v_cur[li],
+                                    st.k_sink_raw[li], st.v_sink[li])
+            spans = []
+            if n_sk:
+                spans.append((st.k_sink_rot[li][:, :, :n_sk], st.v_sink[li][:, :, :n_sk]))
+            bias, bspan = None, -1
+            if n_seg:
+                bias = self._seg_bias(st, li, n_seg) if bias_on else None
+                bspan = len(spans)
+                spans.append((st.k_seg_rot[li][:, :, :n_seg], st.v_seg[li][:, :, :n_seg]))
+            if n_prev:
+                spans.append((st.k_prev[li], st.v_prev[li]))
+            spans.append((st.k_cur[li], st.v_cur[li], n_cur))
+            ops.attn_decode(q, spans, out=ao, bias=bias, bias_span=bspan, scale=scale, ws=self.ws)
+            ops.qlinear(lw.wo, ao.view(B, HD), out=x, accumulate=True)
+            ops.qlinear_swiglu(lw.wgu, x, out=hbuf, norm=(lw.ln2, cfg.rms_eps))
+            ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
+        if seg_active:
+            self._score(st, feats, T=1, c0=0, first=ema_first, out_index=step[ops.L.STEP_SLOT:ops.L.STEP_SLOT + 1])
+        return self._logits(x)
+
+    def _qkv(self, lw, x: torch.Tensor, N: int):
+        """q [N,H,D], k [N,G,D], v [N,G,D] views of the fused RMSNorm + QKV projection outputs."""
+        cfg = self.cfg
+        H, G, D = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+        HD, GD = H * D, G * D
+        ln1 = (lw.ln1, cfg.rms_eps)
+        if lw.wq is None:
+            qkv = ops.qlinear(lw.wqkv, x, bias=lw.bqkv, norm=ln1)
+            return qkv[:, :HD].view(N, H, D), qkv[:, HD:HD + GD].view(N, G, D), qkv[:, HD + GD:].view(N, G, D)
+        q = ops.qlinear(lw.wq, x, bias=lw.bq, norm=ln1).view(N, H, D)
+        kv = ops.qlinear(lw.wqkv, x, bias=lw.bqkv, norm=ln1)
+        return q, kv[:, :GD].view(N, G, D), kv[:, GD:].view(N, G, D)
+
     # ------------------------------------------------------------------ device compute
     def _seg_bias(self, st: VAULTv3State, li: int, M: int) -> Optional[torch.Tensor]:
         """Per-head bias on the segment span (src/vault_v3_model.py:1115-1132)."""
@@ -380,33 +529,21 @@ class VAULTv3ForCausalLM:
             else st.seg_head_bias
         return hb.reshape(self.cfg.n_heads, -1).to(torch.float32).contiguous()
 
-    def _layers(self, x: torch.Tensor, st: VAULTv3State, ids_q: int, pos: int, c: int, seg_active: bool,
-                chunk: bool, clen: int = 0) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-        """Run all layers on x [N, d] in place.  Decode (chunk=False): N = batch, one token per sequence
-        at position pos (slot c).  Chunk prefill (chunk=True, batch 1): N = clen tokens at slots [0, clen)
-        of chunk pos // W."""
+    def _layers(self, x: torch.Tensor, st: VAULTv3State, pos: int, seg_active: bool) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """Chunk prefill (batch 1): run all layers in place on x [N, d], the N tokens at slots [0, N)
+        of chunk pos // W (src/vault_v3_model.py:2045-2096)."""
         cfg, w = self.cfg, self.w
         W, H, G, D, d = cfg.window, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_model
         N = x.shape[0]
-        HD, GD = H * D, G * D
+        HD = H * D
         ci = pos // W
         feats = None
         if seg_active:
             feats = torch.empty(N, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device)
-        # attention extents
-        if chunk:
-            n_sk = st.n_pin if ci >= 2 else 0
-            n_seg = int(st.mem_pos.numel()) if (seg_active and ci >= 2) else 0
-            n_prev = W if ci >= 1 else 0
-            eff0 = W if ci >= 1 else 0
-            table, trs = self._rows(eff0), D
-        else:
-            n_sk = st.n_pin if pos >= 2 * W else 0
-            n_seg = int(st.mem_pos.numel()) if (pos >= 2 * W and seg_active) else 0
-            n_prev = W if pos >= W else 0
-            eff = W + c if pos >= W else c
-            table, trs = self._rows(eff), 0
-        u = torch.empty(N, d, dtype=torch.float32, device=self.device)
+        n_sk = st.n_pin if ci >= 2 else 0
+        n_seg = int(st.mem_pos.numel()) if (seg_active and ci >= 2) else 0
+        n_prev = W if ci >= 1 else 0
+        table, trs = self._rows(W if ci >= 1 else 0), D
         ao = torch.empty(N, H, D, dtype=torch.float32, device=self.device)
         hbuf = torch.empty(N, cfg.d_ff, dtype=torch.float32, device=self.device)
         scale = 1.0 / math.sqrt(D)
@@ -414,68 +551,42 @@ class VAULTv3ForCausalLM:
             if seg_active and li in cfg.seg_layers:
                 j = cfg.seg_layers.index(li)
                 feats[:, j * d:(j + 1) * d].copy_(x)
-            ops.rmsnorm(x, lw.ln1, cfg.rms_eps, out=u)
-            if lw.wq is None:
-                qkv = ops.qlinear(lw.wqkv, u, bias=lw.bqkv)
-                q = qkv[:, :HD].view(N, H, D)
-                k = qkv[:, HD:HD + GD].view(N, G, D)
-                v = qkv[:, HD + GD:].view(N, G, D)
-            else:
-                q = ops.qlinear(lw.wq, u, bias=lw.bq).view(N, H, D)
-                kv = ops.qlinear(lw.wqkv, u, bias=lw.bqkv)
-                k = kv[:, :GD].view(N, G, D)
-                v = kv[:, GD:].view(N, G, D)
-            kc, kr, vc = st.k_cur[li], st.kraw_cur[li], st.v_cur[li]          # [B, G, W, D]
-            ks, vs = st.k_sink_raw[li], st.v_sink[li]                          # [B, G, S_cap, D]
-            if chunk:
-                take = max(0, min(N, st.sink_cap - pos))
-                ops.rope_qkv_write(q, k, v, table, trs, kc[0], kr[0], vc[0], D, kc.stride(1),
-                                   ks[0, :, pos] if take else None, vs[0, :, pos] if take else None, take,
-                                   D, ks.stride(1))
-            else:
-                take = N if pos < st.sink_cap else 0
-                ops.rope_qkv_write(q, k, v, table, trs, kc[:, :, c], kr[:, :, c], vc[:, :, c], kc.stride(0),
-                                   kc.stride(1), ks[:, :, pos] if take else None, vs[:, :, pos] if take else None,
-                                   take, ks.stride(0), ks.stride(1))
+            q, k, v = self._qkv(lw, x, N)
+            kc, kr, vc = st.k_cur[li], st.kraw_cur[li], st.v_cur[li]          # [1, G, W, D]
+            ks, vs = st.k_sink_raw[li], st.v_sink[li]                          # [1, G, S_cap, D]
+            take = max(0, min(N, st.sink_cap - pos))
+            ops.rope_qkv_write(q, k, v, table, trs, kc[0], kr[0], vc[0], D, kc.stride(1),
+                               ks[0, :, pos] if take else None, vs[0, :, pos] if take else None, take,
+                               D, ks.stride(1))
             spans = []
             if n_sk:
                 spans.append((st.k_sink_rot[li][:, :, :n_sk], st.v_sink[li][:, :, :n_sk]))
-            bias, bspan = None, -1
             if n_seg:
-                bias = self._seg_bias(st, li, n_seg) if not chunk else None
-                bspan = len(spans)
                 spans.append((st.k_seg_rot[li][:, :, :n_seg], st.v_seg[li][:, :, :n_seg]))
             if n_prev:
                 spans.append((st.k_prev[li], st.v_prev[li]))
-            if chunk:
-                spans.append((kc[:, :, :N], st.v_cur[li][:, :, :N]))
-                ops.attn_decode(q, spans, out=ao, bias=bias, bias_span=bspan, scale=scale, ws=self.ws, causal_base=0)
-            else:
-                spans.append((kc[:, :, :c + 1], st.v_cur[li][:, :, :c + 1]))
-                ops.attn_decode(q, spans, out=ao, bias=bias, bias_span=bspan, scale=scale, ws=self.ws)
+            spans.append((kc[:, :, :N], st.v_cur[li][:, :, :N]))
+            ops.attn_decode(q, spans, out=ao, scale=scale, ws=self.ws, causal_base=0)
             ops.qlinear(lw.wo, ao.view(N, HD), out=x, accumulate=True)
-            ops.rmsnorm(x, lw.ln2, cfg.rms_eps, out=u)
-            ops.qlinear_swiglu(lw.wgu, u, out=hbuf)
+            ops.qlinear_swiglu(lw.wgu, x, out=hbuf, norm=(lw.ln2, cfg.rms_eps))
             ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
         return x, feats
 
-    def _score(self, st: VAULTv3State, feats: torch.Tensor, T: int, c0: int) -> None:
-        """Habituated segment scores of T tokens into sc_cur[c0:c0+T]
-        (src/vault_v3_model.py:1224-1247, 2294-2305)."""
+    def _score(self, st: VAULTv3State, feats: torch.Tensor, T: int, c0: int, first: bool,
+               out_index: Optional[torch.Tensor] = None) -> None:
+        """Habituated segment scores of T tokens into sc_cur[c0:c0+T], shifted by the device slot
+        ``out_index`` when given (src/vault_v3_model.py:1224-1247, 2294-2305)."""
         sw = self.w.scorer
         fd = feats.shape[1]
-        first = not st.ema_ready
         rows = torch.empty(2 * T, fd, dtype=torch.float32, device=self.device)
         ops.ema_habituate(feats, rows[T:], st.seg_feat_ema, first)
         ops.layernorm(feats, sw.ln_w, sw.ln_b, 1e-5, rows[:T])
         ops.layernorm(rows[T:], sw.ln_w, sw.ln_b, 1e-5, rows[T:])
         h1 = ops.qlinear(sw.w1, rows, bias=sw.b1)
-        ops.seg_score_tail(h1, sw.w2, sw.b2, T, first, st.sc_cur[c0:c0 + T])
-        st.ema_ready = True
+        ops.seg_score_tail(h1, sw.w2, sw.b2, T, first, st.sc_cur[c0:c0 + T], out_index=out_index)
 
     def _logits(self, h: torch.Tensor) -> torch.Tensor:
-        u = ops.rmsnorm(h, self.w.norm, self.cfg.rms_eps)
-        return ops.qlinear(self.w.embed, u)
+        return ops.qlinear(self.w.embed, h, norm=(self.w.norm, self.cfg.rms_eps))
 
     def _chunk_recurrent(self, input_ids: torch.Tensor, bud: int, all_logits: bool):
         """Chunk-recurrent prefill / forward for batch 1 (src/vault_v3_model.py:1938-2116)."""
@@ -510,9 +621,10 @@ class VAULTv3ForCausalLM:
                         slen = 0
                 st.cur_seg_id, st.seg_len = s_loc, slen
             x = ops.embed(self.w.embed, ch.to(self.device), pad_row=0)
-            x, feats = self._layers(x, st, ids_q=clen, pos=r0, c=0, seg_active=seg_active, chunk=True)
+            x, feats = self._layers(x, st, pos=r0, seg_active=seg_active)
             if seg_active:
-                self._score(st, feats, T=clen, c0=0)
+                self._score(st, feats, T=clen, c0=0, first=not st.ema_ready)
+                st.ema_ready = True
             if all_logits:
                 outs.append(x)
             last = x[-1:]

@@ -5,7 +5,7 @@ into the HIP library (no torch fallback).  Tensors must live on a ROCm device.
 """
 from __future__ import annotations
 
-from typing import Optional
+from typing import Optional, Tuple
 
 import numpy as np
 import torch
@@ -104,18 +104,15 @@ class QWeight:
         return rows * (self.cols // 32) * BLOCK_BYTES[self.dtype]
 
 
-def qlinear(w: QWeight, x: torch.Tensor, bias: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
-            accumulate: bool = False) -> torch.Tensor:
-    """y = x @ W^T (+ bias); with ``accumulate`` the product is added into ``out``."""
-    if w.gateup:
-        raise ValueError("use qlinear_swiglu for gate/up tensors")
+def _gemv(w: QWeight, x: torch.Tensor, out: Optional[torch.Tensor], epi: int, bias: Optional[torch.Tensor],
+          norm: Optional[Tuple[torch.Tensor, float]]) -> torch.Tensor:
     _need(x, torch.float32, "x")
     x2 = x.reshape(-1, w.cols) if x.dim() != 2 else x
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
     B = x2.shape[0]
     if out is None:
-        if accumulate:
+        if epi == L.EPI_ACCUM:
             raise ValueError("accumulate needs out")
         out = torch.empty(B, w.rows, dtype=torch.float32, device=x.device)
     y2 = out.view(-1, w.rows)
@@ -123,26 +120,30 @@ def qlinear(w: QWeight, x: torch.Tensor, bias: Optional[torch.Tensor] = None, ou
         raise ValueError("out must have unit stride")
     if bias is not None:
         _need(bias, torch.float32, "bias")
-    L.check(L.load().vgx_qlinear(w.dtype, w.packed.data_ptr(), w.rows, w.cols, x2.data_ptr(), x2.stride(0), B,
-                                 _ptr(bias), y2.data_ptr(), y2.stride(0), 1 if accumulate else 0,
-                                 _stream(x.device)), "vgx_qlinear")
+    nw, eps = (None, 0.0) if norm is None else norm
+    if nw is not None:
+        _need(nw, torch.float32, "norm weight")
+    L.check(L.load().vgx_qlinear_ex(w.dtype, w.packed.data_ptr(), w.rows, w.cols, x2.data_ptr(), x2.stride(0), B,
+                                    _ptr(nw), float(eps), _ptr(bias), y2.data_ptr(), y2.stride(0), epi,
+                                    _stream(x.device)), "vgx_qlinear_ex")
     return out
 
 
-def qlinear_swiglu(w: QWeight, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+def qlinear(w: QWeight, x: torch.Tensor, bias: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+            accumulate: bool = False, norm: Optional[Tuple[torch.Tensor, float]] = None) -> torch.Tensor:
+    """y = u @ W^T (+ bias) with u = x, or u = RMSNorm(x) with norm = (weight, eps); with ``accumulate``
+    the product is added into ``out``."""
+    if w.gateup:
+        raise ValueError("use qlinear_swiglu for gate/up tensors")
+    return _gemv(w, x, out, L.EPI_ACCUM if accumulate else L.EPI_STORE, bias, norm)
+
+
+def qlinear_swiglu(w: QWeight, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                   norm: Optional[Tuple[torch.Tensor, float]] = None) -> torch.Tensor:
+    """h = silu(u @ Wg^T) * (u @ Wu^T), u = x or RMSNorm(x)."""
     if not w.gateup:
         raise ValueError("qlinear_swiglu needs a gate/up tensor")
-    _need(x, torch.float32, "x")
-    x2 = x.reshape(-1, w.cols)
-    if x2.stride(-1) != 1:
-        x2 = x2.contiguous()
-    B = x2.shape[0]
-    if out is None:
-        out = torch.empty(B, w.rows, dtype=torch.float32, device=x.device)
-    h2 = out.view(-1, w.rows)
-    L.check(L.load().vgx_qlinear_swiglu(w.dtype, w.packed.data_ptr(), w.rows, w.cols, x2.data_ptr(), x2.stride(0),
-                                        B, h2.data_ptr(), h2.stride(0), _stream(x.device)), "vgx_qlinear_swiglu")
-    return out
+    return _gemv(w, x, out, L.EPI_SWIGLU, None, norm)
 
 
 def embed(w: QWeight, ids: torch.Tensor, pad_row: int = 0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -171,8 +172,9 @@ class Workspace:
         self.buf = torch.empty(0, dtype=torch.uint8, device=device)
 
     def get(self, nbytes: int) -> torch.Tensor:
+        """At least ``nbytes`` bytes (256-byte aligned, zero-filled when first allocated)."""
         if self.buf.numel() < nbytes:
-            self.buf = torch.empty(max(nbytes, 2 * self.buf.numel()), dtype=torch.uint8, device=self.device)
+            self.buf = torch.zeros(max(nbytes, 2 * self.buf.numel()), dtype=torch.uint8, device=self.device)
         return self.buf
 
 
@@ -180,8 +182,9 @@ def attn_decode(q: torch.Tensor, spans, out: Optional[torch.Tensor] = None, bias
                 bias_span: int = -1, scale: Optional[float] = None, ws: Optional[Workspace] = None,
                 causal_base: int = -1) -> torch.Tensor:
     """q: [B, H, D] fp32 post-RoPE (heads and dims contiguous, any batch stride).  spans: list of
-    (K, V) views shaped [B, G, n, D] (unit stride in D and n; any batch / group stride; batch stride 0
-    shares one span across entries).  bias: [H, n_bias] fp32 or None.  causal_base >= 0: the last
+    (K, V) or (K, V, n_dev) with views shaped [B, G, n, D] (unit stride in D and n; any batch / group
+    stride; batch stride 0 shares one span across entries) and n_dev an optional device int32 (one
+    element) capping the span's length on the device.  bias: [H, n_bias] fp32 or None.  causal_base >= 0: the last
     span is causal (entry b sees causal_base + b + 1 keys).  Returns [B, H, D] fp32."""
     _need(q, torch.float32, "q")
     B, H, D = q.shape
@@ -191,7 +194,9 @@ def attn_decode(q: torch.Tensor, spans, out: Optional[torch.Tensor] = None, bias
     arr = (L.KVSpan * 4)()
     n_tot = 0
     G = None
-    for i, (k, v) in enumerate(spans):
+    for i, span in enumerate(spans):
+        k, v = span[0], span[1]
+        dyn = span[2] if len(span) > 2 else None
         if kv_dt is None:
             kv_dt = KV_DTYPES[k.dtype]
         if KV_DTYPES[k.dtype] != kv_dt or v.dtype != k.dtype:
@@ -208,7 +213,9 @@ def attn_decode(q: torch.Tensor, spans, out: Optional[torch.Tensor] = None, bias
         G = k.shape[1]
         n = k.shape[2]
         bs = k.stride(0) if k.shape[0] == B and B > 1 else 0
-        arr[i] = L.KVSpan(k.data_ptr(), v.data_ptr(), n, bs, k.stride(1))
+        if dyn is not None and (dyn.dtype != torch.int32 or not dyn.is_cuda):
+            raise ValueError("dynamic span length must be a device int32 tensor")
+        arr[i] = L.KVSpan(k.data_ptr(), v.data_ptr(), n, bs, k.stride(1), _ptr(dyn))
         n_tot += n
     if out is None:
         out = torch.empty(B, H, D, dtype=torch.float32, device=q.device)
@@ -300,6 +307,32 @@ def layernorm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float, out
     return out
 
 
-def seg_score_tail(h: torch.Tensor, w2: torch.Tensor, b2: torch.Tensor, T: int, first: bool, out: torch.Tensor) -> None:
+def seg_score_tail(h: torch.Tensor, w2: torch.Tensor, b2: torch.Tensor, T: int, first: bool, out: torch.Tensor,
+                   out_index: Optional[torch.Tensor] = None) -> None:
+    """Scores of T tokens into out[0:T] (shifted by the device int32 ``out_index`` when given)."""
     L.check(L.load().vgx_seg_score_tail(h.data_ptr(), h.stride(0), w2.data_ptr(), b2.data_ptr(), h.shape[1], T,
-                                        1 if first else 0, out.data_ptr(), _stream(h.device)), "vgx_seg_score_tail")
+                                        1 if first else 0, out.data_ptr(), _ptr(out_index), _stream(h.device)),
+            "vgx_seg_score_tail")
+
+
+def rope_qkv_write_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: torch.Tensor, table_rstride: int,
+                        step: torch.Tensor, k_rot: Optional[torch.Tensor], k_raw: Optional[torch.Tensor],
+                        v_dst: torch.Tensor, sink_k: Optional[torch.Tensor], sink_v: Optional[torch.Tensor]) -> None:
+    """Decode-step RoPE + ring write for B sequences (one token each).  q [B,H,D], k/v [B,G,D] fp32;
+    k_rot / k_raw / v_dst: ring tensors [B, G, W, D]; sink_k / sink_v: [B, G, S_cap, D]; slot, table
+    row and sink slot come from the device descriptor ``step`` (int32, VGX_STEP_* words)."""
+    B, G, D = k.shape
+    H = q.shape[1]
+    for t in (q, k, v):
+        if t.stride(2) != 1 or t.stride(1) != D:
+            raise ValueError("q/k/v need contiguous heads")
+    for t in (k_rot, k_raw, sink_k):
+        if t is not None and t.stride(2) != D:
+            raise ValueError("ring rows must be contiguous")
+    kv_dt = KV_DTYPES[v_dst.dtype]
+    sk_b, sk_g, sk_r = (sink_k.stride(0), sink_k.stride(1), sink_k.stride(2)) if sink_k is not None else (0, 0, 0)
+    L.check(L.load().vgx_rope_qkv_write_step(
+        kv_dt, q.data_ptr(), q.stride(0), k.data_ptr(), k.stride(0), v.data_ptr(), v.stride(0), B, H, G, D,
+        table.data_ptr(), table_rstride, step.data_ptr(), _ptr(k_rot), _ptr(k_raw), v_dst.data_ptr(),
+        v_dst.stride(0), v_dst.stride(1), v_dst.stride(2), _ptr(sink_k), _ptr(sink_v), sk_b, sk_g, sk_r,
+        _stream(k.device)), "vgx_rope_qkv_write_step")
