@@ -239,11 +239,15 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
 }
 
 // One workgroup per (b, h): out = sum_s e^{m_s - M} acc_s / sum_s e^{m_s - M} l_s.  The split
-// weights are computed once into LDS; every thread then sums its dimension over the splits with
-// eight loads in flight.
-__global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ part, float *__restrict__ out,
-                                                          int H, int G, int D, int n_splits) {
+// weights are computed once into LDS; the D x 2 threads then each sum one dimension over half of
+// the splits with up to 16 loads in flight, and the halves are added through LDS.
+constexpr int kMergeThreads = 256;
+
+__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *__restrict__ part,
+                                                                   float *__restrict__ out, int H, int G, int D,
+                                                                   int n_splits) {
     __shared__ float wgt[kMaxSplits];
+    __shared__ float half_sum[kMergeThreads];
     __shared__ float inv_l;
     const int bh = blockIdx.x;
     const int b = bh / H, h = bh - b * H;
@@ -261,17 +265,22 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict
         if (s == 0) inv_l = 1.0f / L;
     }
     __syncthreads();
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float a = 0.0f;
-        int s = 0;
-        for (; s + 8 <= n_splits; s += 8) {
-            float v[8];
+    const int parts = kMergeThreads / D;               // 2 for D = 128, 4 for D = 64
+    const int d = threadIdx.x % D, pi = threadIdx.x / D;
+    const int s0 = pi * n_splits / parts, s1 = (pi + 1) * n_splits / parts;
+    float a = 0.0f;
+    for (int s = s0; s < s1; s += 16) {
+        float v[16];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = p0[(s + u) * stride + d];
+        for (int u = 0; u < 16; ++u) v[u] = s + u < s1 ? p0[(s + u) * stride + d] : 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) a = fmaf(wgt[s + u], v[u], a);
-        }
-        for (; s < n_splits; ++s) a = fmaf(wgt[s], p0[s * stride + d], a);
+        for (int u = 0; u < 16; ++u)
+            if (s + u < s1) a = fmaf(wgt[s + u], v[u], a);
+    }
+    half_sum[threadIdx.x] = a;
+    __syncthreads();
+    if (pi == 0) {
+        for (int p = 1; p < parts; ++p) a += half_sum[p * D + d];
         out[((int64_t)b * H + h) * D + d] = a * inv_l;
     }
 }
@@ -386,8 +395,8 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
     if (!ok) return VGX_E_LIMIT;
     VGX_CHECK_LAUNCH();
     if (ns > 1) {
-        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * H)), dim3(128), 0, st, part, out, (int)H, (int)G,
-                           (int)D, ns);
+        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * H)), dim3(kMergeThreads), 0, st, part, out, (int)H,
+                           (int)G, (int)D, ns);
         VGX_CHECK_LAUNCH();
     }
     return VGX_OK;

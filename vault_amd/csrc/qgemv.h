@@ -11,18 +11,18 @@
 // blocks of one row-quad: one set of 128-bit loads brings 4 x 32 weights, the 32 activations of
 // the block are read from LDS once and used for the four rows.
 //
-// Two mappings:
-//  * row mode (many rows, e.g. the 151665-row LM head): 16 lanes (one DPP row) per row-quad, four
-//    row-quads per wave, four independent waves per workgroup; lanes stride the blocks by 16.
-//  * split-K mode (fewer rows): a whole wave per row-quad, KW waves of the workgroup split the
-//    blocks of the same row-quad (lane stride 64 * KW) and are reduced through LDS.  This keeps
-//    >= ~1500 waves in flight for 1536 x 8960 (down projection) where row mode had 96.
+// Two mappings (KW waves split the blocks of the same row-quads and are reduced through LDS):
+//  * row mode (many rows: the gate/up pair, the 151665-row LM head): 16 lanes (one DPP row) per
+//    row-quad, four row-quads per wave, 4 x KW waves per workgroup (KW = 1 is launched);
+//  * split-K mode (fewer rows): a whole wave per row-quad, KW waves per workgroup over its blocks
+//    (lane stride 64 * KW).  This keeps ~1500 waves in flight for 1536 x 8960 (down projection).
 // Each lane requests the weights of up to U blocks at once, the first ones before the activations
 // are staged, to keep enough bytes in flight for HBM.
 //
 // Arithmetic is fp32 throughout, as in the reference: per block s = sum_j q_j x_j, acc += d * s.
 // Q4_0 nibbles n are converted unsigned (v_cvt_f32_ubyte*) and the -8 offset is applied once per
-// block as acc += d * (sum_j n_j x_j - 8 * sum_j x_j), with sum_j x_j staged in LDS per block.
+// block as acc += d * (sum_j n_j x_j - 8 * sum_j x_j), sum_j x_j summed by the lane from the same
+// 32 staged activations.
 // With the RMSNorm prologue the staged activations are lnw[c] * x[c]; sum x^2 is accumulated while
 // staging and the dot products are scaled by inv_rms = 1 / sqrt(mean(x^2) + eps) before the
 // epilogue (the GEMV is linear in its input).
@@ -114,7 +114,7 @@ __device__ __forceinline__ void gemv_load(BlockRegs<DT> &r, const uint8_t *__res
 // acc[r][n] += row r of the block . x_n (staged block xb_n = xs + n * stride_n).
 template <int DT, int NB>
 __device__ __forceinline__ void gemv_block(const BlockRegs<DT> &br, const float *__restrict__ xb, int stride_n,
-                                           const float *__restrict__ xsum, int xsum_stride, float (&acc)[4][NB]) {
+                                           float (&acc)[4][NB]) {
     if constexpr (DT == VGX_F32) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -146,7 +146,10 @@ __device__ __forceinline__ void gemv_block(const BlockRegs<DT> &br, const float 
                 xv[j4 * 4 + 0] = t.x; xv[j4 * 4 + 1] = t.y; xv[j4 * 4 + 2] = t.z; xv[j4 * 4 + 3] = t.w;
             }
             if constexpr (DT == VGX_Q4_0) {
-                const float s8 = 8.0f * xsum[n * xsum_stride];
+                float xs_sum = 0.0f;  // sum of the block's activations, for the -8 nibble offset
+#pragma unroll
+                for (int j = 0; j < QK; ++j) xs_sum += xv[j];
+                const float s8 = 8.0f * xs_sum;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const uint32_t wq[4] = {br.q[r].x, br.q[r].y, br.q[r].z, br.q[r].w};
@@ -181,28 +184,29 @@ __device__ __forceinline__ void gemv_block(const BlockRegs<DT> &br, const float 
 }
 
 template <int DT, int NB, int EPI, int MODE, int KW, bool NORM>
-__global__ __launch_bounds__(256) void qgemv_kernel(GemvArgs a, int cbk) {
+__global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_kernel(GemvArgs a, int cbk) {
     extern __shared__ float smem[];
     constexpr int LPR = MODE == MODE_ROWS ? 16 : 64;     // lanes per row-quad
     constexpr int RQW = 64 / LPR;                          // row-quads per wave
-    constexpr int WPG = MODE == MODE_ROWS ? 4 : KW;        // waves per workgroup
-    constexpr int RQG = MODE == MODE_ROWS ? RQW * WPG : 1; // row-quads per workgroup
+    constexpr int RW = MODE == MODE_ROWS ? 4 : 1;          // waves with distinct row-quads
+    constexpr int WPG = RW * KW;                           // waves per workgroup
+    constexpr int RQG = RQW * RW;                          // row-quads per workgroup
     constexpr int NT = 64 * WPG;
-    float *xs = smem;                       // [NB][cbk][kGemvPad]
-    float *xsum = smem + NB * cbk * kGemvPad;   // [NB][cbk]
-    __shared__ float red[WPG][4][NB];
+    float *xs = smem;                                      // [NB][cbk][kGemvPad]
+    __shared__ float red[WPG][RQW][4][NB];
     __shared__ float rsum[WPG][NB];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int li = lane % LPR;
-    const int64_t rq = MODE == MODE_ROWS ? (int64_t)blockIdx.x * RQG + wave * RQW + lane / LPR : (int64_t)blockIdx.x;
+    const int rw = wave / KW, ks = wave - rw * KW;         // row-wave, K-split index
+    const int li = lane % LPR, rqi = lane / LPR;
+    const int64_t rq = (int64_t)blockIdx.x * RQG + rw * RQW + rqi;
     const bool act = rq < a.n_rq;
     const int nblk = a.nblk;
     const int cols = nblk * QK;
-    const int first = MODE == MODE_ROWS ? li : wave * 64 + li;
-    const int stride = MODE == MODE_ROWS ? 16 : 64 * KW;
+    const int first = ks * LPR + li;
+    const int stride = LPR * KW;
 
     float acc[4][NB];
 #pragma unroll
@@ -216,7 +220,9 @@ __global__ __launch_bounds__(256) void qgemv_kernel(GemvArgs a, int cbk) {
     // Each lane issues the loads of U blocks at once (all of its blocks for the model's shapes), the
     // first batch before the activations are staged, so a lane has up to U x 64 B (Q4_0) /
     // U x 128 B (Q8_0) of weights in flight.
-    constexpr int U = DT == VGX_Q4_0 ? 4 : DT == VGX_Q8_0 ? 3 : 1;
+    // Row mode with 3-4 K-split waves gives a lane one block per 48-64 blocks of the row and has at
+    // most 168 / 128 VGPRs (12 / 16 waves per workgroup): one block per batch there.
+    constexpr int U = (MODE == MODE_ROWS && KW >= 3) ? 1 : DT == VGX_Q4_0 ? 4 : DT == VGX_Q8_0 ? 3 : 1;
     BlockRegs<DT> br[U];
     int cb = min(cbk, nblk);
 #pragma unroll
@@ -274,35 +280,25 @@ __global__ __launch_bounds__(256) void qgemv_kernel(GemvArgs a, int cbk) {
             }
         }
         __syncthreads();
-        if constexpr (DT == VGX_Q4_0) {
-            for (int i = tid; i < NB * cb; i += NT) {
-                const int n = i / cb, blk = i - n * cb;
-                const float *p = xs + (n * cbk + blk) * kGemvPad;
-                float s = 0.0f;
+        if (act) {
+            for (int b = first; b < cb; b += U * stride) {
+                if (b != first) {
 #pragma unroll
-                for (int j = 0; j < QK; ++j) s += p[j];
-                xsum[n * cbk + blk] = s;
+                    for (int u = 0; u < U; ++u)
+                        if (b + u * stride < cb) gemv_load<DT>(br[u], a.w, a.soff, rq, nblk, c0 + b + u * stride);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int bb = b + u * stride;
+                    if (bb < cb) gemv_block<DT, NB>(br[u], xs + bb * kGemvPad, cbk * kGemvPad, acc);
+                }
             }
-            __syncthreads();
+            // first batch of the next chunk
+            const int cn = min(cbk, nblk - c0 - cbk);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (first + u * stride < cn) gemv_load<DT>(br[u], a.w, a.soff, rq, nblk, c0 + cbk + first + u * stride);
         }
-        if (!act) continue;
-        for (int b = first; b < cb; b += U * stride) {
-            if (b != first) {
-#pragma unroll
-                for (int u = 0; u < U; ++u)
-                    if (b + u * stride < cb) gemv_load<DT>(br[u], a.w, a.soff, rq, nblk, c0 + b + u * stride);
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int bb = b + u * stride;
-                if (bb < cb) gemv_block<DT, NB>(br[u], xs + bb * kGemvPad, cbk * kGemvPad, xsum + bb, cbk, acc);
-            }
-        }
-        // first batch of the next chunk
-        const int cn = min(cbk, nblk - c0 - cbk);
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (first + u * stride < cn) gemv_load<DT>(br[u], a.w, a.soff, rq, nblk, c0 + cbk + first + u * stride);
     }
 
     // RMSNorm: the staged activations were lnw * x, so every dot product is scaled by 1/rms here
@@ -325,27 +321,27 @@ __global__ __launch_bounds__(256) void qgemv_kernel(GemvArgs a, int cbk) {
         }
     }
 
-    // Reduce over the lanes of the row-quad, then (split-K) over the waves of the workgroup.
+    // Reduce over the lanes of the row-quad, then over the K-split waves of the workgroup.
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int n = 0; n < NB; ++n) acc[r][n] = LPR == 16 ? row16_sum(acc[r][n]) : wave_sum(acc[r][n]);
-    if constexpr (MODE == MODE_SPLITK && KW > 1) {
-        if (lane == 0) {
+    if constexpr (KW > 1) {
+        if (li == 0) {
 #pragma unroll
             for (int r = 0; r < 4; ++r)
 #pragma unroll
-                for (int n = 0; n < NB; ++n) red[wave][r][n] = acc[r][n];
+                for (int n = 0; n < NB; ++n) red[wave][rqi][r][n] = acc[r][n];
         }
         __syncthreads();
-        if (wave != 0) return;
+        if (ks != 0) return;
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
-                float s = red[0][r][n];
+                float s = red[wave][rqi][r][n];
 #pragma unroll
-                for (int w = 1; w < KW; ++w) s += red[w][r][n];
+                for (int w = 1; w < KW; ++w) s += red[wave + w][rqi][r][n];
                 acc[r][n] = s;
             }
     }
@@ -376,12 +372,19 @@ __global__ __launch_bounds__(256) void qgemv_kernel(GemvArgs a, int cbk) {
     }
 }
 
-// Launch the GEMV over all batch rows (passes of up to 4).  Mode and split chosen from the shape.
+// Launch the GEMV over all batch rows (passes of up to 4).  Mapping chosen from the shape:
+//  * row mode (>= 2048 row-quads): 16 lanes per row-quad, 4 waves per workgroup, each lane
+//    requesting all of its (typically 3) blocks at once.  Splitting K across 3 waves here measured
+//    slower on MI355X (gate/up 10.8 vs 10.2 us, LM head 68.7 vs 51.3 us): the extra LDS reduction
+//    costs more than the shorter per-lane chain saves;
+//  * split-K mode: one row-quad per workgroup, KW in {1, 2, 4} waves over its blocks.
 template <int DT>
 int qgemv_launch(GemvArgs a, hipStream_t st) {
     const bool rows_mode = a.n_rq >= 2048;
     int kw = 1;
-    if (!rows_mode) kw = a.nblk >= 192 ? 4 : a.nblk >= 96 ? 2 : 1;
+    if (a.batch == 1) {  // K-split variants are instantiated for batch 1 (the decode step) only
+        if (!rows_mode) kw = a.nblk >= 192 ? 4 : a.nblk >= 96 ? 2 : 1;
+    }
     const bool norm = a.lnw != nullptr;
     for (int64_t b0 = 0; b0 < a.batch; b0 += 4) {
         GemvArgs p = a;
@@ -389,31 +392,37 @@ int qgemv_launch(GemvArgs a, hipStream_t st) {
         p.x = a.x + b0 * a.ldx;
         p.y = a.y + b0 * a.ldy;
         const int cbk = std::min(a.nblk, kGemvMaxChunkFloats / (QK * nb));
-        const size_t lds = (size_t)nb * cbk * (kGemvPad + 1) * sizeof(float);
+        const size_t lds = (size_t)nb * cbk * kGemvPad * sizeof(float);
         const unsigned grid = rows_mode ? (unsigned)((a.n_rq + 15) / 16) : (unsigned)a.n_rq;
-        const unsigned threads = rows_mode ? 256u : 64u * (unsigned)kw;
+        const unsigned threads = (rows_mode ? 256u : 64u) * (unsigned)kw;
 #define VGX_GEMV_GO(NBV, EPIV, MODEV, KWV, NORMV)                                                      \
     hipLaunchKernelGGL((qgemv_kernel<DT, NBV, EPIV, MODEV, KWV, NORMV>), dim3(grid), dim3(threads), lds, st, p, cbk)
 #define VGX_GEMV_KW(NBV, EPIV, NORMV)                                                                  \
     do {                                                                                               \
         if (rows_mode) VGX_GEMV_GO(NBV, EPIV, MODE_ROWS, 1, NORMV);                                    \
-        else if (kw == 4) VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 4, NORMV);                               \
+        else if (kw == 4) VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 4, NORMV);                             \
         else if (kw == 2) VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 2, NORMV);                               \
         else VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 1, NORMV);                                            \
     } while (0)
-#define VGX_GEMV_EPI(NBV)                                                                              \
+#define VGX_GEMV_K1(NBV, EPIV, NORMV)                                                                  \
     do {                                                                                               \
-        if (a.epi == EPI_SWIGLU) { if (norm) VGX_GEMV_KW(NBV, EPI_SWIGLU, true); else VGX_GEMV_KW(NBV, EPI_SWIGLU, false); } \
-        else if (a.epi == EPI_ACCUM) { if (norm) VGX_GEMV_KW(NBV, EPI_ACCUM, true); else VGX_GEMV_KW(NBV, EPI_ACCUM, false); } \
-        else { if (norm) VGX_GEMV_KW(NBV, EPI_STORE, true); else VGX_GEMV_KW(NBV, EPI_STORE, false); } \
+        if (rows_mode) VGX_GEMV_GO(NBV, EPIV, MODE_ROWS, 1, NORMV);                                    \
+        else VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 1, NORMV);                                            \
+    } while (0)
+#define VGX_GEMV_EPI(NBV, SEL)                                                                         \
+    do {                                                                                               \
+        if (a.epi == EPI_SWIGLU) { if (norm) SEL(NBV, EPI_SWIGLU, true); else SEL(NBV, EPI_SWIGLU, false); } \
+        else if (a.epi == EPI_ACCUM) { if (norm) SEL(NBV, EPI_ACCUM, true); else SEL(NBV, EPI_ACCUM, false); } \
+        else { if (norm) SEL(NBV, EPI_STORE, true); else SEL(NBV, EPI_STORE, false); } \
     } while (0)
         switch (nb) {
-            case 1: VGX_GEMV_EPI(1); break;
-            case 2: VGX_GEMV_EPI(2); break;
-            case 3: VGX_GEMV_EPI(3); break;
-            default: VGX_GEMV_EPI(4); break;
+            case 1: VGX_GEMV_EPI(1, VGX_GEMV_KW); break;
+            case 2: VGX_GEMV_EPI(2, VGX_GEMV_K1); break;
+            case 3: VGX_GEMV_EPI(3, VGX_GEMV_K1); break;
+            default: VGX_GEMV_EPI(4, VGX_GEMV_K1); break;
         }
 #undef VGX_GEMV_EPI
+#undef VGX_GEMV_K1
 #undef VGX_GEMV_KW
 #undef VGX_GEMV_GO
         if (hipGetLastError() != hipSuccess) return VGX_E_HIP;
