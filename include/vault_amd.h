@@ -158,6 +158,40 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
                     int64_t H, int64_t G, int64_t D, float scale, void *workspace, int64_t workspace_bytes,
                     void *stream);
 
+/* A run of keys for prefill attention: key j of kv group g at element offset
+ * g*group_stride + j*row_stride of k (and v); rows are head_dim contiguous bf16. */
+typedef struct {
+    const void *k;
+    const void *v;
+    int64_t len;
+    int64_t row_stride;
+    int64_t group_stride;
+} vgx_kv_run;
+
+/* One block of queries (a chunk) for vgx_attn_prefill: query t of head h at q + t*ldq + h*q_hstride
+ * (D contiguous elements, fp32 or bf16), output at out + t*ldo + h*o_hstride (fp32); runs concatenated in
+ * order; when causal_base >= 0 the last run is causal: query t sees its keys j <= causal_base + t. */
+typedef struct {
+    const void *q;
+    int64_t ldq;
+    int64_t q_hstride;
+    float *out;
+    int64_t ldo;
+    int64_t o_hstride;
+    int64_t n_q;
+    int64_t causal_base;
+    int n_runs;
+    vgx_kv_run runs[4];
+} vgx_attn_block;
+
+/* Prefill attention on bf16 MFMA (kv_dtype VGX_BF16; q_dtype VGX_F32 or VGX_BF16; D = 128;
+ * H/G in {1, 2, 4, 6, 8}) for up to 8 query blocks in one launch: out = softmax(q k^T * scale) v per
+ * query head h over kv group h / (H/G), key tiles wholly in a query tile's causal future skipped.
+ * Replaces the SDPA calls of block_sliding_attention (src/vault_v3_model.py:812-863) and of the
+ * chunk-recurrent prefill (:2064-2093). */
+int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H, int64_t G,
+                     int64_t D, float scale, void *stream);
+
 /* ---------------------------------------------------------------- small fused ops -------------- */
 
 /* RMSNorm rows: y[r, :] = w * (x[r, :] / sqrt(mean(x[r, :]^2) + eps)).

@@ -42,6 +42,7 @@ _SIGS = {
     "vgx_qlinear_ex": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P]),
     "vgx_attn_decode_workspace_bytes": (I64, [I64, I64, I64, I64, I64]),
     "vgx_attn_decode": (I32, [I32, P, I64, P, I32, P, I64, I32, I64, P, I64, I64, I64, I64, F, P, I64, P]),
+    "vgx_attn_prefill": (I32, [I32, I32, P, I32, I64, I64, I64, F, P]),
     "vgx_rmsnorm": (I32, [P, I64, P, P, I64, I64, I64, F, P]),
     "vgx_rope_qkv_write": (I32, [I32, P, I64, P, I64, P, I64, I64, I64, I64, I64, P, I64, P, P, P, I64, I64, P, P, I64,
                                  I64, I64, P]),
@@ -59,6 +60,19 @@ class KVSpan(C.Structure):
     """vgx_kv_span (include/vault_amd.h)."""
     _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("len", C.c_int64),
                 ("batch_stride", C.c_int64), ("group_stride", C.c_int64), ("dyn_len", C.c_void_p)]
+
+
+class KVRun(C.Structure):
+    """vgx_kv_run (include/vault_amd.h)."""
+    _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("len", C.c_int64), ("row_stride", C.c_int64),
+                ("group_stride", C.c_int64)]
+
+
+class AttnBlock(C.Structure):
+    """vgx_attn_block (include/vault_amd.h)."""
+    _fields_ = [("q", C.c_void_p), ("ldq", C.c_int64), ("q_hstride", C.c_int64), ("out", C.c_void_p),
+                ("ldo", C.c_int64), ("o_hstride", C.c_int64), ("n_q", C.c_int64), ("causal_base", C.c_int64),
+                ("n_runs", C.c_int), ("runs", KVRun * 4)]
 
 
 class VGXError(RuntimeError):

@@ -1,0 +1,330 @@
+// Prefill attention on bf16 MFMA: blocks of queries over up to four key runs (sinks | segment
+// memory | previous chunk | current chunk), the last run causal.
+//
+// Reference semantics: block_sliding_attention (src/vault_v3_model.py:812-863, sinks re-rotated per
+// query chunk :805-809, 849-856) and the chunk-recurrent attention of _forward_chunk_recurrent
+// (:2029-2037, 2064-2093).  A query block is one chunk; query t of the block sees every key of the
+// first runs and keys j <= causal_base + t of the last run.
+//
+// Mapping.  A workgroup = one (query block, kv group g, tile of 32 queries) with one wave per query
+// head of the group (GRP waves), so every K/V tile staged in LDS serves all GRP heads.  A wave holds
+// its 32 queries as two 16-query MFMA tiles and computes, per 32 keys,
+//   S^T (keys x queries) = K Q^T       with v_mfma_f32_16x16x32_bf16 (A = K rows from LDS, B = Q^T
+//                                       fragments kept in registers),
+//   O^T (dims x queries) += V^T P^T    with v_mfma_f32_16x16x32_f16 (A = V^T from a transposed LDS
+//                                       copy converted bf16 -> fp16 exactly, B = P^T straight from
+//                                       the S^T accumulators as fp16: 11-bit probabilities keep the
+//                                       few-key case inside the bf16 attention bound, where bf16
+//                                       probabilities alone exceed it).
+// In both products a lane of the 16 x 16 output owns one query column, so the online-softmax state
+// (running max, rescale of O) is lane-local; the max over a query's keys needs two cross-lane steps.
+// The K-dimension slots of A and B are assigned the same way in each product (lane group lg holds
+// slots 8 lg .. 8 lg + 7 of both operands), which is all the matrix product needs.
+// Key tiles entirely in the causal future of the 32 queries are not loaded; keys of partially masked
+// tiles get -inf.  Scores use exp2 with the scale pre-multiplied by log2(e).
+#include "common.h"
+
+using namespace vgx;
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kKT = 64;             // keys per LDS tile
+constexpr int kD = 128;             // head dim (the kernel is specialised for 128)
+constexpr int kKRow = kD + 8;       // LDS row of K, bf16 (16 bytes of padding)
+constexpr int kVRow = kKT + 8;      // LDS row of V^T, bf16
+constexpr int kQTile = 32;          // queries per wave
+constexpr int kMaxBlocks = 8;
+constexpr float kNegBig = -1.0e30f;
+
+struct RunArgs {
+    const uint16_t *k;
+    const uint16_t *v;
+    int64_t len;
+    int64_t rstride;   // elements between consecutive keys
+    int64_t gstride;   // elements between kv groups
+};
+
+struct BlockArgs {
+    const void *q;     // query t, head h at t * ldq + h * q_hstride elements (fp32 or bf16)
+    int64_t ldq;
+    int64_t q_hstride;
+    float *out;        // query t, head h at t * ldo + h * o_hstride floats
+    int64_t ldo;
+    int64_t o_hstride;
+    int64_t n_q;
+    int64_t causal_base;
+    int n_runs;
+    int tile0;         // first workgroup index of this block
+    RunArgs run[4];
+};
+
+struct PrefillArgs {
+    BlockArgs blk[kMaxBlocks];
+    int n_blocks;
+    int n_tiles;
+    int H, G;
+    float scale_log2;  // scale * log2(e)
+    int q_bf16;
+};
+
+__device__ __forceinline__ uint16_t f2bf(float f) { return (uint16_t)float_to_bf16_bits(f); }
+
+// bf16 bits -> fp16 bits (exact for |v| in the fp16 normal range; smaller magnitudes become fp16
+// subnormals, larger ones overflow: attention values stay far inside that range).
+__device__ __forceinline__ uint16_t bf2h(uint32_t b) {
+    return __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((b & 0xFFFFu) << 16));
+}
+
+template <int GRP>
+__global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
+    __shared__ __align__(16) uint16_t ks[kKT * kKRow];
+    __shared__ __align__(16) uint16_t vt[kD * kVRow];
+
+    // XCD-aware order: consecutive tiles (same block and group, neighbouring queries, same keys)
+    // on the same XCD so that its L2 serves their shared K/V.
+    int tile = blockIdx.x;
+    if ((a.n_tiles & 7) == 0) tile = (blockIdx.x & 7) * (a.n_tiles >> 3) + (blockIdx.x >> 3);
+    int bi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxBlocks; ++i)
+        if (i < a.n_blocks && a.blk[i].tile0 <= tile) bi = i;
+    const BlockArgs &B = a.blk[bi];
+    const int local = tile - B.tile0;
+    const int g = local % a.G;
+    const int64_t t0 = (int64_t)(local / a.G) * kQTile;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lq = lane & 15, lg = lane >> 4;
+    const int h = g * GRP + wave;
+
+    // Q^T fragments: query t0 + 16 qt + lq, dims 32 kc + 8 lg .. + 7.
+    bf16x8_t qf[2][4];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        const int64_t t = t0 + qt * 16 + lq;
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+            const int d0 = kc * 32 + lg * 8;
+            uint16_t e[8];
+            if (t < B.n_q) {
+                if (a.q_bf16) {
+                    const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(B.q) + t * B.ldq + h * B.q_hstride + d0);
+                    e[0] = w.x & 0xFFFF; e[1] = w.x >> 16; e[2] = w.y & 0xFFFF; e[3] = w.y >> 16;
+                    e[4] = w.z & 0xFFFF; e[5] = w.z >> 16; e[6] = w.w & 0xFFFF; e[7] = w.w >> 16;
+                } else {
+                    const float *qp = static_cast<const float *>(B.q) + t * B.ldq + h * B.q_hstride + d0;
+                    const float4 x0 = reinterpret_cast<const float4 *>(qp)[0], x1 = reinterpret_cast<const float4 *>(qp)[1];
+                    e[0] = f2bf(x0.x); e[1] = f2bf(x0.y); e[2] = f2bf(x0.z); e[3] = f2bf(x0.w);
+                    e[4] = f2bf(x1.x); e[5] = f2bf(x1.y); e[6] = f2bf(x1.z); e[7] = f2bf(x1.w);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) e[i] = 0;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qf[qt][kc][i] = __builtin_bit_cast(__bf16, e[i]);
+        }
+    }
+
+    f32x4_t o[2][8];
+    float m[2], lsum[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        m[qt] = kNegBig;
+        lsum[qt] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) o[qt][dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    for (int r = 0; r < B.n_runs; ++r) {
+        const RunArgs R = B.run[r];
+        const bool causal = (r == B.n_runs - 1) && B.causal_base >= 0;
+        int64_t n = R.len;
+        if (causal) n = min(n, B.causal_base + t0 + kQTile);   // later keys are in every query's future
+        const uint16_t *kbase = R.k + (int64_t)g * R.gstride;
+        const uint16_t *vbase = R.v + (int64_t)g * R.gstride;
+        for (int64_t j0 = 0; j0 < n; j0 += kKT) {
+            __syncthreads();
+            // Stage K [kKT][kD] and V^T [kD][kKT] (rows past n zero-filled).
+            for (int c = tid; c < kKT * (kD / 8); c += 64 * GRP) {
+                const int row = c >> 4, cc = c & 15;
+                uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
+                if (j0 + row < n) {
+                    kw = *reinterpret_cast<const uint4 *>(kbase + (j0 + row) * R.rstride + cc * 8);
+                    vw = *reinterpret_cast<const uint4 *>(vbase + (j0 + row) * R.rstride + cc * 8);
+                }
+                *reinterpret_cast<uint4 *>(ks + row * kKRow + cc * 8) = kw;
+                const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    vt[(cc * 8 + 2 * e) * kVRow + row] = bf2h(vv[e]);
+                    vt[(cc * 8 + 2 * e + 1) * kVRow + row] = bf2h(vv[e] >> 16);
+                }
+            }
+            __syncthreads();
+            for (int c = 0; c < kKT && j0 + c < n; c += 32) {
+                f32x4_t s[2][2];
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    s[qt][0] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                    s[qt][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+#pragma unroll
+                for (int kc = 0; kc < 4; ++kc) {
+                    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(ks + (c + lq) * kKRow + kc * 32 + lg * 8);
+                    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(ks + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt) {
+                        s[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[qt][kc], s[qt][0], 0, 0, 0);
+                        s[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[qt][kc], s[qt][1], 0, 0, 0);
+                    }
+                }
+                f16x8_t pb[2];
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    const int64_t t = t0 + qt * 16 + lq;
+                    float v[8];
+#pragma unroll
+                    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int64_t key = j0 + c + kt * 16 + lg * 4 + i;
+                            const bool vis = key < n && (!causal || key <= B.causal_base + t);
+                            v[kt * 4 + i] = vis ? s[qt][kt][i] * a.scale_log2 : -INFINITY;
+                        }
+                    float mt = v[0];
+#pragma unroll
+                    for (int i = 1; i < 8; ++i) mt = fmaxf(mt, v[i]);
+                    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+                    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+                    const float mn = fmaxf(m[qt], mt);
+                    const float corr = exp2f(m[qt] - mn);
+                    m[qt] = mn;
+                    float ps = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float p = exp2f(v[i] - mn);
+                        ps += p;
+                        pb[qt][i] = (_Float16)p;
+                    }
+                    lsum[qt] = lsum[qt] * corr + ps;
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt) o[qt][dt] *= corr;
+                }
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) {
+                    const uint16_t *vr = vt + (dt * 16 + lq) * kVRow + c + lg * 4;
+                    const uint2 lo = *reinterpret_cast<const uint2 *>(vr);
+                    const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16);
+                    const uint4 pk = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                    const f16x8_t va = __builtin_bit_cast(f16x8_t, pk);
+#pragma unroll
+                    for (int qt = 0; qt < 2; ++qt)
+                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qt], o[qt][dt], 0, 0, 0);
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+        float L = lsum[qt];
+        L += __shfl_xor(L, 16, kWave);
+        L += __shfl_xor(L, 32, kWave);
+        const float inv = 1.0f / L;
+        const int64_t t = t0 + qt * 16 + lq;
+        if (t >= B.n_q) continue;
+        float *op = B.out + t * B.ldo + (int64_t)h * B.o_hstride;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            float4 w;
+            w.x = o[qt][dt][0] * inv; w.y = o[qt][dt][1] * inv; w.z = o[qt][dt][2] * inv; w.w = o[qt][dt][3] * inv;
+            *reinterpret_cast<float4 *>(op + dt * 16 + lg * 4) = w;
+        }
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H, int64_t G,
+                     int64_t D, float scale, void *stream) {
+    if (kv_dtype != VGX_BF16) return VGX_E_DTYPE;
+    if (q_dtype != VGX_F32 && q_dtype != VGX_BF16) return VGX_E_DTYPE;
+    if (!blocks) return VGX_E_ARG;
+    if (n_blocks < 0 || n_blocks > kMaxBlocks) return VGX_E_LIMIT;
+    if (H <= 0 || G <= 0 || H % G) return VGX_E_SIZE;
+    if (D != kD) return VGX_E_LIMIT;
+    const int grp = (int)(H / G);
+    if (grp != 1 && grp != 2 && grp != 4 && grp != 6 && grp != 8) return VGX_E_LIMIT;
+    PrefillArgs a{};
+    a.H = (int)H;
+    a.G = (int)G;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.q_bf16 = q_dtype == VGX_BF16;
+    int64_t tiles = 0;
+    int nb = 0;
+    for (int i = 0; i < n_blocks; ++i) {
+        const vgx_attn_block &b = blocks[i];
+        if (b.n_q < 0 || b.n_runs < 1 || b.n_runs > 4) return VGX_E_SIZE;
+        if (b.n_q == 0) continue;
+        if (!b.q || !b.out) return VGX_E_ARG;
+        const int qel = q_dtype == VGX_BF16 ? 2 : 4;
+        if (b.q_hstride < D || b.o_hstride < D || b.ldq < 0 || b.ldo < 0) return VGX_E_SIZE;
+        if (((uintptr_t)b.q % 16) || ((uintptr_t)b.out % 16) || (b.ldq * qel) % 16 || (b.q_hstride * qel) % 16 ||
+            (b.ldo * 4) % 16 || (b.o_hstride * 4) % 16)
+            return VGX_E_ALIGN;
+        BlockArgs &B = a.blk[nb];
+        B.q = b.q;
+        B.ldq = b.ldq;
+        B.q_hstride = b.q_hstride;
+        B.out = b.out;
+        B.ldo = b.ldo;
+        B.o_hstride = b.o_hstride;
+        B.n_q = b.n_q;
+        B.causal_base = b.causal_base;
+        B.n_runs = b.n_runs;
+        B.tile0 = (int)tiles;
+        int64_t n_keys = 0;
+        for (int r = 0; r < b.n_runs; ++r) {
+            const vgx_kv_run &R = b.runs[r];
+            if (R.len < 0) return VGX_E_SIZE;
+            if (R.len > 0 && (!R.k || !R.v)) return VGX_E_ARG;
+            if (R.len > 0 && (((uintptr_t)R.k | (uintptr_t)R.v) % 16 || (R.row_stride * 2) % 16 ||
+                              (R.group_stride * 2) % 16))
+                return VGX_E_ALIGN;
+            B.run[r].k = static_cast<const uint16_t *>(R.k);
+            B.run[r].v = static_cast<const uint16_t *>(R.v);
+            B.run[r].len = R.len;
+            B.run[r].rstride = R.row_stride;
+            B.run[r].gstride = R.group_stride;
+            n_keys += R.len;
+        }
+        if (b.causal_base >= 0 && b.causal_base + 1 > b.runs[b.n_runs - 1].len) return VGX_E_SIZE;
+        if (n_keys == 0) return VGX_E_SIZE;
+        tiles += (b.n_q + kQTile - 1) / kQTile * G;
+        ++nb;
+    }
+    if (nb == 0) return VGX_OK;
+    if (tiles > 0x7FFFFFFF) return VGX_E_LIMIT;
+    a.n_blocks = nb;
+    a.n_tiles = (int)tiles;
+    hipStream_t st = (hipStream_t)stream;
+    const dim3 grid((unsigned)tiles);
+    switch (grp) {
+        case 1: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(64), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(128), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(attn_prefill_kernel<4>, grid, dim3(256), 0, st, a); break;
+        case 6: hipLaunchKernelGGL(attn_prefill_kernel<6>, grid, dim3(384), 0, st, a); break;
+        case 8: hipLaunchKernelGGL(attn_prefill_kernel<8>, grid, dim3(512), 0, st, a); break;
+    }
+    VGX_CHECK_LAUNCH();
+    return VGX_OK;
+}
+
+}  // extern "C"
