@@ -178,6 +178,34 @@ def attn_figures(dev, reps: int = 20):
             "gbs": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 3)}
 
 
+PREFILL_FLOPS = 90.22e9   # unmasked (query, key) pairs x 4 x D x H for L = 8192, W = 1024, 512 sinks
+
+
+def prefill_figures(dev, reps: int = 10):
+    """Block sliding-window attention prefill, bf16: batch 1, L = 8192, 12 q / 2 kv heads, D = 128,
+    W = 1024, 512 sinks re-rotated per chunk (drop-in block_sliding_attention: 6 sink re-rotations + one
+    MFMA attention launch over the 8 chunks).  Algorithmic work: 4 D H flops per visible (query, key)
+    pair = 90.22 GFLOP; peak 2.5 PFLOP/s dense bf16."""
+    import torch
+    from vault_amd import attention as vatt
+    B, H, G, D, L, W, S = 1, 12, 2, 128, 8192, 1024, 512
+    g = torch.Generator().manual_seed(13)
+    q, k, v, kr = (torch.randn(B, n, L, D, generator=g).to(dev, torch.bfloat16) for n in (H, G, G, G))
+    run = lambda: vatt.block_sliding_attention(q, k, v, W, k_raw=kr, n_sink=S, head_dim=D, rope_theta=1e6)
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    tf = PREFILL_FLOPS / us / 1e6
+    return {"config": "bf16 L=8192 W=1024 sinks=512 12q/2kv D=128", "us": round(us, 1), "tflops": round(tf, 1),
+            "frac": round(tf / 2500.0, 4)}
+
+
 def cpu_baseline(cfg, tensors, budget_s: float = 15.0):
     """The reference C runtime (runtime/vault3.c, compiled into oracle/_ref) stepping the same model
     from a state seeded at the same context position, on the host's cores."""
@@ -244,6 +272,7 @@ def main() -> int:
     if not args.no_kernels:
         kernels["gemv"] = gemv_figures(dev)
         kernels["attn_decode"] = attn_figures(dev)
+        kernels["attn_prefill"] = prefill_figures(dev)
         _log("kernel figures done")
     cpu = None
     if not args.no_cpu and args.batch == 1 and args.kv == "fp32":

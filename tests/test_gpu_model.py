@@ -144,3 +144,22 @@ def test_graph_replay_equals_eager(dev, kv):
         assert torch.equal(a, b), sg.pos
     assert len(sg.graphs) >= 2
     assert np.array_equal(sg.mem_pos.numpy(), se.mem_pos.numpy())
+
+
+def test_bf16_prefill_mfma_consistency(dev):
+    """bf16 KV: chunk prefill runs the MFMA attention; prefill(split) + step stream must match the
+    pure step stream (VALU decode attention) within the bf16 full-model bar, with top-1 agreement."""
+    cfg = modelgen.tiny_cfg(head_dim=128, window=64, seg_budget=24)
+    tensors, _, _ = modelgen.build(cfg, "q4_0", seed=8)
+    m = _gpu_model(cfg, tensors, dev, kv=torch.bfloat16)
+    ids = torch.tensor([modelgen.ids_stream(cfg, 230, seed=21)])
+    stream, _ = _stream(m, ids[0].tolist(), dev)
+    for split in (70, 150, 200):
+        last, st = m.prefill(ids[:, :split])
+        rows = [last[0].double().cpu().numpy()]
+        for t in range(split, ids.shape[1]):
+            rows.append(m.step(ids[:, t], st)[0].double().cpu().numpy())
+        got = np.stack(rows)
+        want = stream[split - 1:]
+        assert np.abs(got - want).max() <= 5e-2, split
+        assert np.array_equal(got.argmax(-1), want.argmax(-1)), split

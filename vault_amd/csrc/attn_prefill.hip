@@ -9,8 +9,10 @@
 // Mapping.  A workgroup = one (query block, kv group g, tile of 32 queries) with one wave per query
 // head of the group (GRP waves), so every K/V tile staged in LDS serves all GRP heads.  A wave holds
 // its 32 queries as two 16-query MFMA tiles and computes, per 32 keys,
-//   S^T (keys x queries) = K Q^T       with v_mfma_f32_16x16x32_bf16 (A = K rows from LDS, B = Q^T
-//                                       fragments kept in registers),
+//   S^T (keys x queries) = K Q^T       with v_mfma_f32_16x16x32_f16 (A = K rows staged in LDS as fp16,
+//                                       exact from bf16; B = Q^T fragments kept in registers: fp32
+//                                       queries as an fp16 hi + lo pair, two MFMAs, so the scores
+//                                       keep fp32-level accuracy; bf16 queries as one exact fp16),
 //   O^T (dims x queries) += V^T P^T    with v_mfma_f32_16x16x32_f16 (A = V^T from a transposed LDS
 //                                       copy converted bf16 -> fp16 exactly, B = P^T straight from
 //                                       the S^T accumulators as fp16: 11-bit probabilities keep the
@@ -28,7 +30,6 @@ using namespace vgx;
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -71,15 +72,14 @@ struct PrefillArgs {
     int q_bf16;
 };
 
-__device__ __forceinline__ uint16_t f2bf(float f) { return (uint16_t)float_to_bf16_bits(f); }
-
 // bf16 bits -> fp16 bits (exact for |v| in the fp16 normal range; smaller magnitudes become fp16
-// subnormals, larger ones overflow: attention values stay far inside that range).
+// subnormals (error below 2^-25), magnitudes beyond 65504 are not representable: K and V must stay
+// inside that range, as attention keys and values do).
 __device__ __forceinline__ uint16_t bf2h(uint32_t b) {
     return __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((b & 0xFFFFu) << 16));
 }
 
-template <int GRP>
+template <int GRP, bool QSPLIT>
 __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     __shared__ __align__(16) uint16_t ks[kKT * kKRow];
     __shared__ __align__(16) uint16_t vt[kD * kVRow];
@@ -101,32 +101,40 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     const int lq = lane & 15, lg = lane >> 4;
     const int h = g * GRP + wave;
 
-    // Q^T fragments: query t0 + 16 qt + lq, dims 32 kc + 8 lg .. + 7.
-    bf16x8_t qf[2][4];
+    // Q^T fragments: query t0 + 16 qt + lq, dims 32 kc + 8 lg .. + 7 (fp16 hi and, for fp32 queries,
+    // the fp16 residual lo = q - hi).
+    f16x8_t qh[2][4], ql[2][4];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         const int64_t t = t0 + qt * 16 + lq;
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
             const int d0 = kc * 32 + lg * 8;
-            uint16_t e[8];
+            float e[8];
             if (t < B.n_q) {
-                if (a.q_bf16) {
+                if constexpr (!QSPLIT) {
                     const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(B.q) + t * B.ldq + h * B.q_hstride + d0);
-                    e[0] = w.x & 0xFFFF; e[1] = w.x >> 16; e[2] = w.y & 0xFFFF; e[3] = w.y >> 16;
-                    e[4] = w.z & 0xFFFF; e[5] = w.z >> 16; e[6] = w.w & 0xFFFF; e[7] = w.w >> 16;
+                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        e[2 * i] = __uint_as_float(ww[i] << 16);
+                        e[2 * i + 1] = __uint_as_float(ww[i] & 0xFFFF0000u);
+                    }
                 } else {
                     const float *qp = static_cast<const float *>(B.q) + t * B.ldq + h * B.q_hstride + d0;
                     const float4 x0 = reinterpret_cast<const float4 *>(qp)[0], x1 = reinterpret_cast<const float4 *>(qp)[1];
-                    e[0] = f2bf(x0.x); e[1] = f2bf(x0.y); e[2] = f2bf(x0.z); e[3] = f2bf(x0.w);
-                    e[4] = f2bf(x1.x); e[5] = f2bf(x1.y); e[6] = f2bf(x1.z); e[7] = f2bf(x1.w);
+                    e[0] = x0.x; e[1] = x0.y; e[2] = x0.z; e[3] = x0.w; e[4] = x1.x; e[5] = x1.y; e[6] = x1.z; e[7] = x1.w;
                 }
             } else {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) e[i] = 0;
+                for (int i = 0; i < 8; ++i) e[i] = 0.0f;
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) qf[qt][kc][i] = __builtin_bit_cast(__bf16, e[i]);
+            for (int i = 0; i < 8; ++i) {
+                const _Float16 hi = (_Float16)e[i];
+                qh[qt][kc][i] = hi;
+                ql[qt][kc][i] = (_Float16)(e[i] - (float)hi);
+            }
         }
     }
 
@@ -157,7 +165,11 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                     kw = *reinterpret_cast<const uint4 *>(kbase + (j0 + row) * R.rstride + cc * 8);
                     vw = *reinterpret_cast<const uint4 *>(vbase + (j0 + row) * R.rstride + cc * 8);
                 }
-                *reinterpret_cast<uint4 *>(ks + row * kKRow + cc * 8) = kw;
+                const uint4 kh = make_uint4(bf2h(kw.x) | ((uint32_t)bf2h(kw.x >> 16) << 16),
+                                            bf2h(kw.y) | ((uint32_t)bf2h(kw.y >> 16) << 16),
+                                            bf2h(kw.z) | ((uint32_t)bf2h(kw.z >> 16) << 16),
+                                            bf2h(kw.w) | ((uint32_t)bf2h(kw.w >> 16) << 16));
+                *reinterpret_cast<uint4 *>(ks + row * kKRow + cc * 8) = kh;
                 const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -175,12 +187,16 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                 }
 #pragma unroll
                 for (int kc = 0; kc < 4; ++kc) {
-                    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(ks + (c + lq) * kKRow + kc * 32 + lg * 8);
-                    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(ks + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
+                    const f16x8_t a0 = *reinterpret_cast<const f16x8_t *>(ks + (c + lq) * kKRow + kc * 32 + lg * 8);
+                    const f16x8_t a1 = *reinterpret_cast<const f16x8_t *>(ks + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
 #pragma unroll
                     for (int qt = 0; qt < 2; ++qt) {
-                        s[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[qt][kc], s[qt][0], 0, 0, 0);
-                        s[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[qt][kc], s[qt][1], 0, 0, 0);
+                        s[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qh[qt][kc], s[qt][0], 0, 0, 0);
+                        s[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qh[qt][kc], s[qt][1], 0, 0, 0);
+                        if constexpr (QSPLIT) {
+                            s[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, ql[qt][kc], s[qt][0], 0, 0, 0);
+                            s[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, ql[qt][kc], s[qt][1], 0, 0, 0);
+                        }
                     }
                 }
                 f16x8_t pb[2];
@@ -316,13 +332,22 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, in
     a.n_tiles = (int)tiles;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)tiles);
-    switch (grp) {
-        case 1: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(64), 0, st, a); break;
-        case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(128), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(attn_prefill_kernel<4>, grid, dim3(256), 0, st, a); break;
-        case 6: hipLaunchKernelGGL(attn_prefill_kernel<6>, grid, dim3(384), 0, st, a); break;
-        case 8: hipLaunchKernelGGL(attn_prefill_kernel<8>, grid, dim3(512), 0, st, a); break;
+#define VGX_PREFILL_GO(G_, S_) hipLaunchKernelGGL((attn_prefill_kernel<G_, S_>), grid, dim3(64 * G_), 0, st, a)
+#define VGX_PREFILL_GRP(S_)                      \
+    switch (grp) {                               \
+        case 1: VGX_PREFILL_GO(1, S_); break;    \
+        case 2: VGX_PREFILL_GO(2, S_); break;    \
+        case 4: VGX_PREFILL_GO(4, S_); break;    \
+        case 6: VGX_PREFILL_GO(6, S_); break;    \
+        case 8: VGX_PREFILL_GO(8, S_); break;    \
     }
+    if (a.q_bf16) {
+        VGX_PREFILL_GRP(false)
+    } else {
+        VGX_PREFILL_GRP(true)
+    }
+#undef VGX_PREFILL_GRP
+#undef VGX_PREFILL_GO
     VGX_CHECK_LAUNCH();
     return VGX_OK;
 }

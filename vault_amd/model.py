@@ -547,6 +547,7 @@ class VAULTv3ForCausalLM:
         ao = torch.empty(N, H, D, dtype=torch.float32, device=self.device)
         hbuf = torch.empty(N, cfg.d_ff, dtype=torch.float32, device=self.device)
         scale = 1.0 / math.sqrt(D)
+        mfma = st.kv_dtype == torch.bfloat16 and D == 128 and H // G in (1, 2, 4, 6, 8)
         for li, lw in enumerate(w.layers):
             if seg_active and li in cfg.seg_layers:
                 j = cfg.seg_layers.index(li)
@@ -566,7 +567,12 @@ class VAULTv3ForCausalLM:
             if n_prev:
                 spans.append((st.k_prev[li], st.v_prev[li]))
             spans.append((kc[:, :, :N], st.v_cur[li][:, :, :N]))
-            ops.attn_decode(q, spans, out=ao, scale=scale, ws=self.ws, causal_base=0)
+            if mfma:
+                # bf16 cache: block attention on MFMA (runs are the [G, n, D] views of batch entry 0)
+                ops.attn_prefill([{"q": q, "out": ao, "runs": [(k_[0], v_[0]) for k_, v_ in spans],
+                                   "causal_base": 0}], H, G, scale)
+            else:
+                ops.attn_decode(q, spans, out=ao, scale=scale, ws=self.ws, causal_base=0)
             ops.qlinear(lw.wo, ao.view(N, HD), out=x, accumulate=True)
             ops.qlinear_swiglu(lw.wgu, x, out=hbuf, norm=(lw.ln2, cfg.rms_eps))
             ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
