@@ -28,6 +28,22 @@ def rope_table_fp32(positions: np.ndarray, head_dim: int, theta: float) -> np.nd
     return np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
 
 
+_TABLES: dict = {}
+
+
+def _sink_table(n: int, W: int, S: int, D: int, theta: float, device) -> torch.Tensor:
+    """Device RoPE rows of the re-rotated sink positions of chunks 2 .. n-1, built once per shape."""
+    key = (n, W, S, D, float(theta), str(device))
+    t = _TABLES.get(key)
+    if t is None:
+        pos = np.concatenate([np.maximum(0, (i - 1) * W - S + np.arange(S)) for i in range(2, n)])
+        t = torch.from_numpy(rope_table_fp32(pos, D, theta)).to(device)
+        if len(_TABLES) > 16:
+            _TABLES.clear()
+        _TABLES[key] = t
+    return t
+
+
 def block_sliding_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int,
                             k_raw: Optional[torch.Tensor] = None, n_sink: int = 0, head_dim: int = 0,
                             rope_theta: float = 0.0) -> torch.Tensor:
@@ -47,8 +63,7 @@ def block_sliding_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, w
     sinks = sink_v = None
     if S and n >= 3:
         # sink keys re-rotated for every chunk i >= 2: [n-2][B][G][S][D]; values [B][G][S][D]
-        pos = np.concatenate([np.maximum(0, (i - 1) * W - S + np.arange(S)) for i in range(2, n)])
-        tab = torch.from_numpy(rope_table_fp32(pos, D, rope_theta or 1.0)).to(q.device)
+        tab = _sink_table(n, W, S, D, rope_theta or 1.0, q.device)
         kr = k_raw.to(torch.bfloat16)[:, :, :S].contiguous().view(B * G, S, D)
         sinks = torch.empty(n - 2, B, G, S, D, dtype=torch.bfloat16, device=q.device)
         sink_v = vb[:, :, :S].contiguous()

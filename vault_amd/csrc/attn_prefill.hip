@@ -8,29 +8,29 @@
 //
 // Mapping.  A workgroup = one (query block, kv group g, tile of 32 queries) with one wave per query
 // head of the group (GRP waves), so every K/V tile staged in LDS serves all GRP heads.  A wave holds
-// its 32 queries as two 16-query MFMA tiles and computes, per 32 keys,
-//   S^T (keys x queries) = K Q^T       with v_mfma_f32_16x16x32_f16 (A = K rows staged in LDS as fp16,
-//                                       exact from bf16; B = Q^T fragments kept in registers: fp32
-//                                       queries as an fp16 hi + lo pair, two MFMAs, so the scores
-//                                       keep fp32-level accuracy; bf16 queries as one exact fp16),
-//   O^T (dims x queries) += V^T P^T    with v_mfma_f32_16x16x32_f16 (A = V^T from a transposed LDS
-//                                       copy converted bf16 -> fp16 exactly, B = P^T straight from
-//                                       the S^T accumulators as fp16: 11-bit probabilities keep the
-//                                       few-key case inside the bf16 attention bound, where bf16
-//                                       probabilities alone exceed it).
-// In both products a lane of the 16 x 16 output owns one query column, so the online-softmax state
-// (running max, rescale of O) is lane-local; the max over a query's keys needs two cross-lane steps.
-// The K-dimension slots of A and B are assigned the same way in each product (lane group lg holds
-// slots 8 lg .. 8 lg + 7 of both operands), which is all the matrix product needs.
-// Key tiles entirely in the causal future of the 32 queries are not loaded; keys of partially masked
-// tiles get -inf.  Scores use exp2 with the scale pre-multiplied by log2(e).
+// its 32 queries as two 16-query MFMA tiles and computes, per 32 keys, with v_mfma_f32_16x16x32_bf16:
+//   S^T (keys x queries) = K Q^T       A = K rows from LDS, B = Q^T fragments kept in registers;
+//                                      fp32 queries enter as a bf16 hi + lo pair (two MFMAs), so
+//                                      the scores keep fp32-level accuracy;
+//   O^T (dims x queries) += V^T P^T    A = V^T from a transposed LDS copy, B = P^T straight from
+//                                      the S^T accumulators as a bf16 hi + lo pair (two MFMAs):
+//                                      8-bit probabilities alone exceed the bf16 attention bound
+//                                      when few keys carry the weight.
+// K and V stay bf16 end to end (no conversions in the staging loop): MFMA throughput is abundant
+// here, VALU issue is what bounds the kernel.  In both products a lane of the 16 x 16 output owns
+// one query column, so the online-softmax state (running max, rescale of O) is lane-local; the max
+// over a query's keys needs two cross-lane steps.  The K-dimension slots of A and B are assigned the
+// same way in each product (lane group lg holds slots 8 lg .. 8 lg + 7 of both operands), which is
+// all the matrix product needs.  Key tiles entirely in the causal future of the 32 queries are not
+// loaded; keys of partially masked 32-key chunks get -inf (fully visible chunks skip the mask).
+// Scores are scaled by scale * log2(e) and use exp2.
 #include "common.h"
 
 using namespace vgx;
 
 namespace {
 
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kKT = 64;             // keys per LDS tile
@@ -72,12 +72,6 @@ struct PrefillArgs {
     int q_bf16;
 };
 
-// bf16 bits -> fp16 bits (exact for |v| in the fp16 normal range; smaller magnitudes become fp16
-// subnormals (error below 2^-25), magnitudes beyond 65504 are not representable: K and V must stay
-// inside that range, as attention keys and values do).
-__device__ __forceinline__ uint16_t bf2h(uint32_t b) {
-    return __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((b & 0xFFFFu) << 16));
-}
 
 template <int GRP, bool QSPLIT>
 __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
@@ -101,39 +95,44 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     const int lq = lane & 15, lg = lane >> 4;
     const int h = g * GRP + wave;
 
-    // Q^T fragments: query t0 + 16 qt + lq, dims 32 kc + 8 lg .. + 7 (fp16 hi and, for fp32 queries,
-    // the fp16 residual lo = q - hi).
-    f16x8_t qh[2][4], ql[2][4];
+    // Q^T fragments (bf16): query t0 + 16 qt + lq, dims 32 kc + 8 lg .. + 7; fp32 queries as
+    // hi = bf16(q) and lo = bf16(q - hi).
+    bf16x8_t qh[2][4], ql[2][4];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
         const int64_t t = t0 + qt * 16 + lq;
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
             const int d0 = kc * 32 + lg * 8;
-            float e[8];
+            uint32_t hb[8], lb[8];
             if (t < B.n_q) {
                 if constexpr (!QSPLIT) {
                     const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(B.q) + t * B.ldq + h * B.q_hstride + d0);
                     const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        e[2 * i] = __uint_as_float(ww[i] << 16);
-                        e[2 * i + 1] = __uint_as_float(ww[i] & 0xFFFF0000u);
+                        hb[2 * i] = ww[i] & 0xFFFFu;
+                        hb[2 * i + 1] = ww[i] >> 16;
+                        lb[2 * i] = lb[2 * i + 1] = 0;
                     }
                 } else {
                     const float *qp = static_cast<const float *>(B.q) + t * B.ldq + h * B.q_hstride + d0;
                     const float4 x0 = reinterpret_cast<const float4 *>(qp)[0], x1 = reinterpret_cast<const float4 *>(qp)[1];
-                    e[0] = x0.x; e[1] = x0.y; e[2] = x0.z; e[3] = x0.w; e[4] = x1.x; e[5] = x1.y; e[6] = x1.z; e[7] = x1.w;
+                    const float e[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        hb[i] = float_to_bf16_bits(e[i]);
+                        lb[i] = float_to_bf16_bits(e[i] - bf16_bits_to_float(hb[i]));
+                    }
                 }
             } else {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) e[i] = 0.0f;
+                for (int i = 0; i < 8; ++i) hb[i] = lb[i] = 0;
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const _Float16 hi = (_Float16)e[i];
-                qh[qt][kc][i] = hi;
-                ql[qt][kc][i] = (_Float16)(e[i] - (float)hi);
+                qh[qt][kc][i] = __builtin_bit_cast(__bf16, (uint16_t)hb[i]);
+                ql[qt][kc][i] = __builtin_bit_cast(__bf16, (uint16_t)lb[i]);
             }
         }
     }
@@ -148,109 +147,167 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
         for (int dt = 0; dt < 8; ++dt) o[qt][dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    for (int r = 0; r < B.n_runs; ++r) {
-        const RunArgs R = B.run[r];
-        const bool causal = (r == B.n_runs - 1) && B.causal_base >= 0;
-        int64_t n = R.len;
-        if (causal) n = min(n, B.causal_base + t0 + kQTile);   // later keys are in every query's future
-        const uint16_t *kbase = R.k + (int64_t)g * R.gstride;
-        const uint16_t *vbase = R.v + (int64_t)g * R.gstride;
-        for (int64_t j0 = 0; j0 < n; j0 += kKT) {
-            __syncthreads();
-            // Stage K [kKT][kD] and V^T [kD][kKT] (rows past n zero-filled).
-            for (int c = tid; c < kKT * (kD / 8); c += 64 * GRP) {
-                const int row = c >> 4, cc = c & 15;
-                uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
-                if (j0 + row < n) {
-                    kw = *reinterpret_cast<const uint4 *>(kbase + (j0 + row) * R.rstride + cc * 8);
-                    vw = *reinterpret_cast<const uint4 *>(vbase + (j0 + row) * R.rstride + cc * 8);
-                }
-                const uint4 kh = make_uint4(bf2h(kw.x) | ((uint32_t)bf2h(kw.x >> 16) << 16),
-                                            bf2h(kw.y) | ((uint32_t)bf2h(kw.y >> 16) << 16),
-                                            bf2h(kw.z) | ((uint32_t)bf2h(kw.z >> 16) << 16),
-                                            bf2h(kw.w) | ((uint32_t)bf2h(kw.w >> 16) << 16));
-                *reinterpret_cast<uint4 *>(ks + row * kKRow + cc * 8) = kh;
-                const uint32_t vv[4] = {vw.x, vw.y, vw.z, vw.w};
+    // Key tiles in order over the runs; the global loads of the next tile are issued before the
+    // current tile is computed (register double buffer), then stored into LDS (K as is, V transposed).
+    auto run_len = [&](int r) -> int64_t {
+        int64_t n = B.run[r].len;
+        if (r == B.n_runs - 1 && B.causal_base >= 0) n = min(n, B.causal_base + t0 + kQTile);  // the rest is in every query's future
+        return n;
+    };
+    constexpr int NT = 64 * GRP;
+    constexpr int KCH = kKT * (kD / 8);            // 16-byte K chunks per tile
+    constexpr int VCH = kKT / 2 * (kD / 8);        // V chunks per tile, counted in row pairs
+    constexpr int KIT = (KCH + NT - 1) / NT, VIT = (VCH + NT - 1) / NT;
+    uint4 kreg[KIT], vreg[VIT][2];
+    auto fetch = [&](int r, int64_t j0) {
+        const RunArgs &R = B.run[r];
+        const int64_t n = run_len(r);
+        const int rs = (int)R.rstride;
+        const uint16_t *kb = R.k + (int64_t)g * R.gstride + j0 * R.rstride;   // wave-uniform
+        const uint16_t *vb = R.v + (int64_t)g * R.gstride + j0 * R.rstride;
+        const int lim = (int)min<int64_t>(n - j0, kKT);                       // rows of this tile
+#pragma unroll
+        for (int i = 0; i < KIT; ++i) {
+            const int c = tid + i * NT;
+            const int row = c >> 4, cc = c & 15;
+            kreg[i] = (c < KCH && row < lim) ? *reinterpret_cast<const uint4 *>(kb + row * rs + cc * 8)
+                                             : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < VIT; ++i) {
+            const int c = tid + i * NT;
+            const int rp = c & 31, cc = c >> 5;    // consecutive lanes: consecutive row pairs
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int row = 2 * rp + h2;
+                vreg[i][h2] = (c < VCH && row < lim) ? *reinterpret_cast<const uint4 *>(vb + row * rs + cc * 8)
+                                                     : make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < KIT; ++i) {
+            const int c = tid + i * NT;
+            if (c < KCH) *reinterpret_cast<uint4 *>(ks + (c >> 4) * kKRow + (c & 15) * 8) = kreg[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VIT; ++i) {
+            const int c = tid + i * NT;
+            if (c < VCH) {
+                const int rp = c & 31, cc = c >> 5;
+                const uint32_t a0[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
+                const uint32_t a1[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    vt[(cc * 8 + 2 * e) * kVRow + row] = bf2h(vv[e]);
-                    vt[(cc * 8 + 2 * e + 1) * kVRow + row] = bf2h(vv[e] >> 16);
-                }
-            }
-            __syncthreads();
-            for (int c = 0; c < kKT && j0 + c < n; c += 32) {
-                f32x4_t s[2][2];
-#pragma unroll
-                for (int qt = 0; qt < 2; ++qt) {
-                    s[qt][0] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                    s[qt][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                }
-#pragma unroll
-                for (int kc = 0; kc < 4; ++kc) {
-                    const f16x8_t a0 = *reinterpret_cast<const f16x8_t *>(ks + (c + lq) * kKRow + kc * 32 + lg * 8);
-                    const f16x8_t a1 = *reinterpret_cast<const f16x8_t *>(ks + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt) {
-                        s[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qh[qt][kc], s[qt][0], 0, 0, 0);
-                        s[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qh[qt][kc], s[qt][1], 0, 0, 0);
-                        if constexpr (QSPLIT) {
-                            s[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, ql[qt][kc], s[qt][0], 0, 0, 0);
-                            s[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, ql[qt][kc], s[qt][1], 0, 0, 0);
-                        }
-                    }
-                }
-                f16x8_t pb[2];
-#pragma unroll
-                for (int qt = 0; qt < 2; ++qt) {
-                    const int64_t t = t0 + qt * 16 + lq;
-                    float v[8];
-#pragma unroll
-                    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int64_t key = j0 + c + kt * 16 + lg * 4 + i;
-                            const bool vis = key < n && (!causal || key <= B.causal_base + t);
-                            v[kt * 4 + i] = vis ? s[qt][kt][i] * a.scale_log2 : -INFINITY;
-                        }
-                    float mt = v[0];
-#pragma unroll
-                    for (int i = 1; i < 8; ++i) mt = fmaxf(mt, v[i]);
-                    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-                    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-                    const float mn = fmaxf(m[qt], mt);
-                    const float corr = exp2f(m[qt] - mn);
-                    m[qt] = mn;
-                    float ps = 0.0f;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const float p = exp2f(v[i] - mn);
-                        ps += p;
-                        pb[qt][i] = (_Float16)p;
-                    }
-                    lsum[qt] = lsum[qt] * corr + ps;
-#pragma unroll
-                    for (int dt = 0; dt < 8; ++dt) o[qt][dt] *= corr;
-                }
-#pragma unroll
-                for (int dt = 0; dt < 8; ++dt) {
-                    const uint16_t *vr = vt + (dt * 16 + lq) * kVRow + c + lg * 4;
-                    const uint2 lo = *reinterpret_cast<const uint2 *>(vr);
-                    const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16);
-                    const uint4 pk = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                    const f16x8_t va = __builtin_bit_cast(f16x8_t, pk);
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt)
-                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[qt], o[qt][dt], 0, 0, 0);
+                    // dims 8 cc + 2 e and + 1 of keys 2 rp, 2 rp + 1: one 4-byte word each
+                    *reinterpret_cast<uint32_t *>(vt + (cc * 8 + 2 * e) * kVRow + 2 * rp) =
+                        (a0[e] & 0xFFFFu) | (a1[e] << 16);
+                    *reinterpret_cast<uint32_t *>(vt + (cc * 8 + 2 * e + 1) * kVRow + 2 * rp) =
+                        (a0[e] >> 16) | (a1[e] & 0xFFFF0000u);
                 }
             }
         }
+    };
+
+    const float sl2 = a.scale_log2;
+    int r = 0;
+    while (r < B.n_runs && run_len(r) <= 0) ++r;
+    int64_t j0 = 0;
+    if (r < B.n_runs) fetch(r, j0);
+    while (r < B.n_runs) {
+        const int64_t n = run_len(r);
+        const bool causal = (r == B.n_runs - 1) && B.causal_base >= 0;
+        int rn = r;
+        int64_t jn = j0 + kKT;
+        if (jn >= n) {
+            jn = 0;
+            do { ++rn; } while (rn < B.n_runs && run_len(rn) <= 0);
+        }
+        __syncthreads();
+        stage();
+        __syncthreads();
+        if (rn < B.n_runs) fetch(rn, jn);
+        for (int c = 0; c < kKT && j0 + c < n; c += 32) {
+            f32x4_t sc[2][2];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                sc[qt][0] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                sc[qt][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc) {
+                const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(ks + (c + lq) * kKRow + kc * 32 + lg * 8);
+                const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(ks + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qh[qt][kc], sc[qt][0], 0, 0, 0);
+                    sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qh[qt][kc], sc[qt][1], 0, 0, 0);
+                    if constexpr (QSPLIT) {
+                        sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ql[qt][kc], sc[qt][0], 0, 0, 0);
+                        sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ql[qt][kc], sc[qt][1], 0, 0, 0);
+                    }
+                }
+            }
+            bf16x8_t ph[2], pl[2];
+            // 32-key chunk fully visible to all 32 queries: no per-score mask
+            const bool full = j0 + c + 32 <= n && (!causal || j0 + c + 31 <= B.causal_base + t0);
+            // key index relative to the causal limit of query t0 (fits in 32 bits)
+            const int kbase = (int)(j0 + c - (causal ? B.causal_base + t0 : 0));
+            const int klim = (int)(n - (j0 + c));
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                float v[8];
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int kk = kt * 16 + lg * 4 + i;       // key within the 32-key chunk
+                        const bool vis = full || (kk < klim && (!causal || kbase + kk <= qt * 16 + lq));
+                        v[kt * 4 + i] = vis ? sc[qt][kt][i] * sl2 : -INFINITY;
+                    }
+                float mt = v[0];
+#pragma unroll
+                for (int i = 1; i < 8; ++i) mt = fmaxf(mt, v[i]);
+                mt = xor32_max(xor16_max(mt));
+                const float mn = fmaxf(m[qt], mt);                    // running max in log2 units
+                const float corr = exp2f(m[qt] - mn);
+                m[qt] = mn;
+                float ps = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float p = exp2f(v[i] - mn);
+                    ps += p;
+                    const uint32_t pbh = float_to_bf16_bits(p);
+                    ph[qt][i] = __builtin_bit_cast(__bf16, (uint16_t)pbh);
+                    pl[qt][i] = __builtin_bit_cast(__bf16, (uint16_t)float_to_bf16_bits(p - bf16_bits_to_float(pbh)));
+                }
+                lsum[qt] = lsum[qt] * corr + ps;
+                if (__ballot(corr != 1.0f)) {   // some query's running max moved: rescale O
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt) o[qt][dt] *= corr;
+                }
+            }
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                const uint16_t *vr = vt + (dt * 16 + lq) * kVRow + c + lg * 4;
+                const uint2 lo = *reinterpret_cast<const uint2 *>(vr);
+                const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16);
+                const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[qt], o[qt][dt], 0, 0, 0);
+                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[qt], o[qt][dt], 0, 0, 0);
+                }
+            }
+        }
+        r = rn;
+        j0 = jn;
     }
 
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-        float L = lsum[qt];
-        L += __shfl_xor(L, 16, kWave);
-        L += __shfl_xor(L, 32, kWave);
+        const float L = xor32_sum(xor16_sum(lsum[qt]));
         const float inv = 1.0f / L;
         const int64_t t = t0 + qt * 16 + lq;
         if (t >= B.n_q) continue;
@@ -314,6 +371,7 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, in
             if (R.len > 0 && (((uintptr_t)R.k | (uintptr_t)R.v) % 16 || (R.row_stride * 2) % 16 ||
                               (R.group_stride * 2) % 16))
                 return VGX_E_ALIGN;
+            if (R.row_stride < D || R.row_stride >= (1 << 24)) return VGX_E_SIZE;   // tile offsets are 32-bit
             B.run[r].k = static_cast<const uint16_t *>(R.k);
             B.run[r].v = static_cast<const uint16_t *>(R.v);
             B.run[r].len = R.len;

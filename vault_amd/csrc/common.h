@@ -55,6 +55,26 @@ VGX_DEV float wave_max(float v) {
     return v;
 }
 
+// Combine a value with the same value in lane l ^ 16 / l ^ 32 using the gfx950 VALU lane swaps
+// (v_permlane16_swap / v_permlane32_swap) instead of an LDS permute.  With both operands equal to x,
+// the two results of a swap hold, in every lane l, x[l] and x[l ^ 16] (resp. x[l ^ 32]).
+VGX_DEV float xor16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+VGX_DEV float xor32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+VGX_DEV float xor16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+VGX_DEV float xor32_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 VGX_DEV float half_bits_to_float(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)(h & 0xFFFFu));
 }
