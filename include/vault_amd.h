@@ -107,6 +107,20 @@ int vgx_qlinear_ex(int dtype, const void *w_packed, int64_t rows, int64_t cols, 
                    int64_t batch, const float *norm_w, float eps, const float *bias, float *y, int64_t ldy,
                    int epilogue, void *stream);
 
+/* Workspace bytes of vgx_qgemm for these sizes and epilogue (256-byte aligned buffer: bf16 hi / lo
+ * splits of the activations, their per-block sums, and K-split partial sums when the GEMM splits K
+ * to fill the GPU). */
+int64_t vgx_qgemm_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, int epilogue);
+
+/* vgx_qlinear_ex for many activation rows on bf16 MFMA (Q8_0 / Q4_0 weights): same arguments and
+ * epilogues, plus a caller workspace.  The activations (after the optional RMSNorm) enter as a bf16
+ * hi + lo pair (2^-17 relative); weights, scales and the per-block fp32 accumulation are exact as in
+ * the GEMV.  Replaces the chunk-prefill projections (src/vault_v3_model.py:2051, 2095-2096 on
+ * [clen x d] blocks) and batched decode projections. */
+int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx, int64_t batch,
+              const float *norm_w, float eps, const float *bias, float *y, int64_t ldy, int epilogue, void *workspace,
+              int64_t workspace_bytes, void *stream);
+
 /* h[b, r] = silu(gate_r . x_b) * (up_r . x_b) over a vgx_qweight_pack_gateup tensor; `rows` is
  * the number of output rows (d_ff).  Replaces mlp_gu_run (runtime/vault3.c:1942-1956) and
  * F.silu(gate_proj(x)) * up_proj(x) (src/vault_v3_model.py:1149-1150). */

@@ -1,0 +1,94 @@
+"""GPU parity of the bf16-MFMA Q8_0 / Q4_0 GEMM (vgx_qgemm, used by ops.qlinear from 8 activation
+rows on) against the fp64 oracle.
+
+Bar: the GEMV accumulation bound of oracle.linalg with the relative term raised to 8e-6 for the
+bf16 hi + lo activation split (2^-17 relative per element); a dropped block, a wrong scale or a
+transposed operand is orders of magnitude beyond it.  Shapes: the model's projections at prefill and
+batched-decode row counts, ragged row and batch counts, every epilogue, with and without the fused
+RMSNorm; an invariant check that the GEMM equals the GEMV row by row within the same bound.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import codec, linalg
+from vault_amd import ops, vlt3
+
+pytestmark = pytest.mark.gpu
+
+
+def _blocks(dt, rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((rows, cols)).astype(np.float32) * 0.05
+    return vlt3.quantize(dt, w)
+
+
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
+@pytest.mark.parametrize("rows,cols,batch,epi,norm", [
+    (1536, 1536, 16, "store", False), (2048, 1536, 300, "store", True), (1536, 8960, 37, "accum", False),
+    (8960, 1536, 64, "swiglu", True), (13, 96, 9, "store", True), (256, 4608, 1024, "store", False),
+    (2, 64, 8, "swiglu", False)])
+def test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm):
+    rng = np.random.default_rng(rows + cols + batch)
+    x = (rng.standard_normal((batch, cols)) * 2.0).astype(np.float32)
+    g = rng.uniform(0.8, 1.2, cols).astype(np.float32)
+    u = linalg.rmsnorm(x, g, 1e-6) if norm else x.astype(np.float64)
+    nrm = (torch.from_numpy(g).to(dev), 1e-6) if norm else None
+    xt = torch.from_numpy(x).to(dev)
+    if epi == "swiglu":
+        gate, up = _blocks(dt, rows, cols, 1), _blocks(dt, rows, cols, 2)
+        w = ops.QWeight.gateup_from_blocks(dt, rows, cols, gate, up, dev)
+        h = ops.qlinear_swiglu(w, xt, norm=nrm).cpu().numpy().astype(np.float64)
+        gf, uf = codec.decode(dt, gate, rows, cols), codec.decode(dt, up, rows, cols)
+        gg, uu = linalg.gemv(gf, u), linalg.gemv(uf, u)
+        ref = linalg.swiglu(gg, uu)
+        tg, tu = linalg.gemv_bound(gf, u, dt, rel=8e-6), linalg.gemv_bound(uf, u, dt, rel=8e-6)
+        tol = 1.1 * np.abs(uu) * tg + np.abs(gg) * tu + 1e-6 * np.abs(ref) + 1e-30
+        err = np.abs(h - ref)
+        assert np.all(err <= tol), float((err / tol).max())
+        return
+    raw = _blocks(dt, rows, cols, 3)
+    wq = ops.QWeight.from_blocks(dt, rows, cols, raw, dev)
+    wf = codec.decode(dt, raw, rows, cols)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    ref = linalg.gemv(wf, u, bias)
+    out = None
+    if epi == "accum":
+        y0 = rng.standard_normal((batch, rows)).astype(np.float32)
+        ref = ref + y0
+        out = torch.from_numpy(y0).to(dev)
+    y = ops.qlinear(wq, xt, bias=torch.from_numpy(bias).to(dev), out=out, accumulate=epi == "accum",
+                    norm=nrm).cpu().numpy().astype(np.float64)
+    tol = linalg.gemv_bound(wf, u, dt, rel=8e-6) + np.abs(ref) * 2e-7
+    err = np.abs(y - ref)
+    assert np.all(err <= tol), float((err / tol).max())
+
+
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
+def test_qgemm_equals_gemv_rows(dev, dt):
+    """The GEMM over 40 rows equals the batch-1 GEMV applied to each row (both vs the same bound)."""
+    rows, cols, batch = 1536, 1536, 40
+    raw = _blocks(dt, rows, cols, 4)
+    wq = ops.QWeight.from_blocks(dt, rows, cols, raw, dev)
+    x = torch.randn(batch, cols, generator=torch.Generator().manual_seed(5)).to(dev)
+    big = ops.qlinear(wq, x)
+    one = torch.cat([ops.qlinear(wq, x[i:i + 1]) for i in range(batch)])
+    wf = codec.decode(dt, raw, rows, cols)
+    tol = torch.from_numpy(2 * linalg.gemv_bound(wf, x.cpu().numpy(), dt, rel=8e-6)).to(dev)
+    assert bool(((big.double() - one.double()).abs() <= tol).all())
+
+
+@pytest.mark.parametrize("dt", [codec.Q4_0])
+@pytest.mark.parametrize("rows,cols,batch", [(64, 7200, 8), (16, 4096, 8)])
+def test_qgemm_k_split_edges(dev, dt, rows, cols, batch):
+    """Few weight rows and long rows: the GEMM splits K over many workgroups (up to 16), including
+    a possibly empty last split (225 blocks over 16 splits)."""
+    rng = np.random.default_rng(rows + cols)
+    raw = _blocks(dt, rows, cols, 6)
+    wq = ops.QWeight.from_blocks(dt, rows, cols, raw, dev)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    y = ops.qlinear(wq, torch.from_numpy(x).to(dev)).cpu().numpy().astype(np.float64)
+    wf = codec.decode(dt, raw, rows, cols)
+    ref = linalg.gemv(wf, x)
+    tol = linalg.gemv_bound(wf, x, dt, rel=8e-6)
+    assert np.all(np.abs(y - ref) <= tol)

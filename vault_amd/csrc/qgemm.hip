@@ -1,0 +1,404 @@
+// Q8_0 / Q4_0 block-dequant GEMM on bf16 MFMA for many activation rows (chunk prefill, batched
+// decode): Y[b, r] = sum_c W[r, c] * u[b, c] (+ bias, residual or SwiGLU epilogue), u = x or
+// RMSNorm(x).
+//
+// Reference semantics: the same projections as the GEMV (runtime/vault3.c:499-624, 1942-1956;
+// src/vault_v3_model.py:1036-1047, 1145-1150, 2051, 2095-2096) applied to a [rows of tokens x cols]
+// activation block.
+//
+// Exactness.  One v_mfma_f32_16x16x32_bf16 spans exactly one 32-weight quant block.  The weights
+// enter the MFMA as unsigned integers, exact in bf16: Q8_0 as q + 128 (byte ^ 0x80), Q4_0 as the
+// nibble n.  The activations enter as a bf16 pair hi + lo (hi = bf16(u), lo = bf16(u - hi); 2^-17
+// relative), prepared once by xsplit_kernel together with the per-block sums S_b = sum_j (hi + lo).
+// Per block the fp32 MFMA result C (= sum_j w_j (hi_j + lo_j)) is corrected and scaled in fp32:
+//   acc += d * (C - off * S_b),   off = 128 (Q8_0) or 8 (Q4_0),
+// which is the reference's sum_b d_b sum_j q_j x_j with the activations rounded to 16 significant
+// bits.
+//
+// Mapping.  A workgroup of 4 waves covers 128 weight rows x 16 NC activation rows; each wave owns
+// 32 weight rows (two 16-row MFMA tiles) x 16 NC activation rows.  In the MFMA a lane of a 16-row
+// tile owns one weight row (l % 16) for the A operand and one activation row (l % 16) for the B
+// operand, both with the K slots 8 (l / 16) .. + 7 of the block (weights 8 lg .. 8 lg + 7); the
+// accumulator lane holds weight rows 4 (l / 16) .. + 3 (one packed row-quad, whose four fp16 scales
+// are one 8-byte load) of activation row l % 16.  Blocks go in groups of four with the next group's
+// weights, scales and activation fragments requested before the current group is multiplied.
+#include "qgemv.h"
+
+using namespace vgx;
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// u = (norm ? lnw * x * inv_rms : x); writes hi / lo bf16 rows and per-block sums of hi + lo.
+// One workgroup of 256 threads per activation row.
+__global__ __launch_bounds__(256) void xsplit_kernel(const float *__restrict__ x, int64_t ldx,
+                                                      const float *__restrict__ lnw, float eps, int cols,
+                                                      uint16_t *__restrict__ xh, uint16_t *__restrict__ xl,
+                                                      float *__restrict__ xsum) {
+    __shared__ float red[4];
+    const int64_t b = blockIdx.x;
+    const float *xr = x + b * ldx;
+    float inv = 1.0f;
+    if (lnw) {
+        float s = 0.0f;
+        for (int i = threadIdx.x; i < cols; i += 256) s = fmaf(xr[i], xr[i], s);
+        s = wave_sum(s);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+        __syncthreads();
+        inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)cols + eps);
+    }
+    const int nblk = cols / QK;
+    // a wave handles blocks, a lane two consecutive elements (64 lanes = 2 blocks per step)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int blk0 = wave * 2; blk0 < nblk; blk0 += 8) {
+        const int blk = blk0 + (lane >> 5);
+        const bool ok = blk < nblk;
+        float hs = 0.0f;
+        if (ok) {
+            const int c = blk * QK + (lane & 31);
+            float u = xr[c];
+            if (lnw) u = lnw[c] * (u * inv);
+            const uint32_t hb = float_to_bf16_bits(u);
+            const uint32_t lb = float_to_bf16_bits(u - bf16_bits_to_float(hb));
+            xh[b * cols + c] = (uint16_t)hb;
+            xl[b * cols + c] = (uint16_t)lb;
+            hs = bf16_bits_to_float(hb) + bf16_bits_to_float(lb);
+        }
+        // sum over the 32 lanes of each half-wave
+        hs = row16_sum(hs);
+        hs += __shfl_xor(hs, 16, kWave);
+        if (ok && (lane & 31) == 0) xsum[b * nblk + blk] = hs;
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ uint2 load_a(const uint8_t *__restrict__ W, int64_t rq, int nblk, int blk, int r4, int lg) {
+    // Q8_0: bytes 8 lg .. + 7 of row r4 of the row-quad block; Q4_0: bytes 8 (lg & 1) .. + 7
+    constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
+    const uint8_t *p = W + ((rq * nblk + blk) * 4 + r4) * QB + (DT == VGX_Q8_0 ? 8 * lg : 8 * (lg & 1));
+    return *reinterpret_cast<const uint2 *>(p);
+}
+
+// 8 quant values -> 8 unsigned integers as bf16 (exact): weights 8 lg .. 8 lg + 7 of the block.
+template <int DT>
+__device__ __forceinline__ bf16x8_t a_frag(uint2 w, int lg) {
+    uint32_t u[2] = {w.x, w.y};
+    if constexpr (DT == VGX_Q8_0) {
+        u[0] ^= 0x80808080u;
+        u[1] ^= 0x80808080u;
+    } else {
+        const int sh = (lg >> 1) * 4;   // low nibbles for weights 0..15, high nibbles for 16..31
+        u[0] = (u[0] >> sh) & 0x0F0F0F0Fu;
+        u[1] = (u[1] >> sh) & 0x0F0F0F0Fu;
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float f0 = (float)(u[i] & 0xFFu), f1 = (float)((u[i] >> 8) & 0xFFu);
+        const float f2 = (float)((u[i] >> 16) & 0xFFu), f3 = (float)(u[i] >> 24);
+        // small integers: the bf16 is the top half of the fp32 bits, exactly
+        o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
+        o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xFFFF0000u);
+    }
+    return __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
+template <int DT, int NC, int EPI, bool SPLIT>
+__global__ __launch_bounds__(256) void qgemm_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
+                                                     int nblk, int64_t rows_out, const uint16_t *__restrict__ xh,
+                                                     const uint16_t *__restrict__ xl, const float *__restrict__ xsum,
+                                                     int64_t batch, const float *__restrict__ bias,
+                                                     float *__restrict__ y, int64_t ldy, float *__restrict__ part,
+                                                     int kper) {
+    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 8.0f;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int cols = nblk * QK;
+    // weight rows of this wave: two 16-row tiles = row-quads rq0 + 4 t + (l16 / 4) for the A operand
+    const int64_t rq_wave = ((int64_t)blockIdx.x * 4 + wave) * 8;     // 8 row-quads = 32 rows per wave
+    const int64_t b0 = (int64_t)blockIdx.y * 16 * NC;                  // first activation row
+
+    int64_t arq[2];
+    bool aok[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        arq[t] = rq_wave + 4 * t + (l16 >> 2);
+        aok[t] = arq[t] < n_rq;
+    }
+    const int r4 = l16 & 3;
+    int64_t crq[2];
+    bool cok[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        crq[t] = rq_wave + 4 * t + lg;       // row-quad of the accumulator lane
+        cok[t] = crq[t] < n_rq;
+    }
+    int64_t bb[NC];
+    bool bok[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        bb[c] = b0 + 16 * c + l16;
+        bok[c] = bb[c] < batch;
+    }
+
+    f32x4_t acc[2][NC];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[t][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Register double buffer of kGrp blocks: the loads of group g + 1 are in flight while group g is
+    // multiplied (one block of lookahead cannot cover HBM latency).
+    constexpr int kGrp = 4;
+    struct Blk {
+        uint2 wa[2], sc[2];
+        uint4 xh[NC], xl[NC];
+        float xs[NC];
+    };
+    Blk buf[2][kGrp];
+    // K range of this workgroup (blockIdx.z-th split of kper blocks when SPLIT)
+    const int blk_lo = SPLIT ? (int)blockIdx.z * kper : 0;
+    const int blk_hi = SPLIT ? min(nblk, blk_lo + kper) : nblk;
+    auto fetch = [&](Blk (&gb)[kGrp], int g0) {
+#pragma unroll
+        for (int u = 0; u < kGrp; ++u) {
+            const int blk = g0 + u;
+            const bool in = blk < blk_hi;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                gb[u].wa[t] = (in && aok[t]) ? load_a<DT>(W, arq[t], nblk, blk, r4, lg) : make_uint2(0, 0);
+                gb[u].sc[t] = (in && cok[t]) ? *reinterpret_cast<const uint2 *>(W + soff + (crq[t] * nblk + blk) * 8)
+                                             : make_uint2(0, 0);
+            }
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                if (in && bok[c]) {
+                    const int64_t o = bb[c] * cols + blk * QK + 8 * lg;
+                    gb[u].xh[c] = *reinterpret_cast<const uint4 *>(xh + o);
+                    gb[u].xl[c] = *reinterpret_cast<const uint4 *>(xl + o);
+                    gb[u].xs[c] = xsum[bb[c] * nblk + blk];
+                } else {
+                    gb[u].xh[c] = gb[u].xl[c] = make_uint4(0, 0, 0, 0);
+                    gb[u].xs[c] = 0.0f;
+                }
+            }
+        }
+    };
+    auto compute = [&](const Blk &k) {
+        bf16x8_t af[2];
+        float d[2][4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            af[t] = a_frag<DT>(k.wa[t], lg);
+            d[t][0] = half_bits_to_float(k.sc[t].x);
+            d[t][1] = half_bits_to_float(k.sc[t].x >> 16);
+            d[t][2] = half_bits_to_float(k.sc[t].y);
+            d[t][3] = half_bits_to_float(k.sc[t].y >> 16);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                f32x4_t pr = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, k.xh[c]), pr, 0, 0, 0);
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, k.xl[c]), pr, 0, 0, 0);
+                const float corr = OFF * k.xs[c];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf(d[t][i], pr[i] - corr, acc[t][c][i]);
+            }
+    };
+    // Blocks past blk_hi are zero-filled (weights 0, scales 0): they add nothing.
+    if (blk_lo < blk_hi) fetch(buf[0], blk_lo);   // the last split can be empty (then its partials are zero)
+    for (int g0 = blk_lo, it = 0; g0 < blk_hi; g0 += kGrp, ++it) {
+        if (it & 1) {
+            if (g0 + kGrp < blk_hi) fetch(buf[0], g0 + kGrp);
+#pragma unroll
+            for (int u = 0; u < kGrp; ++u) compute(buf[1][u]);
+        } else {
+            if (g0 + kGrp < blk_hi) fetch(buf[1], g0 + kGrp);
+#pragma unroll
+            for (int u = 0; u < kGrp; ++u) compute(buf[0][u]);
+        }
+    }
+
+    // Split K: raw per-split sums part[z][b][packed row]; the reduce kernel applies the epilogue.
+    if constexpr (SPLIT) {
+        const int64_t rows_p = n_rq * 4;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (!cok[t]) continue;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                if (!bok[c]) continue;
+                float4 v;
+                v.x = acc[t][c][0]; v.y = acc[t][c][1]; v.z = acc[t][c][2]; v.w = acc[t][c][3];
+                *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + bb[c]) * rows_p + crq[t] * 4) = v;
+            }
+        }
+        return;
+    }
+    // Epilogue: lane holds rows 4 crq .. + 3 of activation row bb.
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        if (!cok[t]) continue;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (!bok[c]) continue;
+            float *yr = y + bb[c] * ldy;
+            if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int64_t o = crq[t] * 2 + k;
+                    if (o >= rows_out) continue;
+                    const float g = acc[t][c][k], u = acc[t][c][2 + k];
+                    yr[o] = g / (1.0f + __expf(-g)) * u;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t row = crq[t] * 4 + i;
+                    if (row >= rows_out) continue;
+                    float v = acc[t][c][i];
+                    if (bias) v += bias[row];
+                    if constexpr (EPI == EPI_ACCUM) v += yr[row];
+                    yr[row] = v;
+                }
+            }
+        }
+    }
+}
+
+// Sum of the K-split partials + epilogue.  One thread per output (b, row); SwiGLU reads the gate and
+// up sums of packed row-quad q (sub-rows k and 2 + k) for output row 2 q + k.
+template <int EPI>
+__global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float *__restrict__ part, int ks, int64_t batch,
+                                                            int64_t rows_p, int64_t rows_out,
+                                                            const float *__restrict__ bias, float *__restrict__ y,
+                                                            int64_t ldy) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= batch * rows_out) return;
+    const int64_t b = i / rows_out, r = i - b * rows_out;
+    float *yr = y + b * ldy;
+    if constexpr (EPI == EPI_SWIGLU) {
+        const int64_t q = r >> 1, k = r & 1;
+        float g = 0.0f, u = 0.0f;
+        for (int s = 0; s < ks; ++s) {
+            const float *p = part + (s * batch + b) * rows_p + q * 4;
+            g += p[k];
+            u += p[2 + k];
+        }
+        yr[r] = g / (1.0f + __expf(-g)) * u;
+    } else {
+        float v = 0.0f;
+        for (int s = 0; s < ks; ++s) v += part[(s * batch + b) * rows_p + r];
+        if (bias) v += bias[r];
+        if constexpr (EPI == EPI_ACCUM) v += yr[r];
+        yr[r] = v;
+    }
+}
+
+inline int64_t rows4(int64_t r) { return (r + 3) / 4 * 4; }
+
+int64_t gemm_scale_off(int dt, int64_t rows, int64_t cols) {
+    const int64_t q = rows4(rows) * (cols / QK) * (dt == VGX_Q8_0 ? 32 : 16);
+    return (q + 255) / 256 * 256;
+}
+
+inline int64_t split_bytes(int64_t batch, int64_t cols) {
+    const int64_t h = (batch * cols * 2 + 255) / 256 * 256;
+    return 2 * h + (batch * (cols / QK) * 4 + 255) / 256 * 256;
+}
+
+constexpr int kMaxKSplit = 16;
+constexpr int kTargetWaves = 2048;
+
+// K splits: enough waves to fill the GPU, at least 8 blocks per split.
+int choose_ksplit(int64_t n_rq, int64_t batch, int nc, int nblk) {
+    const int64_t waves = (n_rq + 7) / 8 * ((batch + 16 * nc - 1) / (16 * nc));
+    int64_t ks = (kTargetWaves + waves - 1) / waves;
+    ks = std::min<int64_t>(ks, std::min<int64_t>(kMaxKSplit, nblk / 8));
+    return (int)std::max<int64_t>(1, ks);
+}
+
+inline int64_t part_bytes(int ks, int64_t batch, int64_t rows_p) {
+    return ks > 1 ? ((int64_t)ks * batch * rows_p * 4 + 255) / 256 * 256 : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t vgx_qgemm_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, int epilogue) {
+    if (batch <= 0 || rows <= 0 || cols <= 0) return VGX_E_SIZE;
+    if (cols % QK) return VGX_E_SHAPE;
+    const int64_t rows_p = rows4(epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows);
+    const int nc = batch <= 16 ? 1 : 2;
+    const int ks = choose_ksplit(rows_p / 4, batch, nc, (int)(cols / QK));
+    return split_bytes(batch, cols) + part_bytes(ks, batch, rows_p);
+}
+
+int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx, int64_t batch,
+              const float *norm_w, float eps, const float *bias, float *y, int64_t ldy, int epilogue, void *workspace,
+              int64_t workspace_bytes, void *stream) {
+    if (dtype != VGX_Q8_0 && dtype != VGX_Q4_0) return VGX_E_DTYPE;
+    if (!w_packed || !x || !y) return VGX_E_ARG;
+    if (epilogue != VGX_EPI_STORE && epilogue != VGX_EPI_ACCUM && epilogue != VGX_EPI_SWIGLU) return VGX_E_ARG;
+    if (epilogue == VGX_EPI_SWIGLU && bias) return VGX_E_ARG;
+    if (rows <= 0 || cols <= 0 || batch < 0 || ldx < cols || ldy < rows) return VGX_E_SIZE;
+    if (cols % QK || (epilogue == VGX_EPI_SWIGLU && rows % 2)) return VGX_E_SHAPE;
+    if (norm_w && !(eps > 0.0f)) return VGX_E_ARG;
+    if (batch == 0) return VGX_OK;
+    if (batch > 65535 * 32 || cols / QK > (1 << 24)) return VGX_E_LIMIT;
+    const int64_t rows_packed = epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows;
+    const int nblk = (int)(cols / QK);
+    const int64_t n_rq = rows4(rows_packed) / 4;
+    const int nc = batch <= 16 ? 1 : 2;
+    const int ks = choose_ksplit(n_rq, batch, nc, nblk);
+    if (!workspace || workspace_bytes < split_bytes(batch, cols) + part_bytes(ks, batch, n_rq * 4)) return VGX_E_ARENA;
+    if ((uintptr_t)workspace % 256) return VGX_E_ALIGN;
+    const int64_t soff = gemm_scale_off(dtype, rows_packed, cols);
+    auto *xh = static_cast<uint16_t *>(workspace);
+    auto *xl = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + (batch * cols * 2 + 255) / 256 * 256);
+    auto *xs = reinterpret_cast<float *>(static_cast<char *>(workspace) + 2 * ((batch * cols * 2 + 255) / 256 * 256));
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(xsplit_kernel, dim3((unsigned)batch), dim3(256), 0, st, x, ldx, norm_w, eps, (int)cols, xh, xl,
+                       xs);
+    VGX_CHECK_LAUNCH();
+    auto *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + split_bytes(batch, cols));
+    const int kper = (nblk + ks - 1) / ks;
+    const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 16 * nc - 1) / (16 * nc)), (unsigned)ks);
+    const auto *w = static_cast<const uint8_t *>(w_packed);
+#define VGX_GEMM_GO(DT, NC, EPI, SP)                                                                      \
+    hipLaunchKernelGGL((qgemm_kernel<DT, NC, EPI, SP>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, xh, xl, \
+                       xs, batch, bias, y, ldy, part, kper)
+#define VGX_GEMM_EPI(DT, NC)                                                                              \
+    do {                                                                                                  \
+        if (ks > 1) VGX_GEMM_GO(DT, NC, EPI_STORE, true);                                                 \
+        else if (epilogue == VGX_EPI_SWIGLU) VGX_GEMM_GO(DT, NC, EPI_SWIGLU, false);                      \
+        else if (epilogue == VGX_EPI_ACCUM) VGX_GEMM_GO(DT, NC, EPI_ACCUM, false);                        \
+        else VGX_GEMM_GO(DT, NC, EPI_STORE, false);                                                       \
+    } while (0)
+    if (dtype == VGX_Q8_0) {
+        if (nc == 1) VGX_GEMM_EPI(VGX_Q8_0, 1); else VGX_GEMM_EPI(VGX_Q8_0, 2);
+    } else {
+        if (nc == 1) VGX_GEMM_EPI(VGX_Q4_0, 1); else VGX_GEMM_EPI(VGX_Q4_0, 2);
+    }
+#undef VGX_GEMM_EPI
+#undef VGX_GEMM_GO
+    VGX_CHECK_LAUNCH();
+    if (ks > 1) {
+        const unsigned g = (unsigned)((batch * rows + 255) / 256);
+        if (epilogue == VGX_EPI_SWIGLU)
+            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_SWIGLU>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy);
+        else if (epilogue == VGX_EPI_ACCUM)
+            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_ACCUM>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy);
+        else
+            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_STORE>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy);
+        VGX_CHECK_LAUNCH();
+    }
+    return VGX_OK;
+}
+
+}  // extern "C"

@@ -436,7 +436,8 @@ class VAULTv3ForCausalLM:
             return self._decode_launch(st, spec, bias_on)
         self._size_workspace(st)
         key = spec + tuple(t.data_ptr() for t in (st.k_prev, st.k_cur, st.v_prev, st.v_cur, st.kraw_cur, st.k_seg_rot,
-                                                   st.v_seg, st.sc_cur, self._table, self.ws.buf))
+                                                   st.v_seg, st.sc_cur, self._table, self.ws.buf,
+                                                   ops.gemm_workspace(self.device).buf))
         ent = st.graphs.get(key)
         if ent is None:
             # No destructor may run HIP calls while the stream captures: collect garbage now and keep
@@ -459,10 +460,19 @@ class VAULTv3ForCausalLM:
         return ent[1].clone()
 
     def _size_workspace(self, st: VAULTv3State) -> None:
-        """Grow the attention workspace before a capture (a captured graph holds its address) to the
-        bound of any decode step of this batch size: B * H * 64 splits * (D + 2) floats."""
+        """Grow the workspaces before a capture (a captured graph holds their addresses): attention to
+        the bound of any decode step of this batch size (B * H * 64 splits * (D + 2) floats), and the
+        GEMM activation splits for batches that use the MFMA GEMM."""
         cfg = self.cfg
         self.ws.get(st.batch * cfg.n_heads * 64 * (cfg.head_dim + 2) * 4)
+        if st.batch >= ops.GEMM_MIN_ROWS:
+            lib = ops.L.load()
+            shapes = [(cfg.d_ff, cfg.d_model, ops.L.EPI_SWIGLU), (cfg.d_model, cfg.d_ff, ops.L.EPI_ACCUM),
+                      ((cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim, cfg.d_model, ops.L.EPI_STORE),
+                      (cfg.d_model, cfg.n_heads * cfg.head_dim, ops.L.EPI_ACCUM),
+                      (cfg.vocab_size, cfg.d_model, ops.L.EPI_STORE)]
+            need = max(int(lib.vgx_qgemm_workspace_bytes(st.batch, r, c, e)) for r, c, e in shapes)
+            ops.gemm_workspace(self.device).get(need)
 
     def _decode_launch(self, st: VAULTv3State, spec: tuple, bias_on: bool) -> torch.Tensor:
         """Every kernel of one decode step (embedding -> 28 layers -> scorer -> LM head) for the chunk

@@ -104,6 +104,19 @@ class QWeight:
         return rows * (self.cols // 32) * BLOCK_BYTES[self.dtype]
 
 
+GEMM_MIN_ROWS = 8   # activation rows from which Q8_0 / Q4_0 projections run on the MFMA GEMM
+_GEMM_WS: dict = {}
+
+
+def gemm_workspace(device) -> "Workspace":
+    """Per-device workspace of the MFMA GEMM's activation splits (grow-only; a captured graph holds its
+    address, so callers that capture size it first)."""
+    key = str(torch.device(device))
+    if key not in _GEMM_WS:
+        _GEMM_WS[key] = Workspace(torch.device(device))
+    return _GEMM_WS[key]
+
+
 def _gemv(w: QWeight, x: torch.Tensor, out: Optional[torch.Tensor], epi: int, bias: Optional[torch.Tensor],
           norm: Optional[Tuple[torch.Tensor, float]]) -> torch.Tensor:
     _need(x, torch.float32, "x")
@@ -123,6 +136,14 @@ def _gemv(w: QWeight, x: torch.Tensor, out: Optional[torch.Tensor], epi: int, bi
     nw, eps = (None, 0.0) if norm is None else norm
     if nw is not None:
         _need(nw, torch.float32, "norm weight")
+    if B >= GEMM_MIN_ROWS and w.dtype in (Q8_0, Q4_0):
+        lib = L.load()
+        need = int(lib.vgx_qgemm_workspace_bytes(B, w.rows, w.cols, epi))
+        ws = gemm_workspace(x.device).get(need)
+        L.check(lib.vgx_qgemm(w.dtype, w.packed.data_ptr(), w.rows, w.cols, x2.data_ptr(), x2.stride(0), B, _ptr(nw),
+                              float(eps), _ptr(bias), y2.data_ptr(), y2.stride(0), epi, ws.data_ptr(), ws.numel(),
+                              _stream(x.device)), "vgx_qgemm")
+        return out
     L.check(L.load().vgx_qlinear_ex(w.dtype, w.packed.data_ptr(), w.rows, w.cols, x2.data_ptr(), x2.stride(0), B,
                                     _ptr(nw), float(eps), _ptr(bias), y2.data_ptr(), y2.stride(0), epi,
                                     _stream(x.device)), "vgx_qlinear_ex")
