@@ -235,6 +235,76 @@ def cpu_baseline(cfg, tensors, budget_s: float = 15.0):
                       f"{threads} threads"}
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "traffic_gateup_swiglu_q4_gemv_1p5b.md")
+COPY_BYTES = 256 << 20      # calibration stream for the PMC byte counters (read and written once)
+
+
+def pmc_launches(dev, rounds: int = 8) -> None:
+    """The launches the PMC runs count: the dominant kernel eagerly over the 28 layers' weights
+    (``rounds`` times) and a plain streaming kernel that reads and writes COPY_BYTES once (torch's
+    elementwise negation, a name no other launch here has), ``rounds`` times."""
+    import torch
+    cfg = model_config()
+    model, _ = build_model(cfg, dev, torch.float32)
+    from vault_amd import ops
+    x = torch.randn(1, cfg.d_model, device=dev)
+    h = torch.empty(1, cfg.d_ff, device=dev)
+    lnw = model.w.layers[0].ln2
+    src = torch.randn(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(rounds):
+        for lw in model.w.layers:
+            ops.qlinear_swiglu(lw.wgu, x, out=h, norm=(lnw, cfg.rms_eps))
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    _log(f"pmc launches done: {rounds} x {len(model.w.layers)} gate/up GEMVs, {rounds} streams of {COPY_BYTES} B")
+
+
+def _pmc_avg(csv_path: str, counter: str, name_part: str) -> tuple[float, int]:
+    import csv
+    vals = []
+    with open(csv_path, newline="") as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] == counter and name_part in r["Kernel_Name"]:
+                vals.append(float(r["Counter_Value"]))
+    if not vals:
+        raise SystemExit(f"{csv_path}: no {counter} rows for kernels matching {name_part!r}")
+    return sum(vals) / len(vals), len(vals)
+
+
+def pmc_report(fetch_csv: str, write_csv: str) -> None:
+    """Markdown summary of the two PMC runs: per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the
+    dominant kernel and of the calibration copy, the copy's bytes / counter factor, and the scaled
+    HBM traffic per launch of the dominant kernel (the figure ``roofline.traffic`` reports)."""
+    kern, copy = "qgemv_kernel<9, 1, 2, 0, 1, true>", "neg_kernel"
+    fk, nk = _pmc_avg(fetch_csv, "FETCH_SIZE", kern)
+    fc, nc = _pmc_avg(fetch_csv, "FETCH_SIZE", copy)
+    wk, _ = _pmc_avg(write_csv, "WRITE_SIZE", kern)
+    wc, _ = _pmc_avg(write_csv, "WRITE_SIZE", copy)
+    f_scale, w_scale = COPY_BYTES / (fc * 1024), COPY_BYTES / (wc * 1024)
+    traffic = fk * 1024 * f_scale + wk * 1024 * w_scale
+    algo = 15_524_864
+    print(f"| dispatches | kernel | FETCH_SIZE KiB | WRITE_SIZE KiB |\n|---|---|---|---|\n"
+          f"| {nk} | `{kern}` (gate/up SwiGLU Q4_0 GEMV) | {fk:.1f} | {wk:.1f} |\n"
+          f"| {nc} | torch `neg` elementwise kernel ({COPY_BYTES} B read + written) | {fc:.1f} | {wc:.1f} |\n\n"
+          f"copy calibration: fetch factor {f_scale:.4f}, write factor {w_scale:.4f} (bytes / (KiB x 1024))\n\n"
+          f"algorithmic bytes per launch: {algo}\n\n"
+          f"traffic_bytes_per_launch: {traffic:.0f}\n\n"
+          f"traffic / algorithmic: {traffic / algo:.3f}")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed PMC summary, or None."""
+    import re
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            m = re.search(r"traffic_bytes_per_launch: (\d+)", f.read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -244,7 +314,14 @@ def main() -> int:
     ap.add_argument("--kv", choices=("fp32", "bf16"), default="fp32")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernels", action="store_true", help="skip the secondary kernel figures")
+    ap.add_argument("--pmc", action="store_true",
+                    help="only run the launches the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count")
+    ap.add_argument("--pmc-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two rocprofv3 counter_collection.csv files (no GPU needed)")
     args = ap.parse_args()
+    if args.pmc_report:
+        pmc_report(*args.pmc_report)
+        return 0
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (decode shards by "
               "independent sequences with no exchange); run with --gpus 1", file=sys.stderr)
@@ -256,6 +333,9 @@ def main() -> int:
     from vault_amd import _lib
     _lib.load()
     dev = torch.device("cuda:0")
+    if args.pmc:
+        pmc_launches(dev)
+        return 0
     kv_dtype = torch.float32 if args.kv == "fp32" else torch.bfloat16
     cfg = model_config()
     model, tensors = build_model(cfg, dev, kv_dtype)
@@ -296,7 +376,7 @@ def main() -> int:
                    "kv_dtype": args.kv, "parallelism": "single GPU"},
         "step_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": dom["kernel"], "avg_us": round(dom["avg_us"], 3),
                      "bytes_per_launch": dom["bytes_per_launch"]},
         "cpu_baseline": cpu,

@@ -50,6 +50,8 @@ def _load():
         lib.ref_state_info.argtypes = [C.c_void_p] + [C.c_void_p] * 4
         lib.ref_mem_pos.argtypes = [C.c_void_p, C.c_void_p]
         lib.ref_seed_long_context.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint64]
+        lib.ref_state_field.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p]
+        lib.ref_state_field.restype = C.c_int64
         lib.ref_seed_long_context.restype = C.c_int
         _lib = lib
     return _lib
@@ -97,6 +99,21 @@ class RefRuntime:
         out = np.zeros(max(1, n), dtype=np.uint64)
         _load().ref_mem_pos(self._h, out.ctypes.data)
         return out[:n].astype(np.int64)
+
+    FIELDS = ("k_prev", "k_cur", "v_prev", "v_cur", "kraw_prev", "kraw_cur", "k_sink_raw", "k_sink_rot",
+              "v_sink", "k_seg_raw", "k_seg_rot", "v_seg")
+
+    def state_field(self, layer: int, name: str, n_kv_heads: int, head_dim: int) -> np.ndarray:
+        """One layer's KV field of the runtime state as a [G, rows, D] float32 copy."""
+        lib = _load()
+        f = self.FIELDS.index(name)
+        rows = lib.ref_state_field(self._h, layer, f, None)
+        if rows < 0:
+            raise RuntimeError(f"ref_state_field({layer}, {name}) rejected")
+        out = np.empty((n_kv_heads, rows, head_dim), dtype=np.float32)
+        if rows:
+            lib.ref_state_field(self._h, layer, f, out.ctypes.data)
+        return out
 
     def seed_long_context(self, pos: int, n_pin: int, mem_cnt: int, seed: int = 0) -> None:
         rc = _load().ref_seed_long_context(self._h, pos, n_pin, mem_cnt, seed)

@@ -192,6 +192,23 @@ void ref_mem_pos(ref_ctx *c, uint64_t *out) {
     for (uint32_t i = 0; i < c->s.mem_cnt; i++) out[i] = c->s.mem_pos[i];
 }
 
+/* Copy one layer's KV field out of the state, as [G][rows][D] floats (rows = W for the window
+ * fields 0-5, sink_cap for the sink fields 6-8, seg_cap for the segment fields 9-11; field order
+ * k_prev k_cur v_prev v_cur kraw_prev kraw_cur k_sink_raw k_sink v_sink k_seg_raw k_seg v_seg).
+ * Returns the number of rows, or -1. */
+int64_t ref_state_field(ref_ctx *c, uint32_t layer, uint32_t field, float *out) {
+    const v3_state *s = &c->s;
+    const v3_model *m = &c->m;
+    if (layer >= m->n_layers || field > 11) return -1;
+    const v3_layer_state *L = &s->ls[layer];
+    const float *src[12] = {L->k_prev, L->k_cur, L->v_prev, L->v_cur, L->kraw_prev, L->kraw_cur,
+                            L->k_sink_raw, L->k_sink, L->v_sink, L->k_seg_raw, L->k_seg, L->v_seg};
+    uint64_t rows = field < 6 ? m->window : field < 9 ? s->sink_cap : s->seg_cap;
+    if (!src[field]) return rows ? -1 : 0;
+    if (out) memcpy(out, src[field], sizeof(float) * m->n_kv_heads * rows * m->head_dim);
+    return (int64_t)rows;
+}
+
 static uint64_t splitmix(uint64_t *x) {
     uint64_t z = (*x += 0x9E3779B97F4A7C15ull);
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
