@@ -68,6 +68,14 @@ int vgx_qweight_pack(int dtype, const void *src_blocks, void *dst_packed, int64_
 int vgx_qweight_pack_gateup(int dtype, const void *gate_blocks, const void *up_blocks, void *dst_packed,
                             int64_t rows, int64_t cols, void *stream);
 
+/* Like vgx_qweight_pack with the rows of every head of head_dim rows among the first n_rope_rows
+ * reordered so that packed row-quad j of a head holds rows 2j, 2j + head_dim/2, 2j + 1,
+ * 2j + 1 + head_dim/2 (two RoPE rotation pairs); later rows keep their order.  The layout that
+ * vgx_qkv_rope_step reads (q rows: n_rope_rows = rows; k|v rows: n_rope_rows = the k rows).
+ * Same bytes as the reference tensor, reordered (tools/vlt3.py:98-99 blocks). */
+int vgx_qweight_pack_rope(int dtype, const void *src_blocks, void *dst_packed, int64_t rows, int64_t cols,
+                          int64_t head_dim, int64_t n_rope_rows, void *stream);
+
 /* Packed layout -> VLT3 AoS blocks (inverse of vgx_qweight_pack; bit-exact round trip). */
 int vgx_qweight_unpack(int dtype, const void *packed, void *dst_blocks, int64_t rows, int64_t cols,
                        void *stream);
@@ -241,6 +249,21 @@ int vgx_rope_qkv_write_step(int kv_dtype, float *q, int64_t ldq, const float *k,
                             int64_t dst_bstride, int64_t dst_gstride, int64_t dst_rstride, void *sink_k_raw,
                             void *sink_v, int64_t sink_bstride, int64_t sink_gstride, int64_t sink_rstride,
                             void *stream);
+
+/* One decode token (batch 1): RMSNorm + q / k / v projections + bias, RoPE of q and k, and the
+ * ring / sink writes of vgx_rope_qkv_write_step, in one launch.  wq: [H*D x d_model] and wkv:
+ * [2*G*D x d_model] (k rows then v rows) packed with vgx_qweight_pack_rope (n_rope_rows = H*D for q,
+ * G*D for k|v); dtype pairs (q, k|v): (Q4_0, Q8_0) or equal Q8_0 / Q4_0 / F32.  bq [H*D] and bkv
+ * [2*G*D] are the natural-order biases (may be NULL).  q_out [H][D] receives the rotated query;
+ * k_rot / k_raw / v_dst and sink_k_raw / sink_v (both or neither) are state tensors of kv_dtype
+ * addressed as in vgx_rope_qkv_write_step with batch 0; x_copy (may be NULL) receives a copy of x.
+ * x, norm_w and x_copy must be 16-byte aligned.  Replaces src/vault_v3_model.py:2289-2290,
+ * 1041-1047, 1079-1094 and runtime/vault3.c:2152-2179 for one token. */
+int vgx_qkv_rope_step(int q_dtype, const void *wq, const float *bq, int kv_wdtype, const void *wkv, const float *bkv,
+                      int64_t d_model, int64_t H, int64_t G, int64_t D, const float *x, const float *norm_w, float eps,
+                      float *x_copy, const float *table, int64_t table_rstride, const int32_t *step, float *q_out,
+                      int kv_dtype, void *k_rot, void *k_raw, void *v_dst, int64_t dst_gstride, int64_t dst_rstride,
+                      void *sink_k_raw, void *sink_v, int64_t sink_gstride, int64_t sink_rstride, void *stream);
 
 /* Rotate rows: dst[o, i, :] = R(src[o, i, :]) with angle row table + i*table_rstride, for o < n_outer,
  * i < n_rows (rows contiguous, D elements each; src may equal dst).  Replaces the chunk-boundary

@@ -34,6 +34,7 @@ _SIGS = {
     "vgx_qweight_scale_offset": (I64, [I32, I64, I64]),
     "vgx_qweight_pack": (I32, [I32, P, P, I64, I64, P]),
     "vgx_qweight_pack_gateup": (I32, [I32, P, P, P, I64, I64, P]),
+    "vgx_qweight_pack_rope": (I32, [I32, P, P, I64, I64, I64, I64, P]),
     "vgx_qweight_unpack": (I32, [I32, P, P, I64, I64, P]),
     "vgx_qweight_dequant": (I32, [I32, P, P, I64, I64, P]),
     "vgx_embed_rows": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
@@ -55,6 +56,8 @@ _SIGS = {
     "vgx_seg_score_tail": (I32, [P, I64, P, P, I64, I64, I32, P, P, P]),
     "vgx_rope_qkv_write_step": (I32, [I32, P, I64, P, I64, P, I64, I64, I64, I64, I64, P, I64, P, P, P, P, I64, I64,
                                       I64, P, P, I64, I64, I64, P]),
+    "vgx_qkv_rope_step": (I32, [I32, P, P, I32, P, P, I64, I64, I64, I64, P, P, F, P, P, I64, P, P, I32, P, P, P, I64,
+                                I64, P, P, I64, I64, P]),
 }
 
 

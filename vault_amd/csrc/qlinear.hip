@@ -34,10 +34,12 @@ int64_t packed_bytes(int dt, int64_t rows, int64_t cols) {
 
 // One thread per (packed row p, block b).  mode 0: packed row p <- source row p of `a`.
 // mode 1 (gate/up): packed row-quad q holds a[2q], a[2q+1], b[2q], b[2q+1].
+// mode 2 (RoPE pairs): for p < n_rope, inside each head of hd rows, row-quad j holds rows
+// 2j, 2j + hd/2, 2j + 1, 2j + 1 + hd/2 (the rotation pairs 2j and 2j + 1); rows >= n_rope stay.
 template <int DT>
 __global__ void pack_kernel(const uint8_t *__restrict__ a, const uint8_t *__restrict__ bsrc,
                             uint8_t *__restrict__ dst, int64_t src_rows, int64_t nblk, int64_t soff,
-                            int64_t total, int mode) {
+                            int64_t total, int mode, int hd, int64_t n_rope) {
     constexpr int QB = quant_bytes(DT);
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
@@ -48,6 +50,9 @@ __global__ void pack_kernel(const uint8_t *__restrict__ a, const uint8_t *__rest
     if (mode == 1) {
         r = 2 * rq + (rr & 1);
         src = rr < 2 ? a : bsrc;
+    } else if (mode == 2 && p < n_rope) {
+        const int64_t h = p / hd, w = p - h * hd, j = w >> 2, k = w & 3;
+        r = h * hd + 2 * j + (k >> 1) + (k & 1) * (hd / 2);
     }
     uint8_t *qd = dst + ((rq * nblk + b) * 4 + rr) * QB;
     const bool live = r < src_rows;
@@ -151,7 +156,7 @@ int64_t vgx_qweight_scale_offset(int dtype, int64_t rows, int64_t cols) {
 }
 
 static int pack_common(int dtype, const void *a, const void *b, void *dst, int64_t rows, int64_t cols, int mode,
-                       void *stream) {
+                       void *stream, int hd = 0, int64_t n_rope = 0) {
     if (!dtype_ok(dtype)) return VGX_E_DTYPE;
     if (!a || !dst || (mode == 1 && !b)) return VGX_E_ARG;
     if (rows <= 0 || cols <= 0) return VGX_E_SIZE;
@@ -166,9 +171,9 @@ static int pack_common(int dtype, const void *a, const void *b, void *dst, int64
     const auto *pb = static_cast<const uint8_t *>(b);
     auto *pd = static_cast<uint8_t *>(dst);
     switch (dtype) {
-        case VGX_Q8_0: hipLaunchKernelGGL(pack_kernel<VGX_Q8_0>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode); break;
-        case VGX_Q4_0: hipLaunchKernelGGL(pack_kernel<VGX_Q4_0>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode); break;
-        case VGX_F32: hipLaunchKernelGGL(pack_kernel<VGX_F32>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode); break;
+        case VGX_Q8_0: hipLaunchKernelGGL(pack_kernel<VGX_Q8_0>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode, hd, n_rope); break;
+        case VGX_Q4_0: hipLaunchKernelGGL(pack_kernel<VGX_Q4_0>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode, hd, n_rope); break;
+        case VGX_F32: hipLaunchKernelGGL(pack_kernel<VGX_F32>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode, hd, n_rope); break;
     }
     VGX_CHECK_LAUNCH();
     return VGX_OK;
@@ -181,6 +186,14 @@ int vgx_qweight_pack(int dtype, const void *src_blocks, void *dst_packed, int64_
 int vgx_qweight_pack_gateup(int dtype, const void *gate_blocks, const void *up_blocks, void *dst_packed,
                             int64_t rows, int64_t cols, void *stream) {
     return pack_common(dtype, gate_blocks, up_blocks, dst_packed, rows, cols, 1, stream);
+}
+
+int vgx_qweight_pack_rope(int dtype, const void *src_blocks, void *dst_packed, int64_t rows, int64_t cols,
+                          int64_t head_dim, int64_t n_rope_rows, void *stream) {
+    if (head_dim <= 0 || head_dim % 4 || n_rope_rows < 0 || n_rope_rows > rows || n_rope_rows % head_dim)
+        return VGX_E_SHAPE;
+    if (head_dim > 0x7FFFFFFF) return VGX_E_LIMIT;
+    return pack_common(dtype, src_blocks, nullptr, dst_packed, rows, cols, 2, stream, (int)head_dim, n_rope_rows);
 }
 
 int vgx_qweight_unpack(int dtype, const void *packed, void *dst_blocks, int64_t rows, int64_t cols, void *stream) {

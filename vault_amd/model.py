@@ -490,13 +490,26 @@ class VAULTv3ForCausalLM:
         hbuf = torch.empty(B, cfg.d_ff, dtype=torch.float32, device=self.device)
         table = self._rows(self._p0)
         scale = 1.0 / math.sqrt(D)
+        fused = B == 1 and all(lw.wq_rope is not None for lw in w.layers)
+        qbuf = torch.empty(B, H, D, dtype=torch.float32, device=self.device) if fused else None
         for li, lw in enumerate(w.layers):
+            xc = None
             if seg_active and li in cfg.seg_layers:
                 j = cfg.seg_layers.index(li)
-                feats[:, j * d:(j + 1) * d].copy_(x)
-            q, k, v = self._qkv(lw, x, B)
-            ops.rope_qkv_write_step(q, k, v, table, D, step, st.k_cur[li], st.kraw_cur[li], st.v_cur[li],
-                                    st.k_sink_raw[li], st.v_sink[li])
+                xc = feats[:, j * d:(j + 1) * d]
+                if not fused:
+                    xc.copy_(x)
+            if fused:
+                # one launch: norm + q/k/v + bias + RoPE + ring / sink writes (+ the scorer feature copy)
+                bkv = lw.bqkv[HD:] if lw.wq is None else lw.bqkv
+                ops.qkv_rope_step(lw.wq_rope, lw.bq, lw.wkv_rope, bkv, x, (lw.ln1, cfg.rms_eps), table, D, step,
+                                  qbuf, st.k_cur[li], st.kraw_cur[li], st.v_cur[li], st.k_sink_raw[li],
+                                  st.v_sink[li], x_copy=xc)
+                q = qbuf
+            else:
+                q, k, v = self._qkv(lw, x, B)
+                ops.rope_qkv_write_step(q, k, v, table, D, step, st.k_cur[li], st.kraw_cur[li], st.v_cur[li],
+                                        st.k_sink_raw[li], st.v_sink[li])
             spans = []
             if n_sk:
                 spans.append((st.k_sink_rot[li][:, :, :n_sk], st.v_sink[li][:, :, :n_sk]))

@@ -78,6 +78,19 @@ class QWeight:
                                             _stream(dst.device)), "vgx_qweight_pack_gateup")
         return cls(dtype, rows, cols, dst, gateup=True)
 
+    @classmethod
+    def rope_from_blocks(cls, dtype: int, rows: int, cols: int, data, head_dim: int, n_rope_rows: int,
+                         device) -> "QWeight":
+        """Packed with the RoPE-pair row order of vgx_qweight_pack_rope (for qkv_rope_step)."""
+        lib = L.load()
+        src = cls._upload(data, device)
+        n = lib.vgx_qweight_packed_bytes(dtype, rows, cols)
+        L.check(0 if n > 0 else int(n), "vgx_qweight_packed_bytes")
+        dst = torch.empty(int(n), dtype=torch.uint8, device=device)
+        L.check(lib.vgx_qweight_pack_rope(dtype, src.data_ptr(), dst.data_ptr(), rows, cols, head_dim, n_rope_rows,
+                                          _stream(dst.device)), "vgx_qweight_pack_rope")
+        return cls(dtype, rows, cols, dst)
+
     def unpack(self) -> torch.Tensor:
         """Packed -> AoS blocks (uint8 device tensor)."""
         if self.gateup:
@@ -357,6 +370,34 @@ def rope_qkv_write_step(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table
         table.data_ptr(), table_rstride, step.data_ptr(), _ptr(k_rot), _ptr(k_raw), v_dst.data_ptr(),
         v_dst.stride(0), v_dst.stride(1), v_dst.stride(2), _ptr(sink_k), _ptr(sink_v), sk_b, sk_g, sk_r,
         _stream(k.device)), "vgx_rope_qkv_write_step")
+
+
+def qkv_rope_step(wq: QWeight, bq: Optional[torch.Tensor], wkv: QWeight, bkv: Optional[torch.Tensor],
+                  x: torch.Tensor, norm: Optional[Tuple[torch.Tensor, float]], table: torch.Tensor,
+                  table_rstride: int, step: torch.Tensor, q_out: torch.Tensor, k_rot: torch.Tensor,
+                  k_raw: torch.Tensor, v_dst: torch.Tensor, sink_k: Optional[torch.Tensor],
+                  sink_v: Optional[torch.Tensor], x_copy: Optional[torch.Tensor] = None) -> None:
+    """One decode token: RMSNorm + q/k/v projections (RoPE-pair packed weights) + bias, RoPE, ring and
+    sink writes in one launch.  x [1, d] fp32; q_out [1, H, D] fp32; k_rot / k_raw / v_dst ring
+    tensors [1, G, W, D] and sink_k / sink_v [1, G, S_cap, D] of the state dtype; the slot, table row
+    and sink slot come from ``step``."""
+    G, D = k_rot.shape[1], k_rot.shape[3]
+    H = q_out.shape[1]
+    if x.shape[0] != 1 or not x.is_contiguous() or not q_out.is_contiguous():
+        raise ValueError("qkv_rope_step takes one contiguous token")
+    for t in (k_rot, k_raw, v_dst, sink_k, sink_v):
+        if t is not None and t.stride(2) != D:
+            raise ValueError("ring rows must be contiguous")
+    if x_copy is not None and not x_copy.is_contiguous():
+        raise ValueError("x_copy must be contiguous")
+    nw, eps = (norm[0], float(norm[1])) if norm is not None else (None, 0.0)
+    sk_g, sk_r = (sink_k.stride(1), sink_k.stride(2)) if sink_k is not None else (0, 0)
+    L.check(L.load().vgx_qkv_rope_step(
+        wq.dtype, wq.packed.data_ptr(), _ptr(bq), wkv.dtype, wkv.packed.data_ptr(), _ptr(bkv), x.shape[1], H, G, D,
+        x.data_ptr(), _ptr(nw), eps, _ptr(x_copy), table.data_ptr(), table_rstride, step.data_ptr(),
+        q_out.data_ptr(), KV_DTYPES[v_dst.dtype], k_rot.data_ptr(), k_raw.data_ptr(), v_dst.data_ptr(),
+        v_dst.stride(1), v_dst.stride(2), _ptr(sink_k), _ptr(sink_v), sk_g, sk_r, _stream(x.device)),
+        "vgx_qkv_rope_step")
 
 
 def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:

@@ -29,6 +29,8 @@ class LayerWeights:
     wo: ops.QWeight
     wgu: ops.QWeight
     wd: ops.QWeight
+    wq_rope: Optional[ops.QWeight] = None    # q rows in RoPE-pair order (one-token decode kernel)
+    wkv_rope: Optional[ops.QWeight] = None   # k rows in RoPE-pair order, then v rows
 
 
 @dataclass
@@ -86,6 +88,8 @@ class ModelWeights:
                 wq = ops.QWeight.from_blocks(q.dtype, H * D, d, q.data, dev)
                 wqkv = ops.QWeight.from_blocks(k.dtype, 2 * G * D, d, k.data + v.data, dev)
                 bqkv = torch.cat([bk, bv])
+            wq_rope = ops.QWeight.rope_from_blocks(q.dtype, H * D, d, q.data, D, H * D, dev)
+            wkv_rope = ops.QWeight.rope_from_blocks(k.dtype, 2 * G * D, d, k.data + v.data, D, G * D, dev)
             o = t["self_attn.o_proj.weight"]
             g, u, dn = t["mlp.gate_proj.weight"], t["mlp.up_proj.weight"], t["mlp.down_proj.weight"]
             if _block_dtype(g) != _block_dtype(u):
@@ -96,6 +100,7 @@ class ModelWeights:
                 wo=ops.QWeight.from_blocks(_block_dtype(o), d, H * D, o.data, dev),
                 wgu=ops.QWeight.gateup_from_blocks(g.dtype, F, d, g.data, u.data, dev),
                 wd=ops.QWeight.from_blocks(_block_dtype(dn), d, F, dn.data, dev),
+                wq_rope=wq_rope, wkv_rope=wkv_rope,
             ))
         if cfg.has_seg_scorer and "seg_scorer.ln.weight" in tensors:
             fd = len(cfg.seg_layers) * d
