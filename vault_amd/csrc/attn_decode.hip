@@ -238,22 +238,23 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
     }
 }
 
-// One workgroup per (b, h): out = sum_s e^{m_s - M} acc_s / sum_s e^{m_s - M} l_s.  The split
-// weights are computed once into LDS; the D x 2 threads then each sum one dimension over half of
-// the splits with up to 16 loads in flight, and the halves are added through LDS.
-constexpr int kMergeThreads = 256;
-
-__global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *__restrict__ part,
-                                                                   float *__restrict__ out, int H, int G, int D,
-                                                                   int n_splits) {
+// One workgroup of D threads per (b, h): out = sum_s e^{m_s - M} acc_s / sum_s e^{m_s - M} l_s.
+// Every load is issued before the one barrier: thread d requests acc_s[d] of all n_splits splits, and
+// the first wave also (m_s, l_s) of split s = lane; that wave turns them into the split weights in
+// LDS.  One round trip to the partials instead of one per dependent step.
+__global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict__ part, float *__restrict__ out,
+                                                         int H, int G, int D, int n_splits) {
     __shared__ float wgt[kMaxSplits];
-    __shared__ float half_sum[kMergeThreads];
     __shared__ float inv_l;
     const int bh = blockIdx.x;
     const int b = bh / H, h = bh - b * H;
     const int grp = H / G, g = h / grp, hh = h - g * grp;
     const int64_t stride = (int64_t)grp * (D + 2);
     const float *p0 = part + (((int64_t)b * G + g) * n_splits * grp + hh) * (D + 2);
+    const int d = threadIdx.x;
+    float v[kMaxSplits];
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; ++s) v[s] = s < n_splits ? p0[s * stride + d] : 0.0f;
     if (threadIdx.x < 64) {
         const int s = threadIdx.x;
         const float ms = s < n_splits ? p0[s * stride + D] : kNegBig;
@@ -261,28 +262,15 @@ __global__ __launch_bounds__(kMergeThreads) void attn_merge_kernel(const float *
         const float M = wave_max(ms);
         const float w = s < n_splits ? __expf(ms - M) : 0.0f;
         const float L = wave_sum(w * ls);
-        if (s < n_splits) wgt[s] = w;
+        wgt[s] = w;
         if (s == 0) inv_l = 1.0f / L;
     }
     __syncthreads();
-    const int parts = kMergeThreads / D;               // 2 for D = 128, 4 for D = 64
-    const int d = threadIdx.x % D, pi = threadIdx.x / D;
-    const int s0 = pi * n_splits / parts, s1 = (pi + 1) * n_splits / parts;
     float a = 0.0f;
-    for (int s = s0; s < s1; s += 16) {
-        float v[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = s + u < s1 ? p0[(s + u) * stride + d] : 0.0f;
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-            if (s + u < s1) a = fmaf(wgt[s + u], v[u], a);
-    }
-    half_sum[threadIdx.x] = a;
-    __syncthreads();
-    if (pi == 0) {
-        for (int p = 1; p < parts; ++p) a += half_sum[p * D + d];
-        out[((int64_t)b * H + h) * D + d] = a * inv_l;
-    }
+    for (int s = 0; s < kMaxSplits; ++s)
+        if (s < n_splits) a = fmaf(wgt[s], v[s], a);
+    out[((int64_t)b * H + h) * D + d] = a * inv_l;
 }
 
 int choose_splits(int64_t B, int64_t G, int64_t n_tot, int64_t *kps) {
@@ -395,7 +383,7 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
     if (!ok) return VGX_E_LIMIT;
     VGX_CHECK_LAUNCH();
     if (ns > 1) {
-        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * H)), dim3(kMergeThreads), 0, st, part, out, (int)H,
+        hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * H)), dim3((unsigned)D), 0, st, part, out, (int)H,
                            (int)G, (int)D, ns);
         VGX_CHECK_LAUNCH();
     }

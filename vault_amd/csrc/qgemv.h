@@ -183,8 +183,13 @@ __device__ __forceinline__ void gemv_block(const BlockRegs<DT> &br, const float 
     }
 }
 
-template <int DT, int NB, int EPI, int MODE, int KW, bool NORM>
+// XD (direct activations, split-K mode with one wave and one batch row only): no LDS staging; each
+// lane reads the 32 activations (and RMSNorm weights) of its block from global memory, where every
+// other wave reads the same bytes (L1 / L2 hits).  Saves the staging round trip and barrier of the
+// small projections (measured 4.0 vs 4.4 us for 1536 x 1536 Q4_0).
+template <int DT, int NB, int EPI, int MODE, int KW, bool NORM, bool XD = false>
 __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_kernel(GemvArgs a, int cbk) {
+    static_assert(!XD || (MODE == MODE_SPLITK && KW == 1 && NB == 1), "direct activations: one wave, one row");
     extern __shared__ float smem[];
     constexpr int LPR = MODE == MODE_ROWS ? 16 : 64;     // lanes per row-quad
     constexpr int RQW = 64 / LPR;                          // row-quads per wave
@@ -220,9 +225,9 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
     // Each lane issues the loads of U blocks at once (all of its blocks for the model's shapes), the
     // first batch before the activations are staged, so a lane has up to U x 64 B (Q4_0) /
     // U x 128 B (Q8_0) of weights in flight.
-    // Row mode with 3-4 K-split waves gives a lane one block per 48-64 blocks of the row and has at
-    // most 168 / 128 VGPRs (12 / 16 waves per workgroup): one block per batch there.
-    constexpr int U = (MODE == MODE_ROWS && KW >= 3) ? 1 : DT == VGX_Q4_0 ? 4 : DT == VGX_Q8_0 ? 3 : 1;
+    // With 3 or more K-split waves a lane has at most one or two blocks of the model's rows (8 waves
+    // over the 280-block down projection): one block per batch, fewer registers.
+    constexpr int U = (KW >= 3) ? 1 : DT == VGX_Q4_0 ? 4 : DT == VGX_Q8_0 ? 3 : 1;
     BlockRegs<DT> br[U];
     int cb = min(cbk, nblk);
 #pragma unroll
@@ -233,13 +238,18 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
         cb = min(cbk, nblk - c0);
         if (c0) __syncthreads();
         const bool vec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0) && (a.ldx % 4 == 0);
-        if (vec) {
-            // 4 float4 loads per thread in flight per round
+        if constexpr (XD) {
+            // no staging
+        } else if (vec) {
+            // kStageLoads float4 loads per thread in flight: one round trip for the model's shapes
+            // (1536 activations over 256 threads; 8960 over the 512 threads of the 8-wave split-K)
+            // without holding more staging registers than that needs.
+            constexpr int kStageLoads = KW >= 4 ? 6 : 4;
             const int n4 = NB * cb * 8;
-            for (int i0 = tid; i0 < n4; i0 += 4 * NT) {
-                float4 v[4], gw[4];
+            for (int i0 = tid; i0 < n4; i0 += kStageLoads * NT) {
+                float4 v[kStageLoads], gw[kStageLoads];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int u = 0; u < kStageLoads; ++u) {
                     const int i = i0 + u * NT;
                     if (i < n4) {
                         const int n = i / (cb * 8), rem = i - n * cb * 8;
@@ -249,7 +259,7 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
                     }
                 }
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
+                for (int u = 0; u < kStageLoads; ++u) {
                     const int i = i0 + u * NT;
                     if (i < n4) {
                         const int n = i / (cb * 8), rem = i - n * cb * 8, blk = rem >> 3, j4 = rem & 7;
@@ -279,7 +289,7 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
                 xs[(n * cbk + blk) * kGemvPad + j] = v;
             }
         }
-        __syncthreads();
+        if constexpr (!XD) __syncthreads();
         if (act) {
             for (int b = first; b < cb; b += U * stride) {
                 if (b != first) {
@@ -290,7 +300,31 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int bb = b + u * stride;
-                    if (bb < cb) gemv_block<DT, NB>(br[u], xs + bb * kGemvPad, cbk * kGemvPad, acc);
+                    if (bb >= cb) continue;
+                    if constexpr (XD) {
+                        const int64_t c = (int64_t)(c0 + bb) * QK;
+                        const float4 *xp = reinterpret_cast<const float4 *>(a.x + c);
+                        float4 xv[8], gv[8];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) xv[j] = xp[j];
+                        if constexpr (NORM) {
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) gv[j] = reinterpret_cast<const float4 *>(a.lnw + c)[j];
+                        }
+                        float xb[QK];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            float4 t = xv[j];
+                            if constexpr (NORM) {
+                                ssq[0] += fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, t.w * t.w)));
+                                t.x *= gv[j].x; t.y *= gv[j].y; t.z *= gv[j].z; t.w *= gv[j].w;
+                            }
+                            xb[4 * j] = t.x; xb[4 * j + 1] = t.y; xb[4 * j + 2] = t.z; xb[4 * j + 3] = t.w;
+                        }
+                        gemv_block<DT, NB>(br[u], xb, 0, acc);
+                    } else {
+                        gemv_block<DT, NB>(br[u], xs + bb * kGemvPad, cbk * kGemvPad, acc);
+                    }
                 }
             }
             // first batch of the next chunk
@@ -377,22 +411,26 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
 //    requesting all of its (typically 3) blocks at once.  Splitting K across 3 waves here measured
 //    slower on MI355X (gate/up 10.8 vs 10.2 us, LM head 68.7 vs 51.3 us): the extra LDS reduction
 //    costs more than the shorter per-lane chain saves;
-//  * split-K mode: one row-quad per workgroup, KW in {1, 2, 4} waves over its blocks.
+//  * split-K mode: one row-quad per workgroup, KW in {1, 2, 8} waves over its blocks (8 for the
+//    280-block down projection: 7.1 vs 7.5 us with 4); with one wave and one batch row the
+//    activations are read directly (XD) instead of being staged.
 template <int DT>
 int qgemv_launch(GemvArgs a, hipStream_t st) {
     const bool rows_mode = a.n_rq >= 2048;
     int kw = 1;
     if (a.batch == 1) {  // K-split variants are instantiated for batch 1 (the decode step) only
-        if (!rows_mode) kw = a.nblk >= 192 ? 4 : a.nblk >= 96 ? 2 : 1;
+        if (!rows_mode) kw = a.nblk >= 192 ? 8 : a.nblk >= 96 ? 2 : 1;
     }
     const bool norm = a.lnw != nullptr;
+    const bool xd = a.batch == 1 && !rows_mode && kw == 1 && ((uintptr_t)a.x & 15) == 0 &&
+                    ((uintptr_t)a.lnw & 15) == 0 && DT != VGX_F32;
     for (int64_t b0 = 0; b0 < a.batch; b0 += 4) {
         GemvArgs p = a;
         const int nb = (int)std::min<int64_t>(4, a.batch - b0);
         p.x = a.x + b0 * a.ldx;
         p.y = a.y + b0 * a.ldy;
-        const int cbk = std::min(a.nblk, kGemvMaxChunkFloats / (QK * nb));
-        const size_t lds = (size_t)nb * cbk * kGemvPad * sizeof(float);
+        const int cbk = xd ? a.nblk : std::min(a.nblk, kGemvMaxChunkFloats / (QK * nb));
+        const size_t lds = xd ? 0 : (size_t)nb * cbk * kGemvPad * sizeof(float);
         const unsigned grid = rows_mode ? (unsigned)((a.n_rq + 15) / 16) : (unsigned)a.n_rq;
         const unsigned threads = (rows_mode ? 256u : 64u) * (unsigned)kw;
 #define VGX_GEMV_GO(NBV, EPIV, MODEV, KWV, NORMV)                                                      \
@@ -400,8 +438,11 @@ int qgemv_launch(GemvArgs a, hipStream_t st) {
 #define VGX_GEMV_KW(NBV, EPIV, NORMV)                                                                  \
     do {                                                                                               \
         if (rows_mode) VGX_GEMV_GO(NBV, EPIV, MODE_ROWS, 1, NORMV);                                    \
-        else if (kw == 4) VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 4, NORMV);                             \
+        else if (kw == 8) VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 8, NORMV);                               \
         else if (kw == 2) VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 2, NORMV);                               \
+        else if (xd && DT != VGX_F32)                                                                  \
+            hipLaunchKernelGGL((qgemv_kernel<DT, NBV, EPIV, MODE_SPLITK, 1, NORMV, DT != VGX_F32 && NBV == 1>), \
+                               dim3(grid), dim3(threads), lds, st, p, cbk);                            \
         else VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 1, NORMV);                                            \
     } while (0)
 #define VGX_GEMV_K1(NBV, EPIV, NORMV)                                                                  \
