@@ -277,7 +277,7 @@ def pmc_report(fetch_csv: str, write_csv: str) -> None:
     """Markdown summary of the two PMC runs: per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the
     dominant kernel and of the calibration copy, the copy's bytes / counter factor, and the scaled
     HBM traffic per launch of the dominant kernel (the figure ``roofline.traffic`` reports)."""
-    kern, copy = "qgemv_kernel<9, 1, 2, 0, 1, true>", "neg_kernel"
+    kern, copy = "qgemv_kernel<9, 1, 2, 0, 1, true", "neg_kernel"
     fk, nk = _pmc_avg(fetch_csv, "FETCH_SIZE", kern)
     fc, nc = _pmc_avg(fetch_csv, "FETCH_SIZE", copy)
     wk, _ = _pmc_avg(write_csv, "WRITE_SIZE", kern)
@@ -286,7 +286,7 @@ def pmc_report(fetch_csv: str, write_csv: str) -> None:
     traffic = fk * 1024 * f_scale + wk * 1024 * w_scale
     algo = 15_524_864
     print(f"| dispatches | kernel | FETCH_SIZE KiB | WRITE_SIZE KiB |\n|---|---|---|---|\n"
-          f"| {nk} | `{kern}` (gate/up SwiGLU Q4_0 GEMV) | {fk:.1f} | {wk:.1f} |\n"
+          f"| {nk} | `{kern}...>` (gate/up SwiGLU Q4_0 GEMV) | {fk:.1f} | {wk:.1f} |\n"
           f"| {nc} | torch `neg` elementwise kernel ({COPY_BYTES} B read + written) | {fc:.1f} | {wc:.1f} |\n\n"
           f"copy calibration: fetch factor {f_scale:.4f}, write factor {w_scale:.4f} (bytes / (KiB x 1024))\n\n"
           f"algorithmic bytes per launch: {algo}\n\n"
@@ -314,6 +314,8 @@ def main() -> int:
     ap.add_argument("--kv", choices=("fp32", "bf16"), default="fp32")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernels", action="store_true", help="skip the secondary kernel figures")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the timed decode steps (for per-kernel profiles of the step)")
     ap.add_argument("--pmc", action="store_true",
                     help="only run the launches the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count")
     ap.add_argument("--pmc-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -346,6 +348,10 @@ def main() -> int:
     ms = dt * 1e3 / args.steps
     _log(f"decode: {tok_s:.1f} tokens/s ({ms:.3f} ms/step)")
 
+    if args.decode_only:
+        print(json.dumps({"metric": "decode tokens/s (decode-only profile run)", "value": round(tok_s, 2),
+                          "unit": "tokens/s", "ms_per_step": round(ms, 4), "steps": args.steps}), flush=True)
+        return 0
     dom = dominant_kernel(model)
     _log(f"dominant kernel: {dom['avg_us']:.2f} us, {dom['gbs']:.0f} GB/s")
     kernels = {}

@@ -37,43 +37,59 @@ struct SpanArgs {
     int n;
 };
 
+// One lane's DPL elements of a key row as raw words (F32: DPL words, BF16: DPL / 2 words), loaded
+// with 128-bit (or 64-bit) loads and converted to fp32 at use.
 template <int KV, int DPL>
-__device__ __forceinline__ void load_chunk(const void *base, int64_t elem_off, float (&out)[DPL]) {
-    if constexpr (KV == VGX_F32) {
-        const float *p = static_cast<const float *>(base) + elem_off;
-        if constexpr (DPL % 4 == 0) {
+struct RowRaw {
+    static constexpr int W = KV == VGX_F32 ? DPL : DPL / 2;
+    uint32_t w[W];
+};
+
+template <int KV, int DPL>
+__device__ __forceinline__ void load_raw(const void *base, int64_t elem_off, RowRaw<KV, DPL> &r) {
+    constexpr int W = RowRaw<KV, DPL>::W;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(static_cast<const char *>(base) +
+                                                           elem_off * (KV == VGX_F32 ? 4 : 2));
+    if constexpr (W % 4 == 0) {
 #pragma unroll
-            for (int i = 0; i < DPL / 4; ++i) {
-                const float4 t = reinterpret_cast<const float4 *>(p)[i];
-                out[4 * i] = t.x; out[4 * i + 1] = t.y; out[4 * i + 2] = t.z; out[4 * i + 3] = t.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) out[i] = p[i];
+        for (int i = 0; i < W / 4; ++i) {
+            const uint4 t = reinterpret_cast<const uint4 *>(p)[i];
+            r.w[4 * i] = t.x; r.w[4 * i + 1] = t.y; r.w[4 * i + 2] = t.z; r.w[4 * i + 3] = t.w;
         }
+    } else if constexpr (W == 2) {
+        const uint2 t = *reinterpret_cast<const uint2 *>(p);
+        r.w[0] = t.x; r.w[1] = t.y;
     } else {
-        const uint16_t *p = static_cast<const uint16_t *>(base) + elem_off;
-        if constexpr (DPL == 8) {
-            const uint4 t = *reinterpret_cast<const uint4 *>(p);
-            const uint32_t w[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                out[2 * i] = __uint_as_float(w[i] << 16);
-                out[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-            }
-        } else if constexpr (DPL == 4) {
-            const uint2 t = *reinterpret_cast<const uint2 *>(p);
-            out[0] = __uint_as_float(t.x << 16); out[1] = __uint_as_float(t.x & 0xFFFF0000u);
-            out[2] = __uint_as_float(t.y << 16); out[3] = __uint_as_float(t.y & 0xFFFF0000u);
-        } else {
-#pragma unroll
-            for (int i = 0; i < DPL; ++i) out[i] = __uint_as_float((uint32_t)p[i] << 16);
-        }
+        for (int i = 0; i < W; ++i) r.w[i] = p[i];
     }
 }
 
-// Workspace layout: partials per (b, g, split, head): D accumulators, then m, l.
+template <int KV, int DPL>
+__device__ __forceinline__ float raw_at(const RowRaw<KV, DPL> &r, int d) {
+    if constexpr (KV == VGX_F32) return __uint_as_float(r.w[d]);
+    else return (d & 1) ? __uint_as_float(r.w[d >> 1] & 0xFFFF0000u) : __uint_as_float(r.w[d >> 1] << 16);
+}
 
+// The kKB keys of one DPP row of a 16-key tile.
+template <int KV, int DPL>
+struct KeyTile {
+    RowRaw<KV, DPL> k[kKB], v[kKB];
+};
+
+template <typename T>
+__device__ __forceinline__ T pick4(int s, T a0, T a1, T a2, T a3) {
+    return s == 0 ? a0 : s == 1 ? a1 : s == 2 ? a2 : a3;
+}
+
+// Workspace layout: partials per (b, g, split, head): D accumulators, then m, l.
+//
+// Split z covers global keys [z kps, (z + 1) kps) of the concatenated spans (by capacity).  Inside
+// each span the split's keys are dealt to the waves in 16-key tiles (wave w: tiles lo + 16 w + 64 i).
+// Tile addresses depend only on the span capacities (host values), so the first tile's K/V loads are
+// issued before the query and the device-side lengths arrive; keys at or beyond a span's effective
+// length (device length, causal limit) are masked, and no row beyond a span's capacity is read.
+// With PIPE the next tile's loads are issued before the current tile is reduced.
 template <int KV, int GRP, int DPL>
 __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
     const float *__restrict__ q, int64_t ldq, SpanArgs sp, const float *__restrict__ bias, int64_t bias_hstride,
@@ -81,18 +97,81 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
     float scale, int64_t n_tot, int64_t kps, int n_splits, int64_t causal_base) {
     constexpr int D = DPL * 16;
     constexpr int SLOT = D + 2;
+    constexpr bool PIPE = KV == VGX_BF16;
     __shared__ float red[kWaves][GRP][SLOT];
 
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, row = lane >> 4;
+    const int lane = threadIdx.x & 63, l16 = lane & 15, row = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
+    // per-span key ranges of this split, local to the span: [lo, hi) by capacity (uniform)
+    const int64_t k0 = (int64_t)split * kps;
+    const int64_t k1 = min(n_tot, k0 + kps);
+    int lo[4], hi[4], eff[4];
+    {
+        int64_t base = 0;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int64_t len = s < sp.n ? sp.len[s] : 0;
+            lo[s] = (int)(max(k0, base) - base);
+            hi[s] = (int)(max(min(k1, base + len) - base, (int64_t)lo[s]));
+            base += len;
+        }
+    }
+    // the wave's first tile: span s, local start t (s = 4: none)
+    auto first_in = [&](int s0) -> int2 {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            if (s >= s0 && lo[s] + wave * 16 < hi[s]) return make_int2(s, lo[s] + wave * 16);
+        return make_int2(4, 0);
+    };
+    auto next = [&](int2 c) -> int2 {
+        if (c.y + kWaves * 16 < pick4(c.x, hi[0], hi[1], hi[2], hi[3])) return make_int2(c.x, c.y + kWaves * 16);
+        return first_in(c.x + 1);
+    };
+    auto fetch = [&](KeyTile<KV, DPL> &t, int2 c) {
+        const int s = c.x;
+        const void *kb = pick4(s, sp.k[0], sp.k[1], sp.k[2], sp.k[3]);
+        const void *vb = pick4(s, sp.v[0], sp.v[1], sp.v[2], sp.v[3]);
+        const int64_t o = (int64_t)b * pick4(s, sp.bstride[0], sp.bstride[1], sp.bstride[2], sp.bstride[3]) +
+                          (int64_t)g * pick4(s, sp.gstride[0], sp.gstride[1], sp.gstride[2], sp.gstride[3]) +
+                          (int64_t)(c.y + row * kKB) * D + l16 * DPL;
+        // rows past the split's end in this span re-read its last row (in bounds; masked at use)
+        const int last = pick4(s, hi[0], hi[1], hi[2], hi[3]) - 1 - c.y - row * kKB;
+#pragma unroll
+        for (int j = 0; j < kKB; ++j) {
+            const int64_t oj = o + (int64_t)min(j, last) * D;
+            load_raw<KV, DPL>(kb, oj, t.k[j]);
+            load_raw<KV, DPL>(vb, oj, t.v[j]);
+        }
+    };
+
+    // q of the GRP heads, then the first tile, then the device-side lengths
     float qr[GRP][DPL];
 #pragma unroll
     for (int hh = 0; hh < GRP; ++hh) {
         const float *qp = q + (int64_t)b * ldq + ((int64_t)g * GRP + hh) * D + l16 * DPL;
 #pragma unroll
-        for (int d = 0; d < DPL; ++d) qr[hh][d] = qp[d] * scale;
+        for (int d4 = 0; d4 < DPL / 4; ++d4) {
+            const float4 t = reinterpret_cast<const float4 *>(qp)[d4];
+            qr[hh][4 * d4] = t.x; qr[hh][4 * d4 + 1] = t.y; qr[hh][4 * d4 + 2] = t.z; qr[hh][4 * d4 + 3] = t.w;
+        }
     }
+    KeyTile<KV, DPL> tA, tB;
+    int2 cur = first_in(0);
+    if (cur.x < 4) fetch(tA, cur);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        int64_t e = s < sp.n ? sp.len[s] : 0;
+        if (s < sp.n && sp.dyn_len[s] != nullptr) e = min(e, (int64_t)*sp.dyn_len[s]);
+        if (causal_base >= 0 && s == sp.n - 1) e = min(e, causal_base + (int64_t)b + 1);
+        eff[s] = (int)min((int64_t)hi[s], max(e, (int64_t)0));
+    }
+#pragma unroll
+    for (int hh = 0; hh < GRP; ++hh)
+#pragma unroll
+        for (int d = 0; d < DPL; ++d) qr[hh][d] *= scale;
+
     float m[GRP], l[GRP], acc[GRP][DPL];
 #pragma unroll
     for (int hh = 0; hh < GRP; ++hh) {
@@ -102,81 +181,92 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
         for (int d = 0; d < DPL; ++d) acc[hh][d] = 0.0f;
     }
 
-    const int64_t k0 = (int64_t)split * kps;
-    const int64_t k1 = min(n_tot, k0 + kps);
-    int64_t base = 0;
-    for (int s = 0; s < sp.n; ++s) {
-        const int64_t len = sp.len[s];
-        const int64_t lo = max(k0, base) - base;
-        int64_t hi = min(k1, base + len) - base;
-        if (sp.dyn_len[s] != nullptr) hi = min(hi, (int64_t)*sp.dyn_len[s]);  // device-side length
-        // Causal last span: batch entry b sees its first causal_base + b + 1 keys.
-        if (causal_base >= 0 && s == sp.n - 1) hi = min(hi, causal_base + (int64_t)b + 1);
-        base += len;
-        if (lo >= hi) continue;
-        const int64_t off = (int64_t)b * sp.bstride[s] + (int64_t)g * sp.gstride[s] + l16 * DPL;
-        const void *kb = sp.k[s];
-        const void *vb = sp.v[s];
+    auto compute = [&](const KeyTile<KV, DPL> &t, int2 c) {
+        const int s = c.x;
+        const int e = pick4(s, eff[0], eff[1], eff[2], eff[3]);
         const float *bb = (bias != nullptr && s == bias_span) ? bias + (int64_t)g * GRP * bias_hstride : nullptr;
-        for (int64_t t0 = lo + wave * 4 * kKB; t0 < hi; t0 += kWaves * 4 * kKB) {
-            float kf[kKB][DPL], vf[kKB][DPL];
-            bool valid[kKB];
+        float sc[GRP][kKB];
 #pragma unroll
-            for (int j = 0; j < kKB; ++j) {
-                const int64_t key = t0 + row * kKB + j;
-                valid[j] = key < hi;
-                if (valid[j]) {
-                    load_chunk<KV, DPL>(kb, off + key * D, kf[j]);
-                    load_chunk<KV, DPL>(vb, off + key * D, vf[j]);
-                } else {
-#pragma unroll
-                    for (int d = 0; d < DPL; ++d) { kf[j][d] = 0.0f; vf[j][d] = 0.0f; }
-                }
-            }
-            float sc[GRP][kKB];
-#pragma unroll
-            for (int j = 0; j < kKB; ++j)
-#pragma unroll
-                for (int hh = 0; hh < GRP; ++hh) {
-                    float p = 0.0f;
-#pragma unroll
-                    for (int d = 0; d < DPL; ++d) p = fmaf(qr[hh][d], kf[j][d], p);
-                    sc[hh][j] = row16_sum(p);
-                }
-#pragma unroll
-            for (int j = 0; j < kKB; ++j) {
-                const int64_t key = t0 + row * kKB + j;
-#pragma unroll
-                for (int hh = 0; hh < GRP; ++hh) {
-                    float v = sc[hh][j];
-                    if (bb != nullptr && valid[j]) v += bb[hh * bias_hstride + key];
-                    sc[hh][j] = valid[j] ? v : -INFINITY;
-                }
-            }
+        for (int j = 0; j < kKB; ++j)
 #pragma unroll
             for (int hh = 0; hh < GRP; ++hh) {
-                float mb = sc[hh][0];
+                float p = 0.0f;
 #pragma unroll
-                for (int j = 1; j < kKB; ++j) mb = fmaxf(mb, sc[hh][j]);
-                const float mn = fmaxf(m[hh], mb);
-                const float corr = __expf(m[hh] - mn);
-                m[hh] = mn;
-                float ls = l[hh] * corr;
-#pragma unroll
-                for (int j = 0; j < kKB; ++j) {
-                    const float p = __expf(sc[hh][j] - mn);
-                    sc[hh][j] = p;
-                    ls += p;
-                }
-                l[hh] = ls;
-#pragma unroll
-                for (int d = 0; d < DPL; ++d) {
-                    float a = acc[hh][d] * corr;
-#pragma unroll
-                    for (int j = 0; j < kKB; ++j) a = fmaf(sc[hh][j], vf[j][d], a);
-                    acc[hh][d] = a;
-                }
+                for (int d = 0; d < DPL; ++d) p = fmaf(qr[hh][d], raw_at<KV, DPL>(t.k[j], d), p);
+                sc[hh][j] = row16_sum(p);
             }
+#pragma unroll
+        for (int j = 0; j < kKB; ++j) {
+            const int key = c.y + row * kKB + j;
+            const bool valid = key < e;
+#pragma unroll
+            for (int hh = 0; hh < GRP; ++hh) {
+                float v = sc[hh][j];
+                if (bb != nullptr && valid) v += bb[hh * bias_hstride + key];
+                sc[hh][j] = valid ? v : -INFINITY;
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < GRP; ++hh) {
+            float mb = sc[hh][0];
+#pragma unroll
+            for (int j = 1; j < kKB; ++j) mb = fmaxf(mb, sc[hh][j]);
+            const float mn = fmaxf(m[hh], mb);
+            const float corr = __expf(m[hh] - mn);
+            m[hh] = mn;
+            float ls = l[hh] * corr;
+#pragma unroll
+            for (int j = 0; j < kKB; ++j) {
+                const float p = __expf(sc[hh][j] - mn);
+                sc[hh][j] = p;
+                ls += p;
+            }
+            l[hh] = ls;
+#pragma unroll
+            for (int d = 0; d < DPL; ++d) {
+                float a = acc[hh][d] * corr;
+#pragma unroll
+                for (int j = 0; j < kKB; ++j) a = fmaf(sc[hh][j], raw_at<KV, DPL>(t.v[j], d), a);
+                acc[hh][d] = a;
+            }
+        }
+    };
+    // Masked rows of a tile may hold anything (e.g. unwritten ring slots): their values are replaced
+    // by zeros before use so that p = 0 cannot meet a non-finite value.
+    auto clean = [&](KeyTile<KV, DPL> &t, int2 c) {
+        const int e = pick4(c.x, eff[0], eff[1], eff[2], eff[3]);
+        if (c.y + 16 <= e) return;                 // uniform: the whole tile is valid
+#pragma unroll
+        for (int j = 0; j < kKB; ++j) {
+            const bool valid = c.y + row * kKB + j < e;
+#pragma unroll
+            for (int w = 0; w < RowRaw<KV, DPL>::W; ++w) {
+                t.k[j].w[w] = valid ? t.k[j].w[w] : 0u;
+                t.v[j].w[w] = valid ? t.v[j].w[w] : 0u;
+            }
+        }
+    };
+
+    if constexpr (PIPE) {
+        while (cur.x < 4) {
+            int2 nx = next(cur);
+            if (nx.x < 4) fetch(tB, nx);
+            clean(tA, cur);
+            compute(tA, cur);
+            cur = nx;
+            if (cur.x >= 4) break;
+            nx = next(cur);
+            if (nx.x < 4) fetch(tA, nx);
+            clean(tB, cur);
+            compute(tB, cur);
+            cur = nx;
+        }
+    } else {
+        while (cur.x < 4) {
+            clean(tA, cur);
+            compute(tA, cur);
+            cur = next(cur);
+            if (cur.x < 4) fetch(tA, cur);
         }
     }
 
@@ -252,13 +342,16 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict
     const int64_t stride = (int64_t)grp * (D + 2);
     const float *p0 = part + (((int64_t)b * G + g) * n_splits * grp + hh) * (D + 2);
     const int d = threadIdx.x;
+    // Unconditional loads (splits past n_splits re-read the last one and get weight 0): a branch per
+    // load would make the compiler wait for each load before the next.
     float v[kMaxSplits];
 #pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s) v[s] = s < n_splits ? p0[s * stride + d] : 0.0f;
+    for (int s = 0; s < kMaxSplits; ++s) v[s] = p0[min(s, n_splits - 1) * stride + d];
     if (threadIdx.x < 64) {
         const int s = threadIdx.x;
-        const float ms = s < n_splits ? p0[s * stride + D] : kNegBig;
-        const float ls = s < n_splits ? p0[s * stride + D + 1] : 0.0f;
+        const float *ps = p0 + min(s, n_splits - 1) * stride;
+        const float ms = s < n_splits ? ps[D] : kNegBig;
+        const float ls = s < n_splits ? ps[D + 1] : 0.0f;
         const float M = wave_max(ms);
         const float w = s < n_splits ? __expf(ms - M) : 0.0f;
         const float L = wave_sum(w * ls);
@@ -268,8 +361,7 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict
     __syncthreads();
     float a = 0.0f;
 #pragma unroll
-    for (int s = 0; s < kMaxSplits; ++s)
-        if (s < n_splits) a = fmaf(wgt[s], v[s], a);
+    for (int s = 0; s < kMaxSplits; ++s) a = fmaf(wgt[s], v[s], a);
     out[((int64_t)b * H + h) * D + d] = a * inv_l;
 }
 
@@ -352,6 +444,7 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
     const int elem = kv_dtype == VGX_F32 ? 4 : 2;
     for (int s = 0; s < n_spans; ++s) {
         if (spans[s].len < 0) return VGX_E_SIZE;
+        if (spans[s].len > 0x3FFFFFFF) return VGX_E_LIMIT;
         if (spans[s].len > 0 && (!spans[s].k || !spans[s].v)) return VGX_E_ARG;
         if (spans[s].len > 0 && (((uintptr_t)spans[s].k | (uintptr_t)spans[s].v) % 16)) return VGX_E_ALIGN;
         if (spans[s].len > 0 && ((spans[s].batch_stride * elem) % 16 || (spans[s].group_stride * elem) % 16)) return VGX_E_ALIGN;
@@ -364,6 +457,7 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
         n_tot += spans[s].len;
     }
     if (n_tot <= 0) return VGX_E_SIZE;
+    if (n_tot > 0x3FFFFFFF) return VGX_E_LIMIT;
     int64_t kps = 0;
     const int ns = choose_splits(B, G, n_tot, &kps);
     float *part = nullptr;
