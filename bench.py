@@ -124,7 +124,8 @@ def dominant_kernel(model, rounds: int = 20):
     n = rounds * len(layers)
     wb = layers[0].wgu.stream_bytes
     algo = wb + 4 * cfg.d_model + 4 * cfg.d_ff
-    return {"kernel": "qgemv_kernel<Q4_0, batch 1, SwiGLU epilogue, split-K x1, RMSNorm prologue> (gate|up 2x8960x1536)",
+    return {"kernel": "gemv1_kernel<Q4_0, SwiGLU epilogue, RMSNorm prologue, lane per block, 4 waves, staging first> "
+                      "(gate|up 2x8960x1536)",
             "launches": n, "avg_us": us, "bytes_per_launch": algo, "gbs": algo / us / 1e3}
 
 
@@ -277,7 +278,7 @@ def pmc_report(fetch_csv: str, write_csv: str) -> None:
     """Markdown summary of the two PMC runs: per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the
     dominant kernel and of the calibration copy, the copy's bytes / counter factor, and the scaled
     HBM traffic per launch of the dominant kernel (the figure ``roofline.traffic`` reports)."""
-    kern, copy = "qgemv_kernel<9, 1, 2, 0, 1, true", "neg_kernel"
+    kern, copy = "gemv1_kernel<9, 2, true", "neg_kernel"
     fk, nk = _pmc_avg(fetch_csv, "FETCH_SIZE", kern)
     fc, nc = _pmc_avg(fetch_csv, "FETCH_SIZE", copy)
     wk, _ = _pmc_avg(write_csv, "WRITE_SIZE", kern)

@@ -11,13 +11,10 @@
 // blocks of one row-quad: one set of 128-bit loads brings 4 x 32 weights, the 32 activations of
 // the block are read from LDS once and used for the four rows.
 //
-// Two mappings (KW waves split the blocks of the same row-quads and are reduced through LDS):
-//  * row mode (many rows: the gate/up pair, the 151665-row LM head): 16 lanes (one DPP row) per
-//    row-quad, four row-quads per wave, 4 x KW waves per workgroup (KW = 1 is launched);
-//  * split-K mode (fewer rows): a whole wave per row-quad, KW waves per workgroup over its blocks
-//    (lane stride 64 * KW).  This keeps ~1500 waves in flight for 1536 x 8960 (down projection).
-// Each lane requests the weights of up to U blocks at once, the first ones before the activations
-// are staged, to keep enough bytes in flight for HBM.
+// One activation row (the decode step) runs gemv1_kernel, whose mapping is picked from the shape
+// (below); 2-4 rows per pass run qgemv_kernel in row mode (16 lanes per row-quad, four row-quads per
+// wave, 4 waves per workgroup) for >= 2048 row-quads, else in split-K mode (a wave per row-quad).
+// Each lane requests the weights of up to U blocks at once to keep enough bytes in flight for HBM.
 //
 // Arithmetic is fp32 throughout, as in the reference: per block s = sum_j q_j x_j, acc += d * s.
 // Q4_0 nibbles n are converted unsigned (v_cvt_f32_ubyte*) and the -8 offset is applied once per
@@ -183,13 +180,8 @@ __device__ __forceinline__ void gemv_block(const BlockRegs<DT> &br, const float 
     }
 }
 
-// XD (direct activations, split-K mode with one wave and one batch row only): no LDS staging; each
-// lane reads the 32 activations (and RMSNorm weights) of its block from global memory, where every
-// other wave reads the same bytes (L1 / L2 hits).  Saves the staging round trip and barrier of the
-// small projections (measured 4.0 vs 4.4 us for 1536 x 1536 Q4_0).
-template <int DT, int NB, int EPI, int MODE, int KW, bool NORM, bool XD = false>
+template <int DT, int NB, int EPI, int MODE, int KW, bool NORM>
 __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_kernel(GemvArgs a, int cbk) {
-    static_assert(!XD || (MODE == MODE_SPLITK && KW == 1 && NB == 1), "direct activations: one wave, one row");
     extern __shared__ float smem[];
     constexpr int LPR = MODE == MODE_ROWS ? 16 : 64;     // lanes per row-quad
     constexpr int RQW = 64 / LPR;                          // row-quads per wave
@@ -238,9 +230,7 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
         cb = min(cbk, nblk - c0);
         if (c0) __syncthreads();
         const bool vec = ((reinterpret_cast<uintptr_t>(a.x) & 15) == 0) && (a.ldx % 4 == 0);
-        if constexpr (XD) {
-            // no staging
-        } else if (vec) {
+        if (vec) {
             // kStageLoads float4 loads per thread in flight: one round trip for the model's shapes
             // (1536 activations over 256 threads; 8960 over the 512 threads of the 8-wave split-K)
             // without holding more staging registers than that needs.
@@ -289,7 +279,7 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
                 xs[(n * cbk + blk) * kGemvPad + j] = v;
             }
         }
-        if constexpr (!XD) __syncthreads();
+        __syncthreads();
         if (act) {
             for (int b = first; b < cb; b += U * stride) {
                 if (b != first) {
@@ -300,31 +290,7 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int bb = b + u * stride;
-                    if (bb >= cb) continue;
-                    if constexpr (XD) {
-                        const int64_t c = (int64_t)(c0 + bb) * QK;
-                        const float4 *xp = reinterpret_cast<const float4 *>(a.x + c);
-                        float4 xv[8], gv[8];
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) xv[j] = xp[j];
-                        if constexpr (NORM) {
-#pragma unroll
-                            for (int j = 0; j < 8; ++j) gv[j] = reinterpret_cast<const float4 *>(a.lnw + c)[j];
-                        }
-                        float xb[QK];
-#pragma unroll
-                        for (int j = 0; j < 8; ++j) {
-                            float4 t = xv[j];
-                            if constexpr (NORM) {
-                                ssq[0] += fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, t.w * t.w)));
-                                t.x *= gv[j].x; t.y *= gv[j].y; t.z *= gv[j].z; t.w *= gv[j].w;
-                            }
-                            xb[4 * j] = t.x; xb[4 * j + 1] = t.y; xb[4 * j + 2] = t.z; xb[4 * j + 3] = t.w;
-                        }
-                        gemv_block<DT, NB>(br[u], xb, 0, acc);
-                    } else {
-                        gemv_block<DT, NB>(br[u], xs + bb * kGemvPad, cbk * kGemvPad, acc);
-                    }
+                    if (bb < cb) gemv_block<DT, NB>(br[u], xs + bb * kGemvPad, cbk * kGemvPad, acc);
                 }
             }
             // first batch of the next chunk
@@ -406,45 +372,218 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
     }
 }
 
-// Launch the GEMV over all batch rows (passes of up to 4).  Mapping chosen from the shape:
-//  * row mode (>= 2048 row-quads): 16 lanes per row-quad, 4 waves per workgroup, each lane
-//    requesting all of its (typically 3) blocks at once.  Splitting K across 3 waves here measured
-//    slower on MI355X (gate/up 10.8 vs 10.2 us, LM head 68.7 vs 51.3 us): the extra LDS reduction
-//    costs more than the shorter per-lane chain saves;
-//  * split-K mode: one row-quad per workgroup, KW in {1, 2, 8} waves over its blocks (8 for the
-//    280-block down projection: 7.1 vs 7.5 us with 4); with one wave and one batch row the
-//    activations are read directly (XD) instead of being staged.
+// One-row GEMV (the decode step): lean register budget, one pass over K.
+//   LPR lanes per row-quad (64: a lane per block; 16: a DPP row per row-quad, U blocks per lane),
+//   WPG waves with distinct row-quads, KW waves splitting K (reduced through LDS).
+//   Activations: XD = read directly by each lane; otherwise staged in LDS (lnw * x, sum x^2
+//   accumulated while staging) with SF = the staging loads requested before the weights, so the
+//   barrier after staging does not wait for the weights and each wave multiplies as soon as its
+//   own weights arrive.
+// Measured on MI355X (gate/up 2 x 8960 x 1536 Q4_0): LPR 64 / 4 waves / SF 7.6 us against 9.4 us for
+// the DPP-row mapping; the 151665-row LM head keeps the DPP-row mapping (48 vs 53 us).
+template <int DT, int EPI, bool NORM, int LPR, int WPG, int KW, int U, bool SF, bool XD>
+__global__ __launch_bounds__(64 * WPG * KW) void gemv1_kernel(GemvArgs a) {
+    static_assert(!XD || (WPG == 1 && KW == 1), "direct activations: one wave per workgroup");
+    constexpr int RQW = 64 / LPR;
+    constexpr int NW = WPG * KW;
+    constexpr int NT = 64 * NW;
+    constexpr int CH = KW >= 4 ? 6 : 4;            // staging float4 loads per thread and round
+    extern __shared__ float xs[];                  // [nblk][kGemvPad]
+    __shared__ float red[NW][RQW][4];
+    __shared__ float rsum[NW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rw = wave / KW, ks = wave - rw * KW;
+    const int li = lane % LPR, rqi = lane / LPR;
+    const int64_t rq = (int64_t)blockIdx.x * (WPG * RQW) + rw * RQW + rqi;
+    const bool act = rq < a.n_rq;
+    const int nblk = a.nblk;
+    const int first = ks * LPR + li;
+    constexpr int stride = LPR * KW;
+
+    BlockRegs<DT> br[U];
+    auto load_first = [&]() {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            if (act && first + u * stride < nblk) gemv_load<DT>(br[u], a.w, a.soff, rq, nblk, first + u * stride);
+    };
+    if constexpr (!SF) load_first();
+
+    float acc[4][1] = {{0.0f}, {0.0f}, {0.0f}, {0.0f}};
+    float ssq = 0.0f;
+    if constexpr (!XD) {
+        const int n4 = nblk * 8;
+        auto stage_load = [&](int i0, float4 (&v)[CH], float4 (&gw)[CH]) {
+#pragma unroll
+            for (int u = 0; u < CH; ++u) {
+                const int i = i0 + u * NT;
+                if (i < n4) {
+                    v[u] = reinterpret_cast<const float4 *>(a.x)[i];
+                    if constexpr (NORM) gw[u] = reinterpret_cast<const float4 *>(a.lnw)[i];
+                }
+            }
+        };
+        auto stage_store = [&](int i0, const float4 (&v)[CH], const float4 (&gw)[CH]) {
+#pragma unroll
+            for (int u = 0; u < CH; ++u) {
+                const int i = i0 + u * NT;
+                if (i < n4) {
+                    float4 t = v[u];
+                    if constexpr (NORM) {
+                        ssq += fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, t.w * t.w)));
+                        t.x *= gw[u].x; t.y *= gw[u].y; t.z *= gw[u].z; t.w *= gw[u].w;
+                    }
+                    *reinterpret_cast<float4 *>(xs + (i >> 3) * kGemvPad + (i & 7) * 4) = t;
+                }
+            }
+        };
+        {
+            // first round, then (SF) every thread's weight loads, whether or not it stages anything
+            float4 v[CH], gw[CH];
+            stage_load(tid, v, gw);
+            if constexpr (SF) load_first();
+            stage_store(tid, v, gw);
+        }
+        for (int i0 = tid + CH * NT; i0 < n4; i0 += CH * NT) {
+            float4 v[CH], gw[CH];
+            stage_load(i0, v, gw);
+            stage_store(i0, v, gw);
+        }
+        __syncthreads();
+    } else if constexpr (SF) {
+        load_first();
+    }
+    if (act) {
+        for (int b = first; b < nblk; b += U * stride) {
+            if (b != first) {
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    if (b + u * stride < nblk) gemv_load<DT>(br[u], a.w, a.soff, rq, nblk, b + u * stride);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int bb = b + u * stride;
+                if (bb >= nblk) continue;
+                if constexpr (XD) {
+                    const float4 *xp = reinterpret_cast<const float4 *>(a.x + (int64_t)bb * QK);
+                    float4 xv[8], gv[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) xv[j] = xp[j];
+                    if constexpr (NORM) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) gv[j] = reinterpret_cast<const float4 *>(a.lnw + (int64_t)bb * QK)[j];
+                    }
+                    float xb[QK];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        float4 t = xv[j];
+                        if constexpr (NORM) {
+                            ssq += fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, t.w * t.w)));
+                            t.x *= gv[j].x; t.y *= gv[j].y; t.z *= gv[j].z; t.w *= gv[j].w;
+                        }
+                        xb[4 * j] = t.x; xb[4 * j + 1] = t.y; xb[4 * j + 2] = t.z; xb[4 * j + 3] = t.w;
+                    }
+                    gemv_block<DT, 1>(br[u], xb, 0, acc);
+                } else {
+                    gemv_block<DT, 1>(br[u], xs + bb * kGemvPad, 0, acc);
+                }
+            }
+        }
+    }
+    if constexpr (NORM) {
+        // XD: every lane summed its own blocks, which together cover the row once (one wave).
+        const float t = wave_sum(ssq);
+        if (lane == 0) rsum[wave] = t;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) tot += rsum[w];
+        const float inv = 1.0f / sqrtf(tot / (float)(nblk * QK) + a.eps);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r][0] *= inv;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r][0] = LPR == 64 ? wave_sum(acc[r][0]) : row16_sum(acc[r][0]);
+    if constexpr (KW > 1) {
+        if (li == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][rqi][r] = acc[r][0];
+        }
+        __syncthreads();
+        if (ks != 0) return;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float sum = red[wave][rqi][r];
+#pragma unroll
+            for (int w = 1; w < KW; ++w) sum += red[wave + w][rqi][r];
+            acc[r][0] = sum;
+        }
+    }
+    if (!act || li != 0) return;
+    if constexpr (EPI == EPI_SWIGLU) {
+        const int64_t o0 = rq * 2;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            if (o0 + k >= a.rows_out) continue;
+            const float g = acc[k][0], u = acc[2 + k][0];
+            a.y[o0 + k] = g / (1.0f + __expf(-g)) * u;
+        }
+    } else {
+        const int64_t r0 = rq * 4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = r0 + r;
+            if (row >= a.rows_out) continue;
+            float v = acc[r][0];
+            if (a.bias) v += a.bias[row];
+            if constexpr (EPI == EPI_ACCUM) v += a.y[row];
+            a.y[row] = v;
+        }
+    }
+}
+
+constexpr int kGemv1MaxBlocks = 448;   // LDS staging of one row: 448 * 36 * 4 B = 63 KB
+
+template <int DT, int EPI, bool NORM>
+void gemv1_launch(const GemvArgs &a, hipStream_t st) {
+    const size_t lds = (size_t)a.nblk * kGemvPad * sizeof(float);
+#define VGX_GEMV1(LPR, WPG, KW, U, SF, XD)                                                              \
+    hipLaunchKernelGGL((gemv1_kernel<DT, EPI, NORM, LPR, WPG, KW, U, SF, XD>),                           \
+                       dim3((unsigned)((a.n_rq + WPG * (64 / LPR) - 1) / (WPG * (64 / LPR)))),              \
+                       dim3(64 * WPG * KW), XD ? 0 : lds, st, a)
+    const bool aligned = ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.lnw & 15) == 0;
+    if (a.n_rq >= 16384) VGX_GEMV1(16, 4, 1, 3, false, false);        // LM head: DPP row per row-quad
+    else if (a.n_rq >= 2048) VGX_GEMV1(64, 4, 1, 1, true, false);     // gate/up: lane per block
+    else if (a.nblk >= 192) VGX_GEMV1(64, 1, 8, 1, true, false);      // down: 8 waves over K
+    else if (a.nblk >= 96) VGX_GEMV1(64, 1, 2, 1, true, false);
+    else if (aligned && DT != VGX_F32) VGX_GEMV1(64, 1, 1, 1, false, true);   // small: direct
+    else VGX_GEMV1(64, 2, 1, 1, true, false);
+#undef VGX_GEMV1
+}
+
+// Launch the GEMV over all batch rows.  A single row (the decode step) runs gemv1_kernel; more rows
+// run qgemv_kernel in passes of up to 4, in row mode (16 lanes per row-quad, 4 waves per workgroup)
+// for >= 2048 row-quads, else in split-K mode (one wave per row-quad).
 template <int DT>
 int qgemv_launch(GemvArgs a, hipStream_t st) {
     const bool rows_mode = a.n_rq >= 2048;
-    int kw = 1;
-    if (a.batch == 1) {  // K-split variants are instantiated for batch 1 (the decode step) only
-        if (!rows_mode) kw = a.nblk >= 192 ? 8 : a.nblk >= 96 ? 2 : 1;
-    }
     const bool norm = a.lnw != nullptr;
-    const bool xd = a.batch == 1 && !rows_mode && kw == 1 && ((uintptr_t)a.x & 15) == 0 &&
-                    ((uintptr_t)a.lnw & 15) == 0 && DT != VGX_F32;
+    if (a.batch == 1 && a.nblk <= kGemv1MaxBlocks && ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.lnw & 15) == 0) {
+        if (a.epi == EPI_SWIGLU) { if (norm) gemv1_launch<DT, EPI_SWIGLU, true>(a, st); else gemv1_launch<DT, EPI_SWIGLU, false>(a, st); }
+        else if (a.epi == EPI_ACCUM) { if (norm) gemv1_launch<DT, EPI_ACCUM, true>(a, st); else gemv1_launch<DT, EPI_ACCUM, false>(a, st); }
+        else { if (norm) gemv1_launch<DT, EPI_STORE, true>(a, st); else gemv1_launch<DT, EPI_STORE, false>(a, st); }
+        return hipGetLastError() == hipSuccess ? VGX_OK : VGX_E_HIP;
+    }
     for (int64_t b0 = 0; b0 < a.batch; b0 += 4) {
         GemvArgs p = a;
         const int nb = (int)std::min<int64_t>(4, a.batch - b0);
         p.x = a.x + b0 * a.ldx;
         p.y = a.y + b0 * a.ldy;
-        const int cbk = xd ? a.nblk : std::min(a.nblk, kGemvMaxChunkFloats / (QK * nb));
-        const size_t lds = xd ? 0 : (size_t)nb * cbk * kGemvPad * sizeof(float);
+        const int cbk = std::min(a.nblk, kGemvMaxChunkFloats / (QK * nb));
+        const size_t lds = (size_t)nb * cbk * kGemvPad * sizeof(float);
         const unsigned grid = rows_mode ? (unsigned)((a.n_rq + 15) / 16) : (unsigned)a.n_rq;
-        const unsigned threads = (rows_mode ? 256u : 64u) * (unsigned)kw;
+        const unsigned threads = rows_mode ? 256u : 64u;
 #define VGX_GEMV_GO(NBV, EPIV, MODEV, KWV, NORMV)                                                      \
     hipLaunchKernelGGL((qgemv_kernel<DT, NBV, EPIV, MODEV, KWV, NORMV>), dim3(grid), dim3(threads), lds, st, p, cbk)
-#define VGX_GEMV_KW(NBV, EPIV, NORMV)                                                                  \
-    do {                                                                                               \
-        if (rows_mode) VGX_GEMV_GO(NBV, EPIV, MODE_ROWS, 1, NORMV);                                    \
-        else if (kw == 8) VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 8, NORMV);                               \
-        else if (kw == 2) VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 2, NORMV);                               \
-        else if (xd && DT != VGX_F32)                                                                  \
-            hipLaunchKernelGGL((qgemv_kernel<DT, NBV, EPIV, MODE_SPLITK, 1, NORMV, DT != VGX_F32 && NBV == 1>), \
-                               dim3(grid), dim3(threads), lds, st, p, cbk);                            \
-        else VGX_GEMV_GO(NBV, EPIV, MODE_SPLITK, 1, NORMV);                                            \
-    } while (0)
 #define VGX_GEMV_K1(NBV, EPIV, NORMV)                                                                  \
     do {                                                                                               \
         if (rows_mode) VGX_GEMV_GO(NBV, EPIV, MODE_ROWS, 1, NORMV);                                    \
@@ -457,14 +596,13 @@ int qgemv_launch(GemvArgs a, hipStream_t st) {
         else { if (norm) SEL(NBV, EPI_STORE, true); else SEL(NBV, EPI_STORE, false); } \
     } while (0)
         switch (nb) {
-            case 1: VGX_GEMV_EPI(1, VGX_GEMV_KW); break;
+            case 1: VGX_GEMV_EPI(1, VGX_GEMV_K1); break;
             case 2: VGX_GEMV_EPI(2, VGX_GEMV_K1); break;
             case 3: VGX_GEMV_EPI(3, VGX_GEMV_K1); break;
             default: VGX_GEMV_EPI(4, VGX_GEMV_K1); break;
         }
 #undef VGX_GEMV_EPI
 #undef VGX_GEMV_K1
-#undef VGX_GEMV_KW
 #undef VGX_GEMV_GO
         if (hipGetLastError() != hipSuccess) return VGX_E_HIP;
     }
