@@ -270,17 +270,266 @@ __global__ __launch_bounds__(256) void qgemm_kernel(const uint8_t *__restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Decode batches (up to 64 activation rows): one launch without the split pre-pass.  Each workgroup
+// converts the activations of its K range itself, 4 blocks at a time, into LDS (bf16 hi and lo, the
+// per-block sums of hi + lo), shared by its 4 waves; the chunks are double-buffered so the next
+// chunk's activations and weights are requested before the current one is multiplied (requesting
+// the weights a second chunk earlier measured no faster).  The fused
+// RMSNorm stages lnw * x and scales the finished sums by 1 / rms of the activation row (sum x^2 is
+// accumulated by fixed threads while staging, reduced in a fixed order: deterministic).  K-split
+// partials carry the raw sums and, with the RMSNorm, the per-split sum x^2 of every row.
+constexpr int kCK = 4;                       // blocks per staged chunk
+constexpr int kSRow = kCK * QK + 8;          // bf16 per staged activation row (16 B of padding)
+
+template <int DT, int NC, int EPI, bool SPLIT, bool NORM>
+__global__ __launch_bounds__(256) void qgemm_small_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
+                                                           int nblk, int64_t rows_out, const float *__restrict__ x,
+                                                           int64_t ldx, const float *__restrict__ lnw, float eps,
+                                                           int64_t batch, const float *__restrict__ bias,
+                                                           float *__restrict__ y, int64_t ldy, float *__restrict__ part,
+                                                           float *__restrict__ part_ssq, int kper) {
+    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 8.0f;
+    constexpr int R = 16 * NC;                     // staged activation rows
+    constexpr int F4 = R * kCK * 8 / 256;          // staged float4 per thread per chunk
+    __shared__ __align__(16) uint16_t sh[2][R][kSRow];
+    __shared__ __align__(16) uint16_t sl[2][R][kSRow];
+    __shared__ float ssum[2][R][kCK];
+    __shared__ float sinv[R];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, lg = lane >> 4, r4 = l16 & 3;
+    const int64_t rq_wave = ((int64_t)blockIdx.x * 4 + wave) * 8;
+    const int64_t b0 = (int64_t)blockIdx.y * R;
+    const int cols = nblk * QK;
+
+    int64_t arq[2], crq[2];
+    bool aok[2], cok[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        arq[t] = rq_wave + 4 * t + (l16 >> 2);
+        aok[t] = arq[t] < n_rq;
+        crq[t] = rq_wave + 4 * t + lg;
+        cok[t] = crq[t] < n_rq;
+    }
+    const int blk_lo = SPLIT ? (int)blockIdx.z * kper : 0;
+    const int blk_hi = SPLIT ? min(nblk, blk_lo + kper) : nblk;
+    const int n_chunks = blk_hi > blk_lo ? (blk_hi - blk_lo + kCK - 1) / kCK : 0;
+
+    // staging: thread t takes float4 f = t + 256 i of the chunk (row f / 32, block (f / 8) % 4, quad f % 8)
+    float4 xr[F4], gr[F4];
+    float ssq[F4];
+#pragma unroll
+    for (int i = 0; i < F4; ++i) ssq[i] = 0.0f;
+    auto stage_load = [&](int c) {
+        const int cb0 = blk_lo + c * kCK;
+#pragma unroll
+        for (int i = 0; i < F4; ++i) {
+            const int f = tid + 256 * i, row = f >> 5, blk = cb0 + ((f >> 3) & 3), j4 = f & 7;
+            const int64_t br = b0 + row;
+            xr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            gr[i] = make_float4(1.f, 1.f, 1.f, 1.f);
+            if (br < batch && blk < blk_hi) {
+                xr[i] = *reinterpret_cast<const float4 *>(x + br * ldx + blk * QK + j4 * 4);
+                if constexpr (NORM) gr[i] = *reinterpret_cast<const float4 *>(lnw + blk * QK + j4 * 4);
+            }
+        }
+    };
+    auto stage_store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < F4; ++i) {
+            const int f = tid + 256 * i, row = f >> 5, bl = (f >> 3) & 3, j4 = f & 7;
+            const float e[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
+            const float g[4] = {gr[i].x, gr[i].y, gr[i].z, gr[i].w};
+            uint32_t hb[4], lb[4];
+            float sum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if constexpr (NORM) ssq[i] = fmaf(e[k], e[k], ssq[i]);
+                const float u = NORM ? g[k] * e[k] : e[k];
+                hb[k] = float_to_bf16_bits(u);
+                lb[k] = float_to_bf16_bits(u - bf16_bits_to_float(hb[k]));
+                sum += bf16_bits_to_float(hb[k]) + bf16_bits_to_float(lb[k]);
+            }
+            *reinterpret_cast<uint2 *>(&sh[buf][row][bl * QK + j4 * 4]) =
+                make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
+            *reinterpret_cast<uint2 *>(&sl[buf][row][bl * QK + j4 * 4]) =
+                make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+            // the 8 threads of one (row, block) are 8 consecutive lanes
+            sum += __shfl_xor(sum, 1, kWave);
+            sum += __shfl_xor(sum, 2, kWave);
+            sum += __shfl_xor(sum, 4, kWave);
+            if (j4 == 0) ssum[buf][row][bl] = sum;
+        }
+    };
+
+    struct AReg {
+        uint2 wa[2], sc[2];
+    };
+    AReg ra[kCK], rb[kCK];
+    auto fetch_a = [&](AReg (&r)[kCK], int c) {
+        const int cb0 = blk_lo + c * kCK;
+#pragma unroll
+        for (int u = 0; u < kCK; ++u) {
+            const int blk = cb0 + u;
+            const bool in = blk < blk_hi;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                r[u].wa[t] = (in && aok[t]) ? load_a<DT>(W, arq[t], nblk, blk, r4, lg) : make_uint2(0, 0);
+                r[u].sc[t] = (in && cok[t]) ? *reinterpret_cast<const uint2 *>(W + soff + (crq[t] * nblk + blk) * 8)
+                                            : make_uint2(0, 0);
+            }
+        }
+    };
+
+    f32x4_t acc[2][NC];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[t][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto compute = [&](const AReg (&r)[kCK], int buf) {
+#pragma unroll
+        for (int u = 0; u < kCK; ++u) {
+            bf16x8_t af[2];
+            float d[2][4];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                af[t] = a_frag<DT>(r[u].wa[t], lg);
+                d[t][0] = half_bits_to_float(r[u].sc[t].x);
+                d[t][1] = half_bits_to_float(r[u].sc[t].x >> 16);
+                d[t][2] = half_bits_to_float(r[u].sc[t].y);
+                d[t][3] = half_bits_to_float(r[u].sc[t].y >> 16);
+            }
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const int row = c * 16 + l16;
+                const uint4 xh = *reinterpret_cast<const uint4 *>(&sh[buf][row][u * QK + 8 * lg]);
+                const uint4 xl = *reinterpret_cast<const uint4 *>(&sl[buf][row][u * QK + 8 * lg]);
+                const float corr = OFF * ssum[buf][row][u];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    f32x4_t pr = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                    pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, xh), pr, 0, 0, 0);
+                    pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, xl), pr, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf(d[t][i], pr[i] - corr, acc[t][c][i]);
+                }
+            }
+        }
+    };
+
+    if (n_chunks > 0) {
+        stage_load(0);
+        fetch_a(ra, 0);
+        stage_store(0);
+    }
+    __syncthreads();
+    for (int c = 0; c < n_chunks; c += 2) {
+        // chunk c from buffer 0 with ra; chunk c + 1 staged into buffer 1 meanwhile
+        if (c + 1 < n_chunks) {
+            stage_load(c + 1);
+            fetch_a(rb, c + 1);
+        }
+        compute(ra, 0);
+        if (c + 1 < n_chunks) stage_store(1);
+        __syncthreads();
+        if (c + 1 >= n_chunks) break;
+        if (c + 2 < n_chunks) {
+            stage_load(c + 2);
+            fetch_a(ra, c + 2);
+        }
+        compute(rb, 1);
+        if (c + 2 < n_chunks) stage_store(0);
+        __syncthreads();
+    }
+
+    // RMSNorm: sum x^2 of activation row (tid / 32 + 8 i) over this K range, reduced over its 32 threads
+    if constexpr (NORM) {
+#pragma unroll
+        for (int i = 0; i < F4; ++i) {
+            const float t = xor16_sum(row16_sum(ssq[i]));
+            if ((tid & 31) == 0) sinv[(tid >> 5) + 8 * i] = t;
+        }
+        __syncthreads();
+        if constexpr (SPLIT) {
+            if (blockIdx.x == 0 && tid < R && b0 + tid < batch)
+                part_ssq[(int64_t)blockIdx.z * batch + b0 + tid] = sinv[tid];
+        }
+    }
+
+    int64_t bb[NC];
+    bool bok[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        bb[c] = b0 + 16 * c + l16;
+        bok[c] = bb[c] < batch;
+    }
+    if constexpr (SPLIT) {
+        const int64_t rows_p = n_rq * 4;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (!cok[t]) continue;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                if (!bok[c]) continue;
+                float4 v;
+                v.x = acc[t][c][0]; v.y = acc[t][c][1]; v.z = acc[t][c][2]; v.w = acc[t][c][3];
+                *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + bb[c]) * rows_p + crq[t] * 4) = v;
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        float inv = 1.0f;
+        if constexpr (NORM) inv = 1.0f / sqrtf(sinv[c * 16 + l16] / (float)cols + eps);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            if (!cok[t] || !bok[c]) continue;
+            float *yr = y + bb[c] * ldy;
+            if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int64_t o = crq[t] * 2 + k;
+                    if (o >= rows_out) continue;
+                    const float g = acc[t][c][k] * inv, u = acc[t][c][2 + k] * inv;
+                    yr[o] = g / (1.0f + __expf(-g)) * u;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t row = crq[t] * 4 + i;
+                    if (row >= rows_out) continue;
+                    float v = acc[t][c][i] * inv;
+                    if (bias) v += bias[row];
+                    if constexpr (EPI == EPI_ACCUM) v += yr[row];
+                    yr[row] = v;
+                }
+            }
+        }
+    }
+}
+
 // Sum of the K-split partials + epilogue.  One thread per output (b, row); SwiGLU reads the gate and
 // up sums of packed row-quad q (sub-rows k and 2 + k) for output row 2 q + k.
+// part_ssq (when not null): per-split sum x^2 of every activation row; the sums are then scaled by
+// 1 / sqrt(mean(x^2) + eps) (the RMSNorm of the small-batch kernel).
 template <int EPI>
 __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float *__restrict__ part, int ks, int64_t batch,
                                                             int64_t rows_p, int64_t rows_out,
                                                             const float *__restrict__ bias, float *__restrict__ y,
-                                                            int64_t ldy) {
+                                                            int64_t ldy, const float *__restrict__ part_ssq,
+                                                            int cols, float eps) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= batch * rows_out) return;
     const int64_t b = i / rows_out, r = i - b * rows_out;
     float *yr = y + b * ldy;
+    float inv = 1.0f;
+    if (part_ssq) {
+        float t = 0.0f;
+        for (int s = 0; s < ks; ++s) t += part_ssq[s * batch + b];
+        inv = 1.0f / sqrtf(t / (float)cols + eps);
+    }
     if constexpr (EPI == EPI_SWIGLU) {
         const int64_t q = r >> 1, k = r & 1;
         float g = 0.0f, u = 0.0f;
@@ -289,10 +538,13 @@ __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float *__restri
             g += p[k];
             u += p[2 + k];
         }
+        g *= inv;
+        u *= inv;
         yr[r] = g / (1.0f + __expf(-g)) * u;
     } else {
         float v = 0.0f;
         for (int s = 0; s < ks; ++s) v += part[(s * batch + b) * rows_p + r];
+        v *= inv;
         if (bias) v += bias[r];
         if constexpr (EPI == EPI_ACCUM) v += yr[r];
         yr[r] = v;
@@ -326,6 +578,27 @@ inline int64_t part_bytes(int ks, int64_t batch, int64_t rows_p) {
     return ks > 1 ? ((int64_t)ks * batch * rows_p * 4 + 255) / 256 * 256 : 0;
 }
 
+constexpr int64_t kSmallMaxBatch = 64;
+
+inline int small_nc(int64_t batch) { return batch <= 16 ? 1 : 2; }
+
+// K splits of the small-batch kernel: as choose_ksplit, with whole chunks per split.
+inline int small_ksplit(int64_t n_rq, int64_t batch, int nblk, int *kper) {
+    const int ks0 = choose_ksplit(n_rq, batch, small_nc(batch), nblk);
+    int kp = (nblk + ks0 - 1) / ks0;
+    kp = (kp + kCK - 1) / kCK * kCK;
+    *kper = kp;
+    return (nblk + kp - 1) / kp;
+}
+
+// Workspace of the small-batch path: K-split partials, then the per-split sum x^2 of every row.
+inline int64_t small_bytes(int64_t batch, int64_t n_rq, int nblk) {
+    int kper = 0;
+    const int ks = small_ksplit(n_rq, batch, nblk, &kper);
+    if (ks <= 1) return 0;
+    return part_bytes(ks, batch, n_rq * 4) + ((int64_t)ks * batch * 4 + 255) / 256 * 256;
+}
+
 }  // namespace
 
 extern "C" {
@@ -336,7 +609,8 @@ int64_t vgx_qgemm_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, int
     const int64_t rows_p = rows4(epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows);
     const int nc = batch <= 16 ? 1 : 2;
     const int ks = choose_ksplit(rows_p / 4, batch, nc, (int)(cols / QK));
-    return split_bytes(batch, cols) + part_bytes(ks, batch, rows_p);
+    const int64_t big = split_bytes(batch, cols) + part_bytes(ks, batch, rows_p);
+    return batch <= kSmallMaxBatch ? std::max(big, small_bytes(batch, rows_p / 4, (int)(cols / QK))) : big;
 }
 
 int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx, int64_t batch,
@@ -354,6 +628,54 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     const int64_t rows_packed = epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows;
     const int nblk = (int)(cols / QK);
     const int64_t n_rq = rows4(rows_packed) / 4;
+    const int64_t soff0 = gemm_scale_off(dtype, rows_packed, cols);
+    hipStream_t st0 = (hipStream_t)stream;
+    if (batch <= kSmallMaxBatch && ((uintptr_t)x & 15) == 0 && ldx % 4 == 0 && ((uintptr_t)norm_w & 15) == 0) {
+        int kper = 0;
+        const int ks = small_ksplit(n_rq, batch, nblk, &kper);
+        const int64_t need = small_bytes(batch, n_rq, nblk);
+        if (need > 0 && (!workspace || workspace_bytes < need)) return VGX_E_ARENA;
+        if (need > 0 && (uintptr_t)workspace % 256) return VGX_E_ALIGN;
+        auto *part = static_cast<float *>(workspace);
+        auto *pssq = need > 0 ? reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                                          part_bytes(ks, batch, n_rq * 4))
+                              : nullptr;
+        const int nc = small_nc(batch);
+        const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 16 * nc - 1) / (16 * nc)), (unsigned)ks);
+        const auto *w = static_cast<const uint8_t *>(w_packed);
+#define VGX_SG(DT, NC, EPI, SP, NORM)                                                                         \
+    hipLaunchKernelGGL((qgemm_small_kernel<DT, NC, EPI, SP, NORM>), grid, dim3(256), 0, st0, w, soff0, n_rq, nblk, \
+                       rows, x, ldx, norm_w, eps, batch, bias, y, ldy, part, pssq, kper)
+#define VGX_SG_N(DT, NC, EPI, SP) do { if (norm_w) VGX_SG(DT, NC, EPI, SP, true); else VGX_SG(DT, NC, EPI, SP, false); } while (0)
+#define VGX_SG_E(DT, NC)                                                                                      \
+    do {                                                                                                      \
+        if (ks > 1) VGX_SG_N(DT, NC, EPI_STORE, true);                                                        \
+        else if (epilogue == VGX_EPI_SWIGLU) VGX_SG_N(DT, NC, EPI_SWIGLU, false);                             \
+        else if (epilogue == VGX_EPI_ACCUM) VGX_SG_N(DT, NC, EPI_ACCUM, false);                               \
+        else VGX_SG_N(DT, NC, EPI_STORE, false);                                                              \
+    } while (0)
+        if (dtype == VGX_Q8_0) {
+            if (nc == 1) VGX_SG_E(VGX_Q8_0, 1); else VGX_SG_E(VGX_Q8_0, 2);
+        } else {
+            if (nc == 1) VGX_SG_E(VGX_Q4_0, 1); else VGX_SG_E(VGX_Q4_0, 2);
+        }
+#undef VGX_SG_E
+#undef VGX_SG_N
+#undef VGX_SG
+        VGX_CHECK_LAUNCH();
+        if (ks > 1) {
+            const unsigned g = (unsigned)((batch * rows + 255) / 256);
+            const float *ps = norm_w ? pssq : nullptr;
+            if (epilogue == VGX_EPI_SWIGLU)
+                hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_SWIGLU>, dim3(g), dim3(256), 0, st0, part, ks, batch, n_rq * 4, rows, bias, y, ldy, ps, (int)cols, eps);
+            else if (epilogue == VGX_EPI_ACCUM)
+                hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_ACCUM>, dim3(g), dim3(256), 0, st0, part, ks, batch, n_rq * 4, rows, bias, y, ldy, ps, (int)cols, eps);
+            else
+                hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_STORE>, dim3(g), dim3(256), 0, st0, part, ks, batch, n_rq * 4, rows, bias, y, ldy, ps, (int)cols, eps);
+            VGX_CHECK_LAUNCH();
+        }
+        return VGX_OK;
+    }
     const int nc = batch <= 16 ? 1 : 2;
     const int ks = choose_ksplit(n_rq, batch, nc, nblk);
     if (!workspace || workspace_bytes < split_bytes(batch, cols) + part_bytes(ks, batch, n_rq * 4)) return VGX_E_ARENA;
@@ -391,11 +713,11 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     if (ks > 1) {
         const unsigned g = (unsigned)((batch * rows + 255) / 256);
         if (epilogue == VGX_EPI_SWIGLU)
-            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_SWIGLU>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy);
+            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_SWIGLU>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy, nullptr, (int)cols, 0.0f);
         else if (epilogue == VGX_EPI_ACCUM)
-            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_ACCUM>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy);
+            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_ACCUM>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy, nullptr, (int)cols, 0.0f);
         else
-            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_STORE>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy);
+            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_STORE>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy, nullptr, (int)cols, 0.0f);
         VGX_CHECK_LAUNCH();
     }
     return VGX_OK;
