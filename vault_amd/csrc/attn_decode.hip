@@ -20,6 +20,9 @@ using namespace vgx;
 
 namespace {
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
 constexpr int kKB = 4;       // keys per DPP row per 16-key tile
 constexpr int kWaves = 4;    // waves per workgroup
 constexpr int kMinKeysPerWave = 16;
@@ -328,6 +331,243 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
     }
 }
 
+// bf16 state, D = 128: the same split decode attention on v_mfma_f32_16x16x32_bf16.  The GRP query
+// heads of a KV group are the 16 MFMA columns (GRP <= 16), so per 32-key tile a wave computes
+//   S^T (keys x heads) = K Q^T     A = K rows straight from HBM (lane: key l % 16, dims 8 (l / 16) ..
+//                                  + 7 of a 32-dim chunk), B = Q^T as a bf16 hi + lo pair (fp32-level
+//                                  scores);
+//   O^T (dims x heads) += V^T P^T  A = V^T from a wave-private transposed LDS copy of the tile, B = P^T
+//                                  straight from the S^T accumulators as a bf16 hi + lo pair.
+// A lane of the 16 x 16 outputs owns one head, so the online softmax is lane-local (two cross-lane
+// steps for the max and the final sum), exactly as in the prefill kernel.  The K-slot assignment of
+// the second product (keys 4 lg .. + 3 and 16 + 4 lg .. + 3) is the same in A and B.  The tile walk,
+// masking (rows past a span's device length are zeroed before use) and the partial format are those
+// of attn_decode_kernel, so attn_merge_kernel combines the splits.
+constexpr int kMT = 32;                 // keys per MFMA tile
+constexpr int kMVRow = kMT + 8;         // LDS row of V^T (bf16, 16 bytes of padding)
+
+template <int GRP>
+__global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
+    const float *__restrict__ q, int64_t ldq, SpanArgs sp, const float *__restrict__ bias, int64_t bias_hstride,
+    int bias_span, float *__restrict__ out, float *__restrict__ part, int H, int G, float scale, int64_t n_tot,
+    int64_t kps, int n_splits) {
+    constexpr int D = 128;
+    constexpr int SLOT = D + 2;
+    static_assert(GRP <= 16, "heads per KV group must fit the 16 MFMA columns");
+    __shared__ float red[kWaves][GRP][SLOT];
+    __shared__ __align__(16) uint16_t vt[kWaves][D * kMVRow];
+
+    const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint16_t *vw = vt[wave];
+
+    const int64_t k0 = (int64_t)split * kps;
+    const int64_t k1 = min(n_tot, k0 + kps);
+    int lo[4], hi[4], eff[4];
+    {
+        int64_t base = 0;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int64_t len = s < sp.n ? sp.len[s] : 0;
+            lo[s] = (int)(max(k0, base) - base);
+            hi[s] = (int)(max(min(k1, base + len) - base, (int64_t)lo[s]));
+            base += len;
+        }
+    }
+    auto first_in = [&](int s0) -> int2 {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            if (s >= s0 && lo[s] + wave * kMT < hi[s]) return make_int2(s, lo[s] + wave * kMT);
+        return make_int2(4, 0);
+    };
+    auto next = [&](int2 c) -> int2 {
+        if (c.y + kWaves * kMT < pick4(c.x, hi[0], hi[1], hi[2], hi[3])) return make_int2(c.x, c.y + kWaves * kMT);
+        return first_in(c.x + 1);
+    };
+
+    // tile registers: K as the A operand (2 x 16 keys x 4 dim chunks), V rows as loaded
+    uint4 kr[2][4], vr[4][2];
+    auto fetch = [&](int2 c) {
+        const int s = c.x;
+        const uint16_t *kb = static_cast<const uint16_t *>(pick4(s, sp.k[0], sp.k[1], sp.k[2], sp.k[3]));
+        const uint16_t *vb = static_cast<const uint16_t *>(pick4(s, sp.v[0], sp.v[1], sp.v[2], sp.v[3]));
+        const int64_t o = (int64_t)b * pick4(s, sp.bstride[0], sp.bstride[1], sp.bstride[2], sp.bstride[3]) +
+                          (int64_t)g * pick4(s, sp.gstride[0], sp.gstride[1], sp.gstride[2], sp.gstride[3]);
+        const int last = pick4(s, hi[0], hi[1], hi[2], hi[3]) - 1;   // rows past it re-read it (masked)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            const int64_t row = min(c.y + kt * 16 + l16, last);
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc)
+                kr[kt][kc] = *reinterpret_cast<const uint4 *>(kb + o + row * D + kc * 32 + lg * 8);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ci = lane + 64 * i, rp = ci & 15, cc = ci >> 4;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int64_t row = min(c.y + 2 * rp + h2, last);
+                vr[i][h2] = *reinterpret_cast<const uint4 *>(vb + o + row * D + cc * 8);
+            }
+        }
+    };
+
+    int2 cur = first_in(0);
+    if (cur.x < 4) fetch(cur);
+
+    // Q^T fragments of the group's heads: column l16 = head, dims 32 kc + 8 lg .. + 7, bf16 hi + lo
+    bf16x8_t qh[4], ql[4];
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+        float e[8];
+        if (l16 < GRP) {
+            const float *qp = q + (int64_t)b * ldq + ((int64_t)g * GRP + l16) * D + kc * 32 + lg * 8;
+            const float4 a0 = reinterpret_cast<const float4 *>(qp)[0], a1 = reinterpret_cast<const float4 *>(qp)[1];
+            e[0] = a0.x; e[1] = a0.y; e[2] = a0.z; e[3] = a0.w; e[4] = a1.x; e[5] = a1.y; e[6] = a1.z; e[7] = a1.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) e[j] = 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t hb = float_to_bf16_bits(e[j]);
+            qh[kc][j] = __builtin_bit_cast(__bf16, (uint16_t)hb);
+            ql[kc][j] = __builtin_bit_cast(__bf16, (uint16_t)float_to_bf16_bits(e[j] - bf16_bits_to_float(hb)));
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        int64_t e = s < sp.n ? sp.len[s] : 0;
+        if (s < sp.n && sp.dyn_len[s] != nullptr) e = min(e, (int64_t)*sp.dyn_len[s]);
+        eff[s] = (int)min((int64_t)hi[s], max(e, (int64_t)0));
+    }
+
+    float m = kNegBig, lsum = 0.0f;
+    f32x4_t o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const float *bh = (bias != nullptr && l16 < GRP) ? bias + ((int64_t)g * GRP + l16) * bias_hstride : nullptr;
+
+    while (cur.x < 4) {
+        const int s = cur.x;
+        const int e = pick4(s, eff[0], eff[1], eff[2], eff[3]);
+        // S^T = K Q^T
+        f32x4_t sc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            sc[kt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc) {
+                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, kr[kt][kc]);
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qh[kc], sc[kt], 0, 0, 0);
+                sc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ql[kc], sc[kt], 0, 0, 0);
+            }
+        }
+        // V^T of the tile into the wave's LDS copy; rows past the effective length become zeros
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ci = lane + 64 * i, rp = ci & 15, cc = ci >> 4;
+            const bool v0 = cur.y + 2 * rp < e, v1 = cur.y + 2 * rp + 1 < e;
+            const uint32_t a0[4] = {vr[i][0].x, vr[i][0].y, vr[i][0].z, vr[i][0].w};
+            const uint32_t a1[4] = {vr[i][1].x, vr[i][1].y, vr[i][1].z, vr[i][1].w};
+#pragma unroll
+            for (int q2 = 0; q2 < 4; ++q2) {
+                const uint32_t x0 = v0 ? a0[q2] : 0u, x1 = v1 ? a1[q2] : 0u;
+                *reinterpret_cast<uint32_t *>(vw + (cc * 8 + 2 * q2) * kMVRow + 2 * rp) = (x0 & 0xFFFFu) | (x1 << 16);
+                *reinterpret_cast<uint32_t *>(vw + (cc * 8 + 2 * q2 + 1) * kMVRow + 2 * rp) =
+                    (x0 >> 16) | (x1 & 0xFFFF0000u);
+            }
+        }
+        // online softmax of head l16 over the tile's 32 keys (keys kt * 16 + 4 lg + i of this lane)
+        float v[8];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kk = cur.y + kt * 16 + lg * 4 + i;
+                float t = sc[kt][i] * scale;
+                if (bh != nullptr && s == bias_span && kk < e) t += bh[kk];
+                v[kt * 4 + i] = kk < e ? t : -INFINITY;
+            }
+        float mt = v[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) mt = fmaxf(mt, v[i]);
+        mt = xor32_max(xor16_max(mt));
+        const float mn = fmaxf(m, mt);
+        const float corr = __expf(m - mn);
+        m = mn;
+        bf16x8_t ph, pl;
+        float ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float p = __expf(v[i] - mn);
+            ps += p;
+            const uint32_t pb = float_to_bf16_bits(p);
+            ph[i] = __builtin_bit_cast(__bf16, (uint16_t)pb);
+            pl[i] = __builtin_bit_cast(__bf16, (uint16_t)float_to_bf16_bits(p - bf16_bits_to_float(pb)));
+        }
+        lsum = lsum * corr + ps;
+        if (__ballot(corr != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) o[dt] *= corr;
+        }
+        const int2 nx = next(cur);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's V^T stores before its reads
+        // O^T += V^T P^T
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const uint16_t *vrow = vw + (dt * 16 + l16) * kMVRow + lg * 4;
+            const uint2 x0 = *reinterpret_cast<const uint2 *>(vrow);
+            const uint2 x1 = *reinterpret_cast<const uint2 *>(vrow + 16);
+            const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(x0.x, x0.y, x1.x, x1.y));
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, o[dt], 0, 0, 0);
+        }
+        if (nx.x < 4) fetch(nx);
+        cur = nx;
+    }
+
+    // wave state -> LDS: lane (lg, head l16) holds dims dt * 16 + 4 lg + i
+    const float L = xor32_sum(xor16_sum(lsum));
+    if (l16 < GRP) {
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave][l16][dt * 16 + lg * 4 + i] = o[dt][i];
+        if (lg == 0) {
+            red[wave][l16][D] = m;
+            red[wave][l16][D + 1] = L;
+        }
+    }
+    __syncthreads();
+
+    const int64_t pair = (int64_t)b * G + g;
+    for (int t = threadIdx.x; t < GRP * D; t += 64 * kWaves) {
+        const int hh = t / D, d = t - hh * D;
+        float M = kNegBig;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red[w][hh][D]);
+        float Ls = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float c = __expf(red[w][hh][D] - M);
+            Ls = fmaf(c, red[w][hh][D + 1], Ls);
+            A = fmaf(c, red[w][hh][d], A);
+        }
+        if (n_splits == 1) {
+            out[((int64_t)b * H + (int64_t)g * GRP + hh) * D + d] = A / Ls;
+        } else {
+            float *pp = part + ((pair * n_splits + split) * GRP + hh) * SLOT;
+            pp[d] = A;
+            if (d == 0) {
+                pp[D] = M;
+                pp[D + 1] = Ls;
+            }
+        }
+    }
+}
+
 // One workgroup of D threads per (b, h): out = sum_s e^{m_s - M} acc_s / sum_s e^{m_s - M} l_s.
 // Every load is issued before the one barrier: thread d requests acc_s[d] of all n_splits splits, and
 // the first wave also (m_s, l_s) of split s = lane; that wave turns them into the split weights in
@@ -373,6 +613,18 @@ int choose_splits(int64_t B, int64_t G, int64_t n_tot, int64_t *kps) {
     want = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(want, cap), kMaxSplits));
     int64_t k = (n_tot + want - 1) / want;
     k = (k + 15) / 16 * 16;
+    *kps = k;
+    return (int)((n_tot + k - 1) / k);
+}
+
+// Splits of the MFMA kernel: the same target, 32-key tiles, at least one tile per wave.
+int choose_splits_mfma(int64_t B, int64_t G, int64_t n_tot, int64_t *kps) {
+    const int64_t pairs = B * G;
+    int64_t want = (kTargetWaves / kWaves + pairs - 1) / pairs;
+    const int64_t cap = (n_tot + kWaves * kMT - 1) / (kWaves * kMT);
+    want = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(want, cap), kMaxSplits));
+    int64_t k = (n_tot + want - 1) / want;
+    k = (k + kMT - 1) / kMT * kMT;
     *kps = k;
     return (int)((n_tot + k - 1) / k);
 }
@@ -458,6 +710,40 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
     }
     if (n_tot <= 0) return VGX_E_SIZE;
     if (n_tot > 0x3FFFFFFF) return VGX_E_LIMIT;
+    const int grp = (int)(H / G);
+    hipStream_t st = (hipStream_t)stream;
+    const bool mfma = kv_dtype == VGX_BF16 && D == 128 && causal_base < 0 &&
+                      (grp == 1 || grp == 2 || grp == 4 || grp == 6 || grp == 8) &&
+                      ((uintptr_t)q & 15) == 0 && ldq % 4 == 0;
+    if (mfma) {
+        int64_t kps = 0;
+        const int ns = choose_splits_mfma(B, G, n_tot, &kps);   // never more splits than the VALU path
+        float *part = nullptr;
+        if (ns > 1) {
+            if (!workspace || workspace_bytes < partial_bytes(B, H, D, ns)) return VGX_E_ARENA;
+            if ((uintptr_t)workspace % 16) return VGX_E_ALIGN;
+            part = static_cast<float *>(workspace);
+        }
+        const dim3 grid((unsigned)ns, (unsigned)G, (unsigned)B);
+#define VGX_AM(GRPV)                                                                                         \
+    hipLaunchKernelGGL(attn_decode_mfma_kernel<GRPV>, grid, dim3(64 * kWaves), 0, st, q, ldq, sp, bias, bias_hstride, \
+                       bias_span, out, part, (int)H, (int)G, scale, n_tot, kps, ns)
+        switch (grp) {
+            case 1: VGX_AM(1); break;
+            case 2: VGX_AM(2); break;
+            case 4: VGX_AM(4); break;
+            case 6: VGX_AM(6); break;
+            default: VGX_AM(8); break;
+        }
+#undef VGX_AM
+        VGX_CHECK_LAUNCH();
+        if (ns > 1) {
+            hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * H)), dim3((unsigned)D), 0, st, part, out,
+                               (int)H, (int)G, (int)D, ns);
+            VGX_CHECK_LAUNCH();
+        }
+        return VGX_OK;
+    }
     int64_t kps = 0;
     const int ns = choose_splits(B, G, n_tot, &kps);
     float *part = nullptr;
@@ -466,8 +752,6 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
         if ((uintptr_t)workspace % 16) return VGX_E_ALIGN;
         part = static_cast<float *>(workspace);
     }
-    const int grp = (int)(H / G);
-    hipStream_t st = (hipStream_t)stream;
     dim3 grid((unsigned)ns, (unsigned)G, (unsigned)B);
     bool ok = kv_dtype == VGX_F32
                   ? dispatch_grp<VGX_F32>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out,
