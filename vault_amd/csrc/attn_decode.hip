@@ -479,6 +479,9 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
                     (x0 >> 16) | (x1 & 0xFFFF0000u);
             }
         }
+        // K and V of this tile are consumed: request the next tile now, behind the softmax and P V
+        const int2 nx = next(cur);
+        if (nx.x < 4) fetch(nx);
         // online softmax of head l16 over the tile's 32 keys (keys kt * 16 + 4 lg + i of this lane)
         float v[8];
 #pragma unroll
@@ -512,7 +515,6 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) o[dt] *= corr;
         }
-        const int2 nx = next(cur);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's V^T stores before its reads
         // O^T += V^T P^T
 #pragma unroll
@@ -524,7 +526,6 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph, o[dt], 0, 0, 0);
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, o[dt], 0, 0, 0);
         }
-        if (nx.x < 4) fetch(nx);
         cur = nx;
     }
 
