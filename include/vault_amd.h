@@ -161,9 +161,11 @@ typedef struct {
     const int32_t *dyn_len;
 } vgx_kv_span;
 
-/* Workspace bytes vgx_attn_decode needs for these sizes (0 when one split suffices): the per-split
- * softmax partials (m, l, acc) that a second, merge launch combines.  16-byte aligned.  Calls sharing
- * one workspace must not overlap in time. */
+/* Workspace bytes vgx_attn_decode needs for these sizes (0 when one split suffices): one int32 ticket
+ * per (batch entry, kv group), then the per-split softmax partials (m, l, acc) that the workgroup
+ * finishing a pair last combines.  256-byte aligned.  The workspace must be zero-filled before its
+ * first use and written by nothing else: every call leaves the tickets at zero (so a captured graph
+ * needs no memset).  Calls sharing one workspace must not overlap in time. */
 int64_t vgx_attn_decode_workspace_bytes(int64_t B, int64_t H, int64_t G, int64_t D, int64_t n_keys);
 
 /* Decode attention: out[b, h, :] = softmax_j(q[b,h].k_j * scale + bias[h, j]) v_j over the keys of

@@ -57,6 +57,41 @@ def test_decode_batched_config3(dev, dtype):
     assert np.abs(out - ref).max() <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B", [16, 64])
+def test_decode_split_tickets_reset_between_calls(dev, dtype, B):
+    """Few splits per (b, g) (batch 16 and 64): the last workgroup of a pair merges its splits and puts
+    the pair's ticket back to zero.  Five calls on one workspace (and a graph replayed three times)
+    give the same bits and match the oracle; the ticket words are zero afterwards."""
+    rng = np.random.default_rng(B)
+    H, G, D = 12, 2, 128
+    lens = [512, 1024, 1024, 1024]
+    sp = _spans(rng, B, G, D, lens, dtype, dev)
+    q = torch.from_numpy(rng.standard_normal((B, H, D)).astype(np.float32)).to(dev)
+    ws = ops.Workspace(dev)
+    outs = [ops.attn_decode(q, sp, ws=ws).clone() for _ in range(5)]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    ref = oatt.decode(q.cpu().numpy(), _np(sp))
+    assert np.abs(outs[0].cpu().numpy() - ref).max() <= TOL[dtype]
+    out = torch.empty_like(q)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.attn_decode(q, sp, out=out, ws=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.attn_decode(q, sp, out=out, ws=ws)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, outs[0])
+    assert int(ws.buf[:B * G * 4].view(torch.int32).abs().sum()) == 0
+
+
 @pytest.mark.parametrize("grp,D", [(1, 64), (2, 128), (4, 64), (6, 128), (8, 128)])
 def test_decode_group_and_dim(dev, grp, D):
     rng = np.random.default_rng(grp * D)

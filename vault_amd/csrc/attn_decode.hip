@@ -11,9 +11,10 @@
 // so one load instruction fetches four whole key rows.  q.k partials are reduced over the 16 lanes
 // with DPP; every DPP row keeps its own online-softmax state (m, l, acc).  The states are merged
 // across DPP rows with lane shuffles and across the waves of the workgroup through LDS; with more
-// than one split, each split writes (m, l, acc) partials to the workspace and attn_merge_kernel
-// combines them (a second launch: merging inside the first kernel would need a device-scope
-// release fence per workgroup, an L2 write-back that measured 2x slower at batch 64).
+// than one split, each split writes (m, l, acc) partials to the workspace; up to 8 splits are
+// combined by the workgroup that finishes a (b, g) pair last (ticket_merge: agent-scope atomic
+// stores and loads of the partials instead of a release fence, whose write-back of the whole L2
+// measured 2x slower), more by attn_merge_kernel, a second launch spread over B * H workgroups.
 #include "common.h"
 
 using namespace vgx;
@@ -39,6 +40,76 @@ struct SpanArgs {
     const int32_t *dyn_len[4];
     int n;
 };
+
+// Merging the splits of a (b, g) pair without a second launch.  Every workgroup writes its partials
+// with agent-scope atomic stores (written through to the device-coherent level, no L2 write-back of
+// the whole cache as a release fence would need), waits for them to complete, then takes a ticket
+// from the pair's counter; the workgroup that draws the last ticket reads every split's partials with
+// agent-scope atomic loads, combines them in split order (deterministic) and resets the counter to
+// zero for the next launch (no memset, so a captured graph replays it).
+constexpr int kTicketLds = 2 * 8 * kMaxSplits + 8;    // floats of LDS scratch for GRP <= 8
+
+template <int GRP, int D>
+__device__ __forceinline__ void store_partial(float *pp, int d, float A, float M, float L) {
+    __hip_atomic_store(pp + d, A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == 0) {
+        __hip_atomic_store(pp + D, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pp + D + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int GRP, int D>
+__device__ __forceinline__ void ticket_merge(const float *__restrict__ part_pair, int *__restrict__ cnt, int n_splits,
+                                             float *__restrict__ outp, float *sc, int *flag) {
+    constexpr int SLOT = D + 2;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's partial stores have completed
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == n_splits - 1;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    float *wm = sc, *wl = sc + GRP * kMaxSplits, *inv = sc + 2 * GRP * kMaxSplits;
+    for (int i = tid; i < GRP * n_splits; i += nt) {
+        const int hh = i / n_splits, sp = i - hh * n_splits;
+        const float *pp = part_pair + ((int64_t)sp * GRP + hh) * SLOT;
+        wm[hh * kMaxSplits + sp] = __hip_atomic_load(pp + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wl[hh * kMaxSplits + sp] = __hip_atomic_load(pp + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (tid < GRP) {
+        float M = kNegBig;
+        for (int sp = 0; sp < n_splits; ++sp) M = fmaxf(M, wm[tid * kMaxSplits + sp]);
+        float L = 0.0f;
+        for (int sp = 0; sp < n_splits; ++sp) {
+            const float w = __expf(wm[tid * kMaxSplits + sp] - M);
+            wm[tid * kMaxSplits + sp] = w;
+            L = fmaf(w, wl[tid * kMaxSplits + sp], L);
+        }
+        inv[tid] = 1.0f / L;
+    }
+    __syncthreads();
+    for (int t = tid; t < GRP * D; t += nt) {
+        const int hh = t / D, d = t - hh * D;
+        float A = 0.0f;
+        for (int s0 = 0; s0 < n_splits; s0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int sp = min(s0 + u, n_splits - 1);
+                v[u] = __hip_atomic_load(part_pair + ((int64_t)sp * GRP + hh) * SLOT + d, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (s0 + u < n_splits) A = fmaf(wm[hh * kMaxSplits + s0 + u], v[u], A);
+        }
+        outp[(int64_t)hh * D + d] = A * inv[hh];
+    }
+    if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // One lane's DPL elements of a key row as raw words (F32: DPL words, BF16: DPL / 2 words), loaded
 // with 128-bit (or 64-bit) loads and converted to fp32 at use.
@@ -96,7 +167,7 @@ __device__ __forceinline__ T pick4(int s, T a0, T a1, T a2, T a3) {
 template <int KV, int GRP, int DPL>
 __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
     const float *__restrict__ q, int64_t ldq, SpanArgs sp, const float *__restrict__ bias, int64_t bias_hstride,
-    int bias_span, float *__restrict__ out, float *__restrict__ part, int H, int G,
+    int bias_span, float *__restrict__ out, float *__restrict__ part, int *__restrict__ cnt, int H, int G,
     float scale, int64_t n_tot, int64_t kps, int n_splits, int64_t causal_base) {
     constexpr int D = DPL * 16;
     constexpr int SLOT = D + 2;
@@ -318,16 +389,13 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
             L = fmaf(c, red[w][hh][D + 1], L);
             A = fmaf(c, red[w][hh][d], A);
         }
-        if (n_splits == 1) {
-            out[((int64_t)b * H + (int64_t)g * GRP + hh) * D + d] = A / L;
-        } else {
-            float *pp = part + ((pair * n_splits + split) * GRP + hh) * SLOT;
-            pp[d] = A;
-            if (d == 0) {
-                pp[D] = M;
-                pp[D + 1] = L;
-            }
-        }
+        if (n_splits == 1) out[((int64_t)b * H + (int64_t)g * GRP + hh) * D + d] = A / L;
+        else store_partial<GRP, D>(part + ((pair * n_splits + split) * GRP + hh) * SLOT, d, A, M, L);
+    }
+    if (n_splits > 1 && cnt != nullptr) {
+        __shared__ int last;
+        ticket_merge<GRP, D>(part + pair * n_splits * GRP * SLOT, cnt + pair, n_splits,
+                             out + ((int64_t)b * H + (int64_t)g * GRP) * D, &red[0][0][0], &last);
     }
 }
 
@@ -342,15 +410,15 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
 // steps for the max and the final sum), exactly as in the prefill kernel.  The K-slot assignment of
 // the second product (keys 4 lg .. + 3 and 16 + 4 lg .. + 3) is the same in A and B.  The tile walk,
 // masking (rows past a span's device length are zeroed before use) and the partial format are those
-// of attn_decode_kernel, so attn_merge_kernel combines the splits.
+// of attn_decode_kernel, and the splits are combined the same way.
 constexpr int kMT = 32;                 // keys per MFMA tile
 constexpr int kMVRow = kMT + 8;         // LDS row of V^T (bf16, 16 bytes of padding)
 
 template <int GRP>
 __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
     const float *__restrict__ q, int64_t ldq, SpanArgs sp, const float *__restrict__ bias, int64_t bias_hstride,
-    int bias_span, float *__restrict__ out, float *__restrict__ part, int H, int G, float scale, int64_t n_tot,
-    int64_t kps, int n_splits) {
+    int bias_span, float *__restrict__ out, float *__restrict__ part, int *__restrict__ cnt, int H, int G, float scale,
+    int64_t n_tot, int64_t kps, int n_splits) {
     constexpr int D = 128;
     constexpr int SLOT = D + 2;
     static_assert(GRP <= 16, "heads per KV group must fit the 16 MFMA columns");
@@ -556,16 +624,13 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
             Ls = fmaf(c, red[w][hh][D + 1], Ls);
             A = fmaf(c, red[w][hh][d], A);
         }
-        if (n_splits == 1) {
-            out[((int64_t)b * H + (int64_t)g * GRP + hh) * D + d] = A / Ls;
-        } else {
-            float *pp = part + ((pair * n_splits + split) * GRP + hh) * SLOT;
-            pp[d] = A;
-            if (d == 0) {
-                pp[D] = M;
-                pp[D + 1] = Ls;
-            }
-        }
+        if (n_splits == 1) out[((int64_t)b * H + (int64_t)g * GRP + hh) * D + d] = A / Ls;
+        else store_partial<GRP, D>(part + ((pair * n_splits + split) * GRP + hh) * SLOT, d, A, M, Ls);
+    }
+    if (n_splits > 1 && cnt != nullptr) {
+        __shared__ int last;
+        ticket_merge<GRP, D>(part + pair * n_splits * GRP * SLOT, cnt + pair, n_splits,
+                             out + ((int64_t)b * H + (int64_t)g * GRP) * D, &red[0][0][0], &last);
     }
 }
 
@@ -634,35 +699,42 @@ int64_t partial_bytes(int64_t B, int64_t H, int64_t D, int ns) {
     return B * H * (int64_t)ns * (D + 2) * (int64_t)sizeof(float);
 }
 
+// Workspace: the split tickets (one int32 per (b, g), kept at zero between launches) first, then the
+// partials.  Up to kTicketMaxSplits splits are merged by the last workgroup of a pair; with more, the
+// merge work of a pair is too much for one workgroup (56 splits at batch 1: 15 vs 10 us per layer) and
+// attn_merge_kernel spreads it over B * H workgroups.
+int64_t ticket_bytes(int64_t B, int64_t G) { return (B * G * 4 + 255) / 256 * 256; }
+constexpr int kTicketMaxSplits = 8;
+
 template <int KV, int GRP, int DPL>
 void launch_decode(dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp, const float *bias,
-                   int64_t bhs, int bspan, float *out, float *part, int H, int G, float scale, int64_t n_tot,
-                   int64_t kps, int ns, int64_t cb) {
+                   int64_t bhs, int bspan, float *out, float *part, int *cnt, int H, int G, float scale,
+                   int64_t n_tot, int64_t kps, int ns, int64_t cb) {
     hipLaunchKernelGGL((attn_decode_kernel<KV, GRP, DPL>), grid, dim3(64 * kWaves), 0, st, q, ldq, sp, bias, bhs,
-                       bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
+                       bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
 }
 
 template <int KV, int GRP>
 bool dispatch_dpl(int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp,
-                  const float *bias, int64_t bhs, int bspan, float *out, float *part, int H, int G,
+                  const float *bias, int64_t bhs, int bspan, float *out, float *part, int *cnt, int H, int G,
                   float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb) {
     switch (D) {
-        case 64: launch_decode<KV, GRP, 4>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb); return true;
-        case 128: launch_decode<KV, GRP, 8>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb); return true;
+        case 64: launch_decode<KV, GRP, 4>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb); return true;
+        case 128: launch_decode<KV, GRP, 8>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb); return true;
     }
     return false;
 }
 
 template <int KV>
 bool dispatch_grp(int grp, int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp,
-                  const float *bias, int64_t bhs, int bspan, float *out, float *part, int H, int G,
+                  const float *bias, int64_t bhs, int bspan, float *out, float *part, int *cnt, int H, int G,
                   float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb) {
     switch (grp) {
-        case 1: return dispatch_dpl<KV, 1>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
-        case 2: return dispatch_dpl<KV, 2>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
-        case 4: return dispatch_dpl<KV, 4>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
-        case 6: return dispatch_dpl<KV, 6>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
-        case 8: return dispatch_dpl<KV, 8>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, H, G, scale, n_tot, kps, ns, cb);
+        case 1: return dispatch_dpl<KV, 1>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
+        case 2: return dispatch_dpl<KV, 2>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
+        case 4: return dispatch_dpl<KV, 4>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
+        case 6: return dispatch_dpl<KV, 6>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
+        case 8: return dispatch_dpl<KV, 8>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
     }
     return false;
 }
@@ -676,7 +748,7 @@ int64_t vgx_attn_decode_workspace_bytes(int64_t B, int64_t H, int64_t G, int64_t
     int64_t kps = 0;
     const int ns = choose_splits(B, G, n_keys, &kps);
     if (ns <= 1) return 0;
-    return partial_bytes(B, H, D, ns);
+    return ticket_bytes(B, G) + partial_bytes(B, H, D, ns);
 }
 
 int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span *spans, int n_spans,
@@ -720,15 +792,17 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
         int64_t kps = 0;
         const int ns = choose_splits_mfma(B, G, n_tot, &kps);   // never more splits than the VALU path
         float *part = nullptr;
+        int *cnt = nullptr;
         if (ns > 1) {
-            if (!workspace || workspace_bytes < partial_bytes(B, H, D, ns)) return VGX_E_ARENA;
-            if ((uintptr_t)workspace % 16) return VGX_E_ALIGN;
-            part = static_cast<float *>(workspace);
+            if (!workspace || workspace_bytes < ticket_bytes(B, G) + partial_bytes(B, H, D, ns)) return VGX_E_ARENA;
+            if ((uintptr_t)workspace % 256) return VGX_E_ALIGN;
+            if (ns <= kTicketMaxSplits) cnt = static_cast<int *>(workspace);
+            part = reinterpret_cast<float *>(static_cast<char *>(workspace) + ticket_bytes(B, G));
         }
         const dim3 grid((unsigned)ns, (unsigned)G, (unsigned)B);
 #define VGX_AM(GRPV)                                                                                         \
     hipLaunchKernelGGL(attn_decode_mfma_kernel<GRPV>, grid, dim3(64 * kWaves), 0, st, q, ldq, sp, bias, bias_hstride, \
-                       bias_span, out, part, (int)H, (int)G, scale, n_tot, kps, ns)
+                       bias_span, out, part, cnt, (int)H, (int)G, scale, n_tot, kps, ns)
         switch (grp) {
             case 1: VGX_AM(1); break;
             case 2: VGX_AM(2); break;
@@ -738,7 +812,7 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
         }
 #undef VGX_AM
         VGX_CHECK_LAUNCH();
-        if (ns > 1) {
+        if (ns > 1 && cnt == nullptr) {
             hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * H)), dim3((unsigned)D), 0, st, part, out,
                                (int)H, (int)G, (int)D, ns);
             VGX_CHECK_LAUNCH();
@@ -748,20 +822,22 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
     int64_t kps = 0;
     const int ns = choose_splits(B, G, n_tot, &kps);
     float *part = nullptr;
+    int *cnt = nullptr;
     if (ns > 1) {
-        if (!workspace || workspace_bytes < partial_bytes(B, H, D, ns)) return VGX_E_ARENA;
-        if ((uintptr_t)workspace % 16) return VGX_E_ALIGN;
-        part = static_cast<float *>(workspace);
+        if (!workspace || workspace_bytes < ticket_bytes(B, G) + partial_bytes(B, H, D, ns)) return VGX_E_ARENA;
+        if ((uintptr_t)workspace % 256) return VGX_E_ALIGN;
+        if (ns <= kTicketMaxSplits) cnt = static_cast<int *>(workspace);
+        part = reinterpret_cast<float *>(static_cast<char *>(workspace) + ticket_bytes(B, G));
     }
     dim3 grid((unsigned)ns, (unsigned)G, (unsigned)B);
     bool ok = kv_dtype == VGX_F32
                   ? dispatch_grp<VGX_F32>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out,
-                                          part, (int)H, (int)G, scale, n_tot, kps, ns, causal_base)
+                                          part, cnt, (int)H, (int)G, scale, n_tot, kps, ns, causal_base)
                   : dispatch_grp<VGX_BF16>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out,
-                                           part, (int)H, (int)G, scale, n_tot, kps, ns, causal_base);
+                                           part, cnt, (int)H, (int)G, scale, n_tot, kps, ns, causal_base);
     if (!ok) return VGX_E_LIMIT;
     VGX_CHECK_LAUNCH();
-    if (ns > 1) {
+    if (ns > 1 && cnt == nullptr) {
         hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(B * H)), dim3((unsigned)D), 0, st, part, out, (int)H,
                            (int)G, (int)D, ns);
         VGX_CHECK_LAUNCH();

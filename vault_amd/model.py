@@ -464,7 +464,8 @@ class VAULTv3ForCausalLM:
         the bound of any decode step of this batch size (B * H * 64 splits * (D + 2) floats), and the
         GEMM activation splits for batches that use the MFMA GEMM."""
         cfg = self.cfg
-        self.ws.get(st.batch * cfg.n_heads * 64 * (cfg.head_dim + 2) * 4)
+        self.ws.get((st.batch * cfg.n_kv_heads * 4 + 255) // 256 * 256 +
+                    st.batch * cfg.n_heads * 64 * (cfg.head_dim + 2) * 4)
         if st.batch >= ops.GEMM_MIN_ROWS:
             lib = ops.L.load()
             shapes = [(cfg.d_ff, cfg.d_model, ops.L.EPI_SWIGLU), (cfg.d_model, cfg.d_ff, ops.L.EPI_ACCUM),
