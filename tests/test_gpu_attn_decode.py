@@ -60,9 +60,10 @@ def test_decode_batched_config3(dev, dtype):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B", [16, 64])
 def test_decode_split_tickets_reset_between_calls(dev, dtype, B):
-    """Few splits per (b, g) (batch 16 and 64): the last workgroup of a pair merges its splits and puts
-    the pair's ticket back to zero.  Five calls on one workspace (and a graph replayed three times)
-    give the same bits and match the oracle; the ticket words are zero afterwards."""
+    """Batch 64 (4 splits per (b, g)): the last workgroup of a pair merges its splits and puts the
+    pair's ticket back to zero; batch 16 (16 splits) merges with the second launch.  Five calls on
+    one workspace (and a graph replayed three times) give the same bits and match the oracle; the
+    ticket words are zero afterwards."""
     rng = np.random.default_rng(B)
     H, G, D = 12, 2, 128
     lens = [512, 1024, 1024, 1024]
