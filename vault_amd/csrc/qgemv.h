@@ -555,6 +555,7 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
     else if (a.n_rq >= 2048) VGX_GEMV1(64, 4, 1, 1, true, false);     // gate/up: lane per block
     else if (a.nblk >= 192) VGX_GEMV1(64, 1, 8, 1, true, false);      // down: 8 waves over K (staged: 6.6 vs
                                                                       // 7.0 us with direct activations)
+    else if (a.nblk >= 96 && a.n_rq < 256) VGX_GEMV1(64, 1, 8, 1, true, false);   // few rows: more waves
     else if (a.nblk >= 96) VGX_GEMV1(64, 1, 2, 1, true, false);
     else if (aligned && DT != VGX_F32) VGX_GEMV1(64, 1, 1, 1, false, true);   // small: direct
     else VGX_GEMV1(64, 2, 1, 1, true, false);

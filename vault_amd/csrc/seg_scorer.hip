@@ -57,6 +57,55 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const float *__restrict_
     for (int64_t i = threadIdx.x; i < dim; i += blockDim.x) yr[i] = (xr[i] - mean) * inv * w[i] + b[i];
 }
 
+// Rows of up to 256 x 4 x kLnMaxF4 floats held in registers: every load of the row is issued at once
+// (the loop form above waits for each pass over the row in turn).  One workgroup per row.
+constexpr int kLnMaxF4 = 8;
+
+__global__ __launch_bounds__(256) void layernorm_reg_kernel(const float *__restrict__ x, int64_t ldx,
+                                                             const float *__restrict__ w,
+                                                             const float *__restrict__ b, float *__restrict__ y,
+                                                             int64_t ldy, int dim, float eps) {
+    __shared__ float red[2][4];
+    const float4 *xr = reinterpret_cast<const float4 *>(x + (int64_t)blockIdx.x * ldx);
+    const int n4 = dim / 4;
+    float4 v[kLnMaxF4];
+    float s = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kLnMaxF4; ++u) {
+        const int i = threadIdx.x + u * 256;
+        v[u] = i < n4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < kLnMaxF4; ++u) s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) red[0][threadIdx.x >> 6] = s;
+    __syncthreads();
+    const float mean = (red[0][0] + red[0][1] + red[0][2] + red[0][3]) / (float)dim;
+    float q = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kLnMaxF4; ++u) {
+        if (threadIdx.x + u * 256 < n4) {
+            const float a = v[u].x - mean, c = v[u].y - mean, d = v[u].z - mean, e = v[u].w - mean;
+            q = fmaf(a, a, fmaf(c, c, fmaf(d, d, fmaf(e, e, q))));
+        }
+    }
+    q = wave_sum(q);
+    if ((threadIdx.x & 63) == 0) red[1][threadIdx.x >> 6] = q;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((red[1][0] + red[1][1] + red[1][2] + red[1][3]) / (float)dim + eps);
+    float4 *yr = reinterpret_cast<float4 *>(y + (int64_t)blockIdx.x * ldy);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w), *b4 = reinterpret_cast<const float4 *>(b);
+#pragma unroll
+    for (int u = 0; u < kLnMaxF4; ++u) {
+        const int i = threadIdx.x + u * 256;
+        if (i < n4) {
+            const float4 g = w4[i], o = b4[i];
+            yr[i] = make_float4((v[u].x - mean) * inv * g.x + o.x, (v[u].y - mean) * inv * g.y + o.y,
+                                (v[u].z - mean) * inv * g.z + o.z, (v[u].w - mean) * inv * g.w + o.w);
+        }
+    }
+}
+
 // One wave per token t: raw = gelu(h[t]) . w2 + b2, hab = gelu(h[T + t]) . w2 + b2.
 __global__ __launch_bounds__(64) void score_tail_kernel(const float *__restrict__ h, int64_t ldh,
                                                          const float *__restrict__ w2, const float *__restrict__ b2,
@@ -97,8 +146,14 @@ int vgx_layernorm(const float *x, int64_t ldx, const float *w, const float *b, f
     if (n_rows < 0 || dim <= 0 || ldx < dim || ldy < dim || !(eps > 0.0f)) return VGX_E_SIZE;
     if (n_rows == 0) return VGX_OK;
     if (n_rows > 0x7FFFFFFF) return VGX_E_LIMIT;
-    hipLaunchKernelGGL(layernorm_kernel, dim3((unsigned)n_rows), dim3(256), 0, (hipStream_t)stream, x, ldx, w, b, y,
-                       ldy, dim, eps);
+    const bool reg = dim % 4 == 0 && dim <= 256 * 4 * kLnMaxF4 && ldx % 4 == 0 && ldy % 4 == 0 &&
+                     (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w | (uintptr_t)b) & 15) == 0;
+    if (reg)
+        hipLaunchKernelGGL(layernorm_reg_kernel, dim3((unsigned)n_rows), dim3(256), 0, (hipStream_t)stream, x, ldx, w,
+                           b, y, ldy, (int)dim, eps);
+    else
+        hipLaunchKernelGGL(layernorm_kernel, dim3((unsigned)n_rows), dim3(256), 0, (hipStream_t)stream, x, ldx, w, b,
+                           y, ldy, dim, eps);
     VGX_CHECK_LAUNCH();
     return VGX_OK;
 }

@@ -485,7 +485,8 @@ class VAULTv3ForCausalLM:
         io = st.step_io()
         step, n_cur = io.step, io.step[ops.L.STEP_N_CUR:ops.L.STEP_N_CUR + 1]
         x = ops.embed(w.embed, io.ids, pad_row=0)                              # [B, d]
-        feats = torch.empty(B, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device) \
+        # rows [0, B) receive the scorer features, rows [B, 2B) the habituated ones (one LayerNorm launch)
+        feats = torch.empty(2 * B, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device) \
             if seg_active else None
         ao = torch.empty(B, H, D, dtype=torch.float32, device=self.device)
         hbuf = torch.empty(B, cfg.d_ff, dtype=torch.float32, device=self.device)
@@ -497,7 +498,7 @@ class VAULTv3ForCausalLM:
             xc = None
             if seg_active and li in cfg.seg_layers:
                 j = cfg.seg_layers.index(li)
-                xc = feats[:, j * d:(j + 1) * d]
+                xc = feats[:B, j * d:(j + 1) * d]
                 if not fused:
                     xc.copy_(x)
             if fused:
@@ -563,7 +564,7 @@ class VAULTv3ForCausalLM:
         ci = pos // W
         feats = None
         if seg_active:
-            feats = torch.empty(N, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device)
+            feats = torch.empty(2 * N, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device)
         n_sk = st.n_pin if ci >= 2 else 0
         n_seg = int(st.mem_pos.numel()) if (seg_active and ci >= 2) else 0
         n_prev = W if ci >= 1 else 0
@@ -575,7 +576,7 @@ class VAULTv3ForCausalLM:
         for li, lw in enumerate(w.layers):
             if seg_active and li in cfg.seg_layers:
                 j = cfg.seg_layers.index(li)
-                feats[:, j * d:(j + 1) * d].copy_(x)
+                feats[:N, j * d:(j + 1) * d].copy_(x)
             q, k, v = self._qkv(lw, x, N)
             kc, kr, vc = st.k_cur[li], st.kraw_cur[li], st.v_cur[li]          # [1, G, W, D]
             ks, vs = st.k_sink_raw[li], st.v_sink[li]                          # [1, G, S_cap, D]
@@ -602,17 +603,21 @@ class VAULTv3ForCausalLM:
             ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
         return x, feats
 
-    def _score(self, st: VAULTv3State, feats: torch.Tensor, T: int, c0: int, first: bool,
+    def _score(self, st: VAULTv3State, rows: torch.Tensor, T: int, c0: int, first: bool,
                out_index: Optional[torch.Tensor] = None) -> None:
         """Habituated segment scores of T tokens into sc_cur[c0:c0+T], shifted by the device slot
-        ``out_index`` when given (src/vault_v3_model.py:1224-1247, 2294-2305)."""
+        ``out_index`` when given (src/vault_v3_model.py:1224-1247, 2294-2305).  rows: [2T, fd] with the
+        features in rows[:T]; rows[T:] receive the habituated features, then both halves are
+        LayerNormed in place."""
         sw = self.w.scorer
-        fd = feats.shape[1]
-        rows = torch.empty(2 * T, fd, dtype=torch.float32, device=self.device)
-        ops.ema_habituate(feats, rows[T:], st.seg_feat_ema, first)
-        ops.layernorm(feats, sw.ln_w, sw.ln_b, 1e-5, rows[:T])
-        ops.layernorm(rows[T:], sw.ln_w, sw.ln_b, 1e-5, rows[T:])
-        h1 = ops.qlinear(sw.w1, rows, bias=sw.b1)
+        ops.ema_habituate(rows[:T], rows[T:2 * T], st.seg_feat_ema, first)
+        ops.layernorm(rows[:2 * T], sw.ln_w, sw.ln_b, 1e-5, rows[:2 * T])
+        if T == 1:   # two one-row GEMVs: the one-row kernel splits K over 8 waves for this shape
+            h1 = torch.empty(2, sw.w1.rows, dtype=torch.float32, device=self.device)
+            ops.qlinear(sw.w1, rows[0:1], bias=sw.b1, out=h1[0:1])
+            ops.qlinear(sw.w1, rows[1:2], bias=sw.b1, out=h1[1:2])
+        else:
+            h1 = ops.qlinear(sw.w1, rows[:2 * T], bias=sw.b1)
         ops.seg_score_tail(h1, sw.w2, sw.b2, T, first, st.sc_cur[c0:c0 + T], out_index=out_index)
 
     def _logits(self, h: torch.Tensor) -> torch.Tensor:
