@@ -344,20 +344,27 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
         }
     }
 
-    // Merge the online-softmax states of the four DPP rows of the wave.
+    // Merge the online-softmax states of the four DPP rows of the wave: rows r and r ^ 1, then the two
+    // halves, with the VALU lane swaps (each gives a lane its own and its partner's value, the lower
+    // row's first in every lane of a row pair, so both rows of a pair compute the same merge).
 #pragma unroll
-    for (int sh = 16; sh <= 32; sh <<= 1) {
+    for (int step = 0; step < 2; ++step) {
+        auto pair = [&](float x) {
+            const auto r = step == 0
+                               ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
+                               : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+            return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+        };
 #pragma unroll
         for (int hh = 0; hh < GRP; ++hh) {
-            const float mo = __shfl_xor(m[hh], sh, kWave);
-            const float lo = __shfl_xor(l[hh], sh, kWave);
-            const float mn = fmaxf(m[hh], mo);
-            const float c1 = __expf(m[hh] - mn), c2 = __expf(mo - mn);
-            l[hh] = l[hh] * c1 + lo * c2;
+            const float2 mp = pair(m[hh]), lp = pair(l[hh]);
+            const float mn = fmaxf(mp.x, mp.y);
+            const float c1 = __expf(mp.x - mn), c2 = __expf(mp.y - mn);
+            l[hh] = fmaf(lp.x, c1, lp.y * c2);
 #pragma unroll
             for (int d = 0; d < DPL; ++d) {
-                const float ao = __shfl_xor(acc[hh][d], sh, kWave);
-                acc[hh][d] = acc[hh][d] * c1 + ao * c2;
+                const float2 ap = pair(acc[hh][d]);
+                acc[hh][d] = fmaf(ap.x, c1, ap.y * c2);
             }
             m[hh] = mn;
         }
