@@ -47,7 +47,7 @@ struct SpanArgs {
 // from the pair's counter; the workgroup that draws the last ticket reads every split's partials with
 // agent-scope atomic loads, combines them in split order (deterministic) and resets the counter to
 // zero for the next launch (no memset, so a captured graph replays it).
-constexpr int kTicketLds = 2 * 8 * kMaxSplits + 8;    // floats of LDS scratch for GRP <= 8
+constexpr int kTicketMaxSplits = 32;                // splits merged by the last workgroup of a pair
 
 template <int GRP, int D>
 __device__ __forceinline__ void store_partial(float *pp, int d, float A, float M, float L) {
@@ -91,21 +91,18 @@ __device__ __forceinline__ void ticket_merge(const float *__restrict__ part_pair
         inv[tid] = 1.0f / L;
     }
     __syncthreads();
+    // every split of an output requested at once (n_splits <= kTicketMaxSplits)
     for (int t = tid; t < GRP * D; t += nt) {
         const int hh = t / D, d = t - hh * D;
+        float v[kTicketMaxSplits];
+#pragma unroll
+        for (int u = 0; u < kTicketMaxSplits; ++u)
+            v[u] = __hip_atomic_load(part_pair + ((int64_t)min(u, n_splits - 1) * GRP + hh) * SLOT + d,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         float A = 0.0f;
-        for (int s0 = 0; s0 < n_splits; s0 += 8) {
-            float v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int sp = min(s0 + u, n_splits - 1);
-                v[u] = __hip_atomic_load(part_pair + ((int64_t)sp * GRP + hh) * SLOT + d, __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (s0 + u < n_splits) A = fmaf(wm[hh * kMaxSplits + s0 + u], v[u], A);
-        }
+        for (int u = 0; u < kTicketMaxSplits; ++u)
+            if (u < n_splits) A = fmaf(wm[hh * kMaxSplits + u], v[u], A);
         outp[(int64_t)hh * D + d] = A * inv[hh];
     }
     if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -164,15 +161,15 @@ __device__ __forceinline__ T pick4(int s, T a0, T a1, T a2, T a3) {
 // issued before the query and the device-side lengths arrive; keys at or beyond a span's effective
 // length (device length, causal limit) are masked, and no row beyond a span's capacity is read.
 // With PIPE the next tile's loads are issued before the current tile is reduced.
-template <int KV, int GRP, int DPL>
-__global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
+template <int KV, int GRP, int DPL, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     const float *__restrict__ q, int64_t ldq, SpanArgs sp, const float *__restrict__ bias, int64_t bias_hstride,
     int bias_span, float *__restrict__ out, float *__restrict__ part, int *__restrict__ cnt, int H, int G,
     float scale, int64_t n_tot, int64_t kps, int n_splits, int64_t causal_base) {
     constexpr int D = DPL * 16;
     constexpr int SLOT = D + 2;
     constexpr bool PIPE = KV == VGX_BF16;
-    __shared__ float red[kWaves][GRP][SLOT];
+    __shared__ float red[NW][GRP][SLOT];
 
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, l16 = lane & 15, row = lane >> 4;
@@ -200,7 +197,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
         return make_int2(4, 0);
     };
     auto next = [&](int2 c) -> int2 {
-        if (c.y + kWaves * 16 < pick4(c.x, hi[0], hi[1], hi[2], hi[3])) return make_int2(c.x, c.y + kWaves * 16);
+        if (c.y + NW * 16 < pick4(c.x, hi[0], hi[1], hi[2], hi[3])) return make_int2(c.x, c.y + NW * 16);
         return first_in(c.x + 1);
     };
     auto fetch = [&](KeyTile<KV, DPL> &t, int2 c) {
@@ -384,14 +381,14 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_kernel(
 
     // Merge the waves: thread t owns (head t / D, dim t % D).
     const int64_t pair = (int64_t)b * G + g;
-    for (int t = threadIdx.x; t < GRP * D; t += 64 * kWaves) {
+    for (int t = threadIdx.x; t < GRP * D; t += 64 * NW) {
         const int hh = t / D, d = t - hh * D;
         float M = kNegBig;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red[w][hh][D]);
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, red[w][hh][D]);
         float L = 0.0f, A = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const float c = __expf(red[w][hh][D] - M);
             L = fmaf(c, red[w][hh][D + 1], L);
             A = fmaf(c, red[w][hh][d], A);
@@ -678,11 +675,11 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict
     out[((int64_t)b * H + h) * D + d] = a * inv_l;
 }
 
-int choose_splits(int64_t B, int64_t G, int64_t n_tot, int64_t *kps) {
+int choose_splits(int64_t B, int64_t G, int64_t n_tot, int64_t *kps, int nw = kWaves) {
     // About kTargetWaves waves in flight, at least kMinKeysPerWave keys per wave, at most kMaxSplits.
     const int64_t pairs = B * G;
-    int64_t want = (kTargetWaves / kWaves + pairs - 1) / pairs;
-    const int64_t cap = (n_tot + kWaves * kMinKeysPerWave - 1) / (kWaves * kMinKeysPerWave);
+    int64_t want = (kTargetWaves / nw + pairs - 1) / pairs;
+    const int64_t cap = (n_tot + nw * kMinKeysPerWave - 1) / (nw * kMinKeysPerWave);
     want = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(want, cap), kMaxSplits));
     int64_t k = (n_tot + want - 1) / want;
     k = (k + 15) / 16 * 16;
@@ -708,26 +705,26 @@ int64_t partial_bytes(int64_t B, int64_t H, int64_t D, int ns) {
 
 // Workspace: the split tickets (one int32 per (b, g), kept at zero between launches) first, then the
 // partials.  Up to kTicketMaxSplits splits are merged by the last workgroup of a pair; with more, the
-// merge work of a pair is too much for one workgroup (56 splits at batch 1: 15 vs 10 us per layer) and
-// attn_merge_kernel spreads it over B * H workgroups.
+// merge work of a pair is too much for one workgroup and attn_merge_kernel spreads it over B * H
+// workgroups.
 int64_t ticket_bytes(int64_t B, int64_t G) { return (B * G * 4 + 255) / 256 * 256; }
-constexpr int kTicketMaxSplits = 8;
 
 template <int KV, int GRP, int DPL>
 void launch_decode(dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp, const float *bias,
                    int64_t bhs, int bspan, float *out, float *part, int *cnt, int H, int G, float scale,
-                   int64_t n_tot, int64_t kps, int ns, int64_t cb) {
-    hipLaunchKernelGGL((attn_decode_kernel<KV, GRP, DPL>), grid, dim3(64 * kWaves), 0, st, q, ldq, sp, bias, bhs,
-                       bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
+                   int64_t n_tot, int64_t kps, int ns, int64_t cb, int nw) {
+    (void)nw;
+    hipLaunchKernelGGL((attn_decode_kernel<KV, GRP, DPL, kWaves>), grid, dim3(64 * kWaves), 0, st, q, ldq, sp, bias,
+                       bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
 }
 
 template <int KV, int GRP>
 bool dispatch_dpl(int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp,
                   const float *bias, int64_t bhs, int bspan, float *out, float *part, int *cnt, int H, int G,
-                  float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb) {
+                  float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb, int nw) {
     switch (D) {
-        case 64: launch_decode<KV, GRP, 4>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb); return true;
-        case 128: launch_decode<KV, GRP, 8>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb); return true;
+        case 64: launch_decode<KV, GRP, 4>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw); return true;
+        case 128: launch_decode<KV, GRP, 8>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw); return true;
     }
     return false;
 }
@@ -735,13 +732,13 @@ bool dispatch_dpl(int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq,
 template <int KV>
 bool dispatch_grp(int grp, int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp,
                   const float *bias, int64_t bhs, int bspan, float *out, float *part, int *cnt, int H, int G,
-                  float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb) {
+                  float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb, int nw) {
     switch (grp) {
-        case 1: return dispatch_dpl<KV, 1>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
-        case 2: return dispatch_dpl<KV, 2>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
-        case 4: return dispatch_dpl<KV, 4>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
-        case 6: return dispatch_dpl<KV, 6>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
-        case 8: return dispatch_dpl<KV, 8>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
+        case 1: return dispatch_dpl<KV, 1>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw);
+        case 2: return dispatch_dpl<KV, 2>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw);
+        case 4: return dispatch_dpl<KV, 4>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw);
+        case 6: return dispatch_dpl<KV, 6>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw);
+        case 8: return dispatch_dpl<KV, 8>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw);
     }
     return false;
 }
@@ -826,8 +823,11 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
         }
         return VGX_OK;
     }
+    // Batch 1 keeps 4 waves per workgroup and the merge launch: 8 waves (28 splits, merged by the
+    // last workgroup) measured slower, 790 vs 880 tokens/s (half as many CUs stream the keys).
+    const int nw = kWaves;
     int64_t kps = 0;
-    const int ns = choose_splits(B, G, n_tot, &kps);
+    const int ns = choose_splits(B, G, n_tot, &kps, nw);
     float *part = nullptr;
     int *cnt = nullptr;
     if (ns > 1) {
@@ -839,9 +839,9 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
     dim3 grid((unsigned)ns, (unsigned)G, (unsigned)B);
     bool ok = kv_dtype == VGX_F32
                   ? dispatch_grp<VGX_F32>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out,
-                                          part, cnt, (int)H, (int)G, scale, n_tot, kps, ns, causal_base)
+                                          part, cnt, (int)H, (int)G, scale, n_tot, kps, ns, causal_base, nw)
                   : dispatch_grp<VGX_BF16>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out,
-                                           part, cnt, (int)H, (int)G, scale, n_tot, kps, ns, causal_base);
+                                           part, cnt, (int)H, (int)G, scale, n_tot, kps, ns, causal_base, nw);
     if (!ok) return VGX_E_LIMIT;
     VGX_CHECK_LAUNCH();
     if (ns > 1 && cnt == nullptr) {
