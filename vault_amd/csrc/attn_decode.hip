@@ -501,12 +501,13 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
 #pragma unroll
             for (int j = 0; j < 8; ++j) e[j] = 0.0f;
         }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t hb = float_to_bf16_bits(e[j]);
-            qh[kc][j] = __builtin_bit_cast(__bf16, (uint16_t)hb);
-            ql[kc][j] = __builtin_bit_cast(__bf16, (uint16_t)float_to_bf16_bits(e[j] - bf16_bits_to_float(hb)));
-        }
+        uint4 hw, lw;
+        split_bf16x2(e[0], e[1], hw.x, lw.x);
+        split_bf16x2(e[2], e[3], hw.y, lw.y);
+        split_bf16x2(e[4], e[5], hw.z, lw.z);
+        split_bf16x2(e[6], e[7], hw.w, lw.w);
+        qh[kc] = __builtin_bit_cast(bf16x8_t, hw);
+        ql[kc] = __builtin_bit_cast(bf16x8_t, lw);
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
@@ -572,16 +573,18 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
         const float mn = fmaxf(m, mt);
         const float corr = __expf(m - mn);
         m = mn;
-        bf16x8_t ph, pl;
-        float ps = 0.0f;
+        float ps = 0.0f, pv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float p = __expf(v[i] - mn);
-            ps += p;
-            const uint32_t pb = float_to_bf16_bits(p);
-            ph[i] = __builtin_bit_cast(__bf16, (uint16_t)pb);
-            pl[i] = __builtin_bit_cast(__bf16, (uint16_t)float_to_bf16_bits(p - bf16_bits_to_float(pb)));
+            pv[i] = __expf(v[i] - mn);
+            ps += pv[i];
         }
+        uint4 hw, lw;
+        split_bf16x2(pv[0], pv[1], hw.x, lw.x);
+        split_bf16x2(pv[2], pv[3], hw.y, lw.y);
+        split_bf16x2(pv[4], pv[5], hw.z, lw.z);
+        split_bf16x2(pv[6], pv[7], hw.w, lw.w);
+        const bf16x8_t ph = __builtin_bit_cast(bf16x8_t, hw), pl = __builtin_bit_cast(bf16x8_t, lw);
         lsum = lsum * corr + ps;
         if (__ballot(corr != 1.0f)) {
 #pragma unroll

@@ -120,9 +120,13 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                     const float4 x0 = reinterpret_cast<const float4 *>(qp)[0], x1 = reinterpret_cast<const float4 *>(qp)[1];
                     const float e[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        hb[i] = float_to_bf16_bits(e[i]);
-                        lb[i] = float_to_bf16_bits(e[i] - bf16_bits_to_float(hb[i]));
+                    for (int i = 0; i < 8; i += 2) {
+                        uint32_t hw, lw;
+                        split_bf16x2(e[i], e[i + 1], hw, lw);
+                        hb[i] = hw & 0xFFFFu;
+                        hb[i + 1] = hw >> 16;
+                        lb[i] = lw & 0xFFFFu;
+                        lb[i + 1] = lw >> 16;
                     }
                 }
             } else {
@@ -273,15 +277,19 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                 const float mn = fmaxf(m[qt], mt);                    // running max in log2 units
                 const float corr = exp2f(m[qt] - mn);
                 m[qt] = mn;
-                float ps = 0.0f;
+                float ps = 0.0f, pv[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    const float p = exp2f(v[i] - mn);
-                    ps += p;
-                    const uint32_t pbh = float_to_bf16_bits(p);
-                    ph[qt][i] = __builtin_bit_cast(__bf16, (uint16_t)pbh);
-                    pl[qt][i] = __builtin_bit_cast(__bf16, (uint16_t)float_to_bf16_bits(p - bf16_bits_to_float(pbh)));
+                    pv[i] = exp2f(v[i] - mn);
+                    ps += pv[i];
                 }
+                uint4 hw, lw;
+                split_bf16x2(pv[0], pv[1], hw.x, lw.x);
+                split_bf16x2(pv[2], pv[3], hw.y, lw.y);
+                split_bf16x2(pv[4], pv[5], hw.z, lw.z);
+                split_bf16x2(pv[6], pv[7], hw.w, lw.w);
+                ph[qt] = __builtin_bit_cast(bf16x8_t, hw);
+                pl[qt] = __builtin_bit_cast(bf16x8_t, lw);
                 lsum[qt] = lsum[qt] * corr + ps;
                 if (__ballot(corr != 1.0f)) {   // some query's running max moved: rescale O
 #pragma unroll

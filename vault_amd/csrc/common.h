@@ -81,11 +81,23 @@ VGX_DEV float half_bits_to_float(uint32_t h) {
 
 VGX_DEV float bf16_bits_to_float(uint32_t b) { return __uint_as_float((b & 0xFFFFu) << 16); }
 
-// Round-to-nearest-even fp32 -> bf16 bits (finite inputs).
-VGX_DEV uint32_t float_to_bf16_bits(float f) {
-    uint32_t u = __float_as_uint(f);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return u >> 16;
+// Round-to-nearest-even fp32 -> bf16 bits (finite inputs): the gfx950 conversion instruction
+// (v_cvt_pk_bf16_f32), one VALU operation instead of the four of the integer rounding sequence.
+VGX_DEV uint32_t float_to_bf16_bits(float f) { return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f); }
+
+typedef __bf16 vgx_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float vgx_f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> two RNE bf16 in one word (low half = a), one v_cvt_pk_bf16_f32.
+VGX_DEV uint32_t pack_bf16x2(float a, float b) {
+    const vgx_f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, vgx_bf16x2_t));
+}
+
+// hi = bf16(a, b), lo = bf16(a - hi_a, b - hi_b): the hi + lo split of two floats (2^-17 relative).
+VGX_DEV void split_bf16x2(float a, float b, uint32_t &hi, uint32_t &lo) {
+    hi = pack_bf16x2(a, b);
+    lo = pack_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
 }
 
 }  // namespace vgx

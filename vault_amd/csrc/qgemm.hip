@@ -340,20 +340,24 @@ __global__ __launch_bounds__(256) void qgemm_small_kernel(const uint8_t *__restr
             const int f = tid + 256 * i, row = f >> 5, bl = (f >> 3) & 3, j4 = f & 7;
             const float e[4] = {xr[i].x, xr[i].y, xr[i].z, xr[i].w};
             const float g[4] = {gr[i].x, gr[i].y, gr[i].z, gr[i].w};
-            uint32_t hb[4], lb[4];
-            float sum = 0.0f;
+            float u[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 if constexpr (NORM) ssq[i] = fmaf(e[k], e[k], ssq[i]);
-                const float u = NORM ? g[k] * e[k] : e[k];
-                hb[k] = float_to_bf16_bits(u);
-                lb[k] = float_to_bf16_bits(u - bf16_bits_to_float(hb[k]));
-                sum += bf16_bits_to_float(hb[k]) + bf16_bits_to_float(lb[k]);
+                u[k] = NORM ? g[k] * e[k] : e[k];
             }
-            *reinterpret_cast<uint2 *>(&sh[buf][row][bl * QK + j4 * 4]) =
-                make_uint2(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16));
-            *reinterpret_cast<uint2 *>(&sl[buf][row][bl * QK + j4 * 4]) =
-                make_uint2(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16));
+            uint2 hw, lw;
+            split_bf16x2(u[0], u[1], hw.x, lw.x);
+            split_bf16x2(u[2], u[3], hw.y, lw.y);
+            float sum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t h = k < 2 ? hw.x : hw.y, l = k < 2 ? lw.x : lw.y;
+                const int sh16 = (k & 1) ? 0 : 16;
+                sum += __uint_as_float((h << sh16) & 0xFFFF0000u) + __uint_as_float((l << sh16) & 0xFFFF0000u);
+            }
+            *reinterpret_cast<uint2 *>(&sh[buf][row][bl * QK + j4 * 4]) = hw;
+            *reinterpret_cast<uint2 *>(&sl[buf][row][bl * QK + j4 * 4]) = lw;
             // the 8 threads of one (row, block) are 8 consecutive lanes
             sum += __shfl_xor(sum, 1, kWave);
             sum += __shfl_xor(sum, 2, kWave);
