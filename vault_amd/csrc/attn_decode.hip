@@ -24,9 +24,7 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kKB = 4;       // keys per DPP row per 16-key tile
 constexpr int kWaves = 4;    // waves per workgroup
-constexpr int kMinKeysPerWave = 16;
 constexpr int kTargetWaves = 2048;
 constexpr int kMaxSplits = 64;
 constexpr float kNegBig = -1.0e30f;
@@ -142,10 +140,10 @@ __device__ __forceinline__ float raw_at(const RowRaw<KV, DPL> &r, int d) {
     else return (d & 1) ? __uint_as_float(r.w[d >> 1] & 0xFFFF0000u) : __uint_as_float(r.w[d >> 1] << 16);
 }
 
-// The kKB keys of one DPP row of a 16-key tile.
-template <int KV, int DPL>
+// The KB keys of one DPP row of a 4 KB-key tile.
+template <int KV, int DPL, int KB>
 struct KeyTile {
-    RowRaw<KV, DPL> k[kKB], v[kKB];
+    RowRaw<KV, DPL> k[KB], v[KB];
 };
 
 template <typename T>
@@ -156,20 +154,31 @@ __device__ __forceinline__ T pick4(int s, T a0, T a1, T a2, T a3) {
 // Workspace layout: partials per (b, g, split, head): D accumulators, then m, l.
 //
 // Split z covers global keys [z kps, (z + 1) kps) of the concatenated spans (by capacity).  Inside
-// each span the split's keys are dealt to the waves in 16-key tiles (wave w: tiles lo + 16 w + 64 i).
-// Tile addresses depend only on the span capacities (host values), so the first tile's K/V loads are
-// issued before the query and the device-side lengths arrive; keys at or beyond a span's effective
-// length (device length, causal limit) are masked, and no row beyond a span's capacity is read.
-// With PIPE the next tile's loads are issued before the current tile is reduced.
-template <int KV, int GRP, int DPL, int NW>
+// each span the split's keys are dealt to the waves in TK = 4 KB-key tiles (wave w: tiles lo + TK w +
+// NW TK i).  Tile addresses depend only on the span capacities (host values), so the first tile's K/V
+// loads are issued before the query and the device-side lengths arrive; keys at or beyond a span's
+// effective length (device length, causal limit) are masked, and no row beyond a span's capacity is
+// read.  With PIPE the next tile's loads are issued before the current tile is reduced.
+//
+// The online-softmax states of the 4 NW DPP rows are combined in two stages: RS steps of VALU lane
+// swaps inside each wave (RS = 2: one state per wave), then the remaining P = NW (4 >> RS) states
+// through LDS: per head, the running maxima give P weights e^{m_p - M} (computed once), and each
+// output is a P-term weighted sum.  RS = 0 costs no cross-lane traffic at all (measured faster at
+// batch 1, where a wave's serial instruction count is the latency).
+template <int KV, int GRP, int DPL, int NW, int KB, int RS>
 __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     const float *__restrict__ q, int64_t ldq, SpanArgs sp, const float *__restrict__ bias, int64_t bias_hstride,
     int bias_span, float *__restrict__ out, float *__restrict__ part, int *__restrict__ cnt, int H, int G,
     float scale, int64_t n_tot, int64_t kps, int n_splits, int64_t causal_base) {
     constexpr int D = DPL * 16;
     constexpr int SLOT = D + 2;
+    constexpr int TK = 4 * KB;                      // keys per wave tile
+    constexpr int P = NW * (4 >> RS);               // states combined through LDS
     constexpr bool PIPE = KV == VGX_BF16;
-    __shared__ float red[NW][GRP][SLOT];
+    static_assert(RS >= 0 && RS <= 2, "0, 1 or 2 lane-swap steps");
+    __shared__ float red[P][GRP][SLOT];
+    __shared__ float wgt[GRP][P];
+    __shared__ float mrg[2][GRP];
 
     const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, l16 = lane & 15, row = lane >> 4;
@@ -193,24 +202,24 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     auto first_in = [&](int s0) -> int2 {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-            if (s >= s0 && lo[s] + wave * 16 < hi[s]) return make_int2(s, lo[s] + wave * 16);
+            if (s >= s0 && lo[s] + wave * TK < hi[s]) return make_int2(s, lo[s] + wave * TK);
         return make_int2(4, 0);
     };
     auto next = [&](int2 c) -> int2 {
-        if (c.y + NW * 16 < pick4(c.x, hi[0], hi[1], hi[2], hi[3])) return make_int2(c.x, c.y + NW * 16);
+        if (c.y + NW * TK < pick4(c.x, hi[0], hi[1], hi[2], hi[3])) return make_int2(c.x, c.y + NW * TK);
         return first_in(c.x + 1);
     };
-    auto fetch = [&](KeyTile<KV, DPL> &t, int2 c) {
+    auto fetch = [&](KeyTile<KV, DPL, KB> &t, int2 c) {
         const int s = c.x;
         const void *kb = pick4(s, sp.k[0], sp.k[1], sp.k[2], sp.k[3]);
         const void *vb = pick4(s, sp.v[0], sp.v[1], sp.v[2], sp.v[3]);
         const int64_t o = (int64_t)b * pick4(s, sp.bstride[0], sp.bstride[1], sp.bstride[2], sp.bstride[3]) +
                           (int64_t)g * pick4(s, sp.gstride[0], sp.gstride[1], sp.gstride[2], sp.gstride[3]) +
-                          (int64_t)(c.y + row * kKB) * D + l16 * DPL;
+                          (int64_t)(c.y + row * KB) * D + l16 * DPL;
         // rows past the split's end in this span re-read its last row (in bounds; masked at use)
-        const int last = pick4(s, hi[0], hi[1], hi[2], hi[3]) - 1 - c.y - row * kKB;
+        const int last = pick4(s, hi[0], hi[1], hi[2], hi[3]) - 1 - c.y - row * KB;
 #pragma unroll
-        for (int j = 0; j < kKB; ++j) {
+        for (int j = 0; j < KB; ++j) {
             const int64_t oj = o + (int64_t)min(j, last) * D;
             load_raw<KV, DPL>(kb, oj, t.k[j]);
             load_raw<KV, DPL>(vb, oj, t.v[j]);
@@ -228,7 +237,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
             qr[hh][4 * d4] = t.x; qr[hh][4 * d4 + 1] = t.y; qr[hh][4 * d4 + 2] = t.z; qr[hh][4 * d4 + 3] = t.w;
         }
     }
-    KeyTile<KV, DPL> tA, tB;
+    KeyTile<KV, DPL, KB> tA, tB;
     int2 cur = first_in(0);
     if (cur.x < 4) fetch(tA, cur);
 #pragma unroll
@@ -252,13 +261,13 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
         for (int d = 0; d < DPL; ++d) acc[hh][d] = 0.0f;
     }
 
-    auto compute = [&](const KeyTile<KV, DPL> &t, int2 c) {
+    auto compute = [&](const KeyTile<KV, DPL, KB> &t, int2 c) {
         const int s = c.x;
         const int e = pick4(s, eff[0], eff[1], eff[2], eff[3]);
         const float *bb = (bias != nullptr && s == bias_span) ? bias + (int64_t)g * GRP * bias_hstride : nullptr;
-        float sc[GRP][kKB];
+        float sc[GRP][KB];
 #pragma unroll
-        for (int j = 0; j < kKB; ++j)
+        for (int j = 0; j < KB; ++j)
 #pragma unroll
             for (int hh = 0; hh < GRP; ++hh) {
                 float p = 0.0f;
@@ -267,8 +276,8 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
                 sc[hh][j] = row16_sum(p);
             }
 #pragma unroll
-        for (int j = 0; j < kKB; ++j) {
-            const int key = c.y + row * kKB + j;
+        for (int j = 0; j < KB; ++j) {
+            const int key = c.y + row * KB + j;
             const bool valid = key < e;
 #pragma unroll
             for (int hh = 0; hh < GRP; ++hh) {
@@ -281,13 +290,13 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
         for (int hh = 0; hh < GRP; ++hh) {
             float mb = sc[hh][0];
 #pragma unroll
-            for (int j = 1; j < kKB; ++j) mb = fmaxf(mb, sc[hh][j]);
+            for (int j = 1; j < KB; ++j) mb = fmaxf(mb, sc[hh][j]);
             const float mn = fmaxf(m[hh], mb);
             const float corr = __expf(m[hh] - mn);
             m[hh] = mn;
             float ls = l[hh] * corr;
 #pragma unroll
-            for (int j = 0; j < kKB; ++j) {
+            for (int j = 0; j < KB; ++j) {
                 const float p = __expf(sc[hh][j] - mn);
                 sc[hh][j] = p;
                 ls += p;
@@ -297,19 +306,19 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
             for (int d = 0; d < DPL; ++d) {
                 float a = acc[hh][d] * corr;
 #pragma unroll
-                for (int j = 0; j < kKB; ++j) a = fmaf(sc[hh][j], raw_at<KV, DPL>(t.v[j], d), a);
+                for (int j = 0; j < KB; ++j) a = fmaf(sc[hh][j], raw_at<KV, DPL>(t.v[j], d), a);
                 acc[hh][d] = a;
             }
         }
     };
     // Masked rows of a tile may hold anything (e.g. unwritten ring slots): their values are replaced
     // by zeros before use so that p = 0 cannot meet a non-finite value.
-    auto clean = [&](KeyTile<KV, DPL> &t, int2 c) {
+    auto clean = [&](KeyTile<KV, DPL, KB> &t, int2 c) {
         const int e = pick4(c.x, eff[0], eff[1], eff[2], eff[3]);
-        if (c.y + 16 <= e) return;                 // uniform: the whole tile is valid
+        if (c.y + TK <= e) return;                 // uniform: the whole tile is valid
 #pragma unroll
-        for (int j = 0; j < kKB; ++j) {
-            const bool valid = c.y + row * kKB + j < e;
+        for (int j = 0; j < KB; ++j) {
+            const bool valid = c.y + row * KB + j < e;
 #pragma unroll
             for (int w = 0; w < RowRaw<KV, DPL>::W; ++w) {
                 t.k[j].w[w] = valid ? t.k[j].w[w] : 0u;
@@ -341,11 +350,11 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
         }
     }
 
-    // Merge the online-softmax states of the four DPP rows of the wave: rows r and r ^ 1, then the two
-    // halves, with the VALU lane swaps (each gives a lane its own and its partner's value, the lower
-    // row's first in every lane of a row pair, so both rows of a pair compute the same merge).
+    // RS steps of the in-wave merge: rows r and r ^ 1, then the two halves, with the VALU lane swaps
+    // (each gives a lane its own and its partner's value, the lower row's first in every lane of a row
+    // pair, so both rows of a pair compute the same merge).
 #pragma unroll
-    for (int step = 0; step < 2; ++step) {
+    for (int step = 0; step < RS; ++step) {
         auto pair = [&](float x) {
             const auto r = step == 0
                                ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
@@ -366,35 +375,49 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
             m[hh] = mn;
         }
     }
-    if (row == 0) {
+    // the P remaining states to LDS: state p = wave (4 >> RS) + row >> RS, written by rows with
+    // row % (1 << RS) == 0
+    if ((row & ((1 << RS) - 1)) == 0) {
+        const int p = wave * (4 >> RS) + (row >> RS);
 #pragma unroll
         for (int hh = 0; hh < GRP; ++hh) {
 #pragma unroll
-            for (int d = 0; d < DPL; ++d) red[wave][hh][l16 * DPL + d] = acc[hh][d];
+            for (int d4 = 0; d4 < DPL / 4; ++d4)
+                *reinterpret_cast<float4 *>(&red[p][hh][l16 * DPL + 4 * d4]) =
+                    make_float4(acc[hh][4 * d4], acc[hh][4 * d4 + 1], acc[hh][4 * d4 + 2], acc[hh][4 * d4 + 3]);
             if (l16 == 0) {
-                red[wave][hh][D] = m[hh];
-                red[wave][hh][D + 1] = l[hh];
+                red[p][hh][D] = m[hh];
+                red[p][hh][D + 1] = l[hh];
             }
         }
     }
     __syncthreads();
+    // per head: M = max_p m_p, weights w_p = e^{m_p - M}, L = sum_p w_p l_p
+    for (int i = threadIdx.x; i < GRP * P; i += 64 * NW) {
+        const int hh = i / P, pi = i - hh * P;
+        float M = kNegBig;
+#pragma unroll
+        for (int p = 0; p < P; ++p) M = fmaxf(M, red[p][hh][D]);
+        wgt[hh][pi] = __expf(red[pi][hh][D] - M);
+        if (pi == 0) {
+            float L = 0.0f;
+#pragma unroll
+            for (int p = 0; p < P; ++p) L = fmaf(__expf(red[p][hh][D] - M), red[p][hh][D + 1], L);
+            mrg[0][hh] = M;
+            mrg[1][hh] = L;
+        }
+    }
+    __syncthreads();
 
-    // Merge the waves: thread t owns (head t / D, dim t % D).
+    // thread t owns (head t / D, dim t % D)
     const int64_t pair = (int64_t)b * G + g;
     for (int t = threadIdx.x; t < GRP * D; t += 64 * NW) {
         const int hh = t / D, d = t - hh * D;
-        float M = kNegBig;
+        float A = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) M = fmaxf(M, red[w][hh][D]);
-        float L = 0.0f, A = 0.0f;
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const float c = __expf(red[w][hh][D] - M);
-            L = fmaf(c, red[w][hh][D + 1], L);
-            A = fmaf(c, red[w][hh][d], A);
-        }
-        if (n_splits == 1) out[((int64_t)b * H + (int64_t)g * GRP + hh) * D + d] = A / L;
-        else store_partial<GRP, D>(part + ((pair * n_splits + split) * GRP + hh) * SLOT, d, A, M, L);
+        for (int p = 0; p < P; ++p) A = fmaf(wgt[hh][p], red[p][hh][d], A);
+        if (n_splits == 1) out[((int64_t)b * H + (int64_t)g * GRP + hh) * D + d] = A / mrg[1][hh];
+        else store_partial<GRP, D>(part + ((pair * n_splits + split) * GRP + hh) * SLOT, d, A, mrg[0][hh], mrg[1][hh]);
     }
     if (n_splits > 1 && cnt != nullptr) {
         __shared__ int last;
@@ -678,14 +701,32 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict
     out[((int64_t)b * H + h) * D + d] = a * inv_l;
 }
 
-int choose_splits(int64_t B, int64_t G, int64_t n_tot, int64_t *kps, int nw = kWaves) {
-    // About kTargetWaves waves in flight, at least kMinKeysPerWave keys per wave, at most kMaxSplits.
+// Workgroup shapes of the VALU kernel: waves per workgroup, keys per DPP row of a wave tile.
+struct Tiling {
+    int nw, kb;
+};
+constexpr Tiling kTilings[] = {{4, 4}, {8, 2}};
+constexpr int kNumTilings = sizeof(kTilings) / sizeof(kTilings[0]);
+
+// Measured on MI355X, fp32 K/V, 12 query / 2 KV heads, 3584 keys (attention + merge per layer): batch 1
+// 11.7 us with 4 waves x 16-key tiles against 12.0 us with 8 waves x 8-key tiles (and 13.0 / 15.8 us for
+// 4 x 8 / 8 x 16); batch 4 16.4 vs 20.0 us; batch 16 36.6 vs 34.1 us; batch 64 101.7 vs 90.3 us.
+int pick_tiling(int64_t B, int64_t G) { return B * G >= 32 ? 1 : 0; }
+
+// LDS budget of the cross-row merge: RS lane-swap steps first when the P states would not fit.
+constexpr int pick_rs(int grp, int dpl, int nw) {
+    return nw * 4 * grp * (dpl * 16 + 2) * 4 <= 52 * 1024 ? 0 : nw * 2 * grp * (dpl * 16 + 2) * 4 <= 52 * 1024 ? 1 : 2;
+}
+
+int choose_splits(int64_t B, int64_t G, int64_t n_tot, int64_t *kps, int tiling) {
+    // About kTargetWaves waves in flight, at least one tile per wave, at most kMaxSplits.
+    const int nw = kTilings[tiling].nw, tk = 4 * kTilings[tiling].kb;
     const int64_t pairs = B * G;
     int64_t want = (kTargetWaves / nw + pairs - 1) / pairs;
-    const int64_t cap = (n_tot + nw * kMinKeysPerWave - 1) / (nw * kMinKeysPerWave);
+    const int64_t cap = (n_tot + nw * tk - 1) / (nw * tk);
     want = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(want, cap), kMaxSplits));
     int64_t k = (n_tot + want - 1) / want;
-    k = (k + 15) / 16 * 16;
+    k = (k + tk - 1) / tk * tk;
     *kps = k;
     return (int)((n_tot + k - 1) / k);
 }
@@ -712,22 +753,38 @@ int64_t partial_bytes(int64_t B, int64_t H, int64_t D, int ns) {
 // workgroups.
 int64_t ticket_bytes(int64_t B, int64_t G) { return (B * G * 4 + 255) / 256 * 256; }
 
+template <int KV, int GRP, int DPL, int NW, int KB>
+void launch_tiled(dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp, const float *bias,
+                  int64_t bhs, int bspan, float *out, float *part, int *cnt, int H, int G, float scale,
+                  int64_t n_tot, int64_t kps, int ns, int64_t cb) {
+    constexpr int RS = pick_rs(GRP, DPL, NW);
+    hipLaunchKernelGGL((attn_decode_kernel<KV, GRP, DPL, NW, KB, RS>), grid, dim3(64 * NW), 0, st, q, ldq, sp, bias,
+                       bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
+}
+
 template <int KV, int GRP, int DPL>
 void launch_decode(dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp, const float *bias,
                    int64_t bhs, int bspan, float *out, float *part, int *cnt, int H, int G, float scale,
-                   int64_t n_tot, int64_t kps, int ns, int64_t cb, int nw) {
-    (void)nw;
-    hipLaunchKernelGGL((attn_decode_kernel<KV, GRP, DPL, kWaves>), grid, dim3(64 * kWaves), 0, st, q, ldq, sp, bias,
-                       bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb);
+                   int64_t n_tot, int64_t kps, int ns, int64_t cb, int tiling) {
+    switch (tiling) {
+#define VGX_AT(T)                                                                                              \
+    case T:                                                                                                    \
+        launch_tiled<KV, GRP, DPL, kTilings[T].nw, kTilings[T].kb>(grid, st, q, ldq, sp, bias, bhs, bspan, out, \
+                                                                   part, cnt, H, G, scale, n_tot, kps, ns, cb); \
+        break;
+        VGX_AT(0)
+        VGX_AT(1)
+#undef VGX_AT
+    }
 }
 
 template <int KV, int GRP>
 bool dispatch_dpl(int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp,
                   const float *bias, int64_t bhs, int bspan, float *out, float *part, int *cnt, int H, int G,
-                  float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb, int nw) {
+                  float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb, int tiling) {
     switch (D) {
-        case 64: launch_decode<KV, GRP, 4>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw); return true;
-        case 128: launch_decode<KV, GRP, 8>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw); return true;
+        case 64: launch_decode<KV, GRP, 4>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, tiling); return true;
+        case 128: launch_decode<KV, GRP, 8>(grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, tiling); return true;
     }
     return false;
 }
@@ -735,13 +792,13 @@ bool dispatch_dpl(int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq,
 template <int KV>
 bool dispatch_grp(int grp, int D, dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp,
                   const float *bias, int64_t bhs, int bspan, float *out, float *part, int *cnt, int H, int G,
-                  float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb, int nw) {
+                  float scale, int64_t n_tot, int64_t kps, int ns, int64_t cb, int tiling) {
     switch (grp) {
-        case 1: return dispatch_dpl<KV, 1>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw);
-        case 2: return dispatch_dpl<KV, 2>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw);
-        case 4: return dispatch_dpl<KV, 4>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw);
-        case 6: return dispatch_dpl<KV, 6>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw);
-        case 8: return dispatch_dpl<KV, 8>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, nw);
+        case 1: return dispatch_dpl<KV, 1>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, tiling);
+        case 2: return dispatch_dpl<KV, 2>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, tiling);
+        case 4: return dispatch_dpl<KV, 4>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, tiling);
+        case 6: return dispatch_dpl<KV, 6>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, tiling);
+        case 8: return dispatch_dpl<KV, 8>(D, grid, st, q, ldq, sp, bias, bhs, bspan, out, part, cnt, H, G, scale, n_tot, kps, ns, cb, tiling);
     }
     return false;
 }
@@ -753,7 +810,8 @@ extern "C" {
 int64_t vgx_attn_decode_workspace_bytes(int64_t B, int64_t H, int64_t G, int64_t D, int64_t n_keys) {
     if (B <= 0 || H <= 0 || G <= 0 || D <= 0 || n_keys <= 0 || H % G) return VGX_E_SIZE;
     int64_t kps = 0;
-    const int ns = choose_splits(B, G, n_keys, &kps);
+    int ns = 0;   // the most splits of any workgroup shape, so the caller's workspace fits every choice
+    for (int t = 0; t < kNumTilings; ++t) ns = std::max(ns, choose_splits(B, G, n_keys, &kps, t));
     if (ns <= 1) return 0;
     return ticket_bytes(B, G) + partial_bytes(B, H, D, ns);
 }
@@ -826,11 +884,11 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
         }
         return VGX_OK;
     }
-    // Batch 1 keeps 4 waves per workgroup and the merge launch: 8 waves (28 splits, merged by the
-    // last workgroup) measured slower, 790 vs 880 tokens/s (half as many CUs stream the keys).
-    const int nw = kWaves;
+    // Batch 1 keeps the merge launch: 8 waves of 16-key tiles (28 splits, merged by the last
+    // workgroup) measured slower, 790 vs 880 tokens/s (half as many CUs stream the keys).
+    const int tiling = pick_tiling(B, G);
     int64_t kps = 0;
-    const int ns = choose_splits(B, G, n_tot, &kps, nw);
+    const int ns = choose_splits(B, G, n_tot, &kps, tiling);
     float *part = nullptr;
     int *cnt = nullptr;
     if (ns > 1) {
@@ -842,9 +900,9 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
     dim3 grid((unsigned)ns, (unsigned)G, (unsigned)B);
     bool ok = kv_dtype == VGX_F32
                   ? dispatch_grp<VGX_F32>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out,
-                                          part, cnt, (int)H, (int)G, scale, n_tot, kps, ns, causal_base, nw)
+                                          part, cnt, (int)H, (int)G, scale, n_tot, kps, ns, causal_base, tiling)
                   : dispatch_grp<VGX_BF16>(grp, (int)D, grid, st, q, ldq, sp, bias, bias_hstride, bias_span, out,
-                                           part, cnt, (int)H, (int)G, scale, n_tot, kps, ns, causal_base, nw);
+                                           part, cnt, (int)H, (int)G, scale, n_tot, kps, ns, causal_base, tiling);
     if (!ok) return VGX_E_LIMIT;
     VGX_CHECK_LAUNCH();
     if (ns > 1 && cnt == nullptr) {
