@@ -387,7 +387,7 @@ __global__ __launch_bounds__(64 * WPG * KW) void gemv1_kernel(GemvArgs a) {
     constexpr int RQW = 64 / LPR;
     constexpr int NW = WPG * KW;
     constexpr int NT = 64 * NW;
-    constexpr int CH = KW >= 4 ? 6 : 4;            // staging float4 loads per thread and round
+    constexpr int CH = 4;                          // staging float4 loads per thread and round
     extern __shared__ float xs[];                  // [nblk][kGemvPad]
     __shared__ float red[NW][RQW][4];
     __shared__ float rsum[NW];
@@ -553,8 +553,9 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
     const bool aligned = ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.lnw & 15) == 0;
     if (a.n_rq >= 16384) VGX_GEMV1(16, 4, 1, 3, false, false);        // LM head: DPP row per row-quad
     else if (a.n_rq >= 2048) VGX_GEMV1(64, 4, 1, 1, true, false);     // gate/up: lane per block
-    else if (a.nblk >= 192) VGX_GEMV1(64, 1, 8, 1, true, false);      // down: 8 waves over K (staged: 6.6 vs
-                                                                      // 7.0 us with direct activations)
+    else if (a.nblk >= 192) VGX_GEMV1(64, 2, 8, 1, true, false);      // down: 2 row-quads x 8 waves over K
+                                                                      // (6.6 us; one row-quad 6.9 us, direct
+                                                                      // activations 7.0 us)
     else if (a.nblk >= 96 && a.n_rq < 256) VGX_GEMV1(64, 1, 8, 1, true, false);   // few rows: more waves
     else if (a.nblk >= 96) VGX_GEMV1(64, 1, 2, 1, true, false);
     else if (aligned && DT != VGX_F32) VGX_GEMV1(64, 1, 1, 1, false, true);   // small: direct
