@@ -23,7 +23,8 @@
 // same way in each product (lane group lg holds slots 8 lg .. 8 lg + 7 of both operands), which is
 // all the matrix product needs.  Key tiles entirely in the causal future of the 32 queries are not
 // loaded; keys of partially masked 32-key chunks get -inf (fully visible chunks skip the mask).
-// Scores are scaled by scale * log2(e) and use exp2.
+// Scores are scaled by scale * log2(e) and use the hardware exp2 (v_exp_f32, 1 ulp; results below
+// the normal range flush to zero, which no probability normalised by the running max can notice).
 #include "common.h"
 
 using namespace vgx;
@@ -262,25 +263,32 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
                 float v[8];
+                if (full) {
 #pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
+                    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int kk = kt * 16 + lg * 4 + i;       // key within the 32-key chunk
-                        const bool vis = full || (kk < klim && (!causal || kbase + kk <= qt * 16 + lq));
-                        v[kt * 4 + i] = vis ? sc[qt][kt][i] * sl2 : -INFINITY;
-                    }
+                        for (int i = 0; i < 4; ++i) v[kt * 4 + i] = sc[qt][kt][i] * sl2;
+                } else {
+#pragma unroll
+                    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int kk = kt * 16 + lg * 4 + i;       // key within the 32-key chunk
+                            const bool vis = kk < klim && (!causal || kbase + kk <= qt * 16 + lq);
+                            v[kt * 4 + i] = vis ? sc[qt][kt][i] * sl2 : -INFINITY;
+                        }
+                }
                 float mt = v[0];
 #pragma unroll
                 for (int i = 1; i < 8; ++i) mt = fmaxf(mt, v[i]);
                 mt = xor32_max(xor16_max(mt));
                 const float mn = fmaxf(m[qt], mt);                    // running max in log2 units
-                const float corr = exp2f(m[qt] - mn);
+                const float corr = __builtin_amdgcn_exp2f(m[qt] - mn);
                 m[qt] = mn;
                 float ps = 0.0f, pv[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    pv[i] = exp2f(v[i] - mn);
+                    pv[i] = __builtin_amdgcn_exp2f(v[i] - mn);
                     ps += pv[i];
                 }
                 uint4 hw, lw;
