@@ -41,6 +41,7 @@ constexpr int kVRow = kKT + 8;      // LDS row of V^T, bf16
 constexpr int kQTile = 32;          // queries per wave
 constexpr int kMaxBlocks = 8;
 constexpr float kNegBig = -1.0e30f;
+constexpr float kLazyMax = 8.0f;    // log2 of the largest unnormalised probability
 
 struct RunArgs {
     const uint16_t *k;
@@ -282,9 +283,18 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int i = 1; i < 8; ++i) mt = fmaxf(mt, v[i]);
                 mt = xor32_max(xor16_max(mt));
-                const float mn = fmaxf(m[qt], mt);                    // running max in log2 units
-                const float corr = __builtin_amdgcn_exp2f(m[qt] - mn);
-                m[qt] = mn;
+                // The reference max m (log2 units) moves only when a score exceeds it by more than
+                // kLazyMax: probabilities then stay below 2^kLazyMax, and O and the sum are rescaled
+                // far less often than the running max changes.
+                if (__ballot(mt > m[qt] + kLazyMax)) {
+                    const float mn = fmaxf(m[qt], mt);
+                    const float corr = __builtin_amdgcn_exp2f(m[qt] - mn);
+                    m[qt] = mn;
+                    lsum[qt] *= corr;
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt) o[qt][dt] *= corr;
+                }
+                const float mn = m[qt];
                 float ps = 0.0f, pv[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
@@ -298,11 +308,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                 split_bf16x2(pv[6], pv[7], hw.w, lw.w);
                 ph[qt] = __builtin_bit_cast(bf16x8_t, hw);
                 pl[qt] = __builtin_bit_cast(bf16x8_t, lw);
-                lsum[qt] = lsum[qt] * corr + ps;
-                if (__ballot(corr != 1.0f)) {   // some query's running max moved: rescale O
-#pragma unroll
-                    for (int dt = 0; dt < 8; ++dt) o[qt][dt] *= corr;
-                }
+                lsum[qt] += ps;
             }
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
