@@ -43,6 +43,11 @@ constexpr int kMaxBlocks = 8;
 constexpr float kNegBig = -1.0e30f;
 constexpr float kLazyMax = 8.0f;    // log2 of the largest unnormalised probability
 
+template <typename T>
+__device__ __forceinline__ T sel4(int i, T a0, T a1, T a2, T a3) {
+    return i == 0 ? a0 : i == 1 ? a1 : i == 2 ? a2 : a3;
+}
+
 struct RunArgs {
     const uint16_t *k;
     const uint16_t *v;
@@ -153,24 +158,37 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
         for (int dt = 0; dt < 8; ++dt) o[qt][dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
+    // The block's key runs, read from the kernel arguments once and held in registers: the tile loop
+    // selects among them instead of reloading argument memory at a run-dependent offset.
+    const int n_runs = B.n_runs;
+    const int64_t cbase = B.causal_base;
+    int64_t rlen[4];
+    const uint16_t *rkp[4], *rvp[4];
+    int rrs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const RunArgs &R = B.run[i];
+        int64_t n = i < n_runs ? R.len : 0;
+        if (i == n_runs - 1 && cbase >= 0) n = min(n, cbase + t0 + kQTile);   // the rest is in every query's future
+        rlen[i] = n;
+        rkp[i] = R.k + (int64_t)g * R.gstride;
+        rvp[i] = R.v + (int64_t)g * R.gstride;
+        rrs[i] = (int)R.rstride;
+    }
+
     // Key tiles in order over the runs; the global loads of the next tile are issued before the
     // current tile is computed (register double buffer), then stored into LDS (K as is, V transposed).
-    auto run_len = [&](int r) -> int64_t {
-        int64_t n = B.run[r].len;
-        if (r == B.n_runs - 1 && B.causal_base >= 0) n = min(n, B.causal_base + t0 + kQTile);  // the rest is in every query's future
-        return n;
-    };
+    auto run_len = [&](int r) -> int64_t { return sel4(r, rlen[0], rlen[1], rlen[2], rlen[3]); };
     constexpr int NT = 64 * GRP;
     constexpr int KCH = kKT * (kD / 8);            // 16-byte K chunks per tile
     constexpr int VCH = kKT / 2 * (kD / 8);        // V chunks per tile, counted in row pairs
     constexpr int KIT = (KCH + NT - 1) / NT, VIT = (VCH + NT - 1) / NT;
     uint4 kreg[KIT], vreg[VIT][2];
     auto fetch = [&](int r, int64_t j0) {
-        const RunArgs &R = B.run[r];
         const int64_t n = run_len(r);
-        const int rs = (int)R.rstride;
-        const uint16_t *kb = R.k + (int64_t)g * R.gstride + j0 * R.rstride;   // wave-uniform
-        const uint16_t *vb = R.v + (int64_t)g * R.gstride + j0 * R.rstride;
+        const int rs = sel4(r, rrs[0], rrs[1], rrs[2], rrs[3]);
+        const uint16_t *kb = sel4(r, rkp[0], rkp[1], rkp[2], rkp[3]) + j0 * rs;   // wave-uniform
+        const uint16_t *vb = sel4(r, rvp[0], rvp[1], rvp[2], rvp[3]) + j0 * rs;
         const int lim = (int)min<int64_t>(n - j0, kKT);                       // rows of this tile
 #pragma unroll
         for (int i = 0; i < KIT; ++i) {
@@ -218,22 +236,22 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
 
     const float sl2 = a.scale_log2;
     int r = 0;
-    while (r < B.n_runs && run_len(r) <= 0) ++r;
+    while (r < n_runs && run_len(r) <= 0) ++r;
     int64_t j0 = 0;
-    if (r < B.n_runs) fetch(r, j0);
-    while (r < B.n_runs) {
+    if (r < n_runs) fetch(r, j0);
+    while (r < n_runs) {
         const int64_t n = run_len(r);
-        const bool causal = (r == B.n_runs - 1) && B.causal_base >= 0;
+        const bool causal = (r == n_runs - 1) && cbase >= 0;
         int rn = r;
         int64_t jn = j0 + kKT;
         if (jn >= n) {
             jn = 0;
-            do { ++rn; } while (rn < B.n_runs && run_len(rn) <= 0);
+            do { ++rn; } while (rn < n_runs && run_len(rn) <= 0);
         }
         __syncthreads();
         stage();
         __syncthreads();
-        if (rn < B.n_runs) fetch(rn, jn);
+        if (rn < n_runs) fetch(rn, jn);
         for (int c = 0; c < kKT && j0 + c < n; c += 32) {
             f32x4_t sc[2][2];
 #pragma unroll
@@ -257,9 +275,9 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
             }
             bf16x8_t ph[2], pl[2];
             // 32-key chunk fully visible to all 32 queries: no per-score mask
-            const bool full = j0 + c + 32 <= n && (!causal || j0 + c + 31 <= B.causal_base + t0);
+            const bool full = j0 + c + 32 <= n && (!causal || j0 + c + 31 <= cbase + t0);
             // key index relative to the causal limit of query t0 (fits in 32 bits)
-            const int kbase = (int)(j0 + c - (causal ? B.causal_base + t0 : 0));
+            const int kbase = (int)(j0 + c - (causal ? cbase + t0 : 0));
             const int klim = (int)(n - (j0 + c));
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
