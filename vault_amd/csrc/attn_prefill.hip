@@ -38,7 +38,7 @@ constexpr int kKT = 64;             // keys per LDS tile
 constexpr int kD = 128;             // head dim (the kernel is specialised for 128)
 constexpr int kKRow = kD + 8;       // LDS row of K, bf16 (16 bytes of padding)
 constexpr int kVRow = kKT + 8;      // LDS row of V^T, bf16
-constexpr int kQTile = 32;          // queries per wave
+constexpr int kMaxQTile = 32;       // queries per wave: 16 NQT
 constexpr int kMaxBlocks = 8;
 constexpr float kNegBig = -1.0e30f;
 constexpr float kLazyMax = 8.0f;    // log2 of the largest unnormalised probability
@@ -80,8 +80,9 @@ struct PrefillArgs {
 };
 
 
-template <int GRP, bool QSPLIT>
+template <int GRP, bool QSPLIT, int NQT>
 __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
+    constexpr int kQTile = 16 * NQT;
     __shared__ __align__(16) uint16_t ks[kKT * kKRow];
     __shared__ __align__(16) uint16_t vt[kD * kVRow];
 
@@ -104,9 +105,9 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
 
     // Q^T fragments (bf16): query t0 + 16 qt + lq, dims 32 kc + 8 lg .. + 7; fp32 queries as
     // hi = bf16(q) and lo = bf16(q - hi).
-    bf16x8_t qh[2][4], ql[2][4];
+    bf16x8_t qh[NQT][4], ql[NQT][4];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < NQT; ++qt) {
         const int64_t t = t0 + qt * 16 + lq;
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
@@ -148,10 +149,10 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
         }
     }
 
-    f32x4_t o[2][8];
-    float m[2], lsum[2];
+    f32x4_t o[NQT][8];
+    float m[NQT], lsum[NQT];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < NQT; ++qt) {
         m[qt] = kNegBig;
         lsum[qt] = 0.0f;
 #pragma unroll
@@ -253,9 +254,9 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
         __syncthreads();
         if (rn < n_runs) fetch(rn, jn);
         for (int c = 0; c < kKT && j0 + c < n; c += 32) {
-            f32x4_t sc[2][2];
+            f32x4_t sc[NQT][2];
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+            for (int qt = 0; qt < NQT; ++qt) {
                 sc[qt][0] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
                 sc[qt][1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
             }
@@ -264,7 +265,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                 const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(ks + (c + lq) * kKRow + kc * 32 + lg * 8);
                 const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(ks + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) {
+                for (int qt = 0; qt < NQT; ++qt) {
                     sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qh[qt][kc], sc[qt][0], 0, 0, 0);
                     sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qh[qt][kc], sc[qt][1], 0, 0, 0);
                     if constexpr (QSPLIT) {
@@ -273,14 +274,14 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                     }
                 }
             }
-            bf16x8_t ph[2], pl[2];
+            bf16x8_t ph[NQT], pl[NQT];
             // 32-key chunk fully visible to all 32 queries: no per-score mask
             const bool full = j0 + c + 32 <= n && (!causal || j0 + c + 31 <= cbase + t0);
             // key index relative to the causal limit of query t0 (fits in 32 bits)
             const int kbase = (int)(j0 + c - (causal ? cbase + t0 : 0));
             const int klim = (int)(n - (j0 + c));
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+            for (int qt = 0; qt < NQT; ++qt) {
                 float v[8];
                 if (full) {
 #pragma unroll
@@ -335,7 +336,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                 const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16);
                 const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) {
+                for (int qt = 0; qt < NQT; ++qt) {
                     o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[qt], o[qt][dt], 0, 0, 0);
                     o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[qt], o[qt][dt], 0, 0, 0);
                 }
@@ -346,7 +347,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     }
 
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < NQT; ++qt) {
         const float L = xor32_sum(xor16_sum(lsum[qt]));
         const float inv = 1.0f / L;
         const int64_t t = t0 + qt * 16 + lq;
@@ -360,6 +361,11 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
         }
     }
 }
+
+// 32 queries per wave: 16-query waves (154 instead of 226 VGPRs at 6 heads per group, two workgroups
+// per CU) measured slower, 365 vs 296 us at L = 8192 (twice the K/V staging and K fragment reads per
+// query).
+constexpr int kNqt = 2;
 
 }  // namespace
 
@@ -375,6 +381,7 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, in
     if (D != kD) return VGX_E_LIMIT;
     const int grp = (int)(H / G);
     if (grp != 1 && grp != 2 && grp != 4 && grp != 6 && grp != 8) return VGX_E_LIMIT;
+    const int qtile = 16 * kNqt;
     PrefillArgs a{};
     a.H = (int)H;
     a.G = (int)G;
@@ -421,7 +428,7 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, in
         }
         if (b.causal_base >= 0 && b.causal_base + 1 > b.runs[b.n_runs - 1].len) return VGX_E_SIZE;
         if (n_keys == 0) return VGX_E_SIZE;
-        tiles += (b.n_q + kQTile - 1) / kQTile * G;
+        tiles += (b.n_q + qtile - 1) / qtile * G;
         ++nb;
     }
     if (nb == 0) return VGX_OK;
@@ -430,7 +437,7 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, in
     a.n_tiles = (int)tiles;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)tiles);
-#define VGX_PREFILL_GO(G_, S_) hipLaunchKernelGGL((attn_prefill_kernel<G_, S_>), grid, dim3(64 * G_), 0, st, a)
+#define VGX_PREFILL_GO(G_, S_) hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, kNqt>), grid, dim3(64 * G_), 0, st, a)
 #define VGX_PREFILL_GRP(S_)                      \
     switch (grp) {                               \
         case 1: VGX_PREFILL_GO(1, S_); break;    \
