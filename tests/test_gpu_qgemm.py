@@ -27,7 +27,8 @@ def _blocks(dt, rows, cols, seed):
 @pytest.mark.parametrize("rows,cols,batch,epi,norm", [
     (1536, 1536, 16, "store", False), (2048, 1536, 300, "store", True), (1536, 8960, 37, "accum", False),
     (8960, 1536, 64, "swiglu", True), (13, 96, 9, "store", True), (256, 4608, 1024, "store", False),
-    (2, 64, 8, "swiglu", False)])
+    (2, 64, 8, "swiglu", False), (13, 96, 130, "store", True), (2, 64, 200, "swiglu", False),
+    (1536, 8960, 200, "accum", False)])
 def test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm):
     rng = np.random.default_rng(rows + cols + batch)
     x = (rng.standard_normal((batch, cols)) * 2.0).astype(np.float32)
@@ -79,7 +80,7 @@ def test_qgemm_equals_gemv_rows(dev, dt):
 
 
 @pytest.mark.parametrize("dt", [codec.Q4_0])
-@pytest.mark.parametrize("rows,cols,batch", [(64, 7200, 8), (16, 4096, 8)])
+@pytest.mark.parametrize("rows,cols,batch", [(64, 7200, 8), (16, 4096, 8), (64, 7200, 200)])
 def test_qgemm_k_split_edges(dev, dt, rows, cols, batch):
     """Few weight rows and long rows: the GEMM splits K over many workgroups (up to 16), including
     a possibly empty last split (225 blocks over 16 splits)."""

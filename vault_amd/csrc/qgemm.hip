@@ -15,13 +15,12 @@
 // which is the reference's sum_b d_b sum_j q_j x_j with the activations rounded to 16 significant
 // bits.
 //
-// Mapping.  A workgroup of 4 waves covers 128 weight rows x 16 NC activation rows; each wave owns
-// 32 weight rows (two 16-row MFMA tiles) x 16 NC activation rows.  In the MFMA a lane of a 16-row
-// tile owns one weight row (l % 16) for the A operand and one activation row (l % 16) for the B
-// operand, both with the K slots 8 (l / 16) .. + 7 of the block (weights 8 lg .. 8 lg + 7); the
-// accumulator lane holds weight rows 4 (l / 16) .. + 3 (one packed row-quad, whose four fp16 scales
-// are one 8-byte load) of activation row l % 16.  Blocks go in groups of four with the next group's
-// weights, scales and activation fragments requested before the current group is multiplied.
+// Mapping.  Large batches (prefill chunks) run qgemm_tile_kernel (128 x 128 LDS tiles, below) after
+// the split pre-pass; decode batches of up to 64 rows run qgemm_small_kernel, which converts its
+// activations itself.  In every MFMA a lane of a 16-row tile owns one weight row (l % 16) for the A
+// operand and one activation row (l % 16) for the B operand, both with the K slots 8 (l / 16) .. + 7
+// of the block (weights 8 lg .. 8 lg + 7); the accumulator lane holds weight rows 4 (l / 16) .. + 3
+// (one packed row-quad, whose four fp16 scales are one 8-byte word) of activation row l % 16.
 #include "qgemv.h"
 
 using namespace vgx;
@@ -105,152 +104,161 @@ __device__ __forceinline__ bf16x8_t a_frag(uint2 w, int lg) {
     return __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-template <int DT, int NC, int EPI, bool SPLIT>
-__global__ __launch_bounds__(256) void qgemm_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
-                                                     int nblk, int64_t rows_out, const uint16_t *__restrict__ xh,
-                                                     const uint16_t *__restrict__ xl, const float *__restrict__ xsum,
-                                                     int64_t batch, const float *__restrict__ bias,
-                                                     float *__restrict__ y, int64_t ldy, float *__restrict__ part,
-                                                     int kper) {
+// ---------------------------------------------------------------------------------------------
+// Large batches (prefill chunks, more than 64 activation rows): LDS tiles.  A workgroup of 4 waves
+// owns 128 weight rows (32 row-quads) x 128 activation rows; wave (wm, wn) = (wave & 1, wave >> 1)
+// computes weight rows 64 wm .. + 63 x activation rows 64 wn .. + 63 as 4 x 4 MFMA tiles.  Per quant
+// block the workgroup stages the raw quants and scales of its 128 weight rows and the bf16 hi / lo
+// activations and block sums of its 128 activation rows in LDS (double-buffered, one barrier per
+// block; the next block's global loads are in flight while the current one is multiplied), so every
+// weight fragment serves 4 activation tiles and every activation fragment 4 weight tiles from LDS
+// instead of each wave streaming both from L2.  The offset correction enters as the MFMA's initial
+// accumulator (-off * S_b per activation row), leaving one FMA per output and block for the scale.
+constexpr int kTM = 128;                 // weight rows per workgroup tile
+constexpr int kTN = 128;                 // activation rows per workgroup tile
+constexpr int kBRow = QK + 8;            // bf16 per staged activation row (16 B of padding)
+
+template <int DT, int EPI, bool SPLIT>
+__global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
+                                                          int nblk, int64_t rows_out,
+                                                          const uint16_t *__restrict__ xh,
+                                                          const uint16_t *__restrict__ xl,
+                                                          const float *__restrict__ xsum, int64_t batch,
+                                                          const float *__restrict__ bias, float *__restrict__ y,
+                                                          int64_t ldy, float *__restrict__ part, int kper) {
+    constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
     constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 8.0f;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int APARTS = 4 * QB / 16;                  // 16-byte pieces of one row-quad block
+    constexpr int AQ16 = kTM / 4 * APARTS;               // 16-byte pieces of the tile's block
+    __shared__ __align__(16) uint8_t aq[2][kTM * QB];    // [row-quad][row][QB] as in the packed weights
+    __shared__ __align__(16) uint2 asc[2][kTM / 4];      // four fp16 scales per row-quad
+    __shared__ __align__(16) uint16_t bh[2][kTN * kBRow];
+    __shared__ __align__(16) uint16_t bl[2][kTN * kBRow];
+    __shared__ float bs[2][kTN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, lg = lane >> 4;
+    const int wm = wave & 1, wn = wave >> 1;
     const int cols = nblk * QK;
-    // weight rows of this wave: two 16-row tiles = row-quads rq0 + 4 t + (l16 / 4) for the A operand
-    const int64_t rq_wave = ((int64_t)blockIdx.x * 4 + wave) * 8;     // 8 row-quads = 32 rows per wave
-    const int64_t b0 = (int64_t)blockIdx.y * 16 * NC;                  // first activation row
-
-    int64_t arq[2];
-    bool aok[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        arq[t] = rq_wave + 4 * t + (l16 >> 2);
-        aok[t] = arq[t] < n_rq;
-    }
-    const int r4 = l16 & 3;
-    int64_t crq[2];
-    bool cok[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        crq[t] = rq_wave + 4 * t + lg;       // row-quad of the accumulator lane
-        cok[t] = crq[t] < n_rq;
-    }
-    int64_t bb[NC];
-    bool bok[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        bb[c] = b0 + 16 * c + l16;
-        bok[c] = bb[c] < batch;
-    }
-
-    f32x4_t acc[2][NC];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) acc[t][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    // Register double buffer of kGrp blocks: the loads of group g + 1 are in flight while group g is
-    // multiplied (one block of lookahead cannot cover HBM latency).
-    constexpr int kGrp = 4;
-    struct Blk {
-        uint2 wa[2], sc[2];
-        uint4 xh[NC], xl[NC];
-        float xs[NC];
-    };
-    Blk buf[2][kGrp];
-    // K range of this workgroup (blockIdx.z-th split of kper blocks when SPLIT)
+    const int64_t rq0 = (int64_t)blockIdx.x * (kTM / 4);
+    const int64_t b0 = (int64_t)blockIdx.y * kTN;
     const int blk_lo = SPLIT ? (int)blockIdx.z * kper : 0;
     const int blk_hi = SPLIT ? min(nblk, blk_lo + kper) : nblk;
-    auto fetch = [&](Blk (&gb)[kGrp], int g0) {
-#pragma unroll
-        for (int u = 0; u < kGrp; ++u) {
-            const int blk = g0 + u;
-            const bool in = blk < blk_hi;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                gb[u].wa[t] = (in && aok[t]) ? load_a<DT>(W, arq[t], nblk, blk, r4, lg) : make_uint2(0, 0);
-                gb[u].sc[t] = (in && cok[t]) ? *reinterpret_cast<const uint2 *>(W + soff + (crq[t] * nblk + blk) * 8)
-                                             : make_uint2(0, 0);
-            }
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                if (in && bok[c]) {
-                    const int64_t o = bb[c] * cols + blk * QK + 8 * lg;
-                    gb[u].xh[c] = *reinterpret_cast<const uint4 *>(xh + o);
-                    gb[u].xl[c] = *reinterpret_cast<const uint4 *>(xl + o);
-                    gb[u].xs[c] = xsum[bb[c] * nblk + blk];
-                } else {
-                    gb[u].xh[c] = gb[u].xl[c] = make_uint4(0, 0, 0, 0);
-                    gb[u].xs[c] = 0.0f;
-                }
-            }
-        }
-    };
-    auto compute = [&](const Blk &k) {
-        bf16x8_t af[2];
-        float d[2][4];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            af[t] = a_frag<DT>(k.wa[t], lg);
-            d[t][0] = half_bits_to_float(k.sc[t].x);
-            d[t][1] = half_bits_to_float(k.sc[t].x >> 16);
-            d[t][2] = half_bits_to_float(k.sc[t].y);
-            d[t][3] = half_bits_to_float(k.sc[t].y >> 16);
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                f32x4_t pr = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, k.xh[c]), pr, 0, 0, 0);
-                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, k.xl[c]), pr, 0, 0, 0);
-                const float corr = OFF * k.xs[c];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf(d[t][i], pr[i] - corr, acc[t][c][i]);
-            }
-    };
-    // Blocks past blk_hi are zero-filled (weights 0, scales 0): they add nothing.
-    if (blk_lo < blk_hi) fetch(buf[0], blk_lo);   // the last split can be empty (then its partials are zero)
-    for (int g0 = blk_lo, it = 0; g0 < blk_hi; g0 += kGrp, ++it) {
-        if (it & 1) {
-            if (g0 + kGrp < blk_hi) fetch(buf[0], g0 + kGrp);
-#pragma unroll
-            for (int u = 0; u < kGrp; ++u) compute(buf[1][u]);
+
+    // global -> registers (one block), registers -> LDS buffer
+    uint4 ra = make_uint4(0, 0, 0, 0), rbh0, rbh1, rbl0, rbl1;
+    uint2 rs = make_uint2(0, 0);
+    float rx = 0.0f;
+    auto fetch_b = [&](int idx, int blk, uint4 &h, uint4 &l) {
+        const int row = idx >> 2, pc = idx & 3;
+        const int64_t b = b0 + row;
+        if (b < batch) {
+            const int64_t o = b * cols + (int64_t)blk * QK + pc * 8;
+            h = *reinterpret_cast<const uint4 *>(xh + o);
+            l = *reinterpret_cast<const uint4 *>(xl + o);
         } else {
-            if (g0 + kGrp < blk_hi) fetch(buf[1], g0 + kGrp);
-#pragma unroll
-            for (int u = 0; u < kGrp; ++u) compute(buf[0][u]);
+            h = l = make_uint4(0, 0, 0, 0);
         }
+    };
+    auto fetch = [&](int blk) {
+        if (tid < AQ16) {
+            const int64_t rq = rq0 + tid / APARTS;
+            ra = rq < n_rq ? *reinterpret_cast<const uint4 *>(W + (rq * nblk + blk) * 4 * QB + (tid % APARTS) * 16)
+                           : make_uint4(0, 0, 0, 0);
+        }
+        if (tid < kTM / 4) {
+            const int64_t rq = rq0 + tid;
+            rs = rq < n_rq ? *reinterpret_cast<const uint2 *>(W + soff + (rq * nblk + blk) * 8) : make_uint2(0, 0);
+        }
+        fetch_b(tid, blk, rbh0, rbl0);
+        fetch_b(tid + 256, blk, rbh1, rbl1);
+        if (tid < kTN) {
+            const int64_t b = b0 + tid;
+            rx = b < batch ? xsum[b * nblk + blk] : 0.0f;
+        }
+    };
+    auto stage = [&](int buf) {
+        if (tid < AQ16) *reinterpret_cast<uint4 *>(aq[buf] + tid * 16) = ra;
+        if (tid < kTM / 4) asc[buf][tid] = rs;
+        *reinterpret_cast<uint4 *>(bh[buf] + (tid >> 2) * kBRow + (tid & 3) * 8) = rbh0;
+        *reinterpret_cast<uint4 *>(bl[buf] + (tid >> 2) * kBRow + (tid & 3) * 8) = rbl0;
+        *reinterpret_cast<uint4 *>(bh[buf] + ((tid + 256) >> 2) * kBRow + (tid & 3) * 8) = rbh1;
+        *reinterpret_cast<uint4 *>(bl[buf] + ((tid + 256) >> 2) * kBRow + (tid & 3) * 8) = rbl1;
+        if (tid < kTN) bs[buf][tid] = rx;
+    };
+
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[t][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](int buf) {
+        bf16x8_t af[4];
+        float d[4][4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int rql = wm * 16 + 4 * t + (l16 >> 2);       // A operand: weight row 16 t + l16
+            const uint2 w = *reinterpret_cast<const uint2 *>(aq[buf] + (rql * 4 + (l16 & 3)) * QB +
+                                                              (DT == VGX_Q8_0 ? 8 * lg : 8 * (lg & 1)));
+            af[t] = a_frag<DT>(w, lg);
+            const uint2 sc = asc[buf][wm * 16 + 4 * t + lg];     // accumulator rows 16 t + 4 lg .. + 3
+            d[t][0] = half_bits_to_float(sc.x);
+            d[t][1] = half_bits_to_float(sc.x >> 16);
+            d[t][2] = half_bits_to_float(sc.y);
+            d[t][3] = half_bits_to_float(sc.y >> 16);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int row = wn * 64 + 16 * c + l16;
+            const bf16x8_t hf = *reinterpret_cast<const bf16x8_t *>(bh[buf] + row * kBRow + 8 * lg);
+            const bf16x8_t lf = *reinterpret_cast<const bf16x8_t *>(bl[buf] + row * kBRow + 8 * lg);
+            const float ns = -OFF * bs[buf][row];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                f32x4_t pr = f32x4_t{ns, ns, ns, ns};
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], hf, pr, 0, 0, 0);
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], lf, pr, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf(d[t][i], pr[i], acc[t][c][i]);
+            }
+        }
+    };
+
+    if (blk_lo < blk_hi) {
+        fetch(blk_lo);
+        stage(0);
+    }
+    __syncthreads();
+    int cb = 0;
+    for (int blk = blk_lo; blk < blk_hi; ++blk) {
+        const bool more = blk + 1 < blk_hi;       // uniform over the workgroup
+        if (more) fetch(blk + 1);
+        compute(cb);
+        if (more) stage(cb ^ 1);
+        __syncthreads();
+        cb ^= 1;
     }
 
-    // Split K: raw per-split sums part[z][b][packed row]; the reduce kernel applies the epilogue.
-    if constexpr (SPLIT) {
-        const int64_t rows_p = n_rq * 4;
+    // lane holds weight rows 4 crq .. + 3 (crq = row-quad of tile t) of activation row b (tile c)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            if (!cok[t]) continue;
+    for (int t = 0; t < 4; ++t) {
+        const int64_t crq = rq0 + wm * 16 + 4 * t + lg;
+        if (crq >= n_rq) continue;
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                if (!bok[c]) continue;
+        for (int c = 0; c < 4; ++c) {
+            const int64_t b = b0 + wn * 64 + 16 * c + l16;
+            if (b >= batch) continue;
+            if constexpr (SPLIT) {
                 float4 v;
                 v.x = acc[t][c][0]; v.y = acc[t][c][1]; v.z = acc[t][c][2]; v.w = acc[t][c][3];
-                *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + bb[c]) * rows_p + crq[t] * 4) = v;
+                *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + b) * (n_rq * 4) + crq * 4) = v;
+                continue;
             }
-        }
-        return;
-    }
-    // Epilogue: lane holds rows 4 crq .. + 3 of activation row bb.
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        if (!cok[t]) continue;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            if (!bok[c]) continue;
-            float *yr = y + bb[c] * ldy;
+            float *yr = y + b * ldy;
             if constexpr (EPI == EPI_SWIGLU) {
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
-                    const int64_t o = crq[t] * 2 + k;
+                    const int64_t o = crq * 2 + k;
                     if (o >= rows_out) continue;
                     const float g = acc[t][c][k], u = acc[t][c][2 + k];
                     yr[o] = g / (1.0f + __expf(-g)) * u;
@@ -258,7 +266,7 @@ __global__ __launch_bounds__(256) void qgemm_kernel(const uint8_t *__restrict__ 
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int64_t row = crq[t] * 4 + i;
+                    const int64_t row = crq * 4 + i;
                     if (row >= rows_out) continue;
                     float v = acc[t][c][i];
                     if (bias) v += bias[row];
@@ -578,6 +586,14 @@ int choose_ksplit(int64_t n_rq, int64_t batch, int nc, int nblk) {
     return (int)std::max<int64_t>(1, ks);
 }
 
+// K splits of the tiled kernel: about two workgroups per CU, at least 8 blocks per split.
+int tile_ksplit(int64_t n_rq, int64_t batch, int nblk) {
+    const int64_t tiles = (n_rq + kTM / 4 - 1) / (kTM / 4) * ((batch + kTN - 1) / kTN);
+    int64_t ks = (512 + tiles - 1) / tiles;
+    ks = std::min<int64_t>(ks, std::min<int64_t>(kMaxKSplit, nblk / 8));
+    return (int)std::max<int64_t>(1, ks);
+}
+
 inline int64_t part_bytes(int ks, int64_t batch, int64_t rows_p) {
     return ks > 1 ? ((int64_t)ks * batch * rows_p * 4 + 255) / 256 * 256 : 0;
 }
@@ -611,8 +627,7 @@ int64_t vgx_qgemm_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, int
     if (batch <= 0 || rows <= 0 || cols <= 0) return VGX_E_SIZE;
     if (cols % QK) return VGX_E_SHAPE;
     const int64_t rows_p = rows4(epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows);
-    const int nc = batch <= 16 ? 1 : 2;
-    const int ks = choose_ksplit(rows_p / 4, batch, nc, (int)(cols / QK));
+    const int ks = tile_ksplit(rows_p / 4, batch, (int)(cols / QK));
     const int64_t big = split_bytes(batch, cols) + part_bytes(ks, batch, rows_p);
     return batch <= kSmallMaxBatch ? std::max(big, small_bytes(batch, rows_p / 4, (int)(cols / QK))) : big;
 }
@@ -680,8 +695,7 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
         }
         return VGX_OK;
     }
-    const int nc = batch <= 16 ? 1 : 2;
-    const int ks = choose_ksplit(n_rq, batch, nc, nblk);
+    const int ks = tile_ksplit(n_rq, batch, nblk);
     if (!workspace || workspace_bytes < split_bytes(batch, cols) + part_bytes(ks, batch, n_rq * 4)) return VGX_E_ARENA;
     if ((uintptr_t)workspace % 256) return VGX_E_ALIGN;
     const int64_t soff = gemm_scale_off(dtype, rows_packed, cols);
@@ -694,23 +708,20 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     VGX_CHECK_LAUNCH();
     auto *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + split_bytes(batch, cols));
     const int kper = (nblk + ks - 1) / ks;
-    const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 16 * nc - 1) / (16 * nc)), (unsigned)ks);
+    const dim3 grid((unsigned)((n_rq + kTM / 4 - 1) / (kTM / 4)), (unsigned)((batch + kTN - 1) / kTN), (unsigned)ks);
     const auto *w = static_cast<const uint8_t *>(w_packed);
-#define VGX_GEMM_GO(DT, NC, EPI, SP)                                                                      \
-    hipLaunchKernelGGL((qgemm_kernel<DT, NC, EPI, SP>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, xh, xl, \
+#define VGX_GEMM_GO(DT, EPI, SP)                                                                              \
+    hipLaunchKernelGGL((qgemm_tile_kernel<DT, EPI, SP>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, xh, xl, \
                        xs, batch, bias, y, ldy, part, kper)
-#define VGX_GEMM_EPI(DT, NC)                                                                              \
-    do {                                                                                                  \
-        if (ks > 1) VGX_GEMM_GO(DT, NC, EPI_STORE, true);                                                 \
-        else if (epilogue == VGX_EPI_SWIGLU) VGX_GEMM_GO(DT, NC, EPI_SWIGLU, false);                      \
-        else if (epilogue == VGX_EPI_ACCUM) VGX_GEMM_GO(DT, NC, EPI_ACCUM, false);                        \
-        else VGX_GEMM_GO(DT, NC, EPI_STORE, false);                                                       \
+#define VGX_GEMM_EPI(DT)                                                                                      \
+    do {                                                                                                      \
+        if (ks > 1) VGX_GEMM_GO(DT, EPI_STORE, true);                                                         \
+        else if (epilogue == VGX_EPI_SWIGLU) VGX_GEMM_GO(DT, EPI_SWIGLU, false);                              \
+        else if (epilogue == VGX_EPI_ACCUM) VGX_GEMM_GO(DT, EPI_ACCUM, false);                                \
+        else VGX_GEMM_GO(DT, EPI_STORE, false);                                                               \
     } while (0)
-    if (dtype == VGX_Q8_0) {
-        if (nc == 1) VGX_GEMM_EPI(VGX_Q8_0, 1); else VGX_GEMM_EPI(VGX_Q8_0, 2);
-    } else {
-        if (nc == 1) VGX_GEMM_EPI(VGX_Q4_0, 1); else VGX_GEMM_EPI(VGX_Q4_0, 2);
-    }
+    if (dtype == VGX_Q8_0) VGX_GEMM_EPI(VGX_Q8_0);
+    else VGX_GEMM_EPI(VGX_Q4_0);
 #undef VGX_GEMM_EPI
 #undef VGX_GEMM_GO
     VGX_CHECK_LAUNCH();
