@@ -28,8 +28,13 @@ CFLAGS = [
 ]
 
 
+# Per-file code generation options.  qgemm: MFMA results in VGPRs rather than AGPRs (its per-block
+# scaling reads every MFMA result once; from AGPRs each read is an extra VALU move).
+FILE_FLAGS = {"qgemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str, obj: str) -> None:
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")

@@ -31,6 +31,8 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // u = (norm ? lnw * x * inv_rms : x); writes hi / lo bf16 rows and per-block sums of hi + lo.
+// Inside every group of four, elements 1 and 2 trade places (stored order 0, 2, 1, 3): the K-slot
+// order of the tiled kernel's weight fragments, whose Q4_0 nibble pairs come out of a word that way.
 // One workgroup of 256 threads per activation row.
 __global__ __launch_bounds__(256) void xsplit_kernel(const float *__restrict__ x, int64_t ldx,
                                                       const float *__restrict__ lnw, float eps, int cols,
@@ -61,8 +63,9 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float *__restrict__ x
             if (lnw) u = lnw[c] * (u * inv);
             const uint32_t hb = float_to_bf16_bits(u);
             const uint32_t lb = float_to_bf16_bits(u - bf16_bits_to_float(hb));
-            xh[b * cols + c] = (uint16_t)hb;
-            xl[b * cols + c] = (uint16_t)lb;
+            const int cs = (c & ~3) | ((c & 1) << 1) | ((c >> 1) & 1);
+            xh[b * cols + cs] = (uint16_t)hb;
+            xl[b * cols + cs] = (uint16_t)lb;
             hs = bf16_bits_to_float(hb) + bf16_bits_to_float(lb);
         }
         // sum over the 32 lanes of each half-wave
@@ -118,6 +121,33 @@ constexpr int kTM = 128;                 // weight rows per workgroup tile
 constexpr int kTN = 128;                 // activation rows per workgroup tile
 constexpr int kBRow = QK + 8;            // bf16 per staged activation row (16 B of padding)
 
+// Weights 8 lg .. 8 lg + 7 of the block as the tiled kernel's A fragment, in K-slot order
+// 0, 2, 1, 3, 4, 6, 5, 7 (the split pre-pass stores the activations in the same order).  Q4_0: one
+// AND-OR per two weights gives bf16(128 + n) exactly (exponent of 128, nibble in the mantissa), so the
+// block's offset is 136; Q8_0: q + 128 through the byte conversions.
+template <int DT>
+__device__ __forceinline__ bf16x8_t tile_a_frag(uint2 w, int lg) {
+    uint32_t o[4];
+    if constexpr (DT == VGX_Q4_0) {
+        const int sh = (lg >> 1) * 4;   // low nibbles for weights 0..15, high nibbles for 16..31
+        const uint32_t u0 = w.x >> sh, u1 = w.y >> sh;
+        o[0] = (u0 & 0x000F000Fu) | 0x43004300u;           // weights 0, 2 of the word
+        o[1] = ((u0 >> 8) & 0x000F000Fu) | 0x43004300u;    // weights 1, 3
+        o[2] = (u1 & 0x000F000Fu) | 0x43004300u;
+        o[3] = ((u1 >> 8) & 0x000F000Fu) | 0x43004300u;
+    } else {
+        const uint32_t u[2] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float f0 = (float)(u[i] & 0xFFu), f1 = (float)((u[i] >> 8) & 0xFFu);
+            const float f2 = (float)((u[i] >> 16) & 0xFFu), f3 = (float)(u[i] >> 24);
+            o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f2) & 0xFFFF0000u);
+            o[2 * i + 1] = (__float_as_uint(f1) >> 16) | (__float_as_uint(f3) & 0xFFFF0000u);
+        }
+    }
+    return __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
+}
+
 template <int DT, int EPI, bool SPLIT>
 __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
                                                           int nblk, int64_t rows_out,
@@ -127,7 +157,7 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
                                                           const float *__restrict__ bias, float *__restrict__ y,
                                                           int64_t ldy, float *__restrict__ part, int kper) {
     constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
-    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 8.0f;
+    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 136.0f;
     constexpr int APARTS = 4 * QB / 16;                  // 16-byte pieces of one row-quad block
     constexpr int AQ16 = kTM / 4 * APARTS;               // 16-byte pieces of the tile's block
     __shared__ __align__(16) uint8_t aq[2][kTM * QB];    // [row-quad][row][QB] as in the packed weights
@@ -200,7 +230,7 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
             const int rql = wm * 16 + 4 * t + (l16 >> 2);       // A operand: weight row 16 t + l16
             const uint2 w = *reinterpret_cast<const uint2 *>(aq[buf] + (rql * 4 + (l16 & 3)) * QB +
                                                               (DT == VGX_Q8_0 ? 8 * lg : 8 * (lg & 1)));
-            af[t] = a_frag<DT>(w, lg);
+            af[t] = tile_a_frag<DT>(w, lg);
             const uint2 sc = asc[buf][wm * 16 + 4 * t + lg];     // accumulator rows 16 t + 4 lg .. + 3
             d[t][0] = half_bits_to_float(sc.x);
             d[t][1] = half_bits_to_float(sc.x >> 16);
