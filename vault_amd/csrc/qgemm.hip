@@ -51,27 +51,44 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float *__restrict__ x
         inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)cols + eps);
     }
     const int nblk = cols / QK;
-    // a wave handles blocks, a lane two consecutive elements (64 lanes = 2 blocks per step)
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int blk0 = wave * 2; blk0 < nblk; blk0 += 8) {
-        const int blk = blk0 + (lane >> 5);
-        const bool ok = blk < nblk;
-        float hs = 0.0f;
+    // a thread converts four consecutive elements (one 16-byte load, two 8-byte stores per plane);
+    // the eight threads of a block sum its hi + lo
+    const int n4 = cols / 4;
+    const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+    const float4 *g4 = reinterpret_cast<const float4 *>(lnw);
+    const bool vec = ((uintptr_t)xr & 15) == 0 && (lnw == nullptr || ((uintptr_t)lnw & 15) == 0);
+    for (int i0 = 0; i0 < n4; i0 += 256) {
+        const int i = i0 + (int)threadIdx.x;
+        const bool ok = i < n4;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (ok) {
-            const int c = blk * QK + (lane & 31);
-            float u = xr[c];
-            if (lnw) u = lnw[c] * (u * inv);
-            const uint32_t hb = float_to_bf16_bits(u);
-            const uint32_t lb = float_to_bf16_bits(u - bf16_bits_to_float(hb));
-            const int cs = (c & ~3) | ((c & 1) << 1) | ((c >> 1) & 1);
-            xh[b * cols + cs] = (uint16_t)hb;
-            xl[b * cols + cs] = (uint16_t)lb;
-            hs = bf16_bits_to_float(hb) + bf16_bits_to_float(lb);
+            if (vec) {
+                v = x4[i];
+            } else {
+                v.x = xr[4 * i]; v.y = xr[4 * i + 1]; v.z = xr[4 * i + 2]; v.w = xr[4 * i + 3];
+            }
+            if (lnw) {
+                float4 g;
+                if (vec) g = g4[i];
+                else { g.x = lnw[4 * i]; g.y = lnw[4 * i + 1]; g.z = lnw[4 * i + 2]; g.w = lnw[4 * i + 3]; }
+                v.x = g.x * (v.x * inv); v.y = g.y * (v.y * inv); v.z = g.z * (v.z * inv); v.w = g.w * (v.w * inv);
+            }
         }
-        // sum over the 32 lanes of each half-wave
-        hs = row16_sum(hs);
-        hs += __shfl_xor(hs, 16, kWave);
-        if (ok && (lane & 31) == 0) xsum[b * nblk + blk] = hs;
+        uint32_t h02, l02, h13, l13;   // stored order 0, 2, 1, 3
+        split_bf16x2(v.x, v.z, h02, l02);
+        split_bf16x2(v.y, v.w, h13, l13);
+        auto lo16 = [](uint32_t w) { return __uint_as_float(w << 16); };
+        auto hi16 = [](uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); };
+        float hs = (lo16(h02) + lo16(l02)) + (lo16(h13) + lo16(l13)) + (hi16(h02) + hi16(l02)) +
+                   (hi16(h13) + hi16(l13));
+        if (ok) {
+            *reinterpret_cast<uint2 *>(xh + b * cols + 4 * i) = make_uint2(h02, h13);
+            *reinterpret_cast<uint2 *>(xl + b * cols + 4 * i) = make_uint2(l02, l13);
+        }
+        hs += __shfl_xor(hs, 1, kWave);
+        hs += __shfl_xor(hs, 2, kWave);
+        hs += __shfl_xor(hs, 4, kWave);
+        if (ok && (i & 7) == 0) xsum[b * nblk + i / 8] = hs;
     }
 }
 
