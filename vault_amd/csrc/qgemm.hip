@@ -177,11 +177,17 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
     constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 136.0f;
     constexpr int APARTS = 4 * QB / 16;                  // 16-byte pieces of one row-quad block
     constexpr int AQ16 = kTM / 4 * APARTS;               // 16-byte pieces of the tile's block
-    __shared__ __align__(16) uint8_t aq[2][kTM * QB];    // [row-quad][row][QB] as in the packed weights
-    __shared__ __align__(16) uint2 asc[2][kTM / 4];      // four fp16 scales per row-quad
-    __shared__ __align__(16) uint16_t bh[2][kTN * kBRow];
-    __shared__ __align__(16) uint16_t bl[2][kTN * kBRow];
-    __shared__ float bs[2][kTN];
+    // Stage buffers (two blocks) and, after the K loop, the epilogue's half tile share one LDS area.
+    constexpr int A_B = kTM * QB, SC_B = kTM / 4 * 8, BH_B = kTN * kBRow * 2, BS_B = kTN * 4;
+    constexpr int STAGE_B = A_B + SC_B + 2 * BH_B + BS_B;
+    constexpr int kERow = 64 + 4;                          // floats per activation row of a half tile
+    constexpr int EPI_B = kTN * kERow * 4;
+    __shared__ __align__(16) uint8_t smem[2 * STAGE_B > EPI_B ? 2 * STAGE_B : EPI_B];
+    auto aq = [&](int buf) { return smem + buf * STAGE_B; };                         // [row-quad][row][QB]
+    auto asc = [&](int buf) { return reinterpret_cast<uint2 *>(smem + buf * STAGE_B + A_B); };
+    auto bh = [&](int buf) { return reinterpret_cast<uint16_t *>(smem + buf * STAGE_B + A_B + SC_B); };
+    auto bl = [&](int buf) { return reinterpret_cast<uint16_t *>(smem + buf * STAGE_B + A_B + SC_B + BH_B); };
+    auto bs = [&](int buf) { return reinterpret_cast<float *>(smem + buf * STAGE_B + A_B + SC_B + 2 * BH_B); };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, lg = lane >> 4;
@@ -193,9 +199,13 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
     const int blk_hi = SPLIT ? min(nblk, blk_lo + kper) : nblk;
 
     // global -> registers (one block), registers -> LDS buffer
-    uint4 ra = make_uint4(0, 0, 0, 0), rbh0, rbh1, rbl0, rbl1;
-    uint2 rs = make_uint2(0, 0);
-    float rx = 0.0f;
+    // one block's staging registers; two sets, so the loads of block k + 2 leave while block k is
+    // multiplied and block k + 1 waits in the other set
+    struct Regs {
+        uint4 ra, h0, h1, l0, l1;
+        uint2 rs;
+        float rx;
+    };
     auto fetch_b = [&](int idx, int blk, uint4 &h, uint4 &l) {
         const int row = idx >> 2, pc = idx & 3;
         const int64_t b = b0 + row;
@@ -207,31 +217,33 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
             h = l = make_uint4(0, 0, 0, 0);
         }
     };
-    auto fetch = [&](int blk) {
+    auto fetch = [&](Regs &r, int blk) {
+        r.ra = make_uint4(0, 0, 0, 0);
+        r.rs = make_uint2(0, 0);
+        r.rx = 0.0f;
         if (tid < AQ16) {
             const int64_t rq = rq0 + tid / APARTS;
-            ra = rq < n_rq ? *reinterpret_cast<const uint4 *>(W + (rq * nblk + blk) * 4 * QB + (tid % APARTS) * 16)
-                           : make_uint4(0, 0, 0, 0);
+            if (rq < n_rq) r.ra = *reinterpret_cast<const uint4 *>(W + (rq * nblk + blk) * 4 * QB + (tid % APARTS) * 16);
         }
         if (tid < kTM / 4) {
             const int64_t rq = rq0 + tid;
-            rs = rq < n_rq ? *reinterpret_cast<const uint2 *>(W + soff + (rq * nblk + blk) * 8) : make_uint2(0, 0);
+            if (rq < n_rq) r.rs = *reinterpret_cast<const uint2 *>(W + soff + (rq * nblk + blk) * 8);
         }
-        fetch_b(tid, blk, rbh0, rbl0);
-        fetch_b(tid + 256, blk, rbh1, rbl1);
+        fetch_b(tid, blk, r.h0, r.l0);
+        fetch_b(tid + 256, blk, r.h1, r.l1);
         if (tid < kTN) {
             const int64_t b = b0 + tid;
-            rx = b < batch ? xsum[b * nblk + blk] : 0.0f;
+            if (b < batch) r.rx = xsum[b * nblk + blk];
         }
     };
-    auto stage = [&](int buf) {
-        if (tid < AQ16) *reinterpret_cast<uint4 *>(aq[buf] + tid * 16) = ra;
-        if (tid < kTM / 4) asc[buf][tid] = rs;
-        *reinterpret_cast<uint4 *>(bh[buf] + (tid >> 2) * kBRow + (tid & 3) * 8) = rbh0;
-        *reinterpret_cast<uint4 *>(bl[buf] + (tid >> 2) * kBRow + (tid & 3) * 8) = rbl0;
-        *reinterpret_cast<uint4 *>(bh[buf] + ((tid + 256) >> 2) * kBRow + (tid & 3) * 8) = rbh1;
-        *reinterpret_cast<uint4 *>(bl[buf] + ((tid + 256) >> 2) * kBRow + (tid & 3) * 8) = rbl1;
-        if (tid < kTN) bs[buf][tid] = rx;
+    auto stage = [&](const Regs &r, int buf) {
+        if (tid < AQ16) *reinterpret_cast<uint4 *>(aq(buf) + tid * 16) = r.ra;
+        if (tid < kTM / 4) asc(buf)[tid] = r.rs;
+        *reinterpret_cast<uint4 *>(bh(buf) + (tid >> 2) * kBRow + (tid & 3) * 8) = r.h0;
+        *reinterpret_cast<uint4 *>(bl(buf) + (tid >> 2) * kBRow + (tid & 3) * 8) = r.l0;
+        *reinterpret_cast<uint4 *>(bh(buf) + ((tid + 256) >> 2) * kBRow + (tid & 3) * 8) = r.h1;
+        *reinterpret_cast<uint4 *>(bl(buf) + ((tid + 256) >> 2) * kBRow + (tid & 3) * 8) = r.l1;
+        if (tid < kTN) bs(buf)[tid] = r.rx;
     };
 
     f32x4_t acc[4][4];
@@ -245,10 +257,10 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int rql = wm * 16 + 4 * t + (l16 >> 2);       // A operand: weight row 16 t + l16
-            const uint2 w = *reinterpret_cast<const uint2 *>(aq[buf] + (rql * 4 + (l16 & 3)) * QB +
+            const uint2 w = *reinterpret_cast<const uint2 *>(aq(buf) + (rql * 4 + (l16 & 3)) * QB +
                                                               (DT == VGX_Q8_0 ? 8 * lg : 8 * (lg & 1)));
             af[t] = tile_a_frag<DT>(w, lg);
-            const uint2 sc = asc[buf][wm * 16 + 4 * t + lg];     // accumulator rows 16 t + 4 lg .. + 3
+            const uint2 sc = asc(buf)[wm * 16 + 4 * t + lg];     // accumulator rows 16 t + 4 lg .. + 3
             d[t][0] = half_bits_to_float(sc.x);
             d[t][1] = half_bits_to_float(sc.x >> 16);
             d[t][2] = half_bits_to_float(sc.y);
@@ -257,9 +269,9 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int row = wn * 64 + 16 * c + l16;
-            const bf16x8_t hf = *reinterpret_cast<const bf16x8_t *>(bh[buf] + row * kBRow + 8 * lg);
-            const bf16x8_t lf = *reinterpret_cast<const bf16x8_t *>(bl[buf] + row * kBRow + 8 * lg);
-            const float ns = -OFF * bs[buf][row];
+            const bf16x8_t hf = *reinterpret_cast<const bf16x8_t *>(bh(buf) + row * kBRow + 8 * lg);
+            const bf16x8_t lf = *reinterpret_cast<const bf16x8_t *>(bl(buf) + row * kBRow + 8 * lg);
+            const float ns = -OFF * bs(buf)[row];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 f32x4_t pr = f32x4_t{ns, ns, ns, ns};
@@ -271,57 +283,85 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
         }
     };
 
+    // Blocks k (LDS buffer k % 2), k + 1 (register set (k + 1) % 2), k + 2 (loads in flight).
+    Regs ra, rb;
     if (blk_lo < blk_hi) {
-        fetch(blk_lo);
-        stage(0);
+        fetch(ra, blk_lo);
+        if (blk_lo + 1 < blk_hi) fetch(rb, blk_lo + 1);
+        stage(ra, 0);
     }
     __syncthreads();
-    int cb = 0;
-    for (int blk = blk_lo; blk < blk_hi; ++blk) {
-        const bool more = blk + 1 < blk_hi;       // uniform over the workgroup
-        if (more) fetch(blk + 1);
-        compute(cb);
-        if (more) stage(cb ^ 1);
+    for (int blk = blk_lo; blk < blk_hi; blk += 2) {
+        // even step: block blk in buffer 0, block blk + 1 in rb; ra is free
+        if (blk + 2 < blk_hi) fetch(ra, blk + 2);
+        compute(0);
+        if (blk + 1 < blk_hi) stage(rb, 1);
         __syncthreads();
-        cb ^= 1;
+        if (blk + 1 >= blk_hi) break;
+        // odd step: block blk + 1 in buffer 1, block blk + 2 in ra; rb is free
+        if (blk + 3 < blk_hi) fetch(rb, blk + 3);
+        compute(1);
+        if (blk + 2 < blk_hi) stage(ra, 0);
+        __syncthreads();
     }
 
-    // lane holds weight rows 4 crq .. + 3 (crq = row-quad of tile t) of activation row b (tile c)
+    // Epilogue.  Split K: the raw sums, float4 per (tile, lane).  Otherwise the tile goes through LDS
+    // in two halves of 64 weight rows (waves wm = 0, then wm = 1 write theirs), and all threads then
+    // apply bias / residual / SwiGLU and store rows of y with consecutive threads on consecutive
+    // outputs.
+    if constexpr (SPLIT) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int64_t crq = rq0 + wm * 16 + 4 * t + lg;
-        if (crq >= n_rq) continue;
+        for (int t = 0; t < 4; ++t) {
+            const int64_t crq = rq0 + wm * 16 + 4 * t + lg;
+            if (crq >= n_rq) continue;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int64_t b = b0 + wn * 64 + 16 * c + l16;
-            if (b >= batch) continue;
-            if constexpr (SPLIT) {
+            for (int c = 0; c < 4; ++c) {
+                const int64_t b = b0 + wn * 64 + 16 * c + l16;
+                if (b >= batch) continue;
                 float4 v;
                 v.x = acc[t][c][0]; v.y = acc[t][c][1]; v.z = acc[t][c][2]; v.w = acc[t][c][3];
                 *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + b) * (n_rq * 4) + crq * 4) = v;
-                continue;
-            }
-            float *yr = y + b * ldy;
-            if constexpr (EPI == EPI_SWIGLU) {
-#pragma unroll
-                for (int k = 0; k < 2; ++k) {
-                    const int64_t o = crq * 2 + k;
-                    if (o >= rows_out) continue;
-                    const float g = acc[t][c][k], u = acc[t][c][2 + k];
-                    yr[o] = g / (1.0f + __expf(-g)) * u;
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int64_t row = crq * 4 + i;
-                    if (row >= rows_out) continue;
-                    float v = acc[t][c][i];
-                    if (bias) v += bias[row];
-                    if constexpr (EPI == EPI_ACCUM) v += yr[row];
-                    yr[row] = v;
-                }
             }
         }
+        return;
+    }
+    float *et = reinterpret_cast<float *>(smem);       // [activation row][64 weight rows + pad]
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        if (wm == half) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float4 v;
+                    v.x = acc[t][c][0]; v.y = acc[t][c][1]; v.z = acc[t][c][2]; v.w = acc[t][c][3];
+                    *reinterpret_cast<float4 *>(et + (wn * 64 + 16 * c + l16) * kERow + 16 * t + 4 * lg) = v;
+                }
+        }
+        __syncthreads();
+        const int64_t r0 = (rq0 + half * 16) * 4;           // first packed weight row of this half
+        if constexpr (EPI == EPI_SWIGLU) {
+            // packed row-quad q: rows (gate 2q, gate 2q + 1, up 2q, up 2q + 1) -> outputs 2q, 2q + 1
+            for (int i = tid; i < kTN * 32; i += 256) {
+                const int bl_ = i >> 5, o = i & 31;
+                const int64_t b = b0 + bl_, oo = r0 / 2 + o;
+                if (b >= batch || oo >= rows_out) continue;
+                const float *er = et + bl_ * kERow + (o >> 1) * 4 + (o & 1);
+                const float g = er[0], u = er[2];
+                y[b * ldy + oo] = g / (1.0f + __expf(-g)) * u;
+            }
+        } else {
+            for (int i = tid; i < kTN * 64; i += 256) {
+                const int bl_ = i >> 6, rr = i & 63;
+                const int64_t b = b0 + bl_, row = r0 + rr;
+                if (b >= batch || row >= rows_out) continue;
+                float v = et[bl_ * kERow + rr];
+                if (bias) v += bias[row];
+                if constexpr (EPI == EPI_ACCUM) v += y[b * ldy + row];
+                y[b * ldy + row] = v;
+            }
+        }
+        __syncthreads();
     }
 }
 
