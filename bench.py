@@ -160,6 +160,34 @@ def gemv_figures(dev, batches=(1, 16), reps: int = 20):
     return out
 
 
+def gemm_figures(dev, rows_in: int = 1024, reps: int = 10):
+    """Q4_0 projection GEMMs of one 1024-token prefill chunk (q|k|v, o, gate/up with SwiGLU, down),
+    bf16 MFMA: TFLOP/s of 2 * tokens * in * out (gate/up: both halves) against 2.5 PFLOP/s dense bf16.
+    Each figure includes the activation split pre-pass and, where K is split, the reduce launch."""
+    import numpy as np
+    import torch
+    from vault_amd import ops, vlt3
+    rng = np.random.default_rng(9)
+    dt = vlt3.Q4_0
+    out = []
+    for name, rows, cols, gu in (("qkv", 2048, 1536, False), ("o", 1536, 1536, False),
+                                 ("gate_up", 8960, 1536, True), ("down", 1536, 8960, False)):
+        if gu:
+            w = ops.QWeight.gateup_from_blocks(dt, rows, cols, vlt3.synthetic_blocks(dt, rows, cols, rng),
+                                               vlt3.synthetic_blocks(dt, rows, cols, rng), dev)
+        else:
+            w = ops.QWeight.from_blocks(dt, rows, cols, vlt3.synthetic_blocks(dt, rows, cols, rng), dev)
+        x = torch.randn(rows_in, cols, device=dev)
+        y = torch.empty(rows_in, rows, device=dev)
+        run = (lambda: ops.qlinear_swiglu(w, x, out=y)) if gu else (lambda: ops.qlinear(w, x, out=y))
+        us = graph_time_us(run, 1, reps=reps)
+        fl = 2.0 * rows_in * cols * rows * (2 if gu else 1)
+        out.append({"proj": name, "dtype": "q4_0", "tokens": rows_in, "out": rows, "in": cols, "us": round(us, 1),
+                    "tflops": round(fl / us / 1e6, 1), "frac": round(fl / us / 1e6 / 2500.0, 4)})
+        del w
+    return out
+
+
 def attn_figures(dev, reps: int = 20):
     """Batched decode attention, bf16 KV: B=64, 12 q / 2 KV heads, D=128, keys 512 sink + 1024 segment
     + 2048 window = 3584; algorithmic bytes = K and V once (234,881,024 B) + q + out."""
@@ -373,6 +401,7 @@ def main() -> int:
         kernels["gemv"] = gemv_figures(dev)
         kernels["attn_decode"] = attn_figures(dev)
         kernels["attn_prefill"] = prefill_figures(dev)
+        kernels["gemm_prefill"] = gemm_figures(dev)
         if args.batch == 1:
             kernels["decode_batch32"] = batched_decode(model)
         _log("kernel figures done")

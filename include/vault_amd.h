@@ -123,8 +123,10 @@ int64_t vgx_qgemm_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, int
 /* vgx_qlinear_ex for many activation rows on bf16 MFMA (Q8_0 / Q4_0 weights): same arguments and
  * epilogues, plus a caller workspace.  The activations (after the optional RMSNorm) enter as a bf16
  * hi + lo pair (2^-17 relative); weights, scales and the per-block fp32 accumulation are exact as in
- * the GEMV.  Replaces the chunk-prefill projections (src/vault_v3_model.py:2051, 2095-2096 on
- * [clen x d] blocks) and batched decode projections. */
+ * the GEMV.  F32 weights run on fp32 MFMA (fp32 products and sums; no RMSNorm prologue on that path:
+ * norm_w must be NULL; no workspace).  Replaces the chunk-prefill projections
+ * (src/vault_v3_model.py:2051, 2095-2096 on [clen x d] blocks), batched decode projections, and the
+ * segment scorer's fc1 over a chunk (:1224-1247). */
 int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx, int64_t batch,
               const float *norm_w, float eps, const float *bias, float *y, int64_t ldy, int epilogue, void *workspace,
               int64_t workspace_bytes, void *stream);

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from oracle import codec, linalg
+from vault_amd import _lib as L
 from vault_amd import ops, vlt3
 
 pytestmark = pytest.mark.gpu
@@ -93,3 +94,46 @@ def test_qgemm_k_split_edges(dev, dt, rows, cols, batch):
     ref = linalg.gemv(wf, x)
     tol = linalg.gemv_bound(wf, x, dt, rel=8e-6)
     assert np.all(np.abs(y - ref) <= tol)
+
+
+@pytest.mark.parametrize("rows,cols,batch,epi", [
+    (256, 4608, 2048, "store"), (130, 96, 77, "accum"), (64, 160, 300, "swiglu"), (13, 32, 40, "store")])
+def test_f32_gemm_matches_oracle(dev, rows, cols, batch, epi):
+    """F32 weights over many rows (the scorer's fc1 over a chunk: 4608 -> 256 on 2 x 1024 rows) run the
+    fp32-MFMA GEMM; bar: the fp32 accumulation bound of the fp64 oracle."""
+    rng = np.random.default_rng(rows * 7 + cols + batch)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    xt = torch.from_numpy(x).to(dev)
+    if epi == "swiglu":
+        g = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        u = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+        w = ops.QWeight.gateup_from_blocks(codec.F32, rows, cols, g.tobytes(), u.tobytes(), dev)
+        h = ops.qlinear_swiglu(w, xt).cpu().numpy().astype(np.float64)
+        gg, uu = linalg.gemv(g.astype(np.float64), x), linalg.gemv(u.astype(np.float64), x)
+        ref = linalg.swiglu(gg, uu)
+        tg = linalg.gemv_bound(g, x, codec.F32, rel=8e-6)
+        tu = linalg.gemv_bound(u, x, codec.F32, rel=8e-6)
+        tol = 1.1 * np.abs(uu) * tg + np.abs(gg) * tu + 1e-6 * np.abs(ref) + 1e-30
+        assert np.all(np.abs(h - ref) <= tol)
+        return
+    wm = (rng.standard_normal((rows, cols)) * 0.05).astype(np.float32)
+    wq = ops.QWeight.from_blocks(codec.F32, rows, cols, wm.tobytes(), dev)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    ref = linalg.gemv(wm.astype(np.float64), x, bias)
+    out = None
+    if epi == "accum":
+        y0 = rng.standard_normal((batch, rows)).astype(np.float32)
+        ref = ref + y0
+        out = torch.from_numpy(y0).to(dev)
+    y = ops.qlinear(wq, xt, bias=torch.from_numpy(bias).to(dev), out=out,
+                    accumulate=epi == "accum").cpu().numpy().astype(np.float64)
+    tol = linalg.gemv_bound(wm, x, codec.F32, rel=8e-6) + np.abs(ref) * 2e-7
+    assert np.all(np.abs(y - ref) <= tol), float((np.abs(y - ref) / tol).max())
+
+
+def test_f32_gemm_rejects_rmsnorm(dev):
+    lib = L.load()
+    z = torch.zeros(1 << 16, device=dev)
+    p = z.data_ptr()
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib.vgx_qgemm(L.F32, p, 64, 64, p, 64, 100, p, 1e-6, None, p, 64, L.EPI_STORE, None, 0, s) < 0

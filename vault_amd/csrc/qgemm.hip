@@ -366,6 +366,122 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
 }
 
 // ---------------------------------------------------------------------------------------------
+// F32 weights (the segment scorer's fc1, F32 model files) for many activation rows: fp32 MFMA
+// (v_mfma_f32_16x16x4_f32), so products and sums stay fp32 as in the reference.  A workgroup of 4
+// waves owns 64 weight rows x 64 activation rows (each wave 32 x 32 as 2 x 2 tiles); per 32-wide
+// block of K the workgroup stages both 64 x 32 fp32 tiles in LDS (double-buffered, one barrier per
+// block, next block's loads in flight during the current one's MFMAs).  Weights are read from the
+// packed row-quad layout (a row-quad block is 4 rows x 32 floats, contiguous).
+constexpr int kFT = 64;                   // rows of each operand per workgroup tile
+constexpr int kFRow = QK + 1;             // floats per staged row (one float of padding)
+
+template <int EPI, bool VEC>
+__global__ __launch_bounds__(256) void f32gemm_tile_kernel(const float *__restrict__ W, int64_t n_rq, int nblk,
+                                                           int64_t rows_out, const float *__restrict__ x,
+                                                           int64_t ldx, int64_t batch, const float *__restrict__ bias,
+                                                           float *__restrict__ y, int64_t ldy) {
+    __shared__ float as[2][kFT * kFRow];
+    __shared__ float bs[2][kFT * kFRow];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int64_t rq0 = (int64_t)blockIdx.x * (kFT / 4);
+    const int64_t b0 = (int64_t)blockIdx.y * kFT;
+
+    float4 ra[2], rb[2];
+    auto fetch = [&](int blk) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + 256 * i;
+            // weights: row-quad idx / 32, row (idx / 8) % 4, float4 idx % 8 of the block
+            const int64_t rq = rq0 + (idx >> 5);
+            ra[i] = rq < n_rq ? reinterpret_cast<const float4 *>(W + ((rq * nblk + blk) * 4 + ((idx >> 3) & 3)) * QK)[idx & 7]
+                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const int64_t b = b0 + (idx >> 3);
+            if (b < batch) {
+                const float *xp = x + b * ldx + (int64_t)blk * QK + (idx & 7) * 4;
+                if constexpr (VEC) rb[i] = *reinterpret_cast<const float4 *>(xp);
+                else rb[i] = make_float4(xp[0], xp[1], xp[2], xp[3]);
+            } else {
+                rb[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        }
+    };
+    auto stage = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + 256 * i, row = idx >> 3, c = (idx & 7) * 4;
+            float *pa = as[buf] + row * kFRow + c;
+            pa[0] = ra[i].x; pa[1] = ra[i].y; pa[2] = ra[i].z; pa[3] = ra[i].w;
+            float *pb = bs[buf] + row * kFRow + c;
+            pb[0] = rb[i].x; pb[1] = rb[i].y; pb[2] = rb[i].z; pb[3] = rb[i].w;
+        }
+    };
+    f32x4_t acc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc[t][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int kk = 0; kk < QK / 4; ++kk) {
+            float a[2], b[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) a[t] = as[buf][(wm * 32 + 16 * t + l16) * kFRow + 4 * kk + lg];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) b[c] = bs[buf][(wn * 32 + 16 * c + l16) * kFRow + 4 * kk + lg];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) acc[t][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t], b[c], acc[t][c], 0, 0, 0);
+        }
+    };
+    fetch(0);
+    stage(0);
+    __syncthreads();
+    int cb = 0;
+    for (int blk = 0; blk < nblk; ++blk) {
+        const bool more = blk + 1 < nblk;
+        if (more) fetch(blk + 1);
+        compute(cb);
+        if (more) stage(cb ^ 1);
+        __syncthreads();
+        cb ^= 1;
+    }
+    // lane holds weight rows 4 crq .. + 3 (one packed row-quad) of activation row b
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int64_t crq = rq0 + wm * 8 + 4 * t + lg;
+        if (crq >= n_rq) continue;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int64_t b = b0 + wn * 32 + 16 * c + l16;
+            if (b >= batch) continue;
+            float *yr = y + b * ldy;
+            if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const int64_t o = crq * 2 + k;
+                    if (o >= rows_out) continue;
+                    const float g = acc[t][c][k], u = acc[t][c][2 + k];
+                    yr[o] = g / (1.0f + __expf(-g)) * u;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t row = crq * 4 + i;
+                    if (row >= rows_out) continue;
+                    float v = acc[t][c][i];
+                    if (bias) v += bias[row];
+                    if constexpr (EPI == EPI_ACCUM) v += yr[row];
+                    yr[row] = v;
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Decode batches (up to 64 activation rows): one launch without the split pre-pass.  Each workgroup
 // converts the activations of its K range itself, 4 blocks at a time, into LDS (bf16 hi and lo, the
 // per-block sums of hi + lo), shared by its 4 waves; the chunks are double-buffered so the next
@@ -722,7 +838,7 @@ int64_t vgx_qgemm_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, int
 int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx, int64_t batch,
               const float *norm_w, float eps, const float *bias, float *y, int64_t ldy, int epilogue, void *workspace,
               int64_t workspace_bytes, void *stream) {
-    if (dtype != VGX_Q8_0 && dtype != VGX_Q4_0) return VGX_E_DTYPE;
+    if (dtype != VGX_Q8_0 && dtype != VGX_Q4_0 && dtype != VGX_F32) return VGX_E_DTYPE;
     if (!w_packed || !x || !y) return VGX_E_ARG;
     if (epilogue != VGX_EPI_STORE && epilogue != VGX_EPI_ACCUM && epilogue != VGX_EPI_SWIGLU) return VGX_E_ARG;
     if (epilogue == VGX_EPI_SWIGLU && bias) return VGX_E_ARG;
@@ -734,6 +850,25 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     const int64_t rows_packed = epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows;
     const int nblk = (int)(cols / QK);
     const int64_t n_rq = rows4(rows_packed) / 4;
+    if (dtype == VGX_F32) {
+        if (norm_w) return VGX_E_ARG;                 // F32 weights: no fused RMSNorm on this path
+        const auto *wf = static_cast<const float *>(w_packed);
+        const dim3 grid((unsigned)((n_rq + kFT / 4 - 1) / (kFT / 4)), (unsigned)((batch + kFT - 1) / kFT));
+        const bool vec = ((uintptr_t)x & 15) == 0 && ldx % 4 == 0;
+        hipStream_t sf = (hipStream_t)stream;
+#define VGX_F32G(EPI, V) hipLaunchKernelGGL((f32gemm_tile_kernel<EPI, V>), grid, dim3(256), 0, sf, wf, n_rq, nblk, rows, x, ldx, batch, bias, y, ldy)
+#define VGX_F32E(V)                                                         \
+    do {                                                                    \
+        if (epilogue == VGX_EPI_SWIGLU) VGX_F32G(EPI_SWIGLU, V);             \
+        else if (epilogue == VGX_EPI_ACCUM) VGX_F32G(EPI_ACCUM, V);          \
+        else VGX_F32G(EPI_STORE, V);                                        \
+    } while (0)
+        if (vec) VGX_F32E(true); else VGX_F32E(false);
+#undef VGX_F32E
+#undef VGX_F32G
+        VGX_CHECK_LAUNCH();
+        return VGX_OK;
+    }
     const int64_t soff0 = gemm_scale_off(dtype, rows_packed, cols);
     hipStream_t st0 = (hipStream_t)stream;
     if (batch <= kSmallMaxBatch && ((uintptr_t)x & 15) == 0 && ldx % 4 == 0 && ((uintptr_t)norm_w & 15) == 0) {

@@ -149,7 +149,7 @@ def _gemv(w: QWeight, x: torch.Tensor, out: Optional[torch.Tensor], epi: int, bi
     nw, eps = (None, 0.0) if norm is None else norm
     if nw is not None:
         _need(nw, torch.float32, "norm weight")
-    if B >= GEMM_MIN_ROWS and w.dtype in (Q8_0, Q4_0):
+    if B >= GEMM_MIN_ROWS and (w.dtype in (Q8_0, Q4_0) or (w.dtype == F32 and nw is None)):
         lib = L.load()
         need = int(lib.vgx_qgemm_workspace_bytes(B, w.rows, w.cols, epi))
         ws = gemm_workspace(x.device).get(need)
