@@ -358,6 +358,8 @@ def main() -> int:
     ap.add_argument("--no-kernels", action="store_true", help="skip the secondary kernel figures")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for per-kernel profiles of the step)")
+    ap.add_argument("--figures", choices=("gemv", "attn_decode", "attn_prefill", "gemm_prefill"),
+                    help="only one set of kernel figures, printed as JSON (for per-kernel profiles)")
     ap.add_argument("--pmc", action="store_true",
                     help="only run the launches the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count")
     ap.add_argument("--pmc-report", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -379,6 +381,11 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.pmc:
         pmc_launches(dev)
+        return 0
+    if args.figures:
+        fig = {"gemv": gemv_figures, "attn_decode": attn_figures, "attn_prefill": prefill_figures,
+               "gemm_prefill": gemm_figures}[args.figures](dev)
+        print(json.dumps({args.figures: fig}), flush=True)
         return 0
     kv_dtype = torch.float32 if args.kv == "fp32" else torch.bfloat16
     cfg = model_config()
