@@ -210,9 +210,10 @@ typedef struct {
     vgx_kv_run runs[4];
 } vgx_attn_block;
 
-/* Prefill attention on bf16 MFMA (kv_dtype VGX_BF16; q_dtype VGX_F32 or VGX_BF16; D = 128;
- * H/G in {1, 2, 4, 6, 8}) for up to 8 query blocks in one launch: out = softmax(q k^T * scale) v per
- * query head h over kv group h / (H/G), key tiles wholly in a query tile's causal future skipped.
+/* Prefill attention on bf16 MFMA (kv_dtype VGX_BF16, or VGX_F32 whose K / V enter the MFMAs as bf16
+ * hi + lo pairs; q_dtype VGX_F32 (hi + lo) or VGX_BF16; D = 128; H/G in {1, 2, 4, 6, 8}) for up to 8
+ * query blocks in one launch: out = softmax(q k^T * scale) v per query head h over kv group h / (H/G),
+ * key tiles wholly in a query tile's causal future skipped.
  * Replaces the SDPA calls of block_sliding_attention (src/vault_v3_model.py:812-863) and of the
  * chunk-recurrent prefill (:2064-2093). */
 int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H, int64_t G,

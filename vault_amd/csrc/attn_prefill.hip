@@ -37,7 +37,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kKT = 64;             // keys per LDS tile
 constexpr int kD = 128;             // head dim (the kernel is specialised for 128)
 constexpr int kKRow = kD + 8;       // LDS row of K, bf16 (16 bytes of padding)
-constexpr int kVRow = kKT + 8;      // LDS row of V^T, bf16
 constexpr int kMaxQTile = 32;       // queries per wave: 16 NQT
 constexpr int kMaxBlocks = 8;
 constexpr float kNegBig = -1.0e30f;
@@ -49,8 +48,8 @@ __device__ __forceinline__ T sel4(int i, T a0, T a1, T a2, T a3) {
 }
 
 struct RunArgs {
-    const uint16_t *k;
-    const uint16_t *v;
+    const void *k;     // bf16 or fp32 rows
+    const void *v;
     int64_t len;
     int64_t rstride;   // elements between consecutive keys
     int64_t gstride;   // elements between kv groups
@@ -80,11 +79,16 @@ struct PrefillArgs {
 };
 
 
-template <int GRP, bool QSPLIT, int NQT>
+template <int GRP, bool QSPLIT, int NQT, bool KF>
 __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     constexpr int kQTile = 16 * NQT;
-    __shared__ __align__(16) uint16_t ks[kKT * kKRow];
-    __shared__ __align__(16) uint16_t vt[kD * kVRow];
+    // KF: fp32 K / V, staged as bf16 hi + lo planes (tiles of 32 keys: the same bytes per tile)
+    constexpr int KT = KF ? 32 : kKT;               // keys per LDS tile
+    constexpr int VROW = KT + 8;                    // LDS row of V^T, bf16 (16 bytes of padding)
+    constexpr int NP = KF ? 2 : 1;                  // bf16 planes per operand
+    constexpr int ESZ = KF ? 4 : 2;                 // bytes per K / V element in memory
+    __shared__ __align__(16) uint16_t ks[NP * KT * kKRow];
+    __shared__ __align__(16) uint16_t vt[NP * kD * VROW];
 
     // XCD-aware order: consecutive tiles (same block and group, neighbouring queries, same keys)
     // on the same XCD so that its L2 serves their shared K/V.
@@ -164,7 +168,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     const int n_runs = B.n_runs;
     const int64_t cbase = B.causal_base;
     int64_t rlen[4];
-    const uint16_t *rkp[4], *rvp[4];
+    const char *rkp[4], *rvp[4];
     int rrs[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -172,40 +176,41 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
         int64_t n = i < n_runs ? R.len : 0;
         if (i == n_runs - 1 && cbase >= 0) n = min(n, cbase + t0 + kQTile);   // the rest is in every query's future
         rlen[i] = n;
-        rkp[i] = R.k + (int64_t)g * R.gstride;
-        rvp[i] = R.v + (int64_t)g * R.gstride;
-        rrs[i] = (int)R.rstride;
+        rkp[i] = static_cast<const char *>(R.k) + (int64_t)g * R.gstride * ESZ;
+        rvp[i] = static_cast<const char *>(R.v) + (int64_t)g * R.gstride * ESZ;
+        rrs[i] = (int)R.rstride * ESZ;             // bytes between consecutive keys
     }
 
     // Key tiles in order over the runs; the global loads of the next tile are issued before the
     // current tile is computed (register double buffer), then stored into LDS (K as is, V transposed).
     auto run_len = [&](int r) -> int64_t { return sel4(r, rlen[0], rlen[1], rlen[2], rlen[3]); };
     constexpr int NT = 64 * GRP;
-    constexpr int KCH = kKT * (kD / 8);            // 16-byte K chunks per tile
-    constexpr int VCH = kKT / 2 * (kD / 8);        // V chunks per tile, counted in row pairs
+    constexpr int CPR = kD * ESZ / 16;             // 16-byte chunks per key row
+    constexpr int KCH = KT * CPR;                  // K chunks per tile
+    constexpr int VCH = KT / 2 * CPR;              // V chunks per tile, counted in row pairs
     constexpr int KIT = (KCH + NT - 1) / NT, VIT = (VCH + NT - 1) / NT;
     uint4 kreg[KIT], vreg[VIT][2];
     auto fetch = [&](int r, int64_t j0) {
         const int64_t n = run_len(r);
         const int rs = sel4(r, rrs[0], rrs[1], rrs[2], rrs[3]);
-        const uint16_t *kb = sel4(r, rkp[0], rkp[1], rkp[2], rkp[3]) + j0 * rs;   // wave-uniform
-        const uint16_t *vb = sel4(r, rvp[0], rvp[1], rvp[2], rvp[3]) + j0 * rs;
-        const int lim = (int)min<int64_t>(n - j0, kKT);                       // rows of this tile
+        const char *kb = sel4(r, rkp[0], rkp[1], rkp[2], rkp[3]) + j0 * rs;   // wave-uniform
+        const char *vb = sel4(r, rvp[0], rvp[1], rvp[2], rvp[3]) + j0 * rs;
+        const int lim = (int)min<int64_t>(n - j0, KT);                        // rows of this tile
 #pragma unroll
         for (int i = 0; i < KIT; ++i) {
             const int c = tid + i * NT;
-            const int row = c >> 4, cc = c & 15;
-            kreg[i] = (c < KCH && row < lim) ? *reinterpret_cast<const uint4 *>(kb + row * rs + cc * 8)
+            const int row = c / CPR, cc = c % CPR;
+            kreg[i] = (c < KCH && row < lim) ? *reinterpret_cast<const uint4 *>(kb + row * rs + cc * 16)
                                              : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int i = 0; i < VIT; ++i) {
             const int c = tid + i * NT;
-            const int rp = c & 31, cc = c >> 5;    // consecutive lanes: consecutive row pairs
+            const int rp = c % (KT / 2), cc = c / (KT / 2);    // consecutive lanes: consecutive row pairs
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
                 const int row = 2 * rp + h2;
-                vreg[i][h2] = (c < VCH && row < lim) ? *reinterpret_cast<const uint4 *>(vb + row * rs + cc * 8)
+                vreg[i][h2] = (c < VCH && row < lim) ? *reinterpret_cast<const uint4 *>(vb + row * rs + cc * 16)
                                                      : make_uint4(0, 0, 0, 0);
             }
         }
@@ -214,22 +219,43 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < KIT; ++i) {
             const int c = tid + i * NT;
-            if (c < KCH) *reinterpret_cast<uint4 *>(ks + (c >> 4) * kKRow + (c & 15) * 8) = kreg[i];
+            if (c >= KCH) continue;
+            if constexpr (!KF) {
+                *reinterpret_cast<uint4 *>(ks + (c >> 4) * kKRow + (c & 15) * 8) = kreg[i];
+            } else {
+                // four fp32 of row c / 32 -> bf16 hi (plane 0) and lo (plane 1)
+                uint2 hw, lw;
+                split_bf16x2(__uint_as_float(kreg[i].x), __uint_as_float(kreg[i].y), hw.x, lw.x);
+                split_bf16x2(__uint_as_float(kreg[i].z), __uint_as_float(kreg[i].w), hw.y, lw.y);
+                uint16_t *kp = ks + (c / CPR) * kKRow + (c % CPR) * 4;
+                *reinterpret_cast<uint2 *>(kp) = hw;
+                *reinterpret_cast<uint2 *>(kp + KT * kKRow) = lw;
+            }
         }
 #pragma unroll
         for (int i = 0; i < VIT; ++i) {
             const int c = tid + i * NT;
-            if (c < VCH) {
-                const int rp = c & 31, cc = c >> 5;
-                const uint32_t a0[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
-                const uint32_t a1[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
+            if (c >= VCH) continue;
+            const int rp = c % (KT / 2), cc = c / (KT / 2);
+            const uint32_t a0[4] = {vreg[i][0].x, vreg[i][0].y, vreg[i][0].z, vreg[i][0].w};
+            const uint32_t a1[4] = {vreg[i][1].x, vreg[i][1].y, vreg[i][1].z, vreg[i][1].w};
+            if constexpr (!KF) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     // dims 8 cc + 2 e and + 1 of keys 2 rp, 2 rp + 1: one 4-byte word each
-                    *reinterpret_cast<uint32_t *>(vt + (cc * 8 + 2 * e) * kVRow + 2 * rp) =
+                    *reinterpret_cast<uint32_t *>(vt + (cc * 8 + 2 * e) * VROW + 2 * rp) =
                         (a0[e] & 0xFFFFu) | (a1[e] << 16);
-                    *reinterpret_cast<uint32_t *>(vt + (cc * 8 + 2 * e + 1) * kVRow + 2 * rp) =
+                    *reinterpret_cast<uint32_t *>(vt + (cc * 8 + 2 * e + 1) * VROW + 2 * rp) =
                         (a0[e] >> 16) | (a1[e] & 0xFFFF0000u);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // dim 4 cc + e of keys 2 rp, 2 rp + 1: the hi word and the lo word
+                    uint32_t hw, lw;
+                    split_bf16x2(__uint_as_float(a0[e]), __uint_as_float(a1[e]), hw, lw);
+                    *reinterpret_cast<uint32_t *>(vt + (cc * 4 + e) * VROW + 2 * rp) = hw;
+                    *reinterpret_cast<uint32_t *>(vt + kD * VROW + (cc * 4 + e) * VROW + 2 * rp) = lw;
                 }
             }
         }
@@ -244,7 +270,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
         const int64_t n = run_len(r);
         const bool causal = (r == n_runs - 1) && cbase >= 0;
         int rn = r;
-        int64_t jn = j0 + kKT;
+        int64_t jn = j0 + KT;
         if (jn >= n) {
             jn = 0;
             do { ++rn; } while (rn < n_runs && run_len(rn) <= 0);
@@ -253,7 +279,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
         stage();
         __syncthreads();
         if (rn < n_runs) fetch(rn, jn);
-        for (int c = 0; c < kKT && j0 + c < n; c += 32) {
+        for (int c = 0; c < KT && j0 + c < n; c += 32) {
             f32x4_t sc[NQT][2];
 #pragma unroll
             for (int qt = 0; qt < NQT; ++qt) {
@@ -262,15 +288,19 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
             }
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
-                const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(ks + (c + lq) * kKRow + kc * 32 + lg * 8);
-                const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(ks + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
 #pragma unroll
-                for (int qt = 0; qt < NQT; ++qt) {
-                    sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qh[qt][kc], sc[qt][0], 0, 0, 0);
-                    sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qh[qt][kc], sc[qt][1], 0, 0, 0);
-                    if constexpr (QSPLIT) {
-                        sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ql[qt][kc], sc[qt][0], 0, 0, 0);
-                        sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ql[qt][kc], sc[qt][1], 0, 0, 0);
+                for (int pk = 0; pk < NP; ++pk) {        // K plane: hi, then (fp32 K) lo
+                    const uint16_t *kp = ks + pk * KT * kKRow;
+                    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(kp + (c + lq) * kKRow + kc * 32 + lg * 8);
+                    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(kp + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
+#pragma unroll
+                    for (int qt = 0; qt < NQT; ++qt) {
+                        sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qh[qt][kc], sc[qt][0], 0, 0, 0);
+                        sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qh[qt][kc], sc[qt][1], 0, 0, 0);
+                        if constexpr (QSPLIT) {
+                            sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ql[qt][kc], sc[qt][0], 0, 0, 0);
+                            sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ql[qt][kc], sc[qt][1], 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -331,14 +361,17 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
             }
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
-                const uint16_t *vr = vt + (dt * 16 + lq) * kVRow + c + lg * 4;
-                const uint2 lo = *reinterpret_cast<const uint2 *>(vr);
-                const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16);
-                const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-                for (int qt = 0; qt < NQT; ++qt) {
-                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[qt], o[qt][dt], 0, 0, 0);
-                    o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[qt], o[qt][dt], 0, 0, 0);
+                for (int pv_ = 0; pv_ < NP; ++pv_) {     // V plane: hi, then (fp32 V) lo
+                    const uint16_t *vr = vt + pv_ * kD * VROW + (dt * 16 + lq) * VROW + c + lg * 4;
+                    const uint2 lo = *reinterpret_cast<const uint2 *>(vr);
+                    const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16);
+                    const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                    for (int qt = 0; qt < NQT; ++qt) {
+                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[qt], o[qt][dt], 0, 0, 0);
+                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[qt], o[qt][dt], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -373,7 +406,8 @@ extern "C" {
 
 int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H, int64_t G,
                      int64_t D, float scale, void *stream) {
-    if (kv_dtype != VGX_BF16) return VGX_E_DTYPE;
+    if (kv_dtype != VGX_BF16 && kv_dtype != VGX_F32) return VGX_E_DTYPE;
+    const int esz = kv_dtype == VGX_F32 ? 4 : 2;
     if (q_dtype != VGX_F32 && q_dtype != VGX_BF16) return VGX_E_DTYPE;
     if (!blocks) return VGX_E_ARG;
     if (n_blocks < 0 || n_blocks > kMaxBlocks) return VGX_E_LIMIT;
@@ -415,12 +449,12 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, in
             const vgx_kv_run &R = b.runs[r];
             if (R.len < 0) return VGX_E_SIZE;
             if (R.len > 0 && (!R.k || !R.v)) return VGX_E_ARG;
-            if (R.len > 0 && (((uintptr_t)R.k | (uintptr_t)R.v) % 16 || (R.row_stride * 2) % 16 ||
-                              (R.group_stride * 2) % 16))
+            if (R.len > 0 && (((uintptr_t)R.k | (uintptr_t)R.v) % 16 || (R.row_stride * esz) % 16 ||
+                              (R.group_stride * esz) % 16))
                 return VGX_E_ALIGN;
             if (R.row_stride < D || R.row_stride >= (1 << 24)) return VGX_E_SIZE;   // tile offsets are 32-bit
-            B.run[r].k = static_cast<const uint16_t *>(R.k);
-            B.run[r].v = static_cast<const uint16_t *>(R.v);
+            B.run[r].k = R.k;
+            B.run[r].v = R.v;
             B.run[r].len = R.len;
             B.run[r].rstride = R.row_stride;
             B.run[r].gstride = R.group_stride;
@@ -437,7 +471,11 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, in
     a.n_tiles = (int)tiles;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)tiles);
-#define VGX_PREFILL_GO(G_, S_) hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, kNqt>), grid, dim3(64 * G_), 0, st, a)
+#define VGX_PREFILL_GO(G_, S_)                                                                               \
+    do {                                                                                                     \
+        if (kv_dtype == VGX_F32) hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, kNqt, true>), grid, dim3(64 * G_), 0, st, a); \
+        else hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, kNqt, false>), grid, dim3(64 * G_), 0, st, a);   \
+    } while (0)
 #define VGX_PREFILL_GRP(S_)                      \
     switch (grp) {                               \
         case 1: VGX_PREFILL_GO(1, S_); break;    \

@@ -572,7 +572,7 @@ class VAULTv3ForCausalLM:
         ao = torch.empty(N, H, D, dtype=torch.float32, device=self.device)
         hbuf = torch.empty(N, cfg.d_ff, dtype=torch.float32, device=self.device)
         scale = 1.0 / math.sqrt(D)
-        mfma = st.kv_dtype == torch.bfloat16 and D == 128 and H // G in (1, 2, 4, 6, 8)
+        mfma = D == 128 and H // G in (1, 2, 4, 6, 8)
         for li, lw in enumerate(w.layers):
             if seg_active and li in cfg.seg_layers:
                 j = cfg.seg_layers.index(li)
@@ -593,7 +593,8 @@ class VAULTv3ForCausalLM:
                 spans.append((st.k_prev[li], st.v_prev[li]))
             spans.append((kc[:, :, :N], st.v_cur[li][:, :, :N]))
             if mfma:
-                # bf16 cache: block attention on MFMA (runs are the [G, n, D] views of batch entry 0)
+                # block attention on MFMA (fp32 cache: K / V as bf16 hi + lo; runs are the [G, n, D] views
+                # of batch entry 0)
                 ops.attn_prefill([{"q": q, "out": ao, "runs": [(k_[0], v_[0]) for k_, v_ in spans],
                                    "causal_base": 0}], H, G, scale)
             else:

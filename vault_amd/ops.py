@@ -401,17 +401,20 @@ def qkv_rope_step(wq: QWeight, bq: Optional[torch.Tensor], wkv: QWeight, bkv: Op
 
 
 def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
-    """MFMA prefill attention (bf16 K/V) for up to 8 query blocks per launch (more are split).
+    """MFMA prefill attention for up to 8 query blocks per launch (more are split).
 
     Each block is a dict: ``q`` [n_q, H, D] view (fp32 or bf16, any token / head stride, D contiguous),
-    ``out`` [n_q, H, D] fp32 view, ``runs``: list of (K, V) views [G, n, D] (bf16, D contiguous, any row
-    and group stride), ``causal_base``: -1, or b >= 0 making the last run causal (query t sees its keys
-    j <= b + t)."""
+    ``out`` [n_q, H, D] fp32 view, ``runs``: list of (K, V) views [G, n, D] (bf16, or fp32 entering the
+    MFMAs as bf16 hi + lo; one dtype for all runs; D contiguous, any row and group stride),
+    ``causal_base``: -1, or b >= 0 making the last run causal (query t sees its keys j <= b + t)."""
     lib = L.load()
     if not blocks:
         return
     D = blocks[0]["q"].shape[-1]
     qdt = blocks[0]["q"].dtype
+    kvdt = blocks[0]["runs"][0][0].dtype
+    if kvdt not in (torch.bfloat16, torch.float32):
+        raise ValueError("key runs must be bf16 or fp32")
     scale = float(scale if scale is not None else D ** -0.5)
     for i0 in range(0, len(blocks), 8):
         part = blocks[i0:i0 + 8]
@@ -426,8 +429,8 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
                 raise ValueError("1 to 4 key runs per block")
             ra = (L.KVRun * 4)()
             for j, (k, v) in enumerate(runs):
-                if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16 or k.shape != v.shape:
-                    raise ValueError("key runs must be bf16 K/V of one shape")
+                if k.dtype != kvdt or v.dtype != kvdt or k.shape != v.shape:
+                    raise ValueError("key runs must be K/V of one dtype and shape")
                 if k.stride(-1) != 1 or v.stride(-1) != 1 or k.stride(0) != v.stride(0) or k.stride(1) != v.stride(1):
                     raise ValueError("K and V views need equal strides and contiguous rows")
                 ra[j] = L.KVRun(k.data_ptr(), v.data_ptr(), k.shape[1], k.stride(1), k.stride(0))
@@ -435,5 +438,5 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
             arr[i] = L.AttnBlock(q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
                                  q.shape[0], int(b.get("causal_base", -1)), len(runs), ra)
         qd = L.BF16 if qdt == torch.bfloat16 else L.F32
-        L.check(lib.vgx_attn_prefill(L.BF16, qd, arr, len(part), H, G, D, scale, _stream(part[0]["q"].device)),
+        L.check(lib.vgx_attn_prefill(KV_DTYPES[kvdt], qd, arr, len(part), H, G, D, scale, _stream(part[0]["q"].device)),
                 "vgx_attn_prefill")
