@@ -100,6 +100,9 @@ def load() -> C.CDLL:
         return _lib
     if not os.path.exists(LIB_PATH):
         raise VGXError(f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+    # torch first: its HIP runtime is then the one the library binds to, so device pointers and streams
+    # from torch are valid in the library's calls (loading the library first can bring in a second runtime)
+    import torch  # noqa: F401
     lib = C.CDLL(LIB_PATH)
     for name, (res, args) in _SIGS.items():
         fn = getattr(lib, name)
