@@ -185,7 +185,8 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
                     void *stream);
 
 /* A run of keys for prefill attention: key j of kv group g at element offset
- * g*group_stride + j*row_stride of k (and v); rows are head_dim contiguous bf16. */
+ * g*group_stride + j*row_stride of k (and v); rows are head_dim contiguous elements of the KV dtype
+ * (bf16 or fp32; every run of one call has the same dtype). */
 typedef struct {
     const void *k;
     const void *v;
