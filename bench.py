@@ -188,39 +188,67 @@ def gemm_figures(dev, rows_in: int = 1024, reps: int = 10):
     return out
 
 
-def attn_figures(dev, reps: int = 20):
+def _kv_copies(base, n: int):
+    """n distinct versions of one set of KV span tensors (keys rotated by i, sign flipped for odd i), so
+    that a round of calls reads n x the bytes and no call finds its KV in a cache."""
+    import torch
+    out = []
+    for i in range(n):
+        sgn = -1.0 if i & 1 else 1.0
+        out.append([(sgn * torch.roll(k, i, dims=2), sgn * torch.roll(v, i, dims=2)) for k, v in base])
+    return out
+
+
+def attn_figures(dev, reps: int = 10):
     """Batched decode attention, bf16 KV: B=64, 12 q / 2 KV heads, D=128, keys 512 sink + 1024 segment
-    + 2048 window = 3584; algorithmic bytes = K and V once (234,881,024 B) + q + out."""
+    + 2048 window = 3584; algorithmic bytes = K and V once (234,881,024 B) + q + out.  One graph replays
+    a call over each of 2 KV copies (470 MB, beyond the 256 MB Infinity Cache); time per call."""
     import torch
     from vault_amd import ops
     B, H, G, D = 64, 12, 2, 128
     lens = (512, 1024, 1024, 1024)
     g = torch.Generator().manual_seed(11)
-    spans = [(torch.randn(B, G, n, D, generator=g).to(dev, torch.bfloat16),
-              torch.randn(B, G, n, D, generator=g).to(dev, torch.bfloat16)) for n in lens]
+    base = [(torch.randn(B, G, n, D, generator=g).to(dev, torch.bfloat16),
+             torch.randn(B, G, n, D, generator=g).to(dev, torch.bfloat16)) for n in lens]
+    sets = _kv_copies(base, 2)
     q = torch.randn(B, H, D, generator=g).to(dev)
     out = torch.empty(B, H, D, device=dev)
     ws = ops.Workspace(dev)
-    us = graph_time_us(lambda: ops.attn_decode(q, spans, out=out, ws=ws), 1, reps=reps)
+
+    def run():
+        for sp in sets:
+            ops.attn_decode(q, sp, out=out, ws=ws)
+    us = graph_time_us(run, len(sets), reps=reps)
     algo = B * sum(lens) * G * D * 2 * 2 + 2 * B * H * D * 4
     return {"config": "B=64 bf16 KV, 3584 keys (512 sink | 1024 seg | 2048 window)", "us": round(us, 2),
             "gbs": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 3)}
 
 
-def batched_decode(model, batch: int = 32, steps: int = 16, warmup: int = 4):
-    """The same 1.54B model decoding 32 sequences at 100K context with bf16 KV (segment memory is off
-    for batch > 1, as in the reference's batched path): tokens/s of the whole batch."""
+def attn_b1_figures(dev, reps: int = 20):
+    """Single-layer decode attention, fp32 KV, batch 1: 12 q / 2 KV heads, D=128, keys 64 sink + 1024
+    previous + 1024 current window = 2112; algorithmic bytes = K and V once (4,325,376 B) + q + out.
+    One query per KV pair of rows, so the split launch and its merge launch are bound by latency, not
+    by bandwidth.  One graph replays a call over each of 64 KV copies (277 MB, as the 28 layers of a
+    decode step stream theirs); time per call (both launches)."""
     import torch
-    from vault_amd.model import VAULTv3ForCausalLM
-    m2 = VAULTv3ForCausalLM(model.w, kv_dtype=torch.bfloat16)
-    st = seeded_state(m2, batch)
-    dt = time_decode(m2, st, steps, warmup, batch)
-    del st
-    return {"config": f"batch {batch}, bf16 KV, 100K context (512 sinks + 2048 window)",
-            "tokens_per_s": round(batch * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 3)}
+    from vault_amd import ops
+    B, H, G, D = 1, 12, 2, 128
+    lens = (64, 1024, 1024)
+    g = torch.Generator().manual_seed(12)
+    base = [(torch.randn(B, G, n, D, generator=g).to(dev), torch.randn(B, G, n, D, generator=g).to(dev))
+            for n in lens]
+    sets = _kv_copies(base, 64)
+    q = torch.randn(B, H, D, generator=g).to(dev)
+    out = torch.empty(B, H, D, device=dev)
+    ws = ops.Workspace(dev)
 
-
-PREFILL_FLOPS = 90.22e9   # unmasked (query, key) pairs x 4 x D x H for L = 8192, W = 1024, 512 sinks
+    def run():
+        for sp in sets:
+            ops.attn_decode(q, sp, out=out, ws=ws)
+    us = graph_time_us(run, len(sets), reps=reps)
+    algo = B * sum(lens) * G * D * 4 * 2 + 2 * B * H * D * 4
+    return {"config": "B=1 fp32 KV, 2112 keys (64 sink | 2048 window)", "us": round(us, 2),
+            "gbs": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 3)}
 
 
 def prefill_figures(dev, reps: int = 10):
@@ -358,7 +386,7 @@ def main() -> int:
     ap.add_argument("--no-kernels", action="store_true", help="skip the secondary kernel figures")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for per-kernel profiles of the step)")
-    ap.add_argument("--figures", choices=("gemv", "attn_decode", "attn_prefill", "gemm_prefill"),
+    ap.add_argument("--figures", choices=("gemv", "attn_decode", "attn_decode_b1", "attn_prefill", "gemm_prefill"),
                     help="only one set of kernel figures, printed as JSON (for per-kernel profiles)")
     ap.add_argument("--pmc", action="store_true",
                     help="only run the launches the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count")
@@ -383,7 +411,8 @@ def main() -> int:
         pmc_launches(dev)
         return 0
     if args.figures:
-        fig = {"gemv": gemv_figures, "attn_decode": attn_figures, "attn_prefill": prefill_figures,
+        fig = {"gemv": gemv_figures, "attn_decode": attn_figures, "attn_decode_b1": attn_b1_figures,
+               "attn_prefill": prefill_figures,
                "gemm_prefill": gemm_figures}[args.figures](dev)
         print(json.dumps({args.figures: fig}), flush=True)
         return 0
@@ -407,6 +436,7 @@ def main() -> int:
     if not args.no_kernels:
         kernels["gemv"] = gemv_figures(dev)
         kernels["attn_decode"] = attn_figures(dev)
+        kernels["attn_decode_b1"] = attn_b1_figures(dev)
         kernels["attn_prefill"] = prefill_figures(dev)
         kernels["gemm_prefill"] = gemm_figures(dev)
         if args.batch == 1:
