@@ -397,7 +397,7 @@ def main() -> int:
         pmc_report(*args.pmc_report)
         return 0
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (decode shards by "
+        print("bench.py measures one GPU: the library has no multi-GPU path (decode shards by "
               "independent sequences with no exchange); run with --gpus 1", file=sys.stderr)
         return 2
     import torch

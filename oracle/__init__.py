@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in ``vault_amd`` imports this package; only
 ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` use it, and only as the checker (never as the thing measured or
+``bench.py`` use it, and only to check results (never as the thing measured or
 shipped).
 
 Contents (each function cites the reference file:line it restates):

@@ -1,6 +1,6 @@
 """GPU parity of split-K decode attention and the row kernels against the float64 oracle.
 
-Bars (BASELINE north star): attention max |d| <= 1e-5 with fp32 KV, <= 2e-3 with bf16 KV (oracle
+Bars: attention max |d| <= 1e-5 with fp32 KV, <= 2e-3 with bf16 KV (oracle
 fed the same bf16-rounded K/V); RoPE / RMSNorm within fp32 rounding; gather bit-exact.
 """
 import numpy as np
