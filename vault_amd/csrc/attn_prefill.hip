@@ -37,7 +37,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kKT = 64;             // keys per LDS tile
 constexpr int kD = 128;             // head dim (the kernel is specialised for 128)
 constexpr int kKRow = kD + 8;       // LDS row of K, bf16 (16 bytes of padding)
-constexpr int kMaxQTile = 32;       // queries per wave: 16 NQT
 constexpr int kMaxBlocks = 8;
 constexpr float kNegBig = -1.0e30f;
 constexpr float kLazyMax = 8.0f;    // log2 of the largest unnormalised probability
