@@ -251,6 +251,22 @@ def attn_b1_figures(dev, reps: int = 20):
             "gbs": round(algo / us / 1e3, 1), "frac": round(algo / us / 1e3 / HBM_PEAK_GBS, 3)}
 
 
+def batched_decode(model, batch: int = 32, steps: int = 16, warmup: int = 4):
+    """The same 1.54B model decoding 32 sequences at 100K context with bf16 KV (segment memory is off
+    for batch > 1, as in the reference's batched path): tokens/s of the whole batch."""
+    import torch
+    from vault_amd.model import VAULTv3ForCausalLM
+    m2 = VAULTv3ForCausalLM(model.w, kv_dtype=torch.bfloat16)
+    st = seeded_state(m2, batch)
+    dt = time_decode(m2, st, steps, warmup, batch)
+    del st
+    return {"config": f"batch {batch}, bf16 KV, 100K context (512 sinks + 2048 window)",
+            "tokens_per_s": round(batch * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 3)}
+
+
+PREFILL_FLOPS = 90.22e9   # unmasked (query, key) pairs x 4 x D x H for L = 8192, W = 1024, 512 sinks
+
+
 def prefill_figures(dev, reps: int = 10):
     """Block sliding-window attention prefill, bf16: batch 1, L = 8192, 12 q / 2 kv heads, D = 128,
     W = 1024, 512 sinks re-rotated per chunk (drop-in block_sliding_attention: 6 sink re-rotations + one
