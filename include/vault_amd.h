@@ -196,13 +196,14 @@ typedef struct {
 } vgx_kv_run;
 
 /* One block of queries (a chunk) for vgx_attn_prefill: query t of head h at q + t*ldq + h*q_hstride
- * (D contiguous elements, fp32 or bf16), output at out + t*ldo + h*o_hstride (fp32); runs concatenated in
+ * (D contiguous elements, fp32 or bf16), output at out + t*ldo + h*o_hstride (elements of the call's
+ * output dtype); runs concatenated in
  * order; when causal_base >= 0 the last run is causal: query t sees its keys j <= causal_base + t. */
 typedef struct {
     const void *q;
     int64_t ldq;
     int64_t q_hstride;
-    float *out;
+    void *out;
     int64_t ldo;
     int64_t o_hstride;
     int64_t n_q;
@@ -214,11 +215,12 @@ typedef struct {
 /* Prefill attention on bf16 MFMA (kv_dtype VGX_BF16, or VGX_F32 whose K / V enter the MFMAs as bf16
  * hi + lo pairs; q_dtype VGX_F32 (hi + lo) or VGX_BF16; D = 128; H/G in {1, 2, 4, 6, 8}) for up to 8
  * query blocks in one launch: out = softmax(q k^T * scale) v per query head h over kv group h / (H/G),
- * key tiles wholly in a query tile's causal future skipped.
+ * key tiles wholly in a query tile's causal future skipped.  out_dtype VGX_F32, or VGX_BF16 (the fp32
+ * result rounded to nearest even, for bf16 callers).
  * Replaces the SDPA calls of block_sliding_attention (src/vault_v3_model.py:812-863) and of the
  * chunk-recurrent prefill (:2064-2093). */
-int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H, int64_t G,
-                     int64_t D, float scale, void *stream);
+int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H,
+                     int64_t G, int64_t D, float scale, void *stream);
 
 /* ---------------------------------------------------------------- small fused ops -------------- */
 

@@ -89,6 +89,22 @@ def test_block_sliding_matches_oracle(dev, B, L, W, S):
         assert np.abs(got - ref).max() <= 2 * TOL, b
 
 
+@pytest.mark.parametrize("B,L,W,S", [(2, 1100, 256, 64), (1, 40, 16, 5)])
+def test_block_sliding_bf16_output_is_rounded_fp32(dev, B, L, W, S):
+    """bf16 callers get the kernel's bf16 output: bit-exactly the fp32 result of the same call rounded
+    to nearest even (no separate conversion pass)."""
+    rng = np.random.default_rng(L + S + 7)
+    H, G, D, theta = 12, 2, 128, 1e6
+    q = _bf(rng.standard_normal((B, H, L, D))).to(dev)
+    k = _bf(rng.standard_normal((B, G, L, D))).to(dev)
+    v = _bf(rng.standard_normal((B, G, L, D))).to(dev)
+    kr = _bf(rng.standard_normal((B, G, L, D))).to(dev)
+    got = vatt.block_sliding_attention(q, k, v, W, k_raw=kr, n_sink=S, head_dim=D, rope_theta=theta)
+    assert got.dtype == torch.bfloat16
+    ref = vatt.block_sliding_attention(q.float(), k, v, W, k_raw=kr, n_sink=S, head_dim=D, rope_theta=theta)
+    assert torch.equal(got, ref.to(torch.bfloat16))
+
+
 def test_block_sliding_full_workload_sampled(dev):
     """L = 8192, W = 1024, 512 sinks, 12 q / 2 kv heads, D = 128: 48 sampled query rows (every chunk,
     first / last / random positions) against the oracle's per-query attention over exactly the keys the

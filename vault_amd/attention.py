@@ -58,28 +58,33 @@ def block_sliding_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, w
     vb = v.to(torch.bfloat16).contiguous()
     qq = q if q.dtype in (torch.float32, torch.bfloat16) else q.float()
     qq = qq.contiguous()
-    out = torch.empty(B, H, Lq, D, dtype=torch.float32, device=q.device)
+    # bf16 callers get the kernel's bf16 output (fp32 result rounded to nearest even); others fp32
+    odt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
+    out = torch.empty(B, H, Lq, D, dtype=odt, device=q.device)
     n = (Lq + W - 1) // W
     sinks = sink_v = None
     if S and n >= 3:
-        # sink keys re-rotated for every chunk i >= 2: [n-2][B][G][S][D]; values [B][G][S][D]
+        # sink keys re-rotated for every chunk i >= 2 in one launch: the raw keys repeated per chunk,
+        # [B*G][n-2][S][D], row (i - 2) * S + s rotated by table row (i - 2) * S + s
         tab = _sink_table(n, W, S, D, rope_theta or 1.0, q.device)
-        kr = k_raw.to(torch.bfloat16)[:, :, :S].contiguous().view(B * G, S, D)
-        sinks = torch.empty(n - 2, B, G, S, D, dtype=torch.bfloat16, device=q.device)
-        sink_v = vb[:, :, :S].contiguous()
-        for i in range(2, n):
-            ops.rope_rotate(kr, sinks[i - 2].view(B * G, S, D), tab[(i - 2) * S:], D)
+        kr = k_raw[:, :, :S].to(torch.bfloat16).reshape(B * G, 1, S, D).expand(B * G, n - 2, S, D)
+        kr = kr.contiguous().view(B * G, (n - 2) * S, D)
+        sinks = torch.empty(B * G, (n - 2) * S, D, dtype=torch.bfloat16, device=q.device)
+        ops.rope_rotate(kr, sinks, tab, D)
+        sinks = sinks.view(B, G, n - 2, S, D)
+        # values in the same layout (a K / V run shares one pair of strides)
+        sink_v = vb[:, :, :S].reshape(B, G, 1, S, D).expand(B, G, n - 2, S, D).contiguous()
     blocks = []
     for b in range(B):
         for i in range(n):
             r0, r1 = i * W, min(Lq, (i + 1) * W)
             runs = []
             if i >= 2 and S:
-                runs.append((sinks[i - 2, b], sink_v[b]))
+                runs.append((sinks[b, :, i - 2], sink_v[b, :, i - 2]))
             if i >= 1:
                 runs.append((kb[b, :, r0 - W:r0], vb[b, :, r0 - W:r0]))
             runs.append((kb[b, :, r0:r1], vb[b, :, r0:r1]))
             blocks.append({"q": qq[b, :, r0:r1].transpose(0, 1), "out": out[b, :, r0:r1].transpose(0, 1),
                            "runs": runs, "causal_base": 0})
     ops.attn_prefill(blocks, H, G)
-    return out if q.dtype == torch.float32 else out.to(q.dtype)
+    return out if out.dtype == q.dtype else out.to(q.dtype)

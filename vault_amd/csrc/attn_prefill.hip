@@ -58,7 +58,7 @@ struct BlockArgs {
     const void *q;     // query t, head h at t * ldq + h * q_hstride elements (fp32 or bf16)
     int64_t ldq;
     int64_t q_hstride;
-    float *out;        // query t, head h at t * ldo + h * o_hstride floats
+    void *out;         // query t, head h at t * ldo + h * o_hstride elements (fp32 or bf16)
     int64_t ldo;
     int64_t o_hstride;
     int64_t n_q;
@@ -75,6 +75,7 @@ struct PrefillArgs {
     int H, G;
     float scale_log2;  // scale * log2(e)
     int q_bf16;
+    int o_bf16;        // output rounded to bf16 (round to nearest even) instead of fp32
 };
 
 
@@ -384,12 +385,22 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
         const float inv = 1.0f / L;
         const int64_t t = t0 + qt * 16 + lq;
         if (t >= B.n_q) continue;
-        float *op = B.out + t * B.ldo + (int64_t)h * B.o_hstride;
+        const int64_t oo = t * B.ldo + (int64_t)h * B.o_hstride;
+        if (a.o_bf16) {
+            uint16_t *op = static_cast<uint16_t *>(B.out) + oo;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            float4 w;
-            w.x = o[qt][dt][0] * inv; w.y = o[qt][dt][1] * inv; w.z = o[qt][dt][2] * inv; w.w = o[qt][dt][3] * inv;
-            *reinterpret_cast<float4 *>(op + dt * 16 + lg * 4) = w;
+            for (int dt = 0; dt < 8; ++dt)
+                *reinterpret_cast<uint2 *>(op + dt * 16 + lg * 4) =
+                    make_uint2(pack_bf16x2(o[qt][dt][0] * inv, o[qt][dt][1] * inv),
+                               pack_bf16x2(o[qt][dt][2] * inv, o[qt][dt][3] * inv));
+        } else {
+            float *op = static_cast<float *>(B.out) + oo;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) {
+                float4 w;
+                w.x = o[qt][dt][0] * inv; w.y = o[qt][dt][1] * inv; w.z = o[qt][dt][2] * inv; w.w = o[qt][dt][3] * inv;
+                *reinterpret_cast<float4 *>(op + dt * 16 + lg * 4) = w;
+            }
         }
     }
 }
@@ -403,9 +414,11 @@ constexpr int kNqt = 2;
 
 extern "C" {
 
-int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H, int64_t G,
-                     int64_t D, float scale, void *stream) {
+int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H,
+                     int64_t G, int64_t D, float scale, void *stream) {
     if (kv_dtype != VGX_BF16 && kv_dtype != VGX_F32) return VGX_E_DTYPE;
+    if (out_dtype != VGX_F32 && out_dtype != VGX_BF16) return VGX_E_DTYPE;
+    const int oel = out_dtype == VGX_BF16 ? 2 : 4;
     const int esz = kv_dtype == VGX_F32 ? 4 : 2;
     if (q_dtype != VGX_F32 && q_dtype != VGX_BF16) return VGX_E_DTYPE;
     if (!blocks) return VGX_E_ARG;
@@ -420,6 +433,7 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, in
     a.G = (int)G;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.q_bf16 = q_dtype == VGX_BF16;
+    a.o_bf16 = out_dtype == VGX_BF16;
     int64_t tiles = 0;
     int nb = 0;
     for (int i = 0; i < n_blocks; ++i) {
@@ -430,7 +444,7 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, const vgx_attn_block *blocks, in
         const int qel = q_dtype == VGX_BF16 ? 2 : 4;
         if (b.q_hstride < D || b.o_hstride < D || b.ldq < 0 || b.ldo < 0) return VGX_E_SIZE;
         if (((uintptr_t)b.q % 16) || ((uintptr_t)b.out % 16) || (b.ldq * qel) % 16 || (b.q_hstride * qel) % 16 ||
-            (b.ldo * 4) % 16 || (b.o_hstride * 4) % 16)
+            (b.ldo * oel) % 16 || (b.o_hstride * oel) % 16)
             return VGX_E_ALIGN;
         BlockArgs &B = a.blk[nb];
         B.q = b.q;

@@ -404,7 +404,7 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
     """MFMA prefill attention for up to 8 query blocks per launch (more are split).
 
     Each block is a dict: ``q`` [n_q, H, D] view (fp32 or bf16, any token / head stride, D contiguous),
-    ``out`` [n_q, H, D] fp32 view, ``runs``: list of (K, V) views [G, n, D] (bf16, or fp32 entering the
+    ``out`` [n_q, H, D] view, fp32 or bf16 (one dtype for all blocks), ``runs``: list of (K, V) views [G, n, D] (bf16, or fp32 entering the
     MFMAs as bf16 hi + lo; one dtype for all runs; D contiguous, any row and group stride),
     ``causal_base``: -1, or b >= 0 making the last run causal (query t sees its keys j <= b + t)."""
     lib = L.load()
@@ -413,6 +413,9 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
     D = blocks[0]["q"].shape[-1]
     qdt = blocks[0]["q"].dtype
     kvdt = blocks[0]["runs"][0][0].dtype
+    odt = blocks[0]["out"].dtype
+    if odt not in (torch.float32, torch.bfloat16):
+        raise ValueError("out must be fp32 or bf16")
     if kvdt not in (torch.bfloat16, torch.float32):
         raise ValueError("key runs must be bf16 or fp32")
     scale = float(scale if scale is not None else D ** -0.5)
@@ -422,8 +425,8 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
         keep = []
         for i, b in enumerate(part):
             q, out = b["q"], b["out"]
-            if q.dtype != qdt or out.dtype != torch.float32 or q.stride(-1) != 1 or out.stride(-1) != 1:
-                raise ValueError("q must share one dtype, out must be fp32, both D-contiguous")
+            if q.dtype != qdt or out.dtype != odt or q.stride(-1) != 1 or out.stride(-1) != 1:
+                raise ValueError("q and out must each share one dtype, both D-contiguous")
             runs = b["runs"]
             if not 1 <= len(runs) <= 4:
                 raise ValueError("1 to 4 key runs per block")
@@ -438,5 +441,7 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
             arr[i] = L.AttnBlock(q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
                                  q.shape[0], int(b.get("causal_base", -1)), len(runs), ra)
         qd = L.BF16 if qdt == torch.bfloat16 else L.F32
-        L.check(lib.vgx_attn_prefill(KV_DTYPES[kvdt], qd, arr, len(part), H, G, D, scale, _stream(part[0]["q"].device)),
+        od = L.BF16 if odt == torch.bfloat16 else L.F32
+        L.check(lib.vgx_attn_prefill(KV_DTYPES[kvdt], qd, od, arr, len(part), H, G, D, scale,
+                                     _stream(part[0]["q"].device)),
                 "vgx_attn_prefill")
