@@ -1,0 +1,47 @@
+"""GPU parity of the segment scorer's EMA habituation (vgx_ema_habituate) against the per-token rule of
+the oracle model (oracle/model.py, restating src/vault_v3_model.py:2294-2305): the first token of a
+stream sets ema = f; every later token gives hab = f - 0.65 ema (before the update) and
+ema <- 0.985 ema + 0.015 f.  Chunk lengths that are and are not multiples of the kernel's 32-token
+load batches.  Bar: fp32 recurrence against float64, 1e-5 relative to the feature scale (the
+recurrence contracts, so rounding does not grow with T).
+"""
+import numpy as np
+import pytest
+import torch
+
+from vault_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(f, ema0, first):
+    f = f.astype(np.float64)
+    T, fd = f.shape
+    e = f[0].copy() if first else ema0.astype(np.float64).copy()
+    hab = np.empty_like(f)
+    for t in range(T):
+        hab[t] = f[t] - 0.65 * e
+        if not (first and t == 0):
+            e = 0.985 * e + 0.015 * f[t]
+    return hab, e
+
+
+@pytest.mark.parametrize("T", [1, 33, 1000, 1024])
+@pytest.mark.parametrize("first", [True, False])
+def test_ema_habituate_matches_recurrence(dev, T, first):
+    rng = np.random.default_rng(T + first)
+    fd = 4608
+    f = (rng.standard_normal((T, fd)) * 2.0).astype(np.float32)
+    ema0 = rng.standard_normal(fd).astype(np.float32)
+    ft = torch.from_numpy(f).to(dev)
+    hab = torch.full((T, fd), float("nan"), device=dev)
+    ema = torch.from_numpy(ema0).to(dev)
+    ops.ema_habituate(ft, hab, ema, first)
+    torch.cuda.synchronize()
+    want_h, want_e = _ref(f, ema0, first)
+    tol = 1e-5 * float(np.abs(f).max())
+    got_h = hab.double().cpu().numpy()
+    rows = slice(1, None) if first else slice(None)   # the first token's hab is not used by the model
+    if got_h[rows].size:
+        assert np.abs(got_h[rows] - want_h[rows]).max() <= tol
+    assert np.abs(ema.double().cpu().numpy() - want_e).max() <= tol

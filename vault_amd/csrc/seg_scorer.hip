@@ -19,7 +19,22 @@ __global__ void ema_habituate_kernel(const float *__restrict__ f, int64_t ldf, f
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= fd) return;
     float e = first ? f[i] : ema[i];
-    for (int64_t t = 0; t < T; ++t) {
+    // The features do not depend on the recurrence: load kU of them at once, then run the sequential
+    // update over them (one load round trip per kU steps instead of per step; same arithmetic in the
+    // same order).
+    constexpr int kU = 32;
+    int64_t t = 0;
+    for (; t + kU <= T; t += kU) {
+        float fv[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) fv[u] = f[(t + u) * ldf + i];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            hab[(t + u) * ldh + i] = fv[u] - 0.65f * e;
+            if (!(first && t + u == 0)) e = 0.985f * e + 0.015f * fv[u];
+        }
+    }
+    for (; t < T; ++t) {
         const float ft = f[t * ldf + i];
         hab[t * ldh + i] = ft - 0.65f * e;
         if (!(first && t == 0)) e = 0.985f * e + 0.015f * ft;
