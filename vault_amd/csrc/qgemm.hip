@@ -494,7 +494,7 @@ constexpr int kCK = 4;                       // blocks per staged chunk
 constexpr int kSRow = kCK * QK + 8;          // bf16 per staged activation row (16 B of padding)
 
 template <int DT, int NC, int EPI, bool SPLIT, bool NORM>
-__global__ __launch_bounds__(256) void qgemm_small_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
+__global__ __launch_bounds__(256, 2) void qgemm_small_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
                                                            int nblk, int64_t rows_out, const float *__restrict__ x,
                                                            int64_t ldx, const float *__restrict__ lnw, float eps,
                                                            int64_t batch, const float *__restrict__ bias,
@@ -808,14 +808,16 @@ inline int64_t part_bytes(int ks, int64_t batch, int64_t rows_p) {
 
 constexpr int64_t kSmallMaxBatch = 64;
 
-// Activation tiles of 16 rows per workgroup at every batch size: with two (32 rows) the kernel needs
-// 262 registers, one wave per SIMD, and batch-32 decode measured 8.87K against 9.10K tokens/s with
-// 16-row workgroups reading the weights twice.
-inline int small_nc(int64_t) { return 1; }
+// Activation tiles per workgroup (16 rows each).  Two (32 rows, held to two waves per SIMD by the
+// launch bounds) only for very tall weights with more than 16 activation rows: the LM head (151665 x
+// 1536 Q8_0) at batch 32 / 64 measured 134 / 232 us against 169 / 303 us with 16-row workgroups, which
+// read its 248 MB once per activation tile; for the layer projections 16-row tiles measured ahead
+// (batch-32 decode 9.10K against 9.03K tokens/s).
+inline int small_nc(int64_t batch, int64_t n_rq) { return batch > 16 && n_rq >= 16384 ? 2 : 1; }
 
 // K splits of the small-batch kernel: as choose_ksplit, with whole chunks per split.
 inline int small_ksplit(int64_t n_rq, int64_t batch, int nblk, int *kper) {
-    const int ks0 = choose_ksplit(n_rq, batch, small_nc(batch), nblk);
+    const int ks0 = choose_ksplit(n_rq, batch, small_nc(batch, n_rq), nblk);
     int kp = (nblk + ks0 - 1) / ks0;
     kp = (kp + kCK - 1) / kCK * kCK;
     *kper = kp;
@@ -889,7 +891,7 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
         auto *pssq = need > 0 ? reinterpret_cast<float *>(static_cast<char *>(workspace) +
                                                           part_bytes(ks, batch, n_rq * 4))
                               : nullptr;
-        const int nc = small_nc(batch);
+        const int nc = small_nc(batch, n_rq);
         const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 16 * nc - 1) / (16 * nc)), (unsigned)ks);
         const auto *w = static_cast<const uint8_t *>(w_packed);
 #define VGX_SG(DT, NC, EPI, SP, NORM)                                                                         \
@@ -903,8 +905,8 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
         else if (epilogue == VGX_EPI_ACCUM) VGX_SG_N(DT, NC, EPI_ACCUM, false);                               \
         else VGX_SG_N(DT, NC, EPI_STORE, false);                                                              \
     } while (0)
-        if (dtype == VGX_Q8_0) VGX_SG_E(VGX_Q8_0, 1);
-        else VGX_SG_E(VGX_Q4_0, 1);
+        if (dtype == VGX_Q8_0) { if (nc == 1) VGX_SG_E(VGX_Q8_0, 1); else VGX_SG_E(VGX_Q8_0, 2); }
+        else { if (nc == 1) VGX_SG_E(VGX_Q4_0, 1); else VGX_SG_E(VGX_Q4_0, 2); }
 #undef VGX_SG_E
 #undef VGX_SG_N
 #undef VGX_SG
