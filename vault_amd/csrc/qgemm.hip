@@ -493,8 +493,11 @@ __global__ __launch_bounds__(256) void f32gemm_tile_kernel(const float *__restri
 constexpr int kCK = 4;                       // blocks per staged chunk
 constexpr int kSRow = kCK * QK + 8;          // bf16 per staged activation row (16 B of padding)
 
+// Occupancy: K-split instances (the layer projections of a decode batch) are held to three waves per
+// SIMD (168 registers, a few spilled: batch-32 decode 9.51K against 9.19K tokens/s); the unsplit ones
+// (tall weights such as the LM head) to two (three measured 166 against 101 us for the batch-16 LM head).
 template <int DT, int NC, int EPI, bool SPLIT, bool NORM>
-__global__ __launch_bounds__(256, 2) void qgemm_small_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
+__global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
                                                            int nblk, int64_t rows_out, const float *__restrict__ x,
                                                            int64_t ldx, const float *__restrict__ lnw, float eps,
                                                            int64_t batch, const float *__restrict__ bias,
