@@ -2,8 +2,8 @@
 block_sliding_attention (src/vault_v3_model.py:812-863) against the float64 oracle.
 
 The oracle is fed the same bf16 k / v (and the same q: fp32 queries are used at fp32 accuracy, bf16
-ones as given); the bar is the north-star bf16 attention bound max |d| <= 2e-3.  Shapes: ragged query counts (not multiples of the 32-query
-tile), all four key runs (sinks | segment | prev | causal cur), every supported group size, more than
+ones as given); the bar is the bf16 attention bound max |d| <= 2e-3.  Shapes: ragged query counts
+(not multiples of the 32-query tile), all four key runs (sinks | segment | prev | causal cur), every supported group size, more than
 eight query blocks (split launches), and the full block-sliding prefill workload (L = 8192, W = 1024,
 512 sinks) checked on sampled query rows.
 """

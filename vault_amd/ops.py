@@ -404,9 +404,10 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
     """MFMA prefill attention for up to 8 query blocks per launch (more are split).
 
     Each block is a dict: ``q`` [n_q, H, D] view (fp32 or bf16, any token / head stride, D contiguous),
-    ``out`` [n_q, H, D] view, fp32 or bf16 (one dtype for all blocks), ``runs``: list of (K, V) views [G, n, D] (bf16, or fp32 entering the
-    MFMAs as bf16 hi + lo; one dtype for all runs; D contiguous, any row and group stride),
-    ``causal_base``: -1, or b >= 0 making the last run causal (query t sees its keys j <= b + t)."""
+    ``out`` [n_q, H, D] view, fp32 or bf16 (one dtype for all blocks), ``runs``: list of (K, V) views
+    [G, n, D] (bf16, or fp32 entering the MFMAs as bf16 hi + lo; one dtype for all runs; D contiguous,
+    any row and group stride), ``causal_base``: -1, or b >= 0 making the last run causal (query t sees
+    its keys j <= b + t)."""
     lib = L.load()
     if not blocks:
         return
