@@ -3,7 +3,7 @@
 Oracles: the float64 oracle model (itself pinned against the reference C runtime in
 tests/test_oracle_model.py) and, where oracle/_ref is built, the reference C runtime directly.
 Bars: the reference's differential bar (tests/test_vlt3_runtime.py:90-94) rel < 1e-4 with fp32 KV and
-100% top-1; the north-star full-model bar max|dlogit| <= 5e-2 with 100% top-1 for bf16 KV; the
+100% top-1; the full-model bar max|dlogit| <= 5e-2 with 100% top-1 for bf16 KV; the
 reference's self-consistency invariants (tests/test_vault_v3.py:52-90): forward == step stream and
 prefill(split) + stream == forward, < 1e-4.
 """
