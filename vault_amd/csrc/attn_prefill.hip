@@ -16,8 +16,10 @@
 //                                      the S^T accumulators as a bf16 hi + lo pair (two MFMAs):
 //                                      8-bit probabilities alone exceed the bf16 attention bound
 //                                      when few keys carry the weight.
-// K and V stay bf16 end to end (no conversions in the staging loop): MFMA throughput is abundant
-// here, VALU issue is what bounds the kernel.  In both products a lane of the 16 x 16 output owns
+// bf16 K and V stay bf16 end to end (no conversions in the staging loop): MFMA throughput is abundant
+// here, VALU issue is what bounds the kernel.  fp32 K and V (an fp32 state read in place) are staged
+// as bf16 hi + lo planes; their products take hi x hi, hi x lo and lo x hi, and drop lo x lo, which
+// is below 2^-18 of each product and so under the rounding of the splits themselves.  In both products a lane of the 16 x 16 output owns
 // one query column, so the online-softmax state (running max, rescale of O) is lane-local; the max
 // over a query's keys needs two cross-lane steps.  The K-dimension slots of A and B are assigned the
 // same way in each product (lane group lg holds slots 8 lg .. 8 lg + 7 of both operands), which is
@@ -297,7 +299,9 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                     for (int qt = 0; qt < NQT; ++qt) {
                         sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qh[qt][kc], sc[qt][0], 0, 0, 0);
                         sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qh[qt][kc], sc[qt][1], 0, 0, 0);
-                        if constexpr (QSPLIT) {
+                        // q lo against K hi only: q lo x K lo is below 2^-18 of each product, under the
+                        // 2^-17 rounding of the hi + lo splits themselves
+                        if (QSPLIT && pk == 0) {
                             sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ql[qt][kc], sc[qt][0], 0, 0, 0);
                             sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ql[qt][kc], sc[qt][1], 0, 0, 0);
                         }
@@ -370,7 +374,8 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
                     for (int qt = 0; qt < NQT; ++qt) {
                         o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[qt], o[qt][dt], 0, 0, 0);
-                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[qt], o[qt][dt], 0, 0, 0);
+                        if (pv_ == 0)   // P lo x V lo dropped, as q lo x K lo above
+                            o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[qt], o[qt][dt], 0, 0, 0);
                     }
                 }
             }
