@@ -273,6 +273,27 @@ int vgx_qkv_rope_step(int q_dtype, const void *wq, const float *bq, int kv_wdtyp
                       int kv_dtype, void *k_rot, void *k_raw, void *v_dst, int64_t dst_gstride, int64_t dst_rstride,
                       void *sink_k_raw, void *sink_v, int64_t sink_gstride, int64_t sink_rstride, void *stream);
 
+/* A decode batch (1 <= B <= 64 sequences, one token each): RMSNorm + q / k / v projections + bias,
+ * RoPE of q and k, and the ring / sink writes of vgx_rope_qkv_write_step, with the K-split sums of
+ * the projections taken by the RoPE launch (no reduce launch of their own).  Weights packed with
+ * vgx_qweight_pack (Q8_0 / Q4_0): wq [H*D x d_model] and wkv [2*G*D x d_model] (k rows then v rows),
+ * or wq NULL and wkv [(H+2*G)*D x d_model] holding q, k and v rows (then bq must be NULL and bkv is
+ * the bias of all rows).  x [B][d_model] (row stride ldx, 16-byte aligned, ldx % 4 == 0); norm_w
+ * (16-byte aligned) may be NULL for no RMSNorm.  q_out [B][H][D] (row stride ldq) receives the
+ * rotated queries; the state tensors are addressed as in vgx_rope_qkv_write_step.  workspace: at
+ * least vgx_qkv_rope_batch_workspace_bytes(B, d_model, H, G, D, wq != NULL) bytes, 256-byte aligned.
+ * Replaces src/vault_v3_model.py:1041-1047, 1079-1094 (the batched decode path) and
+ * runtime/vault3.c:2152-2179 per sequence. */
+int64_t vgx_qkv_rope_batch_workspace_bytes(int64_t B, int64_t d_model, int64_t H, int64_t G, int64_t D,
+                                           int separate_q);
+int vgx_qkv_rope_batch(int q_wdtype, const void *wq, const float *bq, int kv_wdtype, const void *wkv,
+                       const float *bkv, int64_t d_model, int64_t H, int64_t G, int64_t D, const float *x, int64_t ldx,
+                       int64_t B, const float *norm_w, float eps, const float *table, int64_t table_rstride,
+                       const int32_t *step, float *q_out, int64_t ldq, int kv_dtype, void *k_rot, void *k_raw,
+                       void *v_dst, int64_t dst_bstride, int64_t dst_gstride, int64_t dst_rstride, void *sink_k_raw,
+                       void *sink_v, int64_t sink_bstride, int64_t sink_gstride, int64_t sink_rstride,
+                       void *workspace, int64_t workspace_bytes, void *stream);
+
 /* Rotate rows: dst[o, i, :] = R(src[o, i, :]) with angle row table + i*table_rstride, for o < n_outer,
  * i < n_rows (rows contiguous, D elements each; src may equal dst).  Replaces the chunk-boundary
  * re-base of k_prev by R_{-W} and the prefix re-rotation of segment/sink keys

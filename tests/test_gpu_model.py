@@ -82,15 +82,18 @@ def test_forward_and_prefill_consistency(dev):
         assert max(errs) < 1e-4 * max(1.0, np.abs(ref_f).max()), (split, max(errs))
 
 
-def test_batched_swa_stream(dev):
-    """Batch 2 without segment memory: each row equals its own batch-1 stream (SWA + sinks)."""
+@pytest.mark.parametrize("batch,fmt", [(2, "q4_0"), (9, "q4_0"), (9, "q8_0")])
+def test_batched_swa_stream(dev, batch, fmt):
+    """A batch without segment memory: each row equals its own batch-1 stream (SWA + sinks).  Batch 9
+    runs the small-batch GEMM, with the q/k/v K-split sums taken by the RoPE launch."""
     cfg = modelgen.tiny_cfg(seg_budget=0)
-    tensors, _, deq = modelgen.build(cfg, "q4_0", seed=2)
+    tensors, _, deq = modelgen.build(cfg, fmt, seed=2)
     m = _gpu_model(cfg, tensors, dev)
-    ids = torch.tensor([modelgen.ids_stream(cfg, 53, seed=s) for s in (6, 7)])
-    out = m.forward(ids).double().cpu().numpy()                     # (2, L, V)
+    assert m._batch_qkv_fusable(batch) == (batch >= 8)
+    ids = torch.tensor([modelgen.ids_stream(cfg, 53, seed=s) for s in range(6, 6 + batch)])
+    out = m.forward(ids).double().cpu().numpy()                     # (B, L, V)
     om = OracleModel(cfg, deq)
-    for b in range(2):
+    for b in range(batch):
         ost = om.new_state()
         om.set_pinned(ost, cfg.n_sink)
         want = om.stream(ids[b].tolist(), ost)

@@ -58,6 +58,9 @@ _SIGS = {
                                       I64, P, P, I64, I64, I64, P]),
     "vgx_qkv_rope_step": (I32, [I32, P, P, I32, P, P, I64, I64, I64, I64, P, P, F, P, P, I64, P, P, I32, P, P, P, I64,
                                 I64, P, P, I64, I64, P]),
+    "vgx_qkv_rope_batch_workspace_bytes": (I64, [I64, I64, I64, I64, I64, I32]),
+    "vgx_qkv_rope_batch": (I32, [I32, P, P, I32, P, P, I64, I64, I64, I64, P, I64, I64, P, F, P, I64, P, P, I64, I32,
+                                 P, P, P, I64, I64, I64, P, P, I64, I64, I64, P, I64, P]),
 }
 
 

@@ -100,6 +100,22 @@ VGX_DEV void split_bf16x2(float a, float b, uint32_t &hi, uint32_t &lo) {
     lo = pack_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
 }
 
+// One element of a KV-state tensor of dtype KV (VGX_F32, or VGX_BF16 rounded to nearest even).
+template <int KV>
+VGX_DEV void store_kv(void *base, int64_t idx, float v) {
+    if constexpr (KV == VGX_F32) {
+        static_cast<float *>(base)[idx] = v;
+    } else {
+        static_cast<uint16_t *>(base)[idx] = (uint16_t)float_to_bf16_bits(v);
+    }
+}
+
+template <int KV>
+VGX_DEV float load_kv(const void *base, int64_t idx) {
+    if constexpr (KV == VGX_F32) return static_cast<const float *>(base)[idx];
+    return bf16_bits_to_float(static_cast<const uint16_t *>(base)[idx]);
+}
+
 }  // namespace vgx
 
 #define VGX_CHECK_LAUNCH()                                  \

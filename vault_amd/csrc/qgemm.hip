@@ -835,6 +835,138 @@ inline int64_t small_bytes(int64_t batch, int64_t n_rq, int nblk) {
     return part_bytes(ks, batch, n_rq * 4) + ((int64_t)ks * batch * 4 + 255) / 256 * 256;
 }
 
+// K-split partials of one projection of a decode batch: part [ks][batch][rows_p] and, with the
+// RMSNorm, the per-split sum x^2 of every activation row pssq [ks][batch]; roff is the first row of
+// the part this launch reads (q rows then k and v rows when one weight holds all three).
+struct SplitSrc {
+    const float *part;
+    const float *pssq;
+    const float *bias;
+    int ks;
+    int64_t rows_p;
+    int64_t roff;
+};
+
+// Sum over the splits (k = 0, 1, ... in order), then the RMSNorm scale and the bias, as
+// qgemm_reduce_kernel does.  KM >= ks is a compile-time bound: the loads of all splits go out at
+// once (indexes clamped to the last split, so none is out of range) instead of one round trip per
+// split of a loop with a run-time count.
+template <int KM>
+__device__ __forceinline__ float split_value(const SplitSrc &s, int64_t batch, int64_t t, int64_t r, float inv) {
+    float p[KM];
+#pragma unroll
+    for (int k = 0; k < KM; ++k) p[k] = s.part[((int64_t)min(k, s.ks - 1) * batch + t) * s.rows_p + s.roff + r];
+    float v = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+        if (k < s.ks) v += p[k];
+    v *= inv;
+    if (s.bias) v += s.bias[s.roff + r];
+    return v;
+}
+
+template <int KM>
+__device__ __forceinline__ float split_inv(const SplitSrc &s, int64_t batch, int64_t t, int cols, float eps) {
+    if (!s.pssq) return 1.0f;
+    float p[KM];
+#pragma unroll
+    for (int k = 0; k < KM; ++k) p[k] = s.pssq[(int64_t)min(k, s.ks - 1) * batch + t];
+    float u = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+        if (k < s.ks) u += p[k];
+    return 1.0f / sqrtf(u / (float)cols + eps);
+}
+
+// q / k / v of a decode batch from the K-split partials of their projections, with RoPE and the
+// ring / sink writes, in one launch.  grid (batch, H + G), threads over the D / 2 RoPE pairs.  The
+// ring slot, RoPE table row and sink slot come from the device step descriptor.
+template <int KV, int KM>
+__global__ __launch_bounds__(256) void qkv_split_rope_kernel(SplitSrc sq, SplitSrc skv, int64_t batch, int cols,
+                                                             float eps, int H, int G, int D,
+                                                             const float *__restrict__ table, int64_t trs,
+                                                             const int32_t *__restrict__ step, float *q_out,
+                                                             int64_t ldq, void *k_rot, void *k_raw, void *v_dst,
+                                                             int64_t dbs, int64_t dgs, int64_t drs, void *sk, void *sv,
+                                                             int64_t sbs, int64_t sgs, int64_t srs) {
+    const int64_t t = blockIdx.x;
+    const int hd = blockIdx.y;
+    const int h2 = D / 2;
+    const int64_t slot = step[VGX_STEP_SLOT];
+    const int64_t sink = step[VGX_STEP_SINK_SLOT];
+    const float *cs = table + (int64_t)step[VGX_STEP_TABLE_ROW] * trs;
+    if (hd < H) {
+        const float inv = split_inv<KM>(sq, batch, t, cols, eps);
+        float *qp = q_out + t * ldq + (int64_t)hd * D;
+        for (int i = threadIdx.x; i < h2; i += blockDim.x) {
+            const float c = cs[i], s = cs[h2 + i];
+            const float a = split_value<KM>(sq, batch, t, (int64_t)hd * D + i, inv);
+            const float b = split_value<KM>(sq, batch, t, (int64_t)hd * D + i + h2, inv);
+            qp[i] = a * c - b * s;
+            qp[i + h2] = b * c + a * s;
+        }
+        return;
+    }
+    const int g = hd - H;
+    const float inv = split_inv<KM>(skv, batch, t, cols, eps);
+    const int64_t kr = (int64_t)g * D, vr = (int64_t)(G + g) * D;
+    const int64_t o = t * dbs + g * dgs + slot * drs;
+    const int64_t so = t * sbs + g * sgs + sink * srs;
+    for (int i = threadIdx.x; i < h2; i += blockDim.x) {
+        const float c = cs[i], s = cs[h2 + i];
+        const float a = split_value<KM>(skv, batch, t, kr + i, inv);
+        const float b = split_value<KM>(skv, batch, t, kr + i + h2, inv);
+        const float va = split_value<KM>(skv, batch, t, vr + i, inv);
+        const float vb = split_value<KM>(skv, batch, t, vr + i + h2, inv);
+        if (k_rot) {
+            store_kv<KV>(k_rot, o + i, a * c - b * s);
+            store_kv<KV>(k_rot, o + i + h2, b * c + a * s);
+        }
+        if (k_raw) {
+            store_kv<KV>(k_raw, o + i, a);
+            store_kv<KV>(k_raw, o + i + h2, b);
+        }
+        store_kv<KV>(v_dst, o + i, va);
+        store_kv<KV>(v_dst, o + i + h2, vb);
+        if (sink >= 0 && sk) {
+            store_kv<KV>(sk, so + i, a);
+            store_kv<KV>(sk, so + i + h2, b);
+            store_kv<KV>(sv, so + i, va);
+            store_kv<KV>(sv, so + i + h2, vb);
+        }
+    }
+}
+
+// Workspace of one split projection (partials, then the per-split sum x^2), 256-byte multiples.
+inline int64_t split_proj_bytes(int64_t batch, int64_t rows, int nblk) {
+    const int64_t n_rq = rows4(rows) / 4;
+    int kper = 0;
+    const int ks = small_ksplit(n_rq, batch, nblk, &kper);
+    return ((int64_t)ks * batch * n_rq * 16 + 255) / 256 * 256 + ((int64_t)ks * batch * 4 + 255) / 256 * 256;
+}
+
+// The small-batch kernel writing K-split partials (one split or more) into part / pssq; returns ks.
+int split_proj_launch(int dtype, const void *wp, int64_t rows, int64_t cols, const float *x, int64_t ldx,
+                      int64_t batch, const float *norm_w, float eps, float *part, float *pssq, hipStream_t st) {
+    const int nblk = (int)(cols / QK);
+    const int64_t n_rq = rows4(rows) / 4;
+    int kper = 0;
+    const int ks = small_ksplit(n_rq, batch, nblk, &kper);
+    const int64_t soff = gemm_scale_off(dtype, rows, cols);
+    const int nc = small_nc(batch, n_rq);
+    const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 16 * nc - 1) / (16 * nc)), (unsigned)ks);
+    const auto *w = static_cast<const uint8_t *>(wp);
+#define VGX_SP(DT, NC, NORM)                                                                                      \
+    hipLaunchKernelGGL((qgemm_small_kernel<DT, NC, EPI_STORE, true, NORM>), grid, dim3(256), 0, st, w, soff, n_rq, \
+                       nblk, rows, x, ldx, norm_w, eps, batch, nullptr, nullptr, (int64_t)0, part, pssq, kper)
+#define VGX_SP_N(DT, NC) do { if (norm_w) VGX_SP(DT, NC, true); else VGX_SP(DT, NC, false); } while (0)
+    if (dtype == VGX_Q8_0) { if (nc == 1) VGX_SP_N(VGX_Q8_0, 1); else VGX_SP_N(VGX_Q8_0, 2); }
+    else { if (nc == 1) VGX_SP_N(VGX_Q4_0, 1); else VGX_SP_N(VGX_Q4_0, 2); }
+#undef VGX_SP_N
+#undef VGX_SP
+    return ks;
+}
+
 }  // namespace
 
 extern "C" {
@@ -967,6 +1099,86 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
             hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_STORE>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy, nullptr, (int)cols, 0.0f);
         VGX_CHECK_LAUNCH();
     }
+    return VGX_OK;
+}
+
+int64_t vgx_qkv_rope_batch_workspace_bytes(int64_t B, int64_t d_model, int64_t H, int64_t G, int64_t D,
+                                           int separate_q) {
+    if (B <= 0 || d_model <= 0 || H <= 0 || G <= 0 || D <= 0) return VGX_E_SIZE;
+    if (d_model % QK) return VGX_E_SHAPE;
+    const int nblk = (int)(d_model / QK);
+    if (separate_q) return split_proj_bytes(B, H * D, nblk) + split_proj_bytes(B, 2 * G * D, nblk);
+    return split_proj_bytes(B, (H + 2 * G) * D, nblk);
+}
+
+int vgx_qkv_rope_batch(int q_wdtype, const void *wq, const float *bq, int kv_wdtype, const void *wkv,
+                       const float *bkv, int64_t d_model, int64_t H, int64_t G, int64_t D, const float *x, int64_t ldx,
+                       int64_t B, const float *norm_w, float eps, const float *table, int64_t table_rstride,
+                       const int32_t *step, float *q_out, int64_t ldq, int kv_dtype, void *k_rot, void *k_raw,
+                       void *v_dst, int64_t dst_bstride, int64_t dst_gstride, int64_t dst_rstride, void *sink_k_raw,
+                       void *sink_v, int64_t sink_bstride, int64_t sink_gstride, int64_t sink_rstride,
+                       void *workspace, int64_t workspace_bytes, void *stream) {
+    const bool sep = wq != nullptr;
+    if (kv_wdtype != VGX_Q8_0 && kv_wdtype != VGX_Q4_0) return VGX_E_DTYPE;
+    if (sep && q_wdtype != VGX_Q8_0 && q_wdtype != VGX_Q4_0) return VGX_E_DTYPE;
+    if (kv_dtype != VGX_F32 && kv_dtype != VGX_BF16) return VGX_E_DTYPE;
+    if (!wkv || !x || !table || !step || !q_out || !v_dst || !workspace) return VGX_E_ARG;
+    if (!sep && bq) return VGX_E_ARG;                  // one weight for q|k|v: its bias is bkv
+    if ((sink_k_raw == nullptr) != (sink_v == nullptr)) return VGX_E_ARG;
+    if (norm_w && !(eps > 0.0f)) return VGX_E_ARG;
+    if (B <= 0 || H <= 0 || G <= 0 || D <= 0 || (D & 1) || d_model <= 0 || ldx < d_model || ldq < H * D)
+        return VGX_E_SIZE;
+    if (d_model % QK) return VGX_E_SHAPE;
+    if (B > kSmallMaxBatch || H + G > 65535 || D / 2 > 4096) return VGX_E_LIMIT;
+    if (((uintptr_t)x & 15) || ldx % 4 || ((uintptr_t)norm_w & 15)) return VGX_E_ALIGN;
+    if ((uintptr_t)workspace % 256) return VGX_E_ALIGN;
+    if (workspace_bytes < vgx_qkv_rope_batch_workspace_bytes(B, d_model, H, G, D, sep ? 1 : 0)) return VGX_E_ARENA;
+    hipStream_t st = (hipStream_t)stream;
+    const int nblk = (int)(d_model / QK);
+    auto *base = static_cast<char *>(workspace);
+    auto carve = [&](int64_t rows, float *&part, float *&pssq) {
+        const int64_t n_rq = rows4(rows) / 4;
+        int kper = 0;
+        const int ks = small_ksplit(n_rq, B, nblk, &kper);
+        part = reinterpret_cast<float *>(base);
+        base += ((int64_t)ks * B * n_rq * 16 + 255) / 256 * 256;
+        pssq = reinterpret_cast<float *>(base);
+        base += ((int64_t)ks * B * 4 + 255) / 256 * 256;
+    };
+    SplitSrc sq{}, skv{};
+    float *part = nullptr, *pssq = nullptr;
+    if (sep) {
+        carve(H * D, part, pssq);
+        sq.ks = split_proj_launch(q_wdtype, wq, H * D, d_model, x, ldx, B, norm_w, eps, part, pssq, st);
+        sq.part = part; sq.pssq = norm_w ? pssq : nullptr; sq.bias = bq; sq.rows_p = rows4(H * D); sq.roff = 0;
+        VGX_CHECK_LAUNCH();
+        carve(2 * G * D, part, pssq);
+        skv.ks = split_proj_launch(kv_wdtype, wkv, 2 * G * D, d_model, x, ldx, B, norm_w, eps, part, pssq, st);
+        skv.part = part; skv.pssq = norm_w ? pssq : nullptr; skv.bias = bkv; skv.rows_p = rows4(2 * G * D);
+        skv.roff = 0;
+    } else {
+        const int64_t rows = (H + 2 * G) * D;
+        carve(rows, part, pssq);
+        skv.ks = split_proj_launch(kv_wdtype, wkv, rows, d_model, x, ldx, B, norm_w, eps, part, pssq, st);
+        skv.part = part; skv.pssq = norm_w ? pssq : nullptr; skv.bias = bkv; skv.rows_p = rows4(rows);
+        sq = skv;
+        skv.roff = H * D;
+    }
+    VGX_CHECK_LAUNCH();
+    const dim3 grid((unsigned)B, (unsigned)(H + G));
+    const int thr = (int)std::min<int64_t>(256, std::max<int64_t>(64, D / 2));
+    const int km = std::max(sq.ks, skv.ks);
+#define VGX_QSR(KV, KM)                                                                                         \
+    hipLaunchKernelGGL((qkv_split_rope_kernel<KV, KM>), grid, dim3(thr), 0, st, sq, skv, B, (int)d_model, eps,   \
+                       (int)H, (int)G, (int)D, table, table_rstride, step, q_out, ldq, k_rot, k_raw, v_dst,       \
+                       dst_bstride, dst_gstride, dst_rstride, sink_k_raw, sink_v, sink_bstride, sink_gstride,     \
+                       sink_rstride)
+#define VGX_QSR_K(KV) do { if (km <= 4) VGX_QSR(KV, 4); else if (km <= 8) VGX_QSR(KV, 8); else VGX_QSR(KV, 16); } while (0)
+    static_assert(kMaxKSplit <= 16, "split bound of qkv_split_rope_kernel");
+    if (kv_dtype == VGX_F32) VGX_QSR_K(VGX_F32); else VGX_QSR_K(VGX_BF16);
+#undef VGX_QSR_K
+#undef VGX_QSR
+    VGX_CHECK_LAUNCH();
     return VGX_OK;
 }
 

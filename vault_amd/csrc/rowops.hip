@@ -9,21 +9,6 @@ using namespace vgx;
 
 namespace {
 
-template <int KV>
-__device__ __forceinline__ void store_kv(void *base, int64_t idx, float v) {
-    if constexpr (KV == VGX_F32) {
-        static_cast<float *>(base)[idx] = v;
-    } else {
-        static_cast<uint16_t *>(base)[idx] = (uint16_t)float_to_bf16_bits(v);
-    }
-}
-
-template <int KV>
-__device__ __forceinline__ float load_kv(const void *base, int64_t idx) {
-    if constexpr (KV == VGX_F32) return static_cast<const float *>(base)[idx];
-    return bf16_bits_to_float(static_cast<const uint16_t *>(base)[idx]);
-}
-
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *__restrict__ x, int64_t ldx,
                                                        const float *__restrict__ w, float *__restrict__ y,
                                                        int64_t ldy, int64_t dim, float eps) {

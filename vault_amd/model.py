@@ -459,6 +459,18 @@ class VAULTv3ForCausalLM:
         ent[0].replay()
         return ent[1].clone()
 
+    def _batch_qkv_fusable(self, B: int) -> bool:
+        """Decode batches that run the small-batch GEMM (8..64 rows) on Q8_0 / Q4_0 q/k/v weights take
+        the projections' K-split sums in the RoPE launch (ops.qkv_rope_batch)."""
+        if not ops.GEMM_MIN_ROWS <= B <= 64:
+            return False
+        for lw in self.w.layers:
+            if lw.wqkv.dtype not in (ops.Q8_0, ops.Q4_0) or lw.ln1.data_ptr() % 16:
+                return False
+            if lw.wq is not None and lw.wq.dtype not in (ops.Q8_0, ops.Q4_0):
+                return False
+        return True
+
     def _size_workspace(self, st: VAULTv3State) -> None:
         """Grow the workspaces before a capture (a captured graph holds their addresses): attention to
         the bound of any decode step of this batch size (B * H * 64 splits * (D + 2) floats), and the
@@ -473,6 +485,9 @@ class VAULTv3ForCausalLM:
                       (cfg.d_model, cfg.n_heads * cfg.head_dim, ops.L.EPI_ACCUM),
                       (cfg.vocab_size, cfg.d_model, ops.L.EPI_STORE)]
             need = max(int(lib.vgx_qgemm_workspace_bytes(st.batch, r, c, e)) for r, c, e in shapes)
+            if self._batch_qkv_fusable(st.batch):
+                need = max([need] + [int(lib.vgx_qkv_rope_batch_workspace_bytes(
+                    st.batch, cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, sep)) for sep in (0, 1)])
             ops.gemm_workspace(self.device).get(need)
 
     def _decode_launch(self, st: VAULTv3State, spec: tuple, bias_on: bool) -> torch.Tensor:
@@ -493,7 +508,8 @@ class VAULTv3ForCausalLM:
         table = self._rows(self._p0)
         scale = 1.0 / math.sqrt(D)
         fused = B == 1 and all(lw.wq_rope is not None for lw in w.layers)
-        qbuf = torch.empty(B, H, D, dtype=torch.float32, device=self.device) if fused else None
+        batch_fused = not fused and self._batch_qkv_fusable(B)
+        qbuf = torch.empty(B, H, D, dtype=torch.float32, device=self.device) if fused or batch_fused else None
         for li, lw in enumerate(w.layers):
             xc = None
             if seg_active and li in cfg.seg_layers:
@@ -507,6 +523,12 @@ class VAULTv3ForCausalLM:
                 ops.qkv_rope_step(lw.wq_rope, lw.bq, lw.wkv_rope, bkv, x, (lw.ln1, cfg.rms_eps), table, D, step,
                                   qbuf, st.k_cur[li], st.kraw_cur[li], st.v_cur[li], st.k_sink_raw[li],
                                   st.v_sink[li], x_copy=xc)
+                q = qbuf
+            elif batch_fused:
+                # projections as K-split partials, summed by the RoPE / ring-write launch
+                ops.qkv_rope_batch(lw.wq, lw.bq if lw.wq is not None else None, lw.wqkv, lw.bqkv, x,
+                                   (lw.ln1, cfg.rms_eps), table, D, step, qbuf, st.k_cur[li], st.kraw_cur[li],
+                                   st.v_cur[li], st.k_sink_raw[li], st.v_sink[li])
                 q = qbuf
             else:
                 q, k, v = self._qkv(lw, x, B)

@@ -400,6 +400,43 @@ def qkv_rope_step(wq: QWeight, bq: Optional[torch.Tensor], wkv: QWeight, bkv: Op
         "vgx_qkv_rope_step")
 
 
+def qkv_rope_batch(wq: Optional[QWeight], bq: Optional[torch.Tensor], wkv: QWeight, bkv: Optional[torch.Tensor],
+                   x: torch.Tensor, norm: Optional[Tuple[torch.Tensor, float]], table: torch.Tensor,
+                   table_rstride: int, step: torch.Tensor, q_out: torch.Tensor, k_rot: Optional[torch.Tensor],
+                   k_raw: Optional[torch.Tensor], v_dst: torch.Tensor, sink_k: Optional[torch.Tensor],
+                   sink_v: Optional[torch.Tensor]) -> None:
+    """A decode batch of B <= 64 sequences (one token each): RMSNorm + q/k/v projections + bias, RoPE,
+    ring and sink writes, with the projections' K-split sums taken by the RoPE launch.  wq [H*D, d] and
+    wkv [2*G*D, d] (k then v rows), or wq None and wkv [(H+2*G)*D, d]; x [B, d] fp32; q_out [B, H, D]
+    fp32; ring tensors [B, G, W, D] and sink tensors [B, G, S_cap, D] of the state dtype."""
+    B, d = x.shape
+    G, D = v_dst.shape[1], v_dst.shape[3]
+    H = q_out.shape[1]
+    if x.stride(1) != 1 or q_out.stride(2) != 1 or q_out.stride(1) != D:
+        raise ValueError("x rows and q_out heads must be contiguous")
+    for t in (k_rot, k_raw, v_dst, sink_k, sink_v):
+        if t is not None and t.stride(2) != D:
+            raise ValueError("ring rows must be contiguous")
+    if k_rot is not None and k_rot.stride() != v_dst.stride():
+        raise ValueError("k_rot and v_dst need equal strides")
+    if k_raw is not None and k_raw.stride() != v_dst.stride():
+        raise ValueError("k_raw and v_dst need equal strides")
+    if sink_k is not None and sink_k.stride() != sink_v.stride():
+        raise ValueError("sink_k and sink_v need equal strides")
+    nw, eps = (norm[0], float(norm[1])) if norm is not None else (None, 0.0)
+    lib = L.load()
+    need = int(lib.vgx_qkv_rope_batch_workspace_bytes(B, d, H, G, D, 1 if wq is not None else 0))
+    ws = gemm_workspace(x.device).get(need)
+    sk_b, sk_g, sk_r = (sink_k.stride(0), sink_k.stride(1), sink_k.stride(2)) if sink_k is not None else (0, 0, 0)
+    L.check(lib.vgx_qkv_rope_batch(
+        wq.dtype if wq is not None else 0, wq.packed.data_ptr() if wq is not None else None, _ptr(bq), wkv.dtype,
+        wkv.packed.data_ptr(), _ptr(bkv), d, H, G, D, x.data_ptr(), x.stride(0), B, _ptr(nw), eps,
+        table.data_ptr(), table_rstride, step.data_ptr(), q_out.data_ptr(), q_out.stride(0), KV_DTYPES[v_dst.dtype],
+        _ptr(k_rot), _ptr(k_raw), v_dst.data_ptr(), v_dst.stride(0), v_dst.stride(1), v_dst.stride(2),
+        _ptr(sink_k), _ptr(sink_v), sk_b, sk_g, sk_r, ws.data_ptr(), ws.numel(), _stream(x.device)),
+        "vgx_qkv_rope_batch")
+
+
 def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
     """MFMA prefill attention for up to 8 query blocks per launch (more are split).
 
