@@ -403,7 +403,7 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for per-kernel profiles of the step)")
     ap.add_argument("--figures", choices=("gemv", "attn_decode", "attn_decode_b1", "attn_prefill", "gemm_prefill",
-                                          "dominant"),
+                                          "dominant", "decode_batch32"),
                     help="only one set of kernel figures, printed as JSON (for per-kernel profiles)")
     ap.add_argument("--pmc", action="store_true",
                     help="only run the launches the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count")
@@ -433,6 +433,12 @@ def main() -> int:
         model, tensors = build_model(cfg, dev, torch.float32)
         del tensors
         print(json.dumps({"dominant": dominant_kernel(model)}), flush=True)
+        return 0
+    if args.figures == "decode_batch32":
+        cfg = model_config()
+        model, tensors = build_model(cfg, dev, torch.float32)
+        del tensors
+        print(json.dumps({"decode_batch32": batched_decode(model)}), flush=True)
         return 0
     if args.figures:
         fig = {"gemv": gemv_figures, "attn_decode": attn_figures, "attn_decode_b1": attn_b1_figures,
