@@ -732,7 +732,9 @@ __global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const u
 // up sums of packed row-quad q (sub-rows k and 2 + k) for output row 2 q + k.
 // part_ssq (when not null): per-split sum x^2 of every activation row; the sums are then scaled by
 // 1 / sqrt(mean(x^2) + eps) (the RMSNorm of the small-batch kernel).
-template <int EPI>
+// KM >= ks is a compile-time bound: every split's load goes out at once (indexes clamped to the last
+// split), then the sums run in split order, instead of one load round trip per split.
+template <int EPI, int KM>
 __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float *__restrict__ part, int ks, int64_t batch,
                                                             int64_t rows_p, int64_t rows_out,
                                                             const float *__restrict__ bias, float *__restrict__ y,
@@ -742,31 +744,63 @@ __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float *__restri
     if (i >= batch * rows_out) return;
     const int64_t b = i / rows_out, r = i - b * rows_out;
     float *yr = y + b * ldy;
+    auto at = [&](int s) -> int64_t { return ((int64_t)min(s, ks - 1) * batch + b) * rows_p; };
     float inv = 1.0f;
     if (part_ssq) {
+        float p[KM];
+#pragma unroll
+        for (int s = 0; s < KM; ++s) p[s] = part_ssq[(int64_t)min(s, ks - 1) * batch + b];
         float t = 0.0f;
-        for (int s = 0; s < ks; ++s) t += part_ssq[s * batch + b];
+#pragma unroll
+        for (int s = 0; s < KM; ++s)
+            if (s < ks) t += p[s];
         inv = 1.0f / sqrtf(t / (float)cols + eps);
     }
     if constexpr (EPI == EPI_SWIGLU) {
         const int64_t q = r >> 1, k = r & 1;
+        float pg[KM], pu[KM];
+#pragma unroll
+        for (int s = 0; s < KM; ++s) {
+            pg[s] = part[at(s) + q * 4 + k];
+            pu[s] = part[at(s) + q * 4 + 2 + k];
+        }
         float g = 0.0f, u = 0.0f;
-        for (int s = 0; s < ks; ++s) {
-            const float *p = part + (s * batch + b) * rows_p + q * 4;
-            g += p[k];
-            u += p[2 + k];
+#pragma unroll
+        for (int s = 0; s < KM; ++s) {
+            if (s < ks) {
+                g += pg[s];
+                u += pu[s];
+            }
         }
         g *= inv;
         u *= inv;
         yr[r] = g / (1.0f + __expf(-g)) * u;
     } else {
+        float p[KM];
+#pragma unroll
+        for (int s = 0; s < KM; ++s) p[s] = part[at(s) + r];
         float v = 0.0f;
-        for (int s = 0; s < ks; ++s) v += part[(s * batch + b) * rows_p + r];
+#pragma unroll
+        for (int s = 0; s < KM; ++s)
+            if (s < ks) v += p[s];
         v *= inv;
         if (bias) v += bias[r];
         if constexpr (EPI == EPI_ACCUM) v += yr[r];
         yr[r] = v;
     }
+}
+
+// Reduce launch with the split bound of ks.
+template <int EPI>
+void reduce_launch(const float *part, int ks, int64_t batch, int64_t rows_p, int64_t rows_out, const float *bias,
+                   float *y, int64_t ldy, const float *part_ssq, int cols, float eps, hipStream_t st) {
+    const unsigned g = (unsigned)((batch * rows_out + 255) / 256);
+#define VGX_RED(KM) hipLaunchKernelGGL((qgemm_reduce_kernel<EPI, KM>), dim3(g), dim3(256), 0, st, part, ks, batch, \
+                                       rows_p, rows_out, bias, y, ldy, part_ssq, cols, eps)
+    if (ks <= 4) VGX_RED(4);
+    else if (ks <= 8) VGX_RED(8);
+    else VGX_RED(16);
+#undef VGX_RED
 }
 
 inline int64_t rows4(int64_t r) { return (r + 3) / 4 * 4; }
@@ -782,6 +816,7 @@ inline int64_t split_bytes(int64_t batch, int64_t cols) {
 }
 
 constexpr int kMaxKSplit = 16;
+static_assert(kMaxKSplit <= 16, "split bound of qgemm_reduce_kernel and qkv_split_rope_kernel");
 constexpr int kTargetWaves = 2048;
 
 // K splits: enough waves to fill the GPU, at least 8 blocks per split.
@@ -1047,14 +1082,13 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
 #undef VGX_SG
         VGX_CHECK_LAUNCH();
         if (ks > 1) {
-            const unsigned g = (unsigned)((batch * rows + 255) / 256);
             const float *ps = norm_w ? pssq : nullptr;
             if (epilogue == VGX_EPI_SWIGLU)
-                hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_SWIGLU>, dim3(g), dim3(256), 0, st0, part, ks, batch, n_rq * 4, rows, bias, y, ldy, ps, (int)cols, eps);
+                reduce_launch<EPI_SWIGLU>(part, ks, batch, n_rq * 4, rows, bias, y, ldy, ps, (int)cols, eps, st0);
             else if (epilogue == VGX_EPI_ACCUM)
-                hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_ACCUM>, dim3(g), dim3(256), 0, st0, part, ks, batch, n_rq * 4, rows, bias, y, ldy, ps, (int)cols, eps);
+                reduce_launch<EPI_ACCUM>(part, ks, batch, n_rq * 4, rows, bias, y, ldy, ps, (int)cols, eps, st0);
             else
-                hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_STORE>, dim3(g), dim3(256), 0, st0, part, ks, batch, n_rq * 4, rows, bias, y, ldy, ps, (int)cols, eps);
+                reduce_launch<EPI_STORE>(part, ks, batch, n_rq * 4, rows, bias, y, ldy, ps, (int)cols, eps, st0);
             VGX_CHECK_LAUNCH();
         }
         return VGX_OK;
@@ -1090,13 +1124,12 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
 #undef VGX_GEMM_GO
     VGX_CHECK_LAUNCH();
     if (ks > 1) {
-        const unsigned g = (unsigned)((batch * rows + 255) / 256);
         if (epilogue == VGX_EPI_SWIGLU)
-            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_SWIGLU>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy, nullptr, (int)cols, 0.0f);
+            reduce_launch<EPI_SWIGLU>(part, ks, batch, n_rq * 4, rows, bias, y, ldy, nullptr, (int)cols, 0.0f, st);
         else if (epilogue == VGX_EPI_ACCUM)
-            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_ACCUM>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy, nullptr, (int)cols, 0.0f);
+            reduce_launch<EPI_ACCUM>(part, ks, batch, n_rq * 4, rows, bias, y, ldy, nullptr, (int)cols, 0.0f, st);
         else
-            hipLaunchKernelGGL(qgemm_reduce_kernel<EPI_STORE>, dim3(g), dim3(256), 0, st, part, ks, batch, n_rq * 4, rows, bias, y, ldy, nullptr, (int)cols, 0.0f);
+            reduce_launch<EPI_STORE>(part, ks, batch, n_rq * 4, rows, bias, y, ldy, nullptr, (int)cols, 0.0f, st);
         VGX_CHECK_LAUNCH();
     }
     return VGX_OK;
@@ -1174,7 +1207,6 @@ int vgx_qkv_rope_batch(int q_wdtype, const void *wq, const float *bq, int kv_wdt
                        dst_bstride, dst_gstride, dst_rstride, sink_k_raw, sink_v, sink_bstride, sink_gstride,     \
                        sink_rstride)
 #define VGX_QSR_K(KV) do { if (km <= 4) VGX_QSR(KV, 4); else if (km <= 8) VGX_QSR(KV, 8); else VGX_QSR(KV, 16); } while (0)
-    static_assert(kMaxKSplit <= 16, "split bound of qkv_split_rope_kernel");
     if (kv_dtype == VGX_F32) VGX_QSR_K(VGX_F32); else VGX_QSR_K(VGX_BF16);
 #undef VGX_QSR_K
 #undef VGX_QSR
