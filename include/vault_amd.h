@@ -90,6 +90,12 @@ int vgx_qweight_dequant(int dtype, const void *packed, float *out, int64_t rows,
 int vgx_embed_rows(int dtype, const void *packed, int64_t rows, int64_t cols, const int64_t *ids, int64_t n_ids,
                    int64_t pad_row, float *out, int64_t ldo, void *stream);
 
+/* Adds to *count (device uint32, zeroed by the caller) the number of non-finite values in a VLT3
+ * payload of n_elems elements: F32 / F16 / BF16 elements, or the fp16 block scales of Q8_0 / Q4_0
+ * AoS blocks (data = the file's block bytes).  Replaces check_tensor_finite (runtime/vault3.c:215-271),
+ * the loader's NaN / Inf rejection. */
+int vgx_count_nonfinite(int dtype, const void *data, int64_t n_elems, uint32_t *count, void *stream);
+
 /* ---------------------------------------------------------------- linear ----------------------- */
 
 /* y[b, r] (+)= sum_c W[r, c] * x[b, c] (+ bias[r]) for b < batch, r < rows.
@@ -163,11 +169,14 @@ typedef struct {
     const int32_t *dyn_len;
 } vgx_kv_span;
 
-/* Workspace bytes vgx_attn_decode needs for these sizes (0 when one split suffices): one int32 ticket
- * per (batch entry, kv group), then the per-split softmax partials (m, l, acc) that the workgroup
- * finishing a pair last combines.  256-byte aligned.  The workspace must be zero-filled before its
- * first use and written by nothing else: every call leaves the tickets at zero (so a captured graph
- * needs no memset).  Calls sharing one workspace must not overlap in time. */
+/* Workspace bytes vgx_attn_decode needs for these sizes (0 when one split suffices): a fixed 16 KiB
+ * region of int32 split tickets (one per (batch entry, kv group) for the first 4096 pairs; its size
+ * and place do not depend on the call), then the per-split softmax partials (m, l, acc) that the
+ * workgroup finishing a pair last combines (or a merge launch, for pairs beyond the ticket region or
+ * more than 32 splits).  256-byte aligned.  The workspace must be zero-filled before its first use
+ * and written by nothing else: every call leaves the tickets at zero (so a captured graph needs no
+ * memset), and calls of any batch / group counts may share one workspace.  Calls sharing one
+ * workspace must not overlap in time. */
 int64_t vgx_attn_decode_workspace_bytes(int64_t B, int64_t H, int64_t G, int64_t D, int64_t n_keys);
 
 /* Decode attention: out[b, h, :] = softmax_j(q[b,h].k_j * scale + bias[h, j]) v_j over the keys of

@@ -2,9 +2,9 @@
 
 Follows src/vault_v3_model.py (step :2214-2311, boundary :1858-1935, prefix re-rotation
 :1842-1856, attention step :1072-1139, scorer :870-883) and runtime/vault3.c (v3_step :2034-2222,
-update_segment_bank :1833-1915), in the offline configuration of both references: no tokenizer
-bytes, so every segment-break tier is 0, no shingles exist and resonance / spoof quarantine are
-inert (seg biases inactive).  RoPE uses the C runtime's angles (double-precision angle, fp32 cos/sin
+update_segment_bank :1833-1915), with the token-byte rules of either reference (see
+``OracleModel.__init__``); shingles, resonance biases and spoof quarantine are not modelled, so the
+token strings of a comparison must produce no shingles (seg biases stay inactive).  RoPE uses the C runtime's angles (double-precision angle, fp32 cos/sin
 of a fp32 inverse frequency, runtime/vault3.c:840-849, 2126-2133, 866-891) by default.
 
 prefill() and forward() are sequences of step() calls: the reference asserts both equal the
@@ -21,6 +21,7 @@ from typing import Dict, List, Optional
 import numpy as np
 
 from . import rope as orope
+from . import tokens as otok
 
 
 def _gelu_erf(x):
@@ -74,12 +75,37 @@ class OracleModel:
     """kv="bf16" stores every cached key/value rounded to bf16 (the model's bf16 KV cache: keys are
     rotated in fp32 and rounded on store, raw keys and values rounded on store)."""
 
-    def __init__(self, cfg, weights: Dict[str, np.ndarray], table=orope.table_c, kv: str = "fp32"):
+    def __init__(self, cfg, weights: Dict[str, np.ndarray], table=orope.table_c, kv: str = "fp32",
+                 token_bytes=None, newline_id: int = 198):
+        """token_bytes: per-id byte strings (the VLT3 file's VTOK) or None.  With them, break tiers
+        and the system-role test follow the bytes and ``newline_id`` is the byte map's entry for
+        '\n' (runtime/vault3.c:937-959, 1920-1928, 2047); without them every tier is 0, the system
+        role is cfg.system_tok_id and the newline id 198 (src/vault_v3_model.py:2224-2268)."""
         self.cfg = cfg
         self.w = {k: np.asarray(v, dtype=np.float64) for k, v in weights.items()}
         self.table = table
         self.has_scorer = cfg.has_seg_scorer and "seg_scorer.ln.weight" in weights
         self._kv = bf16_round if kv == "bf16" else (lambda a: np.asarray(a, dtype=np.float64))
+        self.token_bytes = token_bytes
+        self.newline_id = newline_id if token_bytes is not None else 198
+
+    def _bytes(self, tid: int) -> bytes:
+        tb = self.token_bytes
+        return tb[tid] if tb is not None and 0 <= tid < len(tb) else b""
+
+    def _is_system(self, tid: int) -> bool:
+        if self.token_bytes is None:
+            return tid == self.cfg.system_tok_id
+        return otok.system_role(self._bytes(tid))
+
+    def _seg_break(self, tid: int, seg_len: int) -> bool:
+        """runtime/vault3.c:2109-2122; src/vault_v3_model.py:2260-2268."""
+        c = self.cfg
+        tr = otok.tier(self._bytes(tid))
+        t2 = max(c.seg_min, (c.seg_max * 2) // 3)
+        t3 = max(c.seg_min, c.seg_max - 8 if c.seg_max > 8 else c.seg_min)
+        return (seg_len >= c.seg_max or (tr == 1 and seg_len >= c.seg_min) or (tr == 2 and seg_len >= t2)
+                or (tr == 3 and seg_len >= t3))
 
     # ------------------------------------------------------------------ state
     def new_state(self, seg_budget: Optional[int] = None) -> OState:
@@ -134,12 +160,12 @@ class OracleModel:
             else:
                 st.pin_locked = True
         elif pos == 1 and st.saw_im_start:
-            if tid != c.system_tok_id:
+            if not self._is_system(tid):
                 st.saw_im_start = False
                 st.pin_locked = True
         elif st.saw_im_start and pos < limit:
             if st.awaiting_sys_nl:
-                st.n_pin = max(st.n_pin, pos + 1 if tid == 198 else pos)
+                st.n_pin = max(st.n_pin, pos + 1 if tid == self.newline_id else pos)
                 st.pin_locked = True
                 st.awaiting_sys_nl = False
             elif tid == c.im_end_id:
@@ -242,7 +268,7 @@ class OracleModel:
         if seg_active:
             st.seg_cur[cc] = st.cur_seg_id
             st.seg_len += 1
-            if cc == W - 1 or st.seg_len >= c.seg_max:      # every break tier is 0 offline
+            if cc == W - 1 or self._seg_break(tok, st.seg_len):
                 st.cur_seg_id += 1
                 st.seg_len = 0
         eff = W + cc if pos >= W else cc

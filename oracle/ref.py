@@ -53,6 +53,9 @@ def _load():
         lib.ref_state_field.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p]
         lib.ref_state_field.restype = C.c_int64
         lib.ref_seed_long_context.restype = C.c_int
+        lib.ref_state_flags.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
+        lib.ref_set_seg_budget.argtypes = [C.c_void_p, C.c_uint32]
+        lib.ref_set_seg_budget.restype = C.c_int
         _lib = lib
     return _lib
 
@@ -63,7 +66,9 @@ class RefRuntime:
         err = C.c_int(0)
         self._h = lib.ref_open(vlt3_bytes, len(vlt3_bytes), 1 if verify else 0, C.byref(err))
         if not self._h:
-            raise RuntimeError(f"v3_load / v3_state_init failed: {err.value}")
+            e = RuntimeError(f"v3_load / v3_state_init failed: {err.value}")
+            e.code = err.value
+            raise e
         self.vocab = lib.ref_vocab(self._h)
         self.threads = threads
         lib.ref_set_threads(self._h, threads)
@@ -93,6 +98,16 @@ class RefRuntime:
         pos, n_pin, mem, off = C.c_uint64(), C.c_uint32(), C.c_uint32(), C.c_uint32()
         _load().ref_state_info(self._h, C.byref(pos), C.byref(n_pin), C.byref(mem), C.byref(off))
         return dict(pos=pos.value, n_pin=n_pin.value, mem_cnt=mem.value, seg_id_offset=off.value)
+
+    def flags(self):
+        lk, ba, nu = C.c_int(), C.c_int(), C.c_uint32()
+        _load().ref_state_flags(self._h, C.byref(lk), C.byref(ba), C.byref(nu))
+        return dict(pin_locked=bool(lk.value), seg_bias_active=bool(ba.value), n_uniq_segs=nu.value)
+
+    def set_seg_budget(self, budget: int) -> None:
+        rc = _load().ref_set_seg_budget(self._h, budget)
+        if rc:
+            raise RuntimeError(f"v3_set_seg_budget: {rc}")
 
     def mem_pos(self) -> np.ndarray:
         n = self.info()["mem_cnt"]

@@ -188,6 +188,16 @@ void ref_state_info(ref_ctx *c, uint64_t *pos, uint32_t *n_pin, uint32_t *mem_cn
     *seg_id_offset = c->s.seg_id_offset;
 }
 
+/* Flags of the auto-pin and resonance machinery: pin_locked, seg_bias_active, n_uniq_segs. */
+void ref_state_flags(ref_ctx *c, int *pin_locked, int *seg_bias_active, uint32_t *n_uniq_segs) {
+    *pin_locked = c->s.pin_locked;
+    *seg_bias_active = c->s.seg_bias_active;
+    *n_uniq_segs = c->s.n_uniq_segs;
+}
+
+/* Set the segment budget of the state (v3_set_seg_budget, runtime/vault3.h:158-159). */
+int ref_set_seg_budget(ref_ctx *c, uint32_t budget) { return v3_set_seg_budget(&c->s, budget); }
+
 void ref_mem_pos(ref_ctx *c, uint64_t *out) {
     for (uint32_t i = 0; i < c->s.mem_cnt; i++) out[i] = c->s.mem_pos[i];
 }

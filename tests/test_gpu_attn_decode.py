@@ -242,3 +242,27 @@ def test_gather_rows(dev, kv):
     want = torch.zeros_like(dst)
     want[:, :4] = src[:, [3, 0, 49, 3]]
     assert torch.equal(dst, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_shared_workspace_across_batch_sizes(dev, dtype):
+    """One workspace shared by calls of different (batch, group) counts: batch 1 at 3584 keys (more
+    splits than one workgroup merges: a merge launch over partials) then batch 64 (ticket merge), then
+    batch 1 again; each result equals the same call on a fresh workspace.  With the tickets placed
+    right after a (B, G)-sized prefix, batch 1's partials landed where batch 64 reads its tickets."""
+    rng = np.random.default_rng(11)
+    H, G, D = 12, 2, 128
+    lens = [512, 1024, 1024, 1024]
+    lib = ops.L.load()
+    shared = ops.Workspace(dev)
+    shared.get(max(int(lib.vgx_attn_decode_workspace_bytes(B, H, G, D, sum(lens))) for B in (1, 16, 64)))
+    buf = shared.buf
+    for B in (1, 64, 1, 16, 64):
+        sp = _spans(rng, B, G, D, lens, dtype, dev)
+        q = torch.from_numpy(rng.standard_normal((B, H, D)).astype(np.float32)).to(dev)
+        a = ops.attn_decode(q, sp, ws=shared)
+        b = ops.attn_decode(q, sp, ws=ops.Workspace(dev))
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), B
+        assert shared.buf is buf, "the shared workspace was reallocated"
+        assert int(shared.buf[:16384].view(torch.int32).abs().sum()) == 0, "tickets left non-zero"

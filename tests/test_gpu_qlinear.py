@@ -85,8 +85,10 @@ def test_gemv_benchmark_shapes(dev, dt, rows, cols, batch):
 
 
 @pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
-def test_gemv_lm_head_shape(dev, dt):
-    _check_gemv(dev, dt, 151665, 1536, 1, seed=9)
+@pytest.mark.parametrize("batch", [1, 16])
+def test_gemv_lm_head_shape(dev, dt, batch):
+    """The tied LM head, 151665 x 1536, at batch 1 (one-row GEMV) and 16 (MFMA small-batch GEMM)."""
+    _check_gemv(dev, dt, 151665, 1536, batch, seed=9 + batch)
 
 
 @pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])

@@ -38,6 +38,7 @@ _SIGS = {
     "vgx_qweight_unpack": (I32, [I32, P, P, I64, I64, P]),
     "vgx_qweight_dequant": (I32, [I32, P, P, I64, I64, P]),
     "vgx_embed_rows": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
+    "vgx_count_nonfinite": (I32, [I32, P, I64, P, P]),
     "vgx_qlinear": (I32, [I32, P, I64, I64, P, I64, I64, P, P, I64, I32, P]),
     "vgx_qlinear_swiglu": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
     "vgx_qlinear_ex": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P]),

@@ -66,6 +66,7 @@ class VAULTv3Config:
             seg_budget=h["seg_budget"] if nf else 0, seg_hidden=h["seg_hidden"] if nf else 256,
             seg_min=h["seg_min"] if nf else 16, seg_max=h["seg_max"] if nf else 48,
             seg_layers=tuple(h[f"seg_layer{i}"] for i in range(nf)) if nf else (),
+            im_start_id=h["im_start_id"], im_end_id=h["im_end_id"],
         )
 
 

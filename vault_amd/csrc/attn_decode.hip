@@ -747,11 +747,15 @@ int64_t partial_bytes(int64_t B, int64_t H, int64_t D, int ns) {
     return B * H * (int64_t)ns * (D + 2) * (int64_t)sizeof(float);
 }
 
-// Workspace: the split tickets (one int32 per (b, g), kept at zero between launches) first, then the
-// partials.  Up to kTicketMaxSplits splits are merged by the last workgroup of a pair; with more, the
-// merge work of a pair is too much for one workgroup and attn_merge_kernel spreads it over B * H
-// workgroups.
-int64_t ticket_bytes(int64_t B, int64_t G) { return (B * G * 4 + 255) / 256 * 256; }
+// Workspace: a fixed region of kTicketPairs split tickets (one int32 per (b, g), kept at zero between
+// launches) first, then the partials.  The region's size does not depend on the call, so the partials
+// of one call never overlap the tickets of another call sharing the workspace, whatever their batch
+// and group counts.  Up to kTicketMaxSplits splits of a pair are merged by the pair's last workgroup
+// when the pair has a ticket (b * G + g < kTicketPairs); otherwise attn_merge_kernel spreads the
+// merge over B * H workgroups.
+constexpr int64_t kTicketPairs = 4096;
+int64_t ticket_bytes(int64_t, int64_t) { return kTicketPairs * 4; }
+bool use_tickets(int64_t B, int64_t G, int ns) { return ns <= kTicketMaxSplits && B * G <= kTicketPairs; }
 
 template <int KV, int GRP, int DPL, int NW, int KB>
 void launch_tiled(dim3 grid, hipStream_t st, const float *q, int64_t ldq, const SpanArgs &sp, const float *bias,
@@ -861,7 +865,7 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
         if (ns > 1) {
             if (!workspace || workspace_bytes < ticket_bytes(B, G) + partial_bytes(B, H, D, ns)) return VGX_E_ARENA;
             if ((uintptr_t)workspace % 256) return VGX_E_ALIGN;
-            if (ns <= kTicketMaxSplits) cnt = static_cast<int *>(workspace);
+            if (use_tickets(B, G, ns)) cnt = static_cast<int *>(workspace);
             part = reinterpret_cast<float *>(static_cast<char *>(workspace) + ticket_bytes(B, G));
         }
         const dim3 grid((unsigned)ns, (unsigned)G, (unsigned)B);
@@ -894,7 +898,7 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
     if (ns > 1) {
         if (!workspace || workspace_bytes < ticket_bytes(B, G) + partial_bytes(B, H, D, ns)) return VGX_E_ARENA;
         if ((uintptr_t)workspace % 256) return VGX_E_ALIGN;
-        if (ns <= kTicketMaxSplits) cnt = static_cast<int *>(workspace);
+        if (use_tickets(B, G, ns)) cnt = static_cast<int *>(workspace);
         part = reinterpret_cast<float *>(static_cast<char *>(workspace) + ticket_bytes(B, G));
     }
     dim3 grid((unsigned)ns, (unsigned)G, (unsigned)B);

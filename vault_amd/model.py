@@ -7,10 +7,13 @@ segment-bank compaction and scorer op is a call into the HIP library.  Host-side
 Python as in the reference: the auto-pin FSM, segment-id bookkeeping, and the top-B eviction merge
 (on at most budget + W candidates once per W tokens).
 
-Offline configuration: there is no tokenizer, so every token's segment-break tier is 0 (segments
-close at seg_max or at the chunk end), there are no shingles, and resonance biases and spoof
-quarantine are inert, exactly as the reference behaves without a tokenizer.  A caller-supplied
-per-head bias (``st.seg_head_bias``, ``st.seg_bias_active``) is honoured by the attention kernel.
+Token rules: with the token strings of a VLT3 file (``weights.tokens``) the segment-break tiers,
+the system-role test and the newline id of the auto-pin rule come from the bytes, as in the C
+runtime (runtime/vault3.c:937-959, 1920-1928, 2047); without them (a model built from tensors,
+like the reference Python model offline) every tier is 0, the system role is
+``cfg.system_tok_id`` and the newline id is 198 (src/vault_v3_model.py:2224-2252, 2260-2268).
+Shingles, resonance biases and spoof quarantine are not derived here; a caller-supplied per-head
+bias (``st.seg_head_bias``, ``st.seg_bias_active``) is honoured by the attention kernel.
 
 Differences by design:
 * The KV caches of all layers are single tensors [n_layers, B, G, n, D]; prev/cur are swapped by
@@ -187,6 +190,9 @@ class VAULTv3ForCausalLM:
         self.device = weights.device
         self.kv_dtype = kv_dtype
         self.ws = ops.Workspace(self.device)
+        self.tokens = weights.tokens
+        vs = self.cfg.vocab_size
+        self.tier_lut = self.tokens.tiers if self.tokens is not None else np.zeros(vs, dtype=np.uint8)
         self.use_graphs = True          # replay captured HIP graphs for decode steps
         self._table = None
         self._p0 = 0
@@ -243,7 +249,7 @@ class VAULTv3ForCausalLM:
         if seg_active:
             st.seg_cur_ids[0, c] = st.cur_seg_id
             st.seg_len += 1
-            if c == W - 1 or st.seg_len >= cfg.seg_max:   # break tiers are all 0 without a tokenizer
+            if c == W - 1 or self._breaks(int(ids[0]), st.seg_len):
                 st.cur_seg_id += 1
                 st.seg_len = 0
         if not seg_active or not (pos >= 2 * W and st.mem_pos.numel() > 0):
@@ -293,6 +299,24 @@ class VAULTv3ForCausalLM:
     __call__ = forward
 
     # ------------------------------------------------------------------ host control
+    def _breaks(self, tid: int, seg_len: int) -> bool:
+        """Whether a segment closes after this token (runtime/vault3.c:2109-2122;
+        src/vault_v3_model.py:2260-2268): tier 1 from seg_min tokens on, tier 2 from
+        max(seg_min, 2 seg_max / 3), tier 3 from max(seg_min, seg_max - 8), any token at seg_max."""
+        cfg = self.cfg
+        tr = int(self.tier_lut[tid]) if 0 <= tid < self.tier_lut.shape[0] else 0
+        t2 = max(cfg.seg_min, (cfg.seg_max * 2) // 3)
+        t3 = max(cfg.seg_min, cfg.seg_max - 8 if cfg.seg_max > 8 else cfg.seg_min)
+        return (seg_len >= cfg.seg_max or (tr == 1 and seg_len >= cfg.seg_min) or (tr == 2 and seg_len >= t2)
+                or (tr == 3 and seg_len >= t3))
+
+    def _is_system_role(self, tid: int) -> bool:
+        return self.tokens.is_system_role(tid) if self.tokens is not None else tid == self.cfg.system_tok_id
+
+    @property
+    def newline_id(self) -> int:
+        return self.tokens.newline_id if self.tokens is not None else 198
+
     def _auto_pin(self, st: VAULTv3State, tid: int, pos: int) -> None:
         """Online ChatML system-prompt pinning (src/vault_v3_model.py:2224-2252)."""
         cfg = self.cfg
@@ -303,12 +327,12 @@ class VAULTv3ForCausalLM:
             else:
                 st.pin_locked = True
         elif pos == 1 and st.saw_im_start:
-            if tid != cfg.system_tok_id:
+            if not self._is_system_role(tid):
                 st.saw_im_start = False
                 st.pin_locked = True
         elif st.saw_im_start and pos < limit:
             if st.awaiting_sys_nl:
-                st.n_pin = max(st.n_pin, pos + 1 if tid == 198 else pos)
+                st.n_pin = max(st.n_pin, pos + 1 if tid == self.newline_id else pos)
                 st.pin_locked = True
                 st.awaiting_sys_nl = False
             elif tid == cfg.im_end_id:
@@ -473,13 +497,15 @@ class VAULTv3ForCausalLM:
 
     def _size_workspace(self, st: VAULTv3State) -> None:
         """Grow the workspaces before a capture (a captured graph holds their addresses): attention to
-        the bound of any decode step of this batch size (B * H * 64 splits * (D + 2) floats), and the
-        GEMM activation splits for batches that use the MFMA GEMM."""
+        the bound of any decode step of this batch size (the library's bound at its split cap), and
+        the GEMM activation splits for batches that use the MFMA GEMM."""
         cfg = self.cfg
-        self.ws.get((st.batch * cfg.n_kv_heads * 4 + 255) // 256 * 256 +
-                    st.batch * cfg.n_heads * 64 * (cfg.head_dim + 2) * 4)
+        lib = ops.L.load()
+        # the most any decode step of this batch can need (the split count is capped, so a key count
+        # beyond every state's capacity gives the bound)
+        self.ws.get(int(lib.vgx_attn_decode_workspace_bytes(st.batch, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                                                              1 << 24)))
         if st.batch >= ops.GEMM_MIN_ROWS:
-            lib = ops.L.load()
             shapes = [(cfg.d_ff, cfg.d_model, ops.L.EPI_SWIGLU), (cfg.d_model, cfg.d_ff, ops.L.EPI_ACCUM),
                       ((cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim, cfg.d_model, ops.L.EPI_STORE),
                       (cfg.d_model, cfg.n_heads * cfg.head_dim, ops.L.EPI_ACCUM),
@@ -674,7 +700,7 @@ class VAULTv3ForCausalLM:
                 for j in range(clen):
                     st.seg_cur_ids[0, j] = s_loc
                     slen += 1
-                    if j == W - 1 or slen >= cfg.seg_max:
+                    if j == W - 1 or self._breaks(int(ch[j]), slen):
                         s_loc += 1
                         slen = 0
                 st.cur_seg_id, st.seg_len = s_loc, slen

@@ -117,6 +117,19 @@ class QWeight:
         return rows * (self.cols // 32) * BLOCK_BYTES[self.dtype]
 
 
+def count_nonfinite(items, device) -> list:
+    """Non-finite values per tensor, counted on the device: ``items`` is a list of (dtype, payload
+    bytes, element count) in the VLT3 layouts; one host read for the whole list."""
+    lib = L.load()
+    counts = torch.zeros(max(1, len(items)), dtype=torch.int32, device=device)
+    for i, (dt, data, n) in enumerate(items):
+        # stream-ordered: the upload's memory is reused only after the scan that reads it
+        src = QWeight._upload(data, device)
+        L.check(lib.vgx_count_nonfinite(dt, src.data_ptr(), n, counts[i:].data_ptr(), _stream(torch.device(device))),
+                "vgx_count_nonfinite")
+    return counts[:len(items)].cpu().tolist()
+
+
 GEMM_MIN_ROWS = 8   # activation rows from which Q8_0 / Q4_0 projections run on the MFMA GEMM
 _GEMM_WS: dict = {}
 

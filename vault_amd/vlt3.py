@@ -17,7 +17,9 @@ the code is written from the spec.
 * ``write_vlt3`` / ``read_vlt3``: header (4096 B, CRC32 over bytes 0..4091), 128-byte
   directory entries, 64-byte aligned payloads, and a VTOK tokenizer blob.  ``minimal_vtok``
   emits a structurally valid VTOK with empty token strings (the offline configuration in which
-  every segment-break tier is 0).
+  every segment-break tier is 0); ``vault_amd.tokens.build_vtok`` one with token strings.
+  ``read_vlt3`` also parses the VTOK blob into a ``TokenTable`` and ``scan_finite`` applies the
+  reference loader's NaN / Inf rejection (runtime/vault3.c:215-271) on the host.
 """
 from __future__ import annotations
 
@@ -27,6 +29,8 @@ from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Tuple
 
 import numpy as np
+
+from .tokens import TokenTable, VTOKError
 
 MAGIC = b"VLT3"
 VERSION = 1
@@ -250,6 +254,7 @@ class Tensor:
 class VLT3:
     header: Dict
     tensors: Dict[str, Tensor] = field(default_factory=dict)
+    tokens: Optional[TokenTable] = None
 
 
 def write_vlt3(path: str, tensors: List[Tensor], cfg, fmt_tag: int, tok_blob: Optional[bytes] = None,
@@ -257,9 +262,12 @@ def write_vlt3(path: str, tensors: List[Tensor], cfg, fmt_tag: int, tok_blob: Op
     """Write a VLT3 file from already-encoded tensors; returns the file size."""
     tensors = sorted(tensors, key=lambda t: tensor_id(t.name))
     tok_blob = tok_blob if tok_blob is not None else minimal_vtok(cfg.vocab_size)
-    ids = dict(bos=0, eos=0, im_start=0, im_end=0, pad=0)
+    # the ChatML ids the auto-pin rule reads come from the config unless given explicitly
+    ids = dict(bos=0, eos=0, im_start=int(cfg.im_start_id), im_end=int(cfg.im_end_id), pad=0)
     if special_ids:
         ids.update(special_ids)
+    if not all(0 <= v < cfg.vocab_size for v in ids.values()):
+        raise VLT3Error("special token ids must be below vocab_size")
     dir_off = HEADER_SIZE
     dir_size = ENTRY_SIZE * len(tensors)
     tok_off = -(-(dir_off + dir_size) // ALIGN) * ALIGN
@@ -320,51 +328,154 @@ _HDR_NAMES = (
 )
 
 
+# Loader limits and error codes (runtime/vault3.h:26-48): a rejected file raises VLT3Error whose
+# ``code`` is the reference loader's V3_E_* value for the same defect.
+E_SIZE, E_MAGIC, E_CRC, E_BOUNDS, E_DTYPE, E_MISSING, E_SHAPE, E_TOKENIZER, E_LIMIT, E_NAN = \
+    -1, -2, -3, -4, -5, -6, -7, -9, -10, -12
+MAX_LAYERS, MAX_HEADS, MAX_HEAD_DIM, MAX_SINK, MAX_SEG_FEAT, MAX_SEG_HIDDEN, MAX_SEG_BUDGET = \
+    64, 256, 256, 512, 4, 1024, 16384
+
+
+def _fail(code: int, msg: str):
+    e = VLT3Error(msg)
+    e.code = code
+    raise e
+
+
 def read_vlt3(path: str, check_crc: bool = True) -> VLT3:
-    """Parse and validate a VLT3 file (validation rules: docs/VAULT_v3_SPEC.md:111-136,
-    tools/vlt3.py:453-545)."""
+    """Parse and validate a VLT3 file; see ``parse_vlt3``."""
     with open(path, "rb") as f:
         buf = f.read()
+    return parse_vlt3(buf, check_crc)
+
+
+def parse_vlt3(buf: bytes, check_crc: bool = True) -> VLT3:
+    """Validate a VLT3 image in the order of the reference loader (runtime/vault3.c:273-455):
+    header magic / version / size / endianness, header CRC, file size, alignment, region bounds,
+    legacy fields, hyper-parameter limits, directory entries (reserved word, ndim, dims, dtype size,
+    block shape, alignment and bounds, ascending offsets, optional CRC), tensor ids (missing or
+    duplicated), shapes and dtypes, then the VTOK blob.  Non-finite weights are rejected where the
+    weights are uploaded (``ModelWeights.from_tensors`` scans them on the device)."""
     size = len(buf)
     if size < HEADER_SIZE:
-        raise VLT3Error("file smaller than header")
+        _fail(E_SIZE, "file smaller than header")
+    if buf[:4] != MAGIC or struct.unpack_from("<III", buf, 4) != (VERSION, HEADER_SIZE, ENDIAN_TAG):
+        _fail(E_MAGIC, "bad magic/version/header size/endianness")
     if zlib.crc32(buf[:HEADER_SIZE - 4]) != struct.unpack_from("<I", buf, HEADER_SIZE - 4)[0]:
-        raise VLT3Error("header CRC mismatch")
+        _fail(E_CRC, "header CRC mismatch")
     h = dict(zip(_HDR_NAMES, _HDR.unpack_from(buf, 0)))
-    if h["magic"] != MAGIC or h["version"] != VERSION or h["header_size"] != HEADER_SIZE or h["endian_tag"] != ENDIAN_TAG:
-        raise VLT3Error("bad magic/version/header size/endianness")
-    if h["file_size"] != size or h["alignment"] != ALIGN:
-        raise VLT3Error("file size or alignment mismatch")
+    if h["file_size"] != size:
+        _fail(E_SIZE, "file size mismatch")
+    if h["alignment"] != ALIGN:
+        _fail(E_MAGIC, "alignment mismatch")
     for off_k, size_k in (("tensor_dir_offset", "tensor_dir_size"), ("tokenizer_offset", "tokenizer_size"),
                           ("data_offset", "data_size")):
         o, n = h[off_k], h[size_k]
         if o < HEADER_SIZE or o > size or n > size - o:
-            raise VLT3Error(f"{off_k} out of bounds")
-    if h["tensor_dir_size"] != h["n_tensors"] * ENTRY_SIZE:
-        raise VLT3Error("tensor directory size mismatch")
+            _fail(E_BOUNDS, f"{off_k} out of bounds")
+    if h["n_tensors"] > 8192 or h["tensor_dir_size"] != h["n_tensors"] * ENTRY_SIZE:
+        _fail(E_BOUNDS, "tensor directory size mismatch")
     if any(h[f"kenyon{i}"] for i in range(10)):
-        raise VLT3Error("legacy bank fields must be zero")
-    if h["n_heads"] % max(1, h["n_kv_heads"]) or h["n_heads"] * h["head_dim"] != h["d_model"]:
-        raise VLT3Error("inconsistent head dimensions")
-    if not (np.isfinite(h["rms_eps"]) and h["rms_eps"] > 0 and np.isfinite(h["rope_theta"]) and h["rope_theta"] > 1):
-        raise VLT3Error("bad eps/theta")
+        _fail(E_LIMIT, "legacy bank fields must be zero")
+    if not np.isfinite(h["reserved_eps"]):
+        _fail(E_NAN, "non-finite reserved field")
+    V, d, nl, H, G, D, F, W = (h[k] for k in ("vocab_size", "d_model", "n_layers", "n_heads", "n_kv_heads",
+                                              "head_dim", "d_ff", "window"))
+    if (V == 0 or V > 524288 or d == 0 or d > 16384 or nl == 0 or nl > MAX_LAYERS or H == 0 or H > MAX_HEADS
+            or D == 0 or D > MAX_HEAD_DIM or D % 2 or G == 0 or G > H or H % G or F == 0 or F > 65536
+            or W == 0 or W > 65536 or h["n_sink"] > MAX_SINK or h["n_sink"] > W):
+        _fail(E_LIMIT, "hyper-parameter out of range")
+    if H * D != d:
+        _fail(E_SHAPE, "n_heads * head_dim != d_model")
+    if not (np.isfinite(h["rope_theta"]) and np.isfinite(h["rms_eps"])):
+        _fail(E_NAN, "non-finite eps / theta")
+    if not (h["rope_theta"] > 1.0 and h["rms_eps"] > 0.0):
+        _fail(E_LIMIT, "bad eps / theta")
+    if any(h[k] >= V for k in ("bos_id", "eos_id", "im_start_id", "im_end_id", "pad_id")):
+        _fail(E_LIMIT, "special token id beyond the vocabulary")
+    nf = h["seg_n_feat"]
+    if nf > MAX_SEG_FEAT:
+        _fail(E_LIMIT, "too many scorer feature layers")
+    if nf == 0:
+        if h["seg_budget"] or h["seg_hidden"] or h["seg_min"] or h["seg_max"]:
+            _fail(E_LIMIT, "segment fields set without a scorer")
+    elif (h["seg_budget"] > MAX_SEG_BUDGET or h["seg_hidden"] == 0 or h["seg_hidden"] > MAX_SEG_HIDDEN
+          or h["seg_min"] == 0 or h["seg_min"] > h["seg_max"] or h["seg_max"] > W
+          or any(h[f"seg_layer{i}"] >= nl for i in range(nf))):
+        _fail(E_LIMIT, "segment hyper-parameters out of range")
     out = VLT3(header=h)
     prev_end = 0
+    d_end = h["data_offset"] + h["data_size"]
     for k in range(h["n_tensors"]):
-        e = _ENTRY.unpack_from(buf, h["tensor_dir_offset"] + k * ENTRY_SIZE)
-        tid, dt, ndim, d0, d1, d2, d3, rsv, off, nb, crc, nm = e
-        if rsv or not 1 <= ndim <= 4:
-            raise VLT3Error(f"entry {k}: bad reserved/ndim")
+        tid, dt, ndim, d0, d1, d2, d3, rsv, off, nb, crc, _ = \
+            _ENTRY.unpack_from(buf, h["tensor_dir_offset"] + k * ENTRY_SIZE)
+        if rsv:
+            _fail(E_BOUNDS, f"entry {k}: reserved word set")
+        if not 1 <= ndim <= 4:
+            _fail(E_SHAPE, f"entry {k}: ndim {ndim}")
         shape = tuple((d0, d1, d2, d3)[:ndim])
-        n = int(np.prod(shape))
+        if any(x == 0 for x in shape):
+            _fail(E_SHAPE, f"entry {k}: zero dimension")
+        n = int(np.prod(shape, dtype=object))
+        if dt not in (F32, F16, BF16, Q8_0, Q4_0):
+            _fail(E_DTYPE, f"entry {k}: dtype {dt}")
+        if dt in BLOCK_BYTES and shape[-1] % QK:
+            _fail(E_SHAPE, f"entry {k}: block dtype needs rows of a multiple of 32")
         if nb != nbytes_for(dt, n):
-            raise VLT3Error(f"tensor {tid}: size mismatch")
-        if off % ALIGN or off < h["data_offset"] or nb > h["data_offset"] + h["data_size"] - off or off < prev_end:
-            raise VLT3Error(f"tensor {tid}: bad offset")
+            _fail(E_SHAPE, f"tensor {tid}: size mismatch")
+        if off % ALIGN or off < h["data_offset"] or nb > d_end - off:
+            _fail(E_BOUNDS, f"tensor {tid}: bad offset")
+        if off < prev_end:
+            _fail(E_BOUNDS, f"tensor {tid}: overlaps the previous tensor")
         prev_end = off + nb
         data = buf[off:off + nb]
         if check_crc and zlib.crc32(data) != crc:
-            raise VLT3Error(f"tensor {tid}: CRC mismatch")
-        name = tensor_name(tid)
+            _fail(E_CRC, f"tensor {tid}: CRC mismatch")
+        try:
+            name = tensor_name(tid)
+        except (KeyError, IndexError, VLT3Error):
+            _fail(E_MISSING, f"unknown tensor id {tid}")
+        if name.startswith("layers.") and int(name.split(".")[1]) >= nl:
+            _fail(E_MISSING, f"tensor {tid}: layer beyond n_layers")
+        if name in out.tensors:
+            _fail(E_MISSING, f"tensor {tid}: duplicated")
+        if name.startswith("seg_scorer.") and nf == 0:
+            continue          # the reference ignores scorer tensors of a file without a scorer
         out.tensors[name] = Tensor(name, dt, shape, data)
+    cfg_shapes = _expected_shapes(h)
+    for name, shp in cfg_shapes.items():
+        t = out.tensors.get(name)
+        if t is None or t.shape != shp:
+            _fail(E_SHAPE, f"{name}: missing or shape {None if t is None else t.shape} != {shp}")
+        matmul = name.endswith("_proj.weight") or name in ("embed_tokens.weight", "seg_scorer.fc1.weight",
+                                                           "seg_scorer.fc2.weight")
+        if not matmul and t.dtype != F32:
+            _fail(E_SHAPE, f"{name} must be F32")
+    tb = buf[h["tokenizer_offset"]:h["tokenizer_offset"] + h["tokenizer_size"]]
+    if len(tb) < 128:
+        _fail(E_TOKENIZER, "VTOK blob too small")
+    try:
+        out.tokens = TokenTable.from_vtok(tb, V)
+    except VTOKError as e:
+        _fail(E_TOKENIZER, str(e))
     return out
+
+
+def _expected_shapes(h: Dict) -> Dict[str, tuple]:
+    """Tensor shapes the header implies (runtime/vault3.c:383-423)."""
+    d, H, G, D, F = h["d_model"], h["n_heads"], h["n_kv_heads"], h["head_dim"], h["d_ff"]
+    s = {"embed_tokens.weight": (h["vocab_size"], d), "norm.weight": (d,)}
+    nf = h["seg_n_feat"]
+    if nf:
+        fd, hd = nf * d, h["seg_hidden"]
+        s.update({"seg_scorer.ln.weight": (fd,), "seg_scorer.ln.bias": (fd,), "seg_scorer.fc1.weight": (hd, fd),
+                  "seg_scorer.fc1.bias": (hd,), "seg_scorer.fc2.weight": (1, hd), "seg_scorer.fc2.bias": (1,)})
+    for li in range(h["n_layers"]):
+        p = f"layers.{li}."
+        s.update({p + "input_layernorm.weight": (d,), p + "post_attention_layernorm.weight": (d,),
+                  p + "self_attn.q_proj.weight": (H * D, d), p + "self_attn.k_proj.weight": (G * D, d),
+                  p + "self_attn.v_proj.weight": (G * D, d), p + "self_attn.o_proj.weight": (d, H * D),
+                  p + "mlp.gate_proj.weight": (F, d), p + "mlp.up_proj.weight": (F, d),
+                  p + "mlp.down_proj.weight": (d, F), p + "self_attn.q_proj.bias": (H * D,),
+                  p + "self_attn.k_proj.bias": (G * D,), p + "self_attn.v_proj.bias": (G * D,)})
+    return s

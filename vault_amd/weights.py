@@ -14,6 +14,7 @@ import torch
 
 from . import ops, vlt3
 from .config import VAULTv3Config
+from .tokens import TokenTable
 
 Tensor = vlt3.Tensor
 
@@ -63,12 +64,25 @@ class ModelWeights:
         self.embed: Optional[ops.QWeight] = None
         self.norm: Optional[torch.Tensor] = None
         self.scorer: Optional[ScorerWeights] = None
+        # token strings (VTOK) when known: break tiers, system-role and newline rules of the driver
+        self.tokens: Optional[TokenTable] = None
 
     # ------------------------------------------------------------------ construction
     @classmethod
-    def from_tensors(cls, cfg: VAULTv3Config, tensors: Dict[str, Tensor], device) -> "ModelWeights":
+    def from_tensors(cls, cfg: VAULTv3Config, tensors: Dict[str, Tensor], device,
+                     tokens: Optional[TokenTable] = None, scan: bool = True) -> "ModelWeights":
+        """Upload and pack every tensor.  ``scan``: reject non-finite weights and block scales on the
+        device first (the reference loader's NaN / Inf rule, runtime/vault3.c:215-271)."""
         self = cls(cfg, device)
+        self.tokens = tokens
         dev = self.device
+        if scan:
+            bad = ops.count_nonfinite([(t.dtype, t.data, int(np.prod(t.shape))) for t in tensors.values()], dev)
+            if bad:
+                names = [n for n, k in zip(tensors, bad) if k]
+                e = vlt3.VLT3Error(f"non-finite weights or scales in {names[:4]}")
+                e.code = vlt3.E_NAN
+                raise e
         emb = tensors["embed_tokens.weight"]
         self.embed = ops.QWeight.from_blocks(_block_dtype(emb), cfg.vocab_size, cfg.d_model, emb.data, dev)
         self.norm = _f32(tensors["norm.weight"], dev)
@@ -114,10 +128,12 @@ class ModelWeights:
         return self
 
     @classmethod
-    def from_vlt3(cls, path: str, device) -> "ModelWeights":
-        vf = vlt3.read_vlt3(path)
+    def from_vlt3(cls, path: str, device, check_crc: bool = True) -> "ModelWeights":
+        """Load a VLT3 file: host validation (``vlt3.read_vlt3``), then upload with the device NaN /
+        Inf scan; the file's VTOK token strings drive the break tiers and the auto-pin rules."""
+        vf = vlt3.read_vlt3(path, check_crc=check_crc)
         cfg = VAULTv3Config.from_vlt3_header(vf.header)
-        return cls.from_tensors(cfg, vf.tensors, device)
+        return cls.from_tensors(cfg, vf.tensors, device, tokens=vf.tokens)
 
     # ------------------------------------------------------------------ accounting
     def layer_stream_bytes(self) -> int:
