@@ -78,7 +78,7 @@ class ModelWeights:
         dev = self.device
         if scan:
             bad = ops.count_nonfinite([(t.dtype, t.data, int(np.prod(t.shape))) for t in tensors.values()], dev)
-            if bad:
+            if any(bad):
                 names = [n for n, k in zip(tensors, bad) if k]
                 e = vlt3.VLT3Error(f"non-finite weights or scales in {names[:4]}")
                 e.code = vlt3.E_NAN
