@@ -70,10 +70,16 @@ def chunk(q: np.ndarray, prefix: list, k_cur: np.ndarray, v_cur: np.ndarray, bia
     return np.einsum("htn,hnd->thd", p, Ve)
 
 
+def sink_positions(i: int, W: int, S: int) -> np.ndarray:
+    """Virtual positions of the S sinks for query chunk i >= 2 (src/vault_v3_model.py:805-809)."""
+    return np.maximum(0, (i - 1) * W - S + np.arange(S))
+
+
 def block_sliding(q: np.ndarray, k: np.ndarray, v: np.ndarray, k_raw: np.ndarray, W: int, S: int,
-                  theta: float, table=_rope.table_torch) -> np.ndarray:
+                  theta: float, table=_rope.table_torch, sink_store=None, sink_pos=sink_positions) -> np.ndarray:
     """q: [L, H, D] post-RoPE, k/v: [L, G, D] post-RoPE / values, k_raw: [L, G, D] pre-RoPE.
-    Returns [L, H, D]."""
+    ``sink_store``: applied to the re-rotated sink keys before use (a bf16 rounding, for callers whose
+    re-rotated sinks are stored in bf16).  Returns [L, H, D]."""
     q = np.asarray(q, dtype=np.float64)
     L, H, D = q.shape
     G = k.shape[1]
@@ -87,9 +93,10 @@ def block_sliding(q: np.ndarray, k: np.ndarray, v: np.ndarray, k_raw: np.ndarray
         keys = [np.asarray(k[lo:r1], dtype=np.float64)]
         vals = [np.asarray(v[lo:r1], dtype=np.float64)]
         if i >= 2 and S > 0:
-            pos = np.maximum(0, (i - 1) * W - S + np.arange(S))
-            c, s_ = table(pos, D, theta)
+            c, s_ = table(sink_pos(i, W, S), D, theta)
             ks = _rope.rotate(np.transpose(np.asarray(k_raw[:S], dtype=np.float64), (1, 0, 2)), c, s_)
+            if sink_store is not None:
+                ks = sink_store(ks)
             keys.insert(0, np.transpose(ks, (1, 0, 2)))
             vals.insert(0, np.asarray(v[:S], dtype=np.float64))
         K = np.concatenate(keys, axis=0)   # [nk, G, D]

@@ -331,6 +331,42 @@ class OracleModel:
         h = self._rms(x, w["norm.weight"], c.rms_eps)
         return w["embed_tokens.weight"] @ h
 
+    def forward_block(self, ids, mode: str = "block", n_pin: Optional[int] = None,
+                      sink_pos=None) -> np.ndarray:
+        """Logits of every position of one sequence by the parallel form (src/vault_v3_model.py:
+        1048-1061, 2136-2151): RoPE at absolute positions, full causal attention when mode == "full"
+        or L <= 2W, else block sliding-window attention with ``n_pin`` (default n_sink) sinks
+        re-rotated to their virtual positions (``attention.block_sliding``; ``sink_pos`` replaces the
+        position rule, for tests that plant a mistake)."""
+        from . import attention as oatt
+        c, w = self.cfg, self.w
+        H, G, D, W = c.n_heads, c.n_kv_heads, c.head_dim, c.window
+        ids = np.asarray(ids, dtype=np.int64)
+        L = ids.size
+        S = min(c.n_sink if n_pin is None else n_pin, L)
+        x = w["embed_tokens.weight"][ids].copy()
+        cs, sn = self._cs(np.arange(L))
+        rms = lambda a, g: g * (a / np.sqrt(np.mean(a * a, axis=-1, keepdims=True) + c.rms_eps))
+        rot = lambda a: np.transpose(orope.rotate(np.transpose(a, (1, 0, 2)), cs, sn), (1, 0, 2))
+        kw = {} if sink_pos is None else {"sink_pos": sink_pos}
+        for li in range(c.n_layers):
+            p = f"layers.{li}."
+            u = rms(x, w[p + "input_layernorm.weight"])
+            q = (u @ w[p + "self_attn.q_proj.weight"].T + w[p + "self_attn.q_proj.bias"]).reshape(L, H, D)
+            k = (u @ w[p + "self_attn.k_proj.weight"].T + w[p + "self_attn.k_proj.bias"]).reshape(L, G, D)
+            v = (u @ w[p + "self_attn.v_proj.weight"].T + w[p + "self_attn.v_proj.bias"]).reshape(L, G, D)
+            qr, kr = rot(q), rot(k)
+            if mode == "full" or L <= 2 * W:
+                o = oatt.chunk(qr, [], np.transpose(kr, (1, 0, 2)), np.transpose(v, (1, 0, 2)))
+            else:
+                o = oatt.block_sliding(qr, kr, v, k, W, S, c.rope_theta, table=self.table, **kw)
+            x = x + o.reshape(L, H * D) @ w[p + "self_attn.o_proj.weight"].T
+            u = rms(x, w[p + "post_attention_layernorm.weight"])
+            g = u @ w[p + "mlp.gate_proj.weight"].T
+            up = u @ w[p + "mlp.up_proj.weight"].T
+            x = x + (g / (1.0 + np.exp(-g)) * up) @ w[p + "mlp.down_proj.weight"].T
+        return rms(x, w["norm.weight"]) @ w["embed_tokens.weight"].T
+
     def stream(self, ids, st: Optional[OState] = None, positions=None) -> np.ndarray:
         """Logits for every token of ``ids`` stepped from ``st`` (a fresh state if None)."""
         st = st or self.new_state()

@@ -16,8 +16,9 @@ from vault_amd.weights import quantize_state, random_state
 FMT_TAG = {"f32": vlt3.F32, "q8_0": vlt3.Q8_0, "q4_0": vlt3.Q4_0}
 
 
-def tiny_cfg(head_dim=64, n_layers=2, window=16, seg_budget=12, vocab=2048, **kw) -> VAULTv3Config:
-    H, G = 4, 2
+def tiny_cfg(head_dim=64, n_layers=2, window=16, seg_budget=12, vocab=2048, n_heads=4, n_kv_heads=2,
+             **kw) -> VAULTv3Config:
+    H, G = n_heads, n_kv_heads
     d = H * head_dim
     base = dict(vocab_size=vocab, d_model=d, n_layers=n_layers, n_heads=H, n_kv_heads=G, head_dim=head_dim,
                 d_ff=2 * d, window=window, n_sink=4, max_sink=8, rope_theta=1_000_000.0,

@@ -2,7 +2,9 @@
 block_sliding_attention (src/vault_v3_model.py:812-863) against the float64 oracle.
 
 The oracle is fed the same bf16 k / v (and the same q: fp32 queries are used at fp32 accuracy, bf16
-ones as given); the bar is the bf16 attention bound max |d| <= 2e-3.  Shapes: ragged query counts
+ones as given); the bar is the bf16 attention bound max |d| <= 2e-3, and 1e-5 for fp32 K / V (the
+fp32 bar).  Re-rotated sinks of a bf16 call are rotated in fp32 and stored once in bf16, which the
+oracle models (``sink_store``) so that the comparison measures the attention alone.  Shapes: ragged query counts
 (not multiples of the 32-query tile), all four key runs (sinks | segment | prev | causal cur), every supported group size, more than
 eight query blocks (split launches), and the full block-sliding prefill workload (L = 8192, W = 1024,
 512 sinks) checked on sampled query rows.
@@ -13,11 +15,13 @@ import torch
 
 from oracle import attention as oatt
 from oracle import rope as orope
+from oracle.model import bf16_round
 from vault_amd import attention as vatt
 from vault_amd import ops
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
+TOL32 = 1e-5
 
 
 def _bf(x):
@@ -83,10 +87,28 @@ def test_block_sliding_matches_oracle(dev, B, L, W, S):
     out = vatt.block_sliding_attention(q, k, v, W, k_raw=kr, n_sink=S, head_dim=D, rope_theta=theta)
     for b in range(B):
         ref = oatt.block_sliding(_f64(q[b]).transpose(1, 0, 2), _f64(k[b]).transpose(1, 0, 2),
+                                 _f64(v[b]).transpose(1, 0, 2), _f64(kr[b]).transpose(1, 0, 2), W, S, theta,
+                                 sink_store=bf16_round)
+        got = out[b].double().cpu().numpy().transpose(1, 0, 2)
+        assert np.abs(got - ref).max() <= TOL, b
+
+
+@pytest.mark.parametrize("B,L,W,S", [(2, 1100, 256, 64), (1, 700, 256, 0), (1, 40, 16, 5)])
+def test_block_sliding_fp32_inputs(dev, B, L, W, S):
+    """fp32 q / k / v / k_raw that are not representable in bf16: the drop-in keeps them fp32 (three
+    bf16 pieces per operand in the kernel, sinks rotated and stored in fp32) and meets the fp32 bar."""
+    rng = np.random.default_rng(L + W + S + 1)
+    H, G, D, theta = 12, 2, 128, 1e6
+    f32 = lambda shape: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(dev)
+    q, k, v, kr = f32((B, H, L, D)), f32((B, G, L, D)), f32((B, G, L, D)), f32((B, G, L, D))
+    assert not torch.equal(k, k.to(torch.bfloat16).float())
+    out = vatt.block_sliding_attention(q, k, v, W, k_raw=kr, n_sink=S, head_dim=D, rope_theta=theta)
+    assert out.dtype == torch.float32
+    for b in range(B):
+        ref = oatt.block_sliding(_f64(q[b]).transpose(1, 0, 2), _f64(k[b]).transpose(1, 0, 2),
                                  _f64(v[b]).transpose(1, 0, 2), _f64(kr[b]).transpose(1, 0, 2), W, S, theta)
         got = out[b].double().cpu().numpy().transpose(1, 0, 2)
-        # the sink keys are re-rotated on the GPU and stored in bf16 before use: allow one more bf16 rounding
-        assert np.abs(got - ref).max() <= 2 * TOL, b
+        assert np.abs(got - ref).max() <= TOL32, b
 
 
 @pytest.mark.parametrize("B,L,W,S", [(2, 1100, 256, 64), (1, 40, 16, 5)])
@@ -123,21 +145,21 @@ def test_block_sliding_full_workload_sampled(dev):
         parts_k, parts_v = [], []
         if i >= 2:
             c, s_ = orope.table_torch((i - 1) * W - S + np.arange(S), D, theta)
-            parts_k.append(orope.rotate(krn[:, :S], c, s_))
+            parts_k.append(bf16_round(orope.rotate(krn[:, :S], c, s_)))     # stored once in bf16
             parts_v.append(vn[:, :S])
         lo = max(0, (i - 1) * W)
         parts_k.append(kn[:, lo:t + 1])
         parts_v.append(vn[:, lo:t + 1])
         spans = [(pk[None], pv[None]) for pk, pv in zip(parts_k, parts_v)]
         ref = oatt.decode(qn[:, t][None], spans)[0]
-        assert np.abs(on[:, t] - ref).max() <= 2 * TOL, t
+        assert np.abs(on[:, t] - ref).max() <= TOL, t
 
 
 @pytest.mark.parametrize("T,lens", [(300, (40, 77, 200)), (33, (0, 0, 64)), (1, (5, 0, 0)), (1024, (512, 1024, 1024))])
 def test_prefill_fp32_kv_matches_oracle(dev, T, lens):
-    """fp32 K / V (the fp32-state chunk prefill) on MFMA as bf16 hi + lo planes, fp32 queries as hi + lo:
-    every operand at 16 significant bits, all four hi / lo products accumulated in fp32.  Bar 5e-5 on
-    unit-variance data (the representation error, 2^-17 per operand, through 128-term scores)."""
+    """fp32 K / V (the fp32-state chunk prefill) on MFMA as three bf16 planes, fp32 queries and the
+    probabilities as three bf16 pieces: 24 significant bits per operand, the six products of order
+    <= 2 accumulated in fp32.  The fp32 bar, 1e-5."""
     rng = np.random.default_rng(T + sum(lens) + 7)
     H, G, D = 12, 2, 128
     f32 = lambda shape: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).to(dev)
@@ -147,7 +169,7 @@ def test_prefill_fp32_kv_matches_oracle(dev, T, lens):
     out = torch.empty(T, H, D, device=dev)
     ops.attn_prefill([{"q": q, "out": out, "runs": runs + [(kc, vc)], "causal_base": 0}], H, G)
     ref = oatt.chunk(_f64(q), [(_f64(k), _f64(v)) for k, v in runs], _f64(kc), _f64(vc))
-    assert np.abs(out.double().cpu().numpy() - ref).max() <= 5e-5
+    assert np.abs(out.double().cpu().numpy() - ref).max() <= TOL32
 
 
 def test_prefill_fp32_kv_strided_state_views(dev):
@@ -163,4 +185,4 @@ def test_prefill_fp32_kv_strided_state_views(dev):
     ops.attn_prefill([{"q": q, "out": out, "runs": [(prev_k, prev_v), (ring_k[:, :T], ring_v[:, :T])],
                        "causal_base": 0}], H, G)
     ref = oatt.chunk(_f64(q), [(_f64(prev_k), _f64(prev_v))], _f64(ring_k[:, :T]), _f64(ring_v[:, :T]))
-    assert np.abs(out.double().cpu().numpy() - ref).max() <= 5e-5
+    assert np.abs(out.double().cpu().numpy() - ref).max() <= TOL32

@@ -157,3 +157,52 @@ def test_rope_conventions_agree_at_small_positions():
     cc, sc = orope.table_c(pos, D, theta)
     ct, st = orope.table_torch(pos, D, theta)
     assert np.abs(cc - ct).max() < 1e-5 and np.abs(sc - st).max() < 1e-5
+
+
+def _block_cfg():
+    from tests import modelgen
+    cfg = modelgen.tiny_cfg(seg_budget=0, window=16)
+    return cfg, modelgen.build(cfg, "q8_0", seed=6)[2]
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_block_forward_equals_stream_with_sinks(seed):
+    """The reference's own identity (tests/test_vault_v3.py:52-75): the parallel block form of a batch
+    row (sinks re-rotated to (i-1)W - S + j, absolute positions) equals that row's token stream (sinks
+    pinned, re-based ring positions, re-rotation at every chunk boundary) beyond 2W tokens.  This pins
+    the sink-position rule of ``block_sliding`` through an independent path."""
+    from oracle.model import OracleModel
+    from tests import modelgen
+    cfg, deq = _block_cfg()
+    om = OracleModel(cfg, deq)
+    ids = modelgen.ids_stream(cfg, 75, seed=20 + seed)            # 4.7 chunks: sinks from chunk 2 on
+    blk = om.forward_block(ids)
+    st = om.new_state(seg_budget=0)
+    om.set_pinned(st, cfg.n_sink)
+    stream = om.stream(ids, st)
+    assert np.abs(blk - stream).max() < 1e-4 * max(1.0, np.abs(stream).max())
+    # full causal equals block sliding within 2W tokens (tests/test_vault_v3.py:175-181)
+    short = ids[:2 * cfg.window]
+    assert np.abs(om.forward_block(short, mode="full") - om.forward_block(short)).max() == 0.0
+
+
+@pytest.mark.parametrize("shift", [-1, 1, "chunk"])
+def test_block_forward_identity_catches_wrong_sink_positions(shift):
+    """Planted mistakes in the sink rule (one position off either way, or the sinks placed before the
+    current chunk instead of the previous one) break the identity by far more than its bar."""
+    from oracle import attention as oatt
+    from oracle.model import OracleModel
+    from tests import modelgen
+    cfg, deq = _block_cfg()
+    om = OracleModel(cfg, deq)
+    ids = modelgen.ids_stream(cfg, 75, seed=20)
+    if shift == "chunk":
+        bad = lambda i, W, S: np.maximum(0, i * W - S + np.arange(S))
+    else:
+        bad = lambda i, W, S: np.maximum(0, (i - 1) * W - S + np.arange(S) + shift)
+    st = om.new_state(seg_budget=0)
+    om.set_pinned(st, cfg.n_sink)
+    stream = om.stream(ids, st)
+    wrong = om.forward_block(ids, sink_pos=bad)
+    assert np.abs(wrong - stream).max() > 1e-3 * max(1.0, np.abs(stream).max())
+    assert np.array_equal(oatt.sink_positions(3, 16, 4), [28, 29, 30, 31])

@@ -18,8 +18,12 @@
 //                                      when few keys carry the weight.
 // bf16 K and V stay bf16 end to end (no conversions in the staging loop): MFMA throughput is abundant
 // here, VALU issue is what bounds the kernel.  fp32 K and V (an fp32 state read in place) are staged
-// as bf16 hi + lo planes; their products take hi x hi, hi x lo and lo x hi, and drop lo x lo, which
-// is below 2^-18 of each product and so under the rounding of the splits themselves.  In both products a lane of the 16 x 16 output owns
+// as three bf16 planes (hi, mid, lo: 24 significant bits, the whole fp32 mantissa), and the fp32
+// queries and the probabilities are split the same way; each product keeps the six piece pairs of
+// order <= 2 (hi x hi, hi x mid, mid x hi, hi x lo, lo x hi, mid x mid) and drops those below 2^-24
+// of it, so scores and outputs carry fp32-level error (about 2^-22 relative) instead of the 2^-17 of
+// a hi + lo split.  The fp32 path holds 16 queries per wave: its three query pieces would not fit
+// the registers of two 16-query tiles.  In both products a lane of the 16 x 16 output owns
 // one query column, so the online-softmax state (running max, rescale of O) is lane-local; the max
 // over a query's keys needs two cross-lane steps.  The K-dimension slots of A and B are assigned the
 // same way in each product (lane group lg holds slots 8 lg .. 8 lg + 7 of both operands), which is
@@ -87,7 +91,10 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     // KF: fp32 K / V, staged as bf16 hi + lo planes (tiles of 32 keys: the same bytes per tile)
     constexpr int KT = KF ? 32 : kKT;               // keys per LDS tile
     constexpr int VROW = KT + 8;                    // LDS row of V^T, bf16 (16 bytes of padding)
-    constexpr int NP = KF ? 2 : 1;                  // bf16 planes per operand
+    constexpr int NP = KF ? 3 : 1;                  // bf16 planes per K / V operand
+    constexpr int NQP = QSPLIT ? (KF ? 3 : 2) : 1;  // bf16 pieces per query
+    constexpr int NPP = KF ? 3 : 2;                 // bf16 pieces per probability
+    constexpr int ORD = KF ? 2 : 1;                 // products of pieces i x j kept when i + j <= ORD
     constexpr int ESZ = KF ? 4 : 2;                 // bytes per K / V element in memory
     __shared__ __align__(16) uint16_t ks[NP * KT * kKRow];
     __shared__ __align__(16) uint16_t vt[NP * kD * VROW];
@@ -109,49 +116,39 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     const int lq = lane & 15, lg = lane >> 4;
     const int h = g * GRP + wave;
 
-    // Q^T fragments (bf16): query t0 + 16 qt + lq, dims 32 kc + 8 lg .. + 7; fp32 queries as
-    // hi = bf16(q) and lo = bf16(q - hi).
-    bf16x8_t qh[NQT][4], ql[NQT][4];
+    // Q^T fragments (bf16): query t0 + 16 qt + lq, dims 32 kc + 8 lg .. + 7; fp32 queries as NQP
+    // pieces: hi = bf16(q), then bf16 of what is left (lo, or mid and lo).
+    bf16x8_t qf[NQP][NQT][4];
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
         const int64_t t = t0 + qt * 16 + lq;
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
             const int d0 = kc * 32 + lg * 8;
-            uint32_t hb[8], lb[8];
+            uint32_t pw[NQP][4];
             if (t < B.n_q) {
                 if constexpr (!QSPLIT) {
                     const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(B.q) + t * B.ldq + h * B.q_hstride + d0);
-                    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        hb[2 * i] = ww[i] & 0xFFFFu;
-                        hb[2 * i + 1] = ww[i] >> 16;
-                        lb[2 * i] = lb[2 * i + 1] = 0;
-                    }
+                    pw[0][0] = w.x; pw[0][1] = w.y; pw[0][2] = w.z; pw[0][3] = w.w;
                 } else {
                     const float *qp = static_cast<const float *>(B.q) + t * B.ldq + h * B.q_hstride + d0;
                     const float4 x0 = reinterpret_cast<const float4 *>(qp)[0], x1 = reinterpret_cast<const float4 *>(qp)[1];
                     const float e[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
-                    for (int i = 0; i < 8; i += 2) {
-                        uint32_t hw, lw;
-                        split_bf16x2(e[i], e[i + 1], hw, lw);
-                        hb[i] = hw & 0xFFFFu;
-                        hb[i + 1] = hw >> 16;
-                        lb[i] = lw & 0xFFFFu;
-                        lb[i + 1] = lw >> 16;
+                    for (int i = 0; i < 4; ++i) {
+                        if constexpr (NQP == 3) split3_bf16x2(e[2 * i], e[2 * i + 1], pw[0][i], pw[1][i], pw[2][i]);
+                        else split_bf16x2(e[2 * i], e[2 * i + 1], pw[0][i], pw[NQP - 1][i]);
                     }
                 }
             } else {
 #pragma unroll
-                for (int i = 0; i < 8; ++i) hb[i] = lb[i] = 0;
+                for (int pp = 0; pp < NQP; ++pp)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) pw[pp][i] = 0;
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                qh[qt][kc][i] = __builtin_bit_cast(__bf16, (uint16_t)hb[i]);
-                ql[qt][kc][i] = __builtin_bit_cast(__bf16, (uint16_t)lb[i]);
-            }
+            for (int pp = 0; pp < NQP; ++pp)
+                qf[pp][qt][kc] = __builtin_bit_cast(bf16x8_t, make_uint4(pw[pp][0], pw[pp][1], pw[pp][2], pw[pp][3]));
         }
     }
 
@@ -225,13 +222,14 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
             if constexpr (!KF) {
                 *reinterpret_cast<uint4 *>(ks + (c >> 4) * kKRow + (c & 15) * 8) = kreg[i];
             } else {
-                // four fp32 of row c / 32 -> bf16 hi (plane 0) and lo (plane 1)
-                uint2 hw, lw;
-                split_bf16x2(__uint_as_float(kreg[i].x), __uint_as_float(kreg[i].y), hw.x, lw.x);
-                split_bf16x2(__uint_as_float(kreg[i].z), __uint_as_float(kreg[i].w), hw.y, lw.y);
+                // four fp32 of row c / 32 -> bf16 hi, mid and lo (planes 0, 1, 2)
+                uint2 hw, mw, lw;
+                split3_bf16x2(__uint_as_float(kreg[i].x), __uint_as_float(kreg[i].y), hw.x, mw.x, lw.x);
+                split3_bf16x2(__uint_as_float(kreg[i].z), __uint_as_float(kreg[i].w), hw.y, mw.y, lw.y);
                 uint16_t *kp = ks + (c / CPR) * kKRow + (c % CPR) * 4;
                 *reinterpret_cast<uint2 *>(kp) = hw;
-                *reinterpret_cast<uint2 *>(kp + KT * kKRow) = lw;
+                *reinterpret_cast<uint2 *>(kp + KT * kKRow) = mw;
+                *reinterpret_cast<uint2 *>(kp + 2 * KT * kKRow) = lw;
             }
         }
 #pragma unroll
@@ -253,11 +251,12 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    // dim 4 cc + e of keys 2 rp, 2 rp + 1: the hi word and the lo word
-                    uint32_t hw, lw;
-                    split_bf16x2(__uint_as_float(a0[e]), __uint_as_float(a1[e]), hw, lw);
+                    // dim 4 cc + e of keys 2 rp, 2 rp + 1: the hi, mid and lo words
+                    uint32_t hw, mw, lw;
+                    split3_bf16x2(__uint_as_float(a0[e]), __uint_as_float(a1[e]), hw, mw, lw);
                     *reinterpret_cast<uint32_t *>(vt + (cc * 4 + e) * VROW + 2 * rp) = hw;
-                    *reinterpret_cast<uint32_t *>(vt + kD * VROW + (cc * 4 + e) * VROW + 2 * rp) = lw;
+                    *reinterpret_cast<uint32_t *>(vt + kD * VROW + (cc * 4 + e) * VROW + 2 * rp) = mw;
+                    *reinterpret_cast<uint32_t *>(vt + 2 * kD * VROW + (cc * 4 + e) * VROW + 2 * rp) = lw;
                 }
             }
         }
@@ -291,24 +290,22 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
 #pragma unroll
-                for (int pk = 0; pk < NP; ++pk) {        // K plane: hi, then (fp32 K) lo
+                for (int pk = 0; pk < NP; ++pk) {        // K plane: hi (then, fp32 K, mid and lo)
                     const uint16_t *kp = ks + pk * KT * kKRow;
                     const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(kp + (c + lq) * kKRow + kc * 32 + lg * 8);
                     const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(kp + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
 #pragma unroll
-                    for (int qt = 0; qt < NQT; ++qt) {
-                        sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qh[qt][kc], sc[qt][0], 0, 0, 0);
-                        sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qh[qt][kc], sc[qt][1], 0, 0, 0);
-                        // q lo against K hi only: q lo x K lo is below 2^-18 of each product, under the
-                        // 2^-17 rounding of the hi + lo splits themselves
-                        if (QSPLIT && pk == 0) {
-                            sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ql[qt][kc], sc[qt][0], 0, 0, 0);
-                            sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ql[qt][kc], sc[qt][1], 0, 0, 0);
+                    for (int qp = 0; qp < NQP; ++qp) {
+                        if (pk + qp > ORD) continue;      // below 2^-(8 (ORD + 1)) of the product
+#pragma unroll
+                        for (int qt = 0; qt < NQT; ++qt) {
+                            sc[qt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, qf[qp][qt][kc], sc[qt][0], 0, 0, 0);
+                            sc[qt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, qf[qp][qt][kc], sc[qt][1], 0, 0, 0);
                         }
                     }
                 }
             }
-            bf16x8_t ph[NQT], pl[NQT];
+            bf16x8_t pf[NPP][NQT];
             // 32-key chunk fully visible to all 32 queries: no per-score mask
             const bool full = j0 + c + 32 <= n && (!causal || j0 + c + 31 <= cbase + t0);
             // key index relative to the causal limit of query t0 (fits in 32 bits)
@@ -354,28 +351,31 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                     pv[i] = __builtin_amdgcn_exp2f(v[i] - mn);
                     ps += pv[i];
                 }
-                uint4 hw, lw;
-                split_bf16x2(pv[0], pv[1], hw.x, lw.x);
-                split_bf16x2(pv[2], pv[3], hw.y, lw.y);
-                split_bf16x2(pv[4], pv[5], hw.z, lw.z);
-                split_bf16x2(pv[6], pv[7], hw.w, lw.w);
-                ph[qt] = __builtin_bit_cast(bf16x8_t, hw);
-                pl[qt] = __builtin_bit_cast(bf16x8_t, lw);
+                uint32_t pw[NPP][4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if constexpr (NPP == 3) split3_bf16x2(pv[2 * i], pv[2 * i + 1], pw[0][i], pw[1][i], pw[2][i]);
+                    else split_bf16x2(pv[2 * i], pv[2 * i + 1], pw[0][i], pw[1][i]);
+                }
+#pragma unroll
+                for (int pp = 0; pp < NPP; ++pp)
+                    pf[pp][qt] = __builtin_bit_cast(bf16x8_t, make_uint4(pw[pp][0], pw[pp][1], pw[pp][2], pw[pp][3]));
                 lsum[qt] += ps;
             }
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
-                for (int pv_ = 0; pv_ < NP; ++pv_) {     // V plane: hi, then (fp32 V) lo
+                for (int pv_ = 0; pv_ < NP; ++pv_) {     // V plane: hi (then, fp32 V, mid and lo)
                     const uint16_t *vr = vt + pv_ * kD * VROW + (dt * 16 + lq) * VROW + c + lg * 4;
                     const uint2 lo = *reinterpret_cast<const uint2 *>(vr);
                     const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16);
                     const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-                    for (int qt = 0; qt < NQT; ++qt) {
-                        o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph[qt], o[qt][dt], 0, 0, 0);
-                        if (pv_ == 0)   // P lo x V lo dropped, as q lo x K lo above
-                            o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl[qt], o[qt][dt], 0, 0, 0);
+                    for (int pp = 0; pp < NPP; ++pp) {
+                        if (pv_ + pp > ORD) continue;     // as for the scores
+#pragma unroll
+                        for (int qt = 0; qt < NQT; ++qt)
+                            o[qt][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pf[pp][qt], o[qt][dt], 0, 0, 0);
                     }
                 }
             }
@@ -432,7 +432,7 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_bl
     if (D != kD) return VGX_E_LIMIT;
     const int grp = (int)(H / G);
     if (grp != 1 && grp != 2 && grp != 4 && grp != 6 && grp != 8) return VGX_E_LIMIT;
-    const int qtile = 16 * kNqt;
+    const int qtile = 16 * (kv_dtype == VGX_F32 ? 1 : kNqt);   // fp32 K / V: 16 queries per wave
     PrefillArgs a{};
     a.H = (int)H;
     a.G = (int)G;
@@ -491,7 +491,7 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_bl
     const dim3 grid((unsigned)tiles);
 #define VGX_PREFILL_GO(G_, S_)                                                                               \
     do {                                                                                                     \
-        if (kv_dtype == VGX_F32) hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, kNqt, true>), grid, dim3(64 * G_), 0, st, a); \
+        if (kv_dtype == VGX_F32) hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, 1, true>), grid, dim3(64 * G_), 0, st, a); \
         else hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, kNqt, false>), grid, dim3(64 * G_), 0, st, a);   \
     } while (0)
 #define VGX_PREFILL_GRP(S_)                      \

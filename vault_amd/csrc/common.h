@@ -100,6 +100,34 @@ VGX_DEV void split_bf16x2(float a, float b, uint32_t &hi, uint32_t &lo) {
     lo = pack_bf16x2(a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xFFFF0000u));
 }
 
+// hi = bf16(a, b), mid = bf16(a - hi), lo = bf16(a - hi - mid): three pieces holding 24 significant
+// bits, the whole fp32 mantissa (exact except where a piece falls below the bf16 normal range).
+VGX_DEV void split3_bf16x2(float a, float b, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
+    hi = pack_bf16x2(a, b);
+    const float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xFFFF0000u);
+    mid = pack_bf16x2(ra, rb);
+    lo = pack_bf16x2(ra - __uint_as_float(mid << 16), rb - __uint_as_float(mid & 0xFFFF0000u));
+}
+
+typedef _Float16 vgx_f16x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats -> two RNE fp16 in one word (low half = a).
+VGX_DEV uint32_t pack_f16x2(float a, float b) {
+    const vgx_f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, vgx_f16x2_t));
+}
+
+// hi = bf16(a, b) and lo16 = fp16(16 (a - hi_a), 16 (b - hi_b)); r = {the two elements of (hi + lo16 /
+// 16) that sit in the low halves, those in the high halves} (what the pieces represent, in fp32).
+VGX_DEV void split_bf16_f16x2(float a, float b, uint32_t &hi, uint32_t &lo16, float r[2]) {
+    hi = pack_bf16x2(a, b);
+    const float ha = __uint_as_float(hi << 16), hb = __uint_as_float(hi & 0xFFFF0000u);
+    lo16 = pack_f16x2(16.0f * (a - ha), 16.0f * (b - hb));
+    const auto l = __builtin_bit_cast(vgx_f16x2_t, lo16);
+    r[0] = fmaf((float)l[0], 0.0625f, ha);
+    r[1] = fmaf((float)l[1], 0.0625f, hb);
+}
+
 // One element of a KV-state tensor of dtype KV (VGX_F32, or VGX_BF16 rounded to nearest even).
 template <int KV>
 VGX_DEV void store_kv(void *base, int64_t idx, float v) {

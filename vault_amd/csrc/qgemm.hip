@@ -8,12 +8,15 @@
 //
 // Exactness.  One v_mfma_f32_16x16x32_bf16 spans exactly one 32-weight quant block.  The weights
 // enter the MFMA as unsigned integers, exact in bf16: Q8_0 as q + 128 (byte ^ 0x80), Q4_0 as the
-// nibble n.  The activations enter as a bf16 pair hi + lo (hi = bf16(u), lo = bf16(u - hi); 2^-17
-// relative), prepared once by xsplit_kernel together with the per-block sums S_b = sum_j (hi + lo).
-// Per block the fp32 MFMA result C (= sum_j w_j (hi_j + lo_j)) is corrected and scaled in fp32:
-//   acc += d * (C - off * S_b),   off = 128 (Q8_0) or 8 (Q4_0),
-// which is the reference's sum_b d_b sum_j q_j x_j with the activations rounded to 16 significant
-// bits.
+// nibble n (16 + n in the tiled kernel).  The activations enter in pieces that a bf16 pair hi + lo
+// (2^-18 relative residual) would leave at 2.4e-6 relative error per output, ten times the one-row
+// GEMV's; so the decode-batch kernel takes three bf16 pieces hi + mid + lo (24 significant bits, the
+// whole fp32 mantissa) and the tiled kernel takes hi = bf16(u) and lo16 = fp16(16 (u - hi)) (19
+// significant bits, 2^-20 relative residual; lo16 overflows only past |u| = 2^21), multiplied
+// by the same weights as exact fp16 integers, its product scaled by 1/16.  With S_b the per-block sum
+// of the pieces, per block the fp32 MFMA result C (= sum_j w_j u_j as pieces) is corrected and scaled:
+//   acc += d * (C - off * S_b),   off = 128 (Q8_0), 8 (Q4_0; 24 in the tiled kernel),
+// which is the reference's sum_b d_b sum_j q_j x_j at fp32-level accuracy.
 //
 // Mapping.  Large batches (prefill chunks) run qgemm_tile_kernel (128 x 128 LDS tiles, below) after
 // the split pre-pass; decode batches of up to 64 rows run qgemm_small_kernel, which converts its
@@ -28,9 +31,11 @@ using namespace vgx;
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-// u = (norm ? lnw * x * inv_rms : x); writes hi / lo bf16 rows and per-block sums of hi + lo.
+// u = (norm ? lnw * x * inv_rms : x); writes bf16 hi and fp16 lo16 = 16 (u - hi) rows and per-block
+// sums of hi + lo16 / 16.
 // Inside every group of four, elements 1 and 2 trade places (stored order 0, 2, 1, 3): the K-slot
 // order of the tiled kernel's weight fragments, whose Q4_0 nibble pairs come out of a word that way.
 // One workgroup of 256 threads per activation row.
@@ -75,12 +80,10 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float *__restrict__ x
             }
         }
         uint32_t h02, l02, h13, l13;   // stored order 0, 2, 1, 3
-        split_bf16x2(v.x, v.z, h02, l02);
-        split_bf16x2(v.y, v.w, h13, l13);
-        auto lo16 = [](uint32_t w) { return __uint_as_float(w << 16); };
-        auto hi16 = [](uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); };
-        float hs = (lo16(h02) + lo16(l02)) + (lo16(h13) + lo16(l13)) + (hi16(h02) + hi16(l02)) +
-                   (hi16(h13) + hi16(l13));
+        float r02[2], r13[2];
+        split_bf16_f16x2(v.x, v.z, h02, l02, r02);
+        split_bf16_f16x2(v.y, v.w, h13, l13, r13);
+        float hs = (r02[0] + r13[0]) + (r02[1] + r13[1]);      // the four elements as their pieces represent them
         if (ok) {
             *reinterpret_cast<uint2 *>(xh + b * cols + 4 * i) = make_uint2(h02, h13);
             *reinterpret_cast<uint2 *>(xl + b * cols + 4 * i) = make_uint2(l02, l13);
@@ -128,8 +131,8 @@ __device__ __forceinline__ bf16x8_t a_frag(uint2 w, int lg) {
 // Large batches (prefill chunks, more than 64 activation rows): LDS tiles.  A workgroup of 4 waves
 // owns 128 weight rows (32 row-quads) x 128 activation rows; wave (wm, wn) = (wave & 1, wave >> 1)
 // computes weight rows 64 wm .. + 63 x activation rows 64 wn .. + 63 as 4 x 4 MFMA tiles.  Per quant
-// block the workgroup stages the raw quants and scales of its 128 weight rows and the bf16 hi / lo
-// activations and block sums of its 128 activation rows in LDS (double-buffered, one barrier per
+// block the workgroup stages the raw quants and scales of its 128 weight rows and the bf16 hi / fp16
+// lo16 activations and block sums of its 128 activation rows in LDS (double-buffered, one barrier per
 // block; the next block's global loads are in flight while the current one is multiplied), so every
 // weight fragment serves 4 activation tiles and every activation fragment 4 weight tiles from LDS
 // instead of each wave streaming both from L2.  The offset correction enters as the MFMA's initial
@@ -140,18 +143,32 @@ constexpr int kBRow = QK + 8;            // bf16 per staged activation row (16 B
 
 // Weights 8 lg .. 8 lg + 7 of the block as the tiled kernel's A fragment, in K-slot order
 // 0, 2, 1, 3, 4, 6, 5, 7 (the split pre-pass stores the activations in the same order).  Q4_0: one
-// AND-OR per two weights gives bf16(128 + n) exactly (exponent of 128, nibble in the mantissa), so the
-// block's offset is 136; Q8_0: q + 128 through the byte conversions.
+// AND-OR per two weights gives bf16(16 + n) exactly (exponent of 16, nibble in the top four mantissa
+// bits: 0x4180 | n << 3), so the block's offset is 24; the nibble reaches bits 3..6 by a rotation
+// (right by 29 = left by 3 for the low nibbles, right by 1 for the high ones; the bits it wraps fall
+// outside the mask).  The smallest base whose 16 values share one binade keeps the MFMA's running
+// sums, and so their fp32 rounding, within 5x of the signed weights' (a base of 128 made it 30x).
+// Q8_0: q + 128 through the byte conversions.
+// The same weights divided by 16 as exact fp16 (the B operand lo16 is fp16 and carries a factor 16):
+// Q4_0 as fp16((16 + n) / 16) = 0x3C00 | n << 6 (the nibble rotated to bits 6..9), Q8_0 as
+// fp16((q + 128) / 16) from the same floats.  Both products then add into one accumulator.
 template <int DT>
-__device__ __forceinline__ bf16x8_t tile_a_frag(uint2 w, int lg) {
-    uint32_t o[4];
+__device__ __forceinline__ void tile_a_frags(uint2 w, int lg, bf16x8_t &fb, f16x8_t &fh) {
+    uint32_t o[4], h[4];
     if constexpr (DT == VGX_Q4_0) {
-        const int sh = (lg >> 1) * 4;   // low nibbles for weights 0..15, high nibbles for 16..31
-        const uint32_t u0 = w.x >> sh, u1 = w.y >> sh;
-        o[0] = (u0 & 0x000F000Fu) | 0x43004300u;           // weights 0, 2 of the word
-        o[1] = ((u0 >> 8) & 0x000F000Fu) | 0x43004300u;    // weights 1, 3
-        o[2] = (u1 & 0x000F000Fu) | 0x43004300u;
-        o[3] = ((u1 >> 8) & 0x000F000Fu) | 0x43004300u;
+        const bool hi = (lg >> 1) != 0;       // low nibbles for weights 0..15, high nibbles for 16..31
+        // bf16: nibble to bits 3..6 (and 19..22); fp16: to bits 6..9 (and 22..25), bytes 0 / 2 and
+        // bytes 1 / 3 by rotations of their own (a left turn of six would wrap byte 3's nibble)
+        const int rot = hi ? 1 : 29, rh02 = hi ? 30 : 26, rh13 = hi ? 6 : 2;
+        const uint32_t u0 = __builtin_amdgcn_alignbit(w.x, w.x, rot), u1 = __builtin_amdgcn_alignbit(w.y, w.y, rot);
+        o[0] = (u0 & 0x00780078u) | 0x41804180u;           // weights 0, 2 of the word
+        o[1] = ((u0 >> 8) & 0x00780078u) | 0x41804180u;    // weights 1, 3
+        o[2] = (u1 & 0x00780078u) | 0x41804180u;
+        o[3] = ((u1 >> 8) & 0x00780078u) | 0x41804180u;
+        h[0] = (__builtin_amdgcn_alignbit(w.x, w.x, rh02) & 0x03C003C0u) | 0x3C003C00u;
+        h[1] = (__builtin_amdgcn_alignbit(w.x, w.x, rh13) & 0x03C003C0u) | 0x3C003C00u;
+        h[2] = (__builtin_amdgcn_alignbit(w.y, w.y, rh02) & 0x03C003C0u) | 0x3C003C00u;
+        h[3] = (__builtin_amdgcn_alignbit(w.y, w.y, rh13) & 0x03C003C0u) | 0x3C003C00u;
     } else {
         const uint32_t u[2] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u};
 #pragma unroll
@@ -160,13 +177,16 @@ __device__ __forceinline__ bf16x8_t tile_a_frag(uint2 w, int lg) {
             const float f2 = (float)((u[i] >> 16) & 0xFFu), f3 = (float)(u[i] >> 24);
             o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f2) & 0xFFFF0000u);
             o[2 * i + 1] = (__float_as_uint(f1) >> 16) | (__float_as_uint(f3) & 0xFFFF0000u);
+            h[2 * i] = pack_f16x2(f0 * 0.0625f, f2 * 0.0625f);
+            h[2 * i + 1] = pack_f16x2(f1 * 0.0625f, f3 * 0.0625f);
         }
     }
-    return __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
+    fb = __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
+    fh = __builtin_bit_cast(f16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
 }
 
 template <int DT, int EPI, bool SPLIT>
-__global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
+__global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
                                                           int nblk, int64_t rows_out,
                                                           const uint16_t *__restrict__ xh,
                                                           const uint16_t *__restrict__ xl,
@@ -174,7 +194,7 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
                                                           const float *__restrict__ bias, float *__restrict__ y,
                                                           int64_t ldy, float *__restrict__ part, int kper) {
     constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
-    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 136.0f;
+    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 24.0f;   // w + off: q + 128, or 16 + n for n - 8
     constexpr int APARTS = 4 * QB / 16;                  // 16-byte pieces of one row-quad block
     constexpr int AQ16 = kTM / 4 * APARTS;               // 16-byte pieces of the tile's block
     // Stage buffers (two blocks) and, after the K loop, the epilogue's half tile share one LDS area.
@@ -253,32 +273,31 @@ __global__ __launch_bounds__(256) void qgemm_tile_kernel(const uint8_t *__restri
         for (int c = 0; c < 4; ++c) acc[t][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](int buf) {
         bf16x8_t af[4];
-        float d[4][4];
+        f16x8_t af16[4];
+        vgx_f16x2_t d[4][2];     // fp16 scales, widened inside the FMAs (mixed-precision FMA)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int rql = wm * 16 + 4 * t + (l16 >> 2);       // A operand: weight row 16 t + l16
             const uint2 w = *reinterpret_cast<const uint2 *>(aq(buf) + (rql * 4 + (l16 & 3)) * QB +
                                                               (DT == VGX_Q8_0 ? 8 * lg : 8 * (lg & 1)));
-            af[t] = tile_a_frag<DT>(w, lg);
+            tile_a_frags<DT>(w, lg, af[t], af16[t]);
             const uint2 sc = asc(buf)[wm * 16 + 4 * t + lg];     // accumulator rows 16 t + 4 lg .. + 3
-            d[t][0] = half_bits_to_float(sc.x);
-            d[t][1] = half_bits_to_float(sc.x >> 16);
-            d[t][2] = half_bits_to_float(sc.y);
-            d[t][3] = half_bits_to_float(sc.y >> 16);
+            d[t][0] = __builtin_bit_cast(vgx_f16x2_t, sc.x);
+            d[t][1] = __builtin_bit_cast(vgx_f16x2_t, sc.y);
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int row = wn * 64 + 16 * c + l16;
             const bf16x8_t hf = *reinterpret_cast<const bf16x8_t *>(bh(buf) + row * kBRow + 8 * lg);
-            const bf16x8_t lf = *reinterpret_cast<const bf16x8_t *>(bl(buf) + row * kBRow + 8 * lg);
+            const f16x8_t lf = *reinterpret_cast<const f16x8_t *>(bl(buf) + row * kBRow + 8 * lg);
             const float ns = -OFF * bs(buf)[row];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 f32x4_t pr = f32x4_t{ns, ns, ns, ns};
                 pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], hf, pr, 0, 0, 0);
-                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], lf, pr, 0, 0, 0);
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(af16[t], lf, pr, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf(d[t][i], pr[i], acc[t][c][i]);
+                for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf((float)d[t][i >> 1][i & 1], pr[i], acc[t][c][i]);
             }
         }
     };
@@ -483,8 +502,8 @@ __global__ __launch_bounds__(256) void f32gemm_tile_kernel(const float *__restri
 
 // ---------------------------------------------------------------------------------------------
 // Decode batches (up to 64 activation rows): one launch without the split pre-pass.  Each workgroup
-// converts the activations of its K range itself, 4 blocks at a time, into LDS (bf16 hi and lo, the
-// per-block sums of hi + lo), shared by its 4 waves; the chunks are double-buffered so the next
+// converts the activations of its K range itself, 4 blocks at a time, into LDS (bf16 hi, mid and lo,
+// the per-block sums of the pieces), shared by its 4 waves; the chunks are double-buffered so the next
 // chunk's activations and weights are requested before the current one is multiplied (requesting
 // the weights a second chunk earlier measured no faster).  The fused
 // RMSNorm stages lnw * x and scales the finished sums by 1 / rms of the activation row (sum x^2 is
@@ -507,6 +526,7 @@ __global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const u
     constexpr int R = 16 * NC;                     // staged activation rows
     constexpr int F4 = R * kCK * 8 / 256;          // staged float4 per thread per chunk
     __shared__ __align__(16) uint16_t sh[2][R][kSRow];
+    __shared__ __align__(16) uint16_t sm[2][R][kSRow];
     __shared__ __align__(16) uint16_t sl[2][R][kSRow];
     __shared__ float ssum[2][R][kCK];
     __shared__ float sinv[R];
@@ -560,17 +580,19 @@ __global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const u
                 if constexpr (NORM) ssq[i] = fmaf(e[k], e[k], ssq[i]);
                 u[k] = NORM ? g[k] * e[k] : e[k];
             }
-            uint2 hw, lw;
-            split_bf16x2(u[0], u[1], hw.x, lw.x);
-            split_bf16x2(u[2], u[3], hw.y, lw.y);
+            uint2 hw, mw, lw;
+            split3_bf16x2(u[0], u[1], hw.x, mw.x, lw.x);
+            split3_bf16x2(u[2], u[3], hw.y, mw.y, lw.y);
             float sum = 0.0f;
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-                const uint32_t h = k < 2 ? hw.x : hw.y, l = k < 2 ? lw.x : lw.y;
+                const uint32_t h = k < 2 ? hw.x : hw.y, m = k < 2 ? mw.x : mw.y, l = k < 2 ? lw.x : lw.y;
                 const int sh16 = (k & 1) ? 0 : 16;
-                sum += __uint_as_float((h << sh16) & 0xFFFF0000u) + __uint_as_float((l << sh16) & 0xFFFF0000u);
+                sum += (__uint_as_float((h << sh16) & 0xFFFF0000u) + __uint_as_float((m << sh16) & 0xFFFF0000u)) +
+                       __uint_as_float((l << sh16) & 0xFFFF0000u);
             }
             *reinterpret_cast<uint2 *>(&sh[buf][row][bl * QK + j4 * 4]) = hw;
+            *reinterpret_cast<uint2 *>(&sm[buf][row][bl * QK + j4 * 4]) = mw;
             *reinterpret_cast<uint2 *>(&sl[buf][row][bl * QK + j4 * 4]) = lw;
             // the 8 threads of one (row, block) are 8 consecutive lanes
             sum += __shfl_xor(sum, 1, kWave);
@@ -622,12 +644,14 @@ __global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const u
             for (int c = 0; c < NC; ++c) {
                 const int row = c * 16 + l16;
                 const uint4 xh = *reinterpret_cast<const uint4 *>(&sh[buf][row][u * QK + 8 * lg]);
+                const uint4 xm = *reinterpret_cast<const uint4 *>(&sm[buf][row][u * QK + 8 * lg]);
                 const uint4 xl = *reinterpret_cast<const uint4 *>(&sl[buf][row][u * QK + 8 * lg]);
                 const float corr = OFF * ssum[buf][row][u];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     f32x4_t pr = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
                     pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, xh), pr, 0, 0, 0);
+                    pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, xm), pr, 0, 0, 0);
                     pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, xl), pr, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf(d[t][i], pr[i] - corr, acc[t][c][i]);
@@ -810,9 +834,9 @@ int64_t gemm_scale_off(int dt, int64_t rows, int64_t cols) {
     return (q + 255) / 256 * 256;
 }
 
+inline int64_t split_plane_bytes(int64_t batch, int64_t cols) { return (batch * cols * 2 + 255) / 256 * 256; }
 inline int64_t split_bytes(int64_t batch, int64_t cols) {
-    const int64_t h = (batch * cols * 2 + 255) / 256 * 256;
-    return 2 * h + (batch * (cols / QK) * 4 + 255) / 256 * 256;
+    return 2 * split_plane_bytes(batch, cols) + (batch * (cols / QK) * 4 + 255) / 256 * 256;
 }
 
 constexpr int kMaxKSplit = 16;
@@ -1097,9 +1121,10 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     if (!workspace || workspace_bytes < split_bytes(batch, cols) + part_bytes(ks, batch, n_rq * 4)) return VGX_E_ARENA;
     if ((uintptr_t)workspace % 256) return VGX_E_ALIGN;
     const int64_t soff = gemm_scale_off(dtype, rows_packed, cols);
+    const int64_t pb = split_plane_bytes(batch, cols);
     auto *xh = static_cast<uint16_t *>(workspace);
-    auto *xl = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + (batch * cols * 2 + 255) / 256 * 256);
-    auto *xs = reinterpret_cast<float *>(static_cast<char *>(workspace) + 2 * ((batch * cols * 2 + 255) / 256 * 256));
+    auto *xl = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + pb);
+    auto *xs = reinterpret_cast<float *>(static_cast<char *>(workspace) + 2 * pb);
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(xsplit_kernel, dim3((unsigned)batch), dim3(256), 0, st, x, ldx, norm_w, eps, (int)cols, xh, xl,
                        xs);

@@ -21,8 +21,10 @@ Differences by design:
   content is never read before being overwritten).
 * RoPE uses one device table of fp32 cos/sin rows computed from double-precision angles, as the C
   runtime does (runtime/vault3.c:840-849, 2126-2133).
-* prefill() with batch > 1 and forward() with batch > 1 run the streaming step token by token (the
-  reference asserts these equal its parallel block-sliding forms, tests/test_vault_v3.py:52-90).
+* prefill() / forward() with batch > 1 and forward(mode="full") run the parallel form: every
+  projection over all B * L tokens at once (MFMA GEMM), RoPE at absolute positions with the ring
+  table's double-precision angles, and block_sliding_attention (or full causal attention) on the
+  MFMA prefill kernel; batch-1 prefill / forward keep the chunk-recurrent form (segment memory).
 """
 from __future__ import annotations
 
@@ -35,6 +37,7 @@ import numpy as np
 import torch
 
 from . import ops
+from .attention import block_sliding_attention, causal_attention, rope_table_double
 from .config import VAULTv3Config
 from .weights import ModelWeights
 
@@ -190,11 +193,13 @@ class VAULTv3ForCausalLM:
         self.device = weights.device
         self.kv_dtype = kv_dtype
         self.ws = ops.Workspace(self.device)
+        self.prefill_ws = ops.Workspace(self.device)
         self.tokens = weights.tokens
         vs = self.cfg.vocab_size
         self.tier_lut = self.tokens.tiers if self.tokens is not None else np.zeros(vs, dtype=np.uint8)
         self.use_graphs = True          # replay captured HIP graphs for decode steps
         self._table = None
+        self._abs_table = None
         self._p0 = 0
         self._ensure_table(sink_capacity(self.cfg) + max(1, self.cfg.seg_budget))
 
@@ -206,14 +211,18 @@ class VAULTv3ForCausalLM:
         neg = max(neg, c.window)
         if self._table is not None and -self._p0 >= neg:
             return
-        D = c.head_dim
-        i = np.arange(D // 2, dtype=np.float64)
-        inv = (1.0 / np.exp(np.log(np.float64(np.float32(c.rope_theta))) * (2.0 * i) / D)).astype(np.float32)
-        pos = np.arange(-neg, 2 * c.window, dtype=np.float64)
-        ang = pos[:, None] * inv.astype(np.float64)[None, :]
-        tab = np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
+        tab = rope_table_double(np.arange(-neg, 2 * c.window), c.head_dim, c.rope_theta)
         self._table = torch.from_numpy(tab).to(self.device)
         self._p0 = -neg
+
+    def _abs_rows(self, L: int) -> torch.Tensor:
+        """Table rows of absolute positions [0, L) (the parallel forms rotate at absolute positions),
+        same arithmetic as the ring table; grown on demand."""
+        if self._abs_table is None or self._abs_table.shape[0] < L:
+            n = max(L, 2 * self.cfg.window)
+            self._abs_table = torch.from_numpy(rope_table_double(np.arange(n), self.cfg.head_dim,
+                                                                 self.cfg.rope_theta)).to(self.device)
+        return self._abs_table
 
     def _rows(self, p: int) -> torch.Tensor:
         """Table rows starting at position p."""
@@ -273,12 +282,9 @@ class VAULTv3ForCausalLM:
         if B == 1:
             h, st = self._chunk_recurrent(input_ids, bud, all_logits=False)
             return self._logits(h), st
-        st = self.new_state(B, seg_budget=0)
-        st.set_pinned(self.cfg.n_sink)
-        lg = None
-        for t in range(L):
-            lg = self.step(input_ids[:, t], st)
-        return lg, st
+        # batch > 1: the parallel sliding-window + sink prefill (src/vault_v3_model.py:2177-2212)
+        h, st = self._forward_block(input_ids, mode="block", want_state=True, last_only=True)
+        return self._logits(h), st
 
     @torch.no_grad()
     def forward(self, input_ids: torch.Tensor, mode: str = "block", vault_on: bool = False,
@@ -286,15 +292,13 @@ class VAULTv3ForCausalLM:
         """Logits for every position, (B, L, V)."""
         _ = vault_on
         B, L = input_ids.shape
-        if mode == "full" and L > 2 * self.cfg.window:
-            raise NotImplementedError("full causal attention beyond 2W is not part of the streaming path")
         bud = self.cfg.seg_budget if seg_budget is None else int(seg_budget)
-        if B == 1:
+        if B == 1 and mode == "block":
             h, _ = self._chunk_recurrent(input_ids, bud, all_logits=True)
             return self._logits(h).unsqueeze(0)
-        st = self.new_state(B, seg_budget=0)
-        st.set_pinned(self.cfg.n_sink)
-        return torch.stack([self.step(input_ids[:, t], st) for t in range(L)], dim=1)
+        # batch > 1, or full causal attention: the parallel form (src/vault_v3_model.py:2118-2151)
+        h, _ = self._forward_block(input_ids, mode=mode, want_state=False, last_only=False)
+        return self._logits(h).view(B, L, -1)
 
     __call__ = forward
 
@@ -671,6 +675,121 @@ class VAULTv3ForCausalLM:
 
     def _logits(self, h: torch.Tensor) -> torch.Tensor:
         return ops.qlinear(self.w.embed, h, norm=(self.w.norm, self.cfg.rms_eps))
+
+    def _forward_block(self, input_ids: torch.Tensor, mode: str, want_state: bool, last_only: bool):
+        """Parallel form for B sequences of L tokens (src/vault_v3_model.py:1048-1061, 2118-2151,
+        2177-2212): hidden states of every token (or of each sequence's last token) and, with
+        ``want_state``, the streaming state the reference's batched prefill leaves (n_sink sinks
+        pinned, no segment memory; ring rows re-rotated to their re-based positions)."""
+        cfg, w = self.cfg, self.w
+        B, L = input_ids.shape
+        H, G, D, W = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.window
+        HD, N = H * D, B * L
+        dev = self.device
+        ids = input_ids.reshape(-1).to(dev, torch.int64)
+        st = None
+        if want_state:
+            st = self.new_state(B, seg_budget=0)
+            st.set_pinned(cfg.n_sink)
+            n_pin = st.n_pin
+        else:
+            n_pin = max(0, min(cfg.n_sink, W, sink_capacity(cfg)))
+        ns = min(n_pin, L)
+        tab = self._abs_rows(L)
+        mfma = D == 128 and H // G in (1, 2, 4, 6, 8)
+        x = ops.embed(w.embed, ids, pad_row=0)                                 # [N, d]
+        kr = torch.empty(B, G, L, D, dtype=torch.float32, device=dev)          # rotated keys
+        vv = torch.empty(B, G, L, D, dtype=torch.float32, device=dev)          # values, same strides
+        ao = torch.empty(B, L, H, D, dtype=torch.float32, device=dev)
+        hbuf = torch.empty(N, cfg.d_ff, dtype=torch.float32, device=dev)
+        # raw keys / values of the sink tokens: the state's sink slots, or scratch
+        if st is None and ns:
+            sk_all = torch.empty(B, G, ns, D, dtype=torch.float32, device=dev)
+            sv_all = torch.empty_like(sk_all)
+        last = (L - 1) // W
+        cnt = L - last * W
+        for li, lw in enumerate(w.layers):
+            q, k, v = self._qkv(lw, x, N)                                      # k / v stay raw in place
+            for b in range(B):
+                r = slice(b * L, (b + 1) * L)
+                if ns:
+                    sk, sv = (st.k_sink_raw[li][b], st.v_sink[li][b]) if st is not None else (sk_all[b], sv_all[b])
+                else:
+                    sk = sv = None
+                ops.rope_qkv_write(q[r], k[r], v[r], tab, D, kr[b], None, vv[b], D, L * D,
+                                   sk, sv, ns, D, sk.stride(0) if sk is not None else 0)
+            qv = q.view(B, L, H, D).permute(0, 2, 1, 3)
+            aov = ao.permute(0, 2, 1, 3)
+            full = mode == "full" or L <= 2 * W
+            if mfma and full:
+                causal_attention(qv, kr, vv, aov)
+            elif mfma:
+                block_sliding_attention(qv, kr, vv, W, k_raw=k.view(B, L, G, D).permute(0, 2, 1, 3),
+                                        n_sink=n_pin, head_dim=D, rope_theta=cfg.rope_theta, out=aov,
+                                        angles="double")
+            else:
+                sinks = None
+                if ns and not full:
+                    sinks = (st.k_sink_raw[li], st.v_sink[li]) if st is not None else (sk_all, sv_all)
+                self._block_attn_split(q.view(B, L, H, D), kr, vv, sinks, ns, ao, full)
+            if st is not None:
+                self._fill_ring(st, li, k.view(B, L, G, D), v.view(B, L, G, D), last, cnt)
+            ops.qlinear(lw.wo, ao.view(N, HD), out=x, accumulate=True)
+            ops.qlinear_swiglu(lw.wgu, x, out=hbuf, norm=(lw.ln2, cfg.rms_eps))
+            ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
+        if st is not None:
+            ids_np = input_ids.to("cpu", torch.int64).numpy()
+            st.tok_cur[:, :cnt] = ids_np[:, last * W:L]
+            if last >= 1:
+                st.tok_prev[:, :] = ids_np[:, (last - 1) * W:last * W]
+            st.pos = L
+            if L >= 2 * W:
+                self._refresh_prefix(st, seg_active=False)
+        h = x.view(B, L, -1)[:, L - 1] if last_only else x
+        return h, st
+
+    def _block_attn_split(self, q: torch.Tensor, kr: torch.Tensor, vv: torch.Tensor, sinks, ns: int,
+                          ao: torch.Tensor, full: bool) -> None:
+        """Block sliding-window (or, ``full``, causal) attention on the split-K decode kernel, for head
+        sizes the MFMA prefill kernel does not take: per sequence and W-token query chunk, one call
+        over [sinks re-rotated to (i-1)W - S + j | chunk i-1 | chunk i causal].  q / ao: [B, L, H, D];
+        kr / vv: [B, G, L, D]; sinks: raw (keys, values) [B, G, >= ns, D] or None."""
+        cfg = self.cfg
+        B, L, H, D = q.shape
+        G, W = kr.shape[1], cfg.window
+        tab = self._abs_rows(L)
+        # re-rotated sink keys, laid out like the sink values (a span's K and V share strides)
+        rot = torch.empty_like(sinks[1][0]) if sinks is not None else None
+        scale = 1.0 / math.sqrt(D)
+        for b in range(B):
+            for i in range((L + W - 1) // W):
+                r0, r1 = i * W, min(L, (i + 1) * W)
+                spans = []
+                if full:
+                    lo = 0
+                else:
+                    lo = max(0, r0 - W)
+                    if i >= 2 and sinks is not None:
+                        ops.rope_rotate(sinks[0][b][:, :ns], rot[:, :ns], tab[(i - 1) * W - ns:], D)
+                        spans.append((rot[None, :, :ns], sinks[1][b][None, :, :ns]))
+                if r0 > lo:
+                    spans.append((kr[b:b + 1, :, lo:r0], vv[b:b + 1, :, lo:r0]))
+                spans.append((kr[b:b + 1, :, r0:r1], vv[b:b + 1, :, r0:r1]))
+                ops.attn_decode(q[b, r0:r1], spans, out=ao[b, r0:r1], scale=scale, ws=self.prefill_ws,
+                                causal_base=0)
+
+    def _fill_ring(self, st: VAULTv3State, li: int, k: torch.Tensor, v: torch.Tensor, last: int, cnt: int) -> None:
+        """Ring rows of layer li after a parallel prefill (src/vault_v3_model.py:2197-2206): the last
+        (partial) chunk into cur at re-based positions W + j (j if it is chunk 0), the chunk before
+        it into prev at positions j; raw keys and values alongside.  k / v: [B, L, G, D] raw views."""
+        W, D = self.cfg.window, self.cfg.head_dim
+        for b in range(k.shape[0]):
+            for c0, n, rot, raw, vd, row in ((last * W, cnt, st.k_cur, st.kraw_cur, st.v_cur, W if last >= 1 else 0),
+                                             ((last - 1) * W, W, st.k_prev, st.kraw_prev, st.v_prev, 0)):
+                if c0 < 0:
+                    continue
+                ops.rope_qkv_write(None, k[b, c0:c0 + n], v[b, c0:c0 + n], self._rows(row), D, rot[li][b],
+                                   raw[li][b], vd[li][b], D, W * D)
 
     def _chunk_recurrent(self, input_ids: torch.Tensor, bud: int, all_logits: bool):
         """Chunk-recurrent prefill / forward for batch 1 (src/vault_v3_model.py:1938-2116)."""
