@@ -228,9 +228,10 @@ static uint64_t splitmix(uint64_t *x) {
 
 static void fill(float *p, uint64_t n, uint64_t *rng) {
     for (uint64_t i = 0; i < n; i++) {
-        /* sum of 4 uniforms, centred and scaled to unit variance */
+        /* sum of the four 16-bit uniforms of one draw, centred and scaled to unit variance */
+        const uint64_t z = splitmix(rng);
         double s = 0.0;
-        for (int k = 0; k < 4; k++) s += (double)(splitmix(rng) >> 11) * (1.0 / 9007199254740992.0);
+        for (int k = 0; k < 4; k++) s += ((double)((z >> (16 * k)) & 0xFFFFu) + 0.5) * (1.0 / 65536.0);
         p[i] = (float)((s - 2.0) * 1.7320508075688772);
     }
 }

@@ -88,3 +88,58 @@ def test_decode_across_chunk_boundary_at_100k_matches_reference_runtime(full_mod
     ids = np.random.default_rng(6).integers(0, cfg.vocab_size, 8)
     _compare(m, rt, st, ids)
     assert np.array_equal(rt.mem_pos(), st.mem_pos.numpy())
+
+
+BATCH = 32
+
+
+def _seed_batch_and_reference(cfg, m, rt, pos, ids, kv):
+    """Batch 32 without segment memory (the reference's batched path): sequence b's state is the
+    reference runtime's seeded with seed 200 + b (512 locked sinks, full window, v3_set_seg_budget 0),
+    copied field by field into row b of the GPU state; the runtime then steps that sequence's ids and
+    its logits are kept.  Returns (GPU state, reference logits [B, T, V])."""
+    G, D = cfg.n_kv_heads, cfg.head_dim
+    st = m.new_state(BATCH, seg_budget=0)
+    want = np.empty((BATCH, ids.shape[1], cfg.vocab_size), dtype=np.float32)
+    for b in range(BATCH):
+        rt.reset()
+        rt.set_seg_budget(0)
+        rt.seed_long_context(pos, N_PIN, 0, seed=200 + b)
+        for name in st.KV_FIELDS:
+            if "seg" in name:
+                continue
+            t = getattr(st, name)
+            for li in range(cfg.n_layers):
+                a = rt.state_field(li, name, G, D)
+                t[li, b].copy_(torch.from_numpy(np.ascontiguousarray(a[:, :t.shape[3]])).to(t.dtype))
+        for i, tok in enumerate(ids[b]):
+            rt.step(int(tok), want[b, i])
+    st.pos = pos
+    st.n_pin = N_PIN
+    st.pin_locked = True
+    return st, want
+
+
+@pytest.mark.parametrize("kv", [torch.float32, torch.bfloat16])
+def test_batch32_decode_across_boundary_at_100k_matches_reference_runtime(full_model, kv):
+    """Config 5 at batch 32: 32 sequences at positions 100,348 .. 100,355 (3584 keys, then the chunk
+    boundary at 100,352: re-basing and sink re-rotation at full size), each against the reference C
+    runtime stepping that sequence alone.  fp32 KV: rel < 1e-4 per step and sequence; bf16 KV (what
+    the batch-32 throughput figure runs): max |dlogit| <= 5e-2; 100% top-1 in both."""
+    cfg, m32, rt = full_model
+    m = VAULTv3ForCausalLM(m32.w, kv_dtype=kv)
+    ids = np.random.default_rng(7).integers(0, cfg.vocab_size, (BATCH, 8))
+    st, want = _seed_batch_and_reference(cfg, m, rt, 100_348, ids, kv)
+    worst = 0.0
+    for i in range(ids.shape[1]):
+        got = m.step(torch.from_numpy(ids[:, i]), st).double().cpu().numpy()
+        w = want[:, i].astype(np.float64)
+        err = np.abs(got - w).max(axis=1)
+        rel = err / np.abs(w).max(axis=1)
+        worst = max(worst, float(rel.max()))
+        if kv == torch.float32:
+            assert rel.max() < 1e-4, (i, float(rel.max()))
+        else:
+            assert err.max() <= 5e-2, (i, float(err.max()))
+        assert np.array_equal(got.argmax(1), w.argmax(1)), i
+    print(f"batch 32 {kv}: worst rel {worst:.3e}", flush=True)
