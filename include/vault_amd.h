@@ -193,6 +193,19 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
                     int64_t H, int64_t G, int64_t D, float scale, void *workspace, int64_t workspace_bytes,
                     void *stream);
 
+/* vgx_attn_decode without a caller workspace, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference.  Same arguments, results and kernels as vgx_attn_decode; the split partials and
+ * tickets live in a fixed 2 MiB device array of the library, one per GPU, held until the process
+ * ends (located, and its tickets cleared, by the first call on each device).  Calls that would need
+ * more than 2 MiB of workspace (vgx_attn_decode_workspace_bytes) return VGX_E_LIMIT: at 12 / 2 heads
+ * and D = 128 that admits every batch up to 64 at 3584 keys (1.6 MB at most).  Every call on one GPU uses that GPU's
+ * array, so calls that overlap in time on one GPU (other streams, other threads) race; the array
+ * keeps the last call's contents. */
+int vgx_attn_decode_noalloc(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span *spans, int n_spans,
+                            const float *bias, int64_t bias_hstride, int bias_span, int64_t causal_base, float *out,
+                            int64_t B, int64_t H, int64_t G, int64_t D, float scale, void *stream);
+
 /* A run of keys for prefill attention: key j of kv group g at element offset
  * g*group_stride + j*row_stride of k (and v); rows are head_dim contiguous elements of the KV dtype
  * (bf16 or fp32; every run of one call has the same dtype). */

@@ -17,6 +17,8 @@
 // measured 2x slower), more by attn_merge_kernel, a second launch spread over B * H workgroups.
 #include "common.h"
 
+#include <mutex>
+
 using namespace vgx;
 
 namespace {
@@ -807,6 +809,48 @@ bool dispatch_grp(int grp, int D, dim3 grid, hipStream_t st, const float *q, int
     return false;
 }
 
+int attn_decode_impl(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span *spans, int n_spans,
+                     const float *bias, int64_t bias_hstride, int bias_span, int64_t causal_base, float *out, int64_t B,
+                     int64_t H, int64_t G, int64_t D, float scale, void *workspace, int64_t workspace_bytes,
+                     void *stream);
+
+// ---------------------------------------------------------------------------------------------
+// Scratch of the allocation-free entry point: one fixed array per GPU (the split tickets, then the
+// partials, as in a caller's workspace), never allocated at run time.  Host code uses only the
+// per-device address that hipGetSymbolAddress returns for it (the array's name is a host-side
+// stand-in, not a device address).  The address is looked up, and the ticket region cleared, once
+// per device by the first call on that device.
+constexpr int64_t kScratchBytes = 2ll << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[kMaxDevices] = {};
+
+__global__ void zero_words_kernel(uint32_t *__restrict__ p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+int device_scratch(hipStream_t st, void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return VGX_E_HIP;
+    if (dev >= kMaxDevices) return VGX_E_LIMIT;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return VGX_E_HIP;
+        // the tickets must start at zero (every call leaves them so); a fill kernel, ordered before the
+        // first use on the caller's stream
+        hipLaunchKernelGGL(zero_words_kernel, dim3(16), dim3(256), 0, st, static_cast<uint32_t *>(p),
+                           ticket_bytes(0, 0) / 4);
+        if (hipGetLastError() != hipSuccess) return VGX_E_HIP;
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return VGX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -824,6 +868,41 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
                     const float *bias, int64_t bias_hstride, int bias_span, int64_t causal_base, float *out, int64_t B,
                     int64_t H, int64_t G, int64_t D, float scale, void *workspace, int64_t workspace_bytes,
                     void *stream) {
+    return attn_decode_impl(kv_dtype, q, ldq, spans, n_spans, bias, bias_hstride, bias_span, causal_base, out, B, H, G,
+                            D, scale, workspace, workspace_bytes, stream);
+}
+
+int vgx_attn_decode_noalloc(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span *spans, int n_spans,
+                            const float *bias, int64_t bias_hstride, int bias_span, int64_t causal_base, float *out,
+                            int64_t B, int64_t H, int64_t G, int64_t D, float scale, void *stream) {
+    if (!spans || n_spans < 1 || n_spans > 4) return spans ? VGX_E_LIMIT : VGX_E_ARG;
+    if (B <= 0 || H <= 0 || G <= 0 || D <= 0 || H % G) return VGX_E_SIZE;
+    int64_t n_keys = 0;
+    for (int i = 0; i < n_spans; ++i) {
+        if (spans[i].len < 0 || spans[i].len > 0x3FFFFFFF) return VGX_E_SIZE;
+        n_keys += spans[i].len;
+    }
+    if (n_keys <= 0) return VGX_E_SIZE;
+    const int64_t need = vgx_attn_decode_workspace_bytes(B, H, G, D, n_keys);
+    if (need < 0) return (int)need;
+    if (need > kScratchBytes) return VGX_E_LIMIT;   // beyond the fixed scratch: use vgx_attn_decode
+    void *ws = nullptr;
+    if (need > 0) {
+        const int rc = device_scratch(static_cast<hipStream_t>(stream), &ws);
+        if (rc != VGX_OK) return rc;
+    }
+    return attn_decode_impl(kv_dtype, q, ldq, spans, n_spans, bias, bias_hstride, bias_span, causal_base, out, B, H, G,
+                            D, scale, ws, need > 0 ? kScratchBytes : 0, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int attn_decode_impl(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span *spans, int n_spans,
+                     const float *bias, int64_t bias_hstride, int bias_span, int64_t causal_base, float *out, int64_t B,
+                     int64_t H, int64_t G, int64_t D, float scale, void *workspace, int64_t workspace_bytes,
+                     void *stream) {
     if (kv_dtype != VGX_F32 && kv_dtype != VGX_BF16) return VGX_E_DTYPE;
     if (!q || !spans || !out) return VGX_E_ARG;
     if (n_spans < 1 || n_spans > 4) return VGX_E_LIMIT;
@@ -917,4 +996,4 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
     return VGX_OK;
 }
 
-}  // extern "C"
+}  // namespace
