@@ -331,6 +331,65 @@ int vgx_rope_rotate(int kv_dtype, const void *src, void *dst, int64_t n_outer, i
 int vgx_gather_rows(int dtype, const void *src, void *dst, const int32_t *idx, int64_t n_idx, int64_t src_rows,
                     int64_t n_outer, int64_t src_ostride, int64_t dst_ostride, int64_t D, void *stream);
 
+/* ---------------------------------------------------------------- segment-memory bank ---------- */
+
+/* Control words of a segment bank (int32, on the device): entries in the bank, running global
+ * segment-id offset, segment id and length of the current chunk's open segment.  They mirror
+ * mem_cnt, seg_id_offset, cur_seg_id and cur_seg_len of the reference state (runtime/vault3.h:93-161). */
+enum { VGX_SEG_MEM_CNT = 0, VGX_SEG_ID_OFFSET = 1, VGX_SEG_CUR_ID = 2, VGX_SEG_LEN = 3, VGX_SEG_WORDS = 4 };
+
+/* One decode step's bookkeeping: tok_cur[b * tok_ld + c] = ids[b] for b < B at the ring slot
+ * c = step[VGX_STEP_SLOT]; with seg_cur (batch 1 with segment memory), seg_cur[c] = the open segment
+ * id, then the segment closes after this token at c = window - 1, at seg_max tokens, or by the token's
+ * break tier (tiers[id], a byte per vocabulary entry; NULL = all 0): tier 1 from seg_min tokens, tier
+ * 2 from max(seg_min, 2 seg_max / 3), tier 3 from max(seg_min, seg_max - 8).  Replaces
+ * runtime/vault3.c:2107-2124 and src/vault_v3_model.py:2256-2268. */
+int vgx_seg_step(const int64_t *ids, int64_t B, const int32_t *step, int32_t *tok_cur, int64_t tok_ld,
+                 int32_t *seg_cur, int32_t *ctrl, const uint8_t *tiers, int64_t vocab, int64_t seg_min,
+                 int64_t seg_max, int64_t window, void *stream);
+
+/* The segment-bank update at a chunk boundary, for the evicted chunk ev_chunk (its tokens' scores
+ * sc_prev, local segment ids seg_prev, tokens tok_prev, window entries each): quarantine (a score
+ * <= -1e29 sets its whole segment to -1e30, written back), per-segment maximum, candidates t >= t0
+ * (t0 = the pinned count for chunk 0) scored max - 1e-6 (global segment id mod 16384), then the top
+ * `budget` of bank + candidates by (score desc, position asc), kept in chronological order.  The bank
+ * arrays (mem_pos int64, mem_score fp32, mem_tok / mem_seg int32, capacity >= budget) and the control
+ * words are updated in place; idx_old[j] / idx_new[j] (budget entries each) give new slot j's source
+ * row in the old bank / the evicted chunk, -1 otherwise (for vgx_gather_rows_masked).  window + budget
+ * <= 4096.  One workgroup; replaces update_segment_bank (runtime/vault3.c:1833-1915, quarantine
+ * :2079-2088) and src/vault_v3_model.py:1858-1921 with merge_segment_bank_indices (:918-949). */
+int vgx_seg_evict(float *sc_prev, const int32_t *seg_prev, const int32_t *tok_prev, int64_t window, int64_t *mem_pos,
+                  float *mem_score, int32_t *mem_tok, int32_t *mem_seg, int32_t *ctrl, int64_t ev_chunk,
+                  int64_t t0, int64_t budget, int32_t *idx_old, int32_t *idx_new, void *stream);
+
+/* vgx_gather_rows, except that rows whose index is negative (or beyond src_rows) are left as they are
+ * (the two-source bank compaction: old bank rows, then the evicted chunk's). */
+int vgx_gather_rows_masked(int dtype, const void *src, void *dst, const int32_t *idx, int64_t n_idx, int64_t src_rows,
+                           int64_t n_outer, int64_t src_ostride, int64_t dst_ostride, int64_t D, void *stream);
+
+/* vgx_rope_rotate with the table row of row i at (i + row_base - *dyn) (table = the row of position
+ * 0; negative rows lie before it), rows i >= *dyn skipped when limit_rows != 0: the re-rotation of the
+ * segment keys to [-M, 0) and of the sinks to [-(M + S), -M) with the bank count M on the device
+ * (src/vault_v3_model.py:1842-1856; runtime/vault3.c:859-896). */
+int vgx_rope_rotate_dyn(int kv_dtype, const void *src, void *dst, int64_t n_outer, int64_t src_ostride,
+                        int64_t dst_ostride, int64_t n_rows, int64_t D, const float *table, int64_t table_rstride,
+                        const int32_t *dyn, int64_t row_base, int limit_rows, void *stream);
+
+/* ---------------------------------------------------------------- token selection -------------- */
+
+/* out[b] = the index of the largest of the V logits of row b (row stride ld), the first one on ties;
+ * NaN logits are never selected.  Replaces v3_argmax (runtime/vault3.c:3198-3202). */
+int vgx_argmax(const float *logits, int64_t ld, int64_t B, int64_t V, int64_t *out, void *stream);
+
+/* Top-k sampling per row (k <= 64): the k largest logits (ties: the smaller index first), weights
+ * exp((l_j - l_max) / temp), one draw of the row's xorshift64 state rng[b] (updated in place; 0 is
+ * replaced by 0x9E3779B97F4A7C15): r = ((x >> 40) & 0xFFFFFF) / 2^24 * sum, the first j whose running
+ * sum reaches r.  temp <= 0 or k <= 1 gives the argmax.  workspace: vgx_sample_topk_workspace_bytes.
+ * Replaces v3_sample_topk (runtime/vault3.c:3204-3230). */
+int64_t vgx_sample_topk_workspace_bytes(int64_t B, int64_t V);
+int vgx_sample_topk(const float *logits, int64_t ld, int64_t B, int64_t V, int64_t k, float temp, uint64_t *rng,
+                    int64_t *out, void *workspace, int64_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------- segment-memory scorer -------- */
 
 /* Causal EMA habituation of scorer features over T tokens (rows t*ldf of f, fd features each):

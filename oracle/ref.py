@@ -53,6 +53,10 @@ def _load():
         lib.ref_state_field.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_void_p]
         lib.ref_state_field.restype = C.c_int64
         lib.ref_seed_long_context.restype = C.c_int
+        lib.v3_argmax.restype = C.c_uint32
+        lib.v3_argmax.argtypes = [C.c_void_p, C.c_uint32]
+        lib.v3_sample_topk.restype = C.c_uint32
+        lib.v3_sample_topk.argtypes = [C.c_void_p, C.c_uint32, C.c_uint32, C.c_float, C.POINTER(C.c_uint64)]
         lib.ref_state_flags.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         lib.ref_set_seg_budget.argtypes = [C.c_void_p, C.c_uint32]
         lib.ref_set_seg_budget.restype = C.c_int
@@ -134,3 +138,17 @@ class RefRuntime:
         rc = _load().ref_seed_long_context(self._h, pos, n_pin, mem_cnt, seed)
         if rc:
             raise RuntimeError("seed_long_context rejected the arguments")
+
+
+def argmax(logits: np.ndarray) -> int:
+    """The reference's v3_argmax (runtime/vault3.c:3198-3202) on one fp32 row."""
+    a = np.ascontiguousarray(logits, dtype=np.float32)
+    return int(_load().v3_argmax(a.ctypes.data, a.size))
+
+
+def sample_topk(logits: np.ndarray, k: int, temp: float, state: int):
+    """The reference's v3_sample_topk (runtime/vault3.c:3204-3230): (index, new xorshift state)."""
+    a = np.ascontiguousarray(logits, dtype=np.float32)
+    st = C.c_uint64(state)
+    idx = _load().v3_sample_topk(a.ctypes.data, a.size, k, float(temp), C.byref(st))
+    return int(idx), int(st.value)

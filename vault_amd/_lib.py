@@ -21,6 +21,7 @@ ERRORS = {
 F32, F16, BF16, Q8_0, Q4_0 = 0, 1, 2, 8, 9
 EPI_STORE, EPI_ACCUM, EPI_SWIGLU = 0, 1, 2
 STEP_SLOT, STEP_TABLE_ROW, STEP_SINK_SLOT, STEP_N_CUR, STEP_WORDS = 0, 1, 2, 3, 4
+SEG_MEM_CNT, SEG_ID_OFFSET, SEG_CUR_ID, SEG_LEN, SEG_WORDS = 0, 1, 2, 3, 4
 
 P = C.c_void_p
 I32 = C.c_int
@@ -46,6 +47,13 @@ _SIGS = {
     "vgx_qgemm": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P, I64, P]),
     "vgx_attn_decode_workspace_bytes": (I64, [I64, I64, I64, I64, I64]),
     "vgx_attn_decode": (I32, [I32, P, I64, P, I32, P, I64, I32, I64, P, I64, I64, I64, I64, F, P, I64, P]),
+    "vgx_seg_step": (I32, [P, I64, P, P, I64, P, P, P, I64, I64, I64, I64, P]),
+    "vgx_seg_evict": (I32, [P, P, P, I64, P, P, P, P, P, I64, I64, I64, P, P, P]),
+    "vgx_gather_rows_masked": (I32, [I32, P, P, P, I64, I64, I64, I64, I64, I64, P]),
+    "vgx_rope_rotate_dyn": (I32, [I32, P, P, I64, I64, I64, I64, I64, P, I64, P, I64, I32, P]),
+    "vgx_argmax": (I32, [P, I64, I64, I64, P, P]),
+    "vgx_sample_topk_workspace_bytes": (I64, [I64, I64]),
+    "vgx_sample_topk": (I32, [P, I64, I64, I64, I64, F, P, P, P, I64, P]),
     "vgx_attn_decode_noalloc": (I32, [I32, P, I64, P, I32, P, I64, I32, I64, P, I64, I64, I64, I64, F, P]),
     "vgx_attn_prefill": (I32, [I32, I32, I32, P, I32, I64, I64, I64, F, P]),
     "vgx_rmsnorm": (I32, [P, I64, P, P, I64, I64, I64, F, P]),

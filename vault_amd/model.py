@@ -81,14 +81,19 @@ class StepIO:
         self.i = 0
 
     def write(self, ids: torch.Tensor, slot: int, row: int, sink: int, n_cur: int) -> None:
+        """Host ids travel with the step words; device ids (e.g. the previous step's argmax) are
+        copied on the device after them, so no host read is needed."""
         k = self.i % self.RING
         self.i += 1
         if self.events[k] is not None:
             self.events[k].synchronize()
         h = self.host[k]
         h[:16].view(torch.int32).copy_(torch.tensor([slot, row, sink, n_cur], dtype=torch.int32))
-        h[64:].view(torch.int64).copy_(ids)
+        if not ids.is_cuda:
+            h[64:].view(torch.int64).copy_(ids)
         self.dev.copy_(h, non_blocking=True)
+        if ids.is_cuda:
+            self.ids.copy_(ids.to(torch.int64), non_blocking=True)
         ev = torch.cuda.Event()
         ev.record()
         self.events[k] = ev
@@ -115,20 +120,23 @@ class VAULTv3State:
         self.k_sink_raw, self.k_sink_rot, self.v_sink = z(self.sink_cap), z(self.sink_cap), z(self.sink_cap)
         self.k_seg_raw, self.k_seg_rot, self.v_seg = z(M_cap), z(M_cap), z(M_cap)
         self._seg_tmp_k, self._seg_tmp_v = z(M_cap), z(M_cap)
-        # segment memory bookkeeping (batch 1)
-        self.tok_prev = np.zeros((batch, W), dtype=np.int64)
-        self.tok_cur = np.zeros((batch, W), dtype=np.int64)
-        self.seg_prev_ids = np.zeros((batch, W), dtype=np.int64)
-        self.seg_cur_ids = np.zeros((batch, W), dtype=np.int64)
-        self.sc_prev = torch.zeros(W, dtype=torch.float32, device=self.device)
-        self.sc_cur = torch.zeros(W, dtype=torch.float32, device=self.device)
-        self.seg_id_offset = 0
-        self.cur_seg_id = 0
-        self.seg_len = 0
-        self.mem_pos = torch.empty(0, dtype=torch.long)
-        self.mem_score = torch.empty(0, dtype=torch.float32)
-        self.mem_tok = torch.empty(0, dtype=torch.long)
-        self.mem_seg = torch.empty(0, dtype=torch.long)
+        # Token and segment-id rings, segmenter state and the segment bank live on the device: the
+        # decode step updates them (vgx_seg_step) and the chunk boundary merges the bank
+        # (vgx_seg_evict) without a host round trip.  Host views below read them (a synchronisation).
+        dev = self.device
+        self.tok_prev = torch.zeros(batch, W, dtype=torch.int32, device=dev)
+        self.tok_cur = torch.zeros(batch, W, dtype=torch.int32, device=dev)
+        self.seg_prev_ids = torch.zeros(W, dtype=torch.int32, device=dev)
+        self.seg_cur_ids = torch.zeros(W, dtype=torch.int32, device=dev)
+        self.sc_prev = torch.zeros(W, dtype=torch.float32, device=dev)
+        self.sc_cur = torch.zeros(W, dtype=torch.float32, device=dev)
+        self.ctrl = torch.zeros(ops.L.SEG_WORDS, dtype=torch.int32, device=dev)     # VGX_SEG_* words
+        self.bank_pos = torch.zeros(M_cap, dtype=torch.int64, device=dev)
+        self.bank_score = torch.zeros(M_cap, dtype=torch.float32, device=dev)
+        self.bank_tok = torch.zeros(M_cap, dtype=torch.int32, device=dev)
+        self.bank_seg = torch.zeros(M_cap, dtype=torch.int32, device=dev)
+        self.idx_old = torch.zeros(M_cap, dtype=torch.int32, device=dev)
+        self.idx_new = torch.zeros(M_cap, dtype=torch.int32, device=dev)
         fd = max(1, len(cfg.seg_layers) * cfg.d_model)
         self.ema_ready = False
         self.seg_feat_ema = torch.zeros(fd, dtype=torch.float32, device=self.device)
@@ -138,6 +146,42 @@ class VAULTv3State:
         self.seg_head_bias_hop1: Optional[torch.Tensor] = None
         self.graphs: "OrderedDict[tuple, tuple]" = OrderedDict()   # captured decode steps
         self._io: Optional[StepIO] = None
+
+    # host views of the device bookkeeping (each reads the device: a synchronisation)
+    def _word(self, i: int) -> int:
+        return int(self.ctrl[i].item())
+
+    @property
+    def mem_cnt(self) -> int:
+        return self._word(ops.L.SEG_MEM_CNT)
+
+    @property
+    def seg_id_offset(self) -> int:
+        return self._word(ops.L.SEG_ID_OFFSET)
+
+    @property
+    def cur_seg_id(self) -> int:
+        return self._word(ops.L.SEG_CUR_ID)
+
+    @property
+    def seg_len(self) -> int:
+        return self._word(ops.L.SEG_LEN)
+
+    @property
+    def mem_pos(self) -> torch.Tensor:
+        return self.bank_pos[:self.mem_cnt].cpu()
+
+    @property
+    def mem_score(self) -> torch.Tensor:
+        return self.bank_score[:self.mem_cnt].cpu()
+
+    @property
+    def mem_tok(self) -> torch.Tensor:
+        return self.bank_tok[:self.mem_cnt].to("cpu", torch.int64)
+
+    @property
+    def mem_seg(self) -> torch.Tensor:
+        return self.bank_seg[:self.mem_cnt].to("cpu", torch.int64)
 
     @property
     def layers(self) -> List[LayerView]:
@@ -178,11 +222,12 @@ class VAULTv3State:
         self.pos = int(pos)
         self.n_pin = int(n_pin)
         self.pin_locked = True
-        i = np.arange(mem_cnt, dtype=np.int64)
-        self.mem_pos = torch.from_numpy(i * 8)
-        self.mem_score = torch.zeros(mem_cnt, dtype=torch.float32)
-        self.mem_tok = torch.zeros(mem_cnt, dtype=torch.long)
-        self.mem_seg = torch.from_numpy(i // 16)
+        i = torch.arange(mem_cnt, dtype=torch.int64)
+        self.bank_pos[:mem_cnt].copy_(i * 8)
+        self.bank_score.zero_()
+        self.bank_tok.zero_()
+        self.bank_seg[:mem_cnt].copy_((i // 16).to(torch.int32))
+        self.ctrl.copy_(torch.tensor([mem_cnt, 0, 0, 0], dtype=torch.int32))
         self.ema_ready = True
 
 
@@ -197,6 +242,7 @@ class VAULTv3ForCausalLM:
         self.tokens = weights.tokens
         vs = self.cfg.vocab_size
         self.tier_lut = self.tokens.tiers if self.tokens is not None else np.zeros(vs, dtype=np.uint8)
+        self.tier_dev = torch.from_numpy(self.tier_lut.copy()).to(self.device) if self.tier_lut.any() else None
         self.use_graphs = True          # replay captured HIP graphs for decode steps
         self._table = None
         self._abs_table = None
@@ -239,9 +285,12 @@ class VAULTv3ForCausalLM:
 
     @torch.no_grad()
     def step(self, token_ids: torch.Tensor, st: VAULTv3State, vault_on: bool = False) -> torch.Tensor:
-        """token_ids: (B,) -> logits (B, V) fp32 on the device.  Mutates ``st``."""
+        """token_ids: (B,) on the host or the device -> logits (B, V) fp32 on the device.  Mutates
+        ``st``.  Device ids (e.g. ops.argmax of the previous logits) are not read on the host once the
+        auto-pin prefix is decided: segmentation and the segment bank are updated on the device."""
         _ = vault_on
-        ids = token_ids.reshape(-1).to("cpu", torch.int64)
+        ids = token_ids.reshape(-1)
+        ids = ids if ids.is_cuda else ids.to("cpu", torch.int64)
         B = ids.numel()
         if B != st.batch:
             raise ValueError("batch size differs from the state's")
@@ -254,14 +303,7 @@ class VAULTv3ForCausalLM:
             self._auto_pin(st, int(ids[0]), pos)
         if c == 0 and pos > 0:
             self._boundary(st, seg_active)
-        st.tok_cur[:, c] = ids.numpy()
-        if seg_active:
-            st.seg_cur_ids[0, c] = st.cur_seg_id
-            st.seg_len += 1
-            if c == W - 1 or self._breaks(int(ids[0]), st.seg_len):
-                st.cur_seg_id += 1
-                st.seg_len = 0
-        if not seg_active or not (pos >= 2 * W and st.mem_pos.numel() > 0):
+        if not seg_active or pos < 2 * W:
             st.seg_bias_mode = 0
             st.seg_bias_active = False
             st.seg_head_bias = None
@@ -371,76 +413,37 @@ class VAULTv3ForCausalLM:
         st.tok_prev, st.tok_cur = st.tok_cur, st.tok_prev
         st.sc_prev, st.sc_cur = st.sc_cur, st.sc_prev
         st.seg_prev_ids, st.seg_cur_ids = st.seg_cur_ids, st.seg_prev_ids
-        st.cur_seg_id = 0
-        st.seg_len = 0
+        st.ctrl[ops.L.SEG_CUR_ID:ops.L.SEG_LEN + 1].zero_()
         if pos >= 2 * W:
             self._refresh_prefix(st, seg_active)
 
     def _refresh_prefix(self, st: VAULTv3State, seg_active: bool) -> None:
-        """Segment keys at positions [-M, 0), sinks at [-(M+S), -M) (src/vault_v3_model.py:1842-1856)."""
-        M = int(st.mem_pos.numel()) if seg_active else 0
+        """Segment keys at positions [-M, 0), sinks at [-(M+S), -M) (src/vault_v3_model.py:1842-1856),
+        with the bank count M read on the device."""
         S = st.n_pin
-        if M > 0:
-            ops.rope_rotate(self._flat(st.k_seg_raw)[:, :M], self._flat(st.k_seg_rot)[:, :M], self._rows(-M),
-                            self.cfg.head_dim)
-        if S > 0:
-            ops.rope_rotate(self._flat(st.k_sink_raw)[:, :S], self._flat(st.k_sink_rot)[:, :S],
-                            self._rows(-(M + S)), self.cfg.head_dim)
+        D = self.cfg.head_dim
+        dyn = st.ctrl[ops.L.SEG_MEM_CNT:ops.L.SEG_MEM_CNT + 1]
+        if seg_active:
+            ops.rope_rotate_dyn(self._flat(st.k_seg_raw), self._flat(st.k_seg_rot), self._rows(0), D, dyn, 0, True)
+            if S > 0:
+                ops.rope_rotate_dyn(self._flat(st.k_sink_raw)[:, :S], self._flat(st.k_sink_rot)[:, :S], self._rows(0),
+                                    D, dyn, -S, False)
+        elif S > 0:
+            ops.rope_rotate(self._flat(st.k_sink_raw)[:, :S], self._flat(st.k_sink_rot)[:, :S], self._rows(-S), D)
 
     def _evict(self, st: VAULTv3State, ev: int) -> None:
         """Segment-memory update for the evicted chunk `ev` (src/vault_v3_model.py:1865-1921;
-        runtime/vault3.c:1833-1915): quarantine, per-segment max with the -1e-6 * (seg id mod 16384)
-        tie-break, exact top-B merge ordered by (score desc, position asc), chronological compaction."""
-        W = self.cfg.window
-        sc = st.sc_prev.to("cpu", torch.float32).numpy().copy()
-        seg_ids = st.seg_prev_ids[0]
-        bad = sc <= -1.0e29
-        if bad.any():
-            bad_seg = np.zeros(int(seg_ids.max()) + 1, dtype=bool)
-            bad_seg[seg_ids[bad]] = True
-            sc[bad_seg[seg_ids]] = np.float32(-1.0e30)
-            st.sc_prev.copy_(torch.from_numpy(sc))
-        n_loc = int(seg_ids.max()) + 1
-        mx = np.full(n_loc, -np.inf, dtype=np.float32)
-        np.maximum.at(mx, seg_ids, sc)
-        full_seg = seg_ids + st.seg_id_offset
-        cand_all = (mx[seg_ids] - np.float32(1e-6) * (full_seg % 16384).astype(np.float32)).astype(np.float32)
-        st.seg_id_offset += n_loc
-        t0 = st.n_pin if ev == 0 else 0
-        if t0 >= W:
-            return
-        t = np.arange(t0, W)
-        ok = cand_all[t0:] > -1.0e29
-        c_pos = ev * W + t[ok]
-        c_sc = cand_all[t0:][ok]
-        c_src = t[ok]
-        c_tok = st.tok_prev[0, t0:][ok]
-        c_seg = full_seg[t0:][ok]
-        M = int(st.mem_pos.numel())
-        all_pos = np.concatenate([st.mem_pos.numpy(), c_pos])
-        all_sc = np.concatenate([st.mem_score.numpy(), c_sc]).astype(np.float32)
-        if all_pos.size <= st.seg_budget:
-            win = np.arange(all_pos.size)
-        else:
-            win = np.sort(np.argsort(-all_sc, kind="stable")[:st.seg_budget])
-        keep = win[win < M]
-        add = win[win >= M] - M
-        nk, na = keep.size, add.size
-        # compaction: new bank = old[keep] ++ prev_chunk[c_src[add]], built out of place then swapped in
+        runtime/vault3.c:1833-1915), all on the device: quarantine, per-segment max with the
+        -1e-6 * (seg id mod 16384) tie-break, exact top-B merge ordered by (score desc, position
+        asc) (vgx_seg_evict), then the chronological compaction of the bank's keys / values from the
+        old bank and the evicted chunk into the spare bank, which becomes the bank."""
+        ops.seg_evict(st.sc_prev, st.seg_prev_ids, st.tok_prev[0], st.bank_pos, st.bank_score, st.bank_tok,
+                      st.bank_seg, st.ctrl, ev, st.n_pin if ev == 0 else 0, st.seg_budget, st.idx_old, st.idx_new)
         for bank, tmp, src_prev in ((st.k_seg_raw, st._seg_tmp_k, st.kraw_prev), (st.v_seg, st._seg_tmp_v, st.v_prev)):
-            ft = self._flat(tmp)
-            if nk:
-                ops.gather_rows(self._flat(bank), ft[:, :nk], torch.from_numpy(keep.astype(np.int32)))
-            if na:
-                ops.gather_rows(self._flat(src_prev), ft[:, nk:nk + na], torch.from_numpy(c_src[add].astype(np.int32)))
+            ops.gather_rows_masked(self._flat(bank), self._flat(tmp), st.idx_old)
+            ops.gather_rows_masked(self._flat(src_prev), self._flat(tmp), st.idx_new)
         st.k_seg_raw, st._seg_tmp_k = st._seg_tmp_k, st.k_seg_raw
         st.v_seg, st._seg_tmp_v = st._seg_tmp_v, st.v_seg
-        mem_tok = np.concatenate([st.mem_tok.numpy()[keep], c_tok[add]])
-        mem_seg = np.concatenate([st.mem_seg.numpy()[keep], c_seg[add]])
-        st.mem_pos = torch.from_numpy(all_pos[win].astype(np.int64))
-        st.mem_score = torch.from_numpy(all_sc[win])
-        st.mem_tok = torch.from_numpy(mem_tok.astype(np.int64))
-        st.mem_seg = torch.from_numpy(mem_seg.astype(np.int64))
 
     # ------------------------------------------------------------------ decode step on the device
     def _decode(self, st: VAULTv3State, ids: torch.Tensor, pos: int, c: int, seg_active: bool) -> torch.Tensor:
@@ -455,17 +458,17 @@ class VAULTv3ForCausalLM:
         eff = W + c if pos >= W else c
         io.write(ids, slot=c, row=eff - self._p0, sink=pos if pos < st.sink_cap else -1, n_cur=c + 1)
         n_sk = st.n_pin if pos >= 2 * W else 0
-        n_seg = int(st.mem_pos.numel()) if (pos >= 2 * W and seg_active) else 0
+        has_seg = pos >= 2 * W and seg_active       # the bank span, its length on the device
         n_prev = W if pos >= W else 0
-        bias_on = bool(n_seg and st.seg_bias_active and st.seg_head_bias is not None)
+        bias_on = bool(has_seg and st.seg_bias_active and st.seg_head_bias is not None)
         ema_first = seg_active and not st.ema_ready
-        spec = (B, n_sk, n_seg, n_prev, seg_active, ema_first)
+        spec = (B, n_sk, has_seg, n_prev, seg_active, ema_first)
         if bias_on or not self.use_graphs:
             return self._decode_launch(st, spec, bias_on)
         self._size_workspace(st)
         key = spec + tuple(t.data_ptr() for t in (st.k_prev, st.k_cur, st.v_prev, st.v_cur, st.kraw_cur, st.k_seg_rot,
-                                                   st.v_seg, st.sc_cur, self._table, self.ws.buf,
-                                                   ops.gemm_workspace(self.device).buf))
+                                                   st.v_seg, st.sc_cur, st.tok_cur, st.seg_cur_ids, self._table,
+                                                   self.ws.buf, ops.gemm_workspace(self.device).buf))
         ent = st.graphs.get(key)
         if ent is None:
             # No destructor may run HIP calls while the stream captures: collect garbage now and keep
@@ -523,12 +526,19 @@ class VAULTv3ForCausalLM:
     def _decode_launch(self, st: VAULTv3State, spec: tuple, bias_on: bool) -> torch.Tensor:
         """Every kernel of one decode step (embedding -> 28 layers -> scorer -> LM head) for the chunk
         configuration ``spec``; position-dependent values are read from the step buffer."""
-        B, n_sk, n_seg, n_prev, seg_active, ema_first = spec
+        B, n_sk, has_seg, n_prev, seg_active, ema_first = spec
         cfg, w = self.cfg, self.w
         H, G, D, d = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_model
         HD, GD = H * D, G * D
         io = st.step_io()
         step, n_cur = io.step, io.step[ops.L.STEP_N_CUR:ops.L.STEP_N_CUR + 1]
+        # token ring and segmenter (device words), then the embedding rows
+        ops.seg_step(io.ids, step, st.tok_cur, st.seg_cur_ids if seg_active else None, st.ctrl if seg_active else None,
+                     self.tier_dev, cfg.seg_min, cfg.seg_max)
+        # bank span: its length is the device count; with a host-supplied bias, the host count (the bias
+        # vector covers the bank's entries)
+        m_dev = st.ctrl[ops.L.SEG_MEM_CNT:ops.L.SEG_MEM_CNT + 1]
+        n_seg = (st.mem_cnt if bias_on else st.k_seg_rot.shape[3]) if has_seg else 0
         x = ops.embed(w.embed, io.ids, pad_row=0)                              # [B, d]
         # rows [0, B) receive the scorer features, rows [B, 2B) the habituated ones (one LayerNorm launch)
         feats = torch.empty(2 * B, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device) \
@@ -571,7 +581,10 @@ class VAULTv3ForCausalLM:
             if n_seg:
                 bias = self._seg_bias(st, li, n_seg) if bias_on else None
                 bspan = len(spans)
-                spans.append((st.k_seg_rot[li][:, :, :n_seg], st.v_seg[li][:, :, :n_seg]))
+                if bias_on:
+                    spans.append((st.k_seg_rot[li][:, :, :n_seg], st.v_seg[li][:, :, :n_seg]))
+                else:
+                    spans.append((st.k_seg_rot[li], st.v_seg[li], m_dev))
             if n_prev:
                 spans.append((st.k_prev[li], st.v_prev[li]))
             spans.append((st.k_cur[li], st.v_cur[li], n_cur))
@@ -618,7 +631,7 @@ class VAULTv3ForCausalLM:
         if seg_active:
             feats = torch.empty(2 * N, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device)
         n_sk = st.n_pin if ci >= 2 else 0
-        n_seg = int(st.mem_pos.numel()) if (seg_active and ci >= 2) else 0
+        n_seg = st.mem_cnt if (seg_active and ci >= 2) else 0
         n_prev = W if ci >= 1 else 0
         table, trs = self._rows(W if ci >= 1 else 0), D
         ao = torch.empty(N, H, D, dtype=torch.float32, device=self.device)
@@ -738,10 +751,10 @@ class VAULTv3ForCausalLM:
             ops.qlinear_swiglu(lw.wgu, x, out=hbuf, norm=(lw.ln2, cfg.rms_eps))
             ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
         if st is not None:
-            ids_np = input_ids.to("cpu", torch.int64).numpy()
-            st.tok_cur[:, :cnt] = ids_np[:, last * W:L]
+            ids32 = input_ids.to(dev, torch.int32)
+            st.tok_cur[:, :cnt].copy_(ids32[:, last * W:L])
             if last >= 1:
-                st.tok_prev[:, :] = ids_np[:, (last - 1) * W:last * W]
+                st.tok_prev.copy_(ids32[:, (last - 1) * W:last * W])
             st.pos = L
             if L >= 2 * W:
                 self._refresh_prefix(st, seg_active=False)
@@ -813,16 +826,20 @@ class VAULTv3ForCausalLM:
             if ci > 0:
                 self._boundary(st, seg_active)
             ch = ids_all[r0:r1]
-            st.tok_cur[0, :clen] = ch.numpy()
+            st.tok_cur[0, :clen].copy_(ch.to(torch.int32))
             if seg_active:
+                # the chunk's segment ids (host rule, the prompt is on the host), then the open
+                # segment's id and length as the device segmenter continues from them
+                seg = np.empty(clen, dtype=np.int32)
                 s_loc, slen = 0, 0
                 for j in range(clen):
-                    st.seg_cur_ids[0, j] = s_loc
+                    seg[j] = s_loc
                     slen += 1
                     if j == W - 1 or self._breaks(int(ch[j]), slen):
                         s_loc += 1
                         slen = 0
-                st.cur_seg_id, st.seg_len = s_loc, slen
+                st.seg_cur_ids[:clen].copy_(torch.from_numpy(seg))
+                st.ctrl[ops.L.SEG_CUR_ID:ops.L.SEG_LEN + 1].copy_(torch.tensor([s_loc, slen], dtype=torch.int32))
             x = ops.embed(self.w.embed, ch.to(self.device), pad_row=0)
             x, feats = self._layers(x, st, pos=r0, seg_active=seg_active)
             if seg_active:

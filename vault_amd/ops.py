@@ -496,3 +496,77 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
         L.check(lib.vgx_attn_prefill(KV_DTYPES[kvdt], qd, od, arr, len(part), H, G, D, scale,
                                      _stream(part[0]["q"].device)),
                 "vgx_attn_prefill")
+
+
+# ------------------------------------------------------------------------------------------
+# segment bank and token selection
+# ------------------------------------------------------------------------------------------
+
+def seg_step(ids: torch.Tensor, step: torch.Tensor, tok_cur: torch.Tensor, seg_cur: Optional[torch.Tensor],
+             ctrl: Optional[torch.Tensor], tiers: Optional[torch.Tensor], seg_min: int, seg_max: int) -> None:
+    """Ring and segmenter bookkeeping of one decode step (vgx_seg_step).  ids int64 [B] and step: device
+    words; tok_cur int32 [B, W]; seg_cur int32 [W] and ctrl int32 [VGX_SEG_WORDS] for batch 1 with
+    segment memory, else None; tiers uint8 [V] or None."""
+    B, W = tok_cur.shape
+    L.check(L.load().vgx_seg_step(ids.data_ptr(), B, step.data_ptr(), tok_cur.data_ptr(), tok_cur.stride(0),
+                                  _ptr(seg_cur), _ptr(ctrl), _ptr(tiers), tiers.numel() if tiers is not None else 0,
+                                  seg_min, seg_max, W, _stream(tok_cur.device)), "vgx_seg_step")
+
+
+def seg_evict(sc_prev, seg_prev, tok_prev, mem_pos, mem_score, mem_tok, mem_seg, ctrl, ev: int, t0: int,
+              budget: int, idx_old, idx_new) -> None:
+    """The segment-bank merge at a chunk boundary (vgx_seg_evict), all on the device."""
+    W = sc_prev.numel()
+    L.check(L.load().vgx_seg_evict(sc_prev.data_ptr(), seg_prev.data_ptr(), tok_prev.data_ptr(), W, mem_pos.data_ptr(),
+                                   mem_score.data_ptr(), mem_tok.data_ptr(), mem_seg.data_ptr(), ctrl.data_ptr(), ev,
+                                   t0, budget, idx_old.data_ptr(), idx_new.data_ptr(), _stream(sc_prev.device)),
+            "vgx_seg_evict")
+
+
+def gather_rows_masked(src: torch.Tensor, dst: torch.Tensor, idx: torch.Tensor) -> None:
+    """dst[:, j] = src[:, idx[j]] where idx[j] >= 0 (other rows untouched); [O, n, D] views."""
+    O, n_src, D = src.shape
+    assert dst.shape[0] == O and dst.shape[2] == D and idx.numel() == dst.shape[1] and idx.dtype == torch.int32
+    L.check(L.load().vgx_gather_rows_masked(KV_DTYPES[src.dtype], src.data_ptr(), dst.data_ptr(), idx.data_ptr(),
+                                            idx.numel(), n_src, O, src.stride(0), dst.stride(0), D,
+                                            _stream(src.device)), "vgx_gather_rows_masked")
+
+
+def rope_rotate_dyn(src: torch.Tensor, dst: torch.Tensor, table0: torch.Tensor, table_rstride: int,
+                    dyn: torch.Tensor, row_base: int, limit_rows: bool) -> None:
+    """Row i of every outer slice rotated by the table row of position (i + row_base - *dyn), table0
+    being the row of position 0 (vgx_rope_rotate_dyn); rows i >= *dyn skipped with limit_rows."""
+    O, n, D = src.shape
+    for t in (src, dst):
+        if t.stride(2) != 1 or t.stride(1) != D:
+            raise ValueError("rows must be contiguous")
+    L.check(L.load().vgx_rope_rotate_dyn(KV_DTYPES[src.dtype], src.data_ptr(), dst.data_ptr(), O, src.stride(0),
+                                         dst.stride(0), n, D, table0.data_ptr(), table_rstride, dyn.data_ptr(),
+                                         row_base, 1 if limit_rows else 0, _stream(src.device)), "vgx_rope_rotate_dyn")
+
+
+def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """[B, V] fp32 -> int64 [B] on the device (vgx_argmax; the first index on ties)."""
+    _need(logits, torch.float32, "logits")
+    B, V = logits.shape
+    if logits.stride(1) != 1:
+        raise ValueError("logits rows must be contiguous")
+    out = torch.empty(B, dtype=torch.int64, device=logits.device) if out is None else out
+    L.check(L.load().vgx_argmax(logits.data_ptr(), logits.stride(0), B, V, out.data_ptr(), _stream(logits.device)),
+            "vgx_argmax")
+    return out
+
+
+def sample_topk(logits: torch.Tensor, k: int, temp: float, rng: torch.Tensor,
+                out: Optional[torch.Tensor] = None, ws: Optional["Workspace"] = None) -> torch.Tensor:
+    """Top-k sampling per row with the rows' xorshift64 states ``rng`` (uint64 as int64 [B], updated in
+    place) -> int64 [B] on the device (vgx_sample_topk)."""
+    _need(logits, torch.float32, "logits")
+    B, V = logits.shape
+    lib = L.load()
+    out = torch.empty(B, dtype=torch.int64, device=logits.device) if out is None else out
+    need = int(lib.vgx_sample_topk_workspace_bytes(B, V))
+    buf = (ws or Workspace(logits.device)).get(need)
+    L.check(lib.vgx_sample_topk(logits.data_ptr(), logits.stride(0), B, V, int(k), float(temp), rng.data_ptr(),
+                                out.data_ptr(), buf.data_ptr(), buf.numel(), _stream(logits.device)), "vgx_sample_topk")
+    return out
