@@ -8,9 +8,15 @@ window (W=1024), segment scorer on, batch 1 (``--batch`` for more; segment memor
 batch > 1 as in the reference).  The state is seeded where a long stream leaves it (fixed-size
 state), weights are drawn directly as quantized blocks from a seeded generator.
 
-Prints one JSON line: tokens/s, plus the roofline of the dominant kernel (the fused gate/up SwiGLU
-Q4_0 GEMV, 28 launches per token), secondary kernel figures (Q8_0/Q4_0 GEMV at the model's shapes,
-batched bf16 decode attention at 3584 keys) and the reference C runtime timed on the host cores.
+The timed steps cross a chunk boundary (segment-memory merge, bank compaction, ring swap and
+re-rotations inside the timed region); both ring configurations' step graphs are captured during
+set-up.
+
+Prints one JSON line: tokens/s, plus the roofline of the step's largest kernel by time (batch-1 decode
+attention over the step's four KV spans, fp32 KV, with its split merge), secondary kernel figures
+(the fused gate/up SwiGLU Q4_0 GEMV, Q8_0/Q4_0 GEMV at the model's shapes, batched bf16 decode
+attention at 3584 keys, prefill attention and GEMMs, batch-32 decode) and the reference C runtime
+timed on the host cores.
 """
 from __future__ import annotations
 
@@ -51,13 +57,34 @@ def build_model(cfg, dev, kv_dtype, seed: int = 1234):
     return VAULTv3ForCausalLM(w, kv_dtype=kv_dtype), tensors
 
 
-def seeded_state(model, batch: int, seed: int = 99):
+def seeded_state(model, batch: int, seed: int = 99, pos: int = CTX_POS, st=None):
     import torch
-    st = model.new_state(batch, seg_budget=None if batch == 1 else 0)
+    if st is None:
+        st = model.new_state(batch, seg_budget=None if batch == 1 else 0)
     gen = torch.Generator().manual_seed(seed)
-    st.seed_long_context(CTX_POS, N_PIN, MEM_CNT if batch == 1 else 0,
+    st.seed_long_context(pos, N_PIN, MEM_CNT if batch == 1 else 0,
                          lambda li, name, shape: torch.randn(shape, generator=gen))
     return st
+
+
+def boundary_seeded_state(model, batch: int, steps: int, warmup: int):
+    """A seeded state whose timed steps cross a chunk boundary (the segment-memory merge, the bank
+    compaction, the ring swap and re-rotations run inside the timed region), with both ring
+    configurations' step graphs already captured.  Set-up: seed two positions before the chunk
+    boundary at 99,328 and step across it (the first step's graph and the graph after the swap are
+    captured there), then seed the same buffers again so that boundary 100,352 falls in the middle of
+    the timed steps.  Returns (state, first decoded position)."""
+    import torch
+    W = model.cfg.window
+    b2 = (CTX_POS // W + 1) * W                   # 100,352
+    st = seeded_state(model, batch, pos=b2 - W - 2)
+    g = torch.Generator().manual_seed(77)
+    for t in torch.randint(0, model.cfg.vocab_size, (4, batch), generator=g):
+        model.step(t, st)
+    torch.cuda.synchronize()
+    p0 = max(2 * W, b2 - warmup - steps // 2)
+    seeded_state(model, batch, pos=p0, st=st)
+    return st, p0
 
 
 def _events():
@@ -105,7 +132,40 @@ def time_decode(model, st, steps: int, warmup: int, batch: int, seed: int = 5):
     return dt
 
 
-def dominant_kernel(model, rounds: int = 20):
+ATTN_LENS = (512, 1024, 1024, 1024)        # sinks | segment memory | previous window | current window
+ATTN_COPIES = 40                           # 40 x 7.34 MB of KV: beyond the 256 MB last-level cache
+ATTN_ALGO_BYTES = sum(ATTN_LENS) * 2 * 128 * 4 * 2 + 2 * 12 * 128 * 4   # K and V once, q and out
+
+
+def attention_kernel(dev, reps: int = 20):
+    """The roofline kernel: batch-1 decode attention of the step, fp32 KV (the state dtype), 12 query /
+    2 KV heads, D = 128, 3584 keys in the step's four spans (512 sinks | 1024 segment slots | 1024
+    previous | 1024 current window).  One call = attn_decode_kernel over 56 key splits x 2 KV groups +
+    attn_merge_kernel.  Algorithmic bytes per call: K and V once (7,340,032 B) + q + out = 7,352,320 B.
+    A graph replays one call over each of ATTN_COPIES KV copies (as the 28 layers of a step stream
+    theirs); time per call from HIP events on the replay stream."""
+    import torch
+    from vault_amd import ops
+    B, H, G, D = 1, 12, 2, 128
+    g = torch.Generator().manual_seed(12)
+    base = [(torch.randn(B, G, n, D, generator=g).to(dev), torch.randn(B, G, n, D, generator=g).to(dev))
+            for n in ATTN_LENS]
+    sets = _kv_copies(base, ATTN_COPIES)
+    q = torch.randn(B, H, D, generator=g).to(dev)
+    out = torch.empty(B, H, D, device=dev)
+    ws = ops.Workspace(dev)
+
+    def run():
+        for sp in sets:
+            ops.attn_decode(q, sp, out=out, ws=ws)
+    us = graph_time_us(run, len(sets), reps=reps)
+    return {"kernel": "attn_decode_kernel<fp32 KV, 6 heads per KV group, D/16 = 8, 4 waves, 4 keys per DPP row> "
+                      "+ attn_merge_kernel (batch 1, 12 q / 2 KV heads, D = 128, 3584 keys)",
+            "calls": reps * len(sets), "avg_us": us, "bytes_per_launch": ATTN_ALGO_BYTES,
+            "gbs": ATTN_ALGO_BYTES / us / 1e3}
+
+
+def gateup_kernel(model, rounds: int = 20):
     """Fused gate/up SwiGLU Q4_0 GEMV (2 x 8960 x 1536) over the 28 layers' weights in turn, as in the
     step (433 MB of weights, beyond the 256 MB last-level cache); HIP events on the launch stream."""
     import torch
@@ -257,10 +317,11 @@ def batched_decode(model, batch: int = 32, steps: int = 16, warmup: int = 4):
     import torch
     from vault_amd.model import VAULTv3ForCausalLM
     m2 = VAULTv3ForCausalLM(model.w, kv_dtype=torch.bfloat16)
-    st = seeded_state(m2, batch)
+    st, _ = boundary_seeded_state(m2, batch, steps, warmup)
     dt = time_decode(m2, st, steps, warmup, batch)
     del st
-    return {"config": f"batch {batch}, bf16 KV, 100K context (512 sinks + 2048 window)",
+    return {"config": f"batch {batch}, bf16 KV, 100K context (512 sinks + 2048 window), timed steps across "
+                      f"the chunk boundary at 100,352",
             "tokens_per_s": round(batch * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 3)}
 
 
@@ -315,36 +376,41 @@ def cpu_baseline(cfg, tensors, budget_s: float = 15.0):
         n += 1
     dt = time.perf_counter() - t0
     rt.close()
-    return {"value": round(n / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "reference",
+    return {"value": round(n / dt, 3), "unit": "tokens/s", "cores": threads, "host_cores": os.cpu_count(),
+            "host_cores_usable": len(os.sched_getaffinity(0)), "kind": "reference",
             "sample": f"{n} decode steps of the same 1.54B hybrid-Q4_0 model from position {CTX_POS + 1} "
                       f"(512 sinks, 1024 segment slots, fp32 state) with runtime/vault3.c v3_step, "
-                      f"{threads} threads"}
+                      f"{threads} threads on a host with {os.cpu_count()} cores ({len(os.sched_getaffinity(0))} "
+                      f"usable by this process)"}
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "traffic_gateup_swiglu_q4_gemv_1p5b.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "traffic_attn_decode_fp32_b1_3584.md")
 COPY_BYTES = 256 << 20      # calibration stream for the PMC byte counters (read and written once)
 
 
-def pmc_launches(dev, rounds: int = 8) -> None:
-    """The launches the PMC runs count: the dominant kernel eagerly over the 28 layers' weights
-    (``rounds`` times) and a plain streaming kernel that reads and writes COPY_BYTES once (torch's
-    elementwise negation, a name no other launch here has), ``rounds`` times."""
+def pmc_launches(dev, rounds: int = 4) -> None:
+    """The launches the PMC runs count: the roofline call (attention + merge) eagerly over the
+    ATTN_COPIES KV copies (``rounds`` times) and a plain streaming kernel that reads and writes
+    COPY_BYTES once (torch's elementwise negation, a name no other launch here has), ``rounds`` times."""
     import torch
-    cfg = model_config()
-    model, _ = build_model(cfg, dev, torch.float32)
     from vault_amd import ops
-    x = torch.randn(1, cfg.d_model, device=dev)
-    h = torch.empty(1, cfg.d_ff, device=dev)
-    lnw = model.w.layers[0].ln2
+    B, H, G, D = 1, 12, 2, 128
+    g = torch.Generator().manual_seed(12)
+    base = [(torch.randn(B, G, n, D, generator=g).to(dev), torch.randn(B, G, n, D, generator=g).to(dev))
+            for n in ATTN_LENS]
+    sets = _kv_copies(base, ATTN_COPIES)
+    q = torch.randn(B, H, D, generator=g).to(dev)
+    out = torch.empty(B, H, D, device=dev)
+    ws = ops.Workspace(dev)
     src = torch.randn(COPY_BYTES // 4, device=dev)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     for _ in range(rounds):
-        for lw in model.w.layers:
-            ops.qlinear_swiglu(lw.wgu, x, out=h, norm=(lnw, cfg.rms_eps))
+        for sp in sets:
+            ops.attn_decode(q, sp, out=out, ws=ws)
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
-    _log(f"pmc launches done: {rounds} x {len(model.w.layers)} gate/up GEMVs, {rounds} streams of {COPY_BYTES} B")
+    _log(f"pmc launches done: {rounds} x {len(sets)} attention calls, {rounds} streams of {COPY_BYTES} B")
 
 
 def _pmc_avg(csv_path: str, counter: str, name_part: str) -> tuple[float, int]:
@@ -360,28 +426,31 @@ def _pmc_avg(csv_path: str, counter: str, name_part: str) -> tuple[float, int]:
 
 
 def pmc_report(fetch_csv: str, write_csv: str) -> None:
-    """Markdown summary of the two PMC runs: per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the
-    dominant kernel and of the calibration copy, the copy's bytes / counter factor, and the scaled
-    HBM traffic per launch of the dominant kernel (the figure ``roofline.traffic`` reports)."""
-    kern, copy = "gemv1_kernel<9, 2, true", "neg_kernel"
-    fk, nk = _pmc_avg(fetch_csv, "FETCH_SIZE", kern)
+    """Markdown summary of the two PMC runs: per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the two
+    kernels of the roofline call and of the calibration copy, the copy's bytes / counter factor, and
+    the scaled HBM traffic per call (the figure ``roofline.traffic`` reports)."""
+    kerns = (("attn_decode_kernel<0, 6, 8, 4, 4, 0>", "split attention"), ("attn_merge_kernel", "split merge"))
+    copy = "neg_kernel"
     fc, nc = _pmc_avg(fetch_csv, "FETCH_SIZE", copy)
-    wk, _ = _pmc_avg(write_csv, "WRITE_SIZE", kern)
     wc, _ = _pmc_avg(write_csv, "WRITE_SIZE", copy)
     f_scale, w_scale = COPY_BYTES / (fc * 1024), COPY_BYTES / (wc * 1024)
-    traffic = fk * 1024 * f_scale + wk * 1024 * w_scale
-    algo = 15_524_864
-    print(f"| dispatches | kernel | FETCH_SIZE KiB | WRITE_SIZE KiB |\n|---|---|---|---|\n"
-          f"| {nk} | `{kern}...>` (gate/up SwiGLU Q4_0 GEMV) | {fk:.1f} | {wk:.1f} |\n"
+    rows, traffic = [], 0.0
+    for name, what in kerns:
+        fk, nk = _pmc_avg(fetch_csv, "FETCH_SIZE", name)
+        wk, _ = _pmc_avg(write_csv, "WRITE_SIZE", name)
+        traffic += fk * 1024 * f_scale + wk * 1024 * w_scale
+        rows.append(f"| {nk} | `{name}` ({what}) | {fk:.1f} | {wk:.1f} |")
+    algo = ATTN_ALGO_BYTES
+    print("| dispatches | kernel | FETCH_SIZE KiB | WRITE_SIZE KiB |\n|---|---|---|---|\n" + "\n".join(rows) + "\n"
           f"| {nc} | torch `neg` elementwise kernel ({COPY_BYTES} B read + written) | {fc:.1f} | {wc:.1f} |\n\n"
           f"copy calibration: fetch factor {f_scale:.4f}, write factor {w_scale:.4f} (bytes / (KiB x 1024))\n\n"
-          f"algorithmic bytes per launch: {algo}\n\n"
+          f"algorithmic bytes per call: {algo}\n\n"
           f"traffic_bytes_per_launch: {traffic:.0f}\n\n"
           f"traffic / algorithmic: {traffic / algo:.3f}")
 
 
 def measured_traffic():
-    """HBM bytes per launch of the dominant kernel from the committed PMC summary, or None."""
+    """HBM bytes per call of the roofline kernels from the committed PMC summary, or None."""
     import re
     try:
         with open(TRAFFIC_PROFILE) as f:
@@ -403,7 +472,7 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for per-kernel profiles of the step)")
     ap.add_argument("--figures", choices=("gemv", "attn_decode", "attn_decode_b1", "attn_prefill", "gemm_prefill",
-                                          "dominant", "decode_batch32"),
+                                          "roofline", "gateup", "decode_batch32"),
                     help="only one set of kernel figures, printed as JSON (for per-kernel profiles)")
     ap.add_argument("--pmc", action="store_true",
                     help="only run the launches the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count")
@@ -427,12 +496,15 @@ def main() -> int:
     if args.pmc:
         pmc_launches(dev)
         return 0
-    if args.figures == "dominant":
+    if args.figures == "roofline":
         # the roofline measurement of the default run alone (its launches, for a kernel trace)
+        print(json.dumps({"roofline": attention_kernel(dev)}), flush=True)
+        return 0
+    if args.figures == "gateup":
         cfg = model_config()
         model, tensors = build_model(cfg, dev, torch.float32)
         del tensors
-        print(json.dumps({"dominant": dominant_kernel(model)}), flush=True)
+        print(json.dumps({"gateup_gemv": gateup_kernel(model)}), flush=True)
         return 0
     if args.figures == "decode_batch32":
         cfg = model_config()
@@ -449,8 +521,9 @@ def main() -> int:
     kv_dtype = torch.float32 if args.kv == "fp32" else torch.bfloat16
     cfg = model_config()
     model, tensors = build_model(cfg, dev, kv_dtype)
-    st = seeded_state(model, args.batch)
-    _log(f"model and state ready (state {st.nbytes() / 2**20:.0f} MiB); timing {args.steps} steps")
+    st, p0 = boundary_seeded_state(model, args.batch, args.steps, args.warmup)
+    _log(f"model and state ready (state {st.nbytes() / 2**20:.0f} MiB); timing {args.steps} steps from "
+         f"position {p0 + args.warmup}")
     dt = time_decode(model, st, args.steps, args.warmup, args.batch)
     tok_s = args.batch * args.steps / dt
     ms = dt * 1e3 / args.steps
@@ -460,9 +533,9 @@ def main() -> int:
         print(json.dumps({"metric": "decode tokens/s (decode-only profile run)", "value": round(tok_s, 2),
                           "unit": "tokens/s", "ms_per_step": round(ms, 4), "steps": args.steps}), flush=True)
         return 0
-    dom = dominant_kernel(model)
-    _log(f"dominant kernel: {dom['avg_us']:.2f} us, {dom['gbs']:.0f} GB/s")
-    kernels = {}
+    dom = attention_kernel(dev)
+    _log(f"roofline kernel (attention + merge): {dom['avg_us']:.2f} us, {dom['gbs']:.0f} GB/s")
+    kernels = {"gateup_gemv": gateup_kernel(model)}
     if not args.no_kernels:
         kernels["gemv"] = gemv_figures(dev)
         kernels["attn_decode"] = attn_figures(dev)
@@ -479,8 +552,9 @@ def main() -> int:
             _log(f"cpu baseline: {cpu['value']} tokens/s on {cpu['cores']} threads")
 
     # algorithmic bytes of one decode step (weights + LM head + scorer + KV read)
-    n_keys_avg = N_PIN + (MEM_CNT if args.batch == 1 else 0) + cfg.window + (CTX_POS % cfg.window) + \
-        args.warmup + (args.steps + 1) / 2
+    timed = range(p0 + args.warmup, p0 + args.warmup + args.steps)
+    n_keys_avg = N_PIN + (MEM_CNT if args.batch == 1 else 0) + cfg.window + \
+        sum(p % cfg.window + 1 for p in timed) / max(1, args.steps)
     kv_bytes = cfg.n_layers * n_keys_avg * 2 * cfg.head_dim * 2 * (4 if args.kv == "fp32" else 2) * args.batch
     step_bytes = model.w.layer_stream_bytes() + model.w.embed.stream_bytes + kv_bytes + \
         (model.w.scorer.w1.stream_bytes if (model.w.scorer is not None and args.batch == 1) else 0)
@@ -490,7 +564,8 @@ def main() -> int:
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32" if args.kv == "fp32" else "f32 (bf16 KV)", "data": "synthetic (seeded random-init weights as quantized blocks, seeded KV state)",
         "config": {"workload": "28-layer 1.54B hybrid-Q4_0 decode step at 100K context (512 sinks, 1024 segment KV, "
-                               "2048 window, segment scorer on)", "batch": args.batch, "context": CTX_POS,
+                               "2048 window, segment scorer on), timed steps across the chunk boundary at 100,352",
+                   "batch": args.batch, "context": p0 + args.warmup,
                    "kv_dtype": args.kv, "parallelism": "single GPU"},
         "step_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -10,11 +10,12 @@
 // enter the MFMA as unsigned integers, exact in bf16: Q8_0 as q + 128 (byte ^ 0x80), Q4_0 as the
 // nibble n (16 + n in the tiled kernel).  The activations enter in pieces that a bf16 pair hi + lo
 // (2^-18 relative residual) would leave at 2.4e-6 relative error per output, ten times the one-row
-// GEMV's; so the decode-batch kernel takes three bf16 pieces hi + mid + lo (24 significant bits, the
-// whole fp32 mantissa) and the tiled kernel takes hi = bf16(u) and lo16 = fp16(16 (u - hi)) (19
-// significant bits, 2^-20 relative residual; lo16 overflows only past |u| = 2^21), multiplied
-// by the same weights as exact fp16 integers, its product scaled by 1/16.  With S_b the per-block sum
-// of the pieces, per block the fp32 MFMA result C (= sum_j w_j u_j as pieces) is corrected and scaled:
+// GEMV's; so both kernels take hi = bf16(u) and lo16 = fp16(16 (u - hi)) (19 significant bits, 2^-20
+// relative residual; lo16 overflows only past |u| = 2^21), lo16 multiplied by the same weights divided
+// by 16 as exact fp16 values, the two products added into one accumulator (two MFMAs per block; three
+// bf16 pieces would take three and, in the decode-batch kernel, registers that its occupancy target
+// does not have: spills).  With S_b the per-block sum of the pieces, per block the fp32 MFMA result C
+// (= sum_j w_j u_j as pieces) is corrected and scaled:
 //   acc += d * (C - off * S_b),   off = 128 (Q8_0), 8 (Q4_0; 24 in the tiled kernel),
 // which is the reference's sum_b d_b sum_j q_j x_j at fp32-level accuracy.
 //
@@ -103,9 +104,10 @@ __device__ __forceinline__ uint2 load_a(const uint8_t *__restrict__ W, int64_t r
     return *reinterpret_cast<const uint2 *>(p);
 }
 
-// 8 quant values -> 8 unsigned integers as bf16 (exact): weights 8 lg .. 8 lg + 7 of the block.
-template <int DT>
-__device__ __forceinline__ bf16x8_t a_frag(uint2 w, int lg) {
+// 8 quant values -> 8 unsigned integers as bf16 (exact): weights 8 lg .. 8 lg + 7 of the block, in
+// natural K-slot order; fh (when requested) the same integers divided by 16 as fp16 (exact).
+template <int DT, bool F16 = false>
+__device__ __forceinline__ bf16x8_t a_frag(uint2 w, int lg, f16x8_t *fh = nullptr) {
     uint32_t u[2] = {w.x, w.y};
     if constexpr (DT == VGX_Q8_0) {
         u[0] ^= 0x80808080u;
@@ -115,7 +117,7 @@ __device__ __forceinline__ bf16x8_t a_frag(uint2 w, int lg) {
         u[0] = (u[0] >> sh) & 0x0F0F0F0Fu;
         u[1] = (u[1] >> sh) & 0x0F0F0F0Fu;
     }
-    uint32_t o[4];
+    uint32_t o[4], h[4];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const float f0 = (float)(u[i] & 0xFFu), f1 = (float)((u[i] >> 8) & 0xFFu);
@@ -123,7 +125,12 @@ __device__ __forceinline__ bf16x8_t a_frag(uint2 w, int lg) {
         // small integers: the bf16 is the top half of the fp32 bits, exactly
         o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xFFFF0000u);
         o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xFFFF0000u);
+        if constexpr (F16) {
+            h[2 * i] = pack_f16x2(f0 * 0.0625f, f1 * 0.0625f);
+            h[2 * i + 1] = pack_f16x2(f2 * 0.0625f, f3 * 0.0625f);
+        }
     }
+    if constexpr (F16) *fh = __builtin_bit_cast(f16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
     return __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
@@ -502,8 +509,8 @@ __global__ __launch_bounds__(256) void f32gemm_tile_kernel(const float *__restri
 
 // ---------------------------------------------------------------------------------------------
 // Decode batches (up to 64 activation rows): one launch without the split pre-pass.  Each workgroup
-// converts the activations of its K range itself, 4 blocks at a time, into LDS (bf16 hi, mid and lo,
-// the per-block sums of the pieces), shared by its 4 waves; the chunks are double-buffered so the next
+// converts the activations of its K range itself, 4 blocks at a time, into LDS (bf16 hi and fp16
+// lo16, the per-block sums of the pieces), shared by its 4 waves; the chunks are double-buffered so the next
 // chunk's activations and weights are requested before the current one is multiplied (requesting
 // the weights a second chunk earlier measured no faster).  The fused
 // RMSNorm stages lnw * x and scales the finished sums by 1 / rms of the activation row (sum x^2 is
@@ -526,7 +533,6 @@ __global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const u
     constexpr int R = 16 * NC;                     // staged activation rows
     constexpr int F4 = R * kCK * 8 / 256;          // staged float4 per thread per chunk
     __shared__ __align__(16) uint16_t sh[2][R][kSRow];
-    __shared__ __align__(16) uint16_t sm[2][R][kSRow];
     __shared__ __align__(16) uint16_t sl[2][R][kSRow];
     __shared__ float ssum[2][R][kCK];
     __shared__ float sinv[R];
@@ -580,19 +586,12 @@ __global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const u
                 if constexpr (NORM) ssq[i] = fmaf(e[k], e[k], ssq[i]);
                 u[k] = NORM ? g[k] * e[k] : e[k];
             }
-            uint2 hw, mw, lw;
-            split3_bf16x2(u[0], u[1], hw.x, mw.x, lw.x);
-            split3_bf16x2(u[2], u[3], hw.y, mw.y, lw.y);
-            float sum = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t h = k < 2 ? hw.x : hw.y, m = k < 2 ? mw.x : mw.y, l = k < 2 ? lw.x : lw.y;
-                const int sh16 = (k & 1) ? 0 : 16;
-                sum += (__uint_as_float((h << sh16) & 0xFFFF0000u) + __uint_as_float((m << sh16) & 0xFFFF0000u)) +
-                       __uint_as_float((l << sh16) & 0xFFFF0000u);
-            }
+            uint2 hw, lw;
+            float r01[2], r23[2];
+            split_bf16_f16x2(u[0], u[1], hw.x, lw.x, r01);
+            split_bf16_f16x2(u[2], u[3], hw.y, lw.y, r23);
+            float sum = (r01[0] + r01[1]) + (r23[0] + r23[1]);   // the four elements as the pieces represent them
             *reinterpret_cast<uint2 *>(&sh[buf][row][bl * QK + j4 * 4]) = hw;
-            *reinterpret_cast<uint2 *>(&sm[buf][row][bl * QK + j4 * 4]) = mw;
             *reinterpret_cast<uint2 *>(&sl[buf][row][bl * QK + j4 * 4]) = lw;
             // the 8 threads of one (row, block) are 8 consecutive lanes
             sum += __shfl_xor(sum, 1, kWave);
@@ -631,10 +630,11 @@ __global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const u
 #pragma unroll
         for (int u = 0; u < kCK; ++u) {
             bf16x8_t af[2];
+            f16x8_t ah[2];
             float d[2][4];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                af[t] = a_frag<DT>(r[u].wa[t], lg);
+                af[t] = a_frag<DT, true>(r[u].wa[t], lg, &ah[t]);
                 d[t][0] = half_bits_to_float(r[u].sc[t].x);
                 d[t][1] = half_bits_to_float(r[u].sc[t].x >> 16);
                 d[t][2] = half_bits_to_float(r[u].sc[t].y);
@@ -644,15 +644,13 @@ __global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const u
             for (int c = 0; c < NC; ++c) {
                 const int row = c * 16 + l16;
                 const uint4 xh = *reinterpret_cast<const uint4 *>(&sh[buf][row][u * QK + 8 * lg]);
-                const uint4 xm = *reinterpret_cast<const uint4 *>(&sm[buf][row][u * QK + 8 * lg]);
                 const uint4 xl = *reinterpret_cast<const uint4 *>(&sl[buf][row][u * QK + 8 * lg]);
                 const float corr = OFF * ssum[buf][row][u];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     f32x4_t pr = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
                     pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, xh), pr, 0, 0, 0);
-                    pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, xm), pr, 0, 0, 0);
-                    pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], __builtin_bit_cast(bf16x8_t, xl), pr, 0, 0, 0);
+                    pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[t], __builtin_bit_cast(f16x8_t, xl), pr, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf(d[t][i], pr[i] - corr, acc[t][c][i]);
                 }
