@@ -412,6 +412,75 @@ int vgx_layernorm(const float *x, int64_t ldx, const float *w, const float *b, f
 int vgx_seg_score_tail(const float *h, int64_t ldh, const float *w2, const float *b2, int64_t hidden, int64_t T,
                        int first, float *out, const int32_t *out_index, void *stream);
 
+/* ---------------------------------------------------------------- top candidates of a row ------ */
+
+/* The T (<= 256) largest logits of each row, sorted by value descending, ties by index ascending
+ * (-0 ranks as +0; NaN logits are never candidates): idx[b * T + i], val[b * T + i]; rows with fewer
+ * than T candidates are padded with index -1 and value -inf.  V up to 2^20.
+ * workspace: vgx_topk_workspace_bytes.  For the output
+ * governor's candidate screen (the top-k scans of v3_govern_logits, runtime/vault3.c:3133-3181). */
+int64_t vgx_topk_workspace_bytes(int64_t B, int64_t V, int64_t T);
+int vgx_topk(const float *logits, int64_t ld, int64_t B, int64_t V, int64_t T, int64_t *idx, float *val,
+             void *workspace, int64_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------- host control logic ----------- */
+/* Host-side rules of the decode loop that read token byte strings; no device memory is involved.
+ * Token ids are uint32 in [0, vocab); byte strings come from the VLT3 VTOK table. */
+
+/* Token byte strings: token i is pool[offsets[i] .. offsets[i + 1]) (offsets has n_tokens + 1
+ * entries, non-decreasing); ids >= n_tokens have no bytes.  The handle copies the data.
+ * Replaces v3_token_bytes over the VTOK table (runtime/vault3.c:2303-2308). */
+typedef struct vgx_tokens vgx_tokens;
+vgx_tokens *vgx_tokens_create(const uint8_t *pool, const uint64_t *offsets, uint32_t n_tokens);
+void vgx_tokens_destroy(vgx_tokens *t);
+
+/* Segment-memory resonance for a state with seg_cap bank slots, window W and config n_sink.
+ * vgx_res_rebuild: the tagged-shingle index over the bank's tokens (mem_tok, mem_seg: mem_cnt slots in
+ * bank order); returns the number of distinct segments.  Replaces rebuild_shingle_index
+ * (runtime/vault3.c:1178-1260; src/vault_v3_model.py:1249-1307).
+ * vgx_res_update: one step's query resonance at ring slot c, absolute position pos, n_pin pinned
+ * tokens; tok_prev / tok_cur are the W-slot token rings (tok_cur[c] = this step's token).  Returns the
+ * mode (0: no bias, 1: arch / sup, 2: also hop1) and writes per bank slot (mem_cnt entries) the arch
+ * and sup biases (mode >= 1) and the hop-1 bias (mode 2).  The biased heads are those with
+ * h % grp >= grp / 3 of layers [L / 4, L - L / 14): hop1 in layers below L / 2 in mode 2, else arch
+ * for h % grp < grp - (grp - grp / 3) / 2 and sup above.  Replaces update_query_resonance
+ * (runtime/vault3.c:1426-1786) and _update_step_resonance (src/vault_v3_model.py:1685-1716). */
+typedef struct vgx_resonance vgx_resonance;
+vgx_resonance *vgx_res_create(const vgx_tokens *t, uint32_t window, uint32_t seg_cap, uint32_t n_sink,
+                              uint32_t im_start_id, uint32_t im_end_id);
+void vgx_res_destroy(vgx_resonance *r);
+int vgx_res_rebuild(vgx_resonance *r, const uint32_t *mem_tok, const uint32_t *mem_seg, uint32_t mem_cnt);
+int vgx_res_update(vgx_resonance *r, const uint32_t *tok_prev, const uint32_t *tok_cur, uint32_t c, uint64_t pos,
+                   uint32_t n_pin, float *arch, float *sup, float *hop1);
+
+/* Authority-spoof quarantine: 1 when the lower-cased bytes of the last min(24, pos - n_pin + 1)
+ * tokens of the rings hold "opi_signed_directive" or "urgent opi delegation" (only with n_pin > n_sink
+ * and pos >= n_pin); the step's segment score is then -1e30.  Replaces check_spoof_quarantine
+ * (runtime/vault3.c:1798-1831) and _check_spoof_step (src/vault_v3_model.py:1795-1830). */
+int vgx_spoof_check(const vgx_tokens *t, const uint32_t *tok_prev, const uint32_t *tok_cur, uint32_t window,
+                    uint32_t c, uint64_t pos, uint32_t n_pin, uint32_t n_sink);
+
+/* Output governor: up to 8 rules of 4..32 canonical bytes (Unicode look-alikes folded, separators
+ * dropped); a candidate token is blocked when appending its bytes to the canonical history (or
+ * decoding the raw tail plus its bytes as Base64 / hex) spells a rule forward or reversed.
+ * vgx_gov_arm_system derives the rules from a system prompt (returns the rule count); vgx_gov_screen
+ * takes the top candidates of a logits row (vgx_topk: value desc, index asc, at least 4 x top_k_guard
+ * of them or the whole row) and returns the ids to set to -3.4e38, in up to four passes over the best
+ * top_k_guard (0 or > 64: 64) still unmasked candidates; vgx_gov_commit feeds the chosen token (eos /
+ * im_start / im_end reset the stream).  Replaces v3_gov_init, v3_gov_add_rule, v3_gov_arm_system,
+ * v3_gov_reset_stream, v3_govern_logits, v3_gov_commit (runtime/vault3.c:2814-3193; vault3.h:180-216)
+ * and CAAIGovernor (src/vault_v3_model.py:397-560). */
+typedef struct vgx_governor vgx_governor;
+vgx_governor *vgx_gov_create(const vgx_tokens *t, uint32_t eos_id, uint32_t im_start_id, uint32_t im_end_id);
+void vgx_gov_destroy(vgx_governor *g);
+void vgx_gov_reset_stream(vgx_governor *g);
+int vgx_gov_add_rule(vgx_governor *g, const uint8_t *pat, size_t len);
+int vgx_gov_arm_system(vgx_governor *g, const uint8_t *text, size_t len);
+int vgx_gov_active(const vgx_governor *g);
+int vgx_gov_screen(const vgx_governor *g, const int64_t *cand, const float *cand_val, uint32_t n_cand,
+                   uint32_t top_k_guard, uint32_t vocab, int64_t *masked, uint32_t max_masked);
+int vgx_gov_commit(vgx_governor *g, uint32_t id);
+
 #ifdef __cplusplus
 }
 #endif

@@ -60,6 +60,25 @@ def _load():
         lib.ref_state_flags.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p]
         lib.ref_set_seg_budget.argtypes = [C.c_void_p, C.c_uint32]
         lib.ref_set_seg_budget.restype = C.c_int
+        lib.ref_res_state.argtypes = [C.c_void_p] + [C.c_void_p] * 5
+        lib.ref_rings.argtypes = [C.c_void_p] + [C.c_void_p] * 3
+        lib.ref_model.restype = C.c_void_p
+        lib.ref_model.argtypes = [C.c_void_p]
+        lib.ref_gov_size.restype = C.c_uint64
+        lib.v3_gov_init.argtypes = [C.c_void_p]
+        lib.v3_gov_reset_stream.argtypes = [C.c_void_p]
+        lib.v3_gov_add_rule.argtypes = [C.c_void_p, C.c_char_p, C.c_size_t]
+        lib.v3_gov_add_rule.restype = C.c_int
+        lib.v3_gov_arm_system.argtypes = [C.c_void_p, C.c_char_p, C.c_size_t]
+        lib.v3_govern_logits.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32]
+        lib.v3_gov_commit.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32]
+        lib.ref_res_load_bank.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32]
+        lib.ref_res_load_bank.restype = C.c_int
+        lib.ref_res_update.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint64, C.c_uint32,
+                                       C.c_void_p, C.c_void_p, C.c_void_p]
+        lib.ref_res_update.restype = C.c_int
+        lib.ref_spoof.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint64, C.c_uint32]
+        lib.ref_spoof.restype = C.c_int
         _lib = lib
     return _lib
 
@@ -106,7 +125,52 @@ class RefRuntime:
     def flags(self):
         lk, ba, nu = C.c_int(), C.c_int(), C.c_uint32()
         _load().ref_state_flags(self._h, C.byref(lk), C.byref(ba), C.byref(nu))
-        return dict(pin_locked=bool(lk.value), seg_bias_active=bool(ba.value), n_uniq_segs=nu.value)
+        return dict(pin_locked=bool(lk.value), seg_bias_active=int(ba.value), n_uniq_segs=nu.value)
+
+    def res_state(self):
+        """(mem_tok, mem_seg, arch, sup, hop1) over the bank's mem_cnt slots after the last step."""
+        n = self.info()["mem_cnt"]
+        t, g = np.zeros(max(1, n), dtype=np.uint32), np.zeros(max(1, n), dtype=np.uint32)
+        a, s, h = (np.zeros(max(1, n), dtype=np.float32) for _ in range(3))
+        _load().ref_res_state(self._h, t.ctypes.data, g.ctypes.data, a.ctypes.data, s.ctypes.data, h.ctypes.data)
+        return t[:n], g[:n], a[:n], s[:n], h[:n]
+
+    def rings(self, window: int):
+        """(tok_prev, tok_cur, sc_cur) of the state (W slots each)."""
+        p, c = np.zeros(window, dtype=np.uint32), np.zeros(window, dtype=np.uint32)
+        sc = np.zeros(window, dtype=np.float32)
+        _load().ref_rings(self._h, p.ctypes.data, c.ctypes.data, sc.ctypes.data)
+        return p, c, sc
+
+    def model_ptr(self) -> int:
+        return _load().ref_model(self._h)
+
+    def res_load_bank(self, mem_tok, mem_seg) -> int:
+        """rebuild_shingle_index over a constructed bank; returns the number of distinct segments."""
+        t = np.ascontiguousarray(mem_tok, dtype=np.uint32)
+        g = np.ascontiguousarray(mem_seg, dtype=np.uint32)
+        n = _load().ref_res_load_bank(self._h, t.ctypes.data, g.ctypes.data, t.size)
+        if n < 0:
+            raise RuntimeError("bank larger than the state's segment capacity")
+        self._bank_n = t.size
+        return n
+
+    def res_update(self, tok_prev, tok_cur, c: int, pos: int, n_pin: int):
+        """update_query_resonance on constructed rings: (mode, arch, sup, hop1) over the loaded bank."""
+        p = np.ascontiguousarray(tok_prev, dtype=np.uint32)
+        q = np.ascontiguousarray(tok_cur, dtype=np.uint32)
+        n = max(1, getattr(self, "_bank_n", 0))
+        a, s, h = (np.zeros(n, dtype=np.float32) for _ in range(3))
+        mode = _load().ref_res_update(self._h, p.ctypes.data, q.ctypes.data, c, pos, n_pin, a.ctypes.data,
+                                      s.ctypes.data, h.ctypes.data)
+        m = getattr(self, "_bank_n", 0)
+        return mode, a[:m], s[:m], h[:m]
+
+    def spoof(self, tok_prev, tok_cur, c: int, pos: int, n_pin: int) -> bool:
+        p = np.ascontiguousarray(tok_prev, dtype=np.uint32)
+        q = np.ascontiguousarray(tok_cur, dtype=np.uint32)
+        return bool(_load().ref_spoof(self._h, p.ctypes.data, q.ctypes.data, c, pos, n_pin))
+
 
     def set_seg_budget(self, budget: int) -> None:
         rc = _load().ref_set_seg_budget(self._h, budget)
@@ -138,6 +202,34 @@ class RefRuntime:
         rc = _load().ref_seed_long_context(self._h, pos, n_pin, mem_cnt, seed)
         if rc:
             raise RuntimeError("seed_long_context rejected the arguments")
+
+
+class RefGovernor:
+    """The reference's v3_governor (runtime/vault3.c:2888-3193) over a loaded runtime's model."""
+
+    def __init__(self, rt: RefRuntime):
+        lib = _load()
+        self._rt = rt
+        self._m = rt.model_ptr()
+        self._buf = C.create_string_buffer(int(lib.ref_gov_size()))
+        lib.v3_gov_init(self._buf)
+
+    def arm_system(self, text: bytes) -> None:
+        _load().v3_gov_arm_system(self._buf, text, len(text))
+
+    def add_rule(self, pat: bytes) -> int:
+        return int(_load().v3_gov_add_rule(self._buf, pat, len(pat)))
+
+    def reset_stream(self) -> None:
+        _load().v3_gov_reset_stream(self._buf)
+
+    def govern_logits(self, logits: np.ndarray, top_k_guard: int = 0) -> np.ndarray:
+        a = np.ascontiguousarray(logits, dtype=np.float32).copy()
+        _load().v3_govern_logits(self._buf, self._m, a.ctypes.data, int(top_k_guard))
+        return a
+
+    def commit(self, tid: int) -> None:
+        _load().v3_gov_commit(self._buf, self._m, int(tid))
 
 
 def argmax(logits: np.ndarray) -> int:

@@ -1,19 +1,24 @@
 /* ctypes-facing shim around the reference C runtime (runtime/vault3.h API).
  *
- * TEST INFRASTRUCTURE ONLY.  Compiled together with the reference's runtime/vault3.c into
- * oracle/_ref/libv3ref.so by oracle/Makefile; never linked into the product.
+ * TEST INFRASTRUCTURE ONLY.  Compiled by oracle/Makefile into oracle/_ref/libv3ref.so as one
+ * translation unit with the reference's runtime/vault3.c (included from the reference tree); never
+ * linked into the product.
  *
  * Provides: an aligned model buffer + v3_load (runtime/vault3.c:273-455), a state arena +
  * v3_state_init (:828-852), v3_step (:2034-2222), v3_set_pinned (:898-928), an optional persistent
- * thread pool implementing the v3_parallel_for_fn hook (runtime/vault3.h:103-106), and a helper that
- * seeds the fixed-size state as it stands deep into a long stream (for timing at long context).
+ * thread pool implementing the v3_parallel_for_fn hook (runtime/vault3.h:103-106), a helper that
+ * seeds the fixed-size state as it stands deep into a long stream (for timing at long context), and
+ * read access to the resonance state and the model for the governor (runtime/vault3.h:180-216), and
+ * direct calls of the static resonance / quarantine functions on constructed banks and rings.
  */
 #include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 
-#include "vault3.h"
+/* The runtime's translation unit itself, so that the shim can also reach the static resonance and
+ * quarantine functions (runtime/vault3.c:1178-1831) for direct tests on constructed states. */
+#include "vault3.c"
 
 typedef struct pool pool_t;
 
@@ -202,6 +207,32 @@ void ref_mem_pos(ref_ctx *c, uint64_t *out) {
     for (uint32_t i = 0; i < c->s.mem_cnt; i++) out[i] = c->s.mem_pos[i];
 }
 
+/* The bank's tokens and segment ids and the resonance biases over its mem_cnt slots (the values
+ * v3_step computed for its last step; hop1 meaningful when seg_bias_active == 2). */
+void ref_res_state(ref_ctx *c, uint32_t *mem_tok, uint32_t *mem_seg, float *arch, float *sup, float *hop1) {
+    for (uint32_t i = 0; i < c->s.mem_cnt; i++) {
+        mem_tok[i] = c->s.mem_tok[i];
+        mem_seg[i] = c->s.mem_seg[i];
+        arch[i] = c->s.seg_bias_arch[i];
+        sup[i] = c->s.seg_bias_sup[i];
+        hop1[i] = c->s.seg_bias_hop1[i];
+    }
+}
+
+/* The token rings (W slots each) and the current chunk's segment scores. */
+void ref_rings(ref_ctx *c, uint32_t *tok_prev, uint32_t *tok_cur, float *sc_cur) {
+    uint32_t W = c->m.window;
+    for (uint32_t i = 0; i < W; i++) {
+        tok_prev[i] = c->s.tok_prev[i];
+        tok_cur[i] = c->s.tok_cur[i];
+        sc_cur[i] = c->s.sc_cur ? c->s.sc_cur[i] : 0.0f;
+    }
+}
+
+/* The loaded model (for the governor entry points, runtime/vault3.h:211-216) and the governor's size. */
+const v3_model *ref_model(ref_ctx *c) { return &c->m; }
+uint64_t ref_gov_size(void) { return (uint64_t)sizeof(v3_governor); }
+
 /* Copy one layer's KV field out of the state, as [G][rows][D] floats (rows = W for the window
  * fields 0-5, sink_cap for the sink fields 6-8, seg_cap for the segment fields 9-11; field order
  * k_prev k_cur v_prev v_cur kraw_prev kraw_cur k_sink_raw k_sink v_sink k_seg_raw k_seg v_seg).
@@ -270,4 +301,56 @@ int ref_seed_long_context(ref_ctx *c, uint64_t pos, uint32_t n_pin, uint32_t mem
     s->n_uniq_segs = 0;   /* no shingles: resonance stays inactive */
     s->ema_ready = 1;
     return 0;
+}
+
+/* ---------------------------------------------------------------- direct resonance calls -------- */
+
+/* Load a bank (mem_cnt <= seg_cap slots of tokens and segment ids) into the state and rebuild the
+ * shingle index (rebuild_shingle_index, runtime/vault3.c:1178-1260); returns n_uniq_segs, or -1. */
+int ref_res_load_bank(ref_ctx *c, const uint32_t *mem_tok, const uint32_t *mem_seg, uint32_t mem_cnt) {
+    v3_state *s = &c->s;
+    if (mem_cnt > s->seg_cap) return -1;
+    for (uint32_t i = 0; i < mem_cnt; i++) {
+        s->mem_tok[i] = mem_tok[i];
+        s->mem_seg[i] = mem_seg[i];
+        s->mem_pos[i] = i;
+        s->mem_score[i] = 0.0f;
+    }
+    s->mem_cnt = mem_cnt;
+    rebuild_shingle_index(s);
+    return (int)s->n_uniq_segs;
+}
+
+/* One update_query_resonance (runtime/vault3.c:1426-1786) on given token rings (W slots each), ring
+ * slot c, position and pin count over the loaded bank; returns seg_bias_active and copies the three
+ * bias vectors (mem_cnt slots). */
+int ref_res_update(ref_ctx *c, const uint32_t *tok_prev, const uint32_t *tok_cur, uint32_t ci, uint64_t pos,
+                   uint32_t n_pin, float *arch, float *sup, float *hop1) {
+    v3_state *s = &c->s;
+    uint32_t W = c->m.window;
+    for (uint32_t i = 0; i < W; i++) {
+        s->tok_prev[i] = tok_prev[i];
+        s->tok_cur[i] = tok_cur[i];
+    }
+    s->pos = pos;
+    s->n_pin = n_pin;
+    update_query_resonance(s, ci);
+    for (uint32_t i = 0; i < s->mem_cnt; i++) {
+        arch[i] = s->seg_bias_arch[i];
+        sup[i] = s->seg_bias_sup[i];
+        hop1[i] = s->seg_bias_hop1[i];
+    }
+    return s->seg_bias_active;
+}
+
+/* check_spoof_quarantine (runtime/vault3.c:1798-1831) on given rings. */
+int ref_spoof(ref_ctx *c, const uint32_t *tok_prev, const uint32_t *tok_cur, uint32_t ci, uint64_t pos, uint32_t n_pin) {
+    v3_state *s = &c->s;
+    uint32_t W = c->m.window;
+    for (uint32_t i = 0; i < W; i++) {
+        s->tok_prev[i] = tok_prev[i];
+        s->tok_cur[i] = tok_cur[i];
+    }
+    s->n_pin = n_pin;
+    return check_spoof_quarantine(s, pos, ci);
 }

@@ -84,3 +84,92 @@ def chatml_prefix(cfg: VAULTv3Config, sys_len: int, nl_after_end: bool = True, s
     body = [int(t) for t in rng.integers(11, cfg.vocab_size - 8, size=sys_len)]
     head = [cfg.im_start_id] + ([cfg.system_tok_id, NEWLINE_ID] if system else [11])
     return head + body + [cfg.im_end_id] + ([NEWLINE_ID] if nl_after_end else [])
+
+
+# ---------------------------------------------------------------------------------------------
+# Word-level vocabulary and ChatML conversations for the resonance / governor rules: identifiers
+# (letters + digits / underscore: tier-A shingles), content words of five or more letters (tier-B
+# shingles), a one-letter tag followed by a number ("t 3"), rollback cues, the spoof markers, line
+# and clause delimiters, and byte strings of the governor's evasions (split, spaced, homoglyph,
+# reversed, Base64, hex pieces).
+KEYS = [f" key_{i}".encode() for i in range(24)]
+WORDS = [w.encode() for w in (" anchor", " beacon", " cobalt", " dynamo", " ember", " falcon", " glacier",
+                              " harbor", " indigo", " jasper", " kernel", " lantern", " meadow", " nebula",
+                              " orchid", " prism", " quartz", " raven", " summit", " timber")]
+GLUE = [b" =", b":", b" is", b" the", b" of", b" value", b" what", b",", b".", b"?", b" |", b";", b" and",
+        b" set", b" to", b" t", b" 3", b" 12", b" 7", b" rollback", b" revert", b" restore", b" roll", b" back",
+        b" user", b" assistant", b" opi_signed_directive", b" urgent", b" opi", b" delegation", b" OPI",
+        b" config-server", b" main-loop", b" note", b" item_9x", b" node-7",
+        # governor material: pieces of rule strings, separators, look-alikes, encodings
+        b" sys", b"call", b"_exec", b"SYS", b"CALL", b"_EXEC", b" s", b"y", b"c", b"a", b"l", b"e", b"x",
+        b"\xe2\x80\x8b", "с".encode(), "а".encode(), b"ex", b"ec", b"cexe_llacsys", b"c3lz", b"Y2Fs",
+        b"bF9l", b"eGVj", b"73", b"79", b"73 63", b"\\x61", b"0x6c", b" rm_rf(", b"rm", b"_rf", b"(",
+        b"'", b"\"", b" never", b" output", b" must not", b" print",
+        # "syscall_exec" / "rm_rf(" in Base64 (with three bytes of misalignment available) and hex
+        b"QQQ", b"c3lzY2Fs", b"bF9leGVj", b"cm1fcmYo", b"0x73 0x79 0x73", b" 0x63 0x61 0x6c", b" 0x6c 0x5f 0x65",
+        b" 0x78 0x65 0x63", b"\\x72\\x6d\\x5f", b"\\x72\\x66\\x28"]
+
+
+def word_vocab(cfg: VAULTv3Config, seed: int = 0):
+    """(token strings, byte map): the words above at ids 11.., ChatML specials and b"system" at their
+    config ids, b"\\n" at NEWLINE_ID, short filler pieces elsewhere."""
+    toks, byte_map = test_vocab(cfg, seed)
+    words = KEYS + WORDS + list(GLUE)
+    assert 11 + len(words) < cfg.vocab_size - 8
+    for i, w in enumerate(words):
+        toks[11 + i] = w
+    return toks, byte_map
+
+
+def word_ids(toks: list) -> dict:
+    """bytes -> the first id that carries them."""
+    out = {}
+    for i, t in enumerate(toks):
+        out.setdefault(t, i)
+    return out
+
+
+def conversation(cfg: VAULTv3Config, toks: list, kind: str, seed: int = 0, n_lines: int = 14,
+                 filler: int = 40, answer: int = 30) -> list:
+    """A ChatML stream: a pinned system prompt, a user turn of key / value lines (evicted into the
+    segment bank as the stream goes on), filler turns, a question of ``kind`` ("id", "ids", "words",
+    "rollback", "hop", "spoof", "clause"), <|im_end|>, then ``answer`` assistant tokens."""
+    rng = np.random.default_rng(seed)
+    ids = word_ids(toks)
+    w = lambda *bs: [ids[b] for b in bs]
+    nl = [NEWLINE_ID]
+    out = [cfg.im_start_id, cfg.system_tok_id] + nl + w(b" note", b" the", b" value", b" of", b" key_0", b".") + \
+        [cfg.im_end_id] + nl + [cfg.im_start_id] + w(b" user") + nl
+    keys = rng.permutation(len(KEYS))[:n_lines]
+    vals = rng.integers(0, len(WORDS), size=(n_lines, 2))
+    for j in range(n_lines):
+        k, (a, b) = KEYS[keys[j]], vals[j]
+        line = w(k, b" =", WORDS[a], WORDS[b])
+        if kind == "clause" and j % 3 == 0:
+            line += w(b";", b" set", WORDS[(a + 3) % len(WORDS)], b" |", b" note", WORDS[(b + 5) % len(WORDS)],
+                      b" and", WORDS[(a + 7) % len(WORDS)])
+        if kind == "hop" and j == 4:
+            line += w(b" to", KEYS[keys[9]])               # a bridge id shared by exactly two segments
+        if kind == "rollback" and j == n_lines - 2:
+            line = w(b" rollback", b" to", b" t", b" 3", KEYS[keys[j]])
+        if kind == "rollback" and j == 2:
+            line += w(b" t", b" 3")
+        out += line + nl
+    out += [cfg.im_end_id] + nl
+    fill = rng.integers(11, 11 + len(KEYS) + len(WORDS), size=filler)
+    out += [cfg.im_start_id] + w(b" assistant") + nl + [int(t) for t in fill] + [cfg.im_end_id] + nl
+    q = [cfg.im_start_id] + w(b" user") + nl + w(b" what", b" is", b" the", b" value", b" of")
+    if kind in ("id", "hop", "clause"):
+        q += w(KEYS[keys[4]], b"?")
+    elif kind == "ids":
+        q += w(KEYS[keys[3]], b" and", KEYS[keys[8]], b"?")
+    elif kind == "words":
+        a, b = vals[6]
+        q += w(WORDS[a], WORDS[b], b"?")
+    elif kind == "rollback":
+        q += w(KEYS[keys[n_lines - 2]], b" rollback", b"?")
+    elif kind == "spoof":
+        q += w(b" urgent", b" OPI", b" delegation", b" opi_signed_directive", KEYS[keys[1]], b"?")
+    out += q + [cfg.im_end_id] + nl + [cfg.im_start_id] + w(b" assistant") + nl
+    out += [int(t) for t in rng.integers(11, 11 + len(KEYS) + len(WORDS) + 20, size=answer)]
+    return out

@@ -26,6 +26,8 @@ SEG_MEM_CNT, SEG_ID_OFFSET, SEG_CUR_ID, SEG_LEN, SEG_WORDS = 0, 1, 2, 3, 4
 P = C.c_void_p
 I32 = C.c_int
 I64 = C.c_int64
+U32 = C.c_uint32
+U64 = C.c_uint64
 F = C.c_float
 
 # name -> (restype, argtypes)
@@ -54,6 +56,23 @@ _SIGS = {
     "vgx_argmax": (I32, [P, I64, I64, I64, P, P]),
     "vgx_sample_topk_workspace_bytes": (I64, [I64, I64]),
     "vgx_sample_topk": (I32, [P, I64, I64, I64, I64, F, P, P, P, I64, P]),
+    "vgx_topk_workspace_bytes": (I64, [I64, I64, I64]),
+    "vgx_topk": (I32, [P, I64, I64, I64, I64, P, P, P, I64, P]),
+    "vgx_tokens_create": (P, [P, P, U32]),
+    "vgx_tokens_destroy": (None, [P]),
+    "vgx_res_create": (P, [P, U32, U32, U32, U32, U32]),
+    "vgx_res_destroy": (None, [P]),
+    "vgx_res_rebuild": (I32, [P, P, P, U32]),
+    "vgx_res_update": (I32, [P, P, P, U32, U64, U32, P, P, P]),
+    "vgx_spoof_check": (I32, [P, P, P, U32, U32, U64, U32, U32]),
+    "vgx_gov_create": (P, [P, U32, U32, U32]),
+    "vgx_gov_destroy": (None, [P]),
+    "vgx_gov_reset_stream": (None, [P]),
+    "vgx_gov_add_rule": (I32, [P, P, C.c_size_t]),
+    "vgx_gov_arm_system": (I32, [P, P, C.c_size_t]),
+    "vgx_gov_active": (I32, [P]),
+    "vgx_gov_screen": (I32, [P, P, P, U32, U32, U32, P, U32]),
+    "vgx_gov_commit": (I32, [P, U32]),
     "vgx_attn_decode_noalloc": (I32, [I32, P, I64, P, I32, P, I64, I32, I64, P, I64, I64, I64, I64, F, P]),
     "vgx_attn_prefill": (I32, [I32, I32, I32, P, I32, I64, I64, I64, F, P]),
     "vgx_rmsnorm": (I32, [P, I64, P, P, I64, I64, I64, F, P]),

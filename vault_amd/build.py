@@ -1,7 +1,7 @@
 """Build libvault_amd.so (gfx950) in-tree with hipcc.
 
-Every ``vault_amd/csrc/*.hip`` file is compiled to an object and linked into
-``vault_amd/_lib/libvault_amd.so``.  All HIP code is compiled with packed-FP32 VALU
+Every ``vault_amd/csrc/*.hip`` file (device code) and ``*.cpp`` file (host-only C++) is compiled to
+an object and linked into ``vault_amd/_lib/libvault_amd.so``.  All HIP code is compiled with packed-FP32 VALU
 instructions disabled (``-target-feature -packed-fp32-ops``).
 """
 from __future__ import annotations
@@ -45,12 +45,12 @@ def _compile(src: str, obj: str) -> None:
 
 
 def build(verbose: bool = False) -> str:
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     if not srcs:
         raise RuntimeError("no HIP sources found")
     obj_dir = os.path.join(OUT_DIR, "obj")
     os.makedirs(obj_dir, exist_ok=True)
-    objs = [os.path.join(obj_dir, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    objs = [os.path.join(obj_dir, os.path.splitext(os.path.basename(s))[0] + ".o") for s in srcs]
     jobs = min(len(srcs), max(1, (os.cpu_count() or 4)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         for f in [ex.submit(_compile, s, o) for s, o in zip(srcs, objs)]:

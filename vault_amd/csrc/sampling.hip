@@ -141,6 +141,48 @@ __global__ __launch_bounds__(kThreads) void topk_draw_kernel(const uint64_t *__r
 
 int64_t chunks_of(int64_t V) { return (V + kChunk - 1) / kChunk; }
 
+// Top-T selection: rounds of workgroups that each sort kChunk keys and keep their kKeep largest, the
+// first round over the logits, later rounds over the previous round's survivors, until one chunk
+// holds them all; that last workgroup writes the indices and values.  Ties keep the smaller index
+// first (the key order), so the result is exactly the first T of the row sorted by value desc, index
+// asc.  The survivors of a chunk include the row's top T whenever they fall in it (T <= kKeep).
+constexpr int kKeep = 256;
+
+template <bool LOGITS>
+__global__ __launch_bounds__(kThreads) void select_kernel(const float *__restrict__ x, int64_t ld, int64_t V,
+                                                          const uint64_t *__restrict__ in, int64_t n_in,
+                                                          uint64_t *__restrict__ out, int64_t n_out_per_row, int T,
+                                                          int64_t *__restrict__ idx, float *__restrict__ val) {
+    __shared__ uint64_t s[kChunk];
+    const int64_t b = blockIdx.y;
+    const int64_t base = (int64_t)blockIdx.x * kChunk;
+    for (int i = threadIdx.x; i < kChunk; i += kThreads) {
+        const int64_t g = base + i;
+        if constexpr (LOGITS) s[i] = g < V ? key_of(x[b * ld + g], g) : 0ull;
+        else s[i] = g < n_in ? in[b * n_in + g] : 0ull;
+    }
+    __syncthreads();
+    sort_desc(s, kChunk);
+    if (idx != nullptr) {
+        // the last round: one chunk per row
+        for (int i = threadIdx.x; i < T; i += kThreads) {
+            const uint64_t k = s[i];
+            idx[b * T + i] = k == 0ull ? -1 : index_of(k);
+            val[b * T + i] = k == 0ull ? -INFINITY : value_of(k);
+        }
+        return;
+    }
+    uint64_t *o = out + b * n_out_per_row + (int64_t)blockIdx.x * kKeep;
+    for (int i = threadIdx.x; i < kKeep; i += kThreads) o[i] = s[i];
+}
+
+// Keys left per row after each round, and the workspace (two ping-pong survivor buffers).
+int64_t select_ws_bytes(int64_t B, int64_t V) {
+    const int64_t n1 = chunks_of(V) * kKeep;
+    const int64_t n2 = chunks_of(n1) * kKeep;
+    return V <= kChunk ? 0 : B * (n1 + (n1 > kChunk ? n2 : 0)) * 8;
+}
+
 }  // namespace
 
 extern "C" {
@@ -175,6 +217,51 @@ int vgx_sample_topk(const float *logits, int64_t ld, int64_t B, int64_t V, int64
                        (int)nc, cand);
     VGX_CHECK_LAUNCH();
     hipLaunchKernelGGL(topk_draw_kernel, dim3((unsigned)B), dim3(kThreads), 0, st, cand, (int)nc, (int)k, temp, rng, out);
+    VGX_CHECK_LAUNCH();
+    return VGX_OK;
+}
+
+int64_t vgx_topk_workspace_bytes(int64_t B, int64_t V, int64_t T) {
+    if (B <= 0 || V <= 0 || T <= 0 || T > kKeep) return VGX_E_SIZE;
+    return select_ws_bytes(B, V);
+}
+
+int vgx_topk(const float *logits, int64_t ld, int64_t B, int64_t V, int64_t T, int64_t *idx, float *val,
+             void *workspace, int64_t workspace_bytes, void *stream) {
+    if (!logits || !idx || !val) return VGX_E_ARG;
+    if (B <= 0 || V <= 0 || T <= 0 || ld < V) return VGX_E_SIZE;
+    if (T > kKeep || B > 65535 || V > 0xFFFFFFFFll) return VGX_E_LIMIT;
+    // rows of at most two rounds of survivors: V up to 16 x 16 chunks of 4096 keys
+    if (chunks_of(chunks_of(V) * kKeep) * kKeep > kChunk) return VGX_E_LIMIT;
+    const int64_t need = select_ws_bytes(B, V);
+    if (need > 0 && (!workspace || workspace_bytes < need)) return VGX_E_ARENA;
+    hipStream_t st = (hipStream_t)stream;
+    if (V <= kChunk) {
+        hipLaunchKernelGGL(select_kernel<true>, dim3(1, (unsigned)B), dim3(kThreads), 0, st, logits, ld, V,
+                           (const uint64_t *)nullptr, (int64_t)0, (uint64_t *)nullptr, (int64_t)0, (int)T, idx, val);
+        VGX_CHECK_LAUNCH();
+        return VGX_OK;
+    }
+    auto *s1 = static_cast<uint64_t *>(workspace);
+    const int64_t n1 = chunks_of(V) * kKeep;
+    hipLaunchKernelGGL(select_kernel<true>, dim3((unsigned)chunks_of(V), (unsigned)B), dim3(kThreads), 0, st, logits,
+                       ld, V, (const uint64_t *)nullptr, (int64_t)0, s1, n1, (int)T, (int64_t *)nullptr,
+                       (float *)nullptr);
+    VGX_CHECK_LAUNCH();
+    const uint64_t *last = s1;
+    int64_t n_last = n1;
+    if (n1 > kChunk) {
+        uint64_t *s2 = s1 + B * n1;
+        const int64_t n2 = chunks_of(n1) * kKeep;
+        hipLaunchKernelGGL(select_kernel<false>, dim3((unsigned)chunks_of(n1), (unsigned)B), dim3(kThreads), 0, st,
+                           (const float *)nullptr, (int64_t)0, (int64_t)0, s1, n1, s2, n2, (int)T, (int64_t *)nullptr,
+                           (float *)nullptr);
+        VGX_CHECK_LAUNCH();
+        last = s2;
+        n_last = n2;
+    }
+    hipLaunchKernelGGL(select_kernel<false>, dim3(1, (unsigned)B), dim3(kThreads), 0, st, (const float *)nullptr,
+                       (int64_t)0, (int64_t)0, last, n_last, (uint64_t *)nullptr, (int64_t)0, (int)T, idx, val);
     VGX_CHECK_LAUNCH();
     return VGX_OK;
 }

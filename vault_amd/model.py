@@ -3,17 +3,24 @@
 Mirrors ``VAULTv3ForCausalLM`` / ``VAULTv3State`` of src/vault_v3_model.py (new_state :2159,
 prefill :2163-2212, step :2214-2311, forward :2153) with the same argument meaning and state
 fields; every projection, attention, RoPE, norm, KV-cache write, chunk-boundary re-base/re-rotation,
-segment-bank compaction and scorer op is a call into the HIP library.  Host-side control stays in
-Python as in the reference: the auto-pin FSM, segment-id bookkeeping, and the top-B eviction merge
-(on at most budget + W candidates once per W tokens).
+segment-bank compaction and scorer op is a call into the HIP library.  The auto-pin FSM runs on the
+host (it decides on the prompt's first tokens); the segmenter, the segment rings and the top-B
+eviction merge run on the device.
 
 Token rules: with the token strings of a VLT3 file (``weights.tokens``) the segment-break tiers,
 the system-role test and the newline id of the auto-pin rule come from the bytes, as in the C
 runtime (runtime/vault3.c:937-959, 1920-1928, 2047); without them (a model built from tensors,
 like the reference Python model offline) every tier is 0, the system role is
 ``cfg.system_tok_id`` and the newline id is 198 (src/vault_v3_model.py:2224-2252, 2260-2268).
-Shingles, resonance biases and spoof quarantine are not derived here; a caller-supplied per-head
-bias (``st.seg_head_bias``, ``st.seg_bias_active``) is honoured by the attention kernel.
+Resonance and quarantine (runtime/vault3.c:1178-1831): with token strings and segment memory
+(batch 1), the library's host unit (vault_amd/control.py) keeps a shingle index over the segment bank
+(rebuilt after every bank merge, from the bank's tokens and segment ids read back once per W tokens)
+and evaluates the query resonance of every step on host mirrors of the token rings; an active mode
+writes the per-head bias rows of the state's two device bias buffers (layers [L/4, L/2) and
+[L/2, L - L/14)), which the captured decode step reads on the segment span.  The spoof check
+overwrites the step's segment score with -1e30.  Prefill chunks in which resonance is active at some
+position run through the step path (the same launches as decoding), the others through the chunk
+kernels with the quarantine applied to the chunk's scores.
 
 Differences by design:
 * The KV caches of all layers are single tensors [n_layers, B, G, n, D]; prev/cur are swapped by
@@ -36,7 +43,7 @@ from typing import Dict, List, Optional, Tuple
 import numpy as np
 import torch
 
-from . import ops
+from . import control, ops
 from .attention import block_sliding_attention, causal_attention, rope_table_double
 from .config import VAULTv3Config
 from .weights import ModelWeights
@@ -140,10 +147,15 @@ class VAULTv3State:
         fd = max(1, len(cfg.seg_layers) * cfg.d_model)
         self.ema_ready = False
         self.seg_feat_ema = torch.zeros(fd, dtype=torch.float32, device=self.device)
+        # resonance (batch 1 with token strings): host mirrors of the token rings, the shingle index and
+        # the bias rows [H, bank capacity] of the early / late biased layers
         self.seg_bias_mode = 0
         self.seg_bias_active = False
-        self.seg_head_bias: Optional[torch.Tensor] = None
-        self.seg_head_bias_hop1: Optional[torch.Tensor] = None
+        self.tok_prev_h = np.zeros(W, dtype=np.uint32)
+        self.tok_cur_h = np.zeros(W, dtype=np.uint32)
+        self.res: Optional[control.Resonance] = None
+        self.bias_early: Optional[torch.Tensor] = None
+        self.bias_late: Optional[torch.Tensor] = None
         self.graphs: "OrderedDict[tuple, tuple]" = OrderedDict()   # captured decode steps
         self._io: Optional[StepIO] = None
 
@@ -229,6 +241,8 @@ class VAULTv3State:
         self.bank_seg[:mem_cnt].copy_((i // 16).to(torch.int32))
         self.ctrl.copy_(torch.tensor([mem_cnt, 0, 0, 0], dtype=torch.int32))
         self.ema_ready = True
+        if self.res is not None:
+            self.res.rebuild(self.bank_tok[:mem_cnt].cpu().numpy(), self.bank_seg[:mem_cnt].cpu().numpy())
 
 
 class VAULTv3ForCausalLM:
@@ -244,6 +258,10 @@ class VAULTv3ForCausalLM:
         self.tier_lut = self.tokens.tiers if self.tokens is not None else np.zeros(vs, dtype=np.uint8)
         self.tier_dev = torch.from_numpy(self.tier_lut.copy()).to(self.device) if self.tier_lut.any() else None
         self.use_graphs = True          # replay captured HIP graphs for decode steps
+        # token strings for the host control unit (resonance, quarantine); none: those rules cannot fire
+        self.ctl_tokens = control.TokenBytes(self.tokens.tokens) \
+            if self.tokens is not None and self.tokens.has_strings else None
+        self.head_class = control.head_classes(self.cfg.n_heads, self.cfg.n_kv_heads)
         self._table = None
         self._abs_table = None
         self._p0 = 0
@@ -278,6 +296,12 @@ class VAULTv3ForCausalLM:
     def new_state(self, batch: int = 1, seg_budget: Optional[int] = None) -> VAULTv3State:
         st = VAULTv3State(self.cfg, batch, self.device, self.kv_dtype, seg_budget=seg_budget)
         self._ensure_table(st.sink_cap + max(1, st.seg_budget))
+        if self.ctl_tokens is not None and self._seg_active(st, batch):
+            cfg = self.cfg
+            st.res = control.Resonance(self.ctl_tokens, cfg.window, st.seg_budget, cfg.n_sink, cfg.im_start_id,
+                                       cfg.im_end_id)
+            st.bias_early = torch.zeros(cfg.n_heads, st.seg_budget, dtype=torch.float32, device=self.device)
+            st.bias_late = torch.zeros_like(st.bias_early)
         return st
 
     def _seg_active(self, st: VAULTv3State, batch: int) -> bool:
@@ -287,32 +311,70 @@ class VAULTv3ForCausalLM:
     def step(self, token_ids: torch.Tensor, st: VAULTv3State, vault_on: bool = False) -> torch.Tensor:
         """token_ids: (B,) on the host or the device -> logits (B, V) fp32 on the device.  Mutates
         ``st``.  Device ids (e.g. ops.argmax of the previous logits) are not read on the host once the
-        auto-pin prefix is decided: segmentation and the segment bank are updated on the device."""
+        auto-pin prefix is decided (segmentation and the segment bank are updated on the device),
+        except by the host resonance / quarantine rules of a model with token strings and segment
+        memory, which read each id."""
         _ = vault_on
         ids = token_ids.reshape(-1)
         ids = ids if ids.is_cuda else ids.to("cpu", torch.int64)
         B = ids.numel()
         if B != st.batch:
             raise ValueError("batch size differs from the state's")
-        cfg = self.cfg
-        W = cfg.window
+        return self._advance(st, ids, boundary=True)
+
+    def _advance(self, st: VAULTv3State, ids: torch.Tensor, boundary: bool) -> torch.Tensor:
+        """One token through the step path (runtime/vault3.c:2034-2222); ``boundary`` False when the
+        caller has already crossed this chunk's boundary."""
+        W = self.cfg.window
+        B = ids.numel()
         pos = st.pos
         c = pos % W
         seg_active = self._seg_active(st, B)
         if not st.pin_locked and B == 1:
             self._auto_pin(st, int(ids[0]), pos)
-        if c == 0 and pos > 0:
+        if boundary and c == 0 and pos > 0:
             self._boundary(st, seg_active)
-        if not seg_active or pos < 2 * W:
-            st.seg_bias_mode = 0
-            st.seg_bias_active = False
-            st.seg_head_bias = None
-            st.seg_head_bias_hop1 = None
+        if st.res is not None:
+            st.tok_cur_h[c] = int(ids[0])           # a host read when the id is on the device
+            self._resonance(st, c, pos, seg_active)
         logits = self._decode(st, ids, pos, c, seg_active)
+        if st.res is not None and seg_active and self._spoofed(st, c, pos):
+            st.sc_cur[c:c + 1].fill_(-1.0e30)
         if seg_active:
             st.ema_ready = True
         st.pos = pos + 1
         return logits
+
+    # ------------------------------------------------------------------ resonance / quarantine (host)
+    def _resonance(self, st: VAULTv3State, c: int, pos: int, seg_active: bool) -> None:
+        """This step's query resonance over the host rings; an active mode fills the bias buffers."""
+        mode = 0
+        if seg_active and pos >= 2 * self.cfg.window and st.res.mem_cnt > 0:
+            mode = st.res.update(st.tok_prev_h, st.tok_cur_h, c, pos, st.n_pin)
+        st.seg_bias_mode = mode
+        st.seg_bias_active = mode > 0
+        if mode:
+            M = st.res.mem_cnt
+            vec = {1: st.res.arch[:M], 2: st.res.sup[:M]}
+            late = np.zeros((self.cfg.n_heads, M), dtype=np.float32)
+            for h, k in enumerate(self.head_class):
+                if k:
+                    late[h] = vec[int(k)]
+            early = late.copy()
+            if mode == 2:
+                early[self.head_class > 0] = st.res.hop1[:M]
+            st.bias_late[:, :M].copy_(torch.from_numpy(late))
+            st.bias_early[:, :M].copy_(torch.from_numpy(early))
+
+    def _spoofed(self, st: VAULTv3State, c: int, pos: int, n_pin: Optional[int] = None) -> bool:
+        cfg = self.cfg
+        return control.spoof_check(self.ctl_tokens, st.tok_prev_h, st.tok_cur_h, cfg.window, c, pos,
+                                   st.n_pin if n_pin is None else n_pin, cfg.n_sink)
+
+    def _sync_bank(self, st: VAULTv3State) -> None:
+        """Rebuild the shingle index from the device bank (after a merge: once per W tokens)."""
+        M = st.mem_cnt
+        st.res.rebuild(st.bank_tok[:M].cpu().numpy(), st.bank_seg[:M].cpu().numpy())
 
     @torch.no_grad()
     def prefill(self, input_ids: torch.Tensor, vault_on: bool = False,
@@ -322,8 +384,8 @@ class VAULTv3ForCausalLM:
         B, L = input_ids.shape
         bud = self.cfg.seg_budget if seg_budget is None else int(seg_budget)
         if B == 1:
-            h, st = self._chunk_recurrent(input_ids, bud, all_logits=False)
-            return self._logits(h), st
+            h, st, lg = self._chunk_recurrent(input_ids, bud, all_logits=False)
+            return (self._logits(h) if h is not None else lg), st
         # batch > 1: the parallel sliding-window + sink prefill (src/vault_v3_model.py:2177-2212)
         h, st = self._forward_block(input_ids, mode="block", want_state=True, last_only=True)
         return self._logits(h), st
@@ -336,8 +398,8 @@ class VAULTv3ForCausalLM:
         B, L = input_ids.shape
         bud = self.cfg.seg_budget if seg_budget is None else int(seg_budget)
         if B == 1 and mode == "block":
-            h, _ = self._chunk_recurrent(input_ids, bud, all_logits=True)
-            return self._logits(h).unsqueeze(0)
+            _, _, lg = self._chunk_recurrent(input_ids, bud, all_logits=True)
+            return lg.unsqueeze(0)
         # batch > 1, or full causal attention: the parallel form (src/vault_v3_model.py:2118-2151)
         h, _ = self._forward_block(input_ids, mode=mode, want_state=False, last_only=False)
         return self._logits(h).view(B, L, -1)
@@ -416,6 +478,10 @@ class VAULTv3ForCausalLM:
         st.ctrl[ops.L.SEG_CUR_ID:ops.L.SEG_LEN + 1].zero_()
         if pos >= 2 * W:
             self._refresh_prefix(st, seg_active)
+        if st.res is not None:
+            st.tok_prev_h, st.tok_cur_h = st.tok_cur_h, st.tok_prev_h
+            if pos >= 2 * W and seg_active and st.seg_budget > 0:
+                self._sync_bank(st)
 
     def _refresh_prefix(self, st: VAULTv3State, seg_active: bool) -> None:
         """Segment keys at positions [-M, 0), sinks at [-(M+S), -M) (src/vault_v3_model.py:1842-1856),
@@ -460,15 +526,16 @@ class VAULTv3ForCausalLM:
         n_sk = st.n_pin if pos >= 2 * W else 0
         has_seg = pos >= 2 * W and seg_active       # the bank span, its length on the device
         n_prev = W if pos >= W else 0
-        bias_on = bool(has_seg and st.seg_bias_active and st.seg_head_bias is not None)
+        bias_on = bool(has_seg and st.seg_bias_active)
         ema_first = seg_active and not st.ema_ready
-        spec = (B, n_sk, has_seg, n_prev, seg_active, ema_first)
-        if bias_on or not self.use_graphs:
-            return self._decode_launch(st, spec, bias_on)
+        spec = (B, n_sk, has_seg, n_prev, seg_active, ema_first, bias_on)
+        if not self.use_graphs:
+            return self._decode_launch(st, spec)
         self._size_workspace(st)
         key = spec + tuple(t.data_ptr() for t in (st.k_prev, st.k_cur, st.v_prev, st.v_cur, st.kraw_cur, st.k_seg_rot,
                                                    st.v_seg, st.sc_cur, st.tok_cur, st.seg_cur_ids, self._table,
-                                                   self.ws.buf, ops.gemm_workspace(self.device).buf))
+                                                   self.ws.buf, ops.gemm_workspace(self.device).buf)) + \
+            ((st.bias_early.data_ptr(), st.bias_late.data_ptr()) if bias_on else ())
         ent = st.graphs.get(key)
         if ent is None:
             # No destructor may run HIP calls while the stream captures: collect garbage now and keep
@@ -479,13 +546,13 @@ class VAULTv3ForCausalLM:
             try:
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g):
-                    out = self._decode_launch(st, spec, False)
+                    out = self._decode_launch(st, spec)
             finally:
                 if gc_was_on:
                     gc.enable()
             ent = (g, out)
             st.graphs[key] = ent
-            while len(st.graphs) > 4:
+            while len(st.graphs) > 8:
                 st.graphs.pop(next(iter(st.graphs)))
         ent[0].replay()
         return ent[1].clone()
@@ -523,10 +590,10 @@ class VAULTv3ForCausalLM:
                     st.batch, cfg.d_model, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, sep)) for sep in (0, 1)])
             ops.gemm_workspace(self.device).get(need)
 
-    def _decode_launch(self, st: VAULTv3State, spec: tuple, bias_on: bool) -> torch.Tensor:
+    def _decode_launch(self, st: VAULTv3State, spec: tuple) -> torch.Tensor:
         """Every kernel of one decode step (embedding -> 28 layers -> scorer -> LM head) for the chunk
         configuration ``spec``; position-dependent values are read from the step buffer."""
-        B, n_sk, has_seg, n_prev, seg_active, ema_first = spec
+        B, n_sk, has_seg, n_prev, seg_active, ema_first, bias_on = spec
         cfg, w = self.cfg, self.w
         H, G, D, d = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_model
         HD, GD = H * D, G * D
@@ -535,10 +602,9 @@ class VAULTv3ForCausalLM:
         # token ring and segmenter (device words), then the embedding rows
         ops.seg_step(io.ids, step, st.tok_cur, st.seg_cur_ids if seg_active else None, st.ctrl if seg_active else None,
                      self.tier_dev, cfg.seg_min, cfg.seg_max)
-        # bank span: its length is the device count; with a host-supplied bias, the host count (the bias
-        # vector covers the bank's entries)
+        # bank span: its length is the device count (the bias rows cover the bank's capacity)
         m_dev = st.ctrl[ops.L.SEG_MEM_CNT:ops.L.SEG_MEM_CNT + 1]
-        n_seg = (st.mem_cnt if bias_on else st.k_seg_rot.shape[3]) if has_seg else 0
+        n_seg = st.k_seg_rot.shape[3] if has_seg else 0
         x = ops.embed(w.embed, io.ids, pad_row=0)                              # [B, d]
         # rows [0, B) receive the scorer features, rows [B, 2B) the habituated ones (one LayerNorm launch)
         feats = torch.empty(2 * B, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device) \
@@ -579,12 +645,9 @@ class VAULTv3ForCausalLM:
                 spans.append((st.k_sink_rot[li][:, :, :n_sk], st.v_sink[li][:, :, :n_sk]))
             bias, bspan = None, -1
             if n_seg:
-                bias = self._seg_bias(st, li, n_seg) if bias_on else None
+                bias = self._seg_bias(st, li) if bias_on else None
                 bspan = len(spans)
-                if bias_on:
-                    spans.append((st.k_seg_rot[li][:, :, :n_seg], st.v_seg[li][:, :, :n_seg]))
-                else:
-                    spans.append((st.k_seg_rot[li], st.v_seg[li], m_dev))
+                spans.append((st.k_seg_rot[li], st.v_seg[li], m_dev))
             if n_prev:
                 spans.append((st.k_prev[li], st.v_prev[li]))
             spans.append((st.k_cur[li], st.v_cur[li], n_cur))
@@ -610,14 +673,12 @@ class VAULTv3ForCausalLM:
         return q, kv[:, :GD].view(N, G, D), kv[:, GD:].view(N, G, D)
 
     # ------------------------------------------------------------------ device compute
-    def _seg_bias(self, st: VAULTv3State, li: int, M: int) -> Optional[torch.Tensor]:
-        """Per-head bias on the segment span (src/vault_v3_model.py:1115-1132)."""
-        L = self.cfg.n_layers
-        if not (st.seg_bias_active and st.seg_head_bias is not None and M > 0 and L // 4 <= li < L - L // 14):
-            return None
-        hb = st.seg_head_bias_hop1 if (st.seg_bias_mode == 2 and li < L // 2 and st.seg_head_bias_hop1 is not None) \
-            else st.seg_head_bias
-        return hb.reshape(self.cfg.n_heads, -1).to(torch.float32).contiguous()
+    def _seg_bias(self, st: VAULTv3State, li: int) -> Optional[torch.Tensor]:
+        """The bias rows of layer li on the segment span (runtime/vault3.c:1976-1988): the early buffer
+        (hop-1 in mode 2, else arch / sup) in [L/4, L/2), the late one in [L/2, L - L/14), none
+        elsewhere."""
+        lo, mid, hi = control.biased_layers(self.cfg.n_layers)
+        return st.bias_early if lo <= li < mid else st.bias_late if mid <= li < hi else None
 
     def _layers(self, x: torch.Tensor, st: VAULTv3State, pos: int, seg_active: bool) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
         """Chunk prefill (batch 1): run all layers in place on x [N, d], the N tokens at slots [0, N)
@@ -813,12 +874,14 @@ class VAULTv3ForCausalLM:
         st = self.new_state(1, seg_budget=bud)
         seg_active = self._seg_active(st, 1)
         limit = min(cfg.max_sink, W, st.sink_cap)
+        pin_at = []                     # the pin count each early position saw (resonance, quarantine)
         for p in range(min(L, limit + 1)):
             if st.pin_locked:
                 break
             self._auto_pin(st, int(ids_all[p]), p)
-        outs = []
-        last = None
+            pin_at.append(st.n_pin)
+        n_pin_at = lambda p: pin_at[p] if p < len(pin_at) else st.n_pin
+        outs = []                       # ("h", hidden rows) of chunk kernels, ("l", logits) of steps
         for ci in range((L + W - 1) // W):
             r0, r1 = ci * W, min(L, (ci + 1) * W)
             clen = r1 - r0
@@ -826,6 +889,13 @@ class VAULTv3ForCausalLM:
             if ci > 0:
                 self._boundary(st, seg_active)
             ch = ids_all[r0:r1]
+            if st.res is not None:
+                st.tok_cur_h[:clen] = ch.numpy().astype(np.uint32)
+                if self._chunk_resonates(st, r0, clen, seg_active, n_pin_at):
+                    # resonance active somewhere in the chunk: the step path, token by token
+                    rows = [self._advance(st, ch[j:j + 1], boundary=False) for j in range(clen)]
+                    outs.append(("l", torch.cat(rows, dim=0)))
+                    continue
             st.tok_cur[0, :clen].copy_(ch.to(torch.int32))
             if seg_active:
                 # the chunk's segment ids (host rule, the prompt is on the host), then the open
@@ -845,10 +915,20 @@ class VAULTv3ForCausalLM:
             if seg_active:
                 self._score(st, feats, T=clen, c0=0, first=not st.ema_ready)
                 st.ema_ready = True
-            if all_logits:
-                outs.append(x)
-            last = x[-1:]
+                if st.res is not None:
+                    for j in range(clen):
+                        if self._spoofed(st, j, r0 + j, n_pin_at(r0 + j)):
+                            st.sc_cur[j:j + 1].fill_(-1.0e30)
+            outs.append(("h", x if all_logits else x[-1:]))
         st.pos = L
-        st.seg_bias_active = False
-        h = torch.cat(outs, dim=0) if all_logits else last
-        return h, st
+        if not all_logits:
+            kind, t = outs[-1]
+            return (t[-1:] if kind == "h" else None), st, (None if kind == "h" else t[-1:])
+        return None, st, torch.cat([self._logits(t) if kind == "h" else t for kind, t in outs], dim=0)
+
+    def _chunk_resonates(self, st: VAULTv3State, r0: int, clen: int, seg_active: bool, n_pin_at) -> bool:
+        """Whether the query resonance is active at some position of the chunk [r0, r0 + clen) (the
+        host rings hold the previous chunk and this chunk's tokens)."""
+        if not seg_active or r0 < 2 * self.cfg.window or st.res.mem_cnt == 0:
+            return False
+        return any(st.res.update(st.tok_prev_h, st.tok_cur_h, j, r0 + j, n_pin_at(r0 + j)) for j in range(clen))

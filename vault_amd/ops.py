@@ -557,6 +557,24 @@ def argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Te
     return out
 
 
+def topk(logits: torch.Tensor, T: int, ws: Optional["Workspace"] = None):
+    """[B, V] fp32 -> (int64 [B, T], fp32 [B, T]) on the device: the T (<= 256) largest logits of each
+    row, value desc, index asc (vgx_topk; NaN never a candidate, short rows padded with -1 / -inf)."""
+    _need(logits, torch.float32, "logits")
+    B, V = logits.shape
+    if logits.stride(1) != 1:
+        raise ValueError("logits rows must be contiguous")
+    lib = L.load()
+    need = int(lib.vgx_topk_workspace_bytes(B, V, T))
+    L.check(0 if need >= 0 else need, "vgx_topk_workspace_bytes")
+    buf = (ws or Workspace(logits.device)).get(max(need, 1))
+    idx = torch.empty(B, T, dtype=torch.int64, device=logits.device)
+    val = torch.empty(B, T, dtype=torch.float32, device=logits.device)
+    L.check(lib.vgx_topk(logits.data_ptr(), logits.stride(0), B, V, int(T), idx.data_ptr(), val.data_ptr(),
+                         buf.data_ptr(), buf.numel(), _stream(logits.device)), "vgx_topk")
+    return idx, val
+
+
 def sample_topk(logits: torch.Tensor, k: int, temp: float, rng: torch.Tensor,
                 out: Optional[torch.Tensor] = None, ws: Optional["Workspace"] = None) -> torch.Tensor:
     """Top-k sampling per row with the rows' xorshift64 states ``rng`` (uint64 as int64 [B], updated in
