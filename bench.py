@@ -159,10 +159,32 @@ def attention_kernel(dev, reps: int = 20):
         for sp in sets:
             ops.attn_decode(q, sp, out=out, ws=ws)
     us = graph_time_us(run, len(sets), reps=reps)
+    # the same calls over one KV copy (7.3 MB, resident in the last-level cache): reported separately
+    warm = graph_time_us(lambda: [ops.attn_decode(q, base, out=out, ws=ws) for _ in sets], len(sets), reps=reps)
     return {"kernel": "attn_decode_kernel<fp32 KV, 6 heads per KV group, D/16 = 8, 4 waves, 4 keys per DPP row> "
                       "+ attn_merge_kernel (batch 1, 12 q / 2 KV heads, D = 128, 3584 keys)",
             "calls": reps * len(sets), "avg_us": us, "bytes_per_launch": ATTN_ALGO_BYTES,
-            "gbs": ATTN_ALGO_BYTES / us / 1e3}
+            "gbs": ATTN_ALGO_BYTES / us / 1e3, "cache_resident_us": round(warm, 3)}
+
+
+def copy_peak(dev, reps: int = 20):
+    """Measured HBM copy rate: torch's elementwise negation over 1 GiB (read + written once), HIP events
+    around ``reps`` launches on the current stream; bytes moved / time."""
+    import torch
+    n = (1 << 30) // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    e0, e1 = _events()
+    e0.record()
+    for _ in range(reps):
+        torch.neg(src, out=dst)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    del src, dst
+    return {"bytes": 2 * n * 4, "us": round(us, 1), "gbs": round(2 * n * 4 / us / 1e3, 1)}
 
 
 def gateup_kernel(model, rounds: int = 20):
@@ -535,7 +557,7 @@ def main() -> int:
         return 0
     dom = attention_kernel(dev)
     _log(f"roofline kernel (attention + merge): {dom['avg_us']:.2f} us, {dom['gbs']:.0f} GB/s")
-    kernels = {"gateup_gemv": gateup_kernel(model)}
+    kernels = {"gateup_gemv": gateup_kernel(model), "copy_peak": copy_peak(dev)}
     if not args.no_kernels:
         kernels["gemv"] = gemv_figures(dev)
         kernels["attn_decode"] = attn_figures(dev)
@@ -571,7 +593,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": dom["kernel"], "avg_us": round(dom["avg_us"], 3),
-                     "bytes_per_launch": dom["bytes_per_launch"]},
+                     "bytes_per_launch": dom["bytes_per_launch"], "cache_resident_us": dom["cache_resident_us"]},
         "cpu_baseline": cpu,
         "kernels": kernels,
     }

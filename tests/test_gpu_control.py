@@ -80,6 +80,20 @@ def test_resonance_stream_matches_reference_runtime(word_model, kind):
         assert st.seg_bias_mode == fl["seg_bias_active"], (kind, i)
         assert st.n_pin == rt.info()["n_pin"], (kind, i)
         modes.append(st.seg_bias_mode)
+        if st.seg_bias_mode:
+            # the reference's per-head layout (free heads 0, arch, sup; hop-1 on the biased heads in mode 2)
+            _, _, arch, sup, hop1 = rt.res_state()
+            cls = control.head_classes(cfg.n_heads, cfg.n_kv_heads)
+            late = st.seg_head_bias[0, :, 0].cpu().numpy()
+            for h, k in enumerate(cls):
+                want_h = np.zeros_like(arch) if k == 0 else arch if k == 1 else sup
+                assert np.array_equal(late[h].view(np.uint32), want_h.view(np.uint32)), (kind, i, h)
+            if st.seg_bias_mode == 2:
+                early = st.seg_head_bias_hop1[0, :, 0].cpu().numpy()
+                for h, k in enumerate(cls):
+                    assert np.array_equal(early[h], np.zeros_like(hop1) if k == 0 else hop1), (kind, i, h)
+            else:
+                assert st.seg_head_bias_hop1 is None
         # this step's segment score: quarantined exactly when the reference's is, else to fp32 precision
         s_ref, s_dev = float(rt.rings(cfg.window)[2][c]), float(st.sc_cur[c])
         assert (s_ref <= -1e29) == (s_dev <= -1e29), (kind, i)

@@ -196,6 +196,23 @@ class VAULTv3State:
         return self.bank_seg[:self.mem_cnt].to("cpu", torch.int64)
 
     @property
+    def seg_head_bias(self) -> Optional[torch.Tensor]:
+        """While a resonance mode is active: the (1, H, 1, M) per-head bias of the late biased layers on
+        the bank's M slots (src/vault_v3_model.py:1629-1641, 1711-1716), a view of the device rows."""
+        if not self.seg_bias_active or self.res is None:
+            return None
+        M = self.res.mem_cnt
+        return self.bias_late[:, :M].reshape(1, -1, 1, M)
+
+    @property
+    def seg_head_bias_hop1(self) -> Optional[torch.Tensor]:
+        """In mode 2: the (1, H, 1, M) hop-1 bias of the early biased layers, else None."""
+        if self.seg_bias_mode != 2 or self.res is None:
+            return None
+        M = self.res.mem_cnt
+        return self.bias_early[:, :M].reshape(1, -1, 1, M)
+
+    @property
     def layers(self) -> List[LayerView]:
         """Per-layer views (built on access: a stored list would make a reference cycle, leaving the
         state to the cyclic garbage collector, which may run while a decode graph is captured)."""
