@@ -750,6 +750,275 @@ __global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const u
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Decode batches, K-split projections: qgemm_split_kernel.  A workgroup of 4 waves owns 128 weight
+// rows (32 row-quads; wave w takes row-quads 8 w .. 8 w + 7 as two 16-row MFMA tiles) x 16 activation
+// rows x one K range of at most kSplitMaxBlocks blocks, and writes the range's partial sums.
+//  * Weights: every wave requests its whole K range at the start, as contiguous 16-byte loads (the
+//    blocks of one row-quad are adjacent in the packed layout: for Q4_0 lane l loads bytes 16 (l % 16)
+//    .. + 15 of the chunk's 256-byte run of row-quad 4 h + l / 16) and its scales as one dword per lane.
+//    The fragment-shaped loads of qgemm_small_kernel (a lane's 4-8 bytes, four row-quads 3 KB apart per
+//    instruction) measured twice as slow to stream.  Per 4-block chunk the wave passes the loaded words
+//    through a wave-private LDS area into the MFMA layout: lane (row l % 16, K group l / 16) reads its
+//    four blocks' words of one row as a single 16-byte (Q4_0) or two (Q8_0) LDS loads.
+//  * The loads are unconditional buffer loads: rows past the weight and chunks past the range use
+//    offsets past the buffer, which read as zero without a memory access, so the compiler's waits count
+//    exactly the loads a chunk needs and its math starts when its own words have arrived.
+//  * Activations: the whole K range of the 16 rows is staged once into LDS, as bf16 hi and fp16 lo16
+//    in the K-slot order of the weight fragments, with the per-block sums of the pieces; blocks past
+//    the range are staged as zeros (their weights, read from the neighbouring blocks, then add 0).
+//  * Q4_0 fragments: a lane's word holds bytes 4 lg .. 4 lg + 3 of its row's block, i.e. weights
+//    4 lg + i (low nibbles) and 16 + 4 lg + i (high nibbles); as bf16 16 + n and fp16 1 + n / 16
+//    (offset 24, as the tiled kernel); K-slot order 4lg + {0, 2, 1, 3}, 16 + 4lg + {0, 2, 1, 3}.
+//    Q8_0: the tiled kernel's fragments of bytes 8 lg .. 8 lg + 7 (order 0 2 1 3 4 6 5 7, offset 128).
+constexpr int kSplitMaxBlocks = 16;            // blocks per split (4 chunks)
+constexpr int kSplitMaxChunks = kSplitMaxBlocks / kCK;
+constexpr uint32_t kPastEnd = 0x80000000u;     // a buffer offset past every weight: reads zero
+
+template <int DT>
+struct SplitGeom {
+    static constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;             // bytes of one row's block
+    static constexpr int NLD = DT == VGX_Q8_0 ? 4 : 2;              // 16-byte weight loads per lane and chunk
+    static constexpr int ROW = 4 * QB + 16;                         // LDS bytes per weight row (4 blocks + pad)
+    static constexpr int SCR = 48;                                  // LDS bytes per row-quad of scales
+    static constexpr int WAVE = 32 * ROW + 8 * SCR;                 // LDS bytes per wave
+};
+
+// LDS of one workgroup: the staged activations of kSplitMaxChunks chunks, then 4 waves' areas.
+constexpr int split_lds_bytes(int dt) {
+    return kSplitMaxChunks * (2 * 16 * kSRow * 2 + 16 * kCK * 4) +
+           4 * (dt == VGX_Q8_0 ? SplitGeom<VGX_Q8_0>::WAVE : SplitGeom<VGX_Q4_0>::WAVE);
+}
+static_assert(split_lds_bytes(VGX_Q8_0) <= 64 * 1024, "static LDS of qgemm_split_kernel");
+
+// Q4_0 fragments of one lane's word (bytes 4 lg .. 4 lg + 3 of its row's block).
+__device__ __forceinline__ void q4_word_frags(uint32_t w, bf16x8_t &fb, f16x8_t &fh) {
+    uint32_t o[4], h[4];
+    o[0] = ((w << 3) & 0x00780078u) | 0x41804180u;          // low nibbles of bytes 0, 2
+    o[1] = ((w >> 5) & 0x00780078u) | 0x41804180u;          // bytes 1, 3
+    o[2] = ((w >> 1) & 0x00780078u) | 0x41804180u;          // high nibbles of bytes 0, 2
+    o[3] = ((w >> 9) & 0x00780078u) | 0x41804180u;          // bytes 1, 3
+    h[0] = ((w << 6) & 0x03C003C0u) | 0x3C003C00u;
+    h[1] = ((w >> 2) & 0x03C003C0u) | 0x3C003C00u;
+    h[2] = ((w << 2) & 0x03C003C0u) | 0x3C003C00u;
+    h[3] = ((w >> 6) & 0x03C003C0u) | 0x3C003C00u;
+    fb = __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
+    fh = __builtin_bit_cast(f16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+}
+
+template <int DT, bool NORM>
+__global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
+                                                             int nblk, int w_bytes, const float *__restrict__ x,
+                                                             int64_t ldx, const float *__restrict__ lnw,
+                                                             int64_t batch, float *__restrict__ part,
+                                                             float *__restrict__ part_ssq, int kper) {
+    using G = SplitGeom<DT>;
+    constexpr int QB = G::QB;
+    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 24.0f;
+    constexpr int R = 16;                                     // activation rows
+    constexpr int F4 = R * kCK * 8 / 256;                     // staged float4 per thread and chunk
+    __shared__ __align__(16) uint8_t smem_dyn[split_lds_bytes(DT)];
+    __shared__ float sinv[R];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int64_t rq_wave = ((int64_t)blockIdx.x * 4 + wave) * 8;
+    const int64_t b0 = (int64_t)blockIdx.y * R;
+    const int blk_lo = (int)blockIdx.z * kper;
+    const int blk_hi = min(nblk, blk_lo + kper);
+    const int n_chunks = (blk_hi - blk_lo + kCK - 1) / kCK;   // 1 .. kSplitMaxChunks
+    const int cols = nblk * QK;
+    // LDS: activations [chunk][plane hi, lo][row][kSRow] bf16 / fp16, block sums [chunk][row][kCK],
+    // then the waves' areas
+    constexpr int PL = R * kSRow * 2;
+    uint16_t *xs = reinterpret_cast<uint16_t *>(smem_dyn);
+    float *ssum = reinterpret_cast<float *>(smem_dyn + kSplitMaxChunks * 2 * PL);
+    uint8_t *wl = smem_dyn + kSplitMaxChunks * (2 * PL + R * kCK * 4) + wave * G::WAVE;
+    uint8_t *wsc = wl + 32 * G::ROW;
+
+    // activations first (their wait then leaves the weight loads in flight)
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)x, 0, (int)(((batch - 1) * ldx + cols) * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t grs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)lnw, 0, NORM ? cols * 4 : 0, 0x00020000);
+    float4 xr[kSplitMaxChunks][F4], gr[kSplitMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kSplitMaxChunks; ++c) {
+        const int bl = (tid >> 3) & 3, j4 = tid & 7;
+        const uint32_t ko = (uint32_t)(((blk_lo + c * kCK + bl) * QK + j4 * 4) * 4);
+        if constexpr (NORM) {
+            const auto g = __builtin_amdgcn_raw_buffer_load_b128(grs, ko, 0, 0);
+            gr[c] = make_float4(__uint_as_float(g[0]), __uint_as_float(g[1]), __uint_as_float(g[2]), __uint_as_float(g[3]));
+        }
+#pragma unroll
+        for (int i = 0; i < F4; ++i) {
+            const int64_t br = b0 + ((tid + 256 * i) >> 5);
+            const uint32_t o = br < batch ? (uint32_t)(br * ldx * 4) + ko : kPastEnd;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(xrs, o, 0, 0);
+            xr[c][i] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+        }
+    }
+
+    // weights and scales of the whole range
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, w_bytes, 0x00020000);
+    uint32_t wv[G::NLD], sv;
+#pragma unroll
+    for (int h = 0; h < G::NLD; ++h) {
+        const int64_t rq = rq_wave + (DT == VGX_Q8_0 ? 2 * h + (lane >> 5) : 4 * h + (lane >> 4));
+        wv[h] = rq < n_rq ? (uint32_t)(rq * nblk * 4 * QB) + (uint32_t)((lane & (DT == VGX_Q8_0 ? 31 : 15)) * 16)
+                          : kPastEnd;
+    }
+    {
+        const int64_t rq = rq_wave + (lane >> 3);
+        sv = rq < n_rq ? (uint32_t)(soff + rq * nblk * 8) + (uint32_t)((lane & 7) * 4) : kPastEnd;
+    }
+    // scales of every chunk first, then the quants chunk by chunk (a chunk's wait then leaves the later
+    // chunks' loads in flight)
+    uint4 wr[kSplitMaxChunks][G::NLD];
+    uint32_t sr[kSplitMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kSplitMaxChunks; ++c)
+        sr[c] = __builtin_amdgcn_raw_buffer_load_b32(wrs, sv, c < n_chunks ? (blk_lo + c * kCK) * 8 : 0x40000000, 0);
+#pragma unroll
+    for (int c = 0; c < kSplitMaxChunks; ++c) {
+        const int so = c < n_chunks ? (blk_lo + c * kCK) * 4 * QB : 0x40000000;   // past the range: past the buffer
+#pragma unroll
+        for (int h = 0; h < G::NLD; ++h) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, wv[h], so, 0);
+            wr[c][h] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    }
+
+    // stage the activations: bf16 hi, fp16 lo16, block sums; sum x^2 for the RMSNorm
+    float ssq[F4];
+#pragma unroll
+    for (int i = 0; i < F4; ++i) ssq[i] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kSplitMaxChunks; ++c) {
+        if (c >= n_chunks) break;
+#pragma unroll
+        for (int i = 0; i < F4; ++i) {
+            const int f = tid + 256 * i, row = f >> 5, bl = (f >> 3) & 3, j4 = f & 7;
+            const bool in = blk_lo + c * kCK + bl < blk_hi;
+            const float e[4] = {in ? xr[c][i].x : 0.0f, in ? xr[c][i].y : 0.0f, in ? xr[c][i].z : 0.0f,
+                                in ? xr[c][i].w : 0.0f};
+            float u[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if constexpr (NORM) {
+                    ssq[i] = fmaf(e[k], e[k], ssq[i]);
+                    const float g = k == 0 ? gr[c].x : k == 1 ? gr[c].y : k == 2 ? gr[c].z : gr[c].w;
+                    u[k] = g * e[k];
+                } else {
+                    u[k] = e[k];
+                }
+            }
+            uint2 hw, lw;
+            float r02[2], r13[2];
+            split_bf16_f16x2(u[0], u[2], hw.x, lw.x, r02);     // stored order 0, 2, 1, 3
+            split_bf16_f16x2(u[1], u[3], hw.y, lw.y, r13);
+            float sum = (r02[0] + r13[0]) + (r02[1] + r13[1]);
+            const int pos = DT == VGX_Q4_0 ? 8 * (j4 & 3) + 4 * (j4 >> 2) : 4 * j4;
+            *reinterpret_cast<uint2 *>(xs + ((c * 2) * R + row) * kSRow + bl * QK + pos) = hw;
+            *reinterpret_cast<uint2 *>(xs + ((c * 2 + 1) * R + row) * kSRow + bl * QK + pos) = lw;
+            sum += __shfl_xor(sum, 1, kWave);
+            sum += __shfl_xor(sum, 2, kWave);
+            sum += __shfl_xor(sum, 4, kWave);
+            if (j4 == 0) ssum[(c * R + row) * kCK + bl] = sum;
+        }
+    }
+    __syncthreads();
+
+    f32x4_t acc[2];
+    acc[0] = acc[1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < kSplitMaxChunks; ++c) {
+        if (c >= n_chunks) break;
+        // the chunk's words into the MFMA layout through the wave's LDS area
+#pragma unroll
+        for (int h = 0; h < G::NLD; ++h) {
+            const uint4 v = wr[c][h];
+            if constexpr (DT == VGX_Q4_0) {
+                const int row = (4 * h + (lane >> 4)) * 4 + (lane & 3), u = (lane & 15) >> 2;
+                uint8_t *p = wl + row * G::ROW + u * 4;
+                *reinterpret_cast<uint32_t *>(p) = v.x;
+                *reinterpret_cast<uint32_t *>(p + 16) = v.y;
+                *reinterpret_cast<uint32_t *>(p + 32) = v.z;
+                *reinterpret_cast<uint32_t *>(p + 48) = v.w;
+            } else {
+                const int row = (2 * h + (lane >> 5)) * 4 + ((lane >> 1) & 3), u = (lane & 31) >> 3;
+                uint8_t *p = wl + row * G::ROW + (2 * (lane & 1)) * 32 + u * 8;
+                *reinterpret_cast<uint2 *>(p) = make_uint2(v.x, v.y);
+                *reinterpret_cast<uint2 *>(p + 32) = make_uint2(v.z, v.w);
+            }
+        }
+        *reinterpret_cast<uint32_t *>(wsc + (lane >> 3) * G::SCR + (lane & 7) * 4) = sr[c];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint8_t *rp = wl + (16 * t + l16) * G::ROW + lg * QB;
+            const uint4 s0 = *reinterpret_cast<const uint4 *>(wsc + (4 * t + lg) * G::SCR);
+            const uint4 s1 = *reinterpret_cast<const uint4 *>(wsc + (4 * t + lg) * G::SCR + 16);
+            uint32_t wq4[4];
+            uint2 wq8[4];
+            if constexpr (DT == VGX_Q4_0) {
+                const uint4 a = *reinterpret_cast<const uint4 *>(rp);
+                wq4[0] = a.x; wq4[1] = a.y; wq4[2] = a.z; wq4[3] = a.w;
+            } else {
+                const uint4 a = *reinterpret_cast<const uint4 *>(rp), b = *reinterpret_cast<const uint4 *>(rp + 16);
+                wq8[0] = make_uint2(a.x, a.y); wq8[1] = make_uint2(a.z, a.w);
+                wq8[2] = make_uint2(b.x, b.y); wq8[3] = make_uint2(b.z, b.w);
+            }
+            const uint2 scu[4] = {make_uint2(s0.x, s0.y), make_uint2(s0.z, s0.w), make_uint2(s1.x, s1.y),
+                                  make_uint2(s1.z, s1.w)};
+#pragma unroll
+            for (int u = 0; u < kCK; ++u) {
+                bf16x8_t af;
+                f16x8_t ah;
+                if constexpr (DT == VGX_Q4_0) q4_word_frags(wq4[u], af, ah);
+                else tile_a_frags<DT>(wq8[u], lg, af, ah);
+                const float d[4] = {half_bits_to_float(scu[u].x), half_bits_to_float(scu[u].x >> 16),
+                                    half_bits_to_float(scu[u].y), half_bits_to_float(scu[u].y >> 16)};
+                const uint4 xh = *reinterpret_cast<const uint4 *>(xs + ((c * 2) * R + l16) * kSRow + u * QK + 8 * lg);
+                const uint4 xl = *reinterpret_cast<const uint4 *>(xs + ((c * 2 + 1) * R + l16) * kSRow + u * QK + 8 * lg);
+                const float corr = OFF * ssum[(c * R + l16) * kCK + u];
+                f32x4_t pr = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, __builtin_bit_cast(bf16x8_t, xh), pr, 0, 0, 0);
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, __builtin_bit_cast(f16x8_t, xl), pr, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(d[i], pr[i] - corr, acc[t][i]);
+            }
+        }
+        // this chunk's LDS reads are done before the next chunk's writes (in order within the wave)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    if constexpr (NORM) {
+#pragma unroll
+        for (int i = 0; i < F4; ++i) {
+            const float t = xor16_sum(row16_sum(ssq[i]));
+            if ((tid & 31) == 0) sinv[(tid >> 5) + 8 * i] = t;
+        }
+        __syncthreads();
+        if (blockIdx.x == 0 && tid < R && b0 + tid < batch)
+            part_ssq[(int64_t)blockIdx.z * batch + b0 + tid] = sinv[tid];
+    }
+    const int64_t bb = b0 + l16;
+    if (bb < batch) {
+        const int64_t rows_p = n_rq * 4;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int64_t crq = rq_wave + 4 * t + lg;
+            if (crq >= n_rq) continue;
+            *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + bb) * rows_p + crq * 4) =
+                make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+        }
+    }
+}
+
 // Sum of the K-split partials + epilogue.  One thread per output (b, row); SwiGLU reads the gate and
 // up sums of packed row-quad q (sub-rows k and 2 + k) for output row 2 q + k.
 // part_ssq (when not null): per-split sum x^2 of every activation row; the sums are then scaled by
@@ -821,7 +1090,8 @@ void reduce_launch(const float *part, int ks, int64_t batch, int64_t rows_p, int
                                        rows_p, rows_out, bias, y, ldy, part_ssq, cols, eps)
     if (ks <= 4) VGX_RED(4);
     else if (ks <= 8) VGX_RED(8);
-    else VGX_RED(16);
+    else if (ks <= 16) VGX_RED(16);
+    else VGX_RED(32);
 #undef VGX_RED
 }
 
@@ -838,7 +1108,9 @@ inline int64_t split_bytes(int64_t batch, int64_t cols) {
 }
 
 constexpr int kMaxKSplit = 16;
-static_assert(kMaxKSplit <= 16, "split bound of qgemm_reduce_kernel and qkv_split_rope_kernel");
+// Splits a reduce launch (and qkv_split_rope_kernel) sums: the largest compile-time bound.
+constexpr int kReduceMaxSplits = 32;
+static_assert(kMaxKSplit <= kReduceMaxSplits, "split bound of qgemm_reduce_kernel and qkv_split_rope_kernel");
 constexpr int kTargetWaves = 2048;
 
 // K splits: enough waves to fill the GPU, at least 8 blocks per split.
@@ -875,13 +1147,38 @@ constexpr int64_t kSmallMaxBatch = 64;
 // (batch-32 decode 9.10K against 9.03K tokens/s).
 inline int small_nc(int64_t batch, int64_t n_rq) { return batch > 16 && n_rq >= 16384 ? 2 : 1; }
 
-// K splits of the small-batch kernel: as choose_ksplit, with whole chunks per split.
+// K splits of the decode-batch path: as choose_ksplit, with whole chunks per split.  When the GPU
+// wants more than one split, a split holds at most kSplitMaxBlocks blocks (qgemm_split_kernel stages
+// its whole range; more splits for long rows: the 1536 x 8960 down projection takes 18); one split
+// (tall weights such as the LM head) keeps qgemm_small_kernel's chunk loop.
 inline int small_ksplit(int64_t n_rq, int64_t batch, int nblk, int *kper) {
     const int ks0 = choose_ksplit(n_rq, batch, small_nc(batch, n_rq), nblk);
     int kp = (nblk + ks0 - 1) / ks0;
     kp = (kp + kCK - 1) / kCK * kCK;
+    if (ks0 > 1 && kp > kSplitMaxBlocks && (nblk + kSplitMaxBlocks - 1) / kSplitMaxBlocks <= kReduceMaxSplits)
+        kp = kSplitMaxBlocks;
     *kper = kp;
     return (nblk + kp - 1) / kp;
+}
+
+// Whether qgemm_split_kernel takes a split projection: splits of at most kSplitMaxBlocks blocks and a
+// weight (quants + scales) whose byte offsets fit the 31-bit buffer range.
+inline bool use_split_kernel(int ks, int kper, int64_t w_bytes) {
+    return ks > 1 && kper <= kSplitMaxBlocks && w_bytes < ((int64_t)1 << 30);
+}
+
+// qgemm_split_kernel over grid (row tiles, 16-row activation tiles, splits); writes part / pssq.
+void split_kernel_launch(int dtype, const uint8_t *w, int64_t soff, int64_t n_rq, int nblk, const float *x,
+                         int64_t ldx, const float *norm_w, int64_t batch, float *part, float *pssq, int ks, int kper,
+                         hipStream_t st) {
+    const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 15) / 16), (unsigned)ks);
+    const int wb = (int)(soff + n_rq * nblk * 8);
+#define VGX_SK(DT, NORM)                                                                                       \
+    hipLaunchKernelGGL((qgemm_split_kernel<DT, NORM>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, wb, x, ldx, \
+                       norm_w, batch, part, pssq, kper)
+    if (dtype == VGX_Q8_0) { if (norm_w) VGX_SK(VGX_Q8_0, true); else VGX_SK(VGX_Q8_0, false); }
+    else { if (norm_w) VGX_SK(VGX_Q4_0, true); else VGX_SK(VGX_Q4_0, false); }
+#undef VGX_SK
 }
 
 // Workspace of the small-batch path: K-split partials, then the per-split sum x^2 of every row.
@@ -1010,9 +1307,13 @@ int split_proj_launch(int dtype, const void *wp, int64_t rows, int64_t cols, con
     int kper = 0;
     const int ks = small_ksplit(n_rq, batch, nblk, &kper);
     const int64_t soff = gemm_scale_off(dtype, rows, cols);
+    const auto *w = static_cast<const uint8_t *>(wp);
+    if (use_split_kernel(ks, kper, soff + n_rq * nblk * 8)) {
+        split_kernel_launch(dtype, w, soff, n_rq, nblk, x, ldx, norm_w, batch, part, pssq, ks, kper, st);
+        return ks;
+    }
     const int nc = small_nc(batch, n_rq);
     const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 16 * nc - 1) / (16 * nc)), (unsigned)ks);
-    const auto *w = static_cast<const uint8_t *>(wp);
 #define VGX_SP(DT, NC, NORM)                                                                                      \
     hipLaunchKernelGGL((qgemm_small_kernel<DT, NC, EPI_STORE, true, NORM>), grid, dim3(256), 0, st, w, soff, n_rq, \
                        nblk, rows, x, ldx, norm_w, eps, batch, nullptr, nullptr, (int64_t)0, part, pssq, kper)
@@ -1086,6 +1387,8 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
         const int nc = small_nc(batch, n_rq);
         const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 16 * nc - 1) / (16 * nc)), (unsigned)ks);
         const auto *w = static_cast<const uint8_t *>(w_packed);
+        const bool sk = use_split_kernel(ks, kper, soff0 + n_rq * nblk * 8);
+        if (sk) split_kernel_launch(dtype, w, soff0, n_rq, nblk, x, ldx, norm_w, batch, part, pssq, ks, kper, st0);
 #define VGX_SG(DT, NC, EPI, SP, NORM)                                                                         \
     hipLaunchKernelGGL((qgemm_small_kernel<DT, NC, EPI, SP, NORM>), grid, dim3(256), 0, st0, w, soff0, n_rq, nblk, \
                        rows, x, ldx, norm_w, eps, batch, bias, y, ldy, part, pssq, kper)
@@ -1097,8 +1400,12 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
         else if (epilogue == VGX_EPI_ACCUM) VGX_SG_N(DT, NC, EPI_ACCUM, false);                               \
         else VGX_SG_N(DT, NC, EPI_STORE, false);                                                              \
     } while (0)
-        if (dtype == VGX_Q8_0) { if (nc == 1) VGX_SG_E(VGX_Q8_0, 1); else VGX_SG_E(VGX_Q8_0, 2); }
-        else { if (nc == 1) VGX_SG_E(VGX_Q4_0, 1); else VGX_SG_E(VGX_Q4_0, 2); }
+        if (sk) {
+        } else if (dtype == VGX_Q8_0) {
+            if (nc == 1) VGX_SG_E(VGX_Q8_0, 1); else VGX_SG_E(VGX_Q8_0, 2);
+        } else {
+            if (nc == 1) VGX_SG_E(VGX_Q4_0, 1); else VGX_SG_E(VGX_Q4_0, 2);
+        }
 #undef VGX_SG_E
 #undef VGX_SG_N
 #undef VGX_SG
@@ -1229,7 +1536,7 @@ int vgx_qkv_rope_batch(int q_wdtype, const void *wq, const float *bq, int kv_wdt
                        (int)H, (int)G, (int)D, table, table_rstride, step, q_out, ldq, k_rot, k_raw, v_dst,       \
                        dst_bstride, dst_gstride, dst_rstride, sink_k_raw, sink_v, sink_bstride, sink_gstride,     \
                        sink_rstride)
-#define VGX_QSR_K(KV) do { if (km <= 4) VGX_QSR(KV, 4); else if (km <= 8) VGX_QSR(KV, 8); else VGX_QSR(KV, 16); } while (0)
+#define VGX_QSR_K(KV) do { if (km <= 4) VGX_QSR(KV, 4); else if (km <= 8) VGX_QSR(KV, 8); else if (km <= 16) VGX_QSR(KV, 16); else VGX_QSR(KV, 32); } while (0)
     if (kv_dtype == VGX_F32) VGX_QSR_K(VGX_F32); else VGX_QSR_K(VGX_BF16);
 #undef VGX_QSR_K
 #undef VGX_QSR
