@@ -116,12 +116,30 @@ struct RowRaw {
     uint32_t w[W];
 };
 
+// fp32 rows of D = 128: a lane's 8 elements are two quads 64 apart (dims 4 l .. + 3 and 64 + 4 l ..),
+// so each load instruction of a DPP row reads one contiguous half row (256 bytes) instead of 16-byte
+// pieces with 16-byte gaps; the query, the accumulators and the LDS combine use the same mapping.
+template <int KV, int DPL>
+constexpr bool kSpreadQuads = KV == VGX_F32 && DPL == 8;
+
+// Element offset in its row of quad d4 of lane l16.
+template <int KV, int DPL>
+__device__ __forceinline__ int lane_quad(int l16, int d4) {
+    return kSpreadQuads<KV, DPL> ? d4 * 64 + l16 * 4 : l16 * DPL + 4 * d4;
+}
+
 template <int KV, int DPL>
 __device__ __forceinline__ void load_raw(const void *base, int64_t elem_off, RowRaw<KV, DPL> &r) {
     constexpr int W = RowRaw<KV, DPL>::W;
     const uint32_t *p = reinterpret_cast<const uint32_t *>(static_cast<const char *>(base) +
                                                            elem_off * (KV == VGX_F32 ? 4 : 2));
-    if constexpr (W % 4 == 0) {
+    if constexpr (kSpreadQuads<KV, DPL>) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint4 t = *reinterpret_cast<const uint4 *>(p + 64 * i);
+            r.w[4 * i] = t.x; r.w[4 * i + 1] = t.y; r.w[4 * i + 2] = t.z; r.w[4 * i + 3] = t.w;
+        }
+    } else if constexpr (W % 4 == 0) {
 #pragma unroll
         for (int i = 0; i < W / 4; ++i) {
             const uint4 t = reinterpret_cast<const uint4 *>(p)[i];
@@ -217,7 +235,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
         const void *vb = pick4(s, sp.v[0], sp.v[1], sp.v[2], sp.v[3]);
         const int64_t o = (int64_t)b * pick4(s, sp.bstride[0], sp.bstride[1], sp.bstride[2], sp.bstride[3]) +
                           (int64_t)g * pick4(s, sp.gstride[0], sp.gstride[1], sp.gstride[2], sp.gstride[3]) +
-                          (int64_t)(c.y + row * KB) * D + l16 * DPL;
+                          (int64_t)(c.y + row * KB) * D + lane_quad<KV, DPL>(l16, 0);
         // rows past the split's end in this span re-read its last row (in bounds; masked at use)
         const int last = pick4(s, hi[0], hi[1], hi[2], hi[3]) - 1 - c.y - row * KB;
 #pragma unroll
@@ -232,10 +250,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     float qr[GRP][DPL];
 #pragma unroll
     for (int hh = 0; hh < GRP; ++hh) {
-        const float *qp = q + (int64_t)b * ldq + ((int64_t)g * GRP + hh) * D + l16 * DPL;
+        const float *qp = q + (int64_t)b * ldq + ((int64_t)g * GRP + hh) * D;
 #pragma unroll
         for (int d4 = 0; d4 < DPL / 4; ++d4) {
-            const float4 t = reinterpret_cast<const float4 *>(qp)[d4];
+            const float4 t = *reinterpret_cast<const float4 *>(qp + lane_quad<KV, DPL>(l16, d4));
             qr[hh][4 * d4] = t.x; qr[hh][4 * d4 + 1] = t.y; qr[hh][4 * d4 + 2] = t.z; qr[hh][4 * d4 + 3] = t.w;
         }
     }
@@ -385,7 +403,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
         for (int hh = 0; hh < GRP; ++hh) {
 #pragma unroll
             for (int d4 = 0; d4 < DPL / 4; ++d4)
-                *reinterpret_cast<float4 *>(&red[p][hh][l16 * DPL + 4 * d4]) =
+                *reinterpret_cast<float4 *>(&red[p][hh][lane_quad<KV, DPL>(l16, d4)]) =
                     make_float4(acc[hh][4 * d4], acc[hh][4 * d4 + 1], acc[hh][4 * d4 + 2], acc[hh][4 * d4 + 3]);
             if (l16 == 0) {
                 red[p][hh][D] = m[hh];
