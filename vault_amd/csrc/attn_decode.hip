@@ -48,6 +48,7 @@ struct SpanArgs {
 // agent-scope atomic loads, combines them in split order (deterministic) and resets the counter to
 // zero for the next launch (no memset, so a captured graph replays it).
 constexpr int kTicketMaxSplits = 32;                // splits merged by the last workgroup of a pair
+constexpr int kMergeFast = 8;                       // splits the last workgroup merges in one round trip
 
 template <int GRP, int D>
 __device__ __forceinline__ void store_partial(float *pp, int d, float A, float M, float L) {
@@ -71,6 +72,48 @@ __device__ __forceinline__ void ticket_merge(const float *__restrict__ part_pair
     }
     __syncthreads();
     if (!*flag) return;
+    if (n_splits <= kMergeFast) {
+        // one round trip: every thread requests, for PB outputs at a time, each split's value and the
+        // split's (m, l) of the output's head before using any of them
+        constexpr int PB = 3;
+        for (int t0 = 0; t0 < GRP * D; t0 += nt * PB) {
+            float v[PB][kMergeFast], mm[PB][kMergeFast], ll[PB][kMergeFast];
+#pragma unroll
+            for (int j = 0; j < PB; ++j) {
+                const int t = min(t0 + tid + nt * j, GRP * D - 1);
+                const int hh = t / D, d = t - hh * D;
+#pragma unroll
+                for (int u = 0; u < kMergeFast; ++u) {
+                    const float *pp = part_pair + ((int64_t)min(u, n_splits - 1) * GRP + hh) * SLOT;
+                    v[j][u] = __hip_atomic_load(pp + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    mm[j][u] = __hip_atomic_load(pp + D, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    ll[j][u] = __hip_atomic_load(pp + D + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < PB; ++j) {
+                const int t = t0 + tid + nt * j;
+                if (t >= GRP * D) continue;
+                const int hh = t / D, d = t - hh * D;
+                float M = kNegBig;
+#pragma unroll
+                for (int u = 0; u < kMergeFast; ++u)
+                    if (u < n_splits) M = fmaxf(M, mm[j][u]);
+                float L = 0.0f, A = 0.0f;
+#pragma unroll
+                for (int u = 0; u < kMergeFast; ++u) {
+                    if (u < n_splits) {
+                        const float w = __expf(mm[j][u] - M);
+                        L = fmaf(w, ll[j][u], L);
+                        A = fmaf(w, v[j][u], A);
+                    }
+                }
+                outp[(int64_t)hh * D + d] = A * (1.0f / L);
+            }
+        }
+        if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     float *wm = sc, *wl = sc + GRP * kMaxSplits, *inv = sc + 2 * GRP * kMaxSplits;
     for (int i = tid; i < GRP * n_splits; i += nt) {
         const int hh = i / n_splits, sp = i - hh * n_splits;

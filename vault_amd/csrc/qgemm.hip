@@ -764,13 +764,19 @@ __global__ __launch_bounds__(256, SPLIT ? 3 : 2) void qgemm_small_kernel(const u
 //  * The loads are unconditional buffer loads: rows past the weight and chunks past the range use
 //    offsets past the buffer, which read as zero without a memory access, so the compiler's waits count
 //    exactly the loads a chunk needs and its math starts when its own words have arrived.
-//  * Activations: the whole K range of the 16 rows is staged once into LDS, as bf16 hi and fp16 lo16
-//    in the K-slot order of the weight fragments, with the per-block sums of the pieces; blocks past
-//    the range are staged as zeros (their weights, read from the neighbouring blocks, then add 0).
+//  * Activations: the whole K range of the 16 rows is staged once into LDS, as bf16 hi and fp16 lo in
+//    the K-slot order of the weight fragments, with each block's offset correction (four copies, the
+//    first MFMA's accumulator input); blocks past the range are staged as zeros (their weights, read
+//    from the neighbouring blocks, then add 0).
 //  * Q4_0 fragments: a lane's word holds bytes 4 lg .. 4 lg + 3 of its row's block, i.e. weights
-//    4 lg + i (low nibbles) and 16 + 4 lg + i (high nibbles); as bf16 16 + n and fp16 1 + n / 16
-//    (offset 24, as the tiled kernel); K-slot order 4lg + {0, 2, 1, 3}, 16 + 4lg + {0, 2, 1, 3}.
-//    Q8_0: the tiled kernel's fragments of bytes 8 lg .. 8 lg + 7 (order 0 2 1 3 4 6 5 7, offset 128).
+//    4 lg + i (low nibbles) and 16 + 4 lg + i (high nibbles), K-slot order 4 lg + {0, 1, 2, 3},
+//    16 + 4 lg + {0, 1, 2, 3}.  Each nibble n goes to the low bits of a 16-bit lane beside a constant
+//    high byte with one byte permute per dword: bf16 0x4300 | n = 128 + n, fp16 0x6400 | n = 1024 + n.
+//    The pieces are hi = bf16(16 x), lo = fp16(16 x - hi), so a block's products sum to
+//    sum (n - 8)(hi + lo) + 136 sum hi + 1032 sum lo; the staged correction holds -(136 sum hi +
+//    1032 sum lo) and the partials are scaled by 1/16 at the end.
+//    Q8_0: the tiled kernel's fragments of bytes 8 lg .. 8 lg + 7 (order 0 2 1 3 4 6 5 7, offset 128
+//    against the pieces bf16 hi and fp16 16 (x - hi)).
 constexpr int kSplitMaxBlocks = 16;            // blocks per split (4 chunks)
 constexpr int kSplitMaxChunks = kSplitMaxBlocks / kCK;
 constexpr uint32_t kPastEnd = 0x80000000u;     // a buffer offset past every weight: reads zero
@@ -786,24 +792,26 @@ struct SplitGeom {
 
 // LDS of one workgroup: the staged activations of kSplitMaxChunks chunks, then 4 waves' areas.
 constexpr int split_lds_bytes(int dt) {
-    return kSplitMaxChunks * (2 * 16 * kSRow * 2 + 16 * kCK * 4) +
+    return kSplitMaxChunks * (2 * 16 * kSRow * 2 + 16 * kCK * 16) +
            4 * (dt == VGX_Q8_0 ? SplitGeom<VGX_Q8_0>::WAVE : SplitGeom<VGX_Q4_0>::WAVE);
 }
 static_assert(split_lds_bytes(VGX_Q8_0) <= 64 * 1024, "static LDS of qgemm_split_kernel");
 
-// Q4_0 fragments of one lane's word (bytes 4 lg .. 4 lg + 3 of its row's block).
+// Q4_0 fragments of one lane's word (bytes 4 lg .. 4 lg + 3 of its row's block): bf16 128 + n and
+// fp16 1024 + n, in the order of the nibbles' weights (low nibbles of bytes 0..3, then high nibbles).
+// v_perm_b32 byte selectors: 0..3 pick bytes of the second operand (the nibbles), 4 and 5 the bytes
+// 0x43 and 0x64 of the first.
 __device__ __forceinline__ void q4_word_frags(uint32_t w, bf16x8_t &fb, f16x8_t &fh) {
-    uint32_t o[4], h[4];
-    o[0] = ((w << 3) & 0x00780078u) | 0x41804180u;          // low nibbles of bytes 0, 2
-    o[1] = ((w >> 5) & 0x00780078u) | 0x41804180u;          // bytes 1, 3
-    o[2] = ((w >> 1) & 0x00780078u) | 0x41804180u;          // high nibbles of bytes 0, 2
-    o[3] = ((w >> 9) & 0x00780078u) | 0x41804180u;          // bytes 1, 3
-    h[0] = ((w << 6) & 0x03C003C0u) | 0x3C003C00u;
-    h[1] = ((w >> 2) & 0x03C003C0u) | 0x3C003C00u;
-    h[2] = ((w << 2) & 0x03C003C0u) | 0x3C003C00u;
-    h[3] = ((w >> 6) & 0x03C003C0u) | 0x3C003C00u;
-    fb = __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
-    fh = __builtin_bit_cast(f16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+    constexpr uint32_t C = 0x00006443u;
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    fb = __builtin_bit_cast(bf16x8_t, make_uint4(__builtin_amdgcn_perm(C, lo, 0x04010400u),
+                                                 __builtin_amdgcn_perm(C, lo, 0x04030402u),
+                                                 __builtin_amdgcn_perm(C, hi, 0x04010400u),
+                                                 __builtin_amdgcn_perm(C, hi, 0x04030402u)));
+    fh = __builtin_bit_cast(f16x8_t, make_uint4(__builtin_amdgcn_perm(C, lo, 0x05010500u),
+                                                __builtin_amdgcn_perm(C, lo, 0x05030502u),
+                                                __builtin_amdgcn_perm(C, hi, 0x05010500u),
+                                                __builtin_amdgcn_perm(C, hi, 0x05030502u)));
 }
 
 template <int DT, bool NORM>
@@ -814,7 +822,6 @@ __global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kerne
                                                              float *__restrict__ part_ssq, int kper) {
     using G = SplitGeom<DT>;
     constexpr int QB = G::QB;
-    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 24.0f;
     constexpr int R = 16;                                     // activation rows
     constexpr int F4 = R * kCK * 8 / 256;                     // staged float4 per thread and chunk
     __shared__ __align__(16) uint8_t smem_dyn[split_lds_bytes(DT)];
@@ -827,12 +834,12 @@ __global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kerne
     const int blk_hi = min(nblk, blk_lo + kper);
     const int n_chunks = (blk_hi - blk_lo + kCK - 1) / kCK;   // 1 .. kSplitMaxChunks
     const int cols = nblk * QK;
-    // LDS: activations [chunk][plane hi, lo][row][kSRow] bf16 / fp16, block sums [chunk][row][kCK],
-    // then the waves' areas
+    // LDS: activations [chunk][plane hi, lo][row][kSRow] bf16 / fp16, negated offset corrections
+    // [chunk][row][kCK] (four copies each), then the waves' areas
     constexpr int PL = R * kSRow * 2;
     uint16_t *xs = reinterpret_cast<uint16_t *>(smem_dyn);
-    float *ssum = reinterpret_cast<float *>(smem_dyn + kSplitMaxChunks * 2 * PL);
-    uint8_t *wl = smem_dyn + kSplitMaxChunks * (2 * PL + R * kCK * 4) + wave * G::WAVE;
+    float4 *cneg = reinterpret_cast<float4 *>(smem_dyn + kSplitMaxChunks * 2 * PL);
+    uint8_t *wl = smem_dyn + kSplitMaxChunks * (2 * PL + R * kCK * 16) + wave * G::WAVE;
     uint8_t *wsc = wl + 32 * G::ROW;
 
     // activations first (their wait then leaves the weight loads in flight)
@@ -888,7 +895,7 @@ __global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kerne
         }
     }
 
-    // stage the activations: bf16 hi, fp16 lo16, block sums; sum x^2 for the RMSNorm
+    // stage the activations: bf16 hi, fp16 lo, offset corrections; sum x^2 for the RMSNorm
     float ssq[F4];
 #pragma unroll
     for (int i = 0; i < F4; ++i) ssq[i] = 0.0f;
@@ -913,17 +920,32 @@ __global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kerne
                 }
             }
             uint2 hw, lw;
-            float r02[2], r13[2];
-            split_bf16_f16x2(u[0], u[2], hw.x, lw.x, r02);     // stored order 0, 2, 1, 3
-            split_bf16_f16x2(u[1], u[3], hw.y, lw.y, r13);
-            float sum = (r02[0] + r13[0]) + (r02[1] + r13[1]);
+            float sum;
+            if constexpr (DT == VGX_Q4_0) {
+                // pieces of 16 x in natural order; correction 136 sum hi + 1032 sum lo
+                hw.x = pack_bf16x2(16.0f * u[0], 16.0f * u[1]);
+                hw.y = pack_bf16x2(16.0f * u[2], 16.0f * u[3]);
+                const float h[4] = {__uint_as_float(hw.x << 16), __uint_as_float(hw.x & 0xFFFF0000u),
+                                    __uint_as_float(hw.y << 16), __uint_as_float(hw.y & 0xFFFF0000u)};
+                lw.x = pack_f16x2(fmaf(16.0f, u[0], -h[0]), fmaf(16.0f, u[1], -h[1]));
+                lw.y = pack_f16x2(fmaf(16.0f, u[2], -h[2]), fmaf(16.0f, u[3], -h[3]));
+                const auto l01 = __builtin_bit_cast(vgx_f16x2_t, lw.x), l23 = __builtin_bit_cast(vgx_f16x2_t, lw.y);
+                const float sh = (h[0] + h[1]) + (h[2] + h[3]);
+                const float sl = ((float)l01[0] + (float)l01[1]) + ((float)l23[0] + (float)l23[1]);
+                sum = fmaf(1032.0f, sl, 136.0f * sh);
+            } else {
+                float r02[2], r13[2];
+                split_bf16_f16x2(u[0], u[2], hw.x, lw.x, r02);     // stored order 0, 2, 1, 3
+                split_bf16_f16x2(u[1], u[3], hw.y, lw.y, r13);
+                sum = 128.0f * ((r02[0] + r13[0]) + (r02[1] + r13[1]));
+            }
             const int pos = DT == VGX_Q4_0 ? 8 * (j4 & 3) + 4 * (j4 >> 2) : 4 * j4;
             *reinterpret_cast<uint2 *>(xs + ((c * 2) * R + row) * kSRow + bl * QK + pos) = hw;
             *reinterpret_cast<uint2 *>(xs + ((c * 2 + 1) * R + row) * kSRow + bl * QK + pos) = lw;
             sum += __shfl_xor(sum, 1, kWave);
             sum += __shfl_xor(sum, 2, kWave);
             sum += __shfl_xor(sum, 4, kWave);
-            if (j4 == 0) ssum[(c * R + row) * kCK + bl] = sum;
+            if (j4 == 0) cneg[(c * R + row) * kCK + bl] = make_float4(-sum, -sum, -sum, -sum);
         }
     }
     __syncthreads();
@@ -982,12 +1004,12 @@ __global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kerne
                                     half_bits_to_float(scu[u].y), half_bits_to_float(scu[u].y >> 16)};
                 const uint4 xh = *reinterpret_cast<const uint4 *>(xs + ((c * 2) * R + l16) * kSRow + u * QK + 8 * lg);
                 const uint4 xl = *reinterpret_cast<const uint4 *>(xs + ((c * 2 + 1) * R + l16) * kSRow + u * QK + 8 * lg);
-                const float corr = OFF * ssum[(c * R + l16) * kCK + u];
-                f32x4_t pr = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                const float4 cn = cneg[(c * R + l16) * kCK + u];
+                f32x4_t pr = f32x4_t{cn.x, cn.y, cn.z, cn.w};
                 pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, __builtin_bit_cast(bf16x8_t, xh), pr, 0, 0, 0);
                 pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, __builtin_bit_cast(f16x8_t, xl), pr, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(d[i], pr[i] - corr, acc[t][i]);
+                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(d[i], pr[i], acc[t][i]);
             }
         }
         // this chunk's LDS reads are done before the next chunk's writes (in order within the wave)
@@ -1013,29 +1035,230 @@ __global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kerne
         for (int t = 0; t < 2; ++t) {
             const int64_t crq = rq_wave + 4 * t + lg;
             if (crq >= n_rq) continue;
+            constexpr float S = DT == VGX_Q4_0 ? 0.0625f : 1.0f;   // Q4_0 pieces carry 16 x
             *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + bb) * rows_p + crq * 4) =
-                make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+                make_float4(S * acc[t][0], S * acc[t][1], S * acc[t][2], S * acc[t][3]);
         }
     }
 }
 
-// Sum of the K-split partials + epilogue.  One thread per output (b, row); SwiGLU reads the gate and
-// up sums of packed row-quad q (sub-rows k and 2 + k) for output row 2 q + k.
+// ---------------------------------------------------------------------------------------------
+// Decode batches, K-split Q4_0 projections of 16-block splits: qgemm_kslice_kernel.  A workgroup owns
+// the tile of qgemm_split_kernel (128 weight rows x 16 activation rows x a K range of 16 blocks), but
+// each of its 4 waves takes one 4-block slice of the range for all 128 rows, so the activations never
+// pass through LDS (against qgemm_split_kernel, gate/up of the 1.5B model at batch 32 measured 17.0 ->
+// 15.1 us per launch, down 11.0 -> 9.5 us):
+//  * Activations: lane (row l16, K group lg) loads its 8 values of each block of the slice (K slots
+//    4 lg + {0..3} and 16 + 4 lg + {0..3}, the order of q4_word_frags) and keeps them in registers
+//    as the MFMA B operands, bf16 hi = 16 x and fp16 lo = 16 x - hi (x times the RMSNorm weight);
+//    the block's correction 136 sum hi + 1032 sum lo is summed over the four K groups with lane swaps.
+//  * Weights: the slice of a row-quad is one contiguous 256-byte run (4 blocks x 4 rows x 16 bytes),
+//    loaded as 16-byte pieces into a wave-private LDS area in the MFMA layout: row r, piece lg of its
+//    4 blocks in slot lg ^ ((r >> 2) & 3), so that both the writes and the 16-byte reads of a tile are
+//    free of bank conflicts.  The slice's scales (32 bytes per row-quad) go next to them.
+//  * Per 16-row tile: per block, the bf16 and fp16 MFMAs from a zero accumulator, then the block's
+//    scales into the tile's sums (one fma per output); the offset corrections of the four blocks enter
+//    with one fp32 MFMA (scales of the tile's rows x -correction of the activation rows).
+//  * The four slices' sums are added in slice order through LDS; the workgroup writes one partial per
+//    output, scaled by 1/16, and the per-row sum x^2 of its range.
+//  * Four waves per SIMD (at most 128 VGPRs): 1024 workgroup slots, so gate/up (840 workgroups) runs
+//    in one round.
+constexpr int kKsRow = 64;                         // LDS bytes per weight row of a slice
+constexpr int kKsSlice = 128 * kKsRow + 32 * 32;   // per slice: 128 rows, then 32 row-quads of scales
+constexpr int kKsLds = 4 * kKsSlice;
+static_assert(kKsLds >= 4 * 8 * 64 * 16 + 4 * 16 * 4, "the LDS of qgemm_kslice_kernel holds the cross-slice sums");
+
+template <bool NORM>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void qgemm_kslice_kernel(
+    const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq, int nblk, int w_bytes, const float *__restrict__ x,
+    int64_t ldx, const float *__restrict__ lnw, int64_t batch, float *__restrict__ part, float *__restrict__ part_ssq,
+    int kper) {
+    __shared__ __align__(16) uint8_t smem[kKsLds];
+    const int tid = threadIdx.x, lane = tid & 63, sl = tid >> 6;   // the wave's K slice
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int64_t rq0 = (int64_t)blockIdx.x * 32;
+    const int64_t b0 = (int64_t)blockIdx.y * 16;
+    const int blk_lo = (int)blockIdx.z * kper;
+    const int blk_hi = min(nblk, blk_lo + kper);
+    const int wb0 = blk_lo + 4 * sl;                   // first block of this wave's slice
+    const int cols = nblk * QK;
+    uint8_t *wl = smem + sl * kKsSlice;
+    uint8_t *wsc = wl + 128 * kKsRow;
+
+    // activations of the slice first, then the weights and scales
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)x, 0, (int)(((batch - 1) * ldx + cols) * 4), 0x00020000);
+    const __amdgpu_buffer_rsrc_t grs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)lnw, 0, NORM ? cols * 4 : 0, 0x00020000);
+    const int64_t brow = b0 + l16;
+    float4 xv[4][2], gv[4][2];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const bool in = wb0 + u < blk_hi;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const uint32_t ko = (uint32_t)(((wb0 + u) * QK + 16 * hf + 4 * lg) * 4);
+            const uint32_t o = in && brow < batch ? (uint32_t)(brow * ldx * 4) + ko : kPastEnd;
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(xrs, o, 0, 0);
+            xv[u][hf] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+            if constexpr (NORM) {
+                const auto g = __builtin_amdgcn_raw_buffer_load_b128(grs, in ? ko : kPastEnd, 0, 0);
+                gv[u][hf] = make_float4(__uint_as_float(g[0]), __uint_as_float(g[1]), __uint_as_float(g[2]), __uint_as_float(g[3]));
+            }
+        }
+    }
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, w_bytes, 0x00020000);
+    const bool live = wb0 < blk_hi;                    // wave-uniform: a slice past the range adds nothing
+    uint4 wr[8];
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+        const int64_t rq = rq0 + 4 * h + (lane >> 4);
+        const uint32_t o = live && rq < n_rq ? (uint32_t)(rq * nblk * 64 + (int64_t)wb0 * 64) + (uint32_t)(l16 * 16)
+                                             : kPastEnd;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, o, 0, 0);
+        wr[h] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+    uint4 sr;
+    {
+        const int64_t rq = rq0 + (lane >> 1);
+        const uint32_t o = live && rq < n_rq ? (uint32_t)(soff + rq * nblk * 8 + (int64_t)(wb0 + 2 * (lane & 1)) * 8)
+                                             : kPastEnd;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, o, 0, 0);
+        sr = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+
+    // B operands: hi = bf16(16 v), lo = fp16(16 v - hi), v = x (times the RMSNorm weight)
+    uint4 bh[4], bl[4];
+    float cb[4], ssq = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        float e[8] = {xv[u][0].x, xv[u][0].y, xv[u][0].z, xv[u][0].w, xv[u][1].x, xv[u][1].y, xv[u][1].z, xv[u][1].w};
+        if constexpr (NORM) {
+            const float g[8] = {gv[u][0].x, gv[u][0].y, gv[u][0].z, gv[u][0].w,
+                                gv[u][1].x, gv[u][1].y, gv[u][1].z, gv[u][1].w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ssq = fmaf(e[i], e[i], ssq);
+                e[i] *= g[i];
+            }
+        }
+        uint32_t hw[4], lw[4];
+        float sh = 0.0f, sm = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            hw[i] = pack_bf16x2(16.0f * e[2 * i], 16.0f * e[2 * i + 1]);
+            const float h0 = __uint_as_float(hw[i] << 16), h1 = __uint_as_float(hw[i] & 0xFFFF0000u);
+            lw[i] = pack_f16x2(fmaf(16.0f, e[2 * i], -h0), fmaf(16.0f, e[2 * i + 1], -h1));
+            const auto l2 = __builtin_bit_cast(vgx_f16x2_t, lw[i]);
+            sh += h0 + h1;
+            sm += (float)l2[0] + (float)l2[1];
+        }
+        bh[u] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        bl[u] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        cb[u] = xor32_sum(xor16_sum(fmaf(1032.0f, sm, 136.0f * sh)));
+    }
+    // the correction MFMA's B operand: -correction of (activation row l16, block lg)
+    const float cneg = -(lg == 0 ? cb[0] : lg == 1 ? cb[1] : lg == 2 ? cb[2] : cb[3]);
+
+    // the slice's weights into the MFMA layout, its scales next to them
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+        const int r = 4 * (4 * h + (lane >> 4)) + (lane & 3), u = (lane >> 2) & 3;
+        uint32_t *p = reinterpret_cast<uint32_t *>(wl + r * kKsRow) + u;
+        const int sw = (r >> 2) & 3;
+        p[(0 ^ sw) * 4] = wr[h].x;
+        p[(1 ^ sw) * 4] = wr[h].y;
+        p[(2 ^ sw) * 4] = wr[h].z;
+        p[(3 ^ sw) * 4] = wr[h].w;
+    }
+    *reinterpret_cast<uint4 *>(wsc + (lane >> 1) * 32 + (lane & 1) * 16) = sr;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    f32x4_t acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int row = 16 * t + l16;
+            const uint4 a = *reinterpret_cast<const uint4 *>(wl + row * kKsRow + ((lg ^ ((l16 >> 2) & 3)) * 16));
+            const uint4 s0 = *reinterpret_cast<const uint4 *>(wsc + (4 * t + lg) * 32);
+            const uint4 s1 = *reinterpret_cast<const uint4 *>(wsc + (4 * t + lg) * 32 + 16);
+            const uint32_t da = *reinterpret_cast<const uint16_t *>(wsc + (4 * t + (l16 >> 2)) * 32 + lg * 8 + (l16 & 3) * 2);
+            const uint32_t wq[4] = {a.x, a.y, a.z, a.w};
+            const uint2 scu[4] = {make_uint2(s0.x, s0.y), make_uint2(s0.z, s0.w), make_uint2(s1.x, s1.y),
+                                  make_uint2(s1.z, s1.w)};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                bf16x8_t af;
+                f16x8_t ah;
+                q4_word_frags(wq[u], af, ah);
+                f32x4_t pr = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, __builtin_bit_cast(bf16x8_t, bh[u]), pr, 0, 0, 0);
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, __builtin_bit_cast(f16x8_t, bl[u]), pr, 0, 0, 0);
+                const float d[4] = {half_bits_to_float(scu[u].x), half_bits_to_float(scu[u].x >> 16),
+                                    half_bits_to_float(scu[u].y), half_bits_to_float(scu[u].y >> 16)};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(d[i], pr[i], acc[t][i]);
+            }
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(half_bits_to_float(da), cneg, acc[t], 0, 0, 0);
+        }
+    }
+
+    // the four slices' sums, added in slice order; the per-row sum x^2 of the range
+    __syncthreads();
+    float4 *red = reinterpret_cast<float4 *>(smem);
+    float *rss = reinterpret_cast<float *>(smem + 4 * 8 * 64 * 16);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) red[(sl * 8 + t) * 64 + lane] = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+    if constexpr (NORM) {
+        const float sq = xor32_sum(xor16_sum(ssq));
+        if (lg == 0) rss[sl * 16 + l16] = sq;
+    }
+    __syncthreads();
+    const int64_t rows_p = n_rq * 4;
+    const int64_t bb = b0 + l16;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int t = 2 * sl + j;
+        float4 v = red[t * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const float4 o = red[(w * 8 + t) * 64 + lane];
+            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+        }
+        const int64_t crq = rq0 + 4 * t + lg;
+        if (bb < batch && crq < n_rq)
+            *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + bb) * rows_p + crq * 4) =
+                make_float4(0.0625f * v.x, 0.0625f * v.y, 0.0625f * v.z, 0.0625f * v.w);
+    }
+    if constexpr (NORM) {
+        if (blockIdx.x == 0 && tid < 16 && b0 + tid < batch)
+            part_ssq[(int64_t)blockIdx.z * batch + b0 + tid] = ((rss[tid] + rss[16 + tid]) + rss[32 + tid]) + rss[48 + tid];
+    }
+}
+
+// Sum of the K-split partials + epilogue.  One thread per (activation row b, packed row-quad q): one
+// 16-byte load per split brings the four sums of the quad (SwiGLU: gate rows 2q, 2q + 1 and up rows 2q,
+// 2q + 1; otherwise output rows 4q .. 4q + 3).
 // part_ssq (when not null): per-split sum x^2 of every activation row; the sums are then scaled by
-// 1 / sqrt(mean(x^2) + eps) (the RMSNorm of the small-batch kernel).
-// KM >= ks is a compile-time bound: every split's load goes out at once (indexes clamped to the last
-// split), then the sums run in split order, instead of one load round trip per split.
+// 1 / sqrt(mean(x^2) + eps) (the RMSNorm of the small-batch kernels).
+// KM >= ks is a compile-time bound (equal to ks up to 18 splits): every split's load goes out at once
+// (indexes clamped to the last split), then the sums run in split order, instead of one load round
+// trip per split.
 template <int EPI, int KM>
 __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float *__restrict__ part, int ks, int64_t batch,
                                                             int64_t rows_p, int64_t rows_out,
                                                             const float *__restrict__ bias, float *__restrict__ y,
                                                             int64_t ldy, const float *__restrict__ part_ssq,
                                                             int cols, float eps) {
+    const int64_t nq = rows_p >> 2;
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= batch * rows_out) return;
-    const int64_t b = i / rows_out, r = i - b * rows_out;
+    if (i >= batch * nq) return;
+    const int64_t b = i / nq, q = i - b * nq;
     float *yr = y + b * ldy;
-    auto at = [&](int s) -> int64_t { return ((int64_t)min(s, ks - 1) * batch + b) * rows_p; };
     float inv = 1.0f;
     if (part_ssq) {
         float p[KM];
@@ -1047,37 +1270,38 @@ __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float *__restri
             if (s < ks) t += p[s];
         inv = 1.0f / sqrtf(t / (float)cols + eps);
     }
+    float4 p[KM];
+#pragma unroll
+    for (int s = 0; s < KM; ++s)
+        p[s] = *reinterpret_cast<const float4 *>(part + ((int64_t)min(s, ks - 1) * batch + b) * rows_p + q * 4);
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < KM; ++s) {
+        if (s < ks) {
+            v[0] += p[s].x;
+            v[1] += p[s].y;
+            v[2] += p[s].z;
+            v[3] += p[s].w;
+        }
+    }
     if constexpr (EPI == EPI_SWIGLU) {
-        const int64_t q = r >> 1, k = r & 1;
-        float pg[KM], pu[KM];
 #pragma unroll
-        for (int s = 0; s < KM; ++s) {
-            pg[s] = part[at(s) + q * 4 + k];
-            pu[s] = part[at(s) + q * 4 + 2 + k];
+        for (int k = 0; k < 2; ++k) {
+            const int64_t o = 2 * q + k;
+            if (o >= rows_out) continue;
+            const float g = v[k] * inv, u = v[2 + k] * inv;
+            yr[o] = g / (1.0f + __expf(-g)) * u;
         }
-        float g = 0.0f, u = 0.0f;
-#pragma unroll
-        for (int s = 0; s < KM; ++s) {
-            if (s < ks) {
-                g += pg[s];
-                u += pu[s];
-            }
-        }
-        g *= inv;
-        u *= inv;
-        yr[r] = g / (1.0f + __expf(-g)) * u;
     } else {
-        float p[KM];
 #pragma unroll
-        for (int s = 0; s < KM; ++s) p[s] = part[at(s) + r];
-        float v = 0.0f;
-#pragma unroll
-        for (int s = 0; s < KM; ++s)
-            if (s < ks) v += p[s];
-        v *= inv;
-        if (bias) v += bias[r];
-        if constexpr (EPI == EPI_ACCUM) v += yr[r];
-        yr[r] = v;
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = 4 * q + r;
+            if (row >= rows_out) continue;
+            float t = v[r] * inv;
+            if (bias) t += bias[row];
+            if constexpr (EPI == EPI_ACCUM) t += yr[row];
+            yr[row] = t;
+        }
     }
 }
 
@@ -1085,13 +1309,31 @@ __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float *__restri
 template <int EPI>
 void reduce_launch(const float *part, int ks, int64_t batch, int64_t rows_p, int64_t rows_out, const float *bias,
                    float *y, int64_t ldy, const float *part_ssq, int cols, float eps, hipStream_t st) {
-    const unsigned g = (unsigned)((batch * rows_out + 255) / 256);
+    const unsigned g = (unsigned)((batch * (rows_p / 4) + 255) / 256);
 #define VGX_RED(KM) hipLaunchKernelGGL((qgemm_reduce_kernel<EPI, KM>), dim3(g), dim3(256), 0, st, part, ks, batch, \
                                        rows_p, rows_out, bias, y, ldy, part_ssq, cols, eps)
-    if (ks <= 4) VGX_RED(4);
-    else if (ks <= 8) VGX_RED(8);
-    else if (ks <= 16) VGX_RED(16);
-    else VGX_RED(32);
+    switch (ks) {
+        case 1: case 2: VGX_RED(2); break;
+        case 3: VGX_RED(3); break;
+        case 4: VGX_RED(4); break;
+        case 5: VGX_RED(5); break;
+        case 6: VGX_RED(6); break;
+        case 7: VGX_RED(7); break;
+        case 8: VGX_RED(8); break;
+        case 9: VGX_RED(9); break;
+        case 10: VGX_RED(10); break;
+        case 11: VGX_RED(11); break;
+        case 12: VGX_RED(12); break;
+        case 13: VGX_RED(13); break;
+        case 14: VGX_RED(14); break;
+        case 15: VGX_RED(15); break;
+        case 16: VGX_RED(16); break;
+        case 17: VGX_RED(17); break;
+        case 18: VGX_RED(18); break;
+        default:
+            if (ks <= 24) VGX_RED(24);
+            else VGX_RED(32);
+    }
 #undef VGX_RED
 }
 
@@ -1176,8 +1418,15 @@ void split_kernel_launch(int dtype, const uint8_t *w, int64_t soff, int64_t n_rq
 #define VGX_SK(DT, NORM)                                                                                       \
     hipLaunchKernelGGL((qgemm_split_kernel<DT, NORM>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, wb, x, ldx, \
                        norm_w, batch, part, pssq, kper)
+#define VGX_KS(NORM)                                                                                           \
+    hipLaunchKernelGGL((qgemm_kslice_kernel<NORM>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, wb, x, ldx, norm_w, \
+                       batch, part, pssq, kper)
+    // K slices of 4 blocks: 16-block splits keep all four waves busy; shorter splits (the 1536-column
+    // projections take 8 blocks) stay on qgemm_split_kernel
     if (dtype == VGX_Q8_0) { if (norm_w) VGX_SK(VGX_Q8_0, true); else VGX_SK(VGX_Q8_0, false); }
+    else if (kper == kSplitMaxBlocks) { if (norm_w) VGX_KS(true); else VGX_KS(false); }
     else { if (norm_w) VGX_SK(VGX_Q4_0, true); else VGX_SK(VGX_Q4_0, false); }
+#undef VGX_KS
 #undef VGX_SK
 }
 
