@@ -121,9 +121,13 @@ int vgx_qlinear_ex(int dtype, const void *w_packed, int64_t rows, int64_t cols, 
                    int64_t batch, const float *norm_w, float eps, const float *bias, float *y, int64_t ldy,
                    int epilogue, void *stream);
 
-/* Workspace bytes of vgx_qgemm for these sizes and epilogue (256-byte aligned buffer: bf16 hi / lo
- * splits of the activations, their per-block sums, and K-split partial sums when the GEMM splits K
- * to fill the GPU). */
+/* Workspace bytes of vgx_qgemm for these sizes and epilogue (256-byte aligned buffer: a fixed 64 KiB
+ * region of int32 output-tile counters first, then bf16 hi / lo splits of the activations, their
+ * per-block sums, and K-split partial sums when the GEMM splits K to fill the GPU).  Decode batches
+ * (at most 64 rows) whose splits the split workgroups sum themselves take tickets from the counters:
+ * the workspace must be zero-filled before its first use, every call leaves the counters at zero (so a
+ * captured graph needs no memset), and calls sharing one workspace must not overlap in time.  The
+ * same workspace may serve vgx_qkv_rope_batch, which leaves the counter region untouched. */
 int64_t vgx_qgemm_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, int epilogue);
 
 /* vgx_qlinear_ex for many activation rows on bf16 MFMA (Q8_0 / Q4_0 weights): same arguments and
@@ -303,7 +307,8 @@ int vgx_qkv_rope_step(int q_dtype, const void *wq, const float *bq, int kv_wdtyp
  * the bias of all rows).  x [B][d_model] (row stride ldx, 16-byte aligned, ldx % 4 == 0); norm_w
  * (16-byte aligned) may be NULL for no RMSNorm.  q_out [B][H][D] (row stride ldq) receives the
  * rotated queries; the state tensors are addressed as in vgx_rope_qkv_write_step.  workspace: at
- * least vgx_qkv_rope_batch_workspace_bytes(B, d_model, H, G, D, wq != NULL) bytes, 256-byte aligned.
+ * least vgx_qkv_rope_batch_workspace_bytes(B, d_model, H, G, D, wq != NULL) bytes, 256-byte aligned;
+ * its first 64 KiB (vgx_qgemm's tile counters, when one workspace serves both) are not written.
  * Replaces src/vault_v3_model.py:1041-1047, 1079-1094 (the batched decode path) and
  * runtime/vault3.c:2152-2179 per sequence. */
 int64_t vgx_qkv_rope_batch_workspace_bytes(int64_t B, int64_t d_model, int64_t H, int64_t G, int64_t D,

@@ -92,6 +92,62 @@ def test_qgemm_equals_gemv_rows(dev, dt):
     assert bool(((big.double() - one.double()).abs() <= tol).all())
 
 
+@pytest.mark.parametrize("epi,rows,cols", [("swiglu", 8960, 1536), ("accum", 1536, 8960)])
+def test_qgemm_fused_split_sum_replays(dev, epi, rows, cols):
+    """Decode-batch Q4_0 projections whose K splits are summed by the last workgroup of each output tile
+    (gate/up with the RMSNorm, down with the residual add, batch 32): eager calls one after another and
+    replays of a captured graph, with eager work between the replays, give the same bits each time (the
+    tile counters are back at zero after every call) and stay within the oracle bound."""
+    rng = np.random.default_rng(rows + cols + 7)
+    batch = 32
+    x = torch.from_numpy((rng.standard_normal((batch, cols)) * 2.0).astype(np.float32)).to(dev)
+    if epi == "swiglu":
+        g = torch.from_numpy(rng.uniform(0.8, 1.2, cols).astype(np.float32)).to(dev)
+        gate, up = _blocks(codec.Q4_0, rows, cols, 8), _blocks(codec.Q4_0, rows, cols, 9)
+        w = ops.QWeight.gateup_from_blocks(codec.Q4_0, rows, cols, gate, up, dev)
+        run = lambda out: ops.qlinear_swiglu(w, x, out=out, norm=(g, 1e-6))
+        u = linalg.rmsnorm(x.cpu().numpy(), g.cpu().numpy(), 1e-6)
+        gf, uf = codec.decode(codec.Q4_0, gate, rows, cols), codec.decode(codec.Q4_0, up, rows, cols)
+        gg, uu = linalg.gemv(gf, u), linalg.gemv(uf, u)
+        ref = linalg.swiglu(gg, uu)
+        tol = 1.1 * np.abs(uu) * linalg.gemv_bound(gf, u, codec.Q4_0, rel=8e-6) + \
+            np.abs(gg) * linalg.gemv_bound(uf, u, codec.Q4_0, rel=8e-6) + 1e-6 * np.abs(ref) + 1e-30
+        y0 = torch.zeros(batch, rows, device=dev)
+    else:
+        raw = _blocks(codec.Q4_0, rows, cols, 10)
+        w = ops.QWeight.from_blocks(codec.Q4_0, rows, cols, raw, dev)
+        run = lambda out: ops.qlinear(w, x, out=out, accumulate=True)
+        wf = codec.decode(codec.Q4_0, raw, rows, cols)
+        y0 = torch.from_numpy(rng.standard_normal((batch, rows)).astype(np.float32)).to(dev)
+        ref = linalg.gemv(wf, x.cpu().numpy()) + y0.cpu().numpy()
+        tol = linalg.gemv_bound(wf, x.cpu().numpy(), codec.Q4_0, rel=8e-6) + np.abs(ref) * 2e-7
+    eager = []
+    for _ in range(3):
+        out = y0.clone()
+        run(out)
+        eager.append(out)
+    torch.cuda.synchronize()
+    assert all(torch.equal(e, eager[0]) for e in eager[1:])
+    assert np.all(np.abs(eager[0].cpu().numpy().astype(np.float64) - ref) <= tol)
+    out = y0.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run(out)                      # workspace sized before the capture
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(out)
+    for i in range(3):
+        out.copy_(y0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[0]), f"replay {i}"
+        run(y0.clone())               # eager call between replays
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("dt", [codec.Q4_0])
 @pytest.mark.parametrize("rows,cols,batch", [(64, 7200, 8), (16, 4096, 8), (64, 7200, 200)])
 def test_qgemm_k_split_edges(dev, dt, rows, cols, batch):

@@ -814,6 +814,110 @@ __device__ __forceinline__ void q4_word_frags(uint32_t w, bf16x8_t &fb, f16x8_t 
                                                 __builtin_amdgcn_perm(C, hi, 0x05030502u)));
 }
 
+// ---------------------------------------------------------------------------------------------
+// K splits summed without a second launch.  With FIN >= 0 a workgroup of qgemm_kslice_kernel (128
+// weight rows x 16 activation rows x one K range) writes its partials and its rows' sum x^2 with agent-scope stores
+// (written through to the device-coherent level), waits for them, and takes a ticket from its output
+// tile's counter; the workgroup that draws the last ticket reads the tile's partials of every split
+// with agent-scope loads, adds them in split order (the arithmetic of qgemm_reduce_kernel, so the
+// results are the same bits), applies the epilogue FIN and resets the counter to zero for the next
+// launch.  The counters live in a fixed region at the start of the workspace that stays zero between
+// launches, so a captured graph needs no memset.
+constexpr int kFinNone = -1;                    // FIN of a launch whose partials a reduce launch sums
+constexpr int kQgemmTickets = 16384;            // tile counters at the start of the GEMM workspace
+constexpr int64_t kQgemmTicketBytes = kQgemmTickets * 4;
+constexpr int kFinLoads = 9;                    // splits the finishing workgroup requests at once
+
+// One 16-byte agent-scope store (buffer store with sc1) at byte offset off of the partial buffer.
+__device__ __forceinline__ void store4_agent(__amdgpu_buffer_rsrc_t rs, uint32_t off, float4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(
+        (__attribute__((ext_vector_type(4))) uint32_t){__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                                                     __float_as_uint(v.w)},
+        rs, off, 0, 16);
+}
+
+// The tile's last workgroup: part [ks][batch][rows_p], pssq [ks][gridDim.x][batch] (or null);
+// thread (row-quad tid % 32, activation rows tid / 32 and 8 + tid / 32) of tile (blockIdx.x, blockIdx.y).
+template <int EPI>
+__device__ __forceinline__ void ksplit_finish(const float *part, int ks, int64_t batch, int64_t n_rq, int64_t rows_out,
+                                              const float *pssq, int cols, float eps, const float *bias, float *y,
+                                              int64_t ldy, int *cnt, int *flag) {
+    const int tid = threadIdx.x;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's partial stores have completed
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == ks - 1;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    const int64_t rows_p = n_rq * 4;
+    const int64_t rq = (int64_t)blockIdx.x * 32 + (tid & 31);
+    const int64_t bA = (int64_t)blockIdx.y * 16 + (tid >> 5);
+    const int64_t gx = gridDim.x;
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)part, 0, (int)(ks * batch * rows_p * 4), 0x00020000);
+    float4 v[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
+    float t[2] = {0.0f, 0.0f};
+    for (int s0 = 0; s0 < ks; s0 += kFinLoads) {
+        float4 p[2][kFinLoads];
+        float q[2][kFinLoads];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int64_t b = bA + 8 * i;
+#pragma unroll
+            for (int u = 0; u < kFinLoads; ++u) {
+                const int64_t sp = min(s0 + u, ks - 1);
+                const uint32_t o = b < batch && rq < n_rq ? (uint32_t)(((sp * batch + b) * rows_p + rq * 4) * 4) : kPastEnd;
+                const auto w = __builtin_amdgcn_raw_buffer_load_b128(prs, o, 0, 16);
+                p[i][u] = make_float4(__uint_as_float(w[0]), __uint_as_float(w[1]), __uint_as_float(w[2]), __uint_as_float(w[3]));
+                q[i][u] = pssq && b < batch ? __hip_atomic_load(pssq + (sp * gx + blockIdx.x) * batch + b, __ATOMIC_RELAXED,
+                                                                __HIP_MEMORY_SCOPE_AGENT)
+                                            : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int u = 0; u < kFinLoads; ++u)
+                if (s0 + u < ks) {
+                    v[i].x += p[i][u].x;
+                    v[i].y += p[i][u].y;
+                    v[i].z += p[i][u].z;
+                    v[i].w += p[i][u].w;
+                    t[i] += q[i][u];
+                }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int64_t b = bA + 8 * i;
+        if (b >= batch || rq >= n_rq) continue;
+        const float inv = pssq ? 1.0f / sqrtf(t[i] / (float)cols + eps) : 1.0f;
+        float *yr = y + b * ldy;
+        const float e[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+        if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int64_t o = 2 * rq + k;
+                if (o >= rows_out) continue;
+                const float g = e[k] * inv, u = e[2 + k] * inv;
+                yr[o] = g / (1.0f + __expf(-g)) * u;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = 4 * rq + r;
+                if (row >= rows_out) continue;
+                float a = e[r] * inv;
+                if (bias) a += bias[row];
+                if constexpr (EPI == EPI_ACCUM) a += yr[row];
+                yr[row] = a;
+            }
+        }
+    }
+    if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int DT, bool NORM>
 __global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
                                                              int nblk, int w_bytes, const float *__restrict__ x,
@@ -1068,11 +1172,12 @@ constexpr int kKsSlice = 128 * kKsRow + 32 * 32;   // per slice: 128 rows, then 
 constexpr int kKsLds = 4 * kKsSlice;
 static_assert(kKsLds >= 4 * 8 * 64 * 16 + 4 * 16 * 4, "the LDS of qgemm_kslice_kernel holds the cross-slice sums");
 
-template <bool NORM>
+template <bool NORM, int FIN>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void qgemm_kslice_kernel(
     const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq, int nblk, int w_bytes, const float *__restrict__ x,
     int64_t ldx, const float *__restrict__ lnw, int64_t batch, float *__restrict__ part, float *__restrict__ part_ssq,
-    int kper) {
+    int kper, int64_t rows_out, float eps, const float *__restrict__ bias, float *__restrict__ y, int64_t ldy,
+    int *__restrict__ cnt) {
     __shared__ __align__(16) uint8_t smem[kKsLds];
     const int tid = threadIdx.x, lane = tid & 63, sl = tid >> 6;   // the wave's K slice
     const int l16 = lane & 15, lg = lane >> 4;
@@ -1220,6 +1325,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     __syncthreads();
     const int64_t rows_p = n_rq * 4;
     const int64_t bb = b0 + l16;
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)part, 0, FIN >= 0 ? (int)(gridDim.z * batch * rows_p * 4) : 0, 0x00020000);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int t = 2 * sl + j;
@@ -1230,13 +1337,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
             v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
         }
         const int64_t crq = rq0 + 4 * t + lg;
-        if (bb < batch && crq < n_rq)
-            *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + bb) * rows_p + crq * 4) =
-                make_float4(0.0625f * v.x, 0.0625f * v.y, 0.0625f * v.z, 0.0625f * v.w);
+        const float4 r = make_float4(0.0625f * v.x, 0.0625f * v.y, 0.0625f * v.z, 0.0625f * v.w);
+        if (bb < batch && crq < n_rq) {
+            const int64_t off = ((int64_t)blockIdx.z * batch + bb) * rows_p + crq * 4;
+            if constexpr (FIN >= 0) store4_agent(prs, (uint32_t)(off * 4), r);
+            else *reinterpret_cast<float4 *>(part + off) = r;
+        }
     }
     if constexpr (NORM) {
-        if (blockIdx.x == 0 && tid < 16 && b0 + tid < batch)
-            part_ssq[(int64_t)blockIdx.z * batch + b0 + tid] = ((rss[tid] + rss[16 + tid]) + rss[32 + tid]) + rss[48 + tid];
+        if (tid < 16 && b0 + tid < batch) {
+            const float sq = ((rss[tid] + rss[16 + tid]) + rss[32 + tid]) + rss[48 + tid];
+            if constexpr (FIN >= 0)
+                __hip_atomic_store(part_ssq + ((int64_t)blockIdx.z * gridDim.x + blockIdx.x) * batch + b0 + tid, sq,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else if (blockIdx.x == 0)
+                part_ssq[(int64_t)blockIdx.z * batch + b0 + tid] = sq;
+        }
+    }
+    if constexpr (FIN >= 0) {
+        __shared__ int last;
+        ksplit_finish<FIN>(part, (int)gridDim.z, batch, n_rq, rows_out, NORM ? part_ssq : nullptr, cols, eps, bias, y,
+                           ldy, cnt + (int64_t)blockIdx.y * gridDim.x + blockIdx.x, &last);
     }
 }
 
@@ -1410,32 +1531,62 @@ inline bool use_split_kernel(int ks, int kper, int64_t w_bytes) {
 }
 
 // qgemm_split_kernel over grid (row tiles, 16-row activation tiles, splits); writes part / pssq.
+// The tile epilogue a fused launch applies (kFinNone: partials only, for a reduce launch).
+struct SplitFin {
+    int epi = kFinNone;
+    int64_t rows_out = 0;
+    float eps = 0.0f;
+    const float *bias = nullptr;
+    float *y = nullptr;
+    int64_t ldy = 0;
+    int *cnt = nullptr;
+};
+
+// qgemm_split_kernel / qgemm_kslice_kernel over grid (row tiles, 16-row activation tiles, splits);
+// writes part / pssq, and with fin.epi >= 0 also sums the splits of each tile into y.
 void split_kernel_launch(int dtype, const uint8_t *w, int64_t soff, int64_t n_rq, int nblk, const float *x,
                          int64_t ldx, const float *norm_w, int64_t batch, float *part, float *pssq, int ks, int kper,
-                         hipStream_t st) {
+                         const SplitFin &fin, hipStream_t st) {
     const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 15) / 16), (unsigned)ks);
     const int wb = (int)(soff + n_rq * nblk * 8);
 #define VGX_SK(DT, NORM)                                                                                       \
     hipLaunchKernelGGL((qgemm_split_kernel<DT, NORM>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, wb, x, ldx, \
                        norm_w, batch, part, pssq, kper)
-#define VGX_KS(NORM)                                                                                           \
-    hipLaunchKernelGGL((qgemm_kslice_kernel<NORM>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, wb, x, ldx, norm_w, \
-                       batch, part, pssq, kper)
+#define VGX_KS(NORM, F)                                                                                         \
+    hipLaunchKernelGGL((qgemm_kslice_kernel<NORM, F>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, wb, x, ldx,    \
+                       norm_w, batch, part, pssq, kper, fin.rows_out, fin.eps, fin.bias, fin.y, fin.ldy, fin.cnt)
+#define VGX_KSN(F) do { if (norm_w) VGX_KS(true, F); else VGX_KS(false, F); } while (0)
     // K slices of 4 blocks: 16-block splits keep all four waves busy; shorter splits (the 1536-column
     // projections take 8 blocks) stay on qgemm_split_kernel
     if (dtype == VGX_Q8_0) { if (norm_w) VGX_SK(VGX_Q8_0, true); else VGX_SK(VGX_Q8_0, false); }
-    else if (kper == kSplitMaxBlocks) { if (norm_w) VGX_KS(true); else VGX_KS(false); }
-    else { if (norm_w) VGX_SK(VGX_Q4_0, true); else VGX_SK(VGX_Q4_0, false); }
+    else if (kper != kSplitMaxBlocks) { if (norm_w) VGX_SK(VGX_Q4_0, true); else VGX_SK(VGX_Q4_0, false); }
+    else if (fin.epi == EPI_STORE) VGX_KSN(EPI_STORE);
+    else if (fin.epi == EPI_ACCUM) VGX_KSN(EPI_ACCUM);
+    else if (fin.epi == EPI_SWIGLU) VGX_KSN(EPI_SWIGLU);
+    else VGX_KSN(kFinNone);
+#undef VGX_KSN
 #undef VGX_KS
 #undef VGX_SK
 }
 
-// Workspace of the small-batch path: K-split partials, then the per-split sum x^2 of every row.
+// Whether a split launch sums its own splits: qgemm_kslice_kernel (the fused finish measured slower than
+// the reduce launch behind qgemm_split_kernel's 8-block splits: o-projection at batch 32, 9.6 against 8.5
+// us per call; gate/up 17.0 against 19.1 us), a tile counter for every output tile and partial byte
+// offsets within the 31-bit buffer range.
+inline bool use_fused_finish(int dtype, int kper, int64_t n_rq, int64_t batch, int ks) {
+    const int64_t tiles = (n_rq + 31) / 32 * ((batch + 15) / 16);
+    return dtype == VGX_Q4_0 && kper == kSplitMaxBlocks && tiles <= kQgemmTickets &&
+           (int64_t)ks * batch * n_rq * 16 < ((int64_t)1 << 31);
+}
+
+// Workspace of the small-batch path: the tile counters, the K-split partials, then the per-split sum
+// x^2 of every row (per row tile when the launch sums its own splits).
 inline int64_t small_bytes(int64_t batch, int64_t n_rq, int nblk) {
     int kper = 0;
     const int ks = small_ksplit(n_rq, batch, nblk, &kper);
     if (ks <= 1) return 0;
-    return part_bytes(ks, batch, n_rq * 4) + ((int64_t)ks * batch * 4 + 255) / 256 * 256;
+    return kQgemmTicketBytes + part_bytes(ks, batch, n_rq * 4) +
+           ((int64_t)ks * ((n_rq + 31) / 32) * batch * 4 + 255) / 256 * 256;
 }
 
 // K-split partials of one projection of a decode batch: part [ks][batch][rows_p] and, with the
@@ -1558,7 +1709,7 @@ int split_proj_launch(int dtype, const void *wp, int64_t rows, int64_t cols, con
     const int64_t soff = gemm_scale_off(dtype, rows, cols);
     const auto *w = static_cast<const uint8_t *>(wp);
     if (use_split_kernel(ks, kper, soff + n_rq * nblk * 8)) {
-        split_kernel_launch(dtype, w, soff, n_rq, nblk, x, ldx, norm_w, batch, part, pssq, ks, kper, st);
+        split_kernel_launch(dtype, w, soff, n_rq, nblk, x, ldx, norm_w, batch, part, pssq, ks, kper, SplitFin{}, st);
         return ks;
     }
     const int nc = small_nc(batch, n_rq);
@@ -1583,7 +1734,7 @@ int64_t vgx_qgemm_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, int
     if (cols % QK) return VGX_E_SHAPE;
     const int64_t rows_p = rows4(epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows);
     const int ks = tile_ksplit(rows_p / 4, batch, (int)(cols / QK));
-    const int64_t big = split_bytes(batch, cols) + part_bytes(ks, batch, rows_p);
+    const int64_t big = kQgemmTicketBytes + split_bytes(batch, cols) + part_bytes(ks, batch, rows_p);
     return batch <= kSmallMaxBatch ? std::max(big, small_bytes(batch, rows_p / 4, (int)(cols / QK))) : big;
 }
 
@@ -1629,15 +1780,30 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
         const int64_t need = small_bytes(batch, n_rq, nblk);
         if (need > 0 && (!workspace || workspace_bytes < need)) return VGX_E_ARENA;
         if (need > 0 && (uintptr_t)workspace % 256) return VGX_E_ALIGN;
-        auto *part = static_cast<float *>(workspace);
-        auto *pssq = need > 0 ? reinterpret_cast<float *>(static_cast<char *>(workspace) +
+        auto *tickets = static_cast<int *>(workspace);
+        auto *part = need > 0 ? reinterpret_cast<float *>(static_cast<char *>(workspace) + kQgemmTicketBytes) : nullptr;
+        auto *pssq = need > 0 ? reinterpret_cast<float *>(static_cast<char *>(workspace) + kQgemmTicketBytes +
                                                           part_bytes(ks, batch, n_rq * 4))
                               : nullptr;
         const int nc = small_nc(batch, n_rq);
         const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 16 * nc - 1) / (16 * nc)), (unsigned)ks);
         const auto *w = static_cast<const uint8_t *>(w_packed);
         const bool sk = use_split_kernel(ks, kper, soff0 + n_rq * nblk * 8);
-        if (sk) split_kernel_launch(dtype, w, soff0, n_rq, nblk, x, ldx, norm_w, batch, part, pssq, ks, kper, st0);
+        if (sk && use_fused_finish(dtype, kper, n_rq, batch, ks)) {
+            // the split launch sums its own splits: no reduce launch
+            SplitFin fin;
+            fin.epi = epilogue == VGX_EPI_SWIGLU ? EPI_SWIGLU : epilogue == VGX_EPI_ACCUM ? EPI_ACCUM : EPI_STORE;
+            fin.rows_out = rows;
+            fin.eps = eps;
+            fin.bias = bias;
+            fin.y = y;
+            fin.ldy = ldy;
+            fin.cnt = tickets;
+            split_kernel_launch(dtype, w, soff0, n_rq, nblk, x, ldx, norm_w, batch, part, pssq, ks, kper, fin, st0);
+            VGX_CHECK_LAUNCH();
+            return VGX_OK;
+        }
+        if (sk) split_kernel_launch(dtype, w, soff0, n_rq, nblk, x, ldx, norm_w, batch, part, pssq, ks, kper, SplitFin{}, st0);
 #define VGX_SG(DT, NC, EPI, SP, NORM)                                                                         \
     hipLaunchKernelGGL((qgemm_small_kernel<DT, NC, EPI, SP, NORM>), grid, dim3(256), 0, st0, w, soff0, n_rq, nblk, \
                        rows, x, ldx, norm_w, eps, batch, bias, y, ldy, part, pssq, kper)
@@ -1672,18 +1838,20 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
         return VGX_OK;
     }
     const int ks = tile_ksplit(n_rq, batch, nblk);
-    if (!workspace || workspace_bytes < split_bytes(batch, cols) + part_bytes(ks, batch, n_rq * 4)) return VGX_E_ARENA;
+    if (!workspace || workspace_bytes < kQgemmTicketBytes + split_bytes(batch, cols) + part_bytes(ks, batch, n_rq * 4))
+        return VGX_E_ARENA;
     if ((uintptr_t)workspace % 256) return VGX_E_ALIGN;
     const int64_t soff = gemm_scale_off(dtype, rows_packed, cols);
     const int64_t pb = split_plane_bytes(batch, cols);
-    auto *xh = static_cast<uint16_t *>(workspace);
-    auto *xl = reinterpret_cast<uint16_t *>(static_cast<char *>(workspace) + pb);
-    auto *xs = reinterpret_cast<float *>(static_cast<char *>(workspace) + 2 * pb);
+    char *const wsb = static_cast<char *>(workspace) + kQgemmTicketBytes;   // past the tile counters
+    auto *xh = reinterpret_cast<uint16_t *>(wsb);
+    auto *xl = reinterpret_cast<uint16_t *>(wsb + pb);
+    auto *xs = reinterpret_cast<float *>(wsb + 2 * pb);
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(xsplit_kernel, dim3((unsigned)batch), dim3(256), 0, st, x, ldx, norm_w, eps, (int)cols, xh, xl,
                        xs);
     VGX_CHECK_LAUNCH();
-    auto *part = reinterpret_cast<float *>(static_cast<char *>(workspace) + split_bytes(batch, cols));
+    auto *part = reinterpret_cast<float *>(wsb + split_bytes(batch, cols));
     const int kper = (nblk + ks - 1) / ks;
     const dim3 grid((unsigned)((n_rq + kTM / 4 - 1) / (kTM / 4)), (unsigned)((batch + kTN - 1) / kTN), (unsigned)ks);
     const auto *w = static_cast<const uint8_t *>(w_packed);
@@ -1719,8 +1887,8 @@ int64_t vgx_qkv_rope_batch_workspace_bytes(int64_t B, int64_t d_model, int64_t H
     if (B <= 0 || d_model <= 0 || H <= 0 || G <= 0 || D <= 0) return VGX_E_SIZE;
     if (d_model % QK) return VGX_E_SHAPE;
     const int nblk = (int)(d_model / QK);
-    if (separate_q) return split_proj_bytes(B, H * D, nblk) + split_proj_bytes(B, 2 * G * D, nblk);
-    return split_proj_bytes(B, (H + 2 * G) * D, nblk);
+    if (separate_q) return kQgemmTicketBytes + split_proj_bytes(B, H * D, nblk) + split_proj_bytes(B, 2 * G * D, nblk);
+    return kQgemmTicketBytes + split_proj_bytes(B, (H + 2 * G) * D, nblk);
 }
 
 int vgx_qkv_rope_batch(int q_wdtype, const void *wq, const float *bq, int kv_wdtype, const void *wkv,
@@ -1747,7 +1915,7 @@ int vgx_qkv_rope_batch(int q_wdtype, const void *wq, const float *bq, int kv_wdt
     if (workspace_bytes < vgx_qkv_rope_batch_workspace_bytes(B, d_model, H, G, D, sep ? 1 : 0)) return VGX_E_ARENA;
     hipStream_t st = (hipStream_t)stream;
     const int nblk = (int)(d_model / QK);
-    auto *base = static_cast<char *>(workspace);
+    auto *base = static_cast<char *>(workspace) + kQgemmTicketBytes;   // the GEMM tile counters stay untouched
     auto carve = [&](int64_t rows, float *&part, float *&pssq) {
         const int64_t n_rq = rows4(rows) / 4;
         int kper = 0;

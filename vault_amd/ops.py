@@ -135,8 +135,9 @@ _GEMM_WS: dict = {}
 
 
 def gemm_workspace(device) -> "Workspace":
-    """Per-device workspace of the MFMA GEMM's activation splits (grow-only; a captured graph holds its
-    address, so callers that capture size it first)."""
+    """Per-device workspace of the MFMA GEMM's activation splits and K-split partials (grow-only; a
+    captured graph holds its address, so callers that capture size it first).  Its first 64 KiB are the
+    GEMM's output-tile counters, zero-filled here and left at zero by every call."""
     key = str(torch.device(device))
     if key not in _GEMM_WS:
         _GEMM_WS[key] = Workspace(torch.device(device))
