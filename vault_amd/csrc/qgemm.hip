@@ -918,21 +918,21 @@ __device__ __forceinline__ void ksplit_finish(const float *part, int ks, int64_t
     if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The work of one qgemm_split_kernel workgroup: row tile bx of W (blockIdx.y: activation tile,
+// blockIdx.z: split), with the workgroup's LDS areas passed in.
 template <int DT, bool NORM>
-__global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
-                                                             int nblk, int w_bytes, const float *__restrict__ x,
-                                                             int64_t ldx, const float *__restrict__ lnw,
-                                                             int64_t batch, float *__restrict__ part,
-                                                             float *__restrict__ part_ssq, int kper) {
+__device__ __forceinline__ void split_tile(uint8_t *__restrict__ smem_dyn, float *__restrict__ sinv, int64_t bx,
+                                           const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq, int nblk,
+                                           int w_bytes, const float *__restrict__ x, int64_t ldx,
+                                           const float *__restrict__ lnw, int64_t batch, float *__restrict__ part,
+                                           float *__restrict__ part_ssq, int kper) {
     using G = SplitGeom<DT>;
     constexpr int QB = G::QB;
     constexpr int R = 16;                                     // activation rows
     constexpr int F4 = R * kCK * 8 / 256;                     // staged float4 per thread and chunk
-    __shared__ __align__(16) uint8_t smem_dyn[split_lds_bytes(DT)];
-    __shared__ float sinv[R];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, lg = lane >> 4;
-    const int64_t rq_wave = ((int64_t)blockIdx.x * 4 + wave) * 8;
+    const int64_t rq_wave = (bx * 4 + wave) * 8;
     const int64_t b0 = (int64_t)blockIdx.y * R;
     const int blk_lo = (int)blockIdx.z * kper;
     const int blk_hi = min(nblk, blk_lo + kper);
@@ -1129,7 +1129,7 @@ __global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kerne
             if ((tid & 31) == 0) sinv[(tid >> 5) + 8 * i] = t;
         }
         __syncthreads();
-        if (blockIdx.x == 0 && tid < R && b0 + tid < batch)
+        if (bx == 0 && tid < R && b0 + tid < batch)
             part_ssq[(int64_t)blockIdx.z * batch + b0 + tid] = sinv[tid];
     }
     const int64_t bb = b0 + l16;
@@ -1143,6 +1143,45 @@ __global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kerne
             *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + bb) * rows_p + crq * 4) =
                 make_float4(S * acc[t][0], S * acc[t][1], S * acc[t][2], S * acc[t][3]);
         }
+    }
+}
+
+template <int DT, bool NORM>
+__global__ __launch_bounds__(256, DT == VGX_Q8_0 ? 2 : 3) void qgemm_split_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
+                                                             int nblk, int w_bytes, const float *__restrict__ x,
+                                                             int64_t ldx, const float *__restrict__ lnw,
+                                                             int64_t batch, float *__restrict__ part,
+                                                             float *__restrict__ part_ssq, int kper) {
+    __shared__ __align__(16) uint8_t smem_dyn[split_lds_bytes(DT)];
+    __shared__ float sinv[16];
+    split_tile<DT, NORM>(smem_dyn, sinv, blockIdx.x, W, soff, n_rq, nblk, w_bytes, x, ldx, lnw, batch, part, part_ssq,
+                         kper);
+}
+
+// The q and k|v projections of a decode batch (same activations, same K splits) in one launch: row
+// tiles 0 .. q.gx - 1 of the grid are q's, the rest k|v's, so the two weights' workgroups share the GPU
+// instead of two launches each filling part of it.
+struct SplitJob {
+    const uint8_t *w;
+    int64_t soff, n_rq;
+    int w_bytes, gx, ks;
+    float *part, *pssq;
+};
+
+template <int QDT, int KDT, bool NORM>
+__global__ __launch_bounds__(256, QDT == VGX_Q8_0 || KDT == VGX_Q8_0 ? 2 : 3) void qkv_split_kernel(
+    SplitJob jq, SplitJob jk, int nblk, const float *__restrict__ x, int64_t ldx, const float *__restrict__ lnw,
+    int64_t batch, int kper) {
+    constexpr int LB = split_lds_bytes(QDT) > split_lds_bytes(KDT) ? split_lds_bytes(QDT) : split_lds_bytes(KDT);
+    __shared__ __align__(16) uint8_t smem_dyn[LB];
+    __shared__ float sinv[16];
+    if ((int)blockIdx.x < jq.gx) {
+        if ((int)blockIdx.z < jq.ks)
+            split_tile<QDT, NORM>(smem_dyn, sinv, blockIdx.x, jq.w, jq.soff, jq.n_rq, nblk, jq.w_bytes, x, ldx, lnw,
+                                  batch, jq.part, jq.pssq, kper);
+    } else if ((int)blockIdx.z < jk.ks) {
+        split_tile<KDT, NORM>(smem_dyn, sinv, (int64_t)blockIdx.x - jq.gx, jk.w, jk.soff, jk.n_rq, nblk, jk.w_bytes, x,
+                              ldx, lnw, batch, jk.part, jk.pssq, kper);
     }
 }
 
@@ -1692,6 +1731,20 @@ __global__ __launch_bounds__(256) void qkv_split_rope_kernel(SplitSrc sq, SplitS
 }
 
 // Workspace of one split projection (partials, then the per-split sum x^2), 256-byte multiples.
+// Whether the q and k|v projections of a decode batch run as one qkv_split_kernel launch: both on
+// qgemm_split_kernel's tiles (K splits of the same length, not qgemm_kslice_kernel's 16-block ones).
+inline bool group_qkv(int q_dt, int64_t q_rows, int kv_dt, int64_t kv_rows, int64_t d_model, int64_t batch) {
+    const int nblk = (int)(d_model / QK);
+    int kq = 0, kk = 0;
+    const int64_t nq = rows4(q_rows) / 4, nk = rows4(kv_rows) / 4;
+    const int ksq = small_ksplit(nq, batch, nblk, &kq), ksk = small_ksplit(nk, batch, nblk, &kk);
+    const auto fits = [&](int dt, int64_t n_rq, int ks, int kp) {
+        return use_split_kernel(ks, kp, gemm_scale_off(dt, n_rq * 4, d_model) + n_rq * nblk * 8) &&
+               !(dt == VGX_Q4_0 && kp == kSplitMaxBlocks);
+    };
+    return kq == kk && fits(q_dt, nq, ksq, kq) && fits(kv_dt, nk, ksk, kk);
+}
+
 inline int64_t split_proj_bytes(int64_t batch, int64_t rows, int nblk) {
     const int64_t n_rq = rows4(rows) / 4;
     int kper = 0;
@@ -1927,7 +1980,41 @@ int vgx_qkv_rope_batch(int q_wdtype, const void *wq, const float *bq, int kv_wdt
     };
     SplitSrc sq{}, skv{};
     float *part = nullptr, *pssq = nullptr;
-    if (sep) {
+    if (sep && group_qkv(q_wdtype, H * D, kv_wdtype, 2 * G * D, d_model, B)) {
+        // q and k|v in one launch of qkv_split_kernel
+        const int64_t n_rq_q = rows4(H * D) / 4, n_rq_k = rows4(2 * G * D) / 4;
+        int kper = 0, kper_k = 0;
+        SplitJob jq{}, jk{};
+        jq.ks = small_ksplit(n_rq_q, B, nblk, &kper);
+        jk.ks = small_ksplit(n_rq_k, B, nblk, &kper_k);
+        jq.w = static_cast<const uint8_t *>(wq);
+        jq.soff = gemm_scale_off(q_wdtype, H * D, d_model);
+        jq.n_rq = n_rq_q;
+        jq.w_bytes = (int)(jq.soff + n_rq_q * nblk * 8);
+        jq.gx = (int)((n_rq_q + 31) / 32);
+        carve(H * D, jq.part, jq.pssq);
+        jk.w = static_cast<const uint8_t *>(wkv);
+        jk.soff = gemm_scale_off(kv_wdtype, 2 * G * D, d_model);
+        jk.n_rq = n_rq_k;
+        jk.w_bytes = (int)(jk.soff + n_rq_k * nblk * 8);
+        jk.gx = (int)((n_rq_k + 31) / 32);
+        carve(2 * G * D, jk.part, jk.pssq);
+        const dim3 g3((unsigned)(jq.gx + jk.gx), (unsigned)((B + 15) / 16), (unsigned)std::max(jq.ks, jk.ks));
+#define VGX_QKS(QDT, KDT)                                                                                         \
+    do {                                                                                                          \
+        if (norm_w) hipLaunchKernelGGL((qkv_split_kernel<QDT, KDT, true>), g3, dim3(256), 0, st, jq, jk, nblk, x, ldx, \
+                                       norm_w, B, kper);                                                         \
+        else hipLaunchKernelGGL((qkv_split_kernel<QDT, KDT, false>), g3, dim3(256), 0, st, jq, jk, nblk, x, ldx,    \
+                                norm_w, B, kper);                                                                \
+    } while (0)
+        if (q_wdtype == VGX_Q4_0) { if (kv_wdtype == VGX_Q4_0) VGX_QKS(VGX_Q4_0, VGX_Q4_0); else VGX_QKS(VGX_Q4_0, VGX_Q8_0); }
+        else { if (kv_wdtype == VGX_Q4_0) VGX_QKS(VGX_Q8_0, VGX_Q4_0); else VGX_QKS(VGX_Q8_0, VGX_Q8_0); }
+#undef VGX_QKS
+        sq.ks = jq.ks; sq.part = jq.part; sq.pssq = norm_w ? jq.pssq : nullptr; sq.bias = bq; sq.rows_p = rows4(H * D);
+        sq.roff = 0;
+        skv.ks = jk.ks; skv.part = jk.part; skv.pssq = norm_w ? jk.pssq : nullptr; skv.bias = bkv;
+        skv.rows_p = rows4(2 * G * D); skv.roff = 0;
+    } else if (sep) {
         carve(H * D, part, pssq);
         sq.ks = split_proj_launch(q_wdtype, wq, H * D, d_model, x, ldx, B, norm_w, eps, part, pssq, st);
         sq.part = part; sq.pssq = norm_w ? pssq : nullptr; sq.bias = bq; sq.rows_p = rows4(H * D); sq.roff = 0;
