@@ -1730,7 +1730,6 @@ __global__ __launch_bounds__(256) void qkv_split_rope_kernel(SplitSrc sq, SplitS
     }
 }
 
-// Workspace of one split projection (partials, then the per-split sum x^2), 256-byte multiples.
 // Whether the q and k|v projections of a decode batch run as one qkv_split_kernel launch: both on
 // qgemm_split_kernel's tiles (K splits of the same length, not qgemm_kslice_kernel's 16-block ones).
 inline bool group_qkv(int q_dt, int64_t q_rows, int kv_dt, int64_t kv_rows, int64_t d_model, int64_t batch) {
@@ -1745,6 +1744,7 @@ inline bool group_qkv(int q_dt, int64_t q_rows, int kv_dt, int64_t kv_rows, int6
     return kq == kk && fits(q_dt, nq, ksq, kq) && fits(kv_dt, nk, ksk, kk);
 }
 
+// Workspace of one split projection (partials, then the per-split sum x^2), 256-byte multiples.
 inline int64_t split_proj_bytes(int64_t batch, int64_t rows, int nblk) {
     const int64_t n_rq = rows4(rows) / 4;
     int kper = 0;
