@@ -1497,6 +1497,298 @@ void reduce_launch(const float *part, int ks, int64_t batch, int64_t rows_p, int
 #undef VGX_RED
 }
 
+// ---------------------------------------------------------------------------------------------
+// Decode batches, tall projections without K splits (the LM head, 151665 x 1536 Q8_0): qgemm_wide_kernel.
+// One persistent workgroup of 8 waves per CU holds the whole K of its 16 activation rows in LDS and
+// streams its share of the weight rows past them, so the activations are converted once per workgroup
+// and neither K-split partials nor a reduce launch exist:
+//  * Activations: the RMSNorm (when given) is applied in the staging pass (each workgroup has whole
+//    rows), then row b is scaled by 2^-e_b (e_b from its largest element, so that no value exceeds 2^14)
+//    and stored as fp16 hi = fp16(v) and lo = fp16(v - hi) (22 significant bits), in the K-slot order of
+//    the weight fragments, 16-byte groups swizzled by (row >> 2) & 3 against bank conflicts; with each
+//    block's offset correction off * sum (hi + lo) (off = 1152 for Q8_0, 1032 for Q4_0).
+//  * Weights: one fp16 fragment serves both products.  Q8_0: fp16(1024 + (q ^ 0x80)) = 0x6400 | byte,
+//    the byte beside a constant 0x64 by one byte permute per two weights; Q4_0: fp16(1024 + n) from the
+//    nibbles the same way.  A block's products then sum to sum q (hi + lo) + off sum (hi + lo).
+//  * A wave takes 32 weight rows (two 16-row tiles, sharing each B operand read) over the whole K in
+//    4-block chunks, the next chunk's contiguous 16-byte weight loads in flight while it multiplies the
+//    current one (through a wave-private LDS area into the MFMA layout, as qgemm_kslice_kernel); per
+//    chunk and tile the scales enter with one fma per output and the offset corrections with one fp32
+//    MFMA.  At the end of a tile pair the sums are scaled back by 2^e_b and stored.
+//  * Grid: P row groups x the activation tiles; the workgroups of one row group sit on one XCD (ids
+//    8 k + r for the same r), so the second activation tile reads the group's weights from that XCD's L2.
+constexpr int kWideWaves = 8;
+constexpr int kWideMaxCols = 1536;                      // staged K of 16 rows: 64 KiB per 1024 columns
+constexpr int kWideRow = 80;                            // LDS bytes per weight row of a chunk (Q8_0: 4 x 16 + 16 pad)
+
+template <int DT>
+struct WideGeom {
+    static constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;         // bytes of one row's block
+    static constexpr int NLD = DT == VGX_Q8_0 ? 4 : 2;          // 16-byte weight loads per lane and chunk
+    static constexpr int ROW = DT == VGX_Q8_0 ? 128 : 64;       // LDS bytes per weight row of a chunk
+    static constexpr int WAVE = 32 * ROW + 8 * 32;             // per wave: 32 rows, then 8 row-quads of scales
+};
+
+constexpr int wide_lds_bytes(int dt) {
+    return kWideMaxCols / QK * (2 * 16 * 64 + 16 * 4) + 16 * 4 +
+           kWideWaves * (dt == VGX_Q8_0 ? WideGeom<VGX_Q8_0>::WAVE : WideGeom<VGX_Q4_0>::WAVE);
+}
+static_assert(wide_lds_bytes(VGX_Q8_0) <= 160 * 1024, "LDS of qgemm_wide_kernel");
+
+// One lane's fp16 fragment (1024 + unsigned weight) of one block: Q8_0 from its 8 bytes, Q4_0 from its word.
+template <int DT>
+__device__ __forceinline__ f16x8_t wide_frag(uint2 w) {
+    constexpr uint32_t C = 0x00000064u;                 // byte 4 of the permute: 0x64
+    uint32_t a, b;
+    if constexpr (DT == VGX_Q8_0) {
+        a = w.x ^ 0x80808080u;
+        b = w.y ^ 0x80808080u;
+    } else {
+        a = w.x & 0x0F0F0F0Fu;                          // weights 4 lg + i (low nibbles)
+        b = (w.x >> 4) & 0x0F0F0F0Fu;                   // weights 16 + 4 lg + i
+    }
+    return __builtin_bit_cast(f16x8_t, make_uint4(__builtin_amdgcn_perm(C, a, 0x04010400u),
+                                                  __builtin_amdgcn_perm(C, a, 0x04030402u),
+                                                  __builtin_amdgcn_perm(C, b, 0x04010400u),
+                                                  __builtin_amdgcn_perm(C, b, 0x04030402u)));
+}
+
+template <int DT, bool NORM>
+__global__ __launch_bounds__(64 * kWideWaves, 1) void qgemm_wide_kernel(
+    const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq, int nblk, int w_bytes, const float *__restrict__ x,
+    int64_t ldx, const float *__restrict__ lnw, float eps, int64_t batch, const float *__restrict__ bias,
+    float *__restrict__ y, int64_t ldy, int64_t rows_out, int n_groups) {
+    using G = WideGeom<DT>;
+    constexpr int QB = G::QB;
+    constexpr float OFF = DT == VGX_Q8_0 ? 1152.0f : 1032.0f;
+    __shared__ __align__(16) uint8_t smem[wide_lds_bytes(DT)];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int cols = nblk * QK;
+    // workgroup -> (row group, activation tile): ids 8 k + r with equal k / nbt share row group 8 k' + r
+    const int nbt = (int)((batch + 15) / 16);
+    const int id = blockIdx.x;
+    const int grp = (id / (8 * nbt)) * 8 + (id & 7);
+    const int bt = (id >> 3) % nbt;
+    const int64_t b0 = (int64_t)bt * 16;
+    uint8_t *xs = smem;                                              // [block][plane][row][64 B]
+    float *corr = reinterpret_cast<float *>(smem + kWideMaxCols / QK * 2 * 16 * 64);   // [block][row]
+    float *escale = corr + kWideMaxCols / QK * 16;                  // [row] 2^e_b
+    uint8_t *wl = smem + kWideMaxCols / QK * (2 * 16 * 64 + 16 * 4) + 16 * 4 + wave * G::WAVE;
+    uint8_t *wsc = wl + 32 * G::ROW;
+
+    // ---- staging: thread (row tid / 32, float4 groups (tid % 32) + 32 i)
+    {
+        const int r = tid >> 5, j = tid & 31;
+        const int64_t b = b0 + r;
+        const int n4 = cols / 4;
+        constexpr int MAXI = kWideMaxCols / 4 / 32;
+        float4 v[MAXI];
+        float ssq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MAXI; ++i) {
+            const int k4 = j + 32 * i;
+            v[i] = k4 < n4 && b < batch ? *reinterpret_cast<const float4 *>(x + b * ldx + 4 * k4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            ssq += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+        }
+        float inv = 1.0f;
+        if constexpr (NORM) {
+            const float t = xor16_sum(row16_sum(ssq));               // the 32 threads of the row
+            inv = 1.0f / sqrtf(t / (float)cols + eps);
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < MAXI; ++i) {
+            const int k4 = j + 32 * i;
+            if (NORM && k4 < n4) {
+                const float4 g = *reinterpret_cast<const float4 *>(lnw + 4 * k4);
+                v[i] = make_float4(g.x * (v[i].x * inv), g.y * (v[i].y * inv), g.z * (v[i].z * inv), g.w * (v[i].w * inv));
+            }
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        }
+        mx = xor16_max(row16_max(mx));
+        int ex = 0;
+        (void)frexpf(mx, &ex);                                       // mx < 2^ex
+        const int e = ex > 14 ? ex - 14 : 0;
+        const float sdown = ldexpf(1.0f, -e);
+        if (j == 0) escale[r] = ldexpf(1.0f, e);
+#pragma unroll
+        for (int i = 0; i < MAXI; ++i) {
+            const int k4 = j + 32 * i;
+            if (k4 >= n4) break;
+            const int kb = k4 >> 3, m = k4 & 7;
+            const float e4[4] = {v[i].x * sdown, v[i].y * sdown, v[i].z * sdown, v[i].w * sdown};
+            uint2 hw, lw;
+            float hs = 0.0f;
+            {
+                const uint32_t h01 = pack_f16x2(e4[0], e4[1]), h23 = pack_f16x2(e4[2], e4[3]);
+                const auto f01 = __builtin_bit_cast(vgx_f16x2_t, h01), f23 = __builtin_bit_cast(vgx_f16x2_t, h23);
+                const float h[4] = {(float)f01[0], (float)f01[1], (float)f23[0], (float)f23[1]};
+                const uint32_t l01 = pack_f16x2(e4[0] - h[0], e4[1] - h[1]), l23 = pack_f16x2(e4[2] - h[2], e4[3] - h[3]);
+                const auto g01 = __builtin_bit_cast(vgx_f16x2_t, l01), g23 = __builtin_bit_cast(vgx_f16x2_t, l23);
+                hs = ((h[0] + h[1]) + (h[2] + h[3])) + (((float)g01[0] + (float)g01[1]) + ((float)g23[0] + (float)g23[1]));
+                hw = make_uint2(h01, h23);
+                lw = make_uint2(l01, l23);
+            }
+            // K-slot position (halves) within the row's 32-slot block, then the swizzled 16-byte group
+            const int pos = DT == VGX_Q8_0 ? 4 * m : 8 * (m & 3) + 4 * (m >> 2);
+            const int grp16 = (pos >> 3) ^ ((r >> 2) & 3);
+            uint8_t *row = xs + ((int64_t)kb * 2 * 16 + r) * 64;
+            *reinterpret_cast<uint2 *>(row + grp16 * 16 + (pos & 7) * 2) = hw;
+            *reinterpret_cast<uint2 *>(row + 16 * 64 + grp16 * 16 + (pos & 7) * 2) = lw;
+            hs += __shfl_xor(hs, 1, kWave);
+            hs += __shfl_xor(hs, 2, kWave);
+            hs += __shfl_xor(hs, 4, kWave);
+            if ((j & 7) == 0) corr[kb * 16 + r] = -OFF * hs;
+        }
+    }
+    __syncthreads();
+
+    // ---- streaming: wave w of row group grp takes 32-row pairs of tiles grp * per + w, + 8, ...
+    const int64_t n_pairs = (n_rq + 7) / 8;                          // 8 row-quads per pair
+    const int64_t per = (n_pairs + n_groups - 1) / n_groups;
+    const int64_t p_lo = (int64_t)grp * per, p_hi = min(n_pairs, p_lo + per);
+    const int nch = (nblk + kCK - 1) / kCK;
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, w_bytes, 0x00020000);
+    const int64_t my_first = p_lo + wave;
+    const int64_t my_n = my_first < p_hi ? (p_hi - my_first + kWideWaves - 1) / kWideWaves : 0;
+    const int64_t iters = my_n * nch;
+    // loads of iteration it (pair my_first + 8 (it / nch), chunk it % nch); past the end: reads nothing
+    auto fetch = [&](int64_t it, uint4 (&wv)[G::NLD], uint2 &sv) {
+        const bool in = it < iters;
+        const int64_t pr = my_first + (in ? it / nch : 0) * kWideWaves;
+        const int c = in ? (int)(it % nch) : 0;
+        const int bk = c * kCK;
+#pragma unroll
+        for (int h = 0; h < G::NLD; ++h) {
+            // Q8_0: 32 lanes x 16 bytes per row-quad chunk (4 blocks x 4 rows x 32 bytes), two row-quads
+            // per load; Q4_0: 16 lanes per row-quad chunk (4 blocks x 4 rows x 16 bytes), four per load
+            const int64_t rq = pr * 8 + (DT == VGX_Q8_0 ? 2 * h + (lane >> 5) : 4 * h + (lane >> 4));
+            const uint32_t o = in && rq < n_rq && bk < nblk
+                                   ? (uint32_t)(rq * nblk * 4 * QB + (int64_t)bk * 4 * QB) + (uint32_t)((lane & (DT == VGX_Q8_0 ? 31 : 15)) * 16)
+                                   : kPastEnd;
+            const auto t = __builtin_amdgcn_raw_buffer_load_b128(wrs, o, 0, 0);
+            wv[h] = make_uint4(t[0], t[1], t[2], t[3]);
+        }
+        // scales: 8 row-quads x 4 blocks x 8 bytes, lane l: row-quad l / 8, block l % 8 / 2, half l % 2
+        const int64_t rq = pr * 8 + (lane >> 3);
+        const int blk = bk + ((lane >> 1) & 3);
+        const uint32_t so = in && rq < n_rq && blk < nblk ? (uint32_t)(soff + rq * nblk * 8 + (int64_t)blk * 8 + (lane & 1) * 4)
+                                                         : kPastEnd;
+        const uint32_t s0 = __builtin_amdgcn_raw_buffer_load_b32(wrs, so, 0, 0);
+        sv = make_uint2(s0, 0u);
+    };
+
+    f32x4_t acc[2];
+    acc[0] = acc[1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    auto step = [&](int64_t it, const uint4 (&wv)[G::NLD], const uint2 &sv) {
+        const int c = (int)(it % nch);
+        const int bk = c * kCK;
+        // the chunk's words into the MFMA layout: row r (32 rows of the pair), block u, lane group lg
+#pragma unroll
+        for (int h = 0; h < G::NLD; ++h) {
+            const uint4 v = wv[h];
+            if constexpr (DT == VGX_Q8_0) {
+                // lane: row-quad 2 h + lane / 32, 16-byte piece (lane % 32) = block u = piece / 8, row
+                // r4 = piece / 2 % 4, half hf = piece % 2 (bytes 16 hf .. + 15 of the row's block)
+                const int pc = lane & 31, u = pc >> 3, r4 = (pc >> 1) & 3, hf = pc & 1;
+                const int row = (2 * h + (lane >> 5)) * 4 + r4;
+                // row layout: [lg (0..3)][u][8 bytes], lg-groups of 32 bytes swizzled by (row >> 2) & 3
+                uint8_t *p = wl + row * G::ROW;
+                const int sw = (row >> 2) & 3;
+                *reinterpret_cast<uint2 *>(p + ((2 * hf) ^ sw) * 32 + u * 8) = make_uint2(v.x, v.y);
+                *reinterpret_cast<uint2 *>(p + ((2 * hf + 1) ^ sw) * 32 + u * 8) = make_uint2(v.z, v.w);
+            } else {
+                const int row = (4 * h + (lane >> 4)) * 4 + (lane & 3), u = (lane & 15) >> 2;
+                uint32_t *p = reinterpret_cast<uint32_t *>(wl + row * G::ROW) + u;
+                const int sw = (row >> 2) & 3;
+                p[(0 ^ sw) * 4] = v.x;
+                p[(1 ^ sw) * 4] = v.y;
+                p[(2 ^ sw) * 4] = v.z;
+                p[(3 ^ sw) * 4] = v.w;
+            }
+        }
+        reinterpret_cast<uint32_t *>(wsc)[lane] = sv.x;             // [row-quad][block][4 halves]
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int xsw = (l16 >> 2) & 3;
+        f32x4_t pr[2][4];
+#pragma unroll
+        for (int u = 0; u < kCK; ++u) {
+            const int kb = min(bk + u, nblk - 1);                    // a block past K reads zero weights
+            const uint8_t *xr = xs + ((int64_t)kb * 2 * 16 + l16) * 64 + (lg ^ xsw) * 16;
+            const f16x8_t xh = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4 *>(xr));
+            const f16x8_t xl = __builtin_bit_cast(f16x8_t, *reinterpret_cast<const uint4 *>(xr + 16 * 64));
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int row = 16 * t + l16;
+                const int sw = (row >> 2) & 3;
+                uint2 w;
+                if constexpr (DT == VGX_Q8_0) w = *reinterpret_cast<const uint2 *>(wl + row * G::ROW + (lg ^ sw) * 32 + u * 8);
+                else w = make_uint2(*reinterpret_cast<const uint32_t *>(wl + row * G::ROW + (lg ^ sw) * 16 + u * 4), 0u);
+                const f16x8_t a = wide_frag<DT>(w);
+                f32x4_t q = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                q = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xh, q, 0, 0, 0);
+                q = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, xl, q, 0, 0, 0);
+                pr[t][u] = q;
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            // scales of the tile's row-quads 4 t + lg for the chunk's blocks: wsc [rq][u] 4 halves
+            const uint4 s0 = *reinterpret_cast<const uint4 *>(wsc + (4 * t + lg) * 32);
+            const uint4 s1 = *reinterpret_cast<const uint4 *>(wsc + (4 * t + lg) * 32 + 16);
+            const uint2 scu[4] = {make_uint2(s0.x, s0.y), make_uint2(s0.z, s0.w), make_uint2(s1.x, s1.y),
+                                  make_uint2(s1.z, s1.w)};
+#pragma unroll
+            for (int u = 0; u < kCK; ++u) {
+                const float d[4] = {half_bits_to_float(scu[u].x), half_bits_to_float(scu[u].x >> 16),
+                                    half_bits_to_float(scu[u].y), half_bits_to_float(scu[u].y >> 16)};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(d[i], pr[t][u][i], acc[t][i]);
+            }
+            // offset corrections of the chunk's blocks: scales (row l16 of the tile, block lg) x -corr
+            const uint32_t da = *reinterpret_cast<const uint16_t *>(wsc + (4 * t + (l16 >> 2)) * 32 + lg * 8 + (l16 & 3) * 2);
+            const int kb = bk + lg;
+            const float cn = kb < nblk ? corr[kb * 16 + l16] : 0.0f;
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(half_bits_to_float(da), cn, acc[t], 0, 0, 0);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (c == nch - 1) {
+            // the pair's outputs: lane holds rows 4 lg .. + 3 of tile t for activation row l16
+            const int64_t pr_idx = my_first + (it / nch) * kWideWaves;
+            const int64_t b = b0 + l16;
+            const float sc = escale[l16];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int64_t rq = pr_idx * 8 + 4 * t + lg;
+                if (b < batch && rq < n_rq) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int64_t row = rq * 4 + i;
+                        if (row < rows_out) y[b * ldy + row] = acc[t][i] * sc + (bias ? bias[row] : 0.0f);
+                    }
+                }
+                acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+    };
+
+    uint4 wa[G::NLD], wb[G::NLD];
+    uint2 sa, sb;
+    fetch(0, wa, sa);
+    for (int64_t it = 0; it < iters; it += 2) {
+        fetch(it + 1, wb, sb);
+        step(it, wa, sa);
+        if (it + 1 >= iters) break;
+        fetch(it + 2, wa, sa);
+        step(it + 1, wb, sb);
+    }
+}
+
 inline int64_t rows4(int64_t r) { return (r + 3) / 4 * 4; }
 
 int64_t gemm_scale_off(int dt, int64_t rows, int64_t cols) {
@@ -1561,6 +1853,13 @@ inline int small_ksplit(int64_t n_rq, int64_t batch, int nblk, int *kper) {
         kp = kSplitMaxBlocks;
     *kper = kp;
     return (nblk + kp - 1) / kp;
+}
+
+// Whether qgemm_wide_kernel takes a projection of a decode batch: one split (tall weights), K within its
+// staged width, the store epilogue, byte offsets within the 31-bit buffer range, and enough row
+// tiles for its 256 persistent workgroups to stream.
+inline bool use_wide_kernel(int ks, int64_t n_rq, int64_t cols, int epilogue, int64_t w_bytes) {
+    return ks == 1 && epilogue == VGX_EPI_STORE && cols <= kWideMaxCols && n_rq >= 4096 && w_bytes < ((int64_t)1 << 31);
 }
 
 // Whether qgemm_split_kernel takes a split projection: splits of at most kSplitMaxBlocks blocks and a
@@ -1841,6 +2140,19 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
         const int nc = small_nc(batch, n_rq);
         const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 16 * nc - 1) / (16 * nc)), (unsigned)ks);
         const auto *w = static_cast<const uint8_t *>(w_packed);
+        if (use_wide_kernel(ks, n_rq, cols, epilogue, soff0 + n_rq * nblk * 8)) {
+            const int nbt = (int)((batch + 15) / 16);
+            const int n_groups = 256 / nbt / 8 * 8;
+            const int wb = (int)(soff0 + n_rq * nblk * 8);
+#define VGX_WD(DT, NORM)                                                                                          \
+    hipLaunchKernelGGL((qgemm_wide_kernel<DT, NORM>), dim3((unsigned)(n_groups * nbt)), dim3(64 * kWideWaves), 0, st0, \
+                       w, soff0, n_rq, nblk, wb, x, ldx, norm_w, eps, batch, bias, y, ldy, rows, n_groups)
+            if (dtype == VGX_Q8_0) { if (norm_w) VGX_WD(VGX_Q8_0, true); else VGX_WD(VGX_Q8_0, false); }
+            else { if (norm_w) VGX_WD(VGX_Q4_0, true); else VGX_WD(VGX_Q4_0, false); }
+#undef VGX_WD
+            VGX_CHECK_LAUNCH();
+            return VGX_OK;
+        }
         const bool sk = use_split_kernel(ks, kper, soff0 + n_rq * nblk * 8);
         if (sk && use_fused_finish(dtype, kper, n_rq, batch, ks)) {
             // the split launch sums its own splits: no reduce launch
