@@ -70,13 +70,13 @@ def test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm):
 @pytest.mark.parametrize("rows,cols,batch,epi,norm", [
     (8960, 1536, 1024, "swiglu", True), (10246, 512, 820, "accum", False), (10246, 512, 820, "store", True),
     (65541, 256, 40, "store", True), (65541, 256, 17, "accum", False), (65541, 768, 32, "store", True),
-    (65541, 768, 20, "store", False)])
+    (65541, 768, 20, "store", False), (65541, 1536, 32, "store", True)])
 def test_qgemm_chunk_shapes_match_oracle(dev, dt, rows, cols, batch, epi, norm):
     """Many tiles: the gate/up pair of a full 1024-token prefill chunk (1120 tiles, three rounds of
     workgroups), 10246 x 512 over 820 activation rows (ragged rows and activation rows in the last
-    tiles), and LM-head-like tall weights (65541 rows, ragged; the stores run on the persistent
-    unsplit kernel, with 3, 2 and 2 activation tiles per row group, the accumulate on the 32-row tiles
-    of the small-batch kernel).  Same bar as above."""
+    tiles), and LM-head-like tall weights (65541 rows, ragged; the stores over 768 and 1536 columns run
+    on the persistent unsplit kernel, with 2 activation tiles per row group, the others on the 32-row
+    tiles of the small-batch kernel).  Same bar as above."""
     test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm)
 
 

@@ -1511,13 +1511,13 @@ void reduce_launch(const float *part, int ks, int64_t batch, int64_t rows_p, int
 //    the byte beside a constant 0x64 by one byte permute per two weights; Q4_0: fp16(1024 + n) from the
 //    nibbles the same way.  A block's products then sum to sum q (hi + lo) + off sum (hi + lo).
 //  * A wave takes 32 weight rows (two 16-row tiles, sharing each B operand read) over the whole K in
-//    4-block chunks, the next chunk's contiguous 16-byte weight loads in flight while it multiplies the
-//    current one (through a wave-private LDS area into the MFMA layout, as qgemm_kslice_kernel); per
+//    4-block chunks, the next three chunks' contiguous 16-byte weight loads in flight while it multiplies
+//    the current one (through a wave-private LDS area into the MFMA layout, as qgemm_kslice_kernel); per
 //    chunk and tile the scales enter with one fma per output and the offset corrections with one fp32
 //    MFMA.  At the end of a tile pair the sums are scaled back by 2^e_b and stored.
 //  * Grid: P row groups x the activation tiles; the workgroups of one row group sit on one XCD (ids
 //    8 k + r for the same r), so the second activation tile reads the group's weights from that XCD's L2.
-constexpr int kWideWaves = 8;
+constexpr int kWideWaves = 12;                         // waves 0..7 also stage the activations
 constexpr int kWideMaxCols = 1536;                      // staged K of 16 rows: 64 KiB per 1024 columns
 constexpr int kWideRow = 80;                            // LDS bytes per weight row of a chunk (Q8_0: 4 x 16 + 16 pad)
 
@@ -1553,16 +1553,17 @@ __device__ __forceinline__ f16x8_t wide_frag(uint2 w) {
                                                   __builtin_amdgcn_perm(C, b, 0x04030402u)));
 }
 
-template <int DT, bool NORM>
+template <int DT, bool NORM, int NCH>
 __global__ __launch_bounds__(64 * kWideWaves, 1) void qgemm_wide_kernel(
     const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq, int nblk, int w_bytes, const float *__restrict__ x,
-    int64_t ldx, const float *__restrict__ lnw, float eps, int64_t batch, const float *__restrict__ bias,
-    float *__restrict__ y, int64_t ldy, int64_t rows_out, int n_groups) {
+    int64_t ldx, const float *__restrict__ lnw, float eps, int64_t batch, float *__restrict__ y, int64_t ldy,
+    int64_t rows_out, int n_groups) {
     using G = WideGeom<DT>;
     constexpr int QB = G::QB;
     constexpr float OFF = DT == VGX_Q8_0 ? 1152.0f : 1032.0f;
     __shared__ __align__(16) uint8_t smem[wide_lds_bytes(DT)];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, lg = lane >> 4;
     const int cols = nblk * QK;
     // workgroup -> (row group, activation tile): ids 8 k + r with equal k / nbt share row group 8 k' + r
@@ -1577,8 +1578,8 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void qgemm_wide_kernel(
     uint8_t *wl = smem + kWideMaxCols / QK * (2 * 16 * 64 + 16 * 4) + 16 * 4 + wave * G::WAVE;
     uint8_t *wsc = wl + 32 * G::ROW;
 
-    // ---- staging: thread (row tid / 32, float4 groups (tid % 32) + 32 i)
-    {
+    // ---- staging: thread (row tid / 32, float4 groups (tid % 32) + 32 i) of the first 8 waves
+    if (tid < 16 * 32) {
         const int r = tid >> 5, j = tid & 31;
         const int64_t b = b0 + r;
         const int n4 = cols / 4;
@@ -1648,41 +1649,47 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void qgemm_wide_kernel(
     const int64_t n_pairs = (n_rq + 7) / 8;                          // 8 row-quads per pair
     const int64_t per = (n_pairs + n_groups - 1) / n_groups;
     const int64_t p_lo = (int64_t)grp * per, p_hi = min(n_pairs, p_lo + per);
-    const int nch = (nblk + kCK - 1) / kCK;
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, w_bytes, 0x00020000);
     const int64_t my_first = p_lo + wave;
-    const int64_t my_n = my_first < p_hi ? (p_hi - my_first + kWideWaves - 1) / kWideWaves : 0;
-    const int64_t iters = my_n * nch;
-    // loads of iteration it (pair my_first + 8 (it / nch), chunk it % nch); past the end: reads nothing
-    auto fetch = [&](int64_t it, uint4 (&wv)[G::NLD], uint2 &sv) {
-        const bool in = it < iters;
-        const int64_t pr = my_first + (in ? it / nch : 0) * kWideWaves;
-        const int c = in ? (int)(it % nch) : 0;
-        const int bk = c * kCK;
+    const int my_n = my_first < p_hi ? (int)((p_hi - my_first + kWideWaves - 1) / kWideWaves) : 0;
+    // a position in the wave's stream: its pair (0 .. my_n - 1) and chunk (0 .. NCH - 1)
+    struct Pos {
+        int pair, c;
+    };
+    // loads of chunk q.c of pair q.pair; past the wave's last pair: offsets past the buffer, no traffic.
+    // The offsets are a wave-uniform base plus constant lane parts: row-quads past the weight (the
+    // last pair) read the bytes after it inside the buffer, finite values whose rows are not stored.
+    constexpr int PIECES = DT == VGX_Q8_0 ? 32 : 16;               // 16-byte pieces per row-quad chunk
+    const uint32_t rq_bytes = (uint32_t)nblk * 4 * QB;              // one row-quad's quants
+    const uint32_t lane_w = (uint32_t)(lane / PIECES) * rq_bytes + (uint32_t)(lane % PIECES) * 16;
+    const int lane_blk = (lane >> 1) & 3;
+    const uint32_t lane_s = (uint32_t)(lane >> 3) * (uint32_t)nblk * 8 + (uint32_t)lane_blk * 8 + (lane & 1) * 4;
+    auto fetch = [&](const Pos &q, uint4 (&wv)[G::NLD + 1]) {
+        const bool in = q.pair < my_n;
+        const uint32_t pr = (uint32_t)(my_first + (int64_t)(in ? q.pair : 0) * kWideWaves);
+        const int bk = q.c * kCK;
+        const uint32_t base = pr * 8 * rq_bytes + (uint32_t)bk * 4 * QB;
 #pragma unroll
         for (int h = 0; h < G::NLD; ++h) {
-            // Q8_0: 32 lanes x 16 bytes per row-quad chunk (4 blocks x 4 rows x 32 bytes), two row-quads
-            // per load; Q4_0: 16 lanes per row-quad chunk (4 blocks x 4 rows x 16 bytes), four per load
-            const int64_t rq = pr * 8 + (DT == VGX_Q8_0 ? 2 * h + (lane >> 5) : 4 * h + (lane >> 4));
-            const uint32_t o = in && rq < n_rq && bk < nblk
-                                   ? (uint32_t)(rq * nblk * 4 * QB + (int64_t)bk * 4 * QB) + (uint32_t)((lane & (DT == VGX_Q8_0 ? 31 : 15)) * 16)
-                                   : kPastEnd;
+            const uint32_t o = in ? base + (uint32_t)(h * (64 / PIECES)) * rq_bytes + lane_w : kPastEnd;
             const auto t = __builtin_amdgcn_raw_buffer_load_b128(wrs, o, 0, 0);
             wv[h] = make_uint4(t[0], t[1], t[2], t[3]);
         }
-        // scales: 8 row-quads x 4 blocks x 8 bytes, lane l: row-quad l / 8, block l % 8 / 2, half l % 2
-        const int64_t rq = pr * 8 + (lane >> 3);
-        const int blk = bk + ((lane >> 1) & 3);
-        const uint32_t so = in && rq < n_rq && blk < nblk ? (uint32_t)(soff + rq * nblk * 8 + (int64_t)blk * 8 + (lane & 1) * 4)
-                                                         : kPastEnd;
-        const uint32_t s0 = __builtin_amdgcn_raw_buffer_load_b32(wrs, so, 0, 0);
-        sv = make_uint2(s0, 0u);
+        // scales: 8 row-quads x 4 blocks x 8 bytes, lane l: row-quad l / 8, block l % 8 / 2, half l % 2;
+        // blocks past K (a partial last chunk) read zero, which zeroes their weights' products
+        const uint32_t so = in && bk + lane_blk < nblk ? (uint32_t)soff + pr * 8 * (uint32_t)nblk * 8 + (uint32_t)bk * 8 + lane_s
+                                                      : kPastEnd;
+        wv[G::NLD].x = __builtin_amdgcn_raw_buffer_load_b32(wrs, so, 0, 0);
     };
 
+    // outputs through buffer stores (rows past the weight or the batch: offsets past the buffer), so the
+    // waits for the streamed weights count exactly
+    const __amdgpu_buffer_rsrc_t yrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)y, 0, (int)(((batch - 1) * ldy + rows_out) * 4), 0x00020000);
     f32x4_t acc[2];
     acc[0] = acc[1] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    auto step = [&](int64_t it, const uint4 (&wv)[G::NLD], const uint2 &sv) {
-        const int c = (int)(it % nch);
+    auto step = [&](const Pos &q, const uint4 (&wv)[G::NLD + 1]) {
+        const int c = q.c;
         const int bk = c * kCK;
         // the chunk's words into the MFMA layout: row r (32 rows of the pair), block u, lane group lg
 #pragma unroll
@@ -1708,7 +1715,7 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void qgemm_wide_kernel(
                 p[(3 ^ sw) * 4] = v.w;
             }
         }
-        reinterpret_cast<uint32_t *>(wsc)[lane] = sv.x;             // [row-quad][block][4 halves]
+        reinterpret_cast<uint32_t *>(wsc)[lane] = wv[G::NLD].x;      // [row-quad][block][4 halves]
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1757,35 +1764,39 @@ __global__ __launch_bounds__(64 * kWideWaves, 1) void qgemm_wide_kernel(
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (c == nch - 1) {
+        if (c == NCH - 1) {
             // the pair's outputs: lane holds rows 4 lg .. + 3 of tile t for activation row l16
-            const int64_t pr_idx = my_first + (it / nch) * kWideWaves;
+            const int64_t pr_idx = my_first + (int64_t)q.pair * kWideWaves;
             const int64_t b = b0 + l16;
             const float sc = escale[l16];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const int64_t rq = pr_idx * 8 + 4 * t + lg;
-                if (b < batch && rq < n_rq) {
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int64_t row = rq * 4 + i;
-                        if (row < rows_out) y[b * ldy + row] = acc[t][i] * sc + (bias ? bias[row] : 0.0f);
-                    }
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t row = rq * 4 + i;
+                    const uint32_t o = b < batch && row < rows_out ? (uint32_t)((b * ldy + row) * 4) : kPastEnd;
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[t][i] * sc), yrs, o, 0, 0);
                 }
                 acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
             }
         }
     };
 
-    uint4 wa[G::NLD], wb[G::NLD];
-    uint2 sa, sb;
-    fetch(0, wa, sa);
-    for (int64_t it = 0; it < iters; it += 2) {
-        fetch(it + 1, wb, sb);
-        step(it, wa, sa);
-        if (it + 1 >= iters) break;
-        fetch(it + 2, wa, sa);
-        step(it + 1, wb, sb);
+    // a ring of RB register buffers (RB divides NCH, so chunk c of every pair sits in buffer c % RB):
+    // chunk n + RB - 1 of the stream is requested while chunk n is multiplied
+    constexpr int RB = NCH % 4 == 0 ? 4 : NCH % 3 == 0 ? 3 : 2;
+    uint4 wb[RB][G::NLD + 1];
+#pragma unroll
+    for (int c = 0; c < RB - 1; ++c) fetch(Pos{0, c}, wb[c]);
+    for (int pi = 0; pi < my_n; ++pi) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            constexpr int D = RB - 1;
+            const int cn = c + D;
+            fetch(cn < NCH ? Pos{pi, cn} : Pos{pi + 1, cn - NCH}, wb[cn % RB]);
+            step(Pos{pi, c}, wb[c % RB]);
+        }
     }
 }
 
@@ -1855,11 +1866,12 @@ inline int small_ksplit(int64_t n_rq, int64_t batch, int nblk, int *kper) {
     return (nblk + kp - 1) / kp;
 }
 
-// Whether qgemm_wide_kernel takes a projection of a decode batch: one split (tall weights), K within its
-// staged width, the store epilogue, byte offsets within the 31-bit buffer range, and enough row
+// Whether qgemm_wide_kernel takes a projection of a decode batch (without bias): one split (tall
+// weights), K of 48 or 24 blocks (its compiled chunk counts), the store epilogue, byte offsets within the 31-bit buffer range, and enough row
 // tiles for its 256 persistent workgroups to stream.
 inline bool use_wide_kernel(int ks, int64_t n_rq, int64_t cols, int epilogue, int64_t w_bytes) {
-    return ks == 1 && epilogue == VGX_EPI_STORE && cols <= kWideMaxCols && n_rq >= 4096 && w_bytes < ((int64_t)1 << 31);
+    return ks == 1 && epilogue == VGX_EPI_STORE && (cols == 1536 || cols == 768) && n_rq >= 4096 &&
+           w_bytes < ((int64_t)1 << 31);
 }
 
 // Whether qgemm_split_kernel takes a split projection: splits of at most kSplitMaxBlocks blocks and a
@@ -2140,15 +2152,20 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
         const int nc = small_nc(batch, n_rq);
         const dim3 grid((unsigned)((n_rq + 31) / 32), (unsigned)((batch + 16 * nc - 1) / (16 * nc)), (unsigned)ks);
         const auto *w = static_cast<const uint8_t *>(w_packed);
-        if (use_wide_kernel(ks, n_rq, cols, epilogue, soff0 + n_rq * nblk * 8)) {
+        if (!bias && use_wide_kernel(ks, n_rq, cols, epilogue, soff0 + n_rq * nblk * 8)) {
             const int nbt = (int)((batch + 15) / 16);
             const int n_groups = 256 / nbt / 8 * 8;
             const int wb = (int)(soff0 + n_rq * nblk * 8);
-#define VGX_WD(DT, NORM)                                                                                          \
-    hipLaunchKernelGGL((qgemm_wide_kernel<DT, NORM>), dim3((unsigned)(n_groups * nbt)), dim3(64 * kWideWaves), 0, st0, \
-                       w, soff0, n_rq, nblk, wb, x, ldx, norm_w, eps, batch, bias, y, ldy, rows, n_groups)
-            if (dtype == VGX_Q8_0) { if (norm_w) VGX_WD(VGX_Q8_0, true); else VGX_WD(VGX_Q8_0, false); }
-            else { if (norm_w) VGX_WD(VGX_Q4_0, true); else VGX_WD(VGX_Q4_0, false); }
+#define VGX_WD(DT, NORM, NCH)                                                                                     \
+    hipLaunchKernelGGL((qgemm_wide_kernel<DT, NORM, NCH>), dim3((unsigned)(n_groups * nbt)), dim3(64 * kWideWaves), 0, st0, \
+                       w, soff0, n_rq, nblk, wb, x, ldx, norm_w, eps, batch, y, ldy, rows, n_groups)
+#define VGX_WDN(NCH)                                                                                            \
+    do {                                                                                                        \
+        if (dtype == VGX_Q8_0) { if (norm_w) VGX_WD(VGX_Q8_0, true, NCH); else VGX_WD(VGX_Q8_0, false, NCH); }     \
+        else { if (norm_w) VGX_WD(VGX_Q4_0, true, NCH); else VGX_WD(VGX_Q4_0, false, NCH); }                      \
+    } while (0)
+            if (nblk == 48) VGX_WDN(12); else VGX_WDN(6);
+#undef VGX_WDN
 #undef VGX_WD
             VGX_CHECK_LAUNCH();
             return VGX_OK;
