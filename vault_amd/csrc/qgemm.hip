@@ -17,11 +17,15 @@
 // does not have: spills).  With S_b the per-block sum of the pieces, per block the fp32 MFMA result C
 // (= sum_j w_j u_j as pieces) is corrected and scaled:
 //   acc += d * (C - off * S_b),   off = 128 (Q8_0), 8 (Q4_0; 24 in the tiled kernel),
-// which is the reference's sum_b d_b sum_j q_j x_j at fp32-level accuracy.
+// which is the reference's sum_b d_b sum_j q_j x_j at fp32-level accuracy.  The decode-batch kernels
+// place the weights by byte permutes instead (Q4_0 bf16 128 + n / fp16 1024 + n against pieces of 16 u;
+// fp16 1024 + unsigned weight in qgemm_wide_kernel, whose pieces are both fp16 of a power-of-two-scaled
+// row) with the matching offsets; their comments give the arithmetic.
 //
 // Mapping.  Large batches (prefill chunks) run qgemm_tile_kernel (128 x 128 LDS tiles, below) after
-// the split pre-pass; decode batches of up to 64 rows run qgemm_small_kernel, which converts its
-// activations itself.  In every MFMA a lane of a 16-row tile owns one weight row (l % 16) for the A
+// the split pre-pass; decode batches of up to 64 rows run the K-split kernels (qgemm_kslice_kernel,
+// qgemm_split_kernel, qkv_split_kernel), qgemm_wide_kernel for tall unsplit weights, or
+// qgemm_small_kernel, which converts its activations itself.  In every MFMA a lane of a 16-row tile owns one weight row (l % 16) for the A
 // operand and one activation row (l % 16) for the B operand, both with the K slots 8 (l / 16) .. + 7
 // of the block (weights 8 lg .. 8 lg + 7); the accumulator lane holds weight rows 4 (l / 16) .. + 3
 // (one packed row-quad, whose four fp16 scales are one 8-byte word) of activation row l % 16.
