@@ -92,6 +92,28 @@ def test_gemv_lm_head_shape(dev, dt, batch):
 
 
 @pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
+@pytest.mark.parametrize("rows", [151665, 65540])
+def test_gemv_tall_fused_rmsnorm(dev, dt, rows):
+    """The LM head's own call: final RMSNorm fused into the one-row GEMV over tall 1536-column weights
+    (the persistent streaming kernel; 65540 rows: a row count whose row-quads do not divide evenly
+    among the waves), against oracle rmsnorm -> fp64 GEMV."""
+    cols = 1536
+    rng = np.random.default_rng(rows + 17)
+    x = (rng.standard_normal((1, cols)) * 3.0).astype(np.float32)
+    g = rng.uniform(0.8, 1.2, cols).astype(np.float32)
+    u = linalg.rmsnorm(x, g, 1e-6)
+    raw = _blocks(dt, rows, cols, seed=rows % 97)
+    wq = ops.QWeight.from_blocks(dt, rows, cols, raw, dev)
+    wf = codec.decode(dt, raw, rows, cols)
+    ref = linalg.gemv(wf, u)
+    y = ops.qlinear(wq, torch.from_numpy(x).to(dev), norm=(torch.from_numpy(g).to(dev), 1e-6))
+    y = y.cpu().numpy().astype(np.float64)
+    tol = 2 * linalg.gemv_bound(wf, u, dt) + np.abs(ref) * 2e-7
+    err = np.abs(y - ref)
+    assert np.all(err <= tol), float((err / tol).max())
+
+
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
 def test_gemv_bias_and_residual(dev, dt):
     _check_gemv(dev, dt, 1536, 1536, 1, seed=21, kind="quantized", bias=True)
     _check_gemv(dev, dt, 1536, 1536, 3, seed=22, kind="quantized", accumulate=True)

@@ -12,8 +12,9 @@
 // the block are read from LDS once and used for the four rows.
 //
 // One activation row (the decode step) runs gemv1_kernel, whose mapping is picked from the shape
-// (below); 2-4 rows per pass run qgemv_kernel in row mode (16 lanes per row-quad, four row-quads per
-// wave, 4 waves per workgroup) for >= 2048 row-quads, else in split-K mode (a wave per row-quad).
+// (below), or for tall 1536-column weights (the LM head) the persistent gemv1_stream_kernel; 2-4
+// rows per pass run qgemv_kernel in row mode (16 lanes per row-quad, four row-quads per wave, 4 waves
+// per workgroup) for >= 2048 row-quads, else in split-K mode (a wave per row-quad).
 // Each lane requests the weights of up to U blocks at once to keep enough bytes in flight for HBM.
 //
 // Arithmetic is fp32 throughout, as in the reference: per block s = sum_j q_j x_j, acc += d * s.
@@ -380,7 +381,8 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
 //   barrier after staging does not wait for the weights and each wave multiplies as soon as its
 //   own weights arrive.
 // Measured on MI355X (gate/up 2 x 8960 x 1536 Q4_0): LPR 64 / 4 waves / SF 7.6 us against 9.4 us for
-// the DPP-row mapping; the 151665-row LM head keeps the DPP-row mapping (48 vs 53 us).
+// the DPP-row mapping; other tall weights keep the DPP-row mapping (the 151665-row LM head: 48 vs
+// 53 us, before gemv1_stream_kernel took that shape: 44.7 us Q8_0, 26.2 us Q4_0).
 template <int DT, int EPI, bool NORM, int LPR, int WPG, int KW, int U, bool SF, bool XD>
 __global__ __launch_bounds__(64 * WPG * KW) void gemv1_kernel(GemvArgs a) {
     static_assert(!XD || WPG == 1, "direct activations: one row-quad set per workgroup");
@@ -541,6 +543,203 @@ __global__ __launch_bounds__(64 * WPG * KW) void gemv1_kernel(GemvArgs a) {
     }
 }
 
+// One-row GEMV over tall Q8_0 / Q4_0 weights of 48 blocks per row (1536 columns: the LM head).
+// Persistent: every wave walks row-quads gw, gw + n_waves, ... and keeps RB of them in flight.
+//   Loads: one 16-byte buffer load per lane covers 1 KB of a row-quad's contiguous run (the whole
+//   instruction reads one 1 KB range, not 64 pieces of separate blocks), NL = 6 (Q8_0) / 3 (Q4_0)
+//   loads per row-quad, plus one 2-byte scale load per 16-byte piece.  Q8_0: lane l holds half h =
+//   l & 1 of row r = (l >> 1) & 3 of block 8 j + (l >> 3); Q4_0: row r = l & 3 of block 16 j + (l >> 2).
+//   A lane therefore always meets the same 96 activations; they stay in registers after one pass
+//   through LDS (RMSNorm weight applied, sum x^2 while staging).
+//   Arithmetic per 16-byte piece, fp32: Q8_0 s = sum q x, Q4_0 s = sum n x - 8 sum x; acc += d * s;
+//   the 16 lanes of a row are summed by DPP / lane swaps, the RMSNorm scale applied last (the
+//   product is linear in x).
+//   Every load and store is unconditional: the quants and the scales are two buffers whose bounds
+//   end with the last row-quad, so fetches of row-quads past the end read zero without touching
+//   memory, and their stores land past y's bound; the loop has no branch around memory operations
+//   and the compiler waits for exactly the loads of the row-quad it uses.
+//   Epilogues: store, or SwiGLU over gate/up row-quads (rows 0, 1 gate, rows 2, 3 up of the same two
+//   output rows), the up value taken from the lanes of row r + 2.
+constexpr int kStreamBlocks = 48;
+constexpr int kStreamMinRq = 2048;
+constexpr uint32_t kStreamPastEnd = 0x80000000u;
+
+template <int DT>
+struct StreamGeom {
+    static constexpr int QB = gemv_quant_bytes(DT);
+    static constexpr int RQB = kStreamBlocks * 4 * QB;   // bytes of one row-quad's quants
+    static constexpr int NL = RQB / 1024;                // 16-byte loads per lane per row-quad
+    static constexpr int XL = 96 / NL;                   // activations per lane per load
+    static constexpr int RB = DT == VGX_Q8_0 ? 3 : 4;    // row-quads in flight per wave
+    static constexpr int GROUPS = 512;                    // 2 waves per SIMD (200-212 VGPRs)
+};
+
+template <int DT>
+VGX_DEV int stream_block(int lane, int j) { return DT == VGX_Q8_0 ? 8 * j + (lane >> 3) : 16 * j + (lane >> 2); }
+
+template <int DT, int EPI, bool NORM>
+__global__ __launch_bounds__(256) void gemv1_stream_kernel(GemvArgs a) {
+    using G = StreamGeom<DT>;
+    constexpr int NL = G::NL, XL = G::XL, RB = G::RB;
+    const int lane = threadIdx.x & 63;
+    const int gw = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+    const int nw = (int)gridDim.x * 4;
+    const int n_rq = (int)a.n_rq;
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *)a.w, 0, n_rq * G::RQB, 0x00020000);
+    const __amdgpu_buffer_rsrc_t srs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(a.w + a.soff), 0, n_rq * (kStreamBlocks * 8), 0x00020000);
+    // per-lane parts of the offsets: piece j of a row-quad, its scale
+    uint32_t qoff[NL], sofs[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        qoff[j] = (uint32_t)(j * 1024 + lane * 16);
+        sofs[j] = DT == VGX_Q8_0 ? (uint32_t)(64 * j + 2 * (lane >> 1)) : (uint32_t)(128 * j + 2 * lane);
+    }
+    uint4 wq[RB][NL];
+    uint32_t wsc[RB][NL];
+    // Row-quads past the end are fetched too, without a branch: their offsets stay below 2^32 (the
+    // quants are under 2 GiB and a wave runs at most 2 RB row-quads past the end) and read zero.
+    auto fetch = [&](int s, int rq) {
+        const uint32_t qb = (uint32_t)rq * G::RQB;
+        const uint32_t sb = (uint32_t)rq * (kStreamBlocks * 8);
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, qb + qoff[j], 0, 0);
+            wq[s][j] = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+#pragma unroll
+        for (int j = 0; j < NL; ++j) wsc[s][j] = __builtin_amdgcn_raw_buffer_load_b16(srs, sb + sofs[j], 0, 0);
+    };
+    // lnw * x staged once per workgroup (the activation loads go first, so waiting for them does not
+    // wait for the weights), then the weight ring, then this lane's 96 activations from LDS.
+    __shared__ float xs[kStreamBlocks * QK];
+    __shared__ float red[4];
+    constexpr int N4 = kStreamBlocks * QK / 4;   // 384 float4
+    const int tid = threadIdx.x;
+    float4 xa[2], ga[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + 256 * u;
+        if (i < N4) {
+            xa[u] = reinterpret_cast<const float4 *>(a.x)[i];
+            if constexpr (NORM) ga[u] = reinterpret_cast<const float4 *>(a.lnw)[i];
+        }
+    }
+    // the ring's first fill in the loop's own issue order (slot by slot), so one wait count per use
+    // holds for the first round and the steady state alike
+#pragma unroll
+    for (int s = 0; s < RB; ++s) {
+        fetch(s, gw + s * nw);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    float ssq = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + 256 * u;
+        if (i < N4) {
+            float4 t = xa[u];
+            if constexpr (NORM) {
+                ssq += fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, t.w * t.w)));
+                t.x *= ga[u].x; t.y *= ga[u].y; t.z *= ga[u].z; t.w *= ga[u].w;
+            }
+            reinterpret_cast<float4 *>(xs)[i] = t;
+        }
+    }
+    if constexpr (NORM) {
+        const float w = wave_sum(ssq);
+        if (lane == 0) red[tid >> 6] = w;
+    }
+    __syncthreads();
+    float xv[NL][XL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int c0 = stream_block<DT>(lane, j) * QK + (DT == VGX_Q8_0 ? (lane & 1) * 16 : 0);
+#pragma unroll
+        for (int t4 = 0; t4 < XL / 4; ++t4) {
+            const float4 t = reinterpret_cast<const float4 *>(xs + c0)[t4];
+            xv[j][4 * t4] = t.x; xv[j][4 * t4 + 1] = t.y; xv[j][4 * t4 + 2] = t.z; xv[j][4 * t4 + 3] = t.w;
+        }
+    }
+    float off[NL];   // Q4_0: the -8 offset term of each piece, 8 sum x
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        float s = 0.0f;
+        if constexpr (DT == VGX_Q4_0) {
+#pragma unroll
+            for (int t = 0; t < XL; ++t) s += xv[j][t];
+        }
+        off[j] = 8.0f * s;
+    }
+    float inv = 1.0f;
+    if constexpr (NORM) inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)(kStreamBlocks * QK) + a.eps);
+    const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc((void *)a.y, 0, (int)(a.rows_out * 4), 0x00020000);
+    const int r_out = DT == VGX_Q8_0 ? lane >> 1 : lane;                  // the storing lanes' row
+    // one lane per row of the row-quad (SwiGLU: per gate row)
+    const bool stores = (DT == VGX_Q8_0 ? (lane & 0x39) == 0 : lane < 4) && (EPI != EPI_SWIGLU || r_out < 2);
+    constexpr int kOutPerRq = EPI == EPI_SWIGLU ? 2 : 4;
+
+    // row-quad i of this wave: gw + i * nw, i < cnt; ring slot s holds i = s (mod RB)
+    const int cnt = gw < n_rq ? (n_rq - gw + nw - 1) / nw : 0;
+    auto dot = [&](int s) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const uint32_t q[4] = {wq[s][j].x, wq[s][j].y, wq[s][j].z, wq[s][j].w};
+            float p = 0.0f;
+            if constexpr (DT == VGX_Q8_0) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) p = fmaf(gemv_cvt_s8(q[k], t), xv[j][4 * k + t], p);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t lo = gemv_nibble_mask(q[k]);
+                    const uint32_t hi = gemv_nibble_mask(q[k] >> 4);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        p = fmaf(gemv_cvt_u8(lo, t), xv[j][4 * k + t], p);
+                        p = fmaf(gemv_cvt_u8(hi, t), xv[j][16 + 4 * k + t], p);
+                    }
+                }
+            }
+            if constexpr (DT == VGX_Q4_0) p -= off[j];
+            acc = fmaf(half_bits_to_float(wsc[s][j]), p, acc);
+        }
+        if constexpr (DT == VGX_Q8_0) {
+            acc += dpp_f<DPP_QUAD_1032>(acc);     // lane ^ 1: the other half of the row
+            acc += dpp_f<0x128>(acc);             // row_ror 8: lane ^ 8
+        } else {
+            acc += dpp_f<0x124>(acc);             // row_ror 4 and 8: the lanes of the same l & 3
+            acc += dpp_f<0x128>(acc);
+        }
+        acc = xor32_sum(xor16_sum(acc)) * inv;
+        if constexpr (EPI == EPI_SWIGLU) {
+            const float u = __shfl_xor(acc, DT == VGX_Q8_0 ? 4 : 2, kWave);   // row r + 2: the up row
+            acc = acc / (1.0f + __expf(-acc)) * u;
+        }
+        return acc;
+    };
+    auto store = [&](int i, float v) {
+        const uint32_t yo = stores ? (uint32_t)((gw + i * nw) * kOutPerRq + r_out) * 4 : kStreamPastEnd;   // rows >= rows_out: dropped
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), yrs, yo, 0, 0);
+    };
+    // Whole ring rounds without a branch (the refills of the last round fetch the remainder and
+    // row-quads past the end), then the remainder.
+    const int full = cnt / RB * RB;
+    for (int i = 0; i < full; i += RB) {
+#pragma unroll
+        for (int s = 0; s < RB; ++s) {
+            const float v = dot(s);
+            fetch(s, gw + (i + s + RB) * nw);
+            store(i + s, v);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < RB - 1; ++s)
+        if (full + s < cnt) store(full + s, dot(s));
+}
+
 constexpr int kGemv1MaxBlocks = 448;   // LDS staging of one row: 448 * 36 * 4 B = 63 KB
 
 template <int DT, int EPI, bool NORM>
@@ -551,7 +750,14 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
                        dim3((unsigned)((a.n_rq + WPG * (64 / LPR) - 1) / (WPG * (64 / LPR)))),              \
                        dim3(64 * WPG * KW), XD ? 0 : lds, st, a)
     const bool aligned = ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.lnw & 15) == 0;
-    if (a.n_rq >= 16384) VGX_GEMV1(16, 4, 1, 3, false, false);        // LM head: DPP row per row-quad
+    if constexpr ((EPI == EPI_STORE || EPI == EPI_SWIGLU) && DT != VGX_F32) {
+        if (a.nblk == kStreamBlocks && !a.bias && a.n_rq >= kStreamMinRq && a.soff < ((int64_t)1 << 31) && aligned) {
+            const unsigned grid = (unsigned)std::min<int64_t>(StreamGeom<DT>::GROUPS, (a.n_rq + 3) / 4);
+            hipLaunchKernelGGL((gemv1_stream_kernel<DT, EPI, NORM>), dim3(grid), dim3(256), 0, st, a);
+            return;
+        }
+    }
+    if (a.n_rq >= 16384) VGX_GEMV1(16, 4, 1, 3, false, false);        // other tall weights: DPP row per row-quad
     else if (a.n_rq >= 2048) VGX_GEMV1(64, 4, 1, 1, true, false);     // gate/up: lane per block
     else if (a.nblk >= 192) VGX_GEMV1(64, 2, 8, 1, true, false);      // down: 2 row-quads x 8 waves over K
                                                                       // (6.6 us; one row-quad 6.9 us, direct
