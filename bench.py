@@ -206,8 +206,8 @@ def gateup_kernel(model, rounds: int = 20):
     n = rounds * len(layers)
     wb = layers[0].wgu.stream_bytes
     algo = wb + 4 * cfg.d_model + 4 * cfg.d_ff
-    return {"kernel": "gemv1_kernel<Q4_0, SwiGLU epilogue, RMSNorm prologue, lane per block, 4 waves, staging first> "
-                      "(gate|up 2x8960x1536)",
+    return {"kernel": "gemv1_stream_kernel<Q4_0, SwiGLU epilogue, RMSNorm prologue> (persistent, 1 KB per load "
+                      "instruction; gate|up 2x8960x1536)",
             "launches": n, "avg_us": us, "bytes_per_launch": algo, "gbs": algo / us / 1e3}
 
 
