@@ -211,13 +211,13 @@ def gateup_kernel(model, rounds: int = 20):
             "launches": n, "avg_us": us, "bytes_per_launch": algo, "gbs": algo / us / 1e3}
 
 
-def gemv_figures(dev, batches=(1, 16), reps: int = 20):
+def gemv_figures(dev, batches=(1, 16), reps: int = 20, shapes=None):
     """Q8_0 / Q4_0 GEMV at the model's projection shapes, weights rotated over copies that exceed the
     last-level cache; GB/s of algorithmic bytes (weights + x + y)."""
     import numpy as np
     import torch
     from vault_amd import ops, vlt3
-    shapes = [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (151665, 1536)]
+    shapes = shapes or [(1536, 1536), (256, 1536), (8960, 1536), (1536, 8960), (151665, 1536)]
     rng = np.random.default_rng(7)
     out = []
     for dt, name in ((vlt3.Q8_0, "q8_0"), (vlt3.Q4_0, "q4_0")):
@@ -494,7 +494,7 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for per-kernel profiles of the step)")
     ap.add_argument("--figures", choices=("gemv", "attn_decode", "attn_decode_b1", "attn_prefill", "gemm_prefill",
-                                          "roofline", "gateup", "decode_batch32"),
+                                          "roofline", "gateup", "decode_batch32", "lm_head"),
                     help="only one set of kernel figures, printed as JSON (for per-kernel profiles)")
     ap.add_argument("--pmc", action="store_true",
                     help="only run the launches the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count")
@@ -533,6 +533,10 @@ def main() -> int:
         model, tensors = build_model(cfg, dev, torch.float32)
         del tensors
         print(json.dumps({"decode_batch32": batched_decode(model)}), flush=True)
+        return 0
+    if args.figures == "lm_head":
+        # the 151665 x 1536 rows of the gemv figures at batch 1 (for the streaming kernel's profiles)
+        print(json.dumps({"lm_head": gemv_figures(dev, batches=(1,), shapes=[(151665, 1536)])}), flush=True)
         return 0
     if args.figures:
         fig = {"gemv": gemv_figures, "attn_decode": attn_figures, "attn_decode_b1": attn_b1_figures,
