@@ -12,8 +12,9 @@
 // the block are read from LDS once and used for the four rows.
 //
 // One activation row (the decode step) runs gemv1_kernel, whose mapping is picked from the shape
-// (below), or for tall 1536-column weights (the LM head) the persistent gemv1_stream_kernel; 2-4
-// rows per pass run qgemv_kernel in row mode (16 lanes per row-quad, four row-quads per wave, 4 waves
+// (below), for 1536-column weights of >= 8192 rows (gate/up, the LM head) the persistent
+// gemv1_stream_kernel, for long Q4_0 rows (the down projection) gemv1_pieces_kernel; 2-4 rows per
+// pass run qgemv_kernel in row mode (16 lanes per row-quad, four row-quads per wave, 4 waves
 // per workgroup) for >= 2048 row-quads, else in split-K mode (a wave per row-quad).
 // Each lane requests the weights of up to U blocks at once to keep enough bytes in flight for HBM.
 //
@@ -740,6 +741,130 @@ __global__ __launch_bounds__(256) void gemv1_stream_kernel(GemvArgs a) {
         if (full + s < cnt) store(full + s, dot(s));
 }
 
+// One-row Q4_0 GEMV over long rows (192-320 blocks: the down projection, 1536 x 8960): a workgroup of
+// NW waves takes RQG row-quads; their runs are cut into 1 KB pieces (16 blocks x 4 rows, the last
+// piece of a row-quad partial), and each wave takes every NW-th of the RQG x pieces, one 16-byte
+// buffer load per lane and piece (row l & 3 of block 16 p + l / 4), all requested before the
+// activations are needed.  The activations are staged once per workgroup in LDS, blocks padded to 36
+// floats (the 16 blocks a piece reads at once would otherwise share one bank), with their per-block
+// sums (the -8 offset term); the lanes of a row and then the waves are summed in a fixed order
+// (deterministic).
+constexpr int kPiecesMaxBlocks = 320;
+
+template <int EPI, int NW, int RQG>
+__global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
+    constexpr int MAXI = (RQG * (kPiecesMaxBlocks / 16) + NW - 1) / NW;   // pieces per wave
+    extern __shared__ float4 xs4[];                   // [nblk][36] activations, then [nblk] block sums
+    float *xs = reinterpret_cast<float *>(xs4);
+    __shared__ float red[NW][RQG][4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nblk = a.nblk, cols = nblk * QK;
+    const int npc = (nblk + 15) / 16;                 // pieces per row-quad
+    const int64_t rq0 = (int64_t)blockIdx.x * RQG;
+    const int n_rq = (int)a.n_rq;
+    float *xsum = xs + nblk * kGemvPad;
+
+    // activations first (their wait then covers no weights), 8 float4 = one block per 8 threads
+    const int n4 = cols / 4;
+    constexpr int NT = 64 * NW;
+    constexpr int XR = (kPiecesMaxBlocks * 8 + NT - 1) / NT;
+    float4 xv4[XR];
+#pragma unroll
+    for (int u = 0; u < XR; ++u) {
+        const int i = tid + NT * u;
+        xv4[u] = i < n4 ? reinterpret_cast<const float4 *>(a.x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    // weights: piece item i = wave + NW k of the workgroup's RQG x npc; past the end: offsets past the
+    // buffers (no traffic, zero quants and scales)
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *)a.w, 0, (int)a.soff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t srs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(a.w + a.soff), 0, (int)(a.n_rq * nblk * 8), 0x00020000);
+    uint4 wq[MAXI];
+    uint32_t wsc[MAXI];
+    int blk_of[MAXI];
+#pragma unroll
+    for (int k = 0; k < MAXI; ++k) {
+        const int it = wave + NW * k;
+        const int rql = it / npc, pc = it - rql * npc;
+        const int64_t rq = rq0 + rql;
+        const int blk = 16 * pc + (lane >> 2);
+        const bool ok = it < RQG * npc && rq < n_rq && blk < nblk;
+        blk_of[k] = min(blk, nblk - 1);
+        const uint32_t qo = ok ? (uint32_t)((rq * nblk + blk) * 64 + (lane & 3) * 16) : kStreamPastEnd;
+        const uint32_t so = ok ? (uint32_t)((rq * nblk + blk) * 8 + (lane & 3) * 2) : kStreamPastEnd;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, qo, 0, 0);
+        wq[k] = make_uint4(v[0], v[1], v[2], v[3]);
+        wsc[k] = __builtin_amdgcn_raw_buffer_load_b16(srs, so, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < XR; ++u) {
+        const int i = tid + NT * u;
+        const float4 t = xv4[u];
+        if (i < n4) xs4[(i >> 3) * (kGemvPad / 4) + (i & 7)] = t;   // padded rows: no bank conflicts
+        float s = (t.x + t.y) + (t.z + t.w);        // the block's 8 float4 are 8 consecutive threads
+        s += __shfl_xor(s, 1, kWave);
+        s += __shfl_xor(s, 2, kWave);
+        s += __shfl_xor(s, 4, kWave);
+        if (i < n4 && (i & 7) == 0) xsum[i >> 3] = 8.0f * s;
+    }
+    __syncthreads();
+
+    float acc[RQG];
+#pragma unroll
+    for (int r = 0; r < RQG; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAXI; ++k) {
+        const int it = wave + NW * k;
+        if (it >= RQG * npc) break;                   // uniform: the wave's item count
+        const float4 *xb = xs4 + blk_of[k] * (kGemvPad / 4);
+        float xv[QK];
+#pragma unroll
+        for (int j4 = 0; j4 < 8; ++j4) {
+            const float4 t = xb[j4];
+            xv[4 * j4] = t.x; xv[4 * j4 + 1] = t.y; xv[4 * j4 + 2] = t.z; xv[4 * j4 + 3] = t.w;
+        }
+        const uint32_t q[4] = {wq[k].x, wq[k].y, wq[k].z, wq[k].w};
+        float p = 0.0f;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const uint32_t lo = gemv_nibble_mask(q[kk]);
+            const uint32_t hi = gemv_nibble_mask(q[kk] >> 4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                p = fmaf(gemv_cvt_u8(lo, t), xv[4 * kk + t], p);
+                p = fmaf(gemv_cvt_u8(hi, t), xv[16 + 4 * kk + t], p);
+            }
+        }
+        const float v = half_bits_to_float(wsc[k]) * (p - xsum[blk_of[k]]);
+        const int rql = it / npc;
+#pragma unroll
+        for (int r = 0; r < RQG; ++r)
+            if (r == rql) acc[r] += v;
+    }
+#pragma unroll
+    for (int r = 0; r < RQG; ++r) {
+        float v = acc[r];
+        v += dpp_f<0x124>(v);                         // row_ror 4 and 8: the lanes of the same l & 3
+        v += dpp_f<0x128>(v);
+        v = xor32_sum(xor16_sum(v));
+        if (lane < 4) red[wave][r][lane] = v;
+    }
+    __syncthreads();
+    if (tid < 4 * RQG) {
+        const int rql = tid >> 2, r = tid & 3;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[w][rql][r];
+        const int64_t row = (rq0 + rql) * 4 + r;
+        if (row < a.rows_out) {
+            if (a.bias) v += a.bias[row];
+            if constexpr (EPI == EPI_ACCUM) v += a.y[row];
+            a.y[row] = v;
+        }
+    }
+}
+
 constexpr int kGemv1MaxBlocks = 448;   // LDS staging of one row: 448 * 36 * 4 B = 63 KB
 
 template <int DT, int EPI, bool NORM>
@@ -757,9 +882,20 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
             return;
         }
     }
+    if constexpr (DT == VGX_Q4_0 && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
+        if (a.nblk >= 192 && a.nblk <= kPiecesMaxBlocks && a.soff < ((int64_t)1 << 31) && aligned) {
+            // 16 waves x 2 row-quads: 5.5 us for 1536 x 8960 (8 x 2: 5.8, 8 x 1: 6.0, 16 x 1: 5.9, 16 x 4: 7.3,
+            // 4 x 1: 6.8; the lane-per-block kernel: 6.6)
+            constexpr int NW = 16, RQG = 2;
+            hipLaunchKernelGGL((gemv1_pieces_kernel<EPI, NW, RQG>), dim3((unsigned)((a.n_rq + RQG - 1) / RQG)), dim3(64 * NW),
+                               (size_t)(a.nblk * kGemvPad + a.nblk) * sizeof(float), st, a);
+            return;
+        }
+    }
     if (a.n_rq >= 16384) VGX_GEMV1(16, 4, 1, 3, false, false);        // other tall weights: DPP row per row-quad
-    else if (a.n_rq >= 2048) VGX_GEMV1(64, 4, 1, 1, true, false);     // gate/up: lane per block
-    else if (a.nblk >= 192) VGX_GEMV1(64, 2, 8, 1, true, false);      // down: 2 row-quads x 8 waves over K
+    else if (a.n_rq >= 2048) VGX_GEMV1(64, 4, 1, 1, true, false);     // lane per block (gate/up before the streaming kernel)
+    else if (a.nblk >= 192) VGX_GEMV1(64, 2, 8, 1, true, false);      // long rows (Q8_0, fused norm, or beyond the
+                                                                      // pieces kernel): 2 row-quads x 8 waves over K
                                                                       // (6.6 us; one row-quad 6.9 us, direct
                                                                       // activations 7.0 us)
     else if (a.nblk >= 96 && a.n_rq < 256) VGX_GEMV1(64, 1, 8, 1, true, false);   // few rows: more waves
