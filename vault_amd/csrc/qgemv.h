@@ -13,7 +13,7 @@
 //
 // One activation row (the decode step) runs gemv1_kernel, whose mapping is picked from the shape
 // (below), for 1536-column weights of >= 8192 rows (gate/up, the LM head) the persistent
-// gemv1_stream_kernel, for long Q4_0 rows (the down projection) gemv1_pieces_kernel; 2-4 rows per
+// gemv1_stream_kernel, for other Q4_0 rows (the down and o projections) gemv1_pieces_kernel; 2-4 rows per
 // pass run qgemv_kernel in row mode (16 lanes per row-quad, four row-quads per wave, 4 waves
 // per workgroup) for >= 2048 row-quads, else in split-K mode (a wave per row-quad).
 // Each lane requests the weights of up to U blocks at once to keep enough bytes in flight for HBM.
@@ -741,8 +741,9 @@ __global__ __launch_bounds__(256) void gemv1_stream_kernel(GemvArgs a) {
         if (full + s < cnt) store(full + s, dot(s));
 }
 
-// One-row Q4_0 GEMV over long rows (192-320 blocks: the down projection, 1536 x 8960): a workgroup of
-// NW waves takes RQG row-quads; their runs are cut into 1 KB pieces (16 blocks x 4 rows, the last
+// One-row Q4_0 GEMV over rows of up to MAXB blocks (the down projection, 1536 x 8960: 16 waves x 2
+// row-quads; the o-projection, 1536 x 1536: 4 waves x 1 row-quad): a workgroup of NW waves takes RQG
+// row-quads; their runs are cut into 1 KB pieces (16 blocks x 4 rows, the last
 // piece of a row-quad partial), and each wave takes every NW-th of the RQG x pieces, one 16-byte
 // buffer load per lane and piece (row l & 3 of block 16 p + l / 4), all requested before the
 // activations are needed.  The activations are staged once per workgroup in LDS, blocks padded to 36
@@ -751,9 +752,9 @@ __global__ __launch_bounds__(256) void gemv1_stream_kernel(GemvArgs a) {
 // (deterministic).
 constexpr int kPiecesMaxBlocks = 320;
 
-template <int EPI, int NW, int RQG>
+template <int EPI, int NW, int RQG, int MAXB>
 __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
-    constexpr int MAXI = (RQG * (kPiecesMaxBlocks / 16) + NW - 1) / NW;   // pieces per wave
+    constexpr int MAXI = (RQG * ((MAXB + 15) / 16) + NW - 1) / NW;   // pieces per wave (rows of <= MAXB blocks)
     extern __shared__ float4 xs4[];                   // [nblk][36] activations, then [nblk] block sums
     float *xs = reinterpret_cast<float *>(xs4);
     __shared__ float red[NW][RQG][4];
@@ -768,7 +769,7 @@ __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
     // activations first (their wait then covers no weights), 8 float4 = one block per 8 threads
     const int n4 = cols / 4;
     constexpr int NT = 64 * NW;
-    constexpr int XR = (kPiecesMaxBlocks * 8 + NT - 1) / NT;
+    constexpr int XR = (MAXB * 8 + NT - 1) / NT;
     float4 xv4[XR];
 #pragma unroll
     for (int u = 0; u < XR; ++u) {
@@ -887,7 +888,17 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
             // 16 waves x 2 row-quads: 5.5 us for 1536 x 8960 (8 x 2: 5.8, 8 x 1: 6.0, 16 x 1: 5.9, 16 x 4: 7.3,
             // 4 x 1: 6.8; the lane-per-block kernel: 6.6)
             constexpr int NW = 16, RQG = 2;
-            hipLaunchKernelGGL((gemv1_pieces_kernel<EPI, NW, RQG>), dim3((unsigned)((a.n_rq + RQG - 1) / RQG)), dim3(64 * NW),
+            hipLaunchKernelGGL((gemv1_pieces_kernel<EPI, NW, RQG, kPiecesMaxBlocks>), dim3((unsigned)((a.n_rq + RQG - 1) / RQG)), dim3(64 * NW),
+                               (size_t)(a.nblk * kGemvPad + a.nblk) * sizeof(float), st, a);
+            return;
+        }
+    }
+    if constexpr (DT == VGX_Q4_0 && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
+        if (a.nblk == kStreamBlocks && a.n_rq < kStreamMinRq && a.soff < ((int64_t)1 << 31) && aligned) {
+            // 1536-column rows (the o-projection, 1536 x 1536): a workgroup of 4 waves per row-quad, one 1 KB
+            // piece per wave (3 of them busy): 3.2 us against 4.2 us for the lane-per-block kernel (2 x 2: 3.7,
+            // 4 x 2: 3.6, 3 x 1: 3.2, 6 x 2: 3.4, 8 x 4: 3.6)
+            hipLaunchKernelGGL((gemv1_pieces_kernel<EPI, 4, 1, kStreamBlocks>), dim3((unsigned)a.n_rq), dim3(256),
                                (size_t)(a.nblk * kGemvPad + a.nblk) * sizeof(float), st, a);
             return;
         }
