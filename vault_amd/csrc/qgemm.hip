@@ -1523,7 +1523,6 @@ void reduce_launch(const float *part, int ks, int64_t batch, int64_t rows_p, int
 //    8 k + r for the same r), so the second activation tile reads the group's weights from that XCD's L2.
 constexpr int kWideWaves = 12;                         // waves 0..7 also stage the activations
 constexpr int kWideMaxCols = 1536;                      // staged K of 16 rows: 64 KiB per 1024 columns
-constexpr int kWideRow = 80;                            // LDS bytes per weight row of a chunk (Q8_0: 4 x 16 + 16 pad)
 
 template <int DT>
 struct WideGeom {

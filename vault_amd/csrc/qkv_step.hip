@@ -11,9 +11,10 @@
 // two tensors that may have different block dtypes (hybrid Q4_0 q with Q8_0 k|v); workgroups
 // [0, H D / 4) take q row-quads, the rest k|v, each with the code of its dtype.
 //
-// Mapping: one wave per row-quad, lane i takes blocks i, i + 64, ... of the row-quad (all 48 blocks
-// of d_model = 1536 in one pass), loading its activation block and RMSNorm weights directly (the
-// same 12 KB for every wave: L1 / L2 hits); sum x^2 of the wave's blocks is the full sum.  The
+// Mapping (rows of up to 64 Q8_0 / Q4_0 blocks: qkv_rope_step_pieces_kernel, below; otherwise
+// qkv_rope_step_kernel): one wave per row-quad, lane i takes blocks i, i + 64, ... of the row-quad,
+// loading its activation block and RMSNorm weights directly (the same 12 KB for every wave: L1 / L2
+// hits); sum x^2 of the wave's blocks is the full sum.  The
 // position-dependent values (ring slot, RoPE table row, sink slot) come from the device step
 // descriptor, so a captured graph replays at every position of a chunk.
 #include "qgemv.h"
@@ -88,24 +89,13 @@ __device__ __forceinline__ void rq_dot(const uint8_t *__restrict__ W, int64_t so
     }
 }
 
-template <int DTQ, int DTKV, int KV>
-__global__ __launch_bounds__(64) void qkv_rope_step_kernel(QkvStepArgs a) {
-    const int D = a.D, h2 = D / 2, qpd = D / 4;          // row-quads per head
+// Bias, RoPE and the ring / sink writes of row-quad wg (q row-quads first, then k, then v) from the
+// four finished dot products acc[0..3] (rows 4 wg .. + 3, RMSNorm scale applied), held by every lane
+// of the calling wave.
+template <int KV>
+__device__ __forceinline__ void qkv_epilogue(const QkvStepArgs &a, int64_t wg, int lane, const float (&acc)[4][1]) {
+    const int D = a.D, h2 = D / 2, qpd = D / 4;
     const int64_t nq = (int64_t)a.H * qpd, nk = (int64_t)a.G * qpd;
-    const int64_t wg = blockIdx.x;
-    const int lane = threadIdx.x;
-    float acc[4][1] = {{0.0f}, {0.0f}, {0.0f}, {0.0f}};
-    float ssq = 0.0f;
-    float *xc = wg == 0 ? a.x_copy : nullptr;
-    if (wg < nq) rq_dot<DTQ>(a.wq, a.soff_q, wg, a.nblk, a.x, a.lnw, xc, acc, ssq);
-    else rq_dot<DTKV>(a.wkv, a.soff_kv, wg - nq, a.nblk, a.x, a.lnw, xc, acc, ssq);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r][0] = wave_sum(acc[r][0]);
-    if (a.lnw) {
-        const float inv = 1.0f / sqrtf(wave_sum(ssq) / (float)(a.nblk * QK) + a.eps);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r][0] *= inv;
-    }
     const int64_t slot = a.step[VGX_STEP_SLOT];
     const int64_t sink = a.step[VGX_STEP_SINK_SLOT];
     const float *cs = a.table + (int64_t)a.step[VGX_STEP_TABLE_ROW] * a.trs;
@@ -152,8 +142,182 @@ __global__ __launch_bounds__(64) void qkv_rope_step_kernel(QkvStepArgs a) {
     if (sink >= 0 && a.sv) put<KV>(a.sv, g * a.sgs + sink * a.srs + i, v);
 }
 
+template <int DTQ, int DTKV, int KV>
+__global__ __launch_bounds__(64) void qkv_rope_step_kernel(QkvStepArgs a) {
+    const int qpd = a.D / 4;                              // row-quads per head
+    const int64_t nq = (int64_t)a.H * qpd;
+    const int64_t wg = blockIdx.x;
+    const int lane = threadIdx.x;
+    float acc[4][1] = {{0.0f}, {0.0f}, {0.0f}, {0.0f}};
+    float ssq = 0.0f;
+    float *xc = wg == 0 ? a.x_copy : nullptr;
+    if (wg < nq) rq_dot<DTQ>(a.wq, a.soff_q, wg, a.nblk, a.x, a.lnw, xc, acc, ssq);
+    else rq_dot<DTKV>(a.wkv, a.soff_kv, wg - nq, a.nblk, a.x, a.lnw, xc, acc, ssq);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r][0] = wave_sum(acc[r][0]);
+    if (a.lnw) {
+        const float inv = 1.0f / sqrtf(wave_sum(ssq) / (float)(a.nblk * QK) + a.eps);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r][0] *= inv;
+    }
+    qkv_epilogue<KV>(a, wg, lane, acc);
+}
+
+// Q8_0 / Q4_0 weights of rows up to 64 blocks (d_model <= 2048): a workgroup of 4 waves per row-quad.
+// The row-quad's run is cut into 1 KB pieces (Q4_0: 16 blocks x 4 rows, lane l row l & 3 of block
+// 16 p + l / 4; Q8_0: 8 blocks x 4 rows, lane l half l & 1 of row (l >> 1) & 3 of block 8 p + l / 8),
+// one 16-byte buffer load per lane and piece, wave w taking pieces w and w + 4; every load instruction
+// reads one contiguous 1 KB range.  The workgroup stages lnw * x once in LDS (blocks padded to 36
+// floats against bank conflicts, Q4_0 block sums for the -8 offset) with sum x^2 for the RMSNorm
+// scale; the lanes of a row and then the 4 waves are summed in a fixed order, and wave 0 runs the
+// epilogue.
+constexpr int kQkvPiecesMaxBlocks = 64;
+
+template <int DT>
+__device__ __forceinline__ float qkv_piece_dot(uint4 w, uint32_t sc, const float *xs, const float *xsum, int blk,
+                                               int lane) {
+    const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+    float p = 0.0f;
+    if constexpr (DT == VGX_Q4_0) {
+        const float4 *xb = reinterpret_cast<const float4 *>(xs + blk * kGemvPad);
+        float xv[QK];
+#pragma unroll
+        for (int j4 = 0; j4 < 8; ++j4) {
+            const float4 t = xb[j4];
+            xv[4 * j4] = t.x; xv[4 * j4 + 1] = t.y; xv[4 * j4 + 2] = t.z; xv[4 * j4 + 3] = t.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = gemv_nibble_mask(q[k]);
+            const uint32_t hi = gemv_nibble_mask(q[k] >> 4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                p = fmaf(gemv_cvt_u8(lo, t), xv[4 * k + t], p);
+                p = fmaf(gemv_cvt_u8(hi, t), xv[16 + 4 * k + t], p);
+            }
+        }
+        p -= xsum[blk];
+    } else {
+        const float4 *xb = reinterpret_cast<const float4 *>(xs + blk * kGemvPad + (lane & 1) * 16);
+        float xv[16];
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+            const float4 t = xb[j4];
+            xv[4 * j4] = t.x; xv[4 * j4 + 1] = t.y; xv[4 * j4 + 2] = t.z; xv[4 * j4 + 3] = t.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) p = fmaf(gemv_cvt_s8(q[k], t), xv[4 * k + t], p);
+    }
+    return half_bits_to_float(sc) * p;
+}
+
+// the row-quad's dot products, summed over the workgroup: every lane of wave 0 gets rows 0..3
+template <int DT>
+__device__ __forceinline__ void qkv_pieces_rq(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq, int64_t rq,
+                                              int nblk, const float *xs, const float *xsum, float (*red)[4],
+                                              int wave, int lane) {
+    constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
+    constexpr int BPP = 1024 / (4 * QB);               // blocks per piece
+    const int npc = (nblk + BPP - 1) / BPP;
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, (int)soff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t srs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(W + soff), 0, (int)(n_rq * nblk * 8), 0x00020000);
+    const int row = DT == VGX_Q8_0 ? (lane >> 1) & 3 : lane & 3;
+    uint4 wq[2];
+    uint32_t wsc[2];
+    int blk_of[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int pc = wave + 4 * k;
+        const int blk = BPP * pc + (DT == VGX_Q8_0 ? lane >> 3 : lane >> 2);
+        const bool ok = pc < npc && blk < nblk;
+        blk_of[k] = min(blk, nblk - 1);
+        const uint32_t qo = ok ? (uint32_t)((rq * nblk + blk) * 4 * QB + row * QB + (DT == VGX_Q8_0 ? (lane & 1) * 16 : 0))
+                               : kStreamPastEnd;
+        const uint32_t so = ok ? (uint32_t)((rq * nblk + blk) * 8 + row * 2) : kStreamPastEnd;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, qo, 0, 0);
+        wq[k] = make_uint4(v[0], v[1], v[2], v[3]);
+        wsc[k] = __builtin_amdgcn_raw_buffer_load_b16(srs, so, 0, 0);
+    }
+    __syncthreads();                                   // the activations are staged
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+        if (wave + 4 * k < npc) acc += qkv_piece_dot<DT>(wq[k], wsc[k], xs, xsum, blk_of[k], lane);
+    if constexpr (DT == VGX_Q8_0) {
+        acc += dpp_f<DPP_QUAD_1032>(acc);             // lane ^ 1: the other half of the row
+        acc += dpp_f<0x128>(acc);                     // row_ror 8: lane ^ 8
+    } else {
+        acc += dpp_f<0x124>(acc);                     // row_ror 4 and 8: the lanes of the same l & 3
+        acc += dpp_f<0x128>(acc);
+    }
+    acc = xor32_sum(xor16_sum(acc));
+    if (DT == VGX_Q8_0 ? (lane & 0x39) == 0 : lane < 4) red[wave][row] = acc;
+    __syncthreads();
+}
+
+template <int DTQ, int DTKV, int KV>
+__global__ __launch_bounds__(256) void qkv_rope_step_pieces_kernel(QkvStepArgs a) {
+    __shared__ __align__(16) float xs[kQkvPiecesMaxBlocks * kGemvPad];
+    __shared__ float xsum[kQkvPiecesMaxBlocks];
+    __shared__ float red[4][4];
+    __shared__ float rss[4];
+    const int qpd = a.D / 4;
+    const int64_t nq = (int64_t)a.H * qpd;
+    const int64_t wg = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nblk = a.nblk, n4 = nblk * 8;
+    // lnw * x staged (two float4 per thread cover 64 blocks), sum x^2, Q4_0 block sums
+    float4 xv[2], gv[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + 256 * u;
+        xv[u] = i < n4 ? reinterpret_cast<const float4 *>(a.x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        gv[u] = a.lnw && i < n4 ? reinterpret_cast<const float4 *>(a.lnw)[i] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
+    float ssq = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + 256 * u;
+        float4 t = xv[u];
+        if (i < n4 && wg == 0 && a.x_copy) reinterpret_cast<float4 *>(a.x_copy)[i] = t;
+        ssq += fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, t.w * t.w)));
+        t.x *= gv[u].x; t.y *= gv[u].y; t.z *= gv[u].z; t.w *= gv[u].w;
+        if (i < n4) reinterpret_cast<float4 *>(xs)[(i >> 3) * (kGemvPad / 4) + (i & 7)] = t;
+        float s = (t.x + t.y) + (t.z + t.w);          // the block's 8 float4 are 8 consecutive threads
+        s += __shfl_xor(s, 1, kWave);
+        s += __shfl_xor(s, 2, kWave);
+        s += __shfl_xor(s, 4, kWave);
+        if (i < n4 && (i & 7) == 0) xsum[i >> 3] = 8.0f * s;
+    }
+    ssq = wave_sum(ssq);
+    if (lane == 0) rss[wave] = ssq;
+    if (wg < nq) qkv_pieces_rq<DTQ>(a.wq, a.soff_q, nq, wg, nblk, xs, xsum, red, wave, lane);
+    else qkv_pieces_rq<DTKV>(a.wkv, a.soff_kv, (int64_t)2 * a.G * qpd, wg - nq, nblk, xs, xsum, red, wave, lane);
+    if (wave != 0) return;
+    float acc[4][1];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r][0] = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
+    if (a.lnw) {
+        const float inv = 1.0f / sqrtf(((rss[0] + rss[1]) + (rss[2] + rss[3])) / (float)(nblk * QK) + a.eps);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r][0] *= inv;
+    }
+    qkv_epilogue<KV>(a, wg, lane, acc);
+}
+
 template <int DTQ, int DTKV>
 void launch(int kv, const QkvStepArgs &a, unsigned grid, hipStream_t st) {
+    const bool pieces = DTQ != VGX_F32 && a.nblk <= kQkvPiecesMaxBlocks && a.soff_q < ((int64_t)1 << 31) &&
+                        a.soff_kv < ((int64_t)1 << 31);
+    if (pieces) {
+        if (kv == VGX_F32) hipLaunchKernelGGL((qkv_rope_step_pieces_kernel<DTQ, DTKV, VGX_F32>), dim3(grid), dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((qkv_rope_step_pieces_kernel<DTQ, DTKV, VGX_BF16>), dim3(grid), dim3(256), 0, st, a);
+        return;
+    }
     if (kv == VGX_F32) hipLaunchKernelGGL((qkv_rope_step_kernel<DTQ, DTKV, VGX_F32>), dim3(grid), dim3(64), 0, st, a);
     else hipLaunchKernelGGL((qkv_rope_step_kernel<DTQ, DTKV, VGX_BF16>), dim3(grid), dim3(64), 0, st, a);
 }
