@@ -13,7 +13,7 @@
 //
 // One activation row (the decode step) runs gemv1_kernel, whose mapping is picked from the shape
 // (below), for 1536-column weights of >= 8192 rows (gate/up, the LM head) the persistent
-// gemv1_stream_kernel, for other Q4_0 rows (the down and o projections) gemv1_pieces_kernel; 2-4 rows per
+// gemv1_stream_kernel, for other rows (the down and o projections) gemv1_pieces_kernel; 2-4 rows per
 // pass run qgemv_kernel in row mode (16 lanes per row-quad, four row-quads per wave, 4 waves
 // per workgroup) for >= 2048 row-quads, else in split-K mode (a wave per row-quad).
 // Each lane requests the weights of up to U blocks at once to keep enough bytes in flight for HBM.
@@ -741,30 +741,75 @@ __global__ __launch_bounds__(256) void gemv1_stream_kernel(GemvArgs a) {
         if (full + s < cnt) store(full + s, dot(s));
 }
 
-// One-row Q4_0 GEMV over rows of up to MAXB blocks (the down projection, 1536 x 8960: 16 waves x 2
-// row-quads; the o-projection, 1536 x 1536: 4 waves x 1 row-quad): a workgroup of NW waves takes RQG
-// row-quads; their runs are cut into 1 KB pieces (16 blocks x 4 rows, the last
+// One lane's 16-byte piece of a row-quad run against activations staged in LDS as padded blocks
+// (kGemvPad floats per block) with Q4_0 block sums x 8: Q4_0 row l & 3 of block blk (32 nibbles), Q8_0
+// half l & 1 of row (l >> 1) & 3 of block blk (16 bytes); d * (sum q x [- 8 sum x]).
+template <int DT>
+__device__ __forceinline__ float gemv_piece_dot(uint4 w, uint32_t sc, const float *xs, const float *xsum, int blk,
+                                               int lane) {
+    const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+    float p = 0.0f;
+    if constexpr (DT == VGX_Q4_0) {
+        const float4 *xb = reinterpret_cast<const float4 *>(xs + blk * kGemvPad);
+        float xv[QK];
+#pragma unroll
+        for (int j4 = 0; j4 < 8; ++j4) {
+            const float4 t = xb[j4];
+            xv[4 * j4] = t.x; xv[4 * j4 + 1] = t.y; xv[4 * j4 + 2] = t.z; xv[4 * j4 + 3] = t.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = gemv_nibble_mask(q[k]);
+            const uint32_t hi = gemv_nibble_mask(q[k] >> 4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                p = fmaf(gemv_cvt_u8(lo, t), xv[4 * k + t], p);
+                p = fmaf(gemv_cvt_u8(hi, t), xv[16 + 4 * k + t], p);
+            }
+        }
+        p -= xsum[blk];
+    } else {
+        const float4 *xb = reinterpret_cast<const float4 *>(xs + blk * kGemvPad + (lane & 1) * 16);
+        float xv[16];
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+            const float4 t = xb[j4];
+            xv[4 * j4] = t.x; xv[4 * j4 + 1] = t.y; xv[4 * j4 + 2] = t.z; xv[4 * j4 + 3] = t.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) p = fmaf(gemv_cvt_s8(q[k], t), xv[4 * k + t], p);
+    }
+    return half_bits_to_float(sc) * p;
+}
+
+// One-row Q8_0 / Q4_0 GEMV over rows of up to MAXB blocks (the down projection, 1536 x 8960: 16 waves
+// x 2 row-quads; the o-projection, 1536 x 1536: 4 waves x 1 row-quad): a workgroup of NW waves takes
+// RQG row-quads; their runs are cut into 1 KB pieces (Q4_0 16 blocks, Q8_0 8 blocks x 4 rows, the last
 // piece of a row-quad partial), and each wave takes every NW-th of the RQG x pieces, one 16-byte
-// buffer load per lane and piece (row l & 3 of block 16 p + l / 4), all requested before the
-// activations are needed.  The activations are staged once per workgroup in LDS, blocks padded to 36
+// buffer load per lane and piece (gemv_piece_dot), all requested before the activations are needed.  The activations are staged once per workgroup in LDS, blocks padded to 36
 // floats (the 16 blocks a piece reads at once would otherwise share one bank), with their per-block
 // sums (the -8 offset term); the lanes of a row and then the waves are summed in a fixed order
 // (deterministic).
 constexpr int kPiecesMaxBlocks = 320;
 
-template <int EPI, int NW, int RQG, int MAXB>
+template <int DT, int EPI, int NW, int RQG, int MAXB>
 __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
-    constexpr int MAXI = (RQG * ((MAXB + 15) / 16) + NW - 1) / NW;   // pieces per wave (rows of <= MAXB blocks)
+    constexpr int QB = gemv_quant_bytes(DT);
+    constexpr int BPP = 1024 / (4 * QB);              // blocks per 1 KB piece: 16 (Q4_0) / 8 (Q8_0)
+    constexpr int MAXI = (RQG * ((MAXB + BPP - 1) / BPP) + NW - 1) / NW;   // pieces per wave
     extern __shared__ float4 xs4[];                   // [nblk][36] activations, then [nblk] block sums
     float *xs = reinterpret_cast<float *>(xs4);
     __shared__ float red[NW][RQG][4];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nblk = a.nblk, cols = nblk * QK;
-    const int npc = (nblk + 15) / 16;                 // pieces per row-quad
+    const int npc = (nblk + BPP - 1) / BPP;           // pieces per row-quad
     const int64_t rq0 = (int64_t)blockIdx.x * RQG;
     const int n_rq = (int)a.n_rq;
     float *xsum = xs + nblk * kGemvPad;
+    const int row = DT == VGX_Q8_0 ? (lane >> 1) & 3 : lane & 3;   // the lane's row of the row-quad
 
     // activations first (their wait then covers no weights), 8 float4 = one block per 8 threads
     const int n4 = cols / 4;
@@ -789,11 +834,12 @@ __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
         const int it = wave + NW * k;
         const int rql = it / npc, pc = it - rql * npc;
         const int64_t rq = rq0 + rql;
-        const int blk = 16 * pc + (lane >> 2);
+        const int blk = BPP * pc + (DT == VGX_Q8_0 ? lane >> 3 : lane >> 2);
         const bool ok = it < RQG * npc && rq < n_rq && blk < nblk;
         blk_of[k] = min(blk, nblk - 1);
-        const uint32_t qo = ok ? (uint32_t)((rq * nblk + blk) * 64 + (lane & 3) * 16) : kStreamPastEnd;
-        const uint32_t so = ok ? (uint32_t)((rq * nblk + blk) * 8 + (lane & 3) * 2) : kStreamPastEnd;
+        const uint32_t qo = ok ? (uint32_t)((rq * nblk + blk) * 4 * QB + row * QB + (DT == VGX_Q8_0 ? (lane & 1) * 16 : 0))
+                               : kStreamPastEnd;
+        const uint32_t so = ok ? (uint32_t)((rq * nblk + blk) * 8 + row * 2) : kStreamPastEnd;
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, qo, 0, 0);
         wq[k] = make_uint4(v[0], v[1], v[2], v[3]);
         wsc[k] = __builtin_amdgcn_raw_buffer_load_b16(srs, so, 0, 0);
@@ -818,26 +864,7 @@ __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
     for (int k = 0; k < MAXI; ++k) {
         const int it = wave + NW * k;
         if (it >= RQG * npc) break;                   // uniform: the wave's item count
-        const float4 *xb = xs4 + blk_of[k] * (kGemvPad / 4);
-        float xv[QK];
-#pragma unroll
-        for (int j4 = 0; j4 < 8; ++j4) {
-            const float4 t = xb[j4];
-            xv[4 * j4] = t.x; xv[4 * j4 + 1] = t.y; xv[4 * j4 + 2] = t.z; xv[4 * j4 + 3] = t.w;
-        }
-        const uint32_t q[4] = {wq[k].x, wq[k].y, wq[k].z, wq[k].w};
-        float p = 0.0f;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const uint32_t lo = gemv_nibble_mask(q[kk]);
-            const uint32_t hi = gemv_nibble_mask(q[kk] >> 4);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                p = fmaf(gemv_cvt_u8(lo, t), xv[4 * kk + t], p);
-                p = fmaf(gemv_cvt_u8(hi, t), xv[16 + 4 * kk + t], p);
-            }
-        }
-        const float v = half_bits_to_float(wsc[k]) * (p - xsum[blk_of[k]]);
+        const float v = gemv_piece_dot<DT>(wq[k], wsc[k], xs, xsum, blk_of[k], lane);
         const int rql = it / npc;
 #pragma unroll
         for (int r = 0; r < RQG; ++r)
@@ -846,10 +873,15 @@ __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < RQG; ++r) {
         float v = acc[r];
-        v += dpp_f<0x124>(v);                         // row_ror 4 and 8: the lanes of the same l & 3
-        v += dpp_f<0x128>(v);
+        if constexpr (DT == VGX_Q8_0) {
+            v += dpp_f<DPP_QUAD_1032>(v);             // lane ^ 1: the other half of the row
+            v += dpp_f<0x128>(v);                     // row_ror 8: lane ^ 8
+        } else {
+            v += dpp_f<0x124>(v);                     // row_ror 4 and 8: the lanes of the same l & 3
+            v += dpp_f<0x128>(v);
+        }
         v = xor32_sum(xor16_sum(v));
-        if (lane < 4) red[wave][r][lane] = v;
+        if (DT == VGX_Q8_0 ? (lane & 0x39) == 0 : lane < 4) red[wave][r][row] = v;
     }
     __syncthreads();
     if (tid < 4 * RQG) {
@@ -857,11 +889,11 @@ __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) v += red[w][rql][r];
-        const int64_t row = (rq0 + rql) * 4 + r;
-        if (row < a.rows_out) {
-            if (a.bias) v += a.bias[row];
-            if constexpr (EPI == EPI_ACCUM) v += a.y[row];
-            a.y[row] = v;
+        const int64_t orow = (rq0 + rql) * 4 + r;
+        if (orow < a.rows_out) {
+            if (a.bias) v += a.bias[orow];
+            if constexpr (EPI == EPI_ACCUM) v += a.y[orow];
+            a.y[orow] = v;
         }
     }
 }
@@ -883,22 +915,22 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
             return;
         }
     }
-    if constexpr (DT == VGX_Q4_0 && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
+    if constexpr (DT != VGX_F32 && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
         if (a.nblk >= 192 && a.nblk <= kPiecesMaxBlocks && a.soff < ((int64_t)1 << 31) && aligned) {
             // 16 waves x 2 row-quads: 5.5 us for 1536 x 8960 (8 x 2: 5.8, 8 x 1: 6.0, 16 x 1: 5.9, 16 x 4: 7.3,
             // 4 x 1: 6.8; the lane-per-block kernel: 6.6)
             constexpr int NW = 16, RQG = 2;
-            hipLaunchKernelGGL((gemv1_pieces_kernel<EPI, NW, RQG, kPiecesMaxBlocks>), dim3((unsigned)((a.n_rq + RQG - 1) / RQG)), dim3(64 * NW),
+            hipLaunchKernelGGL((gemv1_pieces_kernel<DT, EPI, NW, RQG, kPiecesMaxBlocks>), dim3((unsigned)((a.n_rq + RQG - 1) / RQG)), dim3(64 * NW),
                                (size_t)(a.nblk * kGemvPad + a.nblk) * sizeof(float), st, a);
             return;
         }
     }
-    if constexpr (DT == VGX_Q4_0 && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
+    if constexpr (DT != VGX_F32 && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
         if (a.nblk == kStreamBlocks && a.n_rq < kStreamMinRq && a.soff < ((int64_t)1 << 31) && aligned) {
             // 1536-column rows (the o-projection, 1536 x 1536): a workgroup of 4 waves per row-quad, one 1 KB
             // piece per wave (3 of them busy): 3.2 us against 4.2 us for the lane-per-block kernel (2 x 2: 3.7,
             // 4 x 2: 3.6, 3 x 1: 3.2, 6 x 2: 3.4, 8 x 4: 3.6)
-            hipLaunchKernelGGL((gemv1_pieces_kernel<EPI, 4, 1, kStreamBlocks>), dim3((unsigned)a.n_rq), dim3(256),
+            hipLaunchKernelGGL((gemv1_pieces_kernel<DT, EPI, 4, 1, kStreamBlocks>), dim3((unsigned)a.n_rq), dim3(256),
                                (size_t)(a.nblk * kGemvPad + a.nblk) * sizeof(float), st, a);
             return;
         }

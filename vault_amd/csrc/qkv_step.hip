@@ -173,46 +173,6 @@ __global__ __launch_bounds__(64) void qkv_rope_step_kernel(QkvStepArgs a) {
 // epilogue.
 constexpr int kQkvPiecesMaxBlocks = 64;
 
-template <int DT>
-__device__ __forceinline__ float qkv_piece_dot(uint4 w, uint32_t sc, const float *xs, const float *xsum, int blk,
-                                               int lane) {
-    const uint32_t q[4] = {w.x, w.y, w.z, w.w};
-    float p = 0.0f;
-    if constexpr (DT == VGX_Q4_0) {
-        const float4 *xb = reinterpret_cast<const float4 *>(xs + blk * kGemvPad);
-        float xv[QK];
-#pragma unroll
-        for (int j4 = 0; j4 < 8; ++j4) {
-            const float4 t = xb[j4];
-            xv[4 * j4] = t.x; xv[4 * j4 + 1] = t.y; xv[4 * j4 + 2] = t.z; xv[4 * j4 + 3] = t.w;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t lo = gemv_nibble_mask(q[k]);
-            const uint32_t hi = gemv_nibble_mask(q[k] >> 4);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                p = fmaf(gemv_cvt_u8(lo, t), xv[4 * k + t], p);
-                p = fmaf(gemv_cvt_u8(hi, t), xv[16 + 4 * k + t], p);
-            }
-        }
-        p -= xsum[blk];
-    } else {
-        const float4 *xb = reinterpret_cast<const float4 *>(xs + blk * kGemvPad + (lane & 1) * 16);
-        float xv[16];
-#pragma unroll
-        for (int j4 = 0; j4 < 4; ++j4) {
-            const float4 t = xb[j4];
-            xv[4 * j4] = t.x; xv[4 * j4 + 1] = t.y; xv[4 * j4 + 2] = t.z; xv[4 * j4 + 3] = t.w;
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-#pragma unroll
-            for (int t = 0; t < 4; ++t) p = fmaf(gemv_cvt_s8(q[k], t), xv[4 * k + t], p);
-    }
-    return half_bits_to_float(sc) * p;
-}
-
 // the row-quad's dot products, summed over the workgroup: every lane of wave 0 gets rows 0..3
 template <int DT>
 __device__ __forceinline__ void qkv_pieces_rq(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq, int64_t rq,
@@ -245,7 +205,7 @@ __device__ __forceinline__ void qkv_pieces_rq(const uint8_t *__restrict__ W, int
     float acc = 0.0f;
 #pragma unroll
     for (int k = 0; k < 2; ++k)
-        if (wave + 4 * k < npc) acc += qkv_piece_dot<DT>(wq[k], wsc[k], xs, xsum, blk_of[k], lane);
+        if (wave + 4 * k < npc) acc += gemv_piece_dot<DT>(wq[k], wsc[k], xs, xsum, blk_of[k], lane);
     if constexpr (DT == VGX_Q8_0) {
         acc += dpp_f<DPP_QUAD_1032>(acc);             // lane ^ 1: the other half of the row
         acc += dpp_f<0x128>(acc);                     // row_ror 8: lane ^ 8
