@@ -113,6 +113,14 @@ def test_gemv_tall_fused_rmsnorm(dev, dt, rows):
     assert np.all(err <= tol), float((err / tol).max())
 
 
+@pytest.mark.parametrize("batch", [1, 2])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_gemv_f32_scorer_shape(dev, batch, accumulate):
+    """F32 weights at the segment scorer's fc1 shape (256 x 4608) with bias, one and two activation rows
+    (the decode step's features and habituated features in one pass), store and accumulate."""
+    _check_gemv(dev, codec.F32, 256, 4608, batch, seed=31 + batch, bias=True, accumulate=accumulate)
+
+
 @pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
 def test_gemv_bias_and_residual(dev, dt):
     _check_gemv(dev, dt, 1536, 1536, 1, seed=21, kind="quantized", bias=True)

@@ -898,6 +898,91 @@ __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
     }
 }
 
+// One or two activation rows against F32 weights of up to 160 blocks per row (the segment scorer's fc1,
+// 256 x 4608, on the token's features and their habituated copy): the weights are read once for both
+// rows.  A workgroup of 16 waves per row-quad; the row-quad's run (512 bytes per block) is cut into 1 KB
+// pieces, lane l holding floats 4 (l & 7) .. + 3 of row (l >> 3) & 3 of block 2 p + l / 32, one 16-byte
+// buffer load per lane and piece, all requested before the activations (staged once in LDS) are read.
+constexpr int kF32PiecesMaxBlocks = 160;
+constexpr int kF32PiecesWaves = 16;
+
+template <int NB, int EPI>
+__global__ __launch_bounds__(64 * kF32PiecesWaves) void gemv_f32_pieces_kernel(GemvArgs a) {
+    constexpr int NW = kF32PiecesWaves;
+    constexpr int MAXI = (kF32PiecesMaxBlocks / 2 + NW - 1) / NW;   // pieces per wave
+    __shared__ float4 xs4[NB * kF32PiecesMaxBlocks * 8];
+    __shared__ float red[NW][4][NB];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nblk = a.nblk, n4 = nblk * 8;
+    const int npc = (nblk + 1) / 2;                   // pieces per row-quad
+    const int64_t rq = blockIdx.x;
+    const int row = (lane >> 3) & 3;
+    // activations (both rows), then the weights
+    constexpr int XR = (NB * kF32PiecesMaxBlocks * 8 + 64 * NW - 1) / (64 * NW);
+    float4 xv[XR];
+#pragma unroll
+    for (int u = 0; u < XR; ++u) {
+        const int i = tid + 64 * NW * u, n = i / n4, c = i - n * n4;
+        xv[u] = n < NB ? reinterpret_cast<const float4 *>(a.x + n * a.ldx)[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.w, 0, (int)(a.n_rq * nblk * 512), 0x00020000);
+    float4 wv[MAXI];
+    int blk_of[MAXI];
+#pragma unroll
+    for (int k = 0; k < MAXI; ++k) {
+        const int pc = wave + NW * k;
+        const int blk = 2 * pc + (lane >> 5);
+        const bool ok = pc < npc && blk < nblk;
+        blk_of[k] = min(blk, nblk - 1);
+        const uint32_t o = ok ? (uint32_t)((rq * nblk + blk) * 512 + (lane & 31) * 16) : kStreamPastEnd;
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, o, 0, 0);
+        wv[k] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+    }
+#pragma unroll
+    for (int u = 0; u < XR; ++u) {
+        const int i = tid + 64 * NW * u;
+        if (i < NB * n4) xs4[i] = xv[u];
+    }
+    __syncthreads();
+    float acc[NB];
+#pragma unroll
+    for (int n = 0; n < NB; ++n) acc[n] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MAXI; ++k) {
+        if (wave + NW * k >= npc) break;              // uniform: the wave's piece count
+        const float4 w = wv[k];
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const float4 x = xs4[n * n4 + blk_of[k] * 8 + (lane & 7)];
+            acc[n] = fmaf(w.x, x.x, fmaf(w.y, x.y, fmaf(w.z, x.z, fmaf(w.w, x.w, acc[n]))));
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+        float v = acc[n];
+        v += dpp_f<DPP_QUAD_1032>(v);                 // lanes of the same row: bits 0..2 and 5
+        v += dpp_f<DPP_QUAD_2301>(v);
+        v += dpp_f<DPP_ROW_HALF_MIRROR>(v);
+        v = xor32_sum(v);
+        if ((lane & 0x27) == 0) red[wave][row][n] = v;
+    }
+    __syncthreads();
+    if (tid < 4 * NB) {
+        const int r = tid >> (NB == 2 ? 1 : 0), n = NB == 2 ? tid & 1 : 0;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[w][r][n];
+        const int64_t orow = rq * 4 + r;
+        if (orow < a.rows_out) {
+            if (a.bias) v += a.bias[orow];
+            if constexpr (EPI == EPI_ACCUM) v += a.y[n * a.ldy + orow];
+            a.y[n * a.ldy + orow] = v;
+        }
+    }
+}
+
 constexpr int kGemv1MaxBlocks = 448;   // LDS staging of one row: 448 * 36 * 4 B = 63 KB
 
 template <int DT, int EPI, bool NORM>
@@ -955,6 +1040,16 @@ template <int DT>
 int qgemv_launch(GemvArgs a, hipStream_t st) {
     const bool rows_mode = a.n_rq >= 2048;
     const bool norm = a.lnw != nullptr;
+    if constexpr (DT == VGX_F32) {
+        if (a.batch <= 2 && !norm && a.epi != EPI_SWIGLU && a.nblk <= kF32PiecesMaxBlocks &&
+            a.n_rq * a.nblk * 512 < ((int64_t)1 << 31) && ((uintptr_t)a.x & 15) == 0 && a.ldx % 4 == 0) {
+#define VGX_F32P(NB, EPIV) hipLaunchKernelGGL((gemv_f32_pieces_kernel<NB, EPIV>), dim3((unsigned)a.n_rq), dim3(64 * kF32PiecesWaves), 0, st, a)
+            if (a.batch == 2) { if (a.epi == EPI_ACCUM) VGX_F32P(2, EPI_ACCUM); else VGX_F32P(2, EPI_STORE); }
+            else { if (a.epi == EPI_ACCUM) VGX_F32P(1, EPI_ACCUM); else VGX_F32P(1, EPI_STORE); }
+#undef VGX_F32P
+            return hipGetLastError() == hipSuccess ? VGX_OK : VGX_E_HIP;
+        }
+    }
     if (a.batch == 1 && a.nblk <= kGemv1MaxBlocks && ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.lnw & 15) == 0) {
         if (a.epi == EPI_SWIGLU) { if (norm) gemv1_launch<DT, EPI_SWIGLU, true>(a, st); else gemv1_launch<DT, EPI_SWIGLU, false>(a, st); }
         else if (a.epi == EPI_ACCUM) { if (norm) gemv1_launch<DT, EPI_ACCUM, true>(a, st); else gemv1_launch<DT, EPI_ACCUM, false>(a, st); }

@@ -756,12 +756,7 @@ class VAULTv3ForCausalLM:
         sw = self.w.scorer
         ops.ema_habituate(rows[:T], rows[T:2 * T], st.seg_feat_ema, first)
         ops.layernorm(rows[:2 * T], sw.ln_w, sw.ln_b, 1e-5, rows[:2 * T])
-        if T == 1:   # two one-row GEMVs: the one-row kernel splits K over 8 waves for this shape
-            h1 = torch.empty(2, sw.w1.rows, dtype=torch.float32, device=self.device)
-            ops.qlinear(sw.w1, rows[0:1], bias=sw.b1, out=h1[0:1])
-            ops.qlinear(sw.w1, rows[1:2], bias=sw.b1, out=h1[1:2])
-        else:
-            h1 = ops.qlinear(sw.w1, rows[:2 * T], bias=sw.b1)
+        h1 = ops.qlinear(sw.w1, rows[:2 * T], bias=sw.b1)   # T = 1: both rows in one pass over the weights
         ops.seg_score_tail(h1, sw.w2, sw.b2, T, first, st.sc_cur[c0:c0 + T], out_index=out_index)
 
     def _logits(self, h: torch.Tensor) -> torch.Tensor:
