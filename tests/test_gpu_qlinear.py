@@ -113,6 +113,16 @@ def test_gemv_tall_fused_rmsnorm(dev, dt, rows):
     assert np.all(err <= tol), float((err / tol).max())
 
 
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
+@pytest.mark.parametrize("rows,cols", [(1026, 8960), (1026, 1536), (6, 6400)])
+def test_gemv_pieces_ragged(dev, dt, rows, cols):
+    """One-row GEMV on 1 KB pieces at ragged shapes: an odd row-quad count (the last workgroup of two
+    row-quads holds one), rows not a multiple of 4, a row length whose last piece is partial (200 blocks),
+    with bias and with the residual add."""
+    _check_gemv(dev, dt, rows, cols, 1, seed=rows + cols, kind="quantized", bias=True)
+    _check_gemv(dev, dt, rows, cols, 1, seed=rows + cols + 1, kind="quantized", accumulate=True)
+
+
 @pytest.mark.parametrize("batch", [1, 2])
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_gemv_f32_scorer_shape(dev, batch, accumulate):
