@@ -29,7 +29,8 @@ def _blocks(dt, rows, cols, seed):
     (1536, 1536, 16, "store", False), (2048, 1536, 300, "store", True), (1536, 8960, 37, "accum", False),
     (8960, 1536, 64, "swiglu", True), (13, 96, 9, "store", True), (256, 4608, 1024, "store", False),
     (2, 64, 8, "swiglu", False), (13, 96, 130, "store", True), (2, 64, 200, "swiglu", False),
-    (1536, 8960, 200, "accum", False)])
+    (1536, 8960, 200, "accum", False), (1536, 1536, 32, "accum", False), (1026, 1536, 27, "store", True),
+    (1024, 1024, 20, "swiglu", True)])
 def test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm):
     rng = np.random.default_rng(rows + cols + batch)
     x = (rng.standard_normal((batch, cols)) * 2.0).astype(np.float32)
@@ -94,10 +95,10 @@ def test_qgemm_equals_gemv_rows(dev, dt):
     assert bool(((big.double() - one.double()).abs() <= tol).all())
 
 
-@pytest.mark.parametrize("epi,rows,cols", [("swiglu", 8960, 1536), ("accum", 1536, 8960)])
+@pytest.mark.parametrize("epi,rows,cols", [("swiglu", 8960, 1536), ("accum", 1536, 8960), ("accum", 1536, 1536)])
 def test_qgemm_fused_split_sum_replays(dev, epi, rows, cols):
     """Decode-batch Q4_0 projections whose K splits are summed by the last workgroup of each output tile
-    (gate/up with the RMSNorm, down with the residual add, batch 32): eager calls one after another and
+    (gate/up with the RMSNorm, down with the residual add, the o-projection on 64-row tiles, batch 32): eager calls one after another and
     replays of a captured graph, with eager work between the replays, give the same bits each time (the
     tile counters are back at zero after every call) and stay within the oracle bound."""
     rng = np.random.default_rng(rows + cols + 7)

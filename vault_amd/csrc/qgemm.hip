@@ -842,7 +842,7 @@ __device__ __forceinline__ void store4_agent(__amdgpu_buffer_rsrc_t rs, uint32_t
 
 // The tile's last workgroup: part [ks][batch][rows_p], pssq [ks][gridDim.x][batch] (or null);
 // thread (row-quad tid % 32, activation rows tid / 32 and 8 + tid / 32) of tile (blockIdx.x, blockIdx.y).
-template <int EPI>
+template <int EPI, int RQT = 32>
 __device__ __forceinline__ void ksplit_finish(const float *part, int ks, int64_t batch, int64_t n_rq, int64_t rows_out,
                                               const float *pssq, int cols, float eps, const float *bias, float *y,
                                               int64_t ldy, int *cnt, int *flag) {
@@ -855,20 +855,27 @@ __device__ __forceinline__ void ksplit_finish(const float *part, int ks, int64_t
     }
     __syncthreads();
     if (!*flag) return;
+    // thread: row-quad tid % RQT of the tile, activation rows tid / RQT + (256 / RQT) i
+    constexpr int NI = RQT / 16, BS = 256 / RQT;
     const int64_t rows_p = n_rq * 4;
-    const int64_t rq = (int64_t)blockIdx.x * 32 + (tid & 31);
-    const int64_t bA = (int64_t)blockIdx.y * 16 + (tid >> 5);
+    const int64_t rq = (int64_t)blockIdx.x * RQT + (tid % RQT);
+    const int64_t bA = (int64_t)blockIdx.y * 16 + tid / RQT;
     const int64_t gx = gridDim.x;
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc((void *)part, 0, (int)(ks * batch * rows_p * 4), 0x00020000);
-    float4 v[2] = {make_float4(0.0f, 0.0f, 0.0f, 0.0f), make_float4(0.0f, 0.0f, 0.0f, 0.0f)};
-    float t[2] = {0.0f, 0.0f};
-    for (int s0 = 0; s0 < ks; s0 += kFinLoads) {
-        float4 p[2][kFinLoads];
-        float q[2][kFinLoads];
+    float4 v[NI];
+    float t[NI];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int64_t b = bA + 8 * i;
+    for (int i = 0; i < NI; ++i) {
+        v[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        t[i] = 0.0f;
+    }
+    for (int s0 = 0; s0 < ks; s0 += kFinLoads) {
+        float4 p[NI][kFinLoads];
+        float q[NI][kFinLoads];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int64_t b = bA + BS * i;
 #pragma unroll
             for (int u = 0; u < kFinLoads; ++u) {
                 const int64_t sp = min(s0 + u, ks - 1);
@@ -881,7 +888,7 @@ __device__ __forceinline__ void ksplit_finish(const float *part, int ks, int64_t
             }
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < NI; ++i)
 #pragma unroll
             for (int u = 0; u < kFinLoads; ++u)
                 if (s0 + u < ks) {
@@ -893,8 +900,8 @@ __device__ __forceinline__ void ksplit_finish(const float *part, int ks, int64_t
                 }
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int64_t b = bA + 8 * i;
+    for (int i = 0; i < NI; ++i) {
+        const int64_t b = bA + BS * i;
         if (b >= batch || rq >= n_rq) continue;
         const float inv = pssq ? 1.0f / sqrtf(t[i] / (float)cols + eps) : 1.0f;
         float *yr = y + b * ldy;
@@ -1215,7 +1222,7 @@ constexpr int kKsSlice = 128 * kKsRow + 32 * 32;   // per slice: 128 rows, then 
 constexpr int kKsLds = 4 * kKsSlice;
 static_assert(kKsLds >= 4 * 8 * 64 * 16 + 4 * 16 * 4, "the LDS of qgemm_kslice_kernel holds the cross-slice sums");
 
-template <bool NORM, int FIN>
+template <bool NORM, int FIN, int RQT = 32>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) void qgemm_kslice_kernel(
     const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq, int nblk, int w_bytes, const float *__restrict__ x,
     int64_t ldx, const float *__restrict__ lnw, int64_t batch, float *__restrict__ part, float *__restrict__ part_ssq,
@@ -1224,7 +1231,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     __shared__ __align__(16) uint8_t smem[kKsLds];
     const int tid = threadIdx.x, lane = tid & 63, sl = tid >> 6;   // the wave's K slice
     const int l16 = lane & 15, lg = lane >> 4;
-    const int64_t rq0 = (int64_t)blockIdx.x * 32;
+    constexpr int NT = RQT / 4;                        // 16-row MFMA tiles of the workgroup's rows
+    static_assert(RQT == 32 || RQT == 16, "row tiles of 128 or 64 rows");
+    const int64_t rq0 = (int64_t)blockIdx.x * RQT;
     const int64_t b0 = (int64_t)blockIdx.y * 16;
     const int blk_lo = (int)blockIdx.z * kper;
     const int blk_hi = min(nblk, blk_lo + kper);
@@ -1257,9 +1266,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     }
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, w_bytes, 0x00020000);
     const bool live = wb0 < blk_hi;                    // wave-uniform: a slice past the range adds nothing
-    uint4 wr[8];
+    uint4 wr[NT];
 #pragma unroll
-    for (int h = 0; h < 8; ++h) {
+    for (int h = 0; h < NT; ++h) {
         const int64_t rq = rq0 + 4 * h + (lane >> 4);
         const uint32_t o = live && rq < n_rq ? (uint32_t)(rq * nblk * 64 + (int64_t)wb0 * 64) + (uint32_t)(l16 * 16)
                                              : kPastEnd;
@@ -1269,8 +1278,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     uint4 sr;
     {
         const int64_t rq = rq0 + (lane >> 1);
-        const uint32_t o = live && rq < n_rq ? (uint32_t)(soff + rq * nblk * 8 + (int64_t)(wb0 + 2 * (lane & 1)) * 8)
-                                             : kPastEnd;
+        const uint32_t o = live && (lane >> 1) < RQT && rq < n_rq
+                               ? (uint32_t)(soff + rq * nblk * 8 + (int64_t)(wb0 + 2 * (lane & 1)) * 8)
+                               : kPastEnd;
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, o, 0, 0);
         sr = make_uint4(v[0], v[1], v[2], v[3]);
     }
@@ -1310,7 +1320,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 
     // the slice's weights into the MFMA layout, its scales next to them
 #pragma unroll
-    for (int h = 0; h < 8; ++h) {
+    for (int h = 0; h < NT; ++h) {
         const int r = 4 * (4 * h + (lane >> 4)) + (lane & 3), u = (lane >> 2) & 3;
         uint32_t *p = reinterpret_cast<uint32_t *>(wl + r * kKsRow) + u;
         const int sw = (r >> 2) & 3;
@@ -1324,12 +1334,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    f32x4_t acc[8];
+    f32x4_t acc[NT];
 #pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t = 0; t < NT; ++t) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     if (live) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
+        for (int t = 0; t < NT; ++t) {
             const int row = 16 * t + l16;
             const uint4 a = *reinterpret_cast<const uint4 *>(wl + row * kKsRow + ((lg ^ ((l16 >> 2) & 3)) * 16));
             const uint4 s0 = *reinterpret_cast<const uint4 *>(wsc + (4 * t + lg) * 32);
@@ -1360,7 +1370,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     float4 *red = reinterpret_cast<float4 *>(smem);
     float *rss = reinterpret_cast<float *>(smem + 4 * 8 * 64 * 16);
 #pragma unroll
-    for (int t = 0; t < 8; ++t) red[(sl * 8 + t) * 64 + lane] = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+    for (int t = 0; t < NT; ++t) red[(sl * NT + t) * 64 + lane] = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
     if constexpr (NORM) {
         const float sq = xor32_sum(xor16_sum(ssq));
         if (lg == 0) rss[sl * 16 + l16] = sq;
@@ -1371,12 +1381,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc((void *)part, 0, FIN >= 0 ? (int)(gridDim.z * batch * rows_p * 4) : 0, 0x00020000);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int t = 2 * sl + j;
+    for (int j = 0; j < NT / 4; ++j) {
+        const int t = (NT / 4) * sl + j;
         float4 v = red[t * 64 + lane];
 #pragma unroll
         for (int w = 1; w < 4; ++w) {
-            const float4 o = red[(w * 8 + t) * 64 + lane];
+            const float4 o = red[(w * NT + t) * 64 + lane];
             v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
         }
         const int64_t crq = rq0 + 4 * t + lg;
@@ -1399,8 +1409,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     }
     if constexpr (FIN >= 0) {
         __shared__ int last;
-        ksplit_finish<FIN>(part, (int)gridDim.z, batch, n_rq, rows_out, NORM ? part_ssq : nullptr, cols, eps, bias, y,
-                           ldy, cnt + (int64_t)blockIdx.y * gridDim.x + blockIdx.x, &last);
+        ksplit_finish<FIN, RQT>(part, (int)gridDim.z, batch, n_rq, rows_out, NORM ? part_ssq : nullptr, cols, eps, bias,
+                                y, ldy, cnt + (int64_t)blockIdx.y * gridDim.x + blockIdx.x, &last);
     }
 }
 
@@ -1934,7 +1944,21 @@ inline bool use_fused_finish(int dtype, int kper, int64_t n_rq, int64_t batch, i
 
 // Workspace of the small-batch path: the tile counters, the K-split partials, then the per-split sum
 // x^2 of every row (per row tile when the launch sums its own splits).
-inline int64_t small_bytes(int64_t batch, int64_t n_rq, int nblk) {
+// Whether a short-K Q4_0 projection of a decode batch (the 1536-column o-projection) runs
+// qgemm_kslice_kernel on 64-row tiles over 16-block splits, summing its own splits: twice the
+// workgroups of the 128-row tiles, no reduce launch.
+inline bool use_short_kslice(int dtype, int nblk, int64_t n_rq, int64_t batch) {
+    const int ks = (nblk + kSplitMaxBlocks - 1) / kSplitMaxBlocks;
+    return dtype == VGX_Q4_0 && nblk % kSplitMaxBlocks == 0 && ks >= 2 && ks <= 4 && n_rq <= 1024 &&
+           (n_rq + 15) / 16 * ((batch + 15) / 16) <= kQgemmTickets && (int64_t)ks * batch * n_rq * 16 < ((int64_t)1 << 31);
+}
+
+inline int64_t small_bytes(int64_t batch, int64_t n_rq, int nblk, int dtype = VGX_Q4_0) {
+    if (use_short_kslice(dtype, nblk, n_rq, batch)) {
+        const int ks = nblk / kSplitMaxBlocks;
+        return kQgemmTicketBytes + part_bytes(ks, batch, n_rq * 4) +
+               ((int64_t)ks * ((n_rq + 15) / 16) * batch * 4 + 255) / 256 * 256;
+    }
     int kper = 0;
     const int ks = small_ksplit(n_rq, batch, nblk, &kper);
     if (ks <= 1) return 0;
@@ -2102,7 +2126,10 @@ int64_t vgx_qgemm_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, int
     const int64_t rows_p = rows4(epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows);
     const int ks = tile_ksplit(rows_p / 4, batch, (int)(cols / QK));
     const int64_t big = kQgemmTicketBytes + split_bytes(batch, cols) + part_bytes(ks, batch, rows_p);
-    return batch <= kSmallMaxBatch ? std::max(big, small_bytes(batch, rows_p / 4, (int)(cols / QK))) : big;
+    // the weight dtype is not an argument: the larger of the Q4_0 and Q8_0 layouts
+    const int64_t sq4 = small_bytes(batch, rows_p / 4, (int)(cols / QK), VGX_Q4_0);
+    const int64_t sq8 = small_bytes(batch, rows_p / 4, (int)(cols / QK), VGX_Q8_0);
+    return batch <= kSmallMaxBatch ? std::max(big, std::max(sq4, sq8)) : big;
 }
 
 int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx, int64_t batch,
@@ -2144,7 +2171,7 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     if (batch <= kSmallMaxBatch && ((uintptr_t)x & 15) == 0 && ldx % 4 == 0 && ((uintptr_t)norm_w & 15) == 0) {
         int kper = 0;
         const int ks = small_ksplit(n_rq, batch, nblk, &kper);
-        const int64_t need = small_bytes(batch, n_rq, nblk);
+        const int64_t need = small_bytes(batch, n_rq, nblk, dtype);
         if (need > 0 && (!workspace || workspace_bytes < need)) return VGX_E_ARENA;
         if (need > 0 && (uintptr_t)workspace % 256) return VGX_E_ALIGN;
         auto *tickets = static_cast<int *>(workspace);
@@ -2170,6 +2197,25 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
             if (nblk == 48) VGX_WDN(12); else VGX_WDN(6);
 #undef VGX_WDN
 #undef VGX_WD
+            VGX_CHECK_LAUNCH();
+            return VGX_OK;
+        }
+        if (!bias && use_short_kslice(dtype, nblk, n_rq, batch) && soff0 + n_rq * nblk * 8 < ((int64_t)1 << 30)) {
+            // 64-row tiles, 16-block splits summed by the launch (partials, then per-tile sum x^2)
+            const int ks16 = nblk / kSplitMaxBlocks;
+            auto *pssq16 = reinterpret_cast<float *>(static_cast<char *>(workspace) + kQgemmTicketBytes +
+                                                     part_bytes(ks16, batch, n_rq * 4));
+            const dim3 g16((unsigned)((n_rq + 15) / 16), (unsigned)((batch + 15) / 16), (unsigned)ks16);
+            const int wb = (int)(soff0 + n_rq * nblk * 8);
+#define VGX_KS16(NORM, F)                                                                                       \
+    hipLaunchKernelGGL((qgemm_kslice_kernel<NORM, F, 16>), g16, dim3(256), 0, st0, w, soff0, n_rq, nblk, wb, x, ldx, \
+                       norm_w, batch, part, pssq16, kSplitMaxBlocks, rows, eps, bias, y, ldy, tickets)
+#define VGX_KS16N(F) do { if (norm_w) VGX_KS16(true, F); else VGX_KS16(false, F); } while (0)
+            if (epilogue == VGX_EPI_SWIGLU) VGX_KS16N(EPI_SWIGLU);
+            else if (epilogue == VGX_EPI_ACCUM) VGX_KS16N(EPI_ACCUM);
+            else VGX_KS16N(EPI_STORE);
+#undef VGX_KS16N
+#undef VGX_KS16
             VGX_CHECK_LAUNCH();
             return VGX_OK;
         }
