@@ -25,7 +25,8 @@
 // Mapping.  Large batches (prefill chunks) run qgemm_tile_kernel (128 x 128 LDS tiles, below) after
 // the split pre-pass; decode batches of up to 64 rows run the K-split kernels (qgemm_kslice_kernel,
 // qgemm_split_kernel, qkv_split_kernel), qgemm_wide_kernel for tall unsplit weights, or
-// qgemm_small_kernel, which converts its activations itself.  In every MFMA a lane of a 16-row tile owns one weight row (l % 16) for the A
+// qgemm_small_kernel, which converts its activations itself.  In every MFMA a lane of a 16-row tile
+// owns one weight row (l % 16) for the A
 // operand and one activation row (l % 16) for the B operand, both with the K slots 8 (l / 16) .. + 7
 // of the block (weights 8 lg .. 8 lg + 7); the accumulator lane holds weight rows 4 (l / 16) .. + 3
 // (one packed row-quad, whose four fp16 scales are one 8-byte word) of activation row l % 16.
@@ -1198,8 +1199,9 @@ __global__ __launch_bounds__(256, QDT == VGX_Q8_0 || KDT == VGX_Q8_0 ? 2 : 3) vo
 
 // ---------------------------------------------------------------------------------------------
 // Decode batches, K-split Q4_0 projections of 16-block splits: qgemm_kslice_kernel.  A workgroup owns
-// the tile of qgemm_split_kernel (128 weight rows x 16 activation rows x a K range of 16 blocks), but
-// each of its 4 waves takes one 4-block slice of the range for all 128 rows, so the activations never
+// the tile of qgemm_split_kernel (128 weight rows, or 64 for projections of few rows such as o and down
+// (RQT = 16), x 16 activation rows x a K range of 16 blocks), but each of its 4 waves takes one 4-block
+// slice of the range for all the tile's rows, so the activations never
 // pass through LDS (against qgemm_split_kernel, gate/up of the 1.5B model at batch 32 measured 17.0 ->
 // 15.1 us per launch, down 11.0 -> 9.5 us):
 //  * Activations: lane (row l16, K group lg) loads its 8 values of each block of the slice (K slots
