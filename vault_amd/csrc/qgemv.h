@@ -571,8 +571,11 @@ struct StreamGeom {
     static constexpr int RQB = kStreamBlocks * 4 * QB;   // bytes of one row-quad's quants
     static constexpr int NL = RQB / 1024;                // 16-byte loads per lane per row-quad
     static constexpr int XL = 96 / NL;                   // activations per lane per load
-    static constexpr int RB = DT == VGX_Q8_0 ? 3 : 4;    // row-quads in flight per wave
-    static constexpr int GROUPS = 512;                    // 2 waves per SIMD (200-212 VGPRs)
+    // row-quads in flight per wave and workgroups: Q8_0 2 and 768 (3 waves per SIMD), Q4_0 3 and 512 (2 per
+    // SIMD); measured against 3 / 512 and 4 / 512: LM head Q8_0 43.1 vs 43.6 us, Q4_0 25.6 vs 28.2 us, gate/up
+    // 6.69 vs 6.93 us (Q4_0 4 / 768, 6 / 512 and 2 / 768 measured slower)
+    static constexpr int RB = DT == VGX_Q8_0 ? 2 : 3;
+    static constexpr int GROUPS = DT == VGX_Q8_0 ? 768 : 512;
 };
 
 template <int DT>
