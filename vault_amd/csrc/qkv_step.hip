@@ -163,34 +163,35 @@ __global__ __launch_bounds__(64) void qkv_rope_step_kernel(QkvStepArgs a) {
     qkv_epilogue<KV>(a, wg, lane, acc);
 }
 
-// Q8_0 / Q4_0 weights of rows up to 64 blocks (d_model <= 2048): a workgroup of 4 waves per row-quad.
+// Q8_0 / Q4_0 weights of rows up to 64 blocks (d_model <= 2048): a workgroup of NW waves per row-quad.
 // The row-quad's run is cut into 1 KB pieces (Q4_0: 16 blocks x 4 rows, lane l row l & 3 of block
 // 16 p + l / 4; Q8_0: 8 blocks x 4 rows, lane l half l & 1 of row (l >> 1) & 3 of block 8 p + l / 8),
-// one 16-byte buffer load per lane and piece, wave w taking pieces w and w + 4; every load instruction
+// one 16-byte buffer load per lane and piece, wave w taking pieces w, w + NW, ...; every load instruction
 // reads one contiguous 1 KB range.  The workgroup stages lnw * x once in LDS (blocks padded to 36
 // floats against bank conflicts, Q4_0 block sums for the -8 offset) with sum x^2 for the RMSNorm
-// scale; the lanes of a row and then the 4 waves are summed in a fixed order, and wave 0 runs the
+// scale; the lanes of a row and then the waves are summed in a fixed order, and wave 0 runs the
 // epilogue.
 constexpr int kQkvPiecesMaxBlocks = 64;
 
 // the row-quad's dot products, summed over the workgroup: every lane of wave 0 gets rows 0..3
-template <int DT>
+template <int DT, int NW>
 __device__ __forceinline__ void qkv_pieces_rq(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq, int64_t rq,
                                               int nblk, const float *xs, const float *xsum, float (*red)[4],
                                               int wave, int lane) {
     constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
     constexpr int BPP = 1024 / (4 * QB);               // blocks per piece
+    constexpr int MAXI = (kQkvPiecesMaxBlocks / BPP + NW - 1) / NW;   // pieces per wave
     const int npc = (nblk + BPP - 1) / BPP;
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc((void *)W, 0, (int)soff, 0x00020000);
     const __amdgpu_buffer_rsrc_t srs =
         __builtin_amdgcn_make_buffer_rsrc((void *)(W + soff), 0, (int)(n_rq * nblk * 8), 0x00020000);
     const int row = DT == VGX_Q8_0 ? (lane >> 1) & 3 : lane & 3;
-    uint4 wq[2];
-    uint32_t wsc[2];
-    int blk_of[2];
+    uint4 wq[MAXI];
+    uint32_t wsc[MAXI];
+    int blk_of[MAXI];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int pc = wave + 4 * k;
+    for (int k = 0; k < MAXI; ++k) {
+        const int pc = wave + NW * k;
         const int blk = BPP * pc + (DT == VGX_Q8_0 ? lane >> 3 : lane >> 2);
         const bool ok = pc < npc && blk < nblk;
         blk_of[k] = min(blk, nblk - 1);
@@ -204,8 +205,8 @@ __device__ __forceinline__ void qkv_pieces_rq(const uint8_t *__restrict__ W, int
     __syncthreads();                                   // the activations are staged
     float acc = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 2; ++k)
-        if (wave + 4 * k < npc) acc += gemv_piece_dot<DT>(wq[k], wsc[k], xs, xsum, blk_of[k], lane);
+    for (int k = 0; k < MAXI; ++k)
+        if (wave + NW * k < npc) acc += gemv_piece_dot<DT>(wq[k], wsc[k], xs, xsum, blk_of[k], lane);
     if constexpr (DT == VGX_Q8_0) {
         acc += dpp_f<DPP_QUAD_1032>(acc);             // lane ^ 1: the other half of the row
         acc += dpp_f<0x128>(acc);                     // row_ror 8: lane ^ 8
@@ -218,30 +219,32 @@ __device__ __forceinline__ void qkv_pieces_rq(const uint8_t *__restrict__ W, int
     __syncthreads();
 }
 
-template <int DTQ, int DTKV, int KV>
-__global__ __launch_bounds__(256) void qkv_rope_step_pieces_kernel(QkvStepArgs a) {
+template <int DTQ, int DTKV, int KV, int NW>
+__global__ __launch_bounds__(64 * NW) void qkv_rope_step_pieces_kernel(QkvStepArgs a) {
+    constexpr int NT = 64 * NW;
+    constexpr int XR = (kQkvPiecesMaxBlocks * 8 + NT - 1) / NT;   // staging rounds of one float4 per thread
     __shared__ __align__(16) float xs[kQkvPiecesMaxBlocks * kGemvPad];
     __shared__ float xsum[kQkvPiecesMaxBlocks];
-    __shared__ float red[4][4];
-    __shared__ float rss[4];
+    __shared__ float red[NW][4];
+    __shared__ float rss[NW];
     const int qpd = a.D / 4;
     const int64_t nq = (int64_t)a.H * qpd;
     const int64_t wg = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nblk = a.nblk, n4 = nblk * 8;
-    // lnw * x staged (two float4 per thread cover 64 blocks), sum x^2, Q4_0 block sums
-    float4 xv[2], gv[2];
+    // lnw * x staged (XR float4 per thread cover 64 blocks), sum x^2, Q4_0 block sums
+    float4 xv[XR], gv[XR];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int i = tid + 256 * u;
+    for (int u = 0; u < XR; ++u) {
+        const int i = tid + NT * u;
         xv[u] = i < n4 ? reinterpret_cast<const float4 *>(a.x)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         gv[u] = a.lnw && i < n4 ? reinterpret_cast<const float4 *>(a.lnw)[i] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
     float ssq = 0.0f;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int i = tid + 256 * u;
+    for (int u = 0; u < XR; ++u) {
+        const int i = tid + NT * u;
         float4 t = xv[u];
         if (i < n4 && wg == 0 && a.x_copy) reinterpret_cast<float4 *>(a.x_copy)[i] = t;
         ssq += fmaf(t.x, t.x, fmaf(t.y, t.y, fmaf(t.z, t.z, t.w * t.w)));
@@ -255,14 +258,22 @@ __global__ __launch_bounds__(256) void qkv_rope_step_pieces_kernel(QkvStepArgs a
     }
     ssq = wave_sum(ssq);
     if (lane == 0) rss[wave] = ssq;
-    if (wg < nq) qkv_pieces_rq<DTQ>(a.wq, a.soff_q, nq, wg, nblk, xs, xsum, red, wave, lane);
-    else qkv_pieces_rq<DTKV>(a.wkv, a.soff_kv, (int64_t)2 * a.G * qpd, wg - nq, nblk, xs, xsum, red, wave, lane);
+    if (wg < nq) qkv_pieces_rq<DTQ, NW>(a.wq, a.soff_q, nq, wg, nblk, xs, xsum, red, wave, lane);
+    else qkv_pieces_rq<DTKV, NW>(a.wkv, a.soff_kv, (int64_t)2 * a.G * qpd, wg - nq, nblk, xs, xsum, red, wave, lane);
     if (wave != 0) return;
     float acc[4][1];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r][0] = (red[0][r] + red[1][r]) + (red[2][r] + red[3][r]);
+    for (int r = 0; r < 4; ++r) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red[w][r];
+        acc[r][0] = v;
+    }
     if (a.lnw) {
-        const float inv = 1.0f / sqrtf(((rss[0] + rss[1]) + (rss[2] + rss[3])) / (float)(nblk * QK) + a.eps);
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) t += rss[w];
+        const float inv = 1.0f / sqrtf(t / (float)(nblk * QK) + a.eps);
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[r][0] *= inv;
     }
@@ -274,8 +285,11 @@ void launch(int kv, const QkvStepArgs &a, unsigned grid, hipStream_t st) {
     const bool pieces = DTQ != VGX_F32 && a.nblk <= kQkvPiecesMaxBlocks && a.soff_q < ((int64_t)1 << 31) &&
                         a.soff_kv < ((int64_t)1 << 31);
     if (pieces) {
-        if (kv == VGX_F32) hipLaunchKernelGGL((qkv_rope_step_pieces_kernel<DTQ, DTKV, VGX_F32>), dim3(grid), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((qkv_rope_step_pieces_kernel<DTQ, DTKV, VGX_BF16>), dim3(grid), dim3(256), 0, st, a);
+        // 8 waves per row-quad (the staging spread over 512 threads; pieces w and w + 8): decode step 1002
+        // against 996 tok/s with 4 waves (2: 982, 3: 990, 6: 997)
+        constexpr int NW = 8;
+        if (kv == VGX_F32) hipLaunchKernelGGL((qkv_rope_step_pieces_kernel<DTQ, DTKV, VGX_F32, NW>), dim3(grid), dim3(64 * NW), 0, st, a);
+        else hipLaunchKernelGGL((qkv_rope_step_pieces_kernel<DTQ, DTKV, VGX_BF16, NW>), dim3(grid), dim3(64 * NW), 0, st, a);
         return;
     }
     if (kv == VGX_F32) hipLaunchKernelGGL((qkv_rope_step_kernel<DTQ, DTKV, VGX_F32>), dim3(grid), dim3(64), 0, st, a);
