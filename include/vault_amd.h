@@ -37,7 +37,8 @@ enum {
     VGX_E_LIMIT = -10, /* V3_E_LIMIT: exceeds a compiled limit */
     VGX_E_ALIGN = -11, /* V3_E_ALIGN: pointer not aligned as required */
     VGX_E_ARG = -31,   /* null pointer or invalid flag */
-    VGX_E_HIP = -32    /* a HIP launch failed */
+    VGX_E_HIP = -32,   /* a HIP launch failed */
+    VGX_E_STATE = -33  /* not allowed in the caller's current state (see the entry point) */
 };
 
 enum { VGX_F32 = 0, VGX_F16 = 1, VGX_BF16 = 2, VGX_Q8_0 = 8, VGX_Q4_0 = 9 };
@@ -201,7 +202,9 @@ int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span
  * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
  * the reference.  Same arguments, results and kernels as vgx_attn_decode; the split partials and
  * tickets live in a fixed 2 MiB device array of the library, one per GPU, held until the process
- * ends (located, and its tickets cleared, by the first call on each device).  Calls that would need
+ * ends (located, and its tickets cleared by a fill kernel, by the first call on each device; that first
+ * call must not be made while the stream is being captured into a graph, which would record the fill
+ * instead of running it: it then returns VGX_E_STATE and records nothing).  Calls that would need
  * more than 2 MiB of workspace (vgx_attn_decode_workspace_bytes) return VGX_E_LIMIT: at 12 / 2 heads
  * and D = 128 that admits every batch up to 64 at 3584 keys (1.6 MB at most).  Every call on one GPU uses that GPU's
  * array, so calls that overlap in time on one GPU (other streams, other threads) race; the array

@@ -20,13 +20,15 @@ from typing import Dict, List, Optional
 
 import numpy as np
 
+from . import cmath
 from . import rope as orope
 from . import tokens as otok
 
 
-def _gelu_erf(x):
-    from scipy.special import erf
-    return 0.5 * x * (1.0 + erf(x / math.sqrt(2.0)))
+def _gelu_c(x):
+    """The C runtime's scorer GELU (runtime/vault3.c:118-129, 974: A&S 7.1.26 erf, fp32), which the
+    segment scores follow; src/vault_v3_model.py:882 uses the exact erf (within 1.5e-7 of it)."""
+    return cmath.geluf(np.asarray(x, dtype=np.float32)).astype(np.float64)
 
 
 @dataclass
@@ -146,7 +148,7 @@ class OracleModel:
         mu = f.mean()
         var = ((f - mu) ** 2).mean()
         h = (f - mu) / np.sqrt(var + 1e-5) * w["seg_scorer.ln.weight"] + w["seg_scorer.ln.bias"]
-        h = _gelu_erf(w["seg_scorer.fc1.weight"] @ h + w["seg_scorer.fc1.bias"])
+        h = _gelu_c(w["seg_scorer.fc1.weight"] @ h + w["seg_scorer.fc1.bias"])
         return float(w["seg_scorer.fc2.weight"].reshape(-1) @ h + w["seg_scorer.fc2.bias"][0])
 
     def _auto_pin(self, st: OState, tid: int) -> None:

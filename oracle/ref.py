@@ -79,6 +79,10 @@ def _load():
         lib.ref_res_update.restype = C.c_int
         lib.ref_spoof.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint64, C.c_uint32]
         lib.ref_spoof.restype = C.c_int
+        lib.ref_math.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_uint64]
+        lib.ref_seg_update.argtypes = [C.c_void_p, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32] + \
+            [C.c_void_p] * 3 + [C.c_uint32] + [C.c_void_p] * 9
+        lib.ref_seg_update.restype = C.c_int
         _lib = lib
     return _lib
 
@@ -198,6 +202,29 @@ class RefRuntime:
             lib.ref_state_field(self._h, layer, f, out.ctypes.data)
         return out
 
+    def seg_update(self, ev: int, n_pin: int, offset: int, budget: int, sc, seg, tok, mem_pos, mem_score, mem_tok,
+                   mem_seg):
+        """update_segment_bank on constructed rings and bank: ((pos, score, tok, seg) of the new bank,
+        new seg-id offset)."""
+        sc = np.ascontiguousarray(sc, dtype=np.float32)
+        seg = np.ascontiguousarray(seg, dtype=np.uint32)
+        tok = np.ascontiguousarray(tok, dtype=np.uint32)
+        m = len(mem_pos)
+        ip = np.zeros(max(1, m), np.uint64)
+        isc = np.zeros(max(1, m), np.float32)
+        it = np.zeros(max(1, m), np.uint32)
+        ig = np.zeros(max(1, m), np.uint32)
+        ip[:m], isc[:m], it[:m], ig[:m] = mem_pos, mem_score, mem_tok, mem_seg
+        n = max(1, budget)
+        op, osc, ot, og = np.zeros(n, np.uint64), np.zeros(n, np.float32), np.zeros(n, np.uint32), np.zeros(n, np.uint32)
+        off = C.c_uint32()
+        k = _load().ref_seg_update(self._h, ev, n_pin, offset, budget, sc.ctypes.data, seg.ctypes.data,
+                                   tok.ctypes.data, m, ip.ctypes.data, isc.ctypes.data, it.ctypes.data, ig.ctypes.data,
+                                   op.ctypes.data, osc.ctypes.data, ot.ctypes.data, og.ctypes.data, C.byref(off))
+        if k < 0:
+            raise RuntimeError("budget beyond the state's segment capacity")
+        return (op[:k].astype(np.int64), osc[:k], ot[:k].astype(np.int64), og[:k].astype(np.int64)), off.value
+
     def seed_long_context(self, pos: int, n_pin: int, mem_cnt: int, seed: int = 0) -> None:
         rc = _load().ref_seed_long_context(self._h, pos, n_pin, mem_cnt, seed)
         if rc:
@@ -236,6 +263,14 @@ def argmax(logits: np.ndarray) -> int:
     """The reference's v3_argmax (runtime/vault3.c:3198-3202) on one fp32 row."""
     a = np.ascontiguousarray(logits, dtype=np.float32)
     return int(_load().v3_argmax(a.ctypes.data, a.size))
+
+
+def math(fn: str, x: np.ndarray) -> np.ndarray:
+    """The reference's own v3_expf / v3_erff / v3_geluf (runtime/vault3.c:104-129), element-wise."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(a)
+    _load().ref_math(("exp", "erf", "gelu").index(fn), a.ctypes.data, out.ctypes.data, a.size)
+    return out
 
 
 def sample_topk(logits: np.ndarray, k: int, temp: float, state: int):

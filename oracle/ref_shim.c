@@ -354,3 +354,47 @@ int ref_spoof(ref_ctx *c, const uint32_t *tok_prev, const uint32_t *tok_cur, uin
     s->n_pin = n_pin;
     return check_spoof_quarantine(s, pos, ci);
 }
+
+/* The runtime's own v3_expf (fn 0), v3_erff (fn 1) and v3_geluf (fn 2) (runtime/vault3.c:104-129),
+ * element-wise. */
+void ref_math(int fn, const float *x, float *y, uint64_t n) {
+    for (uint64_t i = 0; i < n; i++) y[i] = fn == 0 ? v3_expf(x[i]) : fn == 1 ? v3_erff(x[i]) : v3_geluf(x[i]);
+}
+
+/* One update_segment_bank (runtime/vault3.c:1833-1915) on given evicted-chunk rings (W slots: scores,
+ * local segment ids, tokens) and a given bank of mem_cnt slots, with the segment budget, pin count
+ * and seg-id offset set first.  Returns the new mem_cnt (or -1 if the budget exceeds the state's
+ * capacity) and copies the new bank and seg-id offset out.  The quarantine that v3_step applies before
+ * the call (:2079-2088) is not part of this function: callers pass scores it leaves unchanged. */
+int ref_seg_update(ref_ctx *c, uint64_t ev_chunk_idx, uint32_t n_pin, uint32_t seg_id_offset, uint32_t budget,
+                   const float *sc_prev, const uint32_t *seg_prev, const uint32_t *tok_prev, uint32_t mem_cnt,
+                   const uint64_t *mem_pos, const float *mem_score, const uint32_t *mem_tok, const uint32_t *mem_seg,
+                   uint64_t *o_pos, float *o_score, uint32_t *o_tok, uint32_t *o_seg, uint32_t *o_offset) {
+    v3_state *s = &c->s;
+    uint32_t W = c->m.window;
+    if (budget > s->seg_cap || mem_cnt > budget) return -1;
+    s->seg_budget = budget;
+    s->n_pin = n_pin;
+    s->seg_id_offset = seg_id_offset;
+    for (uint32_t t = 0; t < W; t++) {
+        s->sc_prev[t] = sc_prev[t];
+        s->seg_prev[t] = seg_prev[t];
+        s->tok_prev[t] = tok_prev[t];
+    }
+    for (uint32_t i = 0; i < mem_cnt; i++) {
+        s->mem_pos[i] = mem_pos[i];
+        s->mem_score[i] = mem_score[i];
+        s->mem_tok[i] = mem_tok[i];
+        s->mem_seg[i] = mem_seg[i];
+    }
+    s->mem_cnt = mem_cnt;
+    update_segment_bank(s, ev_chunk_idx);
+    for (uint32_t i = 0; i < s->mem_cnt; i++) {
+        o_pos[i] = s->mem_pos[i];
+        o_score[i] = s->mem_score[i];
+        o_tok[i] = s->mem_tok[i];
+        o_seg[i] = s->mem_seg[i];
+    }
+    *o_offset = s->seg_id_offset;
+    return (int)s->mem_cnt;
+}

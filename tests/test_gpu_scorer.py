@@ -45,3 +45,28 @@ def test_ema_habituate_matches_recurrence(dev, T, first):
     if got_h[rows].size:
         assert np.abs(got_h[rows] - want_h[rows]).max() <= tol
     assert np.abs(ema.double().cpu().numpy() - want_e).max() <= tol
+
+
+@pytest.mark.skipif(not __import__("oracle.ref", fromlist=["ref"]).available(), reason="oracle/_ref not built")
+def test_score_tail_gelu_is_the_runtimes(dev):
+    """The scorer tail's GELU is the C runtime's v3_geluf (runtime/vault3.c:118-129, 974) bit for bit.
+    With fc2 = e_0 and b2 = 0 the tail's score of token t is exactly gelu(h[t, 0]) (every other term
+    adds zero, and the habituated row equals the raw one, so the combine adds zero): 2^20 inputs over
+    the range the hidden units take, the erf clamp at |x / sqrt 2| = 4 and both signs."""
+    from oracle import ref
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.uniform(-8, 8, 1 << 19), rng.standard_normal(1 << 18) * 2,
+                        np.linspace(5.6, 5.72, 1 << 17), -np.linspace(5.6, 5.72, 1 << 17)]).astype(np.float32)
+    T, hidden = x.size, 64
+    h = torch.zeros((2 * T, hidden), dtype=torch.float32, device=dev)
+    xt = torch.from_numpy(x).to(dev)
+    h[:T, 0] = xt
+    h[T:, 0] = xt
+    w2 = torch.zeros(hidden, dtype=torch.float32, device=dev)
+    w2[0] = 1.0
+    b2 = torch.zeros(1, dtype=torch.float32, device=dev)
+    out = torch.empty(T, dtype=torch.float32, device=dev)
+    ops.seg_score_tail(h, w2, b2, T, False, out)
+    got = out.cpu().numpy()
+    want = ref.math("gelu", x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

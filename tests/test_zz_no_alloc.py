@@ -74,3 +74,76 @@ def test_noalloc_rejects_beyond_its_scratch(dev):
     out = torch.zeros(B, H, D, device=dev)
     rc = _call(lib, "vgx_attn_decode_noalloc", L.BF16, q, [(k, k)], out, None, -1, None)
     assert rc == -10   # VGX_E_LIMIT
+
+
+def _graph_case(dev, gen):
+    H, G, D, B = 12, 2, 128, 1
+    spans = _spans(B, G, D, [512, 1024, 1024, 1024], torch.float32, dev, gen)
+    q = torch.randn(B, H, D, generator=gen).to(dev)
+    return q, spans
+
+
+def test_noalloc_inside_graph_capture_replays_exactly(dev):
+    """A captured noalloc call (after the device's set-up call outside capture) replayed three times,
+    with eager work on the same data between the replays, equals vgx_attn_decode each time."""
+    lib = L.load()
+    gen = torch.Generator().manual_seed(11)
+    q, spans = _graph_case(dev, gen)
+    B, H, D = q.shape
+    need = int(lib.vgx_attn_decode_workspace_bytes(B, H, 2, D, 3584))
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    ref_out = torch.empty_like(q)
+    out = torch.full_like(q, float("nan"))
+    assert _call(lib, "vgx_attn_decode_noalloc", L.F32, q, spans, out, None, -1, None) == 0   # set-up, eager
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            rc = _call(lib, "vgx_attn_decode_noalloc", L.F32, q, spans, out, None, -1, None)
+    assert rc == 0
+    for i in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen).to(dev))
+        out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert _call(lib, "vgx_attn_decode", L.F32, q, spans, ref_out, None, -1, ws) == 0
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all() and torch.equal(out, ref_out), i
+
+
+_FRESH = r"""
+import json, sys, torch
+sys.path.insert(0, sys.argv[1])
+from tests.test_zz_no_alloc import _call, _graph_case
+from vault_amd import _lib as L
+lib = L.load()
+dev = torch.device("cuda:0")
+q, spans = _graph_case(dev, torch.Generator().manual_seed(12))
+out = torch.zeros_like(q)
+g = torch.cuda.CUDAGraph()
+s = torch.cuda.Stream()
+with torch.cuda.stream(s):
+    with torch.cuda.graph(g, stream=s):
+        rc_capture = _call(lib, "vgx_attn_decode_noalloc", L.F32, q, spans, out, None, -1, None)
+torch.cuda.synchronize()
+rc_eager = _call(lib, "vgx_attn_decode_noalloc", L.F32, q, spans, out, None, -1, None)
+torch.cuda.synchronize()
+print(json.dumps({"capture": rc_capture, "eager": rc_eager, "finite": bool(torch.isfinite(out).all())}))
+"""
+
+
+def test_noalloc_first_call_inside_capture_is_refused():
+    """In a fresh process the device's first noalloc call made inside a stream capture returns
+    VGX_E_STATE (its set-up would launch a fill kernel that the capture records instead of running);
+    the next call, outside capture, sets the device up and computes."""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("fresh-process noalloc capture case", flush=True)
+    r = subprocess.run([sys.executable, "-c", _FRESH, root], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res == {"capture": -33, "eager": 0, "finite": True}

@@ -15,7 +15,7 @@ HEADER = os.path.join(HERE, "..", "include", "vault_amd.h")
 VGX_OK = 0
 ERRORS = {
     -1: "VGX_E_SIZE", -5: "VGX_E_DTYPE", -7: "VGX_E_SHAPE", -8: "VGX_E_ARENA", -10: "VGX_E_LIMIT",
-    -11: "VGX_E_ALIGN", -31: "VGX_E_ARG", -32: "VGX_E_HIP",
+    -11: "VGX_E_ALIGN", -31: "VGX_E_ARG", -32: "VGX_E_HIP", -33: "VGX_E_STATE",
 }
 
 F32, F16, BF16, Q8_0, Q4_0 = 0, 1, 2, 8, 9

@@ -880,7 +880,7 @@ int attn_decode_impl(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_spa
 // partials, as in a caller's workspace), never allocated at run time.  Host code uses only the
 // per-device address that hipGetSymbolAddress returns for it (the array's name is a host-side
 // stand-in, not a device address).  The address is looked up, and the ticket region cleared, once
-// per device by the first call on that device.
+// per device by the first call on that device, which must come outside any stream capture.
 constexpr int64_t kScratchBytes = 2ll << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
@@ -899,6 +899,10 @@ int device_scratch(hipStream_t st, void **out) {
     if (dev >= kMaxDevices) return VGX_E_LIMIT;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     if (!g_scratch[dev]) {
+        // the set-up launches a fill kernel, which a stream capture would record instead of running
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess) return VGX_E_HIP;
+        if (cs != hipStreamCaptureStatusNone) return VGX_E_STATE;
         void *p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return VGX_E_HIP;
         // the tickets must start at zero (every call leaves them so); a fill kernel, ordered before the

@@ -128,6 +128,47 @@ VGX_DEV void split_bf16_f16x2(float a, float b, uint32_t &hi, uint32_t &lo16, fl
     r[1] = fmaf((float)l[1], 0.0625f, hb);
 }
 
+// The reference runtime's own exp / erf / GELU (runtime/vault3.c:104-129), step for step, so that
+// results that select indices (the top-k draw, the segment scores that rank the bank) are the
+// runtime's bit for bit.  The runtime is C compiled in a standard mode, which does not contract a * b
+// + c into an FMA; contraction is switched off here for the same reason.  exp: range reduction by a
+// two-piece ln 2, a degree-7 Taylor polynomial in Horner form, scaling by an exponent built in the
+// bits (two steps below 2^-126, so subnormal results round as the runtime's do).  erf: Abramowitz &
+// Stegun 7.1.26 (|error| <= 1.5e-7).
+VGX_DEV float bits_f(uint32_t u) { return __uint_as_float(u); }
+
+VGX_DEV float ref_expf(float x) {
+#pragma clang fp contract(off)
+    if (x > 88.72f) return bits_f(0x7F800000u);
+    if (x < -103.9f) return 0.0f;
+    const float kf = x * 1.44269504088896341f;
+    const int k = (int)(kf + (kf >= 0.0f ? 0.5f : -0.5f));
+    const float r = (x - (float)k * 0.693145751953125f) - (float)k * 1.428606765330187e-06f;
+    const float p =
+        1.0f + r * (1.0f + r * (0.5f + r * (1.6666667e-1f + r * (4.1666668e-2f + r * (8.3333338e-3f +
+                                                                                     r * (1.3888889e-3f +
+                                                                                          r * 1.9841270e-4f))))));
+    if (k > 127) return p * bits_f(254u << 23) * 2.0f;
+    if (k < -126) return p * bits_f((uint32_t)(k + 126 + 127) << 23) * bits_f(1u << 23);
+    return p * bits_f((uint32_t)(k + 127) << 23);
+}
+
+VGX_DEV float ref_erff(float x) {
+#pragma clang fp contract(off)
+    const float z = x < 0.0f ? -x : x;
+    if (z > 4.0f) return x < 0.0f ? -1.0f : 1.0f;
+    const float t = 1.0f / (1.0f + 0.3275911f * z);
+    const float p = (((((1.061405429f * t - 1.453152027f) * t) + 1.421413741f) * t - 0.284496736f) * t +
+                     0.254829592f) * t;
+    const float y = 1.0f - p * ref_expf(-z * z);
+    return x < 0.0f ? -y : y;
+}
+
+VGX_DEV float ref_geluf(float x) {
+#pragma clang fp contract(off)
+    return 0.5f * x * (1.0f + ref_erff(x * 0.70710678118654752f));
+}
+
 // One element of a KV-state tensor of dtype KV (VGX_F32, or VGX_BF16 rounded to nearest even).
 template <int KV>
 VGX_DEV void store_kv(void *base, int64_t idx, float v) {

@@ -1,7 +1,8 @@
 // Next-token selection on the device: argmax and top-k sampling over the logits rows, so that a decode
 // loop can feed one step's choice to the next step without reading the logits on the host.
 //
-// Reference semantics: v3_argmax and v3_sample_topk (runtime/vault3.c:3198-3230).
+// Reference semantics: v3_argmax and v3_sample_topk (runtime/vault3.c:3198-3230); the candidate
+// weights use the runtime's own exp arithmetic (ref_expf), so draws select the runtime's index.
 //
 // Ordering.  A logit l at index i gets the 64-bit key (ord(l) << 32) | (2^32 - 1 - i), ord the
 // order-preserving map of the fp32 bits, so that larger keys are larger logits and, among equal
@@ -119,7 +120,7 @@ __global__ __launch_bounds__(kThreads) void topk_draw_kernel(const uint64_t *__r
     const float top = value_of(s[0]);
     float p[kMaxK], sum = 0.0f;
     for (int j = 0; j < cnt; ++j) {
-        p[j] = expf((value_of(s[j]) - top) / temp);
+        p[j] = ref_expf((value_of(s[j]) - top) / temp);
         sum += p[j];
     }
     uint64_t xs = rng[b] ? rng[b] : 0x9E3779B97F4A7C15ull;

@@ -2,8 +2,10 @@
 // and the GELU . fc2 tail with the habituated-score combine.
 //
 // Reference semantics: src/vault_v3_model.py:870-883 (SegmentScorer: LayerNorm eps 1e-5 ->
-// Linear -> exact-erf GELU -> Linear), :1224-1247 (_score_chunk_habituated) and :2294-2305 (step);
-// runtime/vault3.c:961-977, 2201-2216.  Per token t with features f_t and EMA state e:
+// Linear -> GELU -> Linear), :1224-1247 (_score_chunk_habituated) and :2294-2305 (step);
+// runtime/vault3.c:961-977, 2201-2216.  The GELU is the C runtime's (v3_geluf, A&S 7.1.26 erf,
+// runtime/vault3.c:118-129, 974: ref_geluf), bit for bit; the Python model's exact erf is within
+// 1.5e-7 of it.  Per token t with features f_t and EMA state e:
 //   hab_in_t = f_t - 0.65 e_{t-1};  e_t = 0.985 e_{t-1} + 0.015 f_t   (e_0 = f_0 on the first token)
 //   score_t  = raw_t + 0.35 max(0, hab_t - raw_t)                     (score_0 = raw_0 on the first)
 // The fc1 GEMV between LayerNorm and the tail runs through vgx_qlinear (F32 weights).
@@ -132,8 +134,8 @@ __global__ __launch_bounds__(64) void score_tail_kernel(const float *__restrict_
     float r = 0.0f, a = 0.0f;
     for (int64_t i = threadIdx.x; i < hidden; i += 64) {
         const float x0 = h[t * ldh + i], x1 = h[(T + t) * ldh + i];
-        r = fmaf(0.5f * x0 * (1.0f + erff(x0 * 0.70710678118654752f)), w2[i], r);
-        a = fmaf(0.5f * x1 * (1.0f + erff(x1 * 0.70710678118654752f)), w2[i], a);
+        r = fmaf(ref_geluf(x0), w2[i], r);
+        a = fmaf(ref_geluf(x1), w2[i], a);
     }
     r = wave_sum(r) + b2[0];
     a = wave_sum(a) + b2[0];
