@@ -1,4 +1,4 @@
-"""Q8_0 / Q4_0 block codec restated in numpy (TEST INFRASTRUCTURE ONLY).
+"""Q8_0 / Q4_0 block codec (and the BF16 / F16 element decode) restated in numpy (TEST INFRASTRUCTURE ONLY).
 
 Block layouts (little endian), tools/vlt3.py:98-99 and docs/VAULT_v3_SPEC.md:141-142:
 
@@ -71,6 +71,12 @@ def decode(dtype: int, raw, rows: int, cols: int) -> np.ndarray:
         return q4_0_decode(raw, rows, cols)
     if dtype == F32:
         return np.frombuffer(bytes(raw), dtype="<f4").reshape(rows, cols).copy()
+    if dtype == BF16:
+        # the runtime widens by placing the 16 bits on top of a zero mantissa tail (runtime/vault3.c:517-525)
+        h = np.frombuffer(bytes(raw), dtype="<u2").astype(np.uint32) << 16
+        return h.view(np.float32).reshape(rows, cols).copy()
+    if dtype == F16:
+        return f16_bits_to_f32(np.frombuffer(bytes(raw), dtype="<u2")).reshape(rows, cols)
     raise ValueError(dtype)
 
 

@@ -13,7 +13,7 @@ from vault_amd.config import VAULTv3Config
 from vault_amd.tokens import build_vtok
 from vault_amd.weights import quantize_state, random_state
 
-FMT_TAG = {"f32": vlt3.F32, "q8_0": vlt3.Q8_0, "q4_0": vlt3.Q4_0}
+FMT_TAG = {"f32": vlt3.F32, "bf16": vlt3.BF16, "q8_0": vlt3.Q8_0, "q4_0": vlt3.Q4_0}
 
 
 def tiny_cfg(head_dim=64, n_layers=2, window=16, seg_budget=12, vocab=2048, n_heads=4, n_kv_heads=2,

@@ -34,7 +34,7 @@ def _rel(a, b):
     return float(np.abs(a - b).max() / np.abs(b).max())
 
 
-@pytest.mark.parametrize("fmt", ["f32", "q8_0", "q4_0"])
+@pytest.mark.parametrize("fmt", ["f32", "bf16", "q8_0", "q4_0"])
 @pytest.mark.parametrize("head_dim", [64, 128])
 def test_step_stream_matches_oracle(dev, fmt, head_dim):
     cfg = modelgen.tiny_cfg(head_dim=head_dim)
@@ -82,14 +82,14 @@ def test_forward_and_prefill_consistency(dev):
         assert max(errs) < 1e-4 * max(1.0, np.abs(ref_f).max()), (split, max(errs))
 
 
-@pytest.mark.parametrize("batch,fmt", [(2, "q4_0"), (9, "q4_0"), (9, "q8_0")])
+@pytest.mark.parametrize("batch,fmt", [(2, "q4_0"), (9, "q4_0"), (9, "q8_0"), (9, "bf16")])
 def test_batched_swa_stream(dev, batch, fmt):
     """A batch without segment memory: each row equals its own batch-1 stream (SWA + sinks).  Batch 9
     runs the small-batch GEMM, with the q/k/v K-split sums taken by the RoPE launch."""
     cfg = modelgen.tiny_cfg(seg_budget=0)
     tensors, _, deq = modelgen.build(cfg, fmt, seed=2)
     m = _gpu_model(cfg, tensors, dev)
-    assert m._batch_qkv_fusable(batch) == (batch >= 8)
+    assert m._batch_qkv_fusable(batch) == (batch >= 8 and fmt != "bf16")
     ids = torch.tensor([modelgen.ids_stream(cfg, 53, seed=s) for s in range(6, 6 + batch)])
     out = m.forward(ids).double().cpu().numpy()                     # (B, L, V)
     om = OracleModel(cfg, deq)
@@ -169,14 +169,15 @@ def test_bf16_prefill_mfma_consistency(dev):
 
 
 @pytest.mark.skipif(not ref.available(), reason="oracle/_ref not built")
-def test_prefill_mfma_matches_reference_runtime(dev):
+@pytest.mark.parametrize("fmt", ["q4_0", "bf16"])
+def test_prefill_mfma_matches_reference_runtime(dev, fmt):
     """Chunk-recurrent prefill on the MFMA attention at head_dim 128 with 12 query / 2 KV heads (the
     real head layout) and fp32 state (K / V as three bf16 pieces), then the step stream, against the
     reference C runtime stepping the same ids with segment memory on: rel < 1e-4 and 100% top-1,
     segment-memory slots exactly."""
     kv = torch.float32
     cfg = modelgen.tiny_cfg(head_dim=128, n_heads=12, n_kv_heads=2, window=64, seg_budget=24, seg_layers=(0, 1))
-    tensors, image, _ = modelgen.build(cfg, "q4_0", seed=12)
+    tensors, image, _ = modelgen.build(cfg, fmt, seed=12)
     ids = modelgen.ids_stream(cfg, 230, seed=31)
     rt = ref.RefRuntime(image, threads=4)
     want = np.stack([rt.step(t).astype(np.float64) for t in ids])

@@ -1,4 +1,4 @@
-"""GPU parity of the Q8_0 / Q4_0 / F32 weight kernels against the oracle.
+"""GPU parity of the Q8_0 / Q4_0 / F32 / BF16 / F16 weight kernels against the oracle.
 
 Bars: packing round trip and dequantization bit-exact; GEMV within the fp32 accumulation bound
 ``oracle.linalg.gemv_bound`` of the fp64 oracle (a dropped term or a wrong scale is ~1e3x that
@@ -20,13 +20,15 @@ def _blocks(dt, rows, cols, seed, kind="synthetic"):
     rng = np.random.default_rng(seed)
     if dt == codec.F32:
         return rng.standard_normal((rows, cols)).astype(np.float32).tobytes()
+    if dt in (codec.BF16, codec.F16):
+        return vlt3.quantize(dt, rng.standard_normal((rows, cols)).astype(np.float32) * 0.05)
     if kind == "synthetic":
         return vlt3.synthetic_blocks(dt, rows, cols, rng)
     w = rng.standard_normal((rows, cols)).astype(np.float32) * 0.05
     return vlt3.quantize(dt, w)
 
 
-@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0, codec.F32])
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0, codec.F32, codec.BF16, codec.F16])
 @pytest.mark.parametrize("rows,cols", [(1, 32), (13, 96), (64, 1536), (1030, 8960)])
 def test_pack_unpack_dequant_bit_exact(dev, dt, rows, cols):
     raw = _blocks(dt, rows, cols, seed=rows + cols, kind="quantized")
@@ -38,7 +40,7 @@ def test_pack_unpack_dequant_bit_exact(dev, dt, rows, cols):
     assert np.array_equal(deq.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0, codec.BF16, codec.F16])
 def test_embed_rows(dev, dt):
     rows, cols = 301, 1536
     raw = _blocks(dt, rows, cols, seed=5, kind="quantized")
@@ -71,27 +73,27 @@ def _check_gemv(dev, dt, rows, cols, batch, seed, kind="synthetic", bias=False, 
     return err, tol
 
 
-@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0, codec.F32])
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0, codec.F32, codec.BF16, codec.F16])
 @pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 16])
 def test_gemv_small_ragged(dev, dt, batch):
     _check_gemv(dev, dt, 13, 96, batch, seed=11 * batch, kind="quantized")
 
 
-@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0, codec.BF16, codec.F16])
 @pytest.mark.parametrize("rows,cols", BENCH_SHAPES)
 @pytest.mark.parametrize("batch", [1, 16])
 def test_gemv_benchmark_shapes(dev, dt, rows, cols, batch):
     _check_gemv(dev, dt, rows, cols, batch, seed=rows * 3 + cols + batch)
 
 
-@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0, codec.BF16])
 @pytest.mark.parametrize("batch", [1, 16])
 def test_gemv_lm_head_shape(dev, dt, batch):
     """The tied LM head, 151665 x 1536, at batch 1 (one-row GEMV) and 16 (MFMA small-batch GEMM)."""
     _check_gemv(dev, dt, 151665, 1536, batch, seed=9 + batch)
 
 
-@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0, codec.BF16])
 @pytest.mark.parametrize("rows", [151665, 65540])
 def test_gemv_tall_fused_rmsnorm(dev, dt, rows):
     """The LM head's own call: final RMSNorm fused into the one-row GEMV over tall 1536-column weights
@@ -222,3 +224,25 @@ def test_gemv_fused_rmsnorm_equals_separate(dev, dt):
     fused = ops.qlinear(wq, x, norm=(g, 1e-6))
     sep = ops.qlinear(wq, ops.rmsnorm(x, g, 1e-6))
     assert torch.allclose(fused, sep, rtol=0, atol=1e-5 * float(sep.abs().max()))
+
+
+@pytest.mark.parametrize("dt", [codec.BF16, codec.F16])
+@pytest.mark.parametrize("batch", [1, 3, 8, 40, 200])
+def test_plain16_swiglu_and_norm(dev, dt, batch):
+    """BF16 / F16 gate/up with the fused SwiGLU, and the projections with an RMSNorm prologue, over the
+    GEMV (batch < 8) and the fp32 MFMA GEMM (batch >= 8, the norm applied by a separate launch)."""
+    rows, cols = 512, 1536
+    rng = np.random.default_rng(batch + dt)
+    rg, ru = _blocks(dt, rows, cols, 1), _blocks(dt, rows, cols, 2)
+    w = ops.QWeight.gateup_from_blocks(dt, rows, cols, rg, ru, dev)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    gamma = rng.uniform(0.8, 1.2, cols).astype(np.float32)
+    u = linalg.rmsnorm(x, gamma, 1e-6)
+    wg, wu = codec.decode(dt, rg, rows, cols), codec.decode(dt, ru, rows, cols)
+    h = ops.qlinear_swiglu(w, torch.from_numpy(x).to(dev), norm=(torch.from_numpy(gamma).to(dev), 1e-6))
+    g, up = linalg.gemv(wg, u), linalg.gemv(wu, u)
+    ref = linalg.swiglu(g, up)
+    tol = (2 * linalg.gemv_bound(wg, u, dt) * np.abs(up) + 2 * linalg.gemv_bound(wu, u, dt) * np.abs(g) +
+           np.abs(ref) * 1e-6)
+    err = np.abs(h.cpu().numpy().astype(np.float64) - ref)
+    assert np.all(err <= tol), float((err / tol).max())

@@ -95,3 +95,20 @@ def test_synthetic_blocks_ranges():
     assert q.min() >= -127 and q.max() <= 127
     d = raw8[:, :2].copy().view(np.float16).astype(np.float32)
     assert np.all(d >= 0) and np.all(d < 0.02 * 8 / 127)
+
+
+def test_bf16_f16_element_decode_known_answers():
+    """BF16: the 16 bits on top of a zero mantissa tail (runtime/vault3.c:517-525); F16: IEEE half.
+    Known answers, subnormals, and the writer's round-to-nearest-even BF16 encode against torch's cast."""
+    import torch
+    from vault_amd import vlt3
+    bits = np.array([0x3F80, 0xC000, 0x0001, 0x8000, 0x7F7F, 0x3E4C], dtype="<u2")
+    got = codec.decode(codec.BF16, bits.tobytes(), 1, 6)[0]
+    want = np.array([1.0, -2.0, 2.0 ** -133, -0.0, 3.3895313892515355e38, 0.19921875], dtype=np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    h = np.array([0x3C00, 0xC000, 0x0001, 0x7BFF, 0x3555, 0x8400], dtype="<u2")
+    got = codec.decode(codec.F16, h.tobytes(), 1, 6)[0]
+    assert np.array_equal(got, h.view(np.float16).astype(np.float32))
+    x = np.random.default_rng(0).standard_normal(4096).astype(np.float32) * 0.05
+    enc = np.frombuffer(vlt3.quantize(vlt3.BF16, x), dtype="<u2")
+    assert np.array_equal(enc, torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16))

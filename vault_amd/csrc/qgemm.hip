@@ -397,7 +397,8 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
 }
 
 // ---------------------------------------------------------------------------------------------
-// F32 weights (the segment scorer's fc1, F32 model files) for many activation rows: fp32 MFMA
+// F32 / BF16 / F16 weights (the segment scorer's fc1, F32 and BF16 model files) for many activation
+// rows, 16-bit elements widened exactly to fp32 as they are fetched: fp32 MFMA
 // (v_mfma_f32_16x16x4_f32), so products and sums stay fp32 as in the reference.  A workgroup of 4
 // waves owns 64 weight rows x 64 activation rows (each wave 32 x 32 as 2 x 2 tiles); per 32-wide
 // block of K the workgroup stages both 64 x 32 fp32 tiles in LDS (double-buffered, one barrier per
@@ -406,8 +407,8 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
 constexpr int kFT = 64;                   // rows of each operand per workgroup tile
 constexpr int kFRow = QK + 1;             // floats per staged row (one float of padding)
 
-template <int EPI, bool VEC>
-__global__ __launch_bounds__(256) void f32gemm_tile_kernel(const float *__restrict__ W, int64_t n_rq, int nblk,
+template <int WDT, int EPI, bool VEC>
+__global__ __launch_bounds__(256) void f32gemm_tile_kernel(const void *__restrict__ W, int64_t n_rq, int nblk,
                                                            int64_t rows_out, const float *__restrict__ x,
                                                            int64_t ldx, int64_t batch, const float *__restrict__ bias,
                                                            float *__restrict__ y, int64_t ldy) {
@@ -426,8 +427,21 @@ __global__ __launch_bounds__(256) void f32gemm_tile_kernel(const float *__restri
             const int idx = tid + 256 * i;
             // weights: row-quad idx / 32, row (idx / 8) % 4, float4 idx % 8 of the block
             const int64_t rq = rq0 + (idx >> 5);
-            ra[i] = rq < n_rq ? reinterpret_cast<const float4 *>(W + ((rq * nblk + blk) * 4 + ((idx >> 3) & 3)) * QK)[idx & 7]
-                              : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const int64_t e0 = ((rq * nblk + blk) * 4 + ((idx >> 3) & 3)) * QK + (idx & 7) * 4;
+            if (rq >= n_rq) {
+                ra[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            } else if constexpr (WDT == VGX_F32) {
+                ra[i] = *reinterpret_cast<const float4 *>(static_cast<const float *>(W) + e0);
+            } else {
+                // BF16 / F16 elements widened exactly (runtime/vault3.c:510-533)
+                const uint2 h = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(W) + e0);
+                if constexpr (WDT == VGX_BF16)
+                    ra[i] = make_float4(__uint_as_float(h.x << 16), __uint_as_float(h.x & 0xFFFF0000u),
+                                        __uint_as_float(h.y << 16), __uint_as_float(h.y & 0xFFFF0000u));
+                else
+                    ra[i] = make_float4(half_bits_to_float(h.x), half_bits_to_float(h.x >> 16),
+                                        half_bits_to_float(h.y), half_bits_to_float(h.y >> 16));
+            }
             const int64_t b = b0 + (idx >> 3);
             if (b < batch) {
                 const float *xp = x + b * ldx + (int64_t)blk * QK + (idx & 7) * 4;
@@ -2139,7 +2153,8 @@ int64_t vgx_qgemm_workspace_bytes(int64_t batch, int64_t rows, int64_t cols, int
 int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx, int64_t batch,
               const float *norm_w, float eps, const float *bias, float *y, int64_t ldy, int epilogue, void *workspace,
               int64_t workspace_bytes, void *stream) {
-    if (dtype != VGX_Q8_0 && dtype != VGX_Q4_0 && dtype != VGX_F32) return VGX_E_DTYPE;
+    if (dtype != VGX_Q8_0 && dtype != VGX_Q4_0 && dtype != VGX_F32 && dtype != VGX_BF16 && dtype != VGX_F16)
+        return VGX_E_DTYPE;
     if (!w_packed || !x || !y) return VGX_E_ARG;
     if (epilogue != VGX_EPI_STORE && epilogue != VGX_EPI_ACCUM && epilogue != VGX_EPI_SWIGLU) return VGX_E_ARG;
     if (epilogue == VGX_EPI_SWIGLU && bias) return VGX_E_ARG;
@@ -2151,20 +2166,24 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     const int64_t rows_packed = epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows;
     const int nblk = (int)(cols / QK);
     const int64_t n_rq = rows4(rows_packed) / 4;
-    if (dtype == VGX_F32) {
-        if (norm_w) return VGX_E_ARG;                 // F32 weights: no fused RMSNorm on this path
-        const auto *wf = static_cast<const float *>(w_packed);
+    if (dtype == VGX_F32 || dtype == VGX_BF16 || dtype == VGX_F16) {
+        if (norm_w) return VGX_E_ARG;                 // plain weights: no fused RMSNorm on this path
+        const void *wf = w_packed;
         const dim3 grid((unsigned)((n_rq + kFT / 4 - 1) / (kFT / 4)), (unsigned)((batch + kFT - 1) / kFT));
         const bool vec = ((uintptr_t)x & 15) == 0 && ldx % 4 == 0;
         hipStream_t sf = (hipStream_t)stream;
-#define VGX_F32G(EPI, V) hipLaunchKernelGGL((f32gemm_tile_kernel<EPI, V>), grid, dim3(256), 0, sf, wf, n_rq, nblk, rows, x, ldx, batch, bias, y, ldy)
-#define VGX_F32E(V)                                                         \
+#define VGX_F32G(WDT, EPI, V) hipLaunchKernelGGL((f32gemm_tile_kernel<WDT, EPI, V>), grid, dim3(256), 0, sf, wf, n_rq, nblk, rows, x, ldx, batch, bias, y, ldy)
+#define VGX_F32E(WDT, V)                                                    \
     do {                                                                    \
-        if (epilogue == VGX_EPI_SWIGLU) VGX_F32G(EPI_SWIGLU, V);             \
-        else if (epilogue == VGX_EPI_ACCUM) VGX_F32G(EPI_ACCUM, V);          \
-        else VGX_F32G(EPI_STORE, V);                                        \
+        if (epilogue == VGX_EPI_SWIGLU) VGX_F32G(WDT, EPI_SWIGLU, V);        \
+        else if (epilogue == VGX_EPI_ACCUM) VGX_F32G(WDT, EPI_ACCUM, V);     \
+        else VGX_F32G(WDT, EPI_STORE, V);                                   \
     } while (0)
-        if (vec) VGX_F32E(true); else VGX_F32E(false);
+#define VGX_F32W(WDT) do { if (vec) VGX_F32E(WDT, true); else VGX_F32E(WDT, false); } while (0)
+        if (dtype == VGX_BF16) VGX_F32W(VGX_BF16);
+        else if (dtype == VGX_F16) VGX_F32W(VGX_F16);
+        else VGX_F32W(VGX_F32);
+#undef VGX_F32W
 #undef VGX_F32E
 #undef VGX_F32G
         VGX_CHECK_LAUNCH();

@@ -1,6 +1,7 @@
-// HBM-streaming Q8_0 / Q4_0 / F32 GEMV for gfx950 (batch 1..4 rows per pass) with fused RMSNorm
-// prologue and bias / residual / SwiGLU epilogues.  Instantiated per weight dtype in
-// qgemv_q8.hip, qgemv_q4.hip and qgemv_f32.hip so the three compile in parallel.
+// HBM-streaming Q8_0 / Q4_0 / F32 / BF16 / F16 GEMV for gfx950 (batch 1..4 rows per pass) with fused
+// RMSNorm prologue and bias / residual / SwiGLU epilogues.  Instantiated per weight dtype in
+// qgemv_q8.hip, qgemv_q4.hip, qgemv_f32.hip, qgemv_bf16.hip and qgemv_f16.hip so they compile in
+// parallel.
 //
 // Reference semantics: runtime/vault3.c:499-624 (row_dot, matvec), 656-660 (rmsnorm),
 // 1942-1956 (mlp_gu_run); src/vault_v3_model.py:764-774, 1041-1047, 1139, 1145-1150, 2150-2151.
@@ -37,9 +38,14 @@ enum { MODE_ROWS = 0, MODE_SPLITK = 1 };
 constexpr int kGemvMaxChunkFloats = 8192;  // activations staged in LDS per chunk (all batch rows)
 constexpr int kGemvPad = 36;               // floats per staged 32-float block (4 floats of padding)
 
+// Bytes of one row's 32-element block in the packed layout (quants only for Q8_0 / Q4_0, whose
+// scales sit in the scale plane; the elements themselves for the plain dtypes F32 / BF16 / F16).
 __host__ __device__ constexpr int gemv_quant_bytes(int dt) {
-    return dt == VGX_Q8_0 ? 32 : dt == VGX_Q4_0 ? 16 : dt == VGX_F32 ? 128 : 0;
+    return dt == VGX_Q8_0 ? 32 : dt == VGX_Q4_0 ? 16 : dt == VGX_F32 ? 128 : (dt == VGX_BF16 || dt == VGX_F16) ? 64 : 0;
 }
+__host__ __device__ constexpr bool gemv_plain(int dt) { return dt == VGX_F32 || dt == VGX_BF16 || dt == VGX_F16; }
+__host__ __device__ constexpr bool gemv_half(int dt) { return dt == VGX_BF16 || dt == VGX_F16; }
+__host__ __device__ constexpr bool gemv_quant(int dt) { return dt == VGX_Q8_0 || dt == VGX_Q4_0; }
 
 struct GemvArgs {
     const uint8_t *w;
@@ -95,6 +101,15 @@ template <>
 struct BlockRegs<VGX_F32> {
     const float4 *p;  // F32 weights are read at use (512 bytes per block would not fit twice)
 };
+// BF16 / F16: the 4 x 64 bytes of a row-quad block (row r in q[4 r .. 4 r + 3]).
+template <>
+struct BlockRegs<VGX_BF16> {
+    uint4 q[16];
+};
+template <>
+struct BlockRegs<VGX_F16> {
+    uint4 q[16];
+};
 
 template <int DT>
 __device__ __forceinline__ void gemv_load(BlockRegs<DT> &r, const uint8_t *__restrict__ W, int64_t soff, int64_t rq,
@@ -103,6 +118,9 @@ __device__ __forceinline__ void gemv_load(BlockRegs<DT> &r, const uint8_t *__res
     const uint8_t *qp = W + (rq * nblk + gb) * 4 * QB;
     if constexpr (DT == VGX_F32) {
         r.p = reinterpret_cast<const float4 *>(qp);
+    } else if constexpr (gemv_half(DT)) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) r.q[i] = reinterpret_cast<const uint4 *>(qp)[i];
     } else {
 #pragma unroll
         for (int i = 0; i < 4 * QB / 16; ++i) r.q[i] = reinterpret_cast<const uint4 *>(qp)[i];
@@ -122,6 +140,35 @@ __device__ __forceinline__ void gemv_block(const BlockRegs<DT> &br, const float 
             for (int j4 = 0; j4 < 8; ++j4) {
                 const float4 t = br.p[r * 8 + j4];
                 wv[j4 * 4 + 0] = t.x; wv[j4 * 4 + 1] = t.y; wv[j4 * 4 + 2] = t.z; wv[j4 * 4 + 3] = t.w;
+            }
+#pragma unroll
+            for (int n = 0; n < NB; ++n) {
+                const float *xn = xb + n * stride_n;
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < QK; ++j) s = fmaf(wv[j], xn[j], s);
+                acc[r][n] += s;
+            }
+        }
+    } else if constexpr (gemv_half(DT)) {
+        // BF16 / F16 elements widened exactly to fp32 (runtime/vault3.c:510-533), products in fp32
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float wv[QK];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 t = br.q[4 * r + i];
+                const uint32_t w4[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    if constexpr (DT == VGX_BF16) {
+                        wv[8 * i + 2 * k] = __uint_as_float(w4[k] << 16);
+                        wv[8 * i + 2 * k + 1] = __uint_as_float(w4[k] & 0xFFFF0000u);
+                    } else {
+                        wv[8 * i + 2 * k] = half_bits_to_float(w4[k]);
+                        wv[8 * i + 2 * k + 1] = half_bits_to_float(w4[k] >> 16);
+                    }
+                }
             }
 #pragma unroll
             for (int n = 0; n < NB; ++n) {
@@ -996,14 +1043,14 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
                        dim3((unsigned)((a.n_rq + WPG * (64 / LPR) - 1) / (WPG * (64 / LPR)))),              \
                        dim3(64 * WPG * KW), XD ? 0 : lds, st, a)
     const bool aligned = ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.lnw & 15) == 0;
-    if constexpr ((EPI == EPI_STORE || EPI == EPI_SWIGLU) && DT != VGX_F32) {
+    if constexpr ((EPI == EPI_STORE || EPI == EPI_SWIGLU) && gemv_quant(DT)) {
         if (a.nblk == kStreamBlocks && !a.bias && a.n_rq >= kStreamMinRq && a.soff < ((int64_t)1 << 31) && aligned) {
             const unsigned grid = (unsigned)std::min<int64_t>(StreamGeom<DT>::GROUPS, (a.n_rq + 3) / 4);
             hipLaunchKernelGGL((gemv1_stream_kernel<DT, EPI, NORM>), dim3(grid), dim3(256), 0, st, a);
             return;
         }
     }
-    if constexpr (DT != VGX_F32 && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
+    if constexpr (gemv_quant(DT) && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
         if (a.nblk >= 192 && a.nblk <= kPiecesMaxBlocks && a.soff < ((int64_t)1 << 31) && aligned) {
             // 16 waves x 2 row-quads: 5.5 us for 1536 x 8960 (8 x 2: 5.8, 8 x 1: 6.0, 16 x 1: 5.9, 16 x 4: 7.3,
             // 4 x 1: 6.8; the lane-per-block kernel: 6.6)
@@ -1013,7 +1060,7 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
             return;
         }
     }
-    if constexpr (DT != VGX_F32 && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
+    if constexpr (gemv_quant(DT) && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
         if (a.nblk == kStreamBlocks && a.n_rq < kStreamMinRq && a.soff < ((int64_t)1 << 31) && aligned) {
             // 1536-column rows (the o-projection, 1536 x 1536): a workgroup of 4 waves per row-quad, one 1 KB
             // piece per wave (3 of them busy): 3.2 us against 4.2 us for the lane-per-block kernel (2 x 2: 3.7,
@@ -1023,15 +1070,19 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
             return;
         }
     }
-    if (a.n_rq >= 16384) VGX_GEMV1(16, 4, 1, 3, false, false);        // other tall weights: DPP row per row-quad
+    constexpr int UT = gemv_half(DT) ? 1 : 3;                           // BF16 / F16 blocks are 64 registers
+    if (a.n_rq >= 16384) VGX_GEMV1(16, 4, 1, UT, false, false);       // other tall weights: DPP row per row-quad
     else if (a.n_rq >= 2048) VGX_GEMV1(64, 4, 1, 1, true, false);     // lane per block (gate/up before the streaming kernel)
-    else if (a.nblk >= 192) VGX_GEMV1(64, 2, 8, 1, true, false);      // long rows (Q8_0, fused norm, or beyond the
+    else if (a.nblk >= 192) {
+        if constexpr (gemv_half(DT)) VGX_GEMV1(64, 1, 8, 1, true, false);   // 64-register blocks: 512 threads
+        else VGX_GEMV1(64, 2, 8, 1, true, false);                     // long rows (Q8_0, fused norm, or beyond the
                                                                       // pieces kernel): 2 row-quads x 8 waves over K
                                                                       // (6.6 us; one row-quad 6.9 us, direct
                                                                       // activations 7.0 us)
+    }
     else if (a.nblk >= 96 && a.n_rq < 256) VGX_GEMV1(64, 1, 8, 1, true, false);   // few rows: more waves
     else if (a.nblk >= 96) VGX_GEMV1(64, 1, 2, 1, true, false);
-    else if (aligned && DT != VGX_F32) VGX_GEMV1(64, 1, 1, 1, false, true);   // small: direct
+    else if (aligned && !gemv_plain(DT)) VGX_GEMV1(64, 1, 1, 1, false, true);   // small: direct
     else VGX_GEMV1(64, 2, 1, 1, true, false);
 #undef VGX_GEMV1
 }
@@ -1097,7 +1148,10 @@ int qgemv_launch(GemvArgs a, hipStream_t st) {
 
 }  // namespace vgx
 
-// One launcher per weight dtype (defined in qgemv_q8.hip / qgemv_q4.hip / qgemv_f32.hip).
+// One launcher per weight dtype (defined in qgemv_q8.hip / qgemv_q4.hip / qgemv_f32.hip /
+// qgemv_bf16.hip / qgemv_f16.hip).
 int vgx_detail_qgemv_q8(const vgx::GemvArgs &a, hipStream_t st);
 int vgx_detail_qgemv_q4(const vgx::GemvArgs &a, hipStream_t st);
 int vgx_detail_qgemv_f32(const vgx::GemvArgs &a, hipStream_t st);
+int vgx_detail_qgemv_bf16(const vgx::GemvArgs &a, hipStream_t st);
+int vgx_detail_qgemv_f16(const vgx::GemvArgs &a, hipStream_t st);

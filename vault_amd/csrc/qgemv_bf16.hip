@@ -1,0 +1,4 @@
+// BF16 instantiation of the GEMV kernels (qgemv.h).
+#include "qgemv.h"
+
+int vgx_detail_qgemv_bf16(const vgx::GemvArgs &a, hipStream_t st) { return vgx::qgemv_launch<VGX_BF16>(a, st); }

@@ -282,15 +282,15 @@ __global__ __launch_bounds__(64 * NW) void qkv_rope_step_pieces_kernel(QkvStepAr
 
 template <int DTQ, int DTKV>
 void launch(int kv, const QkvStepArgs &a, unsigned grid, hipStream_t st) {
-    const bool pieces = DTQ != VGX_F32 && a.nblk <= kQkvPiecesMaxBlocks && a.soff_q < ((int64_t)1 << 31) &&
-                        a.soff_kv < ((int64_t)1 << 31);
-    if (pieces) {
-        // 8 waves per row-quad (the staging spread over 512 threads; pieces w and w + 8): decode step 1002
-        // against 996 tok/s with 4 waves (2: 982, 3: 990, 6: 997)
-        constexpr int NW = 8;
-        if (kv == VGX_F32) hipLaunchKernelGGL((qkv_rope_step_pieces_kernel<DTQ, DTKV, VGX_F32, NW>), dim3(grid), dim3(64 * NW), 0, st, a);
-        else hipLaunchKernelGGL((qkv_rope_step_pieces_kernel<DTQ, DTKV, VGX_BF16, NW>), dim3(grid), dim3(64 * NW), 0, st, a);
-        return;
+    if constexpr (gemv_quant(DTQ) && gemv_quant(DTKV)) {
+        if (a.nblk <= kQkvPiecesMaxBlocks && a.soff_q < ((int64_t)1 << 31) && a.soff_kv < ((int64_t)1 << 31)) {
+            // 8 waves per row-quad (the staging spread over 512 threads; pieces w and w + 8): decode step 1002
+            // against 996 tok/s with 4 waves (2: 982, 3: 990, 6: 997)
+            constexpr int NW = 8;
+            if (kv == VGX_F32) hipLaunchKernelGGL((qkv_rope_step_pieces_kernel<DTQ, DTKV, VGX_F32, NW>), dim3(grid), dim3(64 * NW), 0, st, a);
+            else hipLaunchKernelGGL((qkv_rope_step_pieces_kernel<DTQ, DTKV, VGX_BF16, NW>), dim3(grid), dim3(64 * NW), 0, st, a);
+            return;
+        }
     }
     if (kv == VGX_F32) hipLaunchKernelGGL((qkv_rope_step_kernel<DTQ, DTKV, VGX_F32>), dim3(grid), dim3(64), 0, st, a);
     else hipLaunchKernelGGL((qkv_rope_step_kernel<DTQ, DTKV, VGX_BF16>), dim3(grid), dim3(64), 0, st, a);
@@ -308,7 +308,7 @@ int vgx_qkv_rope_step(int q_dtype, const void *wq, const float *bq, int kv_wdtyp
                       int kv_dtype, void *k_rot, void *k_raw, void *v_dst, int64_t dst_gstride, int64_t dst_rstride,
                       void *sink_k_raw, void *sink_v, int64_t sink_gstride, int64_t sink_rstride, void *stream) {
     const bool pair_ok = (q_dtype == VGX_Q4_0 && kv_wdtype == VGX_Q8_0) ||
-                         (q_dtype == kv_wdtype && (q_dtype == VGX_Q8_0 || q_dtype == VGX_Q4_0 || q_dtype == VGX_F32));
+                         (q_dtype == kv_wdtype && (gemv_quant(q_dtype) || gemv_plain(q_dtype)));
     if (!pair_ok || (kv_dtype != VGX_F32 && kv_dtype != VGX_BF16)) return VGX_E_DTYPE;
     if (!wq || !wkv || !x || !table || !step || !q_out || !k_rot || !k_raw || !v_dst) return VGX_E_ARG;
     if ((sink_k_raw == nullptr) != (sink_v == nullptr)) return VGX_E_ARG;
@@ -320,8 +320,8 @@ int vgx_qkv_rope_step(int q_dtype, const void *wq, const float *bq, int kv_wdtyp
     QkvStepArgs a{};
     a.wq = static_cast<const uint8_t *>(wq);
     a.wkv = static_cast<const uint8_t *>(wkv);
-    a.soff_q = q_dtype == VGX_F32 ? 0 : vgx_qweight_scale_offset(q_dtype, H * D, d_model);
-    a.soff_kv = kv_wdtype == VGX_F32 ? 0 : vgx_qweight_scale_offset(kv_wdtype, 2 * G * D, d_model);
+    a.soff_q = gemv_plain(q_dtype) ? 0 : vgx_qweight_scale_offset(q_dtype, H * D, d_model);
+    a.soff_kv = gemv_plain(kv_wdtype) ? 0 : vgx_qweight_scale_offset(kv_wdtype, 2 * G * D, d_model);
     a.bq = bq;
     a.bkv = bkv;
     a.nblk = (int)(d_model / QK);
@@ -350,6 +350,8 @@ int vgx_qkv_rope_step(int q_dtype, const void *wq, const float *bq, int kv_wdtyp
     if (q_dtype == VGX_Q4_0 && kv_wdtype == VGX_Q8_0) launch<VGX_Q4_0, VGX_Q8_0>(kv_dtype, a, grid, st);
     else if (q_dtype == VGX_Q8_0) launch<VGX_Q8_0, VGX_Q8_0>(kv_dtype, a, grid, st);
     else if (q_dtype == VGX_Q4_0) launch<VGX_Q4_0, VGX_Q4_0>(kv_dtype, a, grid, st);
+    else if (q_dtype == VGX_BF16) launch<VGX_BF16, VGX_BF16>(kv_dtype, a, grid, st);
+    else if (q_dtype == VGX_F16) launch<VGX_F16, VGX_F16>(kv_dtype, a, grid, st);
     else launch<VGX_F32, VGX_F32>(kv_dtype, a, grid, st);
     VGX_CHECK_LAUNCH();
     return VGX_OK;

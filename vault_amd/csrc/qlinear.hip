@@ -1,22 +1,23 @@
-// Q8_0 / Q4_0 / F32 weights on gfx950: packing into the row-quad layout, bit-exact dequant,
-// embedding rows, and the C entry points of the GEMV (kernels in qgemv.h).
+// Q8_0 / Q4_0 / F32 / BF16 / F16 weights on gfx950: packing into the row-quad layout, bit-exact
+// dequant, embedding rows, and the C entry points of the GEMV (kernels in qgemv.h).
 //
-// Reference semantics: runtime/vault3.c:499-654 (row_dot, matvec, embed_row), 1942-1956
-// (mlp_gu_run); tools/vlt3.py:98-157 (block layouts and dequantization).
+// Reference semantics: runtime/vault3.c:499-654 (row_dot with its F32 / BF16 / F16 / Q8_0 / Q4_0
+// cases, matvec, embed_row), 1942-1956 (mlp_gu_run); tools/vlt3.py:98-157 (block layouts and
+// dequantization), 312-342 (BF16 tensors of the "bf16" format and of rows that are not whole blocks).
 #include "qgemv.h"
 
 using namespace vgx;
 
 namespace {
 
-__host__ __device__ constexpr int quant_bytes(int dt) {
-    return dt == VGX_Q8_0 ? 32 : dt == VGX_Q4_0 ? 16 : dt == VGX_F32 ? 128 : 0;
-}
+__host__ __device__ constexpr int quant_bytes(int dt) { return gemv_quant_bytes(dt); }
 __host__ __device__ constexpr int aos_bytes(int dt) { return dt == VGX_Q8_0 ? 34 : dt == VGX_Q4_0 ? 18 : 0; }
 
 inline int64_t rows4(int64_t r) { return (r + 3) / 4 * 4; }
 
-inline bool dtype_ok(int dt) { return dt == VGX_Q8_0 || dt == VGX_Q4_0 || dt == VGX_F32; }
+inline bool dtype_ok(int dt) {
+    return dt == VGX_Q8_0 || dt == VGX_Q4_0 || dt == VGX_F32 || dt == VGX_BF16 || dt == VGX_F16;
+}
 
 int64_t scale_off(int dt, int64_t rows, int64_t cols) {
     const int64_t q = rows4(rows) * (cols / QK) * quant_bytes(dt);
@@ -24,7 +25,7 @@ int64_t scale_off(int dt, int64_t rows, int64_t cols) {
 }
 
 int64_t packed_bytes(int dt, int64_t rows, int64_t cols) {
-    if (dt == VGX_F32) return rows4(rows) * cols * 4;
+    if (gemv_plain(dt)) return rows4(rows) * (cols / QK) * quant_bytes(dt);
     return scale_off(dt, rows, cols) + rows4(rows) * (cols / QK) * 2;
 }
 
@@ -56,10 +57,11 @@ __global__ void pack_kernel(const uint8_t *__restrict__ a, const uint8_t *__rest
     }
     uint8_t *qd = dst + ((rq * nblk + b) * 4 + rr) * QB;
     const bool live = r < src_rows;
-    if constexpr (DT == VGX_F32) {
-        const float *s = reinterpret_cast<const float *>(src) + r * nblk * QK + b * QK;
-        float *d = reinterpret_cast<float *>(qd);
-        for (int j = 0; j < QK; ++j) d[j] = live ? s[j] : 0.0f;
+    if constexpr (gemv_plain(DT)) {
+        // row-major elements: the block's QB bytes as 32-bit words
+        const uint32_t *s = reinterpret_cast<const uint32_t *>(src + (r * nblk + b) * QB);
+        uint32_t *d = reinterpret_cast<uint32_t *>(qd);
+        for (int j = 0; j < QB / 4; ++j) d[j] = live ? s[j] : 0u;
     } else {
         uint16_t *sd = reinterpret_cast<uint16_t *>(dst + soff) + (rq * nblk + b) * 4 + rr;
         const uint8_t *s = src + (r * nblk + b) * aos_bytes(DT);
@@ -77,10 +79,10 @@ __global__ void unpack_kernel(const uint8_t *__restrict__ src, uint8_t *__restri
     const int64_t r = i / nblk, b = i - r * nblk;
     const int64_t rq = r >> 2, rr = r & 3;
     const uint8_t *qs = src + ((rq * nblk + b) * 4 + rr) * QB;
-    if constexpr (DT == VGX_F32) {
-        float *d = reinterpret_cast<float *>(dst) + r * nblk * QK + b * QK;
-        const float *s = reinterpret_cast<const float *>(qs);
-        for (int j = 0; j < QK; ++j) d[j] = s[j];
+    if constexpr (gemv_plain(DT)) {
+        uint32_t *d = reinterpret_cast<uint32_t *>(dst + (r * nblk + b) * QB);
+        const uint32_t *s = reinterpret_cast<const uint32_t *>(qs);
+        for (int j = 0; j < QB / 4; ++j) d[j] = s[j];
     } else {
         const uint16_t sc = reinterpret_cast<const uint16_t *>(src + soff)[(rq * nblk + b) * 4 + rr];
         uint8_t *d = dst + (r * nblk + b) * aos_bytes(DT);
@@ -100,6 +102,12 @@ __device__ __forceinline__ void dequant_block(const uint8_t *__restrict__ w, int
     if constexpr (DT == VGX_F32) {
         const float *s = reinterpret_cast<const float *>(qs);
         for (int j = 0; j < QK; ++j) out[j] = s[j];
+    } else if constexpr (DT == VGX_BF16) {
+        const uint16_t *s = reinterpret_cast<const uint16_t *>(qs);
+        for (int j = 0; j < QK; ++j) out[j] = bf16_bits_to_float(s[j]);
+    } else if constexpr (DT == VGX_F16) {
+        const uint16_t *s = reinterpret_cast<const uint16_t *>(qs);
+        for (int j = 0; j < QK; ++j) out[j] = half_bits_to_float(s[j]);
     } else {
         const float d = half_bits_to_float(reinterpret_cast<const uint16_t *>(w + soff)[(rq * nblk + b) * 4 + rr]);
         if constexpr (DT == VGX_Q8_0) {
@@ -165,7 +173,7 @@ static int pack_common(int dtype, const void *a, const void *b, void *dst, int64
     const int64_t prow = mode == 1 ? 2 * rows : rows;
     const int64_t nblk = cols / QK;
     const int64_t total = rows4(prow) * nblk;
-    const int64_t soff = dtype == VGX_F32 ? 0 : scale_off(dtype, prow, cols);
+    const int64_t soff = gemv_plain(dtype) ? 0 : scale_off(dtype, prow, cols);
     hipStream_t st = (hipStream_t)stream;
     const auto *pa = static_cast<const uint8_t *>(a);
     const auto *pb = static_cast<const uint8_t *>(b);
@@ -174,6 +182,8 @@ static int pack_common(int dtype, const void *a, const void *b, void *dst, int64
         case VGX_Q8_0: hipLaunchKernelGGL(pack_kernel<VGX_Q8_0>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode, hd, n_rope); break;
         case VGX_Q4_0: hipLaunchKernelGGL(pack_kernel<VGX_Q4_0>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode, hd, n_rope); break;
         case VGX_F32: hipLaunchKernelGGL(pack_kernel<VGX_F32>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode, hd, n_rope); break;
+        case VGX_BF16: hipLaunchKernelGGL(pack_kernel<VGX_BF16>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode, hd, n_rope); break;
+        case VGX_F16: hipLaunchKernelGGL(pack_kernel<VGX_F16>, grid_for(total, 256), 256, 0, st, pa, pb, pd, rows, nblk, soff, total, mode, hd, n_rope); break;
     }
     VGX_CHECK_LAUNCH();
     return VGX_OK;
@@ -202,7 +212,7 @@ int vgx_qweight_unpack(int dtype, const void *packed, void *dst_blocks, int64_t 
     if (rows <= 0 || cols <= 0) return VGX_E_SIZE;
     if (cols % QK) return VGX_E_SHAPE;
     const int64_t nblk = cols / QK;
-    const int64_t soff = dtype == VGX_F32 ? 0 : scale_off(dtype, rows, cols);
+    const int64_t soff = gemv_plain(dtype) ? 0 : scale_off(dtype, rows, cols);
     hipStream_t st = (hipStream_t)stream;
     const auto *ps = static_cast<const uint8_t *>(packed);
     auto *pd = static_cast<uint8_t *>(dst_blocks);
@@ -211,6 +221,8 @@ int vgx_qweight_unpack(int dtype, const void *packed, void *dst_blocks, int64_t 
         case VGX_Q8_0: hipLaunchKernelGGL(unpack_kernel<VGX_Q8_0>, g, 256, 0, st, ps, pd, rows, nblk, soff); break;
         case VGX_Q4_0: hipLaunchKernelGGL(unpack_kernel<VGX_Q4_0>, g, 256, 0, st, ps, pd, rows, nblk, soff); break;
         case VGX_F32: hipLaunchKernelGGL(unpack_kernel<VGX_F32>, g, 256, 0, st, ps, pd, rows, nblk, soff); break;
+        case VGX_BF16: hipLaunchKernelGGL(unpack_kernel<VGX_BF16>, g, 256, 0, st, ps, pd, rows, nblk, soff); break;
+        case VGX_F16: hipLaunchKernelGGL(unpack_kernel<VGX_F16>, g, 256, 0, st, ps, pd, rows, nblk, soff); break;
     }
     VGX_CHECK_LAUNCH();
     return VGX_OK;
@@ -222,7 +234,7 @@ int vgx_qweight_dequant(int dtype, const void *packed, float *out, int64_t rows,
     if (rows <= 0 || cols <= 0) return VGX_E_SIZE;
     if (cols % QK) return VGX_E_SHAPE;
     const int64_t nblk = cols / QK;
-    const int64_t soff = dtype == VGX_F32 ? 0 : scale_off(dtype, rows, cols);
+    const int64_t soff = gemv_plain(dtype) ? 0 : scale_off(dtype, rows, cols);
     hipStream_t st = (hipStream_t)stream;
     const auto *pw = static_cast<const uint8_t *>(packed);
     const unsigned g = grid_for(rows * nblk, 256);
@@ -230,6 +242,8 @@ int vgx_qweight_dequant(int dtype, const void *packed, float *out, int64_t rows,
         case VGX_Q8_0: hipLaunchKernelGGL(dequant_kernel<VGX_Q8_0>, g, 256, 0, st, pw, out, rows, nblk, soff); break;
         case VGX_Q4_0: hipLaunchKernelGGL(dequant_kernel<VGX_Q4_0>, g, 256, 0, st, pw, out, rows, nblk, soff); break;
         case VGX_F32: hipLaunchKernelGGL(dequant_kernel<VGX_F32>, g, 256, 0, st, pw, out, rows, nblk, soff); break;
+        case VGX_BF16: hipLaunchKernelGGL(dequant_kernel<VGX_BF16>, g, 256, 0, st, pw, out, rows, nblk, soff); break;
+        case VGX_F16: hipLaunchKernelGGL(dequant_kernel<VGX_F16>, g, 256, 0, st, pw, out, rows, nblk, soff); break;
     }
     VGX_CHECK_LAUNCH();
     return VGX_OK;
@@ -243,7 +257,7 @@ int vgx_embed_rows(int dtype, const void *packed, int64_t rows, int64_t cols, co
     if (cols % QK) return VGX_E_SHAPE;
     if (n_ids == 0) return VGX_OK;
     const int64_t nblk = cols / QK;
-    const int64_t soff = dtype == VGX_F32 ? 0 : scale_off(dtype, rows, cols);
+    const int64_t soff = gemv_plain(dtype) ? 0 : scale_off(dtype, rows, cols);
     hipStream_t st = (hipStream_t)stream;
     const auto *pw = static_cast<const uint8_t *>(packed);
     const unsigned g = grid_for(n_ids * nblk, 256);
@@ -251,6 +265,8 @@ int vgx_embed_rows(int dtype, const void *packed, int64_t rows, int64_t cols, co
         case VGX_Q8_0: hipLaunchKernelGGL(embed_kernel<VGX_Q8_0>, g, 256, 0, st, pw, ids, out, ldo, rows, nblk, soff, n_ids, pad_row); break;
         case VGX_Q4_0: hipLaunchKernelGGL(embed_kernel<VGX_Q4_0>, g, 256, 0, st, pw, ids, out, ldo, rows, nblk, soff, n_ids, pad_row); break;
         case VGX_F32: hipLaunchKernelGGL(embed_kernel<VGX_F32>, g, 256, 0, st, pw, ids, out, ldo, rows, nblk, soff, n_ids, pad_row); break;
+        case VGX_BF16: hipLaunchKernelGGL(embed_kernel<VGX_BF16>, g, 256, 0, st, pw, ids, out, ldo, rows, nblk, soff, n_ids, pad_row); break;
+        case VGX_F16: hipLaunchKernelGGL(embed_kernel<VGX_F16>, g, 256, 0, st, pw, ids, out, ldo, rows, nblk, soff, n_ids, pad_row); break;
     }
     VGX_CHECK_LAUNCH();
     return VGX_OK;
@@ -262,7 +278,7 @@ static int qgemv_dispatch(int dtype, const void *w, int64_t rows_packed, int64_t
     GemvArgs a{};
     a.w = static_cast<const uint8_t *>(w);
     a.nblk = (int)(cols / QK);
-    a.soff = dtype == VGX_F32 ? 0 : scale_off(dtype, rows_packed, cols);
+    a.soff = gemv_plain(dtype) ? 0 : scale_off(dtype, rows_packed, cols);
     a.n_rq = rows4(rows_packed) / 4;
     a.rows_out = rows_out;
     a.x = x;
@@ -279,6 +295,8 @@ static int qgemv_dispatch(int dtype, const void *w, int64_t rows_packed, int64_t
         case VGX_Q8_0: return vgx_detail_qgemv_q8(a, st);
         case VGX_Q4_0: return vgx_detail_qgemv_q4(a, st);
         case VGX_F32: return vgx_detail_qgemv_f32(a, st);
+        case VGX_BF16: return vgx_detail_qgemv_bf16(a, st);
+        case VGX_F16: return vgx_detail_qgemv_f16(a, st);
     }
     return VGX_E_DTYPE;
 }

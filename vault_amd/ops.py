@@ -12,8 +12,16 @@ import torch
 
 from . import _lib as L
 
-F32, Q8_0, Q4_0 = L.F32, L.Q8_0, L.Q4_0
+F32, F16, BF16, Q8_0, Q4_0 = L.F32, L.F16, L.BF16, L.Q8_0, L.Q4_0
 BLOCK_BYTES = {Q8_0: 34, Q4_0: 18}
+ELEM_BYTES = {F32: 4, F16: 2, BF16: 2}       # plain (unquantized) weight dtypes
+
+
+def payload_bytes(dtype: int, rows: int, cols: int) -> int:
+    """Bytes of a [rows x cols] tensor in its VLT3 layout (AoS blocks or row-major elements)."""
+    if dtype in ELEM_BYTES:
+        return rows * cols * ELEM_BYTES[dtype]
+    return rows * (cols // 32) * BLOCK_BYTES[dtype]
 
 
 def _stream(dev: torch.device) -> int:
@@ -56,7 +64,7 @@ class QWeight:
 
     @classmethod
     def from_blocks(cls, dtype: int, rows: int, cols: int, data, device) -> "QWeight":
-        """``data``: VLT3 payload (AoS Q8_0/Q4_0 blocks, or row-major fp32 for F32)."""
+        """``data``: VLT3 payload (AoS Q8_0/Q4_0 blocks, or row-major elements for F32 / BF16 / F16)."""
         lib = L.load()
         src = cls._upload(data, device)
         n = lib.vgx_qweight_packed_bytes(dtype, rows, cols)
@@ -95,7 +103,7 @@ class QWeight:
         """Packed -> AoS blocks (uint8 device tensor)."""
         if self.gateup:
             raise ValueError("unpack of a gate/up tensor is not supported")
-        nbytes = self.rows * self.cols * 4 if self.dtype == F32 else self.rows * (self.cols // 32) * BLOCK_BYTES[self.dtype]
+        nbytes = payload_bytes(self.dtype, self.rows, self.cols)
         out = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         L.check(L.load().vgx_qweight_unpack(self.dtype, self.packed.data_ptr(), out.data_ptr(), self.rows, self.cols,
                                             _stream(self.device)), "vgx_qweight_unpack")
@@ -112,9 +120,7 @@ class QWeight:
     def stream_bytes(self) -> int:
         """Bytes of weights one full pass reads (the algorithmic bytes of one GEMV)."""
         rows = 2 * self.rows if self.gateup else self.rows
-        if self.dtype == F32:
-            return rows * self.cols * 4
-        return rows * (self.cols // 32) * BLOCK_BYTES[self.dtype]
+        return payload_bytes(self.dtype, rows, self.cols)
 
 
 def count_nonfinite(items, device) -> list:
@@ -163,7 +169,11 @@ def _gemv(w: QWeight, x: torch.Tensor, out: Optional[torch.Tensor], epi: int, bi
     nw, eps = (None, 0.0) if norm is None else norm
     if nw is not None:
         _need(nw, torch.float32, "norm weight")
-    if B >= GEMM_MIN_ROWS and (w.dtype in (Q8_0, Q4_0) or (w.dtype == F32 and nw is None)):
+    if B >= GEMM_MIN_ROWS and w.dtype in ELEM_BYTES and nw is not None:
+        # plain weights: the fp32 MFMA GEMM has no RMSNorm prologue; normalise first
+        x2 = rmsnorm(x2, nw, eps)
+        nw = None
+    if B >= GEMM_MIN_ROWS and (w.dtype in (Q8_0, Q4_0) or w.dtype in ELEM_BYTES):
         lib = L.load()
         need = int(lib.vgx_qgemm_workspace_bytes(B, w.rows, w.cols, epi))
         ws = gemm_workspace(x.device).get(need)

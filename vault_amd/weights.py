@@ -51,8 +51,11 @@ def _f32(t: Tensor, device) -> torch.Tensor:
 
 
 def _block_dtype(t: Tensor) -> int:
-    if t.dtype not in (vlt3.Q8_0, vlt3.Q4_0, vlt3.F32):
+    """Projection weights: Q8_0 / Q4_0 blocks, or F32 / BF16 / F16 elements (runtime/vault3.c:499-598)."""
+    if t.dtype not in (vlt3.Q8_0, vlt3.Q4_0, vlt3.F32, vlt3.BF16, vlt3.F16):
         raise vlt3.VLT3Error(f"{t.name}: dtype {t.dtype} is not supported on the device path")
+    if t.shape[-1] % 32:
+        raise vlt3.VLT3Error(f"{t.name}: rows of {t.shape[-1]} elements are not whole 32-element blocks")
     return t.dtype
 
 
@@ -176,7 +179,7 @@ def quantize_state(cfg: VAULTv3Config, state: Dict[str, np.ndarray], fmt: str) -
         dt = vlt3.choose_dtype(name, fmt, cfg.n_layers)
         a = np.asarray(arr, dtype=np.float32)
         if dt in (vlt3.Q8_0, vlt3.Q4_0) and a.shape[-1] % 32:
-            dt = vlt3.F32
+            dt = vlt3.BF16                       # rows that are not whole blocks (tools/vlt3.py:341-342)
         out[name] = Tensor(name, dt, tuple(a.shape), vlt3.quantize(dt, a))
     return out
 
@@ -197,14 +200,19 @@ def random_state(cfg: VAULTv3Config, seed: int, std: float = 0.15) -> Dict[str, 
 
 
 def synthetic_tensors(cfg: VAULTv3Config, fmt: str, seed: int) -> Dict[str, Tensor]:
-    """Random-init weights drawn directly as quantized blocks (hybrid policy), F32 norms U(0.8,1.2),
-    biases N(0, 0.02), scorer fp32 N(0, 0.02): the synthetic recipe of the 1.54B decode workload."""
+    """Random-init weights drawn directly as quantized blocks (hybrid policy; BF16 projections
+    N(0, 0.02) for the "bf16" format), F32 norms U(0.8,1.2), biases N(0, 0.02), scorer fp32 N(0, 0.02):
+    the synthetic recipe of the 1.54B decode workload."""
     rng = np.random.default_rng(seed)
     out = {}
     for name, shp in tensor_shapes(cfg).items():
         dt = vlt3.choose_dtype(name, fmt, cfg.n_layers)
         if dt in (vlt3.Q8_0, vlt3.Q4_0):
             out[name] = Tensor(name, dt, shp, vlt3.synthetic_blocks(dt, shp[0], shp[1], rng))
+            continue
+        if dt in (vlt3.BF16, vlt3.F16):
+            a = rng.standard_normal(shp, dtype=np.float32) * np.float32(0.02)
+            out[name] = Tensor(name, dt, shp, vlt3.quantize(dt, a))
             continue
         if "layernorm" in name or name in ("norm.weight", "seg_scorer.ln.weight"):
             a = rng.uniform(0.8, 1.2, shp).astype(np.float32)
