@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define VGX_ABI_VERSION 1
+#define VGX_ABI_VERSION 2
 
 enum {
     VGX_OK = 0,
@@ -239,6 +239,15 @@ typedef struct {
     int64_t causal_base;
     int n_runs;
     vgx_kv_run runs[4];
+    /* Optional bias on run bias_run (bias == NULL: none): query t of head h adds
+     * bias[t*bias_ldq + bias_head_row[h]*bias_rstride + j] to its score with key j of that run;
+     * bias_head_row (H entries, device memory) < 0 leaves head h unbiased.  The chunk-level resonance
+     * bias on the segment run (src/vault_v3_model.py:1718-1793, 2083-2090). */
+    const float *bias;
+    const int32_t *bias_head_row;
+    int64_t bias_ldq;
+    int64_t bias_rstride;
+    int bias_run;
 } vgx_attn_block;
 
 /* Prefill attention on bf16 MFMA (kv_dtype VGX_BF16, or VGX_F32 whose K / V enter the MFMAs as bf16

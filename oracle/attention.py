@@ -46,7 +46,9 @@ def decode(q: np.ndarray, spans: list, bias: np.ndarray | None = None, bias_span
 
 
 def chunk(q: np.ndarray, prefix: list, k_cur: np.ndarray, v_cur: np.ndarray, bias=None, bias_span=-1) -> np.ndarray:
-    """q: [T, H, D]; prefix: list of (K [G, n, D], V [G, n, D]); k_cur/v_cur: [G, T, D] -> [T, H, D]."""
+    """q: [T, H, D]; prefix: list of (K [G, n, D], V [G, n, D]); k_cur/v_cur: [G, T, D] -> [T, H, D].
+    ``bias`` on prefix run ``bias_span``: [H, n] (every query) or [T, H, n] (per query row: the
+    chunk-level resonance bias added to the scores, src/vault_v3_model.py:2083-2090)."""
     q = np.asarray(q, dtype=np.float64)
     T, H, D = q.shape
     Ks = [np.asarray(k, dtype=np.float64) for k, _ in prefix] + [np.asarray(k_cur, dtype=np.float64)]
@@ -62,7 +64,8 @@ def chunk(q: np.ndarray, prefix: list, k_cur: np.ndarray, v_cur: np.ndarray, bia
     if bias is not None:
         off = sum(np.asarray(k).shape[1] for k, _ in prefix[:bias_span])
         n_b = np.asarray(prefix[bias_span][0]).shape[1]
-        s[:, :, off:off + n_b] += np.asarray(bias, dtype=np.float64)[:, None, :n_b]
+        b = np.asarray(bias, dtype=np.float64)
+        s[:, :, off:off + n_b] += b[:, None, :n_b] if b.ndim == 2 else b.transpose(1, 0, 2)[:, :, :n_b]
     t = np.arange(T)[:, None]
     j = np.arange(P + T)[None, :]
     s = np.where((j <= P + t)[None], s, -np.inf)

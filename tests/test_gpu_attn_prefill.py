@@ -186,3 +186,38 @@ def test_prefill_fp32_kv_strided_state_views(dev):
                        "causal_base": 0}], H, G)
     ref = oatt.chunk(_f64(q), [(_f64(prev_k), _f64(prev_v))], _f64(ring_k[:, :T]), _f64(ring_v[:, :T]))
     assert np.abs(out.double().cpu().numpy() - ref).max() <= TOL32
+
+
+@pytest.mark.parametrize("kvdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,lens", [(300, (40, 77, 200)), (1024, (512, 1024, 1024)), (45, (0, 33, 64))])
+def test_prefill_per_row_bias_on_segment_run(dev, kvdt, T, lens):
+    """The chunk-level resonance bias: query t of head h adds bias[t, row(h), j] to its scores with the
+    segment run's keys (rows: none / arch / sup by head class, 12 query / 2 KV heads), against the
+    float64 oracle with the dense [T, H, n] bias; zero rows (positions where the mode is 0) and a bias
+    run shorter than the bias rows are included."""
+    rng = np.random.default_rng(T * 7 + sum(lens))
+    H, G, D = 12, 2, 128
+    cast = (lambda a: _bf(a)) if kvdt == torch.bfloat16 else (lambda a: torch.as_tensor(a, dtype=torch.float32))
+    runs = [(cast(rng.standard_normal((G, n, D))).to(dev), cast(rng.standard_normal((G, n, D))).to(dev))
+            for n in lens if n > 0]
+    seg = 1 if lens[0] > 0 else 0                     # the segment run's index among the runs
+    n_seg = lens[1]
+    kc = cast(rng.standard_normal((G, T, D))).to(dev)
+    vc = cast(rng.standard_normal((G, T, D))).to(dev)
+    q = torch.from_numpy(rng.standard_normal((T, H, D)).astype(np.float32)).to(dev)
+    rows = [-1, -1, 0, 0, 1, 1] * 2
+    bias = (rng.standard_normal((T, 2, n_seg + 7)) * 3).astype(np.float32)
+    bias[rng.random(T) < 0.3] = 0.0
+    out = torch.empty(T, H, D, device=dev)
+    ops.attn_prefill([{"q": q, "out": out, "runs": runs + [(kc, vc)], "causal_base": 0,
+                       "bias": torch.from_numpy(bias).to(dev), "bias_head_row": rows, "bias_run": seg}], H, G)
+    dense = np.zeros((T, H, n_seg))
+    for h, r in enumerate(rows):
+        if r >= 0:
+            dense[:, h] = bias[:, r, :n_seg]
+    ref = oatt.chunk(_f64(q), [(_f64(k), _f64(v)) for k, v in runs], _f64(kc), _f64(vc), bias=dense, bias_span=seg)
+    err = np.abs(out.double().cpu().numpy() - ref).max()
+    assert err <= (TOL if kvdt == torch.bfloat16 else TOL32), err
+    # the same bias on the wrong run is far outside the bar
+    wrong = oatt.chunk(_f64(q), [(_f64(k), _f64(v)) for k, v in runs], _f64(kc), _f64(vc))
+    assert np.abs(wrong - ref).max() > 100 * TOL

@@ -49,10 +49,13 @@ def test_topk_matches_host_sort(dev, B, V):
         assert np.array_equal(val[b, :n], x[b, want[:n]]), b
 
 
-@pytest.fixture(scope="module", params=[128, 40], ids=["bank_keeps_all", "bank_evicts"])
+@pytest.fixture(scope="module", params=[(128, 64), (40, 64), (40, 128)],
+                ids=["bank_keeps_all", "bank_evicts", "bank_evicts_d128"])
 def word_model(request, dev):
-    cfg = modelgen.tiny_cfg(window=32, seg_budget=request.param, vocab=512, seg_max=7, max_sink=32, n_sink=4,
-                            head_dim=64, n_layers=4)
+    budget, head_dim = request.param
+    heads = dict(n_heads=12, n_kv_heads=2) if head_dim == 128 else {}
+    cfg = modelgen.tiny_cfg(window=32, seg_budget=budget, vocab=512, seg_max=7, max_sink=32, n_sink=4,
+                            head_dim=head_dim, n_layers=4, **heads)
     toks, bmap = modelgen.word_vocab(cfg)
     _, image, _ = modelgen.build(cfg, "q8_0", seed=6, vocab=(toks, bmap))
     with tempfile.TemporaryDirectory() as td:
@@ -114,12 +117,33 @@ def test_resonance_stream_matches_reference_runtime(word_model, kind):
 @pytest.mark.parametrize("kind,split", [("ids", 150), ("rollback", 100), ("spoof", 160), ("hop", 140)])
 def test_resonance_prefill_matches_stream(word_model, kind, split):
     """prefill(split tokens) then the stream, and forward() over the whole conversation: every logit row
-    against the reference runtime stepping the same ids."""
+    against the reference runtime stepping the same ids.  At head_dim 128 (the MFMA chunk attention)
+    chunks in which resonance is active keep the chunk path with per-row bias (the prefill's chunks are
+    checked to have carried one); at head_dim 64 they run the step path."""
     cfg, toks, image, m = word_model
     ids = modelgen.conversation(cfg, toks, kind, seed=1)
     rt = ref.RefRuntime(image, threads=2)
-    want = np.stack([rt.step(t).astype(np.float64) for t in ids])
-    last, st = m.prefill(torch.tensor([ids[:split]]))
+    want, ref_modes = [], []
+    for t in ids:
+        want.append(rt.step(t).astype(np.float64))
+        ref_modes.append(rt.flags()["seg_bias_active"])
+    want = np.stack(want)
+    biased = []
+    chunk_bias = m._chunk_bias
+
+    def spy(*a, **k):
+        r = chunk_bias(*a, **k)
+        biased.append(r is not None)
+        return r
+
+    m._chunk_bias = spy
+    try:
+        last, st = m.prefill(torch.tensor([ids[:split]]))
+    finally:
+        del m._chunk_bias
+    if m._mfma_prefill():
+        # the chunk-bias path ran exactly when the reference's resonance was active inside the prefill
+        assert any(biased) == any(ref_modes[:split]), (biased, max(ref_modes[:split]))
     rows = [last[0].double().cpu().numpy()]
     for t in ids[split:]:
         rows.append(m.step(torch.tensor([t]), st)[0].double().cpu().numpy())

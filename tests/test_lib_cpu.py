@@ -22,7 +22,7 @@ def test_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib.vgx_abi_version() == 1
+    assert lib.vgx_abi_version() == 2
 
 
 @pytest.mark.parametrize("dt,rows,cols,expect", [

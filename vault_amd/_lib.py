@@ -109,7 +109,8 @@ class AttnBlock(C.Structure):
     """vgx_attn_block (include/vault_amd.h)."""
     _fields_ = [("q", C.c_void_p), ("ldq", C.c_int64), ("q_hstride", C.c_int64), ("out", C.c_void_p),
                 ("ldo", C.c_int64), ("o_hstride", C.c_int64), ("n_q", C.c_int64), ("causal_base", C.c_int64),
-                ("n_runs", C.c_int), ("runs", KVRun * 4)]
+                ("n_runs", C.c_int), ("runs", KVRun * 4), ("bias", C.c_void_p), ("bias_head_row", C.c_void_p),
+                ("bias_ldq", C.c_int64), ("bias_rstride", C.c_int64), ("bias_run", C.c_int)]
 
 
 class VGXError(RuntimeError):
@@ -140,7 +141,7 @@ def load() -> C.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    if lib.vgx_abi_version() != 1:
+    if lib.vgx_abi_version() != 2:
         raise VGXError("ABI version mismatch")
     _lib = lib
     return lib

@@ -4,7 +4,10 @@
 // Reference semantics: block_sliding_attention (src/vault_v3_model.py:812-863, sinks re-rotated per
 // query chunk :805-809, 849-856) and the chunk-recurrent attention of _forward_chunk_recurrent
 // (:2029-2037, 2064-2093).  A query block is one chunk; query t of the block sees every key of the
-// first runs and keys j <= causal_base + t of the last run.
+// first runs and keys j <= causal_base + t of the last run.  A block may carry a bias per (query,
+// head row, key) on one run: the chunk-level resonance bias on the segment-memory run
+// (_build_chunk_resonance_bias, :1718-1793, added to the scores at :2083-2090), whose rows are the
+// per-position biases of the step rule, so a chunk with resonance active stays on this kernel.
 //
 // Mapping.  A workgroup = one (query block, kv group g, tile of 32 queries) with one wave per query
 // head of the group (GRP waves), so every K/V tile staged in LDS serves all GRP heads.  A wave holds
@@ -72,6 +75,13 @@ struct BlockArgs {
     int n_runs;
     int tile0;         // first workgroup index of this block
     RunArgs run[4];
+    // optional bias on run bias_run: query t of head h adds bias[t * bias_ldq + head_row[h] * bias_rstride
+    // + j] to its score with key j of that run (head_row[h] < 0: none)
+    const float *bias;
+    const int32_t *bias_head_row;
+    int64_t bias_ldq;
+    int64_t bias_rstride;
+    int bias_run;
 };
 
 struct PrefillArgs {
@@ -263,6 +273,12 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     };
 
     const float sl2 = a.scale_log2;
+    // this wave's bias rows (query t at brow + t * bias_ldq), when its head is biased
+    const float *brow = nullptr;
+    if (B.bias != nullptr) {
+        const int hr = B.bias_head_row[h];
+        if (hr >= 0) brow = B.bias + (int64_t)hr * B.bias_rstride;
+    }
     int r = 0;
     while (r < n_runs && run_len(r) <= 0) ++r;
     int64_t j0 = 0;
@@ -308,6 +324,8 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
             bf16x8_t pf[NPP][NQT];
             // 32-key chunk fully visible to all 32 queries: no per-score mask
             const bool full = j0 + c + 32 <= n && (!causal || j0 + c + 31 <= cbase + t0);
+            // the biased run of a biased head: its bias (log2 units) is added to the chunk's scores
+            const bool biased = brow != nullptr && r == B.bias_run;   // wave-uniform
             // key index relative to the causal limit of query t0 (fits in 32 bits)
             const int kbase = (int)(j0 + c - (causal ? cbase + t0 : 0));
             const int klim = (int)(n - (j0 + c));
@@ -327,6 +345,16 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                             const int kk = kt * 16 + lg * 4 + i;       // key within the 32-key chunk
                             const bool vis = kk < klim && (!causal || kbase + kk <= qt * 16 + lq);
                             v[kt * 4 + i] = vis ? sc[qt][kt][i] * sl2 : -INFINITY;
+                        }
+                }
+                if (biased) {
+                    const float *bq = brow + min(t0 + qt * 16 + lq, B.n_q - 1) * B.bias_ldq;
+#pragma unroll
+                    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int64_t key = j0 + c + kt * 16 + lg * 4 + i;
+                            if (key < n) v[kt * 4 + i] += bq[key] * 1.4426950408889634f;   // -inf stays -inf
                         }
                 }
                 float mt = v[0];
@@ -462,6 +490,15 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_bl
         B.causal_base = b.causal_base;
         B.n_runs = b.n_runs;
         B.tile0 = (int)tiles;
+        if (b.bias) {
+            if (!b.bias_head_row || b.bias_run < 0 || b.bias_run >= b.n_runs) return VGX_E_ARG;
+            if (b.bias_ldq < 0 || b.bias_rstride < 0) return VGX_E_SIZE;
+            B.bias = b.bias;
+            B.bias_head_row = b.bias_head_row;
+            B.bias_ldq = b.bias_ldq;
+            B.bias_rstride = b.bias_rstride;
+            B.bias_run = b.bias_run;
+        }
         int64_t n_keys = 0;
         for (int r = 0; r < b.n_runs; ++r) {
             const vgx_kv_run &R = b.runs[r];

@@ -697,9 +697,11 @@ class VAULTv3ForCausalLM:
         lo, mid, hi = control.biased_layers(self.cfg.n_layers)
         return st.bias_early if lo <= li < mid else st.bias_late if mid <= li < hi else None
 
-    def _layers(self, x: torch.Tensor, st: VAULTv3State, pos: int, seg_active: bool) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    def _layers(self, x: torch.Tensor, st: VAULTv3State, pos: int, seg_active: bool,
+                bias: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
         """Chunk prefill (batch 1): run all layers in place on x [N, d], the N tokens at slots [0, N)
-        of chunk pos // W (src/vault_v3_model.py:2045-2096)."""
+        of chunk pos // W (src/vault_v3_model.py:2045-2096); ``bias``: the chunk's (early, late)
+        resonance bias rows on the segment run (_chunk_bias), applied in the biased layers."""
         cfg, w = self.cfg, self.w
         W, H, G, D, d = cfg.window, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_model
         N = x.shape[0]
@@ -716,6 +718,10 @@ class VAULTv3ForCausalLM:
         hbuf = torch.empty(N, cfg.d_ff, dtype=torch.float32, device=self.device)
         scale = 1.0 / math.sqrt(D)
         mfma = D == 128 and H // G in (1, 2, 4, 6, 8)
+        lo, mid, hi = control.biased_layers(cfg.n_layers)
+        head_rows = [int(k) - 1 for k in self.head_class]          # arch heads row 0, sup heads row 1
+        if bias is not None and not (mfma and n_seg == bias[1].shape[2]):
+            raise RuntimeError("chunk bias needs the MFMA attention and one bias column per bank slot")
         for li, lw in enumerate(w.layers):
             if seg_active and li in cfg.seg_layers:
                 j = cfg.seg_layers.index(li)
@@ -738,8 +744,11 @@ class VAULTv3ForCausalLM:
             if mfma:
                 # block attention on MFMA (fp32 cache: K / V as bf16 hi + lo; runs are the [G, n, D] views
                 # of batch entry 0)
-                ops.attn_prefill([{"q": q, "out": ao, "runs": [(k_[0], v_[0]) for k_, v_ in spans],
-                                   "causal_base": 0}], H, G, scale)
+                blk = {"q": q, "out": ao, "runs": [(k_[0], v_[0]) for k_, v_ in spans], "causal_base": 0}
+                if bias is not None and lo <= li < hi:
+                    blk.update(bias=bias[0] if li < mid else bias[1], bias_head_row=head_rows,
+                               bias_run=1 if n_sk else 0)
+                ops.attn_prefill([blk], H, G, scale)
             else:
                 ops.attn_decode(q, spans, out=ao, scale=scale, ws=self.ws, causal_base=0)
             ops.qlinear(lw.wo, ao.view(N, HD), out=x, accumulate=True)
@@ -901,10 +910,14 @@ class VAULTv3ForCausalLM:
             if ci > 0:
                 self._boundary(st, seg_active)
             ch = ids_all[r0:r1]
+            bias = None
             if st.res is not None:
                 st.tok_cur_h[:clen] = ch.numpy().astype(np.uint32)
-                if self._chunk_resonates(st, r0, clen, seg_active, n_pin_at):
-                    # resonance active somewhere in the chunk: the step path, token by token
+                if self._mfma_prefill():
+                    # the per-position resonance biases of the chunk, added by the chunk attention
+                    bias = self._chunk_bias(st, r0, clen, seg_active, n_pin_at)
+                elif self._chunk_resonates(st, r0, clen, seg_active, n_pin_at):
+                    # shapes the MFMA attention does not take: the step path, token by token
                     rows = [self._advance(st, ch[j:j + 1], boundary=False) for j in range(clen)]
                     outs.append(("l", torch.cat(rows, dim=0)))
                     continue
@@ -923,7 +936,7 @@ class VAULTv3ForCausalLM:
                 st.seg_cur_ids[:clen].copy_(torch.from_numpy(seg))
                 st.ctrl[ops.L.SEG_CUR_ID:ops.L.SEG_LEN + 1].copy_(torch.tensor([s_loc, slen], dtype=torch.int32))
             x = ops.embed(self.w.embed, ch.to(self.device), pad_row=0)
-            x, feats = self._layers(x, st, pos=r0, seg_active=seg_active)
+            x, feats = self._layers(x, st, pos=r0, seg_active=seg_active, bias=bias)
             if seg_active:
                 self._score(st, feats, T=clen, c0=0, first=not st.ema_ready)
                 st.ema_ready = True
@@ -931,12 +944,50 @@ class VAULTv3ForCausalLM:
                     for j in range(clen):
                         if self._spoofed(st, j, r0 + j, n_pin_at(r0 + j)):
                             st.sc_cur[j:j + 1].fill_(-1.0e30)
+            if st.res is not None:
+                # the resonance fields as the step loop leaves them after the chunk's last token
+                st.pos = r1 - 1
+                self._resonance(st, clen - 1, r1 - 1, seg_active)
             outs.append(("h", x if all_logits else x[-1:]))
         st.pos = L
         if not all_logits:
             kind, t = outs[-1]
             return (t[-1:] if kind == "h" else None), st, (None if kind == "h" else t[-1:])
         return None, st, torch.cat([self._logits(t) if kind == "h" else t for kind, t in outs], dim=0)
+
+    def _mfma_prefill(self) -> bool:
+        """Whether the chunk attention runs on the MFMA prefill kernel (head_dim 128, 1-8 heads per group)."""
+        cfg = self.cfg
+        return cfg.head_dim == 128 and cfg.n_heads // cfg.n_kv_heads in (1, 2, 4, 6, 8)
+
+    def _chunk_bias(self, st: VAULTv3State, r0: int, clen: int, seg_active: bool, n_pin_at):
+        """The chunk-level resonance bias (src/vault_v3_model.py:1718-1793): row j holds the biases the
+        step rule gives position r0 + j (runtime/vault3.c:1426-1786, 1976-1988) over the segment bank,
+        as (early, late) fp32 tensors [clen, 2, M]: row 0 for the arch heads, row 1 for the sup heads;
+        late = (arch, sup), early = (hop1, hop1) at mode-2 positions, else as late; zero rows where the
+        mode is 0.  None when no position of the chunk resonates."""
+        if not seg_active or r0 < 2 * self.cfg.window or st.res.mem_cnt == 0:
+            return None
+        M = st.res.mem_cnt
+        late = np.zeros((clen, 2, M), dtype=np.float32)
+        early = None
+        for j in range(clen):
+            mode = st.res.update(st.tok_prev_h, st.tok_cur_h, j, r0 + j, n_pin_at(r0 + j))
+            if not mode:
+                continue
+            late[j, 0] = st.res.arch[:M]
+            late[j, 1] = st.res.sup[:M]
+            if mode == 2:
+                if early is None:
+                    early = late.copy()
+                early[j, 0] = st.res.hop1[:M]
+                early[j, 1] = st.res.hop1[:M]
+            elif early is not None:
+                early[j] = late[j]
+        if not late.any() and early is None:
+            return None
+        lt = torch.from_numpy(late).to(self.device)
+        return (lt if early is None else torch.from_numpy(early).to(self.device)), lt
 
     def _chunk_resonates(self, st: VAULTv3State, r0: int, clen: int, seg_active: bool, n_pin_at) -> bool:
         """Whether the query resonance is active at some position of the chunk [r0, r0 + clen) (the

@@ -461,6 +461,19 @@ def qkv_rope_batch(wq: Optional[QWeight], bq: Optional[torch.Tensor], wkv: QWeig
         "vgx_qkv_rope_batch")
 
 
+_HEAD_ROWS: dict = {}
+
+
+def _head_rows(rows: tuple, device) -> torch.Tensor:
+    """Device int32 copy of a head -> bias-row map (made once per map and device)."""
+    key = (rows, str(device))
+    t = _HEAD_ROWS.get(key)
+    if t is None:
+        t = torch.tensor(rows, dtype=torch.int32, device=device)
+        _HEAD_ROWS[key] = t
+    return t
+
+
 def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
     """MFMA prefill attention for up to 8 query blocks per launch (more are split).
 
@@ -468,7 +481,9 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
     ``out`` [n_q, H, D] view, fp32 or bf16 (one dtype for all blocks), ``runs``: list of (K, V) views
     [G, n, D] (bf16, or fp32 entering the MFMAs as bf16 hi + lo; one dtype for all runs; D contiguous,
     any row and group stride), ``causal_base``: -1, or b >= 0 making the last run causal (query t sees
-    its keys j <= b + t)."""
+    its keys j <= b + t).  Optional ``bias`` fp32 [n_q, R, >= run length] with ``bias_head_row`` (H
+    ints: the bias row of head h, < 0: none) and ``bias_run``: query t of head h adds
+    bias[t, bias_head_row[h], j] to its score with key j of that run."""
     lib = L.load()
     if not blocks:
         return
@@ -502,6 +517,19 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
                 keep.append((k, v))
             arr[i] = L.AttnBlock(q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), out.stride(0), out.stride(1),
                                  q.shape[0], int(b.get("causal_base", -1)), len(runs), ra)
+            if b.get("bias") is not None:
+                bias, rows, run = b["bias"], tuple(int(r) for r in b["bias_head_row"]), int(b["bias_run"])
+                _need(bias, torch.float32, "bias")
+                if bias.dim() != 3 or bias.shape[0] < q.shape[0] or bias.stride(-1) != 1 or len(rows) != H:
+                    raise ValueError("bias must be [n_q, head rows, keys] with unit key stride, bias_head_row H rows")
+                if not 0 <= run < len(runs) or bias.shape[2] < runs[run][0].shape[1]:
+                    raise ValueError("bias_run must name a run no longer than the bias rows")
+                if max(rows) >= bias.shape[1]:
+                    raise ValueError("bias_head_row names a row the bias does not have")
+                rows_dev = _head_rows(rows, bias.device)
+                arr[i].bias, arr[i].bias_head_row = bias.data_ptr(), rows_dev.data_ptr()
+                arr[i].bias_ldq, arr[i].bias_rstride, arr[i].bias_run = bias.stride(0), bias.stride(1), run
+                keep.append((bias, rows_dev))
         qd = L.BF16 if qdt == torch.bfloat16 else L.F32
         od = L.BF16 if odt == torch.bfloat16 else L.F32
         L.check(lib.vgx_attn_prefill(KV_DTYPES[kvdt], qd, od, arr, len(part), H, G, D, scale,
