@@ -15,8 +15,9 @@ set-up.
 Prints one JSON line: tokens/s, plus the roofline of the step's largest kernel by time (batch-1 decode
 attention over the step's four KV spans, fp32 KV, with its split merge), secondary kernel figures
 (the fused gate/up SwiGLU Q4_0 GEMV, Q8_0/Q4_0 GEMV at the model's shapes, batched bf16 decode
-attention at 3584 keys, prefill attention and GEMMs, batch-32 decode) and the reference C runtime
-timed on the host cores.
+attention at 3584 keys, prefill attention and GEMMs, batch-32 decode, and the same model with token
+strings: a 16K-token multi-turn ChatML prefill and decode with the resonance rules active) and the
+reference C runtime timed on the host cores.
 """
 from __future__ import annotations
 
@@ -347,6 +348,85 @@ def batched_decode(model, batch: int = 32, steps: int = 16, warmup: int = 4):
             "tokens_per_s": round(batch * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 3)}
 
 
+CHAT_TOKENS = 16384
+CHAT_KINDS = ("ids", "hop", "rollback", "clause", "words", "id")
+
+
+def chat_prompt(cfg, toks, n_tokens: int = CHAT_TOKENS) -> list:
+    """A multi-turn ChatML prompt of n_tokens: conversations (system line, a user turn of key / value
+    lines, an assistant turn, a user question about earlier lines) back to back, ~150 tokens each, so
+    that user turns end in every 1024-token chunk; it ends with a question and the assistant header."""
+    from tests import modelgen
+    ids, i = [], 0
+    while True:
+        conv = modelgen.conversation(cfg, toks, CHAT_KINDS[i % len(CHAT_KINDS)], seed=i, answer=20)
+        if len(ids) + len(conv) - 20 >= n_tokens:
+            q = modelgen.conversation(cfg, toks, "ids", seed=i, answer=0)
+            return ids[:n_tokens - len(q)] + q
+        ids += conv
+        i += 1
+
+
+def chat_figures(model, decode_steps: int = 48):
+    """The 1.54B model with token strings (a synthetic word vocabulary over the 151665 ids: ChatML
+    specials, key / value words, break-tier punctuation), so the resonance, quarantine and segment
+    rules all run: a CHAT_TOKENS-token multi-turn ChatML prefill (batch 1, fp32 KV, segment memory
+    on), then decode_steps greedy steps fed by host ids (the logits' argmax read on the host) and,
+    after the same prefill again, fed by device ids (ops.argmax).  Reports prefill tokens/s, the
+    chunks whose attention carried a resonance bias, and per-step decode rates (medians, each step
+    timed between synchronisations) of the steps with the resonance bias on and of the others."""
+    import copy
+    import torch
+    from tests import modelgen
+    from vault_amd import ops
+    from vault_amd.model import VAULTv3ForCausalLM
+    from vault_amd.tokens import TokenTable
+    cfg = model.cfg
+    toks, bmap = modelgen.word_vocab(cfg)
+    w = copy.copy(model.w)
+    w.tokens = TokenTable(toks, bmap, cfg.vocab_size)
+    m = VAULTv3ForCausalLM(w, kv_dtype=torch.float32)
+    ids = torch.tensor([chat_prompt(cfg, toks)])
+    biased = []
+    chunk_bias = m._chunk_bias
+
+    def counted(*a, **k):
+        r = chunk_bias(*a, **k)
+        biased.append(r is not None)
+        return r
+
+    m._chunk_bias = counted
+    m.prefill(ids[:, :2048])                          # warm-up (library loads, workspaces)
+    out = {"config": f"{ids.shape[1]}-token multi-turn ChatML prompt, batch 1, fp32 KV, segment memory on, "
+                     f"token strings (resonance / quarantine rules active)"}
+    for leg in ("host_ids", "device_ids"):
+        biased.clear()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        last, st = m.prefill(ids)
+        torch.cuda.synchronize()
+        t_pre = time.perf_counter() - t0
+        if leg == "host_ids":
+            out["prefill_tokens_per_s"] = round(ids.shape[1] / t_pre, 1)
+            out["prefill_chunks_biased"] = f"{sum(biased)} of {len(biased)}"
+        tok = torch.tensor([int(last[0].argmax())]) if leg == "host_ids" else ops.argmax(last)
+        times = {True: [], False: []}
+        for _ in range(decode_steps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            logits = m.step(tok, st)
+            tok = torch.tensor([int(logits[0].argmax())]) if leg == "host_ids" else ops.argmax(logits)
+            torch.cuda.synchronize()
+            times[st.seg_bias_mode > 0].append(time.perf_counter() - t0)
+        # medians: the first step of each graph configuration captures it (an outlier, not a rate)
+        for on, name in ((True, "resonating"), (False, "quiet")):
+            t = sorted(times[on])
+            out[f"decode_{leg}_{name}_steps"] = len(t)
+            if t:
+                out[f"decode_{leg}_{name}_tokens_per_s"] = round(1.0 / t[len(t) // 2], 1)
+    return out
+
+
 PREFILL_FLOPS = 90.22e9   # unmasked (query, key) pairs x 4 x D x H for L = 8192, W = 1024, 512 sinks
 
 
@@ -501,7 +581,7 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for per-kernel profiles of the step)")
     ap.add_argument("--figures", choices=("gemv", "attn_decode", "attn_decode_b1", "attn_prefill", "gemm_prefill",
-                                          "roofline", "gateup", "decode_batch32", "lm_head"),
+                                          "roofline", "gateup", "decode_batch32", "lm_head", "chat"),
                     help="only one set of kernel figures, printed as JSON (for per-kernel profiles)")
     ap.add_argument("--pmc", action="store_true",
                     help="only run the launches the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count")
@@ -541,6 +621,12 @@ def main() -> int:
         del tensors
         print(json.dumps({"decode_batch32": batched_decode(model)}), flush=True)
         return 0
+    if args.figures == "chat":
+        cfg = model_config()
+        model, tensors = build_model(cfg, dev, torch.float32)
+        del tensors
+        print(json.dumps({"chat": chat_figures(model)}), flush=True)
+        return 0
     if args.figures == "lm_head":
         # the 151665 x 1536 rows of the gemv figures at batch 1 (for the streaming kernel's profiles)
         print(json.dumps({"lm_head": gemv_figures(dev, batches=(1,), shapes=[(151665, 1536)])}), flush=True)
@@ -577,6 +663,7 @@ def main() -> int:
         kernels["gemm_prefill"] = gemm_figures(dev)
         if args.batch == 1:
             kernels["decode_batch32"] = batched_decode(model)
+            kernels["chat"] = chat_figures(model)
         _log("kernel figures done")
     cpu = None
     if not args.no_cpu and args.batch == 1 and args.kv == "fp32":
