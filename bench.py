@@ -141,8 +141,9 @@ ATTN_ALGO_BYTES = sum(ATTN_LENS) * 2 * 128 * 4 * 2 + 2 * 12 * 128 * 4   # K and 
 def attention_kernel(dev, reps: int = 20):
     """The roofline kernel: batch-1 decode attention of the step, fp32 KV (the state dtype), 12 query /
     2 KV heads, D = 128, 3584 keys in the step's four spans (512 sinks | 1024 segment slots | 1024
-    previous | 1024 current window).  One call = attn_decode_kernel over 56 key splits x 2 KV groups +
-    attn_merge_kernel.  Algorithmic bytes per call: K and V once (7,340,032 B) + q + out = 7,352,320 B.
+    previous | 1024 current window).  One call = attn_decode_b1_kernel over 56 key splits of 64 keys x
+    2 KV groups (112 workgroups of 8 waves) + b1_merge_kernel (12 heads x 4 dim quarters).  Algorithmic
+    bytes per call: K and V once (7,340,032 B) + q + out = 7,352,320 B.
     A graph replays one call over each of ATTN_COPIES KV copies (as the 28 layers of a step stream
     theirs); time per call from HIP events on the replay stream."""
     import torch
@@ -162,8 +163,8 @@ def attention_kernel(dev, reps: int = 20):
     us = graph_time_us(run, len(sets), reps=reps)
     # the same calls over one KV copy (7.3 MB, resident in the last-level cache): reported separately
     warm = graph_time_us(lambda: [ops.attn_decode(q, base, out=out, ws=ws) for _ in sets], len(sets), reps=reps)
-    return {"kernel": "attn_decode_kernel<fp32 KV, 6 heads per KV group, D/16 = 8, 4 waves, 4 keys per DPP row> "
-                      "+ attn_merge_kernel (batch 1, 12 q / 2 KV heads, D = 128, 3584 keys)",
+    return {"kernel": "attn_decode_b1_kernel<fp32 KV, 6 heads per KV group, 8 waves, 2 key blocks per wave, "
+                      "spans of whole key blocks> + b1_merge_kernel (batch 1, 12 q / 2 KV heads, D = 128, 3584 keys)",
             "calls": reps * len(sets), "avg_us": us, "bytes_per_launch": ATTN_ALGO_BYTES,
             "gbs": ATTN_ALGO_BYTES / us / 1e3, "cache_resident_us": round(warm, 3)}
 
@@ -538,7 +539,7 @@ def pmc_report(fetch_csv: str, write_csv: str) -> None:
     """Markdown summary of the two PMC runs: per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the two
     kernels of the roofline call and of the calibration copy, the copy's bytes / counter factor, and
     the scaled HBM traffic per call (the figure ``roofline.traffic`` reports)."""
-    kerns = (("attn_decode_kernel<0, 6, 8, 4, 4, 0>", "split attention"), ("attn_merge_kernel", "split merge"))
+    kerns = (("attn_decode_b1_kernel<0, 6, 8, 2, 0, true>", "split attention"), ("b1_merge_kernel", "split merge"))
     copy = "neg_kernel"
     fc, nc = _pmc_avg(fetch_csv, "FETCH_SIZE", copy)
     wc, _ = _pmc_avg(write_csv, "WRITE_SIZE", copy)

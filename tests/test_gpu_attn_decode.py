@@ -58,10 +58,11 @@ def test_decode_batched_config3(dev, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("B", [16, 64])
+@pytest.mark.parametrize("B", [1, 2, 16, 64])
 def test_decode_split_tickets_reset_between_calls(dev, dtype, B):
     """Batch 64 (4 splits per (b, g)): the last workgroup of a pair merges its splits and puts the
-    pair's ticket back to zero; batch 16 (16 splits) merges with the second launch.  Five calls on
+    pair's ticket back to zero; batch 16 (16 splits) merges with the second launch; batch 1 and 2
+    (56 splits of 64 keys per pair, one launch) merge in the pair's last workgroup.  Five calls on
     one workspace (and a graph replayed three times) give the same bits and match the oracle; the
     ticket words are zero afterwards."""
     rng = np.random.default_rng(B)
@@ -91,6 +92,36 @@ def test_decode_split_tickets_reset_between_calls(dev, dtype, B):
         torch.cuda.synchronize()
         assert torch.equal(out, outs[0])
     assert int(ws.buf[:B * G * 4].view(torch.int32).abs().sum()) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B", [1, 2])
+@pytest.mark.parametrize("m_live,c_live", [(700, 300), (1024, 1024), (0, 1), (5, 63)])
+def test_decode_step_shape_bias_and_device_lengths(dev, dtype, B, m_live, c_live):
+    """The decode step's spans at batch 1 and 2 (the one-launch kernel for few (batch, group) pairs):
+    512 sinks | a segment bank of capacity 1024 with m_live slots counted on the device, with a bias per
+    head on it (zero rows for the unbiased heads, -1e30 entries) | 1024 previous | the current window
+    with c_live rows counted on the device.  Rows past the device counts hold NaN, which must not reach
+    the output."""
+    rng = np.random.default_rng(m_live * 3 + c_live + B)
+    H, G, D = 12, 2, 128
+    caps = [512, 1024, 1024, 1024]
+    sp = _spans(rng, B, G, D, caps, dtype, dev)
+    for i, n in ((1, m_live), (3, c_live)):
+        sp[i][0][:, :, n:] = float("nan")
+        sp[i][1][:, :, n:] = float("nan")
+    m_dev = torch.tensor([m_live], dtype=torch.int32, device=dev)
+    c_dev = torch.tensor([c_live], dtype=torch.int32, device=dev)
+    spans = [sp[0], (sp[1][0], sp[1][1], m_dev), sp[2], (sp[3][0], sp[3][1], c_dev)]
+    q = rng.standard_normal((B, H, D)).astype(np.float32)
+    bias = (rng.standard_normal((H, 1024)) * 2.0).astype(np.float32)
+    bias[:2] = 0.0
+    bias[2, 3:9] = -1e30
+    out = ops.attn_decode(torch.from_numpy(q).to(dev), spans, bias=torch.from_numpy(bias).to(dev), bias_span=1)
+    live = _np([sp[0], (sp[1][0][:, :, :m_live], sp[1][1][:, :, :m_live]), sp[2],
+                (sp[3][0][:, :, :c_live], sp[3][1][:, :, :c_live])])
+    ref = oatt.decode(q, live, bias=bias[:, :m_live], bias_span=1)
+    assert np.abs(out.cpu().numpy() - ref).max() <= TOL[dtype]
 
 
 @pytest.mark.parametrize("grp,D", [(1, 64), (2, 128), (4, 64), (6, 128), (8, 128)])

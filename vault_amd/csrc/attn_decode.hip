@@ -764,6 +764,486 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *__restrict
     out[((int64_t)b * H + h) * D + d] = a * inv_l;
 }
 
+// Few (batch, group) pairs (the batch-1 decode step), D = 128: one split of 4 KB NW keys per
+// workgroup, every wave on one 4 KB-key tile, so each wave's serial chain is short and many splits
+// keep most CUs streaming the keys.
+//   q        staged once per workgroup in LDS (scaled), read by every DPP row;
+//   scores   the wave's 4 DPP rows take KB keys each (a key row over the 16 lanes of a row: dims
+//            4 l .. + 3 and 64 + 4 l .. + 3 of lane l), q . k summed over the row by DPP; lane hh of a
+//            row writes head hh's score to LDS;
+//   softmax  over the workgroup's keys per head (one wave per head), exactly: max, exp, sum;
+//   P V      each lane weights its own K/V rows' V by the probabilities (read back from LDS), the 4
+//            rows of a wave are summed by two lane-swap steps, the waves through LDS in a fixed order;
+//   splits   MERGE: every workgroup stores (m, l, acc) with agent-scope stores and takes a ticket; the
+//            last workgroup of the pair merges every split (agent-scope vector loads issued at once,
+//            weights e^{m_s - M} / L), then resets the ticket (the ordering argument of ticket_merge).
+//            Otherwise the partials are plain stores and b1_merge_kernel, a second launch spread over
+//            (head, 32 dims) workgroups, merges them.
+// Keys are dealt by capacity over the concatenated spans; a key at or past its span's device length, or
+// past the last span, gets score -inf and weight 0 (its V row is zeroed) and reads an existing row.
+constexpr int kB1MaxSplits = 128;
+constexpr int kB1MaxPairs = 4;               // (batch, group) pairs the kernel takes (beyond: the tiled kernels)
+constexpr int kB1Chunk = 32;                 // split partials one merging thread requests at once
+constexpr int kSC1 = 16;                     // the sc1 cache-policy bit of a buffer access: agent coherent
+
+// One lane's dims 4 l .. + 3 (at elem_off) and 64 + 4 l .. + 3 of a key row, as fp32.
+template <int KV>
+__device__ __forceinline__ void load_quads(const void *base, int64_t elem_off, float (&f)[8]) {
+    if constexpr (KV == VGX_F32) {
+        const float *p = static_cast<const float *>(base) + elem_off;
+        const float4 a = *reinterpret_cast<const float4 *>(p), c = *reinterpret_cast<const float4 *>(p + 64);
+        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = c.x; f[5] = c.y; f[6] = c.z; f[7] = c.w;
+    } else {
+        const uint16_t *p = static_cast<const uint16_t *>(base) + elem_off;
+        const uint2 a = *reinterpret_cast<const uint2 *>(p), c = *reinterpret_cast<const uint2 *>(p + 64);
+        f[0] = __uint_as_float(a.x << 16); f[1] = __uint_as_float(a.x & 0xFFFF0000u);
+        f[2] = __uint_as_float(a.y << 16); f[3] = __uint_as_float(a.y & 0xFFFF0000u);
+        f[4] = __uint_as_float(c.x << 16); f[5] = __uint_as_float(c.x & 0xFFFF0000u);
+        f[6] = __uint_as_float(c.y << 16); f[7] = __uint_as_float(c.y & 0xFFFF0000u);
+    }
+}
+
+// Partials of the kernel: acc [pair][split][head][128] floats, then (m, l) [pair][split][head][2] from
+// float offset ml_off (the acc region rounded up to 256 bytes).
+inline int64_t b1_ml_off(int64_t pairs, int64_t grp, int ns) { return (pairs * ns * grp * 128 + 63) / 64 * 64; }
+inline int64_t b1_part_bytes(int64_t pairs, int64_t grp, int ns) {
+    return (b1_ml_off(pairs, grp, ns) + pairs * ns * grp * 2) * (int64_t)sizeof(float);
+}
+
+template <int KV, int GRP, int NW, int KB, int MERGE, bool ALIGNED>
+__global__ __launch_bounds__(64 * NW) void attn_decode_b1_kernel(
+    const float *__restrict__ q, int64_t ldq, SpanArgs sp, const float *__restrict__ bias, int64_t bias_hstride,
+    int bias_span, float *__restrict__ out, float *__restrict__ part, int64_t ml_off, int *__restrict__ cnt, int H,
+    int G, float scale, int64_t n_tot, int n_splits) {
+    constexpr int D = 128, NT = 64 * NW, KWV = 4 * KB, KWG = NW * KWV;
+    constexpr int KPL = (KWG + 63) / 64;               // keys per lane in the softmax
+    constexpr int NTASK = GRP * (D / 4);               // merge tasks: (head, 4 dims)
+    constexpr int NSUB = NT / NTASK;                   // threads per merge task
+    static_assert(!MERGE || NSUB >= 1, "a thread per merge task");
+    __shared__ __align__(16) float qs[GRP][D];
+    constexpr int RB = NW * GRP * D > 2 * GRP * kB1MaxSplits + 4 * NSUB * NTASK ? NW * GRP * D
+                                                                                  : 2 * GRP * kB1MaxSplits + 4 * NSUB * NTASK;
+    __shared__ float sc[GRP + 1][KWG];                // row GRP: the writes of lanes with no head
+    __shared__ __align__(16) float redbuf[RB];         // per-wave P V sums; the merge's scratch after
+    float (*red)[GRP][D] = reinterpret_cast<float (*)[GRP][D]>(redbuf);
+    __shared__ float mh[GRP], lh[GRP];
+    __shared__ int last;
+
+    const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, row = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // span bases by capacity
+    int64_t base[5];
+    base[0] = 0;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) base[s + 1] = base[s] + (s < sp.n ? sp.len[s] : 0);
+
+    // Requests first, in the order they are used: q (staged to LDS before the first barrier), V of the
+    // wave's KWV keys (lane l: dims 2 l, 2 l + 1 of each, so the P V product needs no exchange between
+    // lanes), K of this lane's KB keys in the DPP-row layout.  Device lengths and the bias after them.
+    float4 qv[(GRP * 32 + 64 * NW - 1) / (64 * NW)];
+#pragma unroll
+    for (int u = 0; u < (GRP * 32 + 64 * NW - 1) / (64 * NW); ++u) {
+        const int i = tid + u * 64 * NW;
+        if (i < GRP * 32) qv[u] = *reinterpret_cast<const float4 *>(q + (int64_t)b * ldq + (int64_t)g * GRP * D + 4 * i);
+    }
+    // row 0 of every span for this (batch, group)
+    constexpr int ESZ = KV == VGX_F32 ? 4 : 2;
+    const char *kp[4], *vp[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int64_t o = ((int64_t)b * sp.bstride[s] + (int64_t)g * sp.gstride[s]) * ESZ;
+        kp[s] = static_cast<const char *>(sp.k[s]) + o;
+        vp[s] = static_cast<const char *>(sp.v[s]) + o;
+    }
+    // V: lane l holds dims 4 (l % 32) .. + 3 of the wave's keys 2 j + l / 32 (j < KWV / 2): every load
+    // instruction reads two whole rows.  K: this lane's KB keys in the DPP-row layout.  ALIGNED (every
+    // span's capacity a multiple of KWV): a wave's keys lie in one span, found once per wave.
+    constexpr int KVH = KWV / 2;
+    float vf[KVH][4];
+    int vs_[KVH];
+    int64_t vl_[KVH];
+    const int half = lane >> 5, l32 = lane & 31;
+    int ks[KB];
+    int64_t kl[KB];
+    float kf[KB][8];
+    if constexpr (ALIGNED) {
+        const int64_t kw0 = (int64_t)split * KWG + wave * KWV;                     // wave-uniform
+        const bool live = kw0 < n_tot;                                             // then all KWV keys are
+        int s = 0;
+#pragma unroll
+        for (int t = 1; t < 4; ++t) s = min(kw0, n_tot - 1) >= base[t] ? t : s;
+        s = __builtin_amdgcn_readfirstlane(s);
+        const int64_t r0 = live ? kw0 - pick4(s, base[0], base[1], base[2], base[3]) : 0;
+        const char *vrow = pick4(s, vp[0], vp[1], vp[2], vp[3]) + r0 * D * ESZ;
+        const char *krow = pick4(s, kp[0], kp[1], kp[2], kp[3]) + r0 * D * ESZ;
+#pragma unroll
+        for (int j = 0; j < KVH; ++j) {
+            vs_[j] = live ? s : -1;
+            vl_[j] = r0 + 2 * j + half;
+            const char *vr = vrow + (int64_t)(2 * j + half) * D * ESZ;
+            if constexpr (KV == VGX_F32) {
+                const float4 t = reinterpret_cast<const float4 *>(vr)[l32];
+                vf[j][0] = t.x; vf[j][1] = t.y; vf[j][2] = t.z; vf[j][3] = t.w;
+            } else {
+                const uint2 t = reinterpret_cast<const uint2 *>(vr)[l32];
+                vf[j][0] = __uint_as_float(t.x << 16); vf[j][1] = __uint_as_float(t.x & 0xFFFF0000u);
+                vf[j][2] = __uint_as_float(t.y << 16); vf[j][3] = __uint_as_float(t.y & 0xFFFF0000u);
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < KB; ++kk) {
+            ks[kk] = live ? s : -1;
+            kl[kk] = r0 + row * KB + kk;
+            load_quads<KV>(krow, (int64_t)(row * KB + kk) * D + 4 * l16, kf[kk]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < KVH; ++j) {
+            const int64_t gk = (int64_t)split * KWG + wave * KWV + 2 * j + half;
+            const int64_t ga = min(gk, n_tot - 1);
+            int s = 0;
+#pragma unroll
+            for (int t = 1; t < 4; ++t) s = ga >= base[t] ? t : s;
+            const int64_t lr = ga - pick4(s, base[0], base[1], base[2], base[3]);
+            vs_[j] = gk < n_tot ? s : -1;
+            vl_[j] = lr;
+            const char *vrow = pick4(s, vp[0], vp[1], vp[2], vp[3]) + lr * D * ESZ;
+            if constexpr (KV == VGX_F32) {
+                const float4 t = reinterpret_cast<const float4 *>(vrow)[l32];
+                vf[j][0] = t.x; vf[j][1] = t.y; vf[j][2] = t.z; vf[j][3] = t.w;
+            } else {
+                const uint2 t = reinterpret_cast<const uint2 *>(vrow)[l32];
+                vf[j][0] = __uint_as_float(t.x << 16); vf[j][1] = __uint_as_float(t.x & 0xFFFF0000u);
+                vf[j][2] = __uint_as_float(t.y << 16); vf[j][3] = __uint_as_float(t.y & 0xFFFF0000u);
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < KB; ++kk) {
+            const int64_t gk = (int64_t)split * KWG + wave * KWV + row * KB + kk;
+            const int64_t ga = min(gk, n_tot - 1);          // an existing key for the address
+            int s = 0;
+#pragma unroll
+            for (int t = 1; t < 4; ++t) s = ga >= base[t] ? t : s;
+            ks[kk] = gk < n_tot ? s : -1;
+            kl[kk] = ga - pick4(s, base[0], base[1], base[2], base[3]);
+            load_quads<KV>(pick4(s, kp[0], kp[1], kp[2], kp[3]), kl[kk] * D + 4 * l16, kf[kk]);
+        }
+    }
+    // bias rows of the biased span (clamped to its last column; used only where it applies)
+    float bv[GRP][KB];
+    if (bias != nullptr) {
+        const int64_t bl = sp.len[bias_span] - 1;
+#pragma unroll
+        for (int kk = 0; kk < KB; ++kk)
+#pragma unroll
+            for (int hh = 0; hh < GRP; ++hh)
+                bv[hh][kk] = bias[((int64_t)g * GRP + hh) * bias_hstride + min(kl[kk], bl)];
+    }
+    // q -> LDS, scaled
+#pragma unroll
+    for (int u = 0; u < (GRP * 32 + 64 * NW - 1) / (64 * NW); ++u) {
+        const int i = tid + u * 64 * NW;
+        if (i < GRP * 32)
+            *reinterpret_cast<float4 *>(&qs[0][0] + 4 * i) =
+                make_float4(qv[u].x * scale, qv[u].y * scale, qv[u].z * scale, qv[u].w * scale);
+    }
+    // effective span lengths (device lengths) and the keys' validity
+    int64_t eff[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        eff[s] = s < sp.n ? sp.len[s] : 0;
+        if (s < sp.n && sp.dyn_len[s] != nullptr) eff[s] = min(eff[s], (int64_t)*sp.dyn_len[s]);
+    }
+    bool vok[KVH], valid[KB];
+#pragma unroll
+    for (int j = 0; j < KVH; ++j) vok[j] = vs_[j] >= 0 && vl_[j] < pick4(max(vs_[j], 0), eff[0], eff[1], eff[2], eff[3]);
+#pragma unroll
+    for (int kk = 0; kk < KB; ++kk) {
+        valid[kk] = ks[kk] >= 0 && kl[kk] < pick4(max(ks[kk], 0), eff[0], eff[1], eff[2], eff[3]);
+        const bool biased = bias != nullptr && valid[kk] && ks[kk] == bias_span;
+#pragma unroll
+        for (int hh = 0; hh < GRP; ++hh) bv[hh][kk] = biased ? bv[hh][kk] : 0.0f;
+    }
+    __syncthreads();
+    // scores: the GRP * KB row sums interleaved step by step (independent DPP operations between
+    // dependent ones); lane hh of each row writes head hh, lanes past the heads a spare row
+    {
+        float sv[GRP][KB];
+#pragma unroll
+        for (int hh = 0; hh < GRP; ++hh) {
+            const float4 qa = *reinterpret_cast<const float4 *>(&qs[hh][4 * l16]);
+            const float4 qc = *reinterpret_cast<const float4 *>(&qs[hh][64 + 4 * l16]);
+            const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qc.x, qc.y, qc.z, qc.w};
+#pragma unroll
+            for (int kk = 0; kk < KB; ++kk) {
+                float p = 0.0f;
+#pragma unroll
+                for (int dd = 0; dd < 8; ++dd) p = fmaf(qv[dd], kf[kk][dd], p);
+                sv[hh][kk] = p;
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < GRP; ++hh)
+#pragma unroll
+            for (int kk = 0; kk < KB; ++kk) sv[hh][kk] += dpp_f<DPP_QUAD_1032>(sv[hh][kk]);
+#pragma unroll
+        for (int hh = 0; hh < GRP; ++hh)
+#pragma unroll
+            for (int kk = 0; kk < KB; ++kk) sv[hh][kk] += dpp_f<DPP_QUAD_2301>(sv[hh][kk]);
+#pragma unroll
+        for (int hh = 0; hh < GRP; ++hh)
+#pragma unroll
+            for (int kk = 0; kk < KB; ++kk) sv[hh][kk] += dpp_f<DPP_ROW_HALF_MIRROR>(sv[hh][kk]);
+#pragma unroll
+        for (int hh = 0; hh < GRP; ++hh)
+#pragma unroll
+            for (int kk = 0; kk < KB; ++kk) sv[hh][kk] += dpp_f<DPP_ROW_MIRROR>(sv[hh][kk]);
+        const int wr = l16 < GRP ? l16 : GRP;
+#pragma unroll
+        for (int kk = 0; kk < KB; ++kk) {
+            float mine = 0.0f;
+#pragma unroll
+            for (int hh = 0; hh < GRP; ++hh) mine = l16 == hh ? sv[hh][kk] + bv[hh][kk] : mine;
+            sc[wr][wave * KWV + row * KB + kk] = valid[kk] ? mine : -INFINITY;
+        }
+    }
+    __syncthreads();
+    // softmax of head hh over the workgroup's keys
+    for (int hh = wave; hh < GRP; hh += NW) {
+        float x[KPL];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < KPL; ++u) {
+            x[u] = lane + 64 * u < KWG ? sc[hh][lane + 64 * u] : -INFINITY;
+            mx = fmaxf(mx, x[u]);
+        }
+        float m = wave_max(mx);
+        float ps = 0.0f;
+        const bool none = m == -INFINITY;                // no valid key: weight 0 everywhere
+        if (none) m = kNegBig;
+#pragma unroll
+        for (int u = 0; u < KPL; ++u) {
+            const float p = none ? 0.0f : __expf(x[u] - m);
+            ps += p;
+            if (lane + 64 * u < KWG) sc[hh][lane + 64 * u] = p;
+        }
+        const float l = wave_sum(ps);
+        if (lane == 0) {
+            mh[hh] = m;
+            lh[hh] = l;
+        }
+    }
+    __syncthreads();
+    // P V: lane l accumulates dims 4 (l % 32) .. + 3 of every head over its half of the wave's keys (a
+    // key past its span's device length weighs 0; its V row, which may hold anything, is replaced by
+    // zeros), the halves summed by one lane swap
+#pragma unroll
+    for (int hh = 0; hh < GRP; ++hh) {
+        float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < KVH; ++j) {
+            const float p = sc[hh][wave * KWV + 2 * j + half];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a[e] = fmaf(p, vok[j] ? vf[j][e] : 0.0f, a[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[e] = xor32_sum(a[e]);
+        if (half == 0) *reinterpret_cast<float4 *>(&red[wave][hh][4 * l32]) = make_float4(a[0], a[1], a[2], a[3]);
+    }
+    __syncthreads();
+    const int64_t pair = (int64_t)b * G + g;
+    float *pa = part + (pair * n_splits + split) * GRP * D;
+    for (int t = tid; t < GRP * D; t += NT) {
+        const int hh = t / D, d = t - hh * D;
+        float a = red[0][hh][d];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) a += red[w][hh][d];
+        if (n_splits == 1) out[((int64_t)b * H + (int64_t)g * GRP + hh) * D + d] = a * (1.0f / lh[hh]);
+        else if constexpr (MERGE) __hip_atomic_store(pa + t, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else pa[t] = a;
+    }
+    if (n_splits == 1) return;
+    if (tid < GRP) {
+        float *pm = part + ml_off + ((pair * n_splits + split) * GRP + tid) * 2;
+        if constexpr (MERGE) {
+            __hip_atomic_store(pm, mh[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(pm + 1, lh[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            pm[0] = mh[tid];
+            pm[1] = lh[tid];
+        }
+    }
+    if constexpr (!MERGE) return;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");    // this thread's partial stores have completed
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(cnt + pair, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_splits - 1;
+    __syncthreads();
+    if (!last) return;
+    // MERGE 2: an agent-scope acquire (the L2 lines that may hold stale partials are invalidated), then
+    // plain loads; MERGE 1: loads that read the device-coherent level (sc1)
+    if constexpr (MERGE == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    constexpr int kLoadAux = MERGE == 2 ? 0 : kSC1;
+
+    // The last workgroup.  (m, l) of every (split, head) and the first chunk of each thread's split
+    // values are requested before any is used; tasks (head, 4 dims) with NSUB threads each, thread sub
+    // taking splits sub, sub + NSUB, ...  Buffer bounds end at the pair's partials: requests past the
+    // last split read zeros.
+    float *mm = redbuf;                           // [GRP][kB1MaxSplits] m, then weights
+    float *ll = mm + GRP * kB1MaxSplits;                 // [GRP][kB1MaxSplits] l
+    float4 *rsum = reinterpret_cast<float4 *>(ll + GRP * kB1MaxSplits);   // [NSUB][NTASK]
+    const __amdgpu_buffer_rsrc_t ars =
+        __builtin_amdgcn_make_buffer_rsrc(part + pair * n_splits * GRP * D, 0, n_splits * GRP * D * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t mrs =
+        __builtin_amdgcn_make_buffer_rsrc(part + ml_off + pair * n_splits * GRP * 2, 0, n_splits * GRP * 8, 0x00020000);
+    constexpr int NE = (GRP * kB1MaxSplits + NT - 1) / NT;
+    uint32_t mlw[NE][2];
+#pragma unroll
+    for (int u = 0; u < NE; ++u) {
+        const auto w = __builtin_amdgcn_raw_buffer_load_b64(mrs, (tid + u * NT) * 8, 0, kLoadAux);
+        mlw[u][0] = w[0];
+        mlw[u][1] = w[1];
+    }
+    const int task = tid % NTASK, sub = tid / NTASK;
+    const bool active = sub < NSUB;
+    const int th = task / (D / 4), td4 = task % (D / 4);
+    float4 vals[kB1Chunk];
+    auto request = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < kB1Chunk; ++u) {
+            const int s = c0 + sub + u * NSUB;
+            const auto w = __builtin_amdgcn_raw_buffer_load_b128(ars, (s * GRP + th) * D * 4 + td4 * 16, 0, kLoadAux);
+            vals[u] = make_float4(__uint_as_float(w[0]), __uint_as_float(w[1]), __uint_as_float(w[2]),
+                                  __uint_as_float(w[3]));
+        }
+    };
+    if (active) request(0);
+#pragma unroll
+    for (int u = 0; u < NE; ++u) {
+        const int e = tid + u * NT;                      // entry (split e / GRP, head e % GRP)
+        if (e < n_splits * GRP) {
+            const int s = e / GRP, hh = e - s * GRP;
+            mm[hh * kB1MaxSplits + s] = __uint_as_float(mlw[u][0]);
+            ll[hh * kB1MaxSplits + s] = __uint_as_float(mlw[u][1]);
+        }
+    }
+    __syncthreads();
+    // weights w_s / L per head: one wave per head, two splits per lane
+    for (int hh = wave; hh < GRP; hh += NW) {
+        const int s0 = lane, s1 = lane + 64;
+        const float m0 = s0 < n_splits ? mm[hh * kB1MaxSplits + s0] : kNegBig;
+        const float m1 = s1 < n_splits ? mm[hh * kB1MaxSplits + s1] : kNegBig;
+        const float M = wave_max(fmaxf(m0, m1));
+        const float w0 = s0 < n_splits ? __expf(m0 - M) : 0.0f;
+        const float w1 = s1 < n_splits ? __expf(m1 - M) : 0.0f;
+        const float L = wave_sum(fmaf(w0, s0 < n_splits ? ll[hh * kB1MaxSplits + s0] : 0.0f,
+                                      w1 * (s1 < n_splits ? ll[hh * kB1MaxSplits + s1] : 0.0f)));
+        const float inv = 1.0f / L;
+        if (s0 < n_splits) mm[hh * kB1MaxSplits + s0] = w0 * inv;
+        if (s1 < n_splits) mm[hh * kB1MaxSplits + s1] = w1 * inv;
+    }
+    __syncthreads();
+    float4 a4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (active) {
+        for (int c0 = 0; c0 < n_splits; c0 += kB1Chunk * NSUB) {
+            if (c0) request(c0);
+#pragma unroll
+            for (int u = 0; u < kB1Chunk; ++u) {
+                const int s = c0 + sub + u * NSUB;
+                if (s < n_splits) {
+                    const float w = mm[th * kB1MaxSplits + s];
+                    a4.x = fmaf(w, vals[u].x, a4.x);
+                    a4.y = fmaf(w, vals[u].y, a4.y);
+                    a4.z = fmaf(w, vals[u].z, a4.z);
+                    a4.w = fmaf(w, vals[u].w, a4.w);
+                }
+            }
+        }
+        rsum[sub * NTASK + task] = a4;
+    }
+    __syncthreads();
+    if (active && sub == 0) {
+#pragma unroll
+        for (int u = 1; u < NSUB; ++u) {
+            const float4 r = rsum[u * NTASK + task];
+            a4.x += r.x; a4.y += r.y; a4.z += r.z; a4.w += r.w;
+        }
+        *reinterpret_cast<float4 *>(out + ((int64_t)b * H + (int64_t)g * GRP + th) * D + td4 * 4) = a4;
+    }
+    if (tid == 0) __hip_atomic_store(cnt + pair, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The second launch of the kernel above (partials as plain stores): one wave per (batch, head, 32 dims).
+// Lane l takes float4 l & 7 of the 32 dims over splits l >> 3, + 8, ...; (m, l) of split = lane (two per
+// lane up to 128 splits); all requested before any is used, as unconditional buffer loads (requests
+// past the last split read zeros), so the loads stay in flight together; lanes sharing a float4 summed
+// by swaps.
+__global__ __launch_bounds__(64) void b1_merge_kernel(const float *__restrict__ part, int64_t ml_off,
+                                                      float *__restrict__ out, int H, int G, int n_splits) {
+    constexpr int D = 128;
+    const int bh = blockIdx.x, dq = blockIdx.y, lane = threadIdx.x;
+    const int b = bh / H, h = bh - b * H, grp = H / G, g = h / grp, hh = h - g * grp;
+    const int64_t pair = (int64_t)b * G + g;
+    const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(part) + pair * n_splits * grp * D, 0, n_splits * grp * D * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(part) + ml_off + pair * n_splits * grp * 2, 0, n_splits * grp * 8, 0x00020000);
+    constexpr int kPer = kB1MaxSplits / 8;
+    const int nper = (n_splits + 7) / 8;                  // splits per lane group (uniform)
+    float4 v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        if (u < nper) {
+            const int s = (lane >> 3) + 8 * u;
+            const auto w = __builtin_amdgcn_raw_buffer_load_b128(ars, ((s * grp + hh) * D + dq * 32 + (lane & 7) * 4) * 4, 0, 0);
+            v[u] = make_float4(__uint_as_float(w[0]), __uint_as_float(w[1]), __uint_as_float(w[2]), __uint_as_float(w[3]));
+        }
+    }
+    const auto ml0 = __builtin_amdgcn_raw_buffer_load_b64(mrs, (lane * grp + hh) * 8, 0, 0);
+    const auto ml1 = __builtin_amdgcn_raw_buffer_load_b64(mrs, ((lane + 64) * grp + hh) * 8, 0, 0);
+    const float m0 = lane < n_splits ? __uint_as_float(ml0[0]) : kNegBig;
+    const float l0 = lane < n_splits ? __uint_as_float(ml0[1]) : 0.0f;
+    const float m1 = lane + 64 < n_splits ? __uint_as_float(ml1[0]) : kNegBig;
+    const float l1 = lane + 64 < n_splits ? __uint_as_float(ml1[1]) : 0.0f;
+    const float M = wave_max(fmaxf(m0, m1));
+    const float w0 = lane < n_splits ? __expf(m0 - M) : 0.0f;
+    const float w1 = lane + 64 < n_splits ? __expf(m1 - M) : 0.0f;
+    const float inv = 1.0f / wave_sum(fmaf(w0, l0, w1 * l1));
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        if (u < nper) {
+            const int s = (lane >> 3) + 8 * u;           // split s's weight: w0 (s < 64) or w1 of lane s % 64
+            const float wlo = __shfl(w0, s & 63, 64), whi = __shfl(w1, s & 63, 64);
+            const float w = s < n_splits ? (s < 64 ? wlo : whi) : 0.0f;
+            a.x = fmaf(w, v[u].x, a.x); a.y = fmaf(w, v[u].y, a.y);
+            a.z = fmaf(w, v[u].z, a.z); a.w = fmaf(w, v[u].w, a.w);
+        }
+    }
+#pragma unroll
+    for (int off = 8; off < 64; off <<= 1) {
+        a.x += __shfl_xor(a.x, off, 64); a.y += __shfl_xor(a.y, off, 64);
+        a.z += __shfl_xor(a.z, off, 64); a.w += __shfl_xor(a.w, off, 64);
+    }
+    if (lane < 8)
+        *reinterpret_cast<float4 *>(out + ((int64_t)b * H + h) * D + dq * 32 + lane * 4) =
+            make_float4(a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+}
+
+// The shape of the kernel and how its splits merge: waves per workgroup, keys per DPP row, and the
+// merge in the last workgroup (ticket) or in b1_merge_kernel.
+constexpr int kB1NW = 8, kB1KB = 2;
+constexpr int kB1Ticket = 0;              // 0: b1_merge_kernel, 1 / 2: the last workgroup (sc1 / acquire)
+constexpr int kB1Keys = 4 * kB1KB * kB1NW;       // keys per workgroup (one split)
+// Splits of the kernel for a call, 0 when it does not take the call's shape.
+inline int b1_splits(int64_t B, int64_t G, int64_t D, int64_t n_keys) {
+    if (D != 128 || B * G > kB1MaxPairs) return 0;
+    const int64_t ns = (n_keys + kB1Keys - 1) / kB1Keys;
+    return ns <= kB1MaxSplits ? (int)ns : 0;
+}
+
 // Workgroup shapes of the VALU kernel: waves per workgroup, keys per DPP row of a wave tile.
 struct Tiling {
     int nw, kb;
@@ -925,8 +1405,10 @@ int64_t vgx_attn_decode_workspace_bytes(int64_t B, int64_t H, int64_t G, int64_t
     int64_t kps = 0;
     int ns = 0;   // the most splits of any workgroup shape, so the caller's workspace fits every choice
     for (int t = 0; t < kNumTilings; ++t) ns = std::max(ns, choose_splits(B, G, n_keys, &kps, t));
-    if (ns <= 1) return 0;
-    return ticket_bytes(B, G) + partial_bytes(B, H, D, ns);
+    int64_t need = ns <= 1 ? 0 : ticket_bytes(B, G) + partial_bytes(B, H, D, ns);
+    const int nb1 = b1_splits(B, G, D, n_keys);
+    if (nb1 > 1) need = std::max(need, ticket_bytes(B, G) + b1_part_bytes(B * G, H / G, nb1));
+    return need;
 }
 
 int vgx_attn_decode(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_span *spans, int n_spans,
@@ -998,6 +1480,51 @@ int attn_decode_impl(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_spa
     if (n_tot > 0x3FFFFFFF) return VGX_E_LIMIT;
     const int grp = (int)(H / G);
     hipStream_t st = (hipStream_t)stream;
+    // few (batch, group) pairs at D = 128: one split per workgroup, then the split merge
+    const int nb1 = causal_base < 0 && grp <= 8 && ((uintptr_t)q & 15) == 0 && ldq % 4 == 0 &&
+                            ((uintptr_t)out & 15) == 0
+                        ? b1_splits(B, G, D, n_tot)
+                        : 0;
+    if (nb1 > 0) {
+        float *part = nullptr;
+        int *cnt = nullptr;
+        const int64_t ml_off = b1_ml_off(B * G, grp, nb1);
+        if (nb1 > 1) {
+            if (!workspace || workspace_bytes < ticket_bytes(B, G) + b1_part_bytes(B * G, grp, nb1)) return VGX_E_ARENA;
+            if ((uintptr_t)workspace % 256) return VGX_E_ALIGN;
+            cnt = static_cast<int *>(workspace);
+            part = reinterpret_cast<float *>(static_cast<char *>(workspace) + ticket_bytes(B, G));
+        }
+        const dim3 grid((unsigned)nb1, (unsigned)G, (unsigned)B);
+#define VGX_B1(KVV, GRPV, ALV)                                                                                   \
+    hipLaunchKernelGGL((attn_decode_b1_kernel<KVV, GRPV, kB1NW, kB1KB, kB1Ticket, ALV>), grid, dim3(64 * kB1NW), 0, st, q, \
+                       ldq, sp, bias, bias_hstride, bias_span, out, part, ml_off, cnt, (int)H, (int)G, scale, n_tot, nb1)
+#define VGX_B1A(KVV, ALV)                             \
+    switch (grp) {                                    \
+        case 1: VGX_B1(KVV, 1, ALV); break;           \
+        case 2: VGX_B1(KVV, 2, ALV); break;           \
+        case 3: VGX_B1(KVV, 3, ALV); break;           \
+        case 4: VGX_B1(KVV, 4, ALV); break;           \
+        case 5: VGX_B1(KVV, 5, ALV); break;           \
+        case 6: VGX_B1(KVV, 6, ALV); break;           \
+        case 7: VGX_B1(KVV, 7, ALV); break;           \
+        default: VGX_B1(KVV, 8, ALV); break;          \
+    }
+#define VGX_B1G(KVV) do { if (aligned) { VGX_B1A(KVV, true) } else { VGX_B1A(KVV, false) } } while (0)
+        bool aligned = true;    // every span's capacity a multiple of a wave's keys
+        for (int i = 0; i < n_spans; ++i) aligned = aligned && spans[i].len % (4 * kB1KB) == 0;
+        if (kv_dtype == VGX_F32) VGX_B1G(VGX_F32); else VGX_B1G(VGX_BF16);
+#undef VGX_B1G
+#undef VGX_B1A
+#undef VGX_B1
+        VGX_CHECK_LAUNCH();
+        if (nb1 > 1 && !kB1Ticket) {
+            hipLaunchKernelGGL(b1_merge_kernel, dim3((unsigned)(B * H), 4), dim3(64), 0, st, part, ml_off, out, (int)H,
+                               (int)G, nb1);
+            VGX_CHECK_LAUNCH();
+        }
+        return VGX_OK;
+    }
     const bool mfma = kv_dtype == VGX_BF16 && D == 128 && causal_base < 0 &&
                       (grp == 1 || grp == 2 || grp == 4 || grp == 6 || grp == 8) &&
                       ((uintptr_t)q & 15) == 0 && ldq % 4 == 0;
@@ -1032,8 +1559,6 @@ int attn_decode_impl(int kv_dtype, const float *q, int64_t ldq, const vgx_kv_spa
         }
         return VGX_OK;
     }
-    // Batch 1 keeps the merge launch: 8 waves of 16-key tiles (28 splits, merged by the last
-    // workgroup) measured slower, 790 vs 880 tokens/s (half as many CUs stream the keys).
     const int tiling = pick_tiling(B, G);
     int64_t kps = 0;
     const int ns = choose_splits(B, G, n_tot, &kps, tiling);
