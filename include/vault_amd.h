@@ -3,7 +3,8 @@
  *
  * Conventions (mirroring runtime/vault3.h:9-12, 35-49, 89, 153-161 of the reference):
  *   - Every entry point is stream-ordered on `stream` (a hipStream_t; NULL = default stream),
- *     takes device pointers and plain sizes, never allocates, never synchronises.
+ *     takes device pointers and plain sizes, never allocates (vgx_host_alloc / vgx_host_free, the
+ *     pinned host ring of the decode step, aside), never synchronises.
  *   - Return value: 0 = VGX_OK, negative = error (codes reuse the reference's V3_E_* numbers
  *     where the meaning matches).  Launch failures return VGX_E_HIP.
  *   - Dtype tags are the VLT3 tensor dtypes (tools/vlt3.py:29; runtime/vault3.h:51).
@@ -121,6 +122,14 @@ enum { VGX_EPI_STORE = 0, VGX_EPI_ACCUM = 1, VGX_EPI_SWIGLU = 2 };
 int vgx_qlinear_ex(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
                    int64_t batch, const float *norm_w, float eps, const float *bias, float *y, int64_t ldy,
                    int epilogue, void *stream);
+
+/* vgx_qlinear_ex whose output address is read on the device when the launch runs: y = the float
+ * pointer stored at *y_addr (an int64 device word, e.g. vgx_step_begin's out_ref).  A captured graph
+ * then writes each replay's output to a buffer the host chose for that replay.  No counterpart in the
+ * reference (its logits are a host array, runtime/vault3.c:2218-2222). */
+int vgx_qlinear_indirect(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
+                         int64_t batch, const float *norm_w, float eps, const float *bias, const int64_t *y_addr,
+                         int64_t ldy, int epilogue, void *stream);
 
 /* Workspace bytes of vgx_qgemm for these sizes and epilogue (256-byte aligned buffer: a fixed 64 KiB
  * region of int32 output-tile counters first, then bf16 hi / lo splits of the activations, their
@@ -364,6 +373,51 @@ enum { VGX_SEG_MEM_CNT = 0, VGX_SEG_ID_OFFSET = 1, VGX_SEG_CUR_ID = 2, VGX_SEG_L
 int vgx_seg_step(const int64_t *ids, int64_t B, const int32_t *step, int32_t *tok_cur, int64_t tok_ld,
                  int32_t *seg_cur, int32_t *ctrl, const uint8_t *tiers, int64_t vocab, int64_t seg_min,
                  int64_t seg_max, int64_t window, void *stream);
+
+/* Host inputs of a graph-captured decode step with no host-to-device copy.  The host writes each step's
+ * descriptor words, token ids, output address and (while a resonance mode is active) segment-bias
+ * vectors into one slot of a ring of n_slots slots in pinned, device-coherent host memory
+ * (vgx_host_alloc); the step's first kernel, vgx_step_begin, reads the slot that the device counter
+ * *counter names (slot *counter mod n_slots), does what vgx_seg_step does with those ids and words
+ * (ids are not written when the slot's ring position lies outside [0, window)),
+ * stores the words where the step's captured kernels read them, and advances the counter.  The host
+ * numbers its slots the same way (the counter starts at 0 and every launch takes one slot) and
+ * rewrites a slot only after the launch that read it has completed.  No counterpart in the reference
+ * (its step reads the host state directly, runtime/vault3.c:2034-2143).
+ *
+ * Slot layout (byte offsets; slot_bytes from vgx_step_slot_bytes, a multiple of 256): */
+enum {
+    VGX_SLOT_STEP = 0,        /* int32[VGX_STEP_WORDS]: the descriptor words */
+    VGX_SLOT_FLAGS = 16,      /* int32: VGX_SLOTF_* */
+    VGX_SLOT_IDS_ADDR = 24,   /* int64: device address of int64 ids[B] (VGX_SLOTF_DEVICE_IDS) */
+    VGX_SLOT_OUT_ADDR = 32,   /* int64: stored to *out_ref (the output address of an indirect GEMV) */
+    VGX_SLOT_IDS = 64         /* int64 ids[B] (host ids), then the bias part at vgx_step_slot_bias_off */
+};
+enum { VGX_SLOTF_DEVICE_IDS = 1, VGX_SLOTF_BIAS = 2 };
+
+/* Bytes of one slot for B ids and (bias_cap > 0) the bias part: int8 row[2][n_heads] (the early
+ * rows' vector per head, then the late rows'; -1 = a zero row), padded to 16 bytes, then float
+ * vec[3][bias_cap].  vgx_step_slot_bias_off: the bias part's offset. */
+int64_t vgx_step_slot_bytes(int64_t B, int64_t n_heads, int64_t bias_cap);
+int64_t vgx_step_slot_bias_off(int64_t B);
+
+/* Pinned host memory the device reads coherently at the same address (hipHostMalloc, coherent and
+ * mapped), zero-filled; for the step ring.  The only allocating entry points of the library. */
+int vgx_host_alloc(int64_t bytes, void **ptr);
+int vgx_host_free(void *ptr);
+
+/* The first kernel of a decode step (one workgroup).  Reads slot (*counter mod n_slots) of ring:
+ * step[0..VGX_STEP_WORDS) = its words; ids[b] = its ids (host ids, or those at its device address);
+ * out_ref (may be NULL) = its output address; then vgx_seg_step's ring and segmenter update with
+ * these ids and words; with bias_early / bias_late (both or neither) and the slot's VGX_SLOTF_BIAS,
+ * row h of bias_early (row stride bias_ld, bias_cap entries) = vec[row[0][h]] and of bias_late =
+ * vec[row[1][h]] (zeros for -1); finally *counter = (*counter + 1) mod n_slots.  Replaces the step's host copies of the
+ * descriptor, ids and bias rows (runtime/vault3.c:1976-1988 fills the bias rows on the host). */
+int vgx_step_begin(const void *ring, int64_t n_slots, int64_t slot_bytes, int32_t *counter, int32_t *step, int64_t *ids,
+                   int64_t B, int64_t *out_ref, int32_t *tok_cur, int64_t tok_ld, int32_t *seg_cur, int32_t *ctrl,
+                   const uint8_t *tiers, int64_t vocab, int64_t seg_min, int64_t seg_max, int64_t window,
+                   float *bias_early, float *bias_late, int64_t n_heads, int64_t bias_ld, int64_t bias_cap,
+                   void *stream);
 
 /* The segment-bank update at a chunk boundary, for the evicted chunk ev_chunk (its tokens' scores
  * sc_prev, local segment ids seg_prev, tokens tok_prev, window entries each): quarantine (a score

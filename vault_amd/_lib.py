@@ -22,6 +22,8 @@ F32, F16, BF16, Q8_0, Q4_0 = 0, 1, 2, 8, 9
 EPI_STORE, EPI_ACCUM, EPI_SWIGLU = 0, 1, 2
 STEP_SLOT, STEP_TABLE_ROW, STEP_SINK_SLOT, STEP_N_CUR, STEP_WORDS = 0, 1, 2, 3, 4
 SEG_MEM_CNT, SEG_ID_OFFSET, SEG_CUR_ID, SEG_LEN, SEG_WORDS = 0, 1, 2, 3, 4
+SLOT_STEP, SLOT_FLAGS, SLOT_IDS_ADDR, SLOT_OUT_ADDR, SLOT_IDS = 0, 16, 24, 32, 64
+SLOTF_DEVICE_IDS, SLOTF_BIAS = 1, 2
 
 P = C.c_void_p
 I32 = C.c_int
@@ -45,11 +47,18 @@ _SIGS = {
     "vgx_qlinear": (I32, [I32, P, I64, I64, P, I64, I64, P, P, I64, I32, P]),
     "vgx_qlinear_swiglu": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
     "vgx_qlinear_ex": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P]),
+    "vgx_qlinear_indirect": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P]),
     "vgx_qgemm_workspace_bytes": (I64, [I64, I64, I64, I32]),
     "vgx_qgemm": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P, I64, P]),
     "vgx_attn_decode_workspace_bytes": (I64, [I64, I64, I64, I64, I64]),
     "vgx_attn_decode": (I32, [I32, P, I64, P, I32, P, I64, I32, I64, P, I64, I64, I64, I64, F, P, I64, P]),
     "vgx_seg_step": (I32, [P, I64, P, P, I64, P, P, P, I64, I64, I64, I64, P]),
+    "vgx_step_slot_bytes": (I64, [I64, I64, I64]),
+    "vgx_step_slot_bias_off": (I64, [I64]),
+    "vgx_host_alloc": (I32, [I64, C.POINTER(C.c_void_p)]),
+    "vgx_host_free": (I32, [P]),
+    "vgx_step_begin": (I32, [P, I64, I64, P, P, P, I64, P, P, I64, P, P, P, I64, I64, I64, I64, P, P, I64, I64, I64,
+                             P]),
     "vgx_seg_evict": (I32, [P, P, P, I64, P, P, P, P, P, I64, I64, I64, P, P, P]),
     "vgx_gather_rows_masked": (I32, [I32, P, P, P, I64, I64, I64, I64, I64, I64, P]),
     "vgx_rope_rotate_dyn": (I32, [I32, P, P, I64, I64, I64, I64, I64, P, I64, P, I64, I32, P]),

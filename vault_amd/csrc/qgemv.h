@@ -62,7 +62,15 @@ struct GemvArgs {
     float *y;
     int64_t ldy;
     int epi;
+    const int64_t *y_ref;   // non-null: y is the address stored in this device word when the launch runs,
+    int64_t y_off;          // plus this many floats
 };
+
+// The output address of a launch whose GemvArgs name it indirectly (a captured graph whose output
+// buffer changes per replay); one uniform load per workgroup.
+__device__ __forceinline__ void gemv_resolve_y(GemvArgs &a) {
+    if (a.y_ref != nullptr) a.y = reinterpret_cast<float *>(*a.y_ref) + a.y_off;
+}
 
 __device__ __forceinline__ float gemv_cvt_u8(uint32_t w, int k) {
     switch (k) {  // each pattern maps onto one v_cvt_f32_ubyte{0..3}
@@ -231,6 +239,7 @@ __device__ __forceinline__ void gemv_block(const BlockRegs<DT> &br, const float 
 
 template <int DT, int NB, int EPI, int MODE, int KW, bool NORM>
 __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_kernel(GemvArgs a, int cbk) {
+    gemv_resolve_y(a);
     extern __shared__ float smem[];
     constexpr int LPR = MODE == MODE_ROWS ? 16 : 64;     // lanes per row-quad
     constexpr int RQW = 64 / LPR;                          // row-quads per wave
@@ -433,6 +442,7 @@ __global__ __launch_bounds__(64 * (MODE == MODE_ROWS ? 4 : 1) * KW) void qgemv_k
 // 53 us, before gemv1_stream_kernel took that shape: 44.7 us Q8_0, 26.2 us Q4_0).
 template <int DT, int EPI, bool NORM, int LPR, int WPG, int KW, int U, bool SF, bool XD>
 __global__ __launch_bounds__(64 * WPG * KW) void gemv1_kernel(GemvArgs a) {
+    gemv_resolve_y(a);
     static_assert(!XD || WPG == 1, "direct activations: one row-quad set per workgroup");
     constexpr int RQW = 64 / LPR;
     constexpr int NW = WPG * KW;
@@ -630,6 +640,7 @@ VGX_DEV int stream_block(int lane, int j) { return DT == VGX_Q8_0 ? 8 * j + (lan
 
 template <int DT, int EPI, bool NORM>
 __global__ __launch_bounds__(256) void gemv1_stream_kernel(GemvArgs a) {
+    gemv_resolve_y(a);
     using G = StreamGeom<DT>;
     constexpr int NL = G::NL, XL = G::XL, RB = G::RB;
     const int lane = threadIdx.x & 63;
@@ -846,6 +857,7 @@ constexpr int kPiecesMaxBlocks = 320;
 
 template <int DT, int EPI, int NW, int RQG, int MAXB>
 __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
+    gemv_resolve_y(a);
     constexpr int QB = gemv_quant_bytes(DT);
     constexpr int BPP = 1024 / (4 * QB);              // blocks per 1 KB piece: 16 (Q4_0) / 8 (Q8_0)
     constexpr int MAXI = (RQG * ((MAXB + BPP - 1) / BPP) + NW - 1) / NW;   // pieces per wave
@@ -958,6 +970,7 @@ constexpr int kF32PiecesWaves = 16;
 
 template <int NB, int EPI>
 __global__ __launch_bounds__(64 * kF32PiecesWaves) void gemv_f32_pieces_kernel(GemvArgs a) {
+    gemv_resolve_y(a);
     constexpr int NW = kF32PiecesWaves;
     constexpr int MAXI = (kF32PiecesMaxBlocks / 2 + NW - 1) / NW;   // pieces per wave
     __shared__ float4 xs4[NB * kF32PiecesMaxBlocks * 8];
@@ -1114,7 +1127,8 @@ int qgemv_launch(GemvArgs a, hipStream_t st) {
         GemvArgs p = a;
         const int nb = (int)std::min<int64_t>(4, a.batch - b0);
         p.x = a.x + b0 * a.ldx;
-        p.y = a.y + b0 * a.ldy;
+        if (a.y_ref != nullptr) p.y_off = a.y_off + b0 * a.ldy;
+        else p.y = a.y + b0 * a.ldy;
         const int cbk = std::min(a.nblk, kGemvMaxChunkFloats / (QK * nb));
         const size_t lds = (size_t)nb * cbk * kGemvPad * sizeof(float);
         const unsigned grid = rows_mode ? (unsigned)((a.n_rq + 15) / 16) : (unsigned)a.n_rq;

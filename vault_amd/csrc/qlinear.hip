@@ -274,7 +274,7 @@ int vgx_embed_rows(int dtype, const void *packed, int64_t rows, int64_t cols, co
 
 static int qgemv_dispatch(int dtype, const void *w, int64_t rows_packed, int64_t rows_out, int64_t cols,
                           const float *x, int64_t ldx, int64_t batch, const float *lnw, float eps, const float *bias,
-                          float *y, int64_t ldy, int epi, void *stream) {
+                          float *y, int64_t ldy, int epi, void *stream, const int64_t *y_ref = nullptr) {
     GemvArgs a{};
     a.w = static_cast<const uint8_t *>(w);
     a.nblk = (int)(cols / QK);
@@ -290,6 +290,7 @@ static int qgemv_dispatch(int dtype, const void *w, int64_t rows_packed, int64_t
     a.y = y;
     a.ldy = ldy;
     a.epi = epi;
+    a.y_ref = y_ref;
     hipStream_t st = (hipStream_t)stream;
     switch (dtype) {
         case VGX_Q8_0: return vgx_detail_qgemv_q8(a, st);
@@ -316,6 +317,26 @@ int vgx_qlinear_ex(int dtype, const void *w_packed, int64_t rows, int64_t cols, 
     const int64_t rows_packed = epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows;
     return qgemv_dispatch(dtype, w_packed, rows_packed, rows, cols, x, ldx, batch, norm_w, eps, bias, y, ldy,
                           epilogue, stream);
+}
+
+int vgx_qlinear_indirect(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
+                         int64_t batch, const float *norm_w, float eps, const float *bias, const int64_t *y_addr,
+                         int64_t ldy, int epilogue, void *stream) {
+    if (!y_addr) return VGX_E_ARG;
+    if (reinterpret_cast<uintptr_t>(y_addr) % 8) return VGX_E_ALIGN;
+    if (!dtype_ok(dtype)) return VGX_E_DTYPE;
+    if (!w_packed || !x) return VGX_E_ARG;
+    if (epilogue != VGX_EPI_STORE && epilogue != VGX_EPI_ACCUM && epilogue != VGX_EPI_SWIGLU) return VGX_E_ARG;
+    if (epilogue == VGX_EPI_SWIGLU && bias) return VGX_E_ARG;
+    if (rows <= 0 || cols <= 0 || batch < 0 || ldx < cols || ldy < rows) return VGX_E_SIZE;
+    if (cols % QK || (epilogue == VGX_EPI_SWIGLU && rows % 2)) return VGX_E_SHAPE;
+    if (cols / QK > (1 << 24)) return VGX_E_LIMIT;
+    if (norm_w && !(eps > 0.0f)) return VGX_E_ARG;
+    if (batch == 0) return VGX_OK;
+    const int64_t rows_packed = epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows;
+    // the launch geometry never depends on y: a placeholder address stands in until the kernel reads *y_addr
+    return qgemv_dispatch(dtype, w_packed, rows_packed, rows, cols, x, ldx, batch, norm_w, eps, bias, nullptr, ldy,
+                          epilogue, stream, y_addr);
 }
 
 int vgx_qlinear(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,

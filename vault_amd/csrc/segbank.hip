@@ -9,6 +9,8 @@
 // Control words (int32, VGX_SEG_*): the bank's entry count, the running segment-id offset, the
 // current chunk's segment id and length.  The bank arrays: positions (int64), scores (fp32), tokens
 // and global segment ids (int32), in chronological order.
+#include <string.h>
+
 #include "common.h"
 
 using namespace vgx;
@@ -17,6 +19,25 @@ namespace {
 
 constexpr int kEvictThreads = 1024;
 constexpr int kEvictMaxItems = 4096;     // bank capacity + W candidates held in LDS
+
+// The segmenter's step for the single sequence's token id at ring slot c: its segment id, then the
+// break rule by the token's tier.
+__device__ void segment_token(int64_t id, int c, int32_t *__restrict__ seg_cur, int32_t *__restrict__ ctrl,
+                              const uint8_t *__restrict__ tiers, int64_t vocab, int seg_min, int seg_max, int W) {
+    const int tr = (tiers != nullptr && id >= 0 && id < vocab) ? (int)tiers[id] : 0;
+    const int t2 = max(seg_min, (seg_max * 2) / 3);
+    const int t3 = max(seg_min, seg_max > 8 ? seg_max - 8 : seg_min);
+    const int cur = ctrl[VGX_SEG_CUR_ID];
+    const int len = ctrl[VGX_SEG_LEN] + 1;
+    seg_cur[c] = cur;
+    const bool brk = (tr == 1 && len >= seg_min) || (tr == 2 && len >= t2) || (tr == 3 && len >= t3);
+    if (c == W - 1 || brk || len >= seg_max) {
+        ctrl[VGX_SEG_CUR_ID] = cur + 1;
+        ctrl[VGX_SEG_LEN] = 0;
+    } else {
+        ctrl[VGX_SEG_LEN] = len;
+    }
+}
 
 // One decode step: ring slot c = step[SLOT] of every sequence gets its token; with seg_cur, the
 // single sequence's segment id and the segmenter's break rule.
@@ -27,22 +48,112 @@ __global__ void seg_step_kernel(const int64_t *__restrict__ ids, int B, const in
     const int c = step[VGX_STEP_SLOT];
     const int b = threadIdx.x + blockIdx.x * blockDim.x;
     if (b < B) tok_cur[b * ldt + c] = (int32_t)ids[b];
-    if (seg_cur != nullptr && b == 0) {
-        const int64_t id = ids[0];
-        const int tr = (tiers != nullptr && id >= 0 && id < vocab) ? (int)tiers[id] : 0;
-        const int t2 = max(seg_min, (seg_max * 2) / 3);
-        const int t3 = max(seg_min, seg_max > 8 ? seg_max - 8 : seg_min);
-        const int cur = ctrl[VGX_SEG_CUR_ID];
-        const int len = ctrl[VGX_SEG_LEN] + 1;
-        seg_cur[c] = cur;
-        const bool brk = (tr == 1 && len >= seg_min) || (tr == 2 && len >= t2) || (tr == 3 && len >= t3);
-        if (c == W - 1 || brk || len >= seg_max) {
-            ctrl[VGX_SEG_CUR_ID] = cur + 1;
-            ctrl[VGX_SEG_LEN] = 0;
-        } else {
-            ctrl[VGX_SEG_LEN] = len;
+    if (seg_cur != nullptr && b == 0) segment_token(ids[0], c, seg_cur, ctrl, tiers, vocab, seg_min, seg_max, W);
+}
+
+// Loads of the pinned host ring at system scope: they reach the host's latest writes through no
+// stale cache line, whatever the ring's earlier use of the same slot left in the device caches.
+template <typename T>
+__device__ __forceinline__ T sys_load(const void *p) {
+    return __hip_atomic_load(static_cast<T *>(const_cast<void *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+constexpr int kBeginThreads = 256;
+constexpr int kBeginBiasUnroll = 4;        // bias entries per thread whose host loads are in flight together
+
+struct StepBeginArgs {
+    const uint8_t *ring;
+    int64_t n_slots, slot_bytes, bias_off;
+    int32_t *counter, *step;
+    int64_t *ids;
+    int B;
+    int64_t *out_ref;
+    int32_t *tok_cur;
+    int64_t ldt;
+    int32_t *seg_cur, *ctrl;
+    const uint8_t *tiers;
+    int64_t vocab;
+    int seg_min, seg_max, W;
+    float *bias_early, *bias_late;
+    int H;
+    int64_t bias_ld;
+    int bias_cap;
+};
+
+// One workgroup.  Every host load of the slot (header, host ids, bias row indices and vectors) is
+// issued before any is used, so the step pays one host round trip; device ids are one more (device)
+// load.  The counter advances after every thread has read it.
+__global__ __launch_bounds__(kBeginThreads) void step_begin_kernel(StepBeginArgs a) {
+    __shared__ int s_k;
+    const int tid = threadIdx.x;
+    if (tid == 0) s_k = *a.counter;
+    __syncthreads();
+    const uint32_t k = (uint32_t)s_k % (uint32_t)a.n_slots;   // in range whatever the word holds
+    const uint8_t *slot = a.ring + (int64_t)k * a.slot_bytes;
+    const int64_t h0 = sys_load<int64_t>(slot + VGX_SLOT_STEP);
+    const int64_t h1 = sys_load<int64_t>(slot + VGX_SLOT_STEP + 8);
+    const int32_t flags = sys_load<int32_t>(slot + VGX_SLOT_FLAGS);
+    const int64_t ids_addr = sys_load<int64_t>(slot + VGX_SLOT_IDS_ADDR);
+    const int64_t out_addr = sys_load<int64_t>(slot + VGX_SLOT_OUT_ADDR);
+    int64_t hid = 0;
+    if (tid < a.B) hid = sys_load<int64_t>(slot + VGX_SLOT_IDS + 8 * tid);
+    const bool bias = a.bias_early != nullptr;
+    int8_t rows[2] = {-1, -1};
+    if (bias && tid < a.H) {
+        rows[0] = sys_load<int8_t>(slot + a.bias_off + tid);
+        rows[1] = sys_load<int8_t>(slot + a.bias_off + a.H + tid);
+    }
+    const int32_t w[VGX_STEP_WORDS] = {(int32_t)h0, (int32_t)(h0 >> 32), (int32_t)h1, (int32_t)(h1 >> 32)};
+    if (tid < VGX_STEP_WORDS) a.step[tid] = w[tid];
+    if (tid == 0 && a.out_ref != nullptr) *a.out_ref = out_addr;
+    const int c = w[VGX_STEP_SLOT];
+    const int64_t *dev_ids = reinterpret_cast<const int64_t *>(ids_addr);
+    const bool on_dev = (flags & VGX_SLOTF_DEVICE_IDS) != 0;
+    for (int b = tid; b < a.B && (uint32_t)c < (uint32_t)a.W; b += kBeginThreads) {   // a slot outside the ring: no write
+        const int64_t id = on_dev ? dev_ids[b] : (b == tid ? hid : sys_load<int64_t>(slot + VGX_SLOT_IDS + 8 * b));
+        a.ids[b] = id;
+        a.tok_cur[b * a.ldt + c] = (int32_t)id;
+        if (a.seg_cur != nullptr && b == 0)
+            segment_token(id, c, a.seg_cur, a.ctrl, a.tiers, a.vocab, a.seg_min, a.seg_max, a.W);
+    }
+    if (bias && (flags & VGX_SLOTF_BIAS)) {
+        __shared__ int8_t s_rows[2][256];
+        if (tid < a.H) {
+            s_rows[0][tid] = rows[0];
+            s_rows[1][tid] = rows[1];
+        }
+        __syncthreads();
+        const float *v = reinterpret_cast<const float *>(slot + a.bias_off + ((2 * a.H + 15) / 16) * 16);
+        // entries m0 + t, m0 + t + 256, ... of the three vectors: all their host loads in flight at once
+        for (int m0 = 0; m0 < a.bias_cap; m0 += kBeginThreads * kBeginBiasUnroll) {
+            float vec[kBeginBiasUnroll][3];
+#pragma unroll
+            for (int u = 0; u < kBeginBiasUnroll; ++u) {
+                const int m = m0 + tid + u * kBeginThreads;
+#pragma unroll
+                for (int r = 0; r < 3; ++r) vec[u][r] = m < a.bias_cap ? sys_load<float>(v + r * a.bias_cap + m) : 0.0f;
+            }
+            for (int h = 0; h < a.H; ++h) {
+                const int re = s_rows[0][h], rl = s_rows[1][h];
+#pragma unroll
+                for (int u = 0; u < kBeginBiasUnroll; ++u) {
+                    const int m = m0 + tid + u * kBeginThreads;
+                    if (m < a.bias_cap) {
+                        float e = 0.0f, l = 0.0f;
+#pragma unroll
+                        for (int r = 0; r < 3; ++r) {
+                            e = re == r ? vec[u][r] : e;
+                            l = rl == r ? vec[u][r] : l;
+                        }
+                        a.bias_early[h * a.bias_ld + m] = e;
+                        a.bias_late[h * a.bias_ld + m] = l;
+                    }
+                }
+            }
         }
     }
+    __syncthreads();
+    if (tid == 0) *a.counter = (int32_t)((k + 1) % (uint32_t)a.n_slots);
 }
 
 __device__ __forceinline__ int f2ord(float f) {      // order-preserving float -> int
@@ -250,6 +361,85 @@ int vgx_seg_step(const int64_t *ids, int64_t B, const int32_t *step, int32_t *to
     hipLaunchKernelGGL(seg_step_kernel, dim3((unsigned)((B + thr - 1) / thr)), dim3(thr), 0, (hipStream_t)stream, ids,
                        (int)B, step, tok_cur, tok_ld, seg_cur, ctrl, tiers, vocab, (int)seg_min, (int)seg_max,
                        (int)window);
+    VGX_CHECK_LAUNCH();
+    return VGX_OK;
+}
+
+int64_t vgx_step_slot_bias_off(int64_t B) { return B < 0 ? -1 : VGX_SLOT_IDS + (8 * B + 15) / 16 * 16; }
+
+int64_t vgx_step_slot_bytes(int64_t B, int64_t n_heads, int64_t bias_cap) {
+    if (B < 0 || n_heads < 0 || bias_cap < 0) return -1;
+    int64_t n = vgx_step_slot_bias_off(B);
+    if (bias_cap > 0) n += (2 * n_heads + 15) / 16 * 16 + 3 * 4 * bias_cap;
+    return (n + 255) / 256 * 256;
+}
+
+int vgx_host_alloc(int64_t bytes, void **ptr) {
+    if (!ptr) return VGX_E_ARG;
+    *ptr = nullptr;
+    if (bytes <= 0) return VGX_E_SIZE;
+    void *p = nullptr;
+    if (hipHostMalloc(&p, (size_t)bytes, hipHostMallocCoherent | hipHostMallocMapped) != hipSuccess) return VGX_E_HIP;
+    void *d = nullptr;
+    if (hipHostGetDevicePointer(&d, p, 0) != hipSuccess || d != p) {   // the device must see the same address
+        (void)hipHostFree(p);
+        return VGX_E_HIP;
+    }
+    memset(p, 0, (size_t)bytes);
+    *ptr = p;
+    return VGX_OK;
+}
+
+int vgx_host_free(void *ptr) {
+    if (!ptr) return VGX_OK;
+    return hipHostFree(ptr) == hipSuccess ? VGX_OK : VGX_E_HIP;
+}
+
+int vgx_step_begin(const void *ring, int64_t n_slots, int64_t slot_bytes, int32_t *counter, int32_t *step, int64_t *ids,
+                   int64_t B, int64_t *out_ref, int32_t *tok_cur, int64_t tok_ld, int32_t *seg_cur, int32_t *ctrl,
+                   const uint8_t *tiers, int64_t vocab, int64_t seg_min, int64_t seg_max, int64_t window,
+                   float *bias_early, float *bias_late, int64_t n_heads, int64_t bias_ld, int64_t bias_cap,
+                   void *stream) {
+    if (!ring || !counter || !step || !ids || !tok_cur) return VGX_E_ARG;
+    if (seg_cur && !ctrl) return VGX_E_ARG;
+    if ((bias_early == nullptr) != (bias_late == nullptr)) return VGX_E_ARG;
+    if (reinterpret_cast<uintptr_t>(ring) % 256 || reinterpret_cast<uintptr_t>(out_ref) % 8 ||
+        reinterpret_cast<uintptr_t>(ids) % 8)
+        return VGX_E_ALIGN;
+    if (B <= 0 || n_slots <= 0 || window <= 0 || tok_ld < window ||
+        (seg_cur && (seg_min <= 0 || seg_max < seg_min)))
+        return VGX_E_SIZE;
+    if (bias_early && (n_heads <= 0 || bias_cap <= 0 || bias_ld < bias_cap)) return VGX_E_SIZE;
+    if (B > kBeginThreads * 64 || window > 0x7FFFFFFF || n_slots > (1 << 20) ||
+        (bias_early && (n_heads > 256 || bias_cap > (1 << 24))))
+        return VGX_E_LIMIT;
+    if (slot_bytes % 256 || slot_bytes < vgx_step_slot_bytes(B, bias_early ? n_heads : 0, bias_early ? bias_cap : 0))
+        return VGX_E_SIZE;
+    StepBeginArgs a{};
+    a.ring = static_cast<const uint8_t *>(ring);
+    a.n_slots = n_slots;
+    a.slot_bytes = slot_bytes;
+    a.bias_off = vgx_step_slot_bias_off(B);
+    a.counter = counter;
+    a.step = step;
+    a.ids = ids;
+    a.B = (int)B;
+    a.out_ref = out_ref;
+    a.tok_cur = tok_cur;
+    a.ldt = tok_ld;
+    a.seg_cur = seg_cur;
+    a.ctrl = ctrl;
+    a.tiers = tiers;
+    a.vocab = vocab;
+    a.seg_min = (int)seg_min;
+    a.seg_max = (int)seg_max;
+    a.W = (int)window;
+    a.bias_early = bias_early;
+    a.bias_late = bias_late;
+    a.H = (int)n_heads;
+    a.bias_ld = bias_ld;
+    a.bias_cap = (int)bias_cap;
+    hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(kBeginThreads), 0, (hipStream_t)stream, a);
     VGX_CHECK_LAUNCH();
     return VGX_OK;
 }

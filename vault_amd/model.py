@@ -72,38 +72,97 @@ class LayerView:
 
 
 class StepIO:
-    """Device words of a decode step (the int32 step descriptor, include/vault_amd.h VGX_STEP_*, and
-    the token ids) plus a ring of pinned host buffers they are copied from, stream-ordered before
-    each launch.  A host buffer is reused only after the event of its previous copy completed."""
+    """Host inputs of the decode step and the device words the step's kernels read them from.
+
+    The host writes each step's descriptor words (include/vault_amd.h VGX_STEP_*), token ids (their
+    values, or the device address of a device tensor), logits address and, while a resonance mode is
+    active, the bias vectors into one slot of a ring in pinned, device-coherent host memory; the
+    step's first launch (ops.step_begin) reads the slot a device counter names and stores the words
+    on the device, so a step makes no host-to-device copy.  Slots are taken in order, one per launch:
+    a slot is rewritten only after the event recorded behind the launch that read it completed."""
 
     RING = 8
 
-    def __init__(self, batch: int, device):
-        self.nbytes = 64 + 8 * batch
-        self.dev = torch.zeros(self.nbytes, dtype=torch.uint8, device=device)
+    def __init__(self, batch: int, device, n_heads: int = 0, bias_cap: int = 0):
+        import ctypes
+        lib = ops.L.load()
+        self.batch, self.H, self.bias_cap = batch, n_heads, bias_cap
+        self.slot_bytes = int(lib.vgx_step_slot_bytes(batch, n_heads, bias_cap))
+        self.bias_off = int(lib.vgx_step_slot_bias_off(batch))
+        ptr = ctypes.c_void_p()
+        ops.L.check(lib.vgx_host_alloc(self.RING * self.slot_bytes, ctypes.byref(ptr)), "vgx_host_alloc")
+        self.ring = int(ptr.value)
+        self.host = np.ctypeslib.as_array((ctypes.c_uint8 * (self.RING * self.slot_bytes)).from_address(self.ring))
+        self.host = self.host.reshape(self.RING, self.slot_bytes)
+        # device words: descriptor [0, 16), slot counter [16, 20), logits address [24, 32), ids [64, ...)
+        self.dev = torch.zeros(64 + 8 * batch, dtype=torch.uint8, device=device)
         self.step = self.dev[:16].view(torch.int32)
+        self.counter = self.dev[16:20].view(torch.int32)
+        self.out_ref = self.dev[24:32].view(torch.int64)
         self.ids = self.dev[64:].view(torch.int64)
-        self.host = [torch.zeros(self.nbytes, dtype=torch.uint8).pin_memory() for _ in range(self.RING)]
         self.events: List[Optional[torch.cuda.Event]] = [None] * self.RING
+        self.keep: List[Optional[torch.Tensor]] = [None] * self.RING    # device ids / logits a slot names
         self.i = 0
 
-    def write(self, ids: torch.Tensor, slot: int, row: int, sink: int, n_cur: int) -> None:
-        """Host ids travel with the step words; device ids (e.g. the previous step's argmax) are
-        copied on the device after them, so no host read is needed."""
+    def close(self) -> None:
+        """Wait for the launches that read the ring, then free it."""
+        if self.ring:
+            for ev in self.events:
+                if ev is not None:
+                    ev.synchronize()
+            ops.L.load().vgx_host_free(self.ring)
+            self.ring, self.host = 0, None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def write(self, ids: torch.Tensor, slot: int, row: int, sink: int, n_cur: int,
+              out: Optional[torch.Tensor] = None, bias: Optional[tuple] = None) -> None:
+        """Fill the next slot: descriptor words, ids (host values, or the address of int64 device ids),
+        the logits address ``out`` and ``bias`` = (row index [2, H] int8, vectors [3, M] fp32)."""
         k = self.i % self.RING
-        self.i += 1
         if self.events[k] is not None:
             self.events[k].synchronize()
         h = self.host[k]
-        h[:16].view(torch.int32).copy_(torch.tensor([slot, row, sink, n_cur], dtype=torch.int32))
-        if not ids.is_cuda:
-            h[64:].view(torch.int64).copy_(ids)
-        self.dev.copy_(h, non_blocking=True)
+        h[0:16].view(np.int32)[:] = (slot, row, sink, n_cur)
+        flags = 0
         if ids.is_cuda:
-            self.ids.copy_(ids.to(torch.int64), non_blocking=True)
+            d = ids if ids.dtype == torch.int64 and ids.is_contiguous() else ids.to(torch.int64).contiguous()
+            h[ops.L.SLOT_IDS_ADDR:ops.L.SLOT_IDS_ADDR + 8].view(np.int64)[0] = d.data_ptr()
+            flags |= ops.L.SLOTF_DEVICE_IDS
+            self.keep[k] = d
+        else:
+            h[ops.L.SLOT_IDS:ops.L.SLOT_IDS + 8 * self.batch].view(np.int64)[:] = ids.numpy()
+            self.keep[k] = None
+        h[ops.L.SLOT_OUT_ADDR:ops.L.SLOT_OUT_ADDR + 8].view(np.int64)[0] = 0 if out is None else out.data_ptr()
+        if bias is not None:
+            rows, vec = bias
+            o = self.bias_off
+            h[o:o + 2 * self.H].view(np.int8)[:] = rows.reshape(-1)
+            v = h[o + (2 * self.H + 15) // 16 * 16:o + (2 * self.H + 15) // 16 * 16 + 12 * self.bias_cap]
+            v = v.view(np.float32).reshape(3, self.bias_cap)
+            M = vec.shape[1]
+            v[:, :M] = vec
+            v[:, M:] = 0.0
+            flags |= ops.L.SLOTF_BIAS
+        h[ops.L.SLOT_FLAGS:ops.L.SLOT_FLAGS + 4].view(np.int32)[0] = flags
+
+    def launched(self) -> None:
+        """The launch that reads the slot of the last write is enqueued (on the current stream)."""
         ev = torch.cuda.Event()
         ev.record()
-        self.events[k] = ev
+        self.events[self.i % self.RING] = ev
+        self.i += 1
+
+    def resync(self) -> None:
+        """After a step that failed between write and launched: align the host's slot number with the
+        device counter (whether or not the first launch ran)."""
+        torch.cuda.synchronize(self.dev.device)
+        c = int(self.counter.item())
+        self.i += (c - self.i) % self.RING
 
 
 class VAULTv3State:
@@ -154,6 +213,7 @@ class VAULTv3State:
         self.tok_prev_h = np.zeros(W, dtype=np.uint32)
         self.tok_cur_h = np.zeros(W, dtype=np.uint32)
         self.res: Optional[control.Resonance] = None
+        self.bias_rows: Optional[tuple] = None     # the next step's bias rows for its slot (StepIO.write)
         self.bias_early: Optional[torch.Tensor] = None
         self.bias_late: Optional[torch.Tensor] = None
         self.graphs: "OrderedDict[tuple, tuple]" = OrderedDict()   # captured decode steps
@@ -220,7 +280,8 @@ class VAULTv3State:
 
     def step_io(self) -> StepIO:
         if self._io is None:
-            self._io = StepIO(self.batch, self.device)
+            cap = self.bias_early.shape[1] if self.bias_early is not None else 0
+            self._io = StepIO(self.batch, self.device, self.cfg.n_heads if cap else 0, cap)
         return self._io
 
     def set_pinned(self, n_pin: int) -> None:
@@ -363,25 +424,34 @@ class VAULTv3ForCausalLM:
         return logits
 
     # ------------------------------------------------------------------ resonance / quarantine (host)
-    def _resonance(self, st: VAULTv3State, c: int, pos: int, seg_active: bool) -> None:
-        """This step's query resonance over the host rings; an active mode fills the bias buffers."""
+    def _resonance(self, st: VAULTv3State, c: int, pos: int, seg_active: bool, direct: bool = False) -> None:
+        """This step's query resonance over the host rings.  An active mode sets the bias rows of the
+        early / late biased layers (runtime/vault3.c:1976-1988): head h's late row is arch (class 1) or
+        sup (class 2), its early row the same, or hop-1 in mode 2; zero for class 0.  They travel as
+        a row index per head and the three vectors in the next decode step's slot (``st.bias_rows``),
+        or with ``direct`` are copied into the device rows now."""
         mode = 0
         if seg_active and pos >= 2 * self.cfg.window and st.res.mem_cnt > 0:
             mode = st.res.update(st.tok_prev_h, st.tok_cur_h, c, pos, st.n_pin)
         st.seg_bias_mode = mode
         st.seg_bias_active = mode > 0
+        st.bias_rows = None
         if mode:
             M = st.res.mem_cnt
-            vec = {1: st.res.arch[:M], 2: st.res.sup[:M]}
-            late = np.zeros((self.cfg.n_heads, M), dtype=np.float32)
-            for h, k in enumerate(self.head_class):
-                if k:
-                    late[h] = vec[int(k)]
-            early = late.copy()
+            cls = np.asarray(self.head_class, dtype=np.int64)
+            rows = np.full((2, self.cfg.n_heads), -1, dtype=np.int8)
+            rows[1][cls > 0] = cls[cls > 0] - 1                 # 0 = arch, 1 = sup
+            rows[0] = rows[1]
             if mode == 2:
-                early[self.head_class > 0] = st.res.hop1[:M]
-            st.bias_late[:, :M].copy_(torch.from_numpy(late))
-            st.bias_early[:, :M].copy_(torch.from_numpy(early))
+                rows[0][cls > 0] = 2                             # hop-1
+            vec = np.stack([st.res.arch[:M], st.res.sup[:M], st.res.hop1[:M]]).astype(np.float32)
+            if direct:
+                zero = np.zeros((1, M), dtype=np.float32)
+                full = np.concatenate([vec, zero])
+                st.bias_early[:, :M].copy_(torch.from_numpy(full[rows[0].astype(np.int64)]))
+                st.bias_late[:, :M].copy_(torch.from_numpy(full[rows[1].astype(np.int64)]))
+            else:
+                st.bias_rows = (rows, vec)
 
     def _spoofed(self, st: VAULTv3State, c: int, pos: int, n_pin: Optional[int] = None) -> bool:
         cfg = self.cfg
@@ -531,48 +601,63 @@ class VAULTv3ForCausalLM:
     # ------------------------------------------------------------------ decode step on the device
     def _decode(self, st: VAULTv3State, ids: torch.Tensor, pos: int, c: int, seg_active: bool) -> torch.Tensor:
         """One decode step on the device.  The position-dependent words (ring slot, RoPE row, sink
-        slot, current-chunk length) and the token ids go through a small device buffer written
-        before the launch, so the launch sequence only depends on the chunk configuration; that
-        sequence is captured once per configuration as a HIP graph and replayed at every position
-        of the chunk (re-captured when the configuration changes: at most twice per W tokens)."""
+        slot, current-chunk length), the token ids, the logits address and the bias rows go through a
+        slot of the pinned host ring that the step's first launch reads, so the launch sequence only
+        depends on the chunk configuration; that sequence is captured once per configuration as a HIP
+        graph and replayed at every position of the chunk (re-captured when the configuration changes:
+        at most twice per W tokens).  GEMV batches (B < ops.GEMM_MIN_ROWS) write the logits straight
+        into a fresh tensor named in the slot; larger batches copy them out of the graph's buffer."""
         cfg = self.cfg
         W, B = cfg.window, ids.numel()
         io = st.step_io()
         eff = W + c if pos >= W else c
-        io.write(ids, slot=c, row=eff - self._p0, sink=pos if pos < st.sink_cap else -1, n_cur=c + 1)
         n_sk = st.n_pin if pos >= 2 * W else 0
         has_seg = pos >= 2 * W and seg_active       # the bank span, its length on the device
         n_prev = W if pos >= W else 0
         bias_on = bool(has_seg and st.seg_bias_active)
         ema_first = seg_active and not st.ema_ready
-        spec = (B, n_sk, has_seg, n_prev, seg_active, ema_first, bias_on)
-        if not self.use_graphs:
-            return self._decode_launch(st, spec)
-        self._size_workspace(st)
-        key = spec + tuple(t.data_ptr() for t in (st.k_prev, st.k_cur, st.v_prev, st.v_cur, st.kraw_cur, st.k_seg_rot,
-                                                   st.v_seg, st.sc_cur, st.tok_cur, st.seg_cur_ids, self._table,
-                                                   self.ws.buf, ops.gemm_workspace(self.device).buf)) + \
-            ((st.bias_early.data_ptr(), st.bias_late.data_ptr()) if bias_on else ())
-        ent = st.graphs.get(key)
-        if ent is None:
-            # No destructor may run HIP calls while the stream captures: collect garbage now and keep
-            # the collector off during the capture.
-            gc.collect()
-            gc_was_on = gc.isenabled()
-            gc.disable()
-            try:
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g):
-                    out = self._decode_launch(st, spec)
-            finally:
-                if gc_was_on:
-                    gc.enable()
-            ent = (g, out)
-            st.graphs[key] = ent
-            while len(st.graphs) > 8:
-                st.graphs.pop(next(iter(st.graphs)))
-        ent[0].replay()
-        return ent[1].clone()
+        indirect = B < ops.GEMM_MIN_ROWS
+        spec = (B, n_sk, has_seg, n_prev, seg_active, ema_first, bias_on, indirect)
+        out = torch.empty(B, self.w.embed.rows, dtype=torch.float32, device=self.device) if indirect else None
+        if bias_on and st.bias_rows is None:
+            raise RuntimeError("a resonance mode is active but this step's bias rows were not computed")
+        io.write(ids, slot=c, row=eff - self._p0, sink=pos if pos < st.sink_cap else -1, n_cur=c + 1, out=out,
+                 bias=st.bias_rows if bias_on else None)
+        try:
+            if not self.use_graphs:
+                lg = self._decode_launch(st, spec)
+                io.launched()
+                return out if indirect else lg
+            self._size_workspace(st)
+            key = spec + tuple(t.data_ptr() for t in (st.k_prev, st.k_cur, st.v_prev, st.v_cur, st.kraw_cur,
+                                                       st.k_seg_rot, st.v_seg, st.sc_cur, st.tok_cur, st.seg_cur_ids,
+                                                       self._table, self.ws.buf,
+                                                       ops.gemm_workspace(self.device).buf)) + \
+                ((st.bias_early.data_ptr(), st.bias_late.data_ptr()) if bias_on else ())
+            ent = st.graphs.get(key)
+            if ent is None:
+                # No destructor may run HIP calls while the stream captures: collect garbage now and keep
+                # the collector off during the capture.
+                gc.collect()
+                gc_was_on = gc.isenabled()
+                gc.disable()
+                try:
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g):
+                        lg = self._decode_launch(st, spec)
+                finally:
+                    if gc_was_on:
+                        gc.enable()
+                ent = (g, lg)
+                st.graphs[key] = ent
+                while len(st.graphs) > 8:
+                    st.graphs.pop(next(iter(st.graphs)))
+            ent[0].replay()
+            io.launched()
+        except BaseException:
+            io.resync()
+            raise
+        return out if indirect else ent[1].clone()
 
     def _batch_qkv_fusable(self, B: int) -> bool:
         """Decode batches that run the small-batch GEMM (8..64 rows) on Q8_0 / Q4_0 q/k/v weights take
@@ -610,15 +695,17 @@ class VAULTv3ForCausalLM:
     def _decode_launch(self, st: VAULTv3State, spec: tuple) -> torch.Tensor:
         """Every kernel of one decode step (embedding -> 28 layers -> scorer -> LM head) for the chunk
         configuration ``spec``; position-dependent values are read from the step buffer."""
-        B, n_sk, has_seg, n_prev, seg_active, ema_first, bias_on = spec
+        B, n_sk, has_seg, n_prev, seg_active, ema_first, bias_on, indirect = spec
         cfg, w = self.cfg, self.w
         H, G, D, d = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_model
         HD, GD = H * D, G * D
         io = st.step_io()
         step, n_cur = io.step, io.step[ops.L.STEP_N_CUR:ops.L.STEP_N_CUR + 1]
-        # token ring and segmenter (device words), then the embedding rows
-        ops.seg_step(io.ids, step, st.tok_cur, st.seg_cur_ids if seg_active else None, st.ctrl if seg_active else None,
-                     self.tier_dev, cfg.seg_min, cfg.seg_max)
+        # the slot's words and ids onto the device, token ring and segmenter, then the embedding rows
+        ops.step_begin(io.ring, io.RING, io.slot_bytes, io.counter, step, io.ids, io.out_ref if indirect else None,
+                       st.tok_cur, st.seg_cur_ids if seg_active else None, st.ctrl if seg_active else None,
+                       self.tier_dev, cfg.seg_min, cfg.seg_max,
+                       bias=(st.bias_early, st.bias_late) if bias_on else None)
         # bank span: its length is the device count (the bias rows cover the bank's capacity)
         m_dev = st.ctrl[ops.L.SEG_MEM_CNT:ops.L.SEG_MEM_CNT + 1]
         n_seg = st.k_seg_rot.shape[3] if has_seg else 0
@@ -674,6 +761,9 @@ class VAULTv3ForCausalLM:
             ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
         if seg_active:
             self._score(st, feats, T=1, c0=0, first=ema_first, out_index=step[ops.L.STEP_SLOT:ops.L.STEP_SLOT + 1])
+        if indirect:
+            ops.qlinear_indirect(self.w.embed, x, io.out_ref, norm=(self.w.norm, cfg.rms_eps))
+            return None
         return self._logits(x)
 
     def _qkv(self, lw, x: torch.Tensor, N: int):
@@ -947,7 +1037,7 @@ class VAULTv3ForCausalLM:
             if st.res is not None:
                 # the resonance fields as the step loop leaves them after the chunk's last token
                 st.pos = r1 - 1
-                self._resonance(st, clen - 1, r1 - 1, seg_active)
+                self._resonance(st, clen - 1, r1 - 1, seg_active, direct=True)
             outs.append(("h", x if all_logits else x[-1:]))
         st.pos = L
         if not all_logits:

@@ -187,6 +187,29 @@ def _gemv(w: QWeight, x: torch.Tensor, out: Optional[torch.Tensor], epi: int, bi
     return out
 
 
+def qlinear_indirect(w: QWeight, x: torch.Tensor, y_addr: torch.Tensor,
+                     norm: Optional[Tuple[torch.Tensor, float]] = None) -> None:
+    """y = u @ W^T into the [B, rows] fp32 buffer whose address the int64 device word ``y_addr`` holds
+    when the launch runs (vgx_qlinear_indirect); GEMV batches (B < GEMM_MIN_ROWS) only."""
+    _need(x, torch.float32, "x")
+    if w.gateup:
+        raise ValueError("qlinear_indirect takes a plain tensor")
+    if y_addr.dtype != torch.int64 or y_addr.numel() != 1 or y_addr.device != x.device:
+        raise ValueError("y_addr must be one int64 word on the activations' device")
+    x2 = x.reshape(-1, w.cols) if x.dim() != 2 else x
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    B = x2.shape[0]
+    if B >= GEMM_MIN_ROWS:
+        raise ValueError("qlinear_indirect runs the GEMV (batches below GEMM_MIN_ROWS)")
+    nw, eps = (None, 0.0) if norm is None else norm
+    if nw is not None:
+        _need(nw, torch.float32, "norm weight")
+    L.check(L.load().vgx_qlinear_indirect(w.dtype, w.packed.data_ptr(), w.rows, w.cols, x2.data_ptr(), x2.stride(0),
+                                          B, _ptr(nw), float(eps), None, y_addr.data_ptr(), w.rows, L.EPI_STORE,
+                                          _stream(x.device)), "vgx_qlinear_indirect")
+
+
 def qlinear(w: QWeight, x: torch.Tensor, bias: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
             accumulate: bool = False, norm: Optional[Tuple[torch.Tensor, float]] = None) -> torch.Tensor:
     """y = u @ W^T (+ bias) with u = x, or u = RMSNorm(x) with norm = (weight, eps); with ``accumulate``
@@ -550,6 +573,22 @@ def seg_step(ids: torch.Tensor, step: torch.Tensor, tok_cur: torch.Tensor, seg_c
     L.check(L.load().vgx_seg_step(ids.data_ptr(), B, step.data_ptr(), tok_cur.data_ptr(), tok_cur.stride(0),
                                   _ptr(seg_cur), _ptr(ctrl), _ptr(tiers), tiers.numel() if tiers is not None else 0,
                                   seg_min, seg_max, W, _stream(tok_cur.device)), "vgx_seg_step")
+
+
+def step_begin(ring: int, n_slots: int, slot_bytes: int, counter: torch.Tensor, step: torch.Tensor, ids: torch.Tensor,
+               out_ref: Optional[torch.Tensor], tok_cur: torch.Tensor, seg_cur: Optional[torch.Tensor],
+               ctrl: Optional[torch.Tensor], tiers: Optional[torch.Tensor], seg_min: int, seg_max: int,
+               bias: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> None:
+    """The decode step's first launch (vgx_step_begin): the step words, ids and output address from
+    slot (*counter mod n_slots) of the pinned host ring at address ``ring``, then vgx_seg_step's
+    bookkeeping; with ``bias`` = (early, late) [H, cap] fp32 rows, the slot's bias rows."""
+    B, W = tok_cur.shape
+    be, bl = bias if bias is not None else (None, None)
+    H, ld, cap = (be.shape[0], be.stride(0), be.shape[1]) if be is not None else (0, 0, 0)
+    L.check(L.load().vgx_step_begin(ring, n_slots, slot_bytes, counter.data_ptr(), step.data_ptr(), ids.data_ptr(), B,
+                                    _ptr(out_ref), tok_cur.data_ptr(), tok_cur.stride(0), _ptr(seg_cur), _ptr(ctrl),
+                                    _ptr(tiers), tiers.numel() if tiers is not None else 0, seg_min, seg_max, W,
+                                    _ptr(be), _ptr(bl), H, ld, cap, _stream(tok_cur.device)), "vgx_step_begin")
 
 
 def seg_evict(sc_prev, seg_prev, tok_prev, mem_pos, mem_score, mem_tok, mem_seg, ctrl, ev: int, t0: int,
