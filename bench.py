@@ -368,6 +368,29 @@ def chat_prompt(cfg, toks, n_tokens: int = CHAT_TOKENS) -> list:
         i += 1
 
 
+def prefill_model_figures(model, L: int = 8192, reps: int = 3):
+    """model.prefill of an L-token prompt of random ids (batch 1, the chunk-recurrent path with segment
+    memory: chunk GEMMs on the tiled kernel, MFMA chunk attention, the boundary's bank merge), fp32 KV
+    (the model's state) and bf16 KV; tokens/s as the median of ``reps`` timed prefills after a warm-up."""
+    import torch
+    from vault_amd.model import VAULTv3ForCausalLM
+    g = torch.Generator().manual_seed(21)
+    ids = torch.randint(0, model.cfg.vocab_size, (1, L), generator=g)
+    out = {"config": f"model.prefill, batch 1, {L} random ids, segment memory on"}
+    for name, kv in (("fp32_kv", torch.float32), ("bf16_kv", torch.bfloat16)):
+        m = model if kv == model.kv_dtype else VAULTv3ForCausalLM(model.w, kv_dtype=kv)
+        m.prefill(ids[:, :2048])
+        ts = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            m.prefill(ids)
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        out[f"{name}_tokens_per_s"] = round(L / sorted(ts)[len(ts) // 2], 1)
+    return out
+
+
 def chat_figures(model, decode_steps: int = 48):
     """The 1.54B model with token strings (a synthetic word vocabulary over the 151665 ids: ChatML
     specials, key / value words, break-tier punctuation), so the resonance, quarantine and segment
@@ -582,7 +605,8 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="only the timed decode steps (for per-kernel profiles of the step)")
     ap.add_argument("--figures", choices=("gemv", "attn_decode", "attn_decode_b1", "attn_prefill", "gemm_prefill",
-                                          "roofline", "gateup", "decode_batch32", "lm_head", "chat"),
+                                          "roofline", "gateup", "decode_batch32", "lm_head", "chat",
+                                          "prefill_model"),
                     help="only one set of kernel figures, printed as JSON (for per-kernel profiles)")
     ap.add_argument("--pmc", action="store_true",
                     help="only run the launches the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs count")
@@ -628,6 +652,12 @@ def main() -> int:
         del tensors
         print(json.dumps({"chat": chat_figures(model)}), flush=True)
         return 0
+    if args.figures == "prefill_model":
+        cfg = model_config()
+        model, tensors = build_model(cfg, dev, torch.float32)
+        del tensors
+        print(json.dumps({"prefill_model": prefill_model_figures(model)}), flush=True)
+        return 0
     if args.figures == "lm_head":
         # the 151665 x 1536 rows of the gemv figures at batch 1 (for the streaming kernel's profiles)
         print(json.dumps({"lm_head": gemv_figures(dev, batches=(1,), shapes=[(151665, 1536)])}), flush=True)
@@ -664,6 +694,7 @@ def main() -> int:
         kernels["gemm_prefill"] = gemm_figures(dev)
         if args.batch == 1:
             kernels["decode_batch32"] = batched_decode(model)
+            kernels["prefill_8192"] = prefill_model_figures(model)
             kernels["chat"] = chat_figures(model)
         _log("kernel figures done")
     cpu = None

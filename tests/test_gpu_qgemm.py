@@ -71,11 +71,14 @@ def test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm):
 @pytest.mark.parametrize("rows,cols,batch,epi,norm", [
     (8960, 1536, 1024, "swiglu", True), (10246, 512, 820, "accum", False), (10246, 512, 820, "store", True),
     (65541, 256, 40, "store", True), (65541, 256, 17, "accum", False), (65541, 768, 32, "store", True),
-    (65541, 768, 20, "store", False), (65541, 1536, 32, "store", True)])
+    (65541, 768, 20, "store", False), (65541, 1536, 32, "store", True), (1536, 8960, 300, "accum", False),
+    (2048, 1536, 1000, "store", True)])
 def test_qgemm_chunk_shapes_match_oracle(dev, dt, rows, cols, batch, epi, norm):
     """Many tiles: the gate/up pair of a full 1024-token prefill chunk (1120 tiles, three rounds of
     workgroups), 10246 x 512 over 820 activation rows (ragged rows and activation rows in the last
-    tiles), and LM-head-like tall weights (65541 rows, ragged; the stores over 768 and 1536 columns run
+    tiles), K-split launches of 512 and more workgroups with ragged activation tiles (1536 x 8960 over
+    300 rows: 36 tiles x 16 splits; 2048 x 1536 over 1000 rows: 128 tiles x 4 splits) on the LDS-DMA
+    kernel, and LM-head-like tall weights (65541 rows, ragged; the stores over 768 and 1536 columns run
     on the persistent unsplit kernel, with 2 activation tiles per row group, the others on the 32-row
     tiles of the small-batch kernel).  Same bar as above."""
     test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm)

@@ -396,6 +396,215 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
     }
 }
 
+// The tiled kernel with its stages filled by LDS DMA: buffer loads that write LDS directly, issued from
+// inline assembly so that the compiler does not make the LDS reads of block k wait for them (it treats
+// every LDS read after a DMA it knows of as dependent on it).  Two stages: the loads of block k + 1
+// leave right after the barrier of block k and land in the other stage while block k is multiplied, and
+// they need no staging registers, which leaves room for three workgroups per CU (163 VGPRs, 38 KB of
+// LDS) instead of two (256 VGPRs with the register double buffer of qgemm_tile_kernel).  Same
+// arithmetic as qgemm_tile_kernel, bit for bit.  The activation rows of a stage are unpadded 64-byte
+// rows whose 16-byte pieces are swizzled by (row >> 2) & 3, so the MFMA operand reads stay free of bank
+// conflicts.  Measured on a 1024-token chunk (Q4_0 / Q8_0): gate/up 228.9 -> 193.5 / 251.4 -> 222.5 us,
+// down 143.0 -> 137.2 / 156.1 -> 144.1, q|k|v 49.2 -> 48.3 / 50.8 -> 49.5, o 43.6 -> 45.8 / 46.6 -> 44.9;
+// with three stages at two workgroups per CU 209.7 us for the Q4_0 gate/up, with four 221.1.
+typedef int dma_rsrc_t __attribute__((ext_vector_type(4)));
+constexpr uint32_t kDmaPast = 0x80000000u;      // a buffer offset past every operand: reads zero
+
+__device__ __forceinline__ dma_rsrc_t dma_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    dma_rsrc_t r;
+    r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu));
+    r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    r.w = 0x00020000;
+    return r;
+}
+
+// Lane l's 16 (4) bytes at byte offset voff of the buffer into LDS at lds + 16 l (4 l); lds is
+// wave-uniform.  Offsets past the buffer read zeros.  M0 (the LDS base) is written here and cannot be
+// declared clobbered (a reserved register); the kernel below makes no other use of M0 (gfx950 LDS
+// instructions do not read it), which its compiled code was checked for.
+__device__ __forceinline__ void dma16(dma_rsrc_t rs, uint32_t voff, const void *lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs)
+                 : "memory");
+}
+__device__ __forceinline__ void dma4(dma_rsrc_t rs, uint32_t voff, const void *lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs)
+                 : "memory");
+}
+
+template <int DT, int EPI, bool SPLIT>
+__global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
+                                                              int nblk, int64_t rows_out,
+                                                              const uint16_t *__restrict__ xh,
+                                                              const uint16_t *__restrict__ xl,
+                                                              const float *__restrict__ xsum, int64_t batch,
+                                                              const float *__restrict__ bias, float *__restrict__ y,
+                                                              int64_t ldy, float *__restrict__ part, int kper) {
+    constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
+    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 24.0f;
+    constexpr int APARTS = 4 * QB / 16;
+    constexpr int NA = kTM / 4 * APARTS / 64;           // 16-byte weight pieces: wave-loads per block
+    constexpr int A_B = kTM * QB, SC_B = kTM / 4 * 8, BH_B = kTN * QK * 2, BS_B = kTN * 4;
+    constexpr int STAGE_B = A_B + SC_B + 2 * BH_B + BS_B;
+    constexpr int NS = 2;
+    constexpr int NJ = NA + 1 + 2 * (BH_B / 1024) + BS_B / 256;   // wave-loads per block
+    constexpr int kERow = 64 + 4;
+    constexpr int EPI_B = kTN * kERow * 4;
+    __shared__ __align__(16) uint8_t smem[NS * STAGE_B > EPI_B ? NS * STAGE_B : EPI_B];
+    auto aq = [&](int buf) { return smem + buf * STAGE_B; };
+    auto asc = [&](int buf) { return reinterpret_cast<uint2 *>(smem + buf * STAGE_B + A_B); };
+    auto bh = [&](int buf) { return reinterpret_cast<uint16_t *>(smem + buf * STAGE_B + A_B + SC_B); };
+    auto bl = [&](int buf) { return reinterpret_cast<uint16_t *>(smem + buf * STAGE_B + A_B + SC_B + BH_B); };
+    auto bs = [&](int buf) { return reinterpret_cast<float *>(smem + buf * STAGE_B + A_B + SC_B + 2 * BH_B); };
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int cols = nblk * QK;
+    const int64_t rq0 = (int64_t)blockIdx.x * (kTM / 4);
+    const int64_t b0 = (int64_t)blockIdx.y * kTN;
+    const int blk_lo = SPLIT ? (int)blockIdx.z * kper : 0;
+    const int blk_hi = SPLIT ? min(nblk, blk_lo + kper) : nblk;
+
+    const dma_rsrc_t wrs = dma_rsrc(W, (uint32_t)(soff + n_rq * nblk * 8));
+    const dma_rsrc_t hrs = dma_rsrc(xh, (uint32_t)(batch * cols * 2));
+    const dma_rsrc_t lrs = dma_rsrc(xl, (uint32_t)(batch * cols * 2));
+    const dma_rsrc_t srs = dma_rsrc(xsum, (uint32_t)(batch * nblk * 4));
+    // wave-load j of a block: weight pieces (j < NA), scales, hi rows, lo rows, block sums
+    auto issue = [&](int blk, int buf) {
+#pragma unroll
+        for (int jj = 0; jj < (NJ + 3) / 4; ++jj) {
+            const int j = jj * 4 + wave;
+            if (j < NA) {
+                const int pc = j * 64 + lane;
+                const int64_t rq = rq0 + pc / APARTS;
+                const uint32_t o = rq < n_rq ? (uint32_t)((rq * nblk + blk) * 4 * QB + (pc % APARTS) * 16) : kDmaPast;
+                dma16(wrs, o, aq(buf) + j * 1024);
+            } else if (j == NA) {
+                const int64_t rq = rq0 + lane / 2;
+                const uint32_t o = rq < n_rq ? (uint32_t)(soff + (rq * nblk + blk) * 8 + (lane & 1) * 4) : kDmaPast;
+                dma4(wrs, o, asc(buf));
+            } else if (j < NA + 1 + 2 * (BH_B / 1024)) {
+                const int jb = j - NA - 1, pl = jb / (BH_B / 1024), jr = jb % (BH_B / 1024);
+                const int row = 16 * jr + (lane >> 2), slot = lane & 3, piece = slot ^ ((row >> 2) & 3);
+                const int64_t b = b0 + row;
+                const uint32_t o = b < batch ? (uint32_t)((b * cols + (int64_t)blk * QK + piece * 8) * 2) : kDmaPast;
+                dma16(pl ? lrs : hrs, o, reinterpret_cast<const uint8_t *>(pl ? bl(buf) : bh(buf)) + jr * 1024);
+            } else if (j < NJ) {
+                const int jb = j - NA - 1 - 2 * (BH_B / 1024);
+                const int64_t b = b0 + 64 * jb + lane;
+                const uint32_t o = b < batch ? (uint32_t)((b * nblk + blk) * 4) : kDmaPast;
+                dma4(srs, o, reinterpret_cast<const uint8_t *>(bs(buf)) + jb * 256);
+            }
+        }
+    };
+    f32x4_t acc[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[t][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](int buf) {
+        bf16x8_t af[4];
+        f16x8_t af16[4];
+        vgx_f16x2_t d[4][2];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int rql = wm * 16 + 4 * t + (l16 >> 2);
+            const uint2 w = *reinterpret_cast<const uint2 *>(aq(buf) + (rql * 4 + (l16 & 3)) * QB +
+                                                              (DT == VGX_Q8_0 ? 8 * lg : 8 * (lg & 1)));
+            tile_a_frags<DT>(w, lg, af[t], af16[t]);
+            const uint2 sc = asc(buf)[wm * 16 + 4 * t + lg];
+            d[t][0] = __builtin_bit_cast(vgx_f16x2_t, sc.x);
+            d[t][1] = __builtin_bit_cast(vgx_f16x2_t, sc.y);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int row = wn * 64 + 16 * c + l16;
+            const int off = row * QK + 8 * (lg ^ ((row >> 2) & 3));
+            const bf16x8_t hf = *reinterpret_cast<const bf16x8_t *>(bh(buf) + off);
+            const f16x8_t lf = *reinterpret_cast<const f16x8_t *>(bl(buf) + off);
+            const float ns = -OFF * bs(buf)[row];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                f32x4_t pr = f32x4_t{ns, ns, ns, ns};
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], hf, pr, 0, 0, 0);
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(af16[t], lf, pr, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf((float)d[t][i >> 1][i & 1], pr[i], acc[t][c][i]);
+            }
+        }
+    };
+
+    const int nb = blk_hi - blk_lo;
+    if (nb > 0) issue(blk_lo, 0);
+    for (int k = 0; k < nb; ++k) {
+        // this wave's loads of block k have landed and its reads of block k - 1 are done; the barrier
+        // extends both to the workgroup, so block k is complete and stage (k + 1) % 2 is free
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (k + 1 < nb) issue(blk_lo + k + 1, (k + 1) % NS);
+        compute(k % NS);
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");   // the stages are free for the epilogue
+
+    if constexpr (SPLIT) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int64_t crq = rq0 + wm * 16 + 4 * t + lg;
+            if (crq >= n_rq) continue;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int64_t b = b0 + wn * 64 + 16 * c + l16;
+                if (b >= batch) continue;
+                float4 v;
+                v.x = acc[t][c][0]; v.y = acc[t][c][1]; v.z = acc[t][c][2]; v.w = acc[t][c][3];
+                *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + b) * (n_rq * 4) + crq * 4) = v;
+            }
+        }
+        return;
+    }
+    float *et = reinterpret_cast<float *>(smem);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        if (wm == half) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    float4 v;
+                    v.x = acc[t][c][0]; v.y = acc[t][c][1]; v.z = acc[t][c][2]; v.w = acc[t][c][3];
+                    *reinterpret_cast<float4 *>(et + (wn * 64 + 16 * c + l16) * kERow + 16 * t + 4 * lg) = v;
+                }
+        }
+        __syncthreads();
+        const int64_t r0 = (rq0 + half * 16) * 4;
+        if constexpr (EPI == EPI_SWIGLU) {
+            for (int i = tid; i < kTN * 32; i += 256) {
+                const int bl_ = i >> 5, o = i & 31;
+                const int64_t b = b0 + bl_, oo = r0 / 2 + o;
+                if (b >= batch || oo >= rows_out) continue;
+                const float *er = et + bl_ * kERow + (o >> 1) * 4 + (o & 1);
+                const float g = er[0], u = er[2];
+                y[b * ldy + oo] = g / (1.0f + __expf(-g)) * u;
+            }
+        } else {
+            for (int i = tid; i < kTN * 64; i += 256) {
+                const int bl_ = i >> 6, rr = i & 63;
+                const int64_t b = b0 + bl_, row = r0 + rr;
+                if (b >= batch || row >= rows_out) continue;
+                float v = et[bl_ * kERow + rr];
+                if (bias) v += bias[row];
+                if constexpr (EPI == EPI_ACCUM) v += y[b * ldy + row];
+                y[b * ldy + row] = v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // F32 / BF16 / F16 weights (the segment scorer's fc1, F32 and BF16 model files) for many activation
 // rows, 16-bit elements widened exactly to fp32 as they are fetched: fp32 MFMA
@@ -2309,9 +2518,20 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     const int kper = (nblk + ks - 1) / ks;
     const dim3 grid((unsigned)((n_rq + kTM / 4 - 1) / (kTM / 4)), (unsigned)((batch + kTN - 1) / kTN), (unsigned)ks);
     const auto *w = static_cast<const uint8_t *>(w_packed);
+    // the DMA kernel for launches of at least 512 workgroups (its buffer ranges are 32-bit): the 1536 x
+    // 1536 o-projection of a 1024-token chunk (480 workgroups, about ten blocks each) measured slower on
+    // it, 45.8 against 43.6 us; q|k|v (512) 48.3 against 49.2
+    const bool dma = (int64_t)grid.x * grid.y * grid.z >= 512 && soff + n_rq * nblk * 8 < ((int64_t)1 << 31) &&
+                     batch * cols * 2 < ((int64_t)1 << 31);
 #define VGX_GEMM_GO(DT, EPI, SP)                                                                              \
-    hipLaunchKernelGGL((qgemm_tile_kernel<DT, EPI, SP>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, xh, xl, \
-                       xs, batch, bias, y, ldy, part, kper)
+    do {                                                                                                      \
+        if (dma)                                                                                              \
+            hipLaunchKernelGGL((qgemm_tile_dma_kernel<DT, EPI, SP>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, \
+                               xh, xl, xs, batch, bias, y, ldy, part, kper);                                   \
+        else                                                                                                  \
+            hipLaunchKernelGGL((qgemm_tile_kernel<DT, EPI, SP>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, xh, \
+                               xl, xs, batch, bias, y, ldy, part, kper);                                      \
+    } while (0)
 #define VGX_GEMM_EPI(DT)                                                                                      \
     do {                                                                                                      \
         if (ks > 1) VGX_GEMM_GO(DT, EPI_STORE, true);                                                         \
