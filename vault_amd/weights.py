@@ -44,9 +44,12 @@ class ScorerWeights:
     b2: torch.Tensor   # [1]
 
 
-def _f32(t: Tensor, device) -> torch.Tensor:
+def _f32(t: Tensor, device, uploaded: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """An F32 tensor as fp32 on the device: the uploaded payload viewed as floats, or a fresh upload."""
     if t.dtype != vlt3.F32:
         raise vlt3.VLT3Error(f"{t.name} must be F32")
+    if uploaded is not None:
+        return uploaded.view(torch.float32)
     return torch.from_numpy(np.frombuffer(t.data, dtype="<f4").copy()).to(device)
 
 
@@ -79,54 +82,62 @@ class ModelWeights:
         self = cls(cfg, device)
         self.tokens = tokens
         dev = self.device
+        # every payload crosses the bus once: the scan and the packing kernels read the same upload
+        up = {n: ops.QWeight._upload(t.data, dev) for n, t in tensors.items()}
         if scan:
-            bad = ops.count_nonfinite([(t.dtype, t.data, int(np.prod(t.shape))) for t in tensors.values()], dev)
+            bad = ops.count_nonfinite([(t.dtype, up[n], int(np.prod(t.shape))) for n, t in tensors.items()], dev)
             if any(bad):
                 names = [n for n, k in zip(tensors, bad) if k]
                 e = vlt3.VLT3Error(f"non-finite weights or scales in {names[:4]}")
                 e.code = vlt3.E_NAN
                 raise e
+        f32 = lambda name: _f32(tensors[name], dev, up[name])
         emb = tensors["embed_tokens.weight"]
-        self.embed = ops.QWeight.from_blocks(_block_dtype(emb), cfg.vocab_size, cfg.d_model, emb.data, dev)
-        self.norm = _f32(tensors["norm.weight"], dev)
+        self.embed = ops.QWeight.from_blocks(_block_dtype(emb), cfg.vocab_size, cfg.d_model, up["embed_tokens.weight"],
+                                             dev)
+        self.norm = f32("norm.weight")
         H, G, D, d, F = cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.d_model, cfg.d_ff
         for li in range(cfg.n_layers):
             p = f"layers.{li}."
             t = {k[len(p):]: v for k, v in tensors.items() if k.startswith(p)}
+            u_ = lambda n: up[p + n]
             q, k, v = t["self_attn.q_proj.weight"], t["self_attn.k_proj.weight"], t["self_attn.v_proj.weight"]
-            bq, bk, bv = (_f32(t[f"self_attn.{n}_proj.bias"], dev) for n in "qkv")
+            bq, bk, bv = (f32(f"{p}self_attn.{n}_proj.bias") for n in "qkv")
+            kv_data = torch.cat([u_("self_attn.k_proj.weight"), u_("self_attn.v_proj.weight")])
             if _block_dtype(q) == _block_dtype(k) == _block_dtype(v):
                 wq = None
-                wqkv = ops.QWeight.from_blocks(q.dtype, H * D + 2 * G * D, d, q.data + k.data + v.data, dev)
+                wqkv = ops.QWeight.from_blocks(q.dtype, H * D + 2 * G * D, d,
+                                               torch.cat([u_("self_attn.q_proj.weight"), kv_data]), dev)
                 bqkv = torch.cat([bq, bk, bv])
             else:
                 if _block_dtype(k) != _block_dtype(v):
                     raise vlt3.VLT3Error("k_proj and v_proj must share a dtype")
-                wq = ops.QWeight.from_blocks(q.dtype, H * D, d, q.data, dev)
-                wqkv = ops.QWeight.from_blocks(k.dtype, 2 * G * D, d, k.data + v.data, dev)
+                wq = ops.QWeight.from_blocks(q.dtype, H * D, d, u_("self_attn.q_proj.weight"), dev)
+                wqkv = ops.QWeight.from_blocks(k.dtype, 2 * G * D, d, kv_data, dev)
                 bqkv = torch.cat([bk, bv])
-            wq_rope = ops.QWeight.rope_from_blocks(q.dtype, H * D, d, q.data, D, H * D, dev)
-            wkv_rope = ops.QWeight.rope_from_blocks(k.dtype, 2 * G * D, d, k.data + v.data, D, G * D, dev)
+            wq_rope = ops.QWeight.rope_from_blocks(q.dtype, H * D, d, u_("self_attn.q_proj.weight"), D, H * D, dev)
+            wkv_rope = ops.QWeight.rope_from_blocks(k.dtype, 2 * G * D, d, kv_data, D, G * D, dev)
             o = t["self_attn.o_proj.weight"]
             g, u, dn = t["mlp.gate_proj.weight"], t["mlp.up_proj.weight"], t["mlp.down_proj.weight"]
             if _block_dtype(g) != _block_dtype(u):
                 raise vlt3.VLT3Error("gate_proj and up_proj must share a dtype")
             self.layers.append(LayerWeights(
-                ln1=_f32(t["input_layernorm.weight"], dev), ln2=_f32(t["post_attention_layernorm.weight"], dev),
+                ln1=f32(p + "input_layernorm.weight"), ln2=f32(p + "post_attention_layernorm.weight"),
                 wq=wq, wqkv=wqkv, bq=bq, bqkv=bqkv,
-                wo=ops.QWeight.from_blocks(_block_dtype(o), d, H * D, o.data, dev),
-                wgu=ops.QWeight.gateup_from_blocks(g.dtype, F, d, g.data, u.data, dev),
-                wd=ops.QWeight.from_blocks(_block_dtype(dn), d, F, dn.data, dev),
+                wo=ops.QWeight.from_blocks(_block_dtype(o), d, H * D, u_("self_attn.o_proj.weight"), dev),
+                wgu=ops.QWeight.gateup_from_blocks(g.dtype, F, d, u_("mlp.gate_proj.weight"), u_("mlp.up_proj.weight"),
+                                                   dev),
+                wd=ops.QWeight.from_blocks(_block_dtype(dn), d, F, u_("mlp.down_proj.weight"), dev),
                 wq_rope=wq_rope, wkv_rope=wkv_rope,
             ))
         if cfg.has_seg_scorer and "seg_scorer.ln.weight" in tensors:
             fd = len(cfg.seg_layers) * d
-            w2 = _f32(tensors["seg_scorer.fc2.weight"], dev)
+            w2 = f32("seg_scorer.fc2.weight")
             self.scorer = ScorerWeights(
-                ln_w=_f32(tensors["seg_scorer.ln.weight"], dev), ln_b=_f32(tensors["seg_scorer.ln.bias"], dev),
-                w1=ops.QWeight.from_blocks(vlt3.F32, cfg.seg_hidden, fd, tensors["seg_scorer.fc1.weight"].data, dev),
-                b1=_f32(tensors["seg_scorer.fc1.bias"], dev), w2=w2.reshape(-1),
-                b2=_f32(tensors["seg_scorer.fc2.bias"], dev))
+                ln_w=f32("seg_scorer.ln.weight"), ln_b=f32("seg_scorer.ln.bias"),
+                w1=ops.QWeight.from_blocks(vlt3.F32, cfg.seg_hidden, fd, up["seg_scorer.fc1.weight"], dev),
+                b1=f32("seg_scorer.fc1.bias"), w2=w2.reshape(-1),
+                b2=f32("seg_scorer.fc2.bias"))
         torch.cuda.synchronize(dev)
         return self
 
