@@ -558,7 +558,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
             const int64_t row = min(c.y + kt * 16 + l16, last);
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc)
-                kr[kt][kc] = *reinterpret_cast<const uint4 *>(kb + o + row * D + kc * 32 + lg * 8);
+                kr[kt][kc] = ld_stream(reinterpret_cast<const uint4 *>(kb + o + row * D + kc * 32 + lg * 8));
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -566,7 +566,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
                 const int64_t row = min(c.y + 2 * rp + h2, last);
-                vr[i][h2] = *reinterpret_cast<const uint4 *>(vb + o + row * D + cc * 8);
+                vr[i][h2] = ld_stream(reinterpret_cast<const uint4 *>(vb + o + row * D + cc * 8));
             }
         }
     };
@@ -791,11 +791,11 @@ template <int KV>
 __device__ __forceinline__ void load_quads(const void *base, int64_t elem_off, float (&f)[8]) {
     if constexpr (KV == VGX_F32) {
         const float *p = static_cast<const float *>(base) + elem_off;
-        const float4 a = *reinterpret_cast<const float4 *>(p), c = *reinterpret_cast<const float4 *>(p + 64);
+        const float4 a = ld_stream(reinterpret_cast<const float4 *>(p)), c = ld_stream(reinterpret_cast<const float4 *>(p + 64));
         f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = c.x; f[5] = c.y; f[6] = c.z; f[7] = c.w;
     } else {
         const uint16_t *p = static_cast<const uint16_t *>(base) + elem_off;
-        const uint2 a = *reinterpret_cast<const uint2 *>(p), c = *reinterpret_cast<const uint2 *>(p + 64);
+        const uint2 a = ld_stream(reinterpret_cast<const uint2 *>(p)), c = ld_stream(reinterpret_cast<const uint2 *>(p + 64));
         f[0] = __uint_as_float(a.x << 16); f[1] = __uint_as_float(a.x & 0xFFFF0000u);
         f[2] = __uint_as_float(a.y << 16); f[3] = __uint_as_float(a.y & 0xFFFF0000u);
         f[4] = __uint_as_float(c.x << 16); f[5] = __uint_as_float(c.x & 0xFFFF0000u);
@@ -884,10 +884,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_b1_kernel(
             vl_[j] = r0 + 2 * j + half;
             const char *vr = vrow + (int64_t)(2 * j + half) * D * ESZ;
             if constexpr (KV == VGX_F32) {
-                const float4 t = reinterpret_cast<const float4 *>(vr)[l32];
+                const float4 t = ld_stream(reinterpret_cast<const float4 *>(vr) + l32);
                 vf[j][0] = t.x; vf[j][1] = t.y; vf[j][2] = t.z; vf[j][3] = t.w;
             } else {
-                const uint2 t = reinterpret_cast<const uint2 *>(vr)[l32];
+                const uint2 t = ld_stream(reinterpret_cast<const uint2 *>(vr) + l32);
                 vf[j][0] = __uint_as_float(t.x << 16); vf[j][1] = __uint_as_float(t.x & 0xFFFF0000u);
                 vf[j][2] = __uint_as_float(t.y << 16); vf[j][3] = __uint_as_float(t.y & 0xFFFF0000u);
             }
@@ -911,10 +911,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_b1_kernel(
             vl_[j] = lr;
             const char *vrow = pick4(s, vp[0], vp[1], vp[2], vp[3]) + lr * D * ESZ;
             if constexpr (KV == VGX_F32) {
-                const float4 t = reinterpret_cast<const float4 *>(vrow)[l32];
+                const float4 t = ld_stream(reinterpret_cast<const float4 *>(vrow) + l32);
                 vf[j][0] = t.x; vf[j][1] = t.y; vf[j][2] = t.z; vf[j][3] = t.w;
             } else {
-                const uint2 t = reinterpret_cast<const uint2 *>(vrow)[l32];
+                const uint2 t = ld_stream(reinterpret_cast<const uint2 *>(vrow) + l32);
                 vf[j][0] = __uint_as_float(t.x << 16); vf[j][1] = __uint_as_float(t.x & 0xFFFF0000u);
                 vf[j][2] = __uint_as_float(t.y << 16); vf[j][3] = __uint_as_float(t.y & 0xFFFF0000u);
             }

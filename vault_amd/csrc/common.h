@@ -169,6 +169,27 @@ VGX_DEV float ref_geluf(float x) {
     return 0.5f * x * (1.0f + ref_erff(x * 0.70710678118654752f));
 }
 
+// Loads of data that a decode step or a prefill chunk reads once (weights, KV rows): the non-temporal
+// cache policy (nt), which streams them past the caches' normal replacement.  kStreamAux is the same
+// policy for buffer loads.  Measured on the 151665 x 1536 Q8_0 LM head GEMV: 43.7 -> 38.3 us.
+constexpr int kStreamAux = 2;
+typedef unsigned vgx_u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned vgx_u32x2_t __attribute__((ext_vector_type(2)));
+typedef float vgx_f32x4_t __attribute__((ext_vector_type(4)));
+
+VGX_DEV uint4 ld_stream(const uint4 *p) {
+    const vgx_u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const vgx_u32x4_t *>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+VGX_DEV uint2 ld_stream(const uint2 *p) {
+    const vgx_u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const vgx_u32x2_t *>(p));
+    return make_uint2(v[0], v[1]);
+}
+VGX_DEV float4 ld_stream(const float4 *p) {
+    const vgx_f32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const vgx_f32x4_t *>(p));
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
+
 // One element of a KV-state tensor of dtype KV (VGX_F32, or VGX_BF16 rounded to nearest even).
 template <int KV>
 VGX_DEV void store_kv(void *base, int64_t idx, float v) {

@@ -128,11 +128,11 @@ __device__ __forceinline__ void gemv_load(BlockRegs<DT> &r, const uint8_t *__res
         r.p = reinterpret_cast<const float4 *>(qp);
     } else if constexpr (gemv_half(DT)) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) r.q[i] = reinterpret_cast<const uint4 *>(qp)[i];
+        for (int i = 0; i < 16; ++i) r.q[i] = ld_stream(reinterpret_cast<const uint4 *>(qp) + i);
     } else {
 #pragma unroll
-        for (int i = 0; i < 4 * QB / 16; ++i) r.q[i] = reinterpret_cast<const uint4 *>(qp)[i];
-        r.s = *reinterpret_cast<const uint2 *>(W + soff + (rq * nblk + gb) * 8);
+        for (int i = 0; i < 4 * QB / 16; ++i) r.q[i] = ld_stream(reinterpret_cast<const uint4 *>(qp) + i);
+        r.s = ld_stream(reinterpret_cast<const uint2 *>(W + soff + (rq * nblk + gb) * 8));
     }
 }
 
@@ -146,7 +146,7 @@ __device__ __forceinline__ void gemv_block(const BlockRegs<DT> &br, const float 
             float wv[QK];
 #pragma unroll
             for (int j4 = 0; j4 < 8; ++j4) {
-                const float4 t = br.p[r * 8 + j4];
+                const float4 t = ld_stream(br.p + r * 8 + j4);
                 wv[j4 * 4 + 0] = t.x; wv[j4 * 4 + 1] = t.y; wv[j4 * 4 + 2] = t.z; wv[j4 * 4 + 3] = t.w;
             }
 #pragma unroll
@@ -666,11 +666,11 @@ __global__ __launch_bounds__(256) void gemv1_stream_kernel(GemvArgs a) {
         const uint32_t sb = (uint32_t)rq * (kStreamBlocks * 8);
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-            const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, qb + qoff[j], 0, 0);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, qb + qoff[j], 0, kStreamAux);
             wq[s][j] = make_uint4(v[0], v[1], v[2], v[3]);
         }
 #pragma unroll
-        for (int j = 0; j < NL; ++j) wsc[s][j] = __builtin_amdgcn_raw_buffer_load_b16(srs, sb + sofs[j], 0, 0);
+        for (int j = 0; j < NL; ++j) wsc[s][j] = __builtin_amdgcn_raw_buffer_load_b16(srs, sb + sofs[j], 0, kStreamAux);
     };
     // lnw * x staged once per workgroup (the activation loads go first, so waiting for them does not
     // wait for the weights), then the weight ring, then this lane's 96 activations from LDS.
@@ -902,9 +902,9 @@ __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
         const uint32_t qo = ok ? (uint32_t)((rq * nblk + blk) * 4 * QB + row * QB + (DT == VGX_Q8_0 ? (lane & 1) * 16 : 0))
                                : kStreamPastEnd;
         const uint32_t so = ok ? (uint32_t)((rq * nblk + blk) * 8 + row * 2) : kStreamPastEnd;
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, qo, 0, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, qo, 0, kStreamAux);
         wq[k] = make_uint4(v[0], v[1], v[2], v[3]);
-        wsc[k] = __builtin_amdgcn_raw_buffer_load_b16(srs, so, 0, 0);
+        wsc[k] = __builtin_amdgcn_raw_buffer_load_b16(srs, so, 0, kStreamAux);
     }
 #pragma unroll
     for (int u = 0; u < XR; ++u) {
@@ -1000,7 +1000,7 @@ __global__ __launch_bounds__(64 * kF32PiecesWaves) void gemv_f32_pieces_kernel(G
         const bool ok = pc < npc && blk < nblk;
         blk_of[k] = min(blk, nblk - 1);
         const uint32_t o = ok ? (uint32_t)((rq * nblk + blk) * 512 + (lane & 31) * 16) : kStreamPastEnd;
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, o, 0, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, o, 0, kStreamAux);
         wv[k] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
     }
 #pragma unroll

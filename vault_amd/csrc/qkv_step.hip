@@ -198,9 +198,9 @@ __device__ __forceinline__ void qkv_pieces_rq(const uint8_t *__restrict__ W, int
         const uint32_t qo = ok ? (uint32_t)((rq * nblk + blk) * 4 * QB + row * QB + (DT == VGX_Q8_0 ? (lane & 1) * 16 : 0))
                                : kStreamPastEnd;
         const uint32_t so = ok ? (uint32_t)((rq * nblk + blk) * 8 + row * 2) : kStreamPastEnd;
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, qo, 0, 0);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, qo, 0, kStreamAux);
         wq[k] = make_uint4(v[0], v[1], v[2], v[3]);
-        wsc[k] = __builtin_amdgcn_raw_buffer_load_b16(srs, so, 0, 0);
+        wsc[k] = __builtin_amdgcn_raw_buffer_load_b16(srs, so, 0, kStreamAux);
     }
     __syncthreads();                                   // the activations are staged
     float acc = 0.0f;
