@@ -558,7 +558,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
             const int64_t row = min(c.y + kt * 16 + l16, last);
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc)
-                kr[kt][kc] = ld_stream(reinterpret_cast<const uint4 *>(kb + o + row * D + kc * 32 + lg * 8));
+                kr[kt][kc] = *reinterpret_cast<const uint4 *>(kb + o + row * D + kc * 32 + lg * 8);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -566,7 +566,7 @@ __global__ __launch_bounds__(64 * kWaves) void attn_decode_mfma_kernel(
 #pragma unroll
             for (int h2 = 0; h2 < 2; ++h2) {
                 const int64_t row = min(c.y + 2 * rp + h2, last);
-                vr[i][h2] = ld_stream(reinterpret_cast<const uint4 *>(vb + o + row * D + cc * 8));
+                vr[i][h2] = *reinterpret_cast<const uint4 *>(vb + o + row * D + cc * 8);
             }
         }
     };
