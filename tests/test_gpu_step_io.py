@@ -186,3 +186,46 @@ def test_qlinear_indirect_graph_replays_into_new_buffers(dev):
         outs.append(o)
     for r in range(5):
         assert torch.equal(outs[r], wants[r]), r
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_step_ring_resyncs_after_failed_steps(dev, graphs):
+    """The ring's host slot number follows the device counter through failures: a slot consumed by a
+    launch whose host bookkeeping never ran (counter ahead), and a step that fails before its first launch
+    (counter behind).  Decoding then continues bit-identical to an undisturbed state."""
+    from vault_amd.model import VAULTv3ForCausalLM
+    from vault_amd.weights import ModelWeights
+    cfg = modelgen.tiny_cfg(head_dim=128, seg_budget=12)
+    tensors, _, _ = modelgen.build(cfg, "q8_0", seed=4)
+    w = ModelWeights.from_tensors(cfg, tensors, dev)
+    ma, mb = VAULTv3ForCausalLM(w), VAULTv3ForCausalLM(w)
+    ma.use_graphs = mb.use_graphs = graphs
+    sa, sb = ma.new_state(1), mb.new_state(1)
+    ids = np.random.default_rng(8).integers(0, cfg.vocab_size - 8, 70)
+    io = sa.step_io()
+    for i, t in enumerate(ids):
+        if i == 5:
+            # a slot consumed on the device without the host's bookkeeping
+            tok = torch.zeros(1, cfg.window, dtype=torch.int32, device=dev)
+            io.write(torch.tensor([7]), 0, 0, -1, 1)
+            ops.step_begin(io.ring, io.RING, io.slot_bytes, io.counter, io.step, io.ids, None, tok, None, None, None,
+                           cfg.seg_min, cfg.seg_max)
+            io.resync()
+            assert io.i % io.RING == int(io.counter[0])
+        if i == 9:
+            # a step that fails after its slot was written, before its first launch (a replayed graph never
+            # calls ops.step_begin from the host: the workspace sizing before the replay fails instead)
+            def failing(*a, **k):
+                raise RuntimeError("planted failure")
+            holder, name = (ma, "_size_workspace") if graphs else (ops, "step_begin")
+            real = getattr(holder, name)
+            setattr(holder, name, failing)
+            try:
+                with pytest.raises(RuntimeError, match="planted"):
+                    ma.step(torch.tensor([int(t)]), sa)
+            finally:
+                setattr(holder, name, real)
+            assert io.i % io.RING == int(io.counter[0]) and sa.pos == i
+        la = ma.step(torch.tensor([int(t)]), sa)
+        lb = mb.step(torch.tensor([int(t)]), sb)
+        assert torch.equal(la, lb), i
