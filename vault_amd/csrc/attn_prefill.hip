@@ -9,29 +9,39 @@
 // (_build_chunk_resonance_bias, :1718-1793, added to the scores at :2083-2090), whose rows are the
 // per-position biases of the step rule, so a chunk with resonance active stays on this kernel.
 //
-// Mapping.  A workgroup = one (query block, kv group g, tile of 32 queries) with one wave per query
-// head of the group (GRP waves), so every K/V tile staged in LDS serves all GRP heads.  A wave holds
-// its 32 queries as two 16-query MFMA tiles and computes, per 32 keys, with v_mfma_f32_16x16x32_bf16:
+// Mapping.  A workgroup = one (query block, kv group g, tile of 16 NQT QW queries) with QW waves per
+// query head of the group (GRP QW waves), so every K/V tile staged in LDS serves all GRP heads and QW
+// query tiles.  A wave holds its 16 NQT queries as NQT 16-query MFMA tiles and computes, per 32 keys,
+// with v_mfma_f32_16x16x32_bf16:
 //   S^T (keys x queries) = K Q^T       A = K rows from LDS, B = Q^T fragments kept in registers;
 //                                      fp32 queries enter as a bf16 hi + lo pair (two MFMAs), so
 //                                      the scores keep fp32-level accuracy;
-//   O^T (dims x queries) += V^T P^T    A = V^T from a transposed LDS copy, B = P^T straight from
-//                                      the S^T accumulators as a bf16 hi + lo pair (two MFMAs):
-//                                      8-bit probabilities alone exceed the bf16 attention bound
-//                                      when few keys carry the weight.
+//   O^T (dims x queries) += V^T P^T    A = V^T from LDS, B = P^T straight from the S^T accumulators
+//                                      as a bf16 hi + lo pair (two MFMAs): 8-bit probabilities alone
+//                                      exceed the bf16 attention bound when few keys carry the weight.
+// Staging.  bf16 K / V at 4 or more heads per group are copied into LDS by LDS DMA (buffer loads that
+// write LDS, no registers or VALU involved), double-buffered in 128-key tiles: the next tile's loads
+// leave right after the barrier that publishes the current one.  Both tiles keep the rows as they are
+// in memory (256 bytes per key), each 16-byte piece p of row r stored at slot p ^ (r & 15), so the
+// 16-byte K reads of 16 rows and the transposed V reads stay free of bank conflicts; the V^T operand
+// comes from ds_read_b64_tr_b16, which hands lane i of a 16-lane group element i % 4 of the 8-byte
+// pieces that lanes i / 4 + 4 k address (k = 0..3): lane lq addresses key 4 lg + lq / 4, dims
+// 16 dt + 4 (lq % 4) .. + 3, and receives dim 16 dt + lq of keys 4 lg .. 4 lg + 3.  Otherwise (fp32
+// K / V, one or two heads per group) each tile is loaded into registers during the previous tile's
+// math and stored into LDS, K as is (padded rows), V transposed.
 // bf16 K and V stay bf16 end to end (no conversions in the staging loop): MFMA throughput is abundant
 // here, VALU issue is what bounds the kernel.  fp32 K and V (an fp32 state read in place) are staged
 // as three bf16 planes (hi, mid, lo: 24 significant bits, the whole fp32 mantissa), and the fp32
 // queries and the probabilities are split the same way; each product keeps the six piece pairs of
 // order <= 2 (hi x hi, hi x mid, mid x hi, hi x lo, lo x hi, mid x mid) and drops those below 2^-24
 // of it, so scores and outputs carry fp32-level error (about 2^-22 relative) instead of the 2^-17 of
-// a hi + lo split.  The fp32 path holds 16 queries per wave: its three query pieces would not fit
-// the registers of two 16-query tiles.  In both products a lane of the 16 x 16 output owns
+// a hi + lo split.  In both products a lane of the 16 x 16 output owns
 // one query column, so the online-softmax state (running max, rescale of O) is lane-local; the max
 // over a query's keys needs two cross-lane steps.  The K-dimension slots of A and B are assigned the
 // same way in each product (lane group lg holds slots 8 lg .. 8 lg + 7 of both operands), which is
-// all the matrix product needs.  Key tiles entirely in the causal future of the 32 queries are not
-// loaded; keys of partially masked 32-key chunks get -inf (fully visible chunks skip the mask).
+// all the matrix product needs.  Key tiles entirely in the causal future of the workgroup's queries
+// are not loaded, a wave skips the 32-key chunks in the future of its own queries, and keys of
+// partially masked chunks get -inf (fully visible chunks skip the mask).
 // Scores are scaled by scale * log2(e) and use the hardware exp2 (v_exp_f32, 1 ulp; results below
 // the normal range flush to zero, which no probability normalised by the running max can notice).
 #include "common.h"
@@ -44,11 +54,21 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kKT = 64;             // keys per LDS tile
+constexpr int kKTDma = 128;         // keys per LDS tile of bf16 K / V staged by LDS DMA
 constexpr int kD = 128;             // head dim (the kernel is specialised for 128)
 constexpr int kKRow = kD + 8;       // LDS row of K, bf16 (16 bytes of padding)
 constexpr int kMaxBlocks = 8;
 constexpr float kNegBig = -1.0e30f;
 constexpr float kLazyMax = 8.0f;    // log2 of the largest unnormalised probability
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef short v8i16_t __attribute__((ext_vector_type(8)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives 16-bit element i % 4 of the 8-byte
+// pieces addressed by lanes i / 4 + 4 k of the group, k = 0..3 (element k of the result).
+__device__ __forceinline__ v4i16_t lds_read_tr16(const uint8_t *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16_t *)(p));
+}
 
 template <typename T>
 __device__ __forceinline__ T sel4(int i, T a0, T a1, T a2, T a3) {
@@ -94,20 +114,20 @@ struct PrefillArgs {
     int o_bf16;        // output rounded to bf16 (round to nearest even) instead of fp32
 };
 
-
-template <int GRP, bool QSPLIT, int NQT, bool KF>
-__global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
-    constexpr int kQTile = 16 * NQT;
-    // KF: fp32 K / V, staged as bf16 hi + lo planes (tiles of 32 keys: the same bytes per tile)
-    constexpr int KT = KF ? 32 : kKT;               // keys per LDS tile
+template <int GRP, bool QSPLIT, int NQT, bool KF, int QW, bool DMA>
+__global__ __launch_bounds__(64 * GRP * QW) void attn_prefill_kernel(PrefillArgs a) {
+    constexpr int kQTile = 16 * NQT * QW;
+    // keys per LDS tile (fp32 K / V: 32, staged as three bf16 planes)
+    constexpr int KT = KF ? 32 : (DMA ? kKTDma : kKT);
     constexpr int VROW = KT + 8;                    // LDS row of V^T, bf16 (16 bytes of padding)
     constexpr int NP = KF ? 3 : 1;                  // bf16 planes per K / V operand
     constexpr int NQP = QSPLIT ? (KF ? 3 : 2) : 1;  // bf16 pieces per query
     constexpr int NPP = KF ? 3 : 2;                 // bf16 pieces per probability
     constexpr int ORD = KF ? 2 : 1;                 // products of pieces i x j kept when i + j <= ORD
     constexpr int ESZ = KF ? 4 : 2;                 // bytes per K / V element in memory
-    __shared__ __align__(16) uint16_t ks[NP * KT * kKRow];
-    __shared__ __align__(16) uint16_t vt[NP * kD * VROW];
+    static_assert(!DMA || !KF, "LDS DMA stages bf16 K / V as they are");
+    __shared__ __align__(16) uint16_t ks[DMA ? 2 * 2 * KT * kD : NP * KT * kKRow];   // DMA: [stage][K, V][key][dim]
+    __shared__ __align__(16) uint16_t vt[DMA ? 8 : NP * kD * VROW];
 
     // XCD-aware order: consecutive tiles (same block and group, neighbouring queries, same keys)
     // on the same XCD so that its L2 serves their shared K/V.
@@ -122,16 +142,17 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     const int g = local % a.G;
     const int64_t t0 = (int64_t)(local / a.G) * kQTile;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lq = lane & 15, lg = lane >> 4;
-    const int h = g * GRP + wave;
+    const int h = g * GRP + wave % GRP;
+    const int64_t tw = t0 + (int64_t)(wave / GRP) * 16 * NQT;   // the wave's first query
 
     // Q^T fragments (bf16): query t0 + 16 qt + lq, dims 32 kc + 8 lg .. + 7; fp32 queries as NQP
     // pieces: hi = bf16(q), then bf16 of what is left (lo, or mid and lo).
     bf16x8_t qf[NQP][NQT][4];
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
-        const int64_t t = t0 + qt * 16 + lq;
+        const int64_t t = tw + qt * 16 + lq;
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
             const int d0 = kc * 32 + lg * 8;
@@ -193,7 +214,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     // Key tiles in order over the runs; the global loads of the next tile are issued before the
     // current tile is computed (register double buffer), then stored into LDS (K as is, V transposed).
     auto run_len = [&](int r) -> int64_t { return sel4(r, rlen[0], rlen[1], rlen[2], rlen[3]); };
-    constexpr int NT = 64 * GRP;
+    constexpr int NT = 64 * GRP * QW;
     constexpr int CPR = kD * ESZ / 16;             // 16-byte chunks per key row
     constexpr int KCH = KT * CPR;                  // K chunks per tile
     constexpr int VCH = KT / 2 * CPR;              // V chunks per tile, counted in row pairs
@@ -222,6 +243,22 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                 vreg[i][h2] = (c < VCH && row < lim) ? *reinterpret_cast<const uint4 *>(vb + row * rs + cc * 16)
                                                      : make_uint4(0, 0, 0, 0);
             }
+        }
+    };
+    auto issue = [&](int r, int64_t j0, int buf) {
+        const int64_t n = run_len(r);
+        const int rs = sel4(r, rrs[0], rrs[1], rrs[2], rrs[3]);
+        const char *kb = sel4(r, rkp[0], rkp[1], rkp[2], rkp[3]) + j0 * rs;
+        const char *vb = sel4(r, rvp[0], rvp[1], rvp[2], rvp[3]) + j0 * rs;
+        const int lim = (int)min<int64_t>(n - j0, KT);
+        const dma_rsrc_t krs = dma_rsrc(kb, (uint32_t)(lim * rs)), vrs = dma_rsrc(vb, (uint32_t)(lim * rs));
+        uint8_t *base = reinterpret_cast<uint8_t *>(ks) + buf * (2 * KT * kD * 2);
+        const int sub = lane >> 4, slot = lane & 15;
+        for (int i = wave; i < KT / 2; i += NT / 64) {     // KT / 4 loads of 4 rows for K, as many for V
+            const bool isv = i >= KT / 4;
+            const int rb = 4 * (isv ? i - KT / 4 : i), row = rb + sub;
+            dma16(isv ? vrs : krs, (uint32_t)(row * rs + ((slot ^ (row & 15)) << 4)),
+                  base + (isv ? KT * kD * 2 : 0) + rb * kD * 2);
         }
     };
     auto stage = [&]() {
@@ -282,7 +319,12 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     int r = 0;
     while (r < n_runs && run_len(r) <= 0) ++r;
     int64_t j0 = 0;
-    if (r < n_runs) fetch(r, j0);
+    int buf = 0;
+    if constexpr (DMA) {
+        if (r < n_runs) issue(r, j0, 0);
+    } else {
+        if (r < n_runs) fetch(r, j0);
+    }
     while (r < n_runs) {
         const int64_t n = run_len(r);
         const bool causal = (r == n_runs - 1) && cbase >= 0;
@@ -292,12 +334,20 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
             jn = 0;
             do { ++rn; } while (rn < n_runs && run_len(rn) <= 0);
         }
-        __syncthreads();
-        stage();
-        __syncthreads();
-        if (rn < n_runs) fetch(rn, jn);
-        for (int c = 0; c < KT && j0 + c < n; c += 32) {
-            f32x4_t sc[NQT][2];
+        if constexpr (DMA) {
+            // this tile's loads landed (each wave waits for its own, the barrier for every wave's), and
+            // every wave is done with the other stage: the next tile's loads go there
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (rn < n_runs) issue(rn, jn, buf ^ 1);
+        } else {
+            __syncthreads();
+            stage();
+            __syncthreads();
+            if (rn < n_runs) fetch(rn, jn);
+        }
+        const uint8_t *kst = reinterpret_cast<const uint8_t *>(ks) + buf * (2 * KT * kD * 2);
+        const uint8_t *vst = kst + KT * kD * 2;
+        auto scores = [&](int c, f32x4_t (&sc)[NQT][2]) {
 #pragma unroll
             for (int qt = 0; qt < NQT; ++qt) {
                 sc[qt][0] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -307,9 +357,17 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
             for (int kc = 0; kc < 4; ++kc) {
 #pragma unroll
                 for (int pk = 0; pk < NP; ++pk) {        // K plane: hi (then, fp32 K, mid and lo)
-                    const uint16_t *kp = ks + pk * KT * kKRow;
-                    const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t *>(kp + (c + lq) * kKRow + kc * 32 + lg * 8);
-                    const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t *>(kp + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
+                    bf16x8_t a0, a1;
+                    if constexpr (DMA) {
+                        // rows c + lq, c + 16 + lq: 16-byte piece kc * 4 + lg stored at slot piece ^ (row & 15)
+                        const int so = ((kc * 4 + lg) ^ lq) << 4;
+                        a0 = *reinterpret_cast<const bf16x8_t *>(kst + (c + lq) * (kD * 2) + so);
+                        a1 = *reinterpret_cast<const bf16x8_t *>(kst + (c + 16 + lq) * (kD * 2) + so);
+                    } else {
+                        const uint16_t *kp = ks + pk * KT * kKRow;
+                        a0 = *reinterpret_cast<const bf16x8_t *>(kp + (c + lq) * kKRow + kc * 32 + lg * 8);
+                        a1 = *reinterpret_cast<const bf16x8_t *>(kp + (c + 16 + lq) * kKRow + kc * 32 + lg * 8);
+                    }
 #pragma unroll
                     for (int qp = 0; qp < NQP; ++qp) {
                         if (pk + qp > ORD) continue;      // below 2^-(8 (ORD + 1)) of the product
@@ -321,13 +379,15 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                     }
                 }
             }
+        };
+        auto finish = [&](int c, f32x4_t (&sc)[NQT][2]) {
             bf16x8_t pf[NPP][NQT];
             // 32-key chunk fully visible to all 32 queries: no per-score mask
-            const bool full = j0 + c + 32 <= n && (!causal || j0 + c + 31 <= cbase + t0);
+            const bool full = j0 + c + 32 <= n && (!causal || j0 + c + 31 <= cbase + tw);
             // the biased run of a biased head: its bias (log2 units) is added to the chunk's scores
             const bool biased = brow != nullptr && r == B.bias_run;   // wave-uniform
             // key index relative to the causal limit of query t0 (fits in 32 bits)
-            const int kbase = (int)(j0 + c - (causal ? cbase + t0 : 0));
+            const int kbase = (int)(j0 + c - (causal ? cbase + tw : 0));
             const int klim = (int)(n - (j0 + c));
 #pragma unroll
             for (int qt = 0; qt < NQT; ++qt) {
@@ -348,7 +408,7 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                         }
                 }
                 if (biased) {
-                    const float *bq = brow + min(t0 + qt * 16 + lq, B.n_q - 1) * B.bias_ldq;
+                    const float *bq = brow + min(tw + qt * 16 + lq, B.n_q - 1) * B.bias_ldq;
 #pragma unroll
                     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -394,10 +454,23 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
             for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
                 for (int pv_ = 0; pv_ < NP; ++pv_) {     // V plane: hi (then, fp32 V, mid and lo)
-                    const uint16_t *vr = vt + pv_ * kD * VROW + (dt * 16 + lq) * VROW + c + lg * 4;
-                    const uint2 lo = *reinterpret_cast<const uint2 *>(vr);
-                    const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16);
-                    const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    bf16x8_t va;
+                    if constexpr (DMA) {
+                        // transposed reads of the row-major tile: lane lq of group lg addresses key
+                        // c + 4 lg + lq / 4, dims 16 dt + 4 (lq % 4) .. + 3, and receives dim 16 dt + lq of
+                        // keys c + 4 lg .. + 3 (then of the same keys + 16)
+                        const int row = c + lg * 4 + (lq >> 2);
+                        const int off = row * (kD * 2) + (((dt * 2 + ((lq & 3) >> 1)) ^ (row & 15)) << 4) + ((lq & 1) << 3);
+                        const v4i16_t lo = lds_read_tr16(vst + off), hi = lds_read_tr16(vst + off + 16 * (kD * 2));
+                        typedef short v8i16_t __attribute__((ext_vector_type(8)));
+                        const v8i16_t w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                        va = __builtin_bit_cast(bf16x8_t, w);
+                    } else {
+                        const uint16_t *vr = vt + pv_ * kD * VROW + (dt * 16 + lq) * VROW + c + lg * 4;
+                        const uint2 lo = *reinterpret_cast<const uint2 *>(vr);
+                        const uint2 hi = *reinterpret_cast<const uint2 *>(vr + 16);
+                        va = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                    }
 #pragma unroll
                     for (int pp = 0; pp < NPP; ++pp) {
                         if (pv_ + pp > ORD) continue;     // as for the scores
@@ -407,16 +480,23 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
                     }
                 }
             }
+        };
+        for (int c = 0; c < KT && j0 + c < n; c += 32) {
+            if (causal && j0 + c > cbase + tw + 16 * NQT - 1) break;   // wave-uniform: the wave's future
+            f32x4_t sc[NQT][2];
+            scores(c, sc);
+            finish(c, sc);
         }
         r = rn;
         j0 = jn;
+        buf ^= 1;
     }
 
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
         const float L = xor32_sum(xor16_sum(lsum[qt]));
         const float inv = 1.0f / L;
-        const int64_t t = t0 + qt * 16 + lq;
+        const int64_t t = tw + qt * 16 + lq;
         if (t >= B.n_q) continue;
         const int64_t oo = t * B.ldo + (int64_t)h * B.o_hstride;
         if (a.o_bf16) {
@@ -438,10 +518,18 @@ __global__ __launch_bounds__(64 * GRP) void attn_prefill_kernel(PrefillArgs a) {
     }
 }
 
-// 32 queries per wave: 16-query waves (154 instead of 226 VGPRs at 6 heads per group, two workgroups
-// per CU) measured slower, 365 vs 296 us at L = 8192 (twice the K/V staging and K fragment reads per
-// query).
-constexpr int kNqt = 2;
+// Launch shape per K / V dtype and heads per group: NQT 16-query tiles per wave, QW waves per head, LDS
+// DMA staging.  At 4 and 6 heads per group a workgroup of 2 GRP waves of 16 queries (at most 168
+// registers, three waves per SIMD: one workgroup of 12 waves per CU at 6 heads) keeps more waves in
+// flight than GRP waves of 32 queries (226-256 registers, two per SIMD, 6 waves per CU), for the same
+// K / V tile per 32 queries.  Measured at L = 8192 (12 query / 2 KV heads, drop-in call): bf16 K / V
+// 333 -> 295 us with 2 x 6 waves of 16 queries, -> 264 us with the tiles staged by LDS DMA (64 keys),
+// -> 247 us with 128-key tiles; fp32 K / V 1082 -> 749 us with 2 x 6 waves.  Eight heads per group
+// keep 8 waves of 32 queries (16 waves would need <= 128 registers and spill), one and two the
+// register-staged 32-query waves.
+constexpr int prefill_nqt(int grp, bool kf) { return kf || grp == 4 || grp == 6 ? 1 : 2; }
+constexpr int prefill_qw(int grp, bool kf) { return (grp == 4 || grp == 6 || (kf && grp == 2)) ? 2 : 1; }
+constexpr bool prefill_dma(int grp, bool kf) { return !kf && grp >= 4; }
 
 }  // namespace
 
@@ -460,7 +548,8 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_bl
     if (D != kD) return VGX_E_LIMIT;
     const int grp = (int)(H / G);
     if (grp != 1 && grp != 2 && grp != 4 && grp != 6 && grp != 8) return VGX_E_LIMIT;
-    const int qtile = 16 * (kv_dtype == VGX_F32 ? 1 : kNqt);   // fp32 K / V: 16 queries per wave
+    const bool kf = kv_dtype == VGX_F32;
+    const int qtile = 16 * prefill_nqt(grp, kf) * prefill_qw(grp, kf);   // queries per workgroup
     PrefillArgs a{};
     a.H = (int)H;
     a.G = (int)G;
@@ -528,8 +617,13 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_bl
     const dim3 grid((unsigned)tiles);
 #define VGX_PREFILL_GO(G_, S_)                                                                               \
     do {                                                                                                     \
-        if (kv_dtype == VGX_F32) hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, 1, true>), grid, dim3(64 * G_), 0, st, a); \
-        else hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, kNqt, false>), grid, dim3(64 * G_), 0, st, a);   \
+        if (kf)                                                                                              \
+            hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, prefill_nqt(G_, true), true, prefill_qw(G_, true), false>), \
+                               grid, dim3(64 * G_ * prefill_qw(G_, true)), 0, st, a);                        \
+        else                                                                                                 \
+            hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, prefill_nqt(G_, false), false, prefill_qw(G_, false), \
+                                                    prefill_dma(G_, false)>),                                \
+                               grid, dim3(64 * G_ * prefill_qw(G_, false)), 0, st, a);                       \
     } while (0)
 #define VGX_PREFILL_GRP(S_)                      \
     switch (grp) {                               \

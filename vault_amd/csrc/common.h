@@ -190,6 +190,40 @@ VGX_DEV float4 ld_stream(const float4 *p) {
     return make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// LDS DMA: buffer loads that write LDS directly (buffer_load ... lds), issued from inline assembly so that
+// the compiler does not make every later LDS read wait for them (it treats any LDS read after a DMA it
+// knows of as dependent on it); the kernel waits for them itself (s_waitcnt vmcnt, then a barrier).
+// Extra outstanding loads only make the compiler's own vmcnt waits wait longer (loads return in order),
+// never shorter.  M0 (the LDS base) is written here and cannot be declared clobbered (a reserved
+// register): a kernel that uses these makes no other use of M0 (gfx950 LDS instructions do not read
+// it), which its compiled code has to be checked for.
+typedef int dma_rsrc_t __attribute__((ext_vector_type(4)));
+constexpr uint32_t kDmaPast = 0x80000000u;      // a buffer offset past every operand: reads zero
+
+// Buffer resource over `bytes` bytes at p (wave-uniform): offsets at or past the end read zeros.
+VGX_DEV dma_rsrc_t dma_rsrc(const void *p, uint32_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    dma_rsrc_t r;
+    r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu));
+    r.z = __builtin_amdgcn_readfirstlane((int)bytes);
+    r.w = 0x00020000;
+    return r;
+}
+
+// Lane l's 16 (4) bytes at byte offset voff of the buffer into LDS at lds + 16 l (4 l); lds is
+// wave-uniform.
+VGX_DEV void dma16(dma_rsrc_t rs, uint32_t voff, const void *lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs)
+                 : "memory");
+}
+VGX_DEV void dma4(dma_rsrc_t rs, uint32_t voff, const void *lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs)
+                 : "memory");
+}
+
 // One element of a KV-state tensor of dtype KV (VGX_F32, or VGX_BF16 rounded to nearest even).
 template <int KV>
 VGX_DEV void store_kv(void *base, int64_t idx, float v) {

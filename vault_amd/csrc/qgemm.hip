@@ -396,9 +396,8 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
     }
 }
 
-// The tiled kernel with its stages filled by LDS DMA: buffer loads that write LDS directly, issued from
-// inline assembly so that the compiler does not make the LDS reads of block k wait for them (it treats
-// every LDS read after a DMA it knows of as dependent on it).  Two stages: the loads of block k + 1
+// The tiled kernel with its stages filled by LDS DMA (dma16 / dma4: buffer loads that write LDS directly;
+// the kernel makes no other use of M0, which its compiled code was checked for).  Two stages: the loads of block k + 1
 // leave right after the barrier of block k and land in the other stage while block k is multiplied, and
 // they need no staging registers, which leaves room for three workgroups per CU (163 VGPRs, 38 KB of
 // LDS) instead of two (256 VGPRs with the register double buffer of qgemm_tile_kernel).  Same
@@ -407,34 +406,6 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
 // conflicts.  Measured on a 1024-token chunk (Q4_0 / Q8_0): gate/up 228.9 -> 193.5 / 251.4 -> 222.5 us,
 // down 143.0 -> 137.2 / 156.1 -> 144.1, q|k|v 49.2 -> 48.3 / 50.8 -> 49.5, o 43.6 -> 45.8 / 46.6 -> 44.9;
 // with three stages at two workgroups per CU 209.7 us for the Q4_0 gate/up, with four 221.1.
-typedef int dma_rsrc_t __attribute__((ext_vector_type(4)));
-constexpr uint32_t kDmaPast = 0x80000000u;      // a buffer offset past every operand: reads zero
-
-__device__ __forceinline__ dma_rsrc_t dma_rsrc(const void *p, uint32_t bytes) {
-    const uint64_t a = (uint64_t)(uintptr_t)p;
-    dma_rsrc_t r;
-    r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-    r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu));
-    r.z = __builtin_amdgcn_readfirstlane((int)bytes);
-    r.w = 0x00020000;
-    return r;
-}
-
-// Lane l's 16 (4) bytes at byte offset voff of the buffer into LDS at lds + 16 l (4 l); lds is
-// wave-uniform.  Offsets past the buffer read zeros.  M0 (the LDS base) is written here and cannot be
-// declared clobbered (a reserved register); the kernel below makes no other use of M0 (gfx950 LDS
-// instructions do not read it), which its compiled code was checked for.
-__device__ __forceinline__ void dma16(dma_rsrc_t rs, uint32_t voff, const void *lds) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs)
-                 : "memory");
-}
-__device__ __forceinline__ void dma4(dma_rsrc_t rs, uint32_t voff, const void *lds) {
-    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m), "v"(voff), "s"(rs)
-                 : "memory");
-}
-
 template <int DT, int EPI, bool SPLIT>
 __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
                                                               int nblk, int64_t rows_out,
