@@ -221,3 +221,50 @@ def test_prefill_per_row_bias_on_segment_run(dev, kvdt, T, lens):
     # the same bias on the wrong run is far outside the bar
     wrong = oatt.chunk(_f64(q), [(_f64(k), _f64(v)) for k, v in runs], _f64(kc), _f64(vc))
     assert np.abs(wrong - ref).max() > 100 * TOL
+
+
+@pytest.mark.parametrize("kvdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("qdt", [torch.float32, torch.bfloat16])
+def test_prefill_launch_shapes_agree(dev, kvdt, qdt):
+    """A launch of many query tiles runs two waves of 16 queries per head and workgroup, a launch of
+    few tiles one (the narrow shape, twice the workgroups); every query's arithmetic is the same in
+    both.  Eight blocks in one launch (262 32-query tiles: the two-wave shape) against the same blocks
+    launched one by one (narrow): equal bit for bit, biased blocks included, and two of the blocks
+    against the float64 oracle."""
+    rng = np.random.default_rng(31 if kvdt == torch.bfloat16 else 32)
+    H, G, D = 12, 2, 128
+    cast = (lambda a: _bf(a)) if kvdt == torch.bfloat16 else (lambda a: torch.as_tensor(a, dtype=torch.float32))
+    sizes = [520, 611, 333, 700, 47, 600, 590, 655]
+    blocks, refs = [], []
+    for i, T in enumerate(sizes):
+        lens = [int(rng.integers(1, 300)), int(rng.integers(1, 400))]
+        runs = [(cast(rng.standard_normal((G, n, D))).to(dev), cast(rng.standard_normal((G, n, D))).to(dev))
+                for n in lens]
+        kc = cast(rng.standard_normal((G, T, D))).to(dev)
+        vc = cast(rng.standard_normal((G, T, D))).to(dev)
+        q = torch.from_numpy(rng.standard_normal((T, H, D)).astype(np.float32)).to(dev).to(qdt)
+        blk = {"q": q, "runs": runs + [(kc, vc)], "causal_base": 0}
+        dense = None
+        if i % 3 == 1:                                  # a resonance bias on the second run
+            rows = [-1, 0, 1, 0, 1, -1] * 2
+            bias = (rng.standard_normal((T, 2, lens[1])) * 3).astype(np.float32)
+            blk.update(bias=torch.from_numpy(bias).to(dev), bias_head_row=rows, bias_run=1)
+            dense = np.zeros((T, H, lens[1]))
+            for h, r in enumerate(rows):
+                if r >= 0:
+                    dense[:, h] = bias[:, r]
+        blocks.append(blk)
+        refs.append(dense)
+    wide = [dict(b, out=torch.empty(b["q"].shape[0], H, D, device=dev)) for b in blocks]
+    ops.attn_prefill(wide, H, G)
+    for b, w in zip(blocks, wide):
+        narrow = dict(b, out=torch.empty_like(w["out"]))
+        ops.attn_prefill([narrow], H, G)
+        assert torch.equal(narrow["out"], w["out"])
+    bar = TOL if kvdt == torch.bfloat16 else TOL32
+    for i in (1, 4):
+        b = blocks[i]
+        (pk, pv), (sk, sv), (kc, vc) = b["runs"]
+        ref = oatt.chunk(_f64(b["q"]), [(_f64(pk), _f64(pv)), (_f64(sk), _f64(sv))], _f64(kc), _f64(vc),
+                         bias=refs[i], bias_span=1 if refs[i] is not None else -1)
+        assert np.abs(wide[i]["out"].double().cpu().numpy() - ref).max() <= bar

@@ -526,9 +526,14 @@ __global__ __launch_bounds__(64 * GRP * QW) void attn_prefill_kernel(PrefillArgs
 // 333 -> 295 us with 2 x 6 waves of 16 queries, -> 264 us with the tiles staged by LDS DMA (64 keys),
 // -> 247 us with 128-key tiles; fp32 K / V 1082 -> 749 us with 2 x 6 waves.  Eight heads per group
 // keep 8 waves of 32 queries (16 waves would need <= 128 registers and spill), one and two the
-// register-staged 32-query waves.
+// register-staged 32-query waves.  A launch of fewer 2-wave-per-head workgroups than CUs (a 2048-query
+// chunk of the chunk-recurrent prefill at 2 KV heads: 128) runs one wave per head instead (narrow):
+// twice the workgroups over the CUs.
+constexpr int kPrefillNarrowBelow = 256;
 constexpr int prefill_nqt(int grp, bool kf) { return kf || grp == 4 || grp == 6 ? 1 : 2; }
-constexpr int prefill_qw(int grp, bool kf) { return (grp == 4 || grp == 6 || (kf && grp == 2)) ? 2 : 1; }
+constexpr int prefill_qw(int grp, bool kf, bool narrow) {
+    return !narrow && (grp == 4 || grp == 6 || (kf && grp == 2)) ? 2 : 1;
+}
 constexpr bool prefill_dma(int grp, bool kf) { return !kf && grp >= 4; }
 
 }  // namespace
@@ -549,7 +554,11 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_bl
     const int grp = (int)(H / G);
     if (grp != 1 && grp != 2 && grp != 4 && grp != 6 && grp != 8) return VGX_E_LIMIT;
     const bool kf = kv_dtype == VGX_F32;
-    const int qtile = 16 * prefill_nqt(grp, kf) * prefill_qw(grp, kf);   // queries per workgroup
+    int64_t wide_tiles = 0;
+    for (int i = 0; i < n_blocks; ++i)
+        if (blocks[i].n_q > 0) wide_tiles += (blocks[i].n_q + 31) / 32 * G;
+    const bool narrow = prefill_qw(grp, kf, false) > 1 && wide_tiles < kPrefillNarrowBelow;
+    const int qtile = 16 * prefill_nqt(grp, kf) * prefill_qw(grp, kf, narrow);   // queries per workgroup
     PrefillArgs a{};
     a.H = (int)H;
     a.G = (int)G;
@@ -615,15 +624,17 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_bl
     a.n_tiles = (int)tiles;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)tiles);
+#define VGX_PREFILL_SHAPE(G_, S_, KF_, N_)                                                                   \
+    hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, prefill_nqt(G_, KF_), KF_, prefill_qw(G_, KF_, N_),        \
+                                            prefill_dma(G_, KF_)>),                                            \
+                       grid, dim3(64 * G_ * prefill_qw(G_, KF_, N_)), 0, st, a)
 #define VGX_PREFILL_GO(G_, S_)                                                                               \
     do {                                                                                                     \
-        if (kf)                                                                                              \
-            hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, prefill_nqt(G_, true), true, prefill_qw(G_, true), false>), \
-                               grid, dim3(64 * G_ * prefill_qw(G_, true)), 0, st, a);                        \
-        else                                                                                                 \
-            hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, prefill_nqt(G_, false), false, prefill_qw(G_, false), \
-                                                    prefill_dma(G_, false)>),                                \
-                               grid, dim3(64 * G_ * prefill_qw(G_, false)), 0, st, a);                       \
+        if (kf) {                                                                                            \
+            if (narrow) VGX_PREFILL_SHAPE(G_, S_, true, true); else VGX_PREFILL_SHAPE(G_, S_, true, false);  \
+        } else {                                                                                             \
+            if (narrow) VGX_PREFILL_SHAPE(G_, S_, false, true); else VGX_PREFILL_SHAPE(G_, S_, false, false);\
+        }                                                                                                    \
     } while (0)
 #define VGX_PREFILL_GRP(S_)                      \
     switch (grp) {                               \
@@ -640,6 +651,7 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_bl
     }
 #undef VGX_PREFILL_GRP
 #undef VGX_PREFILL_GO
+#undef VGX_PREFILL_SHAPE
     VGX_CHECK_LAUNCH();
     return VGX_OK;
 }
