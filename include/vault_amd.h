@@ -483,6 +483,17 @@ int vgx_layernorm(const float *x, int64_t ldx, const float *w, const float *b, f
 int vgx_seg_score_tail(const float *h, int64_t ldh, const float *w2, const float *b2, int64_t hidden, int64_t T,
                        int first, float *out, const int32_t *out_index, void *stream);
 
+/* The scorer of one decode token in two launches: the fc1 GEMV (w1: packed F32 [hidden, fd], bias b1)
+ * on LayerNorm(feat) and LayerNorm(feat - 0.65 e) (ln_w, ln_b, eps; e = ema, or feat when first != 0),
+ * both rows built inside the GEMV's workgroups, into h [2, hidden]; then out[0] (shifted by *out_index
+ * when out_index is not NULL) as vgx_seg_score_tail at T = 1, and the EMA state updated as
+ * vgx_ema_habituate at T = 1.  The same results as vgx_ema_habituate + vgx_layernorm + the fc1
+ * vgx_qlinear + vgx_seg_score_tail, bit for bit.  fd <= 5120 (VGX_E_LIMIT beyond).
+ * Replaces the step's scorer, src/vault_v3_model.py:2294-2305 (runtime/vault3.c:2201-2216). */
+int vgx_seg_score_step(const float *feat, int64_t fd, float *ema, int first, const void *w1, int64_t hidden,
+                       const float *b1, const float *ln_w, const float *ln_b, float eps, const float *w2,
+                       const float *b2, float *h, float *out, const int32_t *out_index, void *stream);
+
 /* ---------------------------------------------------------------- top candidates of a row ------ */
 
 /* The T (<= 256) largest logits of each row, sorted by value descending, ties by index ascending

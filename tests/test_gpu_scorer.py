@@ -74,3 +74,41 @@ def test_score_tail_gelu_is_the_runtimes(dev):
     nz = want != 0
     assert np.array_equal(got[nz].view(np.uint32), want[nz].view(np.uint32))
     assert np.all(got[~nz] == 0)
+
+
+@pytest.mark.parametrize("fd", [4608, 2688, 96])
+@pytest.mark.parametrize("first", [True, False])
+def test_score_step_equals_separate_launches(dev, fd, first):
+    """vgx_seg_score_step (the decode token's scorer: the fc1 GEMV building both LayerNormed rows
+    itself, then the tail with the EMA update) against the separate launches it replaces
+    (vgx_ema_habituate, vgx_layernorm, the fc1 vgx_qlinear, vgx_seg_score_tail at T = 1): the score,
+    the fc1 outputs and the EMA state equal bit for bit; the score lands at the slot a device index
+    names; feature widths of the 1.5B model (3 x 1536), the 0.5B one (3 x 896) and a tiny one."""
+    rng = np.random.default_rng(fd + first)
+    hidden = 256
+    f = torch.from_numpy((rng.standard_normal(fd) * 2.0).astype(np.float32)).to(dev)
+    ema0 = torch.from_numpy(rng.standard_normal(fd).astype(np.float32)).to(dev)
+    ln_w = torch.from_numpy(rng.uniform(0.8, 1.2, fd).astype(np.float32)).to(dev)
+    ln_b = torch.from_numpy((rng.standard_normal(fd) * 0.05).astype(np.float32)).to(dev)
+    w1m = (rng.standard_normal((hidden, fd)) * 0.02).astype(np.float32)
+    w1 = ops.QWeight.from_blocks(ops.L.F32, hidden, fd, w1m.tobytes(), dev)
+    b1 = torch.from_numpy((rng.standard_normal(hidden) * 0.02).astype(np.float32)).to(dev)
+    w2 = torch.from_numpy((rng.standard_normal(hidden) * 0.02).astype(np.float32)).to(dev)
+    b2 = torch.from_numpy((rng.standard_normal(1) * 0.02).astype(np.float32)).to(dev)
+    # separate launches
+    rows = torch.empty(2, fd, device=dev)
+    rows[0] = f
+    ema_a = ema0.clone()
+    ops.ema_habituate(rows[:1], rows[1:2], ema_a, first)
+    ops.layernorm(rows, ln_w, ln_b, 1e-5, rows)
+    h_a = ops.qlinear(w1, rows, bias=b1)
+    out_a = torch.full((8,), -7.0, device=dev)
+    idx = torch.tensor([5], dtype=torch.int32, device=dev)
+    ops.seg_score_tail(h_a, w2, b2, 1, first, out_a[0:1], out_index=idx)
+    # one step
+    ema_b = ema0.clone()
+    out_b = torch.full((8,), -7.0, device=dev)
+    ops.seg_score_step(f, ema_b, first, w1, b1, ln_w, ln_b, 1e-5, w2, b2, out_b[0:1], out_index=idx)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b) and out_b[5].item() != -7.0
+    assert torch.equal(ema_a, ema_b)

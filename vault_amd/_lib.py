@@ -92,6 +92,7 @@ _SIGS = {
     "vgx_ema_habituate": (I32, [P, I64, P, I64, P, I64, I64, I32, P]),
     "vgx_layernorm": (I32, [P, I64, P, P, P, I64, I64, I64, F, P]),
     "vgx_seg_score_tail": (I32, [P, I64, P, P, I64, I64, I32, P, P, P]),
+    "vgx_seg_score_step": (I32, [P, I64, P, I32, P, I64, P, P, P, F, P, P, P, P, P, P]),
     "vgx_rope_qkv_write_step": (I32, [I32, P, I64, P, I64, P, I64, I64, I64, I64, I64, P, I64, P, P, P, P, I64, I64,
                                       I64, P, P, I64, I64, I64, P]),
     "vgx_qkv_rope_step": (I32, [I32, P, P, I32, P, P, I64, I64, I64, I64, P, P, F, P, P, I64, P, P, I32, P, P, P, I64,

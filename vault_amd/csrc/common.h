@@ -190,6 +190,19 @@ VGX_DEV float4 ld_stream(const float4 *p) {
     return make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// The scorer's EMA habituation of one feature (src/vault_v3_model.py:2299-2304): the habituated input
+// f - 0.65 e and the state update 0.985 e + 0.015 f, each product rounded before the sum (no
+// contraction, as the reference's float32 arithmetic), so every kernel that applies them agrees bit
+// for bit.
+VGX_DEV float hab_of(float f, float e) {
+#pragma clang fp contract(off)
+    return f - 0.65f * e;
+}
+VGX_DEV float ema_step(float e, float f) {
+#pragma clang fp contract(off)
+    return 0.985f * e + 0.015f * f;
+}
+
 // LDS DMA: buffer loads that write LDS directly (buffer_load ... lds), issued from inline assembly so that
 // the compiler does not make every later LDS read wait for them (it treats any LDS read after a DMA it
 // knows of as dependent on it); the kernel waits for them itself (s_waitcnt vmcnt, then a barrier).

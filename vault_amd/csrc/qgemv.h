@@ -64,6 +64,12 @@ struct GemvArgs {
     int epi;
     const int64_t *y_ref;   // non-null: y is the address stored in this device word when the launch runs,
     int64_t y_off;          // plus this many floats
+    // Segment-scorer prologue (F32 weights, two output rows): with sc_ema set, the activation rows are
+    // LayerNorm(f) and LayerNorm(f - 0.65 e) of the token's features f = x (e = sc_ema, or f itself
+    // when sc_first), LayerNorm weight lnw, bias sc_lnb, eps.
+    const float *sc_ema;
+    const float *sc_lnb;
+    int sc_first;
 };
 
 // The output address of a launch whose GemvArgs name it indirectly (a captured graph whose output
@@ -967,9 +973,90 @@ __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
 // buffer load per lane and piece, all requested before the activations (staged once in LDS) are read.
 constexpr int kF32PiecesMaxBlocks = 160;
 constexpr int kF32PiecesWaves = 16;
+constexpr int kScLnF4 = 5;                    // float4 per thread of a scorer row (rows up to 5120 floats)
 
-template <int NB, int EPI>
+// The scorer prologue's two rows into LDS (xs4[n * n4 + c]): waves 0-3 build row 0 = LayerNorm(f),
+// waves 4-7 row 1 = LayerNorm(f - 0.65 e), each with the arithmetic of layernorm_reg_kernel (256
+// threads per row, float4 t + 256 u, wave sums added in wave order) and of ema_habituate_kernel at
+// T = 1, so the rows are those of the separate launches bit for bit.  scorer_load requests the
+// thread's features, EMA state and LayerNorm weight and bias (before the weights, so that the rows
+// do not wait for them); scorer_rows builds the rows.
+__device__ __forceinline__ void scorer_load(const GemvArgs &a, float4 (&f)[kScLnF4], float4 (&e)[kScLnF4],
+                                            float4 (&g)[kScLnF4], float4 (&b)[kScLnF4]) {
+    const int tid = threadIdx.x, n = tid >> 8, t = tid & 255;
+    const int n4 = a.nblk * QK / 4;
+    // unconditional buffer loads (offsets past the end read zeros): all of them in flight at once
+    auto rs = [&](const float *p) { return __builtin_amdgcn_make_buffer_rsrc((void *)p, 0, n4 * 16, 0x00020000); };
+    const __amdgpu_buffer_rsrc_t frs = rs(a.x), ers = rs(a.sc_ema), grs = rs(a.lnw), brs = rs(a.sc_lnb);
+    auto ld = [&](__amdgpu_buffer_rsrc_t r, uint32_t o) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0);
+        return make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+    };
+    const bool own_e = n == 1 && !a.sc_first;
+#pragma unroll
+    for (int u = 0; u < kScLnF4; ++u) {
+        const int i = t + u * 256;
+        const uint32_t o = n < 2 && i < n4 ? (uint32_t)i * 16 : kStreamPastEnd;
+        f[u] = ld(frs, o);
+        e[u] = ld(ers, own_e ? o : kStreamPastEnd);
+        g[u] = ld(grs, o);
+        b[u] = ld(brs, o);
+    }
+}
+
+__device__ __forceinline__ void scorer_rows(const GemvArgs &a, const float4 (&f)[kScLnF4], const float4 (&e)[kScLnF4],
+                                            const float4 (&g)[kScLnF4], const float4 (&b)[kScLnF4], float4 *xs4,
+                                            float (*red)[2][4]) {
+    const int tid = threadIdx.x, n = tid >> 8, t = tid & 255, w = t >> 6;
+    const int dim = a.nblk * QK, n4 = dim / 4;
+    const bool own_e = !a.sc_first;
+    float4 v[kScLnF4];
+#pragma unroll
+    for (int u = 0; u < kScLnF4; ++u) {
+        v[u] = f[u];
+        if (n == 1 && t + u * 256 < n4) {
+            const float4 ev = own_e ? e[u] : f[u];
+            v[u] = make_float4(hab_of(f[u].x, ev.x), hab_of(f[u].y, ev.y), hab_of(f[u].z, ev.z), hab_of(f[u].w, ev.w));
+        }
+    }
+    if (n < 2) {
+        float s = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kScLnF4; ++u) s += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+        s = wave_sum(s);
+        if ((tid & 63) == 0) red[n][0][w] = s;
+    }
+    __syncthreads();
+    if (n < 2) {
+        const float mean = (red[n][0][0] + red[n][0][1] + red[n][0][2] + red[n][0][3]) / (float)dim;
+        float q = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kScLnF4; ++u) {
+            if (t + u * 256 < n4) {
+                const float p = v[u].x - mean, c = v[u].y - mean, d = v[u].z - mean, r = v[u].w - mean;
+                q = fmaf(p, p, fmaf(c, c, fmaf(d, d, fmaf(r, r, q))));
+            }
+        }
+        q = wave_sum(q);
+        if ((tid & 63) == 0) red[n][1][w] = q;
+    }
+    __syncthreads();
+    if (n < 2) {
+        const float mean = (red[n][0][0] + red[n][0][1] + red[n][0][2] + red[n][0][3]) / (float)dim;
+        const float inv = 1.0f / sqrtf((red[n][1][0] + red[n][1][1] + red[n][1][2] + red[n][1][3]) / (float)dim + a.eps);
+#pragma unroll
+        for (int u = 0; u < kScLnF4; ++u) {
+            const int i = t + u * 256;
+            if (i < n4)
+                xs4[n * n4 + i] = make_float4((v[u].x - mean) * inv * g[u].x + b[u].x, (v[u].y - mean) * inv * g[u].y + b[u].y,
+                                              (v[u].z - mean) * inv * g[u].z + b[u].z, (v[u].w - mean) * inv * g[u].w + b[u].w);
+        }
+    }
+}
+
+template <int NB, int EPI, bool SCORER = false>
 __global__ __launch_bounds__(64 * kF32PiecesWaves) void gemv_f32_pieces_kernel(GemvArgs a) {
+    static_assert(!SCORER || (NB == 2 && EPI == EPI_STORE), "the scorer prologue builds two rows");
     gemv_resolve_y(a);
     constexpr int NW = kF32PiecesWaves;
     constexpr int MAXI = (kF32PiecesMaxBlocks / 2 + NW - 1) / NW;   // pieces per wave
@@ -981,13 +1068,19 @@ __global__ __launch_bounds__(64 * kF32PiecesWaves) void gemv_f32_pieces_kernel(G
     const int npc = (nblk + 1) / 2;                   // pieces per row-quad
     const int64_t rq = blockIdx.x;
     const int row = (lane >> 3) & 3;
-    // activations (both rows), then the weights
-    constexpr int XR = (NB * kF32PiecesMaxBlocks * 8 + 64 * NW - 1) / (64 * NW);
+    // activations (both rows, or the scorer prologue's inputs), then the weights
+    constexpr int XR = SCORER ? 1 : (NB * kF32PiecesMaxBlocks * 8 + 64 * NW - 1) / (64 * NW);
     float4 xv[XR];
+    constexpr int SF = SCORER ? kScLnF4 : 1;
+    float4 sf[SF], se[SF], sg[SF], sb[SF];
+    if constexpr (SCORER) {
+        scorer_load(a, sf, se, sg, sb);
+    } else {
 #pragma unroll
-    for (int u = 0; u < XR; ++u) {
-        const int i = tid + 64 * NW * u, n = i / n4, c = i - n * n4;
-        xv[u] = n < NB ? reinterpret_cast<const float4 *>(a.x + n * a.ldx)[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int u = 0; u < XR; ++u) {
+            const int i = tid + 64 * NW * u, n = i / n4, c = i - n * n4;
+            xv[u] = n < NB ? reinterpret_cast<const float4 *>(a.x + n * a.ldx)[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
     }
     const __amdgpu_buffer_rsrc_t wrs =
         __builtin_amdgcn_make_buffer_rsrc((void *)a.w, 0, (int)(a.n_rq * nblk * 512), 0x00020000);
@@ -1003,10 +1096,15 @@ __global__ __launch_bounds__(64 * kF32PiecesWaves) void gemv_f32_pieces_kernel(G
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, o, 0, kStreamAux);
         wv[k] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
     }
+    if constexpr (SCORER) {
+        __shared__ float sred[2][2][4];
+        scorer_rows(a, sf, se, sg, sb, xs4, sred);
+    } else {
 #pragma unroll
-    for (int u = 0; u < XR; ++u) {
-        const int i = tid + 64 * NW * u;
-        if (i < NB * n4) xs4[i] = xv[u];
+        for (int u = 0; u < XR; ++u) {
+            const int i = tid + 64 * NW * u;
+            if (i < NB * n4) xs4[i] = xv[u];
+        }
     }
     __syncthreads();
     float acc[NB];
@@ -1108,6 +1206,17 @@ int qgemv_launch(GemvArgs a, hipStream_t st) {
     const bool rows_mode = a.n_rq >= 2048;
     const bool norm = a.lnw != nullptr;
     if constexpr (DT == VGX_F32) {
+        if (a.sc_ema != nullptr) {
+            // the segment scorer's fc1 with its prologue (two rows, F32 weights)
+            if (a.batch != 2 || a.epi != EPI_STORE || a.nblk > kF32PiecesMaxBlocks || a.nblk * QK > 256 * 4 * kScLnF4 ||
+                a.n_rq * a.nblk * 512 >= ((int64_t)1 << 31))
+                return VGX_E_LIMIT;
+            if ((((uintptr_t)a.x | (uintptr_t)a.sc_ema | (uintptr_t)a.lnw | (uintptr_t)a.sc_lnb) & 15) != 0)
+                return VGX_E_ALIGN;
+            hipLaunchKernelGGL((gemv_f32_pieces_kernel<2, EPI_STORE, true>), dim3((unsigned)a.n_rq),
+                               dim3(64 * kF32PiecesWaves), 0, st, a);
+            return hipGetLastError() == hipSuccess ? VGX_OK : VGX_E_HIP;
+        }
         if (a.batch <= 2 && !norm && a.epi != EPI_SWIGLU && a.nblk <= kF32PiecesMaxBlocks &&
             a.n_rq * a.nblk * 512 < ((int64_t)1 << 31) && ((uintptr_t)a.x & 15) == 0 && a.ldx % 4 == 0) {
 #define VGX_F32P(NB, EPIV) hipLaunchKernelGGL((gemv_f32_pieces_kernel<NB, EPIV>), dim3((unsigned)a.n_rq), dim3(64 * kF32PiecesWaves), 0, st, a)

@@ -9,7 +9,7 @@
 //   hab_in_t = f_t - 0.65 e_{t-1};  e_t = 0.985 e_{t-1} + 0.015 f_t   (e_0 = f_0 on the first token)
 //   score_t  = raw_t + 0.35 max(0, hab_t - raw_t)                     (score_0 = raw_0 on the first)
 // The fc1 GEMV between LayerNorm and the tail runs through vgx_qlinear (F32 weights).
-#include "common.h"
+#include "qgemv.h"
 
 using namespace vgx;
 
@@ -32,14 +32,14 @@ __global__ void ema_habituate_kernel(const float *__restrict__ f, int64_t ldf, f
         for (int u = 0; u < kU; ++u) fv[u] = f[(t + u) * ldf + i];
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            hab[(t + u) * ldh + i] = fv[u] - 0.65f * e;
-            if (!(first && t + u == 0)) e = 0.985f * e + 0.015f * fv[u];
+            hab[(t + u) * ldh + i] = hab_of(fv[u], e);
+            if (!(first && t + u == 0)) e = ema_step(e, fv[u]);
         }
     }
     for (; t < T; ++t) {
         const float ft = f[t * ldf + i];
-        hab[t * ldh + i] = ft - 0.65f * e;
-        if (!(first && t == 0)) e = 0.985f * e + 0.015f * ft;
+        hab[t * ldh + i] = hab_of(ft, e);
+        if (!(first && t == 0)) e = ema_step(e, ft);
     }
     ema[i] = e;
 }
@@ -142,6 +142,36 @@ __global__ __launch_bounds__(64) void score_tail_kernel(const float *__restrict_
     if (threadIdx.x == 0) out[t] = (first && t == 0) ? r : r + 0.35f * fmaxf(0.0f, a - r);
 }
 
+// The decode step's tail: block 0 (its first wave) the score of the token, as score_tail_kernel at
+// T = 1; blocks 1.. the EMA state, e = f on the first token, else 0.985 e + 0.015 f (the update of
+// ema_habituate_kernel at T = 1), after the fc1 launch has read the state.
+__global__ __launch_bounds__(256) void score_step_tail_kernel(const float *__restrict__ h, int64_t ldh,
+                                                               const float *__restrict__ w2,
+                                                               const float *__restrict__ b2, int64_t hidden,
+                                                               int first, float *__restrict__ out,
+                                                               const int32_t *__restrict__ out_index,
+                                                               const float *__restrict__ f, float *__restrict__ ema,
+                                                               int64_t fd) {
+    if (blockIdx.x == 0) {
+        if (threadIdx.x >= 64) return;
+        if (out_index) out += *out_index;
+        float r = 0.0f, s = 0.0f;
+        for (int64_t i = threadIdx.x; i < hidden; i += 64) {
+            const float x0 = h[i], x1 = h[ldh + i];
+            r = fmaf(ref_geluf(x0), w2[i], r);
+            s = fmaf(ref_geluf(x1), w2[i], s);
+        }
+        r = wave_sum(r) + b2[0];
+        s = wave_sum(s) + b2[0];
+        if (threadIdx.x == 0) out[0] = first ? r : r + 0.35f * fmaxf(0.0f, s - r);
+        return;
+    }
+    const int64_t i = (int64_t)(blockIdx.x - 1) * 256 + threadIdx.x;
+    if (i >= fd) return;
+    const float fv = f[i];
+    ema[i] = first ? fv : ema_step(ema[i], fv);
+}
+
 }  // namespace
 
 extern "C" {
@@ -171,6 +201,37 @@ int vgx_layernorm(const float *x, int64_t ldx, const float *w, const float *b, f
     else
         hipLaunchKernelGGL(layernorm_kernel, dim3((unsigned)n_rows), dim3(256), 0, (hipStream_t)stream, x, ldx, w, b,
                            y, ldy, dim, eps);
+    VGX_CHECK_LAUNCH();
+    return VGX_OK;
+}
+
+int vgx_seg_score_step(const float *feat, int64_t fd, float *ema, int first, const void *w1, int64_t hidden,
+                       const float *b1, const float *ln_w, const float *ln_b, float eps, const float *w2,
+                       const float *b2, float *h, float *out, const int32_t *out_index, void *stream) {
+    if (!feat || !ema || !w1 || !b1 || !ln_w || !ln_b || !w2 || !b2 || !h || !out) return VGX_E_ARG;
+    if (fd <= 0 || hidden <= 0 || fd % QK || !(eps > 0.0f)) return VGX_E_SIZE;
+    GemvArgs a{};
+    a.w = static_cast<const uint8_t *>(w1);
+    a.nblk = (int)(fd / QK);
+    a.n_rq = (hidden + 3) / 4;
+    a.rows_out = hidden;
+    a.x = feat;
+    a.ldx = fd;
+    a.batch = 2;
+    a.lnw = ln_w;
+    a.eps = eps;
+    a.bias = b1;
+    a.y = h;
+    a.ldy = hidden;
+    a.epi = EPI_STORE;
+    a.sc_ema = ema;
+    a.sc_lnb = ln_b;
+    a.sc_first = first ? 1 : 0;
+    hipStream_t st = (hipStream_t)stream;
+    const int rc = vgx_detail_qgemv_f32(a, st);
+    if (rc != VGX_OK) return rc;
+    hipLaunchKernelGGL(score_step_tail_kernel, dim3((unsigned)(1 + (fd + 255) / 256)), dim3(256), 0, st, h, hidden, w2,
+                       b2, hidden, first ? 1 : 0, out, out_index, feat, ema, fd);
     VGX_CHECK_LAUNCH();
     return VGX_OK;
 }

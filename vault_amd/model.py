@@ -853,6 +853,13 @@ class VAULTv3ForCausalLM:
         features in rows[:T]; rows[T:] receive the habituated features, then both halves are
         LayerNormed in place."""
         sw = self.w.scorer
+        fd = rows.shape[1]
+        if T == 1 and fd <= 5120 and sw.w1.dtype == ops.L.F32 and \
+                all(t.data_ptr() % 16 == 0 for t in (rows, st.seg_feat_ema, sw.ln_w, sw.ln_b)):
+            # one token: the fc1 GEMV builds both LayerNormed rows itself, the tail updates the EMA
+            ops.seg_score_step(rows[0], st.seg_feat_ema, first, sw.w1, sw.b1, sw.ln_w, sw.ln_b, 1e-5, sw.w2, sw.b2,
+                               st.sc_cur[c0:c0 + 1], out_index=out_index)
+            return
         ops.ema_habituate(rows[:T], rows[T:2 * T], st.seg_feat_ema, first)
         ops.layernorm(rows[:2 * T], sw.ln_w, sw.ln_b, 1e-5, rows[:2 * T])
         h1 = ops.qlinear(sw.w1, rows[:2 * T], bias=sw.b1)   # T = 1: both rows in one pass over the weights

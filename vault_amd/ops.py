@@ -388,6 +388,21 @@ def layernorm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float, out
     return out
 
 
+def seg_score_step(feat: torch.Tensor, ema: torch.Tensor, first: bool, w1: "QWeight", b1: torch.Tensor,
+                   ln_w: torch.Tensor, ln_b: torch.Tensor, eps: float, w2: torch.Tensor, b2: torch.Tensor,
+                   out: torch.Tensor, out_index: Optional[torch.Tensor] = None) -> None:
+    """The scorer of one decode token (two launches; the fc1 GEMV builds both LayerNormed rows itself):
+    its score into out[0] (shifted by the device int32 ``out_index``) and the EMA state updated."""
+    fd = feat.numel()
+    if w1.dtype != L.F32 or w1.cols != fd:
+        raise ValueError("seg_score_step needs the F32 fc1 weight of the features' width")
+    h = torch.empty(2, w1.rows, dtype=torch.float32, device=feat.device)
+    L.check(L.load().vgx_seg_score_step(feat.data_ptr(), fd, ema.data_ptr(), 1 if first else 0, w1.packed.data_ptr(),
+                                        w1.rows, b1.data_ptr(), ln_w.data_ptr(), ln_b.data_ptr(), float(eps),
+                                        w2.data_ptr(), b2.data_ptr(), h.data_ptr(), out.data_ptr(), _ptr(out_index),
+                                        _stream(feat.device)), "vgx_seg_score_step")
+
+
 def seg_score_tail(h: torch.Tensor, w2: torch.Tensor, b2: torch.Tensor, T: int, first: bool, out: torch.Tensor,
                    out_index: Optional[torch.Tensor] = None) -> None:
     """Scores of T tokens into out[0:T] (shifted by the device int32 ``out_index`` when given)."""
