@@ -494,6 +494,34 @@ int vgx_seg_score_step(const float *feat, int64_t fd, float *ema, int first, con
                        const float *b1, const float *ln_w, const float *ln_b, float eps, const float *w2,
                        const float *b2, float *h, float *out, const int32_t *out_index, void *stream);
 
+/* One half of vgx_seg_score_step as a job that a GEMV launch can carry (vgx_qlinear_side).
+ * phase 1: the fc1 GEMV on the two LayerNormed rows, into h; phase 2 (after phase 1): the score into
+ * out[0] (shifted by *out_index) and the EMA update.  Phase 1 reads ema, phase 2 writes it. */
+typedef struct vgx_score_side {
+    int phase;
+    const float *feat;          /* the token's features [fd], fd <= 5120 */
+    int64_t fd;
+    float *ema;                 /* the EMA state [fd] */
+    int first;                  /* the stream's first token: e = feat, no EMA update */
+    const void *w1;             /* packed F32 fc1 weight [hidden x fd] */
+    int64_t hidden;
+    const float *b1, *ln_w, *ln_b;
+    float eps;
+    const float *w2, *b2;       /* fc2 [hidden], bias [1] */
+    float *h;                   /* [2][hidden]: written by phase 1, read by phase 2 */
+    float *out;
+    const int32_t *out_index;   /* may be NULL */
+} vgx_score_side;
+
+/* vgx_qlinear_ex, and the scorer job *side (may be NULL): when the GEMV runs the 16-wave pieces kernel
+ * (batch 1, 192-320 blocks per row: the down projection of a decode step, which leaves a quarter of the
+ * CUs idle) the job takes extra workgroups of the same launch; otherwise it is launched after the GEMV.
+ * Results equal those of the separate calls bit for bit.  No counterpart in the reference: it removes
+ * the scorer's launches from the decode step (src/vault_v3_model.py:2294-2305 is the computation). */
+int vgx_qlinear_side(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
+                     int64_t batch, const float *norm_w, float eps, const float *bias, float *y, int64_t ldy,
+                     int epilogue, const vgx_score_side *side, void *stream);
+
 /* ---------------------------------------------------------------- top candidates of a row ------ */
 
 /* The T (<= 256) largest logits of each row, sorted by value descending, ties by index ascending

@@ -112,3 +112,48 @@ def test_score_step_equals_separate_launches(dev, fd, first):
     torch.cuda.synchronize()
     assert torch.equal(out_a, out_b) and out_b[5].item() != -7.0
     assert torch.equal(ema_a, ema_b)
+
+
+@pytest.mark.parametrize("dt,rows,cols", [(9, 1536, 8960), (8, 1536, 8960), (9, 1536, 1536), (9, 256, 1536)])
+@pytest.mark.parametrize("first", [True, False])
+def test_score_jobs_with_a_gemv(dev, dt, rows, cols, first):
+    """vgx_qlinear_side: the scorer's two jobs carried by a batch-1 GEMV launch (the 16-wave pieces
+    GEMV of the down projection's shapes, Q4_0 / Q8_0) or launched after it (other shapes).  The GEMV
+    result (accumulated) equals vgx_qlinear's, the score and the EMA state equal vgx_seg_score_step's,
+    all bit for bit."""
+    from vault_amd import vlt3
+    rng = np.random.default_rng(rows + cols + dt + first)
+    fd, hidden = 4608, 256
+    w = ops.QWeight.from_blocks(dt, rows, cols, vlt3.synthetic_blocks(dt, rows, cols, rng), dev)
+    x = torch.from_numpy(rng.standard_normal((1, cols)).astype(np.float32)).to(dev)
+    y0 = torch.from_numpy(rng.standard_normal((1, rows)).astype(np.float32)).to(dev)
+    f = torch.from_numpy((rng.standard_normal(fd) * 2.0).astype(np.float32)).to(dev)
+    ema0 = torch.from_numpy(rng.standard_normal(fd).astype(np.float32)).to(dev)
+    ln_w = torch.from_numpy(rng.uniform(0.8, 1.2, fd).astype(np.float32)).to(dev)
+    ln_b = torch.from_numpy((rng.standard_normal(fd) * 0.05).astype(np.float32)).to(dev)
+    w1 = ops.QWeight.from_blocks(ops.L.F32, hidden, fd,
+                                 (rng.standard_normal((hidden, fd)) * 0.02).astype(np.float32).tobytes(), dev)
+    b1, w2 = (torch.from_numpy((rng.standard_normal(hidden) * 0.02).astype(np.float32)).to(dev) for _ in range(2))
+    b2 = torch.from_numpy((rng.standard_normal(1) * 0.02).astype(np.float32)).to(dev)
+    idx = torch.tensor([3], dtype=torch.int32, device=dev)
+    # reference: the GEMV and the scorer step on their own
+    y_a = y0.clone()
+    ops.qlinear(w, x, out=y_a, accumulate=True)
+    ema_a, out_a = ema0.clone(), torch.full((8,), -7.0, device=dev)
+    ops.seg_score_step(f, ema_a, first, w1, b1, ln_w, ln_b, 1e-5, w2, b2, out_a[0:1], out_index=idx)
+    # the jobs with the GEMV (phase 1 with one launch, phase 2 with the next)
+    y_b = y0.clone()
+    ema_b, out_b = ema0.clone(), torch.full((8,), -7.0, device=dev)
+    h = torch.full((2, hidden), float("nan"), device=dev)
+    args = (f, ema_b, first, w1, b1, ln_w, ln_b, 1e-5, w2, b2, h, out_b[0:1], idx)
+    ops.qlinear_side(w, x, y_b, True, ops.score_side(1, *args))
+    y_c = y_b.clone()
+    ops.qlinear_side(w, x, y_c, True, ops.score_side(2, *args))
+    torch.cuda.synchronize()
+    assert torch.equal(y_a, y_b)
+    assert torch.equal(out_a, out_b) and out_b[3].item() != -7.0
+    assert torch.equal(ema_a, ema_b)
+    y_d = y_a.clone()
+    ops.qlinear(w, x, out=y_d, accumulate=True)
+    assert torch.equal(y_c, y_d)
+

@@ -73,3 +73,21 @@ def test_state_has_no_reference_cycle():
         assert ref() is None
     finally:
         gc.enable()
+
+
+def test_score_side_rejects_bad_jobs(lib):
+    """vgx_qlinear_side checks its scorer job before any launch: unknown phase, feature widths past the
+    prologue's 5120 or not whole blocks, misaligned rows, null pointers."""
+    p = 1 << 20
+    job = L.ScoreSide(1, p, 4608, p, 0, p, 256, p, p, p, 1e-5, p, p, p, p, None)
+    call = lambda j: lib.vgx_qlinear_side(L.Q4_0, p, 1536, 8960, p, 8960, 1, None, 0.0, None, p, 1536, 1,
+                                          C.byref(j), None)
+    for field, val, code in [("phase", 3, -31), ("fd", 5152, -10), ("fd", 100, -1), ("feat", p + 4, -11),
+                             ("ema", None, -31), ("eps", 0.0, -1)]:
+        bad = L.ScoreSide.from_buffer_copy(job)
+        setattr(bad, field, val)
+        assert call(bad) == code, field
+    bad = L.ScoreSide.from_buffer_copy(job)
+    bad.phase = 2
+    bad.h = None
+    assert call(bad) == -31

@@ -48,6 +48,7 @@ _SIGS = {
     "vgx_qlinear_swiglu": (I32, [I32, P, I64, I64, P, I64, I64, P, I64, P]),
     "vgx_qlinear_ex": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P]),
     "vgx_qlinear_indirect": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P]),
+    "vgx_qlinear_side": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P, P]),
     "vgx_qgemm_workspace_bytes": (I64, [I64, I64, I64, I32]),
     "vgx_qgemm": (I32, [I32, P, I64, I64, P, I64, I64, P, F, P, P, I64, I32, P, I64, P]),
     "vgx_attn_decode_workspace_bytes": (I64, [I64, I64, I64, I64, I64]),
@@ -121,6 +122,14 @@ class AttnBlock(C.Structure):
                 ("ldo", C.c_int64), ("o_hstride", C.c_int64), ("n_q", C.c_int64), ("causal_base", C.c_int64),
                 ("n_runs", C.c_int), ("runs", KVRun * 4), ("bias", C.c_void_p), ("bias_head_row", C.c_void_p),
                 ("bias_ldq", C.c_int64), ("bias_rstride", C.c_int64), ("bias_run", C.c_int)]
+
+
+class ScoreSide(C.Structure):
+    """vgx_score_side (include/vault_amd.h)."""
+    _fields_ = [("phase", C.c_int), ("feat", C.c_void_p), ("fd", C.c_int64), ("ema", C.c_void_p), ("first", C.c_int),
+                ("w1", C.c_void_p), ("hidden", C.c_int64), ("b1", C.c_void_p), ("ln_w", C.c_void_p),
+                ("ln_b", C.c_void_p), ("eps", C.c_float), ("w2", C.c_void_p), ("b2", C.c_void_p), ("h", C.c_void_p),
+                ("out", C.c_void_p), ("out_index", C.c_void_p)]
 
 
 class VGXError(RuntimeError):

@@ -47,6 +47,8 @@ __host__ __device__ constexpr bool gemv_plain(int dt) { return dt == VGX_F32 || 
 __host__ __device__ constexpr bool gemv_half(int dt) { return dt == VGX_BF16 || dt == VGX_F16; }
 __host__ __device__ constexpr bool gemv_quant(int dt) { return dt == VGX_Q8_0 || dt == VGX_Q4_0; }
 
+struct ScoreSide;
+
 struct GemvArgs {
     const uint8_t *w;
     int nblk;            // 32-weight blocks per row
@@ -70,6 +72,7 @@ struct GemvArgs {
     const float *sc_ema;
     const float *sc_lnb;
     int sc_first;
+    const ScoreSide *side;  // host side only: a scorer job launched with this GEMV (in its spare workgroups)
 };
 
 // The output address of a launch whose GemvArgs name it indirectly (a captured graph whose output
@@ -862,7 +865,7 @@ __device__ __forceinline__ float gemv_piece_dot(uint4 w, uint32_t sc, const floa
 constexpr int kPiecesMaxBlocks = 320;
 
 template <int DT, int EPI, int NW, int RQG, int MAXB>
-__global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
+__device__ __forceinline__ void gemv1_pieces_body(GemvArgs a, int bid) {
     gemv_resolve_y(a);
     constexpr int QB = gemv_quant_bytes(DT);
     constexpr int BPP = 1024 / (4 * QB);              // blocks per 1 KB piece: 16 (Q4_0) / 8 (Q8_0)
@@ -874,7 +877,7 @@ __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nblk = a.nblk, cols = nblk * QK;
     const int npc = (nblk + BPP - 1) / BPP;           // pieces per row-quad
-    const int64_t rq0 = (int64_t)blockIdx.x * RQG;
+    const int64_t rq0 = (int64_t)bid * RQG;
     const int n_rq = (int)a.n_rq;
     float *xsum = xs + nblk * kGemvPad;
     const int row = DT == VGX_Q8_0 ? (lane >> 1) & 3 : lane & 3;   // the lane's row of the row-quad
@@ -966,6 +969,11 @@ __global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
     }
 }
 
+template <int DT, int EPI, int NW, int RQG, int MAXB>
+__global__ __launch_bounds__(64 * NW) void gemv1_pieces_kernel(GemvArgs a) {
+    gemv1_pieces_body<DT, EPI, NW, RQG, MAXB>(a, blockIdx.x);
+}
+
 // One or two activation rows against F32 weights of up to 160 blocks per row (the segment scorer's fc1,
 // 256 x 4608, on the token's features and their habituated copy): the weights are read once for both
 // rows.  A workgroup of 16 waves per row-quad; the row-quad's run (512 bytes per block) is cut into 1 KB
@@ -1054,8 +1062,8 @@ __device__ __forceinline__ void scorer_rows(const GemvArgs &a, const float4 (&f)
     }
 }
 
-template <int NB, int EPI, bool SCORER = false>
-__global__ __launch_bounds__(64 * kF32PiecesWaves) void gemv_f32_pieces_kernel(GemvArgs a) {
+template <int NB, int EPI, bool SCORER>
+__device__ __forceinline__ void gemv_f32_pieces_body(GemvArgs a, int64_t rq) {
     static_assert(!SCORER || (NB == 2 && EPI == EPI_STORE), "the scorer prologue builds two rows");
     gemv_resolve_y(a);
     constexpr int NW = kF32PiecesWaves;
@@ -1066,7 +1074,6 @@ __global__ __launch_bounds__(64 * kF32PiecesWaves) void gemv_f32_pieces_kernel(G
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nblk = a.nblk, n4 = nblk * 8;
     const int npc = (nblk + 1) / 2;                   // pieces per row-quad
-    const int64_t rq = blockIdx.x;
     const int row = (lane >> 3) & 3;
     // activations (both rows, or the scorer prologue's inputs), then the weights
     constexpr int XR = SCORER ? 1 : (NB * kF32PiecesMaxBlocks * 8 + 64 * NW - 1) / (64 * NW);
@@ -1144,10 +1151,128 @@ __global__ __launch_bounds__(64 * kF32PiecesWaves) void gemv_f32_pieces_kernel(G
     }
 }
 
+template <int NB, int EPI, bool SCORER = false>
+__global__ __launch_bounds__(64 * kF32PiecesWaves) void gemv_f32_pieces_kernel(GemvArgs a) {
+    gemv_f32_pieces_body<NB, EPI, SCORER>(a, blockIdx.x);
+}
+
+// The decode token's segment scorer as two jobs of 1024-thread workgroups, each either launched on its
+// own (score_side_kernel) or carried by the spare workgroups of a 16-wave GEMV launch (the down
+// projection of a later layer leaves a quarter of the CUs idle at batch 1), so that neither adds a
+// launch to the step.  Phase 1: the fc1 GEMV with the LayerNorm prologue, one workgroup per row-quad
+// (gemv_f32_pieces_body).  Phase 2: the tail (score_tail_kernel's arithmetic at T = 1, first wave of
+// workgroup 0) and the EMA update (ema_habituate_kernel's at T = 1), 1024 features per workgroup.
+struct ScoreSide {
+    int phase;                  // 1 or 2
+    GemvArgs fc1;               // phase 1: x = the features, y = h
+    const float *h;             // phase 2: the fc1 outputs, [2][hidden]
+    int64_t hidden;
+    const float *w2, *b2;
+    int first;
+    float *out;
+    const int32_t *out_index;   // may be null: added to out
+    const float *f;             // the features
+    float *ema;
+    int64_t fd;
+};
+
+inline int64_t score_side_blocks(const ScoreSide &s) { return s.phase == 1 ? s.fc1.n_rq : 1 + (s.fd + 1023) / 1024; }
+
+__device__ __forceinline__ void score_tail_body(const ScoreSide &s, int bid) {
+    if (bid == 0) {
+        if (threadIdx.x >= 64) return;
+        float *out = s.out + (s.out_index ? *s.out_index : 0);
+        float r = 0.0f, a = 0.0f;
+        for (int64_t i = threadIdx.x; i < s.hidden; i += 64) {
+            const float x0 = s.h[i], x1 = s.h[s.hidden + i];
+            r = fmaf(ref_geluf(x0), s.w2[i], r);
+            a = fmaf(ref_geluf(x1), s.w2[i], a);
+        }
+        r = wave_sum(r) + s.b2[0];
+        a = wave_sum(a) + s.b2[0];
+        if (threadIdx.x == 0) out[0] = s.first ? r : r + 0.35f * fmaxf(0.0f, a - r);
+        return;
+    }
+    const int64_t i = (int64_t)(bid - 1) * 1024 + threadIdx.x;
+    if (i >= s.fd) return;
+    const float fv = s.f[i];
+    s.ema[i] = s.first ? fv : ema_step(s.ema[i], fv);
+}
+
+__device__ __forceinline__ void score_side_run(const ScoreSide &s, int bid) {
+    if (s.phase == 1) gemv_f32_pieces_body<2, EPI_STORE, true>(s.fc1, bid);
+    else score_tail_body(s, bid);
+}
+
+// Checks of a scorer job against what its kernels assume (phase 1: the prologue's row width and
+// alignment, the F32 pieces layout; phase 2: pointers).
+inline int score_side_check(const ScoreSide &s) {
+    if (s.phase == 1) {
+        const GemvArgs &a = s.fc1;
+        if (!a.w || !a.x || !a.sc_ema || !a.lnw || !a.sc_lnb || !a.y) return VGX_E_ARG;
+        if (a.batch != 2 || a.epi != EPI_STORE || a.nblk <= 0 || a.nblk > kF32PiecesMaxBlocks ||
+            a.nblk * QK > 256 * 4 * kScLnF4 || a.n_rq <= 0 || a.n_rq * a.nblk * 512 >= ((int64_t)1 << 31))
+            return VGX_E_LIMIT;
+        if ((((uintptr_t)a.x | (uintptr_t)a.sc_ema | (uintptr_t)a.lnw | (uintptr_t)a.sc_lnb) & 15) != 0)
+            return VGX_E_ALIGN;
+        return VGX_OK;
+    }
+    if (s.phase == 2) return s.h && s.w2 && s.b2 && s.out && s.f && s.ema && s.hidden > 0 && s.fd > 0 ? VGX_OK : VGX_E_ARG;
+    return VGX_E_ARG;
+}
+
+// A scorer job from its C description (include/vault_amd.h: vgx_score_side), checked.
+inline int make_score_side(const vgx_score_side &c, ScoreSide &s) {
+    if (c.phase != 1 && c.phase != 2) return VGX_E_ARG;
+    if (c.fd <= 0 || c.hidden <= 0 || c.fd % QK || !(c.eps > 0.0f)) return VGX_E_SIZE;
+    if (!c.feat || !c.ema || !c.w1 || !c.b1 || !c.ln_w || !c.ln_b || !c.w2 || !c.b2 || !c.h || !c.out) return VGX_E_ARG;
+    s = ScoreSide{};
+    s.phase = c.phase;
+    GemvArgs &a = s.fc1;
+    a.w = static_cast<const uint8_t *>(c.w1);
+    a.nblk = (int)(c.fd / QK);
+    a.n_rq = (c.hidden + 3) / 4;
+    a.rows_out = c.hidden;
+    a.x = c.feat;
+    a.ldx = c.fd;
+    a.batch = 2;
+    a.lnw = c.ln_w;
+    a.eps = c.eps;
+    a.bias = c.b1;
+    a.y = c.h;
+    a.ldy = c.hidden;
+    a.epi = EPI_STORE;
+    a.sc_ema = c.ema;
+    a.sc_lnb = c.ln_b;
+    a.sc_first = c.first ? 1 : 0;
+    s.h = c.h;
+    s.hidden = c.hidden;
+    s.w2 = c.w2;
+    s.b2 = c.b2;
+    s.first = c.first ? 1 : 0;
+    s.out = c.out;
+    s.out_index = c.out_index;
+    s.f = c.feat;
+    s.ema = c.ema;
+    s.fd = c.fd;
+    return score_side_check(s);
+}
+
+// Launches a scorer job on its own (score_side_kernel, defined once in qlinear.hip).
+int vgx_detail_score_side(const ScoreSide &s, hipStream_t st);
+
+// The 16-wave pieces GEMV with a scorer job in workgroups main_blocks.. of the same launch.
+template <int DT, int EPI, int RQG, int MAXB>
+__global__ __launch_bounds__(1024) void gemv1_pieces_side_kernel(GemvArgs a, ScoreSide s, int main_blocks) {
+    if ((int)blockIdx.x < main_blocks) gemv1_pieces_body<DT, EPI, 16, RQG, MAXB>(a, blockIdx.x);
+    else score_side_run(s, (int)blockIdx.x - main_blocks);
+}
+
 constexpr int kGemv1MaxBlocks = 448;   // LDS staging of one row: 448 * 36 * 4 B = 63 KB
 
+// Returns whether a scorer job (a.side) went with the launch; otherwise the caller launches it.
 template <int DT, int EPI, bool NORM>
-void gemv1_launch(const GemvArgs &a, hipStream_t st) {
+bool gemv1_launch(const GemvArgs &a, hipStream_t st) {
     const size_t lds = (size_t)a.nblk * kGemvPad * sizeof(float);
 #define VGX_GEMV1(LPR, WPG, KW, U, SF, XD)                                                              \
     hipLaunchKernelGGL((gemv1_kernel<DT, EPI, NORM, LPR, WPG, KW, U, SF, XD>),                           \
@@ -1158,7 +1283,7 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
         if (a.nblk == kStreamBlocks && !a.bias && a.n_rq >= kStreamMinRq && a.soff < ((int64_t)1 << 31) && aligned) {
             const unsigned grid = (unsigned)std::min<int64_t>(StreamGeom<DT>::GROUPS, (a.n_rq + 3) / 4);
             hipLaunchKernelGGL((gemv1_stream_kernel<DT, EPI, NORM>), dim3(grid), dim3(256), 0, st, a);
-            return;
+            return false;
         }
     }
     if constexpr (gemv_quant(DT) && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
@@ -1166,9 +1291,16 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
             // 16 waves x 2 row-quads: 5.5 us for 1536 x 8960 (8 x 2: 5.8, 8 x 1: 6.0, 16 x 1: 5.9, 16 x 4: 7.3,
             // 4 x 1: 6.8; the lane-per-block kernel: 6.6)
             constexpr int NW = 16, RQG = 2;
-            hipLaunchKernelGGL((gemv1_pieces_kernel<DT, EPI, NW, RQG, kPiecesMaxBlocks>), dim3((unsigned)((a.n_rq + RQG - 1) / RQG)), dim3(64 * NW),
-                               (size_t)(a.nblk * kGemvPad + a.nblk) * sizeof(float), st, a);
-            return;
+            const unsigned main = (unsigned)((a.n_rq + RQG - 1) / RQG);
+            const size_t lds = (size_t)(a.nblk * kGemvPad + a.nblk) * sizeof(float);
+            if (a.side != nullptr)
+                hipLaunchKernelGGL((gemv1_pieces_side_kernel<DT, EPI, RQG, kPiecesMaxBlocks>),
+                                   dim3(main + (unsigned)score_side_blocks(*a.side)), dim3(64 * NW), lds, st, a, *a.side,
+                                   (int)main);
+            else
+                hipLaunchKernelGGL((gemv1_pieces_kernel<DT, EPI, NW, RQG, kPiecesMaxBlocks>), dim3(main), dim3(64 * NW),
+                                   lds, st, a);
+            return a.side != nullptr;
         }
     }
     if constexpr (gemv_quant(DT) && !NORM && (EPI == EPI_STORE || EPI == EPI_ACCUM)) {
@@ -1178,7 +1310,7 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
             // 4 x 2: 3.6, 3 x 1: 3.2, 6 x 2: 3.4, 8 x 4: 3.6)
             hipLaunchKernelGGL((gemv1_pieces_kernel<DT, EPI, 4, 1, kStreamBlocks>), dim3((unsigned)a.n_rq), dim3(256),
                                (size_t)(a.nblk * kGemvPad + a.nblk) * sizeof(float), st, a);
-            return;
+            return false;
         }
     }
     constexpr int UT = gemv_half(DT) ? 1 : 3;                           // BF16 / F16 blocks are 64 registers
@@ -1196,27 +1328,17 @@ void gemv1_launch(const GemvArgs &a, hipStream_t st) {
     else if (aligned && !gemv_plain(DT)) VGX_GEMV1(64, 1, 1, 1, false, true);   // small: direct
     else VGX_GEMV1(64, 2, 1, 1, true, false);
 #undef VGX_GEMV1
+    return false;
 }
 
 // Launch the GEMV over all batch rows.  A single row (the decode step) runs gemv1_kernel; more rows
 // run qgemv_kernel in passes of up to 4, in row mode (16 lanes per row-quad, 4 waves per workgroup)
 // for >= 2048 row-quads, else in split-K mode (one wave per row-quad).
 template <int DT>
-int qgemv_launch(GemvArgs a, hipStream_t st) {
+int qgemv_launch_impl(GemvArgs a, hipStream_t st, bool &carried) {
     const bool rows_mode = a.n_rq >= 2048;
     const bool norm = a.lnw != nullptr;
     if constexpr (DT == VGX_F32) {
-        if (a.sc_ema != nullptr) {
-            // the segment scorer's fc1 with its prologue (two rows, F32 weights)
-            if (a.batch != 2 || a.epi != EPI_STORE || a.nblk > kF32PiecesMaxBlocks || a.nblk * QK > 256 * 4 * kScLnF4 ||
-                a.n_rq * a.nblk * 512 >= ((int64_t)1 << 31))
-                return VGX_E_LIMIT;
-            if ((((uintptr_t)a.x | (uintptr_t)a.sc_ema | (uintptr_t)a.lnw | (uintptr_t)a.sc_lnb) & 15) != 0)
-                return VGX_E_ALIGN;
-            hipLaunchKernelGGL((gemv_f32_pieces_kernel<2, EPI_STORE, true>), dim3((unsigned)a.n_rq),
-                               dim3(64 * kF32PiecesWaves), 0, st, a);
-            return hipGetLastError() == hipSuccess ? VGX_OK : VGX_E_HIP;
-        }
         if (a.batch <= 2 && !norm && a.epi != EPI_SWIGLU && a.nblk <= kF32PiecesMaxBlocks &&
             a.n_rq * a.nblk * 512 < ((int64_t)1 << 31) && ((uintptr_t)a.x & 15) == 0 && a.ldx % 4 == 0) {
 #define VGX_F32P(NB, EPIV) hipLaunchKernelGGL((gemv_f32_pieces_kernel<NB, EPIV>), dim3((unsigned)a.n_rq), dim3(64 * kF32PiecesWaves), 0, st, a)
@@ -1227,9 +1349,9 @@ int qgemv_launch(GemvArgs a, hipStream_t st) {
         }
     }
     if (a.batch == 1 && a.nblk <= kGemv1MaxBlocks && ((uintptr_t)a.x & 15) == 0 && ((uintptr_t)a.lnw & 15) == 0) {
-        if (a.epi == EPI_SWIGLU) { if (norm) gemv1_launch<DT, EPI_SWIGLU, true>(a, st); else gemv1_launch<DT, EPI_SWIGLU, false>(a, st); }
-        else if (a.epi == EPI_ACCUM) { if (norm) gemv1_launch<DT, EPI_ACCUM, true>(a, st); else gemv1_launch<DT, EPI_ACCUM, false>(a, st); }
-        else { if (norm) gemv1_launch<DT, EPI_STORE, true>(a, st); else gemv1_launch<DT, EPI_STORE, false>(a, st); }
+        if (a.epi == EPI_SWIGLU) carried = norm ? gemv1_launch<DT, EPI_SWIGLU, true>(a, st) : gemv1_launch<DT, EPI_SWIGLU, false>(a, st);
+        else if (a.epi == EPI_ACCUM) carried = norm ? gemv1_launch<DT, EPI_ACCUM, true>(a, st) : gemv1_launch<DT, EPI_ACCUM, false>(a, st);
+        else carried = norm ? gemv1_launch<DT, EPI_STORE, true>(a, st) : gemv1_launch<DT, EPI_STORE, false>(a, st);
         return hipGetLastError() == hipSuccess ? VGX_OK : VGX_E_HIP;
     }
     for (int64_t b0 = 0; b0 < a.batch; b0 += 4) {
@@ -1267,6 +1389,15 @@ int qgemv_launch(GemvArgs a, hipStream_t st) {
         if (hipGetLastError() != hipSuccess) return VGX_E_HIP;
     }
     return VGX_OK;
+}
+
+// The GEMV, then a scorer job (a.side) that did not go with its launch.
+template <int DT>
+int qgemv_launch(GemvArgs a, hipStream_t st) {
+    bool carried = false;
+    const int rc = qgemv_launch_impl<DT>(a, st, carried);
+    if (rc != VGX_OK || a.side == nullptr || carried) return rc;
+    return vgx_detail_score_side(*a.side, st);
 }
 
 }  // namespace vgx

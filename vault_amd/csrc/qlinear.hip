@@ -143,7 +143,14 @@ __global__ void embed_kernel(const uint8_t *__restrict__ w, const int64_t *__res
 
 inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
 
+__global__ __launch_bounds__(1024) void score_side_kernel(ScoreSide s) { score_side_run(s, (int)blockIdx.x); }
+
 }  // namespace
+
+int vgx::vgx_detail_score_side(const ScoreSide &s, hipStream_t st) {
+    hipLaunchKernelGGL(score_side_kernel, dim3((unsigned)score_side_blocks(s)), dim3(1024), 0, st, s);
+    return hipGetLastError() == hipSuccess ? VGX_OK : VGX_E_HIP;
+}
 
 extern "C" {
 
@@ -274,8 +281,10 @@ int vgx_embed_rows(int dtype, const void *packed, int64_t rows, int64_t cols, co
 
 static int qgemv_dispatch(int dtype, const void *w, int64_t rows_packed, int64_t rows_out, int64_t cols,
                           const float *x, int64_t ldx, int64_t batch, const float *lnw, float eps, const float *bias,
-                          float *y, int64_t ldy, int epi, void *stream, const int64_t *y_ref = nullptr) {
+                          float *y, int64_t ldy, int epi, void *stream, const int64_t *y_ref = nullptr,
+                          const ScoreSide *side = nullptr) {
     GemvArgs a{};
+    a.side = side;
     a.w = static_cast<const uint8_t *>(w);
     a.nblk = (int)(cols / QK);
     a.soff = gemv_plain(dtype) ? 0 : scale_off(dtype, rows_packed, cols);
@@ -317,6 +326,28 @@ int vgx_qlinear_ex(int dtype, const void *w_packed, int64_t rows, int64_t cols, 
     const int64_t rows_packed = epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows;
     return qgemv_dispatch(dtype, w_packed, rows_packed, rows, cols, x, ldx, batch, norm_w, eps, bias, y, ldy,
                           epilogue, stream);
+}
+
+int vgx_qlinear_side(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,
+                     int64_t batch, const float *norm_w, float eps, const float *bias, float *y, int64_t ldy,
+                     int epilogue, const vgx_score_side *side, void *stream) {
+    if (!side)
+        return vgx_qlinear_ex(dtype, w_packed, rows, cols, x, ldx, batch, norm_w, eps, bias, y, ldy, epilogue, stream);
+    ScoreSide sj;
+    const int rc = make_score_side(*side, sj);
+    if (rc != VGX_OK) return rc;
+    if (!dtype_ok(dtype)) return VGX_E_DTYPE;
+    if (!w_packed || !x || !y) return VGX_E_ARG;
+    if (epilogue != VGX_EPI_STORE && epilogue != VGX_EPI_ACCUM && epilogue != VGX_EPI_SWIGLU) return VGX_E_ARG;
+    if (epilogue == VGX_EPI_SWIGLU && bias) return VGX_E_ARG;
+    if (rows <= 0 || cols <= 0 || batch < 0 || ldx < cols || ldy < rows) return VGX_E_SIZE;
+    if (cols % QK || (epilogue == VGX_EPI_SWIGLU && rows % 2)) return VGX_E_SHAPE;
+    if (cols / QK > (1 << 24)) return VGX_E_LIMIT;
+    if (norm_w && !(eps > 0.0f)) return VGX_E_ARG;
+    if (batch == 0) return vgx_detail_score_side(sj, (hipStream_t)stream);
+    const int64_t rows_packed = epilogue == VGX_EPI_SWIGLU ? 2 * rows : rows;
+    return qgemv_dispatch(dtype, w_packed, rows_packed, rows, cols, x, ldx, batch, norm_w, eps, bias, y, ldy, epilogue,
+                          stream, nullptr, &sj);
 }
 
 int vgx_qlinear_indirect(int dtype, const void *w_packed, int64_t rows, int64_t cols, const float *x, int64_t ldx,

@@ -142,36 +142,6 @@ __global__ __launch_bounds__(64) void score_tail_kernel(const float *__restrict_
     if (threadIdx.x == 0) out[t] = (first && t == 0) ? r : r + 0.35f * fmaxf(0.0f, a - r);
 }
 
-// The decode step's tail: block 0 (its first wave) the score of the token, as score_tail_kernel at
-// T = 1; blocks 1.. the EMA state, e = f on the first token, else 0.985 e + 0.015 f (the update of
-// ema_habituate_kernel at T = 1), after the fc1 launch has read the state.
-__global__ __launch_bounds__(256) void score_step_tail_kernel(const float *__restrict__ h, int64_t ldh,
-                                                               const float *__restrict__ w2,
-                                                               const float *__restrict__ b2, int64_t hidden,
-                                                               int first, float *__restrict__ out,
-                                                               const int32_t *__restrict__ out_index,
-                                                               const float *__restrict__ f, float *__restrict__ ema,
-                                                               int64_t fd) {
-    if (blockIdx.x == 0) {
-        if (threadIdx.x >= 64) return;
-        if (out_index) out += *out_index;
-        float r = 0.0f, s = 0.0f;
-        for (int64_t i = threadIdx.x; i < hidden; i += 64) {
-            const float x0 = h[i], x1 = h[ldh + i];
-            r = fmaf(ref_geluf(x0), w2[i], r);
-            s = fmaf(ref_geluf(x1), w2[i], s);
-        }
-        r = wave_sum(r) + b2[0];
-        s = wave_sum(s) + b2[0];
-        if (threadIdx.x == 0) out[0] = first ? r : r + 0.35f * fmaxf(0.0f, s - r);
-        return;
-    }
-    const int64_t i = (int64_t)(blockIdx.x - 1) * 256 + threadIdx.x;
-    if (i >= fd) return;
-    const float fv = f[i];
-    ema[i] = first ? fv : ema_step(ema[i], fv);
-}
-
 }  // namespace
 
 extern "C" {
@@ -208,32 +178,17 @@ int vgx_layernorm(const float *x, int64_t ldx, const float *w, const float *b, f
 int vgx_seg_score_step(const float *feat, int64_t fd, float *ema, int first, const void *w1, int64_t hidden,
                        const float *b1, const float *ln_w, const float *ln_b, float eps, const float *w2,
                        const float *b2, float *h, float *out, const int32_t *out_index, void *stream) {
-    if (!feat || !ema || !w1 || !b1 || !ln_w || !ln_b || !w2 || !b2 || !h || !out) return VGX_E_ARG;
-    if (fd <= 0 || hidden <= 0 || fd % QK || !(eps > 0.0f)) return VGX_E_SIZE;
-    GemvArgs a{};
-    a.w = static_cast<const uint8_t *>(w1);
-    a.nblk = (int)(fd / QK);
-    a.n_rq = (hidden + 3) / 4;
-    a.rows_out = hidden;
-    a.x = feat;
-    a.ldx = fd;
-    a.batch = 2;
-    a.lnw = ln_w;
-    a.eps = eps;
-    a.bias = b1;
-    a.y = h;
-    a.ldy = hidden;
-    a.epi = EPI_STORE;
-    a.sc_ema = ema;
-    a.sc_lnb = ln_b;
-    a.sc_first = first ? 1 : 0;
-    hipStream_t st = (hipStream_t)stream;
-    const int rc = vgx_detail_qgemv_f32(a, st);
+    const vgx_score_side c{1, feat, fd, ema, first, w1, hidden, b1, ln_w, ln_b, eps, w2, b2, h, out, out_index};
+    ScoreSide s1, s2;
+    int rc = make_score_side(c, s1);
     if (rc != VGX_OK) return rc;
-    hipLaunchKernelGGL(score_step_tail_kernel, dim3((unsigned)(1 + (fd + 255) / 256)), dim3(256), 0, st, h, hidden, w2,
-                       b2, hidden, first ? 1 : 0, out, out_index, feat, ema, fd);
-    VGX_CHECK_LAUNCH();
-    return VGX_OK;
+    vgx_score_side c2 = c;
+    c2.phase = 2;
+    rc = make_score_side(c2, s2);
+    if (rc != VGX_OK) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    rc = vgx_detail_score_side(s1, st);
+    return rc != VGX_OK ? rc : vgx_detail_score_side(s2, st);
 }
 
 int vgx_seg_score_tail(const float *h, int64_t ldh, const float *w2, const float *b2, int64_t hidden, int64_t T,

@@ -720,6 +720,9 @@ class VAULTv3ForCausalLM:
         fused = B == 1 and all(lw.wq_rope is not None for lw in w.layers)
         batch_fused = not fused and self._batch_qkv_fusable(B)
         qbuf = torch.empty(B, H, D, dtype=torch.float32, device=self.device) if fused or batch_fused else None
+        # the scorer rides in the down projections of the two layers after its last feature layer (their
+        # launches leave CUs free), instead of launches of its own after the layers
+        sides, h_sc = self._score_sides(st, feats, ema_first, step) if seg_active and fused else ({}, None)
         for li, lw in enumerate(w.layers):
             xc = None
             if seg_active and li in cfg.seg_layers:
@@ -758,8 +761,11 @@ class VAULTv3ForCausalLM:
             ops.attn_decode(q, spans, out=ao, bias=bias, bias_span=bspan, scale=scale, ws=self.ws)
             ops.qlinear(lw.wo, ao.view(B, HD), out=x, accumulate=True)
             ops.qlinear_swiglu(lw.wgu, x, out=hbuf, norm=(lw.ln2, cfg.rms_eps))
-            ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
-        if seg_active:
+            if li in sides:
+                ops.qlinear_side(lw.wd, hbuf, x, True, sides[li])
+            else:
+                ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
+        if seg_active and not sides:
             self._score(st, feats, T=1, c0=0, first=ema_first, out_index=step[ops.L.STEP_SLOT:ops.L.STEP_SLOT + 1])
         if indirect:
             ops.qlinear_indirect(self.w.embed, x, io.out_ref, norm=(self.w.norm, cfg.rms_eps))
@@ -845,6 +851,23 @@ class VAULTv3ForCausalLM:
             ops.qlinear_swiglu(lw.wgu, x, out=hbuf, norm=(lw.ln2, cfg.rms_eps))
             ops.qlinear(lw.wd, hbuf, out=x, accumulate=True)
         return x, feats
+
+    def _score_sides(self, st: VAULTv3State, feats: torch.Tensor, first: bool, step: torch.Tensor):
+        """The decode token's scorer as the two jobs of ops.score_side, keyed by the layer whose down
+        projection carries each (the two layers after the last feature layer; none when the model has
+        no such layers or the scorer does not fit the jobs), and the fc1 output buffer they share (held
+        by the caller until both are launched)."""
+        cfg, sw = self.cfg, self.w.scorer
+        l1 = max(cfg.seg_layers) + 1
+        fd = feats.shape[1]
+        if l1 + 1 >= len(self.w.layers) or fd > 5120 or sw.w1.dtype != ops.L.F32 or \
+                not all(t.data_ptr() % 16 == 0 for t in (feats, st.seg_feat_ema, sw.ln_w, sw.ln_b)):
+            return {}, None
+        h = torch.empty(2, sw.w1.rows, dtype=torch.float32, device=self.device)
+        idx = step[ops.L.STEP_SLOT:ops.L.STEP_SLOT + 1]
+        args = (feats[0], st.seg_feat_ema, first, sw.w1, sw.b1, sw.ln_w, sw.ln_b, 1e-5, sw.w2, sw.b2, h,
+                st.sc_cur[0:1], idx)
+        return {l1: ops.score_side(1, *args), l1 + 1: ops.score_side(2, *args)}, h
 
     def _score(self, st: VAULTv3State, rows: torch.Tensor, T: int, c0: int, first: bool,
                out_index: Optional[torch.Tensor] = None) -> None:

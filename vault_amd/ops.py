@@ -5,6 +5,7 @@ into the HIP library (no torch fallback).  Tensors must live on a ROCm device.
 """
 from __future__ import annotations
 
+import ctypes as C
 from typing import Optional, Tuple
 
 import numpy as np
@@ -217,6 +218,33 @@ def qlinear(w: QWeight, x: torch.Tensor, bias: Optional[torch.Tensor] = None, ou
     if w.gateup:
         raise ValueError("use qlinear_swiglu for gate/up tensors")
     return _gemv(w, x, out, L.EPI_ACCUM if accumulate else L.EPI_STORE, bias, norm)
+
+
+def score_side(phase: int, feat: torch.Tensor, ema: torch.Tensor, first: bool, w1: QWeight, b1: torch.Tensor,
+               ln_w: torch.Tensor, ln_b: torch.Tensor, eps: float, w2: torch.Tensor, b2: torch.Tensor, h: torch.Tensor,
+               out: torch.Tensor, out_index: Optional[torch.Tensor] = None) -> "L.ScoreSide":
+    """One half of seg_score_step as a job for qlinear_side (phase 1: fc1 into h; phase 2: the score and
+    the EMA update).  The tensors must outlive the launches."""
+    if w1.dtype != L.F32 or w1.cols != feat.numel():
+        raise ValueError("the scorer job needs the F32 fc1 weight of the features' width")
+    return L.ScoreSide(phase, feat.data_ptr(), feat.numel(), ema.data_ptr(), 1 if first else 0, w1.packed.data_ptr(),
+                       w1.rows, b1.data_ptr(), ln_w.data_ptr(), ln_b.data_ptr(), float(eps), w2.data_ptr(),
+                       b2.data_ptr(), h.data_ptr(), out.data_ptr(), _ptr(out_index))
+
+
+def qlinear_side(w: QWeight, x: torch.Tensor, out: torch.Tensor, accumulate: bool, side: "L.ScoreSide") -> torch.Tensor:
+    """qlinear on a few rows (below GEMM_MIN_ROWS) with a scorer job riding in the same launch when the
+    GEMV leaves workgroups free for it (else launched after it)."""
+    _need(x, torch.float32, "x")
+    B = x.reshape(-1, w.cols).shape[0]
+    if w.gateup or B >= GEMM_MIN_ROWS or x.stride(-1) != 1 or out.stride(-1) != 1:
+        raise ValueError("qlinear_side takes a plain projection of a few contiguous rows")
+    x2, y2 = x.reshape(B, w.cols), out.view(B, w.rows)
+    L.check(L.load().vgx_qlinear_side(w.dtype, w.packed.data_ptr(), w.rows, w.cols, x2.data_ptr(), x2.stride(0), B,
+                                      None, 0.0, None, y2.data_ptr(), y2.stride(0),
+                                      L.EPI_ACCUM if accumulate else L.EPI_STORE, C.byref(side), _stream(x.device)),
+            "vgx_qlinear_side")
+    return out
 
 
 def qlinear_swiglu(w: QWeight, x: torch.Tensor, out: Optional[torch.Tensor] = None,
