@@ -22,13 +22,14 @@ constexpr int kEvictMaxItems = 4096;     // bank capacity + W candidates held in
 
 // The segmenter's step for the single sequence's token id at ring slot c: its segment id, then the
 // break rule by the token's tier.
-__device__ void segment_token(int64_t id, int c, int32_t *__restrict__ seg_cur, int32_t *__restrict__ ctrl,
-                              const uint8_t *__restrict__ tiers, int64_t vocab, int seg_min, int seg_max, int W) {
+// cur / len0: the segmenter's words (ctrl[VGX_SEG_CUR_ID], ctrl[VGX_SEG_LEN]) as read before the call.
+__device__ void segment_token(int64_t id, int c, int32_t *__restrict__ seg_cur, int32_t *__restrict__ ctrl, int cur,
+                              int len0, const uint8_t *__restrict__ tiers, int64_t vocab, int seg_min, int seg_max,
+                              int W) {
     const int tr = (tiers != nullptr && id >= 0 && id < vocab) ? (int)tiers[id] : 0;
     const int t2 = max(seg_min, (seg_max * 2) / 3);
     const int t3 = max(seg_min, seg_max > 8 ? seg_max - 8 : seg_min);
-    const int cur = ctrl[VGX_SEG_CUR_ID];
-    const int len = ctrl[VGX_SEG_LEN] + 1;
+    const int len = len0 + 1;
     seg_cur[c] = cur;
     const bool brk = (tr == 1 && len >= seg_min) || (tr == 2 && len >= t2) || (tr == 3 && len >= t3);
     if (c == W - 1 || brk || len >= seg_max) {
@@ -48,7 +49,8 @@ __global__ void seg_step_kernel(const int64_t *__restrict__ ids, int B, const in
     const int c = step[VGX_STEP_SLOT];
     const int b = threadIdx.x + blockIdx.x * blockDim.x;
     if (b < B) tok_cur[b * ldt + c] = (int32_t)ids[b];
-    if (seg_cur != nullptr && b == 0) segment_token(ids[0], c, seg_cur, ctrl, tiers, vocab, seg_min, seg_max, W);
+    if (seg_cur != nullptr && b == 0)
+        segment_token(ids[0], c, seg_cur, ctrl, ctrl[VGX_SEG_CUR_ID], ctrl[VGX_SEG_LEN], tiers, vocab, seg_min, seg_max, W);
 }
 
 // Loads of the pinned host ring at system scope: they reach the host's latest writes through no
@@ -59,6 +61,7 @@ __device__ __forceinline__ T sys_load(const void *p) {
 }
 
 constexpr int kBeginThreads = 256;
+constexpr int kBeginSpecSlots = 16;        // rings of up to this many slots: every slot's words read at once
 constexpr int kBeginBiasUnroll = 4;        // bias entries per thread whose host loads are in flight together
 
 struct StepBeginArgs {
@@ -84,19 +87,52 @@ struct StepBeginArgs {
 // issued before any is used, so the step pays one host round trip; device ids are one more (device)
 // load.  The counter advances after every thread has read it.
 __global__ __launch_bounds__(kBeginThreads) void step_begin_kernel(StepBeginArgs a) {
+    // The counter, the words and ids of every slot (rings of up to kBeginSpecSlots slots with
+    // B * n_slots <= kBeginThreads ids) and the segmenter's words are requested together: one host
+    // round trip, then the counter picks the slot.  Larger rings read the picked slot afterwards.
+    __shared__ int64_t s_hdr[kBeginSpecSlots][4];
+    __shared__ int64_t s_id[kBeginThreads];
+    __shared__ int32_t s_flags[kBeginSpecSlots];
     __shared__ int s_k;
     const int tid = threadIdx.x;
+    const bool spec = a.n_slots <= kBeginSpecSlots;
+    const bool spec_ids = spec && a.B * a.n_slots <= kBeginThreads;
     if (tid == 0) s_k = *a.counter;
+    int seg_cur_id = 0, seg_len = 0;
+    if (tid == 0 && a.seg_cur != nullptr) {
+        seg_cur_id = a.ctrl[VGX_SEG_CUR_ID];
+        seg_len = a.ctrl[VGX_SEG_LEN];
+    }
+    if (spec && tid < a.n_slots) {
+        const uint8_t *sl = a.ring + (int64_t)tid * a.slot_bytes;
+        s_hdr[tid][0] = sys_load<int64_t>(sl + VGX_SLOT_STEP);
+        s_hdr[tid][1] = sys_load<int64_t>(sl + VGX_SLOT_STEP + 8);
+        s_hdr[tid][2] = sys_load<int64_t>(sl + VGX_SLOT_IDS_ADDR);
+        s_hdr[tid][3] = sys_load<int64_t>(sl + VGX_SLOT_OUT_ADDR);
+        s_flags[tid] = sys_load<int32_t>(sl + VGX_SLOT_FLAGS);
+    }
+    if (spec_ids && tid < a.B * a.n_slots)
+        s_id[tid] = sys_load<int64_t>(a.ring + (int64_t)(tid / a.B) * a.slot_bytes + VGX_SLOT_IDS + 8 * (tid % a.B));
     __syncthreads();
     const uint32_t k = (uint32_t)s_k % (uint32_t)a.n_slots;   // in range whatever the word holds
     const uint8_t *slot = a.ring + (int64_t)k * a.slot_bytes;
-    const int64_t h0 = sys_load<int64_t>(slot + VGX_SLOT_STEP);
-    const int64_t h1 = sys_load<int64_t>(slot + VGX_SLOT_STEP + 8);
-    const int32_t flags = sys_load<int32_t>(slot + VGX_SLOT_FLAGS);
-    const int64_t ids_addr = sys_load<int64_t>(slot + VGX_SLOT_IDS_ADDR);
-    const int64_t out_addr = sys_load<int64_t>(slot + VGX_SLOT_OUT_ADDR);
+    int64_t h0, h1, ids_addr, out_addr;
+    int32_t flags;
+    if (spec) {
+        h0 = s_hdr[k][0];
+        h1 = s_hdr[k][1];
+        ids_addr = s_hdr[k][2];
+        out_addr = s_hdr[k][3];
+        flags = s_flags[k];
+    } else {
+        h0 = sys_load<int64_t>(slot + VGX_SLOT_STEP);
+        h1 = sys_load<int64_t>(slot + VGX_SLOT_STEP + 8);
+        flags = sys_load<int32_t>(slot + VGX_SLOT_FLAGS);
+        ids_addr = sys_load<int64_t>(slot + VGX_SLOT_IDS_ADDR);
+        out_addr = sys_load<int64_t>(slot + VGX_SLOT_OUT_ADDR);
+    }
     int64_t hid = 0;
-    if (tid < a.B) hid = sys_load<int64_t>(slot + VGX_SLOT_IDS + 8 * tid);
+    if (tid < a.B) hid = spec_ids ? s_id[(int)k * a.B + tid] : sys_load<int64_t>(slot + VGX_SLOT_IDS + 8 * tid);
     const bool bias = a.bias_early != nullptr;
     int8_t rows[2] = {-1, -1};
     if (bias && tid < a.H) {
@@ -114,7 +150,7 @@ __global__ __launch_bounds__(kBeginThreads) void step_begin_kernel(StepBeginArgs
         a.ids[b] = id;
         a.tok_cur[b * a.ldt + c] = (int32_t)id;
         if (a.seg_cur != nullptr && b == 0)
-            segment_token(id, c, a.seg_cur, a.ctrl, a.tiers, a.vocab, a.seg_min, a.seg_max, a.W);
+            segment_token(id, c, a.seg_cur, a.ctrl, seg_cur_id, seg_len, a.tiers, a.vocab, a.seg_min, a.seg_max, a.W);
     }
     if (bias && (flags & VGX_SLOTF_BIAS)) {
         __shared__ int8_t s_rows[2][256];
