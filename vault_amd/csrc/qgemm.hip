@@ -436,8 +436,20 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
     const int l16 = lane & 15, lg = lane >> 4;
     const int wm = wave & 1, wn = wave >> 1;
     const int cols = nblk * QK;
-    const int64_t rq0 = (int64_t)blockIdx.x * (kTM / 4);
-    const int64_t b0 = (int64_t)blockIdx.y * kTN;
+    // XCD-aware tile order: workgroups go to the 8 XCDs round robin (linear id mod 8); each XCD takes a
+    // contiguous run of the activation-tile-major tile sequence, so that it reads few activation tiles
+    // (kept in its L2) and streams the weights, instead of every XCD reading every activation tile.
+    int tr = blockIdx.x, tt = blockIdx.y;
+    {
+        const int64_t G = gridDim.x, total = G * gridDim.y, id = blockIdx.x + G * blockIdx.y;
+        if (total % 8 == 0) {
+            const int64_t s = (id % 8) * (total / 8) + id / 8;
+            tt = (int)(s / G);
+            tr = (int)(s - (int64_t)tt * G);
+        }
+    }
+    const int64_t rq0 = (int64_t)tr * (kTM / 4);
+    const int64_t b0 = (int64_t)tt * kTN;
     const int blk_lo = SPLIT ? (int)blockIdx.z * kper : 0;
     const int blk_hi = SPLIT ? min(nblk, blk_lo + kper) : nblk;
 
