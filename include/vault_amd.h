@@ -269,6 +269,15 @@ typedef struct {
 int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H,
                      int64_t G, int64_t D, float scale, void *stream);
 
+/* vgx_attn_prefill with a workspace (16-byte aligned, at least vgx_attn_prefill_workspace_bytes(H, G)
+ * bytes): a launch of few query tiles (a chunk of the chunk-recurrent prefill) splits each tile's keys
+ * into up to four ranges computed in parallel and combines them (a second launch); results within
+ * the same bars, not bit-equal to the unsplit call (the sums run in another order).  No counterpart in
+ * the reference: the same computation as vgx_attn_prefill. */
+int64_t vgx_attn_prefill_workspace_bytes(int64_t H, int64_t G);
+int vgx_attn_prefill_ws(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H,
+                        int64_t G, int64_t D, float scale, void *workspace, int64_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------- small fused ops -------------- */
 
 /* RMSNorm rows: y[r, :] = w * (x[r, :] / sqrt(mean(x[r, :]^2) + eps)).

@@ -268,3 +268,56 @@ def test_prefill_launch_shapes_agree(dev, kvdt, qdt):
         ref = oatt.chunk(_f64(b["q"]), [(_f64(pk), _f64(pv)), (_f64(sk), _f64(sv))], _f64(kc), _f64(vc),
                          bias=refs[i], bias_span=1 if refs[i] is not None else -1)
         assert np.abs(wide[i]["out"].double().cpu().numpy() - ref).max() <= bar
+
+
+@pytest.mark.parametrize("kvdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,lens", [(1024, (512, 1024, 1024)), (300, (40, 77, 200)), (33, (0, 0, 64)), (1, (5, 0, 0))])
+def test_prefill_key_splits_match_oracle(dev, kvdt, T, lens):
+    """With a workspace, a launch of few query tiles splits each tile's keys into 2-4 ranges and merges
+    them (vgx_attn_prefill_ws): the float64 oracle's bar, fp32 and bf16 queries, a resonance bias on the
+    segment run, and agreement with the unsplit call within the same bar; a workspace below
+    vgx_attn_prefill_workspace_bytes is refused."""
+    rng = np.random.default_rng(T * 3 + sum(lens) + (kvdt == torch.float32))
+    H, G, D = 12, 2, 128
+    cast = (lambda a: _bf(a)) if kvdt == torch.bfloat16 else (lambda a: torch.as_tensor(a, dtype=torch.float32))
+    runs = [(cast(rng.standard_normal((G, n, D))).to(dev), cast(rng.standard_normal((G, n, D))).to(dev))
+            for n in lens if n > 0]
+    kc = cast(rng.standard_normal((G, T, D))).to(dev)
+    vc = cast(rng.standard_normal((G, T, D))).to(dev)
+    bar = TOL if kvdt == torch.bfloat16 else TOL32
+    ws = ops.Workspace(dev)
+    for qdt in (torch.float32, torch.bfloat16):
+        q = torch.from_numpy(rng.standard_normal((T, H, D)).astype(np.float32)).to(dev).to(qdt)
+        blk = {"q": q, "runs": runs + [(kc, vc)], "causal_base": 0}
+        dense, seg = None, 0
+        if len(runs) >= 2:
+            seg, n_seg = 1, runs[1][0].shape[1]
+            rows = [-1, 0, 1, 0, 1, -1] * 2
+            bias = (rng.standard_normal((T, 2, n_seg)) * 3).astype(np.float32)
+            blk.update(bias=torch.from_numpy(bias).to(dev), bias_head_row=rows, bias_run=1)
+            dense = np.zeros((T, H, n_seg))
+            for h, r in enumerate(rows):
+                if r >= 0:
+                    dense[:, h] = bias[:, r]
+        split = dict(blk, out=torch.empty(T, H, D, device=dev))
+        whole = dict(blk, out=torch.empty(T, H, D, device=dev))
+        ops.attn_prefill([split], H, G, ws=ws)
+        ops.attn_prefill([whole], H, G)
+        ref = oatt.chunk(_f64(q), [(_f64(k), _f64(v)) for k, v in runs], _f64(kc), _f64(vc), bias=dense,
+                         bias_span=seg if dense is not None else -1)
+        got = split["out"].double().cpu().numpy()
+        assert np.abs(got - ref).max() <= bar
+        assert np.abs(got - whole["out"].double().cpu().numpy()).max() <= bar
+    from vault_amd import _lib as L
+    lib = L.load()
+    need = int(lib.vgx_attn_prefill_workspace_bytes(H, G))
+    assert need > 0
+    arr = (L.AttnBlock * 1)()
+    ra = (L.KVRun * 4)()
+    ra[0] = L.KVRun(kc.data_ptr(), vc.data_ptr(), T, kc.stride(1), kc.stride(0))
+    out = torch.empty(T, H, D, device=dev)
+    q = torch.zeros(T, H, D, device=dev)
+    arr[0] = L.AttnBlock(q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), out.stride(0), out.stride(1), T, 0, 1, ra)
+    small = torch.empty(need - 256, dtype=torch.uint8, device=dev)
+    kd = L.BF16 if kvdt == torch.bfloat16 else L.F32
+    assert lib.vgx_attn_prefill_ws(kd, L.F32, L.F32, arr, 1, H, G, D, 0.088, small.data_ptr(), small.numel(), None) == -8

@@ -85,6 +85,8 @@ _SIGS = {
     "vgx_gov_commit": (I32, [P, U32]),
     "vgx_attn_decode_noalloc": (I32, [I32, P, I64, P, I32, P, I64, I32, I64, P, I64, I64, I64, I64, F, P]),
     "vgx_attn_prefill": (I32, [I32, I32, I32, P, I32, I64, I64, I64, F, P]),
+    "vgx_attn_prefill_workspace_bytes": (I64, [I64, I64]),
+    "vgx_attn_prefill_ws": (I32, [I32, I32, I32, P, I32, I64, I64, I64, F, P, I64, P]),
     "vgx_rmsnorm": (I32, [P, I64, P, P, I64, I64, I64, F, P]),
     "vgx_rope_qkv_write": (I32, [I32, P, I64, P, I64, P, I64, I64, I64, I64, I64, P, I64, P, P, P, I64, I64, P, P, I64,
                                  I64, I64, P]),

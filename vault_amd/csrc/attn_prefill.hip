@@ -112,7 +112,13 @@ struct PrefillArgs {
     float scale_log2;  // scale * log2(e)
     int q_bf16;
     int o_bf16;        // output rounded to bf16 (round to nearest even) instead of fp32
+    int n_split;       // key ranges per query tile (> 1: partials into ws, then attn_prefill_merge_kernel)
+    float *ws;         // n_tiles * n_split slots of prefill_slot_floats
 };
+
+// Floats of one (query tile, key range) partial: O (unnormalised, the MFMA lane layout) and per query
+// the running max and sum.
+__host__ __device__ constexpr int prefill_slot_floats(int waves, int nqt) { return waves * nqt * (8 * 256 + 32); }
 
 template <int GRP, bool QSPLIT, int NQT, bool KF, int QW, bool DMA>
 __global__ __launch_bounds__(64 * GRP * QW) void attn_prefill_kernel(PrefillArgs a) {
@@ -129,10 +135,12 @@ __global__ __launch_bounds__(64 * GRP * QW) void attn_prefill_kernel(PrefillArgs
     __shared__ __align__(16) uint16_t ks[DMA ? 2 * 2 * KT * kD : NP * KT * kKRow];   // DMA: [stage][K, V][key][dim]
     __shared__ __align__(16) uint16_t vt[DMA ? 8 : NP * kD * VROW];
 
-    // XCD-aware order: consecutive tiles (same block and group, neighbouring queries, same keys)
-    // on the same XCD so that its L2 serves their shared K/V.
-    int tile = blockIdx.x;
-    if ((a.n_tiles & 7) == 0) tile = (blockIdx.x & 7) * (a.n_tiles >> 3) + (blockIdx.x >> 3);
+    // XCD-aware order: consecutive tiles (same block and group, neighbouring queries, same keys; the
+    // key ranges of one tile next to each other) on the same XCD so that its L2 serves their K/V.
+    const int n_work = a.n_tiles * a.n_split;
+    int work = blockIdx.x;
+    if ((n_work & 7) == 0) work = (blockIdx.x & 7) * (n_work >> 3) + (blockIdx.x >> 3);
+    const int tile = work / a.n_split, part = work - tile * a.n_split;
     int bi = 0;
 #pragma unroll
     for (int i = 1; i < kMaxBlocks; ++i)
@@ -316,9 +324,27 @@ __global__ __launch_bounds__(64 * GRP * QW) void attn_prefill_kernel(PrefillArgs
         const int hr = B.bias_head_row[h];
         if (hr >= 0) brow = B.bias + (int64_t)hr * B.bias_rstride;
     }
+    // this workgroup's key range: part of the tile sequence over the runs (all of it without splits)
+    int n_kt = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) n_kt += rlen[i] > 0 ? (int)((rlen[i] + KT - 1) / KT) : 0;
+    const int per = (n_kt + a.n_split - 1) / a.n_split;
+    int skip = part * per;
+    int todo = max(0, min(n_kt, skip + per) - skip);
     int r = 0;
     while (r < n_runs && run_len(r) <= 0) ++r;
     int64_t j0 = 0;
+    while (skip > 0 && r < n_runs) {
+        const int nt = (int)((run_len(r) + KT - 1) / KT);
+        if (skip < nt) {
+            j0 = (int64_t)skip * KT;
+            skip = 0;
+        } else {
+            skip -= nt;
+            do { ++r; } while (r < n_runs && run_len(r) <= 0);
+        }
+    }
+    if (todo == 0) r = n_runs;
     int buf = 0;
     if constexpr (DMA) {
         if (r < n_runs) issue(r, j0, 0);
@@ -334,6 +360,7 @@ __global__ __launch_bounds__(64 * GRP * QW) void attn_prefill_kernel(PrefillArgs
             jn = 0;
             do { ++rn; } while (rn < n_runs && run_len(rn) <= 0);
         }
+        if (todo <= 1) rn = n_runs;             // the range ends with this tile
         if constexpr (DMA) {
             // this tile's loads landed (each wave waits for its own, the barrier for every wave's), and
             // every wave is done with the other stage: the next tile's loads go there
@@ -490,6 +517,24 @@ __global__ __launch_bounds__(64 * GRP * QW) void attn_prefill_kernel(PrefillArgs
         r = rn;
         j0 = jn;
         buf ^= 1;
+        --todo;
+    }
+
+    if (a.n_split > 1) {
+        // the partial of this key range: O as accumulated, and per query the max and sum
+        constexpr int NWV = GRP * QW;
+        float *slot = a.ws + (int64_t)work * prefill_slot_floats(NWV, NQT);
+        float *ml = slot + NWV * NQT * 8 * 256;
+#pragma unroll
+        for (int qt = 0; qt < NQT; ++qt) {
+            const float L = xor32_sum(xor16_sum(lsum[qt]));
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt)
+                *reinterpret_cast<float4 *>(slot + (((wave * NQT + qt) * 8 + dt) * 64 + lane) * 4) =
+                    make_float4(o[qt][dt][0], o[qt][dt][1], o[qt][dt][2], o[qt][dt][3]);
+            if (lg == 0) *reinterpret_cast<float2 *>(ml + ((wave * NQT + qt) * 16 + lq) * 2) = make_float2(m[qt], L);
+        }
+        return;
     }
 
 #pragma unroll
@@ -518,6 +563,74 @@ __global__ __launch_bounds__(64 * GRP * QW) void attn_prefill_kernel(PrefillArgs
     }
 }
 
+// The key ranges of each query tile combined: weights 2^(m_p - max m), O = sum w_p O_p / sum w_p L_p,
+// written as the unsplit kernel writes its output.  One workgroup per query tile, the lanes of the
+// attention kernel's layout.
+template <int GRP, int NQT, int QW>
+__global__ __launch_bounds__(64 * GRP * QW) void attn_prefill_merge_kernel(PrefillArgs a) {
+    constexpr int kQTile = 16 * NQT * QW, NWV = GRP * QW;
+    const int tile = blockIdx.x;
+    int bi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxBlocks; ++i)
+        if (i < a.n_blocks && a.blk[i].tile0 <= tile) bi = i;
+    const BlockArgs &B = a.blk[bi];
+    const int local = tile - B.tile0;
+    const int g = local % a.G;
+    const int64_t t0 = (int64_t)(local / a.G) * kQTile;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int lq = lane & 15, lg = lane >> 4;
+    const int h = g * GRP + wave % GRP;
+    const int64_t tw = t0 + (int64_t)(wave / GRP) * 16 * NQT;
+    const int ns = a.n_split;
+    const float *slot0 = a.ws + (int64_t)tile * ns * prefill_slot_floats(NWV, NQT);
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+        const int64_t t = tw + qt * 16 + lq;
+        float mp[4], lp[4], M = kNegBig;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            mp[p] = kNegBig;
+            lp[p] = 0.0f;
+            if (p < ns) {
+                const float2 v = *reinterpret_cast<const float2 *>(slot0 + (int64_t)p * prefill_slot_floats(NWV, NQT) +
+                                                                   NWV * NQT * 8 * 256 + ((wave * NQT + qt) * 16 + lq) * 2);
+                mp[p] = v.x;
+                lp[p] = v.y;
+                M = fmaxf(M, v.x);
+            }
+        }
+        float w[4], L = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            w[p] = p < ns ? __builtin_amdgcn_exp2f(mp[p] - M) : 0.0f;
+            L += w[p] * lp[p];
+        }
+        const float inv = 1.0f / L;
+        if (t >= B.n_q) continue;
+        const int64_t oo = t * B.ldo + (int64_t)h * B.o_hstride;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                if (p >= ns) continue;
+                const float4 x = *reinterpret_cast<const float4 *>(slot0 + (int64_t)p * prefill_slot_floats(NWV, NQT) +
+                                                                   (((wave * NQT + qt) * 8 + dt) * 64 + lane) * 4);
+                v.x = fmaf(w[p], x.x, v.x); v.y = fmaf(w[p], x.y, v.y); v.z = fmaf(w[p], x.z, v.z); v.w = fmaf(w[p], x.w, v.w);
+            }
+            if (a.o_bf16) {
+                uint16_t *op = static_cast<uint16_t *>(B.out) + oo;
+                *reinterpret_cast<uint2 *>(op + dt * 16 + lg * 4) =
+                    make_uint2(pack_bf16x2(v.x * inv, v.y * inv), pack_bf16x2(v.z * inv, v.w * inv));
+            } else {
+                float *op = static_cast<float *>(B.out) + oo;
+                *reinterpret_cast<float4 *>(op + dt * 16 + lg * 4) = make_float4(v.x * inv, v.y * inv, v.z * inv, v.w * inv);
+            }
+        }
+    }
+}
+
 // Launch shape per K / V dtype and heads per group: NQT 16-query tiles per wave, QW waves per head, LDS
 // DMA staging.  At 4 and 6 heads per group a workgroup of 2 GRP waves of 16 queries (at most 168
 // registers, three waves per SIMD: one workgroup of 12 waves per CU at 6 heads) keeps more waves in
@@ -536,12 +649,18 @@ constexpr int prefill_qw(int grp, bool kf, bool narrow) {
 }
 constexpr bool prefill_dma(int grp, bool kf) { return !kf && grp >= 4; }
 
-}  // namespace
+// Key-range splits: with a workspace, a launch of fewer than kPrefillNarrowBelow workgroups (a
+// 1024-query chunk of the chunk-recurrent prefill at 2 KV heads: 128) splits each tile's keys into up to
+// four ranges, so that the launch fills the CUs; attn_prefill_merge_kernel then combines them.
+constexpr int kPrefillMaxSplit = 4;
+// Workspace bound: at most kPrefillNarrowBelow (tile, range) slots, each of at most 2 GRP waves x 2
+// 16-query tiles.
+inline int64_t prefill_ws_bytes(int grp) {
+    return (int64_t)kPrefillNarrowBelow * prefill_slot_floats(2 * grp, 2) * 4;
+}
 
-extern "C" {
-
-int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H,
-                     int64_t G, int64_t D, float scale, void *stream) {
+int attn_prefill_impl(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H,
+                      int64_t G, int64_t D, float scale, void *workspace, int64_t workspace_bytes, void *stream) {
     if (kv_dtype != VGX_BF16 && kv_dtype != VGX_F32) return VGX_E_DTYPE;
     if (out_dtype != VGX_F32 && out_dtype != VGX_BF16) return VGX_E_DTYPE;
     const int oel = out_dtype == VGX_BF16 ? 2 : 4;
@@ -622,12 +741,24 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_bl
     if (tiles > 0x7FFFFFFF) return VGX_E_LIMIT;
     a.n_blocks = nb;
     a.n_tiles = (int)tiles;
+    a.n_split = 1;
+    if (workspace != nullptr && tiles < kPrefillNarrowBelow) {
+        if (workspace_bytes < prefill_ws_bytes(grp)) return VGX_E_ARENA;
+        if ((uintptr_t)workspace % 16) return VGX_E_ALIGN;
+        a.n_split = (int)std::min<int64_t>(kPrefillMaxSplit, kPrefillNarrowBelow / tiles);
+        a.ws = static_cast<float *>(workspace);
+    }
     hipStream_t st = (hipStream_t)stream;
-    const dim3 grid((unsigned)tiles);
+    const dim3 grid((unsigned)(tiles * a.n_split));
 #define VGX_PREFILL_SHAPE(G_, S_, KF_, N_)                                                                   \
-    hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, prefill_nqt(G_, KF_), KF_, prefill_qw(G_, KF_, N_),        \
-                                            prefill_dma(G_, KF_)>),                                            \
-                       grid, dim3(64 * G_ * prefill_qw(G_, KF_, N_)), 0, st, a)
+    do {                                                                                                     \
+        hipLaunchKernelGGL((attn_prefill_kernel<G_, S_, prefill_nqt(G_, KF_), KF_, prefill_qw(G_, KF_, N_),    \
+                                                prefill_dma(G_, KF_)>),                                        \
+                           grid, dim3(64 * G_ * prefill_qw(G_, KF_, N_)), 0, st, a);                           \
+        if (a.n_split > 1)                                                                                   \
+            hipLaunchKernelGGL((attn_prefill_merge_kernel<G_, prefill_nqt(G_, KF_), prefill_qw(G_, KF_, N_)>),  \
+                               dim3((unsigned)tiles), dim3(64 * G_ * prefill_qw(G_, KF_, N_)), 0, st, a);      \
+    } while (0)
 #define VGX_PREFILL_GO(G_, S_)                                                                               \
     do {                                                                                                     \
         if (kf) {                                                                                            \
@@ -654,6 +785,28 @@ int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_bl
 #undef VGX_PREFILL_SHAPE
     VGX_CHECK_LAUNCH();
     return VGX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vgx_attn_prefill(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H,
+                     int64_t G, int64_t D, float scale, void *stream) {
+    return attn_prefill_impl(kv_dtype, q_dtype, out_dtype, blocks, n_blocks, H, G, D, scale, nullptr, 0, stream);
+}
+
+int64_t vgx_attn_prefill_workspace_bytes(int64_t H, int64_t G) {
+    if (H <= 0 || G <= 0 || H % G) return VGX_E_SIZE;
+    if (H / G > 8) return VGX_E_LIMIT;
+    return prefill_ws_bytes((int)(H / G));
+}
+
+int vgx_attn_prefill_ws(int kv_dtype, int q_dtype, int out_dtype, const vgx_attn_block *blocks, int n_blocks, int64_t H,
+                        int64_t G, int64_t D, float scale, void *workspace, int64_t workspace_bytes, void *stream) {
+    if (!workspace) return VGX_E_ARG;
+    return attn_prefill_impl(kv_dtype, q_dtype, out_dtype, blocks, n_blocks, H, G, D, scale, workspace, workspace_bytes,
+                             stream);
 }
 
 }  // extern "C"

@@ -330,6 +330,7 @@ class VAULTv3ForCausalLM:
         self.device = weights.device
         self.kv_dtype = kv_dtype
         self.ws = ops.Workspace(self.device)
+        self.ws_prefill = ops.Workspace(self.device)   # the chunk attention's key-range partials
         self.prefill_ws = ops.Workspace(self.device)
         self.tokens = weights.tokens
         vs = self.cfg.vocab_size
@@ -844,7 +845,7 @@ class VAULTv3ForCausalLM:
                 if bias is not None and lo <= li < hi:
                     blk.update(bias=bias[0] if li < mid else bias[1], bias_head_row=head_rows,
                                bias_run=1 if n_sk else 0)
-                ops.attn_prefill([blk], H, G, scale)
+                ops.attn_prefill([blk], H, G, scale, ws=self.ws_prefill)
             else:
                 ops.attn_decode(q, spans, out=ao, scale=scale, ws=self.ws, causal_base=0)
             ops.qlinear(lw.wo, ao.view(N, HD), out=x, accumulate=True)

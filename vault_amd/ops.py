@@ -540,7 +540,7 @@ def _head_rows(rows: tuple, device) -> torch.Tensor:
     return t
 
 
-def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
+def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None, ws: Optional["Workspace"] = None) -> None:
     """MFMA prefill attention for up to 8 query blocks per launch (more are split).
 
     Each block is a dict: ``q`` [n_q, H, D] view (fp32 or bf16, any token / head stride, D contiguous),
@@ -549,7 +549,8 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
     any row and group stride), ``causal_base``: -1, or b >= 0 making the last run causal (query t sees
     its keys j <= b + t).  Optional ``bias`` fp32 [n_q, R, >= run length] with ``bias_head_row`` (H
     ints: the bias row of head h, < 0: none) and ``bias_run``: query t of head h adds
-    bias[t, bias_head_row[h], j] to its score with key j of that run."""
+    bias[t, bias_head_row[h], j] to its score with key j of that run.  With ``ws`` (a Workspace) a launch
+    of few query tiles splits its keys over more workgroups (vgx_attn_prefill_ws)."""
     lib = L.load()
     if not blocks:
         return
@@ -598,9 +599,16 @@ def attn_prefill(blocks, H: int, G: int, scale: Optional[float] = None) -> None:
                 keep.append((bias, rows_dev))
         qd = L.BF16 if qdt == torch.bfloat16 else L.F32
         od = L.BF16 if odt == torch.bfloat16 else L.F32
-        L.check(lib.vgx_attn_prefill(KV_DTYPES[kvdt], qd, od, arr, len(part), H, G, D, scale,
-                                     _stream(part[0]["q"].device)),
-                "vgx_attn_prefill")
+        if ws is not None:
+            need = int(lib.vgx_attn_prefill_workspace_bytes(H, G))
+            L.check(0 if need > 0 else need, "vgx_attn_prefill_workspace_bytes")
+            buf = ws.get(need)
+            L.check(lib.vgx_attn_prefill_ws(KV_DTYPES[kvdt], qd, od, arr, len(part), H, G, D, scale, buf.data_ptr(),
+                                            buf.numel(), _stream(part[0]["q"].device)), "vgx_attn_prefill_ws")
+        else:
+            L.check(lib.vgx_attn_prefill(KV_DTYPES[kvdt], qd, od, arr, len(part), H, G, D, scale,
+                                         _stream(part[0]["q"].device)),
+                    "vgx_attn_prefill")
 
 
 # ------------------------------------------------------------------------------------------
