@@ -52,6 +52,35 @@ def test_seg_evict_matches_restatement(dev, W, M, budget, levels, t0, quar):
         assert (idx_old[K:] == -1).all() and (idx_new[K:] == -1).all()
 
 
+@pytest.mark.parametrize("budget", [40, 31])
+def test_seg_evict_nan_and_signed_zero_scores(dev, budget):
+    """Bank scores that are NaN, +0 and -0 among ties: the ranking puts NaN last and -0 level with +0
+    (index order breaks the tie), as the restatement's lexsort does, and keeps exactly `budget` winners."""
+    rng = np.random.default_rng(budget)
+    W, M = 64, 30
+    sc, seg, tok, mem_pos, mem_score, mem_tok, mem_seg = _case(rng, W, M, 4, False)
+    mem_score = np.asarray(mem_score, np.float32).copy()
+    mem_score[[2, 7, 19]] = np.nan
+    mem_score[[3, 11]] = 0.0
+    mem_score[[5, 23]] = -0.0
+    cap = max(budget, M)
+    bank = [torch.zeros(cap, dtype=t, device=dev) for t in (torch.int64, torch.float32, torch.int32, torch.int32)]
+    for b, a in zip(bank, (mem_pos, mem_score, mem_tok, mem_seg)):
+        b[:M].copy_(torch.as_tensor(np.asarray(a)).to(b.dtype))
+    ctrl = torch.tensor([M, 100, 0, 0], dtype=torch.int32, device=dev)
+    idx_old = torch.zeros(budget, dtype=torch.int32, device=dev)
+    idx_new = torch.zeros(budget, dtype=torch.int32, device=dev)
+    ops.seg_evict(_dev(sc, torch.float32, dev), _dev(seg, torch.int32, dev), _dev(tok, torch.int32, dev), *bank, ctrl,
+                  11, 0, budget, idx_old, idx_new)
+    _, off, (pos, score, toks, segs), io, inew = segbank.evict(sc, seg, tok, mem_pos, mem_score, mem_tok, mem_seg,
+                                                              100, 11, 0, budget)
+    K = len(pos)
+    assert K == budget and ctrl.tolist()[:2] == [K, off]
+    assert np.array_equal(bank[0][:K].cpu().numpy(), pos)
+    assert np.array_equal(bank[1][:K].cpu().numpy().view(np.uint32), score.view(np.uint32))
+    assert np.array_equal(idx_old[:K].cpu().numpy(), io) and np.array_equal(idx_new[:K].cpu().numpy(), inew)
+
+
 def test_seg_step_matches_host_rule(dev):
     cfg = modelgen.tiny_cfg(window=32, seg_min=3, seg_max=11)
     toks, bmap = modelgen.test_vocab(cfg)

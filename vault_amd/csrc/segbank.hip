@@ -239,7 +239,9 @@ __global__ __launch_bounds__(kEvictThreads) void seg_evict_kernel(
     __shared__ int32_t s_tok[kEvictMaxItems];
     __shared__ int32_t s_seg[kEvictMaxItems];
     __shared__ int32_t s_src[kEvictMaxItems];     // evicted-chunk row of a candidate
-    __shared__ int s_mx[kEvictMaxItems];          // per local segment: max score (ordered int), bad flag
+    __shared__ int s_mx[kEvictMaxItems];          // per local segment: max score (ordered int), bad flag;
+                                                  // then the winner flags
+    __shared__ uint64_t s_key[kEvictMaxItems];    // (score desc, index asc) sort keys
     __shared__ int sbuf[kEvictThreads / 64 + 1];
     __shared__ int s_any_bad, s_nloc;
     const int tid = threadIdx.x;
@@ -305,25 +307,49 @@ __global__ __launch_bounds__(kEvictThreads) void seg_evict_kernel(
     __syncthreads();
     const int tot = M + n_cand;
     const bool merge = t0 < W;
-    // winners: rank by (score desc, index asc) below the budget (all of them when they fit)
+    // winners: the first `budget` items in (score desc, index asc) order (all of them when they fit):
+    // a bitonic sort of 64-bit keys in LDS, the score's order-preserving bits inverted above the index
+    // (-0 counts as +0, NaN scores sort last), then a flag per winning item
     const int n_items = merge ? tot : M;
+    const bool rank = merge && tot > budget;
+    if (rank) {
+        int np = 1;
+        while (np < tot) np <<= 1;
+        for (int i = tid; i < np; i += kEvictThreads) {
+            uint64_t key = ~0ull;
+            if (i < tot) {
+                const float f = s_score[i] + 0.0f;
+                const uint32_t hi = f != f ? 0xFFFFFFFFu : (uint32_t)((int64_t)0x7FFFFFFF - (int64_t)f2ord(f));
+                key = ((uint64_t)hi << 32) | (uint32_t)i;
+            }
+            s_key[i] = key;
+        }
+        __syncthreads();
+        for (int k = 2; k <= np; k <<= 1) {
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                for (int i = tid; i < np; i += kEvictThreads) {
+                    const int l = i ^ j;
+                    if (l > i) {
+                        const uint64_t a = s_key[i], b = s_key[l];
+                        if (((i & k) == 0) == (a > b)) {
+                            s_key[i] = b;
+                            s_key[l] = a;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        for (int i = tid; i < tot; i += kEvictThreads) s_mx[i] = 0;
+        __syncthreads();
+        for (int p = tid; p < budget; p += kEvictThreads) s_mx[(int)(s_key[p] & 0xFFFFFFFFu)] = 1;
+        __syncthreads();
+    }
     int K = 0;
     for (int i0 = 0; i0 < kEvictMaxItems; i0 += kEvictThreads) {
         const int i = i0 + tid;
         int win = 0;
-        if (i < n_items) {
-            if (!merge || tot <= budget) {
-                win = 1;
-            } else {
-                const float s = s_score[i];
-                int rank = 0;
-                for (int j = 0; j < tot; ++j) {
-                    const float sj = s_score[j];
-                    rank += (sj > s) || (sj == s && j < i);
-                }
-                win = rank < budget;
-            }
-        }
+        if (i < n_items) win = rank ? s_mx[i] : 1;
         int total;
         const int slot = K + block_scan(win, sbuf, &total);
         if (win) {
