@@ -10,20 +10,24 @@
 // enter the MFMA as unsigned integers, exact in bf16: Q8_0 as q + 128 (byte ^ 0x80), Q4_0 as the
 // nibble n (16 + n in the tiled kernel).  The activations enter in pieces that a bf16 pair hi + lo
 // (2^-18 relative residual) would leave at 2.4e-6 relative error per output, ten times the one-row
-// GEMV's; so both kernels take hi = bf16(u) and lo16 = fp16(16 (u - hi)) (19 significant bits, 2^-20
-// relative residual; lo16 overflows only past |u| = 2^21), lo16 multiplied by the same weights divided
-// by 16 as exact fp16 values, the two products added into one accumulator (two MFMAs per block; three
-// bf16 pieces would take three and, in the decode-batch kernel, registers that its occupancy target
-// does not have: spills).  With S_b the per-block sum of the pieces, per block the fp32 MFMA result C
-// (= sum_j w_j u_j as pieces) is corrected and scaled:
-//   acc += d * (C - off * S_b),   off = 128 (Q8_0), 8 (Q4_0; 24 in the tiled kernel),
+// GEMV's; so the decode-batch kernels take hi = bf16(u) and lo16 = fp16(16 (u - hi)) (19 significant
+// bits, 2^-20 relative residual; lo16 overflows only past |u| = 2^21), lo16 multiplied by the same
+// weights divided by 16 as exact fp16 values, the two products added into one accumulator (two MFMAs
+// per block; three bf16 pieces would take three and, in the decode-batch kernel, registers that its
+// occupancy target does not have: spills).  The tiled kernels take two fp16 pieces of the row scaled
+// by a power of two 2^k (hi = fp16(2^k u), lo = fp16(2^k u - hi): about 22 significant bits, both
+// pieces in fp16's normal range for any row), both multiplied by one exact fp16 weight operand, and
+// scale their outputs by 2^-k.  With S_b the per-block sum of the pieces, per block the fp32 MFMA
+// result C (= sum_j w_j u_j as pieces) is corrected and scaled:
+//   acc += d * (C - off * S_b),   off = 128 (Q8_0), 8 (Q4_0; 24 in the tiled kernels),
 // which is the reference's sum_b d_b sum_j q_j x_j at fp32-level accuracy.  The decode-batch kernels
 // place the weights by byte permutes instead (Q4_0 bf16 128 + n / fp16 1024 + n against pieces of 16 u;
 // fp16 1024 + unsigned weight in qgemm_wide_kernel, whose pieces are both fp16 of a power-of-two-scaled
 // row) with the matching offsets; their comments give the arithmetic.
 //
-// Mapping.  Large batches (prefill chunks) run qgemm_tile_kernel (128 x 128 LDS tiles, below) after
-// the split pre-pass; decode batches of up to 64 rows run the K-split kernels (qgemm_kslice_kernel,
+// Mapping.  Large batches (prefill chunks) run qgemm_tile_dma_kernel (256 x 64 LDS tiles filled by
+// LDS DMA; qgemm_tile_kernel, 128 x 128 tiles staged through registers, where a weight or activation
+// block passes 2 GiB) after the split pre-pass; decode batches of up to 64 rows run the K-split kernels (qgemm_kslice_kernel,
 // qgemm_split_kernel, qkv_split_kernel), qgemm_wide_kernel for tall unsplit weights, or
 // qgemm_small_kernel, which converts its activations itself.  In every MFMA a lane of a 16-row tile
 // owns one weight row (l % 16) for the A
@@ -40,56 +44,100 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-// u = (norm ? lnw * x * inv_rms : x); writes bf16 hi and fp16 lo16 = 16 (u - hi) rows and per-block
-// sums of hi + lo16 / 16.
+// u = (norm ? lnw * x * inv_rms : x), scaled per row by a power of two 2^k that puts the largest |u|
+// in [2^14, 2^15), split into two fp16 planes hi = fp16(2^k u) and lo = fp16(2^k u - hi): together
+// about 22 significant bits of every element, with the scale keeping both pieces in fp16's normal
+// range whatever the row's magnitude.  Also the per-block sums of hi + lo (in fp32) and the row's 2^-k,
+// which the GEMM multiplies into its outputs (exactly: a power of two).  k stays within [-100, 126],
+// so 2^-k is a normal float; a row holding an infinity or a NaN is not scaled (k = 0), so that it
+// reaches the outputs as it would unsplit.
 // Inside every group of four, elements 1 and 2 trade places (stored order 0, 2, 1, 3): the K-slot
 // order of the tiled kernel's weight fragments, whose Q4_0 nibble pairs come out of a word that way.
 // One workgroup of 256 threads per activation row.
+constexpr int kXsplitRegs = 20;   // float4 per thread kept in registers: rows of up to 20480 elements
 __global__ __launch_bounds__(256) void xsplit_kernel(const float *__restrict__ x, int64_t ldx,
                                                       const float *__restrict__ lnw, float eps, int cols,
                                                       uint16_t *__restrict__ xh, uint16_t *__restrict__ xl,
-                                                      float *__restrict__ xsum) {
-    __shared__ float red[4];
+                                                      float *__restrict__ xsum, float *__restrict__ xscale) {
+    __shared__ float red[4], redm[4];
     const int64_t b = blockIdx.x;
     const float *xr = x + b * ldx;
-    float inv = 1.0f;
-    if (lnw) {
-        float s = 0.0f;
-        for (int i = threadIdx.x; i < cols; i += 256) s = fmaf(xr[i], xr[i], s);
-        s = wave_sum(s);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
-        __syncthreads();
-        inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)cols + eps);
-    }
-    const int nblk = cols / QK;
-    // a thread converts four consecutive elements (one 16-byte load, two 8-byte stores per plane);
-    // the eight threads of a block sum its hi + lo
     const int n4 = cols / 4;
     const float4 *x4 = reinterpret_cast<const float4 *>(xr);
     const float4 *g4 = reinterpret_cast<const float4 *>(lnw);
     const bool vec = ((uintptr_t)xr & 15) == 0 && (lnw == nullptr || ((uintptr_t)lnw & 15) == 0);
-    for (int i0 = 0; i0 < n4; i0 += 256) {
-        const int i = i0 + (int)threadIdx.x;
-        const bool ok = i < n4;
-        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (ok) {
-            if (vec) {
-                v = x4[i];
-            } else {
-                v.x = xr[4 * i]; v.y = xr[4 * i + 1]; v.z = xr[4 * i + 2]; v.w = xr[4 * i + 3];
-            }
-            if (lnw) {
-                float4 g;
-                if (vec) g = g4[i];
-                else { g.x = lnw[4 * i]; g.y = lnw[4 * i + 1]; g.z = lnw[4 * i + 2]; g.w = lnw[4 * i + 3]; }
-                v.x = g.x * (v.x * inv); v.y = g.y * (v.y * inv); v.z = g.z * (v.z * inv); v.w = g.w * (v.w * inv);
+    auto load_x = [&](int i) {
+        if (vec) return x4[i];
+        return make_float4(xr[4 * i], xr[4 * i + 1], xr[4 * i + 2], xr[4 * i + 3]);
+    };
+    auto load_g = [&](int i) {
+        if (vec) return g4[i];
+        return make_float4(lnw[4 * i], lnw[4 * i + 1], lnw[4 * i + 2], lnw[4 * i + 3]);
+    };
+    // one pass over the row (kept in registers when it fits): the sum of squares and max |lnw x| (the
+    // largest |u| is that max times 1 / rms, up to rounding, which the scale's headroom absorbs)
+    const bool keep = n4 <= 256 * kXsplitRegs;
+    float4 xv[kXsplitRegs];
+    float ss = 0.0f, mx = 0.0f;
+    bool finite = true;
+    auto scan = [&](float4 v, int i) {
+        ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+        if (lnw) {
+            const float4 g = load_g(i);
+            v.x *= g.x; v.y *= g.y; v.z *= g.z; v.w *= g.w;
+        }
+        finite = finite && __builtin_isfinite(v.x) && __builtin_isfinite(v.y) && __builtin_isfinite(v.z) &&
+                 __builtin_isfinite(v.w);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    };
+    if (keep) {
+#pragma unroll
+        for (int j = 0; j < kXsplitRegs; ++j) {
+            const int i = j * 256 + (int)threadIdx.x;
+            if (i < n4) {
+                xv[j] = load_x(i);
+                scan(xv[j], i);
             }
         }
-        uint32_t h02, l02, h13, l13;   // stored order 0, 2, 1, 3
-        float r02[2], r13[2];
-        split_bf16_f16x2(v.x, v.z, h02, l02, r02);
-        split_bf16_f16x2(v.y, v.w, h13, l13, r13);
-        float hs = (r02[0] + r13[0]) + (r02[1] + r13[1]);      // the four elements as their pieces represent them
+    } else {
+        for (int i = threadIdx.x; i < n4; i += 256) scan(load_x(i), i);
+    }
+    ss = wave_sum(ss);
+    mx = wave_max(finite ? mx : __builtin_inff());
+    if ((threadIdx.x & 63) == 0) {
+        red[threadIdx.x >> 6] = ss;
+        redm[threadIdx.x >> 6] = mx;
+    }
+    __syncthreads();
+    const float inv = lnw ? 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)cols + eps) : 1.0f;
+    const float m = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3])) * inv;
+    int k = 0;
+    if (m < __builtin_inff()) {
+        int e = 0;
+        (void)frexpf(m, &e);                  // m = f 2^e, f in [0.5, 1) (e = 0 for m = 0)
+        k = min(max(15 - e, -100), 126);
+    }
+    const float sc = __builtin_ldexpf(1.0f, k);
+    if (threadIdx.x == 0) xscale[b] = __builtin_ldexpf(1.0f, -k);
+    const int nblk = cols / QK;
+    // a thread converts four consecutive elements (two 8-byte stores per plane); the eight threads of
+    // a block sum its hi + lo
+    auto convert = [&](float4 v, int i) {
+        const bool ok = i < n4;
+        if (ok && lnw) {
+            const float4 g = load_g(i);
+            v.x = g.x * (v.x * inv); v.y = g.y * (v.y * inv); v.z = g.z * (v.z * inv); v.w = g.w * (v.w * inv);
+        }
+        if (!ok) v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v.x *= sc; v.y *= sc; v.z *= sc; v.w *= sc;
+        // stored order 0, 2, 1, 3
+        const uint32_t h02 = pack_f16x2(v.x, v.z), h13 = pack_f16x2(v.y, v.w);
+        const auto hp = __builtin_bit_cast(vgx_f16x2_t, h02), hq = __builtin_bit_cast(vgx_f16x2_t, h13);
+        const float hx = (float)hp[0], hz = (float)hp[1], hy = (float)hq[0], hw = (float)hq[1];
+        const uint32_t l02 = pack_f16x2(v.x - hx, v.z - hz), l13 = pack_f16x2(v.y - hy, v.w - hw);
+        const auto lp = __builtin_bit_cast(vgx_f16x2_t, l02), lq = __builtin_bit_cast(vgx_f16x2_t, l13);
+        // the four elements as their pieces represent them
+        float hs = ((hx + (float)lp[0]) + (hy + (float)lq[0])) + ((hz + (float)lp[1]) + (hw + (float)lq[1]));
         if (ok) {
             *reinterpret_cast<uint2 *>(xh + b * cols + 4 * i) = make_uint2(h02, h13);
             *reinterpret_cast<uint2 *>(xl + b * cols + 4 * i) = make_uint2(l02, l13);
@@ -98,6 +146,20 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float *__restrict__ x
         hs += __shfl_xor(hs, 2, kWave);
         hs += __shfl_xor(hs, 4, kWave);
         if (ok && (i & 7) == 0) xsum[b * nblk + i / 8] = hs;
+    };
+    // every lane of a wave takes part in each step (the block sums shuffle across lanes)
+    if (keep) {
+#pragma unroll
+        for (int j = 0; j < kXsplitRegs; ++j) {
+            if (j * 256 >= n4) break;
+            const int i = j * 256 + (int)threadIdx.x;
+            convert(i < n4 ? xv[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f), i);
+        }
+    } else {
+        for (int i0 = 0; i0 < n4; i0 += 256) {
+            const int i = i0 + (int)threadIdx.x;
+            convert(i < n4 ? load_x(i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f), i);
+        }
     }
 }
 
@@ -143,18 +205,18 @@ __device__ __forceinline__ bf16x8_t a_frag(uint2 w, int lg, f16x8_t *fh = nullpt
 // Large batches (prefill chunks, more than 64 activation rows): LDS tiles.  A workgroup of 4 waves
 // owns 128 weight rows (32 row-quads) x 128 activation rows; wave (wm, wn) = (wave & 1, wave >> 1)
 // computes weight rows 64 wm .. + 63 x activation rows 64 wn .. + 63 as 4 x 4 MFMA tiles.  Per quant
-// block the workgroup stages the raw quants and scales of its 128 weight rows and the bf16 hi / fp16
-// lo16 activations and block sums of its 128 activation rows in LDS (double-buffered, one barrier per
+// block the workgroup stages the raw quants and scales of its 128 weight rows and the fp16 hi / lo
+// activations and block sums of its 128 activation rows in LDS (double-buffered, one barrier per
 // block; the next block's global loads are in flight while the current one is multiplied), so every
 // weight fragment serves 4 activation tiles and every activation fragment 4 weight tiles from LDS
 // instead of each wave streaming both from L2.  The offset correction enters as the MFMA's initial
 // accumulator (-off * S_b per activation row), leaving one FMA per output and block for the scale.
 constexpr int kTM = 128;                 // weight rows per workgroup tile
 constexpr int kTN = 128;                 // activation rows per workgroup tile
-constexpr int kBRow = QK + 8;            // bf16 per staged activation row (16 B of padding)
+constexpr int kBRow = QK + 8;            // fp16 per staged activation row (16 B of padding)
 
-// Weights 8 lg .. 8 lg + 7 of the block as the tiled kernel's A fragment, in K-slot order
-// 0, 2, 1, 3, 4, 6, 5, 7 (the split pre-pass stores the activations in the same order).  Q4_0: one
+// Weights 8 lg .. 8 lg + 7 of the block as bf16 and fp16 A fragments, in K-slot order
+// 0, 2, 1, 3, 4, 6, 5, 7 (the activations are staged in the same order).  Q4_0: one
 // AND-OR per two weights gives bf16(16 + n) exactly (exponent of 16, nibble in the top four mantissa
 // bits: 0x4180 | n << 3), so the block's offset is 24; the nibble reaches bits 3..6 by a rotation
 // (right by 29 = left by 3 for the low nibbles, right by 1 for the high ones; the bits it wraps fall
@@ -197,12 +259,45 @@ __device__ __forceinline__ void tile_a_frags(uint2 w, int lg, bf16x8_t &fb, f16x
     fh = __builtin_bit_cast(f16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
 }
 
+// The tiled kernels' A fragment: weights 8 lg .. 8 lg + 7 of the block plus an offset, as exact fp16
+// integers in K-slot order 0, 2, 1, 3, 4, 6, 5, 7 (the split pre-pass stores the activations in the
+// same order); both activation planes (fp16 hi and lo) multiply it.  Q4_0: fp16(16 + n) =
+// 0x4C00 | n << 6, the nibble rotated to bits 6..9 (and 22..25) by one AND-OR per two weights, so the
+// block's offset is 24 (the smallest base whose 16 values share one binade keeps the MFMA's running
+// sums, and so their fp32 rounding, within 5x of the signed weights'); Q8_0: fp16(q + 128) through the
+// byte conversions, offset 128.
+template <int DT>
+__device__ __forceinline__ f16x8_t tile_a_f16(uint2 w, int lg) {
+    uint32_t h[4];
+    if constexpr (DT == VGX_Q4_0) {
+        const bool hi = (lg >> 1) != 0;       // low nibbles for weights 0..15, high nibbles for 16..31
+        // bytes 0 / 2 and bytes 1 / 3 by rotations of their own (a left turn of six would wrap byte 3's
+        // nibble)
+        const int rh02 = hi ? 30 : 26, rh13 = hi ? 6 : 2;
+        h[0] = (__builtin_amdgcn_alignbit(w.x, w.x, rh02) & 0x03C003C0u) | 0x4C004C00u;   // weights 0, 2
+        h[1] = (__builtin_amdgcn_alignbit(w.x, w.x, rh13) & 0x03C003C0u) | 0x4C004C00u;   // weights 1, 3
+        h[2] = (__builtin_amdgcn_alignbit(w.y, w.y, rh02) & 0x03C003C0u) | 0x4C004C00u;
+        h[3] = (__builtin_amdgcn_alignbit(w.y, w.y, rh13) & 0x03C003C0u) | 0x4C004C00u;
+    } else {
+        const uint32_t u[2] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u};
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float f0 = (float)(u[i] & 0xFFu), f1 = (float)((u[i] >> 8) & 0xFFu);
+            const float f2 = (float)((u[i] >> 16) & 0xFFu), f3 = (float)(u[i] >> 24);
+            h[2 * i] = pack_f16x2(f0, f2);
+            h[2 * i + 1] = pack_f16x2(f1, f3);
+        }
+    }
+    return __builtin_bit_cast(f16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+}
+
 template <int DT, int EPI, bool SPLIT>
 __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
                                                           int nblk, int64_t rows_out,
                                                           const uint16_t *__restrict__ xh,
                                                           const uint16_t *__restrict__ xl,
-                                                          const float *__restrict__ xsum, int64_t batch,
+                                                          const float *__restrict__ xsum,
+                                                          const float *__restrict__ xscale, int64_t batch,
                                                           const float *__restrict__ bias, float *__restrict__ y,
                                                           int64_t ldy, float *__restrict__ part, int kper) {
     constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
@@ -284,15 +379,14 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[t][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](int buf) {
-        bf16x8_t af[4];
-        f16x8_t af16[4];
+        f16x8_t af[4];
         vgx_f16x2_t d[4][2];     // fp16 scales, widened inside the FMAs (mixed-precision FMA)
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int rql = wm * 16 + 4 * t + (l16 >> 2);       // A operand: weight row 16 t + l16
             const uint2 w = *reinterpret_cast<const uint2 *>(aq(buf) + (rql * 4 + (l16 & 3)) * QB +
                                                               (DT == VGX_Q8_0 ? 8 * lg : 8 * (lg & 1)));
-            tile_a_frags<DT>(w, lg, af[t], af16[t]);
+            af[t] = tile_a_f16<DT>(w, lg);
             const uint2 sc = asc(buf)[wm * 16 + 4 * t + lg];     // accumulator rows 16 t + 4 lg .. + 3
             d[t][0] = __builtin_bit_cast(vgx_f16x2_t, sc.x);
             d[t][1] = __builtin_bit_cast(vgx_f16x2_t, sc.y);
@@ -300,14 +394,14 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int row = wn * 64 + 16 * c + l16;
-            const bf16x8_t hf = *reinterpret_cast<const bf16x8_t *>(bh(buf) + row * kBRow + 8 * lg);
+            const f16x8_t hf = *reinterpret_cast<const f16x8_t *>(bh(buf) + row * kBRow + 8 * lg);
             const f16x8_t lf = *reinterpret_cast<const f16x8_t *>(bl(buf) + row * kBRow + 8 * lg);
             const float ns = -OFF * bs(buf)[row];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 f32x4_t pr = f32x4_t{ns, ns, ns, ns};
-                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], hf, pr, 0, 0, 0);
-                pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(af16[t], lf, pr, 0, 0, 0);
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], hf, pr, 0, 0, 0);
+                pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], lf, pr, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf((float)d[t][i >> 1][i & 1], pr[i], acc[t][c][i]);
             }
@@ -341,6 +435,10 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
     // apply bias / residual / SwiGLU and store rows of y with consecutive threads on consecutive
     // outputs.
     if constexpr (SPLIT) {
+        // the activation rows' 2^-k, through LDS (the stages are free)
+        float *tsc = reinterpret_cast<float *>(smem);
+        for (int i = tid; i < kTN; i += 256) tsc[i] = b0 + i < batch ? xscale[b0 + i] : 0.0f;
+        __syncthreads();
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int64_t crq = rq0 + wm * 16 + 4 * t + lg;
@@ -349,14 +447,17 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
             for (int c = 0; c < 4; ++c) {
                 const int64_t b = b0 + wn * 64 + 16 * c + l16;
                 if (b >= batch) continue;
+                const float sc = tsc[wn * 64 + 16 * c + l16];
                 float4 v;
-                v.x = acc[t][c][0]; v.y = acc[t][c][1]; v.z = acc[t][c][2]; v.w = acc[t][c][3];
+                v.x = acc[t][c][0] * sc; v.y = acc[t][c][1] * sc; v.z = acc[t][c][2] * sc; v.w = acc[t][c][3] * sc;
                 *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + b) * (n_rq * 4) + crq * 4) = v;
             }
         }
         return;
     }
     float *et = reinterpret_cast<float *>(smem);       // [activation row][64 weight rows + pad]
+    // each activation row's 2^-k in the row's first pad float (the halves below write floats 0..63)
+    for (int i = tid; i < kTN; i += 256) et[i * kERow + 64] = b0 + i < batch ? xscale[b0 + i] : 0.0f;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
         if (wm == half) {
@@ -378,7 +479,8 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
                 const int64_t b = b0 + bl_, oo = r0 / 2 + o;
                 if (b >= batch || oo >= rows_out) continue;
                 const float *er = et + bl_ * kERow + (o >> 1) * 4 + (o & 1);
-                const float g = er[0], u = er[2];
+                const float sc = et[bl_ * kERow + 64];
+                const float g = er[0] * sc, u = er[2] * sc;
                 y[b * ldy + oo] = g / (1.0f + __expf(-g)) * u;
             }
         } else {
@@ -386,7 +488,7 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
                 const int bl_ = i >> 6, rr = i & 63;
                 const int64_t b = b0 + bl_, row = r0 + rr;
                 if (b >= batch || row >= rows_out) continue;
-                float v = et[bl_ * kERow + rr];
+                float v = et[bl_ * kERow + rr] * et[bl_ * kERow + 64];
                 if (bias) v += bias[row];
                 if constexpr (EPI == EPI_ACCUM) v += y[b * ldy + row];
                 y[b * ldy + row] = v;
@@ -406,24 +508,32 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
 // conflicts.  Measured on a 1024-token chunk (Q4_0 / Q8_0): gate/up 228.9 -> 193.5 / 251.4 -> 222.5 us,
 // down 143.0 -> 137.2 / 156.1 -> 144.1, q|k|v 49.2 -> 48.3 / 50.8 -> 49.5, o 43.6 -> 45.8 / 46.6 -> 44.9;
 // with three stages at two workgroups per CU 209.7 us for the Q4_0 gate/up, with four 221.1.
-template <int DT, int EPI, bool SPLIT>
+// Its tile is TM weight rows x TN activation rows, each wave 64 x 64 (wave w: weight rows 64 (w % (TM /
+// 64)), activation rows 64 (w / (TM / 64))).  256 x 64 (kTMDma x kTNDma) stages 12.75 KB per block of
+// a Q4_0 tile instead of the 18.75 KB of 128 x 128 for the same outputs per workgroup: gate/up 195.2
+// -> 182.5 us, down 128.1 -> 122.3, q|k|v 47.4 -> 46.0, o 42.9 -> 43.2.
+constexpr int kTMDma = 256, kTNDma = 64;
+template <int DT, int EPI, bool SPLIT, int TM, int TN>
 __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
                                                               int nblk, int64_t rows_out,
                                                               const uint16_t *__restrict__ xh,
                                                               const uint16_t *__restrict__ xl,
-                                                              const float *__restrict__ xsum, int64_t batch,
+                                                              const float *__restrict__ xsum,
+                                                              const float *__restrict__ xscale, int64_t batch,
                                                               const float *__restrict__ bias, float *__restrict__ y,
                                                               int64_t ldy, float *__restrict__ part, int kper) {
     constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
     constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 24.0f;
     constexpr int APARTS = 4 * QB / 16;
-    constexpr int NA = kTM / 4 * APARTS / 64;           // 16-byte weight pieces: wave-loads per block
-    constexpr int A_B = kTM * QB, SC_B = kTM / 4 * 8, BH_B = kTN * QK * 2, BS_B = kTN * 4;
+    static_assert(TM / 64 * (TN / 64) == 4, "four waves of 64 x 64");
+    constexpr int NA = TM / 4 * APARTS / 64;            // 16-byte weight pieces: wave-loads per block
+    constexpr int NSC = TM / 128;                       // scale wave-loads per block
+    constexpr int A_B = TM * QB, SC_B = TM / 4 * 8, BH_B = TN * QK * 2, BS_B = TN * 4;
     constexpr int STAGE_B = A_B + SC_B + 2 * BH_B + BS_B;
     constexpr int NS = 2;
-    constexpr int NJ = NA + 1 + 2 * (BH_B / 1024) + BS_B / 256;   // wave-loads per block
+    constexpr int NJ = NA + NSC + 2 * (BH_B / 1024) + (BS_B + 255) / 256;   // wave-loads per block
     constexpr int kERow = 64 + 4;
-    constexpr int EPI_B = kTN * kERow * 4;
+    constexpr int EPI_B = TN * kERow * 4;
     __shared__ __align__(16) uint8_t smem[NS * STAGE_B > EPI_B ? NS * STAGE_B : EPI_B];
     auto aq = [&](int buf) { return smem + buf * STAGE_B; };
     auto asc = [&](int buf) { return reinterpret_cast<uint2 *>(smem + buf * STAGE_B + A_B); };
@@ -434,7 +544,7 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l16 = lane & 15, lg = lane >> 4;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = wave % (TM / 64), wn = wave / (TM / 64);
     const int cols = nblk * QK;
     // XCD-aware tile order: workgroups go to the 8 XCDs round robin (linear id mod 8); each XCD takes a
     // contiguous run of the activation-tile-major tile sequence, so that it reads few activation tiles
@@ -448,8 +558,8 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
             tr = (int)(s - (int64_t)tt * G);
         }
     }
-    const int64_t rq0 = (int64_t)tr * (kTM / 4);
-    const int64_t b0 = (int64_t)tt * kTN;
+    const int64_t rq0 = (int64_t)tr * (TM / 4);
+    const int64_t b0 = (int64_t)tt * TN;
     const int blk_lo = SPLIT ? (int)blockIdx.z * kper : 0;
     const int blk_hi = SPLIT ? min(nblk, blk_lo + kper) : nblk;
 
@@ -467,18 +577,18 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
                 const int64_t rq = rq0 + pc / APARTS;
                 const uint32_t o = rq < n_rq ? (uint32_t)((rq * nblk + blk) * 4 * QB + (pc % APARTS) * 16) : kDmaPast;
                 dma16(wrs, o, aq(buf) + j * 1024);
-            } else if (j == NA) {
-                const int64_t rq = rq0 + lane / 2;
+            } else if (j < NA + NSC) {
+                const int64_t rq = rq0 + (j - NA) * 32 + lane / 2;
                 const uint32_t o = rq < n_rq ? (uint32_t)(soff + (rq * nblk + blk) * 8 + (lane & 1) * 4) : kDmaPast;
-                dma4(wrs, o, asc(buf));
-            } else if (j < NA + 1 + 2 * (BH_B / 1024)) {
-                const int jb = j - NA - 1, pl = jb / (BH_B / 1024), jr = jb % (BH_B / 1024);
+                dma4(wrs, o, reinterpret_cast<const uint8_t *>(asc(buf)) + (j - NA) * 256);
+            } else if (j < NA + NSC + 2 * (BH_B / 1024)) {
+                const int jb = j - NA - NSC, pl = jb / (BH_B / 1024), jr = jb % (BH_B / 1024);
                 const int row = 16 * jr + (lane >> 2), slot = lane & 3, piece = slot ^ ((row >> 2) & 3);
                 const int64_t b = b0 + row;
                 const uint32_t o = b < batch ? (uint32_t)((b * cols + (int64_t)blk * QK + piece * 8) * 2) : kDmaPast;
                 dma16(pl ? lrs : hrs, o, reinterpret_cast<const uint8_t *>(pl ? bl(buf) : bh(buf)) + jr * 1024);
             } else if (j < NJ) {
-                const int jb = j - NA - 1 - 2 * (BH_B / 1024);
+                const int jb = j - NA - NSC - 2 * (BH_B / 1024);
                 const int64_t b = b0 + 64 * jb + lane;
                 const uint32_t o = b < batch ? (uint32_t)((b * nblk + blk) * 4) : kDmaPast;
                 dma4(srs, o, reinterpret_cast<const uint8_t *>(bs(buf)) + jb * 256);
@@ -491,15 +601,14 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[t][c] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](int buf) {
-        bf16x8_t af[4];
-        f16x8_t af16[4];
+        f16x8_t af[4];
         vgx_f16x2_t d[4][2];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int rql = wm * 16 + 4 * t + (l16 >> 2);
             const uint2 w = *reinterpret_cast<const uint2 *>(aq(buf) + (rql * 4 + (l16 & 3)) * QB +
                                                               (DT == VGX_Q8_0 ? 8 * lg : 8 * (lg & 1)));
-            tile_a_frags<DT>(w, lg, af[t], af16[t]);
+            af[t] = tile_a_f16<DT>(w, lg);
             const uint2 sc = asc(buf)[wm * 16 + 4 * t + lg];
             d[t][0] = __builtin_bit_cast(vgx_f16x2_t, sc.x);
             d[t][1] = __builtin_bit_cast(vgx_f16x2_t, sc.y);
@@ -508,17 +617,20 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
         for (int c = 0; c < 4; ++c) {
             const int row = wn * 64 + 16 * c + l16;
             const int off = row * QK + 8 * (lg ^ ((row >> 2) & 3));
-            const bf16x8_t hf = *reinterpret_cast<const bf16x8_t *>(bh(buf) + off);
+            const f16x8_t hf = *reinterpret_cast<const f16x8_t *>(bh(buf) + off);
             const f16x8_t lf = *reinterpret_cast<const f16x8_t *>(bl(buf) + off);
             const float ns = -OFF * bs(buf)[row];
+            // four independent accumulator chains, so that the MFMAs of one tile overlap the next's
+            f32x4_t pr[4];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                f32x4_t pr = f32x4_t{ns, ns, ns, ns};
-                pr = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], hf, pr, 0, 0, 0);
-                pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(af16[t], lf, pr, 0, 0, 0);
+            for (int t = 0; t < 4; ++t)
+                pr[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], hf, f32x4_t{ns, ns, ns, ns}, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf((float)d[t][i >> 1][i & 1], pr[i], acc[t][c][i]);
-            }
+            for (int t = 0; t < 4; ++t) pr[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], lf, pr[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][c][i] = fmaf((float)d[t][i >> 1][i & 1], pr[t][i], acc[t][c][i]);
         }
     };
 
@@ -534,6 +646,10 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");   // the stages are free for the epilogue
 
     if constexpr (SPLIT) {
+        // the activation rows' 2^-k, through LDS (the stages are free)
+        float *tsc = reinterpret_cast<float *>(smem);
+        for (int i = tid; i < TN; i += 256) tsc[i] = b0 + i < batch ? xscale[b0 + i] : 0.0f;
+        __syncthreads();
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const int64_t crq = rq0 + wm * 16 + 4 * t + lg;
@@ -542,16 +658,19 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
             for (int c = 0; c < 4; ++c) {
                 const int64_t b = b0 + wn * 64 + 16 * c + l16;
                 if (b >= batch) continue;
+                const float sc = tsc[wn * 64 + 16 * c + l16];
                 float4 v;
-                v.x = acc[t][c][0]; v.y = acc[t][c][1]; v.z = acc[t][c][2]; v.w = acc[t][c][3];
+                v.x = acc[t][c][0] * sc; v.y = acc[t][c][1] * sc; v.z = acc[t][c][2] * sc; v.w = acc[t][c][3] * sc;
                 *reinterpret_cast<float4 *>(part + ((int64_t)blockIdx.z * batch + b) * (n_rq * 4) + crq * 4) = v;
             }
         }
         return;
     }
     float *et = reinterpret_cast<float *>(smem);
+    // each activation row's 2^-k in the row's first pad float (the halves below write floats 0..63)
+    for (int i = tid; i < TN; i += 256) et[i * kERow + 64] = b0 + i < batch ? xscale[b0 + i] : 0.0f;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
+    for (int half = 0; half < TM / 64; ++half) {
         if (wm == half) {
 #pragma unroll
             for (int t = 0; t < 4; ++t)
@@ -565,20 +684,21 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
         __syncthreads();
         const int64_t r0 = (rq0 + half * 16) * 4;
         if constexpr (EPI == EPI_SWIGLU) {
-            for (int i = tid; i < kTN * 32; i += 256) {
+            for (int i = tid; i < TN * 32; i += 256) {
                 const int bl_ = i >> 5, o = i & 31;
                 const int64_t b = b0 + bl_, oo = r0 / 2 + o;
                 if (b >= batch || oo >= rows_out) continue;
                 const float *er = et + bl_ * kERow + (o >> 1) * 4 + (o & 1);
-                const float g = er[0], u = er[2];
+                const float sc = et[bl_ * kERow + 64];
+                const float g = er[0] * sc, u = er[2] * sc;
                 y[b * ldy + oo] = g / (1.0f + __expf(-g)) * u;
             }
         } else {
-            for (int i = tid; i < kTN * 64; i += 256) {
+            for (int i = tid; i < TN * 64; i += 256) {
                 const int bl_ = i >> 6, rr = i & 63;
                 const int64_t b = b0 + bl_, row = r0 + rr;
                 if (b >= batch || row >= rows_out) continue;
-                float v = et[bl_ * kERow + rr];
+                float v = et[bl_ * kERow + rr] * et[bl_ * kERow + 64];
                 if (bias) v += bias[row];
                 if constexpr (EPI == EPI_ACCUM) v += y[b * ldy + row];
                 y[b * ldy + row] = v;
@@ -2029,8 +2149,10 @@ int64_t gemm_scale_off(int dt, int64_t rows, int64_t cols) {
 }
 
 inline int64_t split_plane_bytes(int64_t batch, int64_t cols) { return (batch * cols * 2 + 255) / 256 * 256; }
+// the fp16 hi and lo planes, the per-block sums, the per-row scales
+inline int64_t split_sum_bytes(int64_t batch, int64_t cols) { return (batch * (cols / QK) * 4 + 255) / 256 * 256; }
 inline int64_t split_bytes(int64_t batch, int64_t cols) {
-    return 2 * split_plane_bytes(batch, cols) + (batch * (cols / QK) * 4 + 255) / 256 * 256;
+    return 2 * split_plane_bytes(batch, cols) + split_sum_bytes(batch, cols) + (batch * 4 + 255) / 256 * 256;
 }
 
 constexpr int kMaxKSplit = 16;
@@ -2047,10 +2169,12 @@ int choose_ksplit(int64_t n_rq, int64_t batch, int nc, int nblk) {
     return (int)std::max<int64_t>(1, ks);
 }
 
-// K splits of the tiled kernel: about two workgroups per CU (eight for long rows: measured 139 vs 149 us
-// for the 1536 x 8960 down projection of a 1024-token chunk), at least 8 blocks per split.
+// K splits of the tiled kernels, counted on the DMA kernel's tiles: about 512 workgroups (2048 for long
+// rows: measured 139 vs 149 us for the 1536 x 8960 down projection of a 1024-token chunk), at least 8
+// blocks per split.  Targets of 768 (one round at three workgroups per CU) measured no better: q|k|v and
+// o of a 1024-token chunk 45.4 / 40.7 -> 47.7 / 44.0 us.
 int tile_ksplit(int64_t n_rq, int64_t batch, int nblk) {
-    const int64_t tiles = (n_rq + kTM / 4 - 1) / (kTM / 4) * ((batch + kTN - 1) / kTN);
+    const int64_t tiles = (n_rq + kTMDma / 4 - 1) / (kTMDma / 4) * ((batch + kTNDma - 1) / kTNDma);
     const int64_t target = nblk >= 128 ? 2048 : 512;
     // as many splits as fit the target without exceeding it: 512 workgroups are one round at two per
     // CU, and a few more would run as a mostly idle second round (o-projection of a 1024-token chunk:
@@ -2493,27 +2617,30 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     auto *xh = reinterpret_cast<uint16_t *>(wsb);
     auto *xl = reinterpret_cast<uint16_t *>(wsb + pb);
     auto *xs = reinterpret_cast<float *>(wsb + 2 * pb);
+    auto *xsc = reinterpret_cast<float *>(wsb + 2 * pb + split_sum_bytes(batch, cols));
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(xsplit_kernel, dim3((unsigned)batch), dim3(256), 0, st, x, ldx, norm_w, eps, (int)cols, xh, xl,
-                       xs);
+                       xs, xsc);
     VGX_CHECK_LAUNCH();
     auto *part = reinterpret_cast<float *>(wsb + split_bytes(batch, cols));
     const int kper = (nblk + ks - 1) / ks;
+    constexpr int DTM = kTMDma, DTN = kTNDma;
     const dim3 grid((unsigned)((n_rq + kTM / 4 - 1) / (kTM / 4)), (unsigned)((batch + kTN - 1) / kTN), (unsigned)ks);
+    const dim3 dgrid((unsigned)((n_rq + DTM / 4 - 1) / (DTM / 4)), (unsigned)((batch + DTN - 1) / DTN), (unsigned)ks);
     const auto *w = static_cast<const uint8_t *>(w_packed);
-    // the DMA kernel for launches of at least 512 workgroups (its buffer ranges are 32-bit): the 1536 x
-    // 1536 o-projection of a 1024-token chunk (480 workgroups, about ten blocks each) measured slower on
-    // it, 45.8 against 43.6 us; q|k|v (512) 48.3 against 49.2
-    const bool dma = (int64_t)grid.x * grid.y * grid.z >= 512 && soff + n_rq * nblk * 8 < ((int64_t)1 << 31) &&
-                     batch * cols * 2 < ((int64_t)1 << 31);
+    // the DMA kernel wherever its 32-bit buffer ranges reach: it measured ahead of the register-staged
+    // kernel at every grid size (Q4_0, 80 / 160 / 256 / 512 tokens: q|k|v 36.6 -> 36.1 / 37.5 -> 26.9
+    // / 39.9 -> 30.0 / 47.7 -> 37.0 us, gate/up 59.7 -> 42.4 / 79.0 -> 60.1 / 83.4 -> 75.1 / 101.6 ->
+    // 101.1, down 61.5 -> 40.1 / 73.0 -> 49.4 / 78.9 -> 51.4 / 69.1 -> 68.9)
+    const bool dma = soff + n_rq * nblk * 8 < ((int64_t)1 << 31) && batch * cols * 2 < ((int64_t)1 << 31);
 #define VGX_GEMM_GO(DT, EPI, SP)                                                                              \
     do {                                                                                                      \
         if (dma)                                                                                              \
-            hipLaunchKernelGGL((qgemm_tile_dma_kernel<DT, EPI, SP>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, \
-                               xh, xl, xs, batch, bias, y, ldy, part, kper);                                   \
+            hipLaunchKernelGGL((qgemm_tile_dma_kernel<DT, EPI, SP, DTM, DTN>), dgrid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, \
+                               xh, xl, xs, xsc, batch, bias, y, ldy, part, kper);                              \
         else                                                                                                  \
             hipLaunchKernelGGL((qgemm_tile_kernel<DT, EPI, SP>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, xh, \
-                               xl, xs, batch, bias, y, ldy, part, kper);                                      \
+                               xl, xs, xsc, batch, bias, y, ldy, part, kper);                                 \
     } while (0)
 #define VGX_GEMM_EPI(DT)                                                                                      \
     do {                                                                                                      \
