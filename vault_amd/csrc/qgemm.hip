@@ -14,13 +14,13 @@
 // bits, 2^-20 relative residual; lo16 overflows only past |u| = 2^21), lo16 multiplied by the same
 // weights divided by 16 as exact fp16 values, the two products added into one accumulator (two MFMAs
 // per block; three bf16 pieces would take three and, in the decode-batch kernel, registers that its
-// occupancy target does not have: spills).  The tiled kernels take two fp16 pieces of the row scaled
-// by a power of two 2^k (hi = fp16(2^k u), lo = fp16(2^k u - hi): about 22 significant bits, both
-// pieces in fp16's normal range for any row), both multiplied by one exact fp16 weight operand, and
-// scale their outputs by 2^-k.  With S_b the per-block sum of the pieces, per block the fp32 MFMA
-// result C (= sum_j w_j u_j as pieces) is corrected and scaled:
-//   acc += d * (C - off * S_b),   off = 128 (Q8_0), 8 (Q4_0; 24 in the tiled kernels),
-// which is the reference's sum_b d_b sum_j q_j x_j at fp32-level accuracy.  The decode-batch kernels
+// occupancy target does not have: spills).  With S_b the per-block sum of the pieces, per block the
+// fp32 MFMA result C (= sum_j w_j u_j as pieces) is corrected and scaled:
+//   acc += d * (C - off * S_b),   off = 128 (Q8_0), 8 (Q4_0),
+// which is the reference's sum_b d_b sum_j q_j x_j at fp32-level accuracy.  The tiled kernels take two
+// fp16 pieces of the row scaled by a power of two 2^k (hi = fp16(2^k u), lo = fp16(2^k u - hi): about
+// 22 significant bits, both pieces in fp16's normal range for any row), both multiplied by the signed
+// weights as exact fp16 (no offset, so acc += d * C), and scale their outputs by 2^-k.  The decode-batch kernels
 // place the weights by byte permutes instead (Q4_0 bf16 128 + n / fp16 1024 + n against pieces of 16 u;
 // fp16 1024 + unsigned weight in qgemm_wide_kernel, whose pieces are both fp16 of a power-of-two-scaled
 // row) with the matching offsets; their comments give the arithmetic.
@@ -47,8 +47,8 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 // u = (norm ? lnw * x * inv_rms : x), scaled per row by a power of two 2^k that puts the largest |u|
 // in [2^14, 2^15), split into two fp16 planes hi = fp16(2^k u) and lo = fp16(2^k u - hi): together
 // about 22 significant bits of every element, with the scale keeping both pieces in fp16's normal
-// range whatever the row's magnitude.  Also the per-block sums of hi + lo (in fp32) and the row's 2^-k,
-// which the GEMM multiplies into its outputs (exactly: a power of two).  k stays within [-100, 126],
+// range whatever the row's magnitude.  Also the row's 2^-k, which the GEMM multiplies into its outputs
+// (exactly: a power of two).  k stays within [-100, 126],
 // so 2^-k is a normal float; a row holding an infinity or a NaN is not scaled (k = 0), so that it
 // reaches the outputs as it would unsplit.
 // Inside every group of four, elements 1 and 2 trade places (stored order 0, 2, 1, 3): the K-slot
@@ -58,7 +58,7 @@ constexpr int kXsplitRegs = 20;   // float4 per thread kept in registers: rows o
 __global__ __launch_bounds__(256) void xsplit_kernel(const float *__restrict__ x, int64_t ldx,
                                                       const float *__restrict__ lnw, float eps, int cols,
                                                       uint16_t *__restrict__ xh, uint16_t *__restrict__ xl,
-                                                      float *__restrict__ xsum, float *__restrict__ xscale) {
+                                                      float *__restrict__ xscale) {
     __shared__ float red[4], redm[4];
     const int64_t b = blockIdx.x;
     const float *xr = x + b * ldx;
@@ -119,47 +119,29 @@ __global__ __launch_bounds__(256) void xsplit_kernel(const float *__restrict__ x
     }
     const float sc = __builtin_ldexpf(1.0f, k);
     if (threadIdx.x == 0) xscale[b] = __builtin_ldexpf(1.0f, -k);
-    const int nblk = cols / QK;
-    // a thread converts four consecutive elements (two 8-byte stores per plane); the eight threads of
-    // a block sum its hi + lo
+    // a thread converts four consecutive elements (two 8-byte stores per plane)
     auto convert = [&](float4 v, int i) {
-        const bool ok = i < n4;
-        if (ok && lnw) {
+        if (lnw) {
             const float4 g = load_g(i);
             v.x = g.x * (v.x * inv); v.y = g.y * (v.y * inv); v.z = g.z * (v.z * inv); v.w = g.w * (v.w * inv);
         }
-        if (!ok) v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         v.x *= sc; v.y *= sc; v.z *= sc; v.w *= sc;
         // stored order 0, 2, 1, 3
         const uint32_t h02 = pack_f16x2(v.x, v.z), h13 = pack_f16x2(v.y, v.w);
         const auto hp = __builtin_bit_cast(vgx_f16x2_t, h02), hq = __builtin_bit_cast(vgx_f16x2_t, h13);
-        const float hx = (float)hp[0], hz = (float)hp[1], hy = (float)hq[0], hw = (float)hq[1];
-        const uint32_t l02 = pack_f16x2(v.x - hx, v.z - hz), l13 = pack_f16x2(v.y - hy, v.w - hw);
-        const auto lp = __builtin_bit_cast(vgx_f16x2_t, l02), lq = __builtin_bit_cast(vgx_f16x2_t, l13);
-        // the four elements as their pieces represent them
-        float hs = ((hx + (float)lp[0]) + (hy + (float)lq[0])) + ((hz + (float)lp[1]) + (hw + (float)lq[1]));
-        if (ok) {
-            *reinterpret_cast<uint2 *>(xh + b * cols + 4 * i) = make_uint2(h02, h13);
-            *reinterpret_cast<uint2 *>(xl + b * cols + 4 * i) = make_uint2(l02, l13);
-        }
-        hs += __shfl_xor(hs, 1, kWave);
-        hs += __shfl_xor(hs, 2, kWave);
-        hs += __shfl_xor(hs, 4, kWave);
-        if (ok && (i & 7) == 0) xsum[b * nblk + i / 8] = hs;
+        const uint32_t l02 = pack_f16x2(v.x - (float)hp[0], v.z - (float)hp[1]);
+        const uint32_t l13 = pack_f16x2(v.y - (float)hq[0], v.w - (float)hq[1]);
+        *reinterpret_cast<uint2 *>(xh + b * cols + 4 * i) = make_uint2(h02, h13);
+        *reinterpret_cast<uint2 *>(xl + b * cols + 4 * i) = make_uint2(l02, l13);
     };
-    // every lane of a wave takes part in each step (the block sums shuffle across lanes)
     if (keep) {
 #pragma unroll
         for (int j = 0; j < kXsplitRegs; ++j) {
-            if (j * 256 >= n4) break;
             const int i = j * 256 + (int)threadIdx.x;
-            convert(i < n4 ? xv[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f), i);
+            if (i < n4) convert(xv[j], i);
         }
     } else {
-        for (int i0 = 0; i0 < n4; i0 += 256) {
-            const int i = i0 + (int)threadIdx.x;
-            convert(i < n4 ? load_x(i) : make_float4(0.0f, 0.0f, 0.0f, 0.0f), i);
-        }
+        for (int i = threadIdx.x; i < n4; i += 256) convert(load_x(i), i);
     }
 }
 
@@ -259,13 +241,12 @@ __device__ __forceinline__ void tile_a_frags(uint2 w, int lg, bf16x8_t &fb, f16x
     fh = __builtin_bit_cast(f16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
 }
 
-// The tiled kernels' A fragment: weights 8 lg .. 8 lg + 7 of the block plus an offset, as exact fp16
-// integers in K-slot order 0, 2, 1, 3, 4, 6, 5, 7 (the split pre-pass stores the activations in the
-// same order); both activation planes (fp16 hi and lo) multiply it.  Q4_0: fp16(16 + n) =
-// 0x4C00 | n << 6, the nibble rotated to bits 6..9 (and 22..25) by one AND-OR per two weights, so the
-// block's offset is 24 (the smallest base whose 16 values share one binade keeps the MFMA's running
-// sums, and so their fp32 rounding, within 5x of the signed weights'); Q8_0: fp16(q + 128) through the
-// byte conversions, offset 128.
+// The tiled kernels' A fragment: weights 8 lg .. 8 lg + 7 of the block as exact fp16 signed integers
+// (Q4_0 n - 8, Q8_0 q) in K-slot order 0, 2, 1, 3, 4, 6, 5, 7 (the split pre-pass stores the
+// activations in the same order); both activation planes (fp16 hi and lo) multiply it, and the MFMA
+// sums need no offset correction.  Q4_0: fp16(16 + n) = 0x4C00 | n << 6 (the nibble rotated to bits
+// 6..9 and 22..25, one AND-OR per two weights), then one packed fp16 subtraction of 24 (exact);
+// Q8_0: q + 128 through the byte conversions, packed to fp16, minus 128.
 template <int DT>
 __device__ __forceinline__ f16x8_t tile_a_f16(uint2 w, int lg) {
     uint32_t h[4];
@@ -274,10 +255,18 @@ __device__ __forceinline__ f16x8_t tile_a_f16(uint2 w, int lg) {
         // bytes 0 / 2 and bytes 1 / 3 by rotations of their own (a left turn of six would wrap byte 3's
         // nibble)
         const int rh02 = hi ? 30 : 26, rh13 = hi ? 6 : 2;
-        h[0] = (__builtin_amdgcn_alignbit(w.x, w.x, rh02) & 0x03C003C0u) | 0x4C004C00u;   // weights 0, 2
-        h[1] = (__builtin_amdgcn_alignbit(w.x, w.x, rh13) & 0x03C003C0u) | 0x4C004C00u;   // weights 1, 3
-        h[2] = (__builtin_amdgcn_alignbit(w.y, w.y, rh02) & 0x03C003C0u) | 0x4C004C00u;
-        h[3] = (__builtin_amdgcn_alignbit(w.y, w.y, rh13) & 0x03C003C0u) | 0x4C004C00u;
+        // (r & mask) | base as one v_and_or_b32 (VOP3 takes no literal here: the mask in an SGPR, the
+        // base in a VGPR); the compiler emits an AND and an OR with literals otherwise
+        const uint32_t base = 0x4C004C00u;
+        auto and_or = [&](uint32_t r) {
+            uint32_t o;
+            asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(o) : "v"(r), "s"(0x03C003C0u), "v"(base));
+            return o;
+        };
+        h[0] = and_or(__builtin_amdgcn_alignbit(w.x, w.x, rh02));   // weights 0, 2
+        h[1] = and_or(__builtin_amdgcn_alignbit(w.x, w.x, rh13));   // weights 1, 3
+        h[2] = and_or(__builtin_amdgcn_alignbit(w.y, w.y, rh02));
+        h[3] = and_or(__builtin_amdgcn_alignbit(w.y, w.y, rh13));
     } else {
         const uint32_t u[2] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u};
 #pragma unroll
@@ -288,7 +277,9 @@ __device__ __forceinline__ f16x8_t tile_a_f16(uint2 w, int lg) {
             h[2 * i + 1] = pack_f16x2(f1, f3);
         }
     }
-    return __builtin_bit_cast(f16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+    constexpr _Float16 off = DT == VGX_Q4_0 ? (_Float16)-24.0f : (_Float16)-128.0f;
+    f16x8_t f = __builtin_bit_cast(f16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+    return f + f16x8_t{off, off, off, off, off, off, off, off};
 }
 
 template <int DT, int EPI, bool SPLIT>
@@ -296,17 +287,15 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
                                                           int nblk, int64_t rows_out,
                                                           const uint16_t *__restrict__ xh,
                                                           const uint16_t *__restrict__ xl,
-                                                          const float *__restrict__ xsum,
                                                           const float *__restrict__ xscale, int64_t batch,
                                                           const float *__restrict__ bias, float *__restrict__ y,
                                                           int64_t ldy, float *__restrict__ part, int kper) {
     constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
-    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 24.0f;   // w + off: q + 128, or 16 + n for n - 8
     constexpr int APARTS = 4 * QB / 16;                  // 16-byte pieces of one row-quad block
     constexpr int AQ16 = kTM / 4 * APARTS;               // 16-byte pieces of the tile's block
     // Stage buffers (two blocks) and, after the K loop, the epilogue's half tile share one LDS area.
-    constexpr int A_B = kTM * QB, SC_B = kTM / 4 * 8, BH_B = kTN * kBRow * 2, BS_B = kTN * 4;
-    constexpr int STAGE_B = A_B + SC_B + 2 * BH_B + BS_B;
+    constexpr int A_B = kTM * QB, SC_B = kTM / 4 * 8, BH_B = kTN * kBRow * 2;
+    constexpr int STAGE_B = A_B + SC_B + 2 * BH_B;
     constexpr int kERow = 64 + 4;                          // floats per activation row of a half tile
     constexpr int EPI_B = kTN * kERow * 4;
     __shared__ __align__(16) uint8_t smem[2 * STAGE_B > EPI_B ? 2 * STAGE_B : EPI_B];
@@ -314,7 +303,6 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
     auto asc = [&](int buf) { return reinterpret_cast<uint2 *>(smem + buf * STAGE_B + A_B); };
     auto bh = [&](int buf) { return reinterpret_cast<uint16_t *>(smem + buf * STAGE_B + A_B + SC_B); };
     auto bl = [&](int buf) { return reinterpret_cast<uint16_t *>(smem + buf * STAGE_B + A_B + SC_B + BH_B); };
-    auto bs = [&](int buf) { return reinterpret_cast<float *>(smem + buf * STAGE_B + A_B + SC_B + 2 * BH_B); };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, lg = lane >> 4;
@@ -331,7 +319,6 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
     struct Regs {
         uint4 ra, h0, h1, l0, l1;
         uint2 rs;
-        float rx;
     };
     auto fetch_b = [&](int idx, int blk, uint4 &h, uint4 &l) {
         const int row = idx >> 2, pc = idx & 3;
@@ -347,7 +334,6 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
     auto fetch = [&](Regs &r, int blk) {
         r.ra = make_uint4(0, 0, 0, 0);
         r.rs = make_uint2(0, 0);
-        r.rx = 0.0f;
         if (tid < AQ16) {
             const int64_t rq = rq0 + tid / APARTS;
             if (rq < n_rq) r.ra = *reinterpret_cast<const uint4 *>(W + (rq * nblk + blk) * 4 * QB + (tid % APARTS) * 16);
@@ -358,10 +344,6 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
         }
         fetch_b(tid, blk, r.h0, r.l0);
         fetch_b(tid + 256, blk, r.h1, r.l1);
-        if (tid < kTN) {
-            const int64_t b = b0 + tid;
-            if (b < batch) r.rx = xsum[b * nblk + blk];
-        }
     };
     auto stage = [&](const Regs &r, int buf) {
         if (tid < AQ16) *reinterpret_cast<uint4 *>(aq(buf) + tid * 16) = r.ra;
@@ -370,7 +352,6 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
         *reinterpret_cast<uint4 *>(bl(buf) + (tid >> 2) * kBRow + (tid & 3) * 8) = r.l0;
         *reinterpret_cast<uint4 *>(bh(buf) + ((tid + 256) >> 2) * kBRow + (tid & 3) * 8) = r.h1;
         *reinterpret_cast<uint4 *>(bl(buf) + ((tid + 256) >> 2) * kBRow + (tid & 3) * 8) = r.l1;
-        if (tid < kTN) bs(buf)[tid] = r.rx;
     };
 
     f32x4_t acc[4][4];
@@ -396,10 +377,9 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
             const int row = wn * 64 + 16 * c + l16;
             const f16x8_t hf = *reinterpret_cast<const f16x8_t *>(bh(buf) + row * kBRow + 8 * lg);
             const f16x8_t lf = *reinterpret_cast<const f16x8_t *>(bl(buf) + row * kBRow + 8 * lg);
-            const float ns = -OFF * bs(buf)[row];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                f32x4_t pr = f32x4_t{ns, ns, ns, ns};
+                f32x4_t pr = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
                 pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], hf, pr, 0, 0, 0);
                 pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], lf, pr, 0, 0, 0);
 #pragma unroll
@@ -518,20 +498,18 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
                                                               int nblk, int64_t rows_out,
                                                               const uint16_t *__restrict__ xh,
                                                               const uint16_t *__restrict__ xl,
-                                                              const float *__restrict__ xsum,
                                                               const float *__restrict__ xscale, int64_t batch,
                                                               const float *__restrict__ bias, float *__restrict__ y,
                                                               int64_t ldy, float *__restrict__ part, int kper) {
     constexpr int QB = DT == VGX_Q8_0 ? 32 : 16;
-    constexpr float OFF = DT == VGX_Q8_0 ? 128.0f : 24.0f;
     constexpr int APARTS = 4 * QB / 16;
     static_assert(TM / 64 * (TN / 64) == 4, "four waves of 64 x 64");
     constexpr int NA = TM / 4 * APARTS / 64;            // 16-byte weight pieces: wave-loads per block
     constexpr int NSC = TM / 128;                       // scale wave-loads per block
-    constexpr int A_B = TM * QB, SC_B = TM / 4 * 8, BH_B = TN * QK * 2, BS_B = TN * 4;
-    constexpr int STAGE_B = A_B + SC_B + 2 * BH_B + BS_B;
+    constexpr int A_B = TM * QB, SC_B = TM / 4 * 8, BH_B = TN * QK * 2;
+    constexpr int STAGE_B = A_B + SC_B + 2 * BH_B;
     constexpr int NS = 2;
-    constexpr int NJ = NA + NSC + 2 * (BH_B / 1024) + (BS_B + 255) / 256;   // wave-loads per block
+    constexpr int NJ = NA + NSC + 2 * (BH_B / 1024);   // wave-loads per block
     constexpr int kERow = 64 + 4;
     constexpr int EPI_B = TN * kERow * 4;
     __shared__ __align__(16) uint8_t smem[NS * STAGE_B > EPI_B ? NS * STAGE_B : EPI_B];
@@ -539,7 +517,6 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
     auto asc = [&](int buf) { return reinterpret_cast<uint2 *>(smem + buf * STAGE_B + A_B); };
     auto bh = [&](int buf) { return reinterpret_cast<uint16_t *>(smem + buf * STAGE_B + A_B + SC_B); };
     auto bl = [&](int buf) { return reinterpret_cast<uint16_t *>(smem + buf * STAGE_B + A_B + SC_B + BH_B); };
-    auto bs = [&](int buf) { return reinterpret_cast<float *>(smem + buf * STAGE_B + A_B + SC_B + 2 * BH_B); };
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -566,8 +543,7 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
     const dma_rsrc_t wrs = dma_rsrc(W, (uint32_t)(soff + n_rq * nblk * 8));
     const dma_rsrc_t hrs = dma_rsrc(xh, (uint32_t)(batch * cols * 2));
     const dma_rsrc_t lrs = dma_rsrc(xl, (uint32_t)(batch * cols * 2));
-    const dma_rsrc_t srs = dma_rsrc(xsum, (uint32_t)(batch * nblk * 4));
-    // wave-load j of a block: weight pieces (j < NA), scales, hi rows, lo rows, block sums
+    // wave-load j of a block: weight pieces (j < NA), scales, hi rows, lo rows
     auto issue = [&](int blk, int buf) {
 #pragma unroll
         for (int jj = 0; jj < (NJ + 3) / 4; ++jj) {
@@ -581,17 +557,12 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
                 const int64_t rq = rq0 + (j - NA) * 32 + lane / 2;
                 const uint32_t o = rq < n_rq ? (uint32_t)(soff + (rq * nblk + blk) * 8 + (lane & 1) * 4) : kDmaPast;
                 dma4(wrs, o, reinterpret_cast<const uint8_t *>(asc(buf)) + (j - NA) * 256);
-            } else if (j < NA + NSC + 2 * (BH_B / 1024)) {
+            } else if (j < NJ) {
                 const int jb = j - NA - NSC, pl = jb / (BH_B / 1024), jr = jb % (BH_B / 1024);
                 const int row = 16 * jr + (lane >> 2), slot = lane & 3, piece = slot ^ ((row >> 2) & 3);
                 const int64_t b = b0 + row;
                 const uint32_t o = b < batch ? (uint32_t)((b * cols + (int64_t)blk * QK + piece * 8) * 2) : kDmaPast;
                 dma16(pl ? lrs : hrs, o, reinterpret_cast<const uint8_t *>(pl ? bl(buf) : bh(buf)) + jr * 1024);
-            } else if (j < NJ) {
-                const int jb = j - NA - NSC - 2 * (BH_B / 1024);
-                const int64_t b = b0 + 64 * jb + lane;
-                const uint32_t o = b < batch ? (uint32_t)((b * nblk + blk) * 4) : kDmaPast;
-                dma4(srs, o, reinterpret_cast<const uint8_t *>(bs(buf)) + jb * 256);
             }
         }
     };
@@ -619,12 +590,11 @@ __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *_
             const int off = row * QK + 8 * (lg ^ ((row >> 2) & 3));
             const f16x8_t hf = *reinterpret_cast<const f16x8_t *>(bh(buf) + off);
             const f16x8_t lf = *reinterpret_cast<const f16x8_t *>(bl(buf) + off);
-            const float ns = -OFF * bs(buf)[row];
             // four independent accumulator chains, so that the MFMAs of one tile overlap the next's
             f32x4_t pr[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t)
-                pr[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], hf, f32x4_t{ns, ns, ns, ns}, 0, 0, 0);
+                pr[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], hf, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
 #pragma unroll
             for (int t = 0; t < 4; ++t) pr[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[t], lf, pr[t], 0, 0, 0);
 #pragma unroll
@@ -2149,10 +2119,9 @@ int64_t gemm_scale_off(int dt, int64_t rows, int64_t cols) {
 }
 
 inline int64_t split_plane_bytes(int64_t batch, int64_t cols) { return (batch * cols * 2 + 255) / 256 * 256; }
-// the fp16 hi and lo planes, the per-block sums, the per-row scales
-inline int64_t split_sum_bytes(int64_t batch, int64_t cols) { return (batch * (cols / QK) * 4 + 255) / 256 * 256; }
+// the fp16 hi and lo planes, the per-row scales
 inline int64_t split_bytes(int64_t batch, int64_t cols) {
-    return 2 * split_plane_bytes(batch, cols) + split_sum_bytes(batch, cols) + (batch * 4 + 255) / 256 * 256;
+    return 2 * split_plane_bytes(batch, cols) + (batch * 4 + 255) / 256 * 256;
 }
 
 constexpr int kMaxKSplit = 16;
@@ -2616,11 +2585,10 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     char *const wsb = static_cast<char *>(workspace) + kQgemmTicketBytes;   // past the tile counters
     auto *xh = reinterpret_cast<uint16_t *>(wsb);
     auto *xl = reinterpret_cast<uint16_t *>(wsb + pb);
-    auto *xs = reinterpret_cast<float *>(wsb + 2 * pb);
-    auto *xsc = reinterpret_cast<float *>(wsb + 2 * pb + split_sum_bytes(batch, cols));
+    auto *xsc = reinterpret_cast<float *>(wsb + 2 * pb);
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(xsplit_kernel, dim3((unsigned)batch), dim3(256), 0, st, x, ldx, norm_w, eps, (int)cols, xh, xl,
-                       xs, xsc);
+                       xsc);
     VGX_CHECK_LAUNCH();
     auto *part = reinterpret_cast<float *>(wsb + split_bytes(batch, cols));
     const int kper = (nblk + ks - 1) / ks;
@@ -2637,10 +2605,10 @@ int vgx_qgemm(int dtype, const void *w_packed, int64_t rows, int64_t cols, const
     do {                                                                                                      \
         if (dma)                                                                                              \
             hipLaunchKernelGGL((qgemm_tile_dma_kernel<DT, EPI, SP, DTM, DTN>), dgrid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, \
-                               xh, xl, xs, xsc, batch, bias, y, ldy, part, kper);                              \
+                               xh, xl, xsc, batch, bias, y, ldy, part, kper);                                  \
         else                                                                                                  \
             hipLaunchKernelGGL((qgemm_tile_kernel<DT, EPI, SP>), grid, dim3(256), 0, st, w, soff, n_rq, nblk, rows, xh, \
-                               xl, xs, xsc, batch, bias, y, ldy, part, kper);                                 \
+                               xl, xsc, batch, bias, y, ldy, part, kper);                                     \
     } while (0)
 #define VGX_GEMM_EPI(DT)                                                                                      \
     do {                                                                                                      \
