@@ -1,9 +1,11 @@
-"""GPU parity of the bf16-MFMA Q8_0 / Q4_0 GEMM (vgx_qgemm, used by ops.qlinear from 8 activation
-rows on) against the fp64 oracle.
+"""GPU parity of the MFMA Q8_0 / Q4_0 GEMM (vgx_qgemm, used by ops.qlinear from 8 activation rows on)
+against the fp64 oracle.
 
-Bar: the GEMV accumulation bound of oracle.linalg with the relative term raised to 8e-6 for the
-bf16 hi + lo activation split (2^-17 relative per element); a dropped block, a wrong scale or a
-transposed operand is orders of magnitude beyond it.  Shapes: the model's projections at prefill and
+Bar: the GEMV accumulation bound of oracle.linalg.  Above 64 activation rows (the tiled kernels: fp16
+hi + lo pieces of a power-of-two-scaled row, about 2^-22 relative per element) at the one-row GEMV's
+relative term, 2e-6; up to 64 rows (the decode-batch kernels: bf16 hi + fp16 lo16 pieces, 2^-20) with
+the relative term raised to 8e-6.  A dropped block, a wrong scale or a transposed operand is orders
+of magnitude beyond either.  Shapes: the model's projections at prefill and
 batched-decode row counts, ragged row and batch counts, every epilogue, with and without the fused
 RMSNorm; an invariant check that the GEMM equals the GEMV row by row within the same bound.
 """
@@ -32,6 +34,7 @@ def _blocks(dt, rows, cols, seed):
     (1536, 8960, 200, "accum", False), (1536, 1536, 32, "accum", False), (1026, 1536, 27, "store", True),
     (1024, 1024, 20, "swiglu", True)])
 def test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm):
+    rel = 2e-6 if batch > 64 else 8e-6
     rng = np.random.default_rng(rows + cols + batch)
     x = (rng.standard_normal((batch, cols)) * 2.0).astype(np.float32)
     g = rng.uniform(0.8, 1.2, cols).astype(np.float32)
@@ -45,7 +48,7 @@ def test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm):
         gf, uf = codec.decode(dt, gate, rows, cols), codec.decode(dt, up, rows, cols)
         gg, uu = linalg.gemv(gf, u), linalg.gemv(uf, u)
         ref = linalg.swiglu(gg, uu)
-        tg, tu = linalg.gemv_bound(gf, u, dt, rel=8e-6), linalg.gemv_bound(uf, u, dt, rel=8e-6)
+        tg, tu = linalg.gemv_bound(gf, u, dt, rel=rel), linalg.gemv_bound(uf, u, dt, rel=rel)
         tol = 1.1 * np.abs(uu) * tg + np.abs(gg) * tu + 1e-6 * np.abs(ref) + 1e-30
         err = np.abs(h - ref)
         assert np.all(err <= tol), float((err / tol).max())
@@ -62,7 +65,36 @@ def test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm):
         out = torch.from_numpy(y0).to(dev)
     y = ops.qlinear(wq, xt, bias=torch.from_numpy(bias).to(dev), out=out, accumulate=epi == "accum",
                     norm=nrm).cpu().numpy().astype(np.float64)
-    tol = linalg.gemv_bound(wf, u, dt, rel=8e-6) + np.abs(ref) * 2e-7
+    tol = linalg.gemv_bound(wf, u, dt, rel=rel) + np.abs(ref) * 2e-7
+    err = np.abs(y - ref)
+    assert np.all(err <= tol), float((err / tol).max())
+
+
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0])
+@pytest.mark.parametrize("norm", [False, True])
+def test_qgemm_row_magnitudes(dev, dt, norm):
+    """The tiled kernels scale every activation row by its own power of two before splitting it into
+    fp16 pieces: rows whose magnitudes span 1e-20 .. 1e20 (far outside fp16's range, and past the
+    2^21 where a fixed-scale fp16 residual would overflow) and an all-zero row all meet the GEMV bar
+    relative to their own magnitude (with the fused RMSNorm over 1e-15 .. 1e15, so that the fp32 sum of
+    squares stays finite).  100 rows: the tiled path."""
+    rows, cols, batch = 1536, 1536, 100
+    rng = np.random.default_rng(77 + dt + norm)
+    span = 15 if norm else 20          # with the norm, keep the fp32 sum of squares finite
+    x = rng.standard_normal((batch, cols)) * 10.0 ** rng.uniform(-span, span, (batch, 1))
+    x[7] = 0.0
+    x = x.astype(np.float32)
+    g = rng.uniform(0.8, 1.2, cols).astype(np.float32)
+    u = linalg.rmsnorm(x, g, 1e-6) if norm else x.astype(np.float64)
+    raw = _blocks(dt, rows, cols, 5)
+    wq = ops.QWeight.from_blocks(dt, rows, cols, raw, dev)
+    wf = codec.decode(dt, raw, rows, cols)
+    y = ops.qlinear(wq, torch.from_numpy(x).to(dev), norm=(torch.from_numpy(g).to(dev), 1e-6) if norm else None)
+    y = y.cpu().numpy().astype(np.float64)
+    ref = linalg.gemv(wf, u)
+    tol = linalg.gemv_bound(wf, u, dt, rel=2e-6) + np.abs(ref) * 2e-7
+    assert np.all(np.isfinite(y))
+    assert np.all(y[7] == 0.0)
     err = np.abs(y - ref)
     assert np.all(err <= tol), float((err / tol).max())
 
@@ -80,7 +112,7 @@ def test_qgemm_chunk_shapes_match_oracle(dev, dt, rows, cols, batch, epi, norm):
     300 rows: 36 tiles x 16 splits; 2048 x 1536 over 1000 rows: 128 tiles x 4 splits) on the LDS-DMA
     kernel, and LM-head-like tall weights (65541 rows, ragged; the stores over 768 and 1536 columns run
     on the persistent unsplit kernel, with 2 activation tiles per row group, the others on the 32-row
-    tiles of the small-batch kernel).  Same bar as above."""
+    tiles of the small-batch kernel).  Same bars as above."""
     test_qgemm_matches_oracle(dev, dt, rows, cols, batch, epi, norm)
 
 
