@@ -428,6 +428,19 @@ int vgx_step_begin(const void *ring, int64_t n_slots, int64_t slot_bytes, int32_
                    float *bias_early, float *bias_late, int64_t n_heads, int64_t bias_ld, int64_t bias_cap,
                    void *stream);
 
+/* vgx_step_begin followed, in the same launch, by the embedding rows of the ids it wrote:
+ * emb_out[b * emb_ldo + c] = row ids[b] of the packed embedding table emb_packed (emb_rows x emb_cols
+ * of emb_dtype; out-of-range ids take row 0), as vgx_embed_rows with pad row 0.  One launch instead
+ * of two at the start of a decode step.  emb_packed NULL: vgx_step_begin.  Replaces the step's
+ * embedding lookup after its ids (embed_row, runtime/vault3.c:626-654; nn.Embedding,
+ * src/vault_v3_model.py:2285). */
+int vgx_step_begin_embed(const void *ring, int64_t n_slots, int64_t slot_bytes, int32_t *counter, int32_t *step,
+                         int64_t *ids, int64_t B, int64_t *out_ref, int32_t *tok_cur, int64_t tok_ld, int32_t *seg_cur,
+                         int32_t *ctrl, const uint8_t *tiers, int64_t vocab, int64_t seg_min, int64_t seg_max,
+                         int64_t window, float *bias_early, float *bias_late, int64_t n_heads, int64_t bias_ld,
+                         int64_t bias_cap, int emb_dtype, const void *emb_packed, int64_t emb_rows, int64_t emb_cols,
+                         float *emb_out, int64_t emb_ldo, void *stream);
+
 /* The segment-bank update at a chunk boundary, for the evicted chunk ev_chunk (its tokens' scores
  * sc_prev, local segment ids seg_prev, tokens tok_prev, window entries each): quarantine (a score
  * <= -1e29 sets its whole segment to -1e30, written back), per-segment maximum, candidates t >= t0

@@ -68,6 +68,42 @@ def test_step_begin_matches_seg_step(dev, B):
     io.close()
 
 
+@pytest.mark.parametrize("dt", [codec.Q8_0, codec.Q4_0, codec.F32])
+@pytest.mark.parametrize("B", [1, 3])
+def test_step_begin_embed_equals_embed(dev, dt, B):
+    """vgx_step_begin_embed: the step words, ids, ring and segmenter as vgx_step_begin, and the
+    embedding rows of the ids it wrote equal vgx_embed_rows's (pad row 0) bit for bit, host and device
+    ids, including ids out of the table's range (row 0)."""
+    cfg = modelgen.tiny_cfg(window=32, seg_min=3, seg_max=11)
+    W, rows, cols = cfg.window, 300, 96
+    tiers = _tiers(cfg, dev)
+    rng = np.random.default_rng(B + dt)
+    raw = vlt3.synthetic_blocks(dt, rows, cols, rng) if dt != codec.F32 else \
+        rng.standard_normal((rows, cols)).astype(np.float32).tobytes()
+    table = ops.QWeight.from_blocks(dt, rows, cols, raw, dev)
+    io = StepIO(B, dev)
+    tok_a, tok_b = (torch.zeros(B, W, dtype=torch.int32, device=dev) for _ in range(2))
+    for p in range(2 * W + 3):
+        ids = rng.integers(0, rows, B)
+        if p % 5 == 0:
+            ids[0] = rows + 7 if p % 10 == 0 else -3        # out of range: row 0
+        t = torch.from_numpy(ids).to(torch.int64)
+        words = [p % W, p + 7, -1, p % W + 1]
+        io.write(t if p % 2 else t.to(dev), *words, out=torch.empty(B, 7, device=dev))
+        x = torch.full((B, cols), float("nan"), device=dev)
+        ops.step_begin(io.ring, io.RING, io.slot_bytes, io.counter, io.step, io.ids, None, tok_a, None, None, tiers,
+                       cfg.seg_min, cfg.seg_max, embed=(table, x))
+        io.launched()
+        ref = ops.embed(table, io.ids, pad_row=0)
+        step_b = torch.tensor(words, dtype=torch.int32, device=dev)
+        ops.seg_step(t.to(dev), step_b, tok_b, None, None, tiers, cfg.seg_min, cfg.seg_max)
+        torch.cuda.synchronize()
+        assert io.step.tolist() == words and io.ids.tolist() == ids.tolist(), p
+        assert torch.equal(tok_a, tok_b), p
+        assert torch.equal(x, ref), p
+    io.close()
+
+
 def test_step_begin_host_runs_ahead(dev):
     """40 steps enqueued behind a long device job with no host synchronisation: the host waits for a
     slot's previous launch before rewriting it, so every launch reads its own step's ids."""

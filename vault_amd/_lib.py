@@ -60,6 +60,8 @@ _SIGS = {
     "vgx_host_free": (I32, [P]),
     "vgx_step_begin": (I32, [P, I64, I64, P, P, P, I64, P, P, I64, P, P, P, I64, I64, I64, I64, P, P, I64, I64, I64,
                              P]),
+    "vgx_step_begin_embed": (I32, [P, I64, I64, P, P, P, I64, P, P, I64, P, P, P, I64, I64, I64, I64, P, P, I64, I64,
+                                   I64, I32, P, I64, I64, P, I64, P]),
     "vgx_seg_evict": (I32, [P, P, P, I64, P, P, P, P, P, I64, I64, I64, P, P, P]),
     "vgx_gather_rows_masked": (I32, [I32, P, P, P, I64, I64, I64, I64, I64, I64, P]),
     "vgx_rope_rotate_dyn": (I32, [I32, P, P, I64, I64, I64, I64, I64, P, I64, P, I64, I32, P]),

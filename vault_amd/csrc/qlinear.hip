@@ -92,35 +92,6 @@ __global__ void unpack_kernel(const uint8_t *__restrict__ src, uint8_t *__restri
     }
 }
 
-// Dequantize one 32-weight block of packed row r into out[0..31].
-template <int DT>
-__device__ __forceinline__ void dequant_block(const uint8_t *__restrict__ w, int64_t nblk, int64_t soff, int64_t r,
-                                              int64_t b, float *__restrict__ out) {
-    constexpr int QB = quant_bytes(DT);
-    const int64_t rq = r >> 2, rr = r & 3;
-    const uint8_t *qs = w + ((rq * nblk + b) * 4 + rr) * QB;
-    if constexpr (DT == VGX_F32) {
-        const float *s = reinterpret_cast<const float *>(qs);
-        for (int j = 0; j < QK; ++j) out[j] = s[j];
-    } else if constexpr (DT == VGX_BF16) {
-        const uint16_t *s = reinterpret_cast<const uint16_t *>(qs);
-        for (int j = 0; j < QK; ++j) out[j] = bf16_bits_to_float(s[j]);
-    } else if constexpr (DT == VGX_F16) {
-        const uint16_t *s = reinterpret_cast<const uint16_t *>(qs);
-        for (int j = 0; j < QK; ++j) out[j] = half_bits_to_float(s[j]);
-    } else {
-        const float d = half_bits_to_float(reinterpret_cast<const uint16_t *>(w + soff)[(rq * nblk + b) * 4 + rr]);
-        if constexpr (DT == VGX_Q8_0) {
-            for (int j = 0; j < QK; ++j) out[j] = d * (float)(int8_t)qs[j];
-        } else {
-            for (int j = 0; j < 16; ++j) {
-                out[j] = (float)((int)(qs[j] & 0x0F) - 8) * d;
-                out[j + 16] = (float)((int)(qs[j] >> 4) - 8) * d;
-            }
-        }
-    }
-}
-
 template <int DT>
 __global__ void dequant_kernel(const uint8_t *__restrict__ w, float *__restrict__ out, int64_t rows, int64_t nblk,
                                int64_t soff) {

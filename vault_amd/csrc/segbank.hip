@@ -11,7 +11,7 @@
 // and global segment ids (int32), in chronological order.
 #include <string.h>
 
-#include "common.h"
+#include "qgemv.h"
 
 using namespace vgx;
 
@@ -81,6 +81,11 @@ struct StepBeginArgs {
     int H;
     int64_t bias_ld;
     int bias_cap;
+    // the embedding rows of the step's ids (vgx_step_begin_embed), or emb == nullptr
+    const uint8_t *emb;
+    int emb_dt;
+    int64_t emb_rows, emb_nblk, emb_soff, emb_ldo;
+    float *emb_out;
 };
 
 // One workgroup.  Every host load of the slot (header, host ids, bias row indices and vectors) is
@@ -190,6 +195,24 @@ __global__ __launch_bounds__(kBeginThreads) void step_begin_kernel(StepBeginArgs
     }
     __syncthreads();
     if (tid == 0) *a.counter = (int32_t)((k + 1) % (uint32_t)a.n_slots);
+    if (a.emb != nullptr) {
+        // the embedding rows of the ids just written (visible to the workgroup after the barrier), one
+        // thread per 32-element block, as vgx_embed_rows with pad row 0
+        for (int t = tid; t < a.B * a.emb_nblk; t += kBeginThreads) {
+            const int b = (int)(t / a.emb_nblk);
+            const int64_t blk = t - (int64_t)b * a.emb_nblk;
+            int64_t r = a.ids[b];
+            if (r < 0 || r >= a.emb_rows) r = 0;
+            float *o = a.emb_out + b * a.emb_ldo + blk * QK;
+            switch (a.emb_dt) {
+                case VGX_Q8_0: dequant_block<VGX_Q8_0>(a.emb, a.emb_nblk, a.emb_soff, r, blk, o); break;
+                case VGX_Q4_0: dequant_block<VGX_Q4_0>(a.emb, a.emb_nblk, a.emb_soff, r, blk, o); break;
+                case VGX_F32: dequant_block<VGX_F32>(a.emb, a.emb_nblk, a.emb_soff, r, blk, o); break;
+                case VGX_BF16: dequant_block<VGX_BF16>(a.emb, a.emb_nblk, a.emb_soff, r, blk, o); break;
+                default: dequant_block<VGX_F16>(a.emb, a.emb_nblk, a.emb_soff, r, blk, o); break;
+            }
+        }
+    }
 }
 
 __device__ __forceinline__ int f2ord(float f) {      // order-preserving float -> int
@@ -457,11 +480,20 @@ int vgx_host_free(void *ptr) {
     return hipHostFree(ptr) == hipSuccess ? VGX_OK : VGX_E_HIP;
 }
 
-int vgx_step_begin(const void *ring, int64_t n_slots, int64_t slot_bytes, int32_t *counter, int32_t *step, int64_t *ids,
-                   int64_t B, int64_t *out_ref, int32_t *tok_cur, int64_t tok_ld, int32_t *seg_cur, int32_t *ctrl,
-                   const uint8_t *tiers, int64_t vocab, int64_t seg_min, int64_t seg_max, int64_t window,
-                   float *bias_early, float *bias_late, int64_t n_heads, int64_t bias_ld, int64_t bias_cap,
-                   void *stream) {
+int vgx_step_begin_embed(const void *ring, int64_t n_slots, int64_t slot_bytes, int32_t *counter, int32_t *step,
+                         int64_t *ids, int64_t B, int64_t *out_ref, int32_t *tok_cur, int64_t tok_ld, int32_t *seg_cur,
+                         int32_t *ctrl, const uint8_t *tiers, int64_t vocab, int64_t seg_min, int64_t seg_max,
+                         int64_t window, float *bias_early, float *bias_late, int64_t n_heads, int64_t bias_ld,
+                         int64_t bias_cap, int emb_dtype, const void *emb_packed, int64_t emb_rows, int64_t emb_cols,
+                         float *emb_out, int64_t emb_ldo, void *stream) {
+    if (emb_packed != nullptr) {
+        if (emb_dtype != VGX_Q8_0 && emb_dtype != VGX_Q4_0 && emb_dtype != VGX_F32 && emb_dtype != VGX_BF16 &&
+            emb_dtype != VGX_F16)
+            return VGX_E_DTYPE;
+        if (!emb_out) return VGX_E_ARG;
+        if (emb_rows <= 0 || emb_cols <= 0 || emb_ldo < emb_cols) return VGX_E_SIZE;
+        if (emb_cols % QK) return VGX_E_SHAPE;
+    }
     if (!ring || !counter || !step || !ids || !tok_cur) return VGX_E_ARG;
     if (seg_cur && !ctrl) return VGX_E_ARG;
     if ((bias_early == nullptr) != (bias_late == nullptr)) return VGX_E_ARG;
@@ -501,9 +533,28 @@ int vgx_step_begin(const void *ring, int64_t n_slots, int64_t slot_bytes, int32_
     a.H = (int)n_heads;
     a.bias_ld = bias_ld;
     a.bias_cap = (int)bias_cap;
+    if (emb_packed != nullptr) {
+        a.emb = static_cast<const uint8_t *>(emb_packed);
+        a.emb_dt = emb_dtype;
+        a.emb_rows = emb_rows;
+        a.emb_nblk = emb_cols / QK;
+        a.emb_soff = gemv_plain(emb_dtype) ? 0 : vgx_qweight_scale_offset(emb_dtype, emb_rows, emb_cols);
+        a.emb_out = emb_out;
+        a.emb_ldo = emb_ldo;
+    }
     hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(kBeginThreads), 0, (hipStream_t)stream, a);
     VGX_CHECK_LAUNCH();
     return VGX_OK;
+}
+
+int vgx_step_begin(const void *ring, int64_t n_slots, int64_t slot_bytes, int32_t *counter, int32_t *step, int64_t *ids,
+                   int64_t B, int64_t *out_ref, int32_t *tok_cur, int64_t tok_ld, int32_t *seg_cur, int32_t *ctrl,
+                   const uint8_t *tiers, int64_t vocab, int64_t seg_min, int64_t seg_max, int64_t window,
+                   float *bias_early, float *bias_late, int64_t n_heads, int64_t bias_ld, int64_t bias_cap,
+                   void *stream) {
+    return vgx_step_begin_embed(ring, n_slots, slot_bytes, counter, step, ids, B, out_ref, tok_cur, tok_ld, seg_cur,
+                                ctrl, tiers, vocab, seg_min, seg_max, window, bias_early, bias_late, n_heads, bias_ld,
+                                bias_cap, 0, nullptr, 0, 0, nullptr, 0, stream);
 }
 
 int vgx_seg_evict(float *sc_prev, const int32_t *seg_prev, const int32_t *tok_prev, int64_t window, int64_t *mem_pos,

@@ -702,15 +702,16 @@ class VAULTv3ForCausalLM:
         HD, GD = H * D, G * D
         io = st.step_io()
         step, n_cur = io.step, io.step[ops.L.STEP_N_CUR:ops.L.STEP_N_CUR + 1]
-        # the slot's words and ids onto the device, token ring and segmenter, then the embedding rows
+        # the slot's words and ids onto the device, token ring and segmenter, and the embedding rows of
+        # the ids [B, d], in one launch
+        x = torch.empty(B, d, dtype=torch.float32, device=self.device)
         ops.step_begin(io.ring, io.RING, io.slot_bytes, io.counter, step, io.ids, io.out_ref if indirect else None,
                        st.tok_cur, st.seg_cur_ids if seg_active else None, st.ctrl if seg_active else None,
                        self.tier_dev, cfg.seg_min, cfg.seg_max,
-                       bias=(st.bias_early, st.bias_late) if bias_on else None)
+                       bias=(st.bias_early, st.bias_late) if bias_on else None, embed=(w.embed, x))
         # bank span: its length is the device count (the bias rows cover the bank's capacity)
         m_dev = st.ctrl[ops.L.SEG_MEM_CNT:ops.L.SEG_MEM_CNT + 1]
         n_seg = st.k_seg_rot.shape[3] if has_seg else 0
-        x = ops.embed(w.embed, io.ids, pad_row=0)                              # [B, d]
         # rows [0, B) receive the scorer features, rows [B, 2B) the habituated ones (one LayerNorm launch)
         feats = torch.empty(2 * B, len(cfg.seg_layers) * d, dtype=torch.float32, device=self.device) \
             if seg_active else None

@@ -629,17 +629,28 @@ def seg_step(ids: torch.Tensor, step: torch.Tensor, tok_cur: torch.Tensor, seg_c
 def step_begin(ring: int, n_slots: int, slot_bytes: int, counter: torch.Tensor, step: torch.Tensor, ids: torch.Tensor,
                out_ref: Optional[torch.Tensor], tok_cur: torch.Tensor, seg_cur: Optional[torch.Tensor],
                ctrl: Optional[torch.Tensor], tiers: Optional[torch.Tensor], seg_min: int, seg_max: int,
-               bias: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> None:
+               bias: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+               embed: Optional[Tuple["QWeight", torch.Tensor]] = None) -> None:
     """The decode step's first launch (vgx_step_begin): the step words, ids and output address from
     slot (*counter mod n_slots) of the pinned host ring at address ``ring``, then vgx_seg_step's
-    bookkeeping; with ``bias`` = (early, late) [H, cap] fp32 rows, the slot's bias rows."""
+    bookkeeping; with ``bias`` = (early, late) [H, cap] fp32 rows, the slot's bias rows; with ``embed`` =
+    (table, out [B, cols] fp32), the embedding rows of the ids in the same launch (vgx_step_begin_embed,
+    as embed with pad row 0)."""
     B, W = tok_cur.shape
     be, bl = bias if bias is not None else (None, None)
     H, ld, cap = (be.shape[0], be.stride(0), be.shape[1]) if be is not None else (0, 0, 0)
-    L.check(L.load().vgx_step_begin(ring, n_slots, slot_bytes, counter.data_ptr(), step.data_ptr(), ids.data_ptr(), B,
-                                    _ptr(out_ref), tok_cur.data_ptr(), tok_cur.stride(0), _ptr(seg_cur), _ptr(ctrl),
-                                    _ptr(tiers), tiers.numel() if tiers is not None else 0, seg_min, seg_max, W,
-                                    _ptr(be), _ptr(bl), H, ld, cap, _stream(tok_cur.device)), "vgx_step_begin")
+    args = (ring, n_slots, slot_bytes, counter.data_ptr(), step.data_ptr(), ids.data_ptr(), B, _ptr(out_ref),
+            tok_cur.data_ptr(), tok_cur.stride(0), _ptr(seg_cur), _ptr(ctrl), _ptr(tiers),
+            tiers.numel() if tiers is not None else 0, seg_min, seg_max, W, _ptr(be), _ptr(bl), H, ld, cap)
+    if embed is None:
+        L.check(L.load().vgx_step_begin(*args, _stream(tok_cur.device)), "vgx_step_begin")
+        return
+    w, out = embed
+    _need(out, torch.float32, "embedding rows")
+    if out.dim() != 2 or out.shape != (B, w.cols) or out.stride(1) != 1:
+        raise ValueError("embedding rows must be [B, cols] with unit stride along cols")
+    L.check(L.load().vgx_step_begin_embed(*args, w.dtype, w.packed.data_ptr(), w.rows, w.cols, out.data_ptr(),
+                                          out.stride(0), _stream(tok_cur.device)), "vgx_step_begin_embed")
 
 
 def seg_evict(sc_prev, seg_prev, tok_prev, mem_pos, mem_score, mem_tok, mem_seg, ctrl, ev: int, t0: int,
