@@ -197,45 +197,24 @@ constexpr int kTM = 128;                 // weight rows per workgroup tile
 constexpr int kTN = 128;                 // activation rows per workgroup tile
 constexpr int kBRow = QK + 8;            // fp16 per staged activation row (16 B of padding)
 
-// Weights 8 lg .. 8 lg + 7 of the block as bf16 and fp16 A fragments, in K-slot order
-// 0, 2, 1, 3, 4, 6, 5, 7 (the activations are staged in the same order).  Q4_0: one
-// AND-OR per two weights gives bf16(16 + n) exactly (exponent of 16, nibble in the top four mantissa
-// bits: 0x4180 | n << 3), so the block's offset is 24; the nibble reaches bits 3..6 by a rotation
-// (right by 29 = left by 3 for the low nibbles, right by 1 for the high ones; the bits it wraps fall
-// outside the mask).  The smallest base whose 16 values share one binade keeps the MFMA's running
-// sums, and so their fp32 rounding, within 5x of the signed weights' (a base of 128 made it 30x).
-// Q8_0: q + 128 through the byte conversions.
-// The same weights divided by 16 as exact fp16 (the B operand lo16 is fp16 and carries a factor 16):
-// Q4_0 as fp16((16 + n) / 16) = 0x3C00 | n << 6 (the nibble rotated to bits 6..9), Q8_0 as
-// fp16((q + 128) / 16) from the same floats.  Both products then add into one accumulator.
+// Q8_0 weights 8 lg .. 8 lg + 7 of the block as the decode-batch split kernel's A fragments, in K-slot
+// order 0, 2, 1, 3, 4, 6, 5, 7 (the activations are staged in the same order): q + 128 through the
+// byte conversions as exact bf16, and the same integers divided by 16 as exact fp16 (the B operand lo16
+// is fp16 and carries a factor 16).  Both products then add into one accumulator.
 template <int DT>
 __device__ __forceinline__ void tile_a_frags(uint2 w, int lg, bf16x8_t &fb, f16x8_t &fh) {
+    static_assert(DT == VGX_Q8_0, "Q4_0 fragments come from q4_word_frags");
+    (void)lg;
     uint32_t o[4], h[4];
-    if constexpr (DT == VGX_Q4_0) {
-        const bool hi = (lg >> 1) != 0;       // low nibbles for weights 0..15, high nibbles for 16..31
-        // bf16: nibble to bits 3..6 (and 19..22); fp16: to bits 6..9 (and 22..25), bytes 0 / 2 and
-        // bytes 1 / 3 by rotations of their own (a left turn of six would wrap byte 3's nibble)
-        const int rot = hi ? 1 : 29, rh02 = hi ? 30 : 26, rh13 = hi ? 6 : 2;
-        const uint32_t u0 = __builtin_amdgcn_alignbit(w.x, w.x, rot), u1 = __builtin_amdgcn_alignbit(w.y, w.y, rot);
-        o[0] = (u0 & 0x00780078u) | 0x41804180u;           // weights 0, 2 of the word
-        o[1] = ((u0 >> 8) & 0x00780078u) | 0x41804180u;    // weights 1, 3
-        o[2] = (u1 & 0x00780078u) | 0x41804180u;
-        o[3] = ((u1 >> 8) & 0x00780078u) | 0x41804180u;
-        h[0] = (__builtin_amdgcn_alignbit(w.x, w.x, rh02) & 0x03C003C0u) | 0x3C003C00u;
-        h[1] = (__builtin_amdgcn_alignbit(w.x, w.x, rh13) & 0x03C003C0u) | 0x3C003C00u;
-        h[2] = (__builtin_amdgcn_alignbit(w.y, w.y, rh02) & 0x03C003C0u) | 0x3C003C00u;
-        h[3] = (__builtin_amdgcn_alignbit(w.y, w.y, rh13) & 0x03C003C0u) | 0x3C003C00u;
-    } else {
-        const uint32_t u[2] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u};
+    const uint32_t u[2] = {w.x ^ 0x80808080u, w.y ^ 0x80808080u};
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float f0 = (float)(u[i] & 0xFFu), f1 = (float)((u[i] >> 8) & 0xFFu);
-            const float f2 = (float)((u[i] >> 16) & 0xFFu), f3 = (float)(u[i] >> 24);
-            o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f2) & 0xFFFF0000u);
-            o[2 * i + 1] = (__float_as_uint(f1) >> 16) | (__float_as_uint(f3) & 0xFFFF0000u);
-            h[2 * i] = pack_f16x2(f0 * 0.0625f, f2 * 0.0625f);
-            h[2 * i + 1] = pack_f16x2(f1 * 0.0625f, f3 * 0.0625f);
-        }
+    for (int i = 0; i < 2; ++i) {
+        const float f0 = (float)(u[i] & 0xFFu), f1 = (float)((u[i] >> 8) & 0xFFu);
+        const float f2 = (float)((u[i] >> 16) & 0xFFu), f3 = (float)(u[i] >> 24);
+        o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f2) & 0xFFFF0000u);
+        o[2 * i + 1] = (__float_as_uint(f1) >> 16) | (__float_as_uint(f3) & 0xFFFF0000u);
+        h[2 * i] = pack_f16x2(f0 * 0.0625f, f2 * 0.0625f);
+        h[2 * i + 1] = pack_f16x2(f1 * 0.0625f, f3 * 0.0625f);
     }
     fb = __builtin_bit_cast(bf16x8_t, make_uint4(o[0], o[1], o[2], o[3]));
     fh = __builtin_bit_cast(f16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
@@ -481,17 +460,21 @@ __global__ __launch_bounds__(256, 2) void qgemm_tile_kernel(const uint8_t *__res
 // The tiled kernel with its stages filled by LDS DMA (dma16 / dma4: buffer loads that write LDS directly;
 // the kernel makes no other use of M0, which its compiled code was checked for).  Two stages: the loads of block k + 1
 // leave right after the barrier of block k and land in the other stage while block k is multiplied, and
-// they need no staging registers, which leaves room for three workgroups per CU (163 VGPRs, 38 KB of
-// LDS) instead of two (256 VGPRs with the register double buffer of qgemm_tile_kernel).  Same
-// arithmetic as qgemm_tile_kernel, bit for bit.  The activation rows of a stage are unpadded 64-byte
-// rows whose 16-byte pieces are swizzled by (row >> 2) & 3, so the MFMA operand reads stay free of bank
-// conflicts.  Measured on a 1024-token chunk (Q4_0 / Q8_0): gate/up 228.9 -> 193.5 / 251.4 -> 222.5 us,
-// down 143.0 -> 137.2 / 156.1 -> 144.1, q|k|v 49.2 -> 48.3 / 50.8 -> 49.5, o 43.6 -> 45.8 / 46.6 -> 44.9;
-// with three stages at two workgroups per CU 209.7 us for the Q4_0 gate/up, with four 221.1.
+// they need no staging registers, which leaves room for three workgroups per CU (at most 160 VGPRs,
+// 25.5 KB of LDS for Q4_0, 33.5 KB for Q8_0) instead of two (256 VGPRs with the register double buffer
+// of qgemm_tile_kernel).  Same arithmetic as qgemm_tile_kernel, bit for bit.  The activation rows of a
+// stage are unpadded 64-byte rows whose 16-byte pieces are swizzled by (row >> 2) & 3, so the MFMA
+// operand reads stay free of bank conflicts.  Measured on a 1024-token chunk with the 128 x 128 tiles
+// (Q4_0 / Q8_0): gate/up 228.9 -> 193.5 / 251.4 -> 222.5 us against the register double buffer, down
+// 143.0 -> 137.2 / 156.1 -> 144.1, q|k|v 49.2 -> 48.3 / 50.8 -> 49.5, o 43.6 -> 45.8 / 46.6 -> 44.9; with
+// three stages at two workgroups per CU 209.7 us for the Q4_0 gate/up, with four 221.1.
 // Its tile is TM weight rows x TN activation rows, each wave 64 x 64 (wave w: weight rows 64 (w % (TM /
 // 64)), activation rows 64 (w / (TM / 64))).  256 x 64 (kTMDma x kTNDma) stages 12.75 KB per block of
 // a Q4_0 tile instead of the 18.75 KB of 128 x 128 for the same outputs per workgroup: gate/up 195.2
-// -> 182.5 us, down 128.1 -> 122.3, q|k|v 47.4 -> 46.0, o 42.9 -> 43.2.
+// -> 182.5 us, down 128.1 -> 122.3, q|k|v 47.4 -> 46.0, o 42.9 -> 43.2 (with bf16 hi / fp16 lo16
+// pieces and their offset corrections; the fp16 pieces and signed weights then gave 152.8-155.1 /
+// 108.4-109.1 / 43.8-44.2 / 39.0-42.3 us).  Four waves per SIMD (128 VGPRs, a few bytes spilled)
+// measured no better (gate/up 151.6-152.9 against 153.3-155.1 us).
 constexpr int kTMDma = 256, kTNDma = 64;
 template <int DT, int EPI, bool SPLIT, int TM, int TN>
 __global__ __launch_bounds__(256, 3) void qgemm_tile_dma_kernel(const uint8_t *__restrict__ W, int64_t soff, int64_t n_rq,
