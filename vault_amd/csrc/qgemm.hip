@@ -2121,13 +2121,16 @@ int choose_ksplit(int64_t n_rq, int64_t batch, int nc, int nblk) {
     return (int)std::max<int64_t>(1, ks);
 }
 
-// K splits of the tiled kernels, counted on the DMA kernel's tiles: about 512 workgroups (2048 for long
-// rows: measured 139 vs 149 us for the 1536 x 8960 down projection of a 1024-token chunk), at least 8
-// blocks per split.  Targets of 768 (one round at three workgroups per CU) measured no better: q|k|v and
-// o of a 1024-token chunk 45.4 / 40.7 -> 47.7 / 44.0 us.
+// K splits of the tiled kernels, counted on the DMA kernel's tiles: about 512 workgroups, 768 for long
+// rows (one round at three workgroups per CU), at least 8 blocks per split.  The 1536 x 8960 down
+// projection of a 1024-token chunk (96 tiles): 8 splits 95.6-96.7 us, 16 (a target of 2048) 108.3-108.6,
+// 5 99.4-100.1, 4 110.8-111.9, the split partials (fp32, written and read back by the reduce) being
+// what the extra splits cost; over 512 tokens (48 tiles) 16 and 10 splits 64.6-66.1 us, 8 68.9.  For
+// short rows a target of 768 measured no better (q|k|v and o of a 1024-token chunk 45.4 / 40.7 ->
+// 47.7 / 44.0 us).
 int tile_ksplit(int64_t n_rq, int64_t batch, int nblk) {
     const int64_t tiles = (n_rq + kTMDma / 4 - 1) / (kTMDma / 4) * ((batch + kTNDma - 1) / kTNDma);
-    const int64_t target = nblk >= 128 ? 2048 : 512;
+    const int64_t target = nblk >= 128 ? 768 : 512;
     // as many splits as fit the target without exceeding it: 512 workgroups are one round at two per
     // CU, and a few more would run as a mostly idle second round (o-projection of a 1024-token chunk:
     // 96 tiles x 5 splits, 45.9 us, against 6 splits, 52-54 us)
